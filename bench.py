@@ -1,0 +1,378 @@
+#!/usr/bin/env python3
+"""Benchmark of the rocm backend's fused layer ops on one MI355X.
+
+Workloads (synthetic N(0,1) inputs, bf16 activations unless stated, fp32
+norm weights; names and sizes follow the reference's headline op set):
+  1  fp32 RMSNorm x [1024, 2048], w 1 + N(0, .02), eps 1e-6
+  2  decode step at batch 1: embedding gather of one id from a
+     [128000, 2048] bf16 table, residual add + RMSNorm (H 2048), RoPE on
+     Q [16, 128] and K [4, 128] at a position in [0, 20000]
+  3  prefill RoPE in place: Q [8192, 16, 128], K [8192, 4, 128], positions
+     0..8191, theta 1e4, half-split
+  4  vision block: LayerNorm [4096, 1024] (eps 1e-6) then exact-erf GELU
+  5  MoE-layer prefill chain over 8192 tokens: residual add + RMSNorm
+     [8192, 2048], SwiGLU [8192, 2 x 1408] -> [8192, 1408], RoPE as in 3
+
+One step = one pass of a workload's op chain over one input set. The JSON
+line's `value` is workload 5 (the largest, three fused ops timed as one
+sequence): algorithmic HBM bytes per step / time per step. Every workload's
+µs, GB/s and fraction of the 8 TB/s HBM peak are under "configs"; workload
+2 is reported in µs per decode chain (eager launches and graph replay).
+
+Timing: each workload keeps several input sets whose total exceeds 640 MB,
+more than twice the 256 MB Infinity Cache, and steps rotate through them, so
+every step reads from HBM. The K timed steps are captured once into a HIP
+graph and replayed; HIP events on the replay stream bracket the replay,
+with a device synchronisation on both sides. Per-kernel figures come from
+the same procedure applied to one kernel.
+
+cpu_baseline: the reference's CPU path for workload 5 (the oracle's
+restatement of src/backend/reference/ops.cpp and src/model/page_rope.cpp,
+with the reference's threading: norms over rows on up to 16 threads,
+activations and rope serial) timed on this host.
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBPS = 8000.0  # MI355X HBM3E
+METRIC = "achieved HBM GB/s (% of MI355X peak) per fused op; µs per decode-step op chain"
+ROTATE_BYTES = 640 * 2**20
+
+
+def load_backend():
+    from __graft_entry__ import _load_package
+
+    return _load_package()
+
+
+# ---- algorithmic bytes per launch ------------------------------------------------------------------
+
+def bytes_rms_norm(rows, cols, elem):
+    return 2 * rows * cols * elem + cols * 4                     # R x, W x, R w
+
+
+def bytes_add_rms_norm(rows, cols, elem):
+    return 4 * rows * cols * elem + cols * 4                     # R x, R delta, W x', W h, R w
+
+
+def bytes_swiglu(rows, ffn, elem):
+    return 3 * rows * ffn * elem                                 # R gate|up, W out
+
+
+def bytes_rope(rows, heads, dim, elem, pos_bytes=8):
+    return 2 * rows * heads * dim * elem + rows * pos_bytes     # R/W Q and K, R positions
+
+
+def bytes_layer_norm(rows, cols, elem):
+    return 2 * rows * cols * elem + 2 * cols * 4                 # R x, W y, R w, R b
+
+
+def bytes_gelu(n, elem):
+    return 2 * n * elem
+
+
+def bytes_gather(rows, cols, elem_out, elem_table=2):
+    return rows * (cols * elem_table + cols * elem_out + 8)      # R row, W row, R index
+
+
+# ---- timing helpers ---------------------------------------------------------------------------------
+
+class Timer:
+    def __init__(self, torch, steps, warmup, replays=5):
+        self.torch, self.steps, self.warmup, self.replays = torch, steps, warmup, replays
+
+    def graph(self, step_fns):
+        """Median ms per step over `replays` replays of a graph holding
+        `steps` steps that rotate through step_fns (one per input set)."""
+        torch = self.torch
+        for i in range(self.warmup):
+            step_fns[i % len(step_fns)]()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(self.steps):
+                step_fns[i % len(step_fns)]()
+        g.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(self.replays):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record()
+            g.replay()
+            end.record()
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(end) / self.steps)
+        del g
+        return statistics.median(times), min(times), max(times)
+
+    def eager(self, step_fns):
+        """ms per step for `steps` steps launched one by one from the host."""
+        torch = self.torch
+        for i in range(self.warmup):
+            step_fns[i % len(step_fns)]()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(self.steps):
+            step_fns[i % len(step_fns)]()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / self.steps
+
+
+def n_sets(bytes_per_set):
+    return max(2, math.ceil(ROTATE_BYTES / max(bytes_per_set, 1)))
+
+
+def report(name, nbytes, ms):
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 3), "bytes": int(nbytes), "gbps": round(gbps, 1),
+            "frac": round(gbps / PEAK_GBPS, 4)}
+
+
+# ---- workloads ------------------------------------------------------------------------------------------
+
+def bf16_randn(torch, shape, scale=1.0):
+    return (torch.randn(shape, device="cuda", dtype=torch.float32) * scale).to(torch.bfloat16)
+
+
+def weights(torch, cols):
+    return 1 + 0.02 * torch.randn(cols, device="cuda", dtype=torch.float32)
+
+
+def config1(be, torch, timer):
+    rows, cols = 1024, 2048
+    nbytes = bytes_rms_norm(rows, cols, 4)
+    w = weights(torch, cols)
+    sets = [torch.randn(rows, cols, device="cuda") for _ in range(n_sets(nbytes))]
+    fns = [lambda x=x: be.rms_norm(x, w, 1e-6) for x in sets]
+    ms, lo, hi = timer.graph(fns)
+    out = {"workload": "fp32 RMSNorm [1024, 2048]", "step": report("rms_norm fp32", nbytes, ms),
+           "kernels": {"rms_norm_f32": report("rms_norm fp32", nbytes, ms)}, "sets": len(sets)}
+    return out
+
+
+def config2(be, torch, timer):
+    vocab, hidden, qh, kh, dim = 128000, 2048, 16, 4, 128
+    table = bf16_randn(torch, (vocab, hidden), 0.02)
+    w = weights(torch, hidden)
+    inv = torch.from_numpy(be.rope_inv(dim // 2, 1e4)).cuda()
+    gen = torch.Generator().manual_seed(2)
+    state = torch.tensor([int(torch.randint(0, vocab, (1,), generator=gen)), 0,
+                          int(torch.randint(0, 20001, (1,), generator=gen)), 0, -1], dtype=torch.int64).cuda()
+    x = torch.empty(hidden, dtype=torch.bfloat16, device="cuda")
+    h = torch.empty_like(x)
+    delta = bf16_randn(torch, hidden)
+    q, k = bf16_randn(torch, qh * dim), bf16_randn(torch, kh * dim)
+    chain_bytes = (bytes_gather(1, hidden, 2) + bytes_add_rms_norm(1, hidden, 2)
+                   + bytes_rope(1, qh + kh, dim, 2, pos_bytes=8))
+
+    def chain():
+        be.embed_step(table, state, x)
+        be.add_rms_norm(x, delta, w, h, 1e-6)
+        be.rope_qk_step(q, qh, k, kh, dim, state, inv, None, 0)
+
+    ms_graph, lo, hi = timer.graph([chain])
+    ms_eager = timer.eager([chain])
+    kern = {}
+    kern["embed_step_bf16"] = report("gather", bytes_gather(1, hidden, 2),
+                                     timer.graph([lambda: be.embed_step(table, state, x)])[0])
+    kern["add_rms_norm_bf16"] = report("add_rms_norm", bytes_add_rms_norm(1, hidden, 2),
+                                       timer.graph([lambda: be.add_rms_norm(x, delta, w, h, 1e-6)])[0])
+    kern["rope_qk_step_bf16"] = report("rope", bytes_rope(1, qh + kh, dim, 2, 8), timer.graph(
+        [lambda: be.rope_qk_step(q, qh, k, kh, dim, state, inv, None, 0)])[0])
+    return {"workload": "bf16 decode chain, batch 1: gather [128000, 2048] -> add+RMSNorm 2048 -> RoPE Q[16,128] "
+                        "K[4,128]",
+            "step": report("decode chain", chain_bytes, ms_graph),
+            "us_per_chain_graph": round(ms_graph * 1e3, 3), "us_per_chain_eager": round(ms_eager * 1e3, 3),
+            "kernels": kern}
+
+
+def rope_sets(torch, rows, qh, kh, dim, count):
+    pos = torch.arange(rows, dtype=torch.int64, device="cuda")
+    return [(bf16_randn(torch, (rows, qh * dim)), bf16_randn(torch, (rows, kh * dim)), pos) for _ in range(count)]
+
+
+def config3(be, torch, timer):
+    rows, qh, kh, dim = 8192, 16, 4, 128
+    nbytes = bytes_rope(rows, qh + kh, dim, 2)
+    inv = torch.from_numpy(be.rope_inv(dim // 2, 1e4)).cuda()
+    sets = rope_sets(torch, rows, qh, kh, dim, n_sets(nbytes))
+    fns = [lambda s=s: be.rope_qk(s[0], qh, s[1], kh, dim, s[2], None, inv, None, 0) for s in sets]
+    ms, lo, hi = timer.graph(fns)
+    r = report("rope_qk", nbytes, ms)
+    return {"workload": "bf16 prefill RoPE in place, Q [8192,16,128] K [8192,4,128]", "step": r,
+            "kernels": {"rope_qk_bf16": r}, "sets": len(sets)}
+
+
+def config4(be, torch, timer):
+    rows, cols = 4096, 1024
+    ln_bytes, ge_bytes = bytes_layer_norm(rows, cols, 2), bytes_gelu(rows * cols, 2)
+    w, b = weights(torch, cols), 0.02 * torch.randn(cols, device="cuda")
+    sets = [bf16_randn(torch, (rows, cols)) for _ in range(n_sets(ln_bytes))]
+
+    def step(x):
+        be.layer_norm(x, w, b, 1e-6)
+        be.gelu_erf(x)
+
+    ms, lo, hi = timer.graph([lambda x=x: step(x) for x in sets])
+    ms_ln = timer.graph([lambda x=x: be.layer_norm(x, w, b, 1e-6) for x in sets])[0]
+    ms_ge = timer.graph([lambda x=x: be.gelu_erf(x) for x in sets])[0]
+    return {"workload": "bf16 vision LayerNorm [4096, 1024] then exact GELU", "sets": len(sets),
+            "step": report("ln+gelu", ln_bytes + ge_bytes, ms),
+            "kernels": {"layer_norm_bf16": report("ln", ln_bytes, ms_ln), "gelu_erf_bf16": report("gelu", ge_bytes,
+                                                                                                  ms_ge)}}
+
+
+def config5(be, torch, timer):
+    rows, hidden, ffn, qh, kh, dim = 8192, 2048, 1408, 16, 4, 128
+    b_norm = bytes_add_rms_norm(rows, hidden, 2)
+    b_swi = bytes_swiglu(rows, ffn, 2)
+    b_rope = bytes_rope(rows, qh + kh, dim, 2)
+    total = b_norm + b_swi + b_rope
+    w = weights(torch, hidden)
+    inv = torch.from_numpy(be.rope_inv(dim // 2, 1e4)).cuda()
+    count = n_sets(total)
+    sets = []
+    for s in rope_sets(torch, rows, qh, kh, dim, count):
+        sets.append({"x": bf16_randn(torch, (rows, hidden)), "d": bf16_randn(torch, (rows, hidden)),
+                     "h": torch.empty(rows, hidden, dtype=torch.bfloat16, device="cuda"),
+                     "in": bf16_randn(torch, (rows, 2 * ffn)),
+                     "out": torch.empty(rows, ffn, dtype=torch.bfloat16, device="cuda"),
+                     "q": s[0], "k": s[1], "pos": s[2]})
+
+    def step(s):
+        be.add_rms_norm(s["x"], s["d"], w, s["h"], 1e-6)
+        be.swiglu(s["in"], s["out"])
+        be.rope_qk(s["q"], qh, s["k"], kh, dim, s["pos"], None, inv, None, 0)
+
+    ms, lo, hi = timer.graph([lambda s=s: step(s) for s in sets])
+    ms_eager = timer.eager([lambda s=s: step(s) for s in sets])
+    kern = {
+        "add_rms_norm_bf16": report("add_rms_norm", b_norm, timer.graph(
+            [lambda s=s: be.add_rms_norm(s["x"], s["d"], w, s["h"], 1e-6) for s in sets])[0]),
+        "swiglu_bf16": report("swiglu", b_swi, timer.graph([lambda s=s: be.swiglu(s["in"], s["out"]) for s in sets])[0]),
+        "rope_qk_bf16": report("rope_qk", b_rope, timer.graph(
+            [lambda s=s: be.rope_qk(s["q"], qh, s["k"], kh, dim, s["pos"], None, inv, None, 0) for s in sets])[0]),
+    }
+    return {"workload": "bf16 MoE-layer prefill chain, 8192 tokens: add+RMSNorm [8192,2048] -> SwiGLU "
+                        "[8192,2x1408]->[8192,1408] -> RoPE Q[8192,16,128] K[8192,4,128]",
+            "step": report("chain", total, ms), "ms_range": [round(lo, 5), round(hi, 5)],
+            "ms_per_step_eager": round(ms_eager, 5), "kernels": kern, "sets": len(sets)}
+
+
+# ---- the CPU baseline (the reference's CPU path, restated in the oracle) ------------------------------
+
+def cpu_baseline(budget_s, threads):
+    import numpy as np
+
+    import oracle
+
+    rows, hidden, ffn, qh, kh, dim = 8192, 2048, 1408, 16, 4, 128
+    g = np.random.default_rng(5)
+    bf = lambda a: oracle.bf16_round(a)  # noqa: E731  the bf16 inputs, widened to fp32
+    x = bf(g.standard_normal((rows, hidden), dtype=np.float32))
+    d = bf(g.standard_normal((rows, hidden), dtype=np.float32))
+    w = (1 + 0.02 * g.standard_normal(hidden)).astype(np.float32)
+    inp = bf(g.standard_normal((rows, 2 * ffn), dtype=np.float32))
+    q = bf(g.standard_normal((rows, qh * dim), dtype=np.float32))
+    k = bf(g.standard_normal((rows, kh * dim), dtype=np.float32))
+    pos = np.arange(rows, dtype=np.int64)
+    inv = oracle.rope_inv(dim // 2, 1e4)
+    total = (bytes_add_rms_norm(rows, hidden, 2) + bytes_swiglu(rows, ffn, 2) + bytes_rope(rows, qh + kh, dim, 2))
+
+    def chain():
+        oracle.add_rms_norm(x, d, w, 1e-6)
+        oracle.swiglu(inp)
+        oracle.rope(q, qh, dim, tok=pos, inv_tok=inv)
+        oracle.rope(k, kh, dim, tok=pos, inv_tok=inv)
+
+    def run(nthreads):
+        oracle.set_threads(nthreads)
+        chain()  # warm-up
+        times, t_end = [], time.perf_counter() + budget_s / 2
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+            t0 = time.perf_counter()
+            chain()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
+    t_mt, n_mt = run(threads)
+    t_1, n_1 = run(1)
+    oracle.set_threads(1)
+    return {"value": round(total / t_mt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"workload 5 in full (8192 tokens, {total} algorithmic bytes per chain), median of {n_mt} "
+                      f"chains; norms on {threads} threads, activations and rope serial as in the reference",
+            "ms_per_chain": round(t_mt * 1e3, 2), "ms_per_chain_1_thread": round(t_1 * 1e3, 2),
+            "value_1_thread": round(total / t_1 / 1e9, 3)}
+
+
+# ---- main ---------------------------------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: every op is row-independent and this build measures one GPU's share "
+              f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    be = load_backend()
+    if be.device_count() == 0 or not torch.cuda.is_available():
+        print("no HIP device", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    torch.manual_seed(0)
+    info = be.device_info(0)
+    timer = Timer(torch, args.steps, args.warmup)
+    runners = {"1": config1, "2": config2, "3": config3, "4": config4, "5": config5}
+    configs = {}
+    for c in args.configs.split(","):
+        t0 = time.time()
+        configs[c] = runners[c](be, torch, timer)
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        print(f"[bench] workload {c}: {json.dumps(configs[c]['step'])} ({time.time() - t0:.1f} s)", file=sys.stderr,
+              flush=True)
+
+    head = configs.get("5")
+    line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "compute_dtype": "f32", "data": "synthetic N(0,1), random weights",
+            "device": info["name"]}
+    if head is not None:
+        dom = head["kernels"]["add_rms_norm_bf16"]
+        line.update({
+            "value": head["step"]["gbps"], "ms_per_step": round(head["step"]["us"] / 1e3, 5),
+            "config": {"workload": head["workload"], "tokens": 8192, "hidden": 2048, "ffn": 1408,
+                       "q_heads": 16, "kv_heads": 4, "head_dim": 128, "bytes_per_step": head["step"]["bytes"]},
+            "roofline": {"bound": "hbm", "kernel": "add_rms_norm_bf16 [8192, 2048]", "achieved": dom["gbps"],
+                         "peak": PEAK_GBPS, "unit": "GB/s", "frac": dom["frac"], "traffic": None},
+        })
+    if not args.no_cpu and head is not None:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, threads)
+    line["configs"] = configs
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,341 @@
+"""Python binding of the MI355X (gfx950) rocm backend for grpc-unlimited-ocr's
+fused layer ops.
+
+The product is the C ABI in include/uocr_rocm.h, implemented by the
+hand-written HIP kernels in csrc/ and built in-tree into
+build/libuocr_rocm.so (`make` in this directory). This module loads that
+library through ctypes and mirrors the reference's op set
+(src/backend/cuda/ops.h:30-75, decode_ops.h:17-27) over torch tensors:
+torch supplies device memory and the current stream, nothing else. There is
+no fallback: if the library is not built, every op raises.
+
+Errors follow the reference's convention (src/backend/cuda/context.cu:24-28,
+decode_ops.cu:239): a rejected shape or argument raises ValueError (the
+reference's std::invalid_argument) before anything is enqueued; a runtime or
+launch failure raises RocmError (std::runtime_error), each with the C ABI's
+"<what>: <detail>" message.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+BUILD_DIR = os.path.join(HERE, "build")
+LIB_PATH = os.path.join(BUILD_DIR, "libuocr_rocm.so")
+HEADER_PATH = os.path.join(ROOT, "include", "uocr_rocm.h")
+
+OK, INVALID_ARGUMENT, NO_DEVICE, RUNTIME_ERROR, LAUNCH_ERROR = 0, 1, 2, 3, 4
+H2D, D2H, D2D = 1, 2, 3
+
+
+class RocmError(RuntimeError):
+    """A HIP runtime or launch failure reported by the C ABI."""
+
+
+class StepState(ctypes.Structure):
+    """uocr_rocm_step_state: same fields and order as the reference's
+    uocr::cuda::StepState (src/backend/cuda/decode_ops.h:17-23)."""
+
+    _fields_ = [
+        ("token", ctypes.c_int64),
+        ("pos", ctypes.c_int64),
+        ("tok", ctypes.c_int64),
+        ("page", ctypes.c_int64),
+        ("query_page", ctypes.c_int64),
+    ]
+
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+
+# argtypes of every entry point in include/uocr_rocm.h (restype is int unless
+# stated otherwise).
+_SIGNATURES = {
+    "uocr_rocm_status_string": ([_int], ctypes.c_char_p),
+    "uocr_rocm_last_error": ([], ctypes.c_char_p),
+    "uocr_rocm_abi_version": ([], _int),
+    "uocr_rocm_device_count": ([ctypes.POINTER(_int)], _int),
+    "uocr_rocm_device_info": ([_int, ctypes.c_char_p, _sz, ctypes.POINTER(_int), ctypes.POINTER(_int),
+                               ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], _int),
+    "uocr_rocm_stream_create": ([_int, ctypes.POINTER(_vp)], _int),
+    "uocr_rocm_stream_destroy": ([_vp], _int),
+    "uocr_rocm_stream_synchronize": ([_vp], _int),
+    "uocr_rocm_capture_begin": ([_vp], _int),
+    "uocr_rocm_capture_end": ([_vp, ctypes.POINTER(_vp)], _int),
+    "uocr_rocm_graph_launch": ([_vp, _vp], _int),
+    "uocr_rocm_graph_destroy": ([_vp], _int),
+    "uocr_rocm_malloc": ([ctypes.POINTER(_vp), _sz, _vp], _int),
+    "uocr_rocm_free": ([_vp, _vp], _int),
+    "uocr_rocm_host_alloc": ([ctypes.POINTER(_vp), _sz], _int),
+    "uocr_rocm_host_free": ([_vp], _int),
+    "uocr_rocm_memcpy": ([_vp, _vp, _sz, _int, _vp], _int),
+    "uocr_rocm_zero": ([_vp, _sz, _vp], _int),
+    "uocr_rocm_event_create": ([ctypes.POINTER(_vp)], _int),
+    "uocr_rocm_event_destroy": ([_vp], _int),
+    "uocr_rocm_event_record": ([_vp, _vp], _int),
+    "uocr_rocm_event_elapsed_ms": ([_vp, _vp, ctypes.POINTER(_f32)], _int),
+    "uocr_rocm_add_inplace": ([_vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_copy": ([_vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_rms_norm": ([_vp, _vp, _vp, _i64, _i64, _f32], _int),
+    "uocr_rocm_layer_norm": ([_vp, _vp, _vp, _vp, _i64, _i64, _f32], _int),
+    "uocr_rocm_gelu_erf": ([_vp, _vp, _i64], _int),
+    "uocr_rocm_silu_mul": ([_vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_rope": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64], _int),
+    "uocr_rocm_gather_rows_bf16": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp], _int),
+    "uocr_rocm_gather_row_bf16": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
+    "uocr_rocm_embed_step": ([_vp, _vp, _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_rope_step": ([_vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64], _int),
+    "uocr_rocm_add_rms_norm": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32], _int),
+    "uocr_rocm_swiglu": ([_vp, _vp, _vp, _i64, _i64], _int),
+    "uocr_rocm_rope_qk": ([_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
+                           _i64], _int),
+    "uocr_rocm_rope_qk_step": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64], _int),
+    "uocr_rocm_rms_norm_bf16": ([_vp, _vp, _vp, _i64, _i64, _f32], _int),
+    "uocr_rocm_add_rms_norm_bf16": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32], _int),
+    "uocr_rocm_layer_norm_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _f32], _int),
+    "uocr_rocm_gelu_erf_bf16": ([_vp, _vp, _i64], _int),
+    "uocr_rocm_swiglu_bf16": ([_vp, _vp, _vp, _i64, _i64], _int),
+    "uocr_rocm_rope_bf16": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64], _int),
+    "uocr_rocm_rope_qk_bf16": ([_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
+                                _i64, _i64], _int),
+    "uocr_rocm_rope_qk_step_bf16": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64], _int),
+    "uocr_rocm_gather_rows_bf16_bf16": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp], _int),
+    "uocr_rocm_embed_step_bf16": ([_vp, _vp, _i64, _vp, _i64, _vp], _int),
+}
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded C ABI library; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RocmError(f"{LIB_PATH} is not built: run `make` in {HERE} (or __graft_entry__.build())")
+        # torch ships its own HIP runtime under the soname libamdhip64.so.7.
+        # Loading torch first makes this library bind to that same runtime;
+        # loaded the other way round, a process would hold two HIP runtimes
+        # and torch's streams would be foreign handles here.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        _LIB = handle
+    return _LIB
+
+
+def check(status: int) -> None:
+    """Raise for a non-zero C ABI status, with the library's message."""
+    if status == OK:
+        return
+    message = lib().uocr_rocm_last_error().decode()
+    if status == INVALID_ARGUMENT:
+        raise ValueError(message)
+    raise RocmError(message)
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point by name and raise on a non-zero status."""
+    check(getattr(lib(), name)(*args))
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    check(lib().uocr_rocm_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def device_info(index: int = 0) -> dict:
+    name = ctypes.create_string_buffer(256)
+    arch, cus = ctypes.c_int(0), ctypes.c_int(0)
+    free_b, total_b = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    check(lib().uocr_rocm_device_info(index, name, 256, ctypes.byref(arch), ctypes.byref(cus), ctypes.byref(free_b),
+                                      ctypes.byref(total_b)))
+    return {"name": name.value.decode(), "gfx_arch": arch.value, "compute_units": cus.value,
+            "free_bytes": free_b.value, "total_bytes": total_b.value}
+
+
+# ---- torch plumbing -----------------------------------------------------------
+
+
+def _torch():
+    import torch  # imported lazily: the CPU-side tests need only ctypes
+
+    return torch
+
+
+def current_stream() -> int:
+    """torch's current stream on the current device, as the C ABI takes it."""
+    return _torch().cuda.current_stream().cuda_stream
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return t.data_ptr()
+
+
+def _is_bf16(t) -> bool:
+    torch = _torch()
+    if t.dtype == torch.bfloat16:
+        return True
+    if t.dtype == torch.float32:
+        return False
+    raise ValueError(f"activations must be float32 or bfloat16, got {t.dtype}")
+
+
+def _rows_cols(x):
+    if x.dim() < 1:
+        raise ValueError("tensor must have at least one axis")
+    cols = x.shape[-1]
+    return (x.numel() // cols if cols else 0), cols
+
+
+def _f32_param(t):
+    torch = _torch()
+    if t is not None and t.dtype != torch.float32:
+        raise ValueError("norm weights, biases and rope tables are float32")
+    return _ptr(t)
+
+
+def _op(name: str, stream, *args) -> None:
+    """Call op `name` on `stream` (torch's current stream when None). The
+    stream is resolved after the other arguments have been checked."""
+    call(name, current_stream() if stream is None else stream, *args)
+
+
+# ---- ops (mirroring uocr::cuda / uocr::rocm) -------------------------------------
+
+
+def add_inplace(y, x, stream=None):
+    """y += x (fp32). Reference: add_inplace, src/backend/cuda/ops.h:30."""
+    _op("uocr_rocm_add_inplace", stream, _ptr(y), _ptr(x), y.numel())
+
+
+def copy(dst, src, stream=None):
+    """dst = src (fp32, device to device). Reference: copy, ops.h:68-69."""
+    _op("uocr_rocm_copy", stream, _ptr(dst), _ptr(src), src.numel())
+
+
+def rms_norm(x, w, eps, stream=None):
+    """In place over the rows of x (fp32 or bf16). Reference: rms_norm, ops.h:34."""
+    rows, cols = _rows_cols(x)
+    name = "uocr_rocm_rms_norm_bf16" if _is_bf16(x) else "uocr_rocm_rms_norm"
+    _op(name, stream, _ptr(x), _f32_param(w), rows, cols, eps)
+
+
+def add_rms_norm(x, delta, w, h, eps, stream=None):
+    """x += delta; h = rms_norm(x) * w, fused (fp32 or bf16)."""
+    rows, cols = _rows_cols(x)
+    bf = _is_bf16(x)
+    if _is_bf16(delta) != bf or _is_bf16(h) != bf:
+        raise ValueError("x, delta and h must share a dtype")
+    if delta.numel() != x.numel() or h.numel() != x.numel():
+        raise ValueError("x, delta and h must have the same shape")
+    _op("uocr_rocm_add_rms_norm_bf16" if bf else "uocr_rocm_add_rms_norm", stream, _ptr(x), _ptr(delta),
+         _f32_param(w), _ptr(h), rows, cols, eps)
+
+
+def layer_norm(x, w, b, eps, stream=None):
+    """In place over the rows of x (fp32 or bf16). Reference: layer_norm, ops.h:32-33."""
+    rows, cols = _rows_cols(x)
+    name = "uocr_rocm_layer_norm_bf16" if _is_bf16(x) else "uocr_rocm_layer_norm"
+    _op(name, stream, _ptr(x), _f32_param(w), _f32_param(b), rows, cols, eps)
+
+
+def gelu_erf(x, stream=None):
+    """In place exact GELU (fp32 or bf16). Reference: gelu_erf, ops.h:37."""
+    name = "uocr_rocm_gelu_erf_bf16" if _is_bf16(x) else "uocr_rocm_gelu_erf"
+    _op(name, stream, _ptr(x), x.numel())
+
+
+def silu_mul(g, u, stream=None):
+    """g = silu(g) * u (fp32). Reference: silu_mul, ops.h:39."""
+    _op("uocr_rocm_silu_mul", stream, _ptr(g), _ptr(u), g.numel())
+
+
+def swiglu(inp, out, stream=None):
+    """out [rows, F] = silu(inp[:, :F]) * inp[:, F:] for inp [rows, 2F]."""
+    rows, two_f = _rows_cols(inp)
+    if two_f % 2:
+        raise ValueError("swiglu input width must be 2 * ffn")
+    bf = _is_bf16(inp)
+    if _is_bf16(out) != bf or out.numel() != rows * (two_f // 2):
+        raise ValueError("swiglu output must be [rows, ffn] of the input's dtype")
+    _op("uocr_rocm_swiglu_bf16" if bf else "uocr_rocm_swiglu", stream, _ptr(inp), _ptr(out), rows, two_f // 2)
+
+
+def rope(x, heads, dim, tok, page, inv_tok, inv_page, page_mod, one_tok=0, one_page=0, stream=None):
+    """In place rope on x [rows, heads * dim] (fp32 or bf16). Reference: rope, ops.h:48-52."""
+    rows = x.numel() // (heads * dim) if heads * dim else 0
+    n_tok = 0 if inv_tok is None else inv_tok.numel()
+    n_page = 0 if inv_page is None else inv_page.numel()
+    name = "uocr_rocm_rope_bf16" if _is_bf16(x) else "uocr_rocm_rope"
+    _op(name, stream, _ptr(x), rows, heads, dim, _ptr(tok), _ptr(page), _f32_param(inv_tok), n_tok,
+         _f32_param(inv_page), n_page, page_mod, one_tok, one_page)
+
+
+def rope_qk(q, q_heads, k, k_heads, dim, tok, page, inv_tok, inv_page, page_mod, one_tok=0, one_page=0, stream=None):
+    """rope on Q [rows, q_heads * dim] and K [rows, k_heads * dim] in one launch."""
+    rows = q.numel() // (q_heads * dim) if q_heads * dim else k.numel() // (k_heads * dim)
+    bf = _is_bf16(q)
+    if k is not None and _is_bf16(k) != bf:
+        raise ValueError("q and k must share a dtype")
+    if k is not None and k_heads and k.numel() != rows * k_heads * dim:
+        raise ValueError("k must have the rows of q")
+    n_tok = 0 if inv_tok is None else inv_tok.numel()
+    n_page = 0 if inv_page is None else inv_page.numel()
+    _op("uocr_rocm_rope_qk_bf16" if bf else "uocr_rocm_rope_qk", stream, _ptr(q), q_heads, _ptr(k), k_heads,
+         rows, dim, _ptr(tok), _ptr(page), _f32_param(inv_tok), n_tok, _f32_param(inv_page), n_page, page_mod,
+         one_tok, one_page)
+
+
+def rope_qk_step(q, q_heads, k, k_heads, dim, state, inv_tok, inv_page, page_mod, stream=None):
+    """rope_qk of one decode row at the device StepState `state` (an int64 tensor of 5)."""
+    n_tok = 0 if inv_tok is None else inv_tok.numel()
+    name = "uocr_rocm_rope_qk_step_bf16" if _is_bf16(q) else "uocr_rocm_rope_qk_step"
+    _op(name, stream, _ptr(q), q_heads, _ptr(k), k_heads, dim, _ptr(state), _f32_param(inv_tok), n_tok,
+         _f32_param(inv_page), page_mod)
+
+
+def gather_rows_bf16(table, index, out, table_rows=None, stream=None):
+    """out[r] = table[index[r]] for a bf16 table; out is float32 (widened) or
+    bfloat16 (bit copy). Reference: gather_rows_bf16, ops.h:72-73."""
+    rows, cols = out.shape[0], table.shape[-1]
+    bound = table.shape[0] if table_rows is None else table_rows
+    name = "uocr_rocm_gather_rows_bf16_bf16" if _is_bf16(out) else "uocr_rocm_gather_rows_bf16"
+    _op(name, stream, _ptr(table), bound, _ptr(index), rows, cols, _ptr(out))
+
+
+def gather_row_bf16(table, one_index, out, stream=None):
+    """out = widen(table[one_index]). Reference: gather_row_bf16, ops.h:74-75."""
+    _op("uocr_rocm_gather_row_bf16", stream, _ptr(table), table.shape[0], one_index, table.shape[-1], _ptr(out))
+
+
+def embed_step(table, state, out, stream=None):
+    """out = table[state.token] read on the device. Reference: embed_step, decode_ops.h:25."""
+    name = "uocr_rocm_embed_step_bf16" if _is_bf16(out) else "uocr_rocm_embed_step"
+    _op(name, stream, _ptr(table), table.shape[0], _ptr(state), table.shape[-1], _ptr(out))
+
+
+def rope_inv(n: int, theta: float):
+    """PageRope's frequency table (src/model/page_rope.cpp:17-19):
+    float32(1 / theta ** (i / n)) evaluated in float64, i < n."""
+    import numpy as np
+
+    i = np.arange(n, dtype=np.float64)
+    return (1.0 / np.power(np.float64(theta), i / np.float64(n))).astype(np.float32)

@@ -1,0 +1,194 @@
+// common.hpp: device helpers shared by the gfx950 kernels (bf16 rounding,
+// 128-bit row chunks, wave64 DPP reductions) and the host-side status
+// plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "uocr_rocm.h"
+
+namespace uocr_rocm {
+
+// ---- launch geometry ------------------------------------------------------
+
+constexpr int kWave = 64;                        // CDNA wavefront width
+constexpr int kBlock = 256;                      // 4 waves per workgroup
+constexpr int kWavesPerBlock = kBlock / kWave;   // one row per wave
+
+// ---- bf16 -----------------------------------------------------------------
+
+// bf16 -> fp32 is exact: the 16 bits become the top half of a binary32.
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
+
+// fp32 -> bf16, round to nearest even; a NaN keeps its sign and top payload
+// bits and gets the quiet bit (0x0040 of the bf16). This is the rounding the
+// reference defines for every bf16 value it stores (src/tensor/dtype.h:39-46).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t nan = (u >> 16) | 0x40u;
+  return (u & 0x7fffffffu) > 0x7f800000u ? nan : rne;
+}
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return (f32_to_bf16_bits(lo) & 0xffffu) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// ---- row chunks -------------------------------------------------------------
+// A Chunk<T, VW> is VW consecutive elements of storage type T (float or
+// bf16 bits in uint16_t). VW = 16 / sizeof(T) is one 128-bit global load or
+// store (global_load_dwordx4); VW = 1 is the scalar path for rows whose width
+// or base address does not allow 16-byte chunks.
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <class T, int VW>
+struct Chunk;
+
+template <>
+struct Chunk<float, 4> {
+  u32x4 raw;
+  __device__ __forceinline__ void load(const float* p) { raw = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ void store(float* p) const { *reinterpret_cast<u32x4*>(p) = raw; }
+  __device__ __forceinline__ void widen(float (&v)[4]) const {
+    v[0] = __uint_as_float(raw.x);
+    v[1] = __uint_as_float(raw.y);
+    v[2] = __uint_as_float(raw.z);
+    v[3] = __uint_as_float(raw.w);
+  }
+  __device__ __forceinline__ void narrow(const float (&v)[4]) {
+    raw = u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  }
+  __device__ __forceinline__ void clear() { raw = u32x4{0u, 0u, 0u, 0u}; }
+};
+
+template <>
+struct Chunk<uint16_t, 8> {
+  u32x4 raw;
+  __device__ __forceinline__ void load(const uint16_t* p) { raw = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ void store(uint16_t* p) const { *reinterpret_cast<u32x4*>(p) = raw; }
+  __device__ __forceinline__ void widen(float (&v)[8]) const {
+    v[0] = bf16_lo(raw.x);
+    v[1] = bf16_hi(raw.x);
+    v[2] = bf16_lo(raw.y);
+    v[3] = bf16_hi(raw.y);
+    v[4] = bf16_lo(raw.z);
+    v[5] = bf16_hi(raw.z);
+    v[6] = bf16_lo(raw.w);
+    v[7] = bf16_hi(raw.w);
+  }
+  __device__ __forceinline__ void narrow(const float (&v)[8]) {
+    raw = u32x4{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
+  }
+  __device__ __forceinline__ void clear() { raw = u32x4{0u, 0u, 0u, 0u}; }
+};
+
+template <>
+struct Chunk<float, 1> {
+  float raw;
+  __device__ __forceinline__ void load(const float* p) { raw = *p; }
+  __device__ __forceinline__ void store(float* p) const { *p = raw; }
+  __device__ __forceinline__ void widen(float (&v)[1]) const { v[0] = raw; }
+  __device__ __forceinline__ void narrow(const float (&v)[1]) { raw = v[0]; }
+  __device__ __forceinline__ void clear() { raw = 0.0f; }
+};
+
+template <>
+struct Chunk<uint16_t, 1> {
+  uint16_t raw;
+  __device__ __forceinline__ void load(const uint16_t* p) { raw = *p; }
+  __device__ __forceinline__ void store(uint16_t* p) const { *p = raw; }
+  __device__ __forceinline__ void widen(float (&v)[1]) const { v[0] = bf16_to_f32(raw); }
+  __device__ __forceinline__ void narrow(const float (&v)[1]) {
+    raw = static_cast<uint16_t>(f32_to_bf16_bits(v[0]));
+  }
+  __device__ __forceinline__ void clear() { raw = 0; }
+};
+
+// VW fp32 values (norm weights, cos/sin tables) in 128-bit pieces when VW is
+// a multiple of 4; `p` must then be 16-byte aligned.
+template <int VW>
+__device__ __forceinline__ void load_f32(const float* p, float (&v)[VW]) {
+  if constexpr (VW % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < VW / 4; ++q) {
+      const u32x4 r = *reinterpret_cast<const u32x4*>(p + 4 * q);
+      v[4 * q + 0] = __uint_as_float(r.x);
+      v[4 * q + 1] = __uint_as_float(r.y);
+      v[4 * q + 2] = __uint_as_float(r.z);
+      v[4 * q + 3] = __uint_as_float(r.w);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < VW; ++e) v[e] = p[e];
+  }
+}
+
+// Elements per 128-bit chunk for a storage type.
+template <class T>
+constexpr int kVec = 16 / static_cast<int>(sizeof(T));
+
+// ---- wave64 reductions ------------------------------------------------------
+// A butterfly over DPP lane permutations inside each 16-lane row, then the
+// four row totals read through readlane (SGPRs). Every lane of the wave must
+// be active. The result is wave-uniform and has the same bits in every lane;
+// its summation order is fixed, so a row's result never depends on which
+// wave or launch computed it.
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]: partner lane ^ 1
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]: partner lane ^ 2
+  v += dpp_f32<0x141>(v);  // row_half_mirror: the two quads of each 8 lanes
+  v += dpp_f32<0x140>(v);  // row_mirror: the two halves of each 16-lane row
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Sum over the kBlock threads of a workgroup; `lds` holds kWavesPerBlock
+// floats. Every thread of the block must call it.
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+  v = wave_sum(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) lds[threadIdx.x / kWave] = v;
+  __syncthreads();
+  const float total = (lds[0] + lds[1]) + (lds[2] + lds[3]);
+  __syncthreads();
+  return total;
+}
+
+// ---- host side ----------------------------------------------------------------
+
+// Records "<what>: <detail>" as this thread's last error and returns `status`.
+int fail(int status, const char* what, const std::string& detail);
+// UOCR_ROCM_OK, or UOCR_ROCM_RUNTIME_ERROR with the HIP error string.
+int check_hip(hipError_t err, const char* what);
+// Reports a failed launch through hipGetLastError.
+int check_launch(const char* what);
+// Clears a stale launch error left by earlier work on this thread.
+inline void clear_launch_error() { (void)hipGetLastError(); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+inline unsigned blocks_for_rows(int64_t rows) {
+  return static_cast<unsigned>((rows + kWavesPerBlock - 1) / kWavesPerBlock);
+}
+
+}  // namespace uocr_rocm
+
+#define UOCR_REQUIRE(cond, what, detail)                                  \
+  do {                                                                    \
+    if (!(cond)) return ::uocr_rocm::fail(UOCR_ROCM_INVALID_ARGUMENT, what, detail); \
+  } while (0)

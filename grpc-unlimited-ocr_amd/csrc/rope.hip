@@ -1,0 +1,252 @@
+// rope.hip: rotate-half rotary position embedding, in place, for gfx950;
+// fp32 and bf16 activations, fp32 arithmetic.
+//
+// Layout: X0 [rows, heads0 * dim] and X1 [rows, heads1 * dim] row-major (Q
+// and K of one attention layer; X1 may be absent). One wave64 owns one row
+// (token):
+//   1. The lanes compute the row's dim/2 (cos, sin) pairs, one sincosf per
+//      pair per row rather than per (row, head), into the wave's slice of
+//      LDS.
+//   2. The row's (heads0 + heads1) * dim / (2 VW) chunk pairs are spread
+//      over the lanes: chunk pair (head h, j) is elements [j VW, (j+1) VW) of
+//      the first half of head h and the same span of its second half. A lane
+//      loads both 128-bit chunks, reads its VW cos/sin values from LDS,
+//      rotates, and stores both chunks back, so Q/K make one HBM round trip.
+//      Up to ITERS chunk pairs per lane are loaded before any is rotated.
+//
+// Arithmetic (reference: src/model/page_rope.cpp:26-56 and the
+// uocr::cuda::rope coordinate rule, src/backend/cuda/ops.cu:134-151):
+//   angle = float(tok) * inv_tok[p]              for p <  n_tok
+//   angle = float(page mod page_mod) * inv_page[p - n_tok]   otherwise
+//   c, s = cos(angle), sin(angle) in fp32 (device sincosf)
+//   v[p] = a c - b s,  v[p + half] = b c + a s     (no FMA contraction)
+
+#include "common.hpp"
+
+namespace uocr_rocm {
+namespace {
+
+constexpr int kMaxHalf = 256;  // dim <= 512
+
+template <class T>
+struct RopeArgs {
+  T* x0;
+  T* x1;
+  int heads0;
+  int heads1;
+  int64_t rows;
+  int dim;
+  int half;
+  const int64_t* tok;
+  const int64_t* page;
+  const float* inv_tok;
+  int n_tok;
+  const float* inv_page;
+  int64_t page_mod;
+  int64_t one_tok;
+  int64_t one_page;
+  const uocr_rocm_step_state* state;
+};
+
+template <class T, int VW, int ITERS>
+__global__ __launch_bounds__(kBlock) void rope_rows(RopeArgs<T> a) {
+  __shared__ __attribute__((aligned(16))) float table[kWavesPerBlock][2][kMaxHalf];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
+  const bool active = row < a.rows;
+  float* cosv = table[wave][0];
+  float* sinv = table[wave][1];
+
+  if (active) {
+    int64_t tk, pg;
+    if (a.state != nullptr) {
+      tk = a.state->tok;
+      pg = a.state->page;
+    } else {
+      tk = a.tok != nullptr ? a.tok[row] : a.one_tok;
+      pg = a.page != nullptr ? a.page[row] : a.one_page;
+    }
+    if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
+    const float ft = static_cast<float>(tk);
+    const float fp = static_cast<float>(pg);
+    for (int p = lane; p < a.half; p += kWave) {
+      const float angle = p < a.n_tok ? ft * a.inv_tok[p] : fp * a.inv_page[p - a.n_tok];
+      float sn, cs;
+      sincosf(angle, &sn, &cs);
+      cosv[p] = cs;
+      sinv[p] = sn;
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+
+  const int cpp = a.half / VW;  // chunk pairs per head
+  const int total = (a.heads0 + a.heads1) * cpp;
+  for (int base = 0; base < total; base += kWave * ITERS) {
+    Chunk<T, VW> lo[ITERS], hi[ITERS];
+    T* at[ITERS];
+    int jj[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int c = base + lane + it * kWave;
+      at[it] = nullptr;
+      if (c < total) {
+        const int h = c / cpp;
+        const int j = c - h * cpp;
+        T* head = h < a.heads0 ? a.x0 + (row * a.heads0 + h) * a.dim
+                               : a.x1 + (row * a.heads1 + (h - a.heads0)) * a.dim;
+        at[it] = head + j * VW;
+        jj[it] = j;
+        lo[it].load(at[it]);
+        hi[it].load(at[it] + a.half);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      if (at[it] != nullptr) {
+        float va[VW], vb[VW], cs[VW], sn[VW];
+        lo[it].widen(va);
+        hi[it].widen(vb);
+        load_f32<VW>(cosv + jj[it] * VW, cs);
+        load_f32<VW>(sinv + jj[it] * VW, sn);
+        float ra[VW], rb[VW];
+        {
+#pragma clang fp contract(off)
+#pragma unroll
+          for (int e = 0; e < VW; ++e) {
+            ra[e] = va[e] * cs[e] - vb[e] * sn[e];
+            rb[e] = vb[e] * cs[e] + va[e] * sn[e];
+          }
+        }
+        lo[it].narrow(ra);
+        hi[it].narrow(rb);
+        lo[it].store(at[it]);
+        hi[it].store(at[it] + a.half);
+      }
+    }
+  }
+}
+
+template <class T, int VW>
+void launch_rope_vw(const RopeArgs<T>& a, int iters, hipStream_t s) {
+  const unsigned blocks = blocks_for_rows(a.rows);
+  switch (iters) {
+    case 1: rope_rows<T, VW, 1><<<blocks, kBlock, 0, s>>>(a); break;
+    case 2: rope_rows<T, VW, 2><<<blocks, kBlock, 0, s>>>(a); break;
+    case 3: rope_rows<T, VW, 3><<<blocks, kBlock, 0, s>>>(a); break;
+    default: rope_rows<T, VW, 4><<<blocks, kBlock, 0, s>>>(a); break;
+  }
+}
+
+template <class T>
+int launch_rope(const char* what, void* stream, T* x0, int64_t heads0, T* x1, int64_t heads1, int64_t rows,
+                int64_t dim, const int64_t* tok, const int64_t* page, const float* inv_tok, int64_t n_tok,
+                const float* inv_page, int64_t n_page, int64_t page_mod, int64_t one_tok, int64_t one_page,
+                const uocr_rocm_step_state* state) {
+  UOCR_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), what, "rows must be in [0, 2^31)");
+  UOCR_REQUIRE(heads0 >= 0 && heads1 >= 0, what, "heads must be >= 0");
+  UOCR_REQUIRE(dim > 0 && dim % 2 == 0 && dim / 2 <= kMaxHalf, what, "dim must be even and in [2, 512]");
+  UOCR_REQUIRE(n_tok >= 0 && n_page >= 0 && n_tok + n_page == dim / 2, what, "n_tok + n_page must equal dim / 2");
+  UOCR_REQUIRE((heads0 + heads1) * (dim / 2) < (int64_t{1} << 30), what, "heads * dim too large");
+  if (rows == 0 || heads0 + heads1 == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(heads0 == 0 || x0 != nullptr, what, "null x");
+  UOCR_REQUIRE(heads1 == 0 || x1 != nullptr, what, "null k");
+  UOCR_REQUIRE(n_tok == 0 || inv_tok != nullptr, what, "null inv_tok");
+  UOCR_REQUIRE(n_page == 0 || inv_page != nullptr, what, "null inv_page");
+  UOCR_REQUIRE(heads0 == 0 || heads1 == 0 || x0 != x1, what, "q and k must be distinct buffers");
+
+  RopeArgs<T> a{};
+  a.x0 = heads0 > 0 ? x0 : x1;
+  a.heads0 = static_cast<int>(heads0 > 0 ? heads0 : heads1);
+  a.x1 = heads0 > 0 ? x1 : nullptr;
+  a.heads1 = static_cast<int>(heads0 > 0 ? heads1 : 0);
+  a.rows = rows;
+  a.dim = static_cast<int>(dim);
+  a.half = static_cast<int>(dim / 2);
+  a.tok = tok;
+  a.page = page;
+  a.inv_tok = inv_tok;
+  a.n_tok = static_cast<int>(n_tok);
+  a.inv_page = inv_page;
+  a.page_mod = page_mod;
+  a.one_tok = one_tok;
+  a.one_page = one_page;
+  a.state = state;
+
+  constexpr int kV = kVec<T>;
+  // 16-byte chunks need every head half to start on a 16-byte boundary.
+  const bool vec = a.half % kV == 0 && aligned16(a.x0) && (a.x1 == nullptr || aligned16(a.x1));
+  const int vw = vec ? kV : 1;
+  const int64_t total = static_cast<int64_t>(a.heads0 + a.heads1) * (a.half / vw);
+  int64_t iters = (total + kWave - 1) / kWave;
+  if (iters > 4) iters = 4;
+  clear_launch_error();
+  if (vec) {
+    launch_rope_vw<T, kV>(a, static_cast<int>(iters), as_stream(stream));
+  } else {
+    launch_rope_vw<T, 1>(a, static_cast<int>(iters), as_stream(stream));
+  }
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace uocr_rocm
+
+using namespace uocr_rocm;
+
+extern "C" {
+
+int uocr_rocm_rope(void* stream, float* x, int64_t rows, int64_t heads, int64_t dim, const int64_t* tok,
+                   const int64_t* page, const float* inv_tok, int64_t n_tok, const float* inv_page, int64_t n_page,
+                   int64_t page_mod, int64_t one_tok, int64_t one_page) {
+  return launch_rope<float>("uocr_rocm_rope", stream, x, heads, nullptr, 0, rows, dim, tok, page, inv_tok, n_tok,
+                            inv_page, n_page, page_mod, one_tok, one_page, nullptr);
+}
+
+int uocr_rocm_rope_bf16(void* stream, uint16_t* x, int64_t rows, int64_t heads, int64_t dim, const int64_t* tok,
+                        const int64_t* page, const float* inv_tok, int64_t n_tok, const float* inv_page,
+                        int64_t n_page, int64_t page_mod, int64_t one_tok, int64_t one_page) {
+  return launch_rope<uint16_t>("uocr_rocm_rope_bf16", stream, x, heads, nullptr, 0, rows, dim, tok, page, inv_tok,
+                               n_tok, inv_page, n_page, page_mod, one_tok, one_page, nullptr);
+}
+
+int uocr_rocm_rope_qk(void* stream, float* q, int64_t q_heads, float* k, int64_t k_heads, int64_t rows, int64_t dim,
+                      const int64_t* tok, const int64_t* page, const float* inv_tok, int64_t n_tok,
+                      const float* inv_page, int64_t n_page, int64_t page_mod, int64_t one_tok, int64_t one_page) {
+  return launch_rope<float>("uocr_rocm_rope_qk", stream, q, q_heads, k, k_heads, rows, dim, tok, page, inv_tok, n_tok,
+                            inv_page, n_page, page_mod, one_tok, one_page, nullptr);
+}
+
+int uocr_rocm_rope_qk_bf16(void* stream, uint16_t* q, int64_t q_heads, uint16_t* k, int64_t k_heads, int64_t rows,
+                           int64_t dim, const int64_t* tok, const int64_t* page, const float* inv_tok, int64_t n_tok,
+                           const float* inv_page, int64_t n_page, int64_t page_mod, int64_t one_tok,
+                           int64_t one_page) {
+  return launch_rope<uint16_t>("uocr_rocm_rope_qk_bf16", stream, q, q_heads, k, k_heads, rows, dim, tok, page,
+                               inv_tok, n_tok, inv_page, n_page, page_mod, one_tok, one_page, nullptr);
+}
+
+int uocr_rocm_rope_step(void* stream, float* x, int64_t heads, int64_t dim, const uocr_rocm_step_state* state,
+                        const float* inv_tok, int64_t n_tok, const float* inv_page, int64_t page_mod) {
+  UOCR_REQUIRE(state != nullptr, "uocr_rocm_rope_step", "null state");
+  return launch_rope<float>("uocr_rocm_rope_step", stream, x, heads, nullptr, 0, 1, dim, nullptr, nullptr, inv_tok,
+                            n_tok, inv_page, dim / 2 - n_tok, page_mod, 0, 0, state);
+}
+
+int uocr_rocm_rope_qk_step(void* stream, float* q, int64_t q_heads, float* k, int64_t k_heads, int64_t dim,
+                           const uocr_rocm_step_state* state, const float* inv_tok, int64_t n_tok,
+                           const float* inv_page, int64_t page_mod) {
+  UOCR_REQUIRE(state != nullptr, "uocr_rocm_rope_qk_step", "null state");
+  return launch_rope<float>("uocr_rocm_rope_qk_step", stream, q, q_heads, k, k_heads, 1, dim, nullptr, nullptr,
+                            inv_tok, n_tok, inv_page, dim / 2 - n_tok, page_mod, 0, 0, state);
+}
+
+int uocr_rocm_rope_qk_step_bf16(void* stream, uint16_t* q, int64_t q_heads, uint16_t* k, int64_t k_heads,
+                                int64_t dim, const uocr_rocm_step_state* state, const float* inv_tok, int64_t n_tok,
+                                const float* inv_page, int64_t page_mod) {
+  UOCR_REQUIRE(state != nullptr, "uocr_rocm_rope_qk_step_bf16", "null state");
+  return launch_rope<uint16_t>("uocr_rocm_rope_qk_step_bf16", stream, q, q_heads, k, k_heads, 1, dim, nullptr,
+                               nullptr, inv_tok, n_tok, inv_page, dim / 2 - n_tok, page_mod, 0, 0, state);
+}
+
+}  // extern "C"

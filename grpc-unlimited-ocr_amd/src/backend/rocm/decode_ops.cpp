@@ -1,0 +1,50 @@
+#include "backend/rocm/decode_ops.h"
+
+#include <cstddef>
+
+#include "uocr_rocm.h"
+
+namespace uocr::rocm {
+namespace {
+
+// The C ABI reads the same five int64 fields in the same order.
+static_assert(sizeof(StepState) == sizeof(uocr_rocm_step_state));
+static_assert(offsetof(StepState, token) == offsetof(uocr_rocm_step_state, token));
+static_assert(offsetof(StepState, pos) == offsetof(uocr_rocm_step_state, pos));
+static_assert(offsetof(StepState, tok) == offsetof(uocr_rocm_step_state, tok));
+static_assert(offsetof(StepState, page) == offsetof(uocr_rocm_step_state, page));
+static_assert(offsetof(StepState, query_page) == offsetof(uocr_rocm_step_state, query_page));
+
+const uocr_rocm_step_state* abi(const StepState* s) { return reinterpret_cast<const uocr_rocm_step_state*>(s); }
+
+}  // namespace
+
+void embed_step(const Context& ctx, const std::uint16_t* table, const StepState* state, std::int64_t cols, float* dst) {
+  check(uocr_rocm_embed_step(ctx.stream(), table, -1, abi(state), cols, dst));
+}
+
+void rope_step(const Context& ctx, float* x, std::int64_t heads, std::int64_t dim, const StepState* state,
+               const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t page_mod) {
+  check(uocr_rocm_rope_step(ctx.stream(), x, heads, dim, abi(state), inv_tok, n_tok, inv_page, page_mod));
+}
+
+void rope_qk_step(const Context& ctx, float* q, std::int64_t q_heads, float* k, std::int64_t k_heads, std::int64_t dim,
+                  const StepState* state, const float* inv_tok, std::int64_t n_tok, const float* inv_page,
+                  std::int64_t page_mod) {
+  check(uocr_rocm_rope_qk_step(ctx.stream(), q, q_heads, k, k_heads, dim, abi(state), inv_tok, n_tok, inv_page,
+                               page_mod));
+}
+
+void rope_qk_step_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_heads, std::uint16_t* k,
+                       std::int64_t k_heads, std::int64_t dim, const StepState* state, const float* inv_tok,
+                       std::int64_t n_tok, const float* inv_page, std::int64_t page_mod) {
+  check(uocr_rocm_rope_qk_step_bf16(ctx.stream(), q, q_heads, k, k_heads, dim, abi(state), inv_tok, n_tok, inv_page,
+                                    page_mod));
+}
+
+void embed_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows, const StepState* state,
+                     std::int64_t cols, std::uint16_t* dst) {
+  check(uocr_rocm_embed_step_bf16(ctx.stream(), table, table_rows, abi(state), cols, dst));
+}
+
+}  // namespace uocr::rocm

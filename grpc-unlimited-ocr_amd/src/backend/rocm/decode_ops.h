@@ -1,0 +1,38 @@
+#pragma once
+
+// Ops for one decode step whose shapes do not depend on how many tokens came
+// before: the fed token and its rope coordinate are read from a StepState on
+// the device, so a captured step replays for every token with only the
+// StepState rewritten between replays. Same contract as the reference's
+// src/backend/cuda/decode_ops.h:17-27.
+
+#include <cstdint>
+
+#include "backend/rocm/context.h"
+#include "backend/rocm/ops.h"
+
+namespace uocr::rocm {
+
+struct StepState {
+  std::int64_t token;       // the token being fed
+  std::int64_t pos;         // its position; keys = pos + 1 after the append
+  std::int64_t tok;         // rope token coordinate
+  std::int64_t page;        // rope page coordinate
+  std::int64_t query_page;  // response page for routing, -1 = unrestricted
+};
+
+void embed_step(const Context& ctx, const std::uint16_t* table, const StepState* state, std::int64_t cols, float* dst);
+void rope_step(const Context& ctx, float* x, std::int64_t heads, std::int64_t dim, const StepState* state,
+               const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t page_mod);
+
+// New: Q and K of the step row in one launch, and the bf16-activation forms.
+void rope_qk_step(const Context& ctx, float* q, std::int64_t q_heads, float* k, std::int64_t k_heads, std::int64_t dim,
+                  const StepState* state, const float* inv_tok, std::int64_t n_tok, const float* inv_page,
+                  std::int64_t page_mod);
+void rope_qk_step_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_heads, std::uint16_t* k,
+                       std::int64_t k_heads, std::int64_t dim, const StepState* state, const float* inv_tok,
+                       std::int64_t n_tok, const float* inv_page, std::int64_t page_mod);
+void embed_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows, const StepState* state,
+                     std::int64_t cols, std::uint16_t* dst);
+
+}  // namespace uocr::rocm

@@ -1,0 +1,114 @@
+#include "backend/rocm/ops.h"
+
+#include "uocr_rocm.h"
+
+namespace uocr::rocm {
+
+void add_inplace(const Context& ctx, float* y, const float* x, std::int64_t n) {
+  check(uocr_rocm_add_inplace(ctx.stream(), y, x, n));
+}
+
+void layer_norm(const Context& ctx, float* x, const float* w, const float* b, std::int64_t rows, std::int64_t cols,
+                float eps) {
+  check(uocr_rocm_layer_norm(ctx.stream(), x, w, b, rows, cols, eps));
+}
+
+void rms_norm(const Context& ctx, float* x, const float* w, std::int64_t rows, std::int64_t cols, float eps) {
+  check(uocr_rocm_rms_norm(ctx.stream(), x, w, rows, cols, eps));
+}
+
+void gelu_erf(const Context& ctx, float* x, std::int64_t n) { check(uocr_rocm_gelu_erf(ctx.stream(), x, n)); }
+
+void silu_mul(const Context& ctx, float* g, const float* u, std::int64_t n) {
+  check(uocr_rocm_silu_mul(ctx.stream(), g, u, n));
+}
+
+void rope(const Context& ctx, float* x, std::int64_t rows, std::int64_t heads, std::int64_t dim, const std::int64_t* tok,
+          const std::int64_t* page, const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t n_page,
+          std::int64_t page_mod, std::int64_t one_tok, std::int64_t one_page) {
+  check(uocr_rocm_rope(ctx.stream(), x, rows, heads, dim, tok, page, inv_tok, n_tok, inv_page, n_page, page_mod,
+                       one_tok, one_page));
+}
+
+void copy(const Context& ctx, float* dst, const float* src, std::int64_t n) {
+  check(uocr_rocm_copy(ctx.stream(), dst, src, n));
+}
+
+void gather_rows_bf16(const Context& ctx, const std::uint16_t* table, const std::int64_t* index, std::int64_t rows,
+                      std::int64_t cols, float* dst) {
+  check(uocr_rocm_gather_rows_bf16(ctx.stream(), table, -1, index, rows, cols, dst));
+}
+
+void gather_row_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t one_index, std::int64_t cols,
+                     float* dst) {
+  check(uocr_rocm_gather_row_bf16(ctx.stream(), table, -1, one_index, cols, dst));
+}
+
+void gather_rows_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows, const std::int64_t* index,
+                      std::int64_t rows, std::int64_t cols, float* dst) {
+  check(uocr_rocm_gather_rows_bf16(ctx.stream(), table, table_rows, index, rows, cols, dst));
+}
+
+void add_rms_norm(const Context& ctx, float* x, const float* delta, const float* w, float* h, std::int64_t rows,
+                  std::int64_t cols, float eps) {
+  check(uocr_rocm_add_rms_norm(ctx.stream(), x, delta, w, h, rows, cols, eps));
+}
+
+void swiglu(const Context& ctx, const float* in, float* out, std::int64_t rows, std::int64_t ffn) {
+  check(uocr_rocm_swiglu(ctx.stream(), in, out, rows, ffn));
+}
+
+void rope_qk(const Context& ctx, float* q, std::int64_t q_heads, float* k, std::int64_t k_heads, std::int64_t rows,
+             std::int64_t dim, const std::int64_t* tok, const std::int64_t* page, const float* inv_tok,
+             std::int64_t n_tok, const float* inv_page, std::int64_t n_page, std::int64_t page_mod,
+             std::int64_t one_tok, std::int64_t one_page) {
+  check(uocr_rocm_rope_qk(ctx.stream(), q, q_heads, k, k_heads, rows, dim, tok, page, inv_tok, n_tok, inv_page, n_page,
+                          page_mod, one_tok, one_page));
+}
+
+void rms_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std::int64_t rows, std::int64_t cols,
+                   float eps) {
+  check(uocr_rocm_rms_norm_bf16(ctx.stream(), x, w, rows, cols, eps));
+}
+
+void add_rms_norm_bf16(const Context& ctx, std::uint16_t* x, const std::uint16_t* delta, const float* w,
+                       std::uint16_t* h, std::int64_t rows, std::int64_t cols, float eps) {
+  check(uocr_rocm_add_rms_norm_bf16(ctx.stream(), x, delta, w, h, rows, cols, eps));
+}
+
+void layer_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, const float* b, std::int64_t rows,
+                     std::int64_t cols, float eps) {
+  check(uocr_rocm_layer_norm_bf16(ctx.stream(), x, w, b, rows, cols, eps));
+}
+
+void gelu_erf_bf16(const Context& ctx, std::uint16_t* x, std::int64_t n) {
+  check(uocr_rocm_gelu_erf_bf16(ctx.stream(), x, n));
+}
+
+void swiglu_bf16(const Context& ctx, const std::uint16_t* in, std::uint16_t* out, std::int64_t rows,
+                 std::int64_t ffn) {
+  check(uocr_rocm_swiglu_bf16(ctx.stream(), in, out, rows, ffn));
+}
+
+void rope_bf16(const Context& ctx, std::uint16_t* x, std::int64_t rows, std::int64_t heads, std::int64_t dim,
+               const std::int64_t* tok, const std::int64_t* page, const float* inv_tok, std::int64_t n_tok,
+               const float* inv_page, std::int64_t n_page, std::int64_t page_mod, std::int64_t one_tok,
+               std::int64_t one_page) {
+  check(uocr_rocm_rope_bf16(ctx.stream(), x, rows, heads, dim, tok, page, inv_tok, n_tok, inv_page, n_page, page_mod,
+                            one_tok, one_page));
+}
+
+void rope_qk_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_heads, std::uint16_t* k, std::int64_t k_heads,
+                  std::int64_t rows, std::int64_t dim, const std::int64_t* tok, const std::int64_t* page,
+                  const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t n_page,
+                  std::int64_t page_mod, std::int64_t one_tok, std::int64_t one_page) {
+  check(uocr_rocm_rope_qk_bf16(ctx.stream(), q, q_heads, k, k_heads, rows, dim, tok, page, inv_tok, n_tok, inv_page,
+                               n_page, page_mod, one_tok, one_page));
+}
+
+void gather_rows_bf16_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
+                           const std::int64_t* index, std::int64_t rows, std::int64_t cols, std::uint16_t* dst) {
+  check(uocr_rocm_gather_rows_bf16_bf16(ctx.stream(), table, table_rows, index, rows, cols, dst));
+}
+
+}  // namespace uocr::rocm

@@ -1,0 +1,90 @@
+#pragma once
+
+// The rocm backend's fused layer ops, over raw device pointers so callers
+// can address slices. Every op is enqueued on the context's stream; none
+// synchronises and none allocates, so every op can be captured in a graph.
+// Shapes are row-major, as in the reference backend.
+//
+// The fp32 entry points keep the names and argument order of the reference's
+// uocr::cuda ops (src/backend/cuda/ops.h:30-75), so a model/rocm decoder can
+// mirror model/cuda line for line. The fused ops and the bf16-activation
+// variants are new; each bf16 op computes in fp32 on the widened inputs and
+// rounds once on store (nearest even), so it reduces to its fp32 op.
+// Norm weights and biases are fp32 throughout.
+//
+// Bad shapes throw std::invalid_argument before anything is enqueued;
+// runtime and launch failures throw std::runtime_error("<what>: <detail>").
+
+#include <cstdint>
+
+#include "backend/rocm/context.h"
+
+namespace uocr::rocm {
+
+// ---- reference signatures (fp32 activations, bf16 tables) ------------------
+
+void add_inplace(const Context& ctx, float* y, const float* x, std::int64_t n);  // y += x
+void layer_norm(const Context& ctx, float* x, const float* w, const float* b, std::int64_t rows, std::int64_t cols,
+                float eps);
+void rms_norm(const Context& ctx, float* x, const float* w, std::int64_t rows, std::int64_t cols, float eps);
+void gelu_erf(const Context& ctx, float* x, std::int64_t n);
+void silu_mul(const Context& ctx, float* g, const float* u, std::int64_t n);  // g = silu(g) * u
+
+// Two-axis rope on x [rows, heads * dim], one (tok, page) per row; with
+// null tok/page arrays the single row uses `one_tok` / `one_page`.
+void rope(const Context& ctx, float* x, std::int64_t rows, std::int64_t heads, std::int64_t dim, const std::int64_t* tok,
+          const std::int64_t* page, const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t n_page,
+          std::int64_t page_mod, std::int64_t one_tok = 0, std::int64_t one_page = 0);
+
+// dst = src for n elements (device to device).
+void copy(const Context& ctx, float* dst, const float* src, std::int64_t n);
+
+// bf16 table rows -> fp32 rows (token embeddings); one_index serves a single
+// row without an index array. The table's row count is unknown here, so the
+// indices are trusted as in the reference; the overloads taking table_rows
+// turn an out-of-range device index into a zero row instead.
+void gather_rows_bf16(const Context& ctx, const std::uint16_t* table, const std::int64_t* index, std::int64_t rows,
+                      std::int64_t cols, float* dst);
+void gather_row_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t one_index, std::int64_t cols,
+                     float* dst);
+void gather_rows_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows, const std::int64_t* index,
+                      std::int64_t rows, std::int64_t cols, float* dst);
+
+// ---- fused ops ----------------------------------------------------------------
+
+// Residual add fused with RMSNorm, per row: s = x + delta; x = s;
+// h = w * (s * inv(s)). Replaces add_inplace + copy + rms_norm.
+void add_rms_norm(const Context& ctx, float* x, const float* delta, const float* w, float* h, std::int64_t rows,
+                  std::int64_t cols, float eps);
+// SwiGLU over in [rows, 2 * ffn] laid out [gate | up] per row: out [rows, ffn].
+void swiglu(const Context& ctx, const float* in, float* out, std::int64_t rows, std::int64_t ffn);
+// rope on Q [rows, q_heads * dim] and K [rows, k_heads * dim] in one launch.
+void rope_qk(const Context& ctx, float* q, std::int64_t q_heads, float* k, std::int64_t k_heads, std::int64_t rows,
+             std::int64_t dim, const std::int64_t* tok, const std::int64_t* page, const float* inv_tok,
+             std::int64_t n_tok, const float* inv_page, std::int64_t n_page, std::int64_t page_mod,
+             std::int64_t one_tok = 0, std::int64_t one_page = 0);
+
+// ---- bf16 activations ------------------------------------------------------------
+
+void rms_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std::int64_t rows, std::int64_t cols,
+                   float eps);
+void add_rms_norm_bf16(const Context& ctx, std::uint16_t* x, const std::uint16_t* delta, const float* w,
+                       std::uint16_t* h, std::int64_t rows, std::int64_t cols, float eps);
+void layer_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, const float* b, std::int64_t rows,
+                     std::int64_t cols, float eps);
+void gelu_erf_bf16(const Context& ctx, std::uint16_t* x, std::int64_t n);
+void swiglu_bf16(const Context& ctx, const std::uint16_t* in, std::uint16_t* out, std::int64_t rows,
+                 std::int64_t ffn);
+void rope_bf16(const Context& ctx, std::uint16_t* x, std::int64_t rows, std::int64_t heads, std::int64_t dim,
+               const std::int64_t* tok, const std::int64_t* page, const float* inv_tok, std::int64_t n_tok,
+               const float* inv_page, std::int64_t n_page, std::int64_t page_mod, std::int64_t one_tok = 0,
+               std::int64_t one_page = 0);
+void rope_qk_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_heads, std::uint16_t* k, std::int64_t k_heads,
+                  std::int64_t rows, std::int64_t dim, const std::int64_t* tok, const std::int64_t* page,
+                  const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t n_page,
+                  std::int64_t page_mod, std::int64_t one_tok = 0, std::int64_t one_page = 0);
+// Embedding rows kept in bf16 (a bit copy).
+void gather_rows_bf16_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
+                           const std::int64_t* index, std::int64_t rows, std::int64_t cols, std::uint16_t* dst);
+
+}  // namespace uocr::rocm

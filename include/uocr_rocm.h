@@ -1,0 +1,261 @@
+/*
+ * uocr_rocm.h: the C ABI of the MI355X (gfx950) `rocm` backend for
+ * grpc-unlimited-ocr's fused layer ops.
+ *
+ * Plain C: raw device pointers, explicit int64 shapes, row-major layouts, an
+ * opaque stream handle, and an int status instead of exceptions. The C++23
+ * layer in src/backend/rocm/ (namespace uocr::rocm) wraps these calls with the
+ * same free-function shapes as the reference's uocr::cuda backend and turns a
+ * non-zero status into the reference's exception types.
+ *
+ * Conventions shared by every entry point:
+ *   - `stream` is a hipStream_t (from uocr_rocm_stream_create, or any stream
+ *     the caller owns on the current device). Ops are enqueued on it in order;
+ *     none synchronises and none allocates, so every op can be recorded into a
+ *     graph between uocr_rocm_capture_begin and uocr_rocm_capture_end.
+ *   - bf16 is IEEE binary32's top half stored as uint16_t; every conversion
+ *     from fp32 rounds to nearest even and keeps NaN quiet (bits>>16 | 0x40),
+ *     as the reference's f32_to_bf16 does (src/tensor/dtype.h:39-46).
+ *   - fp32 ops compute in fp32. bf16 ops widen to fp32, compute in fp32 and
+ *     round once on store. Norm weights (gamma, beta) are fp32 in both cases,
+ *     as the reference stores them (src/model/cuda/device_params.h:35-37).
+ *   - Shapes are validated before anything is enqueued. A bad shape, a null
+ *     pointer with a non-empty shape, a misaligned pointer that the op needs
+ *     aligned, or an unsupported size returns UOCR_ROCM_INVALID_ARGUMENT and
+ *     enqueues nothing, where the reference throws std::invalid_argument
+ *     (src/backend/cuda/decode_ops.cu:239, ops.cu:569,655). Empty shapes
+ *     (rows == 0 or n == 0) are valid no-ops.
+ *   - uocr_rocm_last_error() returns this thread's message for the last
+ *     failing call ("<what>: <detail>"), the shape of the reference's check()
+ *     messages (src/backend/cuda/context.cu:24-28).
+ */
+#ifndef UOCR_ROCM_H_
+#define UOCR_ROCM_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define UOCR_ROCM_API __attribute__((visibility("default")))
+#else
+#define UOCR_ROCM_API
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+
+enum uocr_rocm_status {
+  UOCR_ROCM_OK = 0,
+  UOCR_ROCM_INVALID_ARGUMENT = 1, /* reference: std::invalid_argument        */
+  UOCR_ROCM_NO_DEVICE = 2,        /* reference: device_count() == 0 (skip 77) */
+  UOCR_ROCM_RUNTIME_ERROR = 3,    /* a HIP runtime call failed               */
+  UOCR_ROCM_LAUNCH_ERROR = 4      /* hipGetLastError() after a launch failed */
+};
+
+/* Static name of a status code. */
+UOCR_ROCM_API const char* uocr_rocm_status_string(int status);
+/* This thread's message for its last failing call ("" if none). */
+UOCR_ROCM_API const char* uocr_rocm_last_error(void);
+/* ABI version, bumped when an entry point changes: (major << 16) | minor. */
+UOCR_ROCM_API int uocr_rocm_abi_version(void);
+
+/* ---- device, stream, memory, graphs ------------------------------------ */
+
+/* Replaces uocr::cuda::device_count (src/backend/cuda/context.h:22-23,
+ * context.cu:36-39): *count = 0 and UOCR_ROCM_OK when no usable device. */
+UOCR_ROCM_API int uocr_rocm_device_count(int* count);
+
+/* Replaces uocr::cuda::device_info (context.h:14-24, context.cu:41-48).
+ * `name` receives at most name_len-1 chars plus NUL; gfx_arch is e.g. 950. */
+UOCR_ROCM_API int uocr_rocm_device_info(int index, char* name, size_t name_len, int* gfx_arch, int* cu_count,
+                                        uint64_t* free_bytes, uint64_t* total_bytes);
+
+/* Replaces Context's stream (context.h:30-49, context.cu:50-53,65-75): a
+ * non-blocking stream at the default priority on `device`. */
+UOCR_ROCM_API int uocr_rocm_stream_create(int device, void** stream);
+UOCR_ROCM_API int uocr_rocm_stream_destroy(void* stream);
+UOCR_ROCM_API int uocr_rocm_stream_synchronize(void* stream);
+
+/* Replaces Context::begin_capture / end_capture and Graph::launch
+ * (context.h:39-63, context.cu:77-102): everything enqueued on `stream`
+ * between the two calls is recorded, instantiated into *graph, and replayed
+ * by uocr_rocm_graph_launch. */
+UOCR_ROCM_API int uocr_rocm_capture_begin(void* stream);
+UOCR_ROCM_API int uocr_rocm_capture_end(void* stream, void** graph);
+UOCR_ROCM_API int uocr_rocm_graph_launch(void* graph, void* stream);
+UOCR_ROCM_API int uocr_rocm_graph_destroy(void* graph);
+
+/* Replaces Array's stream-ordered allocation (context.cu:120-127). */
+UOCR_ROCM_API int uocr_rocm_malloc(void** ptr, size_t bytes, void* stream);
+UOCR_ROCM_API int uocr_rocm_free(void* ptr, void* stream);
+/* Replaces PinnedBuffer (context.h:67-79, context.cu:104-110). */
+UOCR_ROCM_API int uocr_rocm_host_alloc(void** ptr, size_t bytes);
+UOCR_ROCM_API int uocr_rocm_host_free(void* ptr);
+
+/* Stream-ordered copies; neither waits. Replaces copy_to_device /
+ * copy_to_host (context.h:81-83, context.cu:112-118) and, for device to
+ * device, uocr::cuda::copy's memcpy (ops.h:68-69, ops.cu:264-266). */
+enum uocr_rocm_copy_kind { UOCR_ROCM_H2D = 1, UOCR_ROCM_D2H = 2, UOCR_ROCM_D2D = 3 };
+UOCR_ROCM_API int uocr_rocm_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
+
+/* Replaces Array::zero (context.cu:212-216) with a fill kernel rather than a
+ * memset node, so that it replays correctly inside a captured graph. */
+UOCR_ROCM_API int uocr_rocm_zero(void* ptr, size_t bytes, void* stream);
+
+/* Timing events on a stream (for benches; the reference has none). */
+UOCR_ROCM_API int uocr_rocm_event_create(void** event);
+UOCR_ROCM_API int uocr_rocm_event_destroy(void* event);
+UOCR_ROCM_API int uocr_rocm_event_record(void* event, void* stream);
+UOCR_ROCM_API int uocr_rocm_event_elapsed_ms(void* start, void* end, float* ms);
+
+/* ---- the decode step's device state ------------------------------------ */
+
+/* Same layout as uocr::cuda::StepState (src/backend/cuda/decode_ops.h:17-23):
+ * the length-dependent values of one decode step, read on the device so a
+ * captured step replays for every token. */
+typedef struct uocr_rocm_step_state {
+  int64_t token;      /* the token being fed                         */
+  int64_t pos;        /* its position                                */
+  int64_t tok;        /* rope token coordinate                       */
+  int64_t page;       /* rope page coordinate                        */
+  int64_t query_page; /* response page for routing, -1 unrestricted  */
+} uocr_rocm_step_state;
+
+/* ---- fp32 ops: the reference's uocr::cuda signatures ------------------- */
+
+/* y[i] += x[i]. Replaces add_inplace (src/backend/cuda/ops.h:30,
+ * ops.cu:33-36,311-313); CPU form add_into (src/model/decoder.cpp:39-41). */
+UOCR_ROCM_API int uocr_rocm_add_inplace(void* stream, float* y, const float* x, int64_t n);
+
+/* dst = src, n fp32 elements, device to device. Replaces copy (ops.h:68-69). */
+UOCR_ROCM_API int uocr_rocm_copy(void* stream, float* dst, const float* src, int64_t n);
+
+/* In place, per row of x [rows, cols]: x = w * (x * inv),
+ * inv = 1/sqrt(mean(x^2) + eps). Replaces rms_norm (ops.h:34,
+ * ops.cu:39-81,324-326); oracle src/backend/reference/ops.cpp:129-141. */
+UOCR_ROCM_API int uocr_rocm_rms_norm(void* stream, float* x, const float* w, int64_t rows, int64_t cols, float eps);
+
+/* In place, per row: x = ((x - mean) * inv) * w + b, inv = 1/sqrt(var + eps),
+ * with the mean and the variance of the row (two-pass over registers).
+ * Replaces layer_norm (ops.h:32-33, ops.cu:319-322); oracle ops.cpp:111-127. */
+UOCR_ROCM_API int uocr_rocm_layer_norm(void* stream, float* x, const float* w, const float* b, int64_t rows,
+                                       int64_t cols, float eps);
+
+/* In place: x = 0.5 x (1 + erf(x / sqrt 2)). Replaces gelu_erf (ops.h:37,
+ * ops.cu:83-89,332-334); oracle ops.cpp:151-155. */
+UOCR_ROCM_API int uocr_rocm_gelu_erf(void* stream, float* x, int64_t n);
+
+/* g = silu(g) * u = (g * (1 / (1 + exp(-g)))) * u. Replaces silu_mul
+ * (ops.h:39, ops.cu:91-94,340-342); oracle ops.cpp:40,163-167 plus the
+ * multiply of src/model/feed_forward.cpp:18-24. */
+UOCR_ROCM_API int uocr_rocm_silu_mul(void* stream, float* g, const float* u, int64_t n);
+
+/* Two-axis rotate-half rope in place on x [rows, heads * dim], one (tok, page)
+ * coordinate per row; tok/page may be null, then every row uses one_tok /
+ * one_page. Pair p < n_tok turns by float(tok) * inv_tok[p], pair
+ * p >= n_tok by float(page mod page_mod) * inv_page[p - n_tok]; requires
+ * n_tok + n_page == dim / 2, dim even, dim <= 512. Replaces rope (ops.h:48-52,
+ * ops.cu:134-151,354-360); oracle src/model/page_rope.cpp:26-56. The plain
+ * rope of one frequency table is n_tok = dim / 2, n_page = 0. */
+UOCR_ROCM_API int uocr_rocm_rope(void* stream, float* x, int64_t rows, int64_t heads, int64_t dim, const int64_t* tok,
+                                 const int64_t* page, const float* inv_tok, int64_t n_tok, const float* inv_page,
+                                 int64_t n_page, int64_t page_mod, int64_t one_tok, int64_t one_page);
+
+/* dst[r, :] = widen(table[index[r], :]), bit-exact (bf16 -> fp32 is a
+ * 16-bit shift). Replaces gather_rows_bf16 (ops.h:72-73, ops.cu:177-181,
+ * 382-386); oracle Decoder::embed (src/model/decoder.cpp:85-92) over the
+ * table widened at load (src/model/weight_source.cpp:16-23).
+ * table_rows >= 0 bounds-checks every index: an index outside
+ * [0, table_rows) yields a zero row instead of a read past the table.
+ * table_rows < 0 trusts the caller, as the reference does. */
+UOCR_ROCM_API int uocr_rocm_gather_rows_bf16(void* stream, const uint16_t* table, int64_t table_rows,
+                                             const int64_t* index, int64_t rows, int64_t cols, float* dst);
+
+/* One row by a host index. Replaces gather_row_bf16 (ops.h:74-75,
+ * ops.cu:589-592,647-651). */
+UOCR_ROCM_API int uocr_rocm_gather_row_bf16(void* stream, const uint16_t* table, int64_t table_rows,
+                                            int64_t one_index, int64_t cols, float* dst);
+
+/* One row by state->token, read on the device. Replaces embed_step
+ * (src/backend/cuda/decode_ops.h:25, decode_ops.cu:26-29,203-206). */
+UOCR_ROCM_API int uocr_rocm_embed_step(void* stream, const uint16_t* table, int64_t table_rows,
+                                       const uocr_rocm_step_state* state, int64_t cols, float* dst);
+
+/* rope of one row x [heads * dim] at (state->tok, state->page), read on the
+ * device; the page table has dim / 2 - n_tok entries. Replaces rope_step
+ * (decode_ops.h:26-27, decode_ops.cu:31-47,208-212). */
+UOCR_ROCM_API int uocr_rocm_rope_step(void* stream, float* x, int64_t heads, int64_t dim,
+                                      const uocr_rocm_step_state* state, const float* inv_tok, int64_t n_tok,
+                                      const float* inv_page, int64_t page_mod);
+
+/* ---- fused ops (new; no single reference counterpart) ------------------ */
+
+/* Residual add fused with RMSNorm, per row of [rows, cols]:
+ *   s = x + delta (fp32);  x = s;  h = w * (s * inv),  inv from s.
+ * Replaces the chain add_inplace + copy + rms_norm composed at
+ * src/model/cuda/cuda_decoder.cpp:267-278 and cuda_decode_step.cpp:54-65
+ * (CPU form src/model/decoder.cpp:176-181,196-201): one read of x and delta,
+ * one write of x and h, instead of five full passes. */
+UOCR_ROCM_API int uocr_rocm_add_rms_norm(void* stream, float* x, const float* delta, const float* w, float* h,
+                                         int64_t rows, int64_t cols, float eps);
+
+/* SwiGLU over a concatenated [gate | up] input: in [rows, 2 * ffn] row-major,
+ * out [rows, ffn] = silu(gate) * up. Replaces the gate/up pair +
+ * silu_mul of CudaDecoder::mlp (src/model/cuda/cuda_decoder.cpp:119-135) and
+ * GatedMlp::forward (src/model/feed_forward.cpp:18-24). */
+UOCR_ROCM_API int uocr_rocm_swiglu(void* stream, const float* in, float* out, int64_t rows, int64_t ffn);
+
+/* rope on Q [rows, q_heads * dim] and K [rows, k_heads * dim] in one launch,
+ * sharing each row's cos/sin across all q_heads + k_heads heads. Same
+ * arithmetic and arguments as uocr_rocm_rope; k may be null when k_heads is
+ * 0. Replaces the per-tensor rope calls of CudaDecoder::attention
+ * (src/model/cuda/cuda_decoder.cpp:213-220). */
+UOCR_ROCM_API int uocr_rocm_rope_qk(void* stream, float* q, int64_t q_heads, float* k, int64_t k_heads, int64_t rows,
+                                    int64_t dim, const int64_t* tok, const int64_t* page, const float* inv_tok,
+                                    int64_t n_tok, const float* inv_page, int64_t n_page, int64_t page_mod,
+                                    int64_t one_tok, int64_t one_page);
+
+/* rope_qk for one decode row at (state->tok, state->page). Replaces the
+ * rope_step pair of decode_attention (src/model/cuda/cuda_decode_step.cpp:27-28). */
+UOCR_ROCM_API int uocr_rocm_rope_qk_step(void* stream, float* q, int64_t q_heads, float* k, int64_t k_heads,
+                                         int64_t dim, const uocr_rocm_step_state* state, const float* inv_tok,
+                                         int64_t n_tok, const float* inv_page, int64_t page_mod);
+
+/* ---- bf16-activation variants (new) ------------------------------------
+ * Same arithmetic as the fp32 entry point of the same name on the widened
+ * inputs, rounded to bf16 once on store; each reduces to its fp32 op. */
+
+UOCR_ROCM_API int uocr_rocm_rms_norm_bf16(void* stream, uint16_t* x, const float* w, int64_t rows, int64_t cols,
+                                          float eps);
+UOCR_ROCM_API int uocr_rocm_add_rms_norm_bf16(void* stream, uint16_t* x, const uint16_t* delta, const float* w,
+                                              uint16_t* h, int64_t rows, int64_t cols, float eps);
+UOCR_ROCM_API int uocr_rocm_layer_norm_bf16(void* stream, uint16_t* x, const float* w, const float* b, int64_t rows,
+                                            int64_t cols, float eps);
+UOCR_ROCM_API int uocr_rocm_gelu_erf_bf16(void* stream, uint16_t* x, int64_t n);
+UOCR_ROCM_API int uocr_rocm_swiglu_bf16(void* stream, const uint16_t* in, uint16_t* out, int64_t rows, int64_t ffn);
+UOCR_ROCM_API int uocr_rocm_rope_bf16(void* stream, uint16_t* x, int64_t rows, int64_t heads, int64_t dim,
+                                      const int64_t* tok, const int64_t* page, const float* inv_tok, int64_t n_tok,
+                                      const float* inv_page, int64_t n_page, int64_t page_mod, int64_t one_tok,
+                                      int64_t one_page);
+UOCR_ROCM_API int uocr_rocm_rope_qk_bf16(void* stream, uint16_t* q, int64_t q_heads, uint16_t* k, int64_t k_heads,
+                                         int64_t rows, int64_t dim, const int64_t* tok, const int64_t* page,
+                                         const float* inv_tok, int64_t n_tok, const float* inv_page, int64_t n_page,
+                                         int64_t page_mod, int64_t one_tok, int64_t one_page);
+UOCR_ROCM_API int uocr_rocm_rope_qk_step_bf16(void* stream, uint16_t* q, int64_t q_heads, uint16_t* k,
+                                              int64_t k_heads, int64_t dim, const uocr_rocm_step_state* state,
+                                              const float* inv_tok, int64_t n_tok, const float* inv_page,
+                                              int64_t page_mod);
+/* Embedding rows kept in bf16: a bit copy of table rows. */
+UOCR_ROCM_API int uocr_rocm_gather_rows_bf16_bf16(void* stream, const uint16_t* table, int64_t table_rows,
+                                                  const int64_t* index, int64_t rows, int64_t cols, uint16_t* dst);
+UOCR_ROCM_API int uocr_rocm_embed_step_bf16(void* stream, const uint16_t* table, int64_t table_rows,
+                                            const uocr_rocm_step_state* state, int64_t cols, uint16_t* dst);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UOCR_ROCM_H_ */

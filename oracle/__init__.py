@@ -1,0 +1,229 @@
+"""numpy wrappers over the CPU oracle (oracle/uocr_oracle.c) and, where it was
+built, over the reference's own CPU ops (oracle/_ref/libuocr_ref.so).
+
+TEST INFRASTRUCTURE ONLY. Imported by tests/, by __graft_entry__.smoke() to
+check its result, and by bench.py's cpu_baseline leg to time the reference's
+CPU path. It is never part of a product path: the ops themselves are the HIP
+library in grpc-unlimited-ocr_amd/.
+
+Every wrapper copies its inputs and returns new arrays; float32 in, float32
+out, bf16 as uint16 bits. The C functions each cite the reference file:line
+they restate.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "liboracle.so")
+REF_LIB_PATH = os.path.join(HERE, "_ref", "libuocr_ref.so")
+
+_LIB = None
+_REF = None
+
+_f = ctypes.c_float
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+
+
+def build() -> None:
+    """Compile the oracle (and oracle/_ref when the reference sources exist)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            subprocess.run(["make", "-s", "-C", HERE], check=True)
+        h = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_bf16_to_f32": ([ctypes.c_uint16], _f),
+            "orc_f32_to_bf16": ([_f], ctypes.c_uint16),
+            "orc_f32_to_bf16_array": ([_vp, _vp, _i64], None),
+            "orc_bf16_to_f32_array": ([_vp, _vp, _i64], None),
+            "orc_set_threads": ([ctypes.c_int], None),
+            "orc_threads": ([], ctypes.c_int),
+            "orc_rms_norm": ([_vp, _vp, _i64, _i64, _f], None),
+            "orc_layer_norm": ([_vp, _vp, _vp, _i64, _i64, _f], None),
+            "orc_gelu_erf": ([_vp, _i64], None),
+            "orc_silu": ([_vp, _i64], None),
+            "orc_mul_into": ([_vp, _vp, _i64], None),
+            "orc_add_into": ([_vp, _vp, _i64], None),
+            "orc_rope_inv": ([_vp, _i64, ctypes.c_double], None),
+            "orc_rope_apply": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64], None),
+            "orc_embed": ([_vp, _vp, _i64, _i64, _vp], None),
+            "orc_add_rms_norm": ([_vp, _vp, _vp, _vp, _i64, _i64, _f], None),
+            "orc_swiglu": ([_vp, _vp, _i64, _i64], None),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(h, name)
+            fn.argtypes = args
+            fn.restype = res
+        _LIB = h
+    return _LIB
+
+
+def ref_lib() -> Optional[ctypes.CDLL]:
+    """The reference's own CPU ops, or None where oracle/_ref was not built."""
+    global _REF
+    if _REF is None and os.path.exists(REF_LIB_PATH):
+        h = ctypes.CDLL(REF_LIB_PATH)
+        sig = {
+            "ref_set_threads": ([ctypes.c_uint], None),
+            "ref_f32_to_bf16": ([_f], ctypes.c_uint16),
+            "ref_bf16_to_f32": ([ctypes.c_uint16], _f),
+            "ref_rms_norm": ([_vp, _vp, _i64, _i64, _f], None),
+            "ref_layer_norm": ([_vp, _vp, _vp, _i64, _i64, _f], None),
+            "ref_gelu_erf": ([_vp, _i64], None),
+            "ref_silu": ([_vp, _i64], None),
+            "ref_rope_tables": ([_i64, ctypes.c_double, ctypes.c_double, _i64, _vp, _vp], None),
+            "ref_rope_apply": ([_vp, _i64, _i64, _i64, ctypes.c_double, ctypes.c_double, _i64, _i64, _vp, _vp],
+                               None),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(h, name)
+            fn.argtypes = args
+            fn.restype = res
+        _REF = h
+    return _REF
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).copy()
+
+
+def _p(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data
+
+
+# ---- bf16 ---------------------------------------------------------------------
+
+
+def f32_to_bf16(a) -> np.ndarray:
+    a = _f32(a)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().orc_f32_to_bf16_array(_p(a), _p(out), a.size)
+    return out
+
+
+def bf16_to_f32(b) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    out = np.empty(b.shape, dtype=np.float32)
+    lib().orc_bf16_to_f32_array(_p(b), _p(out), b.size)
+    return out
+
+
+def bf16_round(a) -> np.ndarray:
+    """float32 values rounded to the bf16 grid (nearest even)."""
+    return bf16_to_f32(f32_to_bf16(a))
+
+
+# ---- threading ------------------------------------------------------------------
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def threads() -> int:
+    return lib().orc_threads()
+
+
+# ---- ops --------------------------------------------------------------------------
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    x = _f32(x)
+    w = _f32(w)
+    cols = x.shape[-1]
+    lib().orc_rms_norm(_p(x), _p(w), x.size // cols, cols, eps)
+    return x
+
+
+def layer_norm(x, w, b, eps: float) -> np.ndarray:
+    x = _f32(x)
+    w, b = _f32(w), _f32(b)
+    cols = x.shape[-1]
+    lib().orc_layer_norm(_p(x), _p(w), _p(b), x.size // cols, cols, eps)
+    return x
+
+
+def gelu_erf(x) -> np.ndarray:
+    x = _f32(x)
+    lib().orc_gelu_erf(_p(x), x.size)
+    return x
+
+
+def silu(x) -> np.ndarray:
+    x = _f32(x)
+    lib().orc_silu(_p(x), x.size)
+    return x
+
+
+def silu_mul(g, u) -> np.ndarray:
+    g = silu(g)
+    u = _f32(u)
+    lib().orc_mul_into(_p(g), _p(u), g.size)
+    return g
+
+
+def add(x, y) -> np.ndarray:
+    x = _f32(x)
+    y = _f32(y)
+    lib().orc_add_into(_p(x), _p(y), x.size)
+    return x
+
+
+def add_rms_norm(x, delta, w, eps: float):
+    """(x + delta, rms_norm(x + delta) * w), the reference's add/copy/norm chain."""
+    x = _f32(x)
+    d, w = _f32(delta), _f32(w)
+    h = np.empty_like(x)
+    cols = x.shape[-1]
+    lib().orc_add_rms_norm(_p(x), _p(d), _p(w), _p(h), x.size // cols, cols, eps)
+    return x, h
+
+
+def swiglu(inp) -> np.ndarray:
+    inp = _f32(inp)
+    two_f = inp.shape[-1]
+    rows, ffn = inp.size // two_f, two_f // 2
+    out = np.empty(inp.shape[:-1] + (ffn,), dtype=np.float32)
+    lib().orc_swiglu(_p(inp), _p(out), rows, ffn)
+    return out
+
+
+def rope_inv(n: int, theta: float) -> np.ndarray:
+    inv = np.empty(n, dtype=np.float32)
+    lib().orc_rope_inv(_p(inv), n, theta)
+    return inv
+
+
+def rope(x, heads: int, dim: int, tok=None, page=None, inv_tok=None, inv_page=None, page_mod: int = 0,
+         one_tok: int = 0, one_page: int = 0) -> np.ndarray:
+    x = _f32(x)
+    rows = x.size // (heads * dim)
+    tok = None if tok is None else np.ascontiguousarray(tok, dtype=np.int64)
+    page = None if page is None else np.ascontiguousarray(page, dtype=np.int64)
+    inv_tok = np.zeros(0, np.float32) if inv_tok is None else _f32(inv_tok)
+    inv_page = np.zeros(0, np.float32) if inv_page is None else _f32(inv_page)
+    lib().orc_rope_apply(_p(x), rows, heads, dim, _p(tok), _p(page), _p(inv_tok), inv_tok.size, _p(inv_page),
+                         inv_page.size, page_mod, one_tok, one_page)
+    return x
+
+
+def embed(table_bits, ids) -> np.ndarray:
+    table_bits = np.ascontiguousarray(table_bits, dtype=np.uint16)
+    ids = np.ascontiguousarray(ids, dtype=np.int64)
+    cols = table_bits.shape[-1]
+    out = np.empty((ids.size, cols), dtype=np.float32)
+    lib().orc_embed(_p(table_bits), _p(ids), ids.size, cols, _p(out))
+    return out

@@ -1,0 +1,91 @@
+// ref_shim.cpp: a C entry-point harness over the reference's own CPU ops,
+// compiled together with the reference sources where they lie
+// (src/backend/reference/ops.cpp, src/model/page_rope.cpp) into
+// oracle/_ref/libuocr_ref.so by oracle/Makefile.
+//
+// TEST INFRASTRUCTURE ONLY: tests/test_oracle.py uses it to check the C
+// restatement in oracle/uocr_oracle.c bit for bit against the reference's
+// code. No product path and no GPU run loads it. This file holds no
+// reference code: it only adapts raw pointers to the reference's Tensor.
+
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "backend/reference/ops.h"
+#include "backend/reference/parallel.h"
+#include "model/page_rope.h"
+#include "tensor/dtype.h"
+#include "tensor/tensor.h"
+
+namespace ref = uocr::reference;
+
+namespace {
+
+uocr::Tensor wrap(const float* p, std::vector<std::int64_t> shape) {
+  const std::int64_t n = uocr::Tensor::count(shape);
+  return uocr::Tensor(std::move(shape), std::vector<float>(p, p + n));
+}
+
+void unwrap(const uocr::Tensor& t, float* out) { std::memcpy(out, t.data(), static_cast<std::size_t>(t.numel()) * 4); }
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) void ref_set_threads(unsigned t) { ref::set_thread_count(t); }
+
+__attribute__((visibility("default"))) std::uint16_t ref_f32_to_bf16(float v) { return uocr::f32_to_bf16(v); }
+__attribute__((visibility("default"))) float ref_bf16_to_f32(std::uint16_t b) { return uocr::bf16_to_f32(b); }
+
+__attribute__((visibility("default"))) void ref_rms_norm(float* x, const float* w, std::int64_t rows,
+                                                         std::int64_t cols, float eps) {
+  uocr::Tensor t = wrap(x, {rows, cols});
+  ref::rms_norm(t, wrap(w, {cols}), eps);
+  unwrap(t, x);
+}
+
+__attribute__((visibility("default"))) void ref_layer_norm(float* x, const float* w, const float* b,
+                                                           std::int64_t rows, std::int64_t cols, float eps) {
+  uocr::Tensor t = wrap(x, {rows, cols});
+  ref::layer_norm(t, wrap(w, {cols}), wrap(b, {cols}), eps);
+  unwrap(t, x);
+}
+
+__attribute__((visibility("default"))) void ref_gelu_erf(float* x, std::int64_t n) {
+  uocr::Tensor t = wrap(x, {n});
+  ref::gelu_erf(t);
+  unwrap(t, x);
+}
+
+__attribute__((visibility("default"))) void ref_silu(float* x, std::int64_t n) {
+  uocr::Tensor t = wrap(x, {n});
+  ref::silu(t);
+  unwrap(t, x);
+}
+
+// PageRope's own frequency tables: inv_tok gets dim/2 - page_pairs entries,
+// inv_page gets page_pairs.
+__attribute__((visibility("default"))) void ref_rope_tables(std::int64_t dim, double tok_theta, double page_theta,
+                                                            std::int64_t page_pairs, float* inv_tok,
+                                                            float* inv_page) {
+  const uocr::PageRope rope(dim, tok_theta, page_theta, page_pairs, 2);
+  std::memcpy(inv_tok, rope.inv_tok().data(), rope.inv_tok().size() * 4);
+  std::memcpy(inv_page, rope.inv_page().data(), rope.inv_page().size() * 4);
+}
+
+// PageRope::apply over x [rows, width] (width a multiple of dim) at
+// coordinates (tok[r], page[r]).
+__attribute__((visibility("default"))) void ref_rope_apply(float* x, std::int64_t rows, std::int64_t width,
+                                                           std::int64_t dim, double tok_theta, double page_theta,
+                                                           std::int64_t page_pairs, std::int64_t page_mod,
+                                                           const std::int64_t* tok, const std::int64_t* page) {
+  const uocr::PageRope rope(dim, tok_theta, page_theta, page_pairs, page_mod);
+  uocr::Tensor t = wrap(x, {rows, width});
+  std::vector<uocr::RopeCoord> coords(static_cast<std::size_t>(rows));
+  for (std::int64_t r = 0; r < rows; ++r) coords[static_cast<std::size_t>(r)] = {tok[r], page[r]};
+  rope.apply(t, coords);
+  unwrap(t, x);
+}
+
+}  // extern "C"

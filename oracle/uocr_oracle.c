@@ -1,0 +1,272 @@
+/*
+ * uocr_oracle.c: CPU restatement of grpc-unlimited-ocr's fp32 reference path
+ * for the fused layer ops.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker: the parity tests,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it to compute
+ * the expected values and the CPU baseline time. No product path may load or
+ * call it; the product is the HIP library built from grpc-unlimited-ocr_amd/csrc.
+ *
+ * Each function restates the reference's arithmetic in the reference's
+ * order (the fp64 accumulations and the points where values are cast to
+ * fp32 matter), citing the file:line it follows. Built with -O3 (the
+ * reference's Release build) and -ffp-contract=off, so every fp32 product
+ * and sum is rounded on its own as in the reference's x86-64 build.
+ *
+ * How each function is pinned (tests/test_oracle.py):
+ *   bf16 conversions: the reference's known answers (tests/dtype_test.cpp:20-28)
+ *     plus an exhaustive comparison with an independent rounding rule.
+ *   rms_norm, layer_norm, gelu_erf, silu: the reference's hand-worked values
+ *     (tests/ops_test.cpp:26-50), closed forms in fp64 on random rows, and
+ *     bit-equality with the reference's own ops.cpp compiled into oracle/_ref.
+ *   rope: identity at position 0, per-pair norm, rope(p) then rope(-p),
+ *     an fp64 complex-rotation brute force, and bit-equality with the
+ *     reference's page_rope.cpp compiled into oracle/_ref.
+ *   embed (gather): exact equality with numpy's row take of the widened table.
+ *   The composed chains (add + rms_norm, swiglu) are pinned through their
+ *   parts and an fp64 closed form of the whole chain.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORC_API __attribute__((visibility("default")))
+
+/* ---- bf16 (src/tensor/dtype.h:32-46) ----------------------------------- */
+
+static inline uint32_t f32_bits(float v) {
+  uint32_t u;
+  memcpy(&u, &v, 4);
+  return u;
+}
+static inline float bits_f32(uint32_t u) {
+  float v;
+  memcpy(&v, &u, 4);
+  return v;
+}
+
+/* bf16_to_f32: the bits become the top half of a binary32 (dtype.h:33-35). */
+ORC_API float orc_bf16_to_f32(uint16_t b) { return bits_f32((uint32_t)b << 16); }
+
+/* f32_to_bf16: round to nearest even; NaN keeps its top bits and is made
+ * quiet with 0x0040 (dtype.h:39-46). */
+ORC_API uint16_t orc_f32_to_bf16(float v) {
+  const uint32_t bits = f32_bits(v);
+  if ((bits & 0x7fffffffU) > 0x7f800000U) return (uint16_t)((bits >> 16) | 0x0040U);
+  const uint32_t rounding = 0x7fffU + ((bits >> 16) & 1U);
+  return (uint16_t)((bits + rounding) >> 16);
+}
+
+ORC_API void orc_f32_to_bf16_array(const float* src, uint16_t* dst, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dst[i] = orc_f32_to_bf16(src[i]);
+}
+ORC_API void orc_bf16_to_f32_array(const uint16_t* src, float* dst, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dst[i] = orc_bf16_to_f32(src[i]);
+}
+
+/* ---- threading (src/backend/reference/parallel.h:23-42, ops.cpp:15,88-89)
+ * The reference spreads a row loop over thread_count() threads, thread t
+ * taking rows t, t + T, t + 2T, ...; each row is computed by one thread with
+ * the serial arithmetic, so the result never depends on T. Norms use it;
+ * the activations, the add and rope run serially in the reference. */
+
+static int g_threads = 1;
+ORC_API void orc_set_threads(int t) { g_threads = t < 1 ? 1 : t; }
+ORC_API int orc_threads(void) { return g_threads; }
+
+typedef void (*row_fn)(void* ctx, int64_t row);
+typedef struct {
+  row_fn fn;
+  void* ctx;
+  int64_t t, threads, count;
+} strip_job;
+
+static void* strip_main(void* arg) {
+  const strip_job* j = (const strip_job*)arg;
+  for (int64_t i = j->t; i < j->count; i += j->threads) j->fn(j->ctx, i);
+  return NULL;
+}
+
+static void parallel_for(int64_t count, row_fn fn, void* ctx) {
+  int64_t threads = g_threads < count ? g_threads : count;
+  if (threads <= 1) {
+    for (int64_t i = 0; i < count; ++i) fn(ctx, i);
+    return;
+  }
+  pthread_t* tid = (pthread_t*)malloc((size_t)threads * sizeof(pthread_t));
+  strip_job* jobs = (strip_job*)malloc((size_t)threads * sizeof(strip_job));
+  int64_t started = 0;
+  for (int64_t t = 0; t < threads; ++t) {
+    jobs[t] = (strip_job){fn, ctx, t, threads, count};
+    if (pthread_create(&tid[t], NULL, strip_main, &jobs[t]) != 0) break;
+    ++started;
+  }
+  /* A thread that could not start leaves its rows to the caller. */
+  for (int64_t t = started; t < threads; ++t) strip_main(&jobs[t]);
+  for (int64_t t = 0; t < started; ++t) pthread_join(tid[t], NULL);
+  free(jobs);
+  free(tid);
+}
+
+/* ---- norms --------------------------------------------------------------- */
+
+typedef struct {
+  float* x;
+  const float* w;
+  const float* b;
+  int64_t cols;
+  float eps;
+} norm_ctx;
+
+/* reference::rms_norm, one row (src/backend/reference/ops.cpp:132-140):
+ * ss in fp64, inv = float(1 / sqrt(ss / c + eps)) in fp64, then
+ * v = w * (v * inv) in fp32. */
+static void rms_row(void* p, int64_t r) {
+  const norm_ctx* c = (const norm_ctx*)p;
+  float* v = c->x + r * c->cols;
+  double ss = 0.0;
+  for (int64_t i = 0; i < c->cols; ++i) ss += (double)v[i] * v[i];
+  const float inv = (float)(1.0 / sqrt(ss / (double)c->cols + c->eps));
+  for (int64_t i = 0; i < c->cols; ++i) v[i] = c->w[i] * (v[i] * inv);
+}
+
+ORC_API void orc_rms_norm(float* x, const float* w, int64_t rows, int64_t cols, float eps) {
+  norm_ctx c = {x, w, NULL, cols, eps};
+  parallel_for(rows, rms_row, &c);
+}
+
+/* reference::layer_norm, one row (ops.cpp:114-126): two-pass fp64 mean and
+ * variance, inv = 1 / sqrt(var + eps) in fp64, then
+ * v = float((v - mean) * inv) * w + b with the last product and sum in fp32. */
+static void ln_row(void* p, int64_t r) {
+  const norm_ctx* c = (const norm_ctx*)p;
+  float* v = c->x + r * c->cols;
+  double mean = 0.0;
+  for (int64_t i = 0; i < c->cols; ++i) mean += v[i];
+  mean /= (double)c->cols;
+  double var = 0.0;
+  for (int64_t i = 0; i < c->cols; ++i) var += (v[i] - mean) * (v[i] - mean);
+  var /= (double)c->cols;
+  const double inv = 1.0 / sqrt(var + c->eps);
+  for (int64_t i = 0; i < c->cols; ++i) v[i] = (float)((v[i] - mean) * inv) * c->w[i] + c->b[i];
+}
+
+ORC_API void orc_layer_norm(float* x, const float* w, const float* b, int64_t rows, int64_t cols, float eps) {
+  norm_ctx c = {x, w, b, cols, eps};
+  parallel_for(rows, ln_row, &c);
+}
+
+/* ---- activations (serial, as in the reference) --------------------------- */
+
+/* reference::gelu_erf (ops.cpp:151-155): 0.5f * v * (1 + erf(v * float(M_SQRT1_2)))
+ * with std::erf on a float, i.e. erff. */
+ORC_API void orc_gelu_erf(float* x, int64_t n) {
+  const float k = (float)M_SQRT1_2;
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = x[i];
+    x[i] = 0.5f * v * (1.0f + erff(v * k));
+  }
+}
+
+/* sigmoid (ops.cpp:40): 1 / (1 + exp(-x)) on a float, i.e. expf. */
+static inline float sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+/* reference::silu (ops.cpp:163-167): v * sigmoid(v). */
+ORC_API void orc_silu(float* x, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) x[i] = x[i] * sigmoid(x[i]);
+}
+
+/* g *= u, the multiply of GatedMlp::forward (src/model/feed_forward.cpp:21-22). */
+ORC_API void orc_mul_into(float* g, const float* u, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) g[i] *= u[i];
+}
+
+/* add_into: x += y (src/model/decoder.cpp:39-41). */
+ORC_API void orc_add_into(float* x, const float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) x[i] += y[i];
+}
+
+/* ---- rope ---------------------------------------------------------------- */
+
+/* The frequency table of PageRope's constructor (src/model/page_rope.cpp:17-23):
+ * inv[i] = float(1 / pow(theta, i / n)) in fp64. */
+ORC_API void orc_rope_inv(float* inv, int64_t n, double theta) {
+  for (int64_t i = 0; i < n; ++i) inv[i] = (float)(1.0 / pow(theta, (double)i / (double)n));
+}
+
+/* PageRope::apply (src/model/page_rope.cpp:26-56) over x [rows, heads * dim]:
+ * per row, the fp32 angle float(tok) * inv_tok[i] (token pairs) or
+ * float(page folded mod page_mod) * inv_page[i] (page pairs), cos and sin of
+ * the fp32 angle (cosf / sinf), then the rotate-half update of every head:
+ * v[i] = a c - b s, v[i + half] = b c + a s. tok / page may be NULL, when
+ * every row takes one_tok / one_page (the uocr::cuda::rope convention,
+ * src/backend/cuda/ops.h:48-52). Requires n_tok + n_page == dim / 2. */
+ORC_API void orc_rope_apply(float* x, int64_t rows, int64_t heads, int64_t dim, const int64_t* tok,
+                            const int64_t* page, const float* inv_tok, int64_t n_tok, const float* inv_page,
+                            int64_t n_page, int64_t page_mod, int64_t one_tok, int64_t one_page) {
+  const int64_t half = dim / 2;
+  float* cos_v = (float*)malloc((size_t)(half > 0 ? half : 1) * sizeof(float));
+  float* sin_v = (float*)malloc((size_t)(half > 0 ? half : 1) * sizeof(float));
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t tk = tok != NULL ? tok[r] : one_tok;
+    const int64_t pg = page != NULL ? page[r] : one_page;
+    const float t = (float)tk;
+    const float p = (float)(page_mod > 0 ? ((pg % page_mod) + page_mod) % page_mod : pg);
+    for (int64_t i = 0; i < n_tok; ++i) {
+      const float a = t * inv_tok[i];
+      cos_v[i] = cosf(a);
+      sin_v[i] = sinf(a);
+    }
+    for (int64_t i = 0; i < n_page; ++i) {
+      const float a = p * inv_page[i];
+      cos_v[n_tok + i] = cosf(a);
+      sin_v[n_tok + i] = sinf(a);
+    }
+    float* row = x + r * heads * dim;
+    for (int64_t h = 0; h < heads; ++h) {
+      float* v = row + h * dim;
+      for (int64_t i = 0; i < half; ++i) {
+        const float a = v[i], b = v[i + half];
+        v[i] = a * cos_v[i] - b * sin_v[i];
+        v[i + half] = b * cos_v[i] + a * sin_v[i];
+      }
+    }
+  }
+  free(cos_v);
+  free(sin_v);
+}
+
+/* ---- embedding gather ---------------------------------------------------- */
+
+/* Decoder::embed (src/model/decoder.cpp:85-92) copies rows of the fp32
+ * embedding table, which CheckpointWeights::get widened from bf16 at load
+ * (src/model/weight_source.cpp:16-23): dst[r] = widen(table[ids[r]]). */
+ORC_API void orc_embed(const uint16_t* table, const int64_t* ids, int64_t n, int64_t cols, float* dst) {
+  for (int64_t r = 0; r < n; ++r) {
+    const uint16_t* src = table + ids[r] * cols;
+    for (int64_t i = 0; i < cols; ++i) dst[r * cols + i] = orc_bf16_to_f32(src[i]);
+  }
+}
+
+/* ---- the composed chains the fused ops replace ---------------------------- */
+
+/* Residual add then norm, the order of Decoder::prefill / step
+ * (src/model/decoder.cpp:176-181,196-201) and CudaDecoder::run
+ * (src/model/cuda/cuda_decoder.cpp:267-278): x += delta; h = x;
+ * h = rms_norm(h, w). */
+ORC_API void orc_add_rms_norm(float* x, const float* delta, const float* w, float* h, int64_t rows, int64_t cols,
+                              float eps) {
+  orc_add_into(x, delta, rows * cols);
+  memcpy(h, x, (size_t)(rows * cols) * sizeof(float));
+  orc_rms_norm(h, w, rows, cols, eps);
+}
+
+/* SwiGLU of GatedMlp::forward (src/model/feed_forward.cpp:18-24) on a
+ * concatenated [gate | up] row layout: g = silu(gate); g *= up. */
+ORC_API void orc_swiglu(const float* in, float* out, int64_t rows, int64_t ffn) {
+  for (int64_t r = 0; r < rows; ++r) memcpy(out + r * ffn, in + r * 2 * ffn, (size_t)ffn * sizeof(float));
+  orc_silu(out, rows * ffn);
+  for (int64_t r = 0; r < rows; ++r) orc_mul_into(out + r * ffn, in + r * 2 * ffn + ffn, ffn);
+}

@@ -1,0 +1,39 @@
+/*
+ * uocr_oracle.h: declarations of the CPU oracle (oracle/uocr_oracle.c), the
+ * restatement of the reference's fp32 CPU path. TEST INFRASTRUCTURE ONLY:
+ * included by the parity tests, never by the product.
+ */
+#ifndef UOCR_ORACLE_H_
+#define UOCR_ORACLE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+float orc_bf16_to_f32(uint16_t b);
+uint16_t orc_f32_to_bf16(float v);
+void orc_f32_to_bf16_array(const float* src, uint16_t* dst, int64_t n);
+void orc_bf16_to_f32_array(const uint16_t* src, float* dst, int64_t n);
+void orc_set_threads(int t);
+int orc_threads(void);
+void orc_rms_norm(float* x, const float* w, int64_t rows, int64_t cols, float eps);
+void orc_layer_norm(float* x, const float* w, const float* b, int64_t rows, int64_t cols, float eps);
+void orc_gelu_erf(float* x, int64_t n);
+void orc_silu(float* x, int64_t n);
+void orc_mul_into(float* g, const float* u, int64_t n);
+void orc_add_into(float* x, const float* y, int64_t n);
+void orc_rope_inv(float* inv, int64_t n, double theta);
+void orc_rope_apply(float* x, int64_t rows, int64_t heads, int64_t dim, const int64_t* tok, const int64_t* page,
+                    const float* inv_tok, int64_t n_tok, const float* inv_page, int64_t n_page, int64_t page_mod,
+                    int64_t one_tok, int64_t one_page);
+void orc_embed(const uint16_t* table, const int64_t* ids, int64_t n, int64_t cols, float* dst);
+void orc_add_rms_norm(float* x, const float* delta, const float* w, float* h, int64_t rows, int64_t cols, float eps);
+void orc_swiglu(const float* in, float* out, int64_t rows, int64_t ffn);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UOCR_ORACLE_H_ */

@@ -1,0 +1,348 @@
+// Every rocm op against the CPU oracle (the restatement of the reference's
+// fp32 CPU path, oracle/uocr_oracle.c) on random data, in the shape of the
+// reference's tests/cuda_ops_test.cpp: the same N(0,1) inputs from
+// std::mt19937(5), the same relative-error metric, the same tolerances for
+// the fp32 ops, plus the bf16-activation ops at 2 bf16 ulp, the fused ops,
+// a captured decode step replayed at three StepStates, and the error
+// convention. Exits 77 (skip) without a HIP device.
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <functional>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "backend/rocm/context.h"
+#include "backend/rocm/decode_ops.h"
+#include "backend/rocm/dtype.h"
+#include "backend/rocm/ops.h"
+#include "../../oracle/uocr_oracle.h"
+
+namespace ro = uocr::rocm;
+
+namespace {
+
+void require(bool ok, const std::string& what) {
+  if (!ok) throw std::runtime_error("FAIL: " + what);
+}
+
+template <class Fn>
+void require_throws_invalid(Fn&& fn, const std::string& what) {
+  try {
+    fn();
+  } catch (const std::invalid_argument&) {
+    return;
+  }
+  throw std::runtime_error("FAIL (no std::invalid_argument): " + what);
+}
+
+std::mt19937 rng(5);
+
+// Box-Muller over mt19937 words, so the inputs do not depend on the
+// standard library's normal_distribution.
+std::vector<float> random(std::size_t n, float scale = 1.0f) {
+  std::vector<float> v(n);
+  const double two_pi = 6.283185307179586;
+  for (std::size_t i = 0; i < n; i += 2) {
+    const double u1 = (static_cast<double>(rng()) + 1.0) / 4294967297.0;
+    const double u2 = static_cast<double>(rng()) / 4294967296.0;
+    const double r = std::sqrt(-2.0 * std::log(u1));
+    v[i] = static_cast<float>(r * std::cos(two_pi * u2)) * scale;
+    if (i + 1 < n) v[i + 1] = static_cast<float>(r * std::sin(two_pi * u2)) * scale;
+  }
+  return v;
+}
+
+std::vector<float> bf16_rounded(std::vector<float> v) {
+  for (float& x : v) x = ro::bf16_to_f32(ro::f32_to_bf16(x));
+  return v;
+}
+
+// The reference's metric (tests/cuda_ops_test.cpp:47-54): max |got - want| / max |want|.
+double max_rel(const std::vector<float>& got, const std::vector<float>& want) {
+  double worst = 0.0, scale = 1e-9;
+  for (std::size_t i = 0; i < want.size(); ++i) {
+    worst = std::max(worst, std::fabs(static_cast<double>(got[i]) - want[i]));
+    scale = std::max(scale, std::fabs(static_cast<double>(want[i])));
+  }
+  return worst / scale;
+}
+
+int ordered(std::uint16_t b) { return (b & 0x8000) ? -static_cast<int>(b & 0x7fff) : static_cast<int>(b & 0x7fff); }
+
+// Worst bf16-ulp distance between got (bf16 bits) and the oracle's fp32
+// value rounded to bf16, skipping elements within 2^-21 max|want| of the
+// oracle (the fp32 error floor of the oracle itself, met only where a result
+// cancels far below the size of its inputs).
+int max_ulp(const std::vector<std::uint16_t>& got, const std::vector<float>& want) {
+  double scale = 0.0;
+  for (float w : want) scale = std::max(scale, std::fabs(static_cast<double>(w)));
+  const double floor_abs = std::ldexp(scale, -21);
+  int worst = 0;
+  for (std::size_t i = 0; i < want.size(); ++i) {
+    const double diff = std::fabs(static_cast<double>(ro::bf16_to_f32(got[i])) - want[i]);
+    if (diff <= floor_abs) continue;
+    worst = std::max(worst, std::abs(ordered(got[i]) - ordered(ro::f32_to_bf16(want[i]))));
+  }
+  return worst;
+}
+
+void expect(const char* what, double err, double tol) {
+  std::printf("%-26s rel err %.2e (tol %.0e)\n", what, err, tol);
+  require(err <= tol, what);
+}
+
+void expect_bf16(const char* what, const std::vector<std::uint16_t>& got, const std::vector<float>& want) {
+  std::vector<float> wide(got.size());
+  for (std::size_t i = 0; i < got.size(); ++i) wide[i] = ro::bf16_to_f32(got[i]);
+  const double rel = max_rel(wide, want);
+  const int ulp = max_ulp(got, want);
+  std::printf("%-26s rel err %.2e (tol 1e-02), max %d bf16 ulp (tol 2)\n", what, rel, ulp);
+  require(rel <= 1e-2 && ulp <= 2, what);
+}
+
+ro::Array up(const ro::Context& ctx, const std::vector<float>& v, ro::DType type = ro::DType::kF32) {
+  ro::Array a(ctx, type, static_cast<std::int64_t>(v.size()));
+  a.upload(v.data(), static_cast<std::int64_t>(v.size()));
+  return a;
+}
+
+ro::Array up_ids(const ro::Context& ctx, const std::vector<std::int64_t>& ids) {
+  ro::Array a(ctx, ro::DType::kI64, static_cast<std::int64_t>(ids.size()));
+  a.upload(ids.data(), static_cast<std::int64_t>(ids.size()));
+  return a;
+}
+
+std::vector<float> rope_inv(std::int64_t n, double theta) {
+  std::vector<float> inv(static_cast<std::size_t>(n));
+  orc_rope_inv(inv.data(), n, theta);
+  return inv;
+}
+
+void fp32_ops(const ro::Context& ctx) {
+  const std::int64_t rows = 9, cols = 300;
+  const auto x = random(rows * cols), w = random(cols), b = random(cols);
+  auto want = x;
+  orc_layer_norm(want.data(), w.data(), b.data(), rows, cols, 1e-6f);
+  auto dx = up(ctx, x), dw = up(ctx, w), db = up(ctx, b);
+  ro::layer_norm(ctx, dx.f32(), dw.f32(), db.f32(), rows, cols, 1e-6f);
+  expect("layer_norm", max_rel(dx.download(), want), 1e-5);
+
+  auto rwant = x;
+  orc_rms_norm(rwant.data(), w.data(), rows, cols, 1e-6f);
+  auto dr = up(ctx, x);
+  ro::rms_norm(ctx, dr.f32(), dw.f32(), rows, cols, 1e-6f);
+  expect("rms_norm", max_rel(dr.download(), rwant), 1e-5);
+
+  auto g = x;
+  orc_gelu_erf(g.data(), rows * cols);
+  auto dg = up(ctx, x);
+  ro::gelu_erf(ctx, dg.f32(), rows * cols);
+  expect("gelu_erf", max_rel(dg.download(), g), 1e-6);
+
+  const auto u = random(rows * cols);
+  auto s = x;
+  orc_silu(s.data(), rows * cols);
+  orc_mul_into(s.data(), u.data(), rows * cols);
+  auto ds = up(ctx, x), du = up(ctx, u);
+  ro::silu_mul(ctx, ds.f32(), du.f32(), rows * cols);
+  expect("silu_mul", max_rel(ds.download(), s), 1e-6);
+
+  auto a = x;
+  orc_add_into(a.data(), u.data(), rows * cols);
+  auto da = up(ctx, x);
+  ro::add_inplace(ctx, da.f32(), du.f32(), rows * cols);
+  expect("add_inplace", max_rel(da.download(), a), 0.0);
+
+  ro::Array dc(ctx, ro::DType::kF32, rows * cols);
+  ro::copy(ctx, dc.f32(), du.f32(), rows * cols);
+  expect("copy", max_rel(dc.download(), u), 0.0);
+}
+
+void rope_page2d(const ro::Context& ctx) {
+  // The reference's page-coordinate case (tests/cuda_ops_test.cpp:142-162):
+  // dim 16, 7 token pairs (theta 1e4 over 7) and 1 page pair, page mod 2.
+  const std::int64_t rows = 4, heads = 2, dim = 16;
+  const auto x = random(rows * heads * dim);
+  const std::vector<std::int64_t> tok{0, 5, 300, 7}, page{0, 1, 2, 3};
+  const auto inv_tok = rope_inv(7, 1e4);
+  const std::vector<float> inv_page{1.0f};
+  auto want = x;
+  orc_rope_apply(want.data(), rows, heads, dim, tok.data(), page.data(), inv_tok.data(), 7, inv_page.data(), 1, 2, 0, 0);
+  auto dx = up(ctx, x), dt = up_ids(ctx, tok), dp = up_ids(ctx, page), dit = up(ctx, inv_tok), dip = up(ctx, inv_page);
+  ro::rope(ctx, dx.f32(), rows, heads, dim, dt.i64(), dp.i64(), dit.f32(), 7, dip.f32(), 1, 2);
+  expect("rope page2d", max_rel(dx.download(), want), 1e-5);
+}
+
+void gather(const ro::Context& ctx) {
+  const std::int64_t vocab = 6, cols = 10;
+  const auto table = random(vocab * cols);
+  auto dt = up(ctx, table, ro::DType::kBF16);
+  const std::vector<std::int64_t> idx{4, 0, 4};
+  auto di = up_ids(ctx, idx);
+  ro::Array dst(ctx, ro::DType::kF32, 3 * cols);
+  ro::gather_rows_bf16(ctx, dt.bf16(), di.i64(), 3, cols, dst.f32());
+  const auto bits = dt.download_bf16();
+  std::vector<float> want(3 * cols);
+  orc_embed(bits.data(), idx.data(), 3, cols, want.data());
+  const auto got = dst.download();
+  require(std::equal(got.begin(), got.end(), want.begin(), [](float a, float b) {
+            return std::bit_cast<std::uint32_t>(a) == std::bit_cast<std::uint32_t>(b);
+          }),
+          "gather_rows_bf16 is bit-exact");
+  ro::Array one(ctx, ro::DType::kF32, cols);
+  ro::gather_row_bf16(ctx, dt.bf16(), 5, cols, one.f32());
+  std::vector<float> want5(cols);
+  const std::int64_t five = 5;
+  orc_embed(bits.data(), &five, 1, cols, want5.data());
+  require(one.download() == want5, "gather_row_bf16 is exact");
+  std::printf("%-26s exact\n", "gather_rows_bf16");
+}
+
+void bf16_ops(const ro::Context& ctx) {
+  const std::int64_t rows = 33, cols = 2048, ffn = 1408;
+  const float eps = 1e-6f;
+  {  // residual add + RMSNorm
+    const auto x = bf16_rounded(random(rows * cols)), d = bf16_rounded(random(rows * cols));
+    auto w = random(cols, 0.02f);
+    for (float& v : w) v += 1.0f;
+    auto wx = x;
+    std::vector<float> wh(x.size());
+    orc_add_rms_norm(wx.data(), d.data(), w.data(), wh.data(), rows, cols, eps);
+    auto dx = up(ctx, x, ro::DType::kBF16), dd = up(ctx, d, ro::DType::kBF16), dw = up(ctx, w);
+    ro::Array dh(ctx, ro::DType::kBF16, rows * cols);
+    ro::add_rms_norm_bf16(ctx, dx.bf16(), dd.bf16(), dw.f32(), dh.bf16(), rows, cols, eps);
+    expect_bf16("add_rms_norm_bf16 x'", dx.download_bf16(), wx);
+    expect_bf16("add_rms_norm_bf16 h", dh.download_bf16(), wh);
+  }
+  {  // SwiGLU on [gate | up]
+    const auto in = bf16_rounded(random(rows * 2 * ffn));
+    std::vector<float> want(rows * ffn);
+    orc_swiglu(in.data(), want.data(), rows, ffn);
+    auto din = up(ctx, in, ro::DType::kBF16);
+    ro::Array dout(ctx, ro::DType::kBF16, rows * ffn);
+    ro::swiglu_bf16(ctx, din.bf16(), dout.bf16(), rows, ffn);
+    expect_bf16("swiglu_bf16", dout.download_bf16(), want);
+  }
+  {  // LayerNorm then GELU, the vision block pair
+    const std::int64_t c = 1024;
+    const auto x = bf16_rounded(random(rows * c));
+    auto w = random(c, 0.02f);
+    for (float& v : w) v += 1.0f;
+    const auto b = random(c, 0.02f);
+    auto want = x;
+    orc_layer_norm(want.data(), w.data(), b.data(), rows, c, eps);
+    auto dx = up(ctx, x, ro::DType::kBF16), dw = up(ctx, w), db = up(ctx, b);
+    ro::layer_norm_bf16(ctx, dx.bf16(), dw.f32(), db.f32(), rows, c, eps);
+    const auto ln = dx.download_bf16();
+    expect_bf16("layer_norm_bf16", ln, want);
+    std::vector<float> g(ln.size());
+    for (std::size_t i = 0; i < ln.size(); ++i) g[i] = ro::bf16_to_f32(ln[i]);
+    orc_gelu_erf(g.data(), rows * c);
+    ro::gelu_erf_bf16(ctx, dx.bf16(), rows * c);
+    expect_bf16("gelu_erf_bf16", dx.download_bf16(), g);
+  }
+  {  // rope on Q and K in one launch, positions up to 20000
+    const std::int64_t qh = 16, kh = 4, dim = 128;
+    const auto q = bf16_rounded(random(rows * qh * dim)), k = bf16_rounded(random(rows * kh * dim));
+    std::vector<std::int64_t> pos(rows);
+    for (std::int64_t r = 0; r < rows; ++r) pos[r] = static_cast<std::int64_t>(rng() % 20001);
+    const auto inv = rope_inv(dim / 2, 1e4);
+    auto wq = q, wk = k;
+    orc_rope_apply(wq.data(), rows, qh, dim, pos.data(), nullptr, inv.data(), dim / 2, nullptr, 0, 0, 0, 0);
+    orc_rope_apply(wk.data(), rows, kh, dim, pos.data(), nullptr, inv.data(), dim / 2, nullptr, 0, 0, 0, 0);
+    auto dq = up(ctx, q, ro::DType::kBF16), dk = up(ctx, k, ro::DType::kBF16), dp = up_ids(ctx, pos),
+         di = up(ctx, inv);
+    ro::rope_qk_bf16(ctx, dq.bf16(), qh, dk.bf16(), kh, rows, dim, dp.i64(), nullptr, di.f32(), dim / 2, nullptr, 0,
+                     0);
+    expect_bf16("rope_qk_bf16 q", dq.download_bf16(), wq);
+    expect_bf16("rope_qk_bf16 k", dk.download_bf16(), wk);
+  }
+}
+
+void decode_graph(const ro::Context& ctx) {
+  // gather -> residual add + RMSNorm -> rope on Q/K, captured once and
+  // replayed at three step states, as CudaDecoder::step replays decode_body
+  // (src/model/cuda/cuda_decoder.cpp:309-325).
+  const std::int64_t vocab = 1000, hidden = 2048, qh = 16, kh = 4, dim = 128;
+  const auto table = bf16_rounded(random(vocab * hidden, 0.02f));
+  auto w = random(hidden, 0.02f);
+  for (float& v : w) v += 1.0f;
+  const auto inv = rope_inv(dim / 2, 1e4);
+  auto dtab = up(ctx, table, ro::DType::kBF16), dw = up(ctx, w), dinv = up(ctx, inv);
+  ro::Array x(ctx, ro::DType::kBF16, hidden), delta(ctx, ro::DType::kBF16, hidden), h(ctx, ro::DType::kBF16, hidden),
+      q(ctx, ro::DType::kBF16, qh * dim), k(ctx, ro::DType::kBF16, kh * dim), state(ctx, ro::DType::kI64, 5);
+  const auto* st = reinterpret_cast<const ro::StepState*>(state.data());
+  ctx.synchronize();
+  ctx.begin_capture();
+  ro::embed_step_bf16(ctx, dtab.bf16(), vocab, st, hidden, x.bf16());
+  ro::add_rms_norm_bf16(ctx, x.bf16(), delta.bf16(), dw.f32(), h.bf16(), 1, hidden, 1e-6f);
+  ro::rope_qk_step_bf16(ctx, q.bf16(), qh, k.bf16(), kh, dim, st, dinv.f32(), dim / 2, nullptr, 0);
+  auto graph = ctx.end_capture();
+  const auto tbits = dtab.download_bf16();
+  for (int step = 0; step < 3; ++step) {
+    const std::int64_t token = static_cast<std::int64_t>(rng() % vocab), pos = static_cast<std::int64_t>(rng() % 20001);
+    const auto dv = bf16_rounded(random(hidden)), qv = bf16_rounded(random(qh * dim)), kv = bf16_rounded(random(kh * dim));
+    delta.upload(dv.data(), hidden);
+    q.upload(qv.data(), qh * dim);
+    k.upload(kv.data(), kh * dim);
+    const std::int64_t s[5] = {token, pos, pos, 0, -1};
+    state.upload(s, 5);
+    graph->launch();
+    ctx.synchronize();
+    std::vector<float> wx(hidden), wh(hidden);
+    orc_embed(tbits.data(), &token, 1, hidden, wx.data());
+    orc_add_rms_norm(wx.data(), dv.data(), w.data(), wh.data(), 1, hidden, 1e-6f);
+    auto wq = qv, wk = kv;
+    orc_rope_apply(wq.data(), 1, qh, dim, nullptr, nullptr, inv.data(), dim / 2, nullptr, 0, 0, pos, 0);
+    orc_rope_apply(wk.data(), 1, kh, dim, nullptr, nullptr, inv.data(), dim / 2, nullptr, 0, 0, pos, 0);
+    expect_bf16("decode graph x'", x.download_bf16(), wx);
+    expect_bf16("decode graph h", h.download_bf16(), wh);
+    expect_bf16("decode graph q", q.download_bf16(), wq);
+    expect_bf16("decode graph k", k.download_bf16(), wk);
+  }
+}
+
+void errors(const ro::Context& ctx) {
+  ro::Array x(ctx, ro::DType::kF32, 64), w(ctx, ro::DType::kF32, 64);
+  require_throws_invalid([&] { ro::rms_norm(ctx, x.f32(), w.f32(), -1, 64, 1e-6f); }, "negative rows");
+  require_throws_invalid([&] { ro::rms_norm(ctx, x.f32(), nullptr, 1, 64, 1e-6f); }, "null weight");
+  require_throws_invalid([&] { ro::rope(ctx, x.f32(), 1, 1, 7, nullptr, nullptr, w.f32(), 3, nullptr, 0, 0); },
+                         "odd rope dim");
+  require_throws_invalid([&] { ro::rope(ctx, x.f32(), 1, 1, 8, nullptr, nullptr, w.f32(), 3, nullptr, 0, 0); },
+                         "rope tables that do not cover dim / 2");
+  require_throws_invalid([&] { ro::add_rms_norm(ctx, x.f32(), x.f32(), w.f32(), x.f32(), 1, 64, 1e-6f); },
+                         "aliased add_rms_norm buffers");
+  ro::rms_norm(ctx, x.f32(), w.f32(), 0, 64, 1e-6f);  // empty is a no-op
+  ctx.synchronize();
+  std::printf("%-26s ok\n", "error convention");
+}
+
+}  // namespace
+
+int main() {
+  if (ro::device_count() == 0) {
+    std::fprintf(stderr, "SKIP: no HIP device\n");
+    return 77;
+  }
+  try {
+    const ro::Context ctx(0);
+    const auto info = ro::device_info(0);
+    std::printf("device: %s, %d CUs\n", info.name.c_str(), info.compute_units);
+    fp32_ops(ctx);
+    rope_page2d(ctx);
+    gather(ctx);
+    bf16_ops(ctx);
+    decode_graph(ctx);
+    errors(ctx);
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "%s\n", e.what());
+    return 1;
+  }
+  std::printf("ok\n");
+  return 0;
+}

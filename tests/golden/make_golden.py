@@ -1,0 +1,74 @@
+"""Writes tests/golden/ref_vectors.npz: small input/output vectors produced by
+the reference's own CPU code (src/backend/reference/ops.cpp,
+src/model/page_rope.cpp, src/tensor/dtype.h), compiled from where it lies
+into oracle/_ref/libuocr_ref.so by `make -C oracle ref`.
+
+Run in a container that holds the reference sources:
+    make -C oracle ref && python tests/golden/make_golden.py
+The vectors let every machine (including ones without the reference) check
+the oracle's restatement bit for bit (tests/test_oracle.py)."""
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+import oracle  # noqa: E402
+
+
+def main():
+    ref = oracle.ref_lib()
+    if ref is None:
+        raise SystemExit("oracle/_ref/libuocr_ref.so is not built: run `make -C oracle ref` first")
+    p = lambda a: a.ctypes.data  # noqa: E731
+    g = np.random.default_rng(20260101)
+    out = {}
+
+    # norms: [6, 300] like the reference's device test, eps 1e-6
+    x = g.standard_normal((6, 300), dtype=np.float32) * 2 + 0.5
+    w = (1 + 0.02 * g.standard_normal(300)).astype(np.float32)
+    b = (0.02 * g.standard_normal(300)).astype(np.float32)
+    r = x.copy()
+    ref.ref_rms_norm(p(r), p(w), 6, 300, np.float32(1e-6))
+    l = x.copy()
+    ref.ref_layer_norm(p(l), p(w), p(b), 6, 300, np.float32(1e-6))
+    out.update(norm_x=x, norm_w=w, norm_b=b, norm_eps=np.float32(1e-6), rms_out=r, ln_out=l)
+
+    # activations over a spread that reaches the tails
+    a = (g.standard_normal(2048) * 4).astype(np.float32)
+    ge, si = a.copy(), a.copy()
+    ref.ref_gelu_erf(p(ge), ge.size)
+    ref.ref_silu(p(si), si.size)
+    out.update(act_x=a, gelu_out=ge, silu_out=si)
+
+    # the decoder's two-axis rope: dim 128, 63 token pairs + 1 page pair, page mod 2
+    dim, heads, pairs, rows = 128, 3, 1, 8
+    inv_tok = np.empty(dim // 2 - pairs, np.float32)
+    inv_page = np.empty(pairs, np.float32)
+    ref.ref_rope_tables(dim, 1e4, 256.0, pairs, p(inv_tok), p(inv_page))
+    xr = g.standard_normal((rows, heads * dim), dtype=np.float32)
+    tok = np.array([0, 1, 17, 300, 4095, 8191, 12000, 20000], np.int64)
+    page = np.array([0, 1, 2, 3, -1, 7, 10, 11], np.int64)
+    yr = xr.copy()
+    ref.ref_rope_apply(p(yr), rows, heads * dim, dim, 1e4, 256.0, pairs, 2, p(tok), p(page))
+    out.update(rope_x=xr, rope_out=yr, rope_tok=tok, rope_page=page, rope_inv_tok=inv_tok, rope_inv_page=inv_page,
+               rope_dim=np.int64(dim), rope_heads=np.int64(heads), rope_page_mod=np.int64(2),
+               rope_tok_theta=np.float64(1e4), rope_page_theta=np.float64(256.0))
+
+    # bf16 rounding: ties, near-ties, overflow, NaN, and random patterns
+    special = np.array([0x3F808000, 0x3F818000, 0x3F808001, 0x7F7FFFFF, 0x7F7F8000, 0xFF7F8000, 0x7FC00001,
+                        0xFFA00000, 0x00008000, 0x00018000, 0x80008000, 0x7F800000, 0x00000001], np.uint32)
+    bits = np.concatenate([special, g.integers(0, 1 << 32, 2048, dtype=np.uint64).astype(np.uint32)])
+    bf = np.array([ref.ref_f32_to_bf16(np.float32(v)) for v in bits.view(np.float32)], np.uint16)
+    out.update(bf16_in=bits, bf16_out=bf)
+
+    path = os.path.join(HERE, "ref_vectors.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes)")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,125 @@
+"""The C ABI on the CPU: the library loads, exports every entry point that
+include/uocr_rocm.h declares, and rejects bad arguments with
+UOCR_ROCM_INVALID_ARGUMENT and a "<what>: <detail>" message before touching
+a device, which is the reference's std::invalid_argument convention
+(src/backend/cuda/decode_ops.cu:239, ops.cu:569,655). No call here reaches
+a kernel launch."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import PKG_DIR, ROOT
+
+HEADER = os.path.join(ROOT, "include", "uocr_rocm.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return re.findall(r"UOCR_ROCM_API\s+[\w\s\*]+?\b(uocr_rocm_\w+)\s*\(", text)
+
+
+def test_every_declared_symbol_is_exported(backend):
+    names = declared()
+    assert len(names) == len(set(names)) >= 40
+    out = subprocess.run(["nm", "-D", "--defined-only", backend.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (uocr_rocm_\w+)", out))
+    assert set(names) <= exported, sorted(set(names) - exported)
+    assert set(backend._SIGNATURES) == set(names)
+
+
+def test_library_loads_with_signatures(backend):
+    lib = backend.lib()
+    for name in declared():
+        assert getattr(lib, name) is not None
+    assert lib.uocr_rocm_abi_version() >> 16 == 1
+    assert lib.uocr_rocm_status_string(backend.INVALID_ARGUMENT) == b"invalid argument"
+    assert isinstance(backend.device_count(), int)
+
+
+def test_host_library_and_cpp_test_are_built():
+    host = os.path.join(PKG_DIR, "build", "libuocr_rocm_host.so")
+    ctypes.CDLL(host)  # the C++23 uocr::rocm layer links against the C ABI
+    assert os.access(os.path.join(PKG_DIR, "build", "rocm_ops_test"), os.X_OK)
+
+
+def test_cpp_test_skips_without_device(backend):
+    if backend.device_count() != 0:
+        pytest.skip("a device is present; the GPU suite runs this binary")
+    r = subprocess.run([os.path.join(PKG_DIR, "build", "rocm_ops_test")], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 77, r.stderr
+
+
+def _invalid(backend, name, *args, detail=""):
+    lib = backend.lib()
+    status = getattr(lib, name)(*args)
+    assert status == backend.INVALID_ARGUMENT, (name, status)
+    msg = lib.uocr_rocm_last_error().decode()
+    assert msg.startswith(name + ":") and detail in msg, msg
+    with pytest.raises(ValueError):
+        backend.check(status)
+
+
+FAKE = 0x10000  # an aligned non-null address; never dereferenced: validation fails first
+
+
+def test_shape_errors(backend):
+    _invalid(backend, "uocr_rocm_rms_norm", None, FAKE, FAKE, -1, 64, 1e-6, detail="rows")
+    _invalid(backend, "uocr_rocm_rms_norm_bf16", None, FAKE, FAKE, 4, 0, 1e-6, detail="cols")
+    _invalid(backend, "uocr_rocm_layer_norm", None, FAKE, FAKE, None, 4, 64, 1e-6, detail="null")
+    _invalid(backend, "uocr_rocm_add_rms_norm_bf16", None, FAKE, FAKE, FAKE, FAKE, 4, 64, 1e-6, detail="distinct")
+    _invalid(backend, "uocr_rocm_gelu_erf", None, FAKE, -5, detail="n")
+    _invalid(backend, "uocr_rocm_silu_mul", None, FAKE, FAKE, 8, detail="distinct")
+    _invalid(backend, "uocr_rocm_add_inplace", None, FAKE, FAKE, 8, detail="distinct")
+    _invalid(backend, "uocr_rocm_swiglu_bf16", None, FAKE, FAKE + 64, 4, 16, detail="overlap")
+    _invalid(backend, "uocr_rocm_swiglu", None, FAKE, FAKE, 4, 0, detail="ffn")
+
+
+def test_rope_errors(backend):
+    args = (None, FAKE, 1, 2)
+    _invalid(backend, "uocr_rocm_rope", *args, 7, None, None, FAKE, 3, None, 0, 0, 0, 0, detail="even")
+    _invalid(backend, "uocr_rocm_rope", *args, 8, None, None, FAKE, 3, None, 0, 0, 0, 0, detail="dim / 2")
+    _invalid(backend, "uocr_rocm_rope", *args, 1024, None, None, FAKE, 512, None, 0, 0, 0, 0, detail="512")
+    _invalid(backend, "uocr_rocm_rope_bf16", *args, 16, None, None, FAKE, 7, None, 1, 2, 0, 0, detail="inv_page")
+    _invalid(backend, "uocr_rocm_rope_qk_bf16", None, FAKE, 2, FAKE, 2, 1, 16, None, None, FAKE, 8, None, 0, 0, 0,
+             0, detail="distinct")
+    _invalid(backend, "uocr_rocm_rope_step", None, FAKE, 2, 16, None, FAKE, 8, None, 0, detail="state")
+    _invalid(backend, "uocr_rocm_rope_qk_step", None, FAKE, 2, FAKE, 1, 16, FAKE, FAKE, 9, None, 0,
+             detail="n_tok")
+
+
+def test_gather_errors(backend):
+    _invalid(backend, "uocr_rocm_gather_row_bf16", None, FAKE, 100, 100, 64, FAKE, detail="outside")
+    _invalid(backend, "uocr_rocm_gather_row_bf16", None, FAKE, 100, -1, 64, FAKE, detail="outside")
+    _invalid(backend, "uocr_rocm_gather_rows_bf16", None, FAKE, 100, None, 3, 64, FAKE, detail="index")
+    _invalid(backend, "uocr_rocm_embed_step", None, FAKE, 100, None, 64, FAKE, detail="state")
+    _invalid(backend, "uocr_rocm_gather_rows_bf16_bf16", None, FAKE, 100, FAKE, 3, 0, FAKE, detail="cols")
+
+
+def test_empty_shapes_are_noops(backend):
+    lib = backend.lib()
+    assert lib.uocr_rocm_rms_norm(None, None, None, 0, 64, 1e-6) == 0
+    assert lib.uocr_rocm_add_rms_norm_bf16(None, None, None, None, None, 0, 64, 1e-6) == 0
+    assert lib.uocr_rocm_layer_norm_bf16(None, None, None, None, 0, 0, 1e-6) == 0
+    assert lib.uocr_rocm_gelu_erf_bf16(None, None, 0) == 0
+    assert lib.uocr_rocm_swiglu_bf16(None, None, None, 0, 0) == 0
+    assert lib.uocr_rocm_rope_qk_bf16(None, None, 16, None, 4, 0, 128, None, None, None, 64, None, 0, 0, 0, 0) == 0
+    assert lib.uocr_rocm_gather_rows_bf16(None, None, 10, None, 0, 64, None) == 0
+    assert lib.uocr_rocm_copy(None, None, None, 0) == 0
+    assert lib.uocr_rocm_zero(None, 0, None) == 0
+    assert lib.uocr_rocm_memcpy(None, None, 0, backend.D2D, None) == 0
+
+
+def test_python_layer_rejects_mismatched_tensors(backend):
+    torch = pytest.importorskip("torch")
+    x = torch.zeros(4, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        backend.add_rms_norm(x, torch.zeros(4, 8), torch.ones(8), x.clone(), 1e-6)
+    with pytest.raises(ValueError):
+        backend.rms_norm(torch.zeros(4, 8, dtype=torch.float16), torch.ones(8), 1e-6)
+    with pytest.raises(ValueError):
+        backend.layer_norm(x, torch.ones(8, dtype=torch.bfloat16), torch.zeros(8), 1e-6)
