@@ -87,13 +87,18 @@ def bytes_gather(rows, cols, elem_out, elem_table=2):
 # ---- timing helpers ---------------------------------------------------------------------------------
 
 class Timer:
-    def __init__(self, torch, steps, warmup, replays=5):
+    def __init__(self, torch, steps, warmup, replays=5, use_graphs=True):
         self.torch, self.steps, self.warmup, self.replays = torch, steps, warmup, replays
+        self.use_graphs = use_graphs
 
     def graph(self, step_fns):
         """Median ms per step over `replays` replays of a graph holding
-        `steps` steps that rotate through step_fns (one per input set)."""
+        `steps` steps that rotate through step_fns (one per input set).
+        With graphs off (for counter collection), eager launches instead."""
         torch = self.torch
+        if not self.use_graphs:
+            ms = self.eager(step_fns)
+            return ms, ms, ms
         for i in range(self.warmup):
             step_fns[i % len(step_fns)]()
         torch.cuda.synchronize()
@@ -130,14 +135,29 @@ class Timer:
         return start.elapsed_time(end) / self.steps
 
 
-def n_sets(bytes_per_set):
-    return max(2, math.ceil(ROTATE_BYTES / max(bytes_per_set, 1)))
+def n_sets(footprint_bytes):
+    """Input sets needed so that one rotation touches more than ROTATE_BYTES."""
+    return max(2, math.ceil(ROTATE_BYTES / max(footprint_bytes, 1)))
 
 
 def report(name, nbytes, ms):
     gbps = nbytes / (ms * 1e-3) / 1e9
     return {"us": round(ms * 1e3, 3), "bytes": int(nbytes), "gbps": round(gbps, 1),
             "frac": round(gbps / PEAK_GBPS, 4)}
+
+
+def footprint(tensors):
+    return sum(t.numel() * t.element_size() for t in tensors)
+
+
+def time_kernel(timer, make_set, launch):
+    """Median ms per launch of `launch(set)` rotating over fresh input sets
+    whose footprint together exceeds ROTATE_BYTES."""
+    first = make_set()
+    sets = [first] + [make_set() for _ in range(n_sets(footprint(first)) - 1)]
+    ms = timer.graph([lambda s=s: launch(s) for s in sets])[0]
+    del sets, first
+    return ms
 
 
 # ---- workloads ------------------------------------------------------------------------------------------
@@ -150,16 +170,24 @@ def weights(torch, cols):
     return 1 + 0.02 * torch.randn(cols, device="cuda", dtype=torch.float32)
 
 
+def calibration(be, torch, timer):
+    """A plain device-to-device copy of 256 MiB (the runtime's copy kernel),
+    read + write bytes over time: the practical streaming ceiling."""
+    n = 64 * 2**20  # floats
+    pairs = [(torch.empty(n, device="cuda"), torch.empty(n, device="cuda")) for _ in range(3)]
+    for a, b in pairs:
+        a.normal_()
+    ms = timer.eager([lambda p=p: be.copy(p[1], p[0]) for p in pairs])
+    return {"workload": "device-to-device copy, 256 MiB", "step": report("copy", 2 * 4 * n, ms)}
+
+
 def config1(be, torch, timer):
     rows, cols = 1024, 2048
     nbytes = bytes_rms_norm(rows, cols, 4)
     w = weights(torch, cols)
-    sets = [torch.randn(rows, cols, device="cuda") for _ in range(n_sets(nbytes))]
-    fns = [lambda x=x: be.rms_norm(x, w, 1e-6) for x in sets]
-    ms, lo, hi = timer.graph(fns)
-    out = {"workload": "fp32 RMSNorm [1024, 2048]", "step": report("rms_norm fp32", nbytes, ms),
-           "kernels": {"rms_norm_f32": report("rms_norm fp32", nbytes, ms)}, "sets": len(sets)}
-    return out
+    ms = time_kernel(timer, lambda: torch.randn(rows, cols, device="cuda"), lambda x: be.rms_norm(x, w, 1e-6))
+    r = report("rms_norm fp32", nbytes, ms)
+    return {"workload": "fp32 RMSNorm [1024, 2048]", "step": r, "kernels": {"rms_norm_f32": r}}
 
 
 def config2(be, torch, timer):
@@ -198,40 +226,39 @@ def config2(be, torch, timer):
             "kernels": kern}
 
 
-def rope_sets(torch, rows, qh, kh, dim, count):
-    pos = torch.arange(rows, dtype=torch.int64, device="cuda")
-    return [(bf16_randn(torch, (rows, qh * dim)), bf16_randn(torch, (rows, kh * dim)), pos) for _ in range(count)]
+def rope_set(torch, rows, qh, kh, dim):
+    return (bf16_randn(torch, (rows, qh * dim)), bf16_randn(torch, (rows, kh * dim)),
+            torch.arange(rows, dtype=torch.int64, device="cuda"))
 
 
 def config3(be, torch, timer):
     rows, qh, kh, dim = 8192, 16, 4, 128
     nbytes = bytes_rope(rows, qh + kh, dim, 2)
     inv = torch.from_numpy(be.rope_inv(dim // 2, 1e4)).cuda()
-    sets = rope_sets(torch, rows, qh, kh, dim, n_sets(nbytes))
-    fns = [lambda s=s: be.rope_qk(s[0], qh, s[1], kh, dim, s[2], None, inv, None, 0) for s in sets]
-    ms, lo, hi = timer.graph(fns)
+    ms = time_kernel(timer, lambda: rope_set(torch, rows, qh, kh, dim),
+                     lambda s: be.rope_qk(s[0], qh, s[1], kh, dim, s[2], None, inv, None, 0))
     r = report("rope_qk", nbytes, ms)
     return {"workload": "bf16 prefill RoPE in place, Q [8192,16,128] K [8192,4,128]", "step": r,
-            "kernels": {"rope_qk_bf16": r}, "sets": len(sets)}
+            "kernels": {"rope_qk_bf16": r}}
 
 
 def config4(be, torch, timer):
     rows, cols = 4096, 1024
     ln_bytes, ge_bytes = bytes_layer_norm(rows, cols, 2), bytes_gelu(rows * cols, 2)
     w, b = weights(torch, cols), 0.02 * torch.randn(cols, device="cuda")
-    sets = [bf16_randn(torch, (rows, cols)) for _ in range(n_sets(ln_bytes))]
 
     def step(x):
         be.layer_norm(x, w, b, 1e-6)
         be.gelu_erf(x)
 
-    ms, lo, hi = timer.graph([lambda x=x: step(x) for x in sets])
-    ms_ln = timer.graph([lambda x=x: be.layer_norm(x, w, b, 1e-6) for x in sets])[0]
-    ms_ge = timer.graph([lambda x=x: be.gelu_erf(x) for x in sets])[0]
-    return {"workload": "bf16 vision LayerNorm [4096, 1024] then exact GELU", "sets": len(sets),
+    make = lambda: bf16_randn(torch, (rows, cols))  # noqa: E731
+    ms = time_kernel(timer, make, step)
+    ms_ln = time_kernel(timer, make, lambda x: be.layer_norm(x, w, b, 1e-6))
+    ms_ge = time_kernel(timer, make, lambda x: be.gelu_erf(x))
+    return {"workload": "bf16 vision LayerNorm [4096, 1024] then exact GELU",
             "step": report("ln+gelu", ln_bytes + ge_bytes, ms),
-            "kernels": {"layer_norm_bf16": report("ln", ln_bytes, ms_ln), "gelu_erf_bf16": report("gelu", ge_bytes,
-                                                                                                  ms_ge)}}
+            "kernels": {"layer_norm_bf16": report("ln", ln_bytes, ms_ln),
+                        "gelu_erf_bf16": report("gelu", ge_bytes, ms_ge)}}
 
 
 def config5(be, torch, timer):
@@ -242,33 +269,54 @@ def config5(be, torch, timer):
     total = b_norm + b_swi + b_rope
     w = weights(torch, hidden)
     inv = torch.from_numpy(be.rope_inv(dim // 2, 1e4)).cuda()
-    count = n_sets(total)
-    sets = []
-    for s in rope_sets(torch, rows, qh, kh, dim, count):
-        sets.append({"x": bf16_randn(torch, (rows, hidden)), "d": bf16_randn(torch, (rows, hidden)),
-                     "h": torch.empty(rows, hidden, dtype=torch.bfloat16, device="cuda"),
-                     "in": bf16_randn(torch, (rows, 2 * ffn)),
-                     "out": torch.empty(rows, ffn, dtype=torch.bfloat16, device="cuda"),
-                     "q": s[0], "k": s[1], "pos": s[2]})
 
-    def step(s):
+    def norm_set():
+        return {"x": bf16_randn(torch, (rows, hidden)), "d": bf16_randn(torch, (rows, hidden)),
+                "h": torch.empty(rows, hidden, dtype=torch.bfloat16, device="cuda")}
+
+    def swiglu_set():
+        return {"in": bf16_randn(torch, (rows, 2 * ffn)),
+                "out": torch.empty(rows, ffn, dtype=torch.bfloat16, device="cuda")}
+
+    def chain_set():
+        s = {**norm_set(), **swiglu_set()}
+        s["q"], s["k"], s["pos"] = rope_set(torch, rows, qh, kh, dim)
+        return s
+
+    def norm(s):
         be.add_rms_norm(s["x"], s["d"], w, s["h"], 1e-6)
+
+    def swiglu(s):
         be.swiglu(s["in"], s["out"])
+
+    def rope(s):
         be.rope_qk(s["q"], qh, s["k"], kh, dim, s["pos"], None, inv, None, 0)
 
+    def step(s):
+        norm(s)
+        swiglu(s)
+        rope(s)
+
+    first = chain_set()
+    sets = [first] + [chain_set() for _ in range(n_sets(footprint(first.values())) - 1)]
     ms, lo, hi = timer.graph([lambda s=s: step(s) for s in sets])
     ms_eager = timer.eager([lambda s=s: step(s) for s in sets])
+    nsets = len(sets)
+    del sets, first
     kern = {
-        "add_rms_norm_bf16": report("add_rms_norm", b_norm, timer.graph(
-            [lambda s=s: be.add_rms_norm(s["x"], s["d"], w, s["h"], 1e-6) for s in sets])[0]),
-        "swiglu_bf16": report("swiglu", b_swi, timer.graph([lambda s=s: be.swiglu(s["in"], s["out"]) for s in sets])[0]),
-        "rope_qk_bf16": report("rope_qk", b_rope, timer.graph(
-            [lambda s=s: be.rope_qk(s["q"], qh, s["k"], kh, dim, s["pos"], None, inv, None, 0) for s in sets])[0]),
+        "add_rms_norm_bf16": report("add_rms_norm", b_norm, time_kernel(
+            timer, lambda: tuple(norm_set().values()),
+            lambda s: be.add_rms_norm(s[0], s[1], w, s[2], 1e-6))),
+        "swiglu_bf16": report("swiglu", b_swi, time_kernel(
+            timer, lambda: tuple(swiglu_set().values()), lambda s: be.swiglu(s[0], s[1]))),
+        "rope_qk_bf16": report("rope_qk", b_rope, time_kernel(
+            timer, lambda: rope_set(torch, rows, qh, kh, dim),
+            lambda s: be.rope_qk(s[0], qh, s[1], kh, dim, s[2], None, inv, None, 0))),
     }
     return {"workload": "bf16 MoE-layer prefill chain, 8192 tokens: add+RMSNorm [8192,2048] -> SwiGLU "
                         "[8192,2x1408]->[8192,1408] -> RoPE Q[8192,16,128] K[8192,4,128]",
             "step": report("chain", total, ms), "ms_range": [round(lo, 5), round(hi, 5)],
-            "ms_per_step_eager": round(ms_eager, 5), "kernels": kern, "sets": len(sets)}
+            "ms_per_step_eager": round(ms_eager, 5), "kernels": kern, "sets": nsets}
 
 
 # ---- the CPU baseline (the reference's CPU path, restated in the oracle) ------------------------------
@@ -324,9 +372,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--configs", default="copy,1,2,3,4,5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly (for counter collection)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: every op is row-independent and this build measures one GPU's share "
@@ -342,8 +391,8 @@ def main():
     torch.cuda.set_device(0)
     torch.manual_seed(0)
     info = be.device_info(0)
-    timer = Timer(torch, args.steps, args.warmup)
-    runners = {"1": config1, "2": config2, "3": config3, "4": config4, "5": config5}
+    timer = Timer(torch, args.steps, args.warmup, use_graphs=not args.no_graph)
+    runners = {"1": config1, "2": config2, "3": config3, "4": config4, "5": config5, "copy": calibration}
     configs = {}
     for c in args.configs.split(","):
         t0 = time.time()

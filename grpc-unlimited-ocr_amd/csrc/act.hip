@@ -2,36 +2,70 @@
 // SwiGLU over a concatenated [gate | up] row, and the fp32 residual add.
 // fp32 and bf16 activations, fp32 arithmetic.
 //
-// Flat ops (gelu_erf, silu_mul, add_inplace) stream 128-bit chunks: each
-// thread owns kUnroll chunks spaced one workgroup apart, issues all of their
-// loads before any math, then stores. A ragged tail shorter than one chunk,
-// or any buffer not 16-byte aligned, takes the scalar path.
+// Flat ops (gelu_erf, silu_mul, add_inplace) stream 128-bit chunks, one per
+// thread, over a grid that covers the whole tensor in one pass. A ragged
+// tail shorter than one chunk, or any buffer not 16-byte aligned, takes the
+// scalar path.
 //
-// SwiGLU is row-shaped: one wave64 per row reads the row's gate half and up
-// half (chunks c = lane + 64 k) and writes one output row, so the gate/up
-// pair never round-trips through HBM between the activation and the product.
+// SwiGLU maps one thread to one 128-bit output chunk (row r, chunk j): it
+// reads chunk j of the row's gate half and of its up half and writes chunk
+// j of output row r, so the gate/up pair never round-trips through HBM
+// between the activation and the product. r and j come from the flat thread
+// index by a multiply-high with a host-computed reciprocal (no division in
+// the kernel).
 //
 // Arithmetic (reference: src/backend/reference/ops.cpp:40,151-167 and
-// src/model/feed_forward.cpp:18-24), each rounded where the reference
-// rounds (no FMA contraction):
-//   gelu_erf:  y = (0.5 v) (1 + erf(v * 0.70710678f))
-//   silu:      y = v (1 / (1 + exp(-v)));   silu_mul / swiglu: y = silu(g) u
+// src/model/feed_forward.cpp:18-24) in fp32:
+//   gelu_erf:  y = v Phi(v), Phi the standard normal CDF (= the reference's
+//              0.5 v (1 + erf(v / sqrt 2)))
+//   silu:      y = v / (1 + exp(-v));   silu_mul / swiglu: y = silu(g) u
+// The transcendentals run on the hardware's exp2 and reciprocal so that the
+// ops stay bound by HBM rather than by the fp32 ALUs.
 
 #include "common.hpp"
 
 namespace uocr_rocm {
 namespace {
 
-constexpr int kUnroll = 4;
+// One 128-bit chunk per thread: measured faster on MI355X than several
+// chunks per thread for these streaming shapes (more waves in flight).
+constexpr int kUnroll = 1;
 
-__device__ __forceinline__ float gelu_f(float v) {
-#pragma clang fp contract(off)
-  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+// GELU(x) = x Phi(x), Phi the standard normal CDF, from the upper tail
+// Q(t) = Phi(-t) = 2^P(t): Phi(x) = 1 - Q(|x|) for x >= 0 and Q(|x|) for
+// x < 0, with P a degree-10 polynomial of log2 Q on [0, 5.5] (a Chebyshev
+// fit; csrc/fit_normal_tail.py derives the coefficients and bounds the
+// error) and 2^y from v_exp_f32. The absolute error of Phi stays below 3e-8
+// and the negative side has no cancellation. Past x < -5.5 the result is
+// x * 0, which is what the reference's 0.5 x (1 + erff(x / sqrt 2)) gives
+// there once erff has rounded to -1 (src/backend/reference/ops.cpp:151-155).
+__device__ __forceinline__ float gelu_f(float x) {
+  constexpr float kT = 5.5f;
+  const float t = fminf(fabsf(x), kT);
+  float p = -1.725302567e-08f;
+  p = fmaf(p, t, 5.477549507e-07f);
+  p = fmaf(p, t, -7.458289474e-06f);
+  p = fmaf(p, t, 5.484473149e-05f);
+  p = fmaf(p, t, -2.005067072e-04f);
+  p = fmaf(p, t, -1.761470485e-04f);
+  p = fmaf(p, t, 7.180649787e-03f);
+  p = fmaf(p, t, -5.261564627e-02f);
+  p = fmaf(p, t, -4.591561556e-01f);
+  p = fmaf(p, t, -1.151113272e+00f);
+  p = fmaf(p, t, -9.999998212e-01f);
+  const float q = __builtin_amdgcn_exp2f(p);
+  float phi = x >= 0.0f ? 1.0f - q : q;
+  phi = x < -kT ? 0.0f : phi;
+  return x * phi;
 }
 
+// silu(g) u = g sigmoid(g) u with sigmoid(g) = 1 / (1 + e^-g); e^-g is
+// 2^(-g log2 e) on v_exp_f32 and the reciprocal is v_rcp_f32 (1 ulp each),
+// as in the reference's ops.cpp:40,163-167 and feed_forward.cpp:21-22.
+// g -> -inf gives 1 / inf = 0 and g * 0, as the reference does.
 __device__ __forceinline__ float silu_mul_f(float g, float u) {
-#pragma clang fp contract(off)
-  const float sig = 1.0f / (1.0f + expf(-g));
+  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
   return (g * sig) * u;
 }
 
@@ -115,41 +149,40 @@ int launch_flat(const char* what, void* stream, T* x, const T* y, int64_t n) {
 
 // ---- SwiGLU on [rows, 2 ffn] -> [rows, ffn] -------------------------------------
 
-template <class T, int VW, int ITERS>
-__global__ __launch_bounds__(kBlock) void swiglu_rows(const T* __restrict__ in, T* __restrict__ out, int64_t rows,
-                                                      int ffn) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-  if (row >= rows) return;
-  const int nvec = ffn / VW;
-  const T* gate = in + row * 2 * ffn;
-  const T* up = gate + ffn;
-  T* dst = out + row * ffn;
-  for (int base = 0; base < nvec; base += kWave * ITERS) {
-    Chunk<T, VW> cg[ITERS], cu[ITERS];
+// t / cpr for t < 2^32 as the high word of t * magic, magic = ceil(2^64 / cpr)
+// (exact for every t < 2^64 / cpr); cpr == 1 passes magic = 0.
+__device__ __forceinline__ uint32_t div_by_magic(uint32_t t, uint64_t magic) {
+  return magic == 0 ? t : static_cast<uint32_t>(__umul64hi(static_cast<uint64_t>(t), magic));
+}
+
+template <class T, int VW>
+__global__ __launch_bounds__(kBlock) void swiglu_flat(const T* __restrict__ in, T* __restrict__ out, uint32_t total,
+                                                      uint32_t cpr, uint64_t magic, int ffn) {
+  const uint32_t t = blockIdx.x * kBlock + threadIdx.x;
+  if (t >= total) return;
+  const uint32_t row = div_by_magic(t, magic);
+  const uint32_t j = t - row * cpr;
+  const T* gate = in + static_cast<uint64_t>(row) * 2 * ffn + static_cast<uint64_t>(j) * VW;
+  Chunk<T, VW> cg, cu;
+  cg.load(gate);
+  cu.load(gate + ffn);
+  float g[VW], u[VW];
+  cg.widen(g);
+  cu.widen(u);
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      const int v = base + lane + it * kWave;
-      if (v < nvec) {
-        cg[it].load(gate + v * VW);
-        cu[it].load(up + v * VW);
-      }
-    }
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      const int v = base + lane + it * kWave;
-      if (v < nvec) {
-        float g[VW], u[VW];
-        cg[it].widen(g);
-        cu[it].widen(u);
-#pragma unroll
-        for (int e = 0; e < VW; ++e) g[e] = silu_mul_f(g[e], u[e]);
-        Chunk<T, VW> o;
-        o.narrow(g);
-        o.store(dst + v * VW);
-      }
-    }
-  }
+  for (int e = 0; e < VW; ++e) g[e] = silu_mul_f(g[e], u[e]);
+  Chunk<T, VW> o;
+  o.narrow(g);
+  o.store(out + static_cast<uint64_t>(row) * ffn + static_cast<uint64_t>(j) * VW);
+}
+
+// ceil(2^64 / d) for 2 <= d < 2^32, as floor((2^64 - 1) / d) + 1: for d not
+// a power of two, d does not divide 2^64 and the floor equals floor(2^64 / d);
+// for d = 2^k the floor is 2^(64-k) - 1. Then floor(t * m / 2^64) = t / d for
+// every t < 2^32, because the excess t * (m - 2^64 / d) / 2^64 < 2^-32 < 1 / d.
+uint64_t reciprocal_magic(uint32_t d) {
+  if (d <= 1) return 0;
+  return ~uint64_t{0} / d + 1;
 }
 
 template <class T>
@@ -166,26 +199,20 @@ int launch_swiglu(const char* what, void* stream, const T* in, T* out, int64_t r
   }
   constexpr int kV = kVec<T>;
   const bool vec = ffn % kV == 0 && aligned16(in) && aligned16(out);
-  const int64_t nvec = vec ? ffn / kV : ffn;
-  int64_t iters = (nvec + kWave - 1) / kWave;
-  if (iters > 4) iters = 4;
+  const int64_t cpr = vec ? ffn / kV : ffn;
+  const int64_t total = rows * cpr;
+  UOCR_REQUIRE(total < (int64_t{1} << 32) - kBlock, what, "rows * ffn too large");
+  const uint32_t t32 = static_cast<uint32_t>(total), c32 = static_cast<uint32_t>(cpr);
+  const uint64_t magic = reciprocal_magic(c32);
+  const unsigned blocks = static_cast<unsigned>((total + kBlock - 1) / kBlock);
   const hipStream_t s = as_stream(stream);
-  const unsigned blocks = blocks_for_rows(rows);
   const int f = static_cast<int>(ffn);
   clear_launch_error();
-#define UOCR_SWIGLU_LAUNCH(VW)                                                          \
-  switch (iters) {                                                                      \
-    case 1: swiglu_rows<T, VW, 1><<<blocks, kBlock, 0, s>>>(in, out, rows, f); break;   \
-    case 2: swiglu_rows<T, VW, 2><<<blocks, kBlock, 0, s>>>(in, out, rows, f); break;   \
-    case 3: swiglu_rows<T, VW, 3><<<blocks, kBlock, 0, s>>>(in, out, rows, f); break;   \
-    default: swiglu_rows<T, VW, 4><<<blocks, kBlock, 0, s>>>(in, out, rows, f); break;  \
-  }
   if (vec) {
-    UOCR_SWIGLU_LAUNCH(kV)
+    swiglu_flat<T, kV><<<blocks, kBlock, 0, s>>>(in, out, t32, c32, magic, f);
   } else {
-    UOCR_SWIGLU_LAUNCH(1)
+    swiglu_flat<T, 1><<<blocks, kBlock, 0, s>>>(in, out, t32, c32, magic, f);
   }
-#undef UOCR_SWIGLU_LAUNCH
   return check_launch(what);
 }
 

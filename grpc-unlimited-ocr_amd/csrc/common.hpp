@@ -25,26 +25,38 @@ __device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float
 __device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
-// fp32 -> bf16, round to nearest even; a NaN keeps its sign and top payload
-// bits and gets the quiet bit (0x0040 of the bf16). This is the rounding the
-// reference defines for every bf16 value it stores (src/tensor/dtype.h:39-46).
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t nan = (u >> 16) | 0x40u;
-  return (u & 0x7fffffffu) > 0x7f800000u ? nan : rne;
-}
+// fp32 -> bf16 with gfx950's v_cvt_pk_bf16_f32, two values per instruction.
+// On every one of the 2^32 fp32 bit patterns it gives the reference's
+// rounding (src/tensor/dtype.h:39-46): nearest even, a NaN keeps its sign
+// and top payload bits and gets the quiet bit, denormals are kept
+// (tests/cpp/bf16_cvt_probe.hip checks all of them on the device).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return (f32_to_bf16_bits(lo) & 0xffffu) | (f32_to_bf16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return static_cast<uint16_t>(pack_bf16(f, 0.0f)); }
 
 // ---- row chunks -------------------------------------------------------------
 // A Chunk<T, VW> is VW consecutive elements of storage type T (float or
 // bf16 bits in uint16_t). VW = 16 / sizeof(T) is one 128-bit global load or
 // store (global_load_dwordx4); VW = 1 is the scalar path for rows whose width
-// or base address does not allow 16-byte chunks.
+// or base address does not allow 16-byte chunks. Activations are touched
+// once per op, so chunks move with nontemporal loads and stores (the `nt`
+// streaming hint), which keep them from displacing reused data in the
+// caches; norm weights and rope tables use ordinary loads.
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <class V>
+__device__ __forceinline__ V stream_load(const V* p) {
+  return __builtin_nontemporal_load(p);
+}
+template <class V>
+__device__ __forceinline__ void stream_store(V* p, V v) {
+  __builtin_nontemporal_store(v, p);
+}
 
 template <class T, int VW>
 struct Chunk;
@@ -52,8 +64,8 @@ struct Chunk;
 template <>
 struct Chunk<float, 4> {
   u32x4 raw;
-  __device__ __forceinline__ void load(const float* p) { raw = *reinterpret_cast<const u32x4*>(p); }
-  __device__ __forceinline__ void store(float* p) const { *reinterpret_cast<u32x4*>(p) = raw; }
+  __device__ __forceinline__ void load(const float* p) { raw = stream_load(reinterpret_cast<const u32x4*>(p)); }
+  __device__ __forceinline__ void store(float* p) const { stream_store(reinterpret_cast<u32x4*>(p), raw); }
   __device__ __forceinline__ void widen(float (&v)[4]) const {
     v[0] = __uint_as_float(raw.x);
     v[1] = __uint_as_float(raw.y);
@@ -69,8 +81,8 @@ struct Chunk<float, 4> {
 template <>
 struct Chunk<uint16_t, 8> {
   u32x4 raw;
-  __device__ __forceinline__ void load(const uint16_t* p) { raw = *reinterpret_cast<const u32x4*>(p); }
-  __device__ __forceinline__ void store(uint16_t* p) const { *reinterpret_cast<u32x4*>(p) = raw; }
+  __device__ __forceinline__ void load(const uint16_t* p) { raw = stream_load(reinterpret_cast<const u32x4*>(p)); }
+  __device__ __forceinline__ void store(uint16_t* p) const { stream_store(reinterpret_cast<u32x4*>(p), raw); }
   __device__ __forceinline__ void widen(float (&v)[8]) const {
     v[0] = bf16_lo(raw.x);
     v[1] = bf16_hi(raw.x);
@@ -90,8 +102,8 @@ struct Chunk<uint16_t, 8> {
 template <>
 struct Chunk<float, 1> {
   float raw;
-  __device__ __forceinline__ void load(const float* p) { raw = *p; }
-  __device__ __forceinline__ void store(float* p) const { *p = raw; }
+  __device__ __forceinline__ void load(const float* p) { raw = stream_load(p); }
+  __device__ __forceinline__ void store(float* p) const { stream_store(p, raw); }
   __device__ __forceinline__ void widen(float (&v)[1]) const { v[0] = raw; }
   __device__ __forceinline__ void narrow(const float (&v)[1]) { raw = v[0]; }
   __device__ __forceinline__ void clear() { raw = 0.0f; }
@@ -100,12 +112,10 @@ struct Chunk<float, 1> {
 template <>
 struct Chunk<uint16_t, 1> {
   uint16_t raw;
-  __device__ __forceinline__ void load(const uint16_t* p) { raw = *p; }
-  __device__ __forceinline__ void store(uint16_t* p) const { *p = raw; }
+  __device__ __forceinline__ void load(const uint16_t* p) { raw = stream_load(p); }
+  __device__ __forceinline__ void store(uint16_t* p) const { stream_store(p, raw); }
   __device__ __forceinline__ void widen(float (&v)[1]) const { v[0] = bf16_to_f32(raw); }
-  __device__ __forceinline__ void narrow(const float (&v)[1]) {
-    raw = static_cast<uint16_t>(f32_to_bf16_bits(v[0]));
-  }
+  __device__ __forceinline__ void narrow(const float (&v)[1]) { raw = f32_to_bf16(v[0]); }
   __device__ __forceinline__ void clear() { raw = 0; }
 };
 

@@ -38,14 +38,12 @@ __global__ __launch_bounds__(kBlock) void rms_rows(T* __restrict__ x, const T* _
 
   Chunk<T, VW> cx[VPL];
   Chunk<T, VW> cd[VPL];
-  float wv[VPL][VW];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = lane + k * kWave;
     if (v < nvec) {
       cx[k].load(x + off + static_cast<int64_t>(v) * VW);
       if constexpr (kAdd) cd[k].load(delta + off + static_cast<int64_t>(v) * VW);
-      load_f32<VW>(w + v * VW, wv[k]);
     }
   }
 
@@ -84,11 +82,15 @@ __global__ __launch_bounds__(kBlock) void rms_rows(T* __restrict__ x, const T* _
         xs.narrow(s[k]);
         xs.store(x + at);
       }
+      // w is read after the reduction: it is shared by every row (cache
+      // resident), and loading it late keeps the wave's register count low.
+      float wv[VW];
+      load_f32<VW>(w + v * VW, wv);
       float y[VW];
       {
 #pragma clang fp contract(off)
 #pragma unroll
-        for (int e = 0; e < VW; ++e) y[e] = wv[k][e] * (s[k][e] * inv);
+        for (int e = 0; e < VW; ++e) y[e] = wv[e] * (s[k][e] * inv);
       }
       Chunk<T, VW> o;
       o.narrow(y);
@@ -107,16 +109,10 @@ __global__ __launch_bounds__(kBlock) void ln_rows(T* __restrict__ x, const float
   const int64_t off = row * cols;
 
   Chunk<T, VW> cx[VPL];
-  float wv[VPL][VW];
-  float bv[VPL][VW];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = lane + k * kWave;
-    if (v < nvec) {
-      cx[k].load(x + off + static_cast<int64_t>(v) * VW);
-      load_f32<VW>(w + v * VW, wv[k]);
-      load_f32<VW>(b + v * VW, bv[k]);
-    }
+    if (v < nvec) cx[k].load(x + off + static_cast<int64_t>(v) * VW);
   }
 
   float s[VPL][VW];
@@ -151,11 +147,14 @@ __global__ __launch_bounds__(kBlock) void ln_rows(T* __restrict__ x, const float
   for (int k = 0; k < VPL; ++k) {
     const int v = lane + k * kWave;
     if (v < nvec) {
+      float wv[VW], bv[VW];
+      load_f32<VW>(w + v * VW, wv);
+      load_f32<VW>(b + v * VW, bv);
       float y[VW];
       {
 #pragma clang fp contract(off)
 #pragma unroll
-        for (int e = 0; e < VW; ++e) y[e] = (s[k][e] * inv) * wv[k][e] + bv[k][e];
+        for (int e = 0; e < VW; ++e) y[e] = (s[k][e] * inv) * wv[e] + bv[e];
       }
       Chunk<T, VW> o;
       o.narrow(y);

@@ -12,7 +12,8 @@
 //      the first half of head h and the same span of its second half. A lane
 //      loads both 128-bit chunks, reads its VW cos/sin values from LDS,
 //      rotates, and stores both chunks back, so Q/K make one HBM round trip.
-//      Up to ITERS chunk pairs per lane are loaded before any is rotated.
+//      Up to ITERS chunk pairs per lane are loaded before any is rotated, and
+//      the first ITERS are in flight while step 1 runs.
 //
 // Arithmetic (reference: src/model/page_rope.cpp:26-56 and the
 // uocr::cuda::rope coordinate rule, src/backend/cuda/ops.cu:134-151):
@@ -46,9 +47,46 @@ struct RopeArgs {
   int64_t one_tok;
   int64_t one_page;
   const uocr_rocm_step_state* state;
+  int cpp_shift;  // log2(chunk pairs per head) when that is a power of two
 };
 
-template <class T, int VW, int ITERS>
+// Chunk pair c of a row -> (head h, chunk j): a shift and a mask when the
+// chunk pairs per head are a power of two (kPow2), else a division.
+template <bool kPow2>
+__device__ __forceinline__ void split_chunk(int c, int cpp, int shift, int& h, int& j) {
+  if constexpr (kPow2) {
+    h = c >> shift;
+    j = c & (cpp - 1);
+  } else {
+    h = c / cpp;
+    j = c - h * cpp;
+  }
+}
+
+// Loads chunk pairs base + lane + 64 it (it < ITERS) of `row`; a pair past
+// the row's end, or on an inactive wave, gets at[it] = nullptr.
+template <class T, int VW, int ITERS, bool kPow2>
+__device__ __forceinline__ void load_pairs(const RopeArgs<T>& a, int64_t row, bool active, int lane, int base,
+                                           int total, int cpp, Chunk<T, VW> (&lo)[ITERS], Chunk<T, VW> (&hi)[ITERS],
+                                           T* (&at)[ITERS], int (&jj)[ITERS]) {
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int c = base + lane + it * kWave;
+    at[it] = nullptr;
+    jj[it] = 0;
+    if (active && c < total) {
+      int h, j;
+      split_chunk<kPow2>(c, cpp, a.cpp_shift, h, j);
+      T* head = h < a.heads0 ? a.x0 + (row * a.heads0 + h) * a.dim : a.x1 + (row * a.heads1 + (h - a.heads0)) * a.dim;
+      at[it] = head + j * VW;
+      jj[it] = j;
+      lo[it].load(at[it]);
+      hi[it].load(at[it] + a.half);
+    }
+  }
+}
+
+template <class T, int VW, int ITERS, bool kPow2>
 __global__ __launch_bounds__(kBlock) void rope_rows(RopeArgs<T> a) {
   __shared__ __attribute__((aligned(16))) float table[kWavesPerBlock][2][kMaxHalf];
   const int wave = threadIdx.x / kWave;
@@ -57,6 +95,15 @@ __global__ __launch_bounds__(kBlock) void rope_rows(RopeArgs<T> a) {
   const bool active = row < a.rows;
   float* cosv = table[wave][0];
   float* sinv = table[wave][1];
+  const int cpp = a.half / VW;  // chunk pairs per head
+  const int total = (a.heads0 + a.heads1) * cpp;
+
+  // The first batch of Q/K loads goes out before the row's cos/sin are
+  // computed, so the transcendentals overlap the memory latency.
+  Chunk<T, VW> lo[ITERS], hi[ITERS];
+  T* at[ITERS];
+  int jj[ITERS];
+  load_pairs<T, VW, ITERS, kPow2>(a, row, active, lane, 0, total, cpp, lo, hi, at, jj);
 
   if (active) {
     int64_t tk, pg;
@@ -81,27 +128,8 @@ __global__ __launch_bounds__(kBlock) void rope_rows(RopeArgs<T> a) {
   __syncthreads();
   if (!active) return;
 
-  const int cpp = a.half / VW;  // chunk pairs per head
-  const int total = (a.heads0 + a.heads1) * cpp;
   for (int base = 0; base < total; base += kWave * ITERS) {
-    Chunk<T, VW> lo[ITERS], hi[ITERS];
-    T* at[ITERS];
-    int jj[ITERS];
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      const int c = base + lane + it * kWave;
-      at[it] = nullptr;
-      if (c < total) {
-        const int h = c / cpp;
-        const int j = c - h * cpp;
-        T* head = h < a.heads0 ? a.x0 + (row * a.heads0 + h) * a.dim
-                               : a.x1 + (row * a.heads1 + (h - a.heads0)) * a.dim;
-        at[it] = head + j * VW;
-        jj[it] = j;
-        lo[it].load(at[it]);
-        hi[it].load(at[it] + a.half);
-      }
-    }
+    if (base > 0) load_pairs<T, VW, ITERS, kPow2>(a, row, active, lane, base, total, cpp, lo, hi, at, jj);
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       if (at[it] != nullptr) {
@@ -128,14 +156,26 @@ __global__ __launch_bounds__(kBlock) void rope_rows(RopeArgs<T> a) {
   }
 }
 
-template <class T, int VW>
-void launch_rope_vw(const RopeArgs<T>& a, int iters, hipStream_t s) {
+template <class T, int VW, bool kPow2>
+void launch_rope_iters(const RopeArgs<T>& a, int iters, hipStream_t s) {
   const unsigned blocks = blocks_for_rows(a.rows);
   switch (iters) {
-    case 1: rope_rows<T, VW, 1><<<blocks, kBlock, 0, s>>>(a); break;
-    case 2: rope_rows<T, VW, 2><<<blocks, kBlock, 0, s>>>(a); break;
-    case 3: rope_rows<T, VW, 3><<<blocks, kBlock, 0, s>>>(a); break;
-    default: rope_rows<T, VW, 4><<<blocks, kBlock, 0, s>>>(a); break;
+    case 1: rope_rows<T, VW, 1, kPow2><<<blocks, kBlock, 0, s>>>(a); break;
+    case 2: rope_rows<T, VW, 2, kPow2><<<blocks, kBlock, 0, s>>>(a); break;
+    case 3: rope_rows<T, VW, 3, kPow2><<<blocks, kBlock, 0, s>>>(a); break;
+    default: rope_rows<T, VW, 4, kPow2><<<blocks, kBlock, 0, s>>>(a); break;
+  }
+}
+
+template <class T, int VW>
+void launch_rope_vw(RopeArgs<T>& a, int iters, hipStream_t s) {
+  const int cpp = a.half / VW;
+  if ((cpp & (cpp - 1)) == 0) {
+    a.cpp_shift = __builtin_ctz(static_cast<unsigned>(cpp));
+    launch_rope_iters<T, VW, true>(a, iters, s);
+  } else {
+    a.cpp_shift = -1;
+    launch_rope_iters<T, VW, false>(a, iters, s);
   }
 }
 

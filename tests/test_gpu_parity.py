@@ -357,3 +357,19 @@ def test_cpp_rocm_ops_test(backend):
     r = subprocess.run([binary], capture_output=True, text=True, timeout=120)
     sys.stdout.write(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_rope_qk_with_k_below_q_in_memory(backend):
+    """Q and K as views of one buffer with K first: the kernel must not
+    assume any order between the two tensors."""
+    rows, dim = 23, 128
+    q, k = bf16(normal(70, (rows, 16 * dim))), bf16(normal(71, (rows, 4 * dim)))
+    pos = np.arange(rows, dtype=np.int64) * 911
+    inv = oracle.rope_inv(64, 1e4)
+    buf = torch.empty(rows * 20 * dim, dtype=torch.bfloat16, device="cuda")
+    dk, dq = buf[: rows * 4 * dim], buf[rows * 4 * dim:]
+    dk.copy_(dev_bf16(k).view(-1))
+    dq.copy_(dev_bf16(q).view(-1))
+    backend.rope_qk(dq, 16, dk, 4, dim, dev_i64(pos), None, dev_f32(inv), None, 0)
+    assert_bf16_close(host_bits(dq), oracle.rope(oracle.bf16_to_f32(q), 16, dim, tok=pos, inv_tok=inv), "q")
+    assert_bf16_close(host_bits(dk), oracle.rope(oracle.bf16_to_f32(k), 4, dim, tok=pos, inv_tok=inv), "k")
