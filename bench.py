@@ -365,6 +365,88 @@ def cpu_baseline(budget_s, threads):
             "value_1_thread": round(total / t_1 / 1e9, 3)}
 
 
+# ---- rocprofv3 summaries -------------------------------------------------------------------------------
+
+PROFILES = os.path.join(ROOT, "profiles")
+TRAFFIC_FILE = os.path.join(PROFILES, "pmc_traffic_workload5.md")
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+COPY_BYTES = 256 * 2**20  # the calibration copy: 256 MiB read and 256 MiB written per dispatch
+
+
+def _kernel_label(name):
+    import re
+
+    name = re.sub(r"uocr_rocm::\(anonymous namespace\)::", "", name)
+    name = re.sub(r"\)\s*\(.*$", ")", name) if "(Norm)" in name else re.sub(r"\(.*$", "", name)
+    return name.replace("void ", "").strip()
+
+
+def summarize_trace(trace_dir):
+    """Markdown table of per-kernel durations from a --kernel-trace run."""
+    import csv
+    import statistics as st
+
+    rows = list(csv.DictReader(open(os.path.join(trace_dir, "run_kernel_trace.csv"))))
+    by = {}
+    for r in rows:
+        key = (_kernel_label(r["Kernel_Name"]), r.get("Grid_Size", r.get("Grid_Size_X", "")),
+               r.get("Workgroup_Size", r.get("Workgroup_Size_X", "")))
+        by.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    out = ["| kernel | grid | block | calls | mean us | median us | min us |", "|---|---|---|---|---|---|---|"]
+    for (k, g, b), d in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        if k.startswith("at::") or "at::native" in k:
+            continue
+        out.append(f"| `{k}` | {g} | {b} | {len(d)} | {st.mean(d):.2f} | {st.median(d):.2f} | {min(d):.2f} |")
+    return "\n".join(out)
+
+
+def summarize_pmc(fetch_dir, write_dir):
+    """Markdown table of FETCH_SIZE / WRITE_SIZE (KiB per dispatch, median)
+    per kernel and grid, with both scaled by what the counters read for the
+    256 MiB calibration copy (known bytes / counter bytes)."""
+    import csv
+    import statistics as st
+
+    def load(d, counter):
+        by = {}
+        for r in csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))):
+            if r["Counter_Name"] != counter:
+                continue
+            key = (_kernel_label(r["Kernel_Name"]), r.get("Grid_Size", ""))
+            by.setdefault(key, []).append(float(r["Counter_Value"]))
+        return {k: st.median(v) for k, v in by.items()}
+
+    fetch, write = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
+    cf = [v for (k, g), v in fetch.items() if k == COPY_KERNEL]
+    cw = [v for (k, g), v in write.items() if k == COPY_KERNEL]
+    f_scale = COPY_BYTES / (max(cf) * 1024) if cf else 1.0
+    w_scale = COPY_BYTES / (max(cw) * 1024) if cw else 1.0
+    out = [f"FETCH_SIZE scale {f_scale:.4f}, WRITE_SIZE scale {w_scale:.4f} (256 MiB copy calibration)", "",
+           "| kernel | grid | FETCH KiB | WRITE KiB | traffic bytes (scaled) |", "|---|---|---|---|---|"]
+    for key in sorted(set(fetch) | set(write)):
+        k, g = key
+        if k.startswith("at::") or "at::native" in k:
+            continue
+        f, w = fetch.get(key, 0.0), write.get(key, 0.0)
+        traffic = int(round(f * 1024 * f_scale + w * 1024 * w_scale))
+        out.append(f"| `{k}` | {g} | {f:.1f} | {w:.1f} | {traffic} |")
+    return "\n".join(out)
+
+
+def committed_traffic(kernel_prefix, grid):
+    """Scaled HBM bytes per launch of a kernel from the committed PMC summary, or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
+        if len(cells) == 5 and cells[0].startswith(kernel_prefix) and cells[1] == str(grid):
+            try:
+                return int(cells[4])
+            except ValueError:
+                return None
+    return None
+
+
 # ---- main ---------------------------------------------------------------------------------------------------
 
 def main():
@@ -376,7 +458,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly (for counter collection)")
+    ap.add_argument("--summarize-trace", metavar="DIR", help="print a table from a rocprofv3 --kernel-trace run")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print a table from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return
+    if args.summarize_pmc:
+        print(summarize_pmc(*args.summarize_pmc))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: every op is row-independent and this build measures one GPU's share "
               f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
@@ -414,7 +505,9 @@ def main():
             "config": {"workload": head["workload"], "tokens": 8192, "hidden": 2048, "ffn": 1408,
                        "q_heads": 16, "kv_heads": 4, "head_dim": 128, "bytes_per_step": head["step"]["bytes"]},
             "roofline": {"bound": "hbm", "kernel": "add_rms_norm_bf16 [8192, 2048]", "achieved": dom["gbps"],
-                         "peak": PEAK_GBPS, "unit": "GB/s", "frac": dom["frac"], "traffic": None},
+                         "peak": PEAK_GBPS, "unit": "GB/s", "frac": dom["frac"],
+                         "traffic": committed_traffic("norm_rows<unsigned short, 8, 1, 4, (Norm)1>", 8192 * 64),
+                         "algorithmic_bytes": dom["bytes"]},
         })
     if not args.no_cpu and head is not None:
         threads = max(1, min(16, os.cpu_count() or 1))

@@ -1,12 +1,19 @@
 // norm.hip: RMSNorm, residual add fused with RMSNorm, and LayerNorm for
 // gfx950, fp32 and bf16 activations, fp32 arithmetic, fp32 norm weights.
 //
-// Layout: x [rows, cols] row-major. One wave64 owns one row: each lane holds
-// VPL 128-bit chunks of the row (chunk v = lane + 64 k) in registers, so the
-// row is read from HBM once and written once; the row statistics reduce
-// across the wave with DPP (wave_sum) and never touch LDS. Rows wider than
-// 16 chunks per lane take the *_wide kernels: one workgroup per row, a second
-// read of the row, and a 4-float LDS exchange between the four waves.
+// Layout: x [rows, cols] row-major, cut into 128-bit chunks (VW elements)
+// and the chunks into groups of 64 (one chunk per lane). A row is held in
+// registers by WPR waves (1, or 4 when there are too few rows to fill the
+// GPU with one wave per row): wave w owns groups w, w + WPR, w + 2 WPR, ...
+// so the row is read from HBM once and written once. Rows wider than 64
+// groups take the *_wide kernels: one workgroup per row and a second read of
+// the row.
+//
+// Reduction order: each group's sum is a lane sum over its VW elements in
+// order, then a DPP butterfly over the 64 lanes (wave_sum); the row's sum
+// folds the group sums left to right in group order (through LDS when
+// WPR > 1). The order depends only on cols, so a row's result is bitwise
+// the same whatever the number of rows in the call and whatever WPR.
 //
 // Arithmetic (reference: src/backend/reference/ops.cpp:111-141):
 //   rms_norm:    ss = sum x^2 (fp32), inv = float(1 / sqrt(ss / cols + eps))
@@ -16,149 +23,146 @@
 //                var, y = ((x - mean) * inv) * w + b.
 //   add_rms_norm: s = x + delta (fp32), x <- s, h <- w * (s * inv(s)).
 // The output expressions are evaluated without FMA contraction so that each
-// product and sum is rounded where the reference rounds it.
+// product and sum is rounded where the reference rounds it. Norm weights are
+// read after the reduction: they are shared by every row (cache resident)
+// and loading them late keeps the waves' register count low.
 
 #include "common.hpp"
 
 namespace uocr_rocm {
 namespace {
 
+enum class Norm { kRms, kAddRms, kLayer };
 
-// ---- register-resident rows ------------------------------------------------
+constexpr int kMaxGroups = 64;  // 4 waves x 16 chunks per lane
 
-template <class T, int VW, int VPL, bool kAdd>
-__global__ __launch_bounds__(kBlock) void rms_rows(T* __restrict__ x, const T* __restrict__ delta,
-                                                   const float* __restrict__ w, T* __restrict__ h, int64_t rows,
-                                                   int cols, float eps) {
+// Row totals from per-group partials. `part[k]` is this wave's lane partial
+// for group wr + WPR k; `red` is the row's LDS slot (kMaxGroups floats).
+template <int WPR, int VPL>
+__device__ __forceinline__ float fold_groups(const float (&part)[VPL], int wr, int groups, float* red) {
+  float g[VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) g[k] = wave_sum(part[k]);
+  if constexpr (WPR == 1) {
+    float total = g[0];
+#pragma unroll
+    for (int k = 1; k < VPL; ++k) {
+      if (k < groups) total += g[k];
+    }
+    return total;
+  } else {
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        const int grp = wr + WPR * k;
+        if (grp < groups) red[grp] = g[k];
+      }
+    }
+    __syncthreads();
+    float total = red[0];
+    for (int i = 1; i < groups; ++i) total += red[i];
+    __syncthreads();  // red is reused by the next fold
+    return total;
+  }
+}
+
+template <class T, int VW, int WPR, int VPL, Norm kMode>
+__global__ __launch_bounds__(kBlock) void norm_rows(T* __restrict__ x, const T* __restrict__ delta,
+                                                    const float* __restrict__ w, const float* __restrict__ b,
+                                                    T* __restrict__ h, int64_t rows, int cols, float eps) {
+  constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
+  __shared__ float red[kRowsPerBlock][kMaxGroups];
+  const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-  if (row >= rows) return;  // uniform across the wave
+  const int rloc = wave / WPR, wr = wave % WPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rloc;
+  // Waves past the last row still take part in the block's barriers.
+  const bool active = row < rows;
   const int nvec = cols / VW;
-  const int64_t off = row * cols;
+  const int groups = (nvec + kWave - 1) / kWave;
+  const int64_t off = (active ? row : 0) * cols;
 
   Chunk<T, VW> cx[VPL];
   Chunk<T, VW> cd[VPL];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * kWave;
-    if (v < nvec) {
+    const int v = (wr + WPR * k) * kWave + lane;
+    if (active && v < nvec) {
       cx[k].load(x + off + static_cast<int64_t>(v) * VW);
-      if constexpr (kAdd) cd[k].load(delta + off + static_cast<int64_t>(v) * VW);
+      if constexpr (kMode == Norm::kAddRms) cd[k].load(delta + off + static_cast<int64_t>(v) * VW);
     }
   }
 
   float s[VPL][VW];
-  float ss = 0.0f;
+  float part[VPL];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * kWave;
-    if (v < nvec) {
+    const int v = (wr + WPR * k) * kWave + lane;
+    part[k] = 0.0f;
+    if (active && v < nvec) {
       cx[k].widen(s[k]);
-      if constexpr (kAdd) {
+      if constexpr (kMode == Norm::kAddRms) {
         float d[VW];
         cd[k].widen(d);
 #pragma unroll
         for (int e = 0; e < VW; ++e) s[k][e] += d[e];
       }
 #pragma unroll
-      for (int e = 0; e < VW; ++e) ss += s[k][e] * s[k][e];
+      for (int e = 0; e < VW; ++e) part[k] += kMode == Norm::kLayer ? s[k][e] : s[k][e] * s[k][e];
     } else {
 #pragma unroll
       for (int e = 0; e < VW; ++e) s[k][e] = 0.0f;
     }
   }
-  ss = wave_sum(ss);
-  const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss) / static_cast<double>(cols) +
-                                                  static_cast<double>(eps)));
 
-  T* out = kAdd ? h : x;
+  float inv;
+  if constexpr (kMode == Norm::kLayer) {
+    const float mean = fold_groups<WPR, VPL>(part, wr, groups, red[rloc]) / static_cast<float>(cols);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int v = (wr + WPR * k) * kWave + lane;
+      part[k] = 0.0f;
+      if (active && v < nvec) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          s[k][e] -= mean;
+          part[k] += s[k][e] * s[k][e];
+        }
+      }
+    }
+    const float var = fold_groups<WPR, VPL>(part, wr, groups, red[rloc]) / static_cast<float>(cols);
+    inv = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + static_cast<double>(eps)));
+  } else {
+    const float ss = fold_groups<WPR, VPL>(part, wr, groups, red[rloc]);
+    inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss) / static_cast<double>(cols) +
+                                        static_cast<double>(eps)));
+  }
+  if (!active) return;
+
+  T* out = kMode == Norm::kAddRms ? h : x;
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * kWave;
+    const int v = (wr + WPR * k) * kWave + lane;
     if (v < nvec) {
       const int64_t at = off + static_cast<int64_t>(v) * VW;
-      if constexpr (kAdd) {
+      if constexpr (kMode == Norm::kAddRms) {
         Chunk<T, VW> xs;
         xs.narrow(s[k]);
         xs.store(x + at);
       }
-      // w is read after the reduction: it is shared by every row (cache
-      // resident), and loading it late keeps the wave's register count low.
-      float wv[VW];
+      float wv[VW], bv[VW], y[VW];
       load_f32<VW>(w + v * VW, wv);
-      float y[VW];
+      if constexpr (kMode == Norm::kLayer) load_f32<VW>(b + v * VW, bv);
       {
 #pragma clang fp contract(off)
 #pragma unroll
-        for (int e = 0; e < VW; ++e) y[e] = wv[e] * (s[k][e] * inv);
+        for (int e = 0; e < VW; ++e) {
+          y[e] = kMode == Norm::kLayer ? (s[k][e] * inv) * wv[e] + bv[e] : wv[e] * (s[k][e] * inv);
+        }
       }
       Chunk<T, VW> o;
       o.narrow(y);
       o.store(out + at);
-    }
-  }
-}
-
-template <class T, int VW, int VPL>
-__global__ __launch_bounds__(kBlock) void ln_rows(T* __restrict__ x, const float* __restrict__ w,
-                                                  const float* __restrict__ b, int64_t rows, int cols, float eps) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-  if (row >= rows) return;
-  const int nvec = cols / VW;
-  const int64_t off = row * cols;
-
-  Chunk<T, VW> cx[VPL];
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * kWave;
-    if (v < nvec) cx[k].load(x + off + static_cast<int64_t>(v) * VW);
-  }
-
-  float s[VPL][VW];
-  float sum = 0.0f;
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * kWave;
-    if (v < nvec) {
-      cx[k].widen(s[k]);
-#pragma unroll
-      for (int e = 0; e < VW; ++e) sum += s[k][e];
-    }
-  }
-  const float mean = wave_sum(sum) / static_cast<float>(cols);
-
-  float q = 0.0f;
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * kWave;
-    if (v < nvec) {
-#pragma unroll
-      for (int e = 0; e < VW; ++e) {
-        s[k][e] -= mean;
-        q += s[k][e] * s[k][e];
-      }
-    }
-  }
-  const float var = wave_sum(q) / static_cast<float>(cols);
-  const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + static_cast<double>(eps)));
-
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + k * kWave;
-    if (v < nvec) {
-      float wv[VW], bv[VW];
-      load_f32<VW>(w + v * VW, wv);
-      load_f32<VW>(b + v * VW, bv);
-      float y[VW];
-      {
-#pragma clang fp contract(off)
-#pragma unroll
-        for (int e = 0; e < VW; ++e) y[e] = (s[k][e] * inv) * wv[e] + bv[e];
-      }
-      Chunk<T, VW> o;
-      o.narrow(y);
-      o.store(x + off + static_cast<int64_t>(v) * VW);
     }
   }
 }
@@ -240,25 +244,17 @@ __global__ __launch_bounds__(kBlock) void ln_rows_wide(T* x, const float* w, con
 
 // ---- host dispatch -----------------------------------------------------------
 
-// Chunks per lane rounded up to the instantiated set.
-inline int vpl_bucket(int64_t nvec) {
-  const int64_t need = (nvec + kWave - 1) / kWave;
-  if (need <= 1) return 1;
-  if (need <= 2) return 2;
-  if (need <= 4) return 4;
-  if (need <= 8) return 8;
-  if (need <= 16) return 16;
-  return 0;  // wider than the registers hold
-}
+// Below this many rows one wave per row leaves most of the GPU idle, so
+// each row is spread over 4 waves instead.
+constexpr int64_t kFewRows = 2048;
 
-#define UOCR_VPL_SWITCH(VPL_VALUE, ...)            \
-  switch (VPL_VALUE) {                             \
-    case 1: { constexpr int VPL = 1; __VA_ARGS__; } break;   \
-    case 2: { constexpr int VPL = 2; __VA_ARGS__; } break;   \
-    case 4: { constexpr int VPL = 4; __VA_ARGS__; } break;   \
-    case 8: { constexpr int VPL = 8; __VA_ARGS__; } break;   \
-    default: { constexpr int VPL = 16; __VA_ARGS__; } break; \
-  }
+inline int vpl_bucket(int64_t groups) {
+  if (groups <= 1) return 1;
+  if (groups <= 2) return 2;
+  if (groups <= 4) return 4;
+  if (groups <= 8) return 8;
+  return 16;
+}
 
 int check_rows(const char* what, int64_t rows, int64_t cols) {
   UOCR_REQUIRE(rows >= 0, what, "rows must be >= 0");
@@ -268,54 +264,56 @@ int check_rows(const char* what, int64_t rows, int64_t cols) {
   return UOCR_ROCM_OK;
 }
 
-template <class T, bool kAdd>
-int launch_rms(const char* what, void* stream, T* x, const T* delta, const float* w, T* h, int64_t rows,
-               int64_t cols, float eps) {
+template <class T, int VW, int WPR, Norm kMode>
+void launch_norm_rows(int vpl, hipStream_t s, T* x, const T* delta, const float* w, const float* b, T* h,
+                      int64_t rows, int cols, float eps) {
+  constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
+  const unsigned blocks = static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+  switch (vpl) {
+    case 1: norm_rows<T, VW, WPR, 1, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
+    case 2: norm_rows<T, VW, WPR, 2, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
+    case 4: norm_rows<T, VW, WPR, 4, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
+    case 8: norm_rows<T, VW, WPR, 8, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
+    default: norm_rows<T, VW, WPR, 16, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
+  }
+}
+
+template <class T, Norm kMode>
+int launch_norm(const char* what, void* stream, T* x, const T* delta, const float* w, const float* b, T* h,
+                int64_t rows, int64_t cols, float eps) {
   if (int st = check_rows(what, rows, cols)) return st;
   if (rows == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(x != nullptr && w != nullptr, what, "null x or w");
-  if constexpr (kAdd) {
+  if constexpr (kMode == Norm::kLayer) UOCR_REQUIRE(b != nullptr, what, "null b");
+  if constexpr (kMode == Norm::kAddRms) {
     UOCR_REQUIRE(delta != nullptr && h != nullptr, what, "null delta or h");
     UOCR_REQUIRE(h != x && delta != x && h != delta, what, "x, delta and h must be distinct buffers");
   }
   constexpr int kV = kVec<T>;
-  const bool vec = cols % kV == 0 && aligned16(x) && aligned16(w) && (!kAdd || (aligned16(delta) && aligned16(h)));
+  const bool vec = cols % kV == 0 && aligned16(x) && aligned16(w) && (kMode != Norm::kLayer || aligned16(b)) &&
+                   (kMode != Norm::kAddRms || (aligned16(delta) && aligned16(h)));
   const int64_t nvec = vec ? cols / kV : cols;
-  const int bucket = vpl_bucket(nvec);
+  const int64_t groups = (nvec + kWave - 1) / kWave;
   const hipStream_t s = as_stream(stream);
   const int c32 = static_cast<int>(cols);
   clear_launch_error();
-  if (bucket == 0) {
-    rms_rows_wide<T, kAdd><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, delta, w, h, cols, eps);
-  } else if (vec) {
-    UOCR_VPL_SWITCH(bucket, (rms_rows<T, kV, VPL, kAdd><<<blocks_for_rows(rows), kBlock, 0, s>>>(
-                                x, delta, w, h, rows, c32, eps)))
-  } else {
-    UOCR_VPL_SWITCH(bucket, (rms_rows<T, 1, VPL, kAdd><<<blocks_for_rows(rows), kBlock, 0, s>>>(
-                                x, delta, w, h, rows, c32, eps)))
+  if (groups > kMaxGroups) {
+    if constexpr (kMode == Norm::kLayer) {
+      ln_rows_wide<T><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, w, b, cols, eps);
+    } else {
+      rms_rows_wide<T, kMode == Norm::kAddRms><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, delta, w, h, cols,
+                                                                                               eps);
+    }
+    return check_launch(what);
   }
-  return check_launch(what);
-}
-
-template <class T>
-int launch_ln(const char* what, void* stream, T* x, const float* w, const float* b, int64_t rows, int64_t cols,
-              float eps) {
-  if (int st = check_rows(what, rows, cols)) return st;
-  if (rows == 0) return UOCR_ROCM_OK;
-  UOCR_REQUIRE(x != nullptr && w != nullptr && b != nullptr, what, "null x, w or b");
-  constexpr int kV = kVec<T>;
-  const bool vec = cols % kV == 0 && aligned16(x) && aligned16(w) && aligned16(b);
-  const int64_t nvec = vec ? cols / kV : cols;
-  const int bucket = vpl_bucket(nvec);
-  const hipStream_t s = as_stream(stream);
-  const int c32 = static_cast<int>(cols);
-  clear_launch_error();
-  if (bucket == 0) {
-    ln_rows_wide<T><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, w, b, cols, eps);
-  } else if (vec) {
-    UOCR_VPL_SWITCH(bucket, (ln_rows<T, kV, VPL><<<blocks_for_rows(rows), kBlock, 0, s>>>(x, w, b, rows, c32, eps)))
+  const bool spread = groups > 16 || (rows < kFewRows && groups >= 4);
+  const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
+  if (vec) {
+    if (spread) launch_norm_rows<T, kV, 4, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps);
+    else launch_norm_rows<T, kV, 1, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps);
   } else {
-    UOCR_VPL_SWITCH(bucket, (ln_rows<T, 1, VPL><<<blocks_for_rows(rows), kBlock, 0, s>>>(x, w, b, rows, c32, eps)))
+    if (spread) launch_norm_rows<T, 1, 4, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps);
+    else launch_norm_rows<T, 1, 1, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps);
   }
   return check_launch(what);
 }
@@ -328,31 +326,36 @@ using namespace uocr_rocm;
 extern "C" {
 
 int uocr_rocm_rms_norm(void* stream, float* x, const float* w, int64_t rows, int64_t cols, float eps) {
-  return launch_rms<float, false>("uocr_rocm_rms_norm", stream, x, nullptr, w, nullptr, rows, cols, eps);
+  return launch_norm<float, Norm::kRms>("uocr_rocm_rms_norm", stream, x, nullptr, w, nullptr, nullptr, rows, cols,
+                                        eps);
 }
 
 int uocr_rocm_rms_norm_bf16(void* stream, uint16_t* x, const float* w, int64_t rows, int64_t cols, float eps) {
-  return launch_rms<uint16_t, false>("uocr_rocm_rms_norm_bf16", stream, x, nullptr, w, nullptr, rows, cols, eps);
+  return launch_norm<uint16_t, Norm::kRms>("uocr_rocm_rms_norm_bf16", stream, x, nullptr, w, nullptr, nullptr, rows,
+                                           cols, eps);
 }
 
 int uocr_rocm_add_rms_norm(void* stream, float* x, const float* delta, const float* w, float* h, int64_t rows,
                            int64_t cols, float eps) {
-  return launch_rms<float, true>("uocr_rocm_add_rms_norm", stream, x, delta, w, h, rows, cols, eps);
+  return launch_norm<float, Norm::kAddRms>("uocr_rocm_add_rms_norm", stream, x, delta, w, nullptr, h, rows, cols,
+                                           eps);
 }
 
 int uocr_rocm_add_rms_norm_bf16(void* stream, uint16_t* x, const uint16_t* delta, const float* w, uint16_t* h,
                                 int64_t rows, int64_t cols, float eps) {
-  return launch_rms<uint16_t, true>("uocr_rocm_add_rms_norm_bf16", stream, x, delta, w, h, rows, cols, eps);
+  return launch_norm<uint16_t, Norm::kAddRms>("uocr_rocm_add_rms_norm_bf16", stream, x, delta, w, nullptr, h, rows,
+                                              cols, eps);
 }
 
 int uocr_rocm_layer_norm(void* stream, float* x, const float* w, const float* b, int64_t rows, int64_t cols,
                          float eps) {
-  return launch_ln<float>("uocr_rocm_layer_norm", stream, x, w, b, rows, cols, eps);
+  return launch_norm<float, Norm::kLayer>("uocr_rocm_layer_norm", stream, x, nullptr, w, b, nullptr, rows, cols, eps);
 }
 
 int uocr_rocm_layer_norm_bf16(void* stream, uint16_t* x, const float* w, const float* b, int64_t rows, int64_t cols,
                               float eps) {
-  return launch_ln<uint16_t>("uocr_rocm_layer_norm_bf16", stream, x, w, b, rows, cols, eps);
+  return launch_norm<uint16_t, Norm::kLayer>("uocr_rocm_layer_norm_bf16", stream, x, nullptr, w, b, nullptr, rows,
+                                             cols, eps);
 }
 
 }  // extern "C"

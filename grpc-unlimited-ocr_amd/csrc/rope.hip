@@ -3,8 +3,8 @@
 //
 // Layout: X0 [rows, heads0 * dim] and X1 [rows, heads1 * dim] row-major (Q
 // and K of one attention layer; X1 may be absent). One wave64 owns one row
-// (token):
-//   1. The lanes compute the row's dim/2 (cos, sin) pairs, one sincosf per
+// (token), or two rows when the batch is long:
+//   1. The lanes compute each row's dim/2 (cos, sin) pairs, one sincosf per
 //      pair per row rather than per (row, head), into the wave's slice of
 //      LDS.
 //   2. The row's (heads0 + heads1) * dim / (2 VW) chunk pairs are spread
@@ -63,18 +63,23 @@ __device__ __forceinline__ void split_chunk(int c, int cpp, int shift, int& h, i
   }
 }
 
-// Loads chunk pairs base + lane + 64 it (it < ITERS) of `row`; a pair past
-// the row's end, or on an inactive wave, gets at[it] = nullptr.
-template <class T, int VW, int ITERS, bool kPow2>
-__device__ __forceinline__ void load_pairs(const RopeArgs<T>& a, int64_t row, bool active, int lane, int base,
-                                           int total, int cpp, Chunk<T, VW> (&lo)[ITERS], Chunk<T, VW> (&hi)[ITERS],
-                                           T* (&at)[ITERS], int (&jj)[ITERS]) {
+// Loads chunk pairs base + lane + 64 it (it < ITERS) of the wave's TPW rows
+// (row0, row0 + 1, ...; pair c belongs to row row0 + c / total); a pair past
+// the end gets at[it] = nullptr.
+template <class T, int VW, int ITERS, bool kPow2, int TPW>
+__device__ __forceinline__ void load_pairs(const RopeArgs<T> a, int64_t row0, int lane, int base, int total,
+                                           int cpp, Chunk<T, VW> (&lo)[ITERS], Chunk<T, VW> (&hi)[ITERS],
+                                           T* (&at)[ITERS], int (&jj)[ITERS], int (&tt)[ITERS]) {
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const int c = base + lane + it * kWave;
+    int c = base + lane + it * kWave;
+    const int t = TPW == 1 ? 0 : (c >= total ? 1 : 0);
+    c -= t * total;
+    const int64_t row = row0 + t;
     at[it] = nullptr;
     jj[it] = 0;
-    if (active && c < total) {
+    tt[it] = t;
+    if (row < a.rows && c < total) {
       int h, j;
       split_chunk<kPow2>(c, cpp, a.cpp_shift, h, j);
       T* head = h < a.heads0 ? a.x0 + (row * a.heads0 + h) * a.dim : a.x1 + (row * a.heads1 + (h - a.heads0)) * a.dim;
@@ -86,26 +91,30 @@ __device__ __forceinline__ void load_pairs(const RopeArgs<T>& a, int64_t row, bo
   }
 }
 
-template <class T, int VW, int ITERS, bool kPow2>
+// TPW rows (tokens) per wave: 2 for long prefill batches, so each lane
+// keeps more 128-bit loads in flight; 1 otherwise. The LDS table holds the
+// wave's TPW rows of cos/sin, sized at launch (kWavesPerBlock * TPW * 2 * half
+// floats).
+template <class T, int VW, int ITERS, bool kPow2, int TPW>
 __global__ __launch_bounds__(kBlock) void rope_rows(RopeArgs<T> a) {
-  __shared__ __attribute__((aligned(16))) float table[kWavesPerBlock][2][kMaxHalf];
+  extern __shared__ __attribute__((aligned(16))) float table[];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
-  const bool active = row < a.rows;
-  float* cosv = table[wave][0];
-  float* sinv = table[wave][1];
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave) * TPW;
+  const bool active = row0 < a.rows;
   const int cpp = a.half / VW;  // chunk pairs per head
-  const int total = (a.heads0 + a.heads1) * cpp;
+  const int total = (a.heads0 + a.heads1) * cpp;  // chunk pairs per row
+  float* wave_table = table + wave * TPW * 2 * a.half;
 
-  // The first batch of Q/K loads goes out before the row's cos/sin are
-  // computed, so the transcendentals overlap the memory latency.
-  Chunk<T, VW> lo[ITERS], hi[ITERS];
-  T* at[ITERS];
-  int jj[ITERS];
-  load_pairs<T, VW, ITERS, kPow2>(a, row, active, lane, 0, total, cpp, lo, hi, at, jj);
-
-  if (active) {
+  // Each row's rope coordinates, reduced to the two fp32 multipliers first,
+  // so that no 64-bit argument stays live across the load phase.
+  float ft[TPW], fp[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    ft[t] = 0.0f;
+    fp[t] = 0.0f;
+    const int64_t row = row0 + t;
+    if (row >= a.rows) continue;
     int64_t tk, pg;
     if (a.state != nullptr) {
       tk = a.state->tok;
@@ -115,24 +124,41 @@ __global__ __launch_bounds__(kBlock) void rope_rows(RopeArgs<T> a) {
       pg = a.page != nullptr ? a.page[row] : a.one_page;
     }
     if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
-    const float ft = static_cast<float>(tk);
-    const float fp = static_cast<float>(pg);
-    for (int p = lane; p < a.half; p += kWave) {
-      const float angle = p < a.n_tok ? ft * a.inv_tok[p] : fp * a.inv_page[p - a.n_tok];
-      float sn, cs;
-      sincosf(angle, &sn, &cs);
-      cosv[p] = cs;
-      sinv[p] = sn;
+    ft[t] = static_cast<float>(tk);
+    fp[t] = static_cast<float>(pg);
+  }
+
+  // The first batch of Q/K loads goes out before the rows' cos/sin are
+  // computed, so the transcendentals overlap the memory latency.
+  Chunk<T, VW> lo[ITERS], hi[ITERS];
+  T* at[ITERS];
+  int jj[ITERS], tt[ITERS];
+  load_pairs<T, VW, ITERS, kPow2, TPW>(a, row0, lane, 0, total, cpp, lo, hi, at, jj, tt);
+
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    if (row0 + t < a.rows) {
+      float* cosv = wave_table + t * 2 * a.half;
+      float* sinv = cosv + a.half;
+      for (int p = lane; p < a.half; p += kWave) {
+        const float angle = p < a.n_tok ? ft[t] * a.inv_tok[p] : fp[t] * a.inv_page[p - a.n_tok];
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        cosv[p] = cs;
+        sinv[p] = sn;
+      }
     }
   }
   __syncthreads();
   if (!active) return;
 
-  for (int base = 0; base < total; base += kWave * ITERS) {
-    if (base > 0) load_pairs<T, VW, ITERS, kPow2>(a, row, active, lane, base, total, cpp, lo, hi, at, jj);
+  for (int base = 0; base < TPW * total; base += kWave * ITERS) {
+    if (base > 0) load_pairs<T, VW, ITERS, kPow2, TPW>(a, row0, lane, base, total, cpp, lo, hi, at, jj, tt);
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       if (at[it] != nullptr) {
+        const float* cosv = wave_table + tt[it] * 2 * a.half;
+        const float* sinv = cosv + a.half;
         float va[VW], vb[VW], cs[VW], sn[VW];
         lo[it].widen(va);
         hi[it].widen(vb);
@@ -156,26 +182,41 @@ __global__ __launch_bounds__(kBlock) void rope_rows(RopeArgs<T> a) {
   }
 }
 
-template <class T, int VW, bool kPow2>
+template <class T, int VW, bool kPow2, int TPW>
 void launch_rope_iters(const RopeArgs<T>& a, int iters, hipStream_t s) {
-  const unsigned blocks = blocks_for_rows(a.rows);
+  const int64_t waves = (a.rows + TPW - 1) / TPW;
+  const unsigned blocks = static_cast<unsigned>((waves + kWavesPerBlock - 1) / kWavesPerBlock);
+  const size_t lds = static_cast<size_t>(kWavesPerBlock) * TPW * 2 * a.half * sizeof(float);
   switch (iters) {
-    case 1: rope_rows<T, VW, 1, kPow2><<<blocks, kBlock, 0, s>>>(a); break;
-    case 2: rope_rows<T, VW, 2, kPow2><<<blocks, kBlock, 0, s>>>(a); break;
-    case 3: rope_rows<T, VW, 3, kPow2><<<blocks, kBlock, 0, s>>>(a); break;
-    default: rope_rows<T, VW, 4, kPow2><<<blocks, kBlock, 0, s>>>(a); break;
+    case 1: rope_rows<T, VW, 1, kPow2, TPW><<<blocks, kBlock, lds, s>>>(a); break;
+    case 2: rope_rows<T, VW, 2, kPow2, TPW><<<blocks, kBlock, lds, s>>>(a); break;
+    case 3: rope_rows<T, VW, 3, kPow2, TPW><<<blocks, kBlock, lds, s>>>(a); break;
+    case 4: rope_rows<T, VW, 4, kPow2, TPW><<<blocks, kBlock, lds, s>>>(a); break;
+    case 5: rope_rows<T, VW, 5, kPow2, TPW><<<blocks, kBlock, lds, s>>>(a); break;
+    default: rope_rows<T, VW, 6, kPow2, TPW><<<blocks, kBlock, lds, s>>>(a); break;
   }
 }
 
+// Two rows per wave once there are enough rows to fill the GPU with half as
+// many waves, and when the two rows' chunk pairs fit in 6 loads per lane.
+constexpr int64_t kPairRows = 2048;
+
 template <class T, int VW>
-void launch_rope_vw(RopeArgs<T>& a, int iters, hipStream_t s) {
+void launch_rope_vw(RopeArgs<T>& a, hipStream_t s) {
   const int cpp = a.half / VW;
-  if ((cpp & (cpp - 1)) == 0) {
-    a.cpp_shift = __builtin_ctz(static_cast<unsigned>(cpp));
-    launch_rope_iters<T, VW, true>(a, iters, s);
+  const int total = (a.heads0 + a.heads1) * cpp;
+  const bool pow2 = (cpp & (cpp - 1)) == 0;
+  a.cpp_shift = pow2 ? __builtin_ctz(static_cast<unsigned>(cpp)) : -1;
+  const bool pair = a.rows >= kPairRows && 2 * total <= 6 * kWave;
+  const int per_wave = pair ? 2 * total : total;
+  int iters = (per_wave + kWave - 1) / kWave;
+  if (iters > 6) iters = 6;
+  if (pair) {
+    if (pow2) launch_rope_iters<T, VW, true, 2>(a, iters, s);
+    else launch_rope_iters<T, VW, false, 2>(a, iters, s);
   } else {
-    a.cpp_shift = -1;
-    launch_rope_iters<T, VW, false>(a, iters, s);
+    if (pow2) launch_rope_iters<T, VW, true, 1>(a, iters, s);
+    else launch_rope_iters<T, VW, false, 1>(a, iters, s);
   }
 }
 
@@ -217,15 +258,11 @@ int launch_rope(const char* what, void* stream, T* x0, int64_t heads0, T* x1, in
   constexpr int kV = kVec<T>;
   // 16-byte chunks need every head half to start on a 16-byte boundary.
   const bool vec = a.half % kV == 0 && aligned16(a.x0) && (a.x1 == nullptr || aligned16(a.x1));
-  const int vw = vec ? kV : 1;
-  const int64_t total = static_cast<int64_t>(a.heads0 + a.heads1) * (a.half / vw);
-  int64_t iters = (total + kWave - 1) / kWave;
-  if (iters > 4) iters = 4;
   clear_launch_error();
   if (vec) {
-    launch_rope_vw<T, kV>(a, static_cast<int>(iters), as_stream(stream));
+    launch_rope_vw<T, kV>(a, as_stream(stream));
   } else {
-    launch_rope_vw<T, 1>(a, static_cast<int>(iters), as_stream(stream));
+    launch_rope_vw<T, 1>(a, as_stream(stream));
   }
   return check_launch(what);
 }

@@ -373,3 +373,37 @@ def test_rope_qk_with_k_below_q_in_memory(backend):
     backend.rope_qk(dq, 16, dk, 4, dim, dev_i64(pos), None, dev_f32(inv), None, 0)
     assert_bf16_close(host_bits(dq), oracle.rope(oracle.bf16_to_f32(q), 16, dim, tok=pos, inv_tok=inv), "q")
     assert_bf16_close(host_bits(dk), oracle.rope(oracle.bf16_to_f32(k), 4, dim, tok=pos, inv_tok=inv), "k")
+
+
+@pytest.mark.parametrize("mode", ["rms", "add_rms", "layer"])
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_norm_rows_are_batch_invariant(backend, mode, dtype):
+    """A row's norm is bitwise the same whether it is normalised alone (the
+    kernel spreads a row over 4 waves) or in a 3000-row batch (one wave per
+    row): the reduction order depends only on cols."""
+    cols, rows = 2048, 3000
+    x, dl = normal(80, (rows, cols)), normal(81, (rows, cols))
+    w, b = weights(82, cols), (0.02 * normal(83, cols)).astype(np.float32)
+    if dtype == "bf16":
+        x, dl = oracle.bf16_round(x), oracle.bf16_round(dl)
+        dev = lambda a: dev_bf16(oracle.f32_to_bf16(a))  # noqa: E731
+        back = lambda t: oracle.bf16_to_f32(host_bits(t))  # noqa: E731
+    else:
+        dev, back = dev_f32, host_f32
+
+    def run(sl):
+        dx, dd = dev(x[sl]), dev(dl[sl])
+        h = torch.empty_like(dx)
+        if mode == "rms":
+            backend.rms_norm(dx, dev_f32(w), 1e-6)
+            return back(dx)
+        if mode == "layer":
+            backend.layer_norm(dx, dev_f32(w), dev_f32(b), 1e-6)
+            return back(dx)
+        backend.add_rms_norm(dx, dd, dev_f32(w), h, 1e-6)
+        return back(h)
+
+    full = run(slice(0, rows))
+    for r in (0, 1234, rows - 1):
+        alone = run(slice(r, r + 1))
+        assert np.array_equal(alone.view(np.uint32), full[r:r + 1].view(np.uint32)), (mode, dtype, r)

@@ -4,7 +4,9 @@ assembly hipcc writes for each source in grpc-unlimited-ocr_amd/csrc:
 * no write through the scalar data cache (scalar stores or atomics, its
   write-back or discard): every store is a vector memory instruction;
 * no packed fp32 arithmetic (v_pk_add_f32, v_pk_mul_f32, v_pk_fma_f32): the
-  build turns the packed-fp32 feature off and the kernels use scalar fp32."""
+  build turns the packed-fp32 feature off and the kernels use scalar fp32;
+* no private (scratch) memory traffic: register spills or an argument struct
+  copied to the stack would add HBM bytes to every wave."""
 
 import glob
 import os
@@ -20,6 +22,7 @@ SOURCES = sorted(glob.glob(os.path.join(PKG_DIR, "csrc", "*.hip")))
 SCALAR_WRITE = re.compile(r"^\s+s_(store|atomic|buffer_store|buffer_atomic|scratch_store|dcache_wb|dcache_discard)",
                           re.M)
 PACKED_FP32 = re.compile(r"^\s+v_pk_(add|mul|fma)_f32", re.M)
+SCRATCH = re.compile(r"^\s+scratch_(load|store)", re.M)
 
 
 @pytest.mark.parametrize("src", SOURCES, ids=[os.path.basename(s) for s in SOURCES])
@@ -33,3 +36,4 @@ def test_kernel_isa(src):
     assert "amdhsa" in asm or ".amdgcn_target" in asm
     assert not SCALAR_WRITE.search(asm), SCALAR_WRITE.search(asm).group(0)
     assert not PACKED_FP32.search(asm), PACKED_FP32.search(asm).group(0)
+    assert not SCRATCH.search(asm), SCRATCH.search(asm).group(0)
