@@ -21,9 +21,11 @@ sequence): algorithmic HBM bytes per step / time per step. Every workload's
 
 Timing: each workload keeps several input sets whose total exceeds 640 MB,
 more than twice the 256 MB Infinity Cache, and steps rotate through them, so
-every step reads from HBM. The K timed steps are captured once into a HIP
-graph and replayed; HIP events on the replay stream bracket the replay,
-with a device synchronisation on both sides. Per-kernel figures come from
+every step reads from HBM. After W untimed warm-up steps (which also bring
+the GPU clocks up), the K timed steps are captured once into a HIP graph and
+replayed; HIP events on the replay stream bracket each replay, with a device
+synchronisation on both sides, and the median of 5 replays is reported (each
+replay's time includes its one graph launch). Per-kernel figures come from
 the same procedure applied to one kernel.
 
 cpu_baseline: the reference's CPU path for workload 5 (the oracle's
@@ -452,8 +454,8 @@ def committed_traffic(kernel_prefix, grid):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--configs", default="copy,1,2,3,4,5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)

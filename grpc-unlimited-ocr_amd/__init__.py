@@ -108,6 +108,16 @@ _SIGNATURES = {
     "uocr_rocm_rope_qk_step_bf16": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_gather_rows_bf16_bf16": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp], _int),
     "uocr_rocm_embed_step_bf16": ([_vp, _vp, _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_router_norm": ([_vp, _vp, _vp, _i64, _i64, _f32], _int),
+    "uocr_rocm_router_norm_bf16": ([_vp, _vp, _vp, _i64, _i64, _f32], _int),
+    "uocr_rocm_quick_gelu": ([_vp, _vp, _i64], _int),
+    "uocr_rocm_quick_gelu_bf16": ([_vp, _vp, _i64], _int),
+    "uocr_rocm_softmax_rows": ([_vp, _vp, _i64, _i64], _int),
+    "uocr_rocm_scale_add_mask": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
+    "uocr_rocm_gemv_bf16": ([_vp, _vp, _i64, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_append_step": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
+    "uocr_rocm_attend_scratch_floats": ([_i64, _i64, _i64], _i64),
+    "uocr_rocm_attend_step": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -339,3 +349,83 @@ def rope_inv(n: int, theta: float):
 
     i = np.arange(n, dtype=np.float64)
     return (1.0 / np.power(np.float64(theta), i / np.float64(n))).astype(np.float32)
+
+
+# ---- row ops beside the path ---------------------------------------------------------
+
+
+def router_norm(x, w, eps, stream=None):
+    """In place router norm over the rows of x (fp32 or bf16): non-finite
+    inputs zeroed, scaled by (1 + w), clamped to +-1e4. Reference:
+    router_norm, src/backend/cuda/ops.h:35-36."""
+    rows, cols = _rows_cols(x)
+    name = "uocr_rocm_router_norm_bf16" if _is_bf16(x) else "uocr_rocm_router_norm"
+    _op(name, stream, _ptr(x), _f32_param(w), rows, cols, eps)
+
+
+def quick_gelu(x, stream=None):
+    """In place x * sigmoid(1.702 x) (fp32 or bf16). Reference: quick_gelu, ops.h:38."""
+    name = "uocr_rocm_quick_gelu_bf16" if _is_bf16(x) else "uocr_rocm_quick_gelu"
+    _op(name, stream, _ptr(x), x.numel())
+
+
+def softmax_rows(x, stream=None):
+    """In place softmax over each row of x (fp32); all -inf rows become zeros.
+    Reference: softmax_rows, ops.h:41-43."""
+    if _is_bf16(x):
+        raise ValueError("softmax_rows takes float32")
+    rows, cols = _rows_cols(x)
+    _op("uocr_rocm_softmax_rows", stream, _ptr(x), rows, cols)
+
+
+def scale_add_mask(x, scale, mask, batch, rows, cols, stream=None):
+    """x[b, r, c] = x[b, r, c] * scale + mask[r, c] (fp32; mask may be None).
+    Reference: scale_add_mask, ops.h:44-46."""
+    if _is_bf16(x):
+        raise ValueError("scale_add_mask takes float32")
+    if x.numel() != batch * rows * cols or (mask is not None and mask.numel() != rows * cols):
+        raise ValueError("x must hold batch * rows * cols and mask rows * cols elements")
+    _op("uocr_rocm_scale_add_mask", stream, _ptr(x), scale, _f32_param(mask), batch, rows, cols)
+
+
+# ---- decode-step neighbours ---------------------------------------------------------------
+
+
+def gemv_bf16(x, w, y, bias=None, stream=None):
+    """y[n] = bf16(x) . w[n] (+ bias): x float32 [k], w bfloat16 [n, k], y
+    float32 [n]. Reference: gemv_bf16, src/backend/cuda/gemv_ops.h:25-26."""
+    torch = _torch()
+    if w.dtype != torch.bfloat16 or x.dtype != torch.float32 or y.dtype != torch.float32:
+        raise ValueError("gemv_bf16 takes float32 x and y and bfloat16 w")
+    n, k = w.shape
+    if x.numel() != k or y.numel() != n or (bias is not None and bias.numel() != n):
+        raise ValueError("gemv_bf16 shapes: x [k], w [n, k], y [n], bias [n]")
+    _op("uocr_rocm_gemv_bf16", stream, _ptr(x), k, _ptr(w), n, _f32_param(bias), _ptr(y))
+
+
+def append_step(cache, row, state, capacity=None, stream=None):
+    """cache[state.pos] = row for a cache [capacity, width] (float32).
+    Reference: append_step, decode_ops.h:28-29."""
+    width = row.numel()
+    cap = cache.numel() // width if capacity is None and width else (-1 if capacity is None else capacity)
+    _op("uocr_rocm_append_step", stream, _ptr(cache), _ptr(row), width, _ptr(state), cap)
+
+
+def attend_scratch_floats(heads, hd, capacity) -> int:
+    """Floats of scratch that attend_step needs. Reference: decode_ops.h:42-43."""
+    return int(lib().uocr_rocm_attend_scratch_floats(heads, hd, capacity))
+
+
+def attend_step(q, k_cache, v_cache, heads, hd, mask, scale, state, scratch, out, stream=None):
+    """Masked attention of the one query q [heads * hd] over the keys
+    0..state.pos of k_cache / v_cache [capacity, heads * hd] (float32).
+    Reference: attend_step, decode_ops.h:44-47."""
+    capacity = k_cache.numel() // (heads * hd) if heads * hd else 0
+    if v_cache.numel() != k_cache.numel() or q.numel() != heads * hd or out.numel() != heads * hd:
+        raise ValueError("attend_step shapes: q, out [heads * hd]; k_cache, v_cache [capacity, heads * hd]")
+    if mask is not None and mask.numel() < capacity:
+        raise ValueError("mask must hold capacity floats")
+    if scratch.numel() < attend_scratch_floats(heads, hd, capacity):
+        raise ValueError("scratch is smaller than attend_scratch_floats(heads, hd, capacity)")
+    _op("uocr_rocm_attend_step", stream, _ptr(q), _ptr(k_cache), _ptr(v_cache), heads, hd, _f32_param(mask), scale,
+        _ptr(state), _ptr(scratch), capacity, _ptr(out))

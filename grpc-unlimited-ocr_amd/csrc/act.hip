@@ -69,9 +69,18 @@ __device__ __forceinline__ float silu_mul_f(float g, float u) {
   return (g * sig) * u;
 }
 
+// quick_gelu: v sigmoid(1.702 v) (src/backend/reference/ops.cpp:157-161), the
+// CLIP MLP's activation, on the same exp2 / reciprocal as silu.
+__device__ __forceinline__ float quick_gelu_f(float v) {
+  const float e = __builtin_amdgcn_exp2f(v * (-1.702f * 1.4426950408889634f));
+  return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // ---- flat ops ------------------------------------------------------------------
 
-enum class Flat { kGelu, kSiluMul, kAdd };
+enum class Flat { kGelu, kSiluMul, kAdd, kQuickGelu };
+
+constexpr bool unary(Flat op) { return op == Flat::kGelu || op == Flat::kQuickGelu; }
 
 // x (in place) op= y over n elements; y is unused by kGelu.
 template <Flat kOp, class T, int VW>
@@ -84,7 +93,7 @@ __global__ __launch_bounds__(kBlock) void flat_kernel(T* __restrict__ x, const T
     const int64_t i = first + static_cast<int64_t>(u) * kBlock;
     if (i < nvec) {
       cx[u].load(x + i * VW);
-      if constexpr (kOp != Flat::kGelu) cy[u].load(y + i * VW);
+      if constexpr (!unary(kOp)) cy[u].load(y + i * VW);
     }
   }
 #pragma unroll
@@ -93,10 +102,11 @@ __global__ __launch_bounds__(kBlock) void flat_kernel(T* __restrict__ x, const T
     if (i < nvec) {
       float a[VW], b[VW];
       cx[u].widen(a);
-      if constexpr (kOp != Flat::kGelu) cy[u].widen(b);
+      if constexpr (!unary(kOp)) cy[u].widen(b);
 #pragma unroll
       for (int e = 0; e < VW; ++e) {
         if constexpr (kOp == Flat::kGelu) a[e] = gelu_f(a[e]);
+        if constexpr (kOp == Flat::kQuickGelu) a[e] = quick_gelu_f(a[e]);
         if constexpr (kOp == Flat::kSiluMul) a[e] = silu_mul_f(a[e], b[e]);
         if constexpr (kOp == Flat::kAdd) a[e] = a[e] + b[e];
       }
@@ -113,11 +123,12 @@ __global__ __launch_bounds__(kBlock) void flat_kernel(T* __restrict__ x, const T
       c.load(x + i);
       float a[1], b[1];
       c.widen(a);
-      if constexpr (kOp != Flat::kGelu) {
+      if constexpr (!unary(kOp)) {
         d.load(y + i);
         d.widen(b);
       }
       if constexpr (kOp == Flat::kGelu) a[0] = gelu_f(a[0]);
+      if constexpr (kOp == Flat::kQuickGelu) a[0] = quick_gelu_f(a[0]);
       if constexpr (kOp == Flat::kSiluMul) a[0] = silu_mul_f(a[0], b[0]);
       if constexpr (kOp == Flat::kAdd) a[0] = a[0] + b[0];
       c.narrow(a);
@@ -130,9 +141,9 @@ template <Flat kOp, class T>
 int launch_flat(const char* what, void* stream, T* x, const T* y, int64_t n) {
   UOCR_REQUIRE(n >= 0, what, "n must be >= 0");
   if (n == 0) return UOCR_ROCM_OK;
-  UOCR_REQUIRE(x != nullptr && (kOp == Flat::kGelu || y != nullptr), what, "null pointer");
+  UOCR_REQUIRE(x != nullptr && (unary(kOp) || y != nullptr), what, "null pointer");
   constexpr int kV = kVec<T>;
-  const bool vec = aligned16(x) && (kOp == Flat::kGelu || aligned16(y));
+  const bool vec = aligned16(x) && (unary(kOp) || aligned16(y));
   const int64_t nvec = vec ? n / kV : n;
   int64_t blocks = (nvec + kBlock * kUnroll - 1) / (kBlock * kUnroll);
   if (blocks < 1) blocks = 1;
@@ -148,12 +159,6 @@ int launch_flat(const char* what, void* stream, T* x, const T* y, int64_t n) {
 }
 
 // ---- SwiGLU on [rows, 2 ffn] -> [rows, ffn] -------------------------------------
-
-// t / cpr for t < 2^32 as the high word of t * magic, magic = ceil(2^64 / cpr)
-// (exact for every t < 2^64 / cpr); cpr == 1 passes magic = 0.
-__device__ __forceinline__ uint32_t div_by_magic(uint32_t t, uint64_t magic) {
-  return magic == 0 ? t : static_cast<uint32_t>(__umul64hi(static_cast<uint64_t>(t), magic));
-}
 
 template <class T, int VW>
 __global__ __launch_bounds__(kBlock) void swiglu_flat(const T* __restrict__ in, T* __restrict__ out, uint32_t total,
@@ -174,15 +179,6 @@ __global__ __launch_bounds__(kBlock) void swiglu_flat(const T* __restrict__ in, 
   Chunk<T, VW> o;
   o.narrow(g);
   o.store(out + static_cast<uint64_t>(row) * ffn + static_cast<uint64_t>(j) * VW);
-}
-
-// ceil(2^64 / d) for 2 <= d < 2^32, as floor((2^64 - 1) / d) + 1: for d not
-// a power of two, d does not divide 2^64 and the floor equals floor(2^64 / d);
-// for d = 2^k the floor is 2^(64-k) - 1. Then floor(t * m / 2^64) = t / d for
-// every t < 2^32, because the excess t * (m - 2^64 / d) / 2^64 < 2^-32 < 1 / d.
-uint64_t reciprocal_magic(uint32_t d) {
-  if (d <= 1) return 0;
-  return ~uint64_t{0} / d + 1;
 }
 
 template <class T>
@@ -243,6 +239,14 @@ int uocr_rocm_gelu_erf(void* stream, float* x, int64_t n) {
 
 int uocr_rocm_gelu_erf_bf16(void* stream, uint16_t* x, int64_t n) {
   return launch_flat<Flat::kGelu, uint16_t>("uocr_rocm_gelu_erf_bf16", stream, x, nullptr, n);
+}
+
+int uocr_rocm_quick_gelu(void* stream, float* x, int64_t n) {
+  return launch_flat<Flat::kQuickGelu, float>("uocr_rocm_quick_gelu", stream, x, nullptr, n);
+}
+
+int uocr_rocm_quick_gelu_bf16(void* stream, uint16_t* x, int64_t n) {
+  return launch_flat<Flat::kQuickGelu, uint16_t>("uocr_rocm_quick_gelu_bf16", stream, x, nullptr, n);
 }
 
 int uocr_rocm_silu_mul(void* stream, float* g, const float* u, int64_t n) {

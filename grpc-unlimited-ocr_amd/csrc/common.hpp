@@ -166,6 +166,55 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Row totals over 64-chunk groups held by WPR waves (wave wr holds groups
+// wr, wr + WPR, ...; `part[k]` is this lane's partial for group wr + WPR k).
+// Each group reduces with one wave butterfly; the group results fold left to
+// right in group order (through the row's LDS slot `red`, kMaxGroups floats,
+// when WPR > 1), so the result depends only on the row, never on WPR. kMax
+// folds with max (an exact, order-free fold), else with +. Every wave of the
+// block must call it the same number of times.
+constexpr int kMaxGroups = 64;  // 4 waves x 16 chunks per lane
+
+template <int WPR, int VPL, bool kMax = false>
+__device__ __forceinline__ float fold_groups(const float (&part)[VPL], int wr, int groups, float* red) {
+  float g[VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) g[k] = kMax ? wave_max(part[k]) : wave_sum(part[k]);
+  if constexpr (WPR == 1) {
+    float total = g[0];
+#pragma unroll
+    for (int k = 1; k < VPL; ++k) {
+      if (k < groups) total = kMax ? fmaxf(total, g[k]) : total + g[k];
+    }
+    return total;
+  } else {
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        const int grp = wr + WPR * k;
+        if (grp < groups) red[grp] = g[k];
+      }
+    }
+    __syncthreads();
+    float total = red[0];
+    for (int i = 1; i < groups; ++i) total = kMax ? fmaxf(total, red[i]) : total + red[i];
+    __syncthreads();  // red is reused by the next fold
+    return total;
+  }
+}
+
 // Sum over the kBlock threads of a workgroup; `lds` holds kWavesPerBlock
 // floats. Every thread of the block must call it.
 __device__ __forceinline__ float block_sum(float v, float* lds) {
@@ -175,6 +224,42 @@ __device__ __forceinline__ float block_sum(float v, float* lds) {
   const float total = (lds[0] + lds[1]) + (lds[2] + lds[3]);
   __syncthreads();
   return total;
+}
+
+__device__ __forceinline__ float block_max(float v, float* lds) {
+  v = wave_max(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) lds[threadIdx.x / kWave] = v;
+  __syncthreads();
+  const float total = fmaxf(fmaxf(lds[0], lds[1]), fmaxf(lds[2], lds[3]));
+  __syncthreads();
+  return total;
+}
+
+// Rows below this count leave most of the GPU idle at one wave per row, so
+// row kernels spread each row over 4 waves instead.
+constexpr int64_t kFewRows = 2048;
+
+inline int vpl_bucket(int64_t groups) {
+  if (groups <= 1) return 1;
+  if (groups <= 2) return 2;
+  if (groups <= 4) return 4;
+  if (groups <= 8) return 8;
+  return 16;
+}
+
+// t / d for t < 2^32 as the high word of t * magic, magic = ceil(2^64 / d)
+// (reciprocal_magic); d == 1 passes magic = 0.
+__device__ __forceinline__ uint32_t div_by_magic(uint32_t t, uint64_t magic) {
+  return magic == 0 ? t : static_cast<uint32_t>(__umul64hi(static_cast<uint64_t>(t), magic));
+}
+
+// ceil(2^64 / d) for 2 <= d < 2^32, as floor((2^64 - 1) / d) + 1: for d not
+// a power of two, d does not divide 2^64 and the floor equals floor(2^64 / d);
+// for d = 2^k the floor is 2^(64-k) - 1. Then floor(t * m / 2^64) = t / d for
+// every t < 2^32, because the excess t * (m - 2^64 / d) / 2^64 < 2^-32 < 1 / d.
+inline uint64_t reciprocal_magic(uint32_t d) {
+  if (d <= 1) return 0;
+  return ~uint64_t{0} / d + 1;
 }
 
 // ---- host side ----------------------------------------------------------------

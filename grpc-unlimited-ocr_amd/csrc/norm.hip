@@ -22,6 +22,8 @@
 //                passes over the registers, fp32), inv as above in fp64 from
 //                var, y = ((x - mean) * inv) * w + b.
 //   add_rms_norm: s = x + delta (fp32), x <- s, h <- w * (s * inv(s)).
+//   router_norm: non-finite x count as 0; y = clamp(clamp(x inv) (1 + w))
+//                with clamp to [-1e4, 1e4] (src/model/decoder.cpp:20-34).
 // The output expressions are evaluated without FMA contraction so that each
 // product and sum is rounded where the reference rounds it. Norm weights are
 // read after the reduction: they are shared by every row (cache resident)
@@ -32,39 +34,13 @@
 namespace uocr_rocm {
 namespace {
 
-enum class Norm { kRms, kAddRms, kLayer };
+// kRouter: the router's RMSNorm (non-finite inputs count as 0, output
+// clamp(clamp(x inv, +-1e4) (1 + w), +-1e4); src/model/decoder.cpp:20-34).
+enum class Norm { kRms, kAddRms, kLayer, kRouter };
 
-constexpr int kMaxGroups = 64;  // 4 waves x 16 chunks per lane
+constexpr float kActClamp = 1.0e4f;
 
-// Row totals from per-group partials. `part[k]` is this wave's lane partial
-// for group wr + WPR k; `red` is the row's LDS slot (kMaxGroups floats).
-template <int WPR, int VPL>
-__device__ __forceinline__ float fold_groups(const float (&part)[VPL], int wr, int groups, float* red) {
-  float g[VPL];
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) g[k] = wave_sum(part[k]);
-  if constexpr (WPR == 1) {
-    float total = g[0];
-#pragma unroll
-    for (int k = 1; k < VPL; ++k) {
-      if (k < groups) total += g[k];
-    }
-    return total;
-  } else {
-    if ((threadIdx.x & (kWave - 1)) == 0) {
-#pragma unroll
-      for (int k = 0; k < VPL; ++k) {
-        const int grp = wr + WPR * k;
-        if (grp < groups) red[grp] = g[k];
-      }
-    }
-    __syncthreads();
-    float total = red[0];
-    for (int i = 1; i < groups; ++i) total += red[i];
-    __syncthreads();  // red is reused by the next fold
-    return total;
-  }
-}
+__device__ __forceinline__ float clamp_act(float v) { return fminf(fmaxf(v, -kActClamp), kActClamp); }
 
 template <class T, int VW, int WPR, int VPL, Norm kMode>
 __global__ __launch_bounds__(kBlock) void norm_rows(T* __restrict__ x, const T* __restrict__ delta,
@@ -106,6 +82,10 @@ __global__ __launch_bounds__(kBlock) void norm_rows(T* __restrict__ x, const T* 
         cd[k].widen(d);
 #pragma unroll
         for (int e = 0; e < VW; ++e) s[k][e] += d[e];
+      }
+      if constexpr (kMode == Norm::kRouter) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) s[k][e] = __builtin_isfinite(s[k][e]) ? s[k][e] : 0.0f;
       }
 #pragma unroll
       for (int e = 0; e < VW; ++e) part[k] += kMode == Norm::kLayer ? s[k][e] : s[k][e] * s[k][e];
@@ -157,7 +137,13 @@ __global__ __launch_bounds__(kBlock) void norm_rows(T* __restrict__ x, const T* 
 #pragma clang fp contract(off)
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
-          y[e] = kMode == Norm::kLayer ? (s[k][e] * inv) * wv[e] + bv[e] : wv[e] * (s[k][e] * inv);
+          if constexpr (kMode == Norm::kLayer) {
+            y[e] = (s[k][e] * inv) * wv[e] + bv[e];
+          } else if constexpr (kMode == Norm::kRouter) {
+            y[e] = clamp_act(clamp_act(s[k][e] * inv) * (1.0f + wv[e]));
+          } else {
+            y[e] = wv[e] * (s[k][e] * inv);
+          }
         }
       }
       Chunk<T, VW> o;
@@ -186,7 +172,7 @@ __device__ __forceinline__ void st1(T* p, float f) {
   c.store(p);
 }
 
-template <class T, bool kAdd>
+template <class T, bool kAdd, bool kRouter = false>
 __global__ __launch_bounds__(kBlock) void rms_rows_wide(T* x, const T* delta, const float* w, T* h, int64_t cols,
                                                         float eps) {
   __shared__ float red[kWavesPerBlock];
@@ -195,6 +181,7 @@ __global__ __launch_bounds__(kBlock) void rms_rows_wide(T* x, const T* delta, co
   for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
     float s = ld1(x + off + i);
     if constexpr (kAdd) s += ld1(delta + off + i);
+    if constexpr (kRouter) s = __builtin_isfinite(s) ? s : 0.0f;
     ss += s * s;
   }
   ss = block_sum(ss, red);
@@ -207,10 +194,11 @@ __global__ __launch_bounds__(kBlock) void rms_rows_wide(T* x, const T* delta, co
       s += ld1(delta + off + i);
       st1(x + off + i, s);
     }
+    if constexpr (kRouter) s = __builtin_isfinite(s) ? s : 0.0f;
     float y;
     {
 #pragma clang fp contract(off)
-      y = w[i] * (s * inv);
+      y = kRouter ? clamp_act(clamp_act(s * inv) * (1.0f + w[i])) : w[i] * (s * inv);
     }
     st1(out + off + i, y);
   }
@@ -243,18 +231,6 @@ __global__ __launch_bounds__(kBlock) void ln_rows_wide(T* x, const float* w, con
 }
 
 // ---- host dispatch -----------------------------------------------------------
-
-// Below this many rows one wave per row leaves most of the GPU idle, so
-// each row is spread over 4 waves instead.
-constexpr int64_t kFewRows = 2048;
-
-inline int vpl_bucket(int64_t groups) {
-  if (groups <= 1) return 1;
-  if (groups <= 2) return 2;
-  if (groups <= 4) return 4;
-  if (groups <= 8) return 8;
-  return 16;
-}
 
 int check_rows(const char* what, int64_t rows, int64_t cols) {
   UOCR_REQUIRE(rows >= 0, what, "rows must be >= 0");
@@ -301,8 +277,8 @@ int launch_norm(const char* what, void* stream, T* x, const T* delta, const floa
     if constexpr (kMode == Norm::kLayer) {
       ln_rows_wide<T><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, w, b, cols, eps);
     } else {
-      rms_rows_wide<T, kMode == Norm::kAddRms><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, delta, w, h, cols,
-                                                                                               eps);
+      rms_rows_wide<T, kMode == Norm::kAddRms, kMode == Norm::kRouter>
+          <<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, delta, w, h, cols, eps);
     }
     return check_launch(what);
   }
@@ -356,6 +332,16 @@ int uocr_rocm_layer_norm_bf16(void* stream, uint16_t* x, const float* w, const f
                               float eps) {
   return launch_norm<uint16_t, Norm::kLayer>("uocr_rocm_layer_norm_bf16", stream, x, nullptr, w, b, nullptr, rows,
                                              cols, eps);
+}
+
+int uocr_rocm_router_norm(void* stream, float* x, const float* w, int64_t rows, int64_t cols, float eps) {
+  return launch_norm<float, Norm::kRouter>("uocr_rocm_router_norm", stream, x, nullptr, w, nullptr, nullptr, rows,
+                                           cols, eps);
+}
+
+int uocr_rocm_router_norm_bf16(void* stream, uint16_t* x, const float* w, int64_t rows, int64_t cols, float eps) {
+  return launch_norm<uint16_t, Norm::kRouter>("uocr_rocm_router_norm_bf16", stream, x, nullptr, w, nullptr, nullptr,
+                                              rows, cols, eps);
 }
 
 }  // extern "C"

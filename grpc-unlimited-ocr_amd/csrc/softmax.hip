@@ -1,0 +1,210 @@
+// softmax.hip: row softmax and the attention scores' scale-and-mask for
+// gfx950, fp32. These are the row ops on either side of the attention
+// products in prefill and in the vision encoder (the reference's
+// softmax_rows and scale_add_mask, src/backend/cuda/ops.h:41-46).
+//
+// softmax_rows, layout as the norms (norm.hip): the row in registers, 64-
+// chunk groups, WPR waves per row (4 below kFewRows rows). Three steps over
+// the registers: the row max (an exact fold), e = exp(v - max) and its sum
+// (folded in group order, so the result is bitwise independent of WPR and of
+// the row count), then v = e / sum. Rows wider than the registers hold take
+// softmax_rows_wide (one workgroup per row, three reads of the row).
+//
+// Arithmetic (reference: src/backend/reference/ops.cpp:169-187): fp32 max;
+// exp(v - max) in fp32 (here 2^((v - max) log2 e) on v_exp_f32); sum in fp32
+// over the groups, inv = float(1 / sum) in fp64 as the reference forms it
+// from its fp64 total; a row whose max is -inf (fully masked) becomes zeros.
+//
+// scale_add_mask (src/backend/cuda/ops.cu:129-132): x[b, r, c] =
+// x[b, r, c] * scale + mask[r, c] over `batch` slices, one 128-bit chunk per
+// thread; the slice offset of a chunk comes from a multiply-high.
+
+#include "common.hpp"
+
+namespace uocr_rocm {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int VW, int WPR, int VPL>
+__global__ __launch_bounds__(kBlock) void softmax_rows_k(float* __restrict__ x, int64_t rows, int cols) {
+  constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
+  __shared__ float red[kRowsPerBlock][kMaxGroups];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int rloc = wave / WPR, wr = wave % WPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rloc;
+  const bool active = row < rows;
+  const int nvec = cols / VW;
+  const int groups = (nvec + kWave - 1) / kWave;
+  const int64_t off = (active ? row : 0) * cols;
+
+  Chunk<float, VW> cx[VPL];
+  float v[VPL][VW];
+  float part[VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int c = (wr + WPR * k) * kWave + lane;
+    if (active && c < nvec) cx[k].load(x + off + static_cast<int64_t>(c) * VW);
+  }
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int c = (wr + WPR * k) * kWave + lane;
+    part[k] = -INFINITY;
+    if (active && c < nvec) {
+      cx[k].widen(v[k]);
+#pragma unroll
+      for (int e = 0; e < VW; ++e) part[k] = fmaxf(part[k], v[k][e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) v[k][e] = -INFINITY;
+    }
+  }
+  const float peak = fold_groups<WPR, VPL, true>(part, wr, groups, red[rloc]);
+  const bool masked = peak == -INFINITY;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    part[k] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      v[k][e] = masked ? 0.0f : __builtin_amdgcn_exp2f((v[k][e] - peak) * kLog2e);
+      part[k] += v[k][e];
+    }
+  }
+  const float total = fold_groups<WPR, VPL>(part, wr, groups, red[rloc]);
+  if (!active) return;
+  const float inv = masked ? 0.0f : static_cast<float>(1.0 / static_cast<double>(total));
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int c = (wr + WPR * k) * kWave + lane;
+    if (c < nvec) {
+      float y[VW];
+#pragma unroll
+      for (int e = 0; e < VW; ++e) y[e] = v[k][e] * inv;
+      Chunk<float, VW> o;
+      o.narrow(y);
+      o.store(x + off + static_cast<int64_t>(c) * VW);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void softmax_rows_wide(float* x, int64_t cols) {
+  __shared__ float red[kWavesPerBlock];
+  float* row = x + static_cast<int64_t>(blockIdx.x) * cols;
+  float m = -INFINITY;
+  for (int64_t i = threadIdx.x; i < cols; i += kBlock) m = fmaxf(m, row[i]);
+  const float peak = block_max(m, red);
+  const bool masked = peak == -INFINITY;
+  float sum = 0.0f;
+  for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
+    sum += masked ? 0.0f : __builtin_amdgcn_exp2f((row[i] - peak) * kLog2e);
+  }
+  const float total = block_sum(sum, red);
+  const float inv = masked ? 0.0f : static_cast<float>(1.0 / static_cast<double>(total));
+  for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
+    row[i] = masked ? 0.0f : __builtin_amdgcn_exp2f((row[i] - peak) * kLog2e) * inv;
+  }
+}
+
+template <int VW, int WPR>
+void launch_softmax_rows(int vpl, hipStream_t s, float* x, int64_t rows, int cols) {
+  constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
+  const unsigned blocks = static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+  switch (vpl) {
+    case 1: softmax_rows_k<VW, WPR, 1><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
+    case 2: softmax_rows_k<VW, WPR, 2><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
+    case 4: softmax_rows_k<VW, WPR, 4><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
+    case 8: softmax_rows_k<VW, WPR, 8><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
+    default: softmax_rows_k<VW, WPR, 16><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
+  }
+}
+
+// ---- scale and mask -------------------------------------------------------------
+
+template <int VW>
+__global__ __launch_bounds__(kBlock) void scale_mask_k(float* __restrict__ x, float scale,
+                                                        const float* __restrict__ mask, uint32_t nchunks,
+                                                        uint32_t per_chunks, uint64_t magic) {
+  const uint32_t t = blockIdx.x * kBlock + threadIdx.x;
+  if (t >= nchunks) return;
+  Chunk<float, VW> c;
+  c.load(x + static_cast<uint64_t>(t) * VW);
+  float v[VW], m[VW];
+  c.widen(v);
+  if (mask != nullptr) {
+    const uint32_t slice = div_by_magic(t, magic);
+    load_f32<VW>(mask + static_cast<uint64_t>(t - slice * per_chunks) * VW, m);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VW; ++e) m[e] = 0.0f;
+  }
+  {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int e = 0; e < VW; ++e) v[e] = v[e] * scale + m[e];
+  }
+  c.narrow(v);
+  c.store(x + static_cast<uint64_t>(t) * VW);
+}
+
+}  // namespace
+}  // namespace uocr_rocm
+
+using namespace uocr_rocm;
+
+extern "C" {
+
+int uocr_rocm_softmax_rows(void* stream, float* x, int64_t rows, int64_t cols) {
+  const char* what = "uocr_rocm_softmax_rows";
+  UOCR_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), what, "rows must be in [0, 2^31)");
+  UOCR_REQUIRE(rows == 0 || (cols > 0 && cols < (int64_t{1} << 31)), what, "cols must be in [1, 2^31)");
+  if (rows == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(x != nullptr, what, "null x");
+  const bool vec = cols % 4 == 0 && aligned16(x);
+  const int64_t nvec = vec ? cols / 4 : cols;
+  const int64_t groups = (nvec + kWave - 1) / kWave;
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  if (groups > kMaxGroups) {
+    softmax_rows_wide<<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, cols);
+    return check_launch(what);
+  }
+  const bool spread = groups > 16 || (rows < kFewRows && groups >= 4);
+  const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
+  const int c32 = static_cast<int>(cols);
+  if (vec) {
+    if (spread) launch_softmax_rows<4, 4>(vpl, s, x, rows, c32);
+    else launch_softmax_rows<4, 1>(vpl, s, x, rows, c32);
+  } else {
+    if (spread) launch_softmax_rows<1, 4>(vpl, s, x, rows, c32);
+    else launch_softmax_rows<1, 1>(vpl, s, x, rows, c32);
+  }
+  return check_launch(what);
+}
+
+int uocr_rocm_scale_add_mask(void* stream, float* x, float scale, const float* mask, int64_t batch, int64_t rows,
+                             int64_t cols) {
+  const char* what = "uocr_rocm_scale_add_mask";
+  UOCR_REQUIRE(batch >= 0 && rows >= 0 && cols >= 0, what, "shape must be >= 0");
+  const int64_t per = rows * cols;
+  const int64_t total = batch * per;
+  if (total == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(x != nullptr, what, "null x");
+  UOCR_REQUIRE(total < (int64_t{1} << 32) - kBlock, what, "batch * rows * cols too large");
+  // 16-byte chunks when no chunk straddles two slices.
+  const bool vec = per % 4 == 0 && aligned16(x) && (mask == nullptr || aligned16(mask));
+  const int vw = vec ? 4 : 1;
+  const uint32_t nchunks = static_cast<uint32_t>(total / vw), per_chunks = static_cast<uint32_t>(per / vw);
+  const uint64_t magic = reciprocal_magic(per_chunks);
+  const unsigned blocks = (nchunks + kBlock - 1) / kBlock;
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  if (vec) {
+    scale_mask_k<4><<<blocks, kBlock, 0, s>>>(x, scale, mask, nchunks, per_chunks, magic);
+  } else {
+    scale_mask_k<1><<<blocks, kBlock, 0, s>>>(x, scale, mask, nchunks, per_chunks, magic);
+  }
+  return check_launch(what);
+}
+
+}  // extern "C"

@@ -254,6 +254,70 @@ UOCR_ROCM_API int uocr_rocm_gather_rows_bf16_bf16(void* stream, const uint16_t* 
 UOCR_ROCM_API int uocr_rocm_embed_step_bf16(void* stream, const uint16_t* table, int64_t table_rows,
                                             const uocr_rocm_step_state* state, int64_t cols, uint16_t* dst);
 
+/* ---- row ops beside the path ---------------------------------------------- */
+
+/* The MoE router's norm, in place per row of [rows, cols]: non-finite inputs
+ * become 0, inv = 1 / sqrt(mean(x^2) + eps), x = clamp(clamp(x * inv) *
+ * (1 + w)) with clamp to [-1e4, 1e4]. Replaces router_norm
+ * (src/backend/cuda/ops.h:35-36, ops.cu:39-81 mode 2; CPU form
+ * src/model/decoder.cpp:20-34). */
+UOCR_ROCM_API int uocr_rocm_router_norm(void* stream, float* x, const float* w, int64_t rows, int64_t cols, float eps);
+UOCR_ROCM_API int uocr_rocm_router_norm_bf16(void* stream, uint16_t* x, const float* w, int64_t rows, int64_t cols,
+                                             float eps);
+
+/* x = x * sigmoid(1.702 x), in place over n elements. Replaces quick_gelu
+ * (src/backend/cuda/ops.h:38). */
+UOCR_ROCM_API int uocr_rocm_quick_gelu(void* stream, float* x, int64_t n);
+UOCR_ROCM_API int uocr_rocm_quick_gelu_bf16(void* stream, uint16_t* x, int64_t n);
+
+/* Softmax over each row of x [rows, cols] in place (fp32 max, exp(x - max),
+ * fp32 total, 1 / total formed in fp64); a row that is all -inf becomes
+ * zeros. Replaces softmax_rows (src/backend/cuda/ops.h:41-43). */
+UOCR_ROCM_API int uocr_rocm_softmax_rows(void* stream, float* x, int64_t rows, int64_t cols);
+
+/* x[b, r, c] = x[b, r, c] * scale + mask[r, c] for each of `batch` slices of
+ * [rows, cols]; mask may be null (+ 0). batch * rows * cols < 2^32 - 256.
+ * Replaces scale_add_mask (src/backend/cuda/ops.h:44-46). */
+UOCR_ROCM_API int uocr_rocm_scale_add_mask(void* stream, float* x, float scale, const float* mask, int64_t batch,
+                                           int64_t rows, int64_t cols);
+
+/* ---- decode-step neighbours ---------------------------------------------------- */
+
+/* y[n] = bf16(x) . w[n, :] (+ bias[n]): x fp32 [k] rounded to bf16 (nearest
+ * even) before the product, w bf16 [n, k] row-major, fp32 accumulation; bias
+ * may be null. k <= 12288. Replaces gemv_bf16
+ * (src/backend/cuda/gemv_ops.h:25-26); the same product as linear with m = 1
+ * (src/backend/cuda/ops.h:14-17). */
+UOCR_ROCM_API int uocr_rocm_gemv_bf16(void* stream, const float* x, int64_t k, const uint16_t* w, int64_t n,
+                                      const float* bias, float* y);
+
+/* cache[state->pos, :] = row, rows `width` floats wide. With capacity >= 0 a
+ * position outside [0, capacity) writes nothing; capacity < 0 leaves the
+ * upper bound unchecked, as the reference does (a negative position never
+ * writes). Replaces append_step (src/backend/cuda/decode_ops.h:28-29). */
+UOCR_ROCM_API int uocr_rocm_append_step(void* stream, float* cache, const float* row, int64_t width,
+                                        const uocr_rocm_step_state* state, int64_t capacity);
+
+/* Floats of scratch that uocr_rocm_attend_step needs for (heads, hd,
+ * capacity); 0 for an empty shape. Replaces attend_scratch_floats
+ * (src/backend/cuda/decode_ops.h:42-43). */
+UOCR_ROCM_API int64_t uocr_rocm_attend_scratch_floats(int64_t heads, int64_t hd, int64_t capacity);
+
+/* Masked attention of one query over the keys 0..state->pos of a cache:
+ *   out[h] = sum_j p_j v[j, h],  p = softmax_j(q_h . k[j, h] * scale + mask[j])
+ * q [heads * hd]; k_cache, v_cache [capacity, heads * hd] with head h at
+ * column h * hd; mask [capacity] (null: no mask; -inf masks a key, which is
+ * then not read); out [heads * hd]. Keys past capacity are not read. Keys
+ * all masked give zeros. scratch holds uocr_rocm_attend_scratch_floats(heads,
+ * hd, capacity) floats and must not be shared by overlapping calls.
+ * 1 <= hd <= 256. Two launches whose shapes depend only on (heads, hd,
+ * capacity), so a captured step replays at every position. Replaces
+ * attend_step (src/backend/cuda/decode_ops.h:44-47). */
+UOCR_ROCM_API int uocr_rocm_attend_step(void* stream, const float* q, const float* k_cache, const float* v_cache,
+                                        int64_t heads, int64_t hd, const float* mask, float scale,
+                                        const uocr_rocm_step_state* state, float* scratch, int64_t capacity,
+                                        float* out);
+
 #ifdef __cplusplus
 }
 #endif

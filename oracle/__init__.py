@@ -62,6 +62,12 @@ def lib() -> ctypes.CDLL:
             "orc_embed": ([_vp, _vp, _i64, _i64, _vp], None),
             "orc_add_rms_norm": ([_vp, _vp, _vp, _vp, _i64, _i64, _f], None),
             "orc_swiglu": ([_vp, _vp, _i64, _i64], None),
+            "orc_router_norm": ([_vp, _vp, _i64, _i64, _f], None),
+            "orc_linear": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], None),
+            "orc_softmax_rows": ([_vp, _i64, _i64], None),
+            "orc_attention_one": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _f, _vp], None),
+            "orc_scale_add_mask": ([_vp, _f, _vp, _i64, _i64, _i64], None),
+            "orc_quick_gelu": ([_vp, _i64], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(h, name)
@@ -87,6 +93,10 @@ def ref_lib() -> Optional[ctypes.CDLL]:
             "ref_rope_tables": ([_i64, ctypes.c_double, ctypes.c_double, _i64, _vp, _vp], None),
             "ref_rope_apply": ([_vp, _i64, _i64, _i64, ctypes.c_double, ctypes.c_double, _i64, _i64, _vp, _vp],
                                None),
+            "ref_quick_gelu": ([_vp, _i64], None),
+            "ref_softmax_rows": ([_vp, _i64, _i64], None),
+            "ref_linear": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], None),
+            "ref_attention_head": ([_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _f, _vp], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(h, name)
@@ -227,3 +237,57 @@ def embed(table_bits, ids) -> np.ndarray:
     out = np.empty((ids.size, cols), dtype=np.float32)
     lib().orc_embed(_p(table_bits), _p(ids), ids.size, cols, _p(out))
     return out
+
+
+# ---- the decode-step neighbours and the row ops beside the path ---------------------------------
+
+
+def router_norm(x, w, eps: float) -> np.ndarray:
+    x = _f32(x)
+    w = _f32(w)
+    cols = x.shape[-1]
+    lib().orc_router_norm(_p(x), _p(w), x.size // cols, cols, eps)
+    return x
+
+
+def linear(x, w, bias=None) -> np.ndarray:
+    """x [m, k] times w [n, k] transposed (+ bias [n]): [m, n]."""
+    x = _f32(np.atleast_2d(x))
+    w = _f32(w)
+    b = None if bias is None else _f32(bias)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    lib().orc_linear(_p(x), m, k, _p(w), n, _p(b), _p(y))
+    return y
+
+
+def softmax_rows(x) -> np.ndarray:
+    x = _f32(x)
+    cols = x.shape[-1]
+    lib().orc_softmax_rows(_p(x), x.size // cols, cols)
+    return x
+
+
+def attention_one(q, k, v, heads: int, hd: int, bias=None, scale: float = 1.0) -> np.ndarray:
+    """One query per head over keys [keys, heads * hd] with an optional
+    [keys] additive mask shared by the heads: [heads * hd]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    keys = k.shape[0]
+    b = None if bias is None else _f32(bias)
+    out = np.empty(heads * hd, np.float32)
+    lib().orc_attention_one(_p(q), _p(k), _p(v), keys, heads * hd, heads, hd, _p(b), scale, _p(out))
+    return out
+
+
+def scale_add_mask(x, scale: float, mask, batch: int, rows: int, cols: int) -> np.ndarray:
+    x = _f32(x)
+    m = None if mask is None else _f32(mask)
+    lib().orc_scale_add_mask(_p(x), scale, _p(m), batch, rows, cols)
+    return x
+
+
+def quick_gelu(x) -> np.ndarray:
+    x = _f32(x)
+    lib().orc_quick_gelu(_p(x), x.size)
+    return x

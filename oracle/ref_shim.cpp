@@ -88,4 +88,35 @@ __attribute__((visibility("default"))) void ref_rope_apply(float* x, std::int64_
   unwrap(t, x);
 }
 
+__attribute__((visibility("default"))) void ref_quick_gelu(float* x, std::int64_t n) {
+  uocr::Tensor t = wrap(x, {n});
+  ref::quick_gelu(t);
+  unwrap(t, x);
+}
+
+__attribute__((visibility("default"))) void ref_softmax_rows(float* x, std::int64_t rows, std::int64_t cols) {
+  uocr::Tensor t = wrap(x, {rows, cols});
+  ref::softmax_rows(t);
+  unwrap(t, x);
+}
+
+// y [m, n] = linear(x [m, k], w [n, k], bias [n] or null).
+__attribute__((visibility("default"))) void ref_linear(const float* x, std::int64_t m, std::int64_t k, const float* w,
+                                                       std::int64_t n, const float* bias, float* y) {
+  const uocr::Tensor b = bias != nullptr ? wrap(bias, {n}) : uocr::Tensor();
+  const uocr::Tensor out = ref::linear(wrap(x, {m, k}), wrap(w, {n, k}), bias != nullptr ? &b : nullptr);
+  unwrap(out, y);
+}
+
+// out [lq, dv] = attention_head(q [lq, d], k [lk, d], v [lk, dv], bias [lq, lk] or null, scale).
+__attribute__((visibility("default"))) void ref_attention_head(const float* q, std::int64_t lq, const float* k,
+                                                               std::int64_t lk, std::int64_t d, const float* v,
+                                                               std::int64_t dv, const float* bias, float scale,
+                                                               float* out) {
+  const uocr::Tensor b = bias != nullptr ? wrap(bias, {lq, lk}) : uocr::Tensor();
+  const uocr::Tensor o = ref::attention_head(wrap(q, {lq, d}), wrap(k, {lk, d}), wrap(v, {lk, dv}),
+                                             bias != nullptr ? &b : nullptr, scale);
+  unwrap(o, out);
+}
+
 }  // extern "C"

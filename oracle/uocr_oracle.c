@@ -270,3 +270,125 @@ ORC_API void orc_swiglu(const float* in, float* out, int64_t rows, int64_t ffn) 
   orc_silu(out, rows * ffn);
   for (int64_t r = 0; r < rows; ++r) orc_mul_into(out + r * ffn, in + r * 2 * ffn + ffn, ffn);
 }
+
+/* ---- the decode-step neighbours and the row ops beside the path ---------- */
+
+/* dot (src/backend/reference/ops.cpp:23-38): eight fp32 partial sums in a
+ * fixed order, then ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) + tail. */
+static float ref_dot(const float* a, const float* b, int64_t n) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t i = 0;
+  for (; i + 8 <= n; i += 8) {
+    for (int lane = 0; lane < 8; ++lane) acc[lane] += a[i + lane] * b[i + lane];
+  }
+  float tail = 0.0f;
+  for (; i < n; ++i) tail += a[i] * b[i];
+  return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7])) + tail;
+}
+
+/* The router's RMSNorm (src/model/decoder.cpp:20-34): non-finite inputs
+ * become 0, ss in fp64, inv = float(1 / sqrt(ss / c + eps)), then
+ * n = clamp(v * inv, -1e4, 1e4) and v = clamp(n * (1 + w), -1e4, 1e4). */
+ORC_API void orc_router_norm(float* x, const float* w, int64_t rows, int64_t cols, float eps) {
+  const float clampv = 1.0e4f;
+  for (int64_t r = 0; r < rows; ++r) {
+    float* v = x + r * cols;
+    double ss = 0.0;
+    for (int64_t i = 0; i < cols; ++i) {
+      if (!isfinite(v[i])) v[i] = 0.0f;
+      ss += (double)v[i] * v[i];
+    }
+    const float inv = (float)(1.0 / sqrt(ss / (double)cols + eps));
+    for (int64_t i = 0; i < cols; ++i) {
+      float n = v[i] * inv;
+      n = n < -clampv ? -clampv : (n > clampv ? clampv : n);
+      float y = n * (1.0f + w[i]);
+      v[i] = y < -clampv ? -clampv : (y > clampv ? clampv : y);
+    }
+  }
+}
+
+/* linear (ops.cpp:91-109): y[m, n] = dot(x[m], w[n]) (+ bias[n]). The
+ * reference's bf16 device paths are compared against this on bf16-rounded
+ * x and w (tests/cuda_ops_test.cpp:73-80). */
+ORC_API void orc_linear(const float* x, int64_t m, int64_t k, const float* w, int64_t n, const float* bias, float* y) {
+  for (int64_t r = 0; r < m; ++r) {
+    for (int64_t c = 0; c < n; ++c) {
+      const float sum = ref_dot(x + r * k, w + c * k, k);
+      y[r * n + c] = bias != NULL ? sum + bias[c] : sum;
+    }
+  }
+}
+
+/* softmax_rows (ops.cpp:169-187): fp32 max, v = exp(v - peak) in fp32,
+ * total in fp64, inv = float(1 / total), v *= inv; a row whose max is -inf
+ * (fully masked) becomes zeros. */
+ORC_API void orc_softmax_rows(float* x, int64_t rows, int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r) {
+    float* v = x + r * cols;
+    float peak = -INFINITY;
+    for (int64_t i = 0; i < cols; ++i) peak = v[i] > peak ? v[i] : peak;
+    if (peak == -INFINITY) {
+      for (int64_t i = 0; i < cols; ++i) v[i] = 0.0f;
+      continue;
+    }
+    double total = 0.0;
+    for (int64_t i = 0; i < cols; ++i) {
+      v[i] = expf(v[i] - peak);
+      total += v[i];
+    }
+    const float inv = (float)(1.0 / total);
+    for (int64_t i = 0; i < cols; ++i) v[i] *= inv;
+  }
+}
+
+/* attention_head (ops.cpp:219-251) for one query row per head: for head h,
+ * s_j = dot(q_h, k_j,h) * scale (+ bias[j]), softmax as above but with the
+ * probabilities p_j = exp(s_j - peak) * inv applied to v, out_h = sum p_j v_j,h;
+ * all keys masked gives zeros. q [heads * hd]; k, v [keys, width] with head
+ * h at column h * hd; bias [keys] shared by the heads (the decode-step mask);
+ * out [heads * hd]. */
+ORC_API void orc_attention_one(const float* q, const float* k, const float* v, int64_t keys, int64_t width,
+                               int64_t heads, int64_t hd, const float* bias, float scale, float* out) {
+  float* scores = (float*)malloc((size_t)(keys > 0 ? keys : 1) * sizeof(float));
+  float* kh = (float*)malloc((size_t)(hd > 0 ? hd : 1) * sizeof(float));
+  for (int64_t h = 0; h < heads; ++h) {
+    float* o = out + h * hd;
+    for (int64_t e = 0; e < hd; ++e) o[e] = 0.0f;
+    float peak = -INFINITY;
+    for (int64_t j = 0; j < keys; ++j) {
+      for (int64_t e = 0; e < hd; ++e) kh[e] = k[j * width + h * hd + e];
+      float s = ref_dot(q + h * hd, kh, hd) * scale;
+      if (bias != NULL) s += bias[j];
+      scores[j] = s;
+      peak = s > peak ? s : peak;
+    }
+    if (peak == -INFINITY) continue;
+    double total = 0.0;
+    for (int64_t j = 0; j < keys; ++j) {
+      scores[j] = expf(scores[j] - peak);
+      total += scores[j];
+    }
+    const float inv = (float)(1.0 / total);
+    for (int64_t j = 0; j < keys; ++j) {
+      const float p = scores[j] * inv;
+      for (int64_t e = 0; e < hd; ++e) o[e] += p * v[j * width + h * hd + e];
+    }
+  }
+  free(kh);
+  free(scores);
+}
+
+/* scale_add_mask (src/backend/cuda/ops.cu:129-132,348-352): for each of
+ * `batch` slices of [rows, cols], x = x * scale + mask[r, c] (mask NULL: + 0). */
+ORC_API void orc_scale_add_mask(float* x, float scale, const float* mask, int64_t batch, int64_t rows, int64_t cols) {
+  const int64_t per = rows * cols;
+  for (int64_t b = 0; b < batch; ++b) {
+    for (int64_t i = 0; i < per; ++i) x[b * per + i] = x[b * per + i] * scale + (mask != NULL ? mask[i] : 0.0f);
+  }
+}
+
+/* quick_gelu (ops.cpp:157-161): v * sigmoid(1.702 v). */
+ORC_API void orc_quick_gelu(float* x, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) x[i] = x[i] * sigmoid(1.702f * x[i]);
+}

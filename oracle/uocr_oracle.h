@@ -31,6 +31,13 @@ void orc_rope_apply(float* x, int64_t rows, int64_t heads, int64_t dim, const in
 void orc_embed(const uint16_t* table, const int64_t* ids, int64_t n, int64_t cols, float* dst);
 void orc_add_rms_norm(float* x, const float* delta, const float* w, float* h, int64_t rows, int64_t cols, float eps);
 void orc_swiglu(const float* in, float* out, int64_t rows, int64_t ffn);
+void orc_router_norm(float* x, const float* w, int64_t rows, int64_t cols, float eps);
+void orc_linear(const float* x, int64_t m, int64_t k, const float* w, int64_t n, const float* bias, float* y);
+void orc_softmax_rows(float* x, int64_t rows, int64_t cols);
+void orc_attention_one(const float* q, const float* k, const float* v, int64_t keys, int64_t width, int64_t heads,
+                       int64_t hd, const float* bias, float scale, float* out);
+void orc_scale_add_mask(float* x, float scale, const float* mask, int64_t batch, int64_t rows, int64_t cols);
+void orc_quick_gelu(float* x, int64_t n);
 
 #ifdef __cplusplus
 }

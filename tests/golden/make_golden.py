@@ -65,6 +65,30 @@ def main():
     bf = np.array([ref.ref_f32_to_bf16(np.float32(v)) for v in bits.view(np.float32)], np.uint16)
     out.update(bf16_in=bits, bf16_out=bf)
 
+    # the ops beside the path: softmax_rows, linear, attention_head, quick_gelu
+    sm = (g.standard_normal((5, 333)) * 3).astype(np.float32)
+    sm[2, :] = -np.inf
+    sm[3, ::3] = -np.inf
+    smo = sm.copy()
+    ref.ref_softmax_rows(p(smo), 5, 333)
+    lx = g.standard_normal((3, 200), dtype=np.float32)
+    lw = (g.standard_normal((7, 200)) * 0.1).astype(np.float32)
+    lb = g.standard_normal(7, dtype=np.float32)
+    ly = np.empty((3, 7), np.float32)
+    ref.ref_linear(p(lx), 3, 200, p(lw), 7, p(lb), p(ly))
+    aq = g.standard_normal((1, 64), dtype=np.float32)
+    ak = g.standard_normal((50, 64), dtype=np.float32)
+    av = g.standard_normal((50, 64), dtype=np.float32)
+    am = np.zeros((1, 50), np.float32)
+    am[0, 10:30] = -np.inf
+    ao = np.empty((1, 64), np.float32)
+    ref.ref_attention_head(p(aq), 1, p(ak), 50, 64, p(av), 64, p(am), np.float32(0.125), p(ao))
+    qg = a.copy()
+    ref.ref_quick_gelu(p(qg), qg.size)
+    out.update(softmax_in=sm, softmax_out=smo, linear_x=lx, linear_w=lw, linear_b=lb, linear_y=ly,
+               attn_q=aq, attn_k=ak, attn_v=av, attn_mask=am, attn_scale=np.float32(0.125), attn_out=ao,
+               quick_gelu_out=qg)
+
     path = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes)")

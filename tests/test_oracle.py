@@ -415,3 +415,131 @@ def test_checks_reject_planted_slips(orc):
     c64, s64 = np.cos(ang64)[:, None, :], np.sin(ang64)[:, None, :]
     wide = np.concatenate([a * c64 - b * s64, b * c64 + a * s64], axis=-1).reshape(xr.shape)
     assert rel(wide, truth) > 2e-6
+
+
+# ---- the decode-step neighbours and the row ops beside the path -------------------------------------
+
+
+def test_router_norm_closed_form_and_edges(orc):
+    g = rng(20)
+    x = g.standard_normal((6, 320), dtype=np.float32) * 3
+    w = (0.1 * g.standard_normal(320)).astype(np.float32)
+    y = orc.router_norm(x, w, 1e-6).astype(np.float64)
+    x64 = x.astype(np.float64)
+    n = x64 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + 1e-6)
+    want = np.clip(np.clip(n, -1e4, 1e4) * (1 + w.astype(np.float64)), -1e4, 1e4)
+    assert rel(y, want) < 1e-6
+    # non-finite inputs count as zero; huge gains clamp at 1e4
+    bad = x[:2].copy()
+    bad[0, 5], bad[1, 7], bad[1, 8] = np.nan, np.inf, -np.inf
+    yb = orc.router_norm(bad, w, 1e-6)
+    clean = bad.copy()
+    clean[~np.isfinite(clean)] = 0
+    assert np.array_equal(yb, orc.router_norm(clean, w, 1e-6))
+    assert np.all(np.isfinite(yb))
+    big = orc.router_norm(x[:1], np.full(320, 1e6, np.float32), 1e-6)
+    assert np.all(np.abs(big) <= 1e4) and np.any(np.abs(big) == 1e4)
+
+
+def test_softmax_known_answer_and_masking(orc):
+    # ops_test.cpp:52-56
+    sm = orc.softmax_rows(np.array([[0, 0, math.log(2.0)], [-np.inf] * 3], np.float32))
+    assert near(sm[0, 0], 0.25) and near(sm[0, 2], 0.5)
+    assert sm[1, 0] == 0 and sm[1, 2] == 0
+    x = rng(21).standard_normal((9, 500), dtype=np.float32) * 4
+    y = orc.softmax_rows(x).astype(np.float64)
+    assert np.allclose(y.sum(axis=1), 1.0, atol=1e-6)
+    e = np.exp(x.astype(np.float64) - x.max(axis=1, keepdims=True))
+    assert rel(y, e / e.sum(axis=1, keepdims=True)) < 1e-6
+
+
+def test_linear_closed_form(orc):
+    g = rng(22)
+    x = g.standard_normal((4, 1280), dtype=np.float32)
+    w = (0.05 * g.standard_normal((96, 1280))).astype(np.float32)
+    b = g.standard_normal(96, dtype=np.float32)
+    y = orc.linear(x, w, b)
+    assert rel(y, x.astype(np.float64) @ w.astype(np.float64).T + b) < 1e-6
+
+
+def test_attention_known_answers_and_closed_form(orc):
+    # ops_test.cpp:70-78: a masked second key leaves the first value; a zero
+    # query averages the values.
+    k = np.array([[1, 0], [0, 1]], np.float32)
+    v = np.array([[5, 6], [7, 8]], np.float32)
+    out = orc.attention_one(np.array([1, 0], np.float32), k, v, 1, 2, bias=np.array([0, -np.inf], np.float32))
+    assert near(out[0], 5) and near(out[1], 6)
+    even = orc.attention_one(np.zeros(2, np.float32), k, v, 1, 2)
+    assert near(even[0], 6) and near(even[1], 7)
+    # all keys masked: zeros
+    assert np.all(orc.attention_one(np.ones(2, np.float32), k, v, 1, 2,
+                                    bias=np.full(2, -np.inf, np.float32)) == 0)
+    g = rng(23)
+    heads, hd, keys = 3, 64, 77
+    q = g.standard_normal(heads * hd, dtype=np.float32)
+    kk = g.standard_normal((keys, heads * hd), dtype=np.float32)
+    vv = g.standard_normal((keys, heads * hd), dtype=np.float32)
+    mask = np.where(g.random(keys) < 0.3, -np.inf, 0).astype(np.float32)
+    got = orc.attention_one(q, kk, vv, heads, hd, bias=mask, scale=0.125)
+    for h in range(heads):
+        sl = slice(h * hd, (h + 1) * hd)
+        s = kk[:, sl].astype(np.float64) @ q[sl].astype(np.float64) * 0.125 + mask
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        assert rel(got[sl], p @ vv[:, sl].astype(np.float64)) < 1e-5
+
+
+def test_scale_add_mask_elementwise(orc):
+    g = rng(24)
+    x = g.standard_normal((2, 5, 7), dtype=np.float32)
+    m = g.standard_normal((5, 7), dtype=np.float32)
+    got = orc.scale_add_mask(x, 0.5, m, 2, 5, 7)
+    assert np.array_equal(got, (x * np.float32(0.5) + m[None]).astype(np.float32))
+    assert np.array_equal(orc.scale_add_mask(x, 2.0, None, 2, 5, 7), x * np.float32(2.0))
+
+
+def test_quick_gelu_known_answer(orc):
+    # ops_test.cpp:45-47
+    assert near(orc.quick_gelu(np.array([1.0], np.float32))[0], 1 / (1 + math.exp(-1.702)))
+
+
+def test_golden_row_ops(orc, golden):
+    assert np.array_equal(orc.softmax_rows(golden["softmax_in"]).view(np.uint32), golden["softmax_out"].view(np.uint32))
+    assert np.array_equal(orc.linear(golden["linear_x"], golden["linear_w"], golden["linear_b"]).view(np.uint32),
+                          golden["linear_y"].view(np.uint32))
+    ao = orc.attention_one(golden["attn_q"][0], golden["attn_k"], golden["attn_v"], 1, 64,
+                           bias=golden["attn_mask"][0], scale=float(golden["attn_scale"]))
+    assert np.array_equal(ao.view(np.uint32), golden["attn_out"][0].view(np.uint32))
+    assert np.array_equal(orc.quick_gelu(golden["act_x"]).view(np.uint32), golden["quick_gelu_out"].view(np.uint32))
+
+
+def test_oracle_bit_equals_reference_row_ops(orc, ref):
+    g = rng(25)
+    x = (g.standard_normal((7, 1000)) * 5).astype(np.float32)
+    x[1, ::7] = -np.inf
+    x[4, :] = -np.inf
+    r = x.copy()
+    ref.ref_softmax_rows(_p(r), 7, 1000)
+    assert np.array_equal(r.view(np.uint32), orc.softmax_rows(x).view(np.uint32))
+    lx = g.standard_normal((5, 1283), dtype=np.float32)
+    lw = g.standard_normal((33, 1283), dtype=np.float32)
+    ly = np.empty((5, 33), np.float32)
+    ref.ref_linear(_p(lx), 5, 1283, _p(lw), 33, None, _p(ly))
+    assert np.array_equal(ly.view(np.uint32), orc.linear(lx, lw).view(np.uint32))
+    heads, hd, keys = 2, 128, 300
+    q = g.standard_normal(heads * hd, dtype=np.float32)
+    kk = g.standard_normal((keys, heads * hd), dtype=np.float32)
+    vv = g.standard_normal((keys, heads * hd), dtype=np.float32)
+    mask = np.where(g.random(keys) < 0.4, -np.inf, 0).astype(np.float32)
+    mine = orc.attention_one(q, kk, vv, heads, hd, bias=mask, scale=0.088)
+    for h in range(heads):
+        sl = slice(h * hd, (h + 1) * hd)
+        qh, kh, vh = np.ascontiguousarray(q[sl][None]), np.ascontiguousarray(kk[:, sl]), np.ascontiguousarray(vv[:, sl])
+        o = np.empty((1, hd), np.float32)
+        ref.ref_attention_head(_p(qh), 1, _p(kh), keys, hd, _p(vh), hd, _p(np.ascontiguousarray(mask[None])),
+                               np.float32(0.088), _p(o))
+        assert np.array_equal(o[0].view(np.uint32), mine[sl].view(np.uint32))
+    qx = x[0] * 0.3
+    r2 = qx.copy()
+    ref.ref_quick_gelu(_p(r2), r2.size)
+    assert np.array_equal(r2.view(np.uint32), orc.quick_gelu(qx).view(np.uint32))
