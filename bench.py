@@ -12,6 +12,12 @@ norm weights; names and sizes follow the reference's headline op set):
   4  vision block: LayerNorm [4096, 1024] (eps 1e-6) then exact-erf GELU
   5  MoE-layer prefill chain over 8192 tokens: residual add + RMSNorm
      [8192, 2048], SwiGLU [8192, 2 x 1408] -> [8192, 1408], RoPE as in 3
+  6  prefill attention row ops: fp32 scores [10 x 4096, 4096] scaled with
+     a causal mask, then softmax over each row; quick GELU [4096, 4096] bf16
+  7  one decoder layer's decode step at batch 1 on Unlimited-OCR-2's dims
+     (hidden 1280, 10 heads x 128, FFN 896, KV cache of 8192 positions):
+     add+RMSNorm, bf16 GEMVs, RoPE, cache appends and split-K attention as
+     one graph; the 129280 x 1280 LM-head GEMV on its own
 
 One step = one pass of a workload's op chain over one input set. The JSON
 line's `value` is workload 5 (the largest, three fused ops timed as one
@@ -84,6 +90,28 @@ def bytes_gelu(n, elem):
 
 def bytes_gather(rows, cols, elem_out, elem_table=2):
     return rows * (cols * elem_table + cols * elem_out + 8)      # R row, W row, R index
+
+
+def bytes_softmax(rows, cols):
+    return 2 * rows * cols * 4                                   # R/W x (fp32)
+
+
+def bytes_scale_mask(batch, rows, cols):
+    return 2 * batch * rows * cols * 4 + rows * cols * 4         # R/W x, R mask once
+
+
+def bytes_gemv(n, k, bias=False):
+    return n * k * 2 + k * 4 + n * 4 + (n * 4 if bias else 0)    # R w (bf16), R x, W y, R bias
+
+
+def bytes_attend(keys, heads, hd, splits):
+    width = heads * hd
+    part = heads * splits * (hd + 2) * 4
+    return 2 * keys * width * 4 + 2 * width * 4 + 2 * part       # R K and V rows, R q, W out, W+R records
+
+
+def bytes_append(width):
+    return 2 * width * 4
 
 
 # ---- timing helpers ---------------------------------------------------------------------------------
@@ -321,6 +349,99 @@ def config5(be, torch, timer):
             "ms_per_step_eager": round(ms_eager, 5), "kernels": kern, "sets": nsets}
 
 
+def config6(be, torch, timer):
+    """Prefill attention row ops over 4096 tokens x 10 heads (fp32 scores
+    [10 x 4096, 4096]) and the vision MLP's quick GELU."""
+    heads, rows, keys = 10, 4096, 4096
+    mask = torch.triu(torch.full((rows, keys), float("-inf"), device="cuda"), 1)
+    make = lambda: torch.randn(heads * rows, keys, device="cuda")  # noqa: E731
+    b_sm, b_mask = bytes_softmax(heads * rows, keys), bytes_scale_mask(heads, rows, keys)
+    ms_mask = time_kernel(timer, make, lambda x: be.scale_add_mask(x, 0.088, mask, heads, rows, keys))
+    ms_sm = time_kernel(timer, make, lambda x: be.softmax_rows(x))
+    ms_pair = time_kernel(timer, make, lambda x: (be.scale_add_mask(x, 0.088, mask, heads, rows, keys),
+                                                  be.softmax_rows(x)))
+    qg_rows, qg_cols = 4096, 4096
+    b_qg = bytes_gelu(qg_rows * qg_cols, 2)
+    ms_qg = time_kernel(timer, lambda: bf16_randn(torch, (qg_rows, qg_cols)), lambda x: be.quick_gelu(x))
+    return {"workload": "prefill attention scores [10 x 4096, 4096] fp32: scale + causal mask then softmax; "
+                        "quick GELU [4096, 4096] bf16",
+            "step": report("scale_mask+softmax", b_sm + b_mask, ms_pair),
+            "kernels": {"scale_add_mask_f32": report("scale_add_mask", b_mask, ms_mask),
+                        "softmax_rows_f32": report("softmax_rows", b_sm, ms_sm),
+                        "quick_gelu_bf16": report("quick_gelu", b_qg, ms_qg)}}
+
+
+def config7(be, torch, timer):
+    """One decoder layer's decode step at batch 1 on Unlimited-OCR-2's dims
+    (hidden 1280, 10 heads x 128, FFN 896), fp32 activations, bf16 weights,
+    a KV cache of 8192 positions read in full (pos 8191). Input sets are
+    whole layers (weights and cache), so a rotation reads like a multi-layer
+    step."""
+    hidden, heads, hd, ffn, cap = 1280, 10, 128, 896, 8192
+    width = heads * hd
+    pos = cap - 1
+    inv = torch.from_numpy(be.rope_inv(hd // 2, 1e4)).cuda()
+    state = torch.tensor([0, pos, pos, 0, -1], dtype=torch.int64).cuda()
+    splits_floats = be.attend_scratch_floats(heads, hd, cap)
+    splits = splits_floats // (heads * (hd + 2))
+    scratch = torch.empty(splits_floats, device="cuda")
+    x, delta = torch.randn(hidden, device="cuda"), torch.randn(hidden, device="cuda")
+    h = torch.empty(hidden, device="cuda")
+    qkv = torch.empty(3 * width, device="cuda")
+    attn, o = torch.empty(width, device="cuda"), torch.empty(hidden, device="cuda")
+    gu, act = torch.empty(1, 2 * ffn, device="cuda"), torch.empty(1, ffn, device="cuda")
+    w_norm = weights(torch, hidden)
+    scale = 1.0 / math.sqrt(hd)
+    q, k, v = qkv[:width], qkv[width:2 * width], qkv[2 * width:]
+
+    def layer():
+        return {"qkv": bf16_randn(torch, (3 * width, hidden), 0.03), "o": bf16_randn(torch, (hidden, width), 0.03),
+                "gu": bf16_randn(torch, (2 * ffn, hidden), 0.03), "down": bf16_randn(torch, (hidden, ffn), 0.03),
+                "kc": torch.randn(cap, width, device="cuda"), "vc": torch.randn(cap, width, device="cuda")}
+
+    def step(L):
+        be.add_rms_norm(x, delta, w_norm, h, 1e-6)
+        be.gemv_bf16(h, L["qkv"], qkv)
+        be.rope_qk_step(q, heads, k, heads, hd, state, inv, None, 0)
+        be.append_step(L["kc"], k, state)
+        be.append_step(L["vc"], v, state)
+        be.attend_step(q, L["kc"], L["vc"], heads, hd, None, scale, state, scratch, attn)
+        be.gemv_bf16(attn, L["o"], o)
+        be.add_rms_norm(x, o, w_norm, h, 1e-6)
+        be.gemv_bf16(h, L["gu"], gu.view(-1))
+        be.swiglu(gu, act)
+        be.gemv_bf16(act.view(-1), L["down"], delta)
+
+    b = {"add_rms_norm": 2 * bytes_add_rms_norm(1, hidden, 4), "gemv": (bytes_gemv(3 * width, hidden)
+         + bytes_gemv(hidden, width) + bytes_gemv(2 * ffn, hidden) + bytes_gemv(hidden, ffn)),
+         "rope": bytes_rope(1, 2 * heads, hd, 4), "append": 2 * bytes_append(width),
+         "attend": bytes_attend(cap, heads, hd, splits), "swiglu": bytes_swiglu(1, ffn, 4)}
+    total = sum(b.values())
+    first = layer()
+    sets = [first] + [layer() for _ in range(n_sets(footprint(first.values())) - 1)]
+    ms, lo, hi = timer.graph([lambda s=s: step(s) for s in sets])
+    ms_eager = timer.eager([lambda s=s: step(s) for s in sets])
+    kern = {
+        "attend_step_f32": report("attend", b["attend"], timer.graph(
+            [lambda s=s: be.attend_step(q, s["kc"], s["vc"], heads, hd, None, scale, state, scratch, attn)
+             for s in sets])[0]),
+        "gemv_bf16_qkv": report("gemv qkv", bytes_gemv(3 * width, hidden), timer.graph(
+            [lambda s=s: be.gemv_bf16(h, s["qkv"], qkv) for s in sets])[0]),
+    }
+    nsets = len(sets)
+    del sets, first
+    lm_n, lm_k = 129280, 1280
+    xl, yl = torch.randn(lm_k, device="cuda"), torch.empty(lm_n, device="cuda")
+    kern["gemv_bf16_lm_head"] = report("gemv lm head", bytes_gemv(lm_n, lm_k), time_kernel(
+        timer, lambda: bf16_randn(torch, (lm_n, lm_k), 0.03), lambda w: be.gemv_bf16(xl, w, yl)))
+    return {"workload": "fp32 decode layer at batch 1, hidden 1280, 10 heads x 128, FFN 896, KV cache 8192: "
+                        "add+RMSNorm -> GEMV qkv -> RoPE q,k -> append k,v -> attend -> GEMV o -> add+RMSNorm -> "
+                        "GEMV gate|up -> SwiGLU -> GEMV down",
+            "step": report("decode layer", total, ms), "us_per_layer_graph": round(ms * 1e3, 3),
+            "us_per_layer_eager": round(ms_eager * 1e3, 3), "ms_range": [round(lo, 5), round(hi, 5)],
+            "bytes_by_op": b, "attend_splits": splits, "kernels": kern, "sets": nsets}
+
+
 # ---- the CPU baseline (the reference's CPU path, restated in the oracle) ------------------------------
 
 def cpu_baseline(budget_s, threads):
@@ -456,7 +577,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="copy,1,2,3,4,5")
+    ap.add_argument("--configs", default="copy,1,2,3,4,5,6,7")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly (for counter collection)")
@@ -485,7 +606,8 @@ def main():
     torch.manual_seed(0)
     info = be.device_info(0)
     timer = Timer(torch, args.steps, args.warmup, use_graphs=not args.no_graph)
-    runners = {"1": config1, "2": config2, "3": config3, "4": config4, "5": config5, "copy": calibration}
+    runners = {"1": config1, "2": config2, "3": config3, "4": config4, "5": config5, "6": config6, "7": config7,
+               "copy": calibration}
     configs = {}
     for c in args.configs.split(","):
         t0 = time.time()

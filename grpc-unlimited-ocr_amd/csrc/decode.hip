@@ -32,7 +32,7 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int64_t kMaxHeadDim = 256;
 constexpr int kMaxSplits = 64;
-constexpr int kAttendUnroll = 4;
+constexpr int kMaskTile = 2048;
 
 // ---- append ---------------------------------------------------------------------
 
@@ -83,17 +83,39 @@ struct AttendArgs {
 
 __device__ __forceinline__ float exp_shift(float s, float m) { return __builtin_amdgcn_exp2f((s - m) * kLog2e); }
 
-template <int VW, int G, int VPL>
+// The K and V chunks of U keys of one lane group, with each key's mask value
+// (-inf for a key that is masked or past the end: such a key is not read).
+template <int VW, int VPL, int U>
+struct KeyBatch {
+  Chunk<float, VW> k[U][VPL];
+  Chunk<float, VW> v[U][VPL];
+  float mk[U];
+};
+
+// One lane group's running softmax state over its keys.
+template <int VW, int VPL>
+struct Running {
+  float m = -INFINITY;
+  float l = 0.0f;
+  float acc[VPL][VW];
+};
+
+template <int VW, int G, int VPL, int U>
 __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   constexpr int kSlotsPerWave = kWave / G;
   constexpr int kSlots = kWavesPerBlock * kSlotsPerWave;
   constexpr int kPerLane = VW * VPL;
-  constexpr int U = kAttendUnroll;
+  constexpr int64_t kStride = static_cast<int64_t>(kSlots) * U;  // keys per lane-group batch
+  static_assert(kMaskTile % kStride == 0, "mask tiles hold whole batches");
+  __shared__ float s_mask[kMaskTile];
   __shared__ float s_m[kSlots];
   __shared__ float s_l[kSlots];
   __shared__ float s_acc[kSlots * G * kPerLane];
 
-  const int h = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+  // Split-major: the heads' workgroups of one key range are dispatched
+  // together and read the same cache rows.
+  const int heads = static_cast<int>(a.width / a.hd);
+  const int h = blockIdx.x % heads, split = blockIdx.x / heads;
   const int lane = threadIdx.x & (kWave - 1);
   const int slot = (threadIdx.x / kWave) * kSlotsPerWave + lane / G;
   const int gl = lane % G;
@@ -105,96 +127,136 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   const int nvec = a.hd / VW;
   const int64_t head_off = static_cast<int64_t>(h) * a.hd;
 
+  // This lane's chunks of the head: c = gl + G i; lanes past the head (when
+  // nvec is not a power of two) address the head's last chunk and their
+  // values are dropped.
+  int64_t col[VPL];
+  bool in_head[VPL];
   float qv[VPL][VW];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = gl + G * i;
+    in_head[i] = c < nvec;
+    col[i] = head_off + static_cast<int64_t>(in_head[i] ? c : nvec - 1) * VW;
 #pragma unroll
-    for (int e = 0; e < VW; ++e) qv[i][e] = c < nvec ? a.q[head_off + c * VW + e] : 0.0f;
+    for (int e = 0; e < VW; ++e) qv[i][e] = in_head[i] ? a.q[col[i] + e] : 0.0f;
   }
 
-  float m = -INFINITY, l = 0.0f;
-  float acc[VPL][VW];
+  Running<VW, VPL> run;
 #pragma unroll
   for (int i = 0; i < VPL; ++i)
 #pragma unroll
-    for (int e = 0; e < VW; ++e) acc[i][e] = 0.0f;
+    for (int e = 0; e < VW; ++e) run.acc[i][e] = 0.0f;
 
-  for (int64_t j0 = first + slot; j0 < last; j0 += static_cast<int64_t>(kSlots) * U) {
-    float mk[U];
-    bool live[U];
+  // Loads are issued unconditionally: a key that is masked or past the end
+  // reads the query row instead (cached, never used), so the loop has no
+  // branch around a load and the next batch's loads stay in flight while
+  // the current batch is scored.
+  auto issue = [&](KeyBatch<VW, VPL, U>& b, int64_t jb, int64_t t0, int64_t t1) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = j0 + static_cast<int64_t>(kSlots) * u;
-      live[u] = j < last;
-      mk[u] = live[u] ? (a.mask != nullptr ? a.mask[j] : 0.0f) : -INFINITY;
-      live[u] = live[u] && mk[u] != -INFINITY;
+      const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
+      const bool in = j < t1;
+      b.mk[u] = in ? (a.mask != nullptr ? s_mask[j - t0] : 0.0f) : -INFINITY;
     }
-    Chunk<float, VW> kc[U][VPL], vc[U][VPL];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = j0 + static_cast<int64_t>(kSlots) * u;
+      const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
+      const bool live = b.mk[u] != -INFINITY;
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const int c = gl + G * i;
-        kc[u][i].clear();
-        vc[u][i].clear();
-        if (live[u] && c < nvec) {
-          const int64_t off = j * a.width + head_off + c * VW;
-          kc[u][i].load(a.k + off);
-          vc[u][i].load(a.v + off);
-        }
-      }
+      for (int i = 0; i < VPL; ++i) b.k[u][i].load(live ? a.k + j * a.width + col[i] : a.q + col[i]);
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
+      const bool live = b.mk[u] != -INFINITY;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) b.v[u][i].load(live ? a.v + j * a.width + col[i] : a.q + col[i]);
+    }
+  };
+
+  auto consume = [&](const KeyBatch<VW, VPL, U>& b) {
     float s[U];
-    float peak = m;
+    float peak = run.m;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float d = 0.0f;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         float kv[VW];
-        kc[u][i].widen(kv);
+        b.k[u][i].widen(kv);
 #pragma unroll
-        for (int e = 0; e < VW; ++e) d = fmaf(qv[i][e], kv[e], d);
+        for (int e = 0; e < VW; ++e) d = fmaf(qv[i][e], in_head[i] ? kv[e] : 0.0f, d);
       }
       d = group_sum<G>(d);
       {
 #pragma clang fp contract(off)
-        s[u] = live[u] ? d * a.scale + mk[u] : -INFINITY;
+        s[u] = b.mk[u] != -INFINITY ? d * a.scale + b.mk[u] : -INFINITY;
       }
       peak = fmaxf(peak, s[u]);
     }
-    if (peak == -INFINITY) continue;  // uniform over the lane group
-    const float alpha = exp_shift(m, peak);
-    l *= alpha;
+    if (peak == -INFINITY) return;  // uniform over the lane group
+    const float alpha = exp_shift(run.m, peak);
+    run.l *= alpha;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
-      for (int e = 0; e < VW; ++e) acc[i][e] *= alpha;
+      for (int e = 0; e < VW; ++e) run.acc[i][e] *= alpha;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const float p = exp_shift(s[u], peak);
-      l += p;
+      run.l += p;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         float vv[VW];
-        vc[u][i].widen(vv);
+        b.v[u][i].widen(vv);
 #pragma unroll
-        for (int e = 0; e < VW; ++e) acc[i][e] = fmaf(p, vv[e], acc[i][e]);
+        for (int e = 0; e < VW; ++e) run.acc[i][e] = fmaf(p, in_head[i] ? vv[e] : 0.0f, run.acc[i][e]);
       }
     }
-    m = peak;
+    run.m = peak;
+  };
+
+  // Key tiles: the mask of a tile is staged in LDS by the whole workgroup
+  // (one coalesced load per thread per 256 keys); without a mask the split
+  // is one tile.
+  const int64_t tile = a.mask != nullptr ? kMaskTile : (last > first ? last - first : 1);
+  for (int64_t t0 = first; t0 < last; t0 += tile) {
+    const int64_t t1 = t0 + tile < last ? t0 + tile : last;
+    if (a.mask != nullptr) {
+      constexpr int kPer = kMaskTile / kBlock;
+      float mv[kPer];
+#pragma unroll
+      for (int r = 0; r < kPer; ++r) {
+        const int64_t j = t0 + threadIdx.x + static_cast<int64_t>(r) * kBlock;
+        mv[r] = a.mask[j < t1 ? j : t1 - 1];
+      }
+      __syncthreads();  // the previous tile's readers are done
+#pragma unroll
+      for (int r = 0; r < kPer; ++r) s_mask[threadIdx.x + r * kBlock] = mv[r];
+      __syncthreads();
+    }
+    const int64_t base = t0 + slot;
+    const int iters = base < t1 ? static_cast<int>((t1 - base + kStride - 1) / kStride) : 0;
+    KeyBatch<VW, VPL, U> A, B;
+    issue(A, base, t0, t1);
+    for (int it = 0; it < iters; it += 2) {
+      issue(B, base + (it + 1) * kStride, t0, t1);
+      consume(A);
+      if (it + 1 >= iters) break;
+      issue(A, base + (it + 2) * kStride, t0, t1);
+      consume(B);
+    }
   }
 
   if (gl == 0) {
-    s_m[slot] = m;
-    s_l[slot] = l;
+    s_m[slot] = run.m;
+    s_l[slot] = run.l;
   }
 #pragma unroll
   for (int i = 0; i < VPL; ++i)
 #pragma unroll
-    for (int e = 0; e < VW; ++e) s_acc[slot * G * kPerLane + (gl + G * i) * VW + e] = acc[i][e];
+    for (int e = 0; e < VW; ++e) s_acc[slot * G * kPerLane + (gl + G * i) * VW + e] = run.acc[i][e];
   __syncthreads();
 
   float* rec = a.part + (static_cast<int64_t>(h) * a.splits + split) * (a.hd + 2);
@@ -218,23 +280,64 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   }
 }
 
+// One workgroup per head. Wave 0 reads the splits' (m, l) pairs (one split
+// per lane) and turns them into weights 2^((m_s - M) log2 e) in LDS; then
+// wave w sums splits w, w + 4, ... of the weighted value records, every
+// lane holding VPT elements of the head, with all kMaxSplits / 4 loads per
+// element issued together (indices clamped, weight 0 past `splits`); the
+// four wave partials add in wave order.
+template <int VPT>
 __global__ __launch_bounds__(kBlock) void attend_merge(const float* __restrict__ part, int hd, int splits,
                                                        float* __restrict__ out) {
+  constexpr int kPerWave = kMaxSplits / kWavesPerBlock;
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_total;
+  __shared__ float s_red[kWavesPerBlock][kWave * VPT];
   const int h = blockIdx.x;
-  const float* recs = part + static_cast<int64_t>(h) * splits * (hd + 2);
-  float big = -INFINITY;
-  for (int i = 0; i < splits; ++i) big = fmaxf(big, recs[i * (hd + 2)]);
-  for (int e = threadIdx.x; e < hd; e += kBlock) {
-    float total = 0.0f, sum = 0.0f;
-    if (big != -INFINITY) {
-      for (int i = 0; i < splits; ++i) {
-        const float* r = recs + i * (hd + 2);
-        if (r[0] == -INFINITY) continue;
-        const float wgt = exp_shift(r[0], big);
-        total += r[1] * wgt;
-        sum += r[2 + e] * wgt;
-      }
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t rec_len = hd + 2;
+  const float* recs = part + static_cast<int64_t>(h) * splits * rec_len;
+  // Every load is issued before the first is used: the value records, then
+  // wave 0's (m, l) pairs.
+  float vals[kPerWave][VPT];
+#pragma unroll
+  for (int r = 0; r < kPerWave; ++r) {
+    const int s = wave + kWavesPerBlock * r;
+    const int sc = s < splits ? s : splits - 1;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int e = lane + kWave * i;
+      vals[r][i] = recs[sc * rec_len + 2 + (e < hd ? e : hd - 1)];
     }
+  }
+  if (wave == 0) {
+    const int s = lane < splits ? lane : splits - 1;
+    const float m_raw = recs[s * rec_len];
+    const float l = recs[s * rec_len + 1];
+    const float m = lane < splits ? m_raw : -INFINITY;
+    const float big = wave_max(m);
+    const float w = (m == -INFINITY || big == -INFINITY) ? 0.0f : exp_shift(m, big);
+    s_w[lane] = w;
+    const float total = wave_sum(w * l);
+    if (lane == 0) s_total = total;
+  }
+  __syncthreads();
+  float acc[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kPerWave; ++r) {
+    const int s = wave + kWavesPerBlock * r;
+    const float w = s < splits ? s_w[s] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) acc[i] = fmaf(w, vals[r][i], acc[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) s_red[wave][lane + kWave * i] = acc[i];
+  __syncthreads();
+  const float total = s_total;
+  for (int e = threadIdx.x; e < hd; e += kBlock) {
+    const float sum = (s_red[0][e] + s_red[1][e]) + (s_red[2][e] + s_red[3][e]);
     out[static_cast<int64_t>(h) * hd + e] = total > 0.0f ? sum / total : 0.0f;
   }
 }
@@ -249,26 +352,39 @@ int attend_splits(int64_t heads, int64_t capacity) {
   return static_cast<int>(s < 1 ? 1 : s);
 }
 
-template <int VW, int G, int VPL>
+template <int VW, int G, int VPL, int U>
 void launch_partial(hipStream_t s, const AttendArgs& a, int64_t heads) {
-  attend_partial<VW, G, VPL><<<static_cast<unsigned>(heads * a.splits), kBlock, 0, s>>>(a);
+  attend_partial<VW, G, VPL, U><<<static_cast<unsigned>(heads * a.splits), kBlock, 0, s>>>(a);
 }
 
+// Lanes per key and keys per batch. Up to 8192 positions two keys per batch
+// (the split's keys are few, so fewer dead loads and registers win); beyond,
+// four keys per batch and, for 128-wide heads, 16 lanes of two chunks each
+// per key. Both depend on the capacity only, so a captured step keeps its
+// launch shape at every position.
 void launch_attend_vec(hipStream_t s, const AttendArgs& a, int64_t heads) {
   const int nvec = a.hd / 4;
-  if (nvec <= 1) launch_partial<4, 1, 1>(s, a, heads);
-  else if (nvec <= 2) launch_partial<4, 2, 1>(s, a, heads);
-  else if (nvec <= 4) launch_partial<4, 4, 1>(s, a, heads);
-  else if (nvec <= 8) launch_partial<4, 8, 1>(s, a, heads);
-  else if (nvec <= 16) launch_partial<4, 16, 1>(s, a, heads);
-  else if (nvec <= 32) launch_partial<4, 32, 1>(s, a, heads);
-  else launch_partial<4, 64, 1>(s, a, heads);
+  const bool long_ctx = a.capacity > 8192;
+  if (nvec <= 1) launch_partial<4, 1, 1, 2>(s, a, heads);
+  else if (nvec <= 2) launch_partial<4, 2, 1, 2>(s, a, heads);
+  else if (nvec <= 4) launch_partial<4, 4, 1, 2>(s, a, heads);
+  else if (nvec <= 8) launch_partial<4, 8, 1, 2>(s, a, heads);
+  else if (nvec <= 16) {
+    if (long_ctx) launch_partial<4, 16, 1, 4>(s, a, heads);
+    else launch_partial<4, 16, 1, 2>(s, a, heads);
+  } else if (nvec <= 32) {
+    if (long_ctx) launch_partial<4, 16, 2, 4>(s, a, heads);
+    else launch_partial<4, 32, 1, 2>(s, a, heads);
+  } else {
+    if (long_ctx) launch_partial<4, 64, 1, 4>(s, a, heads);
+    else launch_partial<4, 64, 1, 2>(s, a, heads);
+  }
 }
 
 void launch_attend_any(hipStream_t s, const AttendArgs& a, int64_t heads) {
-  if (a.hd <= 64) launch_partial<1, 64, 1>(s, a, heads);
-  else if (a.hd <= 128) launch_partial<1, 64, 2>(s, a, heads);
-  else launch_partial<1, 64, 4>(s, a, heads);
+  if (a.hd <= 64) launch_partial<1, 64, 1, 2>(s, a, heads);
+  else if (a.hd <= 128) launch_partial<1, 64, 2, 2>(s, a, heads);
+  else launch_partial<1, 64, 4, 2>(s, a, heads);
 }
 
 }  // namespace
@@ -324,7 +440,13 @@ int uocr_rocm_attend_step(void* stream, const float* q, const float* k_cache, co
     launch_attend_any(s, a, heads);
   }
   if (const int st = check_launch(what); st != UOCR_ROCM_OK) return st;
-  attend_merge<<<static_cast<unsigned>(heads), kBlock, 0, s>>>(scratch, a.hd, a.splits, out);
+  if (hd <= kWave) {
+    attend_merge<1><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(scratch, a.hd, a.splits, out);
+  } else if (hd <= 2 * kWave) {
+    attend_merge<2><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(scratch, a.hd, a.splits, out);
+  } else {
+    attend_merge<4><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(scratch, a.hd, a.splits, out);
+  }
   return check_launch(what);
 }
 

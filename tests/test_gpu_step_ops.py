@@ -181,7 +181,10 @@ def attend_case(backend, heads, hd, cap, pos, mask=None, scale=None, seed=0):
 @pytest.mark.parametrize("heads,hd,cap,pos", [(10, 128, 8192, 8191), (10, 128, 8192, 0), (10, 128, 8192, 100),
                                               (10, 128, 4096, 2999), (16, 64, 1024, 777), (4, 80, 500, 499),
                                               (2, 66, 300, 250), (2, 256, 700, 650), (3, 4, 100, 60),
-                                              (1, 128, 7, 50), (10, 128, 64, 63)])
+                                              (1, 128, 7, 50), (10, 128, 64, 63),
+                                              # past 8192 positions: four keys per batch, 16 lanes per key
+                                              (10, 128, 16384, 12000), (4, 64, 9000, 8999), (2, 256, 9000, 5000),
+                                              (3, 80, 10000, 9999)])
 def test_attend_step(backend, heads, hd, cap, pos):
     got, want = attend_case(backend, heads, hd, cap, pos, seed=200 + hd)
     assert_f32_close(got, want, 1e-5, f"attend heads={heads} hd={hd} pos={pos}")
