@@ -497,11 +497,18 @@ COPY_BYTES = 256 * 2**20  # the calibration copy: 256 MiB read and 256 MiB writt
 
 
 def _kernel_label(name):
+    """A kernel's demangled name without namespaces and parameter list."""
     import re
 
-    name = re.sub(r"uocr_rocm::\(anonymous namespace\)::", "", name)
-    name = re.sub(r"\)\s*\(.*$", ")", name) if "(Norm)" in name else re.sub(r"\(.*$", "", name)
-    return name.replace("void ", "").strip()
+    name = re.sub(r"uocr_rocm::\(anonymous namespace\)::", "", name).replace("void ", "").strip()
+    if name.endswith(")"):  # drop the trailing "(params)", keeping "(Norm)1"-style template arguments
+        depth = 0
+        for i in range(len(name) - 1, -1, -1):
+            depth += {")": 1, "(": -1}.get(name[i], 0)
+            if depth == 0:
+                name = name[:i]
+                break
+    return name.strip()
 
 
 def summarize_trace(trace_dir):

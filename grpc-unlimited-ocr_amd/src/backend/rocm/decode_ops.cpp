@@ -47,4 +47,20 @@ void embed_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_
   check(uocr_rocm_embed_step_bf16(ctx.stream(), table, table_rows, abi(state), cols, dst));
 }
 
+void append_step(const Context& ctx, float* cache, const float* row, std::int64_t width, const StepState* state,
+                 std::int64_t capacity) {
+  check(uocr_rocm_append_step(ctx.stream(), cache, row, width, abi(state), capacity));
+}
+
+std::int64_t attend_scratch_floats(std::int64_t heads, std::int64_t hd, std::int64_t capacity) {
+  return uocr_rocm_attend_scratch_floats(heads, hd, capacity);
+}
+
+void attend_step(const Context& ctx, const float* q, const float* k_cache, const float* v_cache, std::int64_t heads,
+                 std::int64_t hd, const float* mask, float scale, const StepState* state, float* scratch,
+                 std::int64_t capacity, float* out) {
+  check(uocr_rocm_attend_step(ctx.stream(), q, k_cache, v_cache, heads, hd, mask, scale, abi(state), scratch, capacity,
+                              out));
+}
+
 }  // namespace uocr::rocm

@@ -35,4 +35,17 @@ void rope_qk_step_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_head
 void embed_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows, const StepState* state,
                      std::int64_t cols, std::uint16_t* dst);
 
+// cache[pos] = row, rows `width` wide (src/backend/cuda/decode_ops.h:28-29).
+// capacity >= 0 bounds pos (an out-of-range pos writes nothing); -1 leaves
+// it unchecked, as the reference does.
+void append_step(const Context& ctx, float* cache, const float* row, std::int64_t width, const StepState* state,
+                 std::int64_t capacity = -1);
+// Masked attention of one query over keys 0..pos: out [heads * hd]
+// (decode_ops.h:42-47). `scratch` holds attend_scratch_floats(heads, hd,
+// capacity) floats; mask may be null.
+std::int64_t attend_scratch_floats(std::int64_t heads, std::int64_t hd, std::int64_t capacity);
+void attend_step(const Context& ctx, const float* q, const float* k_cache, const float* v_cache, std::int64_t heads,
+                 std::int64_t hd, const float* mask, float scale, const StepState* state, float* scratch,
+                 std::int64_t capacity, float* out);
+
 }  // namespace uocr::rocm

@@ -111,4 +111,33 @@ void gather_rows_bf16_bf16(const Context& ctx, const std::uint16_t* table, std::
   check(uocr_rocm_gather_rows_bf16_bf16(ctx.stream(), table, table_rows, index, rows, cols, dst));
 }
 
+void router_norm(const Context& ctx, float* x, const float* w, std::int64_t rows, std::int64_t cols, float eps) {
+  check(uocr_rocm_router_norm(ctx.stream(), x, w, rows, cols, eps));
+}
+
+void router_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std::int64_t rows, std::int64_t cols,
+                      float eps) {
+  check(uocr_rocm_router_norm_bf16(ctx.stream(), x, w, rows, cols, eps));
+}
+
+void quick_gelu(const Context& ctx, float* x, std::int64_t n) { check(uocr_rocm_quick_gelu(ctx.stream(), x, n)); }
+
+void quick_gelu_bf16(const Context& ctx, std::uint16_t* x, std::int64_t n) {
+  check(uocr_rocm_quick_gelu_bf16(ctx.stream(), x, n));
+}
+
+void softmax_rows(const Context& ctx, float* x, std::int64_t rows, std::int64_t cols) {
+  check(uocr_rocm_softmax_rows(ctx.stream(), x, rows, cols));
+}
+
+void scale_add_mask(const Context& ctx, float* x, float scale, const float* mask, std::int64_t batch, std::int64_t rows,
+                    std::int64_t cols) {
+  check(uocr_rocm_scale_add_mask(ctx.stream(), x, scale, mask, batch, rows, cols));
+}
+
+void gemv_bf16(const Context& ctx, const float* x, std::int64_t k, const std::uint16_t* w, std::int64_t n,
+               const float* bias, float* y) {
+  check(uocr_rocm_gemv_bf16(ctx.stream(), x, k, w, n, bias, y));
+}
+
 }  // namespace uocr::rocm

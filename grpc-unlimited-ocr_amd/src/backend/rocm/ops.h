@@ -87,4 +87,25 @@ void rope_qk_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_heads, st
 void gather_rows_bf16_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
                            const std::int64_t* index, std::int64_t rows, std::int64_t cols, std::uint16_t* dst);
 
+// ---- row ops beside the path (reference signatures, src/backend/cuda/ops.h:35-46) -------
+
+// The router's norm: non-finite inputs zeroed, scaled by (1 + w), clamped to +-1e4.
+void router_norm(const Context& ctx, float* x, const float* w, std::int64_t rows, std::int64_t cols, float eps);
+void router_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std::int64_t rows, std::int64_t cols,
+                      float eps);
+void quick_gelu(const Context& ctx, float* x, std::int64_t n);
+void quick_gelu_bf16(const Context& ctx, std::uint16_t* x, std::int64_t n);
+// Softmax over each row of x [rows, cols] in place; a fully masked row
+// (all -inf) becomes zeros.
+void softmax_rows(const Context& ctx, float* x, std::int64_t rows, std::int64_t cols);
+// x[b, r, c] = x[b, r, c] * scale + mask[r, c], for each of `batch` slices.
+void scale_add_mask(const Context& ctx, float* x, float scale, const float* mask, std::int64_t batch, std::int64_t rows,
+                    std::int64_t cols);
+
+// ---- weight streaming (src/backend/cuda/gemv_ops.h:25-26) ---------------------------------
+
+// y[n] = bf16(x) . w[n, :] (+ bias[n]); x fp32 [k] (k <= 12288), w bf16 [n, k].
+void gemv_bf16(const Context& ctx, const float* x, std::int64_t k, const std::uint16_t* w, std::int64_t n,
+               const float* bias, float* y);
+
 }  // namespace uocr::rocm

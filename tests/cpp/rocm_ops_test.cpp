@@ -307,6 +307,53 @@ void decode_graph(const ro::Context& ctx) {
   }
 }
 
+void step_ops(const ro::Context& ctx) {
+  {  // softmax with a masked entry and a fully masked row
+    const std::int64_t rows = 5, cols = 300;
+    auto x = random(rows * cols, 3.0f);
+    x[7] = -INFINITY;
+    for (std::int64_t c = 0; c < cols; ++c) x[2 * cols + c] = -INFINITY;
+    auto want = x;
+    orc_softmax_rows(want.data(), rows, cols);
+    auto dx = up(ctx, x);
+    ro::softmax_rows(ctx, dx.f32(), rows, cols);
+    const auto got = dx.download();
+    expect("softmax_rows", max_rel(got, want), 1e-5);
+    require(got[2 * cols] == 0.0f && got[3 * cols - 1] == 0.0f, "fully masked row is zeros");
+  }
+  {  // GEMV against linear on the bf16-rounded input
+    const std::int64_t k = 1280, n = 96;
+    const auto x = random(k), w = bf16_rounded(random(n * k, 0.05f)), bias = random(n);
+    std::vector<float> want(n);
+    orc_linear(bf16_rounded(x).data(), 1, k, w.data(), n, bias.data(), want.data());
+    auto dx = up(ctx, x), dw = up(ctx, w, ro::DType::kBF16), db = up(ctx, bias);
+    ro::Array dy(ctx, ro::DType::kF32, n);
+    ro::gemv_bf16(ctx, dx.f32(), k, dw.bf16(), n, db.f32(), dy.f32());
+    expect("gemv_bf16", max_rel(dy.download(), want), 1e-5);
+  }
+  {  // append then attend at pos 40 of a 64-position cache, 4 heads of 64
+    const std::int64_t heads = 4, hd = 64, cap = 64, width = heads * hd, pos = 40;
+    const auto kc = random(cap * width), vc = random(cap * width), q = random(width), kr = random(width),
+               vr = random(width);
+    auto dk = up(ctx, kc), dv = up(ctx, vc), dq = up(ctx, q), dkr = up(ctx, kr), dvr = up(ctx, vr);
+    ro::Array state(ctx, ro::DType::kI64, 5), out(ctx, ro::DType::kF32, width),
+        scratch(ctx, ro::DType::kF32, ro::attend_scratch_floats(heads, hd, cap));
+    const std::int64_t s[5] = {0, pos, pos, 0, -1};
+    state.upload(s, 5);
+    const auto* st = reinterpret_cast<const ro::StepState*>(state.data());
+    ro::append_step(ctx, dk.f32(), dkr.f32(), width, st, cap);
+    ro::append_step(ctx, dv.f32(), dvr.f32(), width, st, cap);
+    const float scale = 0.125f;
+    ro::attend_step(ctx, dq.f32(), dk.f32(), dv.f32(), heads, hd, nullptr, scale, st, scratch.f32(), cap, out.f32());
+    auto wk = kc, wv = vc;
+    std::copy(kr.begin(), kr.end(), wk.begin() + pos * width);
+    std::copy(vr.begin(), vr.end(), wv.begin() + pos * width);
+    std::vector<float> want(width);
+    orc_attention_one(q.data(), wk.data(), wv.data(), pos + 1, width, heads, hd, nullptr, scale, want.data());
+    expect("append + attend_step", max_rel(out.download(), want), 1e-5);
+  }
+}
+
 void errors(const ro::Context& ctx) {
   ro::Array x(ctx, ro::DType::kF32, 64), w(ctx, ro::DType::kF32, 64);
   require_throws_invalid([&] { ro::rms_norm(ctx, x.f32(), w.f32(), -1, 64, 1e-6f); }, "negative rows");
@@ -317,6 +364,10 @@ void errors(const ro::Context& ctx) {
                          "rope tables that do not cover dim / 2");
   require_throws_invalid([&] { ro::add_rms_norm(ctx, x.f32(), x.f32(), w.f32(), x.f32(), 1, 64, 1e-6f); },
                          "aliased add_rms_norm buffers");
+  require_throws_invalid([&] { ro::gemv_bf16(ctx, x.f32(), 20000, nullptr, 4, nullptr, w.f32()); }, "gemv k above 12288");
+  require_throws_invalid(
+      [&] { ro::attend_step(ctx, x.f32(), x.f32(), x.f32(), 1, 300, nullptr, 1.0f, nullptr, x.f32(), 4, w.f32()); },
+      "attend head dim above 256");
   ro::rms_norm(ctx, x.f32(), w.f32(), 0, 64, 1e-6f);  // empty is a no-op
   ctx.synchronize();
   std::printf("%-26s ok\n", "error convention");
@@ -338,6 +389,7 @@ int main() {
     gather(ctx);
     bf16_ops(ctx);
     decode_graph(ctx);
+    step_ops(ctx);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());

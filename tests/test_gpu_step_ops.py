@@ -101,7 +101,8 @@ def test_softmax_rows_are_batch_invariant(backend):
 
 
 @pytest.mark.parametrize("batch,rows,cols,masked", [(16, 33, 47, True), (8, 64, 64, True), (10, 577, 577, True),
-                                                    (4, 16, 16, False)])
+                                                    (4, 16, 16, False), (33, 8, 12, True), (1, 7, 9, False),
+                                                    (3, 256, 256, True)])
 def test_scale_add_mask(backend, batch, rows, cols, masked):
     x = normal(140, (batch, rows, cols))
     mask = None

@@ -442,7 +442,7 @@ def test_router_norm_closed_form_and_edges(orc):
 
 
 def test_softmax_known_answer_and_masking(orc):
-    # ops_test.cpp:52-56
+    # ops_test.cpp:51-55
     sm = orc.softmax_rows(np.array([[0, 0, math.log(2.0)], [-np.inf] * 3], np.float32))
     assert near(sm[0, 0], 0.25) and near(sm[0, 2], 0.5)
     assert sm[1, 0] == 0 and sm[1, 2] == 0
@@ -463,7 +463,7 @@ def test_linear_closed_form(orc):
 
 
 def test_attention_known_answers_and_closed_form(orc):
-    # ops_test.cpp:70-78: a masked second key leaves the first value; a zero
+    # ops_test.cpp:68-77: a masked second key leaves the first value; a zero
     # query averages the values.
     k = np.array([[1, 0], [0, 1]], np.float32)
     v = np.array([[5, 6], [7, 8]], np.float32)
@@ -499,7 +499,7 @@ def test_scale_add_mask_elementwise(orc):
 
 
 def test_quick_gelu_known_answer(orc):
-    # ops_test.cpp:45-47
+    # ops_test.cpp:44-46
     assert near(orc.quick_gelu(np.array([1.0], np.float32))[0], 1 / (1 + math.exp(-1.702)))
 
 
