@@ -17,7 +17,8 @@ norm weights; names and sizes follow the reference's headline op set):
   7  one decoder layer's decode step at batch 1 on Unlimited-OCR-2's dims
      (hidden 1280, 10 heads x 128, FFN 896, KV cache of 8192 positions):
      add+RMSNorm, bf16 GEMVs, RoPE, cache appends and split-K attention as
-     one graph; the 129280 x 1280 LM-head GEMV on its own
+     one graph, fused into 6 launches (the 11-launch unfused layer beside
+     it); the 129280 x 1280 LM-head GEMV on its own
 
 One step = one pass of a workload's op chain over one input set. The JSON
 line's `value` is workload 5 (the largest, three fused ops timed as one
@@ -376,7 +377,8 @@ def config7(be, torch, timer):
     (hidden 1280, 10 heads x 128, FFN 896), fp32 activations, bf16 weights,
     a KV cache of 8192 positions read in full (pos 8191). Input sets are
     whole layers (weights and cache), so a rotation reads like a multi-layer
-    step."""
+    step. The step is the fused layer (6 launches); the same layer from the
+    unfused ops (11 launches, the reference's op sequence) is timed beside it."""
     hidden, heads, hd, ffn, cap = 1280, 10, 128, 896, 8192
     width = heads * hd
     pos = cap - 1
@@ -386,6 +388,7 @@ def config7(be, torch, timer):
     splits = splits_floats // (heads * (hd + 2))
     scratch = torch.empty(splits_floats, device="cuda")
     x, delta = torch.randn(hidden, device="cuda"), torch.randn(hidden, device="cuda")
+    x1, x2 = torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda")
     h = torch.empty(hidden, device="cuda")
     qkv = torch.empty(3 * width, device="cuda")
     attn, o = torch.empty(width, device="cuda"), torch.empty(hidden, device="cuda")
@@ -399,7 +402,7 @@ def config7(be, torch, timer):
                 "gu": bf16_randn(torch, (2 * ffn, hidden), 0.03), "down": bf16_randn(torch, (hidden, ffn), 0.03),
                 "kc": torch.randn(cap, width, device="cuda"), "vc": torch.randn(cap, width, device="cuda")}
 
-    def step(L):
+    def unfused(L):
         be.add_rms_norm(x, delta, w_norm, h, 1e-6)
         be.gemv_bf16(h, L["qkv"], qkv)
         be.rope_qk_step(q, heads, k, heads, hd, state, inv, None, 0)
@@ -412,6 +415,15 @@ def config7(be, torch, timer):
         be.swiglu(gu, act)
         be.gemv_bf16(act.view(-1), L["down"], delta)
 
+    def fused(L):
+        be.add_rms_norm_gemv_bf16(x, L["qkv"], qkv, delta=delta, x_out=x1, w_norm=w_norm)
+        be.attend_rope_kv_step(q, k, v, L["kc"], L["vc"], heads, hd, None, scale, state, inv, None, 0, scratch,
+                               attn)
+        be.gemv_bf16(attn, L["o"], o)
+        be.add_rms_norm_swiglu_gemv_bf16(x1, L["gu"][:ffn], L["gu"][ffn:], act.view(-1), delta=o, x_out=x2,
+                                         w_norm=w_norm)
+        be.gemv_bf16(act.view(-1), L["down"], delta)
+
     b = {"add_rms_norm": 2 * bytes_add_rms_norm(1, hidden, 4), "gemv": (bytes_gemv(3 * width, hidden)
          + bytes_gemv(hidden, width) + bytes_gemv(2 * ffn, hidden) + bytes_gemv(hidden, ffn)),
          "rope": bytes_rope(1, 2 * heads, hd, 4), "append": 2 * bytes_append(width),
@@ -419,14 +431,22 @@ def config7(be, torch, timer):
     total = sum(b.values())
     first = layer()
     sets = [first] + [layer() for _ in range(n_sets(footprint(first.values())) - 1)]
-    ms, lo, hi = timer.graph([lambda s=s: step(s) for s in sets])
-    ms_eager = timer.eager([lambda s=s: step(s) for s in sets])
+    ms, lo, hi = timer.graph([lambda s=s: fused(s) for s in sets])
+    ms_eager = timer.eager([lambda s=s: fused(s) for s in sets])
+    ms_unfused = timer.graph([lambda s=s: unfused(s) for s in sets])[0]
+    ms_unfused_eager = timer.eager([lambda s=s: unfused(s) for s in sets])
     kern = {
         "attend_step_f32": report("attend", b["attend"], timer.graph(
             [lambda s=s: be.attend_step(q, s["kc"], s["vc"], heads, hd, None, scale, state, scratch, attn)
              for s in sets])[0]),
+        "attend_rope_kv_step_f32": report("attend+rope+append", b["attend"] + b["append"], timer.graph(
+            [lambda s=s: be.attend_rope_kv_step(q, k, v, s["kc"], s["vc"], heads, hd, None, scale, state, inv, None,
+                                                0, scratch, attn) for s in sets])[0]),
         "gemv_bf16_qkv": report("gemv qkv", bytes_gemv(3 * width, hidden), timer.graph(
             [lambda s=s: be.gemv_bf16(h, s["qkv"], qkv) for s in sets])[0]),
+        "add_rms_norm_gemv_bf16_qkv": report("norm+gemv qkv", bytes_gemv(3 * width, hidden), timer.graph(
+            [lambda s=s: be.add_rms_norm_gemv_bf16(x, s["qkv"], qkv, delta=delta, x_out=x1, w_norm=w_norm)
+             for s in sets])[0]),
     }
     nsets = len(sets)
     del sets, first
@@ -434,11 +454,13 @@ def config7(be, torch, timer):
     xl, yl = torch.randn(lm_k, device="cuda"), torch.empty(lm_n, device="cuda")
     kern["gemv_bf16_lm_head"] = report("gemv lm head", bytes_gemv(lm_n, lm_k), time_kernel(
         timer, lambda: bf16_randn(torch, (lm_n, lm_k), 0.03), lambda w: be.gemv_bf16(xl, w, yl)))
-    return {"workload": "fp32 decode layer at batch 1, hidden 1280, 10 heads x 128, FFN 896, KV cache 8192: "
-                        "add+RMSNorm -> GEMV qkv -> RoPE q,k -> append k,v -> attend -> GEMV o -> add+RMSNorm -> "
-                        "GEMV gate|up -> SwiGLU -> GEMV down",
+    return {"workload": "fp32 decode layer at batch 1, hidden 1280, 10 heads x 128, FFN 896, KV cache 8192, fused "
+                        "(6 launches): add+RMSNorm+GEMV qkv -> RoPE+append+attend (2) -> GEMV o -> add+RMSNorm+GEMV "
+                        "gate|up+SwiGLU -> GEMV down",
             "step": report("decode layer", total, ms), "us_per_layer_graph": round(ms * 1e3, 3),
             "us_per_layer_eager": round(ms_eager * 1e3, 3), "ms_range": [round(lo, 5), round(hi, 5)],
+            "unfused": {"launches": 11, "us_per_layer_graph": round(ms_unfused * 1e3, 3),
+                        "us_per_layer_eager": round(ms_unfused_eager * 1e3, 3)},
             "bytes_by_op": b, "attend_splits": splits, "kernels": kern, "sets": nsets}
 
 

@@ -118,6 +118,11 @@ _SIGNATURES = {
     "uocr_rocm_append_step": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_attend_scratch_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_attend_step": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
+    "uocr_rocm_add_rms_norm_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_add_rms_norm_swiglu_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _vp, _i64, _vp],
+                                                _int),
+    "uocr_rocm_attend_rope_kv_step": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp,
+                                       _i64, _vp, _i64, _vp], _int),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -429,3 +434,38 @@ def attend_step(q, k_cache, v_cache, heads, hd, mask, scale, state, scratch, out
         raise ValueError("scratch is smaller than attend_scratch_floats(heads, hd, capacity)")
     _op("uocr_rocm_attend_step", stream, _ptr(q), _ptr(k_cache), _ptr(v_cache), heads, hd, _f32_param(mask), scale,
         _ptr(state), _ptr(scratch), capacity, _ptr(out))
+
+
+# ---- fused decode-step ops -------------------------------------------------------------------
+
+
+def add_rms_norm_gemv_bf16(x, w, y, delta=None, x_out=None, w_norm=None, eps=1e-6, h_out=None, bias=None,
+                           stream=None):
+    """y = bf16(h) . w^T (+ bias) with h = rms_norm(x + delta) * w_norm in one
+    launch; x_out receives x + delta and h_out the fp32 h when given."""
+    n, k = w.shape
+    _op("uocr_rocm_add_rms_norm_gemv_bf16", stream, _ptr(x), _ptr(delta), _ptr(x_out), _f32_param(w_norm), eps,
+        _ptr(h_out), k, _ptr(w), n, _f32_param(bias), _ptr(y))
+
+
+def add_rms_norm_swiglu_gemv_bf16(x, w_gate, w_up, act, delta=None, x_out=None, w_norm=None, eps=1e-6, h_out=None,
+                                  stream=None):
+    """act = silu(bf16(h) . w_gate^T) * (bf16(h) . w_up^T), h as above, in one launch."""
+    ffn, k = w_gate.shape
+    if tuple(w_up.shape) != (ffn, k):
+        raise ValueError("w_gate and w_up must have the same shape")
+    _op("uocr_rocm_add_rms_norm_swiglu_gemv_bf16", stream, _ptr(x), _ptr(delta), _ptr(x_out), _f32_param(w_norm),
+        eps, _ptr(h_out), k, _ptr(w_gate), _ptr(w_up), ffn, _ptr(act))
+
+
+def attend_rope_kv_step(q, k_row, v_row, k_cache, v_cache, heads, hd, mask, scale, state, inv_tok, inv_page,
+                        page_mod, scratch, out, stream=None):
+    """rope_qk_step on (q, k_row), append of the rotated key and v_row at
+    state.pos, and attend_step, in two launches (q, k_row, v_row untouched)."""
+    capacity = k_cache.numel() // (heads * hd) if heads * hd else 0
+    if scratch.numel() < attend_scratch_floats(heads, hd, capacity):
+        raise ValueError("scratch is smaller than attend_scratch_floats(heads, hd, capacity)")
+    n_tok = 0 if inv_tok is None else inv_tok.numel()
+    _op("uocr_rocm_attend_rope_kv_step", stream, _ptr(q), _ptr(k_row), _ptr(v_row), _ptr(k_cache), _ptr(v_cache),
+        heads, hd, _f32_param(mask), scale, _ptr(state), _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod,
+        _ptr(scratch), capacity, _ptr(out))

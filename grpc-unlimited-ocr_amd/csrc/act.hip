@@ -59,16 +59,6 @@ __device__ __forceinline__ float gelu_f(float x) {
   return x * phi;
 }
 
-// silu(g) u = g sigmoid(g) u with sigmoid(g) = 1 / (1 + e^-g); e^-g is
-// 2^(-g log2 e) on v_exp_f32 and the reciprocal is v_rcp_f32 (1 ulp each),
-// as in the reference's ops.cpp:40,163-167 and feed_forward.cpp:21-22.
-// g -> -inf gives 1 / inf = 0 and g * 0, as the reference does.
-__device__ __forceinline__ float silu_mul_f(float g, float u) {
-  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
-  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
-  return (g * sig) * u;
-}
-
 // quick_gelu: v sigmoid(1.702 v) (src/backend/reference/ops.cpp:157-161), the
 // CLIP MLP's activation, on the same exp2 / reciprocal as silu.
 __device__ __forceinline__ float quick_gelu_f(float v) {

@@ -142,6 +142,18 @@ __device__ __forceinline__ void load_f32(const float* p, float (&v)[VW]) {
 template <class T>
 constexpr int kVec = 16 / static_cast<int>(sizeof(T));
 
+// ---- activations shared by several kernels -----------------------------------
+
+// silu(g) u = g sigmoid(g) u with sigmoid(g) = 1 / (1 + e^-g); e^-g is
+// 2^(-g log2 e) on v_exp_f32 and the reciprocal is v_rcp_f32 (1 ulp each),
+// as in the reference's ops.cpp:40,163-167 and feed_forward.cpp:21-22.
+// g -> -inf gives 1 / inf = 0 and g * 0, as the reference does.
+__device__ __forceinline__ float silu_mul_f(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
+  return (g * sig) * u;
+}
+
 // ---- wave64 reductions ------------------------------------------------------
 // A butterfly over DPP lane permutations inside each 16-lane row, then the
 // four row totals read through readlane (SGPRs). Every lane of the wave must

@@ -79,6 +79,16 @@ struct AttendArgs {
   float scale;
   int hd;
   int splits;
+  // With rope and append (kRope): the step's new K and V rows [width], the
+  // caches to append them to, and the rope tables.
+  const float* k_row;
+  const float* v_row;
+  float* k_out;
+  float* v_out;
+  const float* inv_tok;
+  const float* inv_page;
+  int64_t page_mod;
+  int n_tok;
 };
 
 __device__ __forceinline__ float exp_shift(float s, float m) { return __builtin_amdgcn_exp2f((s - m) * kLog2e); }
@@ -90,6 +100,7 @@ struct KeyBatch {
   Chunk<float, VW> k[U][VPL];
   Chunk<float, VW> v[U][VPL];
   float mk[U];
+  bool is_new[U];  // the step's own key (kRope): its K and V come from LDS
 };
 
 // One lane group's running softmax state over its keys.
@@ -100,7 +111,7 @@ struct Running {
   float acc[VPL][VW];
 };
 
-template <int VW, int G, int VPL, int U>
+template <int VW, int G, int VPL, int U, bool kRope>
 __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   constexpr int kSlotsPerWave = kWave / G;
   constexpr int kSlots = kWavesPerBlock * kSlotsPerWave;
@@ -111,6 +122,7 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   __shared__ float s_m[kSlots];
   __shared__ float s_l[kSlots];
   __shared__ float s_acc[kSlots * G * kPerLane];
+  __shared__ float s_new[kRope ? 3 : 1][kRope ? kMaxHeadDim : 1];  // rotated q, rotated k, v of this head
 
   // Split-major: the heads' workgroups of one key range are dispatched
   // together and read the same cache rows.
@@ -119,13 +131,47 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int slot = (threadIdx.x / kWave) * kSlotsPerWave + lane / G;
   const int gl = lane % G;
-  int64_t keys = a.state->pos + 1;
+  const int64_t pos = a.state->pos;
+  int64_t keys = pos + 1;
   keys = keys < 0 ? 0 : (keys > a.capacity ? a.capacity : keys);
   const int64_t chunk = (keys + a.splits - 1) / a.splits;
   const int64_t first = split * chunk;
   const int64_t last = first + chunk < keys ? first + chunk : keys;
   const int nvec = a.hd / VW;
   const int64_t head_off = static_cast<int64_t>(h) * a.hd;
+
+  if constexpr (kRope) {
+    // rope on this head's q and new k, with rope.hip's arithmetic: angle =
+    // float(tok) inv_tok[p] (or float(page mod page_mod) inv_page[p - n_tok]),
+    // device sincosf, a c - b s / b c + a s without contraction.
+    const int half = a.hd / 2;
+    int64_t pg = a.state->page;
+    if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
+    const float ft = static_cast<float>(a.state->tok), fp = static_cast<float>(pg);
+    for (int p = threadIdx.x; p < half; p += kBlock) {
+      const float angle = p < a.n_tok ? ft * a.inv_tok[p] : fp * a.inv_page[p - a.n_tok];
+      float sn, cs;
+      sincosf(angle, &sn, &cs);
+      const float qa = a.q[head_off + p], qb = a.q[head_off + p + half];
+      const float ka = a.k_row[head_off + p], kb = a.k_row[head_off + p + half];
+      {
+#pragma clang fp contract(off)
+        s_new[0][p] = qa * cs - qb * sn;
+        s_new[0][p + half] = qb * cs + qa * sn;
+        s_new[1][p] = ka * cs - kb * sn;
+        s_new[1][p + half] = kb * cs + ka * sn;
+      }
+    }
+    for (int t = threadIdx.x; t < a.hd; t += kBlock) s_new[2][t] = a.v_row[head_off + t];
+    __syncthreads();
+    // The split that holds key pos appends the head's rotated k and its v.
+    if (pos >= first && pos < last) {
+      for (int t = threadIdx.x; t < a.hd; t += kBlock) {
+        a.k_out[pos * a.width + head_off + t] = s_new[1][t];
+        a.v_out[pos * a.width + head_off + t] = s_new[2][t];
+      }
+    }
+  }
 
   // This lane's chunks of the head: c = gl + G i; lanes past the head (when
   // nvec is not a power of two) address the head's last chunk and their
@@ -139,7 +185,13 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
     in_head[i] = c < nvec;
     col[i] = head_off + static_cast<int64_t>(in_head[i] ? c : nvec - 1) * VW;
 #pragma unroll
-    for (int e = 0; e < VW; ++e) qv[i][e] = in_head[i] ? a.q[col[i] + e] : 0.0f;
+    for (int e = 0; e < VW; ++e) {
+      if constexpr (kRope) {
+        qv[i][e] = in_head[i] ? s_new[0][col[i] - head_off + e] : 0.0f;
+      } else {
+        qv[i][e] = in_head[i] ? a.q[col[i] + e] : 0.0f;
+      }
+    }
   }
 
   Running<VW, VPL> run;
@@ -158,18 +210,19 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
       const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
       const bool in = j < t1;
       b.mk[u] = in ? (a.mask != nullptr ? s_mask[j - t0] : 0.0f) : -INFINITY;
+      b.is_new[u] = kRope && in && j == pos;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
-      const bool live = b.mk[u] != -INFINITY;
+      const bool live = b.mk[u] != -INFINITY && !b.is_new[u];
 #pragma unroll
       for (int i = 0; i < VPL; ++i) b.k[u][i].load(live ? a.k + j * a.width + col[i] : a.q + col[i]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
-      const bool live = b.mk[u] != -INFINITY;
+      const bool live = b.mk[u] != -INFINITY && !b.is_new[u];
 #pragma unroll
       for (int i = 0; i < VPL; ++i) b.v[u][i].load(live ? a.v + j * a.width + col[i] : a.q + col[i]);
     }
@@ -185,6 +238,12 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
       for (int i = 0; i < VPL; ++i) {
         float kv[VW];
         b.k[u][i].widen(kv);
+        if constexpr (kRope) {
+          if (b.is_new[u]) {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) kv[e] = s_new[1][col[i] - head_off + e];
+          }
+        }
 #pragma unroll
         for (int e = 0; e < VW; ++e) d = fmaf(qv[i][e], in_head[i] ? kv[e] : 0.0f, d);
       }
@@ -210,6 +269,12 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
       for (int i = 0; i < VPL; ++i) {
         float vv[VW];
         b.v[u][i].widen(vv);
+        if constexpr (kRope) {
+          if (b.is_new[u]) {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) vv[e] = s_new[2][col[i] - head_off + e];
+          }
+        }
 #pragma unroll
         for (int e = 0; e < VW; ++e) run.acc[i][e] = fmaf(p, in_head[i] ? vv[e] : 0.0f, run.acc[i][e]);
       }
@@ -352,9 +417,9 @@ int attend_splits(int64_t heads, int64_t capacity) {
   return static_cast<int>(s < 1 ? 1 : s);
 }
 
-template <int VW, int G, int VPL, int U>
+template <int VW, int G, int VPL, int U, bool kRope>
 void launch_partial(hipStream_t s, const AttendArgs& a, int64_t heads) {
-  attend_partial<VW, G, VPL, U><<<static_cast<unsigned>(heads * a.splits), kBlock, 0, s>>>(a);
+  attend_partial<VW, G, VPL, U, kRope><<<static_cast<unsigned>(heads * a.splits), kBlock, 0, s>>>(a);
 }
 
 // Lanes per key and keys per batch. Up to 8192 positions two keys per batch
@@ -362,29 +427,41 @@ void launch_partial(hipStream_t s, const AttendArgs& a, int64_t heads) {
 // four keys per batch and, for 128-wide heads, 16 lanes of two chunks each
 // per key. Both depend on the capacity only, so a captured step keeps its
 // launch shape at every position.
+template <bool kRope>
 void launch_attend_vec(hipStream_t s, const AttendArgs& a, int64_t heads) {
   const int nvec = a.hd / 4;
   const bool long_ctx = a.capacity > 8192;
-  if (nvec <= 1) launch_partial<4, 1, 1, 2>(s, a, heads);
-  else if (nvec <= 2) launch_partial<4, 2, 1, 2>(s, a, heads);
-  else if (nvec <= 4) launch_partial<4, 4, 1, 2>(s, a, heads);
-  else if (nvec <= 8) launch_partial<4, 8, 1, 2>(s, a, heads);
+  if (nvec <= 1) launch_partial<4, 1, 1, 2, kRope>(s, a, heads);
+  else if (nvec <= 2) launch_partial<4, 2, 1, 2, kRope>(s, a, heads);
+  else if (nvec <= 4) launch_partial<4, 4, 1, 2, kRope>(s, a, heads);
+  else if (nvec <= 8) launch_partial<4, 8, 1, 2, kRope>(s, a, heads);
   else if (nvec <= 16) {
-    if (long_ctx) launch_partial<4, 16, 1, 4>(s, a, heads);
-    else launch_partial<4, 16, 1, 2>(s, a, heads);
+    if (long_ctx) launch_partial<4, 16, 1, 4, kRope>(s, a, heads);
+    else launch_partial<4, 16, 1, 2, kRope>(s, a, heads);
   } else if (nvec <= 32) {
-    if (long_ctx) launch_partial<4, 16, 2, 4>(s, a, heads);
-    else launch_partial<4, 32, 1, 2>(s, a, heads);
+    if (long_ctx) launch_partial<4, 16, 2, 4, kRope>(s, a, heads);
+    else launch_partial<4, 32, 1, 2, kRope>(s, a, heads);
   } else {
-    if (long_ctx) launch_partial<4, 64, 1, 4>(s, a, heads);
-    else launch_partial<4, 64, 1, 2>(s, a, heads);
+    if (long_ctx) launch_partial<4, 64, 1, 4, kRope>(s, a, heads);
+    else launch_partial<4, 64, 1, 2, kRope>(s, a, heads);
   }
 }
 
+template <bool kRope>
 void launch_attend_any(hipStream_t s, const AttendArgs& a, int64_t heads) {
-  if (a.hd <= 64) launch_partial<1, 64, 1, 2>(s, a, heads);
-  else if (a.hd <= 128) launch_partial<1, 64, 2, 2>(s, a, heads);
-  else launch_partial<1, 64, 4, 2>(s, a, heads);
+  if (a.hd <= 64) launch_partial<1, 64, 1, 2, kRope>(s, a, heads);
+  else if (a.hd <= 128) launch_partial<1, 64, 2, 2, kRope>(s, a, heads);
+  else launch_partial<1, 64, 4, 2, kRope>(s, a, heads);
+}
+
+void launch_merge(hipStream_t s, const AttendArgs& a, int64_t heads, float* out) {
+  if (a.hd <= kWave) {
+    attend_merge<1><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(a.part, a.hd, a.splits, out);
+  } else if (a.hd <= 2 * kWave) {
+    attend_merge<2><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(a.part, a.hd, a.splits, out);
+  } else {
+    attend_merge<4><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(a.part, a.hd, a.splits, out);
+  }
 }
 
 }  // namespace
@@ -430,23 +507,76 @@ int uocr_rocm_attend_step(void* stream, const float* q, const float* k_cache, co
   UOCR_REQUIRE(q != nullptr && k_cache != nullptr && v_cache != nullptr && state != nullptr && scratch != nullptr &&
                    out != nullptr,
                what, "null pointer");
-  AttendArgs a{q, k_cache, v_cache, mask, scratch, state, heads * hd, capacity, scale, static_cast<int>(hd),
-               attend_splits(heads, capacity)};
+  AttendArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.mask = mask;
+  a.part = scratch;
+  a.state = state;
+  a.width = heads * hd;
+  a.capacity = capacity;
+  a.scale = scale;
+  a.hd = static_cast<int>(hd);
+  a.splits = attend_splits(heads, capacity);
   const hipStream_t s = as_stream(stream);
   clear_launch_error();
   if (hd % 4 == 0 && aligned16(q) && aligned16(k_cache) && aligned16(v_cache)) {
-    launch_attend_vec(s, a, heads);
+    launch_attend_vec<false>(s, a, heads);
   } else {
-    launch_attend_any(s, a, heads);
+    launch_attend_any<false>(s, a, heads);
   }
   if (const int st = check_launch(what); st != UOCR_ROCM_OK) return st;
-  if (hd <= kWave) {
-    attend_merge<1><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(scratch, a.hd, a.splits, out);
-  } else if (hd <= 2 * kWave) {
-    attend_merge<2><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(scratch, a.hd, a.splits, out);
+  launch_merge(s, a, heads, out);
+  return check_launch(what);
+}
+
+int uocr_rocm_attend_rope_kv_step(void* stream, const float* q, const float* k_row, const float* v_row,
+                                  float* k_cache, float* v_cache, int64_t heads, int64_t hd, const float* mask,
+                                  float scale, const uocr_rocm_step_state* state, const float* inv_tok, int64_t n_tok,
+                                  const float* inv_page, int64_t page_mod, float* scratch, int64_t capacity,
+                                  float* out) {
+  const char* what = "uocr_rocm_attend_rope_kv_step";
+  UOCR_REQUIRE(heads >= 0 && hd >= 0, what, "heads and hd must be >= 0");
+  if (heads == 0 || hd == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(hd <= kMaxHeadDim && hd % 2 == 0, what, "head dim must be even and at most 256");
+  UOCR_REQUIRE(heads < (int64_t{1} << 24), what, "too many heads");
+  UOCR_REQUIRE(capacity >= 1, what, "capacity must be >= 1");
+  UOCR_REQUIRE(n_tok >= 0 && n_tok <= hd / 2, what, "n_tok must be in [0, hd / 2]");
+  UOCR_REQUIRE(n_tok == 0 || inv_tok != nullptr, what, "null inv_tok");
+  UOCR_REQUIRE(n_tok == hd / 2 || inv_page != nullptr, what, "null inv_page");
+  UOCR_REQUIRE(q != nullptr && k_row != nullptr && v_row != nullptr && k_cache != nullptr && v_cache != nullptr &&
+                   state != nullptr && scratch != nullptr && out != nullptr,
+               what, "null pointer");
+  AttendArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.mask = mask;
+  a.part = scratch;
+  a.state = state;
+  a.width = heads * hd;
+  a.capacity = capacity;
+  a.scale = scale;
+  a.hd = static_cast<int>(hd);
+  a.splits = attend_splits(heads, capacity);
+  a.k_row = k_row;
+  a.v_row = v_row;
+  a.k_out = k_cache;
+  a.v_out = v_cache;
+  a.inv_tok = inv_tok;
+  a.inv_page = inv_page;
+  a.page_mod = page_mod;
+  a.n_tok = static_cast<int>(n_tok);
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  if (hd % 4 == 0 && aligned16(q) && aligned16(k_cache) && aligned16(v_cache)) {
+    launch_attend_vec<true>(s, a, heads);
   } else {
-    attend_merge<4><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(scratch, a.hd, a.splits, out);
+    launch_attend_any<true>(s, a, heads);
   }
+  if (const int st = check_launch(what); st != UOCR_ROCM_OK) return st;
+  launch_merge(s, a, heads, out);
   return check_launch(what);
 }
 

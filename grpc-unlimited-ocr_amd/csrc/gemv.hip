@@ -173,6 +173,224 @@ void launch_reg(hipStream_t s, const float* x, int nchunks, const uint16_t* w, i
   }
 }
 
+// ---- fused decode GEMVs ----------------------------------------------------------
+//
+// The decode step's projections take the residual stream's add + RMSNorm as
+// a prologue: every workgroup reduces the one input row itself (k <= 2048,
+// a few KB from L2), so the normalised row never round-trips through HBM and
+// the norm's launch disappears. The reduction is the row kernel's own
+// (norm.hip): 4-float chunks, 64-chunk groups, one wave butterfly per group,
+// group sums folded in order, inv formed in fp64; h = w * (s * inv) with no
+// contraction. h is therefore bitwise the h that add_rms_norm writes, and y
+// bitwise what gemv_bf16 gives on it. With two weight matrices the rows pair
+// up (gate row r, up row r) and the epilogue is SwiGLU, so
+// y[r] = silu(gate_r . h) (up_r . h), bitwise the swiglu of the two GEMVs.
+
+constexpr int kFusedMaxK = kWave * kGemvRegChunks * 8;  // 2048: bf16(h) stays in VGPRs
+
+struct FusedGemv {
+  const float* x;       // residual row [k]
+  const float* delta;   // added to x first, or null
+  float* x_out;         // x + delta written here by workgroup 0, or null
+  const float* w_norm;  // RMSNorm weight [k], or null for h = x (+ delta)
+  float* h_out;         // the fp32 h written here by workgroup 0, or null
+  const uint16_t* w1;   // [n, k] bf16 (the gate rows when w2 is set)
+  const uint16_t* w2;   // [n, k] bf16 up rows, or null
+  const float* bias;    // [n] or null (single matrix only)
+  float* y;             // [n]
+  int64_t n;
+  int k;
+  float eps;
+};
+
+// The prologue: the workgroup holds the row once, in the row kernel's layout
+// (4-float chunks v = (wave + 4 g) 64 + lane), reduces it in that kernel's
+// order, and writes bf16(h) to LDS, from which every wave reads its 8-float
+// GEMV chunks. x, delta and w_norm are read once per workgroup.
+template <bool kNorm>
+__device__ __forceinline__ void fused_prologue(const FusedGemv& a, float* h_lds, int wave, int lane) {
+  __shared__ float red[kMaxGroups];
+  constexpr int kG = kFusedMaxK / 4 / kWave / kWavesPerBlock;  // 2 groups per wave
+  const int nvec = a.k / 4;
+  const int groups = (nvec + kWave - 1) / kWave;
+  float s[kG][4], wn[kG][4];
+#pragma unroll
+  for (int g = 0; g < kG; ++g) {
+    const int v = (wave + kWavesPerBlock * g) * kWave + lane;
+    const int vc = v < nvec ? v : nvec - 1;
+    load_f32<4>(a.x + 4 * vc, s[g]);
+    if (a.delta != nullptr) {
+      float d[4];
+      load_f32<4>(a.delta + 4 * vc, d);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[g][e] += d[e];
+    }
+    if constexpr (kNorm) load_f32<4>(a.w_norm + 4 * vc, wn[g]);
+  }
+  float part[kG];
+#pragma unroll
+  for (int g = 0; g < kG; ++g) {
+    const int v = (wave + kWavesPerBlock * g) * kWave + lane;
+    part[g] = 0.0f;
+    if (v < nvec) {
+      if (blockIdx.x == 0 && a.x_out != nullptr) {
+        *reinterpret_cast<u32x4*>(a.x_out + 4 * v) = u32x4{__float_as_uint(s[g][0]), __float_as_uint(s[g][1]),
+                                                          __float_as_uint(s[g][2]), __float_as_uint(s[g][3])};
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part[g] += s[g][e] * s[g][e];
+    }
+  }
+  float inv = 0.0f;
+  if constexpr (kNorm) {
+    const float ss = fold_groups<kWavesPerBlock, kG>(part, wave, groups, red);
+    inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss) / static_cast<double>(a.k) +
+                                        static_cast<double>(a.eps)));
+  }
+#pragma unroll
+  for (int g = 0; g < kG; ++g) {
+    const int v = (wave + kWavesPerBlock * g) * kWave + lane;
+    if (v < nvec) {
+      float h[4];
+      if constexpr (kNorm) {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = wn[g][e] * (s[g][e] * inv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = s[g][e];
+      }
+      if (blockIdx.x == 0 && a.h_out != nullptr) {
+        *reinterpret_cast<u32x4*>(a.h_out + 4 * v) =
+            u32x4{__float_as_uint(h[0]), __float_as_uint(h[1]), __float_as_uint(h[2]), __float_as_uint(h[3])};
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h_lds[4 * v + e] = round_bf16(h[e]);
+    }
+  }
+  __syncthreads();
+}
+
+template <int CPL, int RPW, bool kNorm, bool kPair>
+__global__ __launch_bounds__(kBlock) void gemv_fused(const FusedGemv a) {
+  constexpr int kMats = kPair ? 2 : 1;
+  __shared__ __align__(16) float h_lds[kFusedMaxK];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int nchunks = a.k / 8;
+  const int64_t k = a.k;
+  const int64_t groups = (a.n + RPW - 1) / RPW;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  const int64_t g0 = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
+
+  u32x4 wc[kMats][RPW][CPL];
+  auto load_w = [&](int64_t g) {
+    const int64_t row0 = g * RPW;
+#pragma unroll
+    for (int m = 0; m < kMats; ++m) {
+      const uint16_t* w = m == 0 ? a.w1 : a.w2;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const int c = lane + kWave * i;
+          wc[m][r][i] = u32x4{0u, 0u, 0u, 0u};
+          if (row0 + r < a.n && c < nchunks) {
+            wc[m][r][i] = stream_load(reinterpret_cast<const u32x4*>(w + (row0 + r) * k) + c);
+          }
+        }
+      }
+    }
+  };
+  // The first rows' weights go out before the prologue's loads, so both are
+  // in flight together.
+  if (g0 < groups) load_w(g0);
+  fused_prologue<kNorm>(a, h_lds, wave, lane);
+  float xv[CPL][8];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + kWave * i;
+    if (c < nchunks) {
+      load_f32<8>(h_lds + 8 * c, xv[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
+    }
+  }
+  for (int64_t g = g0; g < groups; g += step) {
+    if (g != g0) load_w(g);
+    const int64_t row0 = g * RPW;
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      float d1 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) d1 = dot8(wc[0][r][i], xv[i], d1);
+      d1 = wave_sum(d1);
+      if constexpr (kPair) {
+        float d2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) d2 = dot8(wc[kMats - 1][r][i], xv[i], d2);
+        d2 = wave_sum(d2);
+        // + 0.0f as the single-matrix store forms its outputs (a -0 sum
+        // becomes +0), so the pair matches two GEMVs then silu_mul bitwise.
+        acc[r] = silu_mul_f(d1 + 0.0f, d2 + 0.0f);
+      } else {
+        acc[r] = d1 + (a.bias != nullptr && row0 + r < a.n ? a.bias[row0 + r] : 0.0f);
+      }
+    }
+    for (int r = 0; r < RPW; ++r) {
+      if (lane == r && row0 + r < a.n) a.y[row0 + r] = acc[r];
+    }
+  }
+}
+
+template <int CPL, bool kNorm, bool kPair>
+void launch_fused_rows(hipStream_t s, const FusedGemv& a) {
+  if (a.n >= 16384) {
+    gemv_fused<CPL, 4, kNorm, kPair><<<gemv_blocks((a.n + 3) / 4), kBlock, 0, s>>>(a);
+  } else {
+    gemv_fused<CPL, 1, kNorm, kPair><<<gemv_blocks(a.n), kBlock, 0, s>>>(a);
+  }
+}
+
+template <bool kNorm, bool kPair>
+void launch_fused(hipStream_t s, const FusedGemv& a) {
+  switch ((a.k / 8 + kWave - 1) / kWave) {
+    case 1: launch_fused_rows<1, kNorm, kPair>(s, a); break;
+    case 2: launch_fused_rows<2, kNorm, kPair>(s, a); break;
+    case 3: launch_fused_rows<3, kNorm, kPair>(s, a); break;
+    default: launch_fused_rows<kGemvRegChunks, kNorm, kPair>(s, a); break;
+  }
+}
+
+int fused_entry(const char* what, void* stream, FusedGemv a) {
+  UOCR_REQUIRE(a.k >= 0 && a.n >= 0, what, "k and n must be >= 0");
+  if (a.n == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(a.k % 8 == 0 && a.k >= 8 && a.k <= kFusedMaxK, what, "k must be a multiple of 8 in [8, 2048]");
+  UOCR_REQUIRE(a.x != nullptr && a.w1 != nullptr && a.y != nullptr, what, "null x, w or y");
+  UOCR_REQUIRE(a.n < (int64_t{1} << 40), what, "n too large");
+  UOCR_REQUIRE(aligned16(a.x) && aligned16(a.w1) && (a.w2 == nullptr || aligned16(a.w2)) &&
+                   (a.delta == nullptr || aligned16(a.delta)) && (a.x_out == nullptr || aligned16(a.x_out)) &&
+                   (a.w_norm == nullptr || aligned16(a.w_norm)) && (a.h_out == nullptr || aligned16(a.h_out)),
+               what, "x, delta, x_out, w_norm, h_out and the weights must be 16-byte aligned");
+  // Every workgroup reads x and delta while workgroup 0 writes x_out and
+  // h_out, so those must not overlap the inputs.
+  auto overlaps = [&](const float* out, const float* in) {
+    return out != nullptr && in != nullptr && out < in + a.k && in < out + a.k;
+  };
+  UOCR_REQUIRE(!overlaps(a.x_out, a.x) && !overlaps(a.x_out, a.delta) && !overlaps(a.h_out, a.x) &&
+                   !overlaps(a.h_out, a.delta) && !overlaps(a.x_out, a.h_out),
+               what, "x_out and h_out must not overlap x, delta or each other");
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  const bool norm = a.w_norm != nullptr, pair = a.w2 != nullptr;
+  if (norm && pair) launch_fused<true, true>(s, a);
+  else if (norm) launch_fused<true, false>(s, a);
+  else if (pair) launch_fused<false, true>(s, a);
+  else launch_fused<false, false>(s, a);
+  return check_launch(what);
+}
+
 }  // namespace
 }  // namespace uocr_rocm
 
@@ -208,6 +426,26 @@ int uocr_rocm_gemv_bf16(void* stream, const float* x, int64_t k, const uint16_t*
       break;
   }
   return check_launch(what);
+}
+
+int uocr_rocm_add_rms_norm_gemv_bf16(void* stream, const float* x, const float* delta, float* x_out,
+                                     const float* w_norm, float eps, float* h_out, int64_t k, const uint16_t* w,
+                                     int64_t n, const float* bias, float* y) {
+  if (k < 0 || k > kFusedMaxK) return fail(UOCR_ROCM_INVALID_ARGUMENT, "uocr_rocm_add_rms_norm_gemv_bf16",
+                                           "k must be a multiple of 8 in [8, 2048]");
+  return fused_entry("uocr_rocm_add_rms_norm_gemv_bf16", stream,
+                     FusedGemv{x, delta, x_out, w_norm, h_out, w, nullptr, bias, y, n, static_cast<int>(k), eps});
+}
+
+int uocr_rocm_add_rms_norm_swiglu_gemv_bf16(void* stream, const float* x, const float* delta, float* x_out,
+                                            const float* w_norm, float eps, float* h_out, int64_t k,
+                                            const uint16_t* w_gate, const uint16_t* w_up, int64_t ffn, float* act) {
+  const char* what = "uocr_rocm_add_rms_norm_swiglu_gemv_bf16";
+  if (k < 0 || k > kFusedMaxK) return fail(UOCR_ROCM_INVALID_ARGUMENT, what, "k must be a multiple of 8 in [8, 2048]");
+  UOCR_REQUIRE(ffn == 0 || w_up != nullptr, what, "null up weights");
+  return fused_entry(what, stream,
+                     FusedGemv{x, delta, x_out, w_norm, h_out, w_gate, w_up, nullptr, act, ffn, static_cast<int>(k),
+                               eps});
 }
 
 }  // extern "C"

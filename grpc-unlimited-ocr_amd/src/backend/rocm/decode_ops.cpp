@@ -63,4 +63,12 @@ void attend_step(const Context& ctx, const float* q, const float* k_cache, const
                               out));
 }
 
+void attend_rope_kv_step(const Context& ctx, const float* q, const float* k_row, const float* v_row, float* k_cache,
+                         float* v_cache, std::int64_t heads, std::int64_t hd, const float* mask, float scale,
+                         const StepState* state, const float* inv_tok, std::int64_t n_tok, const float* inv_page,
+                         std::int64_t page_mod, float* scratch, std::int64_t capacity, float* out) {
+  check(uocr_rocm_attend_rope_kv_step(ctx.stream(), q, k_row, v_row, k_cache, v_cache, heads, hd, mask, scale,
+                                      abi(state), inv_tok, n_tok, inv_page, page_mod, scratch, capacity, out));
+}
+
 }  // namespace uocr::rocm

@@ -48,4 +48,12 @@ void attend_step(const Context& ctx, const float* q, const float* k_cache, const
                  std::int64_t hd, const float* mask, float scale, const StepState* state, float* scratch,
                  std::int64_t capacity, float* out);
 
+// New: rope_qk_step on (q, k_row), the appends of the rotated key and of
+// v_row at pos, and attend_step, in attend_step's two launches; q, k_row and
+// v_row are left unrotated.
+void attend_rope_kv_step(const Context& ctx, const float* q, const float* k_row, const float* v_row, float* k_cache,
+                         float* v_cache, std::int64_t heads, std::int64_t hd, const float* mask, float scale,
+                         const StepState* state, const float* inv_tok, std::int64_t n_tok, const float* inv_page,
+                         std::int64_t page_mod, float* scratch, std::int64_t capacity, float* out);
+
 }  // namespace uocr::rocm

@@ -140,4 +140,18 @@ void gemv_bf16(const Context& ctx, const float* x, std::int64_t k, const std::ui
   check(uocr_rocm_gemv_bf16(ctx.stream(), x, k, w, n, bias, y));
 }
 
+void add_rms_norm_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out, const float* w_norm,
+                            float eps, float* h_out, std::int64_t k, const std::uint16_t* w, std::int64_t n,
+                            const float* bias, float* y) {
+  check(uocr_rocm_add_rms_norm_gemv_bf16(ctx.stream(), x, delta, x_out, w_norm, eps, h_out, k, w, n, bias, y));
+}
+
+void add_rms_norm_swiglu_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out,
+                                   const float* w_norm, float eps, float* h_out, std::int64_t k,
+                                   const std::uint16_t* w_gate, const std::uint16_t* w_up, std::int64_t ffn,
+                                   float* act) {
+  check(uocr_rocm_add_rms_norm_swiglu_gemv_bf16(ctx.stream(), x, delta, x_out, w_norm, eps, h_out, k, w_gate, w_up,
+                                                ffn, act));
+}
+
 }  // namespace uocr::rocm

@@ -108,4 +108,15 @@ void scale_add_mask(const Context& ctx, float* x, float scale, const float* mask
 void gemv_bf16(const Context& ctx, const float* x, std::int64_t k, const std::uint16_t* w, std::int64_t n,
                const float* bias, float* y);
 
+// Fused decode projections (new): add + RMSNorm as the GEMV's prologue,
+// optionally a gate/up pair with a SwiGLU epilogue. delta, x_out, w_norm
+// and h_out may be null; k is a multiple of 8 in [8, 2048].
+void add_rms_norm_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out, const float* w_norm,
+                            float eps, float* h_out, std::int64_t k, const std::uint16_t* w, std::int64_t n,
+                            const float* bias, float* y);
+void add_rms_norm_swiglu_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out,
+                                   const float* w_norm, float eps, float* h_out, std::int64_t k,
+                                   const std::uint16_t* w_gate, const std::uint16_t* w_up, std::int64_t ffn,
+                                   float* act);
+
 }  // namespace uocr::rocm

@@ -318,6 +318,53 @@ UOCR_ROCM_API int uocr_rocm_attend_step(void* stream, const float* q, const floa
                                         const uocr_rocm_step_state* state, float* scratch, int64_t capacity,
                                         float* out);
 
+/* ---- fused decode-step ops (new) ---------------------------------------------
+ * One launch where the reference's decode step makes several; each gives
+ * bitwise the result of the unfused entry points it replaces. */
+
+/* add + RMSNorm feeding a bf16 GEMV:
+ *   s = x + delta (delta null: s = x);  x_out = s (null: not written);
+ *   h = w_norm * (s * inv(s)) (w_norm null: h = s);  h_out = h (null: not written);
+ *   y[n] = bf16(h) . w[n, :] (+ bias[n]).
+ * Bitwise uocr_rocm_add_rms_norm (or uocr_rocm_rms_norm) then
+ * uocr_rocm_gemv_bf16 on h. k is a multiple of 8 in [8, 2048]; every pointer
+ * 16-byte aligned; x_out and h_out must not overlap x or delta (every
+ * workgroup reads the input row). Replaces add_inplace + copy + rms_norm +
+ * apply_weight of the decode step (src/model/cuda/cuda_decode_step.cpp:
+ * 18-20,54-59,65-69: the layer's input norm and its projections, the final
+ * norm and the LM head). */
+UOCR_ROCM_API int uocr_rocm_add_rms_norm_gemv_bf16(void* stream, const float* x, const float* delta, float* x_out,
+                                                   const float* w_norm, float eps, float* h_out, int64_t k,
+                                                   const uint16_t* w, int64_t n, const float* bias, float* y);
+
+/* The same prologue feeding a gate/up pair with a SwiGLU epilogue:
+ *   act[r] = silu(bf16(h) . w_gate[r, :]) * (bf16(h) . w_up[r, :]),  r < ffn.
+ * Bitwise the two GEMVs then uocr_rocm_silu_mul. Replaces the residual add,
+ * post-attention norm, gate/up projections and silu_mul of the decode step
+ * (src/model/cuda/cuda_decode_step.cpp:57-61, cuda_decoder.cpp:119-124). */
+UOCR_ROCM_API int uocr_rocm_add_rms_norm_swiglu_gemv_bf16(void* stream, const float* x, const float* delta,
+                                                          float* x_out, const float* w_norm, float eps, float* h_out,
+                                                          int64_t k, const uint16_t* w_gate, const uint16_t* w_up,
+                                                          int64_t ffn, float* act);
+
+/* rope on q [heads * hd] and the step's new key k_row [heads * hd] at
+ * (state->tok, state->page), append of the rotated key and v_row at
+ * state->pos (positions outside [0, capacity) append nothing), and the
+ * masked attention of the rotated query over keys 0..pos, in the two
+ * launches of uocr_rocm_attend_step. q, k_row and v_row are not modified.
+ * Bitwise uocr_rocm_rope_qk_step, two uocr_rocm_append_step and
+ * uocr_rocm_attend_step (with rotated copies of q and k_row). hd even,
+ * at most 256; rope tables as uocr_rocm_rope_step (n_tok token pairs, the
+ * rest page pairs). Replaces the rope_step, append_step and attend_step
+ * calls of decode_attention (src/model/cuda/cuda_decode_step.cpp:27-28,
+ * 31-32,42-43). */
+UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step(void* stream, const float* q, const float* k_row,
+                                                const float* v_row, float* k_cache, float* v_cache, int64_t heads,
+                                                int64_t hd, const float* mask, float scale,
+                                                const uocr_rocm_step_state* state, const float* inv_tok,
+                                                int64_t n_tok, const float* inv_page, int64_t page_mod,
+                                                float* scratch, int64_t capacity, float* out);
+
 #ifdef __cplusplus
 }
 #endif
