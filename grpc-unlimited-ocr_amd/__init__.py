@@ -118,6 +118,7 @@ _SIGNATURES = {
     "uocr_rocm_append_step": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_attend_scratch_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_attend_step": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
+    "uocr_rocm_scale_mask_softmax_rows": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_add_rms_norm_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_add_rms_norm_swiglu_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _vp, _i64, _vp],
                                                 _int),
@@ -391,6 +392,16 @@ def scale_add_mask(x, scale, mask, batch, rows, cols, stream=None):
     if x.numel() != batch * rows * cols or (mask is not None and mask.numel() != rows * cols):
         raise ValueError("x must hold batch * rows * cols and mask rows * cols elements")
     _op("uocr_rocm_scale_add_mask", stream, _ptr(x), scale, _f32_param(mask), batch, rows, cols)
+
+
+def scale_mask_softmax_rows(x, scale, mask, batch, rows, cols, stream=None):
+    """x[b, r] = softmax(x[b, r] * scale + mask[r]) in one pass (fp32; mask may
+    be None); bitwise scale_add_mask then softmax_rows."""
+    if _is_bf16(x):
+        raise ValueError("scale_mask_softmax_rows takes float32")
+    if x.numel() != batch * rows * cols or (mask is not None and mask.numel() != rows * cols):
+        raise ValueError("x must hold batch * rows * cols and mask rows * cols elements")
+    _op("uocr_rocm_scale_mask_softmax_rows", stream, _ptr(x), scale, _f32_param(mask), batch, rows, cols)
 
 
 # ---- decode-step neighbours ---------------------------------------------------------------

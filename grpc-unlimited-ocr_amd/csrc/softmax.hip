@@ -3,6 +3,9 @@
 // products in prefill and in the vision encoder (the reference's
 // softmax_rows and scale_add_mask, src/backend/cuda/ops.h:41-46).
 //
+// scale_mask_softmax_rows fuses the two: the scores are scaled and masked in
+// registers on the softmax's read, so they cross HBM once instead of twice.
+//
 // softmax_rows, layout as the norms (norm.hip): the row in registers, 64-
 // chunk groups, WPR waves per row (4 below kFewRows rows). Three steps over
 // the registers: the row max (an exact fold), e = exp(v - max) and its sum
@@ -27,8 +30,24 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int VW, int WPR, int VPL>
-__global__ __launch_bounds__(kBlock) void softmax_rows_k(float* __restrict__ x, int64_t rows, int cols) {
+// With kMask the row is first scaled and masked in registers, v = x * scale
+// + mask[row mod mask_rows] (no contraction), exactly as scale_add_mask forms
+// it: scale_mask_softmax_rows is then bitwise scale_add_mask + softmax_rows
+// with one read and one write of the scores instead of two of each.
+// Rows are visited mask-row-major: logical row R is slice R mod batch of mask
+// row R / batch, so the `batch` rows that share a mask row run side by side
+// and the mask row is mostly read from cache.
+struct RowMask {
+  const float* mask;  // [mask_rows, cols], or null (+ 0)
+  float scale;
+  int64_t mask_rows;
+  int64_t batch;
+  __device__ __forceinline__ int64_t mask_row(int64_t r) const { return r / batch; }
+  __device__ __forceinline__ int64_t data_row(int64_t r) const { return (r % batch) * mask_rows + r / batch; }
+};
+
+template <int VW, int WPR, int VPL, bool kMask>
+__global__ __launch_bounds__(kBlock) void softmax_rows_k(float* __restrict__ x, int64_t rows, int cols, RowMask rm) {
   constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
   __shared__ float red[kRowsPerBlock][kMaxGroups];
   const int wave = threadIdx.x / kWave;
@@ -38,15 +57,28 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_k(float* __restrict__ x, 
   const bool active = row < rows;
   const int nvec = cols / VW;
   const int groups = (nvec + kWave - 1) / kWave;
-  const int64_t off = (active ? row : 0) * cols;
+  const int64_t off = (active ? (kMask ? rm.data_row(row) : row) : 0) * cols;
 
   Chunk<float, VW> cx[VPL];
   float v[VPL][VW];
   float part[VPL];
+  // The mask chunks load together with the scores: a mask load issued after
+  // the scores' loads and waited on alone would drain the whole queue.
+  float m[kMask ? VPL : 1][VW];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int c = (wr + WPR * k) * kWave + lane;
-    if (active && c < nvec) cx[k].load(x + off + static_cast<int64_t>(c) * VW);
+    if (active && c < nvec) {
+      cx[k].load(x + off + static_cast<int64_t>(c) * VW);
+      if constexpr (kMask) {
+        if (rm.mask != nullptr) {
+          load_f32<VW>(rm.mask + rm.mask_row(row) * cols + static_cast<int64_t>(c) * VW, m[k]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < VW; ++e) m[k][e] = 0.0f;
+        }
+      }
+    }
   }
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
@@ -54,6 +86,11 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_k(float* __restrict__ x, 
     part[k] = -INFINITY;
     if (active && c < nvec) {
       cx[k].widen(v[k]);
+      if constexpr (kMask) {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int e = 0; e < VW; ++e) v[k][e] = v[k][e] * rm.scale + m[k][e];
+      }
 #pragma unroll
       for (int e = 0; e < VW; ++e) part[k] = fmaxf(part[k], v[k][e]);
     } else {
@@ -89,9 +126,22 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_k(float* __restrict__ x, 
   }
 }
 
-__global__ __launch_bounds__(kBlock) void softmax_rows_wide(float* x, int64_t cols) {
+template <bool kMask>
+__global__ __launch_bounds__(kBlock) void softmax_rows_wide(float* x, int64_t cols, RowMask rm) {
   __shared__ float red[kWavesPerBlock];
-  float* row = x + static_cast<int64_t>(blockIdx.x) * cols;
+  float* row = x + (kMask ? rm.data_row(blockIdx.x) : static_cast<int64_t>(blockIdx.x)) * cols;
+  if constexpr (kMask) {
+    // Scale and mask in place first (this workgroup owns the row).
+    const float* mrow = rm.mask != nullptr ? rm.mask + rm.mask_row(blockIdx.x) * cols : nullptr;
+    for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
+      const float mv = mrow != nullptr ? mrow[i] : 0.0f;
+      {
+#pragma clang fp contract(off)
+        row[i] = row[i] * rm.scale + mv;
+      }
+    }
+    __syncthreads();
+  }
   float m = -INFINITY;
   for (int64_t i = threadIdx.x; i < cols; i += kBlock) m = fmaxf(m, row[i]);
   const float peak = block_max(m, red);
@@ -107,17 +157,46 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_wide(float* x, int64_t co
   }
 }
 
-template <int VW, int WPR>
-void launch_softmax_rows(int vpl, hipStream_t s, float* x, int64_t rows, int cols) {
+template <int VW, int WPR, bool kMask>
+void launch_softmax_rows(int vpl, hipStream_t s, float* x, int64_t rows, int cols, const RowMask& rm) {
   constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
   const unsigned blocks = static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
   switch (vpl) {
-    case 1: softmax_rows_k<VW, WPR, 1><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
-    case 2: softmax_rows_k<VW, WPR, 2><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
-    case 4: softmax_rows_k<VW, WPR, 4><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
-    case 8: softmax_rows_k<VW, WPR, 8><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
-    default: softmax_rows_k<VW, WPR, 16><<<blocks, kBlock, 0, s>>>(x, rows, cols); break;
+    case 1: softmax_rows_k<VW, WPR, 1, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
+    case 2: softmax_rows_k<VW, WPR, 2, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
+    case 4: softmax_rows_k<VW, WPR, 4, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
+    case 8: softmax_rows_k<VW, WPR, 8, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
+    default: softmax_rows_k<VW, WPR, 16, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
   }
+}
+
+// Row softmax, optionally scaled and masked first; x [rows, cols], the mask
+// repeating every rm.mask_rows rows.
+template <bool kMask>
+int softmax_entry(const char* what, void* stream, float* x, int64_t rows, int64_t cols, const RowMask& rm) {
+  const bool vec = cols % 4 == 0 && aligned16(x) && (!kMask || rm.mask == nullptr || aligned16(rm.mask));
+  const int64_t nvec = vec ? cols / 4 : cols;
+  const int64_t groups = (nvec + kWave - 1) / kWave;
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  if (groups > kMaxGroups) {
+    softmax_rows_wide<kMask><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, cols, rm);
+    return check_launch(what);
+  }
+  // With a mask each lane holds twice the loads (scores and mask), so rows
+  // of 4+ groups spread over 4 waves to keep the registers, and the waves
+  // per SIMD, of the unmasked kernel.
+  const bool spread = groups > 16 || ((rows < kFewRows || kMask) && groups >= 4);
+  const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
+  const int c32 = static_cast<int>(cols);
+  if (vec) {
+    if (spread) launch_softmax_rows<4, 4, kMask>(vpl, s, x, rows, c32, rm);
+    else launch_softmax_rows<4, 1, kMask>(vpl, s, x, rows, c32, rm);
+  } else {
+    if (spread) launch_softmax_rows<1, 4, kMask>(vpl, s, x, rows, c32, rm);
+    else launch_softmax_rows<1, 1, kMask>(vpl, s, x, rows, c32, rm);
+  }
+  return check_launch(what);
 }
 
 // ---- scale and mask -------------------------------------------------------------
@@ -187,26 +266,19 @@ int uocr_rocm_softmax_rows(void* stream, float* x, int64_t rows, int64_t cols) {
   UOCR_REQUIRE(rows == 0 || (cols > 0 && cols < (int64_t{1} << 31)), what, "cols must be in [1, 2^31)");
   if (rows == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(x != nullptr, what, "null x");
-  const bool vec = cols % 4 == 0 && aligned16(x);
-  const int64_t nvec = vec ? cols / 4 : cols;
-  const int64_t groups = (nvec + kWave - 1) / kWave;
-  const hipStream_t s = as_stream(stream);
-  clear_launch_error();
-  if (groups > kMaxGroups) {
-    softmax_rows_wide<<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, cols);
-    return check_launch(what);
-  }
-  const bool spread = groups > 16 || (rows < kFewRows && groups >= 4);
-  const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
-  const int c32 = static_cast<int>(cols);
-  if (vec) {
-    if (spread) launch_softmax_rows<4, 4>(vpl, s, x, rows, c32);
-    else launch_softmax_rows<4, 1>(vpl, s, x, rows, c32);
-  } else {
-    if (spread) launch_softmax_rows<1, 4>(vpl, s, x, rows, c32);
-    else launch_softmax_rows<1, 1>(vpl, s, x, rows, c32);
-  }
-  return check_launch(what);
+  return softmax_entry<false>(what, stream, x, rows, cols, RowMask{nullptr, 1.0f, 1, 1});
+}
+
+int uocr_rocm_scale_mask_softmax_rows(void* stream, float* x, float scale, const float* mask, int64_t batch,
+                                      int64_t rows, int64_t cols) {
+  const char* what = "uocr_rocm_scale_mask_softmax_rows";
+  UOCR_REQUIRE(batch >= 0 && rows >= 0, what, "batch and rows must be >= 0");
+  UOCR_REQUIRE(batch == 0 || rows < (int64_t{1} << 31) / batch, what, "batch * rows must be below 2^31");
+  const int64_t all = batch * rows;
+  UOCR_REQUIRE(all == 0 || (cols > 0 && cols < (int64_t{1} << 31)), what, "cols must be in [1, 2^31)");
+  if (all == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(x != nullptr, what, "null x");
+  return softmax_entry<true>(what, stream, x, all, cols, RowMask{mask, scale, rows, batch});
 }
 
 int uocr_rocm_scale_add_mask(void* stream, float* x, float scale, const float* mask, int64_t batch, int64_t rows,

@@ -154,4 +154,9 @@ void add_rms_norm_swiglu_gemv_bf16(const Context& ctx, const float* x, const flo
                                                 ffn, act));
 }
 
+void scale_mask_softmax_rows(const Context& ctx, float* x, float scale, const float* mask, std::int64_t batch,
+                             std::int64_t rows, std::int64_t cols) {
+  check(uocr_rocm_scale_mask_softmax_rows(ctx.stream(), x, scale, mask, batch, rows, cols));
+}
+
 }  // namespace uocr::rocm

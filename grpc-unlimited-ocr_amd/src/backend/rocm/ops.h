@@ -102,6 +102,10 @@ void softmax_rows(const Context& ctx, float* x, std::int64_t rows, std::int64_t 
 void scale_add_mask(const Context& ctx, float* x, float scale, const float* mask, std::int64_t batch, std::int64_t rows,
                     std::int64_t cols);
 
+// New: scale_add_mask then softmax_rows in one pass over x (bitwise the same).
+void scale_mask_softmax_rows(const Context& ctx, float* x, float scale, const float* mask, std::int64_t batch,
+                             std::int64_t rows, std::int64_t cols);
+
 // ---- weight streaming (src/backend/cuda/gemv_ops.h:25-26) ---------------------------------
 
 // y[n] = bf16(x) . w[n, :] (+ bias[n]); x fp32 [k] (k <= 12288), w bf16 [n, k].

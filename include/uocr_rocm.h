@@ -281,6 +281,15 @@ UOCR_ROCM_API int uocr_rocm_softmax_rows(void* stream, float* x, int64_t rows, i
 UOCR_ROCM_API int uocr_rocm_scale_add_mask(void* stream, float* x, float scale, const float* mask, int64_t batch,
                                            int64_t rows, int64_t cols);
 
+/* Softmax of the scaled, masked scores in one pass (new): for each of `batch`
+ * slices of [rows, cols], x[b, r, :] = softmax(x[b, r, :] * scale + mask[r, :])
+ * (mask null: + 0). Bitwise uocr_rocm_scale_add_mask then
+ * uocr_rocm_softmax_rows, with one read and one write of x instead of two of
+ * each. batch * rows < 2^31. Replaces the pair in CudaDecoder::attention
+ * (src/model/cuda/cuda_decoder.cpp:241-242). */
+UOCR_ROCM_API int uocr_rocm_scale_mask_softmax_rows(void* stream, float* x, float scale, const float* mask,
+                                                    int64_t batch, int64_t rows, int64_t cols);
+
 /* ---- decode-step neighbours ---------------------------------------------------- */
 
 /* y[n] = bf16(x) . w[n, :] (+ bias[n]): x fp32 [k] rounded to bf16 (nearest

@@ -115,6 +115,24 @@ def test_scale_add_mask(backend, batch, rows, cols, masked):
     assert np.array_equal(host_f32(d), want)
 
 
+@pytest.mark.parametrize("batch,rows,cols,masked", [(10, 577, 577, True), (16, 64, 1024, True), (3, 33, 47, False),
+                                                    (2, 5, 20000, True), (4, 4096, 256, True)])
+def test_scale_mask_softmax_matches_the_pair(backend, batch, rows, cols, masked):
+    x = 4 * normal(145, (batch, rows, cols))
+    mask = None
+    if masked:
+        mask = np.triu(np.full((rows, cols), -np.inf, np.float32), 1) + 0.1 * normal(146, (rows, cols))
+        mask[1 % rows, :] = -np.inf  # a fully masked row becomes zeros
+    dm = None if mask is None else dev_f32(mask)
+    pair, fused = dev_f32(x), dev_f32(x)
+    backend.scale_add_mask(pair, 0.088, dm, batch, rows, cols)
+    backend.softmax_rows(pair.view(batch * rows, cols))
+    backend.scale_mask_softmax_rows(fused, 0.088, dm, batch, rows, cols)
+    assert np.array_equal(host_f32(fused).view(np.uint32), host_f32(pair).view(np.uint32))
+    want = oracle.softmax_rows(oracle.scale_add_mask(x, 0.088, mask, batch, rows, cols).reshape(-1, cols))
+    assert_f32_close(host_f32(fused).reshape(-1, cols), want, 1e-5, "scale_mask_softmax")
+
+
 # ---- GEMV ---------------------------------------------------------------------------------------
 
 
