@@ -237,14 +237,23 @@ def config2(be, torch, timer):
     chain_bytes = (bytes_gather(1, hidden, 2) + bytes_add_rms_norm(1, hidden, 2)
                    + bytes_rope(1, qh + kh, dim, 2, pos_bytes=8))
 
-    def chain():
+    def chain():  # the embedding gather fused with the residual add + RMSNorm: two launches
+        be.embed_add_rms_norm_step(table, state, w, x, h, delta=delta)
+        be.rope_qk_step(q, qh, k, kh, dim, state, inv, None, 0)
+
+    def chain_unfused():
         be.embed_step(table, state, x)
         be.add_rms_norm(x, delta, w, h, 1e-6)
         be.rope_qk_step(q, qh, k, kh, dim, state, inv, None, 0)
 
     ms_graph, lo, hi = timer.graph([chain])
     ms_eager = timer.eager([chain])
+    ms_unfused = timer.graph([chain_unfused])[0]
+    ms_unfused_eager = timer.eager([chain_unfused])
     kern = {}
+    kern["embed_add_rms_norm_step_bf16"] = report("gather+add+norm", bytes_gather(1, hidden, 2) + 2 * hidden * 2,
+                                                  timer.graph([lambda: be.embed_add_rms_norm_step(
+                                                      table, state, w, x, h, delta=delta)])[0])
     kern["embed_step_bf16"] = report("gather", bytes_gather(1, hidden, 2),
                                      timer.graph([lambda: be.embed_step(table, state, x)])[0])
     kern["add_rms_norm_bf16"] = report("add_rms_norm", bytes_add_rms_norm(1, hidden, 2),
@@ -252,9 +261,11 @@ def config2(be, torch, timer):
     kern["rope_qk_step_bf16"] = report("rope", bytes_rope(1, qh + kh, dim, 2, 8), timer.graph(
         [lambda: be.rope_qk_step(q, qh, k, kh, dim, state, inv, None, 0)])[0])
     return {"workload": "bf16 decode chain, batch 1: gather [128000, 2048] -> add+RMSNorm 2048 -> RoPE Q[16,128] "
-                        "K[4,128]",
+                        "K[4,128] (gather fused with add+RMSNorm: 2 launches)",
             "step": report("decode chain", chain_bytes, ms_graph),
             "us_per_chain_graph": round(ms_graph * 1e3, 3), "us_per_chain_eager": round(ms_eager * 1e3, 3),
+            "unfused": {"launches": 3, "us_per_chain_graph": round(ms_unfused * 1e3, 3),
+                        "us_per_chain_eager": round(ms_unfused_eager * 1e3, 3)},
             "kernels": kern}
 
 

@@ -119,6 +119,8 @@ _SIGNATURES = {
     "uocr_rocm_attend_scratch_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_attend_step": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
     "uocr_rocm_scale_mask_softmax_rows": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
+    "uocr_rocm_embed_add_rms_norm_step": ([_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _f32], _int),
+    "uocr_rocm_embed_add_rms_norm_step_bf16": ([_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _f32], _int),
     "uocr_rocm_add_rms_norm_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_add_rms_norm_swiglu_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _vp, _i64, _vp],
                                                 _int),
@@ -448,6 +450,20 @@ def attend_step(q, k_cache, v_cache, heads, hd, mask, scale, state, scratch, out
 
 
 # ---- fused decode-step ops -------------------------------------------------------------------
+
+
+def embed_add_rms_norm_step(table, state, w, x, h, delta=None, eps=1e-6, stream=None):
+    """x = table[state.token] (+ delta); h = rms_norm(x) * w, in one launch
+    (x, h float32 or bfloat16 alike; delta the same dtype or None)."""
+    bf = _is_bf16(x)
+    if _is_bf16(h) != bf or (delta is not None and _is_bf16(delta) != bf):
+        raise ValueError("x, h and delta must share a dtype")
+    cols = table.shape[-1]
+    if x.numel() != cols or h.numel() != cols or (delta is not None and delta.numel() != cols):
+        raise ValueError("x, h and delta must hold one table row")
+    name = "uocr_rocm_embed_add_rms_norm_step_bf16" if bf else "uocr_rocm_embed_add_rms_norm_step"
+    _op(name, stream, _ptr(table), table.shape[0], _ptr(state), _ptr(delta), _f32_param(w), _ptr(x), _ptr(h), cols,
+        eps)
 
 
 def add_rms_norm_gemv_bf16(x, w, y, delta=None, x_out=None, w_norm=None, eps=1e-6, h_out=None, bias=None,

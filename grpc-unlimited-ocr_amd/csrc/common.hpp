@@ -99,6 +99,24 @@ struct Chunk<uint16_t, 8> {
   __device__ __forceinline__ void clear() { raw = u32x4{0u, 0u, 0u, 0u}; }
 };
 
+// Four bf16 (8 bytes): an fp32 row chunk's worth of a bf16 table row.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <>
+struct Chunk<uint16_t, 4> {
+  u32x2 raw;
+  __device__ __forceinline__ void load(const uint16_t* p) { raw = stream_load(reinterpret_cast<const u32x2*>(p)); }
+  __device__ __forceinline__ void store(uint16_t* p) const { stream_store(reinterpret_cast<u32x2*>(p), raw); }
+  __device__ __forceinline__ void widen(float (&v)[4]) const {
+    v[0] = bf16_lo(raw.x);
+    v[1] = bf16_hi(raw.x);
+    v[2] = bf16_lo(raw.y);
+    v[3] = bf16_hi(raw.y);
+  }
+  __device__ __forceinline__ void narrow(const float (&v)[4]) { raw = u32x2{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])}; }
+  __device__ __forceinline__ void clear() { raw = u32x2{0u, 0u}; }
+};
+
 template <>
 struct Chunk<float, 1> {
   float raw;

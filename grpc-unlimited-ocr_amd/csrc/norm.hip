@@ -36,7 +36,15 @@ namespace {
 
 // kRouter: the router's RMSNorm (non-finite inputs count as 0, output
 // clamp(clamp(x inv, +-1e4) (1 + w), +-1e4); src/model/decoder.cpp:20-34).
-enum class Norm { kRms, kAddRms, kLayer, kRouter };
+enum class Norm { kRms, kAddRms, kLayer, kRouter, kEmbedRms };
+
+// kEmbedRms's row source: the bf16 table row of state->token (a zero row for
+// a token outside [0, table_rows) when table_rows >= 0).
+struct EmbedSrc {
+  const uint16_t* table;
+  int64_t table_rows;
+  const uocr_rocm_step_state* state;
+};
 
 constexpr float kActClamp = 1.0e4f;
 
@@ -45,7 +53,10 @@ __device__ __forceinline__ float clamp_act(float v) { return fminf(fmaxf(v, -kAc
 template <class T, int VW, int WPR, int VPL, Norm kMode>
 __global__ __launch_bounds__(kBlock) void norm_rows(T* __restrict__ x, const T* __restrict__ delta,
                                                     const float* __restrict__ w, const float* __restrict__ b,
-                                                    T* __restrict__ h, int64_t rows, int cols, float eps) {
+                                                    T* __restrict__ h, int64_t rows, int cols, float eps,
+                                                    EmbedSrc src) {
+  constexpr bool kEmbed = kMode == Norm::kEmbedRms;
+  constexpr bool kTwoOut = kMode == Norm::kAddRms || kEmbed;  // writes x' and h
   constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
   __shared__ float red[kRowsPerBlock][kMaxGroups];
   const int wave = threadIdx.x / kWave;
@@ -60,12 +71,25 @@ __global__ __launch_bounds__(kBlock) void norm_rows(T* __restrict__ x, const T* 
 
   Chunk<T, VW> cx[VPL];
   Chunk<T, VW> cd[VPL];
+  Chunk<uint16_t, VW> ce[kEmbed ? VPL : 1];
+  const uint16_t* erow = nullptr;
+  if constexpr (kEmbed) {
+    const int64_t id = src.state->token;
+    const bool valid = src.table_rows < 0 || (id >= 0 && id < src.table_rows);
+    erow = valid ? src.table + id * cols : nullptr;
+  }
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = (wr + WPR * k) * kWave + lane;
     if (active && v < nvec) {
-      cx[k].load(x + off + static_cast<int64_t>(v) * VW);
-      if constexpr (kMode == Norm::kAddRms) cd[k].load(delta + off + static_cast<int64_t>(v) * VW);
+      if constexpr (kEmbed) {
+        if (erow != nullptr) ce[k].load(erow + static_cast<int64_t>(v) * VW);
+        else ce[k].clear();
+        if (delta != nullptr) cd[k].load(delta + off + static_cast<int64_t>(v) * VW);
+      } else {
+        cx[k].load(x + off + static_cast<int64_t>(v) * VW);
+        if constexpr (kMode == Norm::kAddRms) cd[k].load(delta + off + static_cast<int64_t>(v) * VW);
+      }
     }
   }
 
@@ -76,7 +100,17 @@ __global__ __launch_bounds__(kBlock) void norm_rows(T* __restrict__ x, const T* 
     const int v = (wr + WPR * k) * kWave + lane;
     part[k] = 0.0f;
     if (active && v < nvec) {
-      cx[k].widen(s[k]);
+      if constexpr (kEmbed) {
+        ce[k].widen(s[k]);
+        if (delta != nullptr) {
+          float d[VW];
+          cd[k].widen(d);
+#pragma unroll
+          for (int e = 0; e < VW; ++e) s[k][e] += d[e];
+        }
+      } else {
+        cx[k].widen(s[k]);
+      }
       if constexpr (kMode == Norm::kAddRms) {
         float d[VW];
         cd[k].widen(d);
@@ -119,13 +153,13 @@ __global__ __launch_bounds__(kBlock) void norm_rows(T* __restrict__ x, const T* 
   }
   if (!active) return;
 
-  T* out = kMode == Norm::kAddRms ? h : x;
+  T* out = kTwoOut ? h : x;
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = (wr + WPR * k) * kWave + lane;
     if (v < nvec) {
       const int64_t at = off + static_cast<int64_t>(v) * VW;
-      if constexpr (kMode == Norm::kAddRms) {
+      if constexpr (kTwoOut) {
         Chunk<T, VW> xs;
         xs.narrow(s[k]);
         xs.store(x + at);
@@ -242,24 +276,32 @@ int check_rows(const char* what, int64_t rows, int64_t cols) {
 
 template <class T, int VW, int WPR, Norm kMode>
 void launch_norm_rows(int vpl, hipStream_t s, T* x, const T* delta, const float* w, const float* b, T* h,
-                      int64_t rows, int cols, float eps) {
+                      int64_t rows, int cols, float eps, const EmbedSrc& e) {
   constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
   const unsigned blocks = static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
   switch (vpl) {
-    case 1: norm_rows<T, VW, WPR, 1, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
-    case 2: norm_rows<T, VW, WPR, 2, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
-    case 4: norm_rows<T, VW, WPR, 4, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
-    case 8: norm_rows<T, VW, WPR, 8, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
-    default: norm_rows<T, VW, WPR, 16, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps); break;
+    case 1: norm_rows<T, VW, WPR, 1, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e); break;
+    case 2: norm_rows<T, VW, WPR, 2, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e); break;
+    case 4: norm_rows<T, VW, WPR, 4, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e); break;
+    case 8: norm_rows<T, VW, WPR, 8, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e); break;
+    default:
+      norm_rows<T, VW, WPR, 16, kMode><<<blocks, kBlock, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e);
+      break;
   }
 }
 
 template <class T, Norm kMode>
 int launch_norm(const char* what, void* stream, T* x, const T* delta, const float* w, const float* b, T* h,
-                int64_t rows, int64_t cols, float eps) {
+                int64_t rows, int64_t cols, float eps, EmbedSrc e = {}) {
   if (int st = check_rows(what, rows, cols)) return st;
   if (rows == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(x != nullptr && w != nullptr, what, "null x or w");
+  if constexpr (kMode == Norm::kEmbedRms) {
+    UOCR_REQUIRE(e.table != nullptr && e.state != nullptr && h != nullptr, what, "null table, state or h");
+    UOCR_REQUIRE(h != x && (delta == nullptr || (delta != x && delta != h)), what,
+                 "x, delta and h must be distinct buffers");
+    UOCR_REQUIRE((cols + kVec<T> - 1) / kVec<T> <= kWave * kMaxGroups, what, "cols too large for one row kernel");
+  }
   if constexpr (kMode == Norm::kLayer) UOCR_REQUIRE(b != nullptr, what, "null b");
   if constexpr (kMode == Norm::kAddRms) {
     UOCR_REQUIRE(delta != nullptr && h != nullptr, what, "null delta or h");
@@ -267,14 +309,18 @@ int launch_norm(const char* what, void* stream, T* x, const T* delta, const floa
   }
   constexpr int kV = kVec<T>;
   const bool vec = cols % kV == 0 && aligned16(x) && aligned16(w) && (kMode != Norm::kLayer || aligned16(b)) &&
-                   (kMode != Norm::kAddRms || (aligned16(delta) && aligned16(h)));
+                   (kMode != Norm::kAddRms || (aligned16(delta) && aligned16(h))) &&
+                   (kMode != Norm::kEmbedRms || (aligned16(e.table) && aligned16(h) && (delta == nullptr ||
+                                                                                       aligned16(delta))));
   const int64_t nvec = vec ? cols / kV : cols;
   const int64_t groups = (nvec + kWave - 1) / kWave;
   const hipStream_t s = as_stream(stream);
   const int c32 = static_cast<int>(cols);
   clear_launch_error();
   if (groups > kMaxGroups) {
-    if constexpr (kMode == Norm::kLayer) {
+    if constexpr (kMode == Norm::kEmbedRms) {
+      return fail(UOCR_ROCM_INVALID_ARGUMENT, what, "cols too large for one row kernel");
+    } else if constexpr (kMode == Norm::kLayer) {
       ln_rows_wide<T><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, w, b, cols, eps);
     } else {
       rms_rows_wide<T, kMode == Norm::kAddRms, kMode == Norm::kRouter>
@@ -285,11 +331,11 @@ int launch_norm(const char* what, void* stream, T* x, const T* delta, const floa
   const bool spread = groups > 16 || (rows < kFewRows && groups >= 4);
   const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
   if (vec) {
-    if (spread) launch_norm_rows<T, kV, 4, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps);
-    else launch_norm_rows<T, kV, 1, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps);
+    if (spread) launch_norm_rows<T, kV, 4, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps, e);
+    else launch_norm_rows<T, kV, 1, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps, e);
   } else {
-    if (spread) launch_norm_rows<T, 1, 4, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps);
-    else launch_norm_rows<T, 1, 1, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps);
+    if (spread) launch_norm_rows<T, 1, 4, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps, e);
+    else launch_norm_rows<T, 1, 1, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps, e);
   }
   return check_launch(what);
 }
@@ -342,6 +388,20 @@ int uocr_rocm_router_norm(void* stream, float* x, const float* w, int64_t rows, 
 int uocr_rocm_router_norm_bf16(void* stream, uint16_t* x, const float* w, int64_t rows, int64_t cols, float eps) {
   return launch_norm<uint16_t, Norm::kRouter>("uocr_rocm_router_norm_bf16", stream, x, nullptr, w, nullptr, nullptr,
                                               rows, cols, eps);
+}
+
+int uocr_rocm_embed_add_rms_norm_step(void* stream, const uint16_t* table, int64_t table_rows,
+                                      const uocr_rocm_step_state* state, const float* delta, const float* w, float* x,
+                                      float* h, int64_t cols, float eps) {
+  return launch_norm<float, Norm::kEmbedRms>("uocr_rocm_embed_add_rms_norm_step", stream, x, delta, w, nullptr, h, 1,
+                                             cols, eps, EmbedSrc{table, table_rows, state});
+}
+
+int uocr_rocm_embed_add_rms_norm_step_bf16(void* stream, const uint16_t* table, int64_t table_rows,
+                                           const uocr_rocm_step_state* state, const uint16_t* delta, const float* w,
+                                           uint16_t* x, uint16_t* h, int64_t cols, float eps) {
+  return launch_norm<uint16_t, Norm::kEmbedRms>("uocr_rocm_embed_add_rms_norm_step_bf16", stream, x, delta, w,
+                                                nullptr, h, 1, cols, eps, EmbedSrc{table, table_rows, state});
 }
 
 }  // extern "C"

@@ -71,4 +71,17 @@ void attend_rope_kv_step(const Context& ctx, const float* q, const float* k_row,
                                       abi(state), inv_tok, n_tok, inv_page, page_mod, scratch, capacity, out));
 }
 
+void embed_add_rms_norm_step(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
+                             const StepState* state, const float* delta, const float* w, float* x, float* h,
+                             std::int64_t cols, float eps) {
+  check(uocr_rocm_embed_add_rms_norm_step(ctx.stream(), table, table_rows, abi(state), delta, w, x, h, cols, eps));
+}
+
+void embed_add_rms_norm_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
+                                  const StepState* state, const std::uint16_t* delta, const float* w,
+                                  std::uint16_t* x, std::uint16_t* h, std::int64_t cols, float eps) {
+  check(uocr_rocm_embed_add_rms_norm_step_bf16(ctx.stream(), table, table_rows, abi(state), delta, w, x, h, cols,
+                                               eps));
+}
+
 }  // namespace uocr::rocm

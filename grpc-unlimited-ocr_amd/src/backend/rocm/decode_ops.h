@@ -48,6 +48,15 @@ void attend_step(const Context& ctx, const float* q, const float* k_cache, const
                  std::int64_t hd, const float* mask, float scale, const StepState* state, float* scratch,
                  std::int64_t capacity, float* out);
 
+// New: the step's embedding row fused with the first norm: x = table[token]
+// (+ delta, which may be null), h = rms_norm(x) * w.
+void embed_add_rms_norm_step(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
+                             const StepState* state, const float* delta, const float* w, float* x, float* h,
+                             std::int64_t cols, float eps);
+void embed_add_rms_norm_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
+                                  const StepState* state, const std::uint16_t* delta, const float* w,
+                                  std::uint16_t* x, std::uint16_t* h, std::int64_t cols, float eps);
+
 // New: rope_qk_step on (q, k_row), the appends of the rotated key and of
 // v_row at pos, and attend_step, in attend_step's two launches; q, k_row and
 // v_row are left unrotated.

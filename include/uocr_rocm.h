@@ -331,6 +331,22 @@ UOCR_ROCM_API int uocr_rocm_attend_step(void* stream, const float* q, const floa
  * One launch where the reference's decode step makes several; each gives
  * bitwise the result of the unfused entry points it replaces. */
 
+/* The step's token embedding fused with the first norm:
+ *   x = widen(table[state->token]) (+ delta; delta null: no add);
+ *   h = w * (x * inv(x)),  one row of `cols`.
+ * x and h are written (bf16 variant: rounded once). Bitwise uocr_rocm_embed_step
+ * then uocr_rocm_add_rms_norm (or, without delta, a copy and
+ * uocr_rocm_rms_norm). A token outside [0, table_rows) gives a zero
+ * embedding when table_rows >= 0. Replaces embed_step + copy + rms_norm at
+ * the top of decode_body (src/model/cuda/cuda_decode_step.cpp:50-55). */
+UOCR_ROCM_API int uocr_rocm_embed_add_rms_norm_step(void* stream, const uint16_t* table, int64_t table_rows,
+                                                    const uocr_rocm_step_state* state, const float* delta,
+                                                    const float* w, float* x, float* h, int64_t cols, float eps);
+UOCR_ROCM_API int uocr_rocm_embed_add_rms_norm_step_bf16(void* stream, const uint16_t* table, int64_t table_rows,
+                                                         const uocr_rocm_step_state* state, const uint16_t* delta,
+                                                         const float* w, uint16_t* x, uint16_t* h, int64_t cols,
+                                                         float eps);
+
 /* add + RMSNorm feeding a bf16 GEMV:
  *   s = x + delta (delta null: s = x);  x_out = s (null: not written);
  *   h = w_norm * (s * inv(s)) (w_norm null: h = s);  h_out = h (null: not written);

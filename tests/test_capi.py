@@ -123,3 +123,55 @@ def test_python_layer_rejects_mismatched_tensors(backend):
         backend.rms_norm(torch.zeros(4, 8, dtype=torch.float16), torch.ones(8), 1e-6)
     with pytest.raises(ValueError):
         backend.layer_norm(x, torch.ones(8, dtype=torch.bfloat16), torch.zeros(8), 1e-6)
+
+
+def test_step_op_errors(backend):
+    _invalid(backend, "uocr_rocm_router_norm", None, FAKE, FAKE, -1, 64, 1e-6, detail="rows")
+    _invalid(backend, "uocr_rocm_router_norm_bf16", None, FAKE, None, 4, 64, 1e-6, detail="null")
+    _invalid(backend, "uocr_rocm_quick_gelu", None, FAKE, -5, detail="n")
+    _invalid(backend, "uocr_rocm_softmax_rows", None, FAKE, -1, 64, detail="rows")
+    _invalid(backend, "uocr_rocm_softmax_rows", None, FAKE, 4, 0, detail="cols")
+    _invalid(backend, "uocr_rocm_scale_add_mask", None, FAKE, 1.0, None, -1, 4, 4, detail="shape")
+    _invalid(backend, "uocr_rocm_scale_mask_softmax_rows", None, FAKE, 1.0, None, 2, 4, 0, detail="cols")
+    _invalid(backend, "uocr_rocm_gemv_bf16", None, FAKE, 20000, FAKE, 4, None, FAKE, detail="12288")
+    _invalid(backend, "uocr_rocm_append_step", None, FAKE, FAKE, 64, None, 16, detail="null")
+    _invalid(backend, "uocr_rocm_attend_step", None, FAKE, FAKE, FAKE, 2, 300, None, 1.0, FAKE, FAKE, 64, FAKE,
+             detail="256")
+    _invalid(backend, "uocr_rocm_attend_step", None, FAKE, FAKE, FAKE, 2, 128, None, 1.0, FAKE, FAKE, 0, FAKE,
+             detail="capacity")
+
+
+def test_fused_step_op_errors(backend):
+    rope = (None, FAKE, FAKE, FAKE, FAKE, FAKE)
+    _invalid(backend, "uocr_rocm_attend_rope_kv_step", *rope, 2, 7, None, 1.0, FAKE, FAKE, 3, None, 0, FAKE, 64,
+             FAKE, detail="even")
+    _invalid(backend, "uocr_rocm_attend_rope_kv_step", *rope, 2, 8, None, 1.0, FAKE, FAKE, 5, None, 0, FAKE, 64,
+             FAKE, detail="n_tok")
+    _invalid(backend, "uocr_rocm_attend_rope_kv_step", *rope, 2, 8, None, 1.0, FAKE, FAKE, 3, None, 0, FAKE, 64,
+             FAKE, detail="inv_page")
+    _invalid(backend, "uocr_rocm_add_rms_norm_gemv_bf16", None, FAKE, None, None, None, 1e-6, None, 100, FAKE, 4,
+             None, FAKE, detail="multiple of 8")
+    _invalid(backend, "uocr_rocm_add_rms_norm_gemv_bf16", None, FAKE, None, None, None, 1e-6, None, 4096, FAKE, 4,
+             None, FAKE, detail="multiple of 8")
+    _invalid(backend, "uocr_rocm_add_rms_norm_gemv_bf16", None, FAKE, None, FAKE, None, 1e-6, None, 128, FAKE, 4,
+             None, FAKE, detail="overlap")
+    _invalid(backend, "uocr_rocm_add_rms_norm_gemv_bf16", None, FAKE + 4, None, None, None, 1e-6, None, 128, FAKE, 4,
+             None, FAKE, detail="aligned")
+    _invalid(backend, "uocr_rocm_add_rms_norm_swiglu_gemv_bf16", None, FAKE, None, None, None, 1e-6, None, 128,
+             FAKE, None, 4, FAKE, detail="up")
+
+
+def test_step_op_empty_shapes_and_scratch_size(backend):
+    lib = backend.lib()
+    assert lib.uocr_rocm_softmax_rows(None, None, 0, 64) == 0
+    assert lib.uocr_rocm_scale_add_mask(None, None, 1.0, None, 0, 4, 4) == 0
+    assert lib.uocr_rocm_scale_mask_softmax_rows(None, None, 1.0, None, 0, 4, 4) == 0
+    assert lib.uocr_rocm_gemv_bf16(None, None, 128, None, 0, None, None) == 0
+    assert lib.uocr_rocm_append_step(None, None, None, 0, None, 16) == 0
+    assert lib.uocr_rocm_attend_step(None, None, None, None, 0, 128, None, 1.0, None, None, 64, None) == 0
+    assert lib.uocr_rocm_add_rms_norm_gemv_bf16(None, None, None, None, None, 1e-6, None, 128, None, 0, None,
+                                                None) == 0
+    assert lib.uocr_rocm_attend_scratch_floats(0, 128, 100) == 0
+    # records only (no per-key scores): heads x splits x (hd + 2), 64 splits at 10 heads and 8192 positions
+    assert lib.uocr_rocm_attend_scratch_floats(10, 128, 8192) == 10 * 64 * 130
+    assert lib.uocr_rocm_attend_scratch_floats(1, 64, 7) == 1 * 1 * 66

@@ -3,6 +3,7 @@ unfused entry points give on the same inputs (that chain is itself checked
 against the oracle in tests/test_gpu_step_ops.py and test_gpu_parity.py),
 and is checked against the oracle directly as well:
 
+  embed_add_rms_norm_step        == embed_step -> add_rms_norm (or copy -> rms_norm)
   add_rms_norm_gemv_bf16         == add_rms_norm (or rms_norm) -> gemv_bf16
   add_rms_norm_swiglu_gemv_bf16  == add_rms_norm -> gemv gate, gemv up -> silu_mul
   attend_rope_kv_step            == rope_qk_step -> append_step x2 -> attend_step
@@ -241,3 +242,26 @@ def test_fused_decode_layer_graph_matches_unfused(backend):
         assert np.array_equal(bits(A["x2"]), bits(B["x2"])), f"residual at pos {pos}"
         assert np.array_equal(bits(A["kc"]), bits(B["kc"])) and np.array_equal(bits(A["vc"]), bits(B["vc"]))
         assert np.array_equal(bits(A["g"]), bits(B["act"]))
+
+
+@pytest.mark.parametrize("dtype,cols,with_delta", [("bf16", 2048, True), ("bf16", 2048, False), ("f32", 1280, True),
+                                                   ("f32", 1280, False), ("bf16", 1283, True), ("f32", 8192, True)])
+def test_embed_add_rms_norm_matches_unfused(backend, dtype, cols, with_delta):
+    vocab = 3000
+    table = weights_bf16(370, (vocab, cols), 0.02)
+    w = dev_f32(1 + 0.02 * normal(371, cols))
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    delta = dev_f32(normal(372, cols)).to(tdt) if with_delta else None
+    for token in (17, vocab - 1, vocab + 5):  # the last row, and one past the table: a zero row
+        state = dev_i64([token, 3, 3, 0, -1])
+        xu, hu = torch.empty(cols, dtype=tdt, device="cuda"), torch.empty(cols, dtype=tdt, device="cuda")
+        backend.embed_step(table, state, xu)  # bounded by the table: out-of-range gives zeros
+        if with_delta:
+            backend.add_rms_norm(xu.view(1, -1), delta.view(1, -1), w, hu.view(1, -1), 1e-6)
+        else:
+            hu.copy_(xu)
+            backend.rms_norm(hu.view(1, -1), w, 1e-6)
+        x, h = torch.empty_like(xu), torch.empty_like(hu)
+        backend.embed_add_rms_norm_step(table, state, w, x, h, delta=delta)
+        view = torch.int16 if dtype == "bf16" else torch.int32
+        assert torch.equal(x.view(view), xu.view(view)) and torch.equal(h.view(view), hu.view(view)), token
