@@ -458,6 +458,12 @@ def config7(be, torch, timer):
         "attend_rope_kv_step_f32": report("attend+rope+append", b["attend"] + b["append"], timer.graph(
             [lambda s=s: be.attend_rope_kv_step(q, k, v, s["kc"], s["vc"], heads, hd, None, scale, state, inv, None,
                                                 0, scratch, attn) for s in sets])[0]),
+        "attend_rope_kv_step_bf16_cache": report("attend+rope+append, bf16 cache", (b["attend"] + b["append"]) // 2,
+                                                 time_kernel(timer, lambda: (bf16_randn(torch, (cap, width)),
+                                                                             bf16_randn(torch, (cap, width))),
+                                                             lambda c: be.attend_rope_kv_step(
+                                                                 q, k, v, c[0], c[1], heads, hd, None, scale, state,
+                                                                 inv, None, 0, scratch, attn))),
         "gemv_bf16_qkv": report("gemv qkv", bytes_gemv(3 * width, hidden), timer.graph(
             [lambda s=s: be.gemv_bf16(h, s["qkv"], qkv) for s in sets])[0]),
         "add_rms_norm_gemv_bf16_qkv": report("norm+gemv qkv", bytes_gemv(3 * width, hidden), timer.graph(
@@ -465,6 +471,16 @@ def config7(be, torch, timer):
              for s in sets])[0]),
     }
     nsets = len(sets)
+    del sets, first
+    # the same fused layer over a bf16 key/value cache (half the cache bytes)
+    def layer_bf16_kv():
+        L = layer()
+        L["kc"], L["vc"] = L["kc"].to(torch.bfloat16), L["vc"].to(torch.bfloat16)
+        return L
+    first = layer_bf16_kv()
+    sets = [first] + [layer_bf16_kv() for _ in range(n_sets(footprint(first.values())) - 1)]
+    ms_bf16_kv = timer.graph([lambda s=s: fused(s) for s in sets])[0]
+    total_bf16_kv = total - (b["attend"] + b["append"]) // 2
     del sets, first
     lm_n, lm_k = 129280, 1280
     xl, yl = torch.randn(lm_k, device="cuda"), torch.empty(lm_n, device="cuda")
@@ -477,6 +493,8 @@ def config7(be, torch, timer):
             "us_per_layer_eager": round(ms_eager * 1e3, 3), "ms_range": [round(lo, 5), round(hi, 5)],
             "unfused": {"launches": 11, "us_per_layer_graph": round(ms_unfused * 1e3, 3),
                         "us_per_layer_eager": round(ms_unfused_eager * 1e3, 3)},
+            "bf16_kv_cache": {"step": report("decode layer, bf16 cache", total_bf16_kv, ms_bf16_kv),
+                              "us_per_layer_graph": round(ms_bf16_kv * 1e3, 3)},
             "bytes_by_op": b, "attend_splits": splits, "kernels": kern, "sets": nsets}
 
 

@@ -116,6 +116,10 @@ _SIGNATURES = {
     "uocr_rocm_scale_add_mask": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_gemv_bf16": ([_vp, _vp, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_append_step": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
+    "uocr_rocm_append_step_bf16": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
+    "uocr_rocm_attend_step_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
+    "uocr_rocm_attend_rope_kv_step_bf16": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64,
+                                            _vp, _i64, _vp, _i64, _vp], _int),
     "uocr_rocm_attend_scratch_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_attend_step": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
     "uocr_rocm_scale_mask_softmax_rows": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
@@ -426,7 +430,8 @@ def append_step(cache, row, state, capacity=None, stream=None):
     Reference: append_step, decode_ops.h:28-29."""
     width = row.numel()
     cap = cache.numel() // width if capacity is None and width else (-1 if capacity is None else capacity)
-    _op("uocr_rocm_append_step", stream, _ptr(cache), _ptr(row), width, _ptr(state), cap)
+    name = "uocr_rocm_append_step_bf16" if _is_bf16(cache) else "uocr_rocm_append_step"
+    _op(name, stream, _ptr(cache), _ptr(row), width, _ptr(state), cap)
 
 
 def attend_scratch_floats(heads, hd, capacity) -> int:
@@ -445,8 +450,11 @@ def attend_step(q, k_cache, v_cache, heads, hd, mask, scale, state, scratch, out
         raise ValueError("mask must hold capacity floats")
     if scratch.numel() < attend_scratch_floats(heads, hd, capacity):
         raise ValueError("scratch is smaller than attend_scratch_floats(heads, hd, capacity)")
-    _op("uocr_rocm_attend_step", stream, _ptr(q), _ptr(k_cache), _ptr(v_cache), heads, hd, _f32_param(mask), scale,
-        _ptr(state), _ptr(scratch), capacity, _ptr(out))
+    bf = _is_bf16(k_cache)
+    if _is_bf16(v_cache) != bf:
+        raise ValueError("k_cache and v_cache must share a dtype")
+    _op("uocr_rocm_attend_step_bf16" if bf else "uocr_rocm_attend_step", stream, _ptr(q), _ptr(k_cache),
+        _ptr(v_cache), heads, hd, _f32_param(mask), scale, _ptr(state), _ptr(scratch), capacity, _ptr(out))
 
 
 # ---- fused decode-step ops -------------------------------------------------------------------
@@ -493,6 +501,10 @@ def attend_rope_kv_step(q, k_row, v_row, k_cache, v_cache, heads, hd, mask, scal
     if scratch.numel() < attend_scratch_floats(heads, hd, capacity):
         raise ValueError("scratch is smaller than attend_scratch_floats(heads, hd, capacity)")
     n_tok = 0 if inv_tok is None else inv_tok.numel()
-    _op("uocr_rocm_attend_rope_kv_step", stream, _ptr(q), _ptr(k_row), _ptr(v_row), _ptr(k_cache), _ptr(v_cache),
+    bf = _is_bf16(k_cache)
+    if _is_bf16(v_cache) != bf:
+        raise ValueError("k_cache and v_cache must share a dtype")
+    name = "uocr_rocm_attend_rope_kv_step_bf16" if bf else "uocr_rocm_attend_rope_kv_step"
+    _op(name, stream, _ptr(q), _ptr(k_row), _ptr(v_row), _ptr(k_cache), _ptr(v_cache),
         heads, hd, _f32_param(mask), scale, _ptr(state), _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod,
         _ptr(scratch), capacity, _ptr(out))

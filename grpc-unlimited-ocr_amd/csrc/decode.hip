@@ -36,8 +36,10 @@ constexpr int kMaskTile = 2048;
 
 // ---- append ---------------------------------------------------------------------
 
-template <int VW>
-__global__ __launch_bounds__(kBlock) void append_k(float* __restrict__ cache, const float* __restrict__ row,
+// TC is the cache's element type: float, or uint16_t for a bf16 cache (the
+// fp32 row rounded to nearest even on the way in).
+template <class TC, int VW>
+__global__ __launch_bounds__(kBlock) void append_k(TC* __restrict__ cache, const float* __restrict__ row,
                                                    int64_t width, const uocr_rocm_step_state* __restrict__ state,
                                                    int64_t capacity) {
   const int64_t pos = state->pos;
@@ -46,7 +48,11 @@ __global__ __launch_bounds__(kBlock) void append_k(float* __restrict__ cache, co
   if (c * VW >= width) return;
   Chunk<float, VW> v;
   v.load(row + c * VW);
-  v.store(cache + pos * width + c * VW);
+  float f[VW];
+  v.widen(f);
+  Chunk<TC, VW> o;
+  o.narrow(f);
+  o.store(cache + pos * width + c * VW);
 }
 
 // ---- attention ------------------------------------------------------------------
@@ -69,8 +75,8 @@ __device__ __forceinline__ float group_sum(float v) {
 
 struct AttendArgs {
   const float* q;
-  const float* k;
-  const float* v;
+  const void* k;  // caches of element type TC (float or bf16 bits)
+  const void* v;
   const float* mask;
   float* part;  // [heads, splits, hd + 2]: m, l, acc[hd]
   const uocr_rocm_step_state* state;
@@ -83,8 +89,8 @@ struct AttendArgs {
   // caches to append them to, and the rope tables.
   const float* k_row;
   const float* v_row;
-  float* k_out;
-  float* v_out;
+  void* k_out;
+  void* v_out;
   const float* inv_tok;
   const float* inv_page;
   int64_t page_mod;
@@ -95,10 +101,10 @@ __device__ __forceinline__ float exp_shift(float s, float m) { return __builtin_
 
 // The K and V chunks of U keys of one lane group, with each key's mask value
 // (-inf for a key that is masked or past the end: such a key is not read).
-template <int VW, int VPL, int U>
+template <class TC, int VW, int VPL, int U>
 struct KeyBatch {
-  Chunk<float, VW> k[U][VPL];
-  Chunk<float, VW> v[U][VPL];
+  Chunk<TC, VW> k[U][VPL];
+  Chunk<TC, VW> v[U][VPL];
   float mk[U];
   bool is_new[U];  // the step's own key (kRope): its K and V come from LDS
 };
@@ -111,8 +117,16 @@ struct Running {
   float acc[VPL][VW];
 };
 
-template <int VW, int G, int VPL, int U, bool kRope>
+__device__ __forceinline__ float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+template <class TC, int VW, int G, int VPL, int U, bool kRope>
 __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
+  constexpr bool kBf16 = sizeof(TC) == 2;
+  const TC* kc = static_cast<const TC*>(a.k);
+  const TC* vc = static_cast<const TC*>(a.v);
+  // A key that is masked or past the end reads the query row instead (valid,
+  // cached, never used); for a bf16 cache its bytes are read as bf16 bits.
+  const TC* dead = reinterpret_cast<const TC*>(a.q);
   constexpr int kSlotsPerWave = kWave / G;
   constexpr int kSlots = kWavesPerBlock * kSlotsPerWave;
   constexpr int kPerLane = VW * VPL;
@@ -161,14 +175,23 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
         s_new[1][p] = ka * cs - kb * sn;
         s_new[1][p + half] = kb * cs + ka * sn;
       }
+      if constexpr (kBf16) {  // the key as the bf16 cache will hold it
+        s_new[1][p] = round_bf16(s_new[1][p]);
+        s_new[1][p + half] = round_bf16(s_new[1][p + half]);
+      }
     }
-    for (int t = threadIdx.x; t < a.hd; t += kBlock) s_new[2][t] = a.v_row[head_off + t];
+    for (int t = threadIdx.x; t < a.hd; t += kBlock) {
+      s_new[2][t] = kBf16 ? round_bf16(a.v_row[head_off + t]) : a.v_row[head_off + t];
+    }
     __syncthreads();
     // The split that holds key pos appends the head's rotated k and its v.
     if (pos >= first && pos < last) {
       for (int t = threadIdx.x; t < a.hd; t += kBlock) {
-        a.k_out[pos * a.width + head_off + t] = s_new[1][t];
-        a.v_out[pos * a.width + head_off + t] = s_new[2][t];
+        Chunk<TC, 1> kk, vv;
+        kk.narrow({s_new[1][t]});
+        vv.narrow({s_new[2][t]});
+        kk.store(static_cast<TC*>(a.k_out) + pos * a.width + head_off + t);
+        vv.store(static_cast<TC*>(a.v_out) + pos * a.width + head_off + t);
       }
     }
   }
@@ -201,10 +224,10 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
     for (int e = 0; e < VW; ++e) run.acc[i][e] = 0.0f;
 
   // Loads are issued unconditionally: a key that is masked or past the end
-  // reads the query row instead (cached, never used), so the loop has no
-  // branch around a load and the next batch's loads stay in flight while
-  // the current batch is scored.
-  auto issue = [&](KeyBatch<VW, VPL, U>& b, int64_t jb, int64_t t0, int64_t t1) {
+  // reads the query row instead (cached; its score is -inf and its value is
+  // replaced by 0), so the loop has no branch around a load and the next
+  // batch's loads stay in flight while the current batch is scored.
+  auto issue = [&](KeyBatch<TC, VW, VPL, U>& b, int64_t jb, int64_t t0, int64_t t1) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
@@ -217,18 +240,18 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
       const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
       const bool live = b.mk[u] != -INFINITY && !b.is_new[u];
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) b.k[u][i].load(live ? a.k + j * a.width + col[i] : a.q + col[i]);
+      for (int i = 0; i < VPL; ++i) b.k[u][i].load(live ? kc + j * a.width + col[i] : dead + col[i]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
       const bool live = b.mk[u] != -INFINITY && !b.is_new[u];
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) b.v[u][i].load(live ? a.v + j * a.width + col[i] : a.q + col[i]);
+      for (int i = 0; i < VPL; ++i) b.v[u][i].load(live ? vc + j * a.width + col[i] : dead + col[i]);
     }
   };
 
-  auto consume = [&](const KeyBatch<VW, VPL, U>& b) {
+  auto consume = [&](const KeyBatch<TC, VW, VPL, U>& b) {
     float s[U];
     float peak = run.m;
 #pragma unroll
@@ -275,8 +298,12 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
             for (int e = 0; e < VW; ++e) vv[e] = s_new[2][col[i] - head_off + e];
           }
         }
+        // A dead key (masked or past the end) holds filler bits, which need
+        // not be finite (bf16 halves of the query row can be NaN): its value
+        // enters as 0, never as 0 * filler.
+        const bool use = in_head[i] && b.mk[u] != -INFINITY;
 #pragma unroll
-        for (int e = 0; e < VW; ++e) run.acc[i][e] = fmaf(p, in_head[i] ? vv[e] : 0.0f, run.acc[i][e]);
+        for (int e = 0; e < VW; ++e) run.acc[i][e] = fmaf(p, use ? vv[e] : 0.0f, run.acc[i][e]);
       }
     }
     run.m = peak;
@@ -303,7 +330,7 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
     }
     const int64_t base = t0 + slot;
     const int iters = base < t1 ? static_cast<int>((t1 - base + kStride - 1) / kStride) : 0;
-    KeyBatch<VW, VPL, U> A, B;
+    KeyBatch<TC, VW, VPL, U> A, B;
     issue(A, base, t0, t1);
     for (int it = 0; it < iters; it += 2) {
       issue(B, base + (it + 1) * kStride, t0, t1);
@@ -417,41 +444,43 @@ int attend_splits(int64_t heads, int64_t capacity) {
   return static_cast<int>(s < 1 ? 1 : s);
 }
 
-template <int VW, int G, int VPL, int U, bool kRope>
+template <class TC, int VW, int G, int VPL, int U, bool kRope>
 void launch_partial(hipStream_t s, const AttendArgs& a, int64_t heads) {
-  attend_partial<VW, G, VPL, U, kRope><<<static_cast<unsigned>(heads * a.splits), kBlock, 0, s>>>(a);
+  attend_partial<TC, VW, G, VPL, U, kRope><<<static_cast<unsigned>(heads * a.splits), kBlock, 0, s>>>(a);
 }
 
-// Lanes per key and keys per batch. Up to 8192 positions two keys per batch
-// (the split's keys are few, so fewer dead loads and registers win); beyond,
-// four keys per batch and, for 128-wide heads, 16 lanes of two chunks each
-// per key. Both depend on the capacity only, so a captured step keeps its
-// launch shape at every position.
-template <bool kRope>
+// Lanes per key and keys per batch, with 16-byte chunks (4 fp32 or 8 bf16
+// cache elements per lane). Up to 8192 positions two keys per batch (the
+// split's keys are few, so fewer dead loads and registers win); beyond, four
+// keys per batch and, where a key spans 32 chunks, 16 lanes of two chunks
+// each. Both depend on the capacity only, so a captured step keeps its launch
+// shape at every position.
+template <class TC, bool kRope>
 void launch_attend_vec(hipStream_t s, const AttendArgs& a, int64_t heads) {
-  const int nvec = a.hd / 4;
+  constexpr int VW = kVec<TC>;
+  const int nvec = a.hd / VW;
   const bool long_ctx = a.capacity > 8192;
-  if (nvec <= 1) launch_partial<4, 1, 1, 2, kRope>(s, a, heads);
-  else if (nvec <= 2) launch_partial<4, 2, 1, 2, kRope>(s, a, heads);
-  else if (nvec <= 4) launch_partial<4, 4, 1, 2, kRope>(s, a, heads);
-  else if (nvec <= 8) launch_partial<4, 8, 1, 2, kRope>(s, a, heads);
+  if (nvec <= 1) launch_partial<TC, VW, 1, 1, 2, kRope>(s, a, heads);
+  else if (nvec <= 2) launch_partial<TC, VW, 2, 1, 2, kRope>(s, a, heads);
+  else if (nvec <= 4) launch_partial<TC, VW, 4, 1, 2, kRope>(s, a, heads);
+  else if (nvec <= 8) launch_partial<TC, VW, 8, 1, 2, kRope>(s, a, heads);
   else if (nvec <= 16) {
-    if (long_ctx) launch_partial<4, 16, 1, 4, kRope>(s, a, heads);
-    else launch_partial<4, 16, 1, 2, kRope>(s, a, heads);
+    if (long_ctx) launch_partial<TC, VW, 16, 1, 4, kRope>(s, a, heads);
+    else launch_partial<TC, VW, 16, 1, 2, kRope>(s, a, heads);
   } else if (nvec <= 32) {
-    if (long_ctx) launch_partial<4, 16, 2, 4, kRope>(s, a, heads);
-    else launch_partial<4, 32, 1, 2, kRope>(s, a, heads);
+    if (long_ctx) launch_partial<TC, VW, 16, 2, 4, kRope>(s, a, heads);
+    else launch_partial<TC, VW, 32, 1, 2, kRope>(s, a, heads);
   } else {
-    if (long_ctx) launch_partial<4, 64, 1, 4, kRope>(s, a, heads);
-    else launch_partial<4, 64, 1, 2, kRope>(s, a, heads);
+    if (long_ctx) launch_partial<TC, VW, 64, 1, 4, kRope>(s, a, heads);
+    else launch_partial<TC, VW, 64, 1, 2, kRope>(s, a, heads);
   }
 }
 
-template <bool kRope>
+template <class TC, bool kRope>
 void launch_attend_any(hipStream_t s, const AttendArgs& a, int64_t heads) {
-  if (a.hd <= 64) launch_partial<1, 64, 1, 2, kRope>(s, a, heads);
-  else if (a.hd <= 128) launch_partial<1, 64, 2, 2, kRope>(s, a, heads);
-  else launch_partial<1, 64, 4, 2, kRope>(s, a, heads);
+  if (a.hd <= 64) launch_partial<TC, 1, 64, 1, 2, kRope>(s, a, heads);
+  else if (a.hd <= 128) launch_partial<TC, 1, 64, 2, 2, kRope>(s, a, heads);
+  else launch_partial<TC, 1, 64, 4, 2, kRope>(s, a, heads);
 }
 
 void launch_merge(hipStream_t s, const AttendArgs& a, int64_t heads, float* out) {
@@ -469,41 +498,56 @@ void launch_merge(hipStream_t s, const AttendArgs& a, int64_t heads, float* out)
 
 using namespace uocr_rocm;
 
-extern "C" {
+namespace uocr_rocm {
+namespace {
 
-int uocr_rocm_append_step(void* stream, float* cache, const float* row, int64_t width,
-                          const uocr_rocm_step_state* state, int64_t capacity) {
-  const char* what = "uocr_rocm_append_step";
+template <class TC>
+int append_entry(const char* what, void* stream, TC* cache, const float* row, int64_t width,
+                 const uocr_rocm_step_state* state, int64_t capacity) {
   UOCR_REQUIRE(width >= 0, what, "width must be >= 0");
   if (width == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(cache != nullptr && row != nullptr && state != nullptr, what, "null pointer");
   UOCR_REQUIRE(width < (int64_t{1} << 36), what, "width too large");
   const hipStream_t s = as_stream(stream);
   clear_launch_error();
-  if (width % 4 == 0 && aligned16(cache) && aligned16(row)) {
+  if (width % 4 == 0 && aligned16(row) && (reinterpret_cast<uintptr_t>(cache) & (4 * sizeof(TC) - 1)) == 0) {
     const unsigned blocks = static_cast<unsigned>((width / 4 + kBlock - 1) / kBlock);
-    append_k<4><<<blocks, kBlock, 0, s>>>(cache, row, width, state, capacity);
+    append_k<TC, 4><<<blocks, kBlock, 0, s>>>(cache, row, width, state, capacity);
   } else {
     const unsigned blocks = static_cast<unsigned>((width + kBlock - 1) / kBlock);
-    append_k<1><<<blocks, kBlock, 0, s>>>(cache, row, width, state, capacity);
+    append_k<TC, 1><<<blocks, kBlock, 0, s>>>(cache, row, width, state, capacity);
   }
   return check_launch(what);
 }
 
-int64_t uocr_rocm_attend_scratch_floats(int64_t heads, int64_t hd, int64_t capacity) {
-  if (heads <= 0 || hd <= 0 || capacity <= 0) return 0;
-  return heads * attend_splits(heads, capacity) * (hd + 2);
-}
-
-int uocr_rocm_attend_step(void* stream, const float* q, const float* k_cache, const float* v_cache, int64_t heads,
-                          int64_t hd, const float* mask, float scale, const uocr_rocm_step_state* state,
-                          float* scratch, int64_t capacity, float* out) {
-  const char* what = "uocr_rocm_attend_step";
-  UOCR_REQUIRE(heads >= 0 && hd >= 0, what, "heads and hd must be >= 0");
-  if (heads == 0 || hd == 0) return UOCR_ROCM_OK;
+int check_attend(const char* what, int64_t heads, int64_t hd, int64_t capacity) {
   UOCR_REQUIRE(hd <= kMaxHeadDim, what, "head dim above 256");
   UOCR_REQUIRE(heads < (int64_t{1} << 24), what, "too many heads");
   UOCR_REQUIRE(capacity >= 1, what, "capacity must be >= 1");
+  return UOCR_ROCM_OK;
+}
+
+template <class TC, bool kRope>
+int attend_entry(const char* what, void* stream, AttendArgs a, int64_t heads, float* out) {
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  if (a.hd % kVec<TC> == 0 && aligned16(a.q) && aligned16(a.k) && aligned16(a.v)) {
+    launch_attend_vec<TC, kRope>(s, a, heads);
+  } else {
+    launch_attend_any<TC, kRope>(s, a, heads);
+  }
+  if (const int st = check_launch(what); st != UOCR_ROCM_OK) return st;
+  launch_merge(s, a, heads, out);
+  return check_launch(what);
+}
+
+template <class TC>
+int attend_plain(const char* what, void* stream, const float* q, const TC* k_cache, const TC* v_cache, int64_t heads,
+                 int64_t hd, const float* mask, float scale, const uocr_rocm_step_state* state, float* scratch,
+                 int64_t capacity, float* out) {
+  UOCR_REQUIRE(heads >= 0 && hd >= 0, what, "heads and hd must be >= 0");
+  if (heads == 0 || hd == 0) return UOCR_ROCM_OK;
+  if (const int st = check_attend(what, heads, hd, capacity)) return st;
   UOCR_REQUIRE(q != nullptr && k_cache != nullptr && v_cache != nullptr && state != nullptr && scratch != nullptr &&
                    out != nullptr,
                what, "null pointer");
@@ -519,29 +563,18 @@ int uocr_rocm_attend_step(void* stream, const float* q, const float* k_cache, co
   a.scale = scale;
   a.hd = static_cast<int>(hd);
   a.splits = attend_splits(heads, capacity);
-  const hipStream_t s = as_stream(stream);
-  clear_launch_error();
-  if (hd % 4 == 0 && aligned16(q) && aligned16(k_cache) && aligned16(v_cache)) {
-    launch_attend_vec<false>(s, a, heads);
-  } else {
-    launch_attend_any<false>(s, a, heads);
-  }
-  if (const int st = check_launch(what); st != UOCR_ROCM_OK) return st;
-  launch_merge(s, a, heads, out);
-  return check_launch(what);
+  return attend_entry<TC, false>(what, stream, a, heads, out);
 }
 
-int uocr_rocm_attend_rope_kv_step(void* stream, const float* q, const float* k_row, const float* v_row,
-                                  float* k_cache, float* v_cache, int64_t heads, int64_t hd, const float* mask,
-                                  float scale, const uocr_rocm_step_state* state, const float* inv_tok, int64_t n_tok,
-                                  const float* inv_page, int64_t page_mod, float* scratch, int64_t capacity,
-                                  float* out) {
-  const char* what = "uocr_rocm_attend_rope_kv_step";
+template <class TC>
+int attend_rope(const char* what, void* stream, const float* q, const float* k_row, const float* v_row, TC* k_cache,
+                TC* v_cache, int64_t heads, int64_t hd, const float* mask, float scale,
+                const uocr_rocm_step_state* state, const float* inv_tok, int64_t n_tok, const float* inv_page,
+                int64_t page_mod, float* scratch, int64_t capacity, float* out) {
   UOCR_REQUIRE(heads >= 0 && hd >= 0, what, "heads and hd must be >= 0");
   if (heads == 0 || hd == 0) return UOCR_ROCM_OK;
-  UOCR_REQUIRE(hd <= kMaxHeadDim && hd % 2 == 0, what, "head dim must be even and at most 256");
-  UOCR_REQUIRE(heads < (int64_t{1} << 24), what, "too many heads");
-  UOCR_REQUIRE(capacity >= 1, what, "capacity must be >= 1");
+  UOCR_REQUIRE(hd % 2 == 0, what, "head dim must be even and at most 256");
+  if (const int st = check_attend(what, heads, hd, capacity)) return st;
   UOCR_REQUIRE(n_tok >= 0 && n_tok <= hd / 2, what, "n_tok must be in [0, hd / 2]");
   UOCR_REQUIRE(n_tok == 0 || inv_tok != nullptr, what, "null inv_tok");
   UOCR_REQUIRE(n_tok == hd / 2 || inv_page != nullptr, what, "null inv_page");
@@ -568,16 +601,59 @@ int uocr_rocm_attend_rope_kv_step(void* stream, const float* q, const float* k_r
   a.inv_page = inv_page;
   a.page_mod = page_mod;
   a.n_tok = static_cast<int>(n_tok);
-  const hipStream_t s = as_stream(stream);
-  clear_launch_error();
-  if (hd % 4 == 0 && aligned16(q) && aligned16(k_cache) && aligned16(v_cache)) {
-    launch_attend_vec<true>(s, a, heads);
-  } else {
-    launch_attend_any<true>(s, a, heads);
-  }
-  if (const int st = check_launch(what); st != UOCR_ROCM_OK) return st;
-  launch_merge(s, a, heads, out);
-  return check_launch(what);
+  return attend_entry<TC, true>(what, stream, a, heads, out);
+}
+
+}  // namespace
+}  // namespace uocr_rocm
+
+extern "C" {
+
+int uocr_rocm_append_step(void* stream, float* cache, const float* row, int64_t width,
+                          const uocr_rocm_step_state* state, int64_t capacity) {
+  return append_entry("uocr_rocm_append_step", stream, cache, row, width, state, capacity);
+}
+
+int uocr_rocm_append_step_bf16(void* stream, uint16_t* cache, const float* row, int64_t width,
+                               const uocr_rocm_step_state* state, int64_t capacity) {
+  return append_entry("uocr_rocm_append_step_bf16", stream, cache, row, width, state, capacity);
+}
+
+int64_t uocr_rocm_attend_scratch_floats(int64_t heads, int64_t hd, int64_t capacity) {
+  if (heads <= 0 || hd <= 0 || capacity <= 0) return 0;
+  return heads * attend_splits(heads, capacity) * (hd + 2);
+}
+
+int uocr_rocm_attend_step(void* stream, const float* q, const float* k_cache, const float* v_cache, int64_t heads,
+                          int64_t hd, const float* mask, float scale, const uocr_rocm_step_state* state,
+                          float* scratch, int64_t capacity, float* out) {
+  return attend_plain("uocr_rocm_attend_step", stream, q, k_cache, v_cache, heads, hd, mask, scale, state, scratch,
+                      capacity, out);
+}
+
+int uocr_rocm_attend_step_bf16(void* stream, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                               int64_t heads, int64_t hd, const float* mask, float scale,
+                               const uocr_rocm_step_state* state, float* scratch, int64_t capacity, float* out) {
+  return attend_plain("uocr_rocm_attend_step_bf16", stream, q, k_cache, v_cache, heads, hd, mask, scale, state,
+                      scratch, capacity, out);
+}
+
+int uocr_rocm_attend_rope_kv_step(void* stream, const float* q, const float* k_row, const float* v_row,
+                                  float* k_cache, float* v_cache, int64_t heads, int64_t hd, const float* mask,
+                                  float scale, const uocr_rocm_step_state* state, const float* inv_tok, int64_t n_tok,
+                                  const float* inv_page, int64_t page_mod, float* scratch, int64_t capacity,
+                                  float* out) {
+  return attend_rope("uocr_rocm_attend_rope_kv_step", stream, q, k_row, v_row, k_cache, v_cache, heads, hd, mask,
+                     scale, state, inv_tok, n_tok, inv_page, page_mod, scratch, capacity, out);
+}
+
+int uocr_rocm_attend_rope_kv_step_bf16(void* stream, const float* q, const float* k_row, const float* v_row,
+                                       uint16_t* k_cache, uint16_t* v_cache, int64_t heads, int64_t hd,
+                                       const float* mask, float scale, const uocr_rocm_step_state* state,
+                                       const float* inv_tok, int64_t n_tok, const float* inv_page, int64_t page_mod,
+                                       float* scratch, int64_t capacity, float* out) {
+  return attend_rope("uocr_rocm_attend_rope_kv_step_bf16", stream, q, k_row, v_row, k_cache, v_cache, heads, hd,
+                     mask, scale, state, inv_tok, n_tok, inv_page, page_mod, scratch, capacity, out);
 }
 
 }  // extern "C"

@@ -48,6 +48,19 @@ void attend_step(const Context& ctx, const float* q, const float* k_cache, const
                  std::int64_t hd, const float* mask, float scale, const StepState* state, float* scratch,
                  std::int64_t capacity, float* out);
 
+// New: a bf16 key/value cache (rows rounded to bf16 on append, widened to
+// fp32 in the attention); half the cache bytes.
+void append_step_bf16(const Context& ctx, std::uint16_t* cache, const float* row, std::int64_t width,
+                      const StepState* state, std::int64_t capacity = -1);
+void attend_step_bf16(const Context& ctx, const float* q, const std::uint16_t* k_cache, const std::uint16_t* v_cache,
+                      std::int64_t heads, std::int64_t hd, const float* mask, float scale, const StepState* state,
+                      float* scratch, std::int64_t capacity, float* out);
+void attend_rope_kv_step_bf16(const Context& ctx, const float* q, const float* k_row, const float* v_row,
+                              std::uint16_t* k_cache, std::uint16_t* v_cache, std::int64_t heads, std::int64_t hd,
+                              const float* mask, float scale, const StepState* state, const float* inv_tok,
+                              std::int64_t n_tok, const float* inv_page, std::int64_t page_mod, float* scratch,
+                              std::int64_t capacity, float* out);
+
 // New: the step's embedding row fused with the first norm: x = table[token]
 // (+ delta, which may be null), h = rms_norm(x) * w.
 void embed_add_rms_norm_step(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,

@@ -307,6 +307,19 @@ UOCR_ROCM_API int uocr_rocm_gemv_bf16(void* stream, const float* x, int64_t k, c
 UOCR_ROCM_API int uocr_rocm_append_step(void* stream, float* cache, const float* row, int64_t width,
                                         const uocr_rocm_step_state* state, int64_t capacity);
 
+/* A bf16 key/value cache (new): the fp32 row is rounded to bf16 (nearest
+ * even) as it is appended, and the attention widens the cached keys and
+ * values to fp32 (q, the scores, the softmax and out stay fp32). Half the
+ * cache bytes of the fp32 forms; otherwise the same contract and the same
+ * arithmetic on the bf16-rounded values (a lane holds 8 cache elements
+ * instead of 4, so sums associate differently). */
+UOCR_ROCM_API int uocr_rocm_append_step_bf16(void* stream, uint16_t* cache, const float* row, int64_t width,
+                                             const uocr_rocm_step_state* state, int64_t capacity);
+UOCR_ROCM_API int uocr_rocm_attend_step_bf16(void* stream, const float* q, const uint16_t* k_cache,
+                                             const uint16_t* v_cache, int64_t heads, int64_t hd, const float* mask,
+                                             float scale, const uocr_rocm_step_state* state, float* scratch,
+                                             int64_t capacity, float* out);
+
 /* Floats of scratch that uocr_rocm_attend_step needs for (heads, hd,
  * capacity); 0 for an empty shape. Replaces attend_scratch_floats
  * (src/backend/cuda/decode_ops.h:42-43). */
@@ -389,6 +402,16 @@ UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step(void* stream, const float* q, co
                                                 const uocr_rocm_step_state* state, const float* inv_tok,
                                                 int64_t n_tok, const float* inv_page, int64_t page_mod,
                                                 float* scratch, int64_t capacity, float* out);
+/* The same over a bf16 cache: the rotated key and the value are rounded to
+ * bf16 as they are appended and scored as the cache holds them. Bitwise
+ * uocr_rocm_rope_qk_step, two uocr_rocm_append_step_bf16 and
+ * uocr_rocm_attend_step_bf16. */
+UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step_bf16(void* stream, const float* q, const float* k_row,
+                                                     const float* v_row, uint16_t* k_cache, uint16_t* v_cache,
+                                                     int64_t heads, int64_t hd, const float* mask, float scale,
+                                                     const uocr_rocm_step_state* state, const float* inv_tok,
+                                                     int64_t n_tok, const float* inv_page, int64_t page_mod,
+                                                     float* scratch, int64_t capacity, float* out);
 
 #ifdef __cplusplus
 }

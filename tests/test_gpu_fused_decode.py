@@ -265,3 +265,39 @@ def test_embed_add_rms_norm_matches_unfused(backend, dtype, cols, with_delta):
         backend.embed_add_rms_norm_step(table, state, w, x, h, delta=delta)
         view = torch.int16 if dtype == "bf16" else torch.int32
         assert torch.equal(x.view(view), xu.view(view)) and torch.equal(h.view(view), hu.view(view)), token
+
+
+@pytest.mark.parametrize("heads,hd,cap,pos,masked", [(10, 128, 8192, 5000, False), (10, 128, 2048, 1500, True),
+                                                     (2, 66, 100, 57, False), (4, 256, 10000, 9999, False)])
+def test_attend_rope_kv_bf16_cache_matches_unfused(backend, heads, hd, cap, pos, masked):
+    width = heads * hd
+    q, k_row, v_row = dev_f32(normal(380, width)), dev_f32(normal(381, width)), dev_f32(normal(382, width))
+    kc0, vc0 = oracle.f32_to_bf16(normal(383, (cap, width))), oracle.f32_to_bf16(normal(384, (cap, width)))
+    inv = dev_f32(oracle.rope_inv(hd // 2, 1e4))
+    mask = None
+    if masked:
+        m = np.where(np.random.default_rng(385).random(cap) < 0.4, -np.inf, 0).astype(np.float32)
+        m[pos] = 0.0
+        mask = dev_f32(m)
+    state = state_of(pos)
+    scale = float(1 / np.sqrt(hd))
+    scratch = torch.empty(backend.attend_scratch_floats(heads, hd, cap), device="cuda")
+    qq, kk = q.clone(), k_row.clone()
+    kc1, vc1 = dev_bf16(kc0), dev_bf16(vc0)
+    out1 = torch.empty(width, device="cuda")
+    backend.rope_qk_step(qq, heads, kk, heads, hd, state, inv, None, 0)
+    backend.append_step(kc1, kk, state)
+    backend.append_step(vc1, v_row, state)
+    backend.attend_step(qq, kc1, vc1, heads, hd, mask, scale, state, scratch, out1)
+    kc2, vc2 = dev_bf16(kc0), dev_bf16(vc0)
+    out2 = torch.empty(width, device="cuda")
+    backend.attend_rope_kv_step(q, k_row, v_row, kc2, vc2, heads, hd, mask, scale, state, inv, None, 0, scratch, out2)
+    assert np.array_equal(bits(out2), bits(out1))
+    assert torch.equal(kc2.view(torch.int16), kc1.view(torch.int16))
+    assert torch.equal(vc2.view(torch.int16), vc1.view(torch.int16))
+    keys = pos + 1
+    kf = oracle.bf16_to_f32(kc2.view(torch.int16).cpu().numpy().view(np.uint16))[:keys]
+    vf = oracle.bf16_to_f32(vc2.view(torch.int16).cpu().numpy().view(np.uint16))[:keys]
+    rq = oracle.rope(host_f32(q), heads, hd, inv_tok=host_f32(inv), one_tok=pos)
+    want = oracle.attention_one(rq, kf, vf, heads, hd, None if mask is None else host_f32(mask)[:keys], scale)
+    assert_f32_close(host_f32(out2), want, 1e-5, "attend_rope_kv bf16 cache")

@@ -261,3 +261,66 @@ def test_decode_attention_graph_replays(backend):
         want = oracle.attention_one(qv, hk[:pos + 1], hv[:pos + 1], heads, hd, None, scale)
         assert_f32_close(host_f32(out), want, 1e-5, f"replay pos={pos}")
         assert np.array_equal(host_f32(kc)[pos], hk[pos])
+
+
+# ---- a bf16 key/value cache -----------------------------------------------------------------------
+
+
+def host_bf16_bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("width", [1280, 1283])
+def test_append_step_bf16_rounds_the_row(backend, width):
+    cap = 8
+    cache = torch.zeros(cap, width, dtype=torch.bfloat16, device="cuda")
+    row = normal(180, width)
+    backend.append_step(cache, dev_f32(row), state_of(3))
+    backend.append_step(cache, dev_f32(row), state_of(cap))  # past the cache: nothing
+    got = host_bf16_bits(cache)
+    assert np.array_equal(got[3], oracle.f32_to_bf16(row))
+    assert not got[np.arange(cap) != 3].any()
+
+
+@pytest.mark.parametrize("heads,hd,cap,pos", [(10, 128, 8192, 8191), (10, 128, 8192, 100), (16, 64, 1024, 777),
+                                              (4, 80, 500, 499), (2, 66, 300, 250), (2, 256, 700, 650),
+                                              (10, 128, 16384, 12000), (1, 128, 7, 50)])
+def test_attend_step_bf16_cache(backend, heads, hd, cap, pos):
+    width = heads * hd
+    q = normal(190 + hd, width)
+    kb, vb = bf16(normal(191, (cap, width))), bf16(normal(192, (cap, width)))
+    scale = 1.0 / np.sqrt(hd)
+    keys = max(0, min(pos + 1, cap))
+    want = oracle.attention_one(q, oracle.bf16_to_f32(kb)[:keys], oracle.bf16_to_f32(vb)[:keys], heads, hd, None,
+                                scale)
+    scratch = torch.empty(max(1, backend.attend_scratch_floats(heads, hd, cap)), device="cuda")
+    out = torch.full((width,), float("nan"), device="cuda")
+    backend.attend_step(dev_f32(q), dev_bf16(kb), dev_bf16(vb), heads, hd, None, float(scale), state_of(pos), scratch,
+                        out)
+    assert_f32_close(host_f32(out), want, 1e-5, f"attend bf16 cache heads={heads} hd={hd} pos={pos}")
+
+
+def test_attend_dead_keys_never_poison_the_sum(backend):
+    """Masked and past-the-end keys load filler bits that the kernel must
+    never multiply into the value sum: here every query float's low half is
+    a bf16 NaN pattern, which a bf16 cache kernel reads as the filler."""
+    heads, hd, cap, pos = 4, 128, 1024, 700
+    width = heads * hd
+    g = np.random.default_rng(195)
+    hi = (g.integers(0x3C00, 0x4000, width, dtype=np.uint32) | (g.integers(0, 2, width, dtype=np.uint32) << 15))
+    q = ((hi << 16) | np.uint32(0x7FC0)).view(np.float32)  # finite fp32, NaN low half
+    assert np.all(np.isfinite(q)) and np.all(np.isnan(oracle.bf16_to_f32(np.full(1, 0x7FC0, np.uint16))))
+    kb, vb = bf16(normal(196, (cap, width))), bf16(normal(197, (cap, width)))
+    mask = np.where(g.random(cap) < 0.5, -np.inf, 0).astype(np.float32)
+    mask[pos] = 0.0
+    keys = pos + 1
+    scale = 1.0 / np.sqrt(hd)
+    want = oracle.attention_one(q, oracle.bf16_to_f32(kb)[:keys], oracle.bf16_to_f32(vb)[:keys], heads, hd,
+                                mask[:keys], scale)
+    scratch = torch.empty(backend.attend_scratch_floats(heads, hd, cap), device="cuda")
+    for kc, vc in ((dev_bf16(kb), dev_bf16(vb)), (dev_f32(oracle.bf16_to_f32(kb)), dev_f32(oracle.bf16_to_f32(vb)))):
+        out = torch.empty(width, device="cuda")
+        backend.attend_step(dev_f32(q), kc, vc, heads, hd, dev_f32(mask), float(scale), state_of(pos), scratch, out)
+        got = host_f32(out)
+        assert np.all(np.isfinite(got))
+        assert_f32_close(got, want, 1e-5, f"dead keys, {kc.dtype} cache")
