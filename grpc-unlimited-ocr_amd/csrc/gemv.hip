@@ -22,7 +22,12 @@ namespace {
 
 constexpr int64_t kGemvMaxK = 12288;        // the reference's bound (gemv_ops.h:16)
 constexpr int kGemvRegChunks = 4;           // register-resident x: k <= 64 * 4 * 8
-constexpr unsigned kGemvMaxBlocks = 2048;   // grid-stride beyond 8192 waves
+// Large matrices: 2 rows per wave and at most 6144 workgroups, walking the
+// rows grid-stride. Measured on the 129280 x 1280 LM head: 49.3 us against
+// 54.3 us for 4 rows and 2048 workgroups, and against 51-65 us for the other
+// combinations of 1, 2, 4 rows and 512 .. unbounded workgroups.
+constexpr unsigned kGemvMaxBlocks = 6144;
+constexpr int kBigRows = 16384;  // from here on, 2 rows per wave
 
 // Eight bf16 weights (one chunk) against eight fp32 inputs, in order.
 __device__ __forceinline__ float dot8(const u32x4 w, const float (&x)[8], float acc) {
@@ -165,9 +170,8 @@ unsigned gemv_blocks(int64_t waves) {
 template <int CPL>
 void launch_reg(hipStream_t s, const float* x, int nchunks, const uint16_t* w, int64_t n, const float* bias,
                 float* y) {
-  // Four rows per wave once there are enough rows to fill the GPU with them.
-  if (n >= 16384) {
-    gemv_reg<CPL, 4><<<gemv_blocks((n + 3) / 4), kBlock, 0, s>>>(x, nchunks, w, n, bias, y);
+  if (n >= kBigRows) {
+    gemv_reg<CPL, 2><<<gemv_blocks((n + 1) / 2), kBlock, 0, s>>>(x, nchunks, w, n, bias, y);
   } else {
     gemv_reg<CPL, 1><<<gemv_blocks(n), kBlock, 0, s>>>(x, nchunks, w, n, bias, y);
   }
@@ -346,8 +350,8 @@ __global__ __launch_bounds__(kBlock) void gemv_fused(const FusedGemv a) {
 
 template <int CPL, bool kNorm, bool kPair>
 void launch_fused_rows(hipStream_t s, const FusedGemv& a) {
-  if (a.n >= 16384) {
-    gemv_fused<CPL, 4, kNorm, kPair><<<gemv_blocks((a.n + 3) / 4), kBlock, 0, s>>>(a);
+  if (a.n >= kBigRows) {
+    gemv_fused<CPL, 2, kNorm, kPair><<<gemv_blocks((a.n + 1) / 2), kBlock, 0, s>>>(a);
   } else {
     gemv_fused<CPL, 1, kNorm, kPair><<<gemv_blocks(a.n), kBlock, 0, s>>>(a);
   }
