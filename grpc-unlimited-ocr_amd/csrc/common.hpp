@@ -292,6 +292,19 @@ inline uint64_t reciprocal_magic(uint32_t d) {
   return ~uint64_t{0} / d + 1;
 }
 
+// ---- XCD-aware block order --------------------------------------------------------
+// MI355X dispatches consecutive workgroups round-robin over its 8 XCDs, each
+// with its own L2. xcd_block(b, n) renumbers block b of n so that XCD x walks
+// one contiguous range of the logical blocks: blocks that share data (rows
+// that read the same mask row) then meet in one L2. A bijection on [0, n).
+constexpr unsigned kXcds = 8;
+
+__device__ __forceinline__ unsigned xcd_block(unsigned b, unsigned n) {
+  const unsigned xcd = b % kXcds, local = b / kXcds;
+  const unsigned per = n / kXcds, extra = n % kXcds;
+  return xcd * per + (xcd < extra ? xcd : extra) + local;
+}
+
 // ---- host side ----------------------------------------------------------------
 
 // Records "<what>: <detail>" as this thread's last error and returns `status`.

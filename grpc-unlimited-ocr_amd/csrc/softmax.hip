@@ -35,8 +35,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 // it: scale_mask_softmax_rows is then bitwise scale_add_mask + softmax_rows
 // with one read and one write of the scores instead of two of each.
 // Rows are visited mask-row-major: logical row R is slice R mod batch of mask
-// row R / batch, so the `batch` rows that share a mask row run side by side
-// and the mask row is mostly read from cache.
+// row R / batch, and the blocks run in XCD-aware order (xcd_block), so the
+// `batch` rows that share a mask row run side by side on one XCD and the
+// mask row is read once into its L2 (258 -> 240 us on [10 x 4096, 4096]).
 struct RowMask {
   const float* mask;  // [mask_rows, cols], or null (+ 0)
   float scale;
@@ -53,7 +54,9 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_k(float* __restrict__ x, 
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int rloc = wave / WPR, wr = wave % WPR;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rloc;
+  // With a mask, XCD-aware order: the rows of one mask row run on one XCD.
+  const unsigned blk = kMask ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int64_t row = static_cast<int64_t>(blk) * kRowsPerBlock + rloc;
   const bool active = row < rows;
   const int nvec = cols / VW;
   const int groups = (nvec + kWave - 1) / kWave;
@@ -204,6 +207,8 @@ int softmax_entry(const char* what, void* stream, float* x, int64_t rows, int64_
 // One thread per mask chunk and group of SB slices: the mask chunk is read
 // once into registers, then the SB slices' chunks are loaded together,
 // scaled, masked and stored. blockIdx.x = group * blocks_per_slice + block.
+// (An XCD-aware, chunk-major order measured no faster: the Infinity Cache
+// already serves the other groups' re-reads of a mask chunk.)
 template <int VW, int SB>
 __global__ __launch_bounds__(kBlock) void scale_mask_k(float* __restrict__ x, float scale,
                                                         const float* __restrict__ mask, uint32_t per_chunks,
