@@ -547,7 +547,7 @@ def cpu_baseline(budget_s, threads):
 # ---- rocprofv3 summaries -------------------------------------------------------------------------------
 
 PROFILES = os.path.join(ROOT, "profiles")
-TRAFFIC_FILE = os.path.join(PROFILES, "pmc_traffic_workload5.md")
+TRAFFIC_FILE = os.path.join(PROFILES, "pmc_traffic_workloads3_to_6.md")
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 COPY_BYTES = 256 * 2**20  # the calibration copy: 256 MiB read and 256 MiB written per dispatch
 

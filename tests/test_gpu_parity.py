@@ -168,6 +168,41 @@ def test_bf16_swiglu_shapes(backend, rows, ffn):
     assert_bf16_close(host_bits(out), oracle.swiglu(oracle.bf16_to_f32(inp)), f"swiglu_bf16 {rows}x{ffn}")
 
 
+# Elementwise grids switch from four-wave to one-wave workgroups past 524288
+# threads (one resident round of waves): sizes at, just past and well past
+# that boundary, with ragged tails, for every flat op and dtype.
+@pytest.mark.parametrize("chunks,tail", [(524288, 0), (524289, 3), (1 << 20, 7)])
+def test_flat_ops_across_workgroup_size_switch(backend, chunks, tail):
+    n = 8 * chunks + tail
+    x = normal(chunks + tail, n, 2.0)
+    xb = bf16(x)
+    d = dev_bf16(xb)
+    backend.gelu_erf(d)
+    assert_bf16_close(host_bits(d), oracle.gelu_erf(oracle.bf16_to_f32(xb)), f"gelu_erf_bf16 n={n}")
+    d = dev_bf16(xb)
+    backend.quick_gelu(d)
+    assert_bf16_close(host_bits(d), oracle.quick_gelu(oracle.bf16_to_f32(xb)), f"quick_gelu_bf16 n={n}")
+    n32 = 4 * chunks + tail
+    x32, y32 = x[:n32].copy(), normal(chunks + 1, n32)
+    d = dev_f32(x32)
+    backend.gelu_erf(d)
+    assert_f32_close(host_f32(d), oracle.gelu_erf(x32), 1e-6, f"gelu_erf n={n32}")
+    g, u = dev_f32(x32), dev_f32(y32)
+    backend.silu_mul(g, u)
+    assert_f32_close(host_f32(g), oracle.silu_mul(x32, y32), 1e-6, f"silu_mul n={n32}")
+    a = dev_f32(x32)
+    backend.add_inplace(a, dev_f32(y32))
+    assert np.array_equal(host_f32(a), oracle.add(x32, y32)), f"add_inplace n={n32}"
+
+
+@pytest.mark.parametrize("rows,ffn", [(2978, 1408), (2980, 1408), (40330, 13)])
+def test_bf16_swiglu_across_workgroup_size_switch(backend, rows, ffn):
+    inp = bf16(normal(rows + ffn, (rows, 2 * ffn), 2.0))
+    out = torch.empty(rows, ffn, dtype=torch.bfloat16, device="cuda")
+    backend.swiglu(dev_bf16(inp), out)
+    assert_bf16_close(host_bits(out), oracle.swiglu(oracle.bf16_to_f32(inp)), f"swiglu_bf16 {rows}x{ffn}")
+
+
 @pytest.mark.parametrize("dim,qh,kh,n_page", [(128, 16, 4, 0), (128, 10, 10, 1), (64, 1, 0, 0), (16, 2, 1, 1),
                                               (6, 3, 2, 0), (512, 2, 1, 0)])
 def test_bf16_rope_shapes(backend, dim, qh, kh, n_page):
