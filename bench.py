@@ -458,6 +458,7 @@ def config7(be, torch, timer):
         "attend_rope_kv_step_f32": report("attend+rope+append", b["attend"] + b["append"], timer.graph(
             [lambda s=s: be.attend_rope_kv_step(q, k, v, s["kc"], s["vc"], heads, hd, None, scale, state, inv, None,
                                                 0, scratch, attn) for s in sets])[0]),
+        # a bf16 cache halves the key/value bytes and, at this shape, the splits (64 against 128)
         "attend_rope_kv_step_bf16_cache": report("attend+rope+append, bf16 cache", (b["attend"] + b["append"]) // 2,
                                                  time_kernel(timer, lambda: (bf16_randn(torch, (cap, width)),
                                                                              bf16_randn(torch, (cap, width))),

@@ -18,8 +18,9 @@
 //            keys (-inf) are neither scored nor read. The 4 * 64 / G lane
 //            groups then fold through LDS into one (m, l, acc[hd]) record
 //            per split.
-//   merge    one workgroup per head folds the splits' records and writes
-//            out = acc / l (zeros when every key is masked).
+//   merge    one workgroup per (head, 64 elements of the head) folds the
+//            splits' records and writes out = acc / l (zeros when every key
+//            is masked).
 // Scores are s = (q . k) * scale + mask (two roundings, as the reference's
 // CPU attention forms them, src/backend/reference/ops.cpp:219-251); every
 // exponential is 2^((s - m) log2 e) on v_exp_f32.
@@ -31,7 +32,7 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int64_t kMaxHeadDim = 256;
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 128;
 constexpr int kMaskTile = 2048;
 
 // ---- append ---------------------------------------------------------------------
@@ -372,73 +373,87 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   }
 }
 
-// One workgroup per head. Wave 0 reads the splits' (m, l) pairs (one split
-// per lane) and turns them into weights 2^((m_s - M) log2 e) in LDS; then
-// wave w sums splits w, w + 4, ... of the weighted value records, every
-// lane holding VPT elements of the head, with all kMaxSplits / 4 loads per
-// element issued together (indices clamped, weight 0 past `splits`); the
-// four wave partials add in wave order.
-template <int VPT>
+// One workgroup per (head, 64-element slice of the head). Wave 0 reads the
+// splits' (m, l) pairs (SPLITS / 64 per lane) and turns them into weights
+// 2^((m_s - M) log2 e) in LDS; then wave w sums splits w, w + 4, ... of the
+// slice's weighted value records, with all SPLITS / 4 loads per lane issued
+// together (indices clamped, weight 0 past `splits`); the four wave
+// partials add in wave order. SPLITS is 64 or 128, the smallest that holds
+// `splits`, so a short cache does not pay for 128 record loads.
+template <int SPLITS>
 __global__ __launch_bounds__(kBlock) void attend_merge(const float* __restrict__ part, int hd, int splits,
                                                        float* __restrict__ out) {
-  constexpr int kPerWave = kMaxSplits / kWavesPerBlock;
-  __shared__ float s_w[kMaxSplits];
+  constexpr int kPerWave = SPLITS / kWavesPerBlock;
+  constexpr int kPerLane = SPLITS / kWave;
+  __shared__ float s_w[SPLITS];
   __shared__ float s_total;
-  __shared__ float s_red[kWavesPerBlock][kWave * VPT];
-  const int h = blockIdx.x;
+  __shared__ float s_red[kWavesPerBlock][kWave];
+  const int slices = (hd + kWave - 1) / kWave;
+  const int h = blockIdx.x / slices;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int e = (blockIdx.x - h * slices) * kWave + lane;
+  const int ec = e < hd ? e : hd - 1;
   const int64_t rec_len = hd + 2;
   const float* recs = part + static_cast<int64_t>(h) * splits * rec_len;
   // Every load is issued before the first is used: the value records, then
   // wave 0's (m, l) pairs.
-  float vals[kPerWave][VPT];
+  float vals[kPerWave];
 #pragma unroll
   for (int r = 0; r < kPerWave; ++r) {
-    const int s = wave + kWavesPerBlock * r;
-    const int sc = s < splits ? s : splits - 1;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int e = lane + kWave * i;
-      vals[r][i] = recs[sc * rec_len + 2 + (e < hd ? e : hd - 1)];
-    }
+    const int sp = wave + kWavesPerBlock * r;
+    vals[r] = recs[(sp < splits ? sp : splits - 1) * rec_len + 2 + ec];
   }
   if (wave == 0) {
-    const int s = lane < splits ? lane : splits - 1;
-    const float m_raw = recs[s * rec_len];
-    const float l = recs[s * rec_len + 1];
-    const float m = lane < splits ? m_raw : -INFINITY;
-    const float big = wave_max(m);
-    const float w = (m == -INFINITY || big == -INFINITY) ? 0.0f : exp_shift(m, big);
-    s_w[lane] = w;
-    const float total = wave_sum(w * l);
+    float m[kPerLane], l[kPerLane];
+    float big = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) {
+      const int sp = lane + kWave * k;
+      const int sc = sp < splits ? sp : splits - 1;
+      const float m_raw = recs[sc * rec_len];
+      l[k] = recs[sc * rec_len + 1];
+      m[k] = sp < splits ? m_raw : -INFINITY;
+      big = fmaxf(big, m[k]);
+    }
+    big = wave_max(big);
+    float tl = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) {
+      const float w = (m[k] == -INFINITY || big == -INFINITY) ? 0.0f : exp_shift(m[k], big);
+      s_w[lane + kWave * k] = w;
+      tl = k == 0 ? w * l[k] : fmaf(w, l[k], tl);
+    }
+    const float total = wave_sum(tl);
     if (lane == 0) s_total = total;
   }
   __syncthreads();
-  float acc[VPT];
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) acc[i] = 0.0f;
+  float acc = 0.0f;
 #pragma unroll
   for (int r = 0; r < kPerWave; ++r) {
-    const int s = wave + kWavesPerBlock * r;
-    const float w = s < splits ? s_w[s] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) acc[i] = fmaf(w, vals[r][i], acc[i]);
+    const int sp = wave + kWavesPerBlock * r;
+    acc = fmaf(sp < splits ? s_w[sp] : 0.0f, vals[r], acc);
   }
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) s_red[wave][lane + kWave * i] = acc[i];
+  s_red[wave][lane] = acc;
   __syncthreads();
-  const float total = s_total;
-  for (int e = threadIdx.x; e < hd; e += kBlock) {
-    const float sum = (s_red[0][e] + s_red[1][e]) + (s_red[2][e] + s_red[3][e]);
+  if (wave == 0 && e < hd) {
+    const float total = s_total;
+    const float sum = (s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane]);
     out[static_cast<int64_t>(h) * hd + e] = total > 0.0f ? sum / total : 0.0f;
   }
 }
 
-// Splits per head: enough workgroups for the 256 CUs at every head count,
-// but no split shorter than 32 keys of capacity.
-int attend_splits(int64_t heads, int64_t capacity) {
-  int64_t s = (1024 + heads - 1) / heads;
-  const int64_t by_keys = (capacity + 31) / 32;
+// Splits per head: about 2048 workgroups (8 per CU) at every head count, but
+// no split under 64 KB of key and value rows at a full cache, and at most
+// 128. Measured at 10 heads of 128 against the 64 splits of a 1024-workgroup
+// target: 6-7% faster for an fp32 cache at 8192 and 32768 positions (128
+// splits), and for a bf16 cache the same at 8192 (64 splits), 4% faster at
+// 32768 and 9% faster at 2048 (16 splits); an fp32 cache at 2048 positions
+// (32 splits) was 4% slower.
+int attend_splits(int64_t heads, int64_t hd, int64_t capacity, int64_t elem_bytes) {
+  int64_t s = (2048 + heads - 1) / heads;
+  int64_t min_keys = 65536 / (2 * hd * elem_bytes);
+  if (min_keys < 32) min_keys = 32;
+  const int64_t by_keys = (capacity + min_keys - 1) / min_keys;
   if (s > by_keys) s = by_keys;
   if (s > kMaxSplits) s = kMaxSplits;
   return static_cast<int>(s < 1 ? 1 : s);
@@ -484,12 +499,11 @@ void launch_attend_any(hipStream_t s, const AttendArgs& a, int64_t heads) {
 }
 
 void launch_merge(hipStream_t s, const AttendArgs& a, int64_t heads, float* out) {
-  if (a.hd <= kWave) {
-    attend_merge<1><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(a.part, a.hd, a.splits, out);
-  } else if (a.hd <= 2 * kWave) {
-    attend_merge<2><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(a.part, a.hd, a.splits, out);
+  const unsigned blocks = static_cast<unsigned>(heads * ((a.hd + kWave - 1) / kWave));
+  if (a.splits <= kWave) {
+    attend_merge<kWave><<<blocks, kBlock, 0, s>>>(a.part, a.hd, a.splits, out);
   } else {
-    attend_merge<4><<<static_cast<unsigned>(heads), kBlock, 0, s>>>(a.part, a.hd, a.splits, out);
+    attend_merge<kMaxSplits><<<blocks, kBlock, 0, s>>>(a.part, a.hd, a.splits, out);
   }
 }
 
@@ -562,7 +576,7 @@ int attend_plain(const char* what, void* stream, const float* q, const TC* k_cac
   a.capacity = capacity;
   a.scale = scale;
   a.hd = static_cast<int>(hd);
-  a.splits = attend_splits(heads, capacity);
+  a.splits = attend_splits(heads, hd, capacity, sizeof(TC));
   return attend_entry<TC, false>(what, stream, a, heads, out);
 }
 
@@ -592,7 +606,7 @@ int attend_rope(const char* what, void* stream, const float* q, const float* k_r
   a.capacity = capacity;
   a.scale = scale;
   a.hd = static_cast<int>(hd);
-  a.splits = attend_splits(heads, capacity);
+  a.splits = attend_splits(heads, hd, capacity, sizeof(TC));
   a.k_row = k_row;
   a.v_row = v_row;
   a.k_out = k_cache;
@@ -621,7 +635,8 @@ int uocr_rocm_append_step_bf16(void* stream, uint16_t* cache, const float* row, 
 
 int64_t uocr_rocm_attend_scratch_floats(int64_t heads, int64_t hd, int64_t capacity) {
   if (heads <= 0 || hd <= 0 || capacity <= 0) return 0;
-  return heads * attend_splits(heads, capacity) * (hd + 2);
+  // An fp32 cache has the most splits; a bf16 cache uses at most as many.
+  return heads * attend_splits(heads, hd, capacity, sizeof(float)) * (hd + 2);
 }
 
 int uocr_rocm_attend_step(void* stream, const float* q, const float* k_cache, const float* v_cache, int64_t heads,

@@ -172,6 +172,9 @@ def test_step_op_empty_shapes_and_scratch_size(backend):
     assert lib.uocr_rocm_add_rms_norm_gemv_bf16(None, None, None, None, None, 1e-6, None, 128, None, 0, None,
                                                 None) == 0
     assert lib.uocr_rocm_attend_scratch_floats(0, 128, 100) == 0
-    # records only (no per-key scores): heads x splits x (hd + 2), 64 splits at 10 heads and 8192 positions
-    assert lib.uocr_rocm_attend_scratch_floats(10, 128, 8192) == 10 * 64 * 130
+    # records only (no per-key scores): heads x splits x (hd + 2), sized for an fp32 cache; 128 splits at 10
+    # heads and 8192 positions, 32 at 2048 (no split under 64 KB of key and value rows), 1 for a 7-key cache
+    assert lib.uocr_rocm_attend_scratch_floats(10, 128, 8192) == 10 * 128 * 130
+    assert lib.uocr_rocm_attend_scratch_floats(10, 128, 2048) == 10 * 32 * 130
+    assert lib.uocr_rocm_attend_scratch_floats(32, 64, 1 << 20) == 32 * 64 * 66
     assert lib.uocr_rocm_attend_scratch_floats(1, 64, 7) == 1 * 1 * 66
