@@ -39,7 +39,8 @@ the same procedure applied to one kernel.
 cpu_baseline: the reference's CPU path for workload 5 (the oracle's
 restatement of src/backend/reference/ops.cpp and src/model/page_rope.cpp,
 with the reference's threading: norms over rows on up to 16 threads,
-activations and rope serial) timed on this host.
+activations and rope serial) timed on this host; workloads 1-5 each carry
+the same CPU figure for their own work under "cpu".
 """
 
 import argparse
@@ -501,48 +502,114 @@ def config7(be, torch, timer):
 
 # ---- the CPU baseline (the reference's CPU path, restated in the oracle) ------------------------------
 
-def cpu_baseline(budget_s, threads):
+def _cpu_median(fn, budget_s, max_runs=20):
+    """Median seconds per call of fn over at least 3 and at most max_runs
+    calls, or as many as budget_s allows, after one warm-up call."""
+    fn()
+    times, t_end = [], time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_workloads(budget_s, threads):
+    """Workloads 1-5 on the reference's CPU path: the oracle's C restatement
+    of src/backend/reference/ops.cpp, src/model/page_rope.cpp and the
+    decoder's add/copy/norm chain, called on preallocated fp32 buffers (the
+    reference's only CPU dtype; bf16 inputs widened) so that no copy beyond
+    the reference's own is timed. Norms run over rows on `threads` threads,
+    activations, rope and the add serially, as in the reference. Returns
+    {workload: figures}; rates use the same algorithmic bytes as the GPU."""
+    import ctypes
+
     import numpy as np
 
     import oracle
 
-    rows, hidden, ffn, qh, kh, dim = 8192, 2048, 1408, 16, 4, 128
+    lib = oracle.lib()
+    p = lambda a: a.ctypes.data  # noqa: E731
     g = np.random.default_rng(5)
-    bf = lambda a: oracle.bf16_round(a)  # noqa: E731  the bf16 inputs, widened to fp32
-    x = bf(g.standard_normal((rows, hidden), dtype=np.float32))
-    d = bf(g.standard_normal((rows, hidden), dtype=np.float32))
-    w = (1 + 0.02 * g.standard_normal(hidden)).astype(np.float32)
-    inp = bf(g.standard_normal((rows, 2 * ffn), dtype=np.float32))
-    q = bf(g.standard_normal((rows, qh * dim), dtype=np.float32))
-    k = bf(g.standard_normal((rows, kh * dim), dtype=np.float32))
-    pos = np.arange(rows, dtype=np.int64)
-    inv = oracle.rope_inv(dim // 2, 1e4)
-    total = (bytes_add_rms_norm(rows, hidden, 2) + bytes_swiglu(rows, ffn, 2) + bytes_rope(rows, qh + kh, dim, 2))
+    rnd = lambda *shape: oracle.bf16_round(g.standard_normal(shape, dtype=np.float32))  # noqa: E731
+    wts = lambda n: (1 + 0.02 * g.standard_normal(n)).astype(np.float32)  # noqa: E731
+    inv = oracle.rope_inv(64, 1e4)
+    out = {}
+    oracle.set_threads(threads)
 
-    def chain():
-        oracle.add_rms_norm(x, d, w, 1e-6)
-        oracle.swiglu(inp)
-        oracle.rope(q, qh, dim, tok=pos, inv_tok=inv)
-        oracle.rope(k, kh, dim, tok=pos, inv_tok=inv)
+    # 1: fp32 RMSNorm [1024, 2048] in place
+    x1, w1 = g.standard_normal((1024, 2048), dtype=np.float32), wts(2048)
+    t, n = _cpu_median(lambda: lib.orc_rms_norm(p(x1), p(w1), 1024, 2048, 1e-6), budget_s)
+    out["1"] = {"ms": round(t * 1e3, 3), "gbps": round(bytes_rms_norm(1024, 2048, 4) / t / 1e9, 3), "runs": n}
 
-    def run(nthreads):
-        oracle.set_threads(nthreads)
-        chain()  # warm-up
-        times, t_end = [], time.perf_counter() + budget_s / 2
-        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
-            t0 = time.perf_counter()
-            chain()
-            times.append(time.perf_counter() - t0)
-        return statistics.median(times), len(times)
+    # 2: decode chain at batch 1 (gather of one row of a [128000, 2048] table, add + RMSNorm, rope q and k)
+    table = np.empty((128000, 2048), np.uint16)  # untouched rows stay unmapped
+    token, pos = 77777, 12345
+    table[token] = oracle.f32_to_bf16(0.02 * g.standard_normal(2048, dtype=np.float32))
+    ids = np.array([token], np.int64)
+    tok = np.array([pos], np.int64)
+    e, d2, h2, w2 = np.empty(2048, np.float32), rnd(2048), np.empty(2048, np.float32), wts(2048)
+    q2, k2 = rnd(16 * 128), rnd(4 * 128)
+    nul = ctypes.c_void_p()
 
-    t_mt, n_mt = run(threads)
-    t_1, n_1 = run(1)
+    def chain2():
+        lib.orc_embed(p(table), p(ids), 1, 2048, p(e))
+        lib.orc_add_rms_norm(p(e), p(d2), p(w2), p(h2), 1, 2048, 1e-6)
+        lib.orc_rope_apply(p(q2), 1, 16, 128, p(tok), nul, p(inv), 64, nul, 0, 0, 0, 0)
+        lib.orc_rope_apply(p(k2), 1, 4, 128, p(tok), nul, p(inv), 64, nul, 0, 0, 0, 0)
+
+    reps = 200
+    t, n = _cpu_median(lambda: [chain2() for _ in range(reps)], budget_s)
+    out["2"] = {"us": round(t / reps * 1e6, 3), "runs": n, "note": f"mean of {reps} chains per run, "
+                "including Python's per-call overhead (4 calls)"}
+    del table
+
+    # 3: RoPE Q [8192, 16, 128], K [8192, 4, 128] in place, positions 0..8191
+    q3, k3, pos3 = rnd(8192, 16 * 128), rnd(8192, 4 * 128), np.arange(8192, dtype=np.int64)
+
+    def rope3():
+        lib.orc_rope_apply(p(q3), 8192, 16, 128, p(pos3), nul, p(inv), 64, nul, 0, 0, 0, 0)
+        lib.orc_rope_apply(p(k3), 8192, 4, 128, p(pos3), nul, p(inv), 64, nul, 0, 0, 0, 0)
+
+    t, n = _cpu_median(rope3, budget_s)
+    out["3"] = {"ms": round(t * 1e3, 3), "gbps": round(bytes_rope(8192, 20, 128, 2) / t / 1e9, 3), "runs": n}
+
+    # 4: LayerNorm [4096, 1024] then GELU, in place
+    x4, w4, b4 = rnd(4096, 1024), wts(1024), (0.02 * g.standard_normal(1024)).astype(np.float32)
+
+    def vision4():
+        lib.orc_layer_norm(p(x4), p(w4), p(b4), 4096, 1024, 1e-6)
+        lib.orc_gelu_erf(p(x4), 4096 * 1024)
+
+    t, n = _cpu_median(vision4, budget_s)
+    out["4"] = {"ms": round(t * 1e3, 3), "runs": n,
+                "gbps": round((bytes_layer_norm(4096, 1024, 2) + bytes_gelu(4096 * 1024, 2)) / t / 1e9, 3)}
+
+    # 5: add + RMSNorm [8192, 2048], SwiGLU [8192, 2 x 1408], rope as 3
+    x5, d5, w5, h5 = rnd(8192, 2048), rnd(8192, 2048), wts(2048), np.empty((8192, 2048), np.float32)
+    in5, o5 = rnd(8192, 2 * 1408), np.empty((8192, 1408), np.float32)
+
+    def chain5():
+        lib.orc_add_rms_norm(p(x5), p(d5), p(w5), p(h5), 8192, 2048, 1e-6)
+        lib.orc_swiglu(p(in5), p(o5), 8192, 1408)
+        rope3()
+
+    total5 = bytes_add_rms_norm(8192, 2048, 2) + bytes_swiglu(8192, 1408, 2) + bytes_rope(8192, 20, 128, 2)
+    t, n = _cpu_median(chain5, budget_s)
     oracle.set_threads(1)
-    return {"value": round(total / t_mt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"workload 5 in full (8192 tokens, {total} algorithmic bytes per chain), median of {n_mt} "
-                      f"chains; norms on {threads} threads, activations and rope serial as in the reference",
-            "ms_per_chain": round(t_mt * 1e3, 2), "ms_per_chain_1_thread": round(t_1 * 1e3, 2),
-            "value_1_thread": round(total / t_1 / 1e9, 3)}
+    t1, n1 = _cpu_median(chain5, budget_s)
+    out["5"] = {"ms": round(t * 1e3, 3), "gbps": round(total5 / t / 1e9, 3), "runs": n,
+                "ms_1_thread": round(t1 * 1e3, 3), "gbps_1_thread": round(total5 / t1 / 1e9, 3)}
+    return out
+
+
+def cpu_baseline(cpu, threads):
+    """The top-level cpu_baseline object: workload 5 from cpu_workloads."""
+    c = cpu["5"]
+    return {"value": c["gbps"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"workload 5 in full (8192 tokens), median of {c['runs']} chains on preallocated fp32 "
+                      f"buffers; norms on {threads} threads, activations and rope serial as in the reference",
+            "ms_per_chain": c["ms"], "ms_per_chain_1_thread": c["ms_1_thread"], "value_1_thread": c["gbps_1_thread"]}
 
 
 # ---- rocprofv3 summaries -------------------------------------------------------------------------------
@@ -699,7 +766,11 @@ def main():
         })
     if not args.no_cpu and head is not None:
         threads = max(1, min(16, os.cpu_count() or 1))
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, threads)
+        cpu = cpu_workloads(args.cpu_seconds / 6, threads)
+        line["cpu_baseline"] = cpu_baseline(cpu, threads)
+        for c, fig in cpu.items():
+            if c in configs:
+                configs[c]["cpu"] = {**fig, "threads": threads, "kind": "port"}
     line["configs"] = configs
     print(json.dumps(line), flush=True)
 

@@ -1,0 +1,96 @@
+"""The host side of bench.py, on the CPU: the one-GPU rule, the CPU baseline
+over workloads 1-5, the algorithmic byte counts the roofline divides by, and
+the rocprofv3 summarisers that write profiles/ (fed small synthetic CSVs)."""
+
+import csv
+import os
+import subprocess
+import sys
+
+import pytest
+
+from conftest import ROOT
+
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_algorithmic_bytes_match_the_workload_definitions():
+    # add+RMSNorm [8192, 2048] bf16: R x, R delta, W x', W h, R w (fp32)
+    assert bench.bytes_add_rms_norm(8192, 2048, 2) == 134_225_920
+    # SwiGLU [8192, 2 x 1408] -> [8192, 1408] bf16
+    assert bench.bytes_swiglu(8192, 1408, 2) == 69_206_016
+    # RoPE Q [8192, 16, 128] + K [8192, 4, 128] bf16 in place + int64 positions
+    assert bench.bytes_rope(8192, 20, 128, 2) == 83_951_616
+    # fp32 RMSNorm [1024, 2048] and the vision pair LayerNorm + GELU [4096, 1024] bf16
+    assert bench.bytes_rms_norm(1024, 2048, 4) == 16_785_408
+    assert bench.bytes_layer_norm(4096, 1024, 2) + bench.bytes_gelu(4096 * 1024, 2) == 33_562_624
+    assert (bench.bytes_add_rms_norm(8192, 2048, 2) + bench.bytes_swiglu(8192, 1408, 2)
+            + bench.bytes_rope(8192, 20, 128, 2)) == 287_383_552
+
+
+def test_cpu_workloads_report_every_workload():
+    cpu = bench.cpu_workloads(0.01, 2)
+    assert set(cpu) == {"1", "2", "3", "4", "5"}
+    for c in ("1", "3", "4", "5"):
+        assert cpu[c]["ms"] > 0 and cpu[c]["gbps"] > 0 and cpu[c]["runs"] >= 3
+    assert cpu["2"]["us"] > 0
+    line = bench.cpu_baseline(cpu, 2)
+    assert line["kind"] == "port" and line["cores"] == 2 and line["unit"] == "GB/s"
+    assert line["value"] == cpu["5"]["gbps"] and line["value_1_thread"] > 0
+
+
+def _write_csv(path, fields, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        w.writerows(rows)
+
+
+def test_trace_summary_takes_durations_per_kernel_and_grid(tmp_path):
+    rows = []
+    for i, dur in enumerate([4000, 5000, 6000]):
+        rows.append({"Kernel_Name": "void uocr_rocm::(anonymous namespace)::rope_rows<unsigned short, 8>(Args)",
+                     "Grid_Size": "262144", "Workgroup_Size": "128", "Start_Timestamp": str(1000 * i),
+                     "End_Timestamp": str(1000 * i + dur)})
+    rows.append({"Kernel_Name": "at::native::vectorized_elementwise_kernel<4>(int)", "Grid_Size": "64",
+                 "Workgroup_Size": "64", "Start_Timestamp": "0", "End_Timestamp": "900"})
+    _write_csv(tmp_path / "run_kernel_trace.csv", list(rows[0]), rows)
+    table = bench.summarize_trace(str(tmp_path))
+    lines = table.splitlines()
+    assert len(lines) == 3  # header, rule, one kernel: torch's own kernels are left out
+    assert "rope_rows<unsigned short, 8>" in lines[2]
+    assert "| 262144 | 128 | 3 | 5.00 | 5.00 | 4.00 |" in lines[2]
+
+
+def test_pmc_summary_scales_by_the_calibration_copy(tmp_path):
+    copy = bench.COPY_KERNEL
+    kib = bench.COPY_BYTES / 1024
+    fetch = [{"Kernel_Name": copy, "Grid_Size": "131072", "Counter_Name": "FETCH_SIZE", "Counter_Value": str(kib / 2)},
+             {"Kernel_Name": "norm_rows<float>(float*)", "Grid_Size": "256", "Counter_Name": "FETCH_SIZE",
+              "Counter_Value": "100"}]
+    write = [{"Kernel_Name": copy, "Grid_Size": "131072", "Counter_Name": "WRITE_SIZE", "Counter_Value": str(kib)},
+             {"Kernel_Name": "norm_rows<float>(float*)", "Grid_Size": "256", "Counter_Name": "WRITE_SIZE",
+              "Counter_Value": "50"}]
+    (tmp_path / "f").mkdir()
+    (tmp_path / "w").mkdir()
+    _write_csv(tmp_path / "f" / "run_counter_collection.csv", list(fetch[0]), fetch)
+    _write_csv(tmp_path / "w" / "run_counter_collection.csv", list(write[0]), write)
+    table = bench.summarize_pmc(str(tmp_path / "f"), str(tmp_path / "w"))
+    assert table.startswith("FETCH_SIZE scale 2.0000, WRITE_SIZE scale 1.0000")
+    row = [ln for ln in table.splitlines() if "norm_rows" in ln]
+    assert row and row[0].endswith(f"| {2 * 100 * 1024 + 50 * 1024} |")
+
+
+def test_committed_traffic_reads_the_profile():
+    got = bench.committed_traffic("norm_rows<unsigned short, 8, 1, 4, (Norm)1>", 8192 * 64)
+    if not os.path.exists(bench.TRAFFIC_FILE):
+        pytest.skip("no committed PMC summary")
+    assert got is not None and abs(got - 134_225_920) / 134_225_920 < 0.01
