@@ -26,6 +26,10 @@ line's `value` is workload 5 (the largest, three fused ops timed as one
 sequence): algorithmic HBM bytes per step / time per step. Every workload's
 µs, GB/s and fraction of the 8 TB/s HBM peak are under "configs"; workload
 2 is reported in µs per decode chain (eager launches and graph replay).
+Beside each streaming kernel, `copy_us` is the library's own streaming copy
+of the same bytes (half read, half written) and `of_copy` the kernel's
+fraction of that rate: the practical ceiling at that transfer size, which
+stays well under 8 TB/s for transfers of tens of MB.
 
 Timing: each workload keeps several input sets whose total exceeds 640 MB,
 more than twice the 256 MB Infinity Cache, and steps rotate through them, so
@@ -204,14 +208,43 @@ def weights(torch, cols):
 
 
 def calibration(be, torch, timer):
-    """A plain device-to-device copy of 256 MiB (the runtime's copy kernel),
-    read + write bytes over time: the practical streaming ceiling."""
+    """A plain device-to-device copy of 256 MiB by the runtime's own copy
+    kernel (the PMC calibration reads its counters), read + write bytes over
+    time."""
     n = 64 * 2**20  # floats
     pairs = [(torch.empty(n, device="cuda"), torch.empty(n, device="cuda")) for _ in range(3)]
     for a, b in pairs:
         a.normal_()
-    ms = timer.eager([lambda p=p: be.copy(p[1], p[0]) for p in pairs])
-    return {"workload": "device-to-device copy, 256 MiB", "step": report("copy", 2 * 4 * n, ms)}
+    ms = timer.eager([lambda p=p: p[1].copy_(p[0]) for p in pairs])
+    return {"workload": "device-to-device copy, 256 MiB (runtime memcpy)", "step": report("copy", 2 * 4 * n, ms)}
+
+
+_CEILING_MS = {}
+
+
+def copy_ceiling_ms(be, torch, timer, nbytes):
+    """ms per launch of the library's streaming copy (uocr_rocm_copy, one
+    16-byte chunk per thread, nontemporal) moving nbytes: half read, half
+    written, over rotating sets like every other timing. No kernel that
+    reads and writes that many bytes in one launch can beat it by much, so
+    it is the practical ceiling at that transfer size."""
+    if nbytes not in _CEILING_MS:
+        n = max(4, nbytes // 8)  # floats per buffer
+        _CEILING_MS[nbytes] = time_kernel(timer, lambda: (torch.empty(n, device="cuda").normal_(),
+                                                          torch.empty(n, device="cuda")),
+                                          lambda s: be.copy(s[1], s[0]))
+    return _CEILING_MS[nbytes]
+
+
+def add_copy_ceilings(be, torch, timer, configs):
+    """Beside every streaming kernel of workloads 1 and 3-6: the copy of the
+    same bytes (`copy_us`) and the kernel's fraction of its rate (`of_copy`)."""
+    for c in ("1", "3", "4", "5", "6"):
+        for k in configs.get(c, {}).get("kernels", {}).values():
+            if k.get("bytes", 0) >= 2**20:
+                ms = copy_ceiling_ms(be, torch, timer, k["bytes"])
+                k["copy_us"] = round(ms * 1e3, 3)
+                k["of_copy"] = round(ms * 1e3 / k["us"], 3)
 
 
 def config1(be, torch, timer):
@@ -747,6 +780,11 @@ def main():
         torch.cuda.empty_cache()
         print(f"[bench] workload {c}: {json.dumps(configs[c]['step'])} ({time.time() - t0:.1f} s)", file=sys.stderr,
               flush=True)
+
+    t0 = time.time()
+    add_copy_ceilings(be, torch, timer, configs)
+    torch.cuda.empty_cache()
+    print(f"[bench] copy ceilings at {len(_CEILING_MS)} sizes ({time.time() - t0:.1f} s)", file=sys.stderr, flush=True)
 
     head = configs.get("5")
     line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

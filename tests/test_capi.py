@@ -141,6 +141,16 @@ def test_step_op_errors(backend):
              detail="capacity")
 
 
+def test_copy_errors(backend):
+    _invalid(backend, "uocr_rocm_copy", None, FAKE, FAKE + 64, -1, detail="n")
+    _invalid(backend, "uocr_rocm_copy", None, FAKE, None, 16, detail="null")
+    _invalid(backend, "uocr_rocm_copy", None, FAKE, FAKE + 32, 16, detail="overlap")
+    _invalid(backend, "uocr_rocm_copy", None, FAKE + 32, FAKE, 16, detail="overlap")
+    _invalid(backend, "uocr_rocm_copy", None, FAKE, FAKE + 64, 1 << 40, detail="too large")
+    # the same buffer on both sides is a copy that changes nothing: no launch
+    assert backend.lib().uocr_rocm_copy(None, FAKE, FAKE, 16) == 0
+
+
 def test_fused_step_op_errors(backend):
     rope = (None, FAKE, FAKE, FAKE, FAKE, FAKE)
     _invalid(backend, "uocr_rocm_attend_rope_kv_step", *rope, 2, 7, None, 1.0, FAKE, FAKE, 3, None, 0, FAKE, 64,

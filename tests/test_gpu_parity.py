@@ -195,6 +195,24 @@ def test_flat_ops_across_workgroup_size_switch(backend, chunks, tail):
     assert np.array_equal(host_f32(a), oracle.add(x32, y32)), f"add_inplace n={n32}"
 
 
+@pytest.mark.parametrize("n,offset", [(1, 0), (3, 0), (4097, 0), (4099, 1), (2_097_152, 0), (2_097_155, 0),
+                                      (4_194_304 + 7, 0), (1_000_003, 3)])
+def test_copy_bitwise(backend, n, offset):
+    """copy moves every bit (NaN payloads and signed zeros included) across
+    the vector and scalar paths, ragged tails and the workgroup-size switch;
+    `offset` elements past a 16-byte boundary takes the scalar path."""
+    g = np.random.default_rng(n)
+    bits = g.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)
+    src = torch.empty(n + 8, device="cuda")
+    dst = torch.full((n + 8,), 7.0, device="cuda")
+    sv, dv = src[offset:offset + n], dst[offset:offset + n]
+    sv.copy_(torch.from_numpy(bits.view(np.float32)).cuda())
+    backend.copy(dv, sv)
+    got = dst.cpu().numpy()
+    assert np.array_equal(got[offset:offset + n].view(np.uint32), bits), f"copy n={n} offset={offset}"
+    assert np.all(got[:offset] == 7.0) and np.all(got[offset + n:] == 7.0), "copy wrote outside dst"
+
+
 @pytest.mark.parametrize("rows,ffn", [(2978, 1408), (2980, 1408), (40330, 13)])
 def test_bf16_swiglu_across_workgroup_size_switch(backend, rows, ffn):
     inp = bf16(normal(rows + ffn, (rows, 2 * ffn), 2.0))
