@@ -7,8 +7,8 @@
 // registers on the softmax's read, so they cross HBM once instead of twice.
 //
 // softmax_rows, layout as the norms (norm.hip): the row in registers, 64-
-// chunk groups, WPR waves per row (4 below kFewRows rows). Three steps over
-// the registers: the row max (an exact fold), e = exp(v - max) and its sum
+// chunk groups, WPR waves per row (about two groups per wave). Three steps
+// over the registers: the row max (an exact fold), e = exp(v - max) and its sum
 // (folded in group order, so the result is bitwise independent of WPR and of
 // the row count), then v = e / sum. Rows wider than the registers hold take
 // softmax_rows_wide (one workgroup per row, three reads of the row).
@@ -47,9 +47,21 @@ struct RowMask {
   __device__ __forceinline__ int64_t data_row(int64_t r) const { return (r % batch) * mask_rows + r / batch; }
 };
 
+// Waves per row (WPR) and workgroup size: one wave per row in 4-wave
+// workgroups for rows of 1-3 chunk groups, else about two groups per wave
+// (WPR = 2, 4, 8) with one row per workgroup. Measured on [10 x rows, cols]
+// fp32 scores (640 MB) against one wave per row (4 waves at a mask): 1024
+// columns 1-3% faster, 2048 6% (unmasked), 4096 13% (unmasked) and 4% (the
+// one-pass masked kernel), 8192 masked 10% faster and unmasked 5% slower.
+template <int WPR>
+constexpr int softmax_block() {
+  return WPR == 1 ? kBlock : WPR * kWave;
+}
+
 template <int VW, int WPR, int VPL, bool kMask>
-__global__ __launch_bounds__(kBlock) void softmax_rows_k(float* __restrict__ x, int64_t rows, int cols, RowMask rm) {
-  constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
+__global__ __launch_bounds__(softmax_block<WPR>()) void softmax_rows_k(float* __restrict__ x, int64_t rows, int cols,
+                                                                      RowMask rm) {
+  constexpr int kRowsPerBlock = softmax_block<WPR>() / kWave / WPR;
   __shared__ float red[kRowsPerBlock][kMaxGroups];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
@@ -162,14 +174,28 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_wide(float* x, int64_t co
 
 template <int VW, int WPR, bool kMask>
 void launch_softmax_rows(int vpl, hipStream_t s, float* x, int64_t rows, int cols, const RowMask& rm) {
-  constexpr int kRowsPerBlock = kWavesPerBlock / WPR;
+  constexpr int kThreads = softmax_block<WPR>();
+  constexpr int kRowsPerBlock = kThreads / kWave / WPR;
   const unsigned blocks = static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
   switch (vpl) {
-    case 1: softmax_rows_k<VW, WPR, 1, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
-    case 2: softmax_rows_k<VW, WPR, 2, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
-    case 4: softmax_rows_k<VW, WPR, 4, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
-    case 8: softmax_rows_k<VW, WPR, 8, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
-    default: softmax_rows_k<VW, WPR, 16, kMask><<<blocks, kBlock, 0, s>>>(x, rows, cols, rm); break;
+    case 1: softmax_rows_k<VW, WPR, 1, kMask><<<blocks, kThreads, 0, s>>>(x, rows, cols, rm); break;
+    case 2: softmax_rows_k<VW, WPR, 2, kMask><<<blocks, kThreads, 0, s>>>(x, rows, cols, rm); break;
+    case 4: softmax_rows_k<VW, WPR, 4, kMask><<<blocks, kThreads, 0, s>>>(x, rows, cols, rm); break;
+    case 8: softmax_rows_k<VW, WPR, 8, kMask><<<blocks, kThreads, 0, s>>>(x, rows, cols, rm); break;
+    default: softmax_rows_k<VW, WPR, 16, kMask><<<blocks, kThreads, 0, s>>>(x, rows, cols, rm); break;
+  }
+}
+
+template <int VW, bool kMask>
+void launch_softmax_wpr(int64_t groups, hipStream_t s, float* x, int64_t rows, int cols, const RowMask& rm) {
+  if (groups < 4) {
+    launch_softmax_rows<VW, 1, kMask>(vpl_bucket(groups), s, x, rows, cols, rm);
+  } else if (groups < 8) {
+    launch_softmax_rows<VW, 2, kMask>(vpl_bucket((groups + 1) / 2), s, x, rows, cols, rm);
+  } else if (groups < 16) {
+    launch_softmax_rows<VW, 4, kMask>(vpl_bucket((groups + 3) / 4), s, x, rows, cols, rm);
+  } else {
+    launch_softmax_rows<VW, 8, kMask>(vpl_bucket((groups + 7) / 8), s, x, rows, cols, rm);
   }
 }
 
@@ -186,18 +212,11 @@ int softmax_entry(const char* what, void* stream, float* x, int64_t rows, int64_
     softmax_rows_wide<kMask><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, cols, rm);
     return check_launch(what);
   }
-  // With a mask each lane holds twice the loads (scores and mask), so rows
-  // of 4+ groups spread over 4 waves to keep the registers, and the waves
-  // per SIMD, of the unmasked kernel.
-  const bool spread = groups > 16 || ((rows < kFewRows || kMask) && groups >= 4);
-  const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
   const int c32 = static_cast<int>(cols);
   if (vec) {
-    if (spread) launch_softmax_rows<4, 4, kMask>(vpl, s, x, rows, c32, rm);
-    else launch_softmax_rows<4, 1, kMask>(vpl, s, x, rows, c32, rm);
+    launch_softmax_wpr<4, kMask>(groups, s, x, rows, c32, rm);
   } else {
-    if (spread) launch_softmax_rows<1, 4, kMask>(vpl, s, x, rows, c32, rm);
-    else launch_softmax_rows<1, 1, kMask>(vpl, s, x, rows, c32, rm);
+    launch_softmax_wpr<1, kMask>(groups, s, x, rows, c32, rm);
   }
   return check_launch(what);
 }
