@@ -799,7 +799,7 @@ def main():
                        "q_heads": 16, "kv_heads": 4, "head_dim": 128, "bytes_per_step": head["step"]["bytes"]},
             "roofline": {"bound": "hbm", "kernel": "add_rms_norm_bf16 [8192, 2048]", "achieved": dom["gbps"],
                          "peak": PEAK_GBPS, "unit": "GB/s", "frac": dom["frac"],
-                         "traffic": committed_traffic("norm_rows<unsigned short, 8, 1, 4, (Norm)1>", 8192 * 64),
+                         "traffic": committed_traffic("norm_rows<unsigned short, 8, 1, 4, (Norm)1", 8192 * 64),
                          "algorithmic_bytes": dom["bytes"]},
         })
     if not args.no_cpu and head is not None:

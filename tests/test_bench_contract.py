@@ -90,7 +90,7 @@ def test_pmc_summary_scales_by_the_calibration_copy(tmp_path):
 
 
 def test_committed_traffic_reads_the_profile():
-    got = bench.committed_traffic("norm_rows<unsigned short, 8, 1, 4, (Norm)1>", 8192 * 64)
+    got = bench.committed_traffic("norm_rows<unsigned short, 8, 1, 4, (Norm)1", 8192 * 64)
     if not os.path.exists(bench.TRAFFIC_FILE):
         pytest.skip("no committed PMC summary")
     assert got is not None and abs(got - 134_225_920) / 134_225_920 < 0.01
