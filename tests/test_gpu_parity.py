@@ -262,6 +262,38 @@ def test_misaligned_views_take_scalar_path(backend):
     assert_bf16_close(host_bits(gv), oracle.gelu_erf(oracle.bf16_to_f32(x[0])), "gelu misaligned")
 
 
+def test_bf16_gelu_every_input(backend):
+    """Every finite bf16 value through gelu_erf_bf16, element by element:
+    above -4.6 the oracle's fp32 GELU rounded to bf16, or its neighbour;
+    from -5.5 to -4.6, where the reference's own 1 + erf(x / sqrt 2)
+    cancels, the exact GELU (fp64) rounded to bf16, or its neighbour; below
+    -5.5 x * 0, which is the reference's result below -5.5426 (between, the
+    reference's is fp32 noise under 2e-7)."""
+    from scipy.special import ndtr
+
+    def ulps(a_bits, b_bits):
+        a, b = a_bits.astype(np.int64), b_bits.astype(np.int64)
+        oa = np.where(a & 0x8000, -(a & 0x7FFF), a & 0x7FFF)
+        ob = np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+        return np.abs(oa - ob)
+
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    x = oracle.bf16_to_f32(bits)
+    keep = np.isfinite(x)
+    bits, x = bits[keep], x[keep]
+    d = dev_bf16(bits)
+    backend.gelu_erf(d)
+    got = host_bits(d)
+    ref = bf16(oracle.gelu_erf(x))
+    exact = bf16((x.astype(np.float64) * ndtr(x.astype(np.float64))).astype(np.float32))
+    hi, mid, lo = x > -4.6, (x <= -4.6) & (x >= -5.5), x < -5.5
+    assert ulps(got[hi], ref[hi]).max() <= 1, "gelu_erf_bf16 above -4.6"
+    assert ulps(got[mid], exact[mid]).max() <= 1, "gelu_erf_bf16 in [-5.5, -4.6]"
+    assert np.all(got[lo] == 0x8000), "gelu_erf_bf16 below -5.5 is -0"
+    far = x < -5.5426
+    assert np.array_equal(got[far], ref[far]), "gelu_erf_bf16 below -5.5426"
+
+
 def test_flat_ops_ragged_tail(backend):
     for n in [1, 7, 9, 1001, 4099]:
         x = bf16(normal(n, n, 3.0))
