@@ -36,14 +36,15 @@ namespace {
 // chunks per thread for these streaming shapes (more waves in flight).
 constexpr int kUnroll = 1;
 
-// Workgroup size by grid size. A grid with more waves than one resident
-// round (8 per SIMD on 1024 SIMDs) runs as one-wave workgroups, which refill
-// a SIMD as soon as any wave retires: 3-5% faster from 33 to 134 MB. A grid
-// that fits in one round keeps four-wave workgroups, which dispatch faster:
-// one-wave groups were 14% slower at 17 MB.
+// Workgroup size by grid size. A grid of more than 1.25 resident rounds of
+// waves (8 per SIMD on 1024 SIMDs) runs as one-wave workgroups, which refill
+// a SIMD as soon as any wave retires: 3-5% faster from 23 to 134 MB. A grid
+// that fits in about one round keeps four-wave workgroups, which dispatch
+// faster: one-wave groups were 14% slower at 17 MB (one round exactly, and
+// a copy of one round plus 256 threads).
 constexpr int64_t kResidentThreads = int64_t{256} * 4 * 8 * kWave;
 
-inline bool one_wave_groups(int64_t threads) { return threads > kResidentThreads; }
+inline bool one_wave_groups(int64_t threads) { return threads > kResidentThreads + kResidentThreads / 4; }
 
 // GELU(x) = x Phi(x), Phi the standard normal CDF, from the upper tail
 // Q(t) = Phi(-t) = 2^P(t): Phi(x) = 1 - Q(|x|) for x >= 0 and Q(|x|) for
@@ -204,34 +205,49 @@ int launch_flat(const char* what, void* stream, T* x, const T* y, int64_t n) {
 
 // ---- copy -----------------------------------------------------------------------
 
-// dst = src over n elements, VW per chunk; the last n % VW elements (VW > 1
+// dst = src over n elements, VW per chunk, UNROLL chunks per thread (chunk
+// i and i + the grid's thread count); the last n % VW elements (VW > 1
 // only) by the first threads of block 0.
-template <int VW, int TB>
+template <int VW, int TB, int UNROLL>
 __global__ __launch_bounds__(TB) void copy_flat(float* __restrict__ dst, const float* __restrict__ src, int64_t n) {
   const int64_t nvec = n / VW;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * TB + threadIdx.x;
-  if (i < nvec) {
-    Chunk<float, VW> c;
-    c.load(src + i * VW);
-    c.store(dst + i * VW);
+  const int64_t threads = static_cast<int64_t>(gridDim.x) * TB;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * TB + threadIdx.x;
+  Chunk<float, VW> c[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t i = i0 + u * threads;
+    if (i < nvec) c[u].load(src + i * VW);
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t i = i0 + u * threads;
+    if (i < nvec) c[u].store(dst + i * VW);
   }
   if constexpr (VW > 1) {
     const int64_t rest = n - nvec * VW;
     if (blockIdx.x == 0 && threadIdx.x < rest) {
-      Chunk<float, 1> c;
-      c.load(src + nvec * VW + threadIdx.x);
-      c.store(dst + nvec * VW + threadIdx.x);
+      Chunk<float, 1> t;
+      t.load(src + nvec * VW + threadIdx.x);
+      t.store(dst + nvec * VW + threadIdx.x);
     }
   }
 }
 
+// A grid just over one resident round would run its last workgroups as a
+// second round of their own (a 16.8 MB copy of 524,544 chunks took 4.48 us
+// against 3.84 us for 524,288), so from one to 1.25 rounds each thread takes
+// two chunks and the grid fits in one round.
 template <int VW>
 void launch_copy_tb(hipStream_t s, float* dst, const float* src, int64_t n) {
   const int64_t nvec = n / VW > 0 ? n / VW : 1;
+  auto blocks = [](int64_t threads, int64_t tb) { return static_cast<unsigned>((threads + tb - 1) / tb); };
   if (one_wave_groups(nvec)) {
-    copy_flat<VW, kWave><<<static_cast<unsigned>((nvec + kWave - 1) / kWave), kWave, 0, s>>>(dst, src, n);
+    copy_flat<VW, kWave, 1><<<blocks(nvec, kWave), kWave, 0, s>>>(dst, src, n);
+  } else if (nvec > kResidentThreads) {
+    copy_flat<VW, kBlock, 2><<<blocks((nvec + 1) / 2, kBlock), kBlock, 0, s>>>(dst, src, n);
   } else {
-    copy_flat<VW, kBlock><<<static_cast<unsigned>((nvec + kBlock - 1) / kBlock), kBlock, 0, s>>>(dst, src, n);
+    copy_flat<VW, kBlock, 1><<<blocks(nvec, kBlock), kBlock, 0, s>>>(dst, src, n);
   }
 }
 

@@ -61,7 +61,9 @@ def unfused_h(backend, x, delta, w_norm, eps=1e-6):
 @pytest.mark.parametrize("k,n,with_delta,with_norm,with_bias", [
     (1280, 3840, True, True, False), (1280, 1280, False, True, True), (2048, 2048, True, True, True),
     (896, 1280, True, False, False), (1280, 16384, True, True, False), (8, 5, False, False, True),
-    (2048, 20000, True, True, True), (1024, 77, False, True, False)])
+    (2048, 20000, True, True, True), (1024, 77, False, True, False),
+    # more row pairs than the grid's waves: waves walk the rows grid-stride
+    (256, 60001, True, True, True)])
 def test_add_rms_norm_gemv_matches_unfused(backend, k, n, with_delta, with_norm, with_bias):
     x = dev_f32(normal(300 + k, k))
     delta = dev_f32(normal(301, k)) if with_delta else None

@@ -168,10 +168,10 @@ def test_bf16_swiglu_shapes(backend, rows, ffn):
     assert_bf16_close(host_bits(out), oracle.swiglu(oracle.bf16_to_f32(inp)), f"swiglu_bf16 {rows}x{ffn}")
 
 
-# Elementwise grids switch from four-wave to one-wave workgroups past 524288
-# threads (one resident round of waves): sizes at, just past and well past
+# Elementwise grids switch from four-wave to one-wave workgroups past 655360
+# threads (1.25 resident rounds of waves): sizes at, just past and well past
 # that boundary, with ragged tails, for every flat op and dtype.
-@pytest.mark.parametrize("chunks,tail", [(524288, 0), (524289, 3), (1 << 20, 7)])
+@pytest.mark.parametrize("chunks,tail", [(655360, 0), (655361, 3), (1 << 20, 7)])
 def test_flat_ops_across_workgroup_size_switch(backend, chunks, tail):
     n = 8 * chunks + tail
     x = normal(chunks + tail, n, 2.0)
@@ -195,12 +195,14 @@ def test_flat_ops_across_workgroup_size_switch(backend, chunks, tail):
     assert np.array_equal(host_f32(a), oracle.add(x32, y32)), f"add_inplace n={n32}"
 
 
-@pytest.mark.parametrize("n,offset", [(1, 0), (3, 0), (4097, 0), (4099, 1), (2_097_152, 0), (2_097_155, 0),
-                                      (4_194_304 + 7, 0), (1_000_003, 3)])
+@pytest.mark.parametrize("n,offset", [(1, 0), (3, 0), (4097, 0), (4099, 1), (2_097_152, 0), (2_097_163, 0),
+                                      (2_621_440, 0), (2_621_447, 0), (4_194_304 + 7, 0), (1_000_003, 3),
+                                      (600_001, 1)])
 def test_copy_bitwise(backend, n, offset):
     """copy moves every bit (NaN payloads and signed zeros included) across
-    the vector and scalar paths, ragged tails and the workgroup-size switch;
-    `offset` elements past a 16-byte boundary takes the scalar path."""
+    the vector and scalar paths, ragged tails, the two-chunks-per-thread grids
+    (just over one resident round) and the workgroup-size switch; `offset`
+    elements past a 16-byte boundary takes the scalar path."""
     g = np.random.default_rng(n)
     bits = g.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)
     src = torch.empty(n + 8, device="cuda")
@@ -213,7 +215,7 @@ def test_copy_bitwise(backend, n, offset):
     assert np.all(got[:offset] == 7.0) and np.all(got[offset + n:] == 7.0), "copy wrote outside dst"
 
 
-@pytest.mark.parametrize("rows,ffn", [(2978, 1408), (2980, 1408), (40330, 13)])
+@pytest.mark.parametrize("rows,ffn", [(3723, 1408), (3724, 1408), (50413, 13)])
 def test_bf16_swiglu_across_workgroup_size_switch(backend, rows, ffn):
     inp = bf16(normal(rows + ffn, (rows, 2 * ffn), 2.0))
     out = torch.empty(rows, ffn, dtype=torch.bfloat16, device="cuda")

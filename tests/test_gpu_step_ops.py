@@ -138,7 +138,9 @@ def test_scale_mask_softmax_matches_the_pair(backend, batch, rows, cols, masked)
 
 @pytest.mark.parametrize("k,n,with_bias", [(1280, 1280, True), (1280, 3840, False), (896, 1280, False),
                                            (2048, 20000, True), (4096, 300, True), (12288, 64, False),
-                                           (100, 33, True), (8, 5, False)])
+                                           (100, 33, True), (8, 5, False),
+                                           # more row pairs than the grid's waves: grid-stride rows
+                                           (1280, 60001, True)])
 def test_gemv_bf16(backend, k, n, with_bias):
     x = normal(150 + k, k)
     wb = bf16(0.05 * normal(151, (n, k)))
