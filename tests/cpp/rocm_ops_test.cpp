@@ -3,13 +3,15 @@
 // reference's tests/cuda_ops_test.cpp: the same N(0,1) inputs from
 // std::mt19937(5), the same relative-error metric, the same tolerances for
 // the fp32 ops, plus the bf16-activation ops at 2 bf16 ulp, the fused ops,
-// a captured decode step replayed at three StepStates, and the error
-// convention. Exits 77 (skip) without a HIP device.
+// a captured decode step replayed at three StepStates, one decoder layer's
+// fused step against its unfused ops, and the error convention. Exits 77
+// (skip) without a HIP device.
 
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <cstring>
 #include <functional>
 #include <random>
 #include <stdexcept>
@@ -89,6 +91,11 @@ int max_ulp(const std::vector<std::uint16_t>& got, const std::vector<float>& wan
     worst = std::max(worst, std::abs(ordered(got[i]) - ordered(ro::f32_to_bf16(want[i]))));
   }
   return worst;
+}
+
+// Bitwise equality (so -0 differs from +0, and a NaN equals itself).
+bool same_bits(const std::vector<float>& a, const std::vector<float>& b) {
+  return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * sizeof(float)) == 0;
 }
 
 void expect(const char* what, double err, double tol) {
@@ -307,6 +314,127 @@ void decode_graph(const ro::Context& ctx) {
   }
 }
 
+void fused_decode_layer(const ro::Context& ctx) {
+  // One dense decoder layer's decode step (the layer loop of
+  // src/model/cuda/cuda_decoder.cpp:265-279 at rows = 1): the unfused op
+  // sequence and the fused one (norm-prologue GEMVs, rope + appends +
+  // attention in one op, SwiGLU epilogue) each captured once and replayed at
+  // growing positions. Every replay's outputs must agree bitwise; the fused
+  // output is also held to the oracle's layer, within the positions the
+  // cache holds.
+  const std::int64_t hidden = 512, heads = 4, hd = 64, width = heads * hd, ffn = 384, cap = 512;
+  const float eps = 1e-6f, scale = 0.125f;
+  const auto inv = rope_inv(hd / 2, 1e4);
+  const auto wqkv = bf16_rounded(random(3 * width * hidden, 0.05f)), wo = bf16_rounded(random(hidden * width, 0.05f)),
+             wg = bf16_rounded(random(ffn * hidden, 0.05f)), wu = bf16_rounded(random(ffn * hidden, 0.05f)),
+             wd = bf16_rounded(random(hidden * ffn, 0.05f));
+  auto n1 = random(hidden, 0.02f), n2 = random(hidden, 0.02f);
+  for (float& v : n1) v += 1.0f;
+  for (float& v : n2) v += 1.0f;
+  auto dinv = up(ctx, inv), dn1 = up(ctx, n1), dn2 = up(ctx, n2);
+  auto dqkv = up(ctx, wqkv, ro::DType::kBF16), dwo = up(ctx, wo, ro::DType::kBF16),
+       dwg = up(ctx, wg, ro::DType::kBF16), dwu = up(ctx, wu, ro::DType::kBF16), dwd = up(ctx, wd, ro::DType::kBF16);
+  struct Buffers {
+    ro::Array x, delta, x1, x2, h, qkv, attn, o, g, u, act, out, kc, vc, scratch, state;
+  };
+  auto buffers = [&] {
+    auto f = [&](std::int64_t n) { return ro::Array(ctx, ro::DType::kF32, n); };
+    Buffers b{f(hidden), f(hidden), f(hidden), f(hidden), f(hidden), f(3 * width), f(width), f(hidden),
+              f(ffn),    f(ffn),    f(ffn),    f(hidden), f(cap * width), f(cap * width),
+              f(ro::attend_scratch_floats(heads, hd, cap)), ro::Array(ctx, ro::DType::kI64, 5)};
+    b.kc.zero();
+    b.vc.zero();
+    b.g.zero();
+    b.act.zero();
+    return b;
+  };
+  Buffers A = buffers(), B = buffers();
+  const auto st = [](const Buffers& b) { return reinterpret_cast<const ro::StepState*>(b.state.data()); };
+  ctx.synchronize();
+  ctx.begin_capture();
+  {
+    float *q = A.qkv.f32(), *k = q + width, *v = k + width;
+    ro::copy(ctx, A.x1.f32(), A.x.f32(), hidden);
+    ro::add_rms_norm(ctx, A.x1.f32(), A.delta.f32(), dn1.f32(), A.h.f32(), 1, hidden, eps);
+    ro::gemv_bf16(ctx, A.h.f32(), hidden, dqkv.bf16(), 3 * width, nullptr, A.qkv.f32());
+    ro::rope_qk_step(ctx, q, heads, k, heads, hd, st(A), dinv.f32(), hd / 2, nullptr, 0);
+    ro::append_step(ctx, A.kc.f32(), k, width, st(A), cap);
+    ro::append_step(ctx, A.vc.f32(), v, width, st(A), cap);
+    ro::attend_step(ctx, q, A.kc.f32(), A.vc.f32(), heads, hd, nullptr, scale, st(A), A.scratch.f32(), cap,
+                    A.attn.f32());
+    ro::gemv_bf16(ctx, A.attn.f32(), width, dwo.bf16(), hidden, nullptr, A.o.f32());
+    ro::copy(ctx, A.x2.f32(), A.x1.f32(), hidden);
+    ro::add_rms_norm(ctx, A.x2.f32(), A.o.f32(), dn2.f32(), A.h.f32(), 1, hidden, eps);
+    ro::gemv_bf16(ctx, A.h.f32(), hidden, dwg.bf16(), ffn, nullptr, A.g.f32());
+    ro::gemv_bf16(ctx, A.h.f32(), hidden, dwu.bf16(), ffn, nullptr, A.u.f32());
+    ro::silu_mul(ctx, A.g.f32(), A.u.f32(), ffn);
+    ro::gemv_bf16(ctx, A.g.f32(), ffn, dwd.bf16(), hidden, nullptr, A.out.f32());
+  }
+  auto unfused = ctx.end_capture();
+  ctx.begin_capture();
+  {
+    float *q = B.qkv.f32(), *k = q + width, *v = k + width;
+    ro::add_rms_norm_gemv_bf16(ctx, B.x.f32(), B.delta.f32(), B.x1.f32(), dn1.f32(), eps, nullptr, hidden,
+                               dqkv.bf16(), 3 * width, nullptr, B.qkv.f32());
+    ro::attend_rope_kv_step(ctx, q, k, v, B.kc.f32(), B.vc.f32(), heads, hd, nullptr, scale, st(B), dinv.f32(),
+                            hd / 2, nullptr, 0, B.scratch.f32(), cap, B.attn.f32());
+    ro::gemv_bf16(ctx, B.attn.f32(), width, dwo.bf16(), hidden, nullptr, B.o.f32());
+    ro::add_rms_norm_swiglu_gemv_bf16(ctx, B.x1.f32(), B.o.f32(), B.x2.f32(), dn2.f32(), eps, nullptr, hidden,
+                                      dwg.bf16(), dwu.bf16(), ffn, B.act.f32());
+    ro::gemv_bf16(ctx, B.act.f32(), ffn, dwd.bf16(), hidden, nullptr, B.out.f32());
+  }
+  auto fused = ctx.end_capture();
+  // The oracle's layer, with the GEMV inputs rounded to bf16 as the kernels
+  // take them, and its own caches.
+  std::vector<float> kc(cap * width, 0.0f), vc(cap * width, 0.0f);
+  auto linear = [](const std::vector<float>& x, const std::vector<float>& w, std::int64_t n) {
+    std::vector<float> y(n);
+    orc_linear(bf16_rounded(x).data(), 1, static_cast<std::int64_t>(x.size()), w.data(), n, nullptr, y.data());
+    return y;
+  };
+  for (const std::int64_t pos : {0, 1, 37, 200, 511, 600}) {
+    const auto xv = random(hidden), dv = random(hidden);
+    const std::int64_t s[5] = {0, pos, pos, 0, -1};
+    for (Buffers* b : {&A, &B}) {
+      b->x.upload(xv.data(), hidden);
+      b->delta.upload(dv.data(), hidden);
+      b->state.upload(s, 5);
+    }
+    unfused->launch();
+    fused->launch();
+    ctx.synchronize();
+    const auto out = B.out.download(), x2 = B.x2.download();
+    require(same_bits(A.out.download(), out) && same_bits(A.x2.download(), x2),
+            "fused layer output and residual are bitwise unfused's");
+    require(same_bits(A.kc.download(), B.kc.download()) && same_bits(A.vc.download(), B.vc.download()),
+            "fused layer caches");
+    require(same_bits(A.g.download(), B.act.download()), "fused SwiGLU epilogue");
+    if (pos >= cap) continue;  // no append; the attention's keys past the cache are not the oracle's
+    auto x1 = xv;
+    std::vector<float> h(hidden);
+    orc_add_rms_norm(x1.data(), dv.data(), n1.data(), h.data(), 1, hidden, eps);
+    auto qkv = linear(h, wqkv, 3 * width);
+    orc_rope_apply(qkv.data(), 1, 2 * heads, hd, nullptr, nullptr, inv.data(), hd / 2, nullptr, 0, 0, pos, 0);
+    std::copy(qkv.begin() + width, qkv.begin() + 2 * width, kc.begin() + pos * width);
+    std::copy(qkv.begin() + 2 * width, qkv.end(), vc.begin() + pos * width);
+    std::vector<float> attn(width);
+    orc_attention_one(qkv.data(), kc.data(), vc.data(), pos + 1, width, heads, hd, nullptr, scale, attn.data());
+    const auto o = linear(attn, wo, hidden);
+    auto wx2 = x1;
+    orc_add_rms_norm(wx2.data(), o.data(), n2.data(), h.data(), 1, hidden, eps);
+    auto g = linear(h, wg, ffn);
+    const auto u = linear(h, wu, ffn);
+    orc_silu(g.data(), ffn);
+    orc_mul_into(g.data(), u.data(), ffn);
+    const auto want = linear(g, wd, hidden);
+    char what[64];
+    std::snprintf(what, sizeof what, "fused layer at pos %lld", static_cast<long long>(pos));
+    expect(what, max_rel(out, want), 1e-3);
+    std::snprintf(what, sizeof what, "fused layer x2 at pos %lld", static_cast<long long>(pos));
+    expect(what, max_rel(x2, wx2), 1e-3);
+  }
+}
+
 void step_ops(const ro::Context& ctx) {
   {  // softmax with a masked entry and a fully masked row
     const std::int64_t rows = 5, cols = 300;
@@ -390,6 +518,7 @@ int main() {
     bf16_ops(ctx);
     decode_graph(ctx);
     step_ops(ctx);
+    fused_decode_layer(ctx);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());
