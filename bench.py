@@ -535,7 +535,7 @@ def config7(be, torch, timer):
 
 # ---- the CPU baseline (the reference's CPU path, restated in the oracle) ------------------------------
 
-def _cpu_median(fn, budget_s, max_runs=20):
+def _cpu_median(fn, budget_s, max_runs=200):
     """Median seconds per call of fn over at least 3 and at most max_runs
     calls, or as many as budget_s allows, after one warm-up call."""
     fn()

@@ -4,7 +4,8 @@
 // fp32 and bf16 activations, fp32 arithmetic.
 //
 // Flat ops (gelu_erf, silu_mul, add_inplace, copy) stream 128-bit chunks,
-// one per thread, over a grid that covers the whole tensor in one pass. A
+// one per thread, over a grid that covers the whole tensor in one pass (one
+// launch per 2^28 chunks, for tensors past the work-items of a dispatch). A
 // ragged tail shorter than one chunk, or any buffer not 16-byte aligned,
 // takes the scalar path.
 //
@@ -45,6 +46,10 @@ constexpr int kUnroll = 1;
 constexpr int64_t kResidentThreads = int64_t{256} * 4 * 8 * kWave;
 
 inline bool one_wave_groups(int64_t threads) { return threads > kResidentThreads + kResidentThreads / 4; }
+
+// Element counts of the flat ops stay below 2^56, so byte offsets and the
+// overlap checks never overflow (any tensor that fits in memory passes).
+constexpr int64_t kMaxElems = int64_t{1} << 56;
 
 // GELU(x) = x Phi(x), Phi the standard normal CDF, from the upper tail
 // Q(t) = Phi(-t) = 2^P(t): Phi(x) = 1 - Q(|x|) for x >= 0 and Q(|x|) for
@@ -189,17 +194,23 @@ int launch_flat(const char* what, void* stream, T* x, const T* y, int64_t n) {
   UOCR_REQUIRE(n >= 0, what, "n must be >= 0");
   if (n == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(x != nullptr && (unary(kOp) || y != nullptr), what, "null pointer");
+  UOCR_REQUIRE(n < kMaxElems, what, "n too large");
   constexpr int kV = kVec<T>;
   const bool vec = aligned16(x) && (unary(kOp) || aligned16(y));
-  const int64_t nvec = vec ? n / kV : n;
-  UOCR_REQUIRE((nvec + kWave * kUnroll - 1) / (kWave * kUnroll) < (int64_t{1} << 31), what, "n too large");
+  const int vw = vec ? kV : 1;
+  const int64_t nvec = n / vw;
   const hipStream_t s = as_stream(stream);
   clear_launch_error();
-  if (vec) {
-    launch_flat_tb<kOp, T, kV>(s, x, y, n, nvec);
-  } else {
-    launch_flat_tb<kOp, T, 1>(s, x, y, n, nvec);
-  }
+  // Pieces of kPieceChunks chunks; the last piece takes the ragged tail.
+  for_each_piece(nvec, kPieceChunks, [&](int64_t c0, int64_t cn) {
+    const int64_t e0 = c0 * vw, en = c0 + cn == nvec ? n - e0 : cn * vw;
+    const T* yp = unary(kOp) ? y : y + e0;
+    if (vec) {
+      launch_flat_tb<kOp, T, kV>(s, x + e0, yp, en, cn);
+    } else {
+      launch_flat_tb<kOp, T, 1>(s, x + e0, yp, en, cn);
+    }
+  });
   return check_launch(what);
 }
 
@@ -301,18 +312,22 @@ int launch_swiglu(const char* what, void* stream, const T* in, T* out, int64_t r
   constexpr int kV = kVec<T>;
   const bool vec = ffn % kV == 0 && aligned16(in) && aligned16(out);
   const int64_t cpr = vec ? ffn / kV : ffn;
-  const int64_t total = rows * cpr;
-  UOCR_REQUIRE(total < (int64_t{1} << 32) - kBlock, what, "rows * ffn too large");
-  const uint32_t t32 = static_cast<uint32_t>(total), c32 = static_cast<uint32_t>(cpr);
+  const uint32_t c32 = static_cast<uint32_t>(cpr);
   const uint64_t magic = reciprocal_magic(c32);
   const hipStream_t s = as_stream(stream);
   const int f = static_cast<int>(ffn);
   clear_launch_error();
-  if (vec) {
-    launch_swiglu_tb<T, kV>(s, in, out, t32, c32, magic, f);
-  } else {
-    launch_swiglu_tb<T, 1>(s, in, out, t32, c32, magic, f);
-  }
+  // Row pieces of about kPieceChunks / 4 chunks (at least one row, under
+  // 2^29 chunks), so the flat chunk index of a launch stays in 32 bits.
+  const int64_t piece = cpr < kPieceChunks / 4 ? kPieceChunks / 4 / cpr : 1;
+  for_each_piece(rows, piece, [&](int64_t r0, int64_t rn) {
+    const uint32_t t32 = static_cast<uint32_t>(rn * cpr);
+    if (vec) {
+      launch_swiglu_tb<T, kV>(s, in + r0 * 2 * ffn, out + r0 * ffn, t32, c32, magic, f);
+    } else {
+      launch_swiglu_tb<T, 1>(s, in + r0 * 2 * ffn, out + r0 * ffn, t32, c32, magic, f);
+    }
+  });
   return check_launch(what);
 }
 
@@ -332,19 +347,25 @@ int uocr_rocm_copy(void* stream, float* dst, const float* src, int64_t n) {
   UOCR_REQUIRE(n >= 0, "uocr_rocm_copy", "n must be >= 0");
   if (n == 0 || dst == src) return UOCR_ROCM_OK;
   UOCR_REQUIRE(dst != nullptr && src != nullptr, "uocr_rocm_copy", "null pointer");
-  UOCR_REQUIRE((n + kWave - 1) / kWave < (int64_t{1} << 31), "uocr_rocm_copy", "n too large");
+  UOCR_REQUIRE(n < kMaxElems, "uocr_rocm_copy", "n too large");
   {
     const auto d = reinterpret_cast<uintptr_t>(dst), r = reinterpret_cast<uintptr_t>(src);
     const auto bytes = static_cast<uintptr_t>(n) * sizeof(float);
     UOCR_REQUIRE(d + bytes <= r || r + bytes <= d, "uocr_rocm_copy", "dst and src must not overlap");
   }
   const hipStream_t s = as_stream(stream);
+  const bool vec = aligned16(dst) && aligned16(src);
+  const int vw = vec ? 4 : 1;
+  const int64_t nvec = n / vw;
   clear_launch_error();
-  if (aligned16(dst) && aligned16(src)) {
-    launch_copy_tb<4>(s, dst, src, n);
-  } else {
-    launch_copy_tb<1>(s, dst, src, n);
-  }
+  for_each_piece(nvec, kPieceChunks, [&](int64_t c0, int64_t cn) {
+    const int64_t e0 = c0 * vw, en = c0 + cn == nvec ? n - e0 : cn * vw;
+    if (vec) {
+      launch_copy_tb<4>(s, dst + e0, src + e0, en);
+    } else {
+      launch_copy_tb<1>(s, dst + e0, src + e0, en);
+    }
+  });
   return check_launch("uocr_rocm_copy");
 }
 

@@ -324,6 +324,28 @@ inline unsigned blocks_for_rows(int64_t rows) {
   return static_cast<unsigned>((rows + kWavesPerBlock - 1) / kWavesPerBlock);
 }
 
+// ---- launches in pieces -----------------------------------------------------------
+// One dispatch holds at most 2^32 - 1 work-items. An op over more rows (or
+// chunks) than one launch of modest size reaches runs as consecutive
+// launches over contiguous pieces: fn(first, count) for pieces of at most
+// `piece` units covering [0, total), in order; one call with count 0 when
+// total is 0. A piece of kPieceRows rows is at most 2^28 work-items (256
+// threads per row on the widest path) and kPieceChunks 128-bit chunks 2^28
+// work-items; both are gigabytes of data, so the extra launches cost
+// nothing measurable.
+constexpr int64_t kPieceRows = int64_t{1} << 20;
+constexpr int64_t kPieceChunks = int64_t{1} << 28;
+
+template <class Fn>
+void for_each_piece(int64_t total, int64_t piece, Fn&& fn) {
+  int64_t first = 0;
+  do {
+    const int64_t count = total - first < piece ? total - first : piece;
+    fn(first, count);
+    first += count;
+  } while (first < total);
+}
+
 }  // namespace uocr_rocm
 
 #define UOCR_REQUIRE(cond, what, detail)                                  \

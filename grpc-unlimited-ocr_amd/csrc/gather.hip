@@ -87,14 +87,19 @@ int launch_gather(const char* what, void* stream, const uint16_t* table, int64_t
                what, "index outside the table");
   const bool vec = cols % 8 == 0 && aligned16(table) && aligned16(dst);
   const hipStream_t s = as_stream(stream);
-  const unsigned blocks = blocks_for_rows(rows);
   const int c32 = static_cast<int>(cols);
   clear_launch_error();
-  if (vec) {
-    gather_rows_kernel<TO, 8><<<blocks, kBlock, 0, s>>>(table, table_rows, index, one_index, state, rows, c32, dst);
-  } else {
-    gather_rows_kernel<TO, 1><<<blocks, kBlock, 0, s>>>(table, table_rows, index, one_index, state, rows, c32, dst);
-  }
+  // Row pieces of kPieceRows (one piece below a million rows).
+  for_each_piece(rows, kPieceRows, [&](int64_t r0, int64_t rn) {
+    const unsigned blocks = blocks_for_rows(rn);
+    const int64_t* ip = index != nullptr ? index + r0 : nullptr;
+    TO* dp = dst + r0 * cols;
+    if (vec) {
+      gather_rows_kernel<TO, 8><<<blocks, kBlock, 0, s>>>(table, table_rows, ip, one_index, state, rn, c32, dp);
+    } else {
+      gather_rows_kernel<TO, 1><<<blocks, kBlock, 0, s>>>(table, table_rows, ip, one_index, state, rn, c32, dp);
+    }
+  });
   return check_launch(what);
 }
 

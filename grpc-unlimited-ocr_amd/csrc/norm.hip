@@ -333,29 +333,38 @@ int launch_norm(const char* what, void* stream, T* x, const T* delta, const floa
                                                                                        aligned16(delta))));
   const int64_t nvec = vec ? cols / kV : cols;
   const int64_t groups = (nvec + kWave - 1) / kWave;
+  if constexpr (kMode == Norm::kEmbedRms) {
+    UOCR_REQUIRE(groups <= kMaxGroups, what, "cols too large for one row kernel");
+  }
   const hipStream_t s = as_stream(stream);
   const int c32 = static_cast<int>(cols);
   clear_launch_error();
-  if (groups > kMaxGroups) {
-    if constexpr (kMode == Norm::kEmbedRms) {
-      return fail(UOCR_ROCM_INVALID_ARGUMENT, what, "cols too large for one row kernel");
-    } else if constexpr (kMode == Norm::kLayer) {
-      ln_rows_wide<T><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, w, b, cols, eps);
-    } else {
-      rms_rows_wide<T, kMode == Norm::kAddRms, kMode == Norm::kRouter>
-          <<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, delta, w, h, cols, eps);
+  // Row pieces of kPieceRows (one piece below a million rows). A row's result
+  // does not depend on its piece: the reduction order is fixed by cols.
+  for_each_piece(rows, kPieceRows, [&](int64_t r0, int64_t rn) {
+    const int64_t o = r0 * cols;
+    T* xp = x + o;
+    const T* dp = delta != nullptr ? delta + o : nullptr;
+    T* hp = h != nullptr ? h + o : nullptr;
+    if (groups > kMaxGroups) {
+      if constexpr (kMode == Norm::kLayer) {
+        ln_rows_wide<T><<<static_cast<unsigned>(rn), kBlock, 0, s>>>(xp, w, b, cols, eps);
+      } else if constexpr (kMode != Norm::kEmbedRms) {
+        rms_rows_wide<T, kMode == Norm::kAddRms, kMode == Norm::kRouter>
+            <<<static_cast<unsigned>(rn), kBlock, 0, s>>>(xp, dp, w, hp, cols, eps);
+      }
+      return;
     }
-    return check_launch(what);
-  }
-  const bool spread = groups > 16 || (rows < kFewRows && groups >= 4);
-  const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
-  if (vec) {
-    if (spread) launch_norm_rows<T, kV, 4, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps, e);
-    else launch_norm_rows<T, kV, 1, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps, e);
-  } else {
-    if (spread) launch_norm_rows<T, 1, 4, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps, e);
-    else launch_norm_rows<T, 1, 1, kMode>(vpl, s, x, delta, w, b, h, rows, c32, eps, e);
-  }
+    const bool spread = groups > 16 || (rn < kFewRows && groups >= 4);
+    const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
+    if (vec) {
+      if (spread) launch_norm_rows<T, kV, 4, kMode>(vpl, s, xp, dp, w, b, hp, rn, c32, eps, e);
+      else launch_norm_rows<T, kV, 1, kMode>(vpl, s, xp, dp, w, b, hp, rn, c32, eps, e);
+    } else {
+      if (spread) launch_norm_rows<T, 1, 4, kMode>(vpl, s, xp, dp, w, b, hp, rn, c32, eps, e);
+      else launch_norm_rows<T, 1, 1, kMode>(vpl, s, xp, dp, w, b, hp, rn, c32, eps, e);
+    }
+  });
   return check_launch(what);
 }
 

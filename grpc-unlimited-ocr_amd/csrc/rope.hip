@@ -263,11 +263,20 @@ int launch_rope(const char* what, void* stream, T* x0, int64_t heads0, T* x1, in
   // 16-byte chunks need every head half to start on a 16-byte boundary.
   const bool vec = a.half % kV == 0 && aligned16(a.x0) && (a.x1 == nullptr || aligned16(a.x1));
   clear_launch_error();
-  if (vec) {
-    launch_rope_vw<T, kV>(a, as_stream(stream));
-  } else {
-    launch_rope_vw<T, 1>(a, as_stream(stream));
-  }
+  // Row pieces of kPieceRows tokens (one piece below a million tokens).
+  for_each_piece(rows, kPieceRows, [&](int64_t r0, int64_t rn) {
+    RopeArgs<T> p = a;
+    p.rows = rn;
+    p.x0 = a.x0 + r0 * a.heads0 * dim;
+    p.x1 = a.x1 != nullptr ? a.x1 + r0 * a.heads1 * dim : nullptr;
+    p.tok = a.tok != nullptr ? a.tok + r0 : nullptr;
+    p.page = a.page != nullptr ? a.page + r0 : nullptr;
+    if (vec) {
+      launch_rope_vw<T, kV>(p, as_stream(stream));
+    } else {
+      launch_rope_vw<T, 1>(p, as_stream(stream));
+    }
+  });
   return check_launch(what);
 }
 

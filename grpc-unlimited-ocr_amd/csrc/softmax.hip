@@ -38,13 +38,18 @@ constexpr float kLog2e = 1.4426950408889634f;
 // row R / batch, and the blocks run in XCD-aware order (xcd_block), so the
 // `batch` rows that share a mask row run side by side on one XCD and the
 // mask row is read once into its L2 (258 -> 240 us on [10 x 4096, 4096]).
+// A launch may cover mask rows first .. of the call (row pieces): its logical
+// row r is slice r mod batch of mask row first + r / batch.
 struct RowMask {
   const float* mask;  // [mask_rows, cols], or null (+ 0)
   float scale;
   int64_t mask_rows;
   int64_t batch;
-  __device__ __forceinline__ int64_t mask_row(int64_t r) const { return r / batch; }
-  __device__ __forceinline__ int64_t data_row(int64_t r) const { return (r % batch) * mask_rows + r / batch; }
+  int64_t first;
+  __device__ __forceinline__ int64_t mask_row(int64_t r) const { return first + r / batch; }
+  __device__ __forceinline__ int64_t data_row(int64_t r) const {
+    return (r % batch) * mask_rows + first + r / batch;
+  }
 };
 
 // Waves per row (WPR) and workgroup size: one wave per row in 4-wave
@@ -207,17 +212,29 @@ int softmax_entry(const char* what, void* stream, float* x, int64_t rows, int64_
   const int64_t nvec = vec ? cols / 4 : cols;
   const int64_t groups = (nvec + kWave - 1) / kWave;
   const hipStream_t s = as_stream(stream);
-  clear_launch_error();
-  if (groups > kMaxGroups) {
-    softmax_rows_wide<kMask><<<static_cast<unsigned>(rows), kBlock, 0, s>>>(x, cols, rm);
-    return check_launch(what);
-  }
   const int c32 = static_cast<int>(cols);
-  if (vec) {
-    launch_softmax_wpr<4, kMask>(groups, s, x, rows, c32, rm);
-  } else {
-    launch_softmax_wpr<1, kMask>(groups, s, x, rows, c32, rm);
-  }
+  clear_launch_error();
+  // Pieces of about kPieceRows rows (one piece below a million rows): whole
+  // mask rows (all batch slices of each) when masked, else plain row ranges.
+  const int64_t unit = kMask ? rm.batch : 1;
+  const int64_t piece = kPieceRows / unit > 0 ? kPieceRows / unit : 1;
+  for_each_piece(rows / unit, piece, [&](int64_t u0, int64_t un) {
+    RowMask p = rm;
+    float* xp = x;
+    if constexpr (kMask) {
+      p.first = u0;
+    } else {
+      xp = x + u0 * cols;
+    }
+    const int64_t rn = un * unit;
+    if (groups > kMaxGroups) {
+      softmax_rows_wide<kMask><<<static_cast<unsigned>(rn), kBlock, 0, s>>>(xp, cols, p);
+    } else if (vec) {
+      launch_softmax_wpr<4, kMask>(groups, s, xp, rn, c32, p);
+    } else {
+      launch_softmax_wpr<1, kMask>(groups, s, xp, rn, c32, p);
+    }
+  });
   return check_launch(what);
 }
 
@@ -290,7 +307,7 @@ int uocr_rocm_softmax_rows(void* stream, float* x, int64_t rows, int64_t cols) {
   UOCR_REQUIRE(rows == 0 || (cols > 0 && cols < (int64_t{1} << 31)), what, "cols must be in [1, 2^31)");
   if (rows == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(x != nullptr, what, "null x");
-  return softmax_entry<false>(what, stream, x, rows, cols, RowMask{nullptr, 1.0f, 1, 1});
+  return softmax_entry<false>(what, stream, x, rows, cols, RowMask{nullptr, 1.0f, 1, 1, 0});
 }
 
 int uocr_rocm_scale_mask_softmax_rows(void* stream, float* x, float scale, const float* mask, int64_t batch,
@@ -302,7 +319,7 @@ int uocr_rocm_scale_mask_softmax_rows(void* stream, float* x, float scale, const
   UOCR_REQUIRE(all == 0 || (cols > 0 && cols < (int64_t{1} << 31)), what, "cols must be in [1, 2^31)");
   if (all == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(x != nullptr, what, "null x");
-  return softmax_entry<true>(what, stream, x, all, cols, RowMask{mask, scale, rows, batch});
+  return softmax_entry<true>(what, stream, x, all, cols, RowMask{mask, scale, rows, batch, 0});
 }
 
 int uocr_rocm_scale_add_mask(void* stream, float* x, float scale, const float* mask, int64_t batch, int64_t rows,

@@ -146,7 +146,8 @@ def test_copy_errors(backend):
     _invalid(backend, "uocr_rocm_copy", None, FAKE, None, 16, detail="null")
     _invalid(backend, "uocr_rocm_copy", None, FAKE, FAKE + 32, 16, detail="overlap")
     _invalid(backend, "uocr_rocm_copy", None, FAKE + 32, FAKE, 16, detail="overlap")
-    _invalid(backend, "uocr_rocm_copy", None, FAKE, FAKE + 64, 1 << 40, detail="too large")
+    _invalid(backend, "uocr_rocm_copy", None, FAKE, FAKE + 64, 1 << 60, detail="too large")
+    _invalid(backend, "uocr_rocm_gelu_erf", None, FAKE, 1 << 60, detail="too large")
     # the same buffer on both sides is a copy that changes nothing: no launch
     assert backend.lib().uocr_rocm_copy(None, FAKE, FAKE, 16) == 0
 

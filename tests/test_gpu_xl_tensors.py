@@ -240,3 +240,84 @@ def test_attend_step_past_2_31_cache_elements(backend, cache):
     backend.attend_step(dev_f32(q), kc, vc, heads, hd, mask, scale, state, scratch, out)
     want = oracle.attention_one(q, kr, vr, heads, hd, bias=bias, scale=scale)
     assert_f32_close(host_f32(out), want, 1e-5, f"attend_step {cache} cache [{capacity}, {width}]")
+
+
+# ---- launches in pieces: calls past a million rows run as several launches --------------------
+
+PIECE_ROWS = 1 << 20  # rows per launch of the row kernels
+
+
+# 4097 bf16 columns: the scalar path, 65 chunk groups, so the wide-row kernel
+@pytest.mark.parametrize("op,cols", [("rms_f32", 12), ("add_rms_f32", 13), ("layer_bf16", 24), ("rms_bf16_wide", 4097)])
+def test_norm_row_pieces(backend, op, cols):
+    rows = PIECE_ROWS + 37
+    bf = op.endswith("bf16") or op.endswith("wide")
+    x = normal(930, (PERIOD, cols), 2.0, 0.3)
+    d = normal(931, (PERIOD, cols))
+    w, b = dev_f32(1 + 0.02 * normal(932, cols)), dev_f32(0.02 * normal(933, cols))
+    up = (lambda a: dev_bf16(oracle.f32_to_bf16(a))) if bf else dev_f32
+    small, sd = up(x), up(d)
+    big, bd = tiled(small.clone(), rows), tiled(sd, rows)
+    for t, dd in ((small, sd), (big, bd)):
+        if op.startswith("rms"):
+            backend.rms_norm(t, w, 1e-6)
+        elif op.startswith("layer"):
+            backend.layer_norm(t, w, b, 1e-6)
+        else:
+            h = torch.empty_like(t)
+            backend.add_rms_norm(t, dd, w, h, 1e-6)
+            if t is small:
+                sh = h
+            else:
+                assert_periodic(h, sh, f"{op} h [{rows}, {cols}]")
+    assert_periodic(big, small, f"{op} [{rows}, {cols}]")
+
+
+def test_rope_row_pieces(backend):
+    rows, dim = PIECE_ROWS + 3, 6  # half 3: the scalar path
+    q, k = normal(934, (PERIOD, dim)), normal(935, (PERIOD, 2 * dim))
+    tok, page = np.arange(PERIOD, dtype=np.int64) * 37, np.arange(PERIOD, dtype=np.int64) - 3
+    inv_tok, inv_page = oracle.rope_inv(2, 1e4), oracle.rope_inv(1, 256.0)
+    sq, sk = dev_f32(q), dev_f32(k)
+    lq, lk = tiled(sq.clone(), rows), tiled(sk.clone(), rows)
+    args = dict(inv_tok=dev_f32(inv_tok), inv_page=dev_f32(inv_page), page_mod=4)
+    backend.rope_qk(sq, 1, sk, 2, dim, dev_i64(tok), dev_i64(page), **args)
+    backend.rope_qk(lq, 1, lk, 2, dim, tiled(dev_i64(tok).view(PERIOD, 1), rows).view(rows),
+                    tiled(dev_i64(page).view(PERIOD, 1), rows).view(rows), **args)
+    assert_periodic(lq, sq, f"rope q [{rows}, 1 x {dim}]")
+    assert_periodic(lk, sk, f"rope k [{rows}, 2 x {dim}]")
+
+
+def test_softmax_row_pieces(backend):
+    rows, cols = PIECE_ROWS + 9, 5
+    x = normal(936, (PERIOD, cols), 3.0)
+    small = dev_f32(x)
+    big = tiled(small.clone(), rows)
+    backend.softmax_rows(small)
+    backend.softmax_rows(big)
+    assert_periodic(big, small, f"softmax_rows [{rows}, {cols}]")
+    batch, cols = 3, 7
+    mrows = PIECE_ROWS // batch + 5
+    x = normal(937, (batch, PERIOD, cols), 3.0)
+    mask = np.where(np.random.default_rng(938).uniform(size=(PERIOD, cols)) < 0.3, -np.inf, 0.0).astype(np.float32)
+    small = dev_f32(x.reshape(batch * PERIOD, cols))
+    backend.scale_mask_softmax_rows(small, 0.5, dev_f32(mask), batch, PERIOD, cols)
+    big = torch.empty(batch, mrows, cols, device="cuda")
+    for s in range(batch):
+        big[s].copy_(tiled(dev_f32(x[s]), mrows))
+    backend.scale_mask_softmax_rows(big.view(batch * mrows, cols), 0.5, tiled(dev_f32(mask), mrows), batch, mrows,
+                                    cols)
+    for s in range(batch):
+        assert_periodic(big[s], small.view(batch, PERIOD, cols)[s], f"scale_mask_softmax slice {s} [{mrows}, {cols}]")
+
+
+def test_gather_row_pieces(backend):
+    vocab, cols, rows = 50, 3, PIECE_ROWS + 11
+    table = oracle.f32_to_bf16(normal(939, (vocab, cols)))
+    ids = np.array([49, 0, 7, 60, 3, -1, 25], dtype=np.int64)  # 60 and -1 fall outside: zero rows
+    out = torch.empty(rows, cols, device="cuda")
+    backend.gather_rows_bf16(dev_bf16(table), tiled(dev_i64(ids).view(PERIOD, 1), rows).view(rows), out,
+                             table_rows=vocab)
+    want = oracle.embed(table, np.clip(ids, 0, vocab - 1))
+    want[(ids < 0) | (ids >= vocab)] = 0.0
+    assert_periodic(out, dev_f32(want), f"gather_rows_bf16 [{rows}, {cols}]")
