@@ -27,8 +27,8 @@
 //                with clamp to [-1e4, 1e4] (src/model/decoder.cpp:20-34).
 // The output expressions are evaluated without FMA contraction so that each
 // product and sum is rounded where the reference rounds it. Norm weights are
-// read after the reduction: they are shared by every row (cache resident)
-// and loading them late keeps the waves' register count low.
+// shared by every row (cache resident): one-wave rows read them after the
+// reduction, rows spread over several waves just before it.
 
 #include "common.hpp"
 
@@ -136,6 +136,24 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
     }
   }
 
+  // Rows spread over several waves (WPR > 1) fold through LDS and a barrier:
+  // their norm weights are requested before the fold, whose latency then
+  // covers the weights' (fp32 [1024, 2048] RMSNorm 4.47 -> 4.37 us). One-wave
+  // rows fold in a few DPP steps and request them after: early weights were
+  // 4-8% slower there, every wave asking for the same lines at once.
+  constexpr bool kEarlyW = WPR > 1;
+  float wv_e[kEarlyW ? VPL : 1][VW], bv_e[kEarlyW && kMode == Norm::kLayer ? VPL : 1][VW];
+  if constexpr (kEarlyW) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int v = (wr + WPR * k) * kWave + lane;
+      const int vc = v < nvec ? v : nvec - 1;
+      load_f32<VW>(w + vc * VW, wv_e[k]);
+      if constexpr (kMode == Norm::kLayer) load_f32<VW>(b + vc * VW, bv_e[k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float inv;
   if constexpr (kMode == Norm::kLayer) {
     const float mean = fold_groups<WPR, VPL>(part, wr, groups, red[rloc]) / static_cast<float>(cols);
@@ -172,8 +190,16 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
         xs.store(x + at);
       }
       float wv[VW], bv[VW], y[VW];
-      load_f32<VW>(w + v * VW, wv);
-      if constexpr (kMode == Norm::kLayer) load_f32<VW>(b + v * VW, bv);
+      if constexpr (kEarlyW) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          wv[e] = wv_e[k][e];
+          if constexpr (kMode == Norm::kLayer) bv[e] = bv_e[k][e];
+        }
+      } else {
+        load_f32<VW>(w + v * VW, wv);
+        if constexpr (kMode == Norm::kLayer) load_f32<VW>(b + v * VW, bv);
+      }
       {
 #pragma clang fp contract(off)
 #pragma unroll
