@@ -68,10 +68,12 @@ PinnedBuffer::PinnedBuffer(std::size_t bytes) : bytes_(bytes) { check(uocr_rocm_
 PinnedBuffer::~PinnedBuffer() { (void)uocr_rocm_host_free(data_); }
 
 void copy_to_device(const Context& ctx, void* device_dst, const PinnedBuffer& src, std::size_t bytes) {
+  if (bytes > src.bytes()) throw std::invalid_argument("copy_to_device: more bytes than the pinned buffer holds");
   check(uocr_rocm_memcpy(device_dst, src.data(), bytes, UOCR_ROCM_H2D, ctx.stream()));
 }
 
 void copy_to_host(const Context& ctx, PinnedBuffer& dst, const void* device_src, std::size_t bytes) {
+  if (bytes > dst.bytes()) throw std::invalid_argument("copy_to_host: more bytes than the pinned buffer holds");
   check(uocr_rocm_memcpy(dst.data(), device_src, bytes, UOCR_ROCM_D2H, ctx.stream()));
 }
 
