@@ -120,8 +120,9 @@ struct Running {
 
 __device__ __forceinline__ float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
-template <class TC, int VW, int G, int VPL, int U, bool kRope>
+template <class TC, int VW, int G, int VPL, int U, bool kRope, bool kEarly>
 __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
+  static_assert(kRope || !kEarly, "the early first batch is the rope kernel's (and only without a mask)");
   constexpr bool kBf16 = sizeof(TC) == 2;
   const TC* kc = static_cast<const TC*>(a.k);
   const TC* vc = static_cast<const TC*>(a.v);
@@ -155,74 +156,17 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   const int nvec = a.hd / VW;
   const int64_t head_off = static_cast<int64_t>(h) * a.hd;
 
-  if constexpr (kRope) {
-    // rope on this head's q and new k, with rope.hip's arithmetic: angle =
-    // float(tok) inv_tok[p] (or float(page mod page_mod) inv_page[p - n_tok]),
-    // device sincosf, a c - b s / b c + a s without contraction.
-    const int half = a.hd / 2;
-    int64_t pg = a.state->page;
-    if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
-    const float ft = static_cast<float>(a.state->tok), fp = static_cast<float>(pg);
-    for (int p = threadIdx.x; p < half; p += kBlock) {
-      const float angle = p < a.n_tok ? ft * a.inv_tok[p] : fp * a.inv_page[p - a.n_tok];
-      float sn, cs;
-      sincosf(angle, &sn, &cs);
-      const float qa = a.q[head_off + p], qb = a.q[head_off + p + half];
-      const float ka = a.k_row[head_off + p], kb = a.k_row[head_off + p + half];
-      {
-#pragma clang fp contract(off)
-        s_new[0][p] = qa * cs - qb * sn;
-        s_new[0][p + half] = qb * cs + qa * sn;
-        s_new[1][p] = ka * cs - kb * sn;
-        s_new[1][p + half] = kb * cs + ka * sn;
-      }
-      if constexpr (kBf16) {  // the key as the bf16 cache will hold it
-        s_new[1][p] = round_bf16(s_new[1][p]);
-        s_new[1][p + half] = round_bf16(s_new[1][p + half]);
-      }
-    }
-    for (int t = threadIdx.x; t < a.hd; t += kBlock) {
-      s_new[2][t] = kBf16 ? round_bf16(a.v_row[head_off + t]) : a.v_row[head_off + t];
-    }
-    __syncthreads();
-    // The split that holds key pos appends the head's rotated k and its v.
-    if (pos >= first && pos < last) {
-      for (int t = threadIdx.x; t < a.hd; t += kBlock) {
-        Chunk<TC, 1> kk, vv;
-        kk.narrow({s_new[1][t]});
-        vv.narrow({s_new[2][t]});
-        kk.store(static_cast<TC*>(a.k_out) + pos * a.width + head_off + t);
-        vv.store(static_cast<TC*>(a.v_out) + pos * a.width + head_off + t);
-      }
-    }
-  }
-
   // This lane's chunks of the head: c = gl + G i; lanes past the head (when
   // nvec is not a power of two) address the head's last chunk and their
   // values are dropped.
   int64_t col[VPL];
   bool in_head[VPL];
-  float qv[VPL][VW];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = gl + G * i;
     in_head[i] = c < nvec;
     col[i] = head_off + static_cast<int64_t>(in_head[i] ? c : nvec - 1) * VW;
-#pragma unroll
-    for (int e = 0; e < VW; ++e) {
-      if constexpr (kRope) {
-        qv[i][e] = in_head[i] ? s_new[0][col[i] - head_off + e] : 0.0f;
-      } else {
-        qv[i][e] = in_head[i] ? a.q[col[i] + e] : 0.0f;
-      }
-    }
   }
-
-  Running<VW, VPL> run;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i)
-#pragma unroll
-    for (int e = 0; e < VW; ++e) run.acc[i][e] = 0.0f;
 
   // Loads are issued unconditionally: a key that is masked or past the end
   // reads the query row instead (cached; its score is -inf and its value is
@@ -251,6 +195,78 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
       for (int i = 0; i < VPL; ++i) b.v[u][i].load(live ? vc + j * a.width + col[i] : dead + col[i]);
     }
   };
+
+  KeyBatch<TC, VW, VPL, U> A, B;
+
+  if constexpr (kRope) {
+    // rope on this head's q and new k, with rope.hip's arithmetic: angle =
+    // float(tok) inv_tok[p] (or float(page mod page_mod) inv_page[p - n_tok]),
+    // device sincosf, a c - b s / b c + a s without contraction. Thread p
+    // takes pair p and element p of v (hd <= kBlock: one of each at most).
+    // The row loads are unconditional (indices clamped into the head) and
+    // issued first: without a mask (kEarly) the first key batch follows
+    // them at once, and as a wave's loads complete in order, the rope
+    // arithmetic then waits for the rows only while the batch is in flight.
+    static_assert(kMaxHeadDim <= kBlock, "one rope pair and one v element per thread");
+    const int half = a.hd / 2;
+    const int p = threadIdx.x;
+    const int pc = p < half ? p : half - 1, tc = p < a.hd ? p : a.hd - 1;
+    const float qa = a.q[head_off + pc], qb = a.q[head_off + pc + half];
+    const float ka = a.k_row[head_off + pc], kb = a.k_row[head_off + pc + half];
+    const float inv = *(pc < a.n_tok ? a.inv_tok + pc : a.inv_page + (pc - a.n_tok));
+    const float vr = a.v_row[head_off + tc];
+    if constexpr (kEarly) issue(A, first + slot, first, last);
+    int64_t pg = a.state->page;
+    if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
+    const float ft = static_cast<float>(a.state->tok), fp = static_cast<float>(pg);
+    if (p < half) {
+      const float angle = (p < a.n_tok ? ft : fp) * inv;
+      float sn, cs;
+      sincosf(angle, &sn, &cs);
+      {
+#pragma clang fp contract(off)
+        s_new[0][p] = qa * cs - qb * sn;
+        s_new[0][p + half] = qb * cs + qa * sn;
+        s_new[1][p] = ka * cs - kb * sn;
+        s_new[1][p + half] = kb * cs + ka * sn;
+      }
+      if constexpr (kBf16) {  // the key as the bf16 cache will hold it
+        s_new[1][p] = round_bf16(s_new[1][p]);
+        s_new[1][p + half] = round_bf16(s_new[1][p + half]);
+      }
+    }
+    if (p < a.hd) s_new[2][p] = kBf16 ? round_bf16(vr) : vr;
+    __syncthreads();
+    // The split that holds key pos appends the head's rotated k and its v.
+    if (pos >= first && pos < last) {
+      for (int t = threadIdx.x; t < a.hd; t += kBlock) {
+        Chunk<TC, 1> kk, vv;
+        kk.narrow({s_new[1][t]});
+        vv.narrow({s_new[2][t]});
+        kk.store(static_cast<TC*>(a.k_out) + pos * a.width + head_off + t);
+        vv.store(static_cast<TC*>(a.v_out) + pos * a.width + head_off + t);
+      }
+    }
+  }
+
+  float qv[VPL][VW];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      if constexpr (kRope) {
+        qv[i][e] = in_head[i] ? s_new[0][col[i] - head_off + e] : 0.0f;
+      } else {
+        qv[i][e] = in_head[i] ? a.q[col[i] + e] : 0.0f;
+      }
+    }
+  }
+
+  Running<VW, VPL> run;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+#pragma unroll
+    for (int e = 0; e < VW; ++e) run.acc[i][e] = 0.0f;
 
   auto consume = [&](const KeyBatch<TC, VW, VPL, U>& b) {
     float s[U];
@@ -331,8 +347,7 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
     }
     const int64_t base = t0 + slot;
     const int iters = base < t1 ? static_cast<int>((t1 - base + kStride - 1) / kStride) : 0;
-    KeyBatch<TC, VW, VPL, U> A, B;
-    issue(A, base, t0, t1);
+    if (!(kEarly && t0 == first)) issue(A, base, t0, t1);
     for (int it = 0; it < iters; it += 2) {
       issue(B, base + (it + 1) * kStride, t0, t1);
       consume(A);
@@ -461,7 +476,12 @@ int attend_splits(int64_t heads, int64_t hd, int64_t capacity, int64_t elem_byte
 
 template <class TC, int VW, int G, int VPL, int U, bool kRope>
 void launch_partial(hipStream_t s, const AttendArgs& a, int64_t heads) {
-  attend_partial<TC, VW, G, VPL, U, kRope><<<static_cast<unsigned>(heads * a.splits), kBlock, 0, s>>>(a);
+  const unsigned blocks = static_cast<unsigned>(heads * a.splits);
+  if (kRope && a.mask == nullptr) {
+    attend_partial<TC, VW, G, VPL, U, kRope, kRope><<<blocks, kBlock, 0, s>>>(a);
+  } else {
+    attend_partial<TC, VW, G, VPL, U, kRope, false><<<blocks, kBlock, 0, s>>>(a);
+  }
 }
 
 // Lanes per key and keys per batch, with 16-byte chunks (4 fp32 or 8 bf16
