@@ -410,8 +410,20 @@ __global__ __launch_bounds__(kBlock) void attend_merge(const float* __restrict__
   const int ec = e < hd ? e : hd - 1;
   const int64_t rec_len = hd + 2;
   const float* recs = part + static_cast<int64_t>(h) * splits * rec_len;
-  // Every load is issued before the first is used: the value records, then
-  // wave 0's (m, l) pairs.
+  // Every load is issued before the first is used: wave 0's (m, l) pairs
+  // first (a wave's loads complete in order, and the weights are formed from
+  // them while the value records are still arriving), then the value
+  // records.
+  float m[kPerLane], l[kPerLane];
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) {
+      const int sp = lane + kWave * k;
+      const int sc = sp < splits ? sp : splits - 1;
+      m[k] = recs[sc * rec_len];
+      l[k] = recs[sc * rec_len + 1];
+    }
+  }
   float vals[kPerWave];
 #pragma unroll
   for (int r = 0; r < kPerWave; ++r) {
@@ -419,15 +431,11 @@ __global__ __launch_bounds__(kBlock) void attend_merge(const float* __restrict__
     vals[r] = recs[(sp < splits ? sp : splits - 1) * rec_len + 2 + ec];
   }
   if (wave == 0) {
-    float m[kPerLane], l[kPerLane];
     float big = -INFINITY;
 #pragma unroll
     for (int k = 0; k < kPerLane; ++k) {
       const int sp = lane + kWave * k;
-      const int sc = sp < splits ? sp : splits - 1;
-      const float m_raw = recs[sc * rec_len];
-      l[k] = recs[sc * rec_len + 1];
-      m[k] = sp < splits ? m_raw : -INFINITY;
+      m[k] = sp < splits ? m[k] : -INFINITY;
       big = fmaxf(big, m[k]);
     }
     big = wave_max(big);
