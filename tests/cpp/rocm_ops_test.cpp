@@ -4,8 +4,9 @@
 // std::mt19937(5), the same relative-error metric, the same tolerances for
 // the fp32 ops, plus the bf16-activation ops at 2 bf16 ulp, the fused ops,
 // a captured decode step replayed at three StepStates, one decoder layer's
-// fused step against its unfused ops, and the error convention. Exits 77
-// (skip) without a HIP device.
+// fused step against its unfused ops, the captured whole-step dense decoder
+// against the oracle's, and the error convention. Exits 77 (skip) without a
+// HIP device.
 
 #include <algorithm>
 #include <cmath>
@@ -22,6 +23,7 @@
 #include "backend/rocm/decode_ops.h"
 #include "backend/rocm/dtype.h"
 #include "backend/rocm/ops.h"
+#include "model/rocm/dense_decode_step.h"
 #include "../../oracle/uocr_oracle.h"
 
 namespace ro = uocr::rocm;
@@ -435,6 +437,118 @@ void fused_decode_layer(const ro::Context& ctx) {
   }
 }
 
+void dense_decode_step(const ro::Context& ctx, bool bf16_cache) {
+  // The captured whole-step decoder (embedding, 2 layers, final norm, LM
+  // head) fed 8 tokens in sequence, each step's logits held to the oracle's
+  // decoder on the same weights and cache rounding. The GEMVs round their
+  // inputs to bf16, so a one-ulp difference in an fp32 sum upstream can flip
+  // one input's rounding (2^-8 of that element) now and then: every step is
+  // held to 1e-2, and most steps (the median) to 1e-5.
+  ro::DenseDecoderDims d;
+  d.hidden = 256;
+  d.heads = 4;
+  d.head_dim = 64;
+  d.ffn = 192;
+  d.vocab = 500;
+  d.capacity = 64;
+  d.bf16_cache = bf16_cache;
+  const std::int64_t H = d.hidden, W = d.heads * d.head_dim, F = d.ffn, V = d.vocab, half = d.head_dim / 2;
+  const int layers = 2;
+  auto norm_w = [&](std::int64_t n) {
+    auto w = random(static_cast<std::size_t>(n), 0.02f);
+    for (float& v : w) v += 1.0f;
+    return w;
+  };
+  const auto embed = bf16_rounded(random(V * H, 0.5f)), lm = bf16_rounded(random(V * H, 0.05f));
+  const auto final_norm = norm_w(H);
+  struct HostLayer {
+    std::vector<float> in, qkv, o, post, gate, up, down;
+  };
+  std::vector<HostLayer> hl(layers);
+  for (auto& l : hl) {
+    l = {norm_w(H), bf16_rounded(random(3 * W * H, 0.06f)), bf16_rounded(random(H * W, 0.06f)), norm_w(H),
+         bf16_rounded(random(F * H, 0.06f)), bf16_rounded(random(F * H, 0.06f)), bf16_rounded(random(H * F, 0.07f))};
+  }
+  std::vector<ro::Array> keep;
+  auto dev = [&](const std::vector<float>& v, ro::DType t) {
+    keep.push_back(up(ctx, v, t));
+    return keep.back().data();
+  };
+  std::vector<ro::DenseLayerWeights> lw;
+  for (const auto& l : hl) {
+    lw.push_back({static_cast<const float*>(dev(l.in, ro::DType::kF32)),
+                  static_cast<const std::uint16_t*>(dev(l.qkv, ro::DType::kBF16)),
+                  static_cast<const std::uint16_t*>(dev(l.o, ro::DType::kBF16)),
+                  static_cast<const float*>(dev(l.post, ro::DType::kF32)),
+                  static_cast<const std::uint16_t*>(dev(l.gate, ro::DType::kBF16)),
+                  static_cast<const std::uint16_t*>(dev(l.up, ro::DType::kBF16)),
+                  static_cast<const std::uint16_t*>(dev(l.down, ro::DType::kBF16))});
+  }
+  const auto* demb = static_cast<const std::uint16_t*>(dev(embed, ro::DType::kBF16));
+  const auto* dfin = static_cast<const float*>(dev(final_norm, ro::DType::kF32));
+  const auto* dlm = static_cast<const std::uint16_t*>(dev(lm, ro::DType::kBF16));
+  ro::DenseDecodeStep step(ctx, d, demb, lw, dfin, dlm);
+
+  // The oracle's decoder: the GEMVs' inputs rounded to bf16, the caches
+  // holding what the device caches hold.
+  const auto inv = rope_inv(half, d.rope_theta);
+  std::vector<std::vector<float>> kc(layers, std::vector<float>(d.capacity * W, 0.0f)), vc = kc;
+  auto linear = [](const std::vector<float>& x, const std::vector<float>& w, std::int64_t n) {
+    std::vector<float> y(static_cast<std::size_t>(n));
+    orc_linear(bf16_rounded(x).data(), 1, static_cast<std::int64_t>(x.size()), w.data(), n, nullptr, y.data());
+    return y;
+  };
+  const float scale = 1.0f / std::sqrt(static_cast<float>(d.head_dim));
+  std::vector<double> errs;
+  for (std::int64_t pos = 0; pos < 8; ++pos) {
+    const std::int64_t token = static_cast<std::int64_t>(rng() % static_cast<unsigned>(V));
+    const auto got = step.step(token, pos);
+    std::vector<float> x(H), h(H), pending;
+    for (std::int64_t c = 0; c < H; ++c) x[c] = embed[token * H + c];
+    for (int li = 0; li < layers; ++li) {
+      const auto& l = hl[li];
+      if (pending.empty()) {
+        h = x;
+        orc_rms_norm(h.data(), l.in.data(), 1, H, d.eps);
+      } else {
+        orc_add_rms_norm(x.data(), pending.data(), l.in.data(), h.data(), 1, H, d.eps);
+      }
+      auto qkv = linear(h, l.qkv, 3 * W);
+      orc_rope_apply(qkv.data(), 1, 2 * d.heads, d.head_dim, nullptr, nullptr, inv.data(), half, nullptr, 0, 0, pos, 0);
+      for (std::int64_t c = 0; c < W; ++c) {
+        float kk = qkv[W + c], vv = qkv[2 * W + c];
+        if (bf16_cache) {
+          kk = ro::bf16_to_f32(ro::f32_to_bf16(kk));
+          vv = ro::bf16_to_f32(ro::f32_to_bf16(vv));
+        }
+        kc[li][pos * W + c] = kk;
+        vc[li][pos * W + c] = vv;
+      }
+      std::vector<float> attn(W);
+      orc_attention_one(qkv.data(), kc[li].data(), vc[li].data(), pos + 1, W, d.heads, d.head_dim, nullptr, scale,
+                        attn.data());
+      const auto o = linear(attn, l.o, H);
+      orc_add_rms_norm(x.data(), o.data(), l.post.data(), h.data(), 1, H, d.eps);
+      auto g = linear(h, l.gate, F);
+      const auto u = linear(h, l.up, F);
+      orc_silu(g.data(), F);
+      orc_mul_into(g.data(), u.data(), F);
+      pending = linear(g, l.down, H);
+    }
+    orc_add_rms_norm(x.data(), pending.data(), final_norm.data(), h.data(), 1, H, d.eps);
+    const auto want = linear(h, lm, V);
+    char what[64];
+    std::snprintf(what, sizeof what, "decode step %s pos %lld", bf16_cache ? "bf16" : "fp32",
+                  static_cast<long long>(pos));
+    errs.push_back(max_rel(got, want));
+    expect(what, errs.back(), 1e-2);
+  }
+  std::sort(errs.begin(), errs.end());
+  expect(bf16_cache ? "decode step bf16 median" : "decode step fp32 median", errs[errs.size() / 2], 1e-5);
+  require_throws_invalid([&] { step.step(0, d.capacity); }, "decode step past the cache");
+  require_throws_invalid([&] { step.step(V, 0); }, "decode step token past the vocabulary");
+}
+
 void step_ops(const ro::Context& ctx) {
   {  // softmax with a masked entry and a fully masked row
     const std::int64_t rows = 5, cols = 300;
@@ -519,6 +633,8 @@ int main() {
     decode_graph(ctx);
     step_ops(ctx);
     fused_decode_layer(ctx);
+    dense_decode_step(ctx, true);
+    dense_decode_step(ctx, false);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());

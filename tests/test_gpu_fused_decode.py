@@ -128,7 +128,7 @@ def state_of(pos, tok=None, page=0):
 @pytest.mark.parametrize("heads,hd,cap,pos,n_tok,page_mod,masked", [
     (10, 128, 8192, 5000, 64, 0, False), (10, 128, 8192, 8191, 48, 4, True), (4, 64, 300, 299, 32, 0, False),
     (2, 66, 100, 57, 33, 0, False), (2, 256, 9000, 8000, 100, 3, False), (10, 128, 64, 70, 64, 0, False),
-    (3, 128, 512, 0, 64, 0, False), (10, 128, 2048, 1500, 64, 0, True)])
+    (3, 128, 512, 0, 64, 0, False), (10, 128, 2048, 1500, 64, 0, True), (4, 64, 300, 123, 0, 5, False)])
 def test_attend_rope_kv_matches_unfused(backend, heads, hd, cap, pos, n_tok, page_mod, masked):
     width = heads * hd
     q, k_row, v_row = dev_f32(normal(330, width)), dev_f32(normal(331, width)), dev_f32(normal(332, width))
