@@ -521,6 +521,7 @@ def config7(be, torch, timer):
     xl, yl = torch.randn(lm_k, device="cuda"), torch.empty(lm_n, device="cuda")
     kern["gemv_bf16_lm_head"] = report("gemv lm head", bytes_gemv(lm_n, lm_k), time_kernel(
         timer, lambda: bf16_randn(torch, (lm_n, lm_k), 0.03), lambda w: be.gemv_bf16(xl, w, yl)))
+    whole = decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, scratch, b, lm_n)
     return {"workload": "fp32 decode layer at batch 1, hidden 1280, 10 heads x 128, FFN 896, KV cache 8192, fused "
                         "(6 launches): add+RMSNorm+GEMV qkv -> RoPE+append+attend (2) -> GEMV o -> add+RMSNorm+GEMV "
                         "gate|up+SwiGLU -> GEMV down",
@@ -530,7 +531,62 @@ def config7(be, torch, timer):
                         "us_per_layer_eager": round(ms_unfused_eager * 1e3, 3)},
             "bf16_kv_cache": {"step": report("decode layer, bf16 cache", total_bf16_kv, ms_bf16_kv),
                               "us_per_layer_graph": round(ms_bf16_kv * 1e3, 3)},
-            "bytes_by_op": b, "attend_splits": splits, "kernels": kern, "sets": nsets}
+            "bytes_by_op": b, "attend_splits": splits, "kernels": kern, "sets": nsets,
+            "decode_step_12_layers": whole}
+
+
+def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, scratch, b, vocab, layers=12):
+    """A whole decode step as one graph, the C++ DenseDecodeStep's body
+    (src/model/rocm/dense_decode_step.cpp) at 12 layers: the embedding row,
+    12 fused layers over bf16 key/value caches of 8192 positions read in
+    full, the final norm fused into the LM-head GEMV. Every layer has the
+    dense FFN of 896 (the model's layers 1-11 are mixture-of-experts, whose
+    expert GEMVs are not built here). One set of weights and caches (1.4 GB)
+    already exceeds the Infinity Cache several times over."""
+    width = heads * hd
+    scale = 1.0 / math.sqrt(hd)
+    table = bf16_randn(torch, (vocab, hidden), 0.5)
+    lm = bf16_randn(torch, (vocab, hidden), 0.03)
+    final_norm = weights(torch, hidden)
+    Ls = [{"in": weights(torch, hidden), "post": weights(torch, hidden),
+           "qkv": bf16_randn(torch, (3 * width, hidden), 0.03), "o": bf16_randn(torch, (hidden, width), 0.03),
+           "gate": bf16_randn(torch, (ffn, hidden), 0.03), "up": bf16_randn(torch, (ffn, hidden), 0.03),
+           "down": bf16_randn(torch, (hidden, ffn), 0.03),
+           "kc": bf16_randn(torch, (cap, width)), "vc": bf16_randn(torch, (cap, width))} for _ in range(layers)]
+    xs = [torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda")]
+    delta, qkv = torch.empty(hidden, device="cuda"), torch.empty(3 * width, device="cuda")
+    attn, o = torch.empty(width, device="cuda"), torch.empty(hidden, device="cuda")
+    act, logits = torch.empty(ffn, device="cuda"), torch.empty(vocab, device="cuda")
+    q, k, v = qkv[:width], qkv[width:2 * width], qkv[2 * width:]
+
+    def step():
+        cur = 0
+        be.embed_step(table, state, xs[cur])
+        pending = None
+        for L in Ls:
+            be.add_rms_norm_gemv_bf16(xs[cur], L["qkv"], qkv, delta=pending,
+                                      x_out=None if pending is None else xs[1 - cur], w_norm=L["in"])
+            if pending is not None:
+                cur = 1 - cur
+            be.attend_rope_kv_step(q, k, v, L["kc"], L["vc"], heads, hd, None, scale, state, inv, None, 0, scratch,
+                                   attn)
+            be.gemv_bf16(attn, L["o"], o)
+            be.add_rms_norm_swiglu_gemv_bf16(xs[cur], L["gate"], L["up"], act, delta=o, x_out=xs[1 - cur],
+                                             w_norm=L["post"])
+            cur = 1 - cur
+            be.gemv_bf16(act, L["down"], delta)
+            pending = delta
+        be.add_rms_norm_gemv_bf16(xs[cur], lm, logits, delta=pending, w_norm=final_norm)
+
+    per_layer = (b["add_rms_norm"] + b["gemv"] + b["rope"] + b["swiglu"]
+                 + (b["attend"] + b["append"]) // 2)  # the bf16 cache halves the attention's bytes
+    total = bytes_gather(1, hidden, 4) + layers * per_layer + bytes_gemv(vocab, hidden)
+    ms = timer.graph([step])[0]
+    out = {"workload": f"whole decode step: embedding, {layers} fused layers (dense FFN {ffn}, bf16 KV cache "
+                       f"{cap} positions), final norm + LM head [{vocab}, {hidden}]; {2 + 5 * layers} launches",
+           "step": report("decode step", total, ms), "us_per_token": round(ms * 1e3, 2)}
+    del Ls, table, lm
+    return out
 
 
 # ---- the CPU baseline (the reference's CPU path, restated in the oracle) ------------------------------
