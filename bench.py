@@ -583,7 +583,7 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
     total = bytes_gather(1, hidden, 4) + layers * per_layer + bytes_gemv(vocab, hidden)
     ms = timer.graph([step])[0]
     out = {"workload": f"whole decode step: embedding, {layers} fused layers (dense FFN {ffn}, bf16 KV cache "
-                       f"{cap} positions), final norm + LM head [{vocab}, {hidden}]; {2 + 5 * layers} launches",
+                       f"{cap} positions), final norm + LM head [{vocab}, {hidden}]; {2 + 6 * layers} launches",
            "step": report("decode step", total, ms), "us_per_token": round(ms * 1e3, 2)}
     del Ls, table, lm
     return out

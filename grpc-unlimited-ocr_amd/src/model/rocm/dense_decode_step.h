@@ -14,9 +14,9 @@
 //   h = rms(x) w_post;  x += (silu(h Wg) * (h Wu)) Wd
 // and after the last layer logits = (rms(x) w_final) W_lm. The reference's
 // block routing, mixture-of-experts layers and int8 weights are not part of
-// it. Each step runs 1 + 5 per layer + 1 launches: the residual add of
+// it. Each step runs 1 + 6 per layer + 1 launches: the residual add of
 // each sublayer is the prologue of the next projection (the fused GEMVs),
-// and rope + both appends + attention are one op.
+// and rope + both appends + attention are one op of two launches.
 
 #include <cstdint>
 #include <memory>
