@@ -130,6 +130,9 @@ _SIGNATURES = {
                                                 _int),
     "uocr_rocm_attend_rope_kv_step": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp,
                                        _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_expert_topk": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp], _int),
+    "uocr_rocm_expert_scratch_floats": ([_i64, _i64], _i64),
+    "uocr_rocm_expert_ffn_one": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp], _int),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -508,3 +511,38 @@ def attend_rope_kv_step(q, k_row, v_row, k_cache, v_cache, heads, hd, mask, scal
     _op(name, stream, _ptr(q), _ptr(k_row), _ptr(v_row), _ptr(k_cache), _ptr(v_cache),
         heads, hd, _f32_param(mask), scale, _ptr(state), _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod,
         _ptr(scratch), capacity, _ptr(out))
+
+
+# ---- mixture of experts at decode -------------------------------------------------------------
+
+
+def expert_topk(logits, k, ids, weights, stream=None):
+    """Softmax over each row of logits [rows, experts] (float32), then the top
+    k (lower index on a tie): ids [rows, k] int64, weights [rows, k] float32.
+    Reference: expert_topk, src/backend/cuda/ops.h:77-81."""
+    rows, experts = _rows_cols(logits)
+    if logits.dtype != _torch().float32 or ids.numel() != rows * k or weights.numel() != rows * k:
+        raise ValueError("expert_topk: float32 logits [rows, experts], ids and weights [rows, k]")
+    _op("uocr_rocm_expert_topk", stream, _ptr(logits), rows, experts, k, _ptr(ids), _ptr(weights))
+
+
+def expert_scratch_floats(k: int, ffn: int) -> int:
+    """Floats of scratch that expert_ffn_one needs."""
+    return int(lib().uocr_rocm_expert_scratch_floats(k, ffn))
+
+
+def expert_ffn_one(x, gate, up, down, ids, weights, scratch, out, stream=None):
+    """One decode row x [hidden] through its k routed experts: gate/up
+    [experts, ffn, hidden] (or [experts * ffn, hidden]) and down [experts,
+    hidden, ffn] bf16 stacks, ids [k] int64, weights [k] float32.
+    Reference: expert_ffn_one, src/backend/cuda/ops.h:82-90."""
+    hidden = x.numel()
+    ffn = down.shape[-1]
+    experts = down.numel() // (hidden * ffn) if hidden * ffn else 0
+    k = ids.numel()
+    if gate.numel() != experts * ffn * hidden or up.numel() != gate.numel() or out.numel() != hidden:
+        raise ValueError("expert_ffn_one shapes: gate/up [experts, ffn, hidden], down [experts, hidden, ffn]")
+    if weights.numel() != k or scratch.numel() < expert_scratch_floats(k, ffn):
+        raise ValueError("expert_ffn_one: weights [k] and scratch of expert_scratch_floats(k, ffn) floats")
+    _op("uocr_rocm_expert_ffn_one", stream, _ptr(x), hidden, ffn, _ptr(gate), _ptr(up), _ptr(down), experts,
+        _ptr(ids), _ptr(weights), k, _ptr(scratch), _ptr(out))

@@ -281,7 +281,22 @@ struct FusedGemv {
   int64_t n;
   int k;
   float eps;
+  // Expert rows (mixture of experts): with ids set, row r of the call is row
+  // r mod slot_rows of expert ids[r / slot_rows] in stacks of `experts`
+  // experts (an id outside the stack reads expert 0; its rows are not used).
+  const int64_t* ids = nullptr;
+  int64_t slot_rows = 0;
+  int64_t experts = 0;
 };
+
+// The weight row that output row r of a fused GEMV reads.
+__device__ __forceinline__ int64_t fused_weight_row(const FusedGemv& a, int64_t r) {
+  if (a.ids == nullptr) return r;
+  const int64_t slot = r / a.slot_rows;
+  int64_t id = a.ids[slot];
+  id = id >= 0 && id < a.experts ? id : 0;
+  return id * a.slot_rows + (r - slot * a.slot_rows);
+}
 
 // The prologue: the workgroup holds the row once, in the row kernel's layout
 // (4-float chunks v = (wave + 8 g) 64 + lane), reduces it in that kernel's
@@ -377,7 +392,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_fused(const FusedGemv a) {
           const int c = lane + kWave * i;
           wc[m][r][i] = u32x4{0u, 0u, 0u, 0u};
           if (row0 + r < a.n && c < nchunks) {
-            wc[m][r][i] = stream_load(reinterpret_cast<const u32x4*>(w + (row0 + r) * k) + c);
+            wc[m][r][i] = stream_load(reinterpret_cast<const u32x4*>(w + fused_weight_row(a, row0 + r) * k) + c);
           }
         }
       }
@@ -475,6 +490,148 @@ int fused_entry(const char* what, void* stream, FusedGemv a) {
   return check_launch(what);
 }
 
+// ---- mixture of experts at decode (src/backend/cuda/ops.h:77-90) ------------------
+//
+// expert_topk: the gate's softmax over each row of logits [rows, experts],
+// then the k highest scores (the lower index first on a tie) as expert ids
+// and their (unnormalised) scores, the rule of MixtureOfExperts::forward
+// (src/model/feed_forward.cpp:36-53): peak = max, total = sum of
+// float(exp(v - peak)) in fp64, score = float(exp(v - peak)) * float(1 /
+// total). One wave per row, two experts per lane (experts <= 128); each of
+// the k rounds is a wave argmax over (score, -index).
+//
+// expert_ffn_one: the routed experts of one decode row, weights stacked by
+// expert (gate/up [experts * ffn, hidden], down [experts * hidden, ffn]):
+//   act_j = silu(gate_j . bf16(x)) * (up_j . bf16(x))      (the fused pair
+//           GEMV over k * ffn rows, expert rows picked through the ids)
+//   out[c] = sum_j w_j (down_j[c] . bf16(act_j))           (in j order)
+// with each down product formed exactly as gemv_bf16 forms it, so the call
+// is bitwise k pair GEMVs, k GEMVs and the weighted sum (mul then add).
+
+constexpr int kMaxExperts = 2 * kWave;
+constexpr int kMaxExpertSlots = 8;
+constexpr int kExpertActFloats = 8192;  // k * ffn staged in LDS by the down kernel
+
+__device__ __forceinline__ bool topk_better(float v, int e, float bv, int be) { return v > bv || (v == bv && e < be); }
+
+__global__ __launch_bounds__(kBlock) void expert_topk_k(const float* __restrict__ logits, int64_t rows, int experts,
+                                                        int k, int64_t* __restrict__ ids, float* __restrict__ wts) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const float* lr = logits + row * experts;
+  float v[2];
+  float peak = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int e = lane + kWave * i;
+    v[i] = e < experts ? lr[e] : -INFINITY;
+    peak = fmaxf(peak, v[i]);
+  }
+  peak = wave_max(peak);
+  // A row of -inf logits scores every expert 0, as softmax_rows leaves a
+  // fully masked row (src/backend/reference/ops.cpp:175-178).
+  const bool dead = peak == -INFINITY;
+  double total = 0.0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (lane + kWave * i < experts) {
+      v[i] = dead ? 0.0f : expf(v[i] - peak);
+      total += static_cast<double>(v[i]);
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) total += __shfl_xor(total, off);
+  const float inv = dead ? 0.0f : static_cast<float>(1.0 / total);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) v[i] = lane + kWave * i < experts ? v[i] * inv : -INFINITY;
+  for (int j = 0; j < k; ++j) {
+    float best = v[0];
+    int best_e = lane;
+    if (topk_better(v[1], lane + kWave, best, best_e)) {
+      best = v[1];
+      best_e = lane + kWave;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      const float ob = __shfl_xor(best, off);
+      const int oe = __shfl_xor(best_e, off);
+      if (topk_better(ob, oe, best, best_e)) {
+        best = ob;
+        best_e = oe;
+      }
+    }
+    if (lane == 0) {
+      ids[row * k + j] = best_e;
+      wts[row * k + j] = best;
+    }
+    if (best_e == lane) v[0] = -INFINITY;
+    if (best_e == lane + kWave) v[1] = -INFINITY;
+  }
+}
+
+// out[c] = sum_j w_j (down[ids[j] * hidden + c] . bf16(act_j)): bf16(act) of
+// every slot in LDS; a wave per output row requests the row of every slot,
+// then forms each product as gemv_reg does (chunk c = lane + 64 i, dot8 in
+// order, wave butterfly, + 0) and adds w_j d_j in slot order.
+template <int CPL>
+__global__ __launch_bounds__(kGemvBlock) void expert_down_k(const float* __restrict__ act, int nchunks,
+                                                            const uint16_t* __restrict__ down, int64_t hidden,
+                                                            const int64_t* __restrict__ ids,
+                                                            const float* __restrict__ wts, int k, int64_t experts,
+                                                            float* __restrict__ out) {
+  __shared__ __align__(16) float xs[kExpertActFloats];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int ffn = nchunks * 8;
+  for (int t = threadIdx.x; t < 2 * nchunks * k; t += kGemvBlock) {
+    float v[4];
+    load_f32<4>(act + 4 * static_cast<int64_t>(t), v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xs[4 * t + e] = round_bf16(v[e]);
+  }
+  __syncthreads();
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kGemvWaves;
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kGemvWaves + threadIdx.x / kWave; c < hidden; c += step) {
+    u32x4 wc[kMaxExpertSlots][CPL];
+#pragma unroll
+    for (int j = 0; j < kMaxExpertSlots; ++j) {
+      const int64_t id = j < k ? ids[j] : 0;
+      const bool live = j < k && id >= 0 && id < experts;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int ci = lane + kWave * i;
+        wc[j][i] = u32x4{0u, 0u, 0u, 0u};
+        if (live && ci < nchunks) wc[j][i] = stream_load(reinterpret_cast<const u32x4*>(down + (id * hidden + c) * ffn) + ci);
+      }
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxExpertSlots; ++j) {
+      if (j < k && ids[j] >= 0 && ids[j] < experts) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const int ci = lane + kWave * i;
+          float xv[8];
+          if (ci < nchunks) {
+            load_f32<8>(xs + j * ffn + 8 * ci, xv);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
+          }
+          a = dot8(wc[j][i], xv, a);
+        }
+        const float d = wave_sum(a) + 0.0f;
+        {
+#pragma clang fp contract(off)
+          total = total + wts[j] * d;
+        }
+      }
+    }
+    if (lane == 0) out[c] = total;
+  }
+}
+
 }  // namespace
 }  // namespace uocr_rocm
 
@@ -530,6 +687,63 @@ int uocr_rocm_add_rms_norm_swiglu_gemv_bf16(void* stream, const float* x, const 
   return fused_entry(what, stream,
                      FusedGemv{x, delta, x_out, w_norm, h_out, w_gate, w_up, nullptr, act, ffn, static_cast<int>(k),
                                eps});
+}
+
+int uocr_rocm_expert_topk(void* stream, const float* logits, int64_t rows, int64_t experts, int64_t k, int64_t* ids,
+                          float* weights) {
+  const char* what = "uocr_rocm_expert_topk";
+  UOCR_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), what, "rows must be in [0, 2^31)");
+  UOCR_REQUIRE(experts >= 1 && experts <= kMaxExperts, what, "experts must be in [1, 128]");
+  UOCR_REQUIRE(k >= 1 && k <= experts, what, "k must be in [1, experts]");
+  if (rows == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(logits != nullptr && ids != nullptr && weights != nullptr, what, "null pointer");
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  expert_topk_k<<<blocks_for_rows(rows), kBlock, 0, s>>>(logits, rows, static_cast<int>(experts), static_cast<int>(k),
+                                                          ids, weights);
+  return check_launch(what);
+}
+
+int64_t uocr_rocm_expert_scratch_floats(int64_t k, int64_t ffn) { return k > 0 && ffn > 0 ? k * ffn : 0; }
+
+int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64_t ffn, const uint16_t* gate,
+                             const uint16_t* up, const uint16_t* down, int64_t experts, const int64_t* ids,
+                             const float* weights, int64_t k, float* scratch, float* out) {
+  const char* what = "uocr_rocm_expert_ffn_one";
+  UOCR_REQUIRE(hidden % 8 == 0 && hidden >= 8 && hidden <= kFusedMaxK, what,
+               "hidden must be a multiple of 8 in [8, 2048]");
+  UOCR_REQUIRE(ffn % 8 == 0 && ffn >= 8 && ffn / 8 <= kWave * kGemvRegChunks, what,
+               "ffn must be a multiple of 8 in [8, 2048]");
+  UOCR_REQUIRE(k >= 1 && k <= kMaxExpertSlots && k * ffn <= kExpertActFloats, what,
+               "k must be in [1, 8] with k * ffn <= 8192");
+  UOCR_REQUIRE(experts >= 1, what, "experts must be >= 1");
+  UOCR_REQUIRE(x != nullptr && gate != nullptr && up != nullptr && down != nullptr && ids != nullptr &&
+                   weights != nullptr && scratch != nullptr && out != nullptr,
+               what, "null pointer");
+  UOCR_REQUIRE(aligned16(x) && aligned16(gate) && aligned16(up) && aligned16(down) && aligned16(scratch), what,
+               "x, the weights and scratch must be 16-byte aligned");
+  auto overlaps = [](const float* a, int64_t na, const float* b, int64_t nb) { return a < b + nb && b < a + na; };
+  UOCR_REQUIRE(!overlaps(scratch, k * ffn, x, hidden) && !overlaps(scratch, k * ffn, out, hidden) &&
+                   !overlaps(out, hidden, x, hidden),
+               what, "x, scratch and out must not overlap");
+  FusedGemv a{x, nullptr, nullptr, nullptr, nullptr, gate, up, nullptr, scratch, k * ffn, static_cast<int>(hidden),
+              0.0f};
+  a.ids = ids;
+  a.slot_rows = ffn;
+  a.experts = experts;
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  launch_fused<false, true>(s, a);
+  const int nchunks = static_cast<int>(ffn / 8);
+  const unsigned blocks = gemv_reg_blocks(hidden);
+  const int kk = static_cast<int>(k);
+  switch ((nchunks + kWave - 1) / kWave) {
+    case 1: expert_down_k<1><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, out); break;
+    case 2: expert_down_k<2><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, out); break;
+    case 3: expert_down_k<3><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, out); break;
+    default: expert_down_k<kGemvRegChunks><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, out); break;
+  }
+  return check_launch(what);
 }
 
 }  // extern "C"

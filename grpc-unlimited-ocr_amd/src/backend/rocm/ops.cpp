@@ -159,4 +159,19 @@ void scale_mask_softmax_rows(const Context& ctx, float* x, float scale, const fl
   check(uocr_rocm_scale_mask_softmax_rows(ctx.stream(), x, scale, mask, batch, rows, cols));
 }
 
+void expert_topk(const Context& ctx, const float* logits, std::int64_t rows, std::int64_t experts, std::int64_t k,
+                 std::int64_t* ids, float* weights) {
+  check(uocr_rocm_expert_topk(ctx.stream(), logits, rows, experts, k, ids, weights));
+}
+
+std::int64_t expert_scratch_floats(std::int64_t k, std::int64_t ffn) { return uocr_rocm_expert_scratch_floats(k, ffn); }
+
+void expert_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::int64_t ffn,
+                    const std::uint16_t* gate, const std::uint16_t* up, const std::uint16_t* down,
+                    std::int64_t experts, const std::int64_t* ids, const float* weights, std::int64_t k,
+                    float* scratch, float* out) {
+  check(uocr_rocm_expert_ffn_one(ctx.stream(), x, hidden, ffn, gate, up, down, experts, ids, weights, k, scratch,
+                                 out));
+}
+
 }  // namespace uocr::rocm

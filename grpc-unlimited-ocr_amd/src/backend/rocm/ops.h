@@ -123,4 +123,22 @@ void add_rms_norm_swiglu_gemv_bf16(const Context& ctx, const float* x, const flo
                                    const std::uint16_t* w_gate, const std::uint16_t* w_up, std::int64_t ffn,
                                    float* act);
 
+// ---- mixture of experts at decode (src/backend/cuda/ops.h:77-90) ------------------
+
+// Softmax over each row of gate logits [rows, experts], then the top k
+// (lower index on a tie) as expert ids and their scores.
+void expert_topk(const Context& ctx, const float* logits, std::int64_t rows, std::int64_t experts, std::int64_t k,
+                 std::int64_t* ids, float* weights);
+// Floats of scratch that expert_ffn_one needs.
+std::int64_t expert_scratch_floats(std::int64_t k, std::int64_t ffn);
+// One decode row through its k routed experts (stacks of `experts`):
+//   out[c] = sum_j weights[j] down[ids[j]] (silu(gate[ids[j]] x) * up[ids[j]] x)
+// with x and the activation rounded to bf16 for the products. The
+// reference's signature plus `experts` and `scratch`, so nothing is
+// allocated and a captured step can hold the call.
+void expert_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::int64_t ffn,
+                    const std::uint16_t* gate, const std::uint16_t* up, const std::uint16_t* down,
+                    std::int64_t experts, const std::int64_t* ids, const float* weights, std::int64_t k,
+                    float* scratch, float* out);
+
 }  // namespace uocr::rocm

@@ -413,6 +413,37 @@ UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step_bf16(void* stream, const float* 
                                                      int64_t n_tok, const float* inv_page, int64_t page_mod,
                                                      float* scratch, int64_t capacity, float* out);
 
+/* ---- mixture of experts at decode ------------------------------------------ */
+
+/* The gate's routing (src/backend/cuda/ops.h:77-81, the rule of
+ * src/model/feed_forward.cpp:36-53): softmax over each row of logits
+ * [rows, experts], then the k highest scores, the lower index first on a
+ * tie, as ids [rows, k] (descending) and their unnormalised scores weights
+ * [rows, k]. experts <= 128, 1 <= k <= experts. A row of -inf logits scores
+ * every expert 0. */
+UOCR_ROCM_API int uocr_rocm_expert_topk(void* stream, const float* logits, int64_t rows, int64_t experts, int64_t k,
+                                        int64_t* ids, float* weights);
+
+/* Floats of scratch that uocr_rocm_expert_ffn_one needs: k * ffn. */
+UOCR_ROCM_API int64_t uocr_rocm_expert_scratch_floats(int64_t k, int64_t ffn);
+
+/* One decode row x [hidden] through its k routed experts (ops.h:82-90;
+ * gemv_ops.cu:144-191), weights stacked by expert: gate/up
+ * [experts * ffn, hidden], down [experts * hidden, ffn] bf16:
+ *   out[c] = sum_j weights[j] (down[ids[j]] [c] . bf16(act_j)),
+ *   act_j = silu(gate[ids[j]] . bf16(x)) * (up[ids[j]] . bf16(x)).
+ * Bitwise, per slot, uocr_rocm_add_rms_norm_swiglu_gemv_bf16 (no norm) on
+ * the expert's gate/up rows and uocr_rocm_gemv_bf16 on its down rows, the
+ * products summed in slot order as w * d then +. New beside the reference's
+ * signature: `experts` (an id outside [0, experts) contributes nothing) and
+ * `scratch` (uocr_rocm_expert_scratch_floats(k, ffn) floats for act), so
+ * the call allocates nothing. hidden and ffn multiples of 8 in [8, 2048],
+ * k <= 8 and k * ffn <= 8192; two launches. */
+UOCR_ROCM_API int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64_t ffn,
+                                           const uint16_t* gate, const uint16_t* up, const uint16_t* down,
+                                           int64_t experts, const int64_t* ids, const float* weights, int64_t k,
+                                           float* scratch, float* out);
+
 #ifdef __cplusplus
 }
 #endif

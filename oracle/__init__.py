@@ -68,6 +68,7 @@ def lib() -> ctypes.CDLL:
             "orc_attention_one": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _f, _vp], None),
             "orc_scale_add_mask": ([_vp, _f, _vp, _i64, _i64, _i64], None),
             "orc_quick_gelu": ([_vp, _i64], None),
+            "orc_expert_topk": ([_vp, _i64, _i64, _i64, _vp, _vp], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(h, name)
@@ -267,6 +268,19 @@ def softmax_rows(x) -> np.ndarray:
     cols = x.shape[-1]
     lib().orc_softmax_rows(_p(x), x.size // cols, cols)
     return x
+
+
+def expert_topk(logits, k: int):
+    """Softmax over each row of gate logits [rows, experts], then the k top
+    scores, lower index first on a tie (src/model/feed_forward.cpp:36-53):
+    (ids int64 [rows, k], weights float32 [rows, k])."""
+    x = _f32(logits)
+    experts = x.shape[-1]
+    rows = x.size // experts
+    ids = np.empty((rows, k), np.int64)
+    w = np.empty((rows, k), np.float32)
+    lib().orc_expert_topk(_p(x), rows, experts, k, _p(ids), _p(w))
+    return ids, w
 
 
 def attention_one(q, k, v, heads: int, hd: int, bias=None, scale: float = 1.0) -> np.ndarray:

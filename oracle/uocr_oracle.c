@@ -342,6 +342,33 @@ ORC_API void orc_softmax_rows(float* x, int64_t rows, int64_t cols) {
   }
 }
 
+/* MixtureOfExperts::forward's routing (src/model/feed_forward.cpp:36-53):
+ * the gate logits go through softmax_rows, then per row the k experts of
+ * highest score, ordered by (score descending, index ascending) as the
+ * partial_sort comparator orders them, with the scores as weights
+ * (unnormalised). ids and weights [rows, k]. */
+ORC_API void orc_expert_topk(const float* logits, int64_t rows, int64_t experts, int64_t k, int64_t* ids,
+                             float* weights) {
+  float* s = (float*)malloc((size_t)experts * sizeof(float));
+  unsigned char* used = (unsigned char*)malloc((size_t)experts);
+  for (int64_t r = 0; r < rows; ++r) {
+    memcpy(s, logits + r * experts, (size_t)experts * sizeof(float));
+    orc_softmax_rows(s, 1, experts);
+    memset(used, 0, (size_t)experts);
+    for (int64_t j = 0; j < k; ++j) {
+      int64_t best = -1;
+      for (int64_t e = 0; e < experts; ++e) {
+        if (!used[e] && (best < 0 || s[e] > s[best])) best = e;  /* ties keep the lower index */
+      }
+      used[best] = 1;
+      ids[r * k + j] = best;
+      weights[r * k + j] = s[best];
+    }
+  }
+  free(used);
+  free(s);
+}
+
 /* attention_head (ops.cpp:219-251) for one query row per head: for head h,
  * s_j = dot(q_h, k_j,h) * scale (+ bias[j]), softmax as above but with the
  * probabilities p_j = exp(s_j - peak) * inv applied to v, out_h = sum p_j v_j,h;

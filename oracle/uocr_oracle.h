@@ -36,6 +36,7 @@ void orc_linear(const float* x, int64_t m, int64_t k, const float* w, int64_t n,
 void orc_softmax_rows(float* x, int64_t rows, int64_t cols);
 void orc_attention_one(const float* q, const float* k, const float* v, int64_t keys, int64_t width, int64_t heads,
                        int64_t hd, const float* bias, float scale, float* out);
+void orc_expert_topk(const float* logits, int64_t rows, int64_t experts, int64_t k, int64_t* ids, float* weights);
 void orc_scale_add_mask(float* x, float scale, const float* mask, int64_t batch, int64_t rows, int64_t cols);
 void orc_quick_gelu(float* x, int64_t n);
 

@@ -1,0 +1,118 @@
+"""GPU parity of the mixture-of-experts decode ops (src/backend/cuda/ops.h:
+77-90): the gate's top-k against the oracle's routing rule
+(src/model/feed_forward.cpp:36-53), and expert_ffn_one bitwise against the
+ops it fuses (per slot the SwiGLU pair GEMV on the expert's gate/up rows
+and the GEMV on its down rows, summed in slot order as w * d then +) and
+against the oracle's expert MLP."""
+
+import numpy as np
+import pytest
+
+import oracle
+from parity import assert_f32_close, dev_bf16, dev_f32, dev_i64, host_f32, normal
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device(backend):
+    if not torch.cuda.is_available() or backend.device_count() == 0:
+        pytest.skip("no HIP device")
+    torch.cuda.set_device(0)
+    yield
+    torch.cuda.synchronize()
+
+
+def topk(backend, logits, k):
+    rows = logits.shape[0]
+    ids = torch.empty(rows, k, dtype=torch.int64, device="cuda")
+    w = torch.empty(rows, k, device="cuda")
+    backend.expert_topk(dev_f32(logits), k, ids, w)
+    return ids.cpu().numpy(), host_f32(w)
+
+
+@pytest.mark.parametrize("rows,experts,k", [(1, 64, 6), (7, 128, 8), (300, 100, 1), (33, 8, 8), (5, 65, 3)])
+def test_expert_topk_matches_oracle(backend, rows, experts, k):
+    logits = normal(900 + experts, (rows, experts), 2.0)
+    ids, w = topk(backend, logits, k)
+    want_ids, want_w = oracle.expert_topk(logits, k)
+    assert np.array_equal(ids, want_ids), f"top-{k} of {experts} over {rows} rows"
+    assert_f32_close(w, want_w, 1e-6, "expert scores")
+
+
+def test_expert_topk_ties_and_masked_rows(backend):
+    logits = normal(910, (4, 64))
+    logits[0] = 0.0  # every score ties: ids in index order
+    logits[1, [5, 9, 40]] = 9.0  # a three-way tie at the top
+    logits[2] = -np.inf  # a fully masked row scores every expert 0
+    ids, w = topk(backend, logits, 6)
+    want_ids, want_w = oracle.expert_topk(logits, 6)
+    assert np.array_equal(ids, want_ids)
+    assert ids[0].tolist() == [0, 1, 2, 3, 4, 5] and ids[1, :3].tolist() == [5, 9, 40]
+    assert ids[2].tolist() == [0, 1, 2, 3, 4, 5] and not w[2].any()
+    assert_f32_close(w, want_w, 1e-6, "expert scores")
+
+
+def expert_stacks(seed, experts, hidden, ffn):
+    g = oracle.f32_to_bf16(normal(seed, (experts, ffn, hidden), 0.04))
+    u = oracle.f32_to_bf16(normal(seed + 1, (experts, ffn, hidden), 0.04))
+    d = oracle.f32_to_bf16(normal(seed + 2, (experts, hidden, ffn), 0.04))
+    return g, u, d
+
+
+@pytest.mark.parametrize("hidden,ffn,experts,k,bad", [(1280, 896, 64, 6, False), (64, 24, 5, 3, False),
+                                                       (256, 512, 16, 8, True), (2048, 1024, 8, 8, False),
+                                                       (128, 2048, 4, 4, False)])
+def test_expert_ffn_one_matches_its_parts_and_the_oracle(backend, hidden, ffn, experts, k, bad):
+    g, u, d = expert_stacks(920 + hidden, experts, hidden, ffn)
+    dg, du, dd = dev_bf16(g), dev_bf16(u), dev_bf16(d)
+    x = normal(930, hidden)
+    rng = np.random.default_rng(931 + k)
+    ids = rng.choice(experts, size=k, replace=False).astype(np.int64)
+    if bad:
+        ids[2] = experts + 3  # outside the stack: the slot contributes nothing
+    wts = rng.uniform(0.01, 0.3, k).astype(np.float32)
+    scratch = torch.empty(backend.expert_scratch_floats(k, ffn), device="cuda")
+    out = torch.empty(hidden, device="cuda")
+    backend.expert_ffn_one(dev_f32(x), dg, du, dd, dev_i64(ids), dev_f32(wts), scratch, out)
+    got = host_f32(out)
+    # the parts, on the device: per slot the SwiGLU pair GEMV and the down GEMV
+    total = np.zeros(hidden, np.float32)
+    want_parts = []
+    for j in range(k):
+        if not 0 <= ids[j] < experts:
+            continue
+        e = int(ids[j])
+        act = torch.empty(ffn, device="cuda")
+        backend.add_rms_norm_swiglu_gemv_bf16(dev_f32(x), dg[e], du[e], act)
+        dj = torch.empty(hidden, device="cuda")
+        backend.gemv_bf16(act, dd[e], dj)
+        total = total + np.float32(wts[j]) * host_f32(dj)
+        want_parts.append((e, j))
+    assert np.array_equal(got.view(np.uint32), total.view(np.uint32)), f"expert_ffn_one {hidden}x{ffn} k={k}"
+    # the oracle's expert MLP, with x and act rounded to bf16 as the device rounds them
+    xb = oracle.bf16_round(x)
+    want = np.zeros(hidden, np.float32)
+    for e, j in want_parts:
+        gg = oracle.linear(xb[None], oracle.bf16_to_f32(g[e]))[0]
+        uu = oracle.linear(xb[None], oracle.bf16_to_f32(u[e]))[0]
+        act = oracle.bf16_round(oracle.silu_mul(gg, uu))
+        want = want + np.float32(wts[j]) * oracle.linear(act[None], oracle.bf16_to_f32(d[e]))[0]
+    # the bf16 rounding of act can flip between two fp32 sums that differ
+    # in their last bit (2^-8 of one element): 2e-4 relative
+    assert_f32_close(got, want, 2e-4, "expert_ffn_one vs oracle")
+
+
+def test_expert_ffn_one_rejects_bad_shapes(backend):
+    x = torch.zeros(64, device="cuda")
+    g = torch.zeros(4, 24, 64, dtype=torch.bfloat16, device="cuda")
+    d = torch.zeros(4, 64, 24, dtype=torch.bfloat16, device="cuda")
+    ids, w = dev_i64([0, 1]), dev_f32([0.5, 0.5])
+    out = torch.empty(64, device="cuda")
+    with pytest.raises(ValueError):  # scratch too small
+        backend.expert_ffn_one(x, g, g, d, ids, w, torch.empty(10, device="cuda"), out)
+    with pytest.raises(ValueError):  # k above 8
+        backend.expert_ffn_one(x, g, g, d, dev_i64(list(range(4)) * 3), dev_f32([0.1] * 12),
+                               torch.empty(12 * 24, device="cuda"), out)

@@ -543,3 +543,31 @@ def test_oracle_bit_equals_reference_row_ops(orc, ref):
     r2 = qx.copy()
     ref.ref_quick_gelu(_p(r2), r2.size)
     assert np.array_equal(r2.view(np.uint32), orc.quick_gelu(qx).view(np.uint32))
+
+
+def test_expert_topk_known_answer_ties_and_brute_force(orc):
+    """The routing rule of src/model/feed_forward.cpp:36-53: softmax, then
+    the k top scores with the lower index first on a tie."""
+    ids, w = orc.expert_topk(np.array([[1.0, 2.0, 3.0, 2.0]], np.float32), 3)
+    assert ids.tolist() == [[2, 1, 3]]  # 1 and 3 tie: the lower index first
+    e = np.exp(np.array([1.0, 2.0, 3.0, 2.0]) - 3.0)
+    assert np.allclose(w[0], (e / e.sum())[[2, 1, 3]], rtol=1e-6)
+    # equal logits: every score ties, so the ids come out in index order
+    ids, w = orc.expert_topk(np.zeros((1, 7), np.float32), 7)
+    assert ids.tolist() == [list(range(7))] and np.allclose(w, 1 / 7)
+    # a row of -inf logits scores every expert 0 (softmax_rows' masked row)
+    ids, w = orc.expert_topk(np.full((1, 5), -np.inf, np.float32), 2)
+    assert ids.tolist() == [[0, 1]] and not w.any()
+    # brute force: a stable sort on (-score, index) over the oracle's own scores
+    g = np.random.default_rng(77)
+    logits = g.standard_normal((40, 64)).astype(np.float32)
+    logits[:, 10] = logits[:, 11] = 5.0  # an exact tie at the top of every row
+    ids, w = orc.expert_topk(logits, 6)
+    scores = orc.softmax_rows(logits.copy())
+    for r in range(40):
+        order = sorted(range(64), key=lambda e: (-scores[r, e], e))[:6]
+        assert ids[r].tolist() == order and np.array_equal(w[r], scores[r, order])
+        assert ids[r, :2].tolist() == [10, 11]
+    # a planted slip (ties to the higher index) fails the same check
+    slip = sorted(range(64), key=lambda e: (-scores[0, e], -e))[:6]
+    assert slip != ids[0].tolist()
