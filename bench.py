@@ -521,6 +521,7 @@ def config7(be, torch, timer):
     xl, yl = torch.randn(lm_k, device="cuda"), torch.empty(lm_n, device="cuda")
     kern["gemv_bf16_lm_head"] = report("gemv lm head", bytes_gemv(lm_n, lm_k), time_kernel(
         timer, lambda: bf16_randn(torch, (lm_n, lm_k), 0.03), lambda w: be.gemv_bf16(xl, w, yl)))
+    kern["expert_ffn_one_6_of_64"] = expert_ffn(be, torch, timer, hidden, ffn, 64, 6)
     whole = decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, scratch, b, lm_n)
     return {"workload": "fp32 decode layer at batch 1, hidden 1280, 10 heads x 128, FFN 896, KV cache 8192, fused "
                         "(6 launches): add+RMSNorm+GEMV qkv -> RoPE+append+attend (2) -> GEMV o -> add+RMSNorm+GEMV "
@@ -533,6 +534,24 @@ def config7(be, torch, timer):
                               "us_per_layer_graph": round(ms_bf16_kv * 1e3, 3)},
             "bytes_by_op": b, "attend_splits": splits, "kernels": kern, "sets": nsets,
             "decode_step_12_layers": whole}
+
+
+def expert_ffn(be, torch, timer, hidden, ffn, experts, k):
+    """The routed experts of one decode row (expert_ffn_one) on the model's
+    MoE shape: 6 of 64 experts of FFN 896 at hidden 1280, stacks of 440 MB
+    rotated past the Infinity Cache, and a fresh choice of ids per stack."""
+    g = torch.Generator().manual_seed(7)
+
+    def make():
+        ids = torch.randperm(experts, generator=g)[:k].to(torch.int64).cuda()
+        return (bf16_randn(torch, (experts * ffn, hidden), 0.03), bf16_randn(torch, (experts * ffn, hidden), 0.03),
+                bf16_randn(torch, (experts, hidden, ffn), 0.03), ids)
+    x, out = torch.randn(hidden, device="cuda"), torch.empty(hidden, device="cuda")
+    wts = torch.full((k,), 1.0 / k, device="cuda")
+    scratch = torch.empty(be.expert_scratch_floats(k, ffn), device="cuda")
+    nbytes = 3 * k * ffn * hidden * 2 + 2 * hidden * 4 + 2 * k * ffn * 4
+    ms = time_kernel(timer, make, lambda s: be.expert_ffn_one(x, s[0], s[1], s[2], s[3], wts, scratch, out))
+    return report("expert_ffn_one", nbytes, ms)
 
 
 def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, scratch, b, vocab, layers=12):

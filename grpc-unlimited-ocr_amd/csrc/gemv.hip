@@ -583,16 +583,10 @@ __global__ __launch_bounds__(kGemvBlock) void expert_down_k(const float* __restr
   __shared__ __align__(16) float xs[kExpertActFloats];
   const int lane = threadIdx.x & (kWave - 1);
   const int ffn = nchunks * 8;
-  for (int t = threadIdx.x; t < 2 * nchunks * k; t += kGemvBlock) {
-    float v[4];
-    load_f32<4>(act + 4 * static_cast<int64_t>(t), v);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) xs[4 * t + e] = round_bf16(v[e]);
-  }
-  __syncthreads();
   const int64_t step = static_cast<int64_t>(gridDim.x) * kGemvWaves;
-  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kGemvWaves + threadIdx.x / kWave; c < hidden; c += step) {
-    u32x4 wc[kMaxExpertSlots][CPL];
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kGemvWaves + threadIdx.x / kWave;
+  u32x4 wc[kMaxExpertSlots][CPL];
+  auto load_rows = [&](int64_t c) {
 #pragma unroll
     for (int j = 0; j < kMaxExpertSlots; ++j) {
       const int64_t id = j < k ? ids[j] : 0;
@@ -604,6 +598,19 @@ __global__ __launch_bounds__(kGemvBlock) void expert_down_k(const float* __restr
         if (live && ci < nchunks) wc[j][i] = stream_load(reinterpret_cast<const u32x4*>(down + (id * hidden + c) * ffn) + ci);
       }
     }
+  };
+  // The first rows' weights go out before act is staged (they depend only
+  // on the ids), so both are in flight together, as in gemv_reg.
+  if (c0 < hidden) load_rows(c0);
+  for (int t = threadIdx.x; t < 2 * nchunks * k; t += kGemvBlock) {
+    float v[4];
+    load_f32<4>(act + 4 * static_cast<int64_t>(t), v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xs[4 * t + e] = round_bf16(v[e]);
+  }
+  __syncthreads();
+  for (int64_t c = c0; c < hidden; c += step) {
+    if (c != c0) load_rows(c);
     float total = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxExpertSlots; ++j) {
