@@ -555,8 +555,8 @@ def expert_ffn(be, torch, timer, hidden, ffn, experts, k):
 
 
 def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, scratch, b, vocab, layers=12):
-    """A whole decode step as one graph, the C++ DenseDecodeStep's body
-    (src/model/rocm/dense_decode_step.cpp) at 12 layers: the embedding row,
+    """A whole decode step as one graph, the C++ DecodeStep's body
+    (src/model/rocm/decode_step.cpp) at 12 layers: the embedding row,
     12 fused layers over bf16 key/value caches of 8192 positions read in
     full, the final norm fused into the LM-head GEMV. Every layer has the
     dense FFN of 896 (the model's layers 1-11 are mixture-of-experts, whose

@@ -132,7 +132,8 @@ _SIGNATURES = {
                                        _i64, _vp, _i64, _vp], _int),
     "uocr_rocm_expert_topk": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp], _int),
     "uocr_rocm_expert_scratch_floats": ([_i64, _i64], _i64),
-    "uocr_rocm_expert_ffn_one": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_expert_ffn_one": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp], _int),
+    "uocr_rocm_gemv_f32": ([_vp, _vp, _i64, _vp, _i64, _vp, _vp], _int),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -531,7 +532,16 @@ def expert_scratch_floats(k: int, ffn: int) -> int:
     return int(lib().uocr_rocm_expert_scratch_floats(k, ffn))
 
 
-def expert_ffn_one(x, gate, up, down, ids, weights, scratch, out, stream=None):
+def gemv_f32(x, w, y, bias=None, stream=None):
+    """y = x . w^T (+ bias) with float32 weights w [n, k], x not rounded: the
+    gate logits (src/model/cuda/cuda_decoder.cpp:141-142)."""
+    n, k = w.shape
+    if w.dtype != _torch().float32 or x.numel() != k or y.numel() != n:
+        raise ValueError("gemv_f32: float32 w [n, k], x [k], y [n]")
+    _op("uocr_rocm_gemv_f32", stream, _ptr(x), k, _ptr(w), n, _f32_param(bias), _ptr(y))
+
+
+def expert_ffn_one(x, gate, up, down, ids, weights, scratch, out, base=None, stream=None):
     """One decode row x [hidden] through its k routed experts: gate/up
     [experts, ffn, hidden] (or [experts * ffn, hidden]) and down [experts,
     hidden, ffn] bf16 stacks, ids [k] int64, weights [k] float32.
@@ -544,5 +554,7 @@ def expert_ffn_one(x, gate, up, down, ids, weights, scratch, out, stream=None):
         raise ValueError("expert_ffn_one shapes: gate/up [experts, ffn, hidden], down [experts, hidden, ffn]")
     if weights.numel() != k or scratch.numel() < expert_scratch_floats(k, ffn):
         raise ValueError("expert_ffn_one: weights [k] and scratch of expert_scratch_floats(k, ffn) floats")
+    if base is not None and base.numel() != hidden:
+        raise ValueError("expert_ffn_one: base [hidden]")
     _op("uocr_rocm_expert_ffn_one", stream, _ptr(x), hidden, ffn, _ptr(gate), _ptr(up), _ptr(down), experts,
-        _ptr(ids), _ptr(weights), k, _ptr(scratch), _ptr(out))
+        _ptr(ids), _ptr(weights), k, _ptr(base), _ptr(scratch), _ptr(out))

@@ -579,7 +579,7 @@ __global__ __launch_bounds__(kGemvBlock) void expert_down_k(const float* __restr
                                                             const uint16_t* __restrict__ down, int64_t hidden,
                                                             const int64_t* __restrict__ ids,
                                                             const float* __restrict__ wts, int k, int64_t experts,
-                                                            float* __restrict__ out) {
+                                                            const float* base, float* out) {
   __shared__ __align__(16) float xs[kExpertActFloats];
   const int lane = threadIdx.x & (kWave - 1);
   const int ffn = nchunks * 8;
@@ -635,7 +635,40 @@ __global__ __launch_bounds__(kGemvBlock) void expert_down_k(const float* __restr
         }
       }
     }
-    if (lane == 0) out[c] = total;
+    if (lane == 0) out[c] = base != nullptr ? base[c] + total : total;
+  }
+}
+
+// y[n] = x . w[n, :] (+ bias[n]) with fp32 weights and no rounding of x: the
+// mixture-of-experts gate, which the reference keeps in fp32 for routing
+// (moe_gate_f32, src/model/cuda/cuda_decoder.cpp:141-142). One wave per row,
+// 16-byte chunks when k and the pointers allow, a wave butterfly.
+template <bool kVec>
+__global__ __launch_bounds__(kBlock) void gemv_f32_k(const float* __restrict__ x, int64_t k,
+                                                     const float* __restrict__ w, int64_t n,
+                                                     const float* __restrict__ bias, float* __restrict__ y) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave; row < n; row += step) {
+    const float* wr = w + row * k;
+    float a = 0.0f;
+    if constexpr (kVec) {
+      for (int64_t c = lane; c < k / 4; c += kWave) {
+        float xv[4], wv[4];
+        load_f32<4>(x + 4 * c, xv);
+        const u32x4 q = stream_load(reinterpret_cast<const u32x4*>(wr) + c);
+        wv[0] = __uint_as_float(q.x);
+        wv[1] = __uint_as_float(q.y);
+        wv[2] = __uint_as_float(q.z);
+        wv[3] = __uint_as_float(q.w);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a = fmaf(xv[e], wv[e], a);
+      }
+    } else {
+      for (int64_t c = lane; c < k; c += kWave) a = fmaf(x[c], wr[c], a);
+    }
+    a = wave_sum(a);
+    if (lane == 0) y[row] = a + (bias != nullptr ? bias[row] : 0.0f);
   }
 }
 
@@ -696,6 +729,23 @@ int uocr_rocm_add_rms_norm_swiglu_gemv_bf16(void* stream, const float* x, const 
                                eps});
 }
 
+int uocr_rocm_gemv_f32(void* stream, const float* x, int64_t k, const float* w, int64_t n, const float* bias,
+                       float* y) {
+  const char* what = "uocr_rocm_gemv_f32";
+  UOCR_REQUIRE(k >= 0 && n >= 0, what, "k and n must be >= 0");
+  if (n == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(y != nullptr && (k == 0 || (x != nullptr && w != nullptr)), what, "null pointer");
+  UOCR_REQUIRE(n < (int64_t{1} << 40) && k < (int64_t{1} << 40), what, "n or k too large");
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  if (k % 4 == 0 && aligned16(x) && aligned16(w)) {
+    gemv_f32_k<true><<<gemv_blocks(n), kBlock, 0, s>>>(x, k, w, n, bias, y);
+  } else {
+    gemv_f32_k<false><<<gemv_blocks(n), kBlock, 0, s>>>(x, k, w, n, bias, y);
+  }
+  return check_launch(what);
+}
+
 int uocr_rocm_expert_topk(void* stream, const float* logits, int64_t rows, int64_t experts, int64_t k, int64_t* ids,
                           float* weights) {
   const char* what = "uocr_rocm_expert_topk";
@@ -715,7 +765,7 @@ int64_t uocr_rocm_expert_scratch_floats(int64_t k, int64_t ffn) { return k > 0 &
 
 int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64_t ffn, const uint16_t* gate,
                              const uint16_t* up, const uint16_t* down, int64_t experts, const int64_t* ids,
-                             const float* weights, int64_t k, float* scratch, float* out) {
+                             const float* weights, int64_t k, const float* base, float* scratch, float* out) {
   const char* what = "uocr_rocm_expert_ffn_one";
   UOCR_REQUIRE(hidden % 8 == 0 && hidden >= 8 && hidden <= kFusedMaxK, what,
                "hidden must be a multiple of 8 in [8, 2048]");
@@ -731,8 +781,8 @@ int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64
                "x, the weights and scratch must be 16-byte aligned");
   auto overlaps = [](const float* a, int64_t na, const float* b, int64_t nb) { return a < b + nb && b < a + na; };
   UOCR_REQUIRE(!overlaps(scratch, k * ffn, x, hidden) && !overlaps(scratch, k * ffn, out, hidden) &&
-                   !overlaps(out, hidden, x, hidden),
-               what, "x, scratch and out must not overlap");
+                   !overlaps(out, hidden, x, hidden) && (base == nullptr || !overlaps(scratch, k * ffn, base, hidden)),
+               what, "x, base, scratch and out must not overlap (base may be out itself)");
   FusedGemv a{x, nullptr, nullptr, nullptr, nullptr, gate, up, nullptr, scratch, k * ffn, static_cast<int>(hidden),
               0.0f};
   a.ids = ids;
@@ -745,10 +795,10 @@ int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64
   const unsigned blocks = gemv_reg_blocks(hidden);
   const int kk = static_cast<int>(k);
   switch ((nchunks + kWave - 1) / kWave) {
-    case 1: expert_down_k<1><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, out); break;
-    case 2: expert_down_k<2><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, out); break;
-    case 3: expert_down_k<3><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, out); break;
-    default: expert_down_k<kGemvRegChunks><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, out); break;
+    case 1: expert_down_k<1><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, base, out); break;
+    case 2: expert_down_k<2><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, base, out); break;
+    case 3: expert_down_k<3><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, base, out); break;
+    default: expert_down_k<kGemvRegChunks><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, base, out); break;
   }
   return check_launch(what);
 }

@@ -169,9 +169,14 @@ std::int64_t expert_scratch_floats(std::int64_t k, std::int64_t ffn) { return uo
 void expert_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::int64_t ffn,
                     const std::uint16_t* gate, const std::uint16_t* up, const std::uint16_t* down,
                     std::int64_t experts, const std::int64_t* ids, const float* weights, std::int64_t k,
-                    float* scratch, float* out) {
-  check(uocr_rocm_expert_ffn_one(ctx.stream(), x, hidden, ffn, gate, up, down, experts, ids, weights, k, scratch,
-                                 out));
+                    const float* base, float* scratch, float* out) {
+  check(uocr_rocm_expert_ffn_one(ctx.stream(), x, hidden, ffn, gate, up, down, experts, ids, weights, k, base,
+                                 scratch, out));
+}
+
+void gemv_f32(const Context& ctx, const float* x, std::int64_t k, const float* w, std::int64_t n, const float* bias,
+              float* y) {
+  check(uocr_rocm_gemv_f32(ctx.stream(), x, k, w, n, bias, y));
 }
 
 }  // namespace uocr::rocm

@@ -136,9 +136,13 @@ std::int64_t expert_scratch_floats(std::int64_t k, std::int64_t ffn);
 // with x and the activation rounded to bf16 for the products. The
 // reference's signature plus `experts` and `scratch`, so nothing is
 // allocated and a captured step can hold the call.
+// With base set, out = base + the routed sum (base may be out itself).
 void expert_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::int64_t ffn,
                     const std::uint16_t* gate, const std::uint16_t* up, const std::uint16_t* down,
                     std::int64_t experts, const std::int64_t* ids, const float* weights, std::int64_t k,
-                    float* scratch, float* out);
+                    const float* base, float* scratch, float* out);
+// y[n] = x . w[n, :] (+ bias) with fp32 weights: the gate logits.
+void gemv_f32(const Context& ctx, const float* x, std::int64_t k, const float* w, std::int64_t n, const float* bias,
+              float* y);
 
 }  // namespace uocr::rocm

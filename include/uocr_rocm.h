@@ -435,14 +435,24 @@ UOCR_ROCM_API int64_t uocr_rocm_expert_scratch_floats(int64_t k, int64_t ffn);
  * Bitwise, per slot, uocr_rocm_add_rms_norm_swiglu_gemv_bf16 (no norm) on
  * the expert's gate/up rows and uocr_rocm_gemv_bf16 on its down rows, the
  * products summed in slot order as w * d then +. New beside the reference's
- * signature: `experts` (an id outside [0, experts) contributes nothing) and
- * `scratch` (uocr_rocm_expert_scratch_floats(k, ffn) floats for act), so
- * the call allocates nothing. hidden and ffn multiples of 8 in [8, 2048],
+ * signature: `experts` (an id outside [0, experts) contributes nothing),
+ * `base` (null, or a vector added last: out[c] = base[c] + sum, bitwise
+ * the shared experts' output followed by add_inplace of the routed sum,
+ * cuda_decoder.cpp:149-151; base may be out itself) and `scratch`
+ * (uocr_rocm_expert_scratch_floats(k, ffn) floats for act), so the call
+ * allocates nothing. hidden and ffn multiples of 8 in [8, 2048],
  * k <= 8 and k * ffn <= 8192; two launches. */
 UOCR_ROCM_API int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64_t ffn,
                                            const uint16_t* gate, const uint16_t* up, const uint16_t* down,
                                            int64_t experts, const int64_t* ids, const float* weights, int64_t k,
-                                           float* scratch, float* out);
+                                           const float* base, float* scratch, float* out);
+
+/* y[n] = x . w[n, :] (+ bias[n]) with fp32 weights, x not rounded: the
+ * mixture-of-experts gate logits, which the reference forms from fp32 gate
+ * weights with an fp32 GEMM (moe_gate_f32, src/model/cuda/cuda_decoder.cpp:
+ * 141-142; linear, src/backend/reference/ops.cpp:91-108). */
+UOCR_ROCM_API int uocr_rocm_gemv_f32(void* stream, const float* x, int64_t k, const float* w, int64_t n,
+                                     const float* bias, float* y);
 
 #ifdef __cplusplus
 }

@@ -4,8 +4,9 @@
 // std::mt19937(5), the same relative-error metric, the same tolerances for
 // the fp32 ops, plus the bf16-activation ops at 2 bf16 ulp, the fused ops,
 // a captured decode step replayed at three StepStates, one decoder layer's
-// fused step against its unfused ops, the captured whole-step dense decoder
-// against the oracle's, and the error convention. Exits 77 (skip) without a
+// fused step against its unfused ops, the captured whole-step decoder (a
+// dense and a mixture-of-experts layer) against the oracle's, and the error
+// convention. Exits 77 (skip) without a
 // HIP device.
 
 #include <algorithm>
@@ -23,7 +24,7 @@
 #include "backend/rocm/decode_ops.h"
 #include "backend/rocm/dtype.h"
 #include "backend/rocm/ops.h"
-#include "model/rocm/dense_decode_step.h"
+#include "model/rocm/decode_step.h"
 #include "../../oracle/uocr_oracle.h"
 
 namespace ro = uocr::rocm;
@@ -437,75 +438,104 @@ void fused_decode_layer(const ro::Context& ctx) {
   }
 }
 
-void dense_decode_step(const ro::Context& ctx, bool bf16_cache) {
-  // The captured whole-step decoder (embedding, 2 layers, final norm, LM
-  // head) fed 8 tokens in sequence, each step's logits held to the oracle's
-  // decoder on the same weights and cache rounding. The GEMVs round their
-  // inputs to bf16, so a one-ulp difference in an fp32 sum upstream can flip
-  // one input's rounding (2^-8 of that element) now and then: every step is
-  // held to 1e-2, and most steps (the median) to 1e-5.
-  ro::DenseDecoderDims d;
+void decode_step(const ro::Context& ctx, bool bf16_cache) {
+  // The captured whole-step decoder (embedding, a dense layer, a
+  // mixture-of-experts layer, final norm, LM head) fed 8 tokens in
+  // sequence, each step's logits held to the oracle's decoder on the same
+  // weights and cache rounding. The GEMVs round their inputs to bf16, so a
+  // one-ulp difference in an fp32 sum upstream can flip one input's rounding
+  // (2^-8 of that element) now and then: every step is held to 1e-2, and
+  // most steps (the median) to 1e-5.
+  ro::DecoderDims d;
   d.hidden = 256;
   d.heads = 4;
   d.head_dim = 64;
-  d.ffn = 192;
   d.vocab = 500;
   d.capacity = 64;
   d.bf16_cache = bf16_cache;
-  const std::int64_t H = d.hidden, W = d.heads * d.head_dim, F = d.ffn, V = d.vocab, half = d.head_dim / 2;
-  const int layers = 2;
+  const std::int64_t H = d.hidden, W = d.heads * d.head_dim, V = d.vocab, half = d.head_dim / 2;
+  const std::int64_t F = 192, E = 8, K = 2, EF = 64, SF = 128;
   auto norm_w = [&](std::int64_t n) {
     auto w = random(static_cast<std::size_t>(n), 0.02f);
     for (float& v : w) v += 1.0f;
     return w;
   };
-  const auto embed = bf16_rounded(random(V * H, 0.5f)), lm = bf16_rounded(random(V * H, 0.05f));
+  auto bw = [&](std::int64_t n, float sc) { return bf16_rounded(random(static_cast<std::size_t>(n), sc)); };
+  const auto embed = bw(V * H, 0.5f), lm = bw(V * H, 0.05f);
   const auto final_norm = norm_w(H);
   struct HostLayer {
-    std::vector<float> in, qkv, o, post, gate, up, down;
+    std::vector<float> in, qkv, o, post, gate, up, down;            // dense: [F, H], [F, H], [H, F]
+    std::vector<float> router, gstack, ustack, dstack, sg, su, sd;  // mixture of experts
+    bool moe;
   };
-  std::vector<HostLayer> hl(layers);
-  for (auto& l : hl) {
-    l = {norm_w(H), bf16_rounded(random(3 * W * H, 0.06f)), bf16_rounded(random(H * W, 0.06f)), norm_w(H),
-         bf16_rounded(random(F * H, 0.06f)), bf16_rounded(random(F * H, 0.06f)), bf16_rounded(random(H * F, 0.07f))};
-  }
+  std::vector<HostLayer> hl(2);
+  hl[0] = {norm_w(H), bw(3 * W * H, 0.06f), bw(H * W, 0.06f), norm_w(H), bw(F * H, 0.06f), bw(F * H, 0.06f),
+           bw(H * F, 0.07f), {}, {}, {}, {}, {}, {}, {}, false};
+  hl[1] = {norm_w(H), bw(3 * W * H, 0.06f), bw(H * W, 0.06f), norm_w(H), {}, {}, {}, random(E * H, 0.1f),
+           bw(E * EF * H, 0.06f), bw(E * EF * H, 0.06f), bw(E * H * EF, 0.07f), bw(SF * H, 0.06f),
+           bw(SF * H, 0.06f), bw(H * SF, 0.07f), true};
   std::vector<ro::Array> keep;
   auto dev = [&](const std::vector<float>& v, ro::DType t) {
     keep.push_back(up(ctx, v, t));
     return keep.back().data();
   };
-  std::vector<ro::DenseLayerWeights> lw;
-  for (const auto& l : hl) {
-    lw.push_back({static_cast<const float*>(dev(l.in, ro::DType::kF32)),
-                  static_cast<const std::uint16_t*>(dev(l.qkv, ro::DType::kBF16)),
-                  static_cast<const std::uint16_t*>(dev(l.o, ro::DType::kBF16)),
-                  static_cast<const float*>(dev(l.post, ro::DType::kF32)),
-                  static_cast<const std::uint16_t*>(dev(l.gate, ro::DType::kBF16)),
-                  static_cast<const std::uint16_t*>(dev(l.up, ro::DType::kBF16)),
-                  static_cast<const std::uint16_t*>(dev(l.down, ro::DType::kBF16))});
+  auto b16 = [&](const std::vector<float>& v) { return static_cast<const std::uint16_t*>(dev(v, ro::DType::kBF16)); };
+  auto f32 = [&](const std::vector<float>& v) { return static_cast<const float*>(dev(v, ro::DType::kF32)); };
+  ro::MoeWeights moe;
+  std::vector<ro::LayerWeights> lw(2);
+  for (int li = 0; li < 2; ++li) {
+    const auto& l = hl[li];
+    lw[li].input_norm = f32(l.in);
+    lw[li].qkv = b16(l.qkv);
+    lw[li].o = b16(l.o);
+    lw[li].post_norm = f32(l.post);
+    if (!l.moe) {
+      lw[li].gate = b16(l.gate);
+      lw[li].up = b16(l.up);
+      lw[li].down = b16(l.down);
+      lw[li].ffn = F;
+    } else {
+      moe.gate = f32(l.router);
+      moe.gate_stack = b16(l.gstack);
+      moe.up_stack = b16(l.ustack);
+      moe.down_stack = b16(l.dstack);
+      moe.experts = E;
+      moe.top_k = K;
+      moe.expert_ffn = EF;
+      moe.shared_gate = b16(l.sg);
+      moe.shared_up = b16(l.su);
+      moe.shared_down = b16(l.sd);
+      moe.shared_ffn = SF;
+      lw[li].moe = &moe;
+    }
   }
-  const auto* demb = static_cast<const std::uint16_t*>(dev(embed, ro::DType::kBF16));
-  const auto* dfin = static_cast<const float*>(dev(final_norm, ro::DType::kF32));
-  const auto* dlm = static_cast<const std::uint16_t*>(dev(lm, ro::DType::kBF16));
-  ro::DenseDecodeStep step(ctx, d, demb, lw, dfin, dlm);
+  ro::DecodeStep step(ctx, d, b16(embed), lw, f32(final_norm), b16(lm));
 
-  // The oracle's decoder: the GEMVs' inputs rounded to bf16, the caches
-  // holding what the device caches hold.
+  // The oracle's decoder: the GEMVs' inputs rounded to bf16 (the router's
+  // fp32 product not), the caches holding what the device caches hold.
   const auto inv = rope_inv(half, d.rope_theta);
-  std::vector<std::vector<float>> kc(layers, std::vector<float>(d.capacity * W, 0.0f)), vc = kc;
-  auto linear = [](const std::vector<float>& x, const std::vector<float>& w, std::int64_t n) {
+  std::vector<std::vector<float>> kc(2, std::vector<float>(d.capacity * W, 0.0f)), vc = kc;
+  auto linear = [](const std::vector<float>& x, const float* w, std::int64_t n, bool round = true) {
     std::vector<float> y(static_cast<std::size_t>(n));
-    orc_linear(bf16_rounded(x).data(), 1, static_cast<std::int64_t>(x.size()), w.data(), n, nullptr, y.data());
+    const auto xin = round ? bf16_rounded(x) : x;
+    orc_linear(xin.data(), 1, static_cast<std::int64_t>(x.size()), w, n, nullptr, y.data());
     return y;
+  };
+  auto swiglu_mlp = [&](const std::vector<float>& h, const float* g, const float* u, const float* dn,
+                        std::int64_t ffn) {
+    auto gg = linear(h, g, ffn);
+    const auto uu = linear(h, u, ffn);
+    orc_silu(gg.data(), ffn);
+    orc_mul_into(gg.data(), uu.data(), ffn);
+    return linear(gg, dn, H);
   };
   const float scale = 1.0f / std::sqrt(static_cast<float>(d.head_dim));
   std::vector<double> errs;
   for (std::int64_t pos = 0; pos < 8; ++pos) {
     const std::int64_t token = static_cast<std::int64_t>(rng() % static_cast<unsigned>(V));
     const auto got = step.step(token, pos);
-    std::vector<float> x(H), h(H), pending;
-    for (std::int64_t c = 0; c < H; ++c) x[c] = embed[token * H + c];
-    for (int li = 0; li < layers; ++li) {
+    std::vector<float> x(embed.begin() + token * H, embed.begin() + (token + 1) * H), h(H), pending;
+    for (int li = 0; li < 2; ++li) {
       const auto& l = hl[li];
       if (pending.empty()) {
         h = x;
@@ -513,7 +543,7 @@ void dense_decode_step(const ro::Context& ctx, bool bf16_cache) {
       } else {
         orc_add_rms_norm(x.data(), pending.data(), l.in.data(), h.data(), 1, H, d.eps);
       }
-      auto qkv = linear(h, l.qkv, 3 * W);
+      auto qkv = linear(h, l.qkv.data(), 3 * W);
       orc_rope_apply(qkv.data(), 1, 2 * d.heads, d.head_dim, nullptr, nullptr, inv.data(), half, nullptr, 0, 0, pos, 0);
       for (std::int64_t c = 0; c < W; ++c) {
         float kk = qkv[W + c], vv = qkv[2 * W + c];
@@ -527,16 +557,33 @@ void dense_decode_step(const ro::Context& ctx, bool bf16_cache) {
       std::vector<float> attn(W);
       orc_attention_one(qkv.data(), kc[li].data(), vc[li].data(), pos + 1, W, d.heads, d.head_dim, nullptr, scale,
                         attn.data());
-      const auto o = linear(attn, l.o, H);
+      const auto o = linear(attn, l.o.data(), H);
       orc_add_rms_norm(x.data(), o.data(), l.post.data(), h.data(), 1, H, d.eps);
-      auto g = linear(h, l.gate, F);
-      const auto u = linear(h, l.up, F);
-      orc_silu(g.data(), F);
-      orc_mul_into(g.data(), u.data(), F);
-      pending = linear(g, l.down, H);
+      if (!l.moe) {
+        pending = swiglu_mlp(h, l.gate.data(), l.up.data(), l.down.data(), F);
+      } else {
+        // MixtureOfExperts::forward (src/model/feed_forward.cpp:36-77) for one row
+        pending = swiglu_mlp(h, l.sg.data(), l.su.data(), l.sd.data(), SF);
+        const auto logits = linear(h, l.router.data(), E, false);
+        std::vector<std::int64_t> ids(K);
+        std::vector<float> wts(K);
+        orc_expert_topk(logits.data(), 1, E, K, ids.data(), wts.data());
+        // contributions added in expert order, as the reference adds them
+        std::vector<std::int64_t> order(static_cast<std::size_t>(K));
+        for (std::int64_t j = 0; j < K; ++j) order[static_cast<std::size_t>(j)] = j;
+        std::sort(order.begin(), order.end(), [&](std::int64_t a, std::int64_t b) { return ids[a] < ids[b]; });
+        std::vector<float> routed(H, 0.0f);
+        for (const std::int64_t j : order) {
+          const std::int64_t e = ids[static_cast<std::size_t>(j)];
+          const auto y = swiglu_mlp(h, l.gstack.data() + e * EF * H, l.ustack.data() + e * EF * H,
+                                    l.dstack.data() + e * H * EF, EF);
+          for (std::int64_t c = 0; c < H; ++c) routed[c] += wts[static_cast<std::size_t>(j)] * y[c];
+        }
+        for (std::int64_t c = 0; c < H; ++c) pending[c] += routed[c];
+      }
     }
     orc_add_rms_norm(x.data(), pending.data(), final_norm.data(), h.data(), 1, H, d.eps);
-    const auto want = linear(h, lm, V);
+    const auto want = linear(h, lm.data(), V);
     char what[64];
     std::snprintf(what, sizeof what, "decode step %s pos %lld", bf16_cache ? "bf16" : "fp32",
                   static_cast<long long>(pos));
@@ -633,8 +680,8 @@ int main() {
     decode_graph(ctx);
     step_ops(ctx);
     fused_decode_layer(ctx);
-    dense_decode_step(ctx, true);
-    dense_decode_step(ctx, false);
+    decode_step(ctx, true);
+    decode_step(ctx, false);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());

@@ -116,3 +116,34 @@ def test_expert_ffn_one_rejects_bad_shapes(backend):
     with pytest.raises(ValueError):  # k above 8
         backend.expert_ffn_one(x, g, g, d, dev_i64(list(range(4)) * 3), dev_f32([0.1] * 12),
                                torch.empty(12 * 24, device="cuda"), out)
+
+
+def test_expert_ffn_one_adds_base_last(backend):
+    """out = base + the routed sum, bitwise the shared experts' output and
+    add_inplace of the routed sum (src/model/cuda/cuda_decoder.cpp:149-151),
+    also with base and out the same buffer."""
+    hidden, ffn, experts, k = 1280, 896, 16, 6
+    g, u, d = expert_stacks(940, experts, hidden, ffn)
+    dg, du, dd = dev_bf16(g), dev_bf16(u), dev_bf16(d)
+    x, base = dev_f32(normal(941, hidden)), dev_f32(normal(942, hidden))
+    ids, wts = dev_i64([3, 0, 15, 7, 8, 1]), dev_f32([0.3, 0.2, 0.15, 0.1, 0.05, 0.02])
+    scratch = torch.empty(backend.expert_scratch_floats(k, ffn), device="cuda")
+    routed, out = torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda")
+    backend.expert_ffn_one(x, dg, du, dd, ids, wts, scratch, routed)
+    backend.expert_ffn_one(x, dg, du, dd, ids, wts, scratch, out, base=base)
+    want = base.clone()
+    backend.add_inplace(want, routed)
+    assert torch.equal(out.view(torch.int32), want.view(torch.int32))
+    inplace = base.clone()
+    backend.expert_ffn_one(x, dg, du, dd, ids, wts, scratch, inplace, base=inplace)
+    assert torch.equal(inplace.view(torch.int32), want.view(torch.int32))
+
+
+@pytest.mark.parametrize("n,k", [(64, 1280), (13, 37), (100, 2048)])
+def test_gemv_f32_matches_oracle(backend, n, k):
+    w, x, bias = normal(950, (n, k), 0.05), normal(951, k), normal(952, n)
+    y = torch.empty(n, device="cuda")
+    backend.gemv_f32(dev_f32(x), dev_f32(w), y)
+    assert_f32_close(host_f32(y), oracle.linear(x[None], w)[0], 1e-5, f"gemv_f32 {n}x{k}")
+    backend.gemv_f32(dev_f32(x), dev_f32(w), y, bias=dev_f32(bias))
+    assert_f32_close(host_f32(y), oracle.linear(x[None], w, bias)[0], 1e-5, f"gemv_f32 {n}x{k} + bias")
