@@ -555,27 +555,44 @@ def expert_ffn(be, torch, timer, hidden, ffn, experts, k):
 
 
 def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, scratch, b, vocab, layers=12):
-    """A whole decode step as one graph, the C++ DecodeStep's body
-    (src/model/rocm/decode_step.cpp) at 12 layers: the embedding row,
-    12 fused layers over bf16 key/value caches of 8192 positions read in
-    full, the final norm fused into the LM-head GEMV. Every layer has the
-    dense FFN of 896 (the model's layers 1-11 are mixture-of-experts, whose
-    expert GEMVs are not built here). One set of weights and caches (1.4 GB)
-    already exceeds the Infinity Cache several times over."""
+    """The model's whole decode step as one graph, the C++ DecodeStep's body
+    (src/model/rocm/decode_step.cpp) on Unlimited-OCR-2's decoder shape
+    (weights/architecture.h): the embedding row, layer 0 with a dense FFN of
+    6848, layers 1-11 mixture of experts (an fp32 router over 64 experts, 6
+    routed experts of FFN 896, shared experts of FFN 1792), bf16 key/value
+    caches of 8192 positions read in full, the final norm fused into the
+    LM-head GEMV. The block router's attention mask is not built (full
+    attention over the cache). One set of weights and caches (5.8 GB) exceeds
+    the Infinity Cache many times over."""
     width = heads * hd
     scale = 1.0 / math.sqrt(hd)
+    dense_ffn, experts, top_k, expert_ffn, shared_ffn = 6848, 64, 6, 896, 1792
     table = bf16_randn(torch, (vocab, hidden), 0.5)
     lm = bf16_randn(torch, (vocab, hidden), 0.03)
     final_norm = weights(torch, hidden)
-    Ls = [{"in": weights(torch, hidden), "post": weights(torch, hidden),
-           "qkv": bf16_randn(torch, (3 * width, hidden), 0.03), "o": bf16_randn(torch, (hidden, width), 0.03),
-           "gate": bf16_randn(torch, (ffn, hidden), 0.03), "up": bf16_randn(torch, (ffn, hidden), 0.03),
-           "down": bf16_randn(torch, (hidden, ffn), 0.03),
-           "kc": bf16_randn(torch, (cap, width)), "vc": bf16_randn(torch, (cap, width))} for _ in range(layers)]
+
+    def layer(moe):
+        L = {"in": weights(torch, hidden), "post": weights(torch, hidden),
+             "qkv": bf16_randn(torch, (3 * width, hidden), 0.03), "o": bf16_randn(torch, (hidden, width), 0.03),
+             "kc": bf16_randn(torch, (cap, width)), "vc": bf16_randn(torch, (cap, width))}
+        f = shared_ffn if moe else dense_ffn
+        L.update({"gate": bf16_randn(torch, (f, hidden), 0.03), "up": bf16_randn(torch, (f, hidden), 0.03),
+                  "down": bf16_randn(torch, (hidden, f), 0.03), "ffn": f, "moe": moe})
+        if moe:
+            L.update({"router": 0.05 * torch.randn(experts, hidden, device="cuda"),
+                      "gs": bf16_randn(torch, (experts * expert_ffn, hidden), 0.03),
+                      "us": bf16_randn(torch, (experts * expert_ffn, hidden), 0.03),
+                      "ds": bf16_randn(torch, (experts, hidden, expert_ffn), 0.03)})
+        return L
+
+    Ls = [layer(i > 0) for i in range(layers)]
     xs = [torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda")]
-    delta, qkv = torch.empty(hidden, device="cuda"), torch.empty(3 * width, device="cuda")
+    h, delta, qkv = torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda"), torch.empty(3 * width, device="cuda")
     attn, o = torch.empty(width, device="cuda"), torch.empty(hidden, device="cuda")
-    act, logits = torch.empty(ffn, device="cuda"), torch.empty(vocab, device="cuda")
+    act, logits = torch.empty(dense_ffn, device="cuda"), torch.empty(vocab, device="cuda")
+    rlogits, ids, wts = (torch.empty(1, experts, device="cuda"), torch.empty(1, top_k, dtype=torch.int64, device="cuda"),
+                         torch.empty(1, top_k, device="cuda"))
+    escratch = torch.empty(be.expert_scratch_floats(top_k, expert_ffn), device="cuda")
     q, k, v = qkv[:width], qkv[width:2 * width], qkv[2 * width:]
 
     def step():
@@ -590,19 +607,31 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
             be.attend_rope_kv_step(q, k, v, L["kc"], L["vc"], heads, hd, None, scale, state, inv, None, 0, scratch,
                                    attn)
             be.gemv_bf16(attn, L["o"], o)
-            be.add_rms_norm_swiglu_gemv_bf16(xs[cur], L["gate"], L["up"], act, delta=o, x_out=xs[1 - cur],
-                                             w_norm=L["post"])
+            a = act[:L["ffn"]]
+            be.add_rms_norm_swiglu_gemv_bf16(xs[cur], L["gate"], L["up"], a, delta=o, x_out=xs[1 - cur],
+                                             w_norm=L["post"], h_out=h if L["moe"] else None)
             cur = 1 - cur
-            be.gemv_bf16(act, L["down"], delta)
+            be.gemv_bf16(a, L["down"], delta)
+            if L["moe"]:
+                be.gemv_f32(h, L["router"], rlogits.view(-1))
+                be.expert_topk(rlogits, top_k, ids, wts)
+                be.expert_ffn_one(h, L["gs"], L["us"], L["ds"], ids.view(-1), wts.view(-1), escratch, delta,
+                                  base=delta)
             pending = delta
         be.add_rms_norm_gemv_bf16(xs[cur], lm, logits, delta=pending, w_norm=final_norm)
 
-    per_layer = (b["add_rms_norm"] + b["gemv"] + b["rope"] + b["swiglu"]
-                 + (b["attend"] + b["append"]) // 2)  # the bf16 cache halves the attention's bytes
-    total = bytes_gather(1, hidden, 4) + layers * per_layer + bytes_gemv(vocab, hidden)
+    attn_bytes = b["add_rms_norm"] + b["rope"] + (b["attend"] + b["append"]) // 2 + bytes_gemv(3 * width, hidden) \
+        + bytes_gemv(hidden, width)
+    dense_bytes = 3 * dense_ffn * hidden * 2
+    moe_bytes = 3 * shared_ffn * hidden * 2 + experts * hidden * 4 + 3 * top_k * expert_ffn * hidden * 2
+    total = (bytes_gather(1, hidden, 4) + layers * attn_bytes + dense_bytes + (layers - 1) * moe_bytes
+             + bytes_gemv(vocab, hidden))
     ms = timer.graph([step])[0]
-    out = {"workload": f"whole decode step: embedding, {layers} fused layers (dense FFN {ffn}, bf16 KV cache "
-                       f"{cap} positions), final norm + LM head [{vocab}, {hidden}]; {2 + 6 * layers} launches",
+    launches = 2 + 6 + 10 * (layers - 1)
+    out = {"workload": f"the model's decode step: embedding, layer 0 dense (FFN {dense_ffn}), layers 1-{layers - 1} "
+                       f"mixture of experts ({top_k} of {experts} experts of FFN {expert_ffn}, shared FFN "
+                       f"{shared_ffn}, fp32 router), bf16 KV cache {cap} positions read in full, final norm + LM head "
+                       f"[{vocab}, {hidden}]; {launches} launches; block routing not built",
            "step": report("decode step", total, ms), "us_per_token": round(ms * 1e3, 2)}
     del Ls, table, lm
     return out
