@@ -590,8 +590,8 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
     h, delta, qkv = torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda"), torch.empty(3 * width, device="cuda")
     attn, o = torch.empty(width, device="cuda"), torch.empty(hidden, device="cuda")
     act, logits = torch.empty(dense_ffn, device="cuda"), torch.empty(vocab, device="cuda")
-    rlogits, ids, wts = (torch.empty(1, experts, device="cuda"), torch.empty(1, top_k, dtype=torch.int64, device="cuda"),
-                         torch.empty(1, top_k, device="cuda"))
+    ids, wts = torch.empty(1, top_k, dtype=torch.int64, device="cuda"), torch.empty(1, top_k, device="cuda")
+    rlogits = torch.empty(experts, device="cuda")
     escratch = torch.empty(be.expert_scratch_floats(top_k, expert_ffn), device="cuda")
     q, k, v = qkv[:width], qkv[width:2 * width], qkv[2 * width:]
 
@@ -611,12 +611,12 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
             be.add_rms_norm_swiglu_gemv_bf16(xs[cur], L["gate"], L["up"], a, delta=o, x_out=xs[1 - cur],
                                              w_norm=L["post"], h_out=h if L["moe"] else None)
             cur = 1 - cur
-            be.gemv_bf16(a, L["down"], delta)
             if L["moe"]:
-                be.gemv_f32(h, L["router"], rlogits.view(-1))
-                be.expert_topk(rlogits, top_k, ids, wts)
-                be.expert_ffn_one(h, L["gs"], L["us"], L["ds"], ids.view(-1), wts.view(-1), escratch, delta,
-                                  base=delta)
+                be.gemv_f32(h, L["router"], rlogits)
+                be.moe_ffn_one(h, L["gs"], L["us"], L["ds"], rlogits, ids.view(-1), wts.view(-1), a, L["down"],
+                               escratch, delta)
+            else:
+                be.gemv_bf16(a, L["down"], delta)
             pending = delta
         be.add_rms_norm_gemv_bf16(xs[cur], lm, logits, delta=pending, w_norm=final_norm)
 
@@ -627,7 +627,7 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
     total = (bytes_gather(1, hidden, 4) + layers * attn_bytes + dense_bytes + (layers - 1) * moe_bytes
              + bytes_gemv(vocab, hidden))
     ms = timer.graph([step])[0]
-    launches = 2 + 6 + 10 * (layers - 1)
+    launches = 2 + 6 + 8 * (layers - 1)
     out = {"workload": f"the model's decode step: embedding, layer 0 dense (FFN {dense_ffn}), layers 1-{layers - 1} "
                        f"mixture of experts ({top_k} of {experts} experts of FFN {expert_ffn}, shared FFN "
                        f"{shared_ffn}, fp32 router), bf16 KV cache {cap} positions read in full, final norm + LM head "

@@ -134,6 +134,8 @@ _SIGNATURES = {
     "uocr_rocm_expert_scratch_floats": ([_i64, _i64], _i64),
     "uocr_rocm_expert_ffn_one": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp], _int),
     "uocr_rocm_gemv_f32": ([_vp, _vp, _i64, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_moe_ffn_one": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp,
+                               _vp], _int),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -558,3 +560,26 @@ def expert_ffn_one(x, gate, up, down, ids, weights, scratch, out, base=None, str
         raise ValueError("expert_ffn_one: base [hidden]")
     _op("uocr_rocm_expert_ffn_one", stream, _ptr(x), hidden, ffn, _ptr(gate), _ptr(up), _ptr(down), experts,
         _ptr(ids), _ptr(weights), k, _ptr(base), _ptr(scratch), _ptr(out))
+
+
+def moe_ffn_one(x, gate, up, down, logits, ids, weights, shared_act, shared_down, scratch, out, stream=None):
+    """The routed experts from the router's logits [experts] (their top k
+    written to ids [k] and weights [k]) plus the shared experts' down product
+    in the same launch: out = bf16(shared_act) . shared_down^T + the routed
+    sum (shared_down [hidden, shared_ffn] bf16)."""
+    hidden = x.numel()
+    ffn = down.shape[-1]
+    experts = down.numel() // (hidden * ffn) if hidden * ffn else 0
+    k = ids.numel()
+    shared_ffn = shared_down.shape[-1]
+    if gate.numel() != experts * ffn * hidden or up.numel() != gate.numel() or out.numel() != hidden:
+        raise ValueError("moe_ffn_one shapes: gate/up [experts, ffn, hidden], down [experts, hidden, ffn]")
+    if logits.numel() != experts or logits.dtype != _torch().float32:
+        raise ValueError("moe_ffn_one: float32 logits [experts]")
+    if shared_down.numel() != hidden * shared_ffn or shared_act.numel() != shared_ffn:
+        raise ValueError("moe_ffn_one: shared_down [hidden, shared_ffn], shared_act [shared_ffn]")
+    if weights.numel() != k or scratch.numel() < expert_scratch_floats(k, ffn):
+        raise ValueError("moe_ffn_one: weights [k] and scratch of expert_scratch_floats(k, ffn) floats")
+    _op("uocr_rocm_moe_ffn_one", stream, _ptr(x), hidden, ffn, _ptr(gate), _ptr(up), _ptr(down), experts,
+        _ptr(logits), k, _ptr(ids), _ptr(weights), _ptr(shared_act), _ptr(shared_down), shared_ffn, _ptr(scratch),
+        _ptr(out))

@@ -20,6 +20,8 @@
 // up to kGemvMaxK) keep x in LDS; widths that are not a multiple of 8 or not
 // 16-byte aligned take the element-wise kernel.
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace uocr_rocm {
@@ -253,6 +255,68 @@ void launch_reg(hipStream_t s, const float* x, int nchunks, const uint16_t* w, i
   }
 }
 
+// ---- expert routing (used by the fused GEMVs and the expert kernels) ----------------
+
+constexpr int kMaxExperts = 2 * kWave;
+constexpr int kMaxExpertSlots = 8;
+constexpr int kExpertActFloats = 8192;  // k * ffn staged in LDS by the down kernel
+
+__device__ __forceinline__ bool topk_better(float v, int e, float bv, int be) { return v > bv || (v == bv && e < be); }
+
+// One wave: the softmax and top k of one row of logits lr (global or LDS),
+// ids and scores to ids[0..k) and wts[0..k).
+__device__ __forceinline__ void topk_row(const float* lr, int experts, int k, int64_t* ids, float* wts) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float v[2];
+  float peak = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int e = lane + kWave * i;
+    v[i] = e < experts ? lr[e] : -INFINITY;
+    peak = fmaxf(peak, v[i]);
+  }
+  peak = wave_max(peak);
+  // A row of -inf logits scores every expert 0, as softmax_rows leaves a
+  // fully masked row (src/backend/reference/ops.cpp:175-178).
+  const bool dead = peak == -INFINITY;
+  double total = 0.0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (lane + kWave * i < experts) {
+      v[i] = dead ? 0.0f : expf(v[i] - peak);
+      total += static_cast<double>(v[i]);
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) total += __shfl_xor(total, off);
+  const float inv = dead ? 0.0f : static_cast<float>(1.0 / total);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) v[i] = lane + kWave * i < experts ? v[i] * inv : -INFINITY;
+  for (int j = 0; j < k; ++j) {
+    float best = v[0];
+    int best_e = lane;
+    if (topk_better(v[1], lane + kWave, best, best_e)) {
+      best = v[1];
+      best_e = lane + kWave;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      const float ob = __shfl_xor(best, off);
+      const int oe = __shfl_xor(best_e, off);
+      if (topk_better(ob, oe, best, best_e)) {
+        best = ob;
+        best_e = oe;
+      }
+    }
+    if (lane == 0) {
+      ids[j] = best_e;
+      wts[j] = best;
+    }
+    if (best_e == lane) v[0] = -INFINITY;
+    if (best_e == lane + kWave) v[1] = -INFINITY;
+  }
+}
+
 // ---- fused decode GEMVs ----------------------------------------------------------
 //
 // The decode step's projections take the residual stream's add + RMSNorm as
@@ -287,13 +351,21 @@ struct FusedGemv {
   const int64_t* ids = nullptr;
   int64_t slot_rows = 0;
   int64_t experts = 0;
+  // With logits set (the router's [experts] logits), every workgroup takes
+  // the top_k itself (expert_topk's rule) and uses those ids; workgroup 0
+  // also writes them and their scores to ids_out / wts_out.
+  const float* logits = nullptr;
+  int top_k = 0;
+  int64_t* ids_out = nullptr;
+  float* wts_out = nullptr;
 };
 
-// The weight row that output row r of a fused GEMV reads.
-__device__ __forceinline__ int64_t fused_weight_row(const FusedGemv& a, int64_t r) {
-  if (a.ids == nullptr) return r;
+// The weight row that output row r of a fused GEMV reads (ids: a.ids, or
+// the workgroup's own top k in LDS).
+__device__ __forceinline__ int64_t fused_weight_row(const FusedGemv& a, const int64_t* ids, int64_t r) {
+  if (ids == nullptr) return r;
   const int64_t slot = r / a.slot_rows;
-  int64_t id = a.ids[slot];
+  int64_t id = ids[slot];
   id = id >= 0 && id < a.experts ? id : 0;
   return id * a.slot_rows + (r - slot * a.slot_rows);
 }
@@ -379,6 +451,20 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_fused(const FusedGemv a) {
   const int64_t step = static_cast<int64_t>(gridDim.x) * kGemvWaves;
   const int64_t g0 = static_cast<int64_t>(blockIdx.x) * kGemvWaves + wave;
 
+  // The routed experts' rows: this workgroup's own top k of the router's
+  // logits (bitwise expert_topk's), or the ids given.
+  __shared__ int64_t s_ids[kMaxExpertSlots];
+  __shared__ float s_wts[kMaxExpertSlots];
+  const int64_t* ids = a.ids;
+  if (a.logits != nullptr) {
+    if (wave == 0) topk_row(a.logits, static_cast<int>(a.experts), a.top_k, s_ids, s_wts);
+    __syncthreads();
+    if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < a.top_k) {
+      a.ids_out[threadIdx.x] = s_ids[threadIdx.x];
+      a.wts_out[threadIdx.x] = s_wts[threadIdx.x];
+    }
+    ids = s_ids;
+  }
   u32x4 wc[kMats][RPW][CPL];
   auto load_w = [&](int64_t g) {
     const int64_t row0 = g * RPW;
@@ -392,7 +478,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_fused(const FusedGemv a) {
           const int c = lane + kWave * i;
           wc[m][r][i] = u32x4{0u, 0u, 0u, 0u};
           if (row0 + r < a.n && c < nchunks) {
-            wc[m][r][i] = stream_load(reinterpret_cast<const u32x4*>(w + fused_weight_row(a, row0 + r) * k) + c);
+            wc[m][r][i] = stream_load(reinterpret_cast<const u32x4*>(w + fused_weight_row(a, ids, row0 + r) * k) + c);
           }
         }
       }
@@ -508,85 +594,44 @@ int fused_entry(const char* what, void* stream, FusedGemv a) {
 // with each down product formed exactly as gemv_bf16 forms it, so the call
 // is bitwise k pair GEMVs, k GEMVs and the weighted sum (mul then add).
 
-constexpr int kMaxExperts = 2 * kWave;
-constexpr int kMaxExpertSlots = 8;
-constexpr int kExpertActFloats = 8192;  // k * ffn staged in LDS by the down kernel
-
-__device__ __forceinline__ bool topk_better(float v, int e, float bv, int be) { return v > bv || (v == bv && e < be); }
-
 __global__ __launch_bounds__(kBlock) void expert_topk_k(const float* __restrict__ logits, int64_t rows, int experts,
                                                         int k, int64_t* __restrict__ ids, float* __restrict__ wts) {
-  const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
   if (row >= rows) return;
-  const float* lr = logits + row * experts;
-  float v[2];
-  float peak = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int e = lane + kWave * i;
-    v[i] = e < experts ? lr[e] : -INFINITY;
-    peak = fmaxf(peak, v[i]);
-  }
-  peak = wave_max(peak);
-  // A row of -inf logits scores every expert 0, as softmax_rows leaves a
-  // fully masked row (src/backend/reference/ops.cpp:175-178).
-  const bool dead = peak == -INFINITY;
-  double total = 0.0;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if (lane + kWave * i < experts) {
-      v[i] = dead ? 0.0f : expf(v[i] - peak);
-      total += static_cast<double>(v[i]);
-    }
-  }
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) total += __shfl_xor(total, off);
-  const float inv = dead ? 0.0f : static_cast<float>(1.0 / total);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) v[i] = lane + kWave * i < experts ? v[i] * inv : -INFINITY;
-  for (int j = 0; j < k; ++j) {
-    float best = v[0];
-    int best_e = lane;
-    if (topk_better(v[1], lane + kWave, best, best_e)) {
-      best = v[1];
-      best_e = lane + kWave;
-    }
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-      const float ob = __shfl_xor(best, off);
-      const int oe = __shfl_xor(best_e, off);
-      if (topk_better(ob, oe, best, best_e)) {
-        best = ob;
-        best_e = oe;
-      }
-    }
-    if (lane == 0) {
-      ids[row * k + j] = best_e;
-      wts[row * k + j] = best;
-    }
-    if (best_e == lane) v[0] = -INFINITY;
-    if (best_e == lane + kWave) v[1] = -INFINITY;
-  }
+  topk_row(logits + row * experts, experts, k, ids + row * k, wts + row * k);
 }
 
 // out[c] = sum_j w_j (down[ids[j] * hidden + c] . bf16(act_j)): bf16(act) of
 // every slot in LDS; a wave per output row requests the row of every slot,
 // then forms each product as gemv_reg does (chunk c = lane + 64 i, dot8 in
-// order, wave butterfly, + 0) and adds w_j d_j in slot order.
-template <int CPL>
+// order, wave butterfly, + 0) and adds w_j d_j in slot order. With CPLS > 0
+// the shared experts' down row (shared_down [hidden, shared_ffn] against
+// bf16(shared_act)) is formed the same way and the sum is added to it: out =
+// (shared . act_s + 0) + sum, bitwise their GEMV followed by add_inplace.
+// Otherwise out = base + sum (base may be out), or the sum.
+template <int CPL, int CPLS>
 __global__ __launch_bounds__(kGemvBlock) void expert_down_k(const float* __restrict__ act, int nchunks,
                                                             const uint16_t* __restrict__ down, int64_t hidden,
                                                             const int64_t* __restrict__ ids,
                                                             const float* __restrict__ wts, int k, int64_t experts,
+                                                            const float* __restrict__ shared_act, int shared_nchunks,
+                                                            const uint16_t* __restrict__ shared_down,
                                                             const float* base, float* out) {
   __shared__ __align__(16) float xs[kExpertActFloats];
   const int lane = threadIdx.x & (kWave - 1);
-  const int ffn = nchunks * 8;
+  const int ffn = nchunks * 8, sffn = shared_nchunks * 8;
+  float* xsh = xs + k * ffn;  // bf16(shared_act) after the routed slots
   const int64_t step = static_cast<int64_t>(gridDim.x) * kGemvWaves;
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kGemvWaves + threadIdx.x / kWave;
   u32x4 wc[kMaxExpertSlots][CPL];
+  u32x4 ws[CPLS > 0 ? CPLS : 1];
   auto load_rows = [&](int64_t c) {
+#pragma unroll
+    for (int i = 0; i < CPLS; ++i) {
+      const int ci = lane + kWave * i;
+      ws[i] = u32x4{0u, 0u, 0u, 0u};
+      if (ci < shared_nchunks) ws[i] = stream_load(reinterpret_cast<const u32x4*>(shared_down + c * sffn) + ci);
+    }
 #pragma unroll
     for (int j = 0; j < kMaxExpertSlots; ++j) {
       const int64_t id = j < k ? ids[j] : 0;
@@ -599,8 +644,8 @@ __global__ __launch_bounds__(kGemvBlock) void expert_down_k(const float* __restr
       }
     }
   };
-  // The first rows' weights go out before act is staged (they depend only
-  // on the ids), so both are in flight together, as in gemv_reg.
+  // The first rows' weights go out before the activations are staged (they
+  // depend only on the ids), so both are in flight together, as in gemv_reg.
   if (c0 < hidden) load_rows(c0);
   for (int t = threadIdx.x; t < 2 * nchunks * k; t += kGemvBlock) {
     float v[4];
@@ -608,41 +653,100 @@ __global__ __launch_bounds__(kGemvBlock) void expert_down_k(const float* __restr
 #pragma unroll
     for (int e = 0; e < 4; ++e) xs[4 * t + e] = round_bf16(v[e]);
   }
+  if constexpr (CPLS > 0) {
+    for (int t = threadIdx.x; t < 2 * shared_nchunks; t += kGemvBlock) {
+      float v[4];
+      load_f32<4>(shared_act + 4 * static_cast<int64_t>(t), v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xsh[4 * t + e] = round_bf16(v[e]);
+    }
+  }
   __syncthreads();
+  auto dot_lds = [&](const u32x4* wrow, const float* xrow, int n_chunks, auto cpl) {
+    constexpr int kC = decltype(cpl)::value;
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+      const int ci = lane + kWave * i;
+      float xv[8];
+      if (ci < n_chunks) {
+        load_f32<8>(xrow + 8 * ci, xv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
+      }
+      a = dot8(wrow[i], xv, a);
+    }
+    return wave_sum(a) + 0.0f;
+  };
   for (int64_t c = c0; c < hidden; c += step) {
     if (c != c0) load_rows(c);
     float total = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxExpertSlots; ++j) {
       if (j < k && ids[j] >= 0 && ids[j] < experts) {
-        float a = 0.0f;
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-          const int ci = lane + kWave * i;
-          float xv[8];
-          if (ci < nchunks) {
-            load_f32<8>(xs + j * ffn + 8 * ci, xv);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
-          }
-          a = dot8(wc[j][i], xv, a);
-        }
-        const float d = wave_sum(a) + 0.0f;
+        const float d = dot_lds(wc[j], xs + j * ffn, nchunks, std::integral_constant<int, CPL>{});
         {
 #pragma clang fp contract(off)
           total = total + wts[j] * d;
         }
       }
     }
-    if (lane == 0) out[c] = base != nullptr ? base[c] + total : total;
+    float r;
+    if constexpr (CPLS > 0) {
+      r = dot_lds(ws, xsh, shared_nchunks, std::integral_constant<int, CPLS>{}) + total;
+    } else {
+      r = base != nullptr ? base[c] + total : total;
+    }
+    if (lane == 0) out[c] = r;
   }
+}
+
+template <int CPL>
+void launch_expert_down(hipStream_t s, unsigned blocks, int cpls, const float* act, int nchunks, const uint16_t* down,
+                        int64_t hidden, const int64_t* ids, const float* wts, int k, int64_t experts,
+                        const float* shared_act, int shared_nchunks, const uint16_t* shared_down, const float* base,
+                        float* out) {
+#define UOCR_EXPERT_DOWN(S)                                                                                   \
+  expert_down_k<CPL, S><<<blocks, kGemvBlock, 0, s>>>(act, nchunks, down, hidden, ids, wts, k, experts,      \
+                                                     shared_act, shared_nchunks, shared_down, base, out)
+  switch (cpls) {
+    case 0: UOCR_EXPERT_DOWN(0); break;
+    case 1: UOCR_EXPERT_DOWN(1); break;
+    case 2: UOCR_EXPERT_DOWN(2); break;
+    case 3: UOCR_EXPERT_DOWN(3); break;
+    default: UOCR_EXPERT_DOWN(kGemvRegChunks); break;
+  }
+#undef UOCR_EXPERT_DOWN
 }
 
 // y[n] = x . w[n, :] (+ bias[n]) with fp32 weights and no rounding of x: the
 // mixture-of-experts gate, which the reference keeps in fp32 for routing
 // (moe_gate_f32, src/model/cuda/cuda_decoder.cpp:141-142). One wave per row,
 // 16-byte chunks when k and the pointers allow, a wave butterfly.
+// One wave: x . wr over k fp32 elements (chunk c = lane + 64 i in order).
+template <bool kVec>
+__device__ __forceinline__ float dot_f32_row(const float* x, const float* wr, int64_t k) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float a = 0.0f;
+  if constexpr (kVec) {
+    for (int64_t c = lane; c < k / 4; c += kWave) {
+      float xv[4], wv[4];
+      load_f32<4>(x + 4 * c, xv);
+      const u32x4 q = stream_load(reinterpret_cast<const u32x4*>(wr) + c);
+      wv[0] = __uint_as_float(q.x);
+      wv[1] = __uint_as_float(q.y);
+      wv[2] = __uint_as_float(q.z);
+      wv[3] = __uint_as_float(q.w);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a = fmaf(xv[e], wv[e], a);
+    }
+  } else {
+    for (int64_t c = lane; c < k; c += kWave) a = fmaf(x[c], wr[c], a);
+  }
+  return wave_sum(a);
+}
+
 template <bool kVec>
 __global__ __launch_bounds__(kBlock) void gemv_f32_k(const float* __restrict__ x, int64_t k,
                                                      const float* __restrict__ w, int64_t n,
@@ -650,27 +754,11 @@ __global__ __launch_bounds__(kBlock) void gemv_f32_k(const float* __restrict__ x
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t step = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
   for (int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave; row < n; row += step) {
-    const float* wr = w + row * k;
-    float a = 0.0f;
-    if constexpr (kVec) {
-      for (int64_t c = lane; c < k / 4; c += kWave) {
-        float xv[4], wv[4];
-        load_f32<4>(x + 4 * c, xv);
-        const u32x4 q = stream_load(reinterpret_cast<const u32x4*>(wr) + c);
-        wv[0] = __uint_as_float(q.x);
-        wv[1] = __uint_as_float(q.y);
-        wv[2] = __uint_as_float(q.z);
-        wv[3] = __uint_as_float(q.w);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a = fmaf(xv[e], wv[e], a);
-      }
-    } else {
-      for (int64_t c = lane; c < k; c += kWave) a = fmaf(x[c], wr[c], a);
-    }
-    a = wave_sum(a);
+    const float a = dot_f32_row<kVec>(x, w + row * k, k);
     if (lane == 0) y[row] = a + (bias != nullptr ? bias[row] : 0.0f);
   }
 }
+
 
 }  // namespace
 }  // namespace uocr_rocm
@@ -763,16 +851,23 @@ int uocr_rocm_expert_topk(void* stream, const float* logits, int64_t rows, int64
 
 int64_t uocr_rocm_expert_scratch_floats(int64_t k, int64_t ffn) { return k > 0 && ffn > 0 ? k * ffn : 0; }
 
-int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64_t ffn, const uint16_t* gate,
-                             const uint16_t* up, const uint16_t* down, int64_t experts, const int64_t* ids,
-                             const float* weights, int64_t k, const float* base, float* scratch, float* out) {
-  const char* what = "uocr_rocm_expert_ffn_one";
+namespace {
+
+int expert_ffn_entry(const char* what, void* stream, const float* x, int64_t hidden, int64_t ffn,
+                     const uint16_t* gate, const uint16_t* up, const uint16_t* down, int64_t experts,
+                     const float* logits, int64_t* ids, float* weights, int64_t k, const float* shared_act,
+                     const uint16_t* shared_down, int64_t shared_ffn, const float* base, float* scratch, float* out) {
   UOCR_REQUIRE(hidden % 8 == 0 && hidden >= 8 && hidden <= kFusedMaxK, what,
                "hidden must be a multiple of 8 in [8, 2048]");
   UOCR_REQUIRE(ffn % 8 == 0 && ffn >= 8 && ffn / 8 <= kWave * kGemvRegChunks, what,
                "ffn must be a multiple of 8 in [8, 2048]");
-  UOCR_REQUIRE(k >= 1 && k <= kMaxExpertSlots && k * ffn <= kExpertActFloats, what,
-               "k must be in [1, 8] with k * ffn <= 8192");
+  UOCR_REQUIRE(k >= 1 && k <= kMaxExpertSlots && k * ffn + shared_ffn <= kExpertActFloats, what,
+               "k must be in [1, 8] with k * ffn (+ shared_ffn) <= 8192");
+  UOCR_REQUIRE(shared_ffn == 0 || (shared_ffn % 8 == 0 && shared_ffn / 8 <= kWave * kGemvRegChunks &&
+                                   shared_act != nullptr && shared_down != nullptr && aligned16(shared_act) &&
+                                   aligned16(shared_down) && base == nullptr),
+               what, "shared_ffn must be a multiple of 8 in [8, 2048] with shared_act and shared_down 16-byte "
+                     "aligned, and no base");
   UOCR_REQUIRE(experts >= 1, what, "experts must be >= 1");
   UOCR_REQUIRE(x != nullptr && gate != nullptr && up != nullptr && down != nullptr && ids != nullptr &&
                    weights != nullptr && scratch != nullptr && out != nullptr,
@@ -785,22 +880,51 @@ int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64
                what, "x, base, scratch and out must not overlap (base may be out itself)");
   FusedGemv a{x, nullptr, nullptr, nullptr, nullptr, gate, up, nullptr, scratch, k * ffn, static_cast<int>(hidden),
               0.0f};
-  a.ids = ids;
   a.slot_rows = ffn;
   a.experts = experts;
+  if (logits != nullptr) {
+    UOCR_REQUIRE(experts <= kMaxExperts, what, "experts must be in [1, 128] with router logits");
+    a.logits = logits;
+    a.top_k = static_cast<int>(k);
+    a.ids_out = ids;
+    a.wts_out = weights;
+  } else {
+    a.ids = ids;
+  }
   const hipStream_t s = as_stream(stream);
   clear_launch_error();
   launch_fused<false, true>(s, a);
-  const int nchunks = static_cast<int>(ffn / 8);
+  const int nchunks = static_cast<int>(ffn / 8), snchunks = static_cast<int>(shared_ffn / 8);
   const unsigned blocks = gemv_reg_blocks(hidden);
-  const int kk = static_cast<int>(k);
+  const int kk = static_cast<int>(k), cpls = (snchunks + kWave - 1) / kWave;
   switch ((nchunks + kWave - 1) / kWave) {
-    case 1: expert_down_k<1><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, base, out); break;
-    case 2: expert_down_k<2><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, base, out); break;
-    case 3: expert_down_k<3><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, base, out); break;
-    default: expert_down_k<kGemvRegChunks><<<blocks, kGemvBlock, 0, s>>>(scratch, nchunks, down, hidden, ids, weights, kk, experts, base, out); break;
+    case 1: launch_expert_down<1>(s, blocks, cpls, scratch, nchunks, down, hidden, ids, weights, kk, experts, shared_act, snchunks, shared_down, base, out); break;
+    case 2: launch_expert_down<2>(s, blocks, cpls, scratch, nchunks, down, hidden, ids, weights, kk, experts, shared_act, snchunks, shared_down, base, out); break;
+    case 3: launch_expert_down<3>(s, blocks, cpls, scratch, nchunks, down, hidden, ids, weights, kk, experts, shared_act, snchunks, shared_down, base, out); break;
+    default: launch_expert_down<kGemvRegChunks>(s, blocks, cpls, scratch, nchunks, down, hidden, ids, weights, kk, experts, shared_act, snchunks, shared_down, base, out); break;
   }
   return check_launch(what);
+}
+
+}  // namespace
+
+int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t hidden, int64_t ffn, const uint16_t* gate,
+                             const uint16_t* up, const uint16_t* down, int64_t experts, const int64_t* ids,
+                             const float* weights, int64_t k, const float* base, float* scratch, float* out) {
+  return expert_ffn_entry("uocr_rocm_expert_ffn_one", stream, x, hidden, ffn, gate, up, down, experts, nullptr,
+                          const_cast<int64_t*>(ids), const_cast<float*>(weights), k, nullptr, nullptr, 0, base,
+                          scratch, out);
+}
+
+int uocr_rocm_moe_ffn_one(void* stream, const float* x, int64_t hidden, int64_t ffn, const uint16_t* gate,
+                          const uint16_t* up, const uint16_t* down, int64_t experts, const float* logits, int64_t k,
+                          int64_t* ids, float* weights, const float* shared_act, const uint16_t* shared_down,
+                          int64_t shared_ffn, float* scratch, float* out) {
+  const char* what = "uocr_rocm_moe_ffn_one";
+  UOCR_REQUIRE(shared_ffn >= 8, what, "shared_ffn must be a multiple of 8 in [8, 2048]");
+  UOCR_REQUIRE(logits != nullptr, what, "null logits");
+  return expert_ffn_entry(what, stream, x, hidden, ffn, gate, up, down, experts, logits, ids, weights, k, shared_act,
+                          shared_down, shared_ffn, nullptr, scratch, out);
 }
 
 }  // extern "C"

@@ -174,6 +174,14 @@ void expert_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std
                                  scratch, out));
 }
 
+void moe_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::int64_t ffn,
+                 const std::uint16_t* gate, const std::uint16_t* up, const std::uint16_t* down, std::int64_t experts,
+                 const float* logits, std::int64_t k, std::int64_t* ids, float* weights, const float* shared_act,
+                 const std::uint16_t* shared_down, std::int64_t shared_ffn, float* scratch, float* out) {
+  check(uocr_rocm_moe_ffn_one(ctx.stream(), x, hidden, ffn, gate, up, down, experts, logits, k, ids, weights,
+                              shared_act, shared_down, shared_ffn, scratch, out));
+}
+
 void gemv_f32(const Context& ctx, const float* x, std::int64_t k, const float* w, std::int64_t n, const float* bias,
               float* y) {
   check(uocr_rocm_gemv_f32(ctx.stream(), x, k, w, n, bias, y));

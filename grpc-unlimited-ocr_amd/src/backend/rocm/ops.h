@@ -141,6 +141,14 @@ void expert_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std
                     const std::uint16_t* gate, const std::uint16_t* up, const std::uint16_t* down,
                     std::int64_t experts, const std::int64_t* ids, const float* weights, std::int64_t k,
                     const float* base, float* scratch, float* out);
+// New: the routed experts from the router's logits (the top k formed in
+// the launch and written to ids/weights) with the shared experts' down
+// product in the same launch: out = shared_down . bf16(shared_act) + routed,
+// bitwise expert_topk, the shared GEMV and expert_ffn_one with it as base.
+void moe_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::int64_t ffn,
+                 const std::uint16_t* gate, const std::uint16_t* up, const std::uint16_t* down, std::int64_t experts,
+                 const float* logits, std::int64_t k, std::int64_t* ids, float* weights, const float* shared_act,
+                 const std::uint16_t* shared_down, std::int64_t shared_ffn, float* scratch, float* out);
 // y[n] = x . w[n, :] (+ bias) with fp32 weights: the gate logits.
 void gemv_f32(const Context& ctx, const float* x, std::int64_t k, const float* w, std::int64_t n, const float* bias,
               float* y);

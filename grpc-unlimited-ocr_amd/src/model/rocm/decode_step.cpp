@@ -140,12 +140,10 @@ void DecodeStep::body() {
       add_rms_norm_swiglu_gemv_bf16(ctx_, x_[cur].f32(), o_.f32(), x_[1 - cur].f32(), l.post_norm, d.eps, h_.f32(),
                                     d.hidden, m.shared_gate, m.shared_up, m.shared_ffn, act_.f32());
       cur = 1 - cur;
-      gemv_bf16(ctx_, act_.f32(), m.shared_ffn, m.shared_down, d.hidden, nullptr, delta_.f32());
       gemv_f32(ctx_, h_.f32(), d.hidden, m.gate, m.experts, nullptr, router_logits_.f32());
-      expert_topk(ctx_, router_logits_.f32(), 1, m.experts, m.top_k, expert_ids_.i64(), expert_weights_.f32());
-      expert_ffn_one(ctx_, h_.f32(), d.hidden, m.expert_ffn, m.gate_stack, m.up_stack, m.down_stack, m.experts,
-                     expert_ids_.i64(), expert_weights_.f32(), m.top_k, delta_.f32(), expert_scratch_.f32(),
-                     delta_.f32());
+      moe_ffn_one(ctx_, h_.f32(), d.hidden, m.expert_ffn, m.gate_stack, m.up_stack, m.down_stack, m.experts,
+                  router_logits_.f32(), m.top_k, expert_ids_.i64(), expert_weights_.f32(), act_.f32(), m.shared_down,
+                  m.shared_ffn, expert_scratch_.f32(), delta_.f32());
     }
     pending = delta_.f32();
   }

@@ -447,6 +447,23 @@ UOCR_ROCM_API int uocr_rocm_expert_ffn_one(void* stream, const float* x, int64_t
                                            int64_t experts, const int64_t* ids, const float* weights, int64_t k,
                                            const float* base, float* scratch, float* out);
 
+/* The mixture-of-experts MLP of a decode row after its shared experts'
+ * gate/up and its router logits [experts] (uocr_rocm_gemv_f32): the top k
+ * of the logits as uocr_rocm_expert_topk forms them (written to ids and
+ * weights), the routed experts as uocr_rocm_expert_ffn_one, and the shared
+ * experts' down product (shared_down [hidden, shared_ffn] against
+ * bf16(shared_act)) formed in the same launch as the routed down products:
+ * out = shared + routed. Bitwise uocr_rocm_expert_topk, then
+ * uocr_rocm_gemv_bf16(shared_act, shared_down), then uocr_rocm_expert_ffn_one
+ * with that as base (cuda_decoder.cpp:137-152, whose top-k launch, shared
+ * down GEMV and add_inplace this folds in); two launches. experts <= 128,
+ * shared_ffn a multiple of 8 in [8, 2048], k * ffn + shared_ffn <= 8192. */
+UOCR_ROCM_API int uocr_rocm_moe_ffn_one(void* stream, const float* x, int64_t hidden, int64_t ffn,
+                                       const uint16_t* gate, const uint16_t* up, const uint16_t* down,
+                                       int64_t experts, const float* logits, int64_t k, int64_t* ids, float* weights,
+                                       const float* shared_act, const uint16_t* shared_down, int64_t shared_ffn,
+                                       float* scratch, float* out);
+
 /* y[n] = x . w[n, :] (+ bias[n]) with fp32 weights, x not rounded: the
  * mixture-of-experts gate logits, which the reference forms from fp32 gate
  * weights with an fp32 GEMM (moe_gate_f32, src/model/cuda/cuda_decoder.cpp:

@@ -147,3 +147,28 @@ def test_gemv_f32_matches_oracle(backend, n, k):
     assert_f32_close(host_f32(y), oracle.linear(x[None], w)[0], 1e-5, f"gemv_f32 {n}x{k}")
     backend.gemv_f32(dev_f32(x), dev_f32(w), y, bias=dev_f32(bias))
     assert_f32_close(host_f32(y), oracle.linear(x[None], w, bias)[0], 1e-5, f"gemv_f32 {n}x{k} + bias")
+
+
+@pytest.mark.parametrize("shared_ffn,experts", [(1792, 64), (24, 16), (512, 128)])
+def test_moe_ffn_one_is_topk_shared_gemv_then_experts(backend, shared_ffn, experts):
+    hidden, ffn, k = 1280, 896, 6
+    if k * ffn + shared_ffn > 8192:
+        ffn = 256
+    g, u, d = expert_stacks(970, experts, hidden, ffn)
+    dg, du, dd = dev_bf16(g), dev_bf16(u), dev_bf16(d)
+    x = dev_f32(normal(971, hidden))
+    act_s = dev_f32(normal(972, shared_ffn))
+    sdown = dev_bf16(oracle.f32_to_bf16(normal(973, (hidden, shared_ffn), 0.04)))
+    logits = dev_f32(normal(974, experts, 2.0))
+    scratch = torch.empty(backend.expert_scratch_floats(k, ffn), device="cuda")
+    # the parts: top k, the shared GEMV, the routed experts added to it
+    ids1, w1 = torch.empty(1, k, dtype=torch.int64, device="cuda"), torch.empty(1, k, device="cuda")
+    backend.expert_topk(logits.view(1, -1), k, ids1, w1)
+    shared, want = torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda")
+    backend.gemv_bf16(act_s, sdown, shared)
+    backend.expert_ffn_one(x, dg, du, dd, ids1.view(-1), w1.view(-1), scratch, want, base=shared)
+    ids2, w2 = torch.empty(k, dtype=torch.int64, device="cuda"), torch.empty(k, device="cuda")
+    got = torch.empty(hidden, device="cuda")
+    backend.moe_ffn_one(x, dg, du, dd, logits, ids2, w2, act_s, sdown, scratch, got)
+    assert torch.equal(ids1.view(-1), ids2) and torch.equal(w1.view(-1).view(torch.int32), w2.view(torch.int32))
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
