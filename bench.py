@@ -608,11 +608,14 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
                                    attn)
             be.gemv_bf16(attn, L["o"], o)
             a = act[:L["ffn"]]
-            be.add_rms_norm_swiglu_gemv_bf16(xs[cur], L["gate"], L["up"], a, delta=o, x_out=xs[1 - cur],
-                                             w_norm=L["post"], h_out=h if L["moe"] else None)
+            if L["moe"]:  # the shared experts' pair GEMV and the router in one launch
+                be.add_rms_norm_swiglu_router_gemv_bf16(xs[cur], L["gate"], L["up"], a, L["router"], rlogits,
+                                                        delta=o, x_out=xs[1 - cur], w_norm=L["post"], h_out=h)
+            else:
+                be.add_rms_norm_swiglu_gemv_bf16(xs[cur], L["gate"], L["up"], a, delta=o, x_out=xs[1 - cur],
+                                                 w_norm=L["post"])
             cur = 1 - cur
             if L["moe"]:
-                be.gemv_f32(h, L["router"], rlogits)
                 be.moe_ffn_one(h, L["gs"], L["us"], L["ds"], rlogits, ids.view(-1), wts.view(-1), a, L["down"],
                                escratch, delta)
             else:
@@ -627,7 +630,7 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
     total = (bytes_gather(1, hidden, 4) + layers * attn_bytes + dense_bytes + (layers - 1) * moe_bytes
              + bytes_gemv(vocab, hidden))
     ms = timer.graph([step])[0]
-    launches = 2 + 6 + 8 * (layers - 1)
+    launches = 2 + 6 + 7 * (layers - 1)
     out = {"workload": f"the model's decode step: embedding, layer 0 dense (FFN {dense_ffn}), layers 1-{layers - 1} "
                        f"mixture of experts ({top_k} of {experts} experts of FFN {expert_ffn}, shared FFN "
                        f"{shared_ffn}, fp32 router), bf16 KV cache {cap} positions read in full, final norm + LM head "

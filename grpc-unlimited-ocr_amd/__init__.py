@@ -128,6 +128,8 @@ _SIGNATURES = {
     "uocr_rocm_add_rms_norm_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_add_rms_norm_swiglu_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _vp, _i64, _vp],
                                                 _int),
+    "uocr_rocm_add_rms_norm_swiglu_router_gemv_bf16": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _vp, _i64, _vp,
+                                                        _vp, _i64, _vp], _int),
     "uocr_rocm_attend_rope_kv_step": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp,
                                        _i64, _vp, _i64, _vp], _int),
     "uocr_rocm_expert_topk": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp], _int),
@@ -497,6 +499,21 @@ def add_rms_norm_swiglu_gemv_bf16(x, w_gate, w_up, act, delta=None, x_out=None, 
         raise ValueError("w_gate and w_up must have the same shape")
     _op("uocr_rocm_add_rms_norm_swiglu_gemv_bf16", stream, _ptr(x), _ptr(delta), _ptr(x_out), _f32_param(w_norm),
         eps, _ptr(h_out), k, _ptr(w_gate), _ptr(w_up), ffn, _ptr(act))
+
+
+def add_rms_norm_swiglu_router_gemv_bf16(x, w_gate, w_up, act, router, logits, delta=None, x_out=None, w_norm=None,
+                                         eps=1e-6, h_out=None, stream=None):
+    """add_rms_norm_swiglu_gemv_bf16 and, in the same launch, logits =
+    router (fp32 [experts, k]) . h with h unrounded."""
+    ffn, k = w_gate.shape
+    experts = router.shape[0]
+    if tuple(w_up.shape) != (ffn, k) or tuple(router.shape) != (experts, k) or logits.numel() != experts:
+        raise ValueError("w_gate, w_up [ffn, k]; router [experts, k]; logits [experts]")
+    if router.dtype != _torch().float32 or logits.dtype != _torch().float32:
+        raise ValueError("router and logits must be float32")
+    _op("uocr_rocm_add_rms_norm_swiglu_router_gemv_bf16", stream, _ptr(x), _ptr(delta), _ptr(x_out),
+        _f32_param(w_norm), eps, _ptr(h_out), k, _ptr(w_gate), _ptr(w_up), ffn, _ptr(act), _ptr(router), experts,
+        _ptr(logits))
 
 
 def attend_rope_kv_step(q, k_row, v_row, k_cache, v_cache, heads, hd, mask, scale, state, inv_tok, inv_page,

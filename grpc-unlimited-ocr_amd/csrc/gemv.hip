@@ -264,8 +264,15 @@ constexpr int kExpertActFloats = 8192;  // k * ffn staged in LDS by the down ker
 __device__ __forceinline__ bool topk_better(float v, int e, float bv, int be) { return v > bv || (v == bv && e < be); }
 
 // One wave: the softmax and top k of one row of logits lr (global or LDS),
-// ids and scores to ids[0..k) and wts[0..k).
-__device__ __forceinline__ void topk_row(const float* lr, int experts, int k, int64_t* ids, float* wts) {
+// ids and scores to ids[0..k) and wts[0..k); sv is kMaxExperts floats of
+// LDS for this wave. The top k are the experts whose rank is below k, the
+// rank of e being the number of experts ahead of it under topk_better (a
+// strict total order, so the ranks are 0..experts-1 and equal the rounds in
+// which k successive argmaxes would pick them). Each lane ranks its own
+// experts against all of them read back from LDS: no dependent shuffles,
+// where k wave argmaxes were 12 dependent permutes each. A NaN score ranks
+// below every number.
+__device__ __forceinline__ void topk_row(const float* lr, int experts, int k, int64_t* ids, float* wts, float* sv) {
   const int lane = threadIdx.x & (kWave - 1);
   float v[2];
   float peak = -INFINITY;
@@ -292,28 +299,37 @@ __device__ __forceinline__ void topk_row(const float* lr, int experts, int k, in
   const float inv = dead ? 0.0f : static_cast<float>(1.0 / total);
 #pragma unroll
   for (int i = 0; i < 2; ++i) v[i] = lane + kWave * i < experts ? v[i] * inv : -INFINITY;
-  for (int j = 0; j < k; ++j) {
-    float best = v[0];
-    int best_e = lane;
-    if (topk_better(v[1], lane + kWave, best, best_e)) {
-      best = v[1];
-      best_e = lane + kWave;
-    }
+  float key[2];
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-      const float ob = __shfl_xor(best, off);
-      const int oe = __shfl_xor(best_e, off);
-      if (topk_better(ob, oe, best, best_e)) {
-        best = ob;
-        best_e = oe;
-      }
+  for (int i = 0; i < 2; ++i) {
+    const bool valid = lane + kWave * i < experts;
+    key[i] = valid ? (v[i] == v[i] ? v[i] : -1.0f) : -INFINITY;
+    sv[lane + kWave * i] = key[i];
+  }
+  // A wave's LDS accesses complete in order; the fences keep the compiler
+  // from moving the reads above the writes.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const bool two = experts > kWave;
+  const int quads = ((two ? experts : kWave) + 3) / 4;
+  int rank[2] = {0, 0};
+  for (int q = 0; q < quads; ++q) {
+    const float4 o = reinterpret_cast<const float4*>(sv)[q];
+    const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int e = 4 * q + t;
+      rank[0] += topk_better(ov[t], e, key[0], lane) ? 1 : 0;
+      if (two) rank[1] += topk_better(ov[t], e, key[1], lane + kWave) ? 1 : 0;
     }
-    if (lane == 0) {
-      ids[j] = best_e;
-      wts[j] = best;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (lane + kWave * i < experts && rank[i] < k) {
+      ids[rank[i]] = lane + kWave * i;
+      wts[rank[i]] = v[i];
     }
-    if (best_e == lane) v[0] = -INFINITY;
-    if (best_e == lane + kWave) v[1] = -INFINITY;
   }
 }
 
@@ -358,6 +374,13 @@ struct FusedGemv {
   int top_k = 0;
   int64_t* ids_out = nullptr;
   float* wts_out = nullptr;
+  // fp32 rows against the unrounded h (the router's gate, no bias), formed
+  // by the workgroups from main_blocks on, one row per wave, exactly as
+  // gemv_f32 forms them; main_blocks is set at launch.
+  const float* w_f32 = nullptr;
+  int64_t n_f32 = 0;
+  float* y_f32 = nullptr;
+  unsigned main_blocks = 0;
 };
 
 // The weight row that output row r of a fused GEMV reads (ids: a.ids, or
@@ -375,7 +398,8 @@ __device__ __forceinline__ int64_t fused_weight_row(const FusedGemv& a, const in
 // order, and writes bf16(h) to LDS, from which every wave reads its 8-float
 // GEMV chunks. x, delta and w_norm are read once per workgroup.
 template <bool kNorm, class IssueW>
-__device__ __forceinline__ void fused_prologue(const FusedGemv& a, float* h_lds, int wave, int lane, IssueW issue_w) {
+__device__ __forceinline__ void fused_prologue(const FusedGemv& a, float* h_lds, int wave, int lane, IssueW issue_w,
+                                               bool round_h = true) {
   __shared__ float red[kMaxGroups];
   constexpr int kG = kFusedMaxK / 4 / kWave / kGemvWaves;  // 1 group per wave
   const int nvec = a.k / 4;
@@ -434,7 +458,7 @@ __device__ __forceinline__ void fused_prologue(const FusedGemv& a, float* h_lds,
             u32x4{__float_as_uint(h[0]), __float_as_uint(h[1]), __float_as_uint(h[2]), __float_as_uint(h[3])};
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) h_lds[4 * v + e] = round_bf16(h[e]);
+      for (int e = 0; e < 4; ++e) h_lds[4 * v + e] = round_h ? round_bf16(h[e]) : h[e];
     }
   }
   __syncthreads();
@@ -448,16 +472,52 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_fused(const FusedGemv a) {
   const int nchunks = a.k / 8;
   const int64_t k = a.k;
   const int64_t groups = (a.n + RPW - 1) / RPW;
-  const int64_t step = static_cast<int64_t>(gridDim.x) * kGemvWaves;
+  const int64_t step = static_cast<int64_t>(a.main_blocks) * kGemvWaves;
   const int64_t g0 = static_cast<int64_t>(blockIdx.x) * kGemvWaves + wave;
+
+  if (blockIdx.x >= a.main_blocks) {
+    // An fp32 row per wave against h unrounded in LDS: chunk c = lane + 64 i
+    // in order, fmaf per element, wave butterfly, + 0, as gemv_f32 forms it.
+    // The row's chunks are requested before the prologue's arithmetic.
+    constexpr int kF32Chunks = kFusedMaxK / 4 / kWave;
+    const int nv = a.k / 4;
+    const int64_t row = static_cast<int64_t>(blockIdx.x - a.main_blocks) * kGemvWaves + wave;
+    const float* wr = a.w_f32 + (row < a.n_f32 ? row : a.n_f32 - 1) * k;
+    u32x4 wf[kF32Chunks];
+    fused_prologue<kNorm>(
+        a, h_lds, wave, lane,
+        [&] {
+#pragma unroll
+          for (int i = 0; i < kF32Chunks; ++i) {
+            const int c = lane + kWave * i;
+            wf[i] = stream_load(reinterpret_cast<const u32x4*>(wr) + (c < nv ? c : nv - 1));
+          }
+        },
+        false);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kF32Chunks; ++i) {
+      const int c = lane + kWave * i;
+      if (c < nv) {
+        const float wv[4] = {__uint_as_float(wf[i].x), __uint_as_float(wf[i].y), __uint_as_float(wf[i].z),
+                             __uint_as_float(wf[i].w)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = fmaf(h_lds[4 * c + e], wv[e], acc);
+      }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0 && row < a.n_f32) a.y_f32[row] = acc + 0.0f;
+    return;
+  }
 
   // The routed experts' rows: this workgroup's own top k of the router's
   // logits (bitwise expert_topk's), or the ids given.
   __shared__ int64_t s_ids[kMaxExpertSlots];
   __shared__ float s_wts[kMaxExpertSlots];
+  __shared__ __align__(16) float s_scores[kMaxExperts];
   const int64_t* ids = a.ids;
   if (a.logits != nullptr) {
-    if (wave == 0) topk_row(a.logits, static_cast<int>(a.experts), a.top_k, s_ids, s_wts);
+    if (wave == 0) topk_row(a.logits, static_cast<int>(a.experts), a.top_k, s_ids, s_wts, s_scores);
     __syncthreads();
     if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < a.top_k) {
       a.ids_out[threadIdx.x] = s_ids[threadIdx.x];
@@ -531,10 +591,14 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_fused(const FusedGemv a) {
 
 template <int CPL, bool kNorm, bool kPair>
 void launch_fused_rows(hipStream_t s, const FusedGemv& a) {
+  FusedGemv b = a;
+  const unsigned f32_blocks = a.w_f32 != nullptr ? static_cast<unsigned>((a.n_f32 + kGemvWaves - 1) / kGemvWaves) : 0u;
   if (a.n >= kBigRows) {
-    gemv_fused<CPL, 2, kNorm, kPair><<<gemv_reg_blocks((a.n + 1) / 2), kGemvBlock, 0, s>>>(a);
+    b.main_blocks = gemv_reg_blocks((a.n + 1) / 2);
+    gemv_fused<CPL, 2, kNorm, kPair><<<b.main_blocks + f32_blocks, kGemvBlock, 0, s>>>(b);
   } else {
-    gemv_fused<CPL, 1, kNorm, kPair><<<gemv_reg_blocks(a.n), kGemvBlock, 0, s>>>(a);
+    b.main_blocks = gemv_reg_blocks(a.n);
+    gemv_fused<CPL, 1, kNorm, kPair><<<b.main_blocks + f32_blocks, kGemvBlock, 0, s>>>(b);
   }
 }
 
@@ -583,8 +647,8 @@ int fused_entry(const char* what, void* stream, FusedGemv a) {
 // and their (unnormalised) scores, the rule of MixtureOfExperts::forward
 // (src/model/feed_forward.cpp:36-53): peak = max, total = sum of
 // float(exp(v - peak)) in fp64, score = float(exp(v - peak)) * float(1 /
-// total). One wave per row, two experts per lane (experts <= 128); each of
-// the k rounds is a wave argmax over (score, -index).
+// total). One wave per row, two experts per lane (experts <= 128); an
+// expert is picked when fewer than k experts are ahead of it.
 //
 // expert_ffn_one: the routed experts of one decode row, weights stacked by
 // expert (gate/up [experts * ffn, hidden], down [experts * hidden, ffn]):
@@ -596,9 +660,10 @@ int fused_entry(const char* what, void* stream, FusedGemv a) {
 
 __global__ __launch_bounds__(kBlock) void expert_topk_k(const float* __restrict__ logits, int64_t rows, int experts,
                                                         int k, int64_t* __restrict__ ids, float* __restrict__ wts) {
+  __shared__ __align__(16) float sv[kWavesPerBlock][kMaxExperts];
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
   if (row >= rows) return;
-  topk_row(logits + row * experts, experts, k, ids + row * k, wts + row * k);
+  topk_row(logits + row * experts, experts, k, ids + row * k, wts + row * k, sv[threadIdx.x / kWave]);
 }
 
 // out[c] = sum_j w_j (down[ids[j] * hidden + c] . bf16(act_j)): bf16(act) of
@@ -817,6 +882,26 @@ int uocr_rocm_add_rms_norm_swiglu_gemv_bf16(void* stream, const float* x, const 
                                eps});
 }
 
+int uocr_rocm_add_rms_norm_swiglu_router_gemv_bf16(void* stream, const float* x, const float* delta, float* x_out,
+                                                   const float* w_norm, float eps, float* h_out, int64_t k,
+                                                   const uint16_t* w_gate, const uint16_t* w_up, int64_t ffn,
+                                                   float* act, const float* router, int64_t experts, float* logits) {
+  const char* what = "uocr_rocm_add_rms_norm_swiglu_router_gemv_bf16";
+  if (k < 0 || k > kFusedMaxK) return fail(UOCR_ROCM_INVALID_ARGUMENT, what, "k must be a multiple of 8 in [8, 2048]");
+  UOCR_REQUIRE(ffn >= 1 && experts >= 1 && experts <= (int64_t{1} << 20), what,
+               "ffn must be >= 1 and experts in [1, 2^20]");
+  UOCR_REQUIRE(w_up != nullptr && router != nullptr && logits != nullptr, what, "null up, router or logits");
+  UOCR_REQUIRE(aligned16(router), what, "the router weights must be 16-byte aligned");
+  auto overlaps = [&](const float* in) { return in != nullptr && logits < in + k && in < logits + experts; };
+  UOCR_REQUIRE(!overlaps(x) && !overlaps(delta) && !overlaps(x_out) && !overlaps(h_out), what,
+               "logits must not overlap x, delta, x_out or h_out");
+  FusedGemv a{x, delta, x_out, w_norm, h_out, w_gate, w_up, nullptr, act, ffn, static_cast<int>(k), eps};
+  a.w_f32 = router;
+  a.n_f32 = experts;
+  a.y_f32 = logits;
+  return fused_entry(what, stream, a);
+}
+
 int uocr_rocm_gemv_f32(void* stream, const float* x, int64_t k, const float* w, int64_t n, const float* bias,
                        float* y) {
   const char* what = "uocr_rocm_gemv_f32";
@@ -883,7 +968,8 @@ int expert_ffn_entry(const char* what, void* stream, const float* x, int64_t hid
   a.slot_rows = ffn;
   a.experts = experts;
   if (logits != nullptr) {
-    UOCR_REQUIRE(experts <= kMaxExperts, what, "experts must be in [1, 128] with router logits");
+    UOCR_REQUIRE(experts <= kMaxExperts && k <= experts, what,
+                 "experts must be in [1, 128] and k <= experts with router logits");
     a.logits = logits;
     a.top_k = static_cast<int>(k);
     a.ids_out = ids;

@@ -154,6 +154,14 @@ void add_rms_norm_swiglu_gemv_bf16(const Context& ctx, const float* x, const flo
                                                 ffn, act));
 }
 
+void add_rms_norm_swiglu_router_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out,
+                                          const float* w_norm, float eps, float* h_out, std::int64_t k,
+                                          const std::uint16_t* w_gate, const std::uint16_t* w_up, std::int64_t ffn,
+                                          float* act, const float* router, std::int64_t experts, float* logits) {
+  check(uocr_rocm_add_rms_norm_swiglu_router_gemv_bf16(ctx.stream(), x, delta, x_out, w_norm, eps, h_out, k, w_gate,
+                                                       w_up, ffn, act, router, experts, logits));
+}
+
 void scale_mask_softmax_rows(const Context& ctx, float* x, float scale, const float* mask, std::int64_t batch,
                              std::int64_t rows, std::int64_t cols) {
   check(uocr_rocm_scale_mask_softmax_rows(ctx.stream(), x, scale, mask, batch, rows, cols));

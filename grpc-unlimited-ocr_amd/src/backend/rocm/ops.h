@@ -122,6 +122,12 @@ void add_rms_norm_swiglu_gemv_bf16(const Context& ctx, const float* x, const flo
                                    const float* w_norm, float eps, float* h_out, std::int64_t k,
                                    const std::uint16_t* w_gate, const std::uint16_t* w_up, std::int64_t ffn,
                                    float* act);
+// New: the SwiGLU pair above and the fp32 router logits [experts] on the
+// unrounded h in one launch, bitwise it followed by gemv_f32(h, router).
+void add_rms_norm_swiglu_router_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out,
+                                          const float* w_norm, float eps, float* h_out, std::int64_t k,
+                                          const std::uint16_t* w_gate, const std::uint16_t* w_up, std::int64_t ffn,
+                                          float* act, const float* router, std::int64_t experts, float* logits);
 
 // ---- mixture of experts at decode (src/backend/cuda/ops.h:77-90) ------------------
 

@@ -133,14 +133,15 @@ void DecodeStep::body() {
       cur = 1 - cur;
       gemv_bf16(ctx_, act_.f32(), l.ffn, l.down, d.hidden, nullptr, delta_.f32());
     } else {
-      // The shared experts' MLP on h (the fused prologue also writes h for
-      // the router and the routed experts), then the routed experts' sum
-      // added to it (cuda_decoder.cpp:137-152).
+      // The shared experts' gate/up and the router's logits on h in one
+      // launch (the fused prologue also writes h for the routed experts),
+      // then the routed experts' sum added to the shared experts' down
+      // product (cuda_decoder.cpp:137-152).
       const MoeWeights& m = *l.moe;
-      add_rms_norm_swiglu_gemv_bf16(ctx_, x_[cur].f32(), o_.f32(), x_[1 - cur].f32(), l.post_norm, d.eps, h_.f32(),
-                                    d.hidden, m.shared_gate, m.shared_up, m.shared_ffn, act_.f32());
+      add_rms_norm_swiglu_router_gemv_bf16(ctx_, x_[cur].f32(), o_.f32(), x_[1 - cur].f32(), l.post_norm, d.eps,
+                                           h_.f32(), d.hidden, m.shared_gate, m.shared_up, m.shared_ffn, act_.f32(),
+                                           m.gate, m.experts, router_logits_.f32());
       cur = 1 - cur;
-      gemv_f32(ctx_, h_.f32(), d.hidden, m.gate, m.experts, nullptr, router_logits_.f32());
       moe_ffn_one(ctx_, h_.f32(), d.hidden, m.expert_ffn, m.gate_stack, m.up_stack, m.down_stack, m.experts,
                   router_logits_.f32(), m.top_k, expert_ids_.i64(), expert_weights_.f32(), act_.f32(), m.shared_down,
                   m.shared_ffn, expert_scratch_.f32(), delta_.f32());

@@ -19,12 +19,13 @@
 // (rms(x) w_final) W_lm. The reference's block routing (the attention mask
 // from summary/scores/route steps) and int8 weights are not part of it.
 //
-// Launches per step: 1 + per layer 6 (dense) or 8 (mixture of experts) +
+// Launches per step: 1 + per layer 6 (dense) or 7 (mixture of experts) +
 // 1. The residual add of each sublayer is the prologue of the next
 // projection (the fused GEMVs), rope + both appends + attention are one op
-// of two launches, the top k is taken inside the routed experts' gate/up
-// launch, and the shared experts' down product and the routed experts' sum
-// are formed in the routed experts' down launch.
+// of two launches, the router's logits are formed in the shared experts'
+// gate/up launch, the top k inside the routed experts' gate/up launch, and
+// the shared experts' down product and the routed experts' sum in the routed
+// experts' down launch.
 
 #include <cstdint>
 #include <memory>

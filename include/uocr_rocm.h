@@ -385,6 +385,17 @@ UOCR_ROCM_API int uocr_rocm_add_rms_norm_swiglu_gemv_bf16(void* stream, const fl
                                                           int64_t k, const uint16_t* w_gate, const uint16_t* w_up,
                                                           int64_t ffn, float* act);
 
+/* uocr_rocm_add_rms_norm_swiglu_gemv_bf16 (h_out may be null) and, in the
+ * same launch, the router's logits [experts] = router [experts, k] (fp32)
+ * . h with h unrounded: bitwise that call followed by uocr_rocm_gemv_f32
+ * on h, no bias (the shared experts' gate/up and the gate projection of
+ * cuda_decoder.cpp:137-146, which read the same normed row). New: no
+ * counterpart op in the reference. ffn >= 1, experts in [1, 2^20]. */
+UOCR_ROCM_API int uocr_rocm_add_rms_norm_swiglu_router_gemv_bf16(
+    void* stream, const float* x, const float* delta, float* x_out, const float* w_norm, float eps, float* h_out,
+    int64_t k, const uint16_t* w_gate, const uint16_t* w_up, int64_t ffn, float* act, const float* router,
+    int64_t experts, float* logits);
+
 /* rope on q [heads * hd] and the step's new key k_row [heads * hd] at
  * (state->tok, state->page), append of the rotated key and v_row at
  * state->pos (positions outside [0, capacity) append nothing), and the

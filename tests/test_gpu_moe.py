@@ -172,3 +172,31 @@ def test_moe_ffn_one_is_topk_shared_gemv_then_experts(backend, shared_ffn, exper
     backend.moe_ffn_one(x, dg, du, dd, logits, ids2, w2, act_s, sdown, scratch, got)
     assert torch.equal(ids1.view(-1), ids2) and torch.equal(w1.view(-1).view(torch.int32), w2.view(torch.int32))
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+@pytest.mark.parametrize("k,ffn,experts,with_delta", [(1280, 1792, 64, True), (2048, 1408, 128, False),
+                                                      (512, 20000, 5, True), (64, 24, 100, True)])
+def test_swiglu_router_gemv_is_swiglu_gemv_then_gemv_f32(backend, k, ffn, experts, with_delta):
+    """The shared experts' pair GEMV and the fp32 router in one launch:
+    bitwise add_rms_norm_swiglu_gemv_bf16 (its act, x_out and h_out), then
+    gemv_f32 on h_out (src/model/cuda/cuda_decoder.cpp:137-146)."""
+    x = dev_f32(normal(980, k))
+    delta = dev_f32(normal(981, k)) if with_delta else None
+    w_norm = dev_f32(1 + 0.02 * normal(982, k))
+    wg = dev_bf16(oracle.f32_to_bf16(normal(983, (ffn, k), 0.04)))
+    wu = dev_bf16(oracle.f32_to_bf16(normal(984, (ffn, k), 0.04)))
+    router = dev_f32(normal(985, (experts, k), 0.05))
+    act1, x1, h1 = (torch.empty(n, device="cuda") for n in (ffn, k, k))
+    backend.add_rms_norm_swiglu_gemv_bf16(x, wg, wu, act1, delta=delta, x_out=x1, w_norm=w_norm, h_out=h1)
+    want = torch.empty(experts, device="cuda")
+    backend.gemv_f32(h1, router, want)
+    act2, x2, h2 = (torch.empty(n, device="cuda") for n in (ffn, k, k))
+    got = torch.empty(experts, device="cuda")
+    backend.add_rms_norm_swiglu_router_gemv_bf16(x, wg, wu, act2, router, got, delta=delta, x_out=x2, w_norm=w_norm,
+                                                 h_out=h2)
+    for a, b in ((act1, act2), (x1, x2), (h1, h2), (want, got)):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert_f32_close(host_f32(got), oracle.linear(host_f32(h1)[None], host_f32(router))[0], 1e-5, "router logits")
+    if experts <= k:
+        with pytest.raises(ValueError):  # logits overlapping the input row
+            backend.add_rms_norm_swiglu_router_gemv_bf16(x, wg, wu, act2, router, x[:experts], w_norm=w_norm)
