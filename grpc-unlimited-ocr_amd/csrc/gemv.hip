@@ -272,9 +272,15 @@ __device__ __forceinline__ bool topk_better(float v, int e, float bv, int be) { 
 // experts against all of them read back from LDS: no dependent shuffles,
 // where k wave argmaxes were 12 dependent permutes each. A NaN score ranks
 // below every number.
-__device__ __forceinline__ void topk_row(const float* lr, int experts, int k, int64_t* ids, float* wts, float* sv) {
+struct TopkLane {
+  float v[2];     // the scores of experts lane and lane + 64
+  int rank[2];    // their ranks (meaningful below experts)
+};
+
+__device__ __forceinline__ TopkLane topk_rank(const float* lr, int experts, float* sv) {
   const int lane = threadIdx.x & (kWave - 1);
-  float v[2];
+  TopkLane t;
+  float (&v)[2] = t.v;
   float peak = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -313,24 +319,43 @@ __device__ __forceinline__ void topk_row(const float* lr, int experts, int k, in
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const bool two = experts > kWave;
   const int quads = ((two ? experts : kWave) + 3) / 4;
-  int rank[2] = {0, 0};
-  for (int q = 0; q < quads; ++q) {
-    const float4 o = reinterpret_cast<const float4*>(sv)[q];
-    const float ov[4] = {o.x, o.y, o.z, o.w};
+  int (&rank)[2] = t.rank;
+  rank[0] = rank[1] = 0;
+  if (two) {
+    for (int q = 0; q < quads; ++q) {
+      const float4 o = reinterpret_cast<const float4*>(sv)[q];
+      const float ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int e = 4 * q + t;
-      rank[0] += topk_better(ov[t], e, key[0], lane) ? 1 : 0;
-      if (two) rank[1] += topk_better(ov[t], e, key[1], lane + kWave) ? 1 : 0;
+      for (int t = 0; t < 4; ++t) {
+        rank[0] += topk_better(ov[t], 4 * q + t, key[0], lane) ? 1 : 0;
+        rank[1] += topk_better(ov[t], 4 * q + t, key[1], lane + kWave) ? 1 : 0;
+      }
+    }
+  } else {
+    for (int q = 0; q < quads; ++q) {
+      const float4 o = reinterpret_cast<const float4*>(sv)[q];
+      const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) rank[0] += topk_better(ov[t], 4 * q + t, key[0], lane) ? 1 : 0;
     }
   }
+  return t;
+}
+
+// The top k of a wave's ranks to ids[0..k) and wts[0..k).
+__device__ __forceinline__ void topk_store(const TopkLane& t, int experts, int k, int64_t* ids, float* wts) {
+  const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    if (lane + kWave * i < experts && rank[i] < k) {
-      ids[rank[i]] = lane + kWave * i;
-      wts[rank[i]] = v[i];
+    if (lane + kWave * i < experts && t.rank[i] < k) {
+      ids[t.rank[i]] = lane + kWave * i;
+      wts[t.rank[i]] = t.v[i];
     }
   }
+}
+
+__device__ __forceinline__ void topk_row(const float* lr, int experts, int k, int64_t* ids, float* wts, float* sv) {
+  topk_store(topk_rank(lr, experts, sv), experts, k, ids, wts);
 }
 
 // ---- fused decode GEMVs ----------------------------------------------------------
@@ -383,8 +408,7 @@ struct FusedGemv {
   unsigned main_blocks = 0;
 };
 
-// The weight row that output row r of a fused GEMV reads (ids: a.ids, or
-// the workgroup's own top k in LDS).
+// The weight row that output row r of a fused GEMV reads with the ids given.
 __device__ __forceinline__ int64_t fused_weight_row(const FusedGemv& a, const int64_t* ids, int64_t r) {
   if (ids == nullptr) return r;
   const int64_t slot = r / a.slot_rows;
@@ -510,21 +534,20 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_fused(const FusedGemv a) {
     return;
   }
 
-  // The routed experts' rows: this workgroup's own top k of the router's
-  // logits (bitwise expert_topk's), or the ids given.
+  // The routed experts' rows: the workgroup's own top k of the router's
+  // logits (bitwise expert_topk's), formed by wave 0 once the prologue's row
+  // loads are in flight, or the ids given.
+  __shared__ __align__(16) float s_scores[kMaxExperts];
   __shared__ int64_t s_ids[kMaxExpertSlots];
   __shared__ float s_wts[kMaxExpertSlots];
-  __shared__ __align__(16) float s_scores[kMaxExperts];
-  const int64_t* ids = a.ids;
-  if (a.logits != nullptr) {
-    if (wave == 0) topk_row(a.logits, static_cast<int>(a.experts), a.top_k, s_ids, s_wts, s_scores);
-    __syncthreads();
-    if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < a.top_k) {
-      a.ids_out[threadIdx.x] = s_ids[threadIdx.x];
-      a.wts_out[threadIdx.x] = s_wts[threadIdx.x];
-    }
-    ids = s_ids;
-  }
+  const bool routed = a.logits != nullptr;
+  auto weight_row = [&](int64_t r) -> int64_t {
+    if (!routed) return fused_weight_row(a, a.ids, r);
+    const int64_t slot = r / a.slot_rows;
+    int64_t id = s_ids[slot];
+    id = id >= 0 && id < a.experts ? id : 0;
+    return id * a.slot_rows + (r - slot * a.slot_rows);
+  };
   u32x4 wc[kMats][RPW][CPL];
   auto load_w = [&](int64_t g) {
     const int64_t row0 = g * RPW;
@@ -533,12 +556,15 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_fused(const FusedGemv a) {
       const uint16_t* w = m == 0 ? a.w1 : a.w2;
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
+        // formed by the whole wave (the expert lookup is a ballot), for a
+        // row clamped into [0, n) (the ids path reads ids[row / slot_rows])
+        const uint16_t* wrow = w + weight_row(row0 + r < a.n ? row0 + r : a.n - 1) * k;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
           const int c = lane + kWave * i;
           wc[m][r][i] = u32x4{0u, 0u, 0u, 0u};
           if (row0 + r < a.n && c < nchunks) {
-            wc[m][r][i] = stream_load(reinterpret_cast<const u32x4*>(w + fused_weight_row(a, ids, row0 + r) * k) + c);
+            wc[m][r][i] = stream_load(reinterpret_cast<const u32x4*>(wrow) + c);
           }
         }
       }
@@ -548,6 +574,14 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_fused(const FusedGemv a) {
   // both are in flight together and the row's arithmetic waits only for the
   // row (fused QKV 5.03 -> 4.88 us, with x written by the kernel before).
   fused_prologue<kNorm>(a, h_lds, wave, lane, [&] {
+    if (routed) {
+      if (wave == 0) topk_row(a.logits, static_cast<int>(a.experts), a.top_k, s_ids, s_wts, s_scores);
+      __syncthreads();
+      if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < a.top_k) {
+        a.ids_out[threadIdx.x] = s_ids[threadIdx.x];
+        a.wts_out[threadIdx.x] = s_wts[threadIdx.x];
+      }
+    }
     if (g0 < groups) load_w(g0);
   });
   float xv[CPL][8];
