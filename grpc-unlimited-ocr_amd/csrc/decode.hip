@@ -471,7 +471,8 @@ __global__ __launch_bounds__(kBlock) void attend_merge(const float* __restrict__
 // target: 6-7% faster for an fp32 cache at 8192 and 32768 positions (128
 // splits), and for a bf16 cache the same at 8192 (64 splits), 4% faster at
 // 32768 and 9% faster at 2048 (16 splits); an fp32 cache at 2048 positions
-// (32 splits) was 4% slower.
+// (32 splits) was 4% slower. Halving the 64 KB floor (128 splits for a bf16
+// cache at 8192 positions) was 11% slower (12.95 to 14.4 us).
 int attend_splits(int64_t heads, int64_t hd, int64_t capacity, int64_t elem_bytes) {
   int64_t s = (2048 + heads - 1) / heads;
   int64_t min_keys = 65536 / (2 * hd * elem_bytes);
