@@ -170,6 +170,23 @@ def test_fused_step_op_errors(backend):
              None, FAKE, detail="aligned")
     _invalid(backend, "uocr_rocm_add_rms_norm_swiglu_gemv_bf16", None, FAKE, None, None, None, 1e-6, None, 128,
              FAKE, None, 4, FAKE, detail="up")
+    # the fused router: experts >= 1, and logits never overlapping the row
+    _invalid(backend, "uocr_rocm_add_rms_norm_swiglu_router_gemv_bf16", None, FAKE, None, None, None, 1e-6, None,
+             128, FAKE, FAKE, 4, 0x30000, 0x40000, 0, 0x50000, detail="experts in [1, 2^20]")
+    _invalid(backend, "uocr_rocm_add_rms_norm_swiglu_router_gemv_bf16", None, FAKE, None, None, None, 1e-6, None,
+             128, FAKE, FAKE, 4, 0x30000, 0x40000, 64, FAKE + 64, detail="must not overlap")
+
+
+def test_expert_op_errors(backend):
+    x, scratch, out = 0x10000, 0x20000, 0x30000  # distinct, so only the tested rule fails
+    _invalid(backend, "uocr_rocm_expert_topk", None, FAKE, 4, 129, 6, FAKE, FAKE, detail="experts must be in [1, 128]")
+    _invalid(backend, "uocr_rocm_expert_topk", None, FAKE, 4, 6, 7, FAKE, FAKE, detail="k must be in [1, experts]")
+    _invalid(backend, "uocr_rocm_expert_ffn_one", None, x, 128, 64, FAKE, FAKE, FAKE, 16, FAKE, FAKE, 9, None,
+             scratch, out, detail="k must be in [1, 8]")
+    _invalid(backend, "uocr_rocm_moe_ffn_one", None, x, 128, 64, FAKE, FAKE, FAKE, 6, FAKE, 7, FAKE, FAKE, 0x40000,
+             0x50000, 64, scratch, out, detail="k <= experts")
+    _invalid(backend, "uocr_rocm_moe_ffn_one", None, x, 128, 64, FAKE, FAKE, FAKE, 200, FAKE, 6, FAKE, FAKE, 0x40000,
+             0x50000, 64, scratch, out, detail="experts must be in [1, 128]")
 
 
 def test_step_op_empty_shapes_and_scratch_size(backend):
