@@ -1,6 +1,6 @@
 """Tolerances and host<->device helpers shared by the GPU parity tests.
 
-Tolerances (BASELINE's parity gates):
+Tolerances (the parity gates of these ops):
   * gather: bit-exact.
   * fp32 ops: the reference's metric max|got - want| / max|want|
     (tests/cuda_ops_test.cpp:47-54) at most 1e-5 (1e-6 for the elementwise
