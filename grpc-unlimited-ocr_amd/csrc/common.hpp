@@ -18,6 +18,14 @@ constexpr int kWave = 64;                        // CDNA wavefront width
 constexpr int kBlock = 256;                      // 4 waves per workgroup
 constexpr int kWavesPerBlock = kBlock / kWave;   // one row per wave
 
+// The wave's index in its workgroup as a wave-uniform value (an SGPR): row
+// and head base pointers formed from it stay scalar, so each lane's address
+// is one 32-bit offset from a scalar base (global_load ... v_off, s[base])
+// instead of a 64-bit vector address.
+__device__ __forceinline__ int wave_in_block() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+}
+
 // ---- bf16 -----------------------------------------------------------------
 
 // bf16 -> fp32 is exact: the 16 bits become the top half of a binary32.

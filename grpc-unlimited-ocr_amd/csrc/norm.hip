@@ -54,7 +54,10 @@ __device__ __forceinline__ float clamp_act(float v) { return fminf(fmaxf(v, -kAc
 // TB threads per workgroup: kBlock, or one wave (one row per workgroup) for
 // one-wave rows in calls of fewer than kOneRowGroupsBelow rows. At 2048-4096
 // rows of 1024-2048 columns the one-wave groups ran LayerNorm and RMSNorm 2-8%
-// faster (add + RMSNorm -6% to +3%); at 8192 rows they were no faster.
+// faster (add + RMSNorm -6% to +3%), also against 4- and 8-wave groups that
+// share the weights through LDS (LayerNorm [4096, 1024] 4.46 against 4.66
+// and 4.76 us); at 8192 rows the 4-wave groups with shared weights are
+// faster (add+RMSNorm [8192, 2048] 1.5%).
 constexpr int64_t kOneRowGroupsBelow = 8192;
 
 template <class T, int VW, int WPR, int VPL, Norm kMode, int TB>
@@ -66,7 +69,17 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
   constexpr bool kTwoOut = kMode == Norm::kAddRms || kEmbed;  // writes x' and h
   constexpr int kRowsPerBlock = TB / kWave / WPR;
   __shared__ float red[kRowsPerBlock][kMaxGroups];
-  const int wave = threadIdx.x / kWave;
+  // One-wave rows in multi-wave workgroups share the norm weights through
+  // LDS: the block's waves each request a slice of w (and b) right after
+  // their row loads, write it to LDS after the fold, and every row reads its
+  // weights back from LDS. One request per block instead of one per row.
+  constexpr int kWavesPerGroup = TB / kWave;
+  constexpr bool kStage = WPR == 1 && kWavesPerGroup > 1 && VPL <= 8;
+  constexpr int kStageSlices = kStage ? (VPL + kWavesPerGroup - 1) / kWavesPerGroup : 1;
+  constexpr bool kStageB = kStage && kMode == Norm::kLayer;
+  __shared__ __attribute__((aligned(16))) float wst[kStage ? VPL * kWave * VW : 1];
+  __shared__ __attribute__((aligned(16))) float bst[kStageB ? VPL * kWave * VW : 1];
+  const int wave = wave_in_block();
   const int lane = threadIdx.x & (kWave - 1);
   const int rloc = wave / WPR, wr = wave % WPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rloc;
@@ -76,26 +89,50 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
   const int groups = (nvec + kWave - 1) / kWave;
   const int64_t off = (active ? row : 0) * cols;
 
+  // Every lane issues its row loads unconditionally: a chunk past the row
+  // (v >= nvec) or a wave past the last row reads a valid chunk instead and
+  // its values are dropped below. With no branch around them, the compiler
+  // waits for each chunk's own loads only (vmcnt counts down in order), so
+  // chunk k is formed, folded into its partial and its x' stored while
+  // chunks k + 1, ... are still in flight.
   Chunk<T, VW> cx[VPL];
   Chunk<T, VW> cd[VPL];
   Chunk<uint16_t, VW> ce[kEmbed ? VPL : 1];
+  bool live[VPL];
   const uint16_t* erow = nullptr;
+  bool erow_valid = false;
   if constexpr (kEmbed) {
     const int64_t id = src.state->token;
-    const bool valid = src.table_rows < 0 || (id >= 0 && id < src.table_rows);
-    erow = valid ? src.table + id * cols : nullptr;
+    erow_valid = src.table_rows < 0 || (id >= 0 && id < src.table_rows);
+    erow = src.table + (erow_valid ? id : 0) * cols;
   }
+  // Row bases are wave-uniform; a lane adds a 32-bit element offset.
+  T* const xrow = x + off;
+  const T* const drow = delta != nullptr ? delta + off : nullptr;
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = (wr + WPR * k) * kWave + lane;
-    if (active && v < nvec) {
-      if constexpr (kEmbed) {
-        if (erow != nullptr) ce[k].load(erow + static_cast<int64_t>(v) * VW);
-        else ce[k].clear();
-        if (delta != nullptr) cd[k].load(delta + off + static_cast<int64_t>(v) * VW);
-      } else {
-        cx[k].load(x + off + static_cast<int64_t>(v) * VW);
-        if constexpr (kMode == Norm::kAddRms) cd[k].load(delta + off + static_cast<int64_t>(v) * VW);
+    live[k] = active && v < nvec;
+    const uint32_t at = static_cast<uint32_t>(v < nvec ? v : nvec - 1) * VW;
+    if constexpr (kEmbed) {
+      ce[k].load(erow + at);
+      if (delta != nullptr) cd[k].load(drow + at);
+    } else {
+      cx[k].load(xrow + at);
+      if constexpr (kMode == Norm::kAddRms) cd[k].load(drow + at);
+    }
+  }
+
+  float wsl[kStageSlices][VW], bsl[kStageB ? kStageSlices : 1][VW];
+  if constexpr (kStage) {
+#pragma unroll
+    for (int j = 0; j < kStageSlices; ++j) {
+      const int g = wave + kWavesPerGroup * j;
+      const int v = g * kWave + lane;
+      const int vc = v < nvec ? v : nvec - 1;
+      if (g < groups) {
+        load_f32<VW>(w + vc * VW, wsl[j]);
+        if constexpr (kStageB) load_f32<VW>(b + vc * VW, bsl[j]);
       }
     }
   }
@@ -105,34 +142,42 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = (wr + WPR * k) * kWave + lane;
-    part[k] = 0.0f;
-    if (active && v < nvec) {
-      if constexpr (kEmbed) {
-        ce[k].widen(s[k]);
-        if (delta != nullptr) {
-          float d[VW];
-          cd[k].widen(d);
+    if constexpr (kEmbed) {
+      ce[k].widen(s[k]);
 #pragma unroll
-          for (int e = 0; e < VW; ++e) s[k][e] += d[e];
-        }
-      } else {
-        cx[k].widen(s[k]);
-      }
-      if constexpr (kMode == Norm::kAddRms) {
+      for (int e = 0; e < VW; ++e) s[k][e] = erow_valid ? s[k][e] : 0.0f;
+      if (delta != nullptr) {
         float d[VW];
         cd[k].widen(d);
 #pragma unroll
         for (int e = 0; e < VW; ++e) s[k][e] += d[e];
       }
-      if constexpr (kMode == Norm::kRouter) {
-#pragma unroll
-        for (int e = 0; e < VW; ++e) s[k][e] = __builtin_isfinite(s[k][e]) ? s[k][e] : 0.0f;
-      }
-#pragma unroll
-      for (int e = 0; e < VW; ++e) part[k] += kMode == Norm::kLayer ? s[k][e] : s[k][e] * s[k][e];
     } else {
+      cx[k].widen(s[k]);
+    }
+    if constexpr (kMode == Norm::kAddRms) {
+      float d[VW];
+      cd[k].widen(d);
 #pragma unroll
-      for (int e = 0; e < VW; ++e) s[k][e] = 0.0f;
+      for (int e = 0; e < VW; ++e) s[k][e] += d[e];
+    }
+    if constexpr (kMode == Norm::kRouter) {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) s[k][e] = __builtin_isfinite(s[k][e]) ? s[k][e] : 0.0f;
+    }
+    part[k] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) part[k] += kMode == Norm::kLayer ? s[k][e] : s[k][e] * s[k][e];
+    part[k] = live[k] ? part[k] : 0.0f;  // a dropped chunk adds nothing
+    // x' = x + delta does not depend on the reduction: it leaves as soon as
+    // its chunk is formed, so half of the kernel's writes overlap the row
+    // loads still in flight.
+    if constexpr (kTwoOut) {
+      if (live[k]) {
+        Chunk<T, VW> xs;
+        xs.narrow(s[k]);
+        xs.store(xrow + static_cast<uint32_t>(v) * VW);
+      }
     }
   }
 
@@ -176,19 +221,28 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
     inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss) / static_cast<double>(cols) +
                                         static_cast<double>(eps)));
   }
+  if constexpr (kStage) {
+#pragma unroll
+    for (int j = 0; j < kStageSlices; ++j) {
+      const int g = wave + kWavesPerGroup * j;
+      if (g < groups) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          wst[(g * kWave + lane) * VW + e] = wsl[j][e];
+          if constexpr (kStageB) bst[(g * kWave + lane) * VW + e] = bsl[j][e];
+        }
+      }
+    }
+    __syncthreads();
+  }
   if (!active) return;
 
-  T* out = kTwoOut ? h : x;
+  T* const orow = (kTwoOut ? h : x) + off;
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = (wr + WPR * k) * kWave + lane;
     if (v < nvec) {
-      const int64_t at = off + static_cast<int64_t>(v) * VW;
-      if constexpr (kTwoOut) {
-        Chunk<T, VW> xs;
-        xs.narrow(s[k]);
-        xs.store(x + at);
-      }
+      const uint32_t at = static_cast<uint32_t>(v) * VW;
       float wv[VW], bv[VW], y[VW];
       if constexpr (kEarlyW) {
 #pragma unroll
@@ -196,6 +250,9 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
           wv[e] = wv_e[k][e];
           if constexpr (kMode == Norm::kLayer) bv[e] = bv_e[k][e];
         }
+      } else if constexpr (kStage) {
+        load_f32<VW>(wst + v * VW, wv);
+        if constexpr (kMode == Norm::kLayer) load_f32<VW>(bst + v * VW, bv);
       } else {
         load_f32<VW>(w + v * VW, wv);
         if constexpr (kMode == Norm::kLayer) load_f32<VW>(b + v * VW, bv);
@@ -215,7 +272,7 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
       }
       Chunk<T, VW> o;
       o.narrow(y);
-      o.store(out + at);
+      o.store(orow + at);
     }
   }
 }

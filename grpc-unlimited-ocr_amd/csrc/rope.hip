@@ -102,7 +102,7 @@ __device__ __forceinline__ void load_pairs(const RopeArgs<T> a, int64_t row0, in
 template <class T, int VW, int ITERS, bool kPow2, int TPW>
 __global__ __launch_bounds__(kRopeBlock) void rope_rows(RopeArgs<T> a) {
   extern __shared__ __attribute__((aligned(16))) float table[];
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_block();
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kRopeWaves + wave) * TPW;
   const bool active = row0 < a.rows;
@@ -110,30 +110,10 @@ __global__ __launch_bounds__(kRopeBlock) void rope_rows(RopeArgs<T> a) {
   const int total = (a.heads0 + a.heads1) * cpp;  // chunk pairs per row
   float* wave_table = table + wave * TPW * 2 * a.half;
 
-  // Each row's rope coordinates, reduced to the two fp32 multipliers first,
-  // so that no 64-bit argument stays live across the load phase.
-  float ft[TPW], fp[TPW];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    ft[t] = 0.0f;
-    fp[t] = 0.0f;
-    const int64_t row = row0 + t;
-    if (row >= a.rows) continue;
-    int64_t tk, pg;
-    if (a.state != nullptr) {
-      tk = a.state->tok;
-      pg = a.state->page;
-    } else {
-      tk = a.tok != nullptr ? a.tok[row] : a.one_tok;
-      pg = a.page != nullptr ? a.page[row] : a.one_page;
-    }
-    if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
-    ft[t] = static_cast<float>(tk);
-    fp[t] = static_cast<float>(pg);
-  }
-
-  // The first batch of Q/K loads goes out before the rows' cos/sin are
-  // computed, so the transcendentals overlap the memory latency.
+  // The first batch of Q/K loads goes out before anything else: the rows'
+  // coordinates and frequencies are read after it, so no wave spends a
+  // dependent round trip on its positions before its first data request
+  // (reading them first cost RoPE on Q/K [8192, 16+4, 128] 5%).
   Chunk<T, VW> lo[ITERS], hi[ITERS];
   T* at[ITERS];
   int jj[ITERS], tt[ITERS];
@@ -141,11 +121,22 @@ __global__ __launch_bounds__(kRopeBlock) void rope_rows(RopeArgs<T> a) {
 
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    if (row0 + t < a.rows) {
+    const int64_t row = row0 + t;
+    if (row < a.rows) {
+      int64_t tk, pg;
+      if (a.state != nullptr) {
+        tk = a.state->tok;
+        pg = a.state->page;
+      } else {
+        tk = a.tok != nullptr ? a.tok[row] : a.one_tok;
+        pg = a.page != nullptr ? a.page[row] : a.one_page;
+      }
+      if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
+      const float ft = static_cast<float>(tk), fp = static_cast<float>(pg);
       float* cosv = wave_table + t * 2 * a.half;
       float* sinv = cosv + a.half;
       for (int p = lane; p < a.half; p += kWave) {
-        const float angle = p < a.n_tok ? ft[t] * a.inv_tok[p] : fp[t] * a.inv_page[p - a.n_tok];
+        const float angle = p < a.n_tok ? ft * a.inv_tok[p] : fp * a.inv_page[p - a.n_tok];
         float sn, cs;
         sincosf(angle, &sn, &cs);
         cosv[p] = cs;
