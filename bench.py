@@ -37,14 +37,17 @@ every step reads from HBM. After W untimed warm-up steps (which also bring
 the GPU clocks up), the K timed steps are captured once into a HIP graph and
 replayed; HIP events on the replay stream bracket each replay, with a device
 synchronisation on both sides, and the median of 5 replays is reported (each
-replay's time includes its one graph launch). Per-kernel figures come from
-the same procedure applied to one kernel.
+replay's time includes its one graph launch and the replay's fixed cost).
+Per-kernel and per-workload figures come from the same procedure with
+max(K, 100) launches per replay, so the replay's fixed cost of about 10 us
+is spread over at least 100 launches; the headline times exactly K steps.
 
 cpu_baseline: the reference's CPU path for workload 5 (the oracle's
 restatement of src/backend/reference/ops.cpp and src/model/page_rope.cpp,
-with the reference's threading: norms over rows on up to 16 threads,
-activations and rope serial) timed on this host; workloads 1-5 each carry
-the same CPU figure for their own work under "cpu".
+with the reference's threading: norms over rows on one thread per CPU this
+process may use, activations and rope serial) timed on this host, median
+of at least 20 runs after 3 warm-ups; workloads 1-5 each carry the same
+CPU figure for their own work under "cpu".
 """
 
 import argparse
@@ -123,16 +126,28 @@ def bytes_append(width):
 
 # ---- timing helpers ---------------------------------------------------------------------------------
 
+# Launches per graph replay for the per-kernel and per-workload figures (the
+# headline times exactly --steps). A replay carries a fixed cost of about
+# 10 us beyond its kernels (measured: 20 launches of add+RMSNorm [8192, 2048]
+# per replay 23.5 us each, 100 launches 22.9 us each; a spin kernel queued
+# ahead of the replay, which hides the host's submission, changed neither),
+# so a kernel's figure spreads it over at least this many launches.
+KERNEL_STEPS = 100
+
+
 class Timer:
     def __init__(self, torch, steps, warmup, replays=5, use_graphs=True):
         self.torch, self.steps, self.warmup, self.replays = torch, steps, warmup, replays
+        self.kernel_steps = max(steps, KERNEL_STEPS)
         self.use_graphs = use_graphs
 
-    def graph(self, step_fns):
+    def graph(self, step_fns, steps=None):
         """Median ms per step over `replays` replays of a graph holding
-        `steps` steps that rotate through step_fns (one per input set).
-        With graphs off (for counter collection), eager launches instead."""
+        `steps` steps (default: kernel_steps) that rotate through step_fns
+        (one per input set). With graphs off (for counter collection), eager
+        launches instead."""
         torch = self.torch
+        steps = self.kernel_steps if steps is None else steps
         if not self.use_graphs:
             ms = self.eager(step_fns)
             return ms, ms, ms
@@ -141,7 +156,7 @@ class Timer:
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for i in range(self.steps):
+            for i in range(steps):
                 step_fns[i % len(step_fns)]()
         g.replay()
         torch.cuda.synchronize()
@@ -153,7 +168,7 @@ class Timer:
             g.replay()
             end.record()
             torch.cuda.synchronize()
-            times.append(start.elapsed_time(end) / self.steps)
+            times.append(start.elapsed_time(end) / steps)
         del g
         return statistics.median(times), min(times), max(times)
 
@@ -376,7 +391,8 @@ def config5(be, torch, timer):
 
     first = chain_set()
     sets = [first] + [chain_set() for _ in range(n_sets(footprint(first.values())) - 1)]
-    ms, lo, hi = timer.graph([lambda s=s: step(s) for s in sets])
+    # the headline: exactly --steps steps per replay
+    ms, lo, hi = timer.graph([lambda s=s: step(s) for s in sets], steps=timer.steps)
     ms_eager = timer.eager([lambda s=s: step(s) for s in sets])
     nsets = len(sets)
     del sets, first
@@ -642,12 +658,13 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
 
 # ---- the CPU baseline (the reference's CPU path, restated in the oracle) ------------------------------
 
-def _cpu_median(fn, budget_s, max_runs=200):
-    """Median seconds per call of fn over at least 3 and at most max_runs
-    calls, or as many as budget_s allows, after one warm-up call."""
-    fn()
+def _cpu_median(fn, budget_s, max_runs=200, min_runs=20):
+    """Median seconds per call of fn after 3 warm-up calls, over at least
+    min_runs and at most max_runs calls (as many as budget_s allows)."""
+    for _ in range(3):
+        fn()
     times, t_end = [], time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < max_runs):
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
@@ -686,22 +703,15 @@ def cpu_workloads(budget_s, threads):
     table = np.empty((128000, 2048), np.uint16)  # untouched rows stay unmapped
     token, pos = 77777, 12345
     table[token] = oracle.f32_to_bf16(0.02 * g.standard_normal(2048, dtype=np.float32))
-    ids = np.array([token], np.int64)
-    tok = np.array([pos], np.int64)
     e, d2, h2, w2 = np.empty(2048, np.float32), rnd(2048), np.empty(2048, np.float32), wts(2048)
     q2, k2 = rnd(16 * 128), rnd(4 * 128)
     nul = ctypes.c_void_p()
 
-    def chain2():
-        lib.orc_embed(p(table), p(ids), 1, 2048, p(e))
-        lib.orc_add_rms_norm(p(e), p(d2), p(w2), p(h2), 1, 2048, 1e-6)
-        lib.orc_rope_apply(p(q2), 1, 16, 128, p(tok), nul, p(inv), 64, nul, 0, 0, 0, 0)
-        lib.orc_rope_apply(p(k2), 1, 4, 128, p(tok), nul, p(inv), 64, nul, 0, 0, 0, 0)
-
-    reps = 200
-    t, n = _cpu_median(lambda: [chain2() for _ in range(reps)], budget_s)
-    out["2"] = {"us": round(t / reps * 1e6, 3), "runs": n, "note": f"mean of {reps} chains per run, "
-                "including Python's per-call overhead (4 calls)"}
+    reps = 200  # chains per C call: the gather, add + RMSNorm and both ropes, with no Python between them
+    t, n = _cpu_median(lambda: lib.orc_decode_chain(p(table), token, p(d2), p(w2), p(e), p(h2), 2048, 1e-6, p(q2), 16,
+                                                    p(k2), 4, 128, pos, p(inv), 64, reps), budget_s)
+    out["2"] = {"us": round(t / reps * 1e6, 3), "runs": n,
+                "note": f"mean of {reps} chains per C call (one call per run)"}
     del table
 
     # 3: RoPE Q [8192, 16, 128], K [8192, 4, 128] in place, positions 0..8191
@@ -743,12 +753,30 @@ def cpu_workloads(budget_s, threads):
     return out
 
 
-def cpu_baseline(cpu, threads):
+def host_cpu():
+    """The host's CPU as this process sees it: the model string, the online
+    processor count (what std::thread::hardware_concurrency reports, the
+    reference's default thread count, src/backend/reference/ops.cpp:15) and
+    the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "nproc": os.cpu_count() or 1, "affinity": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline(cpu, threads, info):
     """The top-level cpu_baseline object: workload 5 from cpu_workloads."""
     c = cpu["5"]
     return {"value": c["gbps"], "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"workload 5 in full (8192 tokens), median of {c['runs']} chains on preallocated fp32 "
-                      f"buffers; norms on {threads} threads, activations and rope serial as in the reference",
+            "sample": f"workload 5 in full (8192 tokens), median of {c['runs']} chains after 3 warm-ups on "
+                      f"preallocated fp32 buffers; norms on {threads} threads (the CPUs this process may use), "
+                      f"activations and rope serial as in the reference",
+            "cpu_model": info["model"], "nproc": info["nproc"], "affinity_cpus": info["affinity"],
             "ms_per_chain": c["ms"], "ms_per_chain_1_thread": c["ms_1_thread"], "value_1_thread": c["gbps_1_thread"]}
 
 
@@ -910,9 +938,10 @@ def main():
                          "algorithmic_bytes": dom["bytes"]},
         })
     if not args.no_cpu and head is not None:
-        threads = max(1, min(16, os.cpu_count() or 1))
+        info_cpu = host_cpu()
+        threads = info_cpu["affinity"]
         cpu = cpu_workloads(args.cpu_seconds / 6, threads)
-        line["cpu_baseline"] = cpu_baseline(cpu, threads)
+        line["cpu_baseline"] = cpu_baseline(cpu, threads, info_cpu)
         for c, fig in cpu.items():
             if c in configs:
                 configs[c]["cpu"] = {**fig, "threads": threads, "kind": "port"}

@@ -264,6 +264,9 @@ void launch_copy_tb(hipStream_t s, float* dst, const float* src, int64_t n) {
 
 // ---- SwiGLU on [rows, 2 ffn] -> [rows, ffn] -------------------------------------
 
+// The 128-bit output chunks are stored with the sc1 policy bit (through a
+// buffer resource over the launch's output, at most 1 GiB): at [8192,
+// 2 x 1408] bf16 that measured 1.5-2.5% faster than nontemporal stores.
 template <class T, int VW, int TB>
 __global__ __launch_bounds__(TB) void swiglu_flat(const T* __restrict__ in, T* __restrict__ out, uint32_t total,
                                                   uint32_t cpr, uint64_t magic, int ffn) {
@@ -282,7 +285,12 @@ __global__ __launch_bounds__(TB) void swiglu_flat(const T* __restrict__ in, T* _
   for (int e = 0; e < VW; ++e) g[e] = silu_mul_f(g[e], u[e]);
   Chunk<T, VW> o;
   o.narrow(g);
-  o.store(out + static_cast<uint64_t>(row) * ffn + static_cast<uint64_t>(j) * VW);
+  if constexpr (VW * sizeof(T) == 16) {
+    const uint32_t bytes = total * 16u;  // total <= 2^26 chunks
+    buffer_store16<kPolicySc1>(buffer_rsrc(out, bytes), t * 16u, o.raw);
+  } else {
+    o.store(out + static_cast<uint64_t>(row) * ffn + static_cast<uint64_t>(j) * VW);
+  }
 }
 
 template <class T, int VW>

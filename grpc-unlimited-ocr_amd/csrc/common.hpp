@@ -107,6 +107,23 @@ struct Chunk<uint16_t, 8> {
   __device__ __forceinline__ void clear() { raw = u32x4{0u, 0u, 0u, 0u}; }
 };
 
+// A raw buffer resource over `bytes` bytes at `base` (gfx950 word 3: raw
+// 32-bit dwords, no swizzle). Accesses through it take a 32-bit byte offset;
+// the hardware drops a store past `bytes` and returns zero for such a load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// Cache-policy bits of a buffer access on gfx950 (the instruction's sc0, nt
+// and sc1 modifiers).
+constexpr int kPolicySc0 = 1, kPolicyNt = 2, kPolicySc1 = 16;
+
+// A 128-bit store through a buffer resource with policy bits `kPolicy`.
+template <int kPolicy>
+__device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t r, uint32_t offset, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, offset, 0, kPolicy);
+}
+
 // Four bf16 (8 bytes): an fp32 row chunk's worth of a bf16 table row.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 

@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
             "orc_rope_apply": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64], None),
             "orc_embed": ([_vp, _vp, _i64, _i64, _vp], None),
             "orc_add_rms_norm": ([_vp, _vp, _vp, _vp, _i64, _i64, _f], None),
+            "orc_decode_chain": ([_vp, _i64, _vp, _vp, _vp, _vp, _i64, _f, _vp, _i64, _vp, _i64, _i64, _i64, _vp,
+                                  _i64, _i64], None),
             "orc_swiglu": ([_vp, _vp, _i64, _i64], None),
             "orc_router_norm": ([_vp, _vp, _i64, _i64, _f], None),
             "orc_linear": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], None),

@@ -263,6 +263,24 @@ ORC_API void orc_add_rms_norm(float* x, const float* delta, const float* w, floa
   orc_rms_norm(h, w, rows, cols, eps);
 }
 
+/* The batch-1 decode chain of the CPU baseline, `reps` times in one call so
+ * that no interpreter overhead sits between the ops: the embedding row of
+ * `token` (Decoder::embed, src/model/decoder.cpp:85-92), the residual add
+ * and RMSNorm (orc_add_rms_norm above), then rope on q and k at position
+ * `pos` (PageRope::apply, src/model/page_rope.cpp:26-56). x receives the
+ * embedding row each time, so every repetition does the same work. */
+ORC_API void orc_decode_chain(const uint16_t* table, int64_t token, const float* delta, const float* w, float* x,
+                              float* h, int64_t cols, float eps, float* q, int64_t q_heads, float* k,
+                              int64_t k_heads, int64_t dim, int64_t pos, const float* inv, int64_t n_tok,
+                              int64_t reps) {
+  for (int64_t r = 0; r < reps; ++r) {
+    orc_embed(table, &token, 1, cols, x);
+    orc_add_rms_norm(x, delta, w, h, 1, cols, eps);
+    orc_rope_apply(q, 1, q_heads, dim, &pos, NULL, inv, n_tok, NULL, 0, 0, 0, 0);
+    orc_rope_apply(k, 1, k_heads, dim, &pos, NULL, inv, n_tok, NULL, 0, 0, 0, 0);
+  }
+}
+
 /* SwiGLU of GatedMlp::forward (src/model/feed_forward.cpp:18-24) on a
  * concatenated [gate | up] row layout: g = silu(gate); g *= up. */
 ORC_API void orc_swiglu(const float* in, float* out, int64_t rows, int64_t ffn) {

@@ -30,6 +30,9 @@ void orc_rope_apply(float* x, int64_t rows, int64_t heads, int64_t dim, const in
                     int64_t one_tok, int64_t one_page);
 void orc_embed(const uint16_t* table, const int64_t* ids, int64_t n, int64_t cols, float* dst);
 void orc_add_rms_norm(float* x, const float* delta, const float* w, float* h, int64_t rows, int64_t cols, float eps);
+void orc_decode_chain(const uint16_t* table, int64_t token, const float* delta, const float* w, float* x, float* h,
+                      int64_t cols, float eps, float* q, int64_t q_heads, float* k, int64_t k_heads, int64_t dim,
+                      int64_t pos, const float* inv, int64_t n_tok, int64_t reps);
 void orc_swiglu(const float* in, float* out, int64_t rows, int64_t ffn);
 void orc_router_norm(float* x, const float* w, int64_t rows, int64_t cols, float eps);
 void orc_linear(const float* x, int64_t m, int64_t k, const float* w, int64_t n, const float* bias, float* y);

@@ -13,6 +13,9 @@ from conftest import ROOT
 
 sys.path.insert(0, ROOT)
 import bench  # noqa: E402
+import numpy as np  # noqa: E402
+
+import oracle  # noqa: E402
 
 
 def test_more_than_one_gpu_is_refused():
@@ -42,9 +45,36 @@ def test_cpu_workloads_report_every_workload():
     for c in ("1", "3", "4", "5"):
         assert cpu[c]["ms"] > 0 and cpu[c]["gbps"] > 0 and cpu[c]["runs"] >= 3
     assert cpu["2"]["us"] > 0
-    line = bench.cpu_baseline(cpu, 2)
+    for c in ("1", "2", "3", "4", "5"):
+        assert cpu[c]["runs"] >= 20  # at least 20 timed runs after 3 warm-ups
+    info = bench.host_cpu()
+    assert info["nproc"] >= 1 and 1 <= info["affinity"] <= info["nproc"] and info["model"]
+    line = bench.cpu_baseline(cpu, 2, info)
     assert line["kind"] == "port" and line["cores"] == 2 and line["unit"] == "GB/s"
     assert line["value"] == cpu["5"]["gbps"] and line["value_1_thread"] > 0
+    assert line["cpu_model"] == info["model"] and line["nproc"] == info["nproc"]
+
+
+def test_decode_chain_in_one_call_is_the_composed_ops():
+    """orc_decode_chain (workload 2's CPU figure in one C call) is the
+    gather, add + RMSNorm and the two ropes, bit for bit."""
+    g = np.random.default_rng(3)
+    cols, qh, kh, dim, token, pos = 256, 4, 2, 64, 5, 777
+    table = oracle.f32_to_bf16(g.standard_normal((9, cols), dtype=np.float32))
+    delta = g.standard_normal(cols, dtype=np.float32)
+    w = (1 + 0.02 * g.standard_normal(cols)).astype(np.float32)
+    q0 = g.standard_normal(qh * dim, dtype=np.float32)
+    k0 = g.standard_normal(kh * dim, dtype=np.float32)
+    inv = oracle.rope_inv(dim // 2, 1e4)
+    x, h, q, k = np.empty(cols, np.float32), np.empty(cols, np.float32), q0.copy(), k0.copy()
+    p = lambda a: a.ctypes.data  # noqa: E731
+    oracle.lib().orc_decode_chain(p(table), token, p(delta), p(w), p(x), p(h), cols, 1e-6, p(q), qh, p(k), kh, dim,
+                                  pos, p(inv), dim // 2, 1)
+    want_x, want_h = oracle.add_rms_norm(oracle.embed(table, np.array([token])).ravel(), delta, w, 1e-6)
+    tok = np.array([pos], np.int64)
+    assert np.array_equal(x, want_x) and np.array_equal(h, want_h)
+    assert np.array_equal(q, oracle.rope(q0.reshape(1, -1), qh, dim, tok=tok, inv_tok=inv).ravel())
+    assert np.array_equal(k, oracle.rope(k0.reshape(1, -1), kh, dim, tok=tok, inv_tok=inv).ravel())
 
 
 def _write_csv(path, fields, rows):
