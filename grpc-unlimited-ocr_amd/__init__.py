@@ -122,6 +122,7 @@ _SIGNATURES = {
                                             _vp, _i64, _vp, _i64, _vp], _int),
     "uocr_rocm_attend_scratch_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_attend_step": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
+    "uocr_rocm_attend_step_noalloc": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _i64, _vp], _int),
     "uocr_rocm_scale_mask_softmax_rows": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_embed_add_rms_norm_step": ([_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _f32], _int),
     "uocr_rocm_embed_add_rms_norm_step_bf16": ([_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _f32], _int),
@@ -463,6 +464,21 @@ def attend_step(q, k_cache, v_cache, heads, hd, mask, scale, state, scratch, out
         raise ValueError("k_cache and v_cache must share a dtype")
     _op("uocr_rocm_attend_step_bf16" if bf else "uocr_rocm_attend_step", stream, _ptr(q), _ptr(k_cache),
         _ptr(v_cache), heads, hd, _f32_param(mask), scale, _ptr(state), _ptr(scratch), capacity, _ptr(out))
+
+
+def attend_step_noalloc(q, k_cache, v_cache, heads, hd, mask, scale, state, out, stream=None):
+    """attend_step with no scratch argument: the split records go to the
+    library's fixed per-device array (at most 1,048,576 floats), so the call
+    allocates nothing. Calls that overlap on one GPU race on that array."""
+    capacity = k_cache.numel() // (heads * hd) if heads * hd else 0
+    if v_cache.numel() != k_cache.numel() or q.numel() != heads * hd or out.numel() != heads * hd:
+        raise ValueError("attend_step_noalloc shapes: q, out [heads * hd]; k_cache, v_cache [capacity, heads * hd]")
+    if mask is not None and mask.numel() < capacity:
+        raise ValueError("mask must hold capacity floats")
+    if _is_bf16(k_cache) or _is_bf16(v_cache):
+        raise ValueError("attend_step_noalloc takes float32 caches")
+    _op("uocr_rocm_attend_step_noalloc", stream, _ptr(q), _ptr(k_cache), _ptr(v_cache), heads, hd,
+        _f32_param(mask), scale, _ptr(state), capacity, _ptr(out))
 
 
 # ---- fused decode-step ops -------------------------------------------------------------------

@@ -648,6 +648,15 @@ int attend_rope(const char* what, void* stream, const float* q, const float* k_r
 }
 
 }  // namespace
+
+// uocr_rocm_attend_step's body under a caller-chosen name (the entry point
+// that allocates nothing reports its errors under its own name).
+int attend_step_f32(const char* what, void* stream, const float* q, const float* k_cache, const float* v_cache,
+                    int64_t heads, int64_t hd, const float* mask, float scale, const uocr_rocm_step_state* state,
+                    float* scratch, int64_t capacity, float* out) {
+  return attend_plain(what, stream, q, k_cache, v_cache, heads, hd, mask, scale, state, scratch, capacity, out);
+}
+
 }  // namespace uocr_rocm
 
 extern "C" {

@@ -340,6 +340,22 @@ UOCR_ROCM_API int uocr_rocm_attend_step(void* stream, const float* q, const floa
                                         const uocr_rocm_step_state* state, float* scratch, int64_t capacity,
                                         float* out);
 
+/* uocr_rocm_attend_step without the scratch argument: the same kernels and
+ * results, with the split records in a fixed device array of 1,048,576
+ * floats (4 MiB) that each GPU the library runs on holds until the process
+ * ends, so the call allocates nothing (no hipMalloc, hipFree or allocating
+ * library routine). It has no counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation). A (heads, hd, capacity) whose
+ * uocr_rocm_attend_scratch_floats exceeds 1,048,576 is rejected with
+ * UOCR_ROCM_INVALID_ARGUMENT. Every call on one GPU shares that GPU's array
+ * and leaves its records there; calls that overlap on one GPU (two streams,
+ * or two host threads) race on it. */
+UOCR_ROCM_API int uocr_rocm_attend_step_noalloc(void* stream, const float* q, const float* k_cache,
+                                                const float* v_cache, int64_t heads, int64_t hd, const float* mask,
+                                                float scale, const uocr_rocm_step_state* state, int64_t capacity,
+                                                float* out);
+
 /* ---- fused decode-step ops (new) ---------------------------------------------
  * One launch where the reference's decode step makes several; each gives
  * bitwise the result of the unfused entry points it replaces. */
