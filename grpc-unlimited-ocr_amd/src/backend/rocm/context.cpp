@@ -2,7 +2,6 @@
 
 #include <stdexcept>
 #include <string>
-#include <utility>
 
 #include "backend/rocm/dtype.h"
 #include "uocr_rocm.h"
@@ -10,14 +9,16 @@
 namespace uocr::rocm {
 namespace {
 
-std::size_t element_bytes(DType t) {
-  switch (t) {
-    case DType::kI8: return 1;
-    case DType::kBF16: return 2;
-    case DType::kF32: return 4;
-    case DType::kI64: return 8;
-  }
-  return 1;
+// Bytes per element, indexed by the DType enumerator's value.
+constexpr std::size_t kElementBytes[] = {4, 2, 8, 1};  // kF32, kBF16, kI64, kI8
+static_assert(static_cast<int>(DType::kF32) == 0 && static_cast<int>(DType::kBF16) == 1 &&
+              static_cast<int>(DType::kI64) == 2 && static_cast<int>(DType::kI8) == 3);
+
+constexpr std::size_t bytes_of(DType t) { return kElementBytes[static_cast<std::size_t>(t)]; }
+
+const char* type_name(DType t) {
+  constexpr const char* kNames[] = {"fp32", "bf16", "int64", "int8"};
+  return kNames[static_cast<std::size_t>(t)];
 }
 
 }  // namespace
@@ -77,51 +78,21 @@ void copy_to_host(const Context& ctx, PinnedBuffer& dst, const void* device_src,
   check(uocr_rocm_memcpy(dst.data(), device_src, bytes, UOCR_ROCM_D2H, ctx.stream()));
 }
 
-Array::Array(const Context& ctx, DType type, std::int64_t count) : ctx_(&ctx), count_(count), type_(type) {
-  if (count < 0) throw std::invalid_argument("Array: negative element count");
-  const std::size_t bytes = static_cast<std::size_t>(count) * element_bytes(type);
-  check(uocr_rocm_malloc(&data_, bytes, ctx.stream()));
+Array::Array(const Context& ctx, DType type, std::int64_t count)
+    : ctx_(&ctx), block_(nullptr, StreamRelease{ctx.stream()}), count_(count), type_(type) {
+  if (count < 0) throw std::invalid_argument("Array: the element count must not be negative");
+  void* p = nullptr;
+  check(uocr_rocm_malloc(&p, static_cast<std::size_t>(count) * bytes_of(type), ctx.stream()));
+  block_.reset(p);
 }
 
-void Array::release() noexcept {
-  if (data_ != nullptr && ctx_ != nullptr) (void)uocr_rocm_free(data_, ctx_->stream());
-  data_ = nullptr;
+void StreamRelease::operator()(void* p) const noexcept {
+  if (p != nullptr) (void)uocr_rocm_free(p, stream);
 }
 
-Array::~Array() { release(); }
-
-Array::Array(Array&& o) noexcept
-    : ctx_(o.ctx_), data_(std::exchange(o.data_, nullptr)), count_(std::exchange(o.count_, 0)), type_(o.type_) {}
-
-Array& Array::operator=(Array&& o) noexcept {
-  if (this != &o) {
-    release();
-    ctx_ = o.ctx_;
-    data_ = std::exchange(o.data_, nullptr);
-    count_ = std::exchange(o.count_, 0);
-    type_ = o.type_;
-  }
-  return *this;
-}
-
-float* Array::f32() const {
-  if (type_ != DType::kF32) throw std::logic_error("Array: not fp32");
-  return static_cast<float*>(data_);
-}
-
-std::uint16_t* Array::bf16() const {
-  if (type_ != DType::kBF16) throw std::logic_error("Array: not bf16");
-  return static_cast<std::uint16_t*>(data_);
-}
-
-std::int64_t* Array::i64() const {
-  if (type_ != DType::kI64) throw std::logic_error("Array: not int64");
-  return static_cast<std::int64_t*>(data_);
-}
-
-std::int8_t* Array::i8() const {
-  if (type_ != DType::kI8) throw std::logic_error("Array: not int8");
-  return static_cast<std::int8_t*>(data_);
+void Array::type_mismatch(DType want) const {
+  throw std::logic_error(std::string("Array: a ") + type_name(want) + " view of an array of " + type_name(type_) +
+                         " elements");
 }
 
 namespace {
@@ -169,7 +140,7 @@ std::vector<float> Array::download() const {
   }
   std::vector<float> out(static_cast<std::size_t>(count_));
   if (type_ == DType::kF32) {
-    check(uocr_rocm_memcpy(out.data(), data_, out.size() * 4, UOCR_ROCM_D2H, ctx_->stream()));
+    check(uocr_rocm_memcpy(out.data(), data(), out.size() * 4, UOCR_ROCM_D2H, ctx_->stream()));
     ctx_->synchronize();
     return out;
   }
@@ -186,7 +157,7 @@ std::vector<std::uint16_t> Array::download_bf16() const {
 }
 
 void Array::zero() {
-  check(uocr_rocm_zero(data_, static_cast<std::size_t>(count_) * element_bytes(type_), ctx_->stream()));
+  check(uocr_rocm_zero(data(), static_cast<std::size_t>(count_) * bytes_of(type_), ctx_->stream()));
 }
 
 }  // namespace uocr::rocm

@@ -33,8 +33,9 @@ void check(int status);
 
 class Graph;
 
-// One device and one non-blocking stream. Every op runs on this stream in
-// order; host reads synchronise explicitly.
+// A device and the one non-blocking HIP stream every op of this backend is
+// queued on, in submission order. Nothing here waits for the device unless
+// a call says it does (synchronize, the download functions).
 class Context {
  public:
   explicit Context(int device = 0);
@@ -44,8 +45,9 @@ class Context {
 
   void synchronize() const;
 
-  // Records everything enqueued between the two calls as a graph instead of
-  // running it.
+  // Between begin_capture and end_capture, work queued on the stream is not
+  // executed: it is collected, and end_capture returns it as a replayable
+  // graph.
   void begin_capture() const;
   std::unique_ptr<Graph> end_capture() const;
 
@@ -58,8 +60,8 @@ class Context {
   void* stream_ = nullptr;
 };
 
-// A captured, instantiated sequence of device work, replayed on the
-// context's stream.
+// Work collected by Context::begin_capture / end_capture, instantiated once;
+// launch() queues one replay on the stream it was captured from.
 class Graph {
  public:
   Graph(void* handle, void* stream) : handle_(handle), stream_(stream) {}
@@ -73,8 +75,8 @@ class Graph {
   void* stream_ = nullptr;
 };
 
-// Page-locked host memory, so copies to and from the device are enqueued
-// without blocking the host.
+// Host memory pinned for DMA: a copy between it and the device is queued
+// on the stream and the host continues at once.
 class PinnedBuffer {
  public:
   explicit PinnedBuffer(std::size_t bytes);
@@ -89,52 +91,71 @@ class PinnedBuffer {
   std::size_t bytes_ = 0;
 };
 
-// Stream-ordered copies; neither waits.
+// Queue a copy of `bytes` (at most the pinned buffer's size) behind the
+// stream's earlier work and return without waiting for it.
 void copy_to_device(const Context& ctx, void* device_dst, const PinnedBuffer& src, std::size_t bytes);
 void copy_to_host(const Context& ctx, PinnedBuffer& dst, const void* device_src, std::size_t bytes);
 
 enum class DType : std::uint8_t { kF32, kBF16, kI64, kI8 };
 
-// Device memory of `count` elements of one type, allocated and freed in
-// stream order. Contents are undefined until written.
+// Gives an Array's block back to the device pool on the stream it was taken
+// on (the deleter of Array's owning pointer).
+struct StreamRelease {
+  void* stream = nullptr;
+  void operator()(void* p) const noexcept;
+};
+
+// `count` device elements of one DType. The block is taken from and given
+// back to the device's pool on the context's stream, so its lifetime is
+// ordered with the work queued there; it holds garbage until written. A
+// moved-from Array owns nothing.
 class Array {
  public:
   Array() = default;
   Array(const Context& ctx, DType type, std::int64_t count);
-  ~Array();
-  Array(Array&& other) noexcept;
-  Array& operator=(Array&& other) noexcept;
+  ~Array() = default;
+  Array(Array&&) noexcept = default;
+  Array& operator=(Array&&) noexcept = default;
   Array(const Array&) = delete;
   Array& operator=(const Array&) = delete;
 
-  // Host fp32 in; stored as `type()` (bf16 rounds to nearest even).
+  // From host fp32 values: copied as they are into a kF32 array, rounded to
+  // bf16 (nearest even) for a kBF16 one. Waits for the copy.
   void upload(const float* host, std::int64_t count, std::int64_t offset = 0);
-  // Host bf16 bits in, for kBF16 arrays.
+  // Raw bf16 bit patterns into a kBF16 array. Waits for the copy.
   void upload(const std::uint16_t* host, std::int64_t count, std::int64_t offset = 0);
-  // Host indices in, for kI64 arrays.
+  // 64-bit integers (indices, positions) into a kI64 array.
   void upload(const std::int64_t* host, std::int64_t count, std::int64_t offset = 0);
-  // Host bytes in, for kI8 arrays.
+  // Signed bytes into a kI8 array.
   void upload(const std::int8_t* host, std::int64_t count, std::int64_t offset = 0);
-  // Device contents widened to fp32 (synchronises the stream).
+  // The whole array as fp32 on the host (bf16 widened exactly); waits for
+  // the stream.
   std::vector<float> download() const;
-  // Raw bf16 bits (synchronises the stream), for kBF16 arrays.
+  // The bit patterns of a kBF16 array; waits for the stream.
   std::vector<std::uint16_t> download_bf16() const;
   void zero();
 
-  void* data() const { return data_; }
-  float* f32() const;
-  std::uint16_t* bf16() const;
-  std::int64_t* i64() const;
-  std::int8_t* i8() const;
+  void* data() const { return block_.get(); }
+  // Typed views of data(); each throws std::logic_error when the array
+  // holds another element type.
+  float* f32() const { return typed<float>(DType::kF32); }
+  std::uint16_t* bf16() const { return typed<std::uint16_t>(DType::kBF16); }
+  std::int64_t* i64() const { return typed<std::int64_t>(DType::kI64); }
+  std::int8_t* i8() const { return typed<std::int8_t>(DType::kI8); }
   std::int64_t count() const { return count_; }
   DType type() const { return type_; }
   const Context* context() const { return ctx_; }
 
  private:
-  void release() noexcept;
+  template <class T>
+  T* typed(DType want) const {
+    if (type_ != want) type_mismatch(want);
+    return static_cast<T*>(block_.get());
+  }
+  [[noreturn]] void type_mismatch(DType want) const;
 
   const Context* ctx_ = nullptr;
-  void* data_ = nullptr;
+  std::unique_ptr<void, StreamRelease> block_;
   std::int64_t count_ = 0;
   DType type_ = DType::kF32;
 };

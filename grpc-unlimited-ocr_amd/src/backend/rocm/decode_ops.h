@@ -13,12 +13,14 @@
 
 namespace uocr::rocm {
 
+// The five int64 words a decode step reads from the device (the layout of
+// src/backend/cuda/decode_ops.h:17-23, which the kernels index directly).
 struct StepState {
-  std::int64_t token;       // the token being fed
-  std::int64_t pos;         // its position; keys = pos + 1 after the append
-  std::int64_t tok;         // rope token coordinate
-  std::int64_t page;        // rope page coordinate
-  std::int64_t query_page;  // response page for routing, -1 = unrestricted
+  std::int64_t token;       // id whose embedding row enters the step
+  std::int64_t pos;         // cache row written this step; pos + 1 keys are live after it
+  std::int64_t tok;         // rotary coordinate on the token axis
+  std::int64_t page;        // rotary coordinate on the page axis
+  std::int64_t query_page;  // page the block router confines this query to (-1: any)
 };
 
 void embed_step(const Context& ctx, const std::uint16_t* table, const StepState* state, std::int64_t cols, float* dst);
@@ -35,14 +37,15 @@ void rope_qk_step_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_head
 void embed_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows, const StepState* state,
                      std::int64_t cols, std::uint16_t* dst);
 
-// cache[pos] = row, rows `width` wide (src/backend/cuda/decode_ops.h:28-29).
-// capacity >= 0 bounds pos (an out-of-range pos writes nothing); -1 leaves
-// it unchecked, as the reference does.
+// Writes `row` (width floats) into row state->pos of `cache`
+// (src/backend/cuda/decode_ops.h:28-29). With capacity >= 0 a pos outside
+// [0, capacity) writes nothing; -1 trusts pos, as the reference does.
 void append_step(const Context& ctx, float* cache, const float* row, std::int64_t width, const StepState* state,
                  std::int64_t capacity = -1);
-// Masked attention of one query over keys 0..pos: out [heads * hd]
-// (decode_ops.h:42-47). `scratch` holds attend_scratch_floats(heads, hd,
-// capacity) floats; mask may be null.
+// One query row [heads * hd] attends over cache rows 0..state->pos with an
+// optional additive key mask; out [heads * hd] (decode_ops.h:42-47). The
+// per-split records go to `scratch`, attend_scratch_floats(heads, hd,
+// capacity) floats that the caller owns.
 std::int64_t attend_scratch_floats(std::int64_t heads, std::int64_t hd, std::int64_t capacity);
 void attend_step(const Context& ctx, const float* q, const float* k_cache, const float* v_cache, std::int64_t heads,
                  std::int64_t hd, const float* mask, float scale, const StepState* state, float* scratch,

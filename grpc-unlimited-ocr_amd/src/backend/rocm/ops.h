@@ -30,17 +30,20 @@ void rms_norm(const Context& ctx, float* x, const float* w, std::int64_t rows, s
 void gelu_erf(const Context& ctx, float* x, std::int64_t n);
 void silu_mul(const Context& ctx, float* g, const float* u, std::int64_t n);  // g = silu(g) * u
 
-// Two-axis rope on x [rows, heads * dim], one (tok, page) per row; with
-// null tok/page arrays the single row uses `one_tok` / `one_page`.
+// Rotary embedding of x [rows, heads * dim] in place: pairs below n_tok
+// turn by the row's token coordinate, the rest by its page coordinate
+// (mod page_mod). Coordinates come per row from tok / page, or, when those
+// are null, from one_tok / one_page for every row.
 void rope(const Context& ctx, float* x, std::int64_t rows, std::int64_t heads, std::int64_t dim, const std::int64_t* tok,
           const std::int64_t* page, const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t n_page,
           std::int64_t page_mod, std::int64_t one_tok = 0, std::int64_t one_page = 0);
 
-// dst = src for n elements (device to device).
+// Copies n floats from src to dst, both on the device; the two ranges must
+// not overlap.
 void copy(const Context& ctx, float* dst, const float* src, std::int64_t n);
 
-// bf16 table rows -> fp32 rows (token embeddings); one_index serves a single
-// row without an index array. The table's row count is unknown here, so the
+// Token embeddings: rows of a bf16 table widened into fp32 rows (exact);
+// one_index picks a single row without a device index array. The table's row count is unknown here, so the
 // indices are trusted as in the reference; the overloads taking table_rows
 // turn an out-of-range device index into a zero row instead.
 void gather_rows_bf16(const Context& ctx, const std::uint16_t* table, const std::int64_t* index, std::int64_t rows,
@@ -95,10 +98,11 @@ void router_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std:
                       float eps);
 void quick_gelu(const Context& ctx, float* x, std::int64_t n);
 void quick_gelu_bf16(const Context& ctx, std::uint16_t* x, std::int64_t n);
-// Softmax over each row of x [rows, cols] in place; a fully masked row
-// (all -inf) becomes zeros.
+// Each row of x [rows, cols] becomes its softmax, in place. A row whose
+// entries are all -inf becomes all zeros.
 void softmax_rows(const Context& ctx, float* x, std::int64_t rows, std::int64_t cols);
-// x[b, r, c] = x[b, r, c] * scale + mask[r, c], for each of `batch` slices.
+// For every slice b of `batch` [rows, cols] slices of x:
+// x[b] = x[b] * scale + mask, the one mask [rows, cols] shared by the slices.
 void scale_add_mask(const Context& ctx, float* x, float scale, const float* mask, std::int64_t batch, std::int64_t rows,
                     std::int64_t cols);
 
@@ -131,15 +135,17 @@ void add_rms_norm_swiglu_router_gemv_bf16(const Context& ctx, const float* x, co
 
 // ---- mixture of experts at decode (src/backend/cuda/ops.h:77-90) ------------------
 
-// Softmax over each row of gate logits [rows, experts], then the top k
-// (lower index on a tie) as expert ids and their scores.
+// For each row of router logits [rows, experts]: its softmax, then the k
+// largest probabilities (the lower expert index first where two are equal)
+// written as ids and weights.
 void expert_topk(const Context& ctx, const float* logits, std::int64_t rows, std::int64_t experts, std::int64_t k,
                  std::int64_t* ids, float* weights);
 // Floats of scratch that expert_ffn_one needs.
 std::int64_t expert_scratch_floats(std::int64_t k, std::int64_t ffn);
-// One decode row through its k routed experts (stacks of `experts`):
-//   out[c] = sum_j weights[j] down[ids[j]] (silu(gate[ids[j]] x) * up[ids[j]] x)
-// with x and the activation rounded to bf16 for the products. The
+// One decode row x through its k routed experts, each expert e a slice of
+// the stacked gate, up and down weights: out = the weights[j]-weighted sum
+// over j of down_e . (silu(gate_e . x) * (up_e . x)), e = ids[j], with x and
+// the activation rounded to bf16 for the products. The
 // reference's signature plus `experts` and `scratch`, so nothing is
 // allocated and a captured step can hold the call.
 // With base set, out = base + the routed sum (base may be out itself).
