@@ -71,6 +71,14 @@ def lib() -> ctypes.CDLL:
             "orc_scale_add_mask": ([_vp, _f, _vp, _i64, _i64, _i64], None),
             "orc_quick_gelu": ([_vp, _i64], None),
             "orc_expert_topk": ([_vp, _i64, _i64, _i64, _vp, _vp], None),
+            "orc_block_summaries": ([_vp, _i64, _i64, _vp, _i64, _vp], None),
+            "orc_block_scores": ([_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp], None),
+            "orc_entmax15": ([_vp, _i64], None),
+            "orc_select_blocks": ([_vp, _i64, _i64, _vp, _i64, _i64, _f, _f, _f, _vp, _vp, _vp], _i64),
+            "orc_key_mask": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp], None),
+            "orc_page_candidates": ([_vp, _vp, _i64, _i64, _i64, _vp], ctypes.c_int),
+            "orc_route_one": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f, _f,
+                               _f, _vp, _vp], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(h, name)
@@ -100,6 +108,11 @@ def ref_lib() -> Optional[ctypes.CDLL]:
             "ref_softmax_rows": ([_vp, _i64, _i64], None),
             "ref_linear": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], None),
             "ref_attention_head": ([_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _f, _vp], None),
+            "ref_block_summaries": ([_vp, _i64, _i64, _vp, _i64, _vp], None),
+            "ref_block_scores": ([_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp], None),
+            "ref_entmax15": ([_vp, _i64], None),
+            "ref_select_blocks": ([_vp, _i64, _i64, _vp, _i64, _i64, _f, _f, _f, _vp, _vp, _vp], _i64),
+            "ref_key_mask": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(h, name)
@@ -307,3 +320,84 @@ def quick_gelu(x) -> np.ndarray:
     x = _f32(x)
     lib().orc_quick_gelu(_p(x), x.size)
     return x
+
+
+# ---- the block router (src/model/block_router.cpp, attention_plan.cpp) -----------------------
+
+
+class RouterParams:
+    """The reference's RouterParams (src/model/block_router.h:16-26) with
+    Decoder::default_router's idx_scale (src/model/decoder.cpp:58-62)."""
+
+    def __init__(self, block_size=32, local_blocks=4, top_m=16, top_k=12, idx_scale=None, floor=1e-4, sigma=1.0):
+        self.block_size, self.local_blocks, self.top_m, self.top_k = block_size, local_blocks, top_m, top_k
+        self.idx_scale = float(np.float32(128.0) / np.sqrt(np.float32(128.0))) if idx_scale is None else idx_scale
+        self.floor, self.sigma = floor, sigma
+
+
+def block_summaries(rk, cls, block_size: int) -> np.ndarray:
+    rk, cls = _f32(rk), _f32(cls)
+    keys, d = rk.shape
+    out = np.empty(((keys + block_size - 1) // block_size, d), np.float32)
+    lib().orc_block_summaries(_p(rk), keys, d, _p(cls), block_size, _p(out))
+    return out
+
+
+def block_scores(rq, summaries, q_pos, block_size: int, local_blocks: int) -> np.ndarray:
+    rq, summaries = _f32(rq).reshape(-1, _f32(summaries).shape[1]), _f32(summaries)
+    q_pos = np.ascontiguousarray(q_pos, dtype=np.int64)
+    out = np.empty((rq.shape[0], summaries.shape[0]), np.float32)
+    lib().orc_block_scores(_p(rq), rq.shape[0], _p(summaries), summaries.shape[0], summaries.shape[1], _p(q_pos),
+                           block_size, local_blocks, _p(out))
+    return out
+
+
+def entmax15(x) -> np.ndarray:
+    x = _f32(x)
+    lib().orc_entmax15(_p(x), x.size)
+    return x
+
+
+def select_blocks(scores, candidate, p: RouterParams):
+    """(block, bias, valid) [lq, width] of each score row."""
+    scores = _f32(scores)
+    lq, nblk = scores.shape
+    cand = None if candidate is None else np.ascontiguousarray(candidate, dtype=np.uint8)
+    cap = max(1, p.top_k)
+    block, bias, valid = np.empty(lq * cap, np.int64), np.empty(lq * cap, np.float32), np.empty(lq * cap, np.uint8)
+    w = lib().orc_select_blocks(_p(scores), lq, nblk, _p(cand), p.top_m, p.top_k, p.idx_scale, p.floor, p.sigma,
+                                _p(block), _p(bias), _p(valid))
+    return block[:lq * w].reshape(lq, w), bias[:lq * w].reshape(lq, w), valid[:lq * w].reshape(lq, w)
+
+
+def key_mask(block, bias, valid, first_pos: int, keys: int, p: RouterParams) -> np.ndarray:
+    block = np.ascontiguousarray(block, dtype=np.int64)
+    bias, valid = _f32(bias), np.ascontiguousarray(valid, dtype=np.uint8)
+    rows, width = block.shape
+    out = np.empty((rows, keys), np.float32)
+    lib().orc_key_mask(_p(block), _p(bias), _p(valid), width, rows, first_pos, keys, p.block_size, p.local_blocks,
+                       _p(out))
+    return out
+
+
+def page_candidates(min_page, max_page, page: int, nblk: int):
+    """[nblk] uint8, or None for no restriction."""
+    lo = np.ascontiguousarray(min_page, dtype=np.int64)
+    hi = np.ascontiguousarray(max_page, dtype=np.int64)
+    out = np.zeros(max(1, nblk), np.uint8)
+    any_ = lib().orc_page_candidates(_p(lo), _p(hi), lo.size, page, nblk, _p(out))
+    return out[:nblk] if any_ else None
+
+
+def route_one(rq, rk, pos: int, cls, p: RouterParams, min_page=None, max_page=None, query_page: int = -1):
+    """(summaries, mask [pos + 1]) of one decode query over router keys rk [pos + 1, d]."""
+    rq, rk, cls = _f32(rq), _f32(rk), _f32(cls)
+    d = rq.size
+    lo = np.zeros(1, np.int64) if min_page is None else np.ascontiguousarray(min_page, dtype=np.int64)
+    hi = np.zeros(1, np.int64) if max_page is None else np.ascontiguousarray(max_page, dtype=np.int64)
+    known = 0 if min_page is None else lo.size
+    summaries = np.empty(((pos + 1 + p.block_size - 1) // p.block_size, d), np.float32)
+    mask = np.empty(pos + 1, np.float32)
+    lib().orc_route_one(_p(rq), _p(rk), pos, d, _p(cls), _p(lo), _p(hi), known, query_page, p.block_size,
+                        p.local_blocks, p.top_m, p.top_k, p.idx_scale, p.floor, p.sigma, _p(summaries), _p(mask))
+    return summaries, mask

@@ -14,6 +14,8 @@
 
 #include "backend/reference/ops.h"
 #include "backend/reference/parallel.h"
+#include "model/attention_plan.h"
+#include "model/block_router.h"
 #include "model/page_rope.h"
 #include "tensor/dtype.h"
 #include "tensor/tensor.h"
@@ -117,6 +119,70 @@ __attribute__((visibility("default"))) void ref_attention_head(const float* q, s
   const uocr::Tensor o = ref::attention_head(wrap(q, {lq, d}), wrap(k, {lk, d}), wrap(v, {lk, dv}),
                                              bias != nullptr ? &b : nullptr, scale);
   unwrap(o, out);
+}
+
+// block_summaries(rk [keys, d], head_cls [d], block_size) -> out [ceil(keys / block_size), d].
+__attribute__((visibility("default"))) void ref_block_summaries(const float* rk, std::int64_t keys, std::int64_t d,
+                                                                const float* cls, std::int64_t block_size,
+                                                                float* out) {
+  unwrap(uocr::block_summaries(wrap(rk, {keys, d}), wrap(cls, {d}), block_size), out);
+}
+
+// block_scores(rq [lq, d], summaries [nblk, d], q_pos [lq]) -> out [lq, nblk].
+__attribute__((visibility("default"))) void ref_block_scores(const float* rq, std::int64_t lq,
+                                                             const float* summaries, std::int64_t nblk, std::int64_t d,
+                                                             const std::int64_t* q_pos, std::int64_t block_size,
+                                                             std::int64_t local_blocks, float* out) {
+  uocr::RouterParams p;
+  p.block_size = block_size;
+  p.local_blocks = local_blocks;
+  const std::vector<std::int64_t> pos(q_pos, q_pos + lq);
+  unwrap(uocr::block_scores(wrap(rq, {lq, d}), wrap(summaries, {nblk, d}), pos, 0, p), out);
+}
+
+__attribute__((visibility("default"))) void ref_entmax15(float* x, std::int64_t n) {
+  std::vector<float> v(x, x + n);
+  uocr::entmax15(v);
+  std::memcpy(x, v.data(), static_cast<std::size_t>(n) * 4);
+}
+
+// select_blocks(scores [lq, nblk], candidate [lq, nblk] or null) -> block,
+// bias, valid [lq, width]; returns width.
+__attribute__((visibility("default"))) std::int64_t ref_select_blocks(
+    const float* scores, std::int64_t lq, std::int64_t nblk, const std::uint8_t* candidate, std::int64_t top_m,
+    std::int64_t top_k, float idx_scale, float floor_p, float sigma, std::int64_t* block, float* bias,
+    std::uint8_t* valid) {
+  uocr::RouterParams p;
+  p.top_m = top_m;
+  p.top_k = top_k;
+  p.idx_scale = idx_scale;
+  p.floor = floor_p;
+  p.sigma = sigma;
+  std::vector<std::uint8_t> cand;
+  if (candidate != nullptr) cand.assign(candidate, candidate + lq * nblk);
+  const uocr::BlockSelection sel = uocr::select_blocks(wrap(scores, {lq, nblk}), cand, p);
+  std::memcpy(block, sel.block.data(), sel.block.size() * 8);
+  std::memcpy(bias, sel.bias.data(), sel.bias.size() * 4);
+  std::memcpy(valid, sel.valid.data(), sel.valid.size());
+  return sel.width;
+}
+
+// key_mask of a selection (block, bias, valid [rows, width]) -> mask [rows, keys].
+__attribute__((visibility("default"))) void ref_key_mask(const std::int64_t* block, const float* bias,
+                                                         const std::uint8_t* valid, std::int64_t width,
+                                                         std::int64_t rows, std::int64_t first_pos, std::int64_t keys,
+                                                         std::int64_t block_size, std::int64_t local_blocks,
+                                                         float* mask) {
+  uocr::BlockSelection sel;
+  sel.width = width;
+  sel.block.assign(block, block + rows * width);
+  sel.bias.assign(bias, bias + rows * width);
+  sel.valid.assign(valid, valid + rows * width);
+  uocr::RouterParams p;
+  p.block_size = block_size;
+  p.local_blocks = local_blocks;
+  const std::vector<float> m = uocr::key_mask(sel, rows, first_pos, keys, p);
+  std::memcpy(mask, m.data(), m.size() * 4);
 }
 
 }  // extern "C"

@@ -437,3 +437,241 @@ ORC_API void orc_scale_add_mask(float* x, float scale, const float* mask, int64_
 ORC_API void orc_quick_gelu(float* x, int64_t n) {
   for (int64_t i = 0; i < n; ++i) x[i] = x[i] * sigmoid(1.702f * x[i]);
 }
+
+/* ---- the block router of sparse decode attention ------------------------- */
+
+static inline float clamp_act(float v) { return v < -1.0e4f ? -1.0e4f : (v > 1.0e4f ? 1.0e4f : v); }
+
+/* Block summaries (src/model/block_router.cpp:20-47): for each block of
+ * `block_size` router keys rk [keys, d], logits a_t = clamp(dot(rk_t, cls)
+ * / sqrt(d)) with the dot summed over e in order, w_t = exp(a_t - max),
+ * total = max(sum w_t, 1e-6), out[b] = sum_t (w_t / total) rk_t (summed over
+ * t in order, starting from 0). */
+ORC_API void orc_block_summaries(const float* rk, int64_t keys, int64_t d, const float* cls, int64_t block_size,
+                                 float* out) {
+  const int64_t nblk = (keys + block_size - 1) / block_size;
+  const float inv_sqrt_d = 1.0f / sqrtf((float)d);
+  float* w = (float*)malloc((size_t)(block_size > 0 ? block_size : 1) * sizeof(float));
+  for (int64_t b = 0; b < nblk; ++b) {
+    const int64_t first = b * block_size, last = first + block_size < keys ? first + block_size : keys;
+    float peak = -3.402823466e+38f;
+    for (int64_t t = first; t < last; ++t) {
+      float a = 0.0f;
+      for (int64_t e = 0; e < d; ++e) a += rk[t * d + e] * cls[e];
+      a = clamp_act(a * inv_sqrt_d);
+      w[t - first] = a;
+      if (a > peak) peak = a;
+    }
+    float total = 0.0f;
+    for (int64_t t = first; t < last; ++t) {
+      w[t - first] = expf(w[t - first] - peak);
+      total += w[t - first];
+    }
+    if (total < 1e-6f) total = 1e-6f;
+    float* o = out + b * d;
+    for (int64_t e = 0; e < d; ++e) o[e] = 0.0f;
+    for (int64_t t = first; t < last; ++t) {
+      const float p = w[t - first] / total;
+      for (int64_t e = 0; e < d; ++e) o[e] += p * rk[t * d + e];
+    }
+  }
+  free(w);
+}
+
+/* Block scores (block_router.cpp:49-66): for query i at position q_pos[i],
+ * blocks b <= q_pos / block_size - local_blocks score clamp(dot(rq_i, S_b)
+ * / sqrt(d)); the rest score -1e9 (kScoreMasked). */
+ORC_API void orc_block_scores(const float* rq, int64_t lq, const float* summaries, int64_t nblk, int64_t d,
+                              const int64_t* q_pos, int64_t block_size, int64_t local_blocks, float* out) {
+  const float inv_sqrt_d = 1.0f / sqrtf((float)d);
+  for (int64_t i = 0; i < lq; ++i) {
+    const int64_t last_remote = q_pos[i] / block_size - local_blocks;
+    for (int64_t b = 0; b < nblk; ++b) {
+      if (b > last_remote) {
+        out[i * nblk + b] = -1.0e9f;
+        continue;
+      }
+      float z = 0.0f;
+      for (int64_t e = 0; e < d; ++e) z += rq[i * d + e] * summaries[b * d + e];
+      out[i * nblk + b] = clamp_act(z * inv_sqrt_d);
+    }
+  }
+}
+
+static int desc_float(const void* a, const void* b) {
+  const float x = *(const float*)a, y = *(const float*)b;
+  return x < y ? 1 : (x > y ? -1 : 0);
+}
+
+/* 1.5-entmax of one row in place (block_router.cpp:68-91): halve the
+ * shifted row, sort descending, running mean and mean square give the
+ * threshold candidates tau_k = mean - sqrt(max((1 - rho (msq - mean^2)) /
+ * rho, 0)), the support is the count of tau_k <= sorted_k, and the output
+ * is max(x - tau*, 0)^2, all in fp32. */
+ORC_API void orc_entmax15(float* x, int64_t n) {
+  if (n <= 0) return;
+  float peak = x[0];
+  for (int64_t i = 1; i < n; ++i) if (x[i] > peak) peak = x[i];
+  for (int64_t i = 0; i < n; ++i) x[i] = (x[i] - peak) / 2.0f;
+  float* sorted = (float*)malloc((size_t)n * sizeof(float));
+  float* tau = (float*)malloc((size_t)n * sizeof(float));
+  memcpy(sorted, x, (size_t)n * sizeof(float));
+  qsort(sorted, (size_t)n, sizeof(float), desc_float);
+  float sum = 0.0f, sum_sq = 0.0f;
+  int64_t support = 0;
+  for (int64_t k = 0; k < n; ++k) {
+    sum += sorted[k];
+    sum_sq += sorted[k] * sorted[k];
+    const float rho = (float)(k + 1);
+    const float mean = sum / rho, mean_sq = sum_sq / rho;
+    const float ss = rho * (mean_sq - mean * mean);
+    float delta = (1.0f - ss) / rho;
+    if (delta < 0.0f) delta = 0.0f;
+    tau[k] = mean - sqrtf(delta);
+    if (tau[k] <= sorted[k]) ++support;
+  }
+  const float tau_star = tau[(support > 1 ? support : 1) - 1];
+  for (int64_t i = 0; i < n; ++i) {
+    float t = x[i] - tau_star;
+    if (t < 0.0f) t = 0.0f;
+    x[i] = t * t;
+  }
+  free(sorted);
+  free(tau);
+}
+
+/* Block selection (block_router.cpp:93-154) for each row of scores [lq,
+ * nblk]: a block is a candidate when it is remote (score > -5e8) and allowed
+ * (candidate NULL, or candidate[i, b] != 0); a row with no candidate falls
+ * back to every remote block. Candidates keep score * idx_scale, the rest
+ * -1e4; the top m = clamp(top_m, 1, nblk) in descending order (ties: the
+ * lower block first) go through 1.5-entmax; the first k = clamp(top_k, 1,
+ * m) are the selection: block, valid (= candidate), logp = log(max(p,
+ * floor)), and bias (logp - mean logp of the valid ones) / sigma for valid
+ * slots, 0 otherwise. block, bias and valid are [lq, k]; returns k. */
+ORC_API int64_t orc_select_blocks(const float* scores, int64_t lq, int64_t nblk, const uint8_t* candidate,
+                                  int64_t top_m, int64_t top_k, float idx_scale, float floor_p, float sigma,
+                                  int64_t* block, float* bias, uint8_t* valid) {
+  const int64_t m = top_m < nblk ? (top_m > 1 ? top_m : 1) : (nblk > 1 ? nblk : 1);
+  const int64_t k = top_k < m ? (top_k > 1 ? top_k : 1) : m;
+  uint8_t* cand = (uint8_t*)malloc((size_t)(nblk > 0 ? nblk : 1));
+  float* x = (float*)malloc((size_t)(nblk > 0 ? nblk : 1) * sizeof(float));
+  int64_t* order = (int64_t*)malloc((size_t)(nblk > 0 ? nblk : 1) * sizeof(int64_t));
+  float* top = (float*)malloc((size_t)m * sizeof(float));
+  float* logp = (float*)malloc((size_t)k * sizeof(float));
+  for (int64_t i = 0; i < lq; ++i) {
+    const float* row = scores + i * nblk;
+    int any = 0;
+    for (int64_t b = 0; b < nblk; ++b) {
+      const int remote = row[b] > -1.0e9f * 0.5f;
+      const int allowed = candidate == NULL || candidate[i * nblk + b] != 0;
+      cand[b] = (uint8_t)(remote && allowed);
+      any |= remote && allowed;
+    }
+    if (!any) {
+      for (int64_t b = 0; b < nblk; ++b) cand[b] = (uint8_t)(row[b] > -1.0e9f * 0.5f);
+    }
+    for (int64_t b = 0; b < nblk; ++b) x[b] = cand[b] ? row[b] * idx_scale : -1.0e4f;
+    /* order by x descending, ties by the lower index: a stable insertion */
+    for (int64_t b = 0; b < nblk; ++b) {
+      int64_t j = b;
+      while (j > 0 && x[order[j - 1]] < x[b]) {
+        order[j] = order[j - 1];
+        --j;
+      }
+      order[j] = b;
+    }
+    for (int64_t j = 0; j < m; ++j) top[j] = x[order[j]];
+    orc_entmax15(top, m);
+    int64_t count = 0;
+    float logp_sum = 0.0f;
+    for (int64_t j = 0; j < k; ++j) {
+      const int64_t b = order[j];
+      block[i * k + j] = b;
+      valid[i * k + j] = cand[b];
+      logp[j] = logf(top[j] > floor_p ? top[j] : floor_p);
+      if (cand[b]) {
+        logp_sum += logp[j];
+        ++count;
+      }
+    }
+    const float mu = logp_sum / (float)(count > 1 ? count : 1);
+    for (int64_t j = 0; j < k; ++j) bias[i * k + j] = valid[i * k + j] ? (logp[j] - mu) / sigma : 0.0f;
+  }
+  free(cand);
+  free(x);
+  free(order);
+  free(top);
+  free(logp);
+  return k;
+}
+
+/* The additive key mask of a selection (src/model/attention_plan.cpp:34-56)
+ * for queries at first_pos.. over keys 0..keys-1: 0 inside the local window
+ * (j > pos - local_blocks * block_size), the block's bias for a key of a
+ * valid selected block, -inf elsewhere and past pos. mask [rows, keys]. */
+ORC_API void orc_key_mask(const int64_t* block, const float* bias, const uint8_t* valid, int64_t width, int64_t rows,
+                          int64_t first_pos, int64_t keys, int64_t block_size, int64_t local_blocks, float* mask) {
+  const int64_t nblk = (keys + block_size - 1) / block_size;
+  const int64_t window = local_blocks * block_size;
+  float* block_bias = (float*)malloc((size_t)(nblk > 0 ? nblk : 1) * sizeof(float));
+  for (int64_t i = 0; i < rows; ++i) {
+    for (int64_t b = 0; b < nblk; ++b) block_bias[b] = -INFINITY;
+    for (int64_t j = 0; j < width; ++j) {
+      if (valid[i * width + j]) block_bias[block[i * width + j]] = bias[i * width + j];
+    }
+    const int64_t pos = first_pos + i;
+    float* row = mask + i * keys;
+    for (int64_t j = 0; j < keys; ++j) row[j] = -INFINITY;
+    for (int64_t j = 0; j <= pos && j < keys; ++j) row[j] = j > pos - window ? 0.0f : block_bias[j / block_size];
+  }
+  free(block_bias);
+}
+
+/* A query's candidate blocks from the prompt's per-block image pages
+ * (src/model/decoder.cpp:42-56): block b of the first min(nblk, known)
+ * blocks is a candidate when min_page[b] >= 0 and min_page[b] <= page <=
+ * max_page[b]. Writes out [nblk] and returns 1; returns 0 (no restriction,
+ * out untouched) when page < 0 or no block qualifies. */
+ORC_API int orc_page_candidates(const int64_t* min_page, const int64_t* max_page, int64_t known, int64_t page,
+                                int64_t nblk, uint8_t* out) {
+  if (page < 0) return 0;
+  int any = 0;
+  for (int64_t b = 0; b < nblk; ++b) out[b] = 0;
+  const int64_t n = nblk < known ? nblk : known;
+  for (int64_t b = 0; b < n; ++b) {
+    if (min_page[b] >= 0 && min_page[b] <= page && page <= max_page[b]) {
+      out[b] = 1;
+      any = 1;
+    }
+  }
+  return any;
+}
+
+/* The routed key mask of one decode query (Decoder::attention for one row,
+ * src/model/decoder.cpp:104-120, through the functions above): summaries of
+ * the router keys rk [pos + 1, d], scores of rq [d] at position pos, the
+ * page candidates of query_page, the selection and its key mask [pos + 1].
+ * summaries [ceil((pos + 1) / block_size), d] receives the summaries. */
+ORC_API void orc_route_one(const float* rq, const float* rk, int64_t pos, int64_t d, const float* cls,
+                           const int64_t* min_page, const int64_t* max_page, int64_t known, int64_t query_page,
+                           int64_t block_size, int64_t local_blocks, int64_t top_m, int64_t top_k, float idx_scale,
+                           float floor_p, float sigma, float* summaries, float* mask) {
+  const int64_t keys = pos + 1, nblk = (keys + block_size - 1) / block_size;
+  orc_block_summaries(rk, keys, d, cls, block_size, summaries);
+  float* z = (float*)malloc((size_t)nblk * sizeof(float));
+  orc_block_scores(rq, 1, summaries, nblk, d, &pos, block_size, local_blocks, z);
+  uint8_t* cand = (uint8_t*)malloc((size_t)nblk);
+  const int restricted = orc_page_candidates(min_page, max_page, known, query_page, nblk, cand);
+  int64_t* block = (int64_t*)malloc((size_t)(top_k > 0 ? top_k : 1) * sizeof(int64_t) + 64);
+  float* bias = (float*)malloc((size_t)(top_k > 0 ? top_k : 1) * sizeof(float) + 64);
+  uint8_t* valid = (uint8_t*)malloc((size_t)(top_k > 0 ? top_k : 1) + 64);
+  const int64_t width =
+      orc_select_blocks(z, 1, nblk, restricted ? cand : NULL, top_m, top_k, idx_scale, floor_p, sigma, block, bias, valid);
+  orc_key_mask(block, bias, valid, width, 1, pos, keys, block_size, local_blocks, mask);
+  free(z);
+  free(cand);
+  free(block);
+  free(bias);
+  free(valid);
+}

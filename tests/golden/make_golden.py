@@ -1,6 +1,7 @@
 """Writes tests/golden/ref_vectors.npz: small input/output vectors produced by
 the reference's own CPU code (src/backend/reference/ops.cpp,
-src/model/page_rope.cpp, src/tensor/dtype.h), compiled from where it lies
+src/model/page_rope.cpp, src/model/block_router.cpp,
+src/model/attention_plan.cpp, src/tensor/dtype.h), compiled from where it lies
 into oracle/_ref/libuocr_ref.so by `make -C oracle ref`.
 
 Run in a container that holds the reference sources:
@@ -88,6 +89,33 @@ def main():
     out.update(softmax_in=sm, softmax_out=smo, linear_x=lx, linear_w=lw, linear_b=lb, linear_y=ly,
                attn_q=aq, attn_k=ak, attn_v=av, attn_mask=am, attn_scale=np.float32(0.125), attn_out=ao,
                quick_gelu_out=qg)
+
+    # the block router: summaries, scores, selection (with candidates), key mask, entmax
+    d, keys = 64, 300
+    rk = (g.standard_normal((keys, d)) * 2).astype(np.float32)
+    cls = g.standard_normal(d, dtype=np.float32)
+    nblk = (keys + 31) // 32
+    summ = np.empty((nblk, d), np.float32)
+    ref.ref_block_summaries(p(rk), keys, d, p(cls), 32, p(summ))
+    rq = g.standard_normal((4, d), dtype=np.float32)
+    qpos = np.array([keys - 4, keys - 3, keys - 2, keys - 1], np.int64)
+    sc = np.empty((4, nblk), np.float32)
+    ref.ref_block_scores(p(rq), 4, p(summ), nblk, d, p(qpos), 32, 4, p(sc))
+    cand = (g.random((4, nblk)) < 0.4).astype(np.uint8)
+    cand[3] = 0  # a row whose candidates exclude every remote block
+    prm = oracle.RouterParams()
+    blk, bia, val = np.empty(4 * 12, np.int64), np.empty(4 * 12, np.float32), np.empty(4 * 12, np.uint8)
+    wid = ref.ref_select_blocks(p(sc), 4, nblk, p(cand), prm.top_m, prm.top_k, np.float32(prm.idx_scale),
+                                np.float32(prm.floor), np.float32(prm.sigma), p(blk), p(bia), p(val))
+    blk, bia, val = blk[:4 * wid].reshape(4, wid), bia[:4 * wid].reshape(4, wid), val[:4 * wid].reshape(4, wid)
+    msk = np.empty((4, keys), np.float32)
+    ref.ref_key_mask(p(blk), p(bia), p(val), wid, 4, keys - 4, keys, 32, 4, p(msk))
+    ei = (g.standard_normal(16) * 3).astype(np.float32)
+    eo = ei.copy()
+    ref.ref_entmax15(p(eo), 16)
+    out.update(router_rk=rk, router_cls=cls, router_summaries=summ, router_rq=rq, router_pos=qpos, router_scores=sc,
+               router_cand=cand, router_block=blk, router_bias=bia, router_valid=val, router_first=np.int64(keys - 4),
+               router_keys=np.int64(keys), router_mask=msk, entmax_in=ei, entmax_out=eo)
 
     path = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(path, **out)

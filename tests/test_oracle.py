@@ -331,7 +331,7 @@ def ref(orc):
 
 
 def _p(a):
-    return a.ctypes.data
+    return None if a is None else a.ctypes.data
 
 
 def test_oracle_bit_equals_reference_norms_and_activations(orc, ref):
@@ -571,3 +571,174 @@ def test_expert_topk_known_answer_ties_and_brute_force(orc):
     # a planted slip (ties to the higher index) fails the same check
     slip = sorted(range(64), key=lambda e: (-scores[0, e], -e))[:6]
     assert slip != ids[0].tolist()
+
+
+# ---- the block router (src/model/block_router.cpp, attention_plan.cpp, decoder.cpp:42-56) -------
+
+
+def test_entmax15_known_answers_and_invariants(orc):
+    # two equal scores split the mass; a far-ahead score takes all of it
+    assert np.allclose(orc.entmax15(np.array([0.0, 0.0], np.float32)), [0.5, 0.5], rtol=0, atol=1e-7)
+    assert orc.entmax15(np.array([10.0, 0.0], np.float32)).tolist() == [1.0, 0.0]
+    assert orc.entmax15(np.array([3.0], np.float32)).tolist() == [1.0]
+    g = rng(60)
+    for n in (2, 5, 16, 32):
+        for _ in range(20):
+            x = (g.standard_normal(n) * 3).astype(np.float32)
+            p = orc.entmax15(x)
+            assert np.all(p >= 0) and abs(float(p.astype(np.float64).sum()) - 1.0) < 1e-5
+            # order-preserving and shift-invariant, and p = max((x - max)/2 - tau, 0)^2 for one tau
+            assert np.all(np.diff(p[np.argsort(-x, kind="stable")]) <= 0)
+            assert np.array_equal(orc.entmax15(x + np.float32(4.0)), p) or np.allclose(orc.entmax15(x + 4), p, atol=1e-6)
+            h = (x.astype(np.float64) - x.max()) / 2
+            on = p > 0
+            taus = h[on] - np.sqrt(p[on].astype(np.float64))
+            assert np.ptp(taus) < 1e-5 and np.all(h[~on] <= taus.mean() + 1e-6)
+
+
+def test_block_summaries_known_answers_and_closed_form(orc):
+    g = rng(61)
+    d, bs = 16, 4
+    rk = g.standard_normal((10, d), dtype=np.float32)
+    cls = g.standard_normal(d, dtype=np.float32)
+    s = orc.block_summaries(rk, cls, bs)
+    assert s.shape == (3, d)
+    one = orc.block_summaries(rk[:9], cls, bs)  # a one-key last block summarises to that key
+    assert np.array_equal(one[2], rk[8])
+    for b in range(3):  # fp64 closed form: the softmax(clamp(rk . cls / sqrt d))-weighted mean
+        rows = rk[b * bs:(b + 1) * bs].astype(np.float64)
+        a = np.clip(rows @ cls.astype(np.float64) / np.sqrt(d), -1e4, 1e4)
+        w = np.exp(a - a.max())
+        want = (w / w.sum()) @ rows
+        assert np.max(np.abs(s[b] - want)) < 1e-5
+
+
+def test_block_scores_mask_the_local_window(orc):
+    g = rng(62)
+    d = 8
+    S = g.standard_normal((20, d), dtype=np.float32)
+    rq = g.standard_normal((3, d), dtype=np.float32)
+    z = orc.block_scores(rq, S, [0, 160, 639], 32, 4)
+    assert np.all(z[0] == -1e9)  # pos 0: no block before the window
+    assert np.all(z[1, 2:] == -1e9) and np.all(z[1, :2] != -1e9)  # pos 160: blocks 0 and 1 (160 // 32 - 4 = 1)
+    assert np.all(z[2, 16:] == -1e9)  # pos 639: blocks 0..15
+    want = np.clip(rq[2].astype(np.float64) @ S[:16].T.astype(np.float64) / np.sqrt(d), -1e4, 1e4)
+    assert np.max(np.abs(z[2, :16] - want)) < 1e-5
+
+
+def test_select_and_mask_known_answer(orc):
+    p = orc.RouterParams(top_m=4, top_k=2, idx_scale=1.0)
+    # three remote blocks, one clear winner; block 3 masked
+    scores = np.array([[0.0, 9.0, 0.0, -1e9]], np.float32)
+    block, bias, valid = orc.select_blocks(scores, None, p)
+    assert block.tolist() == [[1, 0]] and valid.tolist() == [[1, 1]]
+    # entmax over (9, 0, 0, -1e4) puts all mass on block 1: log(1) and log(floor)
+    lp = [0.0, float(np.log(np.float32(1e-4)))]
+    mu = (lp[0] + lp[1]) / 2
+    assert np.allclose(bias[0], [lp[0] - mu, lp[1] - mu], rtol=1e-6)
+    # the key mask of that selection for a query at pos 255 over 256 keys
+    m = orc.key_mask(block, bias, valid, 255, 256, p)[0]
+    assert np.all(m[128:] == 0)  # the local window (4 blocks of 32)
+    assert np.all(m[32:64] == bias[0, 0]) and np.all(m[0:32] == bias[0, 1])
+    assert np.all(m[64:128] == -np.inf)
+    # a candidate list that excludes every remote block falls back to all of them
+    b2, _, v2 = orc.select_blocks(scores, np.array([[0, 0, 0, 1]], np.uint8), p)
+    assert b2.tolist() == [[1, 0]] and v2.tolist() == [[1, 1]]
+    # a candidate list keeps only its blocks valid (ties: the lower index first)
+    b3, _, v3 = orc.select_blocks(np.array([[5.0, 5.0, 5.0, -1e9]], np.float32), np.array([[0, 1, 1, 0]], np.uint8), p)
+    assert b3.tolist() == [[1, 2]] and v3.tolist() == [[1, 1]]
+
+
+def test_page_candidates_known_answers(orc):
+    lo, hi = [0, 0, 1, -1, 2], [0, 1, 2, -1, 2]
+    assert orc.page_candidates(lo, hi, -1, 5) is None  # no page: no restriction
+    assert orc.page_candidates(lo, hi, 1, 5).tolist() == [0, 1, 1, 0, 0]
+    assert orc.page_candidates(lo, hi, 2, 7).tolist() == [0, 0, 1, 0, 1, 0, 0]
+    assert orc.page_candidates(lo, hi, 9, 5) is None  # no block holds the page
+    assert orc.page_candidates(lo, hi, 2, 3).tolist() == [0, 0, 1]  # only the first nblk blocks count
+
+
+def test_oracle_bit_equals_reference_router(orc, ref):
+    g = rng(63)
+    d = 128
+    for keys in (1, 31, 32, 33, 300, 1025):
+        rk = (g.standard_normal((keys, d)) * 3).astype(np.float32)
+        cls = g.standard_normal(d, dtype=np.float32)
+        mine = orc.block_summaries(rk, cls, 32)
+        theirs = np.empty_like(mine)
+        ref.ref_block_summaries(_p(rk), keys, d, _p(cls), 32, _p(theirs))
+        assert np.array_equal(mine.view(np.uint32), theirs.view(np.uint32)), keys
+        rq = g.standard_normal((3, d), dtype=np.float32) * 2
+        pos = np.array([keys - 1, keys // 2, 0], np.int64)
+        z = orc.block_scores(rq, mine, pos, 32, 4)
+        zt = np.empty_like(z)
+        ref.ref_block_scores(_p(rq), 3, _p(mine), mine.shape[0], d, _p(pos), 32, 4, _p(zt))
+        assert np.array_equal(z.view(np.uint32), zt.view(np.uint32))
+    for n in (1, 2, 3, 16, 32):
+        for _ in range(10):
+            x = (g.standard_normal(n) * 4).astype(np.float32)
+            x[g.random(n) < 0.2] = -1e4
+            t = x.copy()
+            ref.ref_entmax15(_p(t), n)
+            assert np.array_equal(orc.entmax15(x).view(np.uint32), t.view(np.uint32))
+    for nblk, cand_kind in ((1, None), (7, None), (40, None), (40, "some"), (40, "no remote"), (300, "some")):
+        p = orc.RouterParams()
+        lq = 4
+        scores = (g.standard_normal((lq, nblk)) * 3).astype(np.float32)
+        scores[:, nblk // 2:] = -1e9  # the window and beyond
+        scores[1, :3] = 2.5  # exact ties
+        cand = None
+        if cand_kind == "some":
+            cand = (g.random((lq, nblk)) < 0.3).astype(np.uint8)
+        elif cand_kind == "no remote":
+            cand = np.zeros((lq, nblk), np.uint8)
+            cand[:, nblk // 2:] = 1
+        block, bias, valid = orc.select_blocks(scores, cand, p)
+        cap = lq * p.top_k
+        tb, tbias, tv = np.empty(cap, np.int64), np.empty(cap, np.float32), np.empty(cap, np.uint8)
+        w = ref.ref_select_blocks(_p(scores), lq, nblk, _p(cand), p.top_m, p.top_k, p.idx_scale, p.floor, p.sigma,
+                                  _p(tb), _p(tbias), _p(tv))
+        assert w == block.shape[1]
+        assert np.array_equal(block.ravel(), tb[:lq * w]) and np.array_equal(valid.ravel(), tv[:lq * w])
+        assert np.array_equal(bias.ravel().view(np.uint32), tbias[:lq * w].view(np.uint32))
+        keys = nblk * 32 - 5
+        for first in (0, keys - lq):
+            m = orc.key_mask(block, bias, valid, first, keys, p)
+            tm = np.empty_like(m)
+            ref.ref_key_mask(_p(block), _p(bias), _p(valid), w, lq, first, keys, 32, 4, _p(tm))
+            assert np.array_equal(m.view(np.uint32), tm.view(np.uint32))
+
+
+def test_golden_router(orc, golden):
+    if "router_rk" not in golden:
+        pytest.skip("golden vectors predate the router")
+    p = orc.RouterParams()
+    s = orc.block_summaries(golden["router_rk"], golden["router_cls"], 32)
+    assert np.array_equal(s.view(np.uint32), golden["router_summaries"].view(np.uint32))
+    z = orc.block_scores(golden["router_rq"], s, golden["router_pos"], 32, 4)
+    assert np.array_equal(z.view(np.uint32), golden["router_scores"].view(np.uint32))
+    block, bias, valid = orc.select_blocks(z, golden["router_cand"], p)
+    assert np.array_equal(block, golden["router_block"]) and np.array_equal(valid, golden["router_valid"])
+    assert np.array_equal(bias.view(np.uint32), golden["router_bias"].view(np.uint32))
+    m = orc.key_mask(block, bias, valid, int(golden["router_first"]), int(golden["router_keys"]), p)
+    assert np.array_equal(m.view(np.uint32), golden["router_mask"].view(np.uint32))
+    assert np.array_equal(orc.entmax15(golden["entmax_in"]).view(np.uint32), golden["entmax_out"].view(np.uint32))
+
+
+def test_router_checks_reject_planted_slips(orc):
+    """Numpy copies of the selection with a planted slip fail the oracle's own
+    answers: ties to the higher index, a softmax instead of entmax, the bias
+    without the mean subtracted."""
+    p = orc.RouterParams(top_m=8, top_k=4, idx_scale=1.0)
+    g = rng(64)
+    z = (g.standard_normal((1, 20)) * 2).astype(np.float32)
+    z[0, 3] = z[0, 7] = np.float32(4.0)
+    block, bias, valid = orc.select_blocks(z, None, p)
+    assert block[0, :2].tolist() == [3, 7]
+    slip_ties = sorted(range(20), key=lambda b: (-z[0, b], -b))[:4]
+    assert slip_ties != block[0].tolist()
+    top = np.sort(z[0])[::-1][:8].astype(np.float32)
+    soft = np.exp(top - top.max()) / np.exp(top - top.max()).sum()
+    assert not np.allclose(orc.entmax15(top), soft, atol=1e-3)
+    logp = np.log(np.maximum(orc.entmax15(top)[:4], np.float32(1e-4)))
+    assert not np.allclose(bias[0], logp, atol=1e-3) and np.allclose(bias[0], logp - logp.mean(), atol=1e-5)
