@@ -49,6 +49,28 @@ class StepState(ctypes.Structure):
     ]
 
 
+class RouteParams(ctypes.Structure):
+    """uocr_rocm_route_params: the reference's RouteParams
+    (src/backend/cuda/ops.h:112-120); defaults are Decoder::default_router's
+    (src/model/decoder.cpp:58-62, src/model/block_router.h:16-26)."""
+
+    _fields_ = [
+        ("block_size", ctypes.c_int64),
+        ("local_blocks", ctypes.c_int64),
+        ("top_m", ctypes.c_int64),
+        ("top_k", ctypes.c_int64),
+        ("idx_scale", ctypes.c_float),
+        ("floor", ctypes.c_float),
+        ("sigma", ctypes.c_float),
+    ]
+
+    def __init__(self, block_size=32, local_blocks=4, top_m=16, top_k=12, idx_scale=None, floor=1e-4, sigma=1.0):
+        import math
+
+        scale = ctypes.c_float(128.0).value / ctypes.c_float(math.sqrt(128.0)).value if idx_scale is None else idx_scale
+        super().__init__(block_size, local_blocks, top_m, top_k, scale, floor, sigma)
+
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
@@ -123,6 +145,14 @@ _SIGNATURES = {
     "uocr_rocm_attend_scratch_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_attend_step": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
     "uocr_rocm_attend_step_noalloc": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _i64, _vp], _int),
+    "uocr_rocm_block_summaries": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_summary_step": ([_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_scores_step": ([_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_route_blocks": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64,
+                                ctypes.POINTER(RouteParams), _vp], _int),
+    "uocr_rocm_route_step": ([_vp, _vp, _i64, _vp, _vp, _i64, _vp, ctypes.POINTER(RouteParams), _vp], _int),
+    "uocr_rocm_route_decode_step": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64,
+                                     _vp, _vp, _i64, _vp, ctypes.POINTER(RouteParams), _i64, _vp, _vp, _vp], _int),
     "uocr_rocm_scale_mask_softmax_rows": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_embed_add_rms_norm_step": ([_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _f32], _int),
     "uocr_rocm_embed_add_rms_norm_step_bf16": ([_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _f32], _int),
@@ -479,6 +509,72 @@ def attend_step_noalloc(q, k_cache, v_cache, heads, hd, mask, scale, state, out,
         raise ValueError("attend_step_noalloc takes float32 caches")
     _op("uocr_rocm_attend_step_noalloc", stream, _ptr(q), _ptr(k_cache), _ptr(v_cache), heads, hd,
         _f32_param(mask), scale, _ptr(state), capacity, _ptr(out))
+
+
+# ---- the block router (src/backend/cuda/ops.h:97-124, decode_ops.h:30-40) --------------------
+
+
+def _i64_param(t):
+    torch = _torch()
+    if t is not None and t.dtype != torch.int64:
+        raise ValueError("block pages and query pages are int64")
+    return _ptr(t)
+
+
+def block_summaries(keys, head_cls, block_size, out, stream=None):
+    """out [ceil(s / block_size), d]: per block of router keys [s, d], the
+    softmax(clamp(k . head_cls / sqrt d))-weighted mean of its keys."""
+    s, d = _rows_cols(keys)
+    if out.numel() != ((s + block_size - 1) // block_size) * d or head_cls.numel() != d:
+        raise ValueError("block_summaries shapes: keys [s, d], head_cls [d], out [ceil(s / block_size), d]")
+    _op("uocr_rocm_block_summaries", stream, _f32_param(keys), s, d, _f32_param(head_cls), block_size, _ptr(out))
+
+
+def summary_step(router_keys, d, head_cls, block_size, state, summaries, stream=None):
+    """The summary of the block holding state.pos, into summaries [max_blocks, d]."""
+    max_blocks = summaries.numel() // d
+    _op("uocr_rocm_summary_step", stream, _f32_param(router_keys), d, _f32_param(head_cls), block_size, _ptr(state),
+        max_blocks, _ptr(summaries))
+
+
+def scores_step(rq, summaries, d, block_size, state, z, stream=None):
+    """z[b] = rq . summaries[b] / sqrt d up to the block holding state.pos (z [max_blocks])."""
+    _op("uocr_rocm_scores_step", stream, _f32_param(rq), _f32_param(summaries), d, block_size, _ptr(state),
+        z.numel(), _ptr(z))
+
+
+def route_blocks(z, first_pos, keys, block_min, block_max, query_page, one_page, params, mask, stream=None):
+    """Key masks [rows, keys] of prompt rows from scores z [rows, nblk]."""
+    rows, nblk = _rows_cols(z)
+    if mask.numel() != rows * keys:
+        raise ValueError("route_blocks: mask [rows, keys]")
+    pb = 0 if block_min is None else block_min.numel()
+    _op("uocr_rocm_route_blocks", stream, _f32_param(z), rows, nblk, first_pos, keys, _i64_param(block_min),
+        _i64_param(block_max), pb, _i64_param(query_page), one_page, ctypes.byref(params), _ptr(mask))
+
+
+def route_step(z, block_min, block_max, state, params, mask, stream=None):
+    """The key mask mask[0..pos] of the decode query at state.pos from z [max_blocks]."""
+    pb = 0 if block_min is None else block_min.numel()
+    _op("uocr_rocm_route_step", stream, _f32_param(z), z.numel(), _i64_param(block_min), _i64_param(block_max), pb,
+        _ptr(state), ctypes.byref(params), _ptr(mask))
+
+
+def route_decode_step(rq, rk, q_norm, k_norm, eps, inv_tok, inv_page, page_mod, head_cls, router_keys, summaries,
+                      block_min, block_max, state, params, mask, z_out=None, rqk_out=None, stream=None):
+    """The router half of a decode step in one launch: router norms, rope,
+    the router key's append, the block summary, the scores and the route into
+    mask [capacity] (keys 0..pos). router_keys [capacity, d]."""
+    d = rq.numel()
+    capacity = router_keys.numel() // d
+    n_tok = 0 if inv_tok is None else inv_tok.numel()
+    pb = 0 if block_min is None else block_min.numel()
+    if mask.numel() < capacity:
+        raise ValueError("route_decode_step: mask [capacity]")
+    _op("uocr_rocm_route_decode_step", stream, _f32_param(rq), _f32_param(rk), _f32_param(q_norm), _f32_param(k_norm),
+        eps, _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod, _f32_param(head_cls), _ptr(router_keys),
+        _ptr(summaries), d, _i64_param(block_min), _i64_param(block_max), pb, _ptr(state), ctypes.byref(params),
+        capacity, _ptr(mask), _ptr(z_out), _ptr(rqk_out))
 
 
 # ---- fused decode-step ops -------------------------------------------------------------------

@@ -117,12 +117,27 @@ UOCR_ROCM_API int uocr_rocm_event_elapsed_ms(void* start, void* end, float* ms);
  * the length-dependent values of one decode step, read on the device so a
  * captured step replays for every token. */
 typedef struct uocr_rocm_step_state {
-  int64_t token;      /* the token being fed                         */
-  int64_t pos;        /* its position                                */
-  int64_t tok;        /* rope token coordinate                       */
-  int64_t page;       /* rope page coordinate                        */
-  int64_t query_page; /* response page for routing, -1 unrestricted  */
+  int64_t token;      /* id whose embedding row enters the step          */
+  int64_t pos;        /* cache row written this step (pos + 1 live keys) */
+  int64_t tok;        /* rotary coordinate on the token axis             */
+  int64_t page;       /* rotary coordinate on the page axis              */
+  int64_t query_page; /* page the block router confines the query to, or -1 */
 } uocr_rocm_step_state;
+
+/* The block router's parameters (the reference's RouteParams,
+ * src/backend/cuda/ops.h:112-120, and RouterParams,
+ * src/model/block_router.h:16-26): keys per block (<= 64), blocks of the
+ * always-attended local window, the entmax window (top_m <= 32), the blocks
+ * read (top_k), the score scale, the probability floor and the bias scale. */
+typedef struct uocr_rocm_route_params {
+  int64_t block_size;
+  int64_t local_blocks;
+  int64_t top_m;
+  int64_t top_k;
+  float idx_scale;
+  float floor;
+  float sigma;
+} uocr_rocm_route_params;
 
 /* ---- fp32 ops: the reference's uocr::cuda signatures ------------------- */
 
@@ -355,6 +370,72 @@ UOCR_ROCM_API int uocr_rocm_attend_step_noalloc(void* stream, const float* q, co
                                                 const float* v_cache, int64_t heads, int64_t hd, const float* mask,
                                                 float scale, const uocr_rocm_step_state* state, int64_t capacity,
                                                 float* out);
+
+/* ---- the block router of sparse decode attention ------------------------------
+ * Router keys rk [keys, d] and queries rq [d] are fp32, d a multiple of 4 in
+ * [4, 256], block_size * d <= 8192; at most 4096 blocks per query row. */
+
+/* Per block of block_size keys of rk [s, d]: the softmax(clamp(rk . head_cls
+ * / sqrt d))-weighted mean of its keys, out [ceil(s / block_size), d].
+ * Replaces block_summaries (src/backend/cuda/ops.h:97-100). */
+UOCR_ROCM_API int uocr_rocm_block_summaries(void* stream, const float* keys, int64_t s, int64_t d,
+                                            const float* head_cls, int64_t block_size, float* out);
+
+/* The summary of the block holding state->pos (keys first..pos of the
+ * router-key cache), written to summaries[pos / block_size]; a pos past
+ * max_blocks blocks writes nothing. Replaces summary_step
+ * (src/backend/cuda/decode_ops.h:30-33), with max_blocks added as a bound. */
+UOCR_ROCM_API int uocr_rocm_summary_step(void* stream, const float* router_keys, int64_t d, const float* head_cls,
+                                         int64_t block_size, const uocr_rocm_step_state* state, int64_t max_blocks,
+                                         float* summaries);
+
+/* z[b] = rq . summaries[b] / sqrt d for every block up to the one holding
+ * state->pos (at most max_blocks <= 4096). Replaces scores_step
+ * (src/backend/cuda/decode_ops.h:34-36). */
+UOCR_ROCM_API int uocr_rocm_scores_step(void* stream, const float* rq, const float* summaries, int64_t d,
+                                        int64_t block_size, const uocr_rocm_step_state* state, int64_t max_blocks,
+                                        float* z);
+
+/* The route of prompt rows: row i (position first_pos + i, page
+ * query_page[i] or, when query_page is null, one_page; a negative page is
+ * unrestricted) scores the blocks before its local window from z [rows,
+ * nblk] (clamped to +-1e4), keeps the blocks holding its page's image tokens
+ * (page ranges per prompt block in block_min / block_max; none in range
+ * means every block), takes the top_m through 1.5-entmax, reads the first
+ * top_k with a log-prior bias, and writes its key mask [keys]: 0 on the
+ * local window, the bias on a selected block's keys, -inf elsewhere and
+ * past its position. Replaces route_blocks (src/backend/cuda/ops.h:102-124). */
+UOCR_ROCM_API int uocr_rocm_route_blocks(void* stream, const float* z, int64_t rows, int64_t nblk, int64_t first_pos,
+                                         int64_t keys, const int64_t* block_min, const int64_t* block_max,
+                                         int64_t prompt_blocks, const int64_t* query_page, int64_t one_page,
+                                         const uocr_rocm_route_params* params, float* mask);
+
+/* The route of the one decode query at state->pos (page state->query_page)
+ * from z, writing mask[0..pos]. Replaces route_step
+ * (src/backend/cuda/decode_ops.h:37-40). */
+UOCR_ROCM_API int uocr_rocm_route_step(void* stream, const float* z, int64_t max_blocks, const int64_t* block_min,
+                                       const int64_t* block_max, int64_t prompt_blocks,
+                                       const uocr_rocm_step_state* state, const uocr_rocm_route_params* params,
+                                       float* mask);
+
+/* New: the router half of a decode step in one launch, bitwise the separate
+ * ops: the router norm of rq and rk (weights q_norm, k_norm), rope on both
+ * at (state->tok, state->page) with the PageRope tables, rk appended to
+ * router_keys [capacity, d] at pos, the summary of the block holding pos,
+ * the scores of the blocks before the window and the route into mask
+ * [capacity] (keys 0..pos written). z_out (capacity blocks) and rqk_out
+ * ([2 d]: rq and rk after norm and rope) are optional outputs for checking.
+ * Replaces the router projections' norms and ropes, append_step of the
+ * router key, summary_step, scores_step and route_step of
+ * CudaDecoder::decode_attention (src/model/cuda/cuda_decode_step.cpp:19-41). */
+UOCR_ROCM_API int uocr_rocm_route_decode_step(void* stream, const float* rq, const float* rk, const float* q_norm,
+                                              const float* k_norm, float eps, const float* inv_tok, int64_t n_tok,
+                                              const float* inv_page, int64_t page_mod, const float* head_cls,
+                                              float* router_keys, float* summaries, int64_t d,
+                                              const int64_t* block_min, const int64_t* block_max,
+                                              int64_t prompt_blocks, const uocr_rocm_step_state* state,
+                                              const uocr_rocm_route_params* params, int64_t capacity, float* mask,
+                                              float* z_out, float* rqk_out);
 
 /* ---- fused decode-step ops (new) ---------------------------------------------
  * One launch where the reference's decode step makes several; each gives
