@@ -105,4 +105,56 @@ void attend_rope_kv_step_bf16(const Context& ctx, const float* q, const float* k
                                            abi(state), inv_tok, n_tok, inv_page, page_mod, scratch, capacity, out));
 }
 
+namespace {
+
+uocr_rocm_route_params abi(const RouteParams& p) {
+  return uocr_rocm_route_params{p.block_size, p.local_blocks, p.top_m, p.top_k, p.idx_scale, p.floor, p.sigma};
+}
+
+}  // namespace
+
+void block_summaries(const Context& ctx, const float* keys, std::int64_t s, std::int64_t d, const float* head_cls,
+                     std::int64_t block_size, float* out) {
+  check(uocr_rocm_block_summaries(ctx.stream(), keys, s, d, head_cls, block_size, out));
+}
+
+void route_blocks(const Context& ctx, const float* z, std::int64_t rows, std::int64_t nblk, std::int64_t first_pos,
+                  std::int64_t keys, const std::int64_t* block_min, const std::int64_t* block_max,
+                  std::int64_t prompt_blocks, const std::int64_t* query_page, std::int64_t one_page,
+                  const RouteParams& params, float* mask) {
+  const auto p = abi(params);
+  check(uocr_rocm_route_blocks(ctx.stream(), z, rows, nblk, first_pos, keys, block_min, block_max, prompt_blocks,
+                               query_page, one_page, &p, mask));
+}
+
+void summary_step(const Context& ctx, const float* router_keys, std::int64_t d, const float* head_cls,
+                  std::int64_t block_size, const StepState* state, std::int64_t max_blocks, float* summaries) {
+  check(uocr_rocm_summary_step(ctx.stream(), router_keys, d, head_cls, block_size, abi(state), max_blocks,
+                               summaries));
+}
+
+void scores_step(const Context& ctx, const float* rq, const float* summaries, std::int64_t d, std::int64_t block_size,
+                 const StepState* state, std::int64_t max_blocks, float* z) {
+  check(uocr_rocm_scores_step(ctx.stream(), rq, summaries, d, block_size, abi(state), max_blocks, z));
+}
+
+void route_step(const Context& ctx, const float* z, std::int64_t max_blocks, const std::int64_t* block_min,
+                const std::int64_t* block_max, std::int64_t prompt_blocks, const StepState* state,
+                const RouteParams& params, float* mask) {
+  const auto p = abi(params);
+  check(uocr_rocm_route_step(ctx.stream(), z, max_blocks, block_min, block_max, prompt_blocks, abi(state), &p, mask));
+}
+
+void route_decode_step(const Context& ctx, const float* rq, const float* rk, const float* q_norm, const float* k_norm,
+                       float eps, const float* inv_tok, std::int64_t n_tok, const float* inv_page,
+                       std::int64_t page_mod, const float* head_cls, float* router_keys, float* summaries,
+                       std::int64_t d, const std::int64_t* block_min, const std::int64_t* block_max,
+                       std::int64_t prompt_blocks, const StepState* state, const RouteParams& params,
+                       std::int64_t capacity, float* mask, float* z_out, float* rqk_out) {
+  const auto p = abi(params);
+  check(uocr_rocm_route_decode_step(ctx.stream(), rq, rk, q_norm, k_norm, eps, inv_tok, n_tok, inv_page, page_mod,
+                                    head_cls, router_keys, summaries, d, block_min, block_max, prompt_blocks,
+                                    abi(state), &p, capacity, mask, z_out, rqk_out));
+}
+
 }  // namespace uocr::rocm

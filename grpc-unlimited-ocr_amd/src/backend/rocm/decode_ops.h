@@ -81,4 +81,27 @@ void attend_rope_kv_step(const Context& ctx, const float* q, const float* k_row,
                          const StepState* state, const float* inv_tok, std::int64_t n_tok, const float* inv_page,
                          std::int64_t page_mod, float* scratch, std::int64_t capacity, float* out);
 
+// ---- the block router of the step (src/backend/cuda/decode_ops.h:30-40) --------------------
+
+// The summary of the block holding pos, into summaries[pos / block_size];
+// max_blocks bounds the summaries buffer.
+void summary_step(const Context& ctx, const float* router_keys, std::int64_t d, const float* head_cls,
+                  std::int64_t block_size, const StepState* state, std::int64_t max_blocks, float* summaries);
+// z[b] = rq . summaries[b] / sqrt d for every block up to the one holding pos.
+void scores_step(const Context& ctx, const float* rq, const float* summaries, std::int64_t d, std::int64_t block_size,
+                 const StepState* state, std::int64_t max_blocks, float* z);
+// The routed key mask mask[0..pos] of the step's query from z.
+void route_step(const Context& ctx, const float* z, std::int64_t max_blocks, const std::int64_t* block_min,
+                const std::int64_t* block_max, std::int64_t prompt_blocks, const StepState* state,
+                const RouteParams& params, float* mask);
+// New: the router half of the step in one launch (router norms, rope at the
+// step's coordinate, the router key's append, summary_step, scores_step and
+// route_step), bitwise the separate steps; z_out and rqk_out may be null.
+void route_decode_step(const Context& ctx, const float* rq, const float* rk, const float* q_norm, const float* k_norm,
+                       float eps, const float* inv_tok, std::int64_t n_tok, const float* inv_page,
+                       std::int64_t page_mod, const float* head_cls, float* router_keys, float* summaries,
+                       std::int64_t d, const std::int64_t* block_min, const std::int64_t* block_max,
+                       std::int64_t prompt_blocks, const StepState* state, const RouteParams& params,
+                       std::int64_t capacity, float* mask, float* z_out = nullptr, float* rqk_out = nullptr);
+
 }  // namespace uocr::rocm

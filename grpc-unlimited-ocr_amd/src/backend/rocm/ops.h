@@ -165,4 +165,28 @@ void moe_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::i
 void gemv_f32(const Context& ctx, const float* x, std::int64_t k, const float* w, std::int64_t n, const float* bias,
               float* y);
 
+// ---- the block router (src/backend/cuda/ops.h:97-124) -----------------------------------
+
+// The block router's parameters; the defaults are the reference decoder's
+// (src/model/block_router.h:16-26, src/model/decoder.cpp:58-62).
+struct RouteParams {
+  std::int64_t block_size = 32;
+  std::int64_t local_blocks = 4;
+  std::int64_t top_m = 16;
+  std::int64_t top_k = 12;
+  float idx_scale = 11.3137083f;  // 128 / sqrt(128) in fp32
+  float floor = 1e-4f;
+  float sigma = 1.0f;
+};
+
+// Per block of block_size router keys [s, d]: the head_cls-weighted softmax
+// mean of its keys, out [ceil(s / block_size), d].
+void block_summaries(const Context& ctx, const float* keys, std::int64_t s, std::int64_t d, const float* head_cls,
+                     std::int64_t block_size, float* out);
+// The key masks [rows, keys] of prompt rows from block scores z [rows, nblk].
+void route_blocks(const Context& ctx, const float* z, std::int64_t rows, std::int64_t nblk, std::int64_t first_pos,
+                  std::int64_t keys, const std::int64_t* block_min, const std::int64_t* block_max,
+                  std::int64_t prompt_blocks, const std::int64_t* query_page, std::int64_t one_page,
+                  const RouteParams& params, float* mask);
+
 }  // namespace uocr::rocm
