@@ -538,7 +538,7 @@ def config7(be, torch, timer):
     kern["gemv_bf16_lm_head"] = report("gemv lm head", bytes_gemv(lm_n, lm_k), time_kernel(
         timer, lambda: bf16_randn(torch, (lm_n, lm_k), 0.03), lambda w: be.gemv_bf16(xl, w, yl)))
     kern["expert_ffn_one_6_of_64"] = expert_ffn(be, torch, timer, hidden, ffn, 64, 6)
-    whole = decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, scratch, b, lm_n)
+    whole = decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, lm_n)
     return {"workload": "fp32 decode layer at batch 1, hidden 1280, 10 heads x 128, FFN 896, KV cache 8192, fused "
                         "(6 launches): add+RMSNorm+GEMV qkv -> RoPE+append+attend (2) -> GEMV o -> add+RMSNorm+GEMV "
                         "gate|up+SwiGLU -> GEMV down",
@@ -570,27 +570,55 @@ def expert_ffn(be, torch, timer, hidden, ffn, experts, k):
     return report("expert_ffn_one", nbytes, ms)
 
 
-def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, scratch, b, vocab, layers=12):
+def bytes_route_decode(pos, d, block_size, local_blocks, prompt_blocks):
+    """The router half of a decode step (route_decode_step) at pos: R rq, rk,
+    both norms and head_cls; R the block's earlier router keys, W the new
+    one; W the block's summary, R the remote blocks' summaries; R the prompt
+    blocks' page ranges; W the key mask over keys 0..pos."""
+    blk = pos // block_size
+    n = pos - blk * block_size + 1
+    nrem = max(blk - local_blocks + 1, 0)
+    return 4 * (5 * d + (n - 1) * d + d + d + nrem * d + pos + 1) + 16 * prompt_blocks
+
+
+def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vocab, layers=12):
     """The model's whole decode step as one graph, the C++ DecodeStep's body
     (src/model/rocm/decode_step.cpp) on Unlimited-OCR-2's decoder shape
     (weights/architecture.h): the embedding row, layer 0 with a dense FFN of
     6848, layers 1-11 mixture of experts (an fp32 router over 64 experts, 6
-    routed experts of FFN 896, shared experts of FFN 1792), bf16 key/value
-    caches of 8192 positions read in full, the final norm fused into the
-    LM-head GEMV. The block router's attention mask is not built (full
-    attention over the cache). One set of weights and caches (5.8 GB) exceeds
-    the Infinity Cache many times over."""
+    routed experts of FFN 896, shared experts of FFN 1792), each layer's
+    attention routed by the block router (the q, k, v and router q/k
+    projections in one GEMV, router norms, PageRope at (tok, page), the
+    router key's append, the block summary, the scores of the 252 remote
+    blocks, top-16 1.5-entmax and the key mask in one launch; rope of q and k,
+    both appends and the masked attention over 8192 positions), the final
+    norm fused into the LM-head GEMV. The prompt's first 4096 positions are
+    128 blocks of 16 pages and the query is confined to one page. Timed over
+    the reference's fp32 key/value cache and over a bf16 one. The weights
+    (5.8 GB) exceed the Infinity Cache many times over."""
     width = heads * hd
     scale = 1.0 / math.sqrt(hd)
     dense_ffn, experts, top_k, expert_ffn, shared_ffn = 6848, 64, 6, 896, 1792
+    d, bs, local, page_mod = hd, 32, 4, 2
+    params = be.RouteParams()
+    pos = cap - 1
+    n_tok = hd // 2 - 1
+    inv_tok = torch.from_numpy(be.rope_inv(n_tok, 1e4)).cuda()
+    inv_page = torch.from_numpy(be.rope_inv(1, 256.0)).cuda()
+    prompt_blocks = 128
+    page_of_block = torch.arange(prompt_blocks, dtype=torch.int64) // 8
+    block_min, block_max = page_of_block.cuda(), page_of_block.cuda()
+    state = torch.tensor([0, pos, pos - 2048, 17, 3], dtype=torch.int64).cuda()
     table = bf16_randn(torch, (vocab, hidden), 0.5)
     lm = bf16_randn(torch, (vocab, hidden), 0.03)
     final_norm = weights(torch, hidden)
 
     def layer(moe):
         L = {"in": weights(torch, hidden), "post": weights(torch, hidden),
-             "qkv": bf16_randn(torch, (3 * width, hidden), 0.03), "o": bf16_randn(torch, (hidden, width), 0.03),
-             "kc": bf16_randn(torch, (cap, width)), "vc": bf16_randn(torch, (cap, width))}
+             "proj": bf16_randn(torch, (3 * width + 2 * d, hidden), 0.03), "o": bf16_randn(torch, (hidden, width), 0.03),
+             "rqn": 0.1 * torch.randn(d, device="cuda"), "rkn": 0.1 * torch.randn(d, device="cuda"),
+             "cls": torch.randn(d, device="cuda"), "rkeys": torch.randn(cap, d, device="cuda"),
+             "summ": torch.randn(cap // bs, d, device="cuda")}
         f = shared_ffn if moe else dense_ffn
         L.update({"gate": bf16_randn(torch, (f, hidden), 0.03), "up": bf16_randn(torch, (f, hidden), 0.03),
                   "down": bf16_randn(torch, (hidden, f), 0.03), "ffn": f, "moe": moe})
@@ -603,25 +631,32 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
 
     Ls = [layer(i > 0) for i in range(layers)]
     xs = [torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda")]
-    h, delta, qkv = torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda"), torch.empty(3 * width, device="cuda")
-    attn, o = torch.empty(width, device="cuda"), torch.empty(hidden, device="cuda")
+    h, delta = torch.empty(hidden, device="cuda"), torch.empty(hidden, device="cuda")
+    proj = torch.empty(3 * width + 2 * d, device="cuda")
+    attn, o, mask = torch.empty(width, device="cuda"), torch.empty(hidden, device="cuda"), torch.empty(cap, device="cuda")
     act, logits = torch.empty(dense_ffn, device="cuda"), torch.empty(vocab, device="cuda")
     ids, wts = torch.empty(1, top_k, dtype=torch.int64, device="cuda"), torch.empty(1, top_k, device="cuda")
     rlogits = torch.empty(experts, device="cuda")
     escratch = torch.empty(be.expert_scratch_floats(top_k, expert_ffn), device="cuda")
-    q, k, v = qkv[:width], qkv[width:2 * width], qkv[2 * width:]
+    q, k, v = proj[:width], proj[width:2 * width], proj[2 * width:3 * width]
+    rq, rk = proj[3 * width:3 * width + d], proj[3 * width + d:]
+
+    def route(L):
+        be.route_decode_step(rq, rk, L["rqn"], L["rkn"], 1e-6, inv_tok, inv_page, page_mod, L["cls"], L["rkeys"],
+                             L["summ"], block_min, block_max, state, params, mask)
 
     def step():
         cur = 0
         be.embed_step(table, state, xs[cur])
         pending = None
         for L in Ls:
-            be.add_rms_norm_gemv_bf16(xs[cur], L["qkv"], qkv, delta=pending,
+            be.add_rms_norm_gemv_bf16(xs[cur], L["proj"], proj, delta=pending,
                                       x_out=None if pending is None else xs[1 - cur], w_norm=L["in"])
             if pending is not None:
                 cur = 1 - cur
-            be.attend_rope_kv_step(q, k, v, L["kc"], L["vc"], heads, hd, None, scale, state, inv, None, 0, scratch,
-                                   attn)
+            route(L)
+            be.attend_rope_kv_step(q, k, v, L["kc"], L["vc"], heads, hd, mask, scale, state, inv_tok, inv_page,
+                                   page_mod, scratch, attn)
             be.gemv_bf16(attn, L["o"], o)
             a = act[:L["ffn"]]
             if L["moe"]:  # the shared experts' pair GEMV and the router in one launch
@@ -639,19 +674,34 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, inv, state, sc
             pending = delta
         be.add_rms_norm_gemv_bf16(xs[cur], lm, logits, delta=pending, w_norm=final_norm)
 
-    attn_bytes = b["add_rms_norm"] + b["rope"] + (b["attend"] + b["append"]) // 2 + bytes_gemv(3 * width, hidden) \
-        + bytes_gemv(hidden, width)
+    route_bytes = bytes_route_decode(pos, d, bs, local, prompt_blocks)
+    kv_bytes = b["attend"] + b["append"] + cap * 4          # fp32 cache, and the mask read
+    proj_bytes = bytes_gemv(3 * width + 2 * d, hidden)
+    attn_fixed = b["add_rms_norm"] + b["rope"] + route_bytes + proj_bytes + bytes_gemv(hidden, width)
     dense_bytes = 3 * dense_ffn * hidden * 2
     moe_bytes = 3 * shared_ffn * hidden * 2 + experts * hidden * 4 + 3 * top_k * expert_ffn * hidden * 2
-    total = (bytes_gather(1, hidden, 4) + layers * attn_bytes + dense_bytes + (layers - 1) * moe_bytes
-             + bytes_gemv(vocab, hidden))
-    ms = timer.graph([step])[0]
-    launches = 2 + 6 + 7 * (layers - 1)
+    rest = bytes_gather(1, hidden, 4) + dense_bytes + (layers - 1) * moe_bytes + bytes_gemv(vocab, hidden)
+    launches = 2 + 7 + 8 * (layers - 1)
+    ms_route = timer.graph([lambda L=L: route(L) for L in Ls])[0]
     out = {"workload": f"the model's decode step: embedding, layer 0 dense (FFN {dense_ffn}), layers 1-{layers - 1} "
                        f"mixture of experts ({top_k} of {experts} experts of FFN {expert_ffn}, shared FFN "
-                       f"{shared_ffn}, fp32 router), bf16 KV cache {cap} positions read in full, final norm + LM head "
-                       f"[{vocab}, {hidden}]; {launches} launches; block routing not built",
-           "step": report("decode step", total, ms), "us_per_token": round(ms * 1e3, 2)}
+                       f"{shared_ffn}, fp32 router), block-routed attention over {cap} positions (block {bs}, local "
+                       f"window {local * bs}, top-{params.top_m} entmax, {params.top_k} blocks, the query confined to "
+                       f"one page of a {prompt_blocks}-block prompt), PageRope (63 token pairs, 1 page pair), final "
+                       f"norm + LM head [{vocab}, {hidden}]; {launches} launches",
+           "route_decode_step": report("route_decode_step", route_bytes, ms_route)}
+    for name, dtype in (("fp32_cache", torch.float32), ("bf16_cache", torch.bfloat16)):
+        for L in Ls:
+            L["kc"] = torch.randn(cap, width, device="cuda").to(dtype)
+            L["vc"] = torch.randn(cap, width, device="cuda").to(dtype)
+        total = rest + layers * (attn_fixed + (kv_bytes if dtype == torch.float32 else
+                                               (b["attend"] + b["append"]) // 2 + cap * 4))
+        ms = timer.graph([step])[0]
+        out[name] = {"step": report(f"decode step, {name}", total, ms), "us_per_token": round(ms * 1e3, 2)}
+        for L in Ls:
+            del L["kc"], L["vc"]
+    out["step"] = out["fp32_cache"]["step"]
+    out["us_per_token"] = out["fp32_cache"]["us_per_token"]
     del Ls, table, lm
     return out
 

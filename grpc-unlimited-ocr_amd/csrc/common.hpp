@@ -209,6 +209,16 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
 }
 
+// A workgroup barrier that orders LDS only: every wave's LDS accesses before
+// it complete before any wave passes it, while global loads and stores stay
+// in flight across it (__syncthreads waits for those as well). For a
+// workgroup whose waves share data through LDS alone.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]: partner lane ^ 1
   v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]: partner lane ^ 2

@@ -56,232 +56,426 @@ struct RouteArgs {
 
 // ---- stages shared by every entry point ----------------------------------------------------
 
-// The summary of one block whose n keys (n <= kMaxBlockKeys) sit in LDS,
-// row-major with row stride d: out[e] = sum_t (w_t / total) key_t[e], w_t =
-// exp(a_t - max a), a_t = clamp(key_t . cls / sqrt d), total = max(sum_t
-// w_t, 1e-6). Wave w forms the logits of keys w, w + waves, ... (lane e
-// takes features e, e + 64, ...); total and the feature sums run over t in
-// order. Every thread of the block must call it.
-__device__ void summarize(const float* keys, int n, int d, const float* __restrict__ cls, float inv_sqrt_d,
-                          float* logit, float* total_slot, float* __restrict__ out) {
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// head_cls as summarize takes it: lane l holds features l, l + 64, l + 128,
+// l + 192 (zero past d).
+__device__ __forceinline__ void load_cls(const float* __restrict__ cls, int d, float (&c)[4]) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = lane + kWave * i < d ? cls[lane + kWave * i] : 0.0f;
+}
+
+// The summary of one block whose n keys (1 <= n <= kMaxBlockKeys) sit in
+// LDS, row-major with row stride d: out[e] = sum_t (w_t / total) key_t[e],
+// w_t = exp(a_t - max a), a_t = clamp(key_t . cls / sqrt d), total =
+// max(sum_t w_t, 1e-6). Wave w forms the logits of keys w, w + waves, ...
+// (lane e takes features e, e + 64, ...); wave 0 then holds a_t in lane t,
+// and total and the feature sums run over t in order. `p` is kMaxBlockKeys
+// floats of LDS. Every thread of the block must call it.
+__device__ void summarize(const float* keys, int n, int d, const float (&cls)[4], float inv_sqrt_d, float* p,
+                          float* __restrict__ out) {
 #pragma clang fp contract(off)
   const int wave = wave_in_block(), lane = threadIdx.x & (kWave - 1);
   const int waves = static_cast<int>(blockDim.x) / kWave;
   for (int t = wave; t < n; t += waves) {
     float part = 0.0f;
-    for (int e = lane; e < d; e += kWave) part += keys[t * d + e] * cls[e];
-    const float a = wave_sum(part);
-    if (lane == 0) logit[t] = clamp_act(a * inv_sqrt_d);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float peak = -3.402823466e+38f;
-    for (int t = 0; t < n; ++t) peak = fmaxf(peak, logit[t]);
-    float total = 0.0f;
-    for (int t = 0; t < n; ++t) {
-      logit[t] = expf(logit[t] - peak);
-      total += logit[t];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (lane + kWave * i < d) part += keys[t * d + lane + kWave * i] * cls[i];
     }
-    *total_slot = fmaxf(total, 1e-6f);
+    const float a = wave_sum(part);
+    if (lane == 0) p[t] = clamp_act(a * inv_sqrt_d);
   }
-  __syncthreads();
-  const float total = *total_slot;
+  lds_barrier();
+  if (wave == 0) {
+    const float a = lane < n ? p[lane] : -3.402823466e+38f;
+    const float peak = wave_max(a);
+    const float w = lane < n ? expf(a - peak) : 0.0f;
+    float total = 0.0f;
+    for (int t = 0; t < n; ++t) total += readlane_f32(w, t);
+    total = fmaxf(total, 1e-6f);
+    if (lane < n) p[lane] = w / total;
+  }
+  lds_barrier();
   for (int e = threadIdx.x; e < d; e += blockDim.x) {
     float acc = 0.0f;
-    for (int t = 0; t < n; ++t) acc += (logit[t] / total) * keys[t * d + e];
+    for (int t = 0; t < n; ++t) acc += p[t] * keys[t * d + e];
     out[e] = acc;
   }
 }
 
-// z[b] = (rq . summaries[b]) / sqrt d for b < n (unclamped), rq [d] in LDS.
-// Wave w scores blocks w, w + waves, ... eight at a time, every lane
-// holding four features (d <= 256, d % 4 == 0): the eight rows' loads go out
-// together. Every thread of the block must call it.
-__device__ void score_blocks(const float* rq, const float* __restrict__ summaries, int d, int n, float inv_sqrt_d,
-                             float* z) {
+// Block scores. A summary row's d / 4 16-byte chunks go to L lanes (d / 4
+// rounded up to 16, 32 or 64), so a wave reads 64 / L rows per load; a pass
+// holds kScoreSteps such loads per lane in registers, all in flight
+// together, then reduces each row over its lanes (DPP inside 16-lane rows,
+// then readlane).
+constexpr int kScoreSteps = 8;
+
+struct ScoreRows {
+  u32x4 row[kScoreSteps];
+};
+
+__device__ __forceinline__ int score_lanes(int d) { return d <= 64 ? 16 : (d <= 128 ? 32 : 64); }
+
+// Rows per pass: waves * (64 / L) * kScoreSteps.
+__device__ __forceinline__ int score_pass_rows(int d) {
+  return static_cast<int>(blockDim.x) / kWave * (kWave / score_lanes(d)) * kScoreSteps;
+}
+
+// Issues the loads of the pass starting at row `base` (rows < n).
+__device__ __forceinline__ void score_load(const float* __restrict__ summaries, int d, int n, int base,
+                                           ScoreRows& s) {
+  const int wave = wave_in_block(), lane = threadIdx.x & (kWave - 1);
+  const int waves = static_cast<int>(blockDim.x) / kWave;
+  const int L = score_lanes(d), R = kWave / L, sub = lane / L, c = lane & (L - 1);
+  const bool on = 4 * c < d;
+#pragma unroll
+  for (int i = 0; i < kScoreSteps; ++i) {
+    const int b = base + (i * waves + wave) * R + sub;
+    s.row[i] = u32x4{0u, 0u, 0u, 0u};
+    if (on && b < n) s.row[i] = *reinterpret_cast<const u32x4*>(summaries + static_cast<int64_t>(b) * d + 4 * c);
+  }
+}
+
+// z[b] = (rq . summaries[b]) / sqrt d for the pass's rows b < n (unclamped),
+// rq [d] in LDS. Each dot is summed as four products per lane, then over
+// the lanes in a fixed order, the same for every entry point.
+__device__ __forceinline__ void score_reduce(const float* rq, int d, int n, int base, float inv_sqrt_d,
+                                             const ScoreRows& s, float* z) {
 #pragma clang fp contract(off)
   const int wave = wave_in_block(), lane = threadIdx.x & (kWave - 1);
   const int waves = static_cast<int>(blockDim.x) / kWave;
-  const bool on = 4 * lane < d;
+  const int L = score_lanes(d), R = kWave / L, c = lane & (L - 1);
+  const bool on = 4 * c < d;
   float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (on) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) q[i] = rq[4 * lane + i];
+    for (int i = 0; i < 4; ++i) q[i] = rq[4 * c + i];
   }
-  constexpr int kBatch = 8;
-  for (int b0 = wave; b0 < n; b0 += waves * kBatch) {
-    u32x4 row[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int b = b0 + i * waves;
-      row[i] = u32x4{0u, 0u, 0u, 0u};
-      if (on && b < n) row[i] = *reinterpret_cast<const u32x4*>(summaries + static_cast<int64_t>(b) * d + 4 * lane);
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int b = b0 + i * waves;  // wave-uniform
-      if (b < n) {
-        float part = 0.0f;
-        part += q[0] * __uint_as_float(row[i].x);
-        part += q[1] * __uint_as_float(row[i].y);
-        part += q[2] * __uint_as_float(row[i].z);
-        part += q[3] * __uint_as_float(row[i].w);
-        const float s = wave_sum(part);
-        if (lane == 0) z[b] = s * inv_sqrt_d;
+  for (int i = 0; i < kScoreSteps; ++i) {
+    const int b0 = base + (i * waves + wave) * R;  // wave-uniform
+    if (b0 < n) {
+      float part = 0.0f;
+      part += q[0] * __uint_as_float(s.row[i].x);
+      part += q[1] * __uint_as_float(s.row[i].y);
+      part += q[2] * __uint_as_float(s.row[i].z);
+      part += q[3] * __uint_as_float(s.row[i].w);
+      part += dpp_f32<0xB1>(part);   // lane ^ 1
+      part += dpp_f32<0x4E>(part);   // lane ^ 2
+      part += dpp_f32<0x141>(part);  // the two quads of each 8 lanes
+      part += dpp_f32<0x140>(part);  // the two halves of each 16-lane row
+      const float r0 = readlane_f32(part, 0), r1 = readlane_f32(part, 16);
+      const float r2 = readlane_f32(part, 32), r3 = readlane_f32(part, 48);
+      if (lane == 0) {
+        if (L == 64) {
+          z[b0] = ((r0 + r1) + (r2 + r3)) * inv_sqrt_d;
+        } else if (L == 32) {
+          z[b0] = (r0 + r1) * inv_sqrt_d;
+          if (b0 + 1 < n) z[b0 + 1] = (r2 + r3) * inv_sqrt_d;
+        } else {
+          z[b0] = r0 * inv_sqrt_d;
+          if (b0 + 1 < n) z[b0 + 1] = r1 * inv_sqrt_d;
+          if (b0 + 2 < n) z[b0 + 2] = r2 * inv_sqrt_d;
+          if (b0 + 3 < n) z[b0 + 3] = r3 * inv_sqrt_d;
+        }
       }
     }
   }
 }
 
+// z[b] for b < n, pass by pass. Every thread of the block must call it.
+__device__ void score_blocks(const float* rq, const float* __restrict__ summaries, int d, int n, float inv_sqrt_d,
+                             float* z) {
+  const int step = score_pass_rows(d);
+  for (int base = 0; base < n; base += step) {
+    ScoreRows s;
+    score_load(summaries, d, n, base, s);
+    score_reduce(rq, d, n, base, inv_sqrt_d, s, z);
+  }
+}
+
 // Block-order key of a candidate score for the top-m: larger scores first,
-// then the lower block index (all scores are finite here).
+// then the lower block index (all scores are finite here; 0 is below every
+// key and marks an empty slot).
 __device__ __forceinline__ uint64_t order_key(float v, int b) {
   uint32_t u = __float_as_uint(v);
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return (static_cast<uint64_t>(u) << 32) | (0xffffffffu - static_cast<uint32_t>(b));
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint64_t o = __shfl_xor(v, off, kWave);
-    v = o > v ? o : v;
-  }
-  return v;
+__device__ __forceinline__ float key_value(uint64_t key) {
+  const uint32_t u = static_cast<uint32_t>(key >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
 }
 
-// LDS working set of route_row for one query row: x the blocks' entmax
-// inputs (it may be the z array itself, which is read before x is written at
-// the same index), cand the candidate flags, block_bias the mask value of a
-// block's keys outside the window, and the top-m values, blocks and logs.
+__device__ __forceinline__ int key_block(uint64_t key) {
+  return static_cast<int>(0xffffffffu - static_cast<uint32_t>(key));
+}
+
+// Inclusive sums over lanes 0..lane in lane order: lane j gets the fp32 sum
+// ((v_0 + v_1) + ...) + v_j, for lanes j < n. n - 1 steps of s = v + (s of
+// the lane below, through a one-lane DPP shift; lane 0 reads 0); after step
+// t the first t + 1 lanes hold their final sums, and as fp32 addition
+// commutes, v_j + s_(j-1) equals s_(j-1) + v_j bit for bit. Every lane of
+// the wave must be active.
+__device__ __forceinline__ float prefix_in_order(float v, int n) {
+#pragma clang fp contract(off)
+  float s = v;
+  for (int t = 1; t < n; ++t) s = v + dpp_f32<0x138>(s);  // wave_shr:1
+  return s;
+}
+
+template <int kCtrl>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v)), kCtrl, 0xF, 0xF, false));
+  const uint32_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v >> 32)), kCtrl, 0xF, 0xF, false));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), lane));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), lane));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// The wave's largest key, in every lane: a DPP butterfly inside each 16-lane
+// row, then the four row maxima. Every lane of the wave must be active.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
+  uint64_t o = dpp_u64<0xB1>(v);
+  v = o > v ? o : v;
+  o = dpp_u64<0x4E>(v);
+  v = o > v ? o : v;
+  o = dpp_u64<0x141>(v);
+  v = o > v ? o : v;
+  o = dpp_u64<0x140>(v);
+  v = o > v ? o : v;
+  const uint64_t r0 = readlane_u64(v, 0), r1 = readlane_u64(v, 16), r2 = readlane_u64(v, 32),
+                 r3 = readlane_u64(v, 48);
+  const uint64_t a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
+  return a > b ? a : b;
+}
+
+// The m largest of the wave's keys (S per lane, m <= 64): lane j returns the
+// j-th largest (0 past the wave's keys). Each lane sorts its S keys, then m
+// rounds take the largest head and the winning lane drops it.
+template <int S>
+__device__ __forceinline__ uint64_t wave_top(uint64_t (&key)[S], int m, int lane) {
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+#pragma unroll
+    for (int j = 0; j + 1 < S - i; ++j) {
+      const uint64_t a = key[j], b = key[j + 1];
+      key[j] = a > b ? a : b;
+      key[j + 1] = a > b ? b : a;
+    }
+  }
+  uint64_t mine = 0;
+  for (int j = 0; j < m; ++j) {
+    const uint64_t win = wave_max_key(key[0]);
+    if (lane == j) mine = win;
+    if (key[0] == win) {
+#pragma unroll
+      for (int i = 0; i + 1 < S; ++i) key[i] = key[i + 1];
+      key[S - 1] = 0;
+    }
+  }
+  return mine;
+}
+
+// LDS working set of the route of one query row: x the blocks' entmax
+// inputs (it may be the z array itself: each thread reads z[b] before it
+// writes x[b]), cand the candidate flags, block_bias the mask value of a
+// block's keys outside the window, and list the per-wave top-m keys (16
+// waves x kMaxTop).
 struct RouteLds {
-  float* x;                 // [nblk]
-  unsigned char* cand;      // [nblk]
-  float* block_bias;        // [nblk]
-  float* top_val;           // [kMaxTop]
-  int* top_idx;             // [kMaxTop]
-  float* top_logp;          // [kMaxTop]
+  float* x;             // [nblk]
+  unsigned char* cand;  // [nblk]
+  float* block_bias;    // [nblk]
+  uint64_t* list;       // [16 * kMaxTop]
+  int* any;             // [16]
 };
 
-// 1.5-entmax of the m values v[0..m) (in descending order), in place, with
-// block_router.cpp:68-91's fp32 steps: v = (v - v0) / 2, running mean and
-// mean square give tau_i = mean - sqrt(max((1 - rho (msq - mean^2)) / rho,
-// 0)), the support is the count of tau_i <= v_i, and v = max(v - tau*, 0)^2
-// with tau* = tau at support - 1 (recomputed by a second pass, so no array
-// is indexed by a run-time value).
-__device__ void entmax15_sorted(float* v, int m) {
-#pragma clang fp contract(off)
-  const float peak = v[0];
-  for (int i = 0; i < m; ++i) v[i] = (v[i] - peak) / 2.0f;
-  int support = 0;
-  {
-    float sum = 0.0f, sum_sq = 0.0f;
-    for (int i = 0; i < m; ++i) {
-      sum += v[i];
-      sum_sq += v[i] * v[i];
-      const float rho = static_cast<float>(i + 1);
-      const float mean = sum / rho, mean_sq = sum_sq / rho;
-      const float ss = rho * (mean_sq - mean * mean);
-      const float delta = fmaxf((1.0f - ss) / rho, 0.0f);
-      if (mean - sqrtf(delta) <= v[i]) ++support;
+// The prompt blocks' page ranges of the blocks this thread owns (b =
+// threadIdx.x + kRouteBlock i, i < 4; -1 where a block has no range or the
+// query no page).
+constexpr int kBlocksPerThread = static_cast<int>(kMaxRouteBlocks) / kRouteBlock;
+
+struct PageRanges {
+  int64_t lo[kBlocksPerThread], hi[kBlocksPerThread];
+};
+
+__device__ __forceinline__ void load_pages(const int64_t* __restrict__ block_min,
+                                           const int64_t* __restrict__ block_max, int64_t prompt_blocks, int nblk,
+                                           int64_t page, PageRanges& r) {
+#pragma unroll
+  for (int i = 0; i < kBlocksPerThread; ++i) {
+    const int b = static_cast<int>(threadIdx.x) + kRouteBlock * i;
+    r.lo[i] = -1;
+    r.hi[i] = -1;
+    if (page >= 0 && b < nblk && b < prompt_blocks) {
+      r.lo[i] = block_min[b];
+      r.hi[i] = block_max[b];
     }
-  }
-  const int at = (support > 1 ? support : 1) - 1;
-  float tau_star = 0.0f;
-  {
-    float sum = 0.0f, sum_sq = 0.0f;
-    for (int i = 0; i <= at; ++i) {
-      sum += v[i];
-      sum_sq += v[i] * v[i];
-      const float rho = static_cast<float>(i + 1);
-      const float mean = sum / rho, mean_sq = sum_sq / rho;
-      const float ss = rho * (mean_sq - mean * mean);
-      const float delta = fmaxf((1.0f - ss) / rho, 0.0f);
-      tau_star = mean - sqrtf(delta);
-    }
-  }
-  for (int i = 0; i < m; ++i) {
-    const float t = fmaxf(v[i] - tau_star, 0.0f);
-    v[i] = t * t;
   }
 }
 
-// Routes one query at position pos over nblk blocks (z[b], raw scores of the
-// blocks b <= last_remote; other entries are not read) and writes its key
-// mask mask[0..keys) (keys past pos get -inf). page < 0: no page
-// restriction. Every thread of the block must call it.
-__device__ void route_row(const float* z, int nblk, int64_t pos, int64_t keys, int64_t page,
-                          const int64_t* __restrict__ block_min, const int64_t* __restrict__ block_max,
-                          int64_t prompt_blocks, const RouteArgs p, RouteLds sh, float* __restrict__ mask) {
-#pragma clang fp contract(off)
-  const int64_t last_remote = pos / p.block_size - p.local_blocks;
+// Whether v holds in any thread of the block, through one LDS slot per wave
+// (`slots`, kRouteBlock / 64 ints, written once per launch).
+__device__ __forceinline__ bool block_any(bool v, int* slots) {
+  const uint64_t lanes = __ballot(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) slots[wave_in_block()] = lanes != 0;
+  lds_barrier();
+  int any = 0;
+  for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) any |= slots[w];
+  return any != 0;
+}
+
+// cand[b], b < nblk: remote (b <= last_remote) and, for a query on a page,
+// one of the page's prompt blocks; a query whose page has no remote block
+// routes over every remote block (decoder.cpp:42-56). Every thread of a
+// kRouteBlock block must call it.
+__device__ __forceinline__ void route_candidates(const PageRanges& r, int nblk, int64_t last_remote, int64_t page,
+                                                 unsigned char* cand, int* any_slots) {
   int any_local = 0;
-  for (int b = threadIdx.x; b < nblk; b += blockDim.x) {
-    const bool remote = b <= last_remote;
-    const bool allowed = page >= 0 && b < prompt_blocks && block_min[b] >= 0 && block_min[b] <= page &&
-                         page <= block_max[b];
-    sh.cand[b] = remote && allowed;
-    any_local |= remote && allowed;
+#pragma unroll
+  for (int i = 0; i < kBlocksPerThread; ++i) {
+    const int b = static_cast<int>(threadIdx.x) + kRouteBlock * i;
+    if (b < nblk) {
+      const bool remote = b <= last_remote;
+      const bool allowed = page >= 0 && r.lo[i] >= 0 && r.lo[i] <= page && page <= r.hi[i];
+      cand[b] = remote && allowed;
+      any_local |= remote && allowed;
+    }
   }
-  // A page with no remote block of its own routes over every remote block.
-  const int any = __syncthreads_or(any_local);
-  for (int b = threadIdx.x; b < nblk; b += blockDim.x) {
-    const bool remote = b <= last_remote;
-    if (!any) sh.cand[b] = remote;
-    const float xb = sh.cand[b] ? clamp_act(z[b]) * p.idx_scale : kEntmaxMasked;
-    sh.x[b] = xb;
-    sh.block_bias[b] = -INFINITY;
+  if (!block_any(any_local != 0, any_slots)) {
+#pragma unroll
+    for (int i = 0; i < kBlocksPerThread; ++i) {
+      const int b = static_cast<int>(threadIdx.x) + kRouteBlock * i;
+      if (b < nblk) cand[b] = b <= last_remote;
+    }
   }
-  __syncthreads();
+}
+
+// The selection and the key mask of one query at position pos over nblk
+// blocks (z[b], raw scores of the blocks b <= last_remote; other entries are
+// not read), given cand: x = clamp(z) * idx_scale on candidates and -1e4
+// elsewhere; the top m = clamp(top_m, 1, nblk) by (x desc, block asc)
+// through 1.5-entmax (block_router.cpp:68-91: the running sums in order,
+// each tau and the support in its own lane); the first k = clamp(top_k, 1,
+// m) with their log-prior bias (logp - mean over the valid ones) / sigma
+// (block_router.cpp:131-151); then mask[0..keys): 0 on the local window,
+// the bias on the keys of a valid selected block, -inf elsewhere and past
+// pos (attention_plan.cpp:34-56). Every thread of a kRouteBlock block must
+// call it.
+__device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys, const RouteArgs p, RouteLds sh,
+                             float* __restrict__ mask) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int i = 0; i < kBlocksPerThread; ++i) {
+    const int b = static_cast<int>(threadIdx.x) + kRouteBlock * i;
+    if (b < nblk) {
+      const float xb = sh.cand[b] ? clamp_act(z[b]) * p.idx_scale : kEntmaxMasked;
+      sh.x[b] = xb;
+      sh.block_bias[b] = -INFINITY;
+    }
+  }
+  lds_barrier();
 
   const int m = p.top_m < nblk ? (p.top_m > 1 ? p.top_m : 1) : (nblk > 1 ? nblk : 1);
   const int k = p.top_k < m ? (p.top_k > 1 ? p.top_k : 1) : m;
-  if (wave_in_block() == 0) {
-    // The top m by m rounds of a wave-wide max over each lane's best block
-    // not yet taken (lane l owns blocks l, l + 64, ...; up to 64 each).
-    const int lane = threadIdx.x & (kWave - 1);
-    uint64_t taken = 0;
-    for (int j = 0; j < m; ++j) {
-      uint64_t best = 0;
-      for (int i = 0, b = lane; b < nblk; ++i, b += kWave) {
-        if ((taken >> i) & 1u) continue;
-        const uint64_t key = order_key(sh.x[b], b);
-        best = key > best ? key : best;
+  const int wave = wave_in_block(), lane = threadIdx.x & (kWave - 1);
+  constexpr int kSlice = 4 * kWave;  // blocks per wave
+  uint64_t mine = 0;
+  if (nblk <= kSlice) {
+    if (wave == 0) {
+      uint64_t key[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = lane + kWave * i;
+        key[i] = b < nblk ? order_key(sh.x[b], b) : 0;
       }
-      const uint64_t win = wave_max_u64(best);
-      const int wb = static_cast<int>(0xffffffffu - static_cast<uint32_t>(win));
-      if ((wb & (kWave - 1)) == lane) taken |= uint64_t{1} << (wb / kWave);
-      if (lane == 0) {
-        sh.top_idx[j] = wb;
-        sh.top_val[j] = sh.x[wb];
-      }
+      mine = wave_top<4>(key, m, lane);
     }
-    if (lane == 0) {
-      // the log-prior bias of the first k (block_router.cpp:131-151)
-      entmax15_sorted(sh.top_val, m);
-      float logp_sum = 0.0f;
-      int count = 0;
-      for (int i = 0; i < k; ++i) {
-        sh.top_logp[i] = logf(fmaxf(sh.top_val[i], p.floor));
-        if (sh.cand[sh.top_idx[i]]) {
-          logp_sum += sh.top_logp[i];
-          ++count;
-        }
-      }
-      const float mu = logp_sum / static_cast<float>(count > 1 ? count : 1);
-      for (int i = 0; i < k; ++i) {
-        if (sh.cand[sh.top_idx[i]]) sh.block_bias[sh.top_idx[i]] = (sh.top_logp[i] - mu) / p.sigma;
-      }
+  } else {
+    // each wave's top m of its slice, then wave 0 takes the top m of those
+    uint64_t key[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = wave * kSlice + lane + kWave * i;
+      key[i] = b < nblk ? order_key(sh.x[b], b) : 0;
+    }
+    const uint64_t best = wave_top<4>(key, m, lane);
+    if (lane < m) sh.list[wave * m + lane] = best;
+    lds_barrier();
+    if (wave == 0) {
+      const int listed = static_cast<int>(blockDim.x) / kWave * m;
+      uint64_t key8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) key8[i] = lane + kWave * i < listed ? sh.list[lane + kWave * i] : 0;
+      mine = wave_top<8>(key8, m, lane);
     }
   }
-  __syncthreads();
+  if (wave == 0) {
+    // lane j < m holds the j-th selection
+    const bool have = lane < m;
+    const int blk = have ? key_block(mine) : 0;
+    const float val = have ? key_value(mine) : 0.0f;
+    const float peak = readlane_f32(val, 0);
+    const float v = have ? (val - peak) / 2.0f : 0.0f;
+    const float sum = prefix_in_order(v, m), sum_sq = prefix_in_order(v * v, m);
+    const float rho = static_cast<float>(lane + 1);
+    const float mean = sum / rho, mean_sq = sum_sq / rho;
+    const float ss = rho * (mean_sq - mean * mean);
+    const float delta = fmaxf((1.0f - ss) / rho, 0.0f);
+    const float tau = mean - sqrtf(delta);
+    const int support = __popcll(__ballot(have && tau <= v));
+    const float tau_star = readlane_f32(tau, (support > 1 ? support : 1) - 1);
+    const float t = fmaxf(v - tau_star, 0.0f);
+    const float prob = t * t;
+    const bool valid = lane < k && sh.cand[blk] != 0;
+    const float logp = logf(fmaxf(prob, p.floor));
+    const float logp_sum = readlane_f32(prefix_in_order(valid ? logp : 0.0f, k), k - 1);
+    const int count = __popcll(__ballot(valid));
+    const float mu = logp_sum / static_cast<float>(count > 1 ? count : 1);
+    if (valid) sh.block_bias[blk] = (logp - mu) / p.sigma;
+  }
+  lds_barrier();
 
   const int64_t window = static_cast<int64_t>(p.local_blocks) * p.block_size;
-  for (int64_t j = threadIdx.x; j < keys; j += blockDim.x) {
+  const uint32_t bs = static_cast<uint32_t>(p.block_size);
+  auto value = [&](int64_t j) {
     float v = -INFINITY;
-    if (j <= pos) v = j > pos - window ? 0.0f : sh.block_bias[j / p.block_size];
-    mask[j] = v;
+    if (j <= pos) v = j > pos - window ? 0.0f : sh.block_bias[static_cast<uint32_t>(j) / bs];
+    return v;
+  };
+  int64_t j0 = 0;
+  if ((reinterpret_cast<uintptr_t>(mask) & 15u) == 0) {  // 16-byte stores
+    const int64_t quads = keys / 4;
+    for (int64_t c = threadIdx.x; c < quads; c += blockDim.x) {
+      const u32x4 q{__float_as_uint(value(4 * c)), __float_as_uint(value(4 * c + 1)),
+                    __float_as_uint(value(4 * c + 2)), __float_as_uint(value(4 * c + 3))};
+      *reinterpret_cast<u32x4*>(mask + 4 * c) = q;
+    }
+    j0 = 4 * quads;
   }
+  for (int64_t j = j0 + threadIdx.x; j < keys; j += blockDim.x) mask[j] = value(j);
+}
+
+// Routes one query row: its candidates, then route_select.
+__device__ void route_row(const float* z, int nblk, int64_t pos, int64_t keys, int64_t page,
+                          const int64_t* __restrict__ block_min, const int64_t* __restrict__ block_max,
+                          int64_t prompt_blocks, const RouteArgs p, RouteLds sh, float* __restrict__ mask) {
+  PageRanges r;
+  load_pages(block_min, block_max, prompt_blocks, nblk, page, r);
+  route_candidates(r, nblk, pos / p.block_size - p.local_blocks, page, sh.cand, sh.any);
+  route_select(z, nblk, pos, keys, p, sh, mask);
 }
 
 // LDS for route_row in a kernel that routes one row and needs nothing else.
@@ -289,10 +483,9 @@ struct RouteShared {
   float x[kMaxRouteBlocks];
   unsigned char cand[kMaxRouteBlocks];
   float block_bias[kMaxRouteBlocks];
-  float top_val[kMaxTop];
-  int top_idx[kMaxTop];
-  float top_logp[kMaxTop];
-  __device__ RouteLds lds() { return RouteLds{x, cand, block_bias, top_val, top_idx, top_logp}; }
+  uint64_t list[kRouteBlock / kWave * kMaxTop];
+  int any[kRouteBlock / kWave];
+  __device__ RouteLds lds() { return RouteLds{x, cand, block_bias, list, any}; }
 };
 
 // Stages rows [first, first + n) of router keys [*, d] into LDS (16-byte
@@ -305,6 +498,34 @@ __device__ void stage_keys(const float* __restrict__ rk, int64_t first, int n, i
   }
 }
 
+// The same rows loaded into registers by a kRouteBlock block (n * d <=
+// kStageFloats: at most two chunks per thread), stored to LDS later.
+constexpr int kStageChunks = kStageFloats / 4 / kRouteBlock;
+
+struct StagedKeys {
+  u32x4 chunk[kStageChunks];
+};
+
+__device__ __forceinline__ void load_keys(const float* __restrict__ rk, int64_t first, int n, int d, StagedKeys& s) {
+  const int chunks = n * d / 4;
+  const float* src = rk + first * d;
+#pragma unroll
+  for (int i = 0; i < kStageChunks; ++i) {
+    const int c = static_cast<int>(threadIdx.x) + kRouteBlock * i;
+    s.chunk[i] = u32x4{0u, 0u, 0u, 0u};
+    if (c < chunks) s.chunk[i] = *reinterpret_cast<const u32x4*>(src + 4 * c);
+  }
+}
+
+__device__ __forceinline__ void store_keys(const StagedKeys& s, int n, int d, float* lds) {
+  const int chunks = n * d / 4;
+#pragma unroll
+  for (int i = 0; i < kStageChunks; ++i) {
+    const int c = static_cast<int>(threadIdx.x) + kRouteBlock * i;
+    if (c < chunks) *reinterpret_cast<u32x4*>(lds + 4 * c) = s.chunk[i];
+  }
+}
+
 // ---- kernels -------------------------------------------------------------------------------
 
 // Every block of s keys: one workgroup per block.
@@ -312,13 +533,14 @@ __global__ __launch_bounds__(256) void block_summaries_k(const float* __restrict
                                                          const float* __restrict__ cls, int block_size,
                                                          float inv_sqrt_d, float* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) float keys[kStageFloats];
-  __shared__ float logit[kMaxBlockKeys];
-  __shared__ float total;
+  __shared__ float p[kMaxBlockKeys];
   const int64_t first = static_cast<int64_t>(blockIdx.x) * block_size;
   const int n = static_cast<int>(s - first < block_size ? s - first : block_size);
+  float c[4];
+  load_cls(cls, d, c);
   stage_keys(rk, first, n, d, keys);
-  __syncthreads();
-  summarize(keys, n, d, cls, inv_sqrt_d, logit, &total, out + static_cast<int64_t>(blockIdx.x) * d);
+  lds_barrier();
+  summarize(keys, n, d, c, inv_sqrt_d, p, out + static_cast<int64_t>(blockIdx.x) * d);
 }
 
 // The summary of the block holding state->pos (keys first..pos).
@@ -327,16 +549,17 @@ __global__ __launch_bounds__(256) void summary_step_k(const float* __restrict__ 
                                                       float inv_sqrt_d, const uocr_rocm_step_state* __restrict__ state,
                                                       int64_t max_blocks, float* __restrict__ summaries) {
   __shared__ __attribute__((aligned(16))) float keys[kStageFloats];
-  __shared__ float logit[kMaxBlockKeys];
-  __shared__ float total;
+  __shared__ float p[kMaxBlockKeys];
   const int64_t pos = state->pos;
   const int64_t blk = pos / block_size;
   if (pos < 0 || blk >= max_blocks) return;  // uniform over the block
   const int64_t first = blk * block_size;
   const int n = static_cast<int>(pos - first + 1);
+  float c[4];
+  load_cls(cls, d, c);
   stage_keys(rk, first, n, d, keys);
-  __syncthreads();
-  summarize(keys, n, d, cls, inv_sqrt_d, logit, &total, summaries + blk * d);
+  lds_barrier();
+  summarize(keys, n, d, c, inv_sqrt_d, p, summaries + blk * d);
 }
 
 // z[b] for every block up to the one holding pos.
@@ -351,9 +574,9 @@ __global__ __launch_bounds__(kRouteBlock) void scores_step_k(const float* __rest
   const int64_t nb = pos < 0 ? 0 : pos / block_size + 1;
   const int n = static_cast<int>(nb < max_blocks ? nb : max_blocks);
   for (int e = threadIdx.x; e < d; e += blockDim.x) q[e] = rq[e];
-  __syncthreads();
+  lds_barrier();
   score_blocks(q, summaries, d, n, inv_sqrt_d, zs);
-  __syncthreads();
+  lds_barrier();
   for (int b = threadIdx.x; b < n; b += blockDim.x) z[b] = zs[b];
 }
 
@@ -413,11 +636,11 @@ struct DecodeRouteArgs {
 };
 
 // The router's RMSNorm of one row of d floats held four per lane (lanes with
-// 4 lane >= d hold zeros): non-finite values count as 0, y = clamp(clamp(v
-// inv) (1 + w)) with inv = 1 / sqrt(ss / d + eps) formed in fp64 from the
-// fp32 sum of squares (src/model/decoder.cpp:20-34).
-__device__ __forceinline__ void router_norm_lane(float (&v)[4], const float* __restrict__ w, int d, float eps,
-                                                 int lane) {
+// 4 lane >= d hold zeros), with its weights w held the same way: non-finite
+// values count as 0, y = clamp(clamp(v inv) (1 + w)) with inv = 1 / sqrt(ss
+// / d + eps) formed in fp64 from the fp32 sum of squares
+// (src/model/decoder.cpp:20-34).
+__device__ __forceinline__ void router_norm_lane(float (&v)[4], const float (&w)[4], int d, float eps, int lane) {
 #pragma clang fp contract(off)
   float part = 0.0f;
 #pragma unroll
@@ -430,51 +653,77 @@ __device__ __forceinline__ void router_norm_lane(float (&v)[4], const float* __r
                                                   static_cast<double>(eps)));
   if (4 * lane < d) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = clamp_act(clamp_act(v[i] * inv) * (1.0f + w[4 * lane + i]));
+    for (int i = 0; i < 4; ++i) v[i] = clamp_act(clamp_act(v[i] * inv) * (1.0f + w[i]));
   }
 }
 
 __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a) {
 #pragma clang fp contract(off)
   // keys holds the staged block of router keys until its summary is formed,
-  // then the blocks' mask values; zs holds the scores, then (in place) the
-  // entmax inputs.
+  // then the blocks' mask values and the per-wave top-m lists; zs holds the
+  // scores, then (in place) the entmax inputs.
   __shared__ __attribute__((aligned(16))) float keys[kStageFloats];
   __shared__ float rqk[2][kMaxIndexDim];  // normed, then rotated rq and rk
   __shared__ float zs[kMaxRouteBlocks];
   __shared__ unsigned char cand[kMaxRouteBlocks];
-  __shared__ float logit[kMaxBlockKeys];
-  __shared__ float top_val[kMaxTop], top_logp[kMaxTop];
-  __shared__ int top_idx[kMaxTop];
-  __shared__ float total;
-  static_assert(kStageFloats >= kMaxRouteBlocks, "the staged keys' space holds the blocks' mask values");
+  __shared__ float p_lds[kMaxBlockKeys];
+  __shared__ int any_slots[kRouteBlock / kWave];
+  static_assert(kStageFloats >= kMaxRouteBlocks + 2 * (kRouteBlock / kWave) * kMaxTop,
+                "the staged keys' space holds the blocks' mask values and the top-m lists");
   const int64_t pos = a.state->pos;
   const int bs = a.p.block_size;
   if (pos < 0 || pos >= a.capacity) return;  // uniform over the block
   const int d = a.d, half = d / 2;
   const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
+  const int64_t blk = pos / bs, first = blk * bs;
+  const int n = static_cast<int>(pos - first + 1);
+  const int64_t last_remote = blk - a.p.local_blocks;
+  const int nrem = last_remote < 0 ? 0 : static_cast<int>(last_remote + 1);
+  const int nblk = static_cast<int>(blk + 1);
+  const int64_t query_page = a.state->query_page;
 
-  // 1. router norm of rq (wave 0) and rk (wave 1), then rope at (tok, page)
-  if (wave < 2) {
+  // 1. every load that does not wait for another: the router rows and their
+  // weights, head_cls, the rope frequency of this thread's pair, the block's
+  // earlier keys, the prompt blocks' page ranges and (the remote blocks being
+  // whole, none of them the block summarized here) the first pass of
+  // summaries
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (wave < 2 && 4 * lane < d) {
     const float* src = wave == 0 ? a.rq : a.rk;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (4 * lane < d) {
+    const float* wn = wave == 0 ? a.q_norm : a.k_norm;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = src[4 * lane + i];
+    for (int i = 0; i < 4; ++i) {
+      v[i] = src[4 * lane + i];
+      w[i] = wn[4 * lane + i];
     }
-    router_norm_lane(v, wave == 0 ? a.q_norm : a.k_norm, d, a.eps, lane);
+  }
+  float cls[4];
+  load_cls(a.cls, d, cls);
+  const int pr = threadIdx.x;
+  float freq = 0.0f;
+  if (pr < half) freq = pr < a.n_tok ? a.inv_tok[pr] : a.inv_page[pr - a.n_tok];
+  StagedKeys staged;
+  load_keys(a.router_keys, first, n - 1, d, staged);
+  PageRanges ranges;
+  load_pages(a.block_min, a.block_max, a.prompt_blocks, nblk, query_page, ranges);
+  const bool early = a.p.local_blocks > 0;
+  ScoreRows rows;
+  if (early) score_load(a.summaries, d, nrem, 0, rows);
+
+  // 2. router norm of rq (wave 0) and rk (wave 1), then rope at (tok, page)
+  if (wave < 2) {
+    router_norm_lane(v, w, d, a.eps, lane);
     if (4 * lane < d) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) rqk[wave][4 * lane + i] = v[i];
     }
   }
-  __syncthreads();
-  if (static_cast<int>(threadIdx.x) < half) {
-    const int pr = threadIdx.x;
+  store_keys(staged, n - 1, d, keys);
+  lds_barrier();
+  if (pr < half) {
     int64_t pg = a.state->page;
     if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
-    const float angle = pr < a.n_tok ? static_cast<float>(a.state->tok) * a.inv_tok[pr]
-                                     : static_cast<float>(pg) * a.inv_page[pr - a.n_tok];
+    const float angle = (pr < a.n_tok ? static_cast<float>(a.state->tok) : static_cast<float>(pg)) * freq;
     float sn, cs;
     sincosf(angle, &sn, &cs);
 #pragma unroll
@@ -484,12 +733,9 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
       rqk[r][pr + half] = x1 * cs + x0 * sn;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
-  // 2. append rk at pos; stage the keys of the block holding pos (the new
-  // one from LDS) and refresh that block's summary
-  const int64_t blk = pos / bs, first = blk * bs;
-  const int n = static_cast<int>(pos - first + 1);
+  // 3. append rk at pos and refresh the summary of the block holding pos
   for (int e = threadIdx.x; e < d; e += blockDim.x) {
     a.router_keys[pos * d + e] = rqk[1][e];
     keys[(n - 1) * d + e] = rqk[1][e];
@@ -498,22 +744,29 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
       a.rqk_out[d + e] = rqk[1][e];
     }
   }
-  stage_keys(a.router_keys, first, n - 1, d, keys);
-  __syncthreads();
-  summarize(keys, n, d, a.cls, a.inv_sqrt_d, logit, &total, a.summaries + blk * d);
+  lds_barrier();
+  summarize(keys, n, d, cls, a.inv_sqrt_d, p_lds, a.summaries + blk * d);
 
-  // 3. scores of the blocks before the window (whole, so unchanged here)
-  const int64_t last_remote = blk - a.p.local_blocks;
-  const int nrem = last_remote < 0 ? 0 : static_cast<int>(last_remote + 1);
-  score_blocks(rqk[0], a.summaries, d, nrem, a.inv_sqrt_d, zs);
-  __syncthreads();
+  // 4. the candidates, and the scores of the blocks before the window
+  route_candidates(ranges, nblk, last_remote, query_page, cand, any_slots);
+  if (!early) {
+    __syncthreads();  // the summary just written is one of the rows scored
+    score_load(a.summaries, d, nrem, 0, rows);
+  }
+  score_reduce(rqk[0], d, nrem, 0, a.inv_sqrt_d, rows, zs);
+  const int pass = score_pass_rows(d);
+  for (int base = pass; base < nrem; base += pass) {
+    score_load(a.summaries, d, nrem, base, rows);
+    score_reduce(rqk[0], d, nrem, base, a.inv_sqrt_d, rows, zs);
+  }
+  lds_barrier();
   if (a.z_out != nullptr) {
     for (int b = threadIdx.x; b < nrem; b += blockDim.x) a.z_out[b] = zs[b];
   }
 
-  // 4. the route and the key mask over keys 0..pos
-  route_row(zs, static_cast<int>(blk + 1), pos, pos + 1, a.state->query_page, a.block_min, a.block_max,
-            a.prompt_blocks, a.p, RouteLds{zs, cand, keys, top_val, top_idx, top_logp}, a.mask);
+  // 5. the selection and the key mask over keys 0..pos
+  route_select(zs, nblk, pos, pos + 1, a.p,
+               RouteLds{zs, cand, keys, reinterpret_cast<uint64_t*>(keys + kMaxRouteBlocks), any_slots}, a.mask);
 }
 
 // ---- host side -----------------------------------------------------------------------------

@@ -42,6 +42,23 @@ void orc_attention_one(const float* q, const float* k, const float* v, int64_t k
 void orc_expert_topk(const float* logits, int64_t rows, int64_t experts, int64_t k, int64_t* ids, float* weights);
 void orc_scale_add_mask(float* x, float scale, const float* mask, int64_t batch, int64_t rows, int64_t cols);
 void orc_quick_gelu(float* x, int64_t n);
+/* The block router (src/model/block_router.cpp, src/model/attention_plan.cpp). */
+void orc_block_summaries(const float* rk, int64_t keys, int64_t d, const float* cls, int64_t block_size,
+                         float* out);
+void orc_block_scores(const float* rq, int64_t lq, const float* summaries, int64_t nblk, int64_t d,
+                      const int64_t* q_pos, int64_t block_size, int64_t local_blocks, float* out);
+void orc_entmax15(float* x, int64_t n);
+int64_t orc_select_blocks(const float* scores, int64_t lq, int64_t nblk, const uint8_t* candidate, int64_t top_m,
+                          int64_t top_k, float idx_scale, float floor_p, float sigma, int64_t* block, float* bias,
+                          uint8_t* valid);
+void orc_key_mask(const int64_t* block, const float* bias, const uint8_t* valid, int64_t width, int64_t rows,
+                  int64_t first_pos, int64_t keys, int64_t block_size, int64_t local_blocks, float* mask);
+int orc_page_candidates(const int64_t* min_page, const int64_t* max_page, int64_t known, int64_t page, int64_t nblk,
+                        uint8_t* out);
+void orc_route_one(const float* rq, const float* rk, int64_t pos, int64_t d, const float* cls,
+                   const int64_t* min_page, const int64_t* max_page, int64_t known, int64_t query_page,
+                   int64_t block_size, int64_t local_blocks, int64_t top_m, int64_t top_k, float idx_scale,
+                   float floor_p, float sigma, float* summaries, float* mask);
 
 #ifdef __cplusplus
 }

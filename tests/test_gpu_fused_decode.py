@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from parity import assert_f32_close, dev_bf16, dev_f32, dev_i64, host_f32, normal
+from parity import assert_bf16_close, assert_f32_close, dev_bf16, dev_f32, dev_i64, host_f32, normal
 
 pytestmark = pytest.mark.gpu
 
@@ -267,6 +267,34 @@ def test_embed_add_rms_norm_matches_unfused(backend, dtype, cols, with_delta):
         backend.embed_add_rms_norm_step(table, state, w, x, h, delta=delta)
         view = torch.int16 if dtype == "bf16" else torch.int32
         assert torch.equal(x.view(view), xu.view(view)) and torch.equal(h.view(view), hu.view(view)), token
+
+
+def test_embed_add_rms_norm_full_vocabulary_against_oracle(backend):
+    """The bf16 embed + add + RMSNorm step on the model's whole table
+    [128000, 2048] (500 MB, generated on the device), rows at both ends and
+    the middle, against the oracle's chain (embedding row, add, RMSNorm in
+    fp32): x = bf16(row + delta) exactly, h within 2 bf16 ulp; a token past
+    the table reads a zero row."""
+    vocab, cols = 128000, 2048
+    g = torch.Generator(device="cuda").manual_seed(373)
+    table = (0.02 * torch.randn(vocab, cols, device="cuda", generator=g)).to(torch.bfloat16)
+    w_host = (1 + 0.02 * normal(374, cols)).astype(np.float32)
+    d_bits = oracle.f32_to_bf16(normal(375, cols))
+    w, delta = dev_f32(w_host), dev_bf16(d_bits)
+    x, h = torch.empty(cols, dtype=torch.bfloat16, device="cuda"), torch.empty(cols, dtype=torch.bfloat16, device="cuda")
+    for token in (127999, 127998, 64000, 0, 128000):
+        backend.embed_add_rms_norm_step(table, dev_i64([token, 5, 5, 0, -1]), w, x, h, delta=delta)
+        torch.cuda.synchronize()
+        if token < vocab:
+            row = oracle.bf16_to_f32(table[token].view(torch.int16).cpu().numpy().view(np.uint16))
+        else:
+            row = np.zeros(cols, np.float32)
+        want_x, want_h = oracle.add_rms_norm(row[None], oracle.bf16_to_f32(d_bits)[None], w_host, 1e-6)
+        got_x = x.view(torch.int16).cpu().numpy().view(np.uint16)
+        got_h = h.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got_x, oracle.f32_to_bf16(want_x[0])), f"x at token {token}"
+        assert_bf16_close(got_h, want_h[0], f"h at token {token}")
+    del table
 
 
 @pytest.mark.parametrize("heads,hd,cap,pos,masked", [(10, 128, 8192, 5000, False), (10, 128, 2048, 1500, True),
