@@ -872,48 +872,59 @@ def summarize_trace(trace_dir):
     return "\n".join(out)
 
 
-def summarize_pmc(fetch_dir, write_dir):
-    """Markdown table of FETCH_SIZE / WRITE_SIZE (KiB per dispatch, median)
-    per kernel and grid, with both scaled by what the counters read for the
-    256 MiB calibration copy (known bytes / counter bytes)."""
+# HBM-side request counters of the L2 (summed over its channels), two runs:
+# the read requests by size, then all read requests and the write requests
+# (at most 4 TCC counters fit one run).
+PMC_PASS_READS = ("TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum")
+PMC_PASS_WRITES = ("TCC_EA0_RDREQ_sum", "TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
+
+
+def _load_counters(d):
+    """{(kernel, grid): {counter: median value per dispatch}} from a --pmc run."""
     import csv
     import statistics as st
 
-    def load(d, counter):
-        by = {}
-        for r in csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))):
-            if r["Counter_Name"] != counter:
-                continue
-            key = (_kernel_label(r["Kernel_Name"]), r.get("Grid_Size", ""))
-            by.setdefault(key, []).append(float(r["Counter_Value"]))
-        return {k: st.median(v) for k, v in by.items()}
+    by = {}
+    for r in csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))):
+        key = (_kernel_label(r["Kernel_Name"]), r.get("Grid_Size", ""))
+        by.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    return {k: {c: st.median(v) for c, v in cs.items()} for k, cs in by.items()}
 
-    fetch, write = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
-    cf = [v for (k, g), v in fetch.items() if k == COPY_KERNEL]
-    cw = [v for (k, g), v in write.items() if k == COPY_KERNEL]
-    f_scale = COPY_BYTES / (max(cf) * 1024) if cf else 1.0
-    w_scale = COPY_BYTES / (max(cw) * 1024) if cw else 1.0
-    out = [f"FETCH_SIZE scale {f_scale:.4f}, WRITE_SIZE scale {w_scale:.4f} (256 MiB copy calibration)", "",
-           "| kernel | grid | FETCH KiB | WRITE KiB | traffic bytes (scaled) |", "|---|---|---|---|---|"]
-    for key in sorted(set(fetch) | set(write)):
+
+def summarize_pmc(reads_dir, writes_dir):
+    """Markdown table of HBM bytes per dispatch from the L2's memory-side
+    request counters, each request counted at its size: reads 32, 64 or 128
+    bytes (RDREQ_32B, _64B, _128B), writes 64 bytes (WRREQ_64B) or 32 (the
+    rest of WRREQ). No calibration factor: the 256 MiB copy's row checks the
+    arithmetic (its read and write bytes are known), and the requests of
+    unknown size (RDREQ less the three sized counts) are listed."""
+    rd, wr = _load_counters(reads_dir), _load_counters(writes_dir)
+    out = ["| kernel | grid | RDREQ 32B | RDREQ 64B | RDREQ 128B | unsized reads | WRREQ | WRREQ 64B | "
+           "read bytes | write bytes | traffic bytes |", "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for key in sorted(set(rd) | set(wr)):
         k, g = key
         if k.startswith("at::") or "at::native" in k:
             continue
-        f, w = fetch.get(key, 0.0), write.get(key, 0.0)
-        traffic = int(round(f * 1024 * f_scale + w * 1024 * w_scale))
-        out.append(f"| `{k}` | {g} | {f:.1f} | {w:.1f} | {traffic} |")
+        r, w = rd.get(key, {}), wr.get(key, {})
+        r32, r64, r128 = (r.get(c, 0.0) for c in PMC_PASS_READS)
+        rall, wall, w64 = (w.get(c, 0.0) for c in PMC_PASS_WRITES)
+        read_b = 32 * r32 + 64 * r64 + 128 * r128
+        write_b = 64 * w64 + 32 * (wall - w64)
+        unsized = rall - (r32 + r64 + r128)
+        out.append(f"| `{k}` | {g} | {r32:.0f} | {r64:.0f} | {r128:.0f} | {unsized:.0f} | {wall:.0f} | {w64:.0f} | "
+                   f"{read_b:.0f} | {write_b:.0f} | {read_b + write_b:.0f} |")
     return "\n".join(out)
 
 
 def committed_traffic(kernel_prefix, grid):
-    """Scaled HBM bytes per launch of a kernel from the committed PMC summary, or None."""
+    """HBM bytes per launch of a kernel from the committed PMC summary, or None."""
     if not os.path.exists(TRAFFIC_FILE):
         return None
     for line in open(TRAFFIC_FILE):
         cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
-        if len(cells) == 5 and cells[0].startswith(kernel_prefix) and cells[1] == str(grid):
+        if len(cells) == 11 and cells[0].startswith(kernel_prefix) and cells[1] == str(grid):
             try:
-                return int(cells[4])
+                return int(float(cells[10]))
             except ValueError:
                 return None
     return None
@@ -931,8 +942,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly (for counter collection)")
     ap.add_argument("--summarize-trace", metavar="DIR", help="print a table from a rocprofv3 --kernel-trace run")
-    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="print a table from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("READS_DIR", "WRITES_DIR"),
+                    help="print a table from the two rocprofv3 --pmc runs (PMC_PASS_READS, PMC_PASS_WRITES)")
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))

@@ -100,23 +100,33 @@ def test_trace_summary_takes_durations_per_kernel_and_grid(tmp_path):
     assert "| 262144 | 128 | 3 | 5.00 | 5.00 | 4.00 |" in lines[2]
 
 
-def test_pmc_summary_scales_by_the_calibration_copy(tmp_path):
+def test_pmc_summary_counts_each_request_at_its_size(tmp_path):
+    """Bytes = 32/64/128 per sized read request and 64/32 per write request;
+    a 256 MiB copy issued as 128-byte reads and 64-byte writes comes out at
+    256 MiB each way, with no scale factor."""
     copy = bench.COPY_KERNEL
-    kib = bench.COPY_BYTES / 1024
-    fetch = [{"Kernel_Name": copy, "Grid_Size": "131072", "Counter_Name": "FETCH_SIZE", "Counter_Value": str(kib / 2)},
-             {"Kernel_Name": "norm_rows<float>(float*)", "Grid_Size": "256", "Counter_Name": "FETCH_SIZE",
-              "Counter_Value": "100"}]
-    write = [{"Kernel_Name": copy, "Grid_Size": "131072", "Counter_Name": "WRITE_SIZE", "Counter_Value": str(kib)},
-             {"Kernel_Name": "norm_rows<float>(float*)", "Grid_Size": "256", "Counter_Name": "WRITE_SIZE",
-              "Counter_Value": "50"}]
-    (tmp_path / "f").mkdir()
+    n128, n64w = bench.COPY_BYTES // 128, bench.COPY_BYTES // 64
+    r32, r64, r128 = bench.PMC_PASS_READS
+    rall, wall, w64 = bench.PMC_PASS_WRITES
+
+    def rows(kernel, grid, values):
+        return [{"Kernel_Name": kernel, "Grid_Size": grid, "Counter_Name": c, "Counter_Value": str(v)}
+                for c, v in values.items()]
+    reads = rows(copy, "131072", {r32: 0, r64: 0, r128: n128}) + \
+        rows("norm_rows<float>(float*)", "256", {r32: 10, r64: 20, r128: 30})
+    writes = rows(copy, "131072", {rall: n128, wall: n64w, w64: n64w}) + \
+        rows("norm_rows<float>(float*)", "256", {rall: 61, wall: 7, w64: 5})
+    (tmp_path / "r").mkdir()
     (tmp_path / "w").mkdir()
-    _write_csv(tmp_path / "f" / "run_counter_collection.csv", list(fetch[0]), fetch)
-    _write_csv(tmp_path / "w" / "run_counter_collection.csv", list(write[0]), write)
-    table = bench.summarize_pmc(str(tmp_path / "f"), str(tmp_path / "w"))
-    assert table.startswith("FETCH_SIZE scale 2.0000, WRITE_SIZE scale 1.0000")
-    row = [ln for ln in table.splitlines() if "norm_rows" in ln]
-    assert row and row[0].endswith(f"| {2 * 100 * 1024 + 50 * 1024} |")
+    _write_csv(tmp_path / "r" / "run_counter_collection.csv", list(reads[0]), reads)
+    _write_csv(tmp_path / "w" / "run_counter_collection.csv", list(writes[0]), writes)
+    table = bench.summarize_pmc(str(tmp_path / "r"), str(tmp_path / "w"))
+    copy_row = [ln for ln in table.splitlines() if copy in ln][0]
+    assert copy_row.endswith(f"| {bench.COPY_BYTES} | {bench.COPY_BYTES} | {2 * bench.COPY_BYTES} |")
+    row = [ln for ln in table.splitlines() if "norm_rows" in ln][0]
+    read_b, write_b = 32 * 10 + 64 * 20 + 128 * 30, 64 * 5 + 32 * 2
+    assert row.endswith(f"| {read_b} | {write_b} | {read_b + write_b} |")
+    assert "| 1 |" in row  # one read request of unknown size (61 - 60)
 
 
 def test_committed_traffic_reads_the_profile():
