@@ -137,6 +137,7 @@ _SIGNATURES = {
     "uocr_rocm_softmax_rows": ([_vp, _vp, _i64, _i64], _int),
     "uocr_rocm_scale_add_mask": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_gemv_bf16": ([_vp, _vp, _i64, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_linear": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_append_step": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_append_step_bf16": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_attend_step_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
@@ -462,6 +463,22 @@ def gemv_bf16(x, w, y, bias=None, stream=None):
     if x.numel() != k or y.numel() != n or (bias is not None and bias.numel() != n):
         raise ValueError("gemv_bf16 shapes: x [k], w [n, k], y [n], bias [n]")
     _op("uocr_rocm_gemv_bf16", stream, _ptr(x), k, _ptr(w), n, _f32_param(bias), _ptr(y))
+
+
+def linear(x, w, y, bias=None, stream=None):
+    """y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]) on the matrix cores,
+    fp32 accumulation: x float32 [m, k], w bfloat16 [n, k], y float32 [m, n].
+    Reference: linear, src/backend/cuda/ops.h:14-17."""
+    torch = _torch()
+    if w.dtype != torch.bfloat16 or x.dtype != torch.float32 or y.dtype != torch.float32:
+        raise ValueError("linear takes float32 x and y and bfloat16 w")
+    n, k = w.shape
+    m = x.numel() // k if k else 0
+    if x.numel() != m * k or y.numel() != m * n or (bias is not None and bias.numel() != n):
+        raise ValueError("linear shapes: x [m, k], w [n, k], y [m, n], bias [n]")
+    if not (x.is_contiguous() and w.is_contiguous() and y.is_contiguous()):
+        raise ValueError("linear takes contiguous x, w and y")
+    _op("uocr_rocm_linear", stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y))
 
 
 def append_step(cache, row, state, capacity=None, stream=None):

@@ -140,6 +140,11 @@ void gemv_bf16(const Context& ctx, const float* x, std::int64_t k, const std::ui
   check(uocr_rocm_gemv_bf16(ctx.stream(), x, k, w, n, bias, y));
 }
 
+void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
+            std::int64_t n, const float* bias, float* y) {
+  check(uocr_rocm_linear(ctx.stream(), x, m, k, w_bf16, n, bias, y));
+}
+
 void add_rms_norm_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out, const float* w_norm,
                             float eps, float* h_out, std::int64_t k, const std::uint16_t* w, std::int64_t n,
                             const float* bias, float* y) {

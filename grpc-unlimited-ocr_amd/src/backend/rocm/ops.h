@@ -115,6 +115,10 @@ void scale_mask_softmax_rows(const Context& ctx, float* x, float scale, const fl
 // y[n] = bf16(x) . w[n, :] (+ bias[n]); x fp32 [k] (k <= 12288), w bf16 [n, k].
 void gemv_bf16(const Context& ctx, const float* x, std::int64_t k, const std::uint16_t* w, std::int64_t n,
                const float* bias, float* y);
+// y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]) on the matrix cores, fp32
+// accumulation (m == 1: the GEMV); the reference's linear.
+void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
+            std::int64_t n, const float* bias, float* y);
 
 // Fused decode projections (new): add + RMSNorm as the GEMV's prologue,
 // optionally a gate/up pair with a SwiGLU epilogue. delta, x_out, w_norm

@@ -305,6 +305,17 @@ UOCR_ROCM_API int uocr_rocm_scale_add_mask(void* stream, float* x, float scale, 
 UOCR_ROCM_API int uocr_rocm_scale_mask_softmax_rows(void* stream, float* x, float scale, const float* mask,
                                                     int64_t batch, int64_t rows, int64_t cols);
 
+/* ---- prefill projections ------------------------------------------------------- */
+
+/* y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]): x fp32 row-major, rounded
+ * to bf16 (nearest even) for the product, w bf16 row-major, fp32
+ * accumulation on the matrix cores, fp32 y; the bias (may be null) is added
+ * to each finished sum. m == 1 (k <= 12288) goes through uocr_rocm_gemv_bf16.
+ * k is a multiple of 8; x and w 16-byte aligned. Replaces linear
+ * (src/backend/cuda/ops.h:14-17). */
+UOCR_ROCM_API int uocr_rocm_linear(void* stream, const float* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
+                                   const float* bias, float* y);
+
 /* ---- decode-step neighbours ---------------------------------------------------- */
 
 /* y[n] = bf16(x) . w[n, :] (+ bias[n]): x fp32 [k] rounded to bf16 (nearest

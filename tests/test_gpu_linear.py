@@ -1,0 +1,94 @@
+"""GPU parity for the prefill projection `linear` (csrc/gemm.hip, bf16 matrix
+cores) through the C ABI, against the oracle's linear on the bf16-rounded
+input (the reference's cuda::linear, src/backend/cuda/ops.h:14-17: x rounded
+to bf16, fp32 accumulation, bias added to the finished sum).
+
+  * small and ragged shapes (m, n not multiples of the 128 x 128 tile; k not
+    a multiple of the 64-wide k step) against the oracle on every element;
+  * the decoder's prefill shapes (S rows of hidden 1280 through q/k/v/router
+    [4096], gate/up [2 x 6848] and down [1280 <- 6848]) against the oracle on
+    a sample of rows (rows are independent, so a sampled row is checked
+    exactly as in a full run) and, in full, against torch's fp32 product of
+    the same bf16-rounded operands;
+  * m == 1 goes through the GEMV, bias or none, and bad shapes are refused.
+
+Tolerance: 1e-5 of the largest |y| (fp32 accumulation in another order)."""
+
+import numpy as np
+import pytest
+
+import oracle
+from parity import assert_f32_close, dev_bf16, dev_f32, host_f32, normal
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device(backend):
+    if not torch.cuda.is_available() or backend.device_count() == 0:
+        pytest.skip("no HIP device")
+    torch.cuda.set_device(0)
+    yield
+    torch.cuda.synchronize()
+
+
+def bf16(a):
+    return oracle.f32_to_bf16(a)
+
+
+@pytest.mark.parametrize("m,k,n,with_bias", [(2, 8, 3, False), (37, 200, 70, True), (128, 128, 128, False),
+                                             (129, 64, 257, True), (5, 1288, 31, False), (300, 1280, 520, True),
+                                             (64, 6848, 96, False)])
+def test_linear_against_the_oracle(backend, m, k, n, with_bias):
+    x = normal(400 + m, (m, k))
+    wb = bf16(0.05 * normal(401 + n, (n, k)))
+    bias = normal(402, n) if with_bias else None
+    want = oracle.linear(oracle.bf16_round(x), oracle.bf16_to_f32(wb), bias)
+    y = torch.full((m, n), float("nan"), device="cuda")
+    backend.linear(dev_f32(x), dev_bf16(wb), y, None if bias is None else dev_f32(bias))
+    assert_f32_close(host_f32(y), want, 1e-5, f"linear m={m} k={k} n={n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(4096, 1280, 4096), (2048, 1280, 13696), (2048, 6848, 1280)])
+def test_linear_model_shapes(backend, m, k, n):
+    g = torch.Generator(device="cuda").manual_seed(m + n)
+    x = torch.randn(m, k, device="cuda", generator=g)
+    w = (0.03 * torch.randn(n, k, device="cuda", generator=g)).to(torch.bfloat16)
+    y = torch.empty(m, n, device="cuda")
+    backend.linear(x, w, y)
+    torch.cuda.synchronize()
+    # sampled rows against the oracle, exactly as a full run would check them
+    rows = np.array([0, 1, m // 2, m - 2, m - 1] + list(np.random.default_rng(403).integers(0, m, 3)))
+    xs = x[torch.from_numpy(rows).cuda()].cpu().numpy()
+    wh = oracle.bf16_to_f32(w.view(torch.int16).cpu().numpy().view(np.uint16))
+    want = oracle.linear(oracle.bf16_round(xs), wh)
+    got = y.cpu().numpy()[rows]
+    assert_f32_close(got, want, 1e-5, f"linear sampled rows m={m} k={k} n={n}")
+    # every element against torch's fp32 product of the same rounded operands
+    ref = torch.matmul(x.to(torch.bfloat16).float(), w.float().t().contiguous())
+    assert_f32_close(y.cpu().numpy(), ref.cpu().numpy(), 1e-5, f"linear full m={m} k={k} n={n}")
+
+
+def test_linear_one_row_is_the_gemv(backend):
+    k, n = 1280, 300
+    x = normal(410, (1, k))
+    wb = bf16(0.05 * normal(411, (n, k)))
+    bias = normal(412, n)
+    y1, y2 = torch.empty(1, n, device="cuda"), torch.empty(n, device="cuda")
+    backend.linear(dev_f32(x), dev_bf16(wb), y1, dev_f32(bias))
+    backend.gemv_bf16(dev_f32(x[0]), dev_bf16(wb), y2, dev_f32(bias))
+    assert np.array_equal(host_f32(y1)[0].view(np.uint32), host_f32(y2).view(np.uint32))
+
+
+def test_linear_rejects_bad_shapes(backend):
+    x = torch.zeros(4, 12, device="cuda")
+    w = torch.zeros(3, 12, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(4, 3, device="cuda")
+    with pytest.raises(ValueError):  # k not a multiple of 8
+        backend.linear(x, w, y)
+    x = torch.zeros(4, 17, device="cuda")[:, 1:].contiguous()
+    w = torch.zeros(3, 16, dtype=torch.bfloat16, device="cuda")
+    backend.linear(x, w, y)  # contiguous copies are aligned
+    assert torch.count_nonzero(y) == 0
