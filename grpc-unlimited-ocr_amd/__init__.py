@@ -138,6 +138,11 @@ _SIGNATURES = {
     "uocr_rocm_scale_add_mask": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_gemv_bf16": ([_vp, _vp, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_linear": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_gemm_nt": ([_vp, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64],
+                          _int),
+    "uocr_rocm_gemm_nn": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64], _int),
+    "uocr_rocm_gather_rows": ([_vp, _vp, _vp, _i64, _i64, _vp], _int),
+    "uocr_rocm_scatter_add_rows": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64], _int),
     "uocr_rocm_append_step": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_append_step_bf16": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_attend_step_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
@@ -479,6 +484,34 @@ def linear(x, w, y, bias=None, stream=None):
     if not (x.is_contiguous() and w.is_contiguous() and y.is_contiguous()):
         raise ValueError("linear takes contiguous x, w and y")
     _op("uocr_rocm_linear", stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y))
+
+
+def gemm_nt(m, n, k, alpha, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch=1, stream=None):
+    """c[s] = alpha a[s] . b[s]^T over `batch` slices (fp32 tensors, leading
+    dimensions and slice strides in elements). Reference: gemm_nt,
+    src/backend/cuda/ops.h:19-25."""
+    _op("uocr_rocm_gemm_nt", stream, m, n, k, alpha, _ptr(a), lda, stride_a, _ptr(b), ldb, stride_b, _ptr(c), ldc,
+        stride_c, batch)
+
+
+def gemm_nn(m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch=1, stream=None):
+    """c[s] = a[s] . b[s] over `batch` slices (fp32). Reference: gemm_nn,
+    src/backend/cuda/ops.h:26-27."""
+    _op("uocr_rocm_gemm_nn", stream, m, n, k, _ptr(a), lda, stride_a, _ptr(b), ldb, stride_b, _ptr(c), ldc, stride_c,
+        batch)
+
+
+def gather_rows(src, index, dst, stream=None):
+    """dst[i] = src[index[i]] (fp32 rows). Reference: gather_rows, ops.h:56-57."""
+    rows, cols = index.numel(), src.shape[-1]
+    _op("uocr_rocm_gather_rows", stream, _ptr(src), _ptr(index), rows, cols, _ptr(dst))
+
+
+def scatter_add_rows(dst, index, weight, src, stream=None):
+    """dst[index[i]] += weight[i] * src[i], i in order. Reference:
+    scatter_add_rows, ops.h:58-59."""
+    rows, cols = index.numel(), dst.shape[-1]
+    _op("uocr_rocm_scatter_add_rows", stream, _ptr(dst), _ptr(index), _ptr(weight), _ptr(src), rows, cols)
 
 
 def append_step(cache, row, state, capacity=None, stream=None):

@@ -140,6 +140,28 @@ void gemv_bf16(const Context& ctx, const float* x, std::int64_t k, const std::ui
   check(uocr_rocm_gemv_bf16(ctx.stream(), x, k, w, n, bias, y));
 }
 
+void gemm_nt(const Context& ctx, std::int64_t m, std::int64_t n, std::int64_t k, float alpha, const float* a,
+             std::int64_t lda, std::int64_t stride_a, const float* b, std::int64_t ldb, std::int64_t stride_b, float* c,
+             std::int64_t ldc, std::int64_t stride_c, std::int64_t batch) {
+  check(uocr_rocm_gemm_nt(ctx.stream(), m, n, k, alpha, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch));
+}
+
+void gemm_nn(const Context& ctx, std::int64_t m, std::int64_t n, std::int64_t k, const float* a, std::int64_t lda,
+             std::int64_t stride_a, const float* b, std::int64_t ldb, std::int64_t stride_b, float* c, std::int64_t ldc,
+             std::int64_t stride_c, std::int64_t batch) {
+  check(uocr_rocm_gemm_nn(ctx.stream(), m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch));
+}
+
+void gather_rows(const Context& ctx, const float* src, const std::int64_t* index, std::int64_t rows, std::int64_t cols,
+                 float* dst) {
+  check(uocr_rocm_gather_rows(ctx.stream(), src, index, rows, cols, dst));
+}
+
+void scatter_add_rows(const Context& ctx, float* dst, const std::int64_t* index, const float* weight, const float* src,
+                      std::int64_t rows, std::int64_t cols) {
+  check(uocr_rocm_scatter_add_rows(ctx.stream(), dst, index, weight, src, rows, cols));
+}
+
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
             std::int64_t n, const float* bias, float* y) {
   check(uocr_rocm_linear(ctx.stream(), x, m, k, w_bf16, n, bias, y));

@@ -115,6 +115,19 @@ void scale_mask_softmax_rows(const Context& ctx, float* x, float scale, const fl
 // y[n] = bf16(x) . w[n, :] (+ bias[n]); x fp32 [k] (k <= 12288), w bf16 [n, k].
 void gemv_bf16(const Context& ctx, const float* x, std::int64_t k, const std::uint16_t* w, std::int64_t n,
                const float* bias, float* y);
+// fp32 products batched over `batch` slices stride_* elements apart:
+// c = alpha a[m, k] b[n, k]^T (gemm_nt), c = a[m, k] b[k, n] (gemm_nn).
+void gemm_nt(const Context& ctx, std::int64_t m, std::int64_t n, std::int64_t k, float alpha, const float* a,
+             std::int64_t lda, std::int64_t stride_a, const float* b, std::int64_t ldb, std::int64_t stride_b, float* c,
+             std::int64_t ldc, std::int64_t stride_c, std::int64_t batch);
+void gemm_nn(const Context& ctx, std::int64_t m, std::int64_t n, std::int64_t k, const float* a, std::int64_t lda,
+             std::int64_t stride_a, const float* b, std::int64_t ldb, std::int64_t stride_b, float* c, std::int64_t ldc,
+             std::int64_t stride_c, std::int64_t batch);
+// Rows by index: dst[i] = src[index[i]]; dst[index[i]] += weight[i] * src[i], i in order.
+void gather_rows(const Context& ctx, const float* src, const std::int64_t* index, std::int64_t rows, std::int64_t cols,
+                 float* dst);
+void scatter_add_rows(const Context& ctx, float* dst, const std::int64_t* index, const float* weight, const float* src,
+                      std::int64_t rows, std::int64_t cols);
 // y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]) on the matrix cores, fp32
 // accumulation (m == 1: the GEMV); the reference's linear.
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,

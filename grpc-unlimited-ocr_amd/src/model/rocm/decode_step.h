@@ -132,6 +132,19 @@ class DecodeStep {
   // the step; none by default.
   void set_prompt_blocks(const std::vector<std::int64_t>& min_page, const std::vector<std::int64_t>& max_page);
 
+  // The prompt rows x [rows, hidden] (host fp32 embeddings) at positions
+  // length() .. length() + rows - 1 through every layer, writing the caches,
+  // and the logits of the last row (CudaDecoder::run, cuda_decoder.cpp:
+  // 248-286; the prompt blocks' pages come from set_prompt_blocks): the
+  // projections on the matrix cores, per row the router's block scores and
+  // key mask, the masked attention as fp32 products and a row softmax, the
+  // dense or mixture-of-experts MLP (the experts' rows gathered by the
+  // device's top-k, their outputs scattered back in expert order). coords
+  // holds one rotary coordinate per row; query_pages one page per row, or
+  // is empty (every row unconfined). Needs the fp32 cache.
+  std::vector<float> prefill(const std::vector<float>& x, const std::vector<RopeCoord>& coords,
+                             const std::vector<std::int64_t>& query_pages = {});
+
   // Feeds `token` at the next position (length() before the call), rotated
   // at `coord`, its attention routed within query_page's blocks (-1: any
   // block), and returns the logits [vocab] (CudaDecoder::step).

@@ -316,6 +316,27 @@ UOCR_ROCM_API int uocr_rocm_scale_mask_softmax_rows(void* stream, float* x, floa
 UOCR_ROCM_API int uocr_rocm_linear(void* stream, const float* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
                                    const float* bias, float* y);
 
+/* c[s] = alpha a[s] . b[s]^T (gemm_nt: a [m, k], b [n, k]) or c[s] = a[s] . b[s]
+ * (gemm_nn: a [m, k], b [k, n]), fp32, row-major with leading dimensions
+ * lda / ldb / ldc, for `batch` slices s whose operands sit stride_a /
+ * stride_b / stride_c elements apart. Replaces gemm_nt and gemm_nn
+ * (src/backend/cuda/ops.h:19-27). */
+UOCR_ROCM_API int uocr_rocm_gemm_nt(void* stream, int64_t m, int64_t n, int64_t k, float alpha, const float* a,
+                                    int64_t lda, int64_t stride_a, const float* b, int64_t ldb, int64_t stride_b,
+                                    float* c, int64_t ldc, int64_t stride_c, int64_t batch);
+UOCR_ROCM_API int uocr_rocm_gemm_nn(void* stream, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda,
+                                    int64_t stride_a, const float* b, int64_t ldb, int64_t stride_b, float* c,
+                                    int64_t ldc, int64_t stride_c, int64_t batch);
+
+/* dst[i] = src[index[i]] for rows [cols] (fp32); and dst[index[i]] +=
+ * weight[i] * src[i] for i in order (an index may repeat). Indices are
+ * trusted, as in the reference. Replace gather_rows and scatter_add_rows
+ * (src/backend/cuda/ops.h:56-60). */
+UOCR_ROCM_API int uocr_rocm_gather_rows(void* stream, const float* src, const int64_t* index, int64_t rows,
+                                        int64_t cols, float* dst);
+UOCR_ROCM_API int uocr_rocm_scatter_add_rows(void* stream, float* dst, const int64_t* index, const float* weight,
+                                             const float* src, int64_t rows, int64_t cols);
+
 /* ---- decode-step neighbours ---------------------------------------------------- */
 
 /* y[n] = bf16(x) . w[n, :] (+ bias[n]): x fp32 [k] rounded to bf16 (nearest

@@ -745,6 +745,283 @@ void decode_step(const ro::Context& ctx, bool bf16_cache) {
   require(step.length() == 0, "decode step reset");
 }
 
+// The oracle's decoder for prefill_then_decode: the reference decoder's
+// arithmetic (src/model/decoder.cpp through the oracle's ops) with the GEMM
+// inputs rounded to bf16 as the device's projections take them, caches of
+// its own, the router's selection from its own scores.
+struct OracleDecoder {
+  ro::DecoderDims d;
+  struct Layer {
+    std::vector<float> in, proj, rqn, rkn, cls, o, post, gate, up, down;
+    std::vector<float> router, gstack, ustack, dstack, sg, su, sd;
+    bool moe = false;
+  };
+  std::vector<Layer> layers;
+  std::vector<float> final_norm, lm;
+  std::int64_t ffn = 0, experts = 0, top_k = 0, expert_ffn = 0, shared_ffn = 0;
+  std::vector<float> inv_tok, inv_page;
+  std::vector<std::vector<float>> kc, vc, rkc;
+  std::vector<std::int64_t> min_page, max_page;
+  std::int64_t length = 0;
+
+  static std::vector<float> linear(const std::vector<float>& x, std::int64_t rows, const std::vector<float>& w,
+                                   const float* w_at, std::int64_t n, bool round = true) {
+    const std::int64_t k = static_cast<std::int64_t>(x.size()) / rows;
+    std::vector<float> y(static_cast<std::size_t>(rows * n));
+    const auto xin = round ? bf16_rounded(x) : x;
+    orc_linear(xin.data(), rows, k, w_at != nullptr ? w_at : w.data(), n, nullptr, y.data());
+    return y;
+  }
+  std::vector<float> swiglu_mlp(const std::vector<float>& h, std::int64_t rows, const float* g, const float* u,
+                                const float* dn, std::int64_t f) const {
+    auto gg = linear(h, rows, {}, g, f);
+    const auto uu = linear(h, rows, {}, u, f);
+    orc_silu(gg.data(), rows * f);
+    orc_mul_into(gg.data(), uu.data(), rows * f);
+    return linear(gg, rows, {}, dn, d.hidden);
+  }
+  // Rows x [rows, hidden] at positions length..; logits of the last row.
+  // Routed experts are added in expert order for a prompt pass (the
+  // reference's scatter loop) and in top-k rank order for one decode row
+  // (expert_ffn_one).
+  std::vector<float> forward(std::vector<float> x, const std::vector<ro::RopeCoord>& coords,
+                             const std::vector<std::int64_t>& qp, bool rank_order) {
+    const std::int64_t rows = static_cast<std::int64_t>(coords.size()), H = d.hidden, W = d.heads * d.head_dim;
+    const std::int64_t D = d.index_dim, hd = d.head_dim, P = 3 * W + 2 * D, first = length, keys = first + rows;
+    const std::int64_t bs = d.router.block_size, nblk = (keys + bs - 1) / bs, n_tok = hd / 2 - d.page_pairs;
+    const auto& rp = d.router;
+    std::vector<std::int64_t> tok(rows), page(rows), pos(rows);
+    for (std::int64_t r = 0; r < rows; ++r) {
+      tok[r] = coords[r].tok;
+      page[r] = coords[r].page;
+      pos[r] = first + r;
+    }
+    const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+    std::vector<float> h;
+    for (std::size_t li = 0; li < layers.size(); ++li) {
+      const Layer& l = layers[li];
+      h = x;
+      orc_rms_norm(h.data(), l.in.data(), rows, H, d.eps);
+      const auto proj = linear(h, rows, l.proj, nullptr, P);
+      std::vector<float> q(rows * W), k(rows * W), v(rows * W), rq(rows * D), rk(rows * D);
+      for (std::int64_t r = 0; r < rows; ++r) {
+        const float* pr = proj.data() + r * P;
+        std::copy(pr, pr + W, q.begin() + r * W);
+        std::copy(pr + W, pr + 2 * W, k.begin() + r * W);
+        std::copy(pr + 2 * W, pr + 3 * W, v.begin() + r * W);
+        std::copy(pr + 3 * W, pr + 3 * W + D, rq.begin() + r * D);
+        std::copy(pr + 3 * W + D, pr + P, rk.begin() + r * D);
+      }
+      orc_router_norm(rq.data(), l.rqn.data(), rows, D, d.eps);
+      orc_router_norm(rk.data(), l.rkn.data(), rows, D, d.eps);
+      orc_rope_apply(q.data(), rows, d.heads, hd, tok.data(), page.data(), inv_tok.data(), n_tok, inv_page.data(),
+                     d.page_pairs, d.page_mod, 0, 0);
+      orc_rope_apply(k.data(), rows, d.heads, hd, tok.data(), page.data(), inv_tok.data(), n_tok, inv_page.data(),
+                     d.page_pairs, d.page_mod, 0, 0);
+      orc_rope_apply(rq.data(), rows, 1, D, tok.data(), page.data(), inv_tok.data(), n_tok, inv_page.data(),
+                     d.page_pairs, d.page_mod, 0, 0);
+      orc_rope_apply(rk.data(), rows, 1, D, tok.data(), page.data(), inv_tok.data(), n_tok, inv_page.data(),
+                     d.page_pairs, d.page_mod, 0, 0);
+      std::copy(k.begin(), k.end(), kc[li].begin() + first * W);
+      std::copy(v.begin(), v.end(), vc[li].begin() + first * W);
+      std::copy(rk.begin(), rk.end(), rkc[li].begin() + first * D);
+      std::vector<float> summaries(nblk * D), z(rows * nblk);
+      orc_block_summaries(rkc[li].data(), keys, D, l.cls.data(), bs, summaries.data());
+      orc_block_scores(rq.data(), rows, summaries.data(), nblk, D, pos.data(), bs, rp.local_blocks, z.data());
+      std::vector<float> attn(rows * W);
+      for (std::int64_t r = 0; r < rows; ++r) {
+        std::vector<std::uint8_t> cand(nblk);
+        const int restricted = orc_page_candidates(min_page.data(), max_page.data(),
+                                                   static_cast<std::int64_t>(min_page.size()), qp[r], nblk,
+                                                   cand.data());
+        std::vector<std::int64_t> blk(rp.top_k + 1);
+        std::vector<float> bias(rp.top_k + 1), mask(keys);
+        std::vector<std::uint8_t> valid(rp.top_k + 1);
+        const std::int64_t width = orc_select_blocks(z.data() + r * nblk, 1, nblk, restricted ? cand.data() : nullptr,
+                                                     rp.top_m, rp.top_k, rp.idx_scale, rp.floor, rp.sigma, blk.data(),
+                                                     bias.data(), valid.data());
+        orc_key_mask(blk.data(), bias.data(), valid.data(), width, 1, pos[r], keys, bs, rp.local_blocks, mask.data());
+        orc_attention_one(q.data() + r * W, kc[li].data(), vc[li].data(), keys, W, d.heads, hd, mask.data(), scale,
+                          attn.data() + r * W);
+      }
+      const auto o = linear(attn, rows, l.o, nullptr, H);
+      orc_add_into(x.data(), o.data(), rows * H);
+      h = x;
+      orc_rms_norm(h.data(), l.post.data(), rows, H, d.eps);
+      std::vector<float> delta;
+      if (!l.moe) {
+        delta = swiglu_mlp(h, rows, l.gate.data(), l.up.data(), l.down.data(), ffn);
+      } else {
+        delta = swiglu_mlp(h, rows, l.sg.data(), l.su.data(), l.sd.data(), shared_ffn);
+        const auto logits = linear(h, rows, l.router, nullptr, experts, false);
+        std::vector<std::int64_t> ids(rows * top_k);
+        std::vector<float> wts(rows * top_k);
+        orc_expert_topk(logits.data(), rows, experts, top_k, ids.data(), wts.data());
+        for (std::int64_t r = 0; r < rows; ++r) {
+          std::vector<std::int64_t> order(top_k);
+          for (std::int64_t j = 0; j < top_k; ++j) order[j] = j;
+          if (!rank_order) {
+            std::sort(order.begin(), order.end(),
+                      [&](std::int64_t a, std::int64_t b) { return ids[r * top_k + a] < ids[r * top_k + b]; });
+          }
+          const std::vector<float> hr(h.begin() + r * H, h.begin() + (r + 1) * H);
+          std::vector<float> routed(H, 0.0f);
+          for (const std::int64_t j : order) {
+            const std::int64_t e = ids[r * top_k + j];
+            const auto y = swiglu_mlp(hr, 1, l.gstack.data() + e * expert_ffn * H, l.ustack.data() + e * expert_ffn * H,
+                                      l.dstack.data() + e * H * expert_ffn, expert_ffn);
+            for (std::int64_t c = 0; c < H; ++c) routed[c] += wts[r * top_k + j] * y[c];
+          }
+          orc_add_into(delta.data() + r * H, routed.data(), H);
+        }
+      }
+      orc_add_into(x.data(), delta.data(), rows * H);
+    }
+    std::vector<float> last(x.end() - H, x.end());
+    orc_rms_norm(last.data(), final_norm.data(), 1, H, d.eps);
+    length = keys;
+    return linear(last, 1, lm, nullptr, d.vocab);
+  }
+};
+
+void prefill_then_decode(const ro::Context& ctx) {
+  // A prompt of 48 rows (8 text rows, then two image pages of 20 rows) run
+  // through DecodeStep::prefill, then 40 decode steps on the caches it
+  // wrote, the logits of each against the oracle's decoder on the same
+  // weights (the shape of the reference's tests/cuda_decoder_test.cpp:
+  // 99-137, which holds both to 2e-2; here the prefill is held to 1e-4, each
+  // step to 1e-3 and the median step to 1e-5: the device and the oracle make
+  // the same routing choices, so only fp32 summation order separates them).
+  // Router as the reference test sets it: block 4, one local block,
+  // idx_scale 4.
+  ro::DecoderDims d;
+  d.hidden = 64;
+  d.heads = 2;
+  d.head_dim = 16;
+  d.index_dim = 16;
+  d.vocab = 300;
+  d.capacity = 128;
+  d.router.block_size = 4;
+  d.router.local_blocks = 1;
+  d.router.idx_scale = 4.0f;
+  const std::int64_t H = d.hidden, W = d.heads * d.head_dim, D = d.index_dim, V = d.vocab, P = 3 * W + 2 * D;
+  OracleDecoder od;
+  od.d = d;
+  od.ffn = 64;
+  od.experts = 8;
+  od.top_k = 3;
+  od.expert_ffn = 32;
+  od.shared_ffn = 32;
+  auto norm_w = [&](std::int64_t n) {
+    auto w = random(static_cast<std::size_t>(n), 0.05f);
+    for (float& v : w) v += 1.0f;
+    return w;
+  };
+  auto bw = [&](std::int64_t n, float sc) { return bf16_rounded(random(static_cast<std::size_t>(n), sc)); };
+  const auto embed = bw(V * H, 0.5f);
+  od.lm = bw(V * H, 0.1f);
+  od.final_norm = norm_w(H);
+  od.layers.resize(2);
+  for (int li = 0; li < 2; ++li) {
+    auto& l = od.layers[li];
+    l.in = norm_w(H);
+    l.proj = bw(P * H, 0.15f);
+    l.rqn = random(D, 0.1f);
+    l.rkn = random(D, 0.1f);
+    l.cls = random(D, 1.0f);
+    l.o = bw(H * W, 0.15f);
+    l.post = norm_w(H);
+    l.moe = li == 1;
+    if (!l.moe) {
+      l.gate = bw(od.ffn * H, 0.15f);
+      l.up = bw(od.ffn * H, 0.15f);
+      l.down = bw(H * od.ffn, 0.15f);
+    } else {
+      l.router = random(od.experts * H, 0.2f);
+      l.gstack = bw(od.experts * od.expert_ffn * H, 0.15f);
+      l.ustack = bw(od.experts * od.expert_ffn * H, 0.15f);
+      l.dstack = bw(od.experts * H * od.expert_ffn, 0.15f);
+      l.sg = bw(od.shared_ffn * H, 0.15f);
+      l.su = bw(od.shared_ffn * H, 0.15f);
+      l.sd = bw(H * od.shared_ffn, 0.15f);
+    }
+  }
+  std::vector<ro::Array> keep;
+  auto dev = [&](const std::vector<float>& v, ro::DType t) {
+    keep.push_back(up(ctx, v, t));
+    return keep.back().data();
+  };
+  auto b16 = [&](const std::vector<float>& v) { return static_cast<const std::uint16_t*>(dev(v, ro::DType::kBF16)); };
+  auto f32 = [&](const std::vector<float>& v) { return static_cast<const float*>(dev(v, ro::DType::kF32)); };
+  ro::MoeWeights moe;
+  std::vector<ro::LayerWeights> lw(2);
+  for (int li = 0; li < 2; ++li) {
+    const auto& l = od.layers[li];
+    lw[li].input_norm = f32(l.in);
+    lw[li].qkv = b16(l.proj);
+    lw[li].router_q_norm = f32(l.rqn);
+    lw[li].router_k_norm = f32(l.rkn);
+    lw[li].head_cls = f32(l.cls);
+    lw[li].o = b16(l.o);
+    lw[li].post_norm = f32(l.post);
+    if (!l.moe) {
+      lw[li].gate = b16(l.gate);
+      lw[li].up = b16(l.up);
+      lw[li].down = b16(l.down);
+      lw[li].ffn = od.ffn;
+    } else {
+      moe = ro::MoeWeights{f32(l.router), b16(l.ustack), b16(l.gstack), b16(l.dstack), od.experts, od.top_k,
+                           od.expert_ffn, b16(l.sg), b16(l.su), b16(l.sd), od.shared_ffn};
+      lw[li].moe = &moe;
+    }
+  }
+  ro::DecodeStep step(ctx, d, b16(embed), lw, f32(od.final_norm), b16(od.lm));
+  // prompt: 8 text rows, then pages 0 and 1 of 20 image rows each
+  const std::int64_t rows = 48;
+  std::vector<ro::RopeCoord> coords(rows);
+  std::vector<std::int64_t> qp(rows);
+  for (std::int64_t r = 0; r < rows; ++r) {
+    const bool image = r >= 8;
+    const std::int64_t pg = image ? (r - 8) / 20 : -1;
+    coords[r] = image ? ro::RopeCoord{8 + (r - 8) % 20, pg} : ro::RopeCoord{r, 0};
+    qp[r] = pg;
+  }
+  od.min_page.assign(12, -1);
+  for (std::int64_t b = 2; b < 12; ++b) od.min_page[b] = (4 * b - 8) / 20;
+  od.max_page = od.min_page;
+  step.set_prompt_blocks(od.min_page, od.max_page);
+  od.inv_tok = rope_inv(d.head_dim / 2 - d.page_pairs, d.rope_theta);
+  od.inv_page = rope_inv(d.page_pairs, d.page_theta);
+  od.kc.assign(2, std::vector<float>(d.capacity * W, 0.0f));
+  od.vc = od.kc;
+  od.rkc.assign(2, std::vector<float>(d.capacity * D, 0.0f));
+  const auto x = random(rows * H, 0.5f);
+  const auto got = step.prefill(x, coords, qp);
+  const auto want = od.forward(x, coords, qp, false);
+  expect("prefill logits (48 rows)", max_rel(got, want), 1e-4);
+  require(step.length() == rows, "prefill length");
+  std::vector<double> errs;
+  for (std::int64_t t = 0; t < 40; ++t) {
+    const std::int64_t token = static_cast<std::int64_t>(rng() % static_cast<unsigned>(V));
+    const ro::RopeCoord c{28 + t, 2 + t / 10};
+    const std::int64_t page = t < 20 ? 0 : 1;
+    const auto g = step.step(token, c, page);
+    const std::vector<float> row(embed.begin() + token * H, embed.begin() + (token + 1) * H);
+    const auto w = od.forward(row, {c}, {page}, true);
+    errs.push_back(max_rel(g, w));
+    if (errs.back() > 1e-3) expect(("decode after prefill, step " + std::to_string(t)).c_str(), errs.back(), 1e-3);
+  }
+  std::sort(errs.begin(), errs.end());
+  expect("decode after prefill worst", errs.back(), 1e-3);
+  expect("decode after prefill median", errs[errs.size() / 2], 1e-5);
+  {  // the bf16 cache has no prefill
+    auto bd = d;
+    bd.bf16_cache = true;
+    ro::DecodeStep s2(ctx, bd, b16(embed), lw, f32(od.final_norm), b16(od.lm));
+    require_throws_invalid([&] { s2.prefill(x, coords, qp); }, "prefill over a bf16 cache");
+  }
+}
+
 void step_ops(const ro::Context& ctx) {
   {  // softmax with a masked entry and a fully masked row
     const std::int64_t rows = 5, cols = 300;
@@ -831,6 +1108,7 @@ int main() {
     fused_decode_layer(ctx);
     decode_step(ctx, true);
     decode_step(ctx, false);
+    prefill_then_decode(ctx);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());
