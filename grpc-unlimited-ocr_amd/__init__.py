@@ -138,6 +138,8 @@ _SIGNATURES = {
     "uocr_rocm_scale_add_mask": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_gemv_bf16": ([_vp, _vp, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_linear": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_linear_bf16x": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_round_bf16": ([_vp, _vp, _i64, _vp], _int),
     "uocr_rocm_gemm_nt": ([_vp, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64],
                           _int),
     "uocr_rocm_gemm_nn": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64], _int),
@@ -475,15 +477,23 @@ def linear(x, w, y, bias=None, stream=None):
     fp32 accumulation: x float32 [m, k], w bfloat16 [n, k], y float32 [m, n].
     Reference: linear, src/backend/cuda/ops.h:14-17."""
     torch = _torch()
-    if w.dtype != torch.bfloat16 or x.dtype != torch.float32 or y.dtype != torch.float32:
-        raise ValueError("linear takes float32 x and y and bfloat16 w")
+    if w.dtype != torch.bfloat16 or x.dtype not in (torch.float32, torch.bfloat16) or y.dtype != torch.float32:
+        raise ValueError("linear takes float32 (or already rounded bfloat16) x, float32 y and bfloat16 w")
     n, k = w.shape
     m = x.numel() // k if k else 0
     if x.numel() != m * k or y.numel() != m * n or (bias is not None and bias.numel() != n):
         raise ValueError("linear shapes: x [m, k], w [n, k], y [m, n], bias [n]")
     if not (x.is_contiguous() and w.is_contiguous() and y.is_contiguous()):
         raise ValueError("linear takes contiguous x, w and y")
-    _op("uocr_rocm_linear", stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y))
+    name = "uocr_rocm_linear_bf16x" if x.dtype == torch.bfloat16 else "uocr_rocm_linear"
+    _op(name, stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y))
+
+
+def round_bf16(src, dst, stream=None):
+    """dst = bf16(src), nearest even (float32 -> bfloat16 tensors)."""
+    if src.numel() != dst.numel():
+        raise ValueError("round_bf16: src and dst sizes differ")
+    _op("uocr_rocm_round_bf16", stream, _ptr(src), src.numel(), _ptr(dst))
 
 
 def gemm_nt(m, n, k, alpha, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch=1, stream=None):

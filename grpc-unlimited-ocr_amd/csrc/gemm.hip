@@ -7,13 +7,20 @@
 // Both operands are k-contiguous (x rows, w rows), so one tile layout serves
 // both. A workgroup of 4 waves computes a 128 x 128 tile of y; wave (wm, wn)
 // owns a 64 x 64 quarter as 2 x 2 v_mfma_f32_32x32x16_bf16 tiles. The k
-// loop steps 64 at a time through LDS, double-buffered: the next step's
-// x (fp32, rounded to bf16 with the hardware's nearest-even conversion as
-// it is staged) and w chunks are loaded into registers while the current
-// step's 16 matrix products run, then written to the other buffer. Tile rows
-// are 8 chunks of 8 bf16 (16 bytes); a chunk's slot is XOR-swizzled by the
-// row so that the 32 rows one operand read spans fall on different banks.
-// The bias is added to each finished sum (one fp32 rounding, as the
+// loop steps 64 at a time through two LDS buffers. Tile rows are 8 chunks of
+// 8 bf16 (16 bytes); a chunk's slot is XOR-swizzled by the row so that the
+// 32 rows one operand read spans fall on different banks. Two kernels:
+//   * x already bf16 and k a multiple of 64: both tiles go from memory
+//     straight into LDS (16-byte global_load_lds, each lane's chunk picked so
+//     that it lands in its swizzled slot), the next step's loads in flight
+//     while the current step's 16 matrix products run;
+//   * otherwise (fp32 x, or a ragged k): chunks staged through registers, x
+//     rounded to bf16 with the hardware's nearest-even conversion on the way,
+//     chunks past k zero-filled.
+// Workgroups are dealt to the 8 XCDs round-robin; each XCD takes a
+// contiguous run of tiles, ordered in groups of 8 tile-rows sweeping the
+// columns, so the tiles resident on one XCD share x rows and w rows in its
+// L2. The bias is added to each finished sum (one fp32 rounding, as the
 // reference's separate bias pass).
 
 #include "common.hpp"
@@ -35,24 +42,42 @@ static_assert(kTileM == kTileN, "one staging pattern for both operands");
 
 __device__ __forceinline__ int slot(int row, int chunk) { return row * kRowChunks + (chunk ^ (row & 7)); }
 
+constexpr int kXcds = 8;
+constexpr int kGroupRows = 8;
+
+// The tile (tm, tn) of workgroup bid: a contiguous run of tiles per XCD,
+// groups of kGroupRows tile-rows sweeping the columns inside a run.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int t = total % kXcds == 0 ? (bid % kXcds) * (total / kXcds) + bid / kXcds : bid;
+  const int per = kGroupRows * tiles_n, group = t / per, first = group * kGroupRows;
+  const int rows = tiles_m - first < kGroupRows ? tiles_m - first : kGroupRows;
+  const int in = t - group * per;
+  tm = first + in % rows;
+  tn = in / rows;
+}
+
 struct LinearArgs {
-  const float* x;
+  const void* x;  // float or bf16 rows
   const uint16_t* w;
   const float* bias;
   float* y;
   int64_t m, n;
   int k;
-  int tiles_n;
+  int tiles_m, tiles_n;
 };
 
 // The registers one k step stages: per thread kChunksPerThread chunks of the
-// x tile (8 floats each, rounded on the way to LDS) and of the w tile.
+// x tile (8 elements each: fp32, rounded on the way to LDS, or bf16) and of
+// the w tile.
+template <bool kF32X>
 struct Staged {
-  u32x4 xa[kChunksPerThread][2];
+  u32x4 xa[kChunksPerThread][kF32X ? 2 : 1];
   u32x4 wb[kChunksPerThread];
 };
 
-__device__ __forceinline__ void load_step(const LinearArgs& a, int64_t m0, int64_t n0, int k0, Staged& s) {
+template <bool kF32X>
+__device__ __forceinline__ void load_step(const LinearArgs& a, int64_t m0, int64_t n0, int k0, Staged<kF32X>& s) {
 #pragma unroll
   for (int i = 0; i < kChunksPerThread; ++i) {
     const int id = static_cast<int>(threadIdx.x) + kGemmThreads * i;
@@ -60,81 +85,67 @@ __device__ __forceinline__ void load_step(const LinearArgs& a, int64_t m0, int64
     const int kc = k0 + 8 * c;
     const bool kin = kc < a.k;
     const int64_t xr = m0 + row, wr = n0 + row;
-    s.xa[i][0] = s.xa[i][1] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int h = 0; h < (kF32X ? 2 : 1); ++h) s.xa[i][h] = u32x4{0u, 0u, 0u, 0u};
     s.wb[i] = u32x4{0u, 0u, 0u, 0u};
     if (kin && xr < a.m) {
-      const u32x4* p = reinterpret_cast<const u32x4*>(a.x + xr * a.k + kc);
-      s.xa[i][0] = p[0];
-      s.xa[i][1] = p[1];
+      if constexpr (kF32X) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const float*>(a.x) + xr * a.k + kc);
+        s.xa[i][0] = p[0];
+        s.xa[i][1] = p[1];
+      } else {
+        s.xa[i][0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xr * a.k + kc);
+      }
     }
     if (kin && wr < a.n) s.wb[i] = *reinterpret_cast<const u32x4*>(a.w + wr * a.k + kc);
   }
 }
 
-__device__ __forceinline__ void store_step(const Staged& s, u32x4* xs, u32x4* ws) {
+template <bool kF32X>
+__device__ __forceinline__ void store_step(const Staged<kF32X>& s, u32x4* xs, u32x4* ws) {
 #pragma unroll
   for (int i = 0; i < kChunksPerThread; ++i) {
     const int id = static_cast<int>(threadIdx.x) + kGemmThreads * i;
     const int row = id / kRowChunks, c = id % kRowChunks;
-    const u32x4 lo = s.xa[i][0], hi = s.xa[i][1];
-    xs[slot(row, c)] = u32x4{pack_bf16(__uint_as_float(lo.x), __uint_as_float(lo.y)),
-                             pack_bf16(__uint_as_float(lo.z), __uint_as_float(lo.w)),
-                             pack_bf16(__uint_as_float(hi.x), __uint_as_float(hi.y)),
-                             pack_bf16(__uint_as_float(hi.z), __uint_as_float(hi.w))};
+    if constexpr (kF32X) {
+      const u32x4 lo = s.xa[i][0], hi = s.xa[i][1];
+      xs[slot(row, c)] = u32x4{pack_bf16(__uint_as_float(lo.x), __uint_as_float(lo.y)),
+                               pack_bf16(__uint_as_float(lo.z), __uint_as_float(lo.w)),
+                               pack_bf16(__uint_as_float(hi.x), __uint_as_float(hi.y)),
+                               pack_bf16(__uint_as_float(hi.z), __uint_as_float(hi.w))};
+    } else {
+      xs[slot(row, c)] = s.xa[i][0];
+    }
     ws[slot(row, c)] = s.wb[i];
   }
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-__global__ __launch_bounds__(kGemmThreads) void linear_bf16_k(const LinearArgs a) {
-  __shared__ u32x4 xs[2][kTileChunks];
-  __shared__ u32x4 ws[2][kTileChunks];
-  const int tile = blockIdx.x;
-  const int64_t m0 = static_cast<int64_t>(tile / a.tiles_n) * kTileM;
-  const int64_t n0 = static_cast<int64_t>(tile % a.tiles_n) * kTileN;
-  const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
-  const int wm = wave >> 1, wn = wave & 1;
-  const int half = lane >> 5, r32 = lane & 31;
-
-  f32x16 acc[2][2];
+// The 16 matrix products of one 64-wide k step of a wave's 64 x 64 quarter
+// from the tiles in LDS.
+__device__ __forceinline__ void mfma_step(const u32x4* xs, const u32x4* ws, int wm, int wn, int half, int r32,
+                                          f32x16 (&acc)[2][2]) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int kk = 0; kk < kTileK / 16; ++kk) {
+    const int c = 2 * kk + half;
+    bf16x8 fa[2], fb[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int i = 0; i < 2; ++i) fa[i] = as_bf16x8(xs[slot(64 * wm + 32 * i + r32, c)]);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int j = 0; j < 2; ++j) fb[j] = as_bf16x8(ws[slot(64 * wn + 32 * j + r32, c)]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
   }
+}
 
-  const int steps = (a.k + kTileK - 1) / kTileK;
-  Staged s;
-  load_step(a, m0, n0, 0, s);
-  store_step(s, xs[0], ws[0]);
-  lds_barrier();
-  for (int t = 0; t < steps; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < steps;
-    if (more) load_step(a, m0, n0, (t + 1) * kTileK, s);
-#pragma unroll
-    for (int kk = 0; kk < kTileK / 16; ++kk) {
-      const int c = 2 * kk + half;
-      bf16x8 fa[2], fb[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = as_bf16x8(xs[buf][slot(64 * wm + 32 * i + r32, c)]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = as_bf16x8(ws[buf][slot(64 * wn + 32 * j + r32, c)]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-      }
-    }
-    if (more) store_step(s, xs[buf ^ 1], ws[buf ^ 1]);
-    lds_barrier();
-  }
-
-  // acc[i][j][r] is y row 8 (r / 4) + 4 half + r % 4 of the 32 x 32 tile, column r32
+// acc[i][j][r] is y row 8 (r / 4) + 4 half + r % 4 of the 32 x 32 tile,
+// column r32.
+__device__ __forceinline__ void store_tile(const LinearArgs& a, int64_t m0, int64_t n0, int wm, int wn, int half,
+                                           int r32, const f32x16 (&acc)[2][2]) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int64_t col = n0 + 64 * wn + 32 * j + r32;
@@ -151,10 +162,115 @@ __global__ __launch_bounds__(kGemmThreads) void linear_bf16_k(const LinearArgs a
   }
 }
 
+__device__ __forceinline__ void zero(f32x16 (&acc)[2][2]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    }
+  }
+}
+
+// Chunks staged through registers (fp32 x, or a k that is not a multiple of 64).
+template <bool kF32X>
+__global__ __launch_bounds__(kGemmThreads) void linear_staged_k(const LinearArgs a) {
+  __shared__ u32x4 xs[2][kTileChunks];
+  __shared__ u32x4 ws[2][kTileChunks];
+  int tm, tn;
+  tile_of(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * kTileM, n0 = static_cast<int64_t>(tn) * kTileN;
+  const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
+  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, r32 = lane & 31;
+  f32x16 acc[2][2];
+  zero(acc);
+  const int steps = (a.k + kTileK - 1) / kTileK;
+  Staged<kF32X> s;
+  load_step(a, m0, n0, 0, s);
+  store_step(s, xs[0], ws[0]);
+  lds_barrier();
+  for (int t = 0; t < steps; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < steps;
+    if (more) load_step(a, m0, n0, (t + 1) * kTileK, s);
+    mfma_step(xs[buf], ws[buf], wm, wn, half, r32, acc);
+    if (more) store_step(s, xs[buf ^ 1], ws[buf ^ 1]);
+    lds_barrier();
+  }
+  store_tile(a, m0, n0, wm, wn, half, r32, acc);
+}
+
+// bf16 x and k a multiple of 64: tiles go straight from memory into LDS.
+// Each wave issues 4 + 4 16-byte global_load_lds per step, each writing 64
+// consecutive chunk slots (lane l to slot base + l) with the chunk that
+// belongs there under the swizzle. Rows past m or n read a valid row (their
+// sums are never stored). The step's loads are waited for with the wave's
+// own vmcnt before the barrier (a fence there would also wait for the next
+// step's loads); the barrier is an s_barrier with a compiler memory clobber.
+__device__ __forceinline__ void dma_step(const LinearArgs& a, int64_t m0, int64_t n0, int k0, u32x4* xs, u32x4* ws,
+                                         int wave, int lane) {
+  const uint16_t* x = static_cast<const uint16_t*>(a.x);
+#pragma unroll
+  for (int i = 0; i < kTileChunks / kGemmThreads; ++i) {
+    const int s0 = (wave * (kTileChunks / kGemmThreads) + i) * kWave;  // wave-uniform
+    const int sl = s0 + lane, row = sl / kRowChunks, c = (sl % kRowChunks) ^ (row & 7);
+    const int64_t xr = m0 + row < a.m ? m0 + row : a.m - 1;
+    const int64_t wr = n0 + row < a.n ? n0 + row : a.n - 1;
+    __builtin_amdgcn_global_load_lds(x + xr * a.k + k0 + 8 * c, xs + s0, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(a.w + wr * a.k + k0 + 8 * c, ws + s0, 16, 0, 0);
+  }
+}
+
+template <int kPending>
+__device__ __forceinline__ void wait_loads_and_barrier() {
+  // s_waitcnt vmcnt(kPending) with the other counters left alone, then the
+  // barrier; the asm's memory clobber keeps LDS accesses on their side.
+  __builtin_amdgcn_s_waitcnt((kPending & 0xF) | (((kPending >> 4) & 3) << 14) | (7 << 4) | (0xF << 8));
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__global__ __launch_bounds__(kGemmThreads) void linear_dma_k(const LinearArgs a) {
+  __shared__ u32x4 xs[2][kTileChunks];
+  __shared__ u32x4 ws[2][kTileChunks];
+  int tm, tn;
+  tile_of(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * kTileM, n0 = static_cast<int64_t>(tn) * kTileN;
+  const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
+  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, r32 = lane & 31;
+  f32x16 acc[2][2];
+  zero(acc);
+  const int steps = a.k / kTileK;
+  dma_step(a, m0, n0, 0, xs[0], ws[0], wave, lane);
+  for (int t = 0; t < steps; ++t) {
+    const int buf = t & 1;
+    wait_loads_and_barrier<0>();  // this step's tiles are in LDS; every wave is done with the other buffer
+    if (t + 1 < steps) dma_step(a, m0, n0, (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
+    mfma_step(xs[buf], ws[buf], wm, wn, half, r32, acc);
+  }
+  store_tile(a, m0, n0, wm, wn, half, r32, acc);
+}
+
+__global__ __launch_bounds__(kBlock) void round_bf16_k(const float* __restrict__ src, int64_t n,
+                                                        uint16_t* __restrict__ dst) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(src + i), hi = *reinterpret_cast<const u32x4*>(src + i + 4);
+    *reinterpret_cast<u32x4*>(dst + i) = u32x4{pack_bf16(__uint_as_float(lo.x), __uint_as_float(lo.y)),
+                                               pack_bf16(__uint_as_float(lo.z), __uint_as_float(lo.w)),
+                                               pack_bf16(__uint_as_float(hi.x), __uint_as_float(hi.y)),
+                                               pack_bf16(__uint_as_float(hi.z), __uint_as_float(hi.w))};
+  } else {
+    for (int64_t j = i; j < n; ++j) dst[j] = f32_to_bf16(src[j]);
+  }
+}
+
 }  // namespace
 
-int linear_entry(const char* what, void* stream, const float* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
-                 const float* bias, float* y) {
+int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64_t m, int64_t k, const uint16_t* w,
+                 int64_t n, const float* bias, float* y) {
   UOCR_REQUIRE(m >= 0 && n >= 0 && k >= 0, what, "m, n and k must be >= 0");
   if (m == 0 || n == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(k % 8 == 0 && k >= 8 && k < (int64_t{1} << 30), what, "k must be a multiple of 8 in [8, 2^30)");
@@ -162,9 +278,16 @@ int linear_entry(const char* what, void* stream, const float* x, int64_t m, int6
   UOCR_REQUIRE(aligned16(x) && aligned16(w), what, "x and w must be 16-byte aligned");
   const int64_t tiles_m = (m + kTileM - 1) / kTileM, tiles_n = (n + kTileN - 1) / kTileN;
   UOCR_REQUIRE(tiles_m * tiles_n < (int64_t{1} << 31), what, "too many tiles");
-  LinearArgs a{x, w, bias, y, m, n, static_cast<int>(k), static_cast<int>(tiles_n)};
+  LinearArgs a{x, w, bias, y, m, n, static_cast<int>(k), static_cast<int>(tiles_m), static_cast<int>(tiles_n)};
+  const unsigned grid = static_cast<unsigned>(tiles_m * tiles_n);
   clear_launch_error();
-  linear_bf16_k<<<static_cast<unsigned>(tiles_m * tiles_n), kGemmThreads, 0, as_stream(stream)>>>(a);
+  if (f32x) {
+    linear_staged_k<true><<<grid, kGemmThreads, 0, as_stream(stream)>>>(a);
+  } else if (k % kTileK == 0) {
+    linear_dma_k<<<grid, kGemmThreads, 0, as_stream(stream)>>>(a);
+  } else {
+    linear_staged_k<false><<<grid, kGemmThreads, 0, as_stream(stream)>>>(a);
+  }
   return check_launch(what);
 }
 
@@ -179,7 +302,25 @@ int uocr_rocm_linear(void* stream, const float* x, int64_t m, int64_t k, const u
   // One row streams the weights once through the GEMV (the reference's
   // m == 1 path, ops.cu:271-274).
   if (m == 1 && k <= 12288) return uocr_rocm_gemv_bf16(stream, x, k, w, n, bias, y);
-  return linear_entry("uocr_rocm_linear", stream, x, m, k, w, n, bias, y);
+  return linear_entry("uocr_rocm_linear", stream, x, true, m, k, w, n, bias, y);
+}
+
+int uocr_rocm_linear_bf16x(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
+                           const float* bias, float* y) {
+  return linear_entry("uocr_rocm_linear_bf16x", stream, x, false, m, k, w, n, bias, y);
+}
+
+int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst) {
+  constexpr const char* kWhat = "uocr_rocm_round_bf16";
+  UOCR_REQUIRE(n >= 0, kWhat, "n must be >= 0");
+  if (n == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(src != nullptr && dst != nullptr, kWhat, "null pointer");
+  UOCR_REQUIRE(aligned16(src) && aligned16(dst), kWhat, "src and dst must be 16-byte aligned");
+  const int64_t blocks = (n + 8 * kBlock - 1) / (8 * kBlock);
+  UOCR_REQUIRE(blocks < (int64_t{1} << 31), kWhat, "n too large");
+  clear_launch_error();
+  round_bf16_k<<<static_cast<unsigned>(blocks), kBlock, 0, as_stream(stream)>>>(src, n, dst);
+  return check_launch(kWhat);
 }
 
 }  // extern "C"

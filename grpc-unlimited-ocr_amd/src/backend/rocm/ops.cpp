@@ -167,6 +167,15 @@ void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, 
   check(uocr_rocm_linear(ctx.stream(), x, m, k, w_bf16, n, bias, y));
 }
 
+void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
+                  std::int64_t n, const float* bias, float* y) {
+  check(uocr_rocm_linear_bf16x(ctx.stream(), x, m, k, w_bf16, n, bias, y));
+}
+
+void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint16_t* dst) {
+  check(uocr_rocm_round_bf16(ctx.stream(), src, n, dst));
+}
+
 void add_rms_norm_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out, const float* w_norm,
                             float eps, float* h_out, std::int64_t k, const std::uint16_t* w, std::int64_t n,
                             const float* bias, float* y) {

@@ -132,6 +132,10 @@ void scatter_add_rows(const Context& ctx, float* dst, const std::int64_t* index,
 // accumulation (m == 1: the GEMV); the reference's linear.
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
             std::int64_t n, const float* bias, float* y);
+// New: linear with x already rounded to bf16; round_bf16 does the rounding.
+void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
+                  std::int64_t n, const float* bias, float* y);
+void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint16_t* dst);
 
 // Fused decode projections (new): add + RMSNorm as the GEMV's prologue,
 // optionally a gate/up pair with a SwiGLU epilogue. delta, x_out, w_norm

@@ -24,16 +24,25 @@ Array ids_on_device(const Context& ctx, const std::vector<std::int64_t>& ids) {
   return a;
 }
 
+// The bf16 rounding of rows [rows, cols] that every projection of them takes
+// (rounded once for all of them).
+Array rounded(const Context& ctx, const float* x, std::int64_t n) {
+  Array r(ctx, DType::kBF16, n);
+  round_bf16(ctx, x, n, r.bf16());
+  return r;
+}
+
 // y [rows, hidden] = silu(x Wg) * (x Wu) Wd over bf16 weights: gate and up
 // [ffn, hidden], down [hidden, ffn] (the reference's mlp,
-// cuda_decoder.cpp:117-135).
-void mlp(const Context& ctx, const float* x, std::int64_t rows, std::int64_t hidden, const std::uint16_t* gate,
+// cuda_decoder.cpp:117-135); xb is x rounded to bf16.
+void mlp(const Context& ctx, const std::uint16_t* xb, std::int64_t rows, std::int64_t hidden, const std::uint16_t* gate,
          const std::uint16_t* up, const std::uint16_t* down, std::int64_t ffn, float* y) {
   Array g(ctx, DType::kF32, rows * ffn), u(ctx, DType::kF32, rows * ffn);
-  linear(ctx, x, rows, hidden, gate, ffn, nullptr, g.f32());
-  linear(ctx, x, rows, hidden, up, ffn, nullptr, u.f32());
+  linear_bf16x(ctx, xb, rows, hidden, gate, ffn, nullptr, g.f32());
+  linear_bf16x(ctx, xb, rows, hidden, up, ffn, nullptr, u.f32());
   silu_mul(ctx, g.f32(), u.f32(), rows * ffn);
-  linear(ctx, g.f32(), rows, ffn, down, hidden, nullptr, y);
+  const Array gb = rounded(ctx, g.f32(), rows * ffn);
+  linear_bf16x(ctx, gb.bf16(), rows, ffn, down, hidden, nullptr, y);
 }
 
 }  // namespace
@@ -92,11 +101,14 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
     const std::uint16_t* wv = wk + W * H;
     const std::uint16_t* wrq = wv + W * H;
     const std::uint16_t* wrk = wrq + D * H;
-    linear(ctx_, h.f32(), rows, H, wq, W, nullptr, q.f32());
-    linear(ctx_, h.f32(), rows, H, wk, W, nullptr, kc);
-    linear(ctx_, h.f32(), rows, H, wv, W, nullptr, vc);
-    linear(ctx_, h.f32(), rows, H, wrq, D, nullptr, rq.f32());
-    linear(ctx_, h.f32(), rows, H, wrk, D, nullptr, rkc);
+    {
+      const Array hb = rounded(ctx_, h.f32(), rows * H);
+      linear_bf16x(ctx_, hb.bf16(), rows, H, wq, W, nullptr, q.f32());
+      linear_bf16x(ctx_, hb.bf16(), rows, H, wk, W, nullptr, kc);
+      linear_bf16x(ctx_, hb.bf16(), rows, H, wv, W, nullptr, vc);
+      linear_bf16x(ctx_, hb.bf16(), rows, H, wrq, D, nullptr, rq.f32());
+      linear_bf16x(ctx_, hb.bf16(), rows, H, wrk, D, nullptr, rkc);
+    }
     router_norm(ctx_, rq.f32(), l.router_q_norm, rows, D, eps);
     router_norm(ctx_, rkc, l.router_k_norm, rows, D, eps);
     for (float* t : {q.f32(), kc}) {
@@ -117,10 +129,14 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
     softmax_rows(ctx_, scores.f32(), d.heads * rows, keys);
     gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_cache_[li].f32(), W, hd, merged.f32(), W, hd,
             d.heads);
-    linear(ctx_, merged.f32(), rows, W, l.o, H, nullptr, delta.f32());
+    {
+      const Array mb = rounded(ctx_, merged.f32(), rows * W);
+      linear_bf16x(ctx_, mb.bf16(), rows, W, l.o, H, nullptr, delta.f32());
+    }
     add_rms_norm(ctx_, x.f32(), delta.f32(), l.post_norm, h.f32(), rows, H, eps);
+    const Array hb = rounded(ctx_, h.f32(), rows * H);
     if (l.moe == nullptr) {
-      mlp(ctx_, h.f32(), rows, H, l.gate, l.up, l.down, l.ffn, delta.f32());
+      mlp(ctx_, hb.bf16(), rows, H, l.gate, l.up, l.down, l.ffn, delta.f32());
       continue;
     }
     // mixture of experts (cuda_decoder.cpp:137-186): the device's softmax
@@ -149,7 +165,7 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
         weight_of[static_cast<std::size_t>(e)].push_back(wts_h[at]);
       }
     }
-    mlp(ctx_, h.f32(), rows, H, m.shared_gate, m.shared_up, m.shared_down, m.shared_ffn, delta.f32());
+    mlp(ctx_, hb.bf16(), rows, H, m.shared_gate, m.shared_up, m.shared_down, m.shared_ffn, delta.f32());
     Array routed = f32(rows * H);
     routed.zero();
     for (std::int64_t e = 0; e < m.experts; ++e) {
@@ -161,7 +177,8 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
       w.upload(weight_of[static_cast<std::size_t>(e)].data(), n);
       Array in = f32(n * H), res = f32(n * H);
       gather_rows(ctx_, h.f32(), idx.i64(), n, H, in.f32());
-      mlp(ctx_, in.f32(), n, H, m.gate_stack + e * m.expert_ffn * H, m.up_stack + e * m.expert_ffn * H,
+      const Array inb = rounded(ctx_, in.f32(), n * H);
+      mlp(ctx_, inb.bf16(), n, H, m.gate_stack + e * m.expert_ffn * H, m.up_stack + e * m.expert_ffn * H,
           m.down_stack + e * H * m.expert_ffn, m.expert_ffn, res.f32());
       scatter_add_rows(ctx_, routed.f32(), idx.i64(), w.f32(), res.f32(), n, H);
     }

@@ -315,6 +315,14 @@ UOCR_ROCM_API int uocr_rocm_scale_mask_softmax_rows(void* stream, float* x, floa
  * (src/backend/cuda/ops.h:14-17). */
 UOCR_ROCM_API int uocr_rocm_linear(void* stream, const float* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
                                    const float* bias, float* y);
+/* New: the same product with x already bf16 [m, k] (the rounding done by the
+ * producer, e.g. uocr_rocm_round_bf16 once for several projections of one
+ * activation); with k a multiple of 64 its tiles go straight from memory
+ * into LDS. */
+UOCR_ROCM_API int uocr_rocm_linear_bf16x(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w,
+                                         int64_t n, const float* bias, float* y);
+/* New: dst[i] = bf16(src[i]), nearest even; both 16-byte aligned. */
+UOCR_ROCM_API int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst);
 
 /* c[s] = alpha a[s] . b[s]^T (gemm_nt: a [m, k], b [n, k]) or c[s] = a[s] . b[s]
  * (gemm_nn: a [m, k], b [k, n]), fp32, row-major with leading dimensions

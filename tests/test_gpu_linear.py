@@ -71,6 +71,26 @@ def test_linear_model_shapes(backend, m, k, n):
     assert_f32_close(y.cpu().numpy(), ref.cpu().numpy(), 1e-5, f"linear full m={m} k={k} n={n}")
 
 
+@pytest.mark.parametrize("m,k,n", [(37, 200, 70), (300, 1280, 520), (129, 64, 257), (1, 128, 33), (64, 6848, 96)])
+def test_linear_bf16_x_is_linear_on_the_rounded_rows(backend, m, k, n):
+    """x already bf16 (k a multiple of 64: tiles loaded straight into LDS;
+    otherwise staged): the same sums as linear on the fp32 rows."""
+    x = normal(420 + m, (m, k))
+    wb = bf16(0.05 * normal(421 + n, (n, k)))
+    bias = normal(422, n)
+    want = oracle.linear(oracle.bf16_round(x), oracle.bf16_to_f32(wb), bias)
+    xb = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(dev_f32(x), xb)
+    assert np.array_equal(xb.view(torch.int16).cpu().numpy().view(np.uint16), bf16(x))  # nearest even
+    y = torch.full((m, n), float("nan"), device="cuda")
+    backend.linear(xb, dev_bf16(wb), y, dev_f32(bias))
+    assert_f32_close(host_f32(y), want, 1e-5, f"linear bf16 x m={m} k={k} n={n}")
+    y2 = torch.empty(m, n, device="cuda")
+    if m > 1:
+        backend.linear(dev_f32(x), dev_bf16(wb), y2, dev_f32(bias))
+        assert_f32_close(host_f32(y2), host_f32(y), 1e-6, "fp32 x and bf16 x agree")
+
+
 def test_linear_one_row_is_the_gemv(backend):
     k, n = 1280, 300
     x = normal(410, (1, k))
