@@ -20,6 +20,9 @@ norm weights; names and sizes follow the reference's headline op set):
      add+RMSNorm, bf16 GEMVs, RoPE, cache appends and split-K attention as
      one graph, fused into 6 launches (the 11-launch unfused layer beside
      it); the 129280 x 1280 LM-head GEMV on its own
+  8  the prefill pass's projections on the matrix cores for a 4096-token
+     prompt at the decoder's shapes (bf16 activations and weights, fp32
+     sums): TFLOP/s and fraction of the 2.5 PFLOP/s dense bf16 peak
 
 One step = one pass of a workload's op chain over one input set. The JSON
 line's `value` is workload 5 (the largest, three fused ops timed as one
@@ -552,6 +555,42 @@ def config7(be, torch, timer):
             "decode_step_12_layers": whole}
 
 
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
+
+
+def config8(be, torch, timer):
+    """The prefill pass's projections on the matrix cores (`linear` over bf16
+    activations, fp32 sums and output) at Unlimited-OCR-2's decoder shapes for
+    a 4096-token prompt: q/k/v + router q/k [4096 <- 1280], o [1280 <- 1280],
+    the dense FFN's gate and up [6848 <- 1280] and down [1280 <- 6848], the
+    shared experts' gate/up [1792 <- 1280] and down [1280 <- 1792]. Each
+    GEMM is timed on its own over fresh weight sets; the step is one dense
+    layer's six projections plus the o projection in sequence."""
+    rows, hidden = 4096, 1280
+    shapes = {"qkv_router": (4096, 1280), "o": (1280, 1280), "gate": (6848, 1280), "up": (6848, 1280),
+              "down": (1280, 6848), "shared_gate_up": (2 * 1792, 1280), "shared_down": (1280, 1792)}
+    xs = {k: bf16_randn(torch, (rows, k)) for k in {1280, 6848, 1792}}
+    ys = {n: torch.empty(rows, n, device="cuda") for n in {4096, 1280, 6848, 2 * 1792}}
+    kern = {}
+    total_flop, total_us = 0.0, 0.0
+    for name, (n, k) in shapes.items():
+        ms = time_kernel(timer, lambda n=n, k=k: (bf16_randn(torch, (n, k), 0.03),),
+                         lambda w, n=n, k=k: be.linear(xs[k], w[0], ys[n]))
+        flop = 2.0 * rows * n * k
+        tf = flop / (ms * 1e-3) / 1e12
+        kern[name] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                      "m": rows, "n": n, "k": k}
+        if name in ("qkv_router", "o", "gate", "up", "down"):
+            total_flop += flop
+            total_us += ms * 1e3
+    tf = total_flop / (total_us * 1e-6) / 1e12
+    return {"workload": "prefill projections of a dense decoder layer for a 4096-token prompt (bf16 activations, "
+                        "bf16 weights, fp32 sums): qkv+router, o, gate, up, down",
+            "step": {"us": round(total_us, 2), "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "bound": "mfma"},
+            "kernels": kern}
+
+
 def expert_ffn(be, torch, timer, hidden, ffn, experts, k):
     """The routed experts of one decode row (expert_ffn_one) on the model's
     MoE shape: 6 of 64 experts of FFN 896 at hidden 1280, stacks of 440 MB
@@ -937,7 +976,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="copy,1,2,3,4,5,6,7")
+    ap.add_argument("--configs", default="copy,1,2,3,4,5,6,7,8")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly (for counter collection)")
@@ -967,7 +1006,7 @@ def main():
     info = be.device_info(0)
     timer = Timer(torch, args.steps, args.warmup, use_graphs=not args.no_graph)
     runners = {"1": config1, "2": config2, "3": config3, "4": config4, "5": config5, "6": config6, "7": config7,
-               "copy": calibration}
+               "8": config8, "copy": calibration}
     configs = {}
     for c in args.configs.split(","):
         t0 = time.time()
