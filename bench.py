@@ -714,7 +714,15 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
         be.add_rms_norm_gemv_bf16(xs[cur], lm, logits, delta=pending, w_norm=final_norm)
 
     route_bytes = bytes_route_decode(pos, d, bs, local, prompt_blocks)
-    kv_bytes = b["attend"] + b["append"] + cap * 4          # fp32 cache, and the mask read
+    # The attention reads the K and V rows of the keys the mask keeps (the
+    # local window and the selected blocks), the mask, q, and writes its out
+    # and split records; `live` is counted from the route of layer 0.
+    route(Ls[0])
+    live = int(torch.isfinite(mask).sum().item())
+    fixed_attend = b["attend"] - 2 * cap * width * 4        # q, out and the split records
+
+    def kv_bytes(elem):
+        return 2 * live * width * elem + fixed_attend + 2 * width * elem + cap * 4
     proj_bytes = bytes_gemv(3 * width + 2 * d, hidden)
     attn_fixed = b["add_rms_norm"] + b["rope"] + route_bytes + proj_bytes + bytes_gemv(hidden, width)
     dense_bytes = 3 * dense_ffn * hidden * 2
@@ -727,14 +735,14 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
                        f"{shared_ffn}, fp32 router), block-routed attention over {cap} positions (block {bs}, local "
                        f"window {local * bs}, top-{params.top_m} entmax, {params.top_k} blocks, the query confined to "
                        f"one page of a {prompt_blocks}-block prompt), PageRope (63 token pairs, 1 page pair), final "
-                       f"norm + LM head [{vocab}, {hidden}]; {launches} launches",
-           "route_decode_step": report("route_decode_step", route_bytes, ms_route)}
+                       f"norm + LM head [{vocab}, {hidden}]; {launches} launches; the mask keeps {live} of "
+                       f"{cap} keys, and only their K/V rows are read",
+           "route_decode_step": report("route_decode_step", route_bytes, ms_route), "live_keys": live}
     for name, dtype in (("fp32_cache", torch.float32), ("bf16_cache", torch.bfloat16)):
         for L in Ls:
             L["kc"] = torch.randn(cap, width, device="cuda").to(dtype)
             L["vc"] = torch.randn(cap, width, device="cuda").to(dtype)
-        total = rest + layers * (attn_fixed + (kv_bytes if dtype == torch.float32 else
-                                               (b["attend"] + b["append"]) // 2 + cap * 4))
+        total = rest + layers * (attn_fixed + kv_bytes(4 if dtype == torch.float32 else 2))
         ms = timer.graph([step])[0]
         out[name] = {"step": report(f"decode step, {name}", total, ms), "us_per_token": round(ms * 1e3, 2)}
         for L in Ls:
