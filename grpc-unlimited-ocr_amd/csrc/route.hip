@@ -60,6 +60,22 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Inclusive sums over lanes 0..lane in lane order: lane j gets the fp32 sum
+// ((v_0 + v_1) + ...) + v_j, for lanes j <= kSteps. kSteps unrolled steps of
+// s = v + (s of the lane below, through a one-lane DPP shift; lane 0 reads
+// 0); after step t the first t + 1 lanes hold their final sums, and as fp32
+// addition commutes, v_j + s_(j-1) equals s_(j-1) + v_j bit for bit. Every
+// lane of the wave must be active.
+template <int kSteps>
+__device__ __forceinline__ float prefix_in_order(float v) {
+#pragma clang fp contract(off)
+  float s = v;
+#pragma unroll
+  for (int t = 0; t < kSteps; ++t) s = v + dpp_f32<0x138>(s);  // wave_shr:1
+  return s;
+}
+
+
 // head_cls as summarize takes it: lane l holds features l, l + 64, l + 128,
 // l + 192 (zero past d).
 __device__ __forceinline__ void load_cls(const float* __restrict__ cls, int d, float (&c)[4]) {
@@ -94,14 +110,15 @@ __device__ void summarize(const float* keys, int n, int d, const float (&cls)[4]
     const float a = lane < n ? p[lane] : -3.402823466e+38f;
     const float peak = wave_max(a);
     const float w = lane < n ? expf(a - peak) : 0.0f;
-    float total = 0.0f;
-    for (int t = 0; t < n; ++t) total += readlane_f32(w, t);
+    // the sum over t in order; lanes past n add +0, which changes nothing
+    float total = readlane_f32(prefix_in_order<kWave - 1>(w), kWave - 1);
     total = fmaxf(total, 1e-6f);
     if (lane < n) p[lane] = w / total;
   }
   lds_barrier();
   for (int e = threadIdx.x; e < d; e += blockDim.x) {
     float acc = 0.0f;
+#pragma unroll 8
     for (int t = 0; t < n; ++t) acc += p[t] * keys[t * d + e];
     out[e] = acc;
   }
@@ -216,19 +233,6 @@ __device__ __forceinline__ int key_block(uint64_t key) {
   return static_cast<int>(0xffffffffu - static_cast<uint32_t>(key));
 }
 
-// Inclusive sums over lanes 0..lane in lane order: lane j gets the fp32 sum
-// ((v_0 + v_1) + ...) + v_j, for lanes j < n. n - 1 steps of s = v + (s of
-// the lane below, through a one-lane DPP shift; lane 0 reads 0); after step
-// t the first t + 1 lanes hold their final sums, and as fp32 addition
-// commutes, v_j + s_(j-1) equals s_(j-1) + v_j bit for bit. Every lane of
-// the wave must be active.
-__device__ __forceinline__ float prefix_in_order(float v, int n) {
-#pragma clang fp contract(off)
-  float s = v;
-  for (int t = 1; t < n; ++t) s = v + dpp_f32<0x138>(s);  // wave_shr:1
-  return s;
-}
-
 template <int kCtrl>
 __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
   const uint32_t lo = static_cast<uint32_t>(
@@ -277,6 +281,7 @@ __device__ __forceinline__ uint64_t wave_top(uint64_t (&key)[S], int m, int lane
     }
   }
   uint64_t mine = 0;
+#pragma unroll 4
   for (int j = 0; j < m; ++j) {
     const uint64_t win = wave_max_key(key[0]);
     if (lane == j) mine = win;
@@ -327,13 +332,15 @@ __device__ __forceinline__ void load_pages(const int64_t* __restrict__ block_min
 }
 
 // Whether v holds in any thread of the block, through one LDS slot per wave
-// (`slots`, kRouteBlock / 64 ints, written once per launch).
+// (`slots`, kRouteBlock / 64 ints, written once per launch); a
+// kRouteBlock block.
 __device__ __forceinline__ bool block_any(bool v, int* slots) {
   const uint64_t lanes = __ballot(v);
   if ((threadIdx.x & (kWave - 1)) == 0) slots[wave_in_block()] = lanes != 0;
   lds_barrier();
   int any = 0;
-  for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) any |= slots[w];
+#pragma unroll
+  for (int w = 0; w < kRouteBlock / kWave; ++w) any |= slots[w];
   return any != 0;
 }
 
@@ -429,7 +436,7 @@ __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys
     const float val = have ? key_value(mine) : 0.0f;
     const float peak = readlane_f32(val, 0);
     const float v = have ? (val - peak) / 2.0f : 0.0f;
-    const float sum = prefix_in_order(v, m), sum_sq = prefix_in_order(v * v, m);
+    const float sum = prefix_in_order<kMaxTop - 1>(v), sum_sq = prefix_in_order<kMaxTop - 1>(v * v);
     const float rho = static_cast<float>(lane + 1);
     const float mean = sum / rho, mean_sq = sum_sq / rho;
     const float ss = rho * (mean_sq - mean * mean);
@@ -441,7 +448,7 @@ __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys
     const float prob = t * t;
     const bool valid = lane < k && sh.cand[blk] != 0;
     const float logp = logf(fmaxf(prob, p.floor));
-    const float logp_sum = readlane_f32(prefix_in_order(valid ? logp : 0.0f, k), k - 1);
+    const float logp_sum = readlane_f32(prefix_in_order<kMaxTop - 1>(valid ? logp : 0.0f), k - 1);
     const int count = __popcll(__ballot(valid));
     const float mu = logp_sum / static_cast<float>(count > 1 ? count : 1);
     if (valid) sh.block_bias[blk] = (logp - mu) / p.sigma;
@@ -670,20 +677,12 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   __shared__ int any_slots[kRouteBlock / kWave];
   static_assert(kStageFloats >= kMaxRouteBlocks + 2 * (kRouteBlock / kWave) * kMaxTop,
                 "the staged keys' space holds the blocks' mask values and the top-m lists");
-  const int64_t pos = a.state->pos;
-  const int bs = a.p.block_size;
-  if (pos < 0 || pos >= a.capacity) return;  // uniform over the block
   const int d = a.d, half = d / 2;
   const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
-  const int64_t blk = pos / bs, first = blk * bs;
-  const int n = static_cast<int>(pos - first + 1);
-  const int64_t last_remote = blk - a.p.local_blocks;
-  const int nrem = last_remote < 0 ? 0 : static_cast<int>(last_remote + 1);
-  const int nblk = static_cast<int>(blk + 1);
-  const int64_t query_page = a.state->query_page;
 
-  // 1. every load that does not wait for another: the router rows and their
-  // weights, head_cls, the rope frequency of this thread's pair, the block's
+  // 1. every load that does not wait for another: first those that need no
+  // position (the router rows and their weights, head_cls, the rope
+  // frequency of this thread's pair), then the step state, then the block's
   // earlier keys, the prompt blocks' page ranges and (the remote blocks being
   // whole, none of them the block summarized here) the first pass of
   // summaries
@@ -702,6 +701,17 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   const int pr = threadIdx.x;
   float freq = 0.0f;
   if (pr < half) freq = pr < a.n_tok ? a.inv_tok[pr] : a.inv_page[pr - a.n_tok];
+
+  const int64_t pos64 = a.state->pos;
+  if (pos64 < 0 || pos64 >= a.capacity) return;  // uniform over the block
+  // capacity / block_size <= 4096 blocks of at most 64 keys: 32-bit from here
+  const int pos = static_cast<int>(pos64), bs = a.p.block_size;
+  const int blk = pos / bs, first = blk * bs;
+  const int n = pos - first + 1;
+  const int last_remote = blk - a.p.local_blocks;
+  const int nrem = last_remote < 0 ? 0 : last_remote + 1;
+  const int nblk = blk + 1;
+  const int64_t query_page = a.state->query_page;
   StagedKeys staged;
   load_keys(a.router_keys, first, n - 1, d, staged);
   PageRanges ranges;
