@@ -185,4 +185,47 @@ __attribute__((visibility("default"))) void ref_key_mask(const std::int64_t* blo
   std::memcpy(mask, m.data(), m.size() * 4);
 }
 
+// out [o, oh, ow] = conv2d(x [c, h, w], weight [o, c, kh, kw], bias [o] or null, stride, pad).
+__attribute__((visibility("default"))) void ref_conv2d(const float* x, std::int64_t c, std::int64_t h, std::int64_t w,
+                                                       const float* weight, const float* bias, std::int64_t o,
+                                                       std::int64_t kh, std::int64_t kw, std::int64_t stride,
+                                                       std::int64_t pad, float* out) {
+  const uocr::Tensor b = bias != nullptr ? wrap(bias, {o}) : uocr::Tensor();
+  const uocr::Tensor y = ref::conv2d(wrap(x, {c, h, w}), wrap(weight, {o, c, kh, kw}), bias != nullptr ? &b : nullptr,
+                                     static_cast<int>(stride), static_cast<int>(pad));
+  unwrap(y, out);
+}
+
+// layer_norm_channels on x [c, h, w] in place.
+__attribute__((visibility("default"))) void ref_layer_norm_channels(float* x, const float* w, const float* b,
+                                                                    std::int64_t c, std::int64_t h, std::int64_t wd,
+                                                                    float eps) {
+  uocr::Tensor t = wrap(x, {c, h, wd});
+  ref::layer_norm_channels(t, wrap(w, {c}), wrap(b, {c}), eps);
+  unwrap(t, x);
+}
+
+// out [c, oh, ow] = resize_bicubic_aa(x [c, h, w]).
+__attribute__((visibility("default"))) void ref_resize_bicubic_aa(const float* x, std::int64_t c, std::int64_t h,
+                                                                  std::int64_t w, std::int64_t oh, std::int64_t ow,
+                                                                  float* out) {
+  unwrap(ref::resize_bicubic_aa(wrap(x, {c, h, w}), oh, ow), out);
+}
+
+// out [out_len, c] = resize_linear_rows(x [len, c]).
+__attribute__((visibility("default"))) void ref_resize_linear_rows(const float* x, std::int64_t len, std::int64_t c,
+                                                                   std::int64_t out_len, float* out) {
+  unwrap(ref::resize_linear_rows(wrap(x, {len, c}), out_len), out);
+}
+
+// y [h, w, c] = chw_to_hwc(x [c, h, w]); y [c, h, w] = hwc_to_chw(x [h, w, c]).
+__attribute__((visibility("default"))) void ref_chw_to_hwc(const float* x, std::int64_t c, std::int64_t h,
+                                                           std::int64_t w, float* y) {
+  unwrap(ref::chw_to_hwc(wrap(x, {c, h, w})), y);
+}
+__attribute__((visibility("default"))) void ref_hwc_to_chw(const float* x, std::int64_t h, std::int64_t w,
+                                                           std::int64_t c, float* y) {
+  unwrap(ref::hwc_to_chw(wrap(x, {h, w, c})), y);
+}
+
 }  // extern "C"
