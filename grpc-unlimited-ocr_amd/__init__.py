@@ -145,6 +145,12 @@ _SIGNATURES = {
     "uocr_rocm_gemm_nn": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_gather_rows": ([_vp, _vp, _vp, _i64, _i64, _vp], _int),
     "uocr_rocm_scatter_add_rows": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64], _int),
+    "uocr_rocm_im2col": ([_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _int),
+    "uocr_rocm_chw_to_hwc": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
+    "uocr_rocm_hwc_to_chw": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
+    "uocr_rocm_concat_cols": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp], _int),
+    "uocr_rocm_rel_pos_bias": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp], _int),
+    "uocr_rocm_rel_pos_softmax_rows": ([_vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp], _int),
     "uocr_rocm_append_step": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_append_step_bf16": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_attend_step_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp], _int),
@@ -522,6 +528,43 @@ def scatter_add_rows(dst, index, weight, src, stream=None):
     scatter_add_rows, ops.h:58-59."""
     rows, cols = index.numel(), dst.shape[-1]
     _op("uocr_rocm_scatter_add_rows", stream, _ptr(dst), _ptr(index), _ptr(weight), _ptr(src), rows, cols)
+
+
+def im2col(x, kh, kw, stride, pad, cols, stream=None):
+    """cols [oh * ow, c * kh * kw] = the patches of x [c, h, w] in weight
+    order. Reference: im2col, ops.h:54-56."""
+    c, h, w = x.shape
+    _op("uocr_rocm_im2col", stream, _ptr(x), c, h, w, kh, kw, stride, pad, _ptr(cols))
+
+
+def chw_to_hwc(x, y, stream=None):
+    """y [h, w, c] = x [c, h, w]. Reference: chw_to_hwc, ops.h:57."""
+    c, h, w = x.shape
+    _op("uocr_rocm_chw_to_hwc", stream, _ptr(x), c, h, w, _ptr(y))
+
+
+def hwc_to_chw(x, y, stream=None):
+    """y [c, h, w] = x [h, w, c]. Reference: hwc_to_chw, ops.h:58."""
+    h, w, c = x.shape
+    _op("uocr_rocm_hwc_to_chw", stream, _ptr(x), h, w, c, _ptr(y))
+
+
+def concat_cols(a, b, out, stream=None):
+    """out[r] = a[r] | b[r]. Reference: concat_cols, ops.h:65-67."""
+    _op("uocr_rocm_concat_cols", stream, _ptr(a), a.shape[-1], _ptr(b), b.shape[-1], a.shape[0], _ptr(out))
+
+
+def rel_pos_bias(q, ldq, h, w, d, rh, rw, bias, q_offset=0, stream=None):
+    """bias [h w, h w] of one window and head; the query rows start q_offset
+    floats into q (a head's columns). Reference: rel_pos_bias, ops.h:91-95."""
+    _op("uocr_rocm_rel_pos_bias", stream, _ptr(q) + 4 * q_offset, ldq, h, w, d, _ptr(rh), _ptr(rw), _ptr(bias))
+
+
+def rel_pos_softmax_rows(scores, windows, q, ldq, h, w, d, rh, rw, q_offset=0, stream=None):
+    """scores [windows, h w, h w] = softmax(scores + rel_pos_bias) per row,
+    query rows from q_offset floats into q (new)."""
+    _op("uocr_rocm_rel_pos_softmax_rows", stream, _ptr(scores), windows, _ptr(q) + 4 * q_offset, ldq, h, w, d,
+        _ptr(rh), _ptr(rw))
 
 
 def append_step(cache, row, state, capacity=None, stream=None):

@@ -14,9 +14,10 @@
 //     straight into LDS (16-byte global_load_lds, each lane's chunk picked so
 //     that it lands in its swizzled slot), the next step's loads in flight
 //     while the current step's 16 matrix products run;
-//   * otherwise (fp32 x, or a ragged k): chunks staged through registers, x
-//     rounded to bf16 with the hardware's nearest-even conversion on the way,
-//     chunks past k zero-filled.
+//   * otherwise (fp32 x, or k not a multiple of 64): chunks staged through
+//     registers, x rounded to bf16 with the hardware's nearest-even
+//     conversion on the way, chunks past k zero-filled; a k that is not a
+//     multiple of 8 (or unaligned rows) loads element by element.
 // Workgroups are dealt to the 8 XCDs round-robin; each XCD takes a
 // contiguous run of tiles, ordered in groups of 8 tile-rows sweeping the
 // columns, so the tiles resident on one XCD share x rows and w rows in its
@@ -101,6 +102,42 @@ __device__ __forceinline__ void load_step(const LinearArgs& a, int64_t m0, int64
   }
 }
 
+// A k that is not a multiple of 8 (rows not 16-byte aligned): each chunk's
+// 8 elements are loaded one by one, those at or past k read as zero.
+template <bool kF32X>
+__device__ __forceinline__ void load_step_ragged(const LinearArgs& a, int64_t m0, int64_t n0, int k0,
+                                                 Staged<kF32X>& s) {
+#pragma unroll
+  for (int i = 0; i < kChunksPerThread; ++i) {
+    const int id = static_cast<int>(threadIdx.x) + kGemmThreads * i;
+    const int row = id / kRowChunks, c = id % kRowChunks;
+    const int kc = k0 + 8 * c;
+    const int64_t xr = m0 + row, wr = n0 + row;
+    uint32_t xv[8], wv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool in = kc + e < a.k;
+      xv[e] = 0u;
+      wv[e] = 0u;
+      if (in && xr < a.m) {
+        if constexpr (kF32X) {
+          xv[e] = __float_as_uint(static_cast<const float*>(a.x)[xr * a.k + kc + e]);
+        } else {
+          xv[e] = static_cast<const uint16_t*>(a.x)[xr * a.k + kc + e];
+        }
+      }
+      if (in && wr < a.n) wv[e] = a.w[wr * a.k + kc + e];
+    }
+    if constexpr (kF32X) {
+      s.xa[i][0] = u32x4{xv[0], xv[1], xv[2], xv[3]};
+      s.xa[i][1] = u32x4{xv[4], xv[5], xv[6], xv[7]};
+    } else {
+      s.xa[i][0] = u32x4{xv[0] | (xv[1] << 16), xv[2] | (xv[3] << 16), xv[4] | (xv[5] << 16), xv[6] | (xv[7] << 16)};
+    }
+    s.wb[i] = u32x4{wv[0] | (wv[1] << 16), wv[2] | (wv[3] << 16), wv[4] | (wv[5] << 16), wv[6] | (wv[7] << 16)};
+  }
+}
+
 template <bool kF32X>
 __device__ __forceinline__ void store_step(const Staged<kF32X>& s, u32x4* xs, u32x4* ws) {
 #pragma unroll
@@ -123,21 +160,28 @@ __device__ __forceinline__ void store_step(const Staged<kF32X>& s, u32x4* xs, u3
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // The 16 matrix products of one 64-wide k step of a wave's 64 x 64 quarter
-// from the tiles in LDS.
+// from the tiles in LDS, the operand reads of each 16-wide slice issued
+// before the previous slice's products.
 __device__ __forceinline__ void mfma_step(const u32x4* xs, const u32x4* ws, int wm, int wn, int half, int r32,
                                           f32x16 (&acc)[2][2]) {
+  bf16x8 fa[2][2], fb[2][2];
+  auto read = [&](int kk, int b) {
+    const int c = 2 * kk + half;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) fa[b][i] = as_bf16x8(xs[slot(64 * wm + 32 * i + r32, c)]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[b][j] = as_bf16x8(ws[slot(64 * wn + 32 * j + r32, c)]);
+  };
+  read(0, 0);
 #pragma unroll
   for (int kk = 0; kk < kTileK / 16; ++kk) {
-    const int c = 2 * kk + half;
-    bf16x8 fa[2], fb[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) fa[i] = as_bf16x8(xs[slot(64 * wm + 32 * i + r32, c)]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) fb[j] = as_bf16x8(ws[slot(64 * wn + 32 * j + r32, c)]);
+    if (kk + 1 < kTileK / 16) read(kk + 1, (kk + 1) & 1);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < 2; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
+      }
     }
   }
 }
@@ -173,8 +217,9 @@ __device__ __forceinline__ void zero(f32x16 (&acc)[2][2]) {
   }
 }
 
-// Chunks staged through registers (fp32 x, or a k that is not a multiple of 64).
-template <bool kF32X>
+// Chunks staged through registers (fp32 x, or a k that is not a multiple of
+// 64; kRagged: not a multiple of 8).
+template <bool kF32X, bool kRagged>
 __global__ __launch_bounds__(kGemmThreads) void linear_staged_k(const LinearArgs a) {
   __shared__ u32x4 xs[2][kTileChunks];
   __shared__ u32x4 ws[2][kTileChunks];
@@ -188,13 +233,20 @@ __global__ __launch_bounds__(kGemmThreads) void linear_staged_k(const LinearArgs
   zero(acc);
   const int steps = (a.k + kTileK - 1) / kTileK;
   Staged<kF32X> s;
-  load_step(a, m0, n0, 0, s);
+  auto load = [&](int k0) {
+    if constexpr (kRagged) {
+      load_step_ragged(a, m0, n0, k0, s);
+    } else {
+      load_step(a, m0, n0, k0, s);
+    }
+  };
+  load(0);
   store_step(s, xs[0], ws[0]);
   lds_barrier();
   for (int t = 0; t < steps; ++t) {
     const int buf = t & 1;
     const bool more = t + 1 < steps;
-    if (more) load_step(a, m0, n0, (t + 1) * kTileK, s);
+    if (more) load((t + 1) * kTileK);
     mfma_step(xs[buf], ws[buf], wm, wn, half, r32, acc);
     if (more) store_step(s, xs[buf ^ 1], ws[buf ^ 1]);
     lds_barrier();
@@ -273,20 +325,27 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
                  int64_t n, const float* bias, float* y) {
   UOCR_REQUIRE(m >= 0 && n >= 0 && k >= 0, what, "m, n and k must be >= 0");
   if (m == 0 || n == 0) return UOCR_ROCM_OK;
-  UOCR_REQUIRE(k % 8 == 0 && k >= 8 && k < (int64_t{1} << 30), what, "k must be a multiple of 8 in [8, 2^30)");
+  UOCR_REQUIRE(k >= 1 && k < (int64_t{1} << 30), what, "k must be in [1, 2^30)");
   UOCR_REQUIRE(x != nullptr && w != nullptr && y != nullptr, what, "null x, w or y");
-  UOCR_REQUIRE(aligned16(x) && aligned16(w), what, "x and w must be 16-byte aligned");
+  const bool ragged = k % 8 != 0 || !aligned16(x) || !aligned16(w);
   const int64_t tiles_m = (m + kTileM - 1) / kTileM, tiles_n = (n + kTileN - 1) / kTileN;
   UOCR_REQUIRE(tiles_m * tiles_n < (int64_t{1} << 31), what, "too many tiles");
   LinearArgs a{x, w, bias, y, m, n, static_cast<int>(k), static_cast<int>(tiles_m), static_cast<int>(tiles_n)};
   const unsigned grid = static_cast<unsigned>(tiles_m * tiles_n);
   clear_launch_error();
-  if (f32x) {
-    linear_staged_k<true><<<grid, kGemmThreads, 0, as_stream(stream)>>>(a);
+  const hipStream_t st = as_stream(stream);
+  if (ragged) {
+    if (f32x) {
+      linear_staged_k<true, true><<<grid, kGemmThreads, 0, st>>>(a);
+    } else {
+      linear_staged_k<false, true><<<grid, kGemmThreads, 0, st>>>(a);
+    }
+  } else if (f32x) {
+    linear_staged_k<true, false><<<grid, kGemmThreads, 0, st>>>(a);
   } else if (k % kTileK == 0) {
-    linear_dma_k<<<grid, kGemmThreads, 0, as_stream(stream)>>>(a);
+    linear_dma_k<<<grid, kGemmThreads, 0, st>>>(a);
   } else {
-    linear_staged_k<false><<<grid, kGemmThreads, 0, as_stream(stream)>>>(a);
+    linear_staged_k<false, false><<<grid, kGemmThreads, 0, st>>>(a);
   }
   return check_launch(what);
 }
@@ -301,7 +360,9 @@ int uocr_rocm_linear(void* stream, const float* x, int64_t m, int64_t k, const u
                      const float* bias, float* y) {
   // One row streams the weights once through the GEMV (the reference's
   // m == 1 path, ops.cu:271-274).
-  if (m == 1 && k <= 12288) return uocr_rocm_gemv_bf16(stream, x, k, w, n, bias, y);
+  if (m == 1 && k % 8 == 0 && k <= 12288 && aligned16(x) && aligned16(w)) {
+    return uocr_rocm_gemv_bf16(stream, x, k, w, n, bias, y);
+  }
   return linear_entry("uocr_rocm_linear", stream, x, true, m, k, w, n, bias, y);
 }
 

@@ -162,6 +162,34 @@ void scatter_add_rows(const Context& ctx, float* dst, const std::int64_t* index,
   check(uocr_rocm_scatter_add_rows(ctx.stream(), dst, index, weight, src, rows, cols));
 }
 
+void im2col(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, std::int64_t kh,
+            std::int64_t kw, int stride, int pad, float* cols) {
+  check(uocr_rocm_im2col(ctx.stream(), x, c, h, w, kh, kw, stride, pad, cols));
+}
+
+void chw_to_hwc(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, float* y) {
+  check(uocr_rocm_chw_to_hwc(ctx.stream(), x, c, h, w, y));
+}
+
+void hwc_to_chw(const Context& ctx, const float* x, std::int64_t h, std::int64_t w, std::int64_t c, float* y) {
+  check(uocr_rocm_hwc_to_chw(ctx.stream(), x, h, w, c, y));
+}
+
+void concat_cols(const Context& ctx, const float* a, std::int64_t ca, const float* b, std::int64_t cb, std::int64_t rows,
+                 float* out) {
+  check(uocr_rocm_concat_cols(ctx.stream(), a, ca, b, cb, rows, out));
+}
+
+void rel_pos_bias(const Context& ctx, const float* q, std::int64_t ldq, std::int64_t h, std::int64_t w, std::int64_t d,
+                  const float* rh, const float* rw, float* bias) {
+  check(uocr_rocm_rel_pos_bias(ctx.stream(), q, ldq, h, w, d, rh, rw, bias));
+}
+
+void rel_pos_softmax_rows(const Context& ctx, float* scores, std::int64_t windows, const float* q, std::int64_t ldq,
+                          std::int64_t h, std::int64_t w, std::int64_t d, const float* rh, const float* rw) {
+  check(uocr_rocm_rel_pos_softmax_rows(ctx.stream(), scores, windows, q, ldq, h, w, d, rh, rw));
+}
+
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
             std::int64_t n, const float* bias, float* y) {
   check(uocr_rocm_linear(ctx.stream(), x, m, k, w_bf16, n, bias, y));

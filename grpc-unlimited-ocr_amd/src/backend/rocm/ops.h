@@ -128,6 +128,22 @@ void gather_rows(const Context& ctx, const float* src, const std::int64_t* index
                  float* dst);
 void scatter_add_rows(const Context& ctx, float* dst, const std::int64_t* index, const float* weight, const float* src,
                       std::int64_t rows, std::int64_t cols);
+// The vision encoder's layout ops: [c, h, w] patches in weight order
+// (oh = (h + 2 pad - kh) / stride + 1), the two layout transposes, and rows
+// joined side by side.
+void im2col(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, std::int64_t kh,
+            std::int64_t kw, int stride, int pad, float* cols);
+void chw_to_hwc(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, float* y);
+void hwc_to_chw(const Context& ctx, const float* x, std::int64_t h, std::int64_t w, std::int64_t c, float* y);
+void concat_cols(const Context& ctx, const float* a, std::int64_t ca, const float* b, std::int64_t cb, std::int64_t rows,
+                 float* out);
+// SAM's relative-position bias of one window and head, bias[t, ky w + kx] =
+// q_t . rh[qy, ky] + q_t . rw[qx, kx]; and (new) the scores of every window
+// of one head replaced by softmax(scores + that bias) in one pass.
+void rel_pos_bias(const Context& ctx, const float* q, std::int64_t ldq, std::int64_t h, std::int64_t w, std::int64_t d,
+                  const float* rh, const float* rw, float* bias);
+void rel_pos_softmax_rows(const Context& ctx, float* scores, std::int64_t windows, const float* q, std::int64_t ldq,
+                          std::int64_t h, std::int64_t w, std::int64_t d, const float* rh, const float* rw);
 // y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]) on the matrix cores, fp32
 // accumulation (m == 1: the GEMV); the reference's linear.
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,

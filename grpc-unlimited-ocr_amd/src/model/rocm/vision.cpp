@@ -1,0 +1,420 @@
+// VisionEncoder: the vision encoder on the rocm backend (the reference's
+// CudaVisionEncoder, src/model/cuda/cuda_vision.cpp, and
+// VisionModel::encode_page, src/model/vision_encoder.cpp:46-68).
+
+#include "model/rocm/vision.h"
+
+#include <algorithm>
+#include <cmath>
+#include <stdexcept>
+#include <string>
+
+#include "backend/rocm/ops.h"
+
+namespace uocr::rocm {
+namespace {
+
+constexpr float kSamEps = 1e-6f;
+constexpr float kClipEps = 1e-5f;
+
+void need(bool ok, const std::string& what) {
+  if (!ok) throw std::invalid_argument("VisionEncoder: " + what);
+}
+
+Array f32(const Context& ctx, std::int64_t n) { return Array(ctx, DType::kF32, std::max<std::int64_t>(n, 1)); }
+
+Array upload_f32(const Context& ctx, const std::vector<float>& v) {
+  Array a = f32(ctx, static_cast<std::int64_t>(v.size()));
+  if (!v.empty()) a.upload(v.data(), static_cast<std::int64_t>(v.size()));
+  return a;
+}
+
+// [rows, c] <-> [c, rows] of host tables (the position grids go through
+// the channel-major layout for the resize).
+std::vector<float> rows_to_channels(const std::vector<float>& x, std::int64_t rows, std::int64_t c) {
+  std::vector<float> y(x.size());
+  for (std::int64_t r = 0; r < rows; ++r)
+    for (std::int64_t ch = 0; ch < c; ++ch) y[ch * rows + r] = x[r * c + ch];
+  return y;
+}
+
+std::vector<float> channels_to_rows(const std::vector<float>& x, std::int64_t rows, std::int64_t c) {
+  std::vector<float> y(x.size());
+  for (std::int64_t ch = 0; ch < c; ++ch)
+    for (std::int64_t r = 0; r < rows; ++r) y[r * c + ch] = x[ch * rows + r];
+  return y;
+}
+
+// The antialiasing cubic, a = -0.5 (ops.cpp:43-54).
+float aa_cubic(float t) {
+  constexpr float a = -0.5f;
+  t = std::fabs(t);
+  if (t < 1.0f) return ((a + 2.0f) * t - (a + 3.0f)) * t * t + 1.0f;
+  if (t < 2.0f) return ((a * t - 5.0f * a) * t + 8.0f * a) * t - 4.0f * a;
+  return 0.0f;
+}
+
+// One axis's filter: for output index i, the first source index and the
+// normalised weights of its taps (ops.cpp:60-86).
+struct AxisFilter {
+  std::vector<std::int64_t> first;
+  std::vector<std::vector<float>> weights;
+};
+
+AxisFilter axis_filter(std::int64_t in, std::int64_t out) {
+  const float scale = static_cast<float>(in) / static_cast<float>(out);
+  const float support = scale >= 1.0f ? 2.0f * scale : 2.0f;
+  const float invscale = scale >= 1.0f ? 1.0f / scale : 1.0f;
+  AxisFilter f;
+  f.first.resize(static_cast<std::size_t>(out));
+  f.weights.resize(static_cast<std::size_t>(out));
+  for (std::int64_t i = 0; i < out; ++i) {
+    const float center = scale * (static_cast<float>(i) + 0.5f);
+    const std::int64_t lo = std::max<std::int64_t>(static_cast<std::int64_t>(center - support + 0.5f), 0);
+    const std::int64_t hi = std::min<std::int64_t>(static_cast<std::int64_t>(center + support + 0.5f), in);
+    auto& wv = f.weights[static_cast<std::size_t>(i)];
+    f.first[static_cast<std::size_t>(i)] = lo;
+    float sum = 0.0f;
+    for (std::int64_t j = lo; j < hi; ++j) {
+      wv.push_back(aa_cubic((static_cast<float>(j) - center + 0.5f) * invscale));
+      sum += wv.back();
+    }
+    if (sum != 0.0f) {
+      for (float& v : wv) v /= sum;
+    }
+  }
+  return f;
+}
+
+}  // namespace
+
+std::vector<float> resize_bicubic_aa(const std::vector<float>& x, std::int64_t c, std::int64_t h, std::int64_t w,
+                                     std::int64_t out_h, std::int64_t out_w) {
+  const AxisFilter fy = axis_filter(h, out_h), fx = axis_filter(w, out_w);
+  std::vector<float> out(static_cast<std::size_t>(c * out_h * out_w));
+  for (std::int64_t ch = 0; ch < c; ++ch) {
+    const float* src = x.data() + ch * h * w;
+    for (std::int64_t oy = 0; oy < out_h; ++oy) {
+      const auto& wy = fy.weights[static_cast<std::size_t>(oy)];
+      const std::int64_t y0 = fy.first[static_cast<std::size_t>(oy)];
+      for (std::int64_t ox = 0; ox < out_w; ++ox) {
+        const auto& wx = fx.weights[static_cast<std::size_t>(ox)];
+        const std::int64_t x0 = fx.first[static_cast<std::size_t>(ox)];
+        float acc = 0.0f;
+        for (std::size_t a = 0; a < wy.size(); ++a) {
+          const float* line = src + (y0 + static_cast<std::int64_t>(a)) * w + x0;
+          float along = 0.0f;
+          for (std::size_t b = 0; b < wx.size(); ++b) along += line[b] * wx[b];
+          acc += along * wy[a];
+        }
+        out[static_cast<std::size_t>((ch * out_h + oy) * out_w + ox)] = acc;
+      }
+    }
+  }
+  return out;
+}
+
+std::vector<float> resize_linear_rows(const std::vector<float>& x, std::int64_t len, std::int64_t c,
+                                      std::int64_t out_len) {
+  const float scale = static_cast<float>(len) / static_cast<float>(out_len);
+  std::vector<float> out(static_cast<std::size_t>(out_len * c));
+  for (std::int64_t i = 0; i < out_len; ++i) {
+    const float pos = std::max(scale * (static_cast<float>(i) + 0.5f) - 0.5f, 0.0f);
+    const auto r0 = static_cast<std::int64_t>(pos);
+    const std::int64_t r1 = r0 < len - 1 ? r0 + 1 : r0;
+    const float b = pos - static_cast<float>(r0), a = 1.0f - b;
+    for (std::int64_t e = 0; e < c; ++e) {
+      out[static_cast<std::size_t>(i * c + e)] =
+          a * x[static_cast<std::size_t>(r0 * c + e)] + b * x[static_cast<std::size_t>(r1 * c + e)];
+    }
+  }
+  return out;
+}
+
+std::vector<float> relative_positions(const std::vector<float>& table, std::int64_t d, std::int64_t size) {
+  const std::int64_t len = static_cast<std::int64_t>(table.size()) / d, span = 2 * size - 1;
+  const std::vector<float> t = len == span ? table : resize_linear_rows(table, len, d, span);
+  std::vector<float> out(static_cast<std::size_t>(size * size * d));
+  for (std::int64_t q = 0; q < size; ++q)
+    for (std::int64_t k = 0; k < size; ++k)
+      std::copy_n(t.begin() + (q - k + size - 1) * d, d, out.begin() + (q * size + k) * d);
+  return out;
+}
+
+VisionEncoder::VisionEncoder(const Context& ctx, const VisionDims& dims, VisionWeights weights)
+    : ctx_(ctx), dims_(dims), w_(std::move(weights)) {
+  const SamDims& s = dims_.sam;
+  const ClipDims& c = dims_.clip;
+  need(s.patch >= 1 && s.image % s.patch == 0 && s.width >= 1 && s.heads >= 1 && s.width % s.heads == 0 &&
+           s.window >= 1 && s.neck >= 1 && s.net2 >= 1 && s.net3 >= 1 && s.mlp >= 1,
+       "bad SAM dims");
+  need(s.width / s.heads <= 256, "SAM head dim above 256");
+  need(c.width == s.net3, "CLIP width must equal SAM's output channels");
+  need(c.heads >= 1 && c.width % c.heads == 0 && c.mlp >= 1 && c.positions >= 2, "bad CLIP dims");
+  const auto src = static_cast<std::int64_t>(std::sqrt(static_cast<double>(c.positions - 1)));
+  need(src * src == c.positions - 1, "CLIP positions must be a square grid plus one");
+  need(static_cast<std::int64_t>(w_.sam_blocks.size()) == s.layers, "one SamBlockWeights per SAM layer");
+  need(static_cast<std::int64_t>(w_.clip_layers.size()) == c.layers, "one ClipLayerWeights per CLIP layer");
+  const std::int64_t pg = s.image / s.patch, hd = s.width / s.heads;
+  need(static_cast<std::int64_t>(w_.sam_pos.size()) == pg * pg * s.width, "sam_pos must be [image/patch]^2 x width");
+  need(static_cast<std::int64_t>(w_.clip_pos.size()) == c.positions * c.width, "clip_pos must be [positions, width]");
+  need(static_cast<std::int64_t>(w_.newline.size()) == dims_.hidden &&
+           static_cast<std::int64_t>(w_.separator.size()) == dims_.hidden,
+       "newline and separator must be [hidden]");
+  for (std::int64_t i = 0; i < s.layers; ++i) {
+    const auto& b = w_.sam_blocks[static_cast<std::size_t>(i)];
+    need(!b.rel_h.empty() && b.rel_h.size() % static_cast<std::size_t>(hd) == 0 && b.rel_w.size() % hd == 0 &&
+             !b.rel_w.empty(),
+         "relative-position tables must be [len, head_dim]");
+    global_.push_back(std::find(s.global_layers.begin(), s.global_layers.end(), i) != s.global_layers.end());
+  }
+}
+
+std::int64_t VisionEncoder::grid(std::int64_t size) const {
+  const std::int64_t g = size / dims_.sam.patch, g2 = (g + 2 - 3) / 2 + 1;
+  return (g2 + 2 - 3) / 2 + 1;
+}
+
+std::int64_t VisionEncoder::page_image_tokens(std::int64_t global_grid, std::int64_t tile_grid,
+                                              std::int64_t tiles_wide, std::int64_t tiles_high, bool tiled) {
+  std::int64_t tokens = global_grid * (global_grid + 1) + 1;
+  if (tiled) tokens += (tile_grid * tiles_wide + 1) * (tile_grid * tiles_high);
+  return tokens;
+}
+
+const Array& VisionEncoder::sam_positions(std::int64_t g) const {
+  if (auto it = sam_pos_.find(g); it != sam_pos_.end()) return it->second;
+  const std::int64_t pg = dims_.sam.image / dims_.sam.patch, c = dims_.sam.width;
+  std::vector<float> pos = w_.sam_pos;
+  if (pg != g) {
+    pos = channels_to_rows(resize_bicubic_aa(rows_to_channels(pos, pg * pg, c), c, pg, pg, g, g), g * g, c);
+  }
+  return sam_pos_.emplace(g, upload_f32(ctx_, pos)).first->second;
+}
+
+const Array& VisionEncoder::clip_positions(std::int64_t g) const {
+  if (auto it = clip_pos_.find(g); it != clip_pos_.end()) return it->second;
+  const std::int64_t c = dims_.clip.width;
+  const auto src = static_cast<std::int64_t>(std::sqrt(static_cast<double>(dims_.clip.positions - 1)));
+  std::vector<float> pos = w_.clip_pos;
+  if (src != g) {
+    const std::vector<float> cells(w_.clip_pos.begin() + c, w_.clip_pos.end());
+    const std::vector<float> resized =
+        channels_to_rows(resize_bicubic_aa(rows_to_channels(cells, src * src, c), c, src, src, g, g), g * g, c);
+    pos.assign(w_.clip_pos.begin(), w_.clip_pos.begin() + c);
+    pos.insert(pos.end(), resized.begin(), resized.end());
+  }
+  return clip_pos_.emplace(g, upload_f32(ctx_, pos)).first->second;
+}
+
+const Array& VisionEncoder::rel_table(std::size_t block, bool height, std::int64_t span) const {
+  const auto key = std::make_tuple(block, height, span);
+  if (auto it = rel_tables_.find(key); it != rel_tables_.end()) return it->second;
+  const auto& b = w_.sam_blocks[block];
+  const std::int64_t hd = dims_.sam.width / dims_.sam.heads;
+  return rel_tables_.emplace(key, upload_f32(ctx_, relative_positions(height ? b.rel_h : b.rel_w, hd, span)))
+      .first->second;
+}
+
+// Windows of a g x g grid in row order, slots in row order within a window
+// (sam_encoder.cpp:17-47): gather[slot] is the grid row that fills it (the
+// zero row g * g for the padding), scatter[cell] the slot a grid cell went to.
+const VisionEncoder::Windows& VisionEncoder::windows(std::int64_t g) const {
+  if (auto it = windows_.find(g); it != windows_.end()) return it->second;
+  const std::int64_t win = dims_.sam.window, per = (g + win - 1) / win, n = win * win;
+  std::vector<std::int64_t> gather(static_cast<std::size_t>(per * per * n), g * g), scatter(static_cast<std::size_t>(g * g));
+  for (std::int64_t y = 0; y < g; ++y)
+    for (std::int64_t x = 0; x < g; ++x) {
+      const std::int64_t slot = ((y / win) * per + x / win) * n + (y % win) * win + x % win;
+      gather[static_cast<std::size_t>(slot)] = y * g + x;
+      scatter[static_cast<std::size_t>(y * g + x)] = slot;
+    }
+  Windows w;
+  w.count = per * per;
+  w.gather = Array(ctx_, DType::kI64, static_cast<std::int64_t>(gather.size()));
+  w.gather.upload(gather.data(), static_cast<std::int64_t>(gather.size()));
+  w.scatter = Array(ctx_, DType::kI64, g * g);
+  w.scatter.upload(scatter.data(), g * g);
+  return windows_.emplace(g, std::move(w)).first->second;
+}
+
+// Attention of one block over `windows` windows of h x w tokens, rows
+// window-major in x [windows * h * w, width]: per head the scores of every
+// window in one batched product, the relative-position bias and softmax in
+// one pass, the values' product into the head's columns; then the output
+// projection (cuda_vision.cpp:151-172).
+void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_t windows, std::int64_t h,
+                                  std::int64_t w, float* out) const {
+  const auto& b = w_.sam_blocks[index];
+  const std::int64_t c = dims_.sam.width, heads = dims_.sam.heads, hd = c / heads, n = h * w, rows = windows * n;
+  Array qkv = f32(ctx_, rows * 3 * c);
+  linear(ctx_, x, rows, c, b.qkv, 3 * c, b.qkv_b, qkv.f32());
+  const Array& rh = rel_table(index, true, h);
+  const Array& rw = rel_table(index, false, w);
+  Array scores = f32(ctx_, windows * n * n), merged = f32(ctx_, rows * c);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  for (std::int64_t head = 0; head < heads; ++head) {
+    const float* q = qkv.f32() + head * hd;
+    gemm_nt(ctx_, n, n, hd, scale, q, 3 * c, n * 3 * c, q + c, 3 * c, n * 3 * c, scores.f32(), n, n * n, windows);
+    rel_pos_softmax_rows(ctx_, scores.f32(), windows, q, 3 * c, h, w, hd, rh.f32(), rw.f32());
+    gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, q + 2 * c, 3 * c, n * 3 * c, merged.f32() + head * hd, c, n * c,
+            windows);
+  }
+  linear(ctx_, merged.f32(), rows, c, b.proj, c, b.proj_b, out);
+}
+
+// One SAM block over x [g * g, width] (cuda_vision.cpp:174-202).
+void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const {
+  const auto& b = w_.sam_blocks[index];
+  const std::int64_t c = dims_.sam.width, cells = g * g;
+  Array normed = f32(ctx_, (cells + 1) * c);  // the extra zero row fills the windows' padding
+  normed.zero();
+  copy(ctx_, normed.f32(), x.f32(), cells * c);
+  layer_norm(ctx_, normed.f32(), b.norm1_w, b.norm1_b, cells, c, kSamEps);
+  Array attended = f32(ctx_, cells * c);
+  if (global_[index]) {
+    sam_attention(index, normed.f32(), 1, g, g, attended.f32());
+  } else {
+    const std::int64_t win = dims_.sam.window;
+    const Windows& wi = windows(g);
+    const std::int64_t rows = wi.count * win * win;
+    Array slots = f32(ctx_, rows * c), out = f32(ctx_, rows * c);
+    gather_rows(ctx_, normed.f32(), wi.gather.i64(), rows, c, slots.f32());
+    sam_attention(index, slots.f32(), wi.count, win, win, out.f32());
+    gather_rows(ctx_, out.f32(), wi.scatter.i64(), cells, c, attended.f32());
+  }
+  add_inplace(ctx_, x.f32(), attended.f32(), cells * c);
+
+  Array hidden = f32(ctx_, cells * c), wide = f32(ctx_, cells * dims_.sam.mlp);
+  copy(ctx_, hidden.f32(), x.f32(), cells * c);
+  layer_norm(ctx_, hidden.f32(), b.norm2_w, b.norm2_b, cells, c, kSamEps);
+  linear(ctx_, hidden.f32(), cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
+  gelu_erf(ctx_, wide.f32(), cells * dims_.sam.mlp);
+  linear(ctx_, wide.f32(), cells, dims_.sam.mlp, b.lin2, c, b.lin2_b, hidden.f32());
+  add_inplace(ctx_, x.f32(), hidden.f32(), cells * c);
+}
+
+// A 3 x 3 convolution (padding 1) of rows hwc [side * side, in_c] into rows
+// out [out_side^2, out_c]: to channel-major, the patch gather, the product.
+void VisionEncoder::conv3(const float* hwc, std::int64_t side, std::int64_t in_c, const std::uint16_t* w,
+                          std::int64_t out_c, int stride, Array& out, std::int64_t& out_side) const {
+  Array chw = f32(ctx_, side * side * in_c);
+  hwc_to_chw(ctx_, hwc, side, side, in_c, chw.f32());
+  out_side = (side + 2 - 3) / stride + 1;
+  Array patches = f32(ctx_, out_side * out_side * in_c * 9);
+  im2col(ctx_, chw.f32(), in_c, side, side, 3, 3, stride, 1, patches.f32());
+  out = f32(ctx_, out_side * out_side * out_c);
+  linear(ctx_, patches.f32(), out_side * out_side, in_c * 9, w, out_c, nullptr, out.f32());
+}
+
+// SAM over one image into cells [g4 * g4, net3] (cuda_vision.cpp:204-237).
+void VisionEncoder::sam_forward(const float* image, std::int64_t size, Array& cells) const {
+  const SamDims& s = dims_.sam;
+  const std::int64_t p = s.patch, g = size / p, c = s.width;
+  Array cols = f32(ctx_, g * g * 3 * p * p);
+  im2col(ctx_, image, 3, size, size, p, p, static_cast<int>(p), 0, cols.f32());
+  Array x = f32(ctx_, g * g * c);
+  linear(ctx_, cols.f32(), g * g, 3 * p * p, w_.patch, c, w_.patch_b, x.f32());
+  add_inplace(ctx_, x.f32(), sam_positions(g).f32(), g * g * c);
+  for (std::size_t i = 0; i < w_.sam_blocks.size(); ++i) sam_block(i, x, g);
+
+  Array y = f32(ctx_, g * g * s.neck);
+  linear(ctx_, x.f32(), g * g, c, w_.neck0, s.neck, nullptr, y.f32());
+  layer_norm(ctx_, y.f32(), w_.neck1_w, w_.neck1_b, g * g, s.neck, kSamEps);
+  Array z, n2;
+  std::int64_t s1 = 0, s2 = 0, s3 = 0;
+  conv3(y.f32(), g, s.neck, w_.neck2, s.neck, 1, z, s1);
+  layer_norm(ctx_, z.f32(), w_.neck3_w, w_.neck3_b, s1 * s1, s.neck, kSamEps);
+  conv3(z.f32(), s1, s.neck, w_.net2, s.net2, 2, n2, s2);
+  conv3(n2.f32(), s2, s.net2, w_.net3, s.net3, 2, cells, s3);
+}
+
+// CLIP over the cells (cuda_vision.cpp:239-266): x [1 + g * g, width].
+void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) const {
+  const ClipDims& cd = dims_.clip;
+  const std::int64_t c = cd.width, n = 1 + g * g, heads = cd.heads, hd = c / heads;
+  x = f32(ctx_, n * c);
+  copy(ctx_, x.f32(), w_.class_embedding, c);
+  copy(ctx_, x.f32() + c, cells, g * g * c);
+  add_inplace(ctx_, x.f32(), clip_positions(g).f32(), n * c);
+  layer_norm(ctx_, x.f32(), w_.pre_ln_w, w_.pre_ln_b, n, c, kClipEps);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  Array normed = f32(ctx_, n * c), qkv = f32(ctx_, n * 3 * c), scores = f32(ctx_, heads * n * n);
+  Array merged = f32(ctx_, n * c), proj = f32(ctx_, n * c), wide = f32(ctx_, n * cd.mlp);
+  for (const auto& l : w_.clip_layers) {
+    copy(ctx_, normed.f32(), x.f32(), n * c);
+    layer_norm(ctx_, normed.f32(), l.ln1_w, l.ln1_b, n, c, kClipEps);
+    linear(ctx_, normed.f32(), n, c, l.qkv, 3 * c, l.qkv_b, qkv.f32());
+    gemm_nt(ctx_, n, n, hd, scale, qkv.f32(), 3 * c, hd, qkv.f32() + c, 3 * c, hd, scores.f32(), n, n * n, heads);
+    softmax_rows(ctx_, scores.f32(), heads * n, n);
+    gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, qkv.f32() + 2 * c, 3 * c, hd, merged.f32(), c, hd, heads);
+    linear(ctx_, merged.f32(), n, c, l.out, c, l.out_b, proj.f32());
+    add_inplace(ctx_, x.f32(), proj.f32(), n * c);
+    copy(ctx_, normed.f32(), x.f32(), n * c);
+    layer_norm(ctx_, normed.f32(), l.ln2_w, l.ln2_b, n, c, kClipEps);
+    linear(ctx_, normed.f32(), n, c, l.fc1, cd.mlp, l.fc1_b, wide.f32());
+    quick_gelu(ctx_, wide.f32(), n * cd.mlp);
+    linear(ctx_, wide.f32(), n, cd.mlp, l.fc2, c, l.fc2_b, proj.f32());
+    add_inplace(ctx_, x.f32(), proj.f32(), n * c);
+  }
+}
+
+void VisionEncoder::encode_view(const float* image_device, std::int64_t size, float* out) const {
+  need(size >= 64 && size % 64 == 0, "image must be [3, S, S] with S a multiple of 64");
+  Array cells;
+  sam_forward(image_device, size, cells);
+  const std::int64_t g = grid(size), n = g * g, cw = dims_.clip.width, sw = dims_.sam.net3;
+  Array clip;
+  clip_forward(cells.f32(), g, clip);
+  Array joined = f32(ctx_, n * (cw + sw));
+  concat_cols(ctx_, clip.f32() + cw, cw, cells.f32(), sw, n, joined.f32());  // the class row dropped
+  linear(ctx_, joined.f32(), n, cw + sw, w_.projector, dims_.hidden, w_.projector_b, out);
+}
+
+std::vector<float> VisionEncoder::encode_view(const View& image) const {
+  need(image.size >= 64 && image.size % 64 == 0 &&
+           static_cast<std::int64_t>(image.pixels.size()) == 3 * image.size * image.size,
+       "image must be [3, S, S] with S a multiple of 64");
+  const Array pixels = upload_f32(ctx_, image.pixels);
+  const std::int64_t g = grid(image.size);
+  Array out = f32(ctx_, g * g * dims_.hidden);
+  encode_view(pixels.f32(), image.size, out.f32());
+  return out.download();
+}
+
+std::vector<float> VisionEncoder::encode_page(const View& global, const std::vector<View>& tiles,
+                                              std::int64_t tiles_wide, std::int64_t tiles_high) const {
+  const std::int64_t width = dims_.hidden;
+  std::vector<float> rows;
+  auto append_grid = [&](const float* cells, std::int64_t grid_rows, std::int64_t grid_cols) {
+    for (std::int64_t r = 0; r < grid_rows; ++r) {
+      rows.insert(rows.end(), cells + r * grid_cols * width, cells + (r + 1) * grid_cols * width);
+      rows.insert(rows.end(), w_.newline.begin(), w_.newline.end());
+    }
+  };
+  if (!tiles.empty()) {
+    need(static_cast<std::int64_t>(tiles.size()) == tiles_wide * tiles_high,
+         "encode_page: tile count does not match the tile grid");
+    std::vector<std::vector<float>> feats;
+    for (const View& t : tiles) feats.push_back(encode_view(t));
+    const std::int64_t g = grid(tiles.front().size), cols = tiles_wide * g;
+    for (const View& t : tiles) need(t.size == tiles.front().size, "encode_page: tiles of different sizes");
+    std::vector<float> stitched(static_cast<std::size_t>(tiles_high * g * cols * width));
+    for (std::int64_t ty = 0; ty < tiles_high; ++ty)
+      for (std::int64_t tx = 0; tx < tiles_wide; ++tx) {
+        const auto& f = feats[static_cast<std::size_t>(ty * tiles_wide + tx)];
+        for (std::int64_t r = 0; r < g; ++r) {
+          std::copy_n(f.begin() + r * g * width, g * width,
+                      stitched.begin() + ((ty * g + r) * cols + tx * g) * width);
+        }
+      }
+    append_grid(stitched.data(), tiles_high * g, cols);
+  }
+  const std::vector<float> view = encode_view(global);
+  const std::int64_t g = grid(global.size);
+  append_grid(view.data(), g, g);
+  rows.insert(rows.end(), w_.separator.begin(), w_.separator.end());
+  return rows;
+}
+
+}  // namespace uocr::rocm

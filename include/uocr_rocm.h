@@ -310,8 +310,9 @@ UOCR_ROCM_API int uocr_rocm_scale_mask_softmax_rows(void* stream, float* x, floa
 /* y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]): x fp32 row-major, rounded
  * to bf16 (nearest even) for the product, w bf16 row-major, fp32
  * accumulation on the matrix cores, fp32 y; the bias (may be null) is added
- * to each finished sum. m == 1 (k <= 12288) goes through uocr_rocm_gemv_bf16.
- * k is a multiple of 8; x and w 16-byte aligned. Replaces linear
+ * to each finished sum. m == 1 (k <= 12288, k a multiple of 8, x and w
+ * 16-byte aligned) goes through uocr_rocm_gemv_bf16. Any k >= 1; rows that
+ * are not 16-byte multiples load element by element. Replaces linear
  * (src/backend/cuda/ops.h:14-17). */
 UOCR_ROCM_API int uocr_rocm_linear(void* stream, const float* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
                                    const float* bias, float* y);
@@ -344,6 +345,42 @@ UOCR_ROCM_API int uocr_rocm_gather_rows(void* stream, const float* src, const in
                                         int64_t cols, float* dst);
 UOCR_ROCM_API int uocr_rocm_scatter_add_rows(void* stream, float* dst, const int64_t* index, const float* weight,
                                              const float* src, int64_t rows, int64_t cols);
+
+/* ---- the vision encoder's layout and attention-bias ops ------------------------- */
+
+/* cols [oh * ow, c * kh * kw] = the patches of x [c, h, w] in the weight's
+ * [c, kh, kw] column order, zero outside the image, oh = (h + 2 pad - kh) /
+ * stride + 1 (ow alike). Replaces im2col (src/backend/cuda/ops.h:54-56). */
+UOCR_ROCM_API int uocr_rocm_im2col(void* stream, const float* x, int64_t c, int64_t h, int64_t w, int64_t kh,
+                                   int64_t kw, int64_t stride, int64_t pad, float* cols);
+
+/* y [h, w, c] = x [c, h, w] and y [c, h, w] = x [h, w, c] (out of place).
+ * Replace chw_to_hwc and hwc_to_chw (src/backend/cuda/ops.h:57-58). */
+UOCR_ROCM_API int uocr_rocm_chw_to_hwc(void* stream, const float* x, int64_t c, int64_t h, int64_t w, float* y);
+UOCR_ROCM_API int uocr_rocm_hwc_to_chw(void* stream, const float* x, int64_t h, int64_t w, int64_t c, float* y);
+
+/* out[r] = a[r] (ca values) followed by b[r] (cb values), rows of fp32.
+ * Replaces concat_cols (src/backend/cuda/ops.h:65-67). */
+UOCR_ROCM_API int uocr_rocm_concat_cols(void* stream, const float* a, int64_t ca, const float* b, int64_t cb,
+                                        int64_t rows, float* out);
+
+/* SAM's decomposed relative-position bias for one head of one window:
+ * bias[t, ky * w + kx] = q_t . rh[qy, ky] + q_t . rw[qx, kx] for query t =
+ * qy * w + qx, q rows ldq apart, rh [h, h, d], rw [w, w, d], bias [h w, h w].
+ * d <= 256, h + w <= 2048. Allocates nothing. Replaces rel_pos_bias
+ * (src/backend/cuda/ops.h:91-95). */
+UOCR_ROCM_API int uocr_rocm_rel_pos_bias(void* stream, const float* q, int64_t ldq, int64_t h, int64_t w, int64_t d,
+                                         const float* rh, const float* rw, float* bias);
+
+/* New: scores [windows, h w, h w] of one head in place = softmax over each
+ * row of (scores + bias), the bias of uocr_rocm_rel_pos_bias formed inside
+ * the row's workgroup from the query rows (window-major, ldq apart: row
+ * window * h w + t at q + (window * h w + t) * ldq). The reference's
+ * rel_pos_bias + add_inplace + softmax_rows over every window
+ * (src/model/cuda/cuda_vision.cpp:161-166) in one pass over the scores. */
+UOCR_ROCM_API int uocr_rocm_rel_pos_softmax_rows(void* stream, float* scores, int64_t windows, const float* q,
+                                                 int64_t ldq, int64_t h, int64_t w, int64_t d, const float* rh,
+                                                 const float* rw);
 
 /* ---- decode-step neighbours ---------------------------------------------------- */
 

@@ -10,6 +10,8 @@ to bf16, fp32 accumulation, bias added to the finished sum).
     a sample of rows (rows are independent, so a sampled row is checked
     exactly as in a full run) and, in full, against torch's fp32 product of
     the same bf16-rounded operands;
+  * k not a multiple of 8 (the vision encoder's convolutions over 12
+    channels: 108 columns) loads element by element, against the oracle;
   * m == 1 goes through the GEMV, bias or none, and bad shapes are refused.
 
 Tolerance: 1e-5 of the largest |y| (fp32 accumulation in another order)."""
@@ -40,7 +42,8 @@ def bf16(a):
 
 @pytest.mark.parametrize("m,k,n,with_bias", [(2, 8, 3, False), (37, 200, 70, True), (128, 128, 128, False),
                                              (129, 64, 257, True), (5, 1288, 31, False), (300, 1280, 520, True),
-                                             (64, 6848, 96, False)])
+                                             (64, 6848, 96, False), (37, 108, 16, True), (200, 12, 33, False),
+                                             (5, 3, 7, True)])
 def test_linear_against_the_oracle(backend, m, k, n, with_bias):
     x = normal(400 + m, (m, k))
     wb = bf16(0.05 * normal(401 + n, (n, k)))
@@ -71,7 +74,8 @@ def test_linear_model_shapes(backend, m, k, n):
     assert_f32_close(y.cpu().numpy(), ref.cpu().numpy(), 1e-5, f"linear full m={m} k={k} n={n}")
 
 
-@pytest.mark.parametrize("m,k,n", [(37, 200, 70), (300, 1280, 520), (129, 64, 257), (1, 128, 33), (64, 6848, 96)])
+@pytest.mark.parametrize("m,k,n", [(37, 200, 70), (300, 1280, 520), (129, 64, 257), (1, 128, 33), (64, 6848, 96),
+                                   (40, 108, 16)])
 def test_linear_bf16_x_is_linear_on_the_rounded_rows(backend, m, k, n):
     """x already bf16 (k a multiple of 64: tiles loaded straight into LDS;
     otherwise staged): the same sums as linear on the fp32 rows."""
@@ -79,9 +83,12 @@ def test_linear_bf16_x_is_linear_on_the_rounded_rows(backend, m, k, n):
     wb = bf16(0.05 * normal(421 + n, (n, k)))
     bias = normal(422, n)
     want = oracle.linear(oracle.bf16_round(x), oracle.bf16_to_f32(wb), bias)
-    xb = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
-    backend.round_bf16(dev_f32(x), xb)
-    assert np.array_equal(xb.view(torch.int16).cpu().numpy().view(np.uint16), bf16(x))  # nearest even
+    if k % 8 == 0:
+        xb = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
+        backend.round_bf16(dev_f32(x), xb)
+        assert np.array_equal(xb.view(torch.int16).cpu().numpy().view(np.uint16), bf16(x))  # nearest even
+    else:
+        xb = dev_bf16(bf16(x))
     y = torch.full((m, n), float("nan"), device="cuda")
     backend.linear(xb, dev_bf16(wb), y, dev_f32(bias))
     assert_f32_close(host_f32(y), want, 1e-5, f"linear bf16 x m={m} k={k} n={n}")
@@ -103,10 +110,10 @@ def test_linear_one_row_is_the_gemv(backend):
 
 
 def test_linear_rejects_bad_shapes(backend):
-    x = torch.zeros(4, 12, device="cuda")
-    w = torch.zeros(3, 12, dtype=torch.bfloat16, device="cuda")
+    x = torch.zeros(4, 0, device="cuda")
+    w = torch.zeros(3, 0, dtype=torch.bfloat16, device="cuda")
     y = torch.empty(4, 3, device="cuda")
-    with pytest.raises(ValueError):  # k not a multiple of 8
+    with pytest.raises(ValueError):  # k = 0
         backend.linear(x, w, y)
     x = torch.zeros(4, 17, device="cuda")[:, 1:].contiguous()
     w = torch.zeros(3, 16, dtype=torch.bfloat16, device="cuda")

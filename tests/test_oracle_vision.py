@@ -316,3 +316,32 @@ def test_device_rounding_stays_within_the_references_bf16_bar(orc, tiny):
     a, b = m.encode_page(img, round_x=False), m.encode_page(img, round_x=True)
     err = np.max(np.abs(a - b)) / np.max(np.abs(a))
     assert 0 < err < 2e-2
+
+
+def test_structural_slips_exceed_the_encoder_bar(orc):
+    """The encoder's device bars (1e-2 of the rounded oracle, 2e-2 of the CPU
+    arithmetic, at the largest feature) have teeth: on the real widths (2 + 2
+    layers, a 256-pixel view) dropping the relative-position tables, making
+    the windowed block global, or skipping a CLIP layer each move the
+    features by more than 3e-2."""
+    sam = dict(image=1024, patch=16, width=768, layers=2, heads=12, mlp=3072, window=14, global_layers=(1,),
+               neck=256, net2=512, net3=1024)
+    clip = dict(width=1024, layers=2, heads=16, mlp=4096, positions=257)
+    g = rng(40)
+    w = {}
+    for name, shape in orc.vision_tensor_shapes(sam, clip, 1280).items():
+        fan = int(np.prod(shape[1:])) if len(shape) in (2, 4) else 1
+        scale = min(0.05, 1 / np.sqrt(fan)) if len(shape) in (2, 4) and "pos" not in name else 0.05
+        v = (scale * g.standard_normal(shape)).astype(np.float32)
+        w[name] = orc.bf16_round(v + 1 if "norm" in name and name.endswith(".weight") else v)
+    img = image(256, 41)
+    base = orc.VisionModel(w, sam, clip, 1280).encode_view(img)
+
+    def moved(weights, s=sam, c=clip):
+        got = orc.VisionModel(weights, s, c, 1280).encode_view(img)
+        return np.max(np.abs(got - base)) / np.max(np.abs(base))
+
+    no_rel = {k: (np.zeros_like(v) if "rel_pos" in k else v) for k, v in w.items()}
+    assert moved(no_rel) > 3e-2
+    assert moved(w, s=dict(sam, global_layers=(0, 1))) > 3e-2
+    assert moved(w, c=dict(clip, layers=1)) > 3e-2
