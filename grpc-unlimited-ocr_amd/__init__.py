@@ -149,6 +149,8 @@ _SIGNATURES = {
     "uocr_rocm_chw_to_hwc": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_hwc_to_chw": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_concat_cols": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp], _int),
+    "uocr_rocm_split_heads": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
+    "uocr_rocm_merge_heads": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_rel_pos_bias": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp], _int),
     "uocr_rocm_rel_pos_softmax_rows": ([_vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp], _int),
     "uocr_rocm_append_step": ([_vp, _vp, _vp, _i64, _vp, _i64], _int),
@@ -552,6 +554,17 @@ def hwc_to_chw(x, y, stream=None):
 def concat_cols(a, b, out, stream=None):
     """out[r] = a[r] | b[r]. Reference: concat_cols, ops.h:65-67."""
     _op("uocr_rocm_concat_cols", stream, _ptr(a), a.shape[-1], _ptr(b), b.shape[-1], a.shape[0], _ptr(out))
+
+
+def split_heads(x, parts, heads, hd, y, stream=None):
+    """y [parts, heads, rows, hd] = x [rows, parts * heads * hd] (new)."""
+    _op("uocr_rocm_split_heads", stream, _ptr(x), x.shape[0], parts, heads, hd, _ptr(y))
+
+
+def merge_heads(x, y, stream=None):
+    """y [rows, heads * hd] = x [heads, rows, hd] (new)."""
+    heads, rows, hd = x.shape
+    _op("uocr_rocm_merge_heads", stream, _ptr(x), heads, rows, hd, _ptr(y))
 
 
 def rel_pos_bias(q, ldq, h, w, d, rh, rw, bias, q_offset=0, stream=None):

@@ -113,6 +113,17 @@ int uocr_rocm_stream_create(int device, void** stream) {
   UOCR_REQUIRE(device >= 0 && device < n, "uocr_rocm_stream_create", "device index out of range");
   int st = check_hip(hipSetDevice(device), "hipSetDevice");
   if (st) return st;
+  // The device pool keeps the blocks Arrays give back instead of returning
+  // them to the driver (its default threshold is 0): a model's per-call
+  // buffers (a vision layer's scores are 0.8 GB) are taken again at once
+  // rather than mapped anew each time. 288 GB of HBM leaves room for it.
+  hipMemPool_t pool = nullptr;
+  if ((st = check_hip(hipDeviceGetDefaultMemPool(&pool, device), "hipDeviceGetDefaultMemPool"))) return st;
+  uint64_t keep = UINT64_MAX;
+  if ((st = check_hip(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep),
+                      "hipMemPoolSetAttribute"))) {
+    return st;
+  }
   hipStream_t s = nullptr;
   // Default priority only: streams of mixed priorities are not used here.
   if ((st = check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags"))) return st;

@@ -20,6 +20,14 @@
 // are written as sums of two of them. The reference's two kernels through a
 // scratch buffer become one launch that allocates nothing.
 //
+// split_heads / merge_heads: the attention's operands between the rows the
+// projections write, x [rows, parts * heads * hd] (parts = 3 for q | k | v),
+// and a head-major layout y [parts, heads, rows, hd], and the heads' outputs
+// back: with every head's (and every window's) rows contiguous, one batched
+// product covers all heads and windows (batch index head * windows + window,
+// one stride) instead of one launch per head. 16-byte chunks, both sides
+// row-contiguous; exact.
+//
 // rel_pos_softmax_rows: the SAM attention's scores of every window of one
 // head, s [windows * n, n], replaced by softmax(s + bias) row by row with
 // the bias formed as above inside the row's workgroup: the reference's
@@ -202,6 +210,36 @@ __global__ __launch_bounds__(kBlock) void rel_pos_softmax_wide_k(float* __restri
   }
 }
 
+// y [parts, heads, rows, hd] = x [rows, parts, heads, hd]; hd % 4 == 0.
+__global__ __launch_bounds__(kBlock) void split_heads_k(const float* __restrict__ x, int64_t rows, int parts_heads,
+                                                         int hd4, float* __restrict__ y) {
+  const int64_t row_chunks = static_cast<int64_t>(parts_heads) * hd4, total = rows * row_chunks;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kBlock) {
+    const int64_t r = i / row_chunks;
+    const int rem = static_cast<int>(i - r * row_chunks), ph = rem / hd4, e = rem - ph * hd4;
+    const u32x4 v = reinterpret_cast<const u32x4*>(x)[i];
+    reinterpret_cast<u32x4*>(y)[(static_cast<int64_t>(ph) * rows + r) * hd4 + e] = v;
+  }
+}
+
+// y [rows, heads, hd] = x [heads, rows, hd]; hd % 4 == 0.
+__global__ __launch_bounds__(kBlock) void merge_heads_k(const float* __restrict__ x, int heads, int64_t rows, int hd4,
+                                                         float* __restrict__ y) {
+  const int64_t row_chunks = static_cast<int64_t>(heads) * hd4, total = rows * row_chunks;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kBlock) {
+    const int64_t r = i / row_chunks;
+    const int rem = static_cast<int>(i - r * row_chunks), h = rem / hd4, e = rem - h * hd4;
+    reinterpret_cast<u32x4*>(y)[i] = reinterpret_cast<const u32x4*>(x)[(static_cast<int64_t>(h) * rows + r) * hd4 + e];
+  }
+}
+
+unsigned flat_grid(int64_t chunks) {
+  const int64_t b = (chunks + kBlock - 1) / kBlock;
+  return static_cast<unsigned>(b < (int64_t{1} << 20) ? (b > 0 ? b : 1) : (int64_t{1} << 20));
+}
+
 unsigned row_grid(int64_t rows) { return static_cast<unsigned>(rows < (int64_t{1} << 20) ? rows : (int64_t{1} << 20)); }
 
 int transpose_entry(const char* what, void* stream, const float* x, int64_t a, int64_t b, float* y) {
@@ -262,6 +300,35 @@ int uocr_rocm_concat_cols(void* stream, const float* a, int64_t ca, const float*
   UOCR_REQUIRE(out != nullptr && (ca == 0 || a != nullptr) && (cb == 0 || b != nullptr), kWhat, "null pointer");
   clear_launch_error();
   concat_cols_k<<<row_grid(rows), kBlock, 0, as_stream(stream)>>>(a, ca, b, cb, rows, out);
+  return check_launch(kWhat);
+}
+
+int uocr_rocm_split_heads(void* stream, const float* x, int64_t rows, int64_t parts, int64_t heads, int64_t hd,
+                          float* y) {
+  constexpr const char* kWhat = "uocr_rocm_split_heads";
+  UOCR_REQUIRE(rows >= 0 && parts >= 1 && heads >= 1 && hd >= 4 && hd % 4 == 0, kWhat,
+               "need rows >= 0, parts and heads >= 1, hd a multiple of 4");
+  UOCR_REQUIRE(parts * heads < (1 << 20) && hd < (1 << 20), kWhat, "too many heads or too wide");
+  if (rows == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(x != nullptr && y != nullptr, kWhat, "null pointer");
+  UOCR_REQUIRE(aligned16(x) && aligned16(y), kWhat, "x and y must be 16-byte aligned");
+  clear_launch_error();
+  split_heads_k<<<flat_grid(rows * parts * heads * hd / 4), kBlock, 0, as_stream(stream)>>>(
+      x, rows, static_cast<int>(parts * heads), static_cast<int>(hd / 4), y);
+  return check_launch(kWhat);
+}
+
+int uocr_rocm_merge_heads(void* stream, const float* x, int64_t heads, int64_t rows, int64_t hd, float* y) {
+  constexpr const char* kWhat = "uocr_rocm_merge_heads";
+  UOCR_REQUIRE(rows >= 0 && heads >= 1 && hd >= 4 && hd % 4 == 0, kWhat,
+               "need rows >= 0, heads >= 1, hd a multiple of 4");
+  UOCR_REQUIRE(heads < (1 << 20) && hd < (1 << 20), kWhat, "too many heads or too wide");
+  if (rows == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(x != nullptr && y != nullptr, kWhat, "null pointer");
+  UOCR_REQUIRE(aligned16(x) && aligned16(y), kWhat, "x and y must be 16-byte aligned");
+  clear_launch_error();
+  merge_heads_k<<<flat_grid(rows * heads * hd / 4), kBlock, 0, as_stream(stream)>>>(
+      x, static_cast<int>(heads), rows, static_cast<int>(hd / 4), y);
   return check_launch(kWhat);
 }
 

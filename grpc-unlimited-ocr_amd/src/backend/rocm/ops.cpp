@@ -180,6 +180,15 @@ void concat_cols(const Context& ctx, const float* a, std::int64_t ca, const floa
   check(uocr_rocm_concat_cols(ctx.stream(), a, ca, b, cb, rows, out));
 }
 
+void split_heads(const Context& ctx, const float* x, std::int64_t rows, std::int64_t parts, std::int64_t heads,
+                 std::int64_t hd, float* y) {
+  check(uocr_rocm_split_heads(ctx.stream(), x, rows, parts, heads, hd, y));
+}
+
+void merge_heads(const Context& ctx, const float* x, std::int64_t heads, std::int64_t rows, std::int64_t hd, float* y) {
+  check(uocr_rocm_merge_heads(ctx.stream(), x, heads, rows, hd, y));
+}
+
 void rel_pos_bias(const Context& ctx, const float* q, std::int64_t ldq, std::int64_t h, std::int64_t w, std::int64_t d,
                   const float* rh, const float* rw, float* bias) {
   check(uocr_rocm_rel_pos_bias(ctx.stream(), q, ldq, h, w, d, rh, rw, bias));

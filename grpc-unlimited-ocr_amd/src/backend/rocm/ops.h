@@ -137,6 +137,11 @@ void chw_to_hwc(const Context& ctx, const float* x, std::int64_t c, std::int64_t
 void hwc_to_chw(const Context& ctx, const float* x, std::int64_t h, std::int64_t w, std::int64_t c, float* y);
 void concat_cols(const Context& ctx, const float* a, std::int64_t ca, const float* b, std::int64_t cb, std::int64_t rows,
                  float* out);
+// New: attention operands to a head-major layout, y [parts, heads, rows, hd]
+// from x [rows, parts * heads * hd], and the heads' outputs back to rows.
+void split_heads(const Context& ctx, const float* x, std::int64_t rows, std::int64_t parts, std::int64_t heads,
+                 std::int64_t hd, float* y);
+void merge_heads(const Context& ctx, const float* x, std::int64_t heads, std::int64_t rows, std::int64_t hd, float* y);
 // SAM's relative-position bias of one window and head, bias[t, ky w + kx] =
 // q_t . rh[qy, ky] + q_t . rw[qx, kx]; and (new) the scores of every window
 // of one head replaced by softmax(scores + that bias) in one pass.

@@ -239,10 +239,13 @@ const VisionEncoder::Windows& VisionEncoder::windows(std::int64_t g) const {
 }
 
 // Attention of one block over `windows` windows of h x w tokens, rows
-// window-major in x [windows * h * w, width]: per head the scores of every
-// window in one batched product, the relative-position bias and softmax in
-// one pass, the values' product into the head's columns; then the output
-// projection (cuda_vision.cpp:151-172).
+// window-major in x [windows * h * w, width] (cuda_vision.cpp:151-172).
+// With the head dim a multiple of 4 the operands go head-major
+// ([3, heads, rows, hd]) and every (head, window) pair is one slice of one
+// batched product: the scores, the relative-position bias + softmax and
+// the values' product are three launches for the whole layer, whose grids
+// cover the GPU even for one 64 x 64 global window. Otherwise head by head
+// over all windows, as the reference does.
 void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_t windows, std::int64_t h,
                                   std::int64_t w, float* out) const {
   const auto& b = w_.sam_blocks[index];
@@ -251,14 +254,26 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_
   linear(ctx_, x, rows, c, b.qkv, 3 * c, b.qkv_b, qkv.f32());
   const Array& rh = rel_table(index, true, h);
   const Array& rw = rel_table(index, false, w);
-  Array scores = f32(ctx_, windows * n * n), merged = f32(ctx_, rows * c);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
-  for (std::int64_t head = 0; head < heads; ++head) {
-    const float* q = qkv.f32() + head * hd;
-    gemm_nt(ctx_, n, n, hd, scale, q, 3 * c, n * 3 * c, q + c, 3 * c, n * 3 * c, scores.f32(), n, n * n, windows);
-    rel_pos_softmax_rows(ctx_, scores.f32(), windows, q, 3 * c, h, w, hd, rh.f32(), rw.f32());
-    gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, q + 2 * c, 3 * c, n * 3 * c, merged.f32() + head * hd, c, n * c,
-            windows);
+  Array merged = f32(ctx_, rows * c);
+  if (hd % 4 == 0) {
+    const std::int64_t slices = heads * windows, part = heads * rows * hd;
+    Array split = f32(ctx_, 3 * part), o = f32(ctx_, part), scores = f32(ctx_, slices * n * n);
+    split_heads(ctx_, qkv.f32(), rows, 3, heads, hd, split.f32());
+    const float* q = split.f32();
+    gemm_nt(ctx_, n, n, hd, scale, q, hd, n * hd, q + part, hd, n * hd, scores.f32(), n, n * n, slices);
+    rel_pos_softmax_rows(ctx_, scores.f32(), slices, q, hd, h, w, hd, rh.f32(), rw.f32());
+    gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, q + 2 * part, hd, n * hd, o.f32(), hd, n * hd, slices);
+    merge_heads(ctx_, o.f32(), heads, rows, hd, merged.f32());
+  } else {
+    Array scores = f32(ctx_, windows * n * n);
+    for (std::int64_t head = 0; head < heads; ++head) {
+      const float* q = qkv.f32() + head * hd;
+      gemm_nt(ctx_, n, n, hd, scale, q, 3 * c, n * 3 * c, q + c, 3 * c, n * 3 * c, scores.f32(), n, n * n, windows);
+      rel_pos_softmax_rows(ctx_, scores.f32(), windows, q, 3 * c, h, w, hd, rh.f32(), rw.f32());
+      gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, q + 2 * c, 3 * c, n * 3 * c, merged.f32() + head * hd, c,
+              n * c, windows);
+    }
   }
   linear(ctx_, merged.f32(), rows, c, b.proj, c, b.proj_b, out);
 }
@@ -339,15 +354,26 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
   add_inplace(ctx_, x.f32(), clip_positions(g).f32(), n * c);
   layer_norm(ctx_, x.f32(), w_.pre_ln_w, w_.pre_ln_b, n, c, kClipEps);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  const bool split = hd % 4 == 0;  // head-major operands, as in sam_attention
   Array normed = f32(ctx_, n * c), qkv = f32(ctx_, n * 3 * c), scores = f32(ctx_, heads * n * n);
   Array merged = f32(ctx_, n * c), proj = f32(ctx_, n * c), wide = f32(ctx_, n * cd.mlp);
+  Array hm = f32(ctx_, split ? 3 * n * c : 1), o = f32(ctx_, split ? n * c : 1);
   for (const auto& l : w_.clip_layers) {
     copy(ctx_, normed.f32(), x.f32(), n * c);
     layer_norm(ctx_, normed.f32(), l.ln1_w, l.ln1_b, n, c, kClipEps);
     linear(ctx_, normed.f32(), n, c, l.qkv, 3 * c, l.qkv_b, qkv.f32());
-    gemm_nt(ctx_, n, n, hd, scale, qkv.f32(), 3 * c, hd, qkv.f32() + c, 3 * c, hd, scores.f32(), n, n * n, heads);
-    softmax_rows(ctx_, scores.f32(), heads * n, n);
-    gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, qkv.f32() + 2 * c, 3 * c, hd, merged.f32(), c, hd, heads);
+    if (split) {
+      split_heads(ctx_, qkv.f32(), n, 3, heads, hd, hm.f32());
+      const float* q = hm.f32();
+      gemm_nt(ctx_, n, n, hd, scale, q, hd, n * hd, q + n * c, hd, n * hd, scores.f32(), n, n * n, heads);
+      softmax_rows(ctx_, scores.f32(), heads * n, n);
+      gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, q + 2 * n * c, hd, n * hd, o.f32(), hd, n * hd, heads);
+      merge_heads(ctx_, o.f32(), heads, n, hd, merged.f32());
+    } else {
+      gemm_nt(ctx_, n, n, hd, scale, qkv.f32(), 3 * c, hd, qkv.f32() + c, 3 * c, hd, scores.f32(), n, n * n, heads);
+      softmax_rows(ctx_, scores.f32(), heads * n, n);
+      gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, qkv.f32() + 2 * c, 3 * c, hd, merged.f32(), c, hd, heads);
+    }
     linear(ctx_, merged.f32(), n, c, l.out, c, l.out_b, proj.f32());
     add_inplace(ctx_, x.f32(), proj.f32(), n * c);
     copy(ctx_, normed.f32(), x.f32(), n * c);

@@ -364,6 +364,18 @@ UOCR_ROCM_API int uocr_rocm_hwc_to_chw(void* stream, const float* x, int64_t h, 
 UOCR_ROCM_API int uocr_rocm_concat_cols(void* stream, const float* a, int64_t ca, const float* b, int64_t cb,
                                         int64_t rows, float* out);
 
+/* New: y [parts, heads, rows, hd] = x [rows, parts, heads, hd] and y [rows,
+ * heads, hd] = x [heads, rows, hd] (fp32, hd a multiple of 4, 16-byte
+ * aligned, exact): the attention operands in a head-major layout, so that
+ * one batched product covers every head (and window) with one stride, and
+ * the heads' outputs back to rows. No counterpart in the reference, which
+ * launches its products head by head (src/model/cuda/cuda_vision.cpp:
+ * 159-170, 252-254). */
+UOCR_ROCM_API int uocr_rocm_split_heads(void* stream, const float* x, int64_t rows, int64_t parts, int64_t heads,
+                                        int64_t hd, float* y);
+UOCR_ROCM_API int uocr_rocm_merge_heads(void* stream, const float* x, int64_t heads, int64_t rows, int64_t hd,
+                                        float* y);
+
 /* SAM's decomposed relative-position bias for one head of one window:
  * bias[t, ky * w + kx] = q_t . rh[qy, ky] + q_t . rw[qx, kx] for query t =
  * qy * w + qx, q rows ldq apart, rh [h, h, d], rw [w, w, d], bias [h w, h w].

@@ -1,7 +1,8 @@
 """GPU parity for the vision encoder's ops (csrc/vision.hip) through the C
 ABI, against the oracle (oracle/uocr_oracle_vision.c):
 
-  * im2col, chw_to_hwc, hwc_to_chw and concat_cols are data movement:
+  * im2col, chw_to_hwc, hwc_to_chw, concat_cols, split_heads and
+    merge_heads are data movement:
     bit-exact, over the encoder's shapes (the 16 x 16 patch embedding, the
     padded stride-1 and stride-2 3 x 3 convolutions) and ragged ones;
   * rel_pos_bias at 1e-5 of the largest |bias| (fp32 dot products, fused
@@ -136,3 +137,15 @@ def test_cpp_rocm_vision_test(backend):
     r = subprocess.run([binary], capture_output=True, text=True, timeout=110)
     sys.stdout.write(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.parametrize("rows,parts,heads,hd", [(4900, 3, 12, 64), (65, 3, 16, 64), (7, 1, 2, 12), (3, 2, 5, 4)])
+def test_split_and_merge_heads_are_exact(backend, rows, parts, heads, hd):
+    x = normal(660 + rows, (rows, parts * heads * hd))
+    y = torch.full((parts, heads, rows, hd), float("nan"), device="cuda")
+    backend.split_heads(dev_f32(x), parts, heads, hd, y)
+    want = x.reshape(rows, parts, heads, hd).transpose(1, 2, 0, 3)
+    assert np.array_equal(host_f32(y), want)
+    back = torch.full((rows, heads * hd), float("nan"), device="cuda")
+    backend.merge_heads(y[parts - 1].contiguous(), back)
+    assert np.array_equal(host_f32(back), x.reshape(rows, parts, heads * hd)[:, parts - 1])
