@@ -23,6 +23,12 @@ norm weights; names and sizes follow the reference's headline op set):
   8  the prefill pass's projections on the matrix cores for a 4096-token
      prompt at the decoder's shapes (bf16 activations and weights, fp32
      sums): TFLOP/s and fraction of the 2.5 PFLOP/s dense bf16 peak
+  9  the vision encoder on one 1024-pixel view (SAM ViT-B: 12 blocks, 8 in
+     14 x 14 windows and 4 global over 64 x 64 tokens, neck and stride-2
+     convolutions; CLIP-L: 24 layers over 257 tokens; projector to 1280),
+     random bf16 weights: ms per view and TFLOP/s of its products, timed by
+     the C++ encoder (tests/cpp/rocm_vision_test.cpp --time) in a child
+     process
 
 One step = one pass of a workload's op chain over one input set. The JSON
 line's `value` is workload 5 (the largest, three fused ops timed as one
@@ -58,6 +64,7 @@ import json
 import math
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -591,6 +598,24 @@ def config8(be, torch, timer):
             "kernels": kern}
 
 
+def config9(be, torch, timer):
+    """The vision encoder (src/model/rocm/vision.cpp) on one 1024-pixel view
+    at the model's dims with random weights: the C++ encoder times 5 calls
+    of encode_view (device image in, device features out) after 2 untimed
+    ones, in a child process (it holds its own 0.8 GB of weights)."""
+    binary = os.path.join(os.path.dirname(be.LIB_PATH), "rocm_vision_test")
+    r = subprocess.run([binary, "--time", "1024", "5"], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        raise RuntimeError(f"rocm_vision_test --time failed ({r.returncode}): {r.stderr[-2000:]}")
+    fig = json.loads(r.stdout.strip().splitlines()[-1])
+    return {"workload": "vision encoder, one 1024-pixel view: SAM ViT-B (12 blocks) + neck + CLIP-L (24 layers) + "
+                        "projector to 1280, bf16 weights, fp32 activations",
+            "step": {"us": round(fig["ms_per_view"] * 1e3, 1), "ms_per_view": fig["ms_per_view"],
+                     "tflop": fig["tflop_per_view"], "tflops": fig["tflops"],
+                     "frac": round(fig["tflops"] / PEAK_BF16_TFLOPS, 4), "bound": "mfma"},
+            "kernels": {}}
+
+
 def expert_ffn(be, torch, timer, hidden, ffn, experts, k):
     """The routed experts of one decode row (expert_ffn_one) on the model's
     MoE shape: 6 of 64 experts of FFN 896 at hidden 1280, stacks of 440 MB
@@ -984,7 +1009,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="copy,1,2,3,4,5,6,7,8")
+    ap.add_argument("--configs", default="copy,1,2,3,4,5,6,7,8,9")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly (for counter collection)")
@@ -1014,7 +1039,7 @@ def main():
     info = be.device_info(0)
     timer = Timer(torch, args.steps, args.warmup, use_graphs=not args.no_graph)
     runners = {"1": config1, "2": config2, "3": config3, "4": config4, "5": config5, "6": config6, "7": config7,
-               "8": config8, "copy": calibration}
+               "8": config8, "9": config9, "copy": calibration}
     configs = {}
     for c in args.configs.split(","):
         t0 = time.time()
