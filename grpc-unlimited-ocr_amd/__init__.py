@@ -149,6 +149,10 @@ _SIGNATURES = {
     "uocr_rocm_chw_to_hwc": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_hwc_to_chw": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_concat_cols": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp], _int),
+    "uocr_rocm_attention": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
+                             _i64, _i64, _f32, _vp, _i64], _int),
+    "uocr_rocm_attention_rel_pos": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                                     _i64, _i64, _i64, _f32, _vp, _vp], _int),
     "uocr_rocm_split_heads": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_merge_heads": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_rel_pos_bias": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp], _int),
@@ -554,6 +558,34 @@ def hwc_to_chw(x, y, stream=None):
 def concat_cols(a, b, out, stream=None):
     """out[r] = a[r] | b[r]. Reference: concat_cols, ops.h:65-67."""
     _op("uocr_rocm_concat_cols", stream, _ptr(a), a.shape[-1], _ptr(b), b.shape[-1], a.shape[0], _ptr(out))
+
+
+def _operand(t, offset, ld, slice_stride):
+    return (_ptr(t) + 4 * offset, ld, slice_stride)
+
+
+def attention(q, k, v, out, slices, rows, keys, hd, scale, mask=None, strides=None, stream=None):
+    """out[s, t] = softmax(scale q[s, t] . k[s, :] + mask[t, :]) v[s, :] in one
+    pass (new). strides: {name: (offset, ld, slice_stride)} for q, k, v, out
+    (elements); default head-major [slices, rows or keys, hd]."""
+    st = strides or {}
+    qo = _operand(q, *st.get("q", (0, hd, rows * hd)))
+    ko = _operand(k, *st.get("k", (0, hd, keys * hd)))
+    vo = _operand(v, *st.get("v", (0, hd, keys * hd)))
+    oo = _operand(out, *st.get("out", (0, hd, rows * hd)))
+    _op("uocr_rocm_attention", stream, *qo, *ko, *vo, *oo, slices, rows, keys, hd, scale, _f32_param(mask),
+        0 if mask is None else mask.shape[-1])
+
+
+def attention_rel_pos(q, k, v, out, slices, h, w, hd, scale, rh, rw, strides=None, stream=None):
+    """attention over h x w windows with SAM's relative-position bias (new)."""
+    n = h * w
+    st = strides or {}
+    qo = _operand(q, *st.get("q", (0, hd, n * hd)))
+    ko = _operand(k, *st.get("k", (0, hd, n * hd)))
+    vo = _operand(v, *st.get("v", (0, hd, n * hd)))
+    oo = _operand(out, *st.get("out", (0, hd, n * hd)))
+    _op("uocr_rocm_attention_rel_pos", stream, *qo, *ko, *vo, *oo, slices, h, w, hd, scale, _ptr(rh), _ptr(rw))
 
 
 def split_heads(x, parts, heads, hd, y, stream=None):

@@ -1,0 +1,338 @@
+// attention.hip: softmax attention over fp32 rows in one pass for gfx950,
+// on the fp32 matrix cores (v_mfma_f32_32x32x2f32): for every slice s
+// (a head, or a head of one window) and query row t
+//   out[s, t] = softmax_k(scale * q[s, t] . k[s, k] + bias[t, k]) . v[s, k]
+// with bias none, a mask [rows, keys] shared by the slices (the decoder's
+// prefill: the routed key mask, -inf where a key is not attended), or SAM's
+// decomposed relative-position bias dh[t, ky] + dw[t, kx] (key = ky * w +
+// kx). It replaces the reference's scores product, bias, row softmax and
+// values product (src/model/cuda/cuda_vision.cpp:159-170,251-254,
+// src/model/cuda/cuda_decoder.cpp:88-105): the scores never reach memory.
+//
+// A workgroup of 4 waves (2 with the relative-position bias) takes 128 (64)
+// query rows of one slice; each wave owns 32 of them and walks the keys 32
+// at a time, the key and value tiles staged in LDS for the workgroup (the
+// next tile's loads in flight in registers while the current one is used). Per tile a wave forms S^T = K Q^T (32 keys x 32
+// queries, hd / 2 products, each summing 2 of the head's columns: lane half
+// h supplies column h * hd / 2 + i to product i, so a lane keeps its query's
+// half row in registers and reads its key's half row from LDS), which leaves
+// lane l holding query l % 32's scores for 16 of the 32 keys (8 (r / 4) + 4 h
+// + r % 4 in register r) and the other 16 in lane l ^ 32. The running max,
+// rescale and sum are per lane plus one exchange with the partner lane. The
+// values' product O^T += V^T P^T takes the probabilities straight from those
+// registers: product i sums keys 8 (i / 4) + r % 4 + 4 h, exactly the keys
+// register i holds, so P needs no movement; each 32 columns of the head are
+// 16 products into 16 accumulators.
+//
+// Arithmetic: fp32 products and sums on the matrix cores; the scores are
+// scaled, then the bias added (the reference's order); e = exp(s - running
+// max) with the running sum and the output rescaled when the max grows;
+// out = O * (1 / sum); a row with no finite score gives zeros, as the
+// reference's softmax does. The sums run in another order than the
+// reference's row softmax and products, so results agree to fp32 rounding.
+
+#include "common.hpp"
+
+namespace uocr_rocm {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+enum class Bias { kNone, kMask, kRelPos };
+constexpr int kQueriesPerWave = 32;
+constexpr int kKeyTile = 32;
+// Waves per workgroup: 4 (128 query rows share each key/value tile), or 2
+// with the relative-position bias, whose per-query dot products take LDS
+// (2 waves keep three workgroups on a CU instead of one).
+template <Bias kBias>
+constexpr int waves_of() {
+  return kBias == Bias::kRelPos ? 2 : 4;
+}
+constexpr int kMaxRelSpan = 256;  // h + w of the relative-position bias
+
+struct AttnArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* out;
+  int64_t ldq, sq, ldk, sk, ldv, sv, ldo, so;  // row and slice strides (elements)
+  int rows, keys;
+  float scale;
+  const float* mask;  // [rows, mask_ld] (kMask)
+  int64_t mask_ld;
+  const float* rh;  // [h, h, hd] (kRelPos)
+  const float* rw;  // [w, w, hd]
+  int h, w;
+};
+
+template <int HD, int kThreads>
+struct Tile {
+  static constexpr int kChunks = kKeyTile * HD / 4;           // float4 chunks of one operand tile
+  static constexpr int kPerThread = kChunks / kThreads;       // 2 to 8
+  static constexpr int kKStride = HD + 4;                     // padded K rows: 16-lane reads conflict-free
+};
+
+template <int HD, int kThreads>
+__device__ __forceinline__ void load_tile(const AttnArgs& a, const float* kb, const float* vb, int key0,
+                                          float4 (&kr)[Tile<HD, kThreads>::kPerThread],
+                                          float4 (&vr)[Tile<HD, kThreads>::kPerThread]) {
+#pragma unroll
+  for (int j = 0; j < Tile<HD, kThreads>::kPerThread; ++j) {
+    const int idx = static_cast<int>(threadIdx.x) + kThreads * j;
+    const int row = idx / (HD / 4), c4 = idx % (HD / 4);
+    const int key = key0 + row;
+    kr[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    vr[j] = kr[j];
+    if (key < a.keys) {
+      kr[j] = *reinterpret_cast<const float4*>(kb + key * a.ldk + 4 * c4);
+      vr[j] = *reinterpret_cast<const float4*>(vb + key * a.ldv + 4 * c4);
+    }
+  }
+}
+
+template <int HD, int kThreads>
+__device__ __forceinline__ void store_tile(float* ks, float* vs, const float4 (&kr)[Tile<HD, kThreads>::kPerThread],
+                                           const float4 (&vr)[Tile<HD, kThreads>::kPerThread]) {
+#pragma unroll
+  for (int j = 0; j < Tile<HD, kThreads>::kPerThread; ++j) {
+    const int idx = static_cast<int>(threadIdx.x) + kThreads * j;
+    const int row = idx / (HD / 4), c4 = idx % (HD / 4);
+    *reinterpret_cast<float4*>(ks + row * Tile<HD, kThreads>::kKStride + 4 * c4) = kr[j];
+    *reinterpret_cast<float4*>(vs + row * HD + 4 * c4) = vr[j];
+  }
+}
+
+__device__ __forceinline__ float partner(float v) { return __shfl_xor(v, 32); }
+
+template <int HD, Bias kBias>
+__global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const AttnArgs a) {
+  constexpr int kThreads = 64 * waves_of<kBias>();
+  constexpr int kQueriesPerBlock = waves_of<kBias>() * kQueriesPerWave;
+  using T = Tile<HD, kThreads>;
+  constexpr int kHalf = HD / 2;  // columns per lane half in the scores' products
+  constexpr int kDBlocks = HD / 32;
+  __shared__ __attribute__((aligned(16))) float ks[kKeyTile * T::kKStride];
+  __shared__ __attribute__((aligned(16))) float vs[kKeyTile * HD];
+  // kRelPos: per query row its h + w dot products, rows h + w + 1 apart so
+  // that the 32 queries of a wave read 32 different banks
+  extern __shared__ float dots[];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, c = lane & 31;
+  const int64_t slice = blockIdx.y;
+  const int q0 = blockIdx.x * kQueriesPerBlock + wave * kQueriesPerWave;
+  const int qrow = q0 + c;
+  const bool qin = qrow < a.rows;
+  const float* qb = a.q + slice * a.sq;
+  const float* kb = a.k + slice * a.sk;
+  const float* vb = a.v + slice * a.sv;
+
+  // the first tile's loads go out first
+  float4 kr[T::kPerThread], vr[T::kPerThread];
+  load_tile<HD, kThreads>(a, kb, vb, 0, kr, vr);
+
+  // this lane's half of its query row
+  float qv[kHalf];
+#pragma unroll
+  for (int i = 0; i < kHalf; i += 4) {
+    float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (qin) t = *reinterpret_cast<const float4*>(qb + qrow * a.ldq + hl * kHalf + i);
+    qv[i] = t.x;
+    qv[i + 1] = t.y;
+    qv[i + 2] = t.z;
+    qv[i + 3] = t.w;
+  }
+
+  float* my_dots = dots + (wave * kQueriesPerWave + c) * (a.h + a.w + 1);
+  if constexpr (kBias == Bias::kRelPos) {
+    // dh[ky] = q . rh[qy, ky] (lane half 0) and dw[kx] = q . rw[qx, kx]
+    // (half 1), fp32 in column order, over the whole query row
+    const int qy = qin ? qrow / a.w : 0, qx = qin ? qrow - qy * a.w : 0;
+    const float* qr = qb + (qin ? qrow : 0) * a.ldq;
+    const int n_dots = hl == 0 ? a.h : a.w;
+    const float* tab = hl == 0 ? a.rh + static_cast<int64_t>(qy) * a.h * HD : a.rw + static_cast<int64_t>(qx) * a.w * HD;
+    for (int j = 0; j < n_dots; ++j) {
+      float s = 0.0f;
+      for (int e = 0; e < HD; ++e) s += qr[e] * tab[j * HD + e];
+      my_dots[(hl == 0 ? 0 : a.h) + j] = s;
+    }
+  }
+
+  store_tile<HD, kThreads>(ks, vs, kr, vr);
+  __syncthreads();
+
+  f32x16 o[kDBlocks];
+#pragma unroll
+  for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] = 0.0f;
+  }
+  float m = -INFINITY, l = 0.0f;
+  const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
+  for (int t = 0; t < tiles; ++t) {
+    const int key0 = t * kKeyTile;
+    const bool more = t + 1 < tiles;
+    if (more) load_tile<HD, kThreads>(a, kb, vb, key0 + kKeyTile, kr, vr);
+
+    // S^T = K Q^T: 32 keys x 32 queries
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+    const float* krow = ks + c * T::kKStride + hl * kHalf;
+#pragma unroll
+    for (int i = 0; i < kHalf; i += 4) {
+      const float4 kk = *reinterpret_cast<const float4*>(krow + i);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.x, qv[i], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.y, qv[i + 1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.z, qv[i + 2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.w, qv[i + 3], s, 0, 0, 0);
+    }
+
+    // scale, bias, running max
+    float tmax = -INFINITY;
+    int ky0 = 0, kx0 = 0;
+    if constexpr (kBias == Bias::kRelPos) {
+      ky0 = key0 / a.w;  // once per tile; the lane's keys step from here
+      kx0 = key0 - ky0 * a.w;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int off = 8 * (r / 4) + 4 * hl + (r % 4), key = key0 + off;
+      float x = s[r] * a.scale;
+      if constexpr (kBias == Bias::kMask) {
+        if (key < a.keys && qin) x = x + a.mask[qrow * a.mask_ld + key];
+      } else if constexpr (kBias == Bias::kRelPos) {
+        int ky = ky0, kx = kx0 + off;
+        while (kx >= a.w) {
+          kx -= a.w;
+          ++ky;
+        }
+        if (key < a.keys) x = x + (my_dots[ky] + my_dots[a.h + kx]);
+      }
+      x = key < a.keys ? x : -INFINITY;
+      s[r] = x;
+      tmax = fmaxf(tmax, x);
+    }
+    tmax = fmaxf(tmax, partner(tmax));
+    const float m_new = fmaxf(m, tmax);
+    const bool dead = m_new == -INFINITY;  // nothing finite yet
+    const float corr = dead ? 1.0f : __builtin_amdgcn_exp2f((m - m_new) * kLog2e);
+    float psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = dead ? 0.0f : __builtin_amdgcn_exp2f((s[r] - m_new) * kLog2e);
+      psum += s[r];
+    }
+    psum += partner(psum);
+    l = l * corr + psum;
+    m = m_new;
+#pragma unroll
+    for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[b][r] *= corr;
+    }
+
+    // O^T += V^T P^T: product i sums keys 8 (i / 4) + i % 4 + 4 h, held in s[i]
+#pragma unroll
+    for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = 8 * (i / 4) + 4 * hl + (i % 4);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * HD + 32 * b + c], s[i], o[b], 0, 0, 0);
+      }
+    }
+
+    __syncthreads();  // every wave is done with this tile
+    if (more) {
+      store_tile<HD, kThreads>(ks, vs, kr, vr);
+      __syncthreads();
+    }
+  }
+
+  if (!qin) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  float* orow = a.out + slice * a.so + qrow * a.ldo;
+#pragma unroll
+  for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * b + 8 * g + 4 * hl;
+      *reinterpret_cast<float4*>(orow + d) =
+          make_float4(o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv);
+    }
+  }
+}
+
+template <Bias kBias>
+int launch(const char* what, void* stream, int64_t hd, int64_t slices, const AttnArgs& a) {
+  constexpr int kThreads = 64 * waves_of<kBias>(), kQueriesPerBlock = waves_of<kBias>() * kQueriesPerWave;
+  const dim3 grid(static_cast<unsigned>((a.rows + kQueriesPerBlock - 1) / kQueriesPerBlock),
+                  static_cast<unsigned>(slices));
+  const size_t dyn =
+      kBias == Bias::kRelPos ? sizeof(float) * kQueriesPerBlock * static_cast<size_t>(a.h + a.w + 1) : 0;
+  clear_launch_error();
+  if (hd == 64) {
+    attention_k<64, kBias><<<grid, kThreads, dyn, as_stream(stream)>>>(a);
+  } else {
+    attention_k<128, kBias><<<grid, kThreads, dyn, as_stream(stream)>>>(a);
+  }
+  return check_launch(what);
+}
+
+int check_common(const char* what, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk, int64_t sk,
+                 const float* v, int64_t ldv, int64_t sv, const float* out, int64_t ldo, int64_t so, int64_t slices,
+                 int64_t rows, int64_t keys, int64_t hd) {
+  UOCR_REQUIRE(hd == 64 || hd == 128, what, "head dim must be 64 or 128");
+  UOCR_REQUIRE(slices >= 1 && slices < 65536 && rows >= 1 && rows < (int64_t{1} << 31) && keys >= 1 &&
+                   keys < (int64_t{1} << 31),
+               what, "need 1 <= slices < 65536 and rows, keys in [1, 2^31)");
+  UOCR_REQUIRE(q != nullptr && k != nullptr && v != nullptr && out != nullptr, what, "null pointer");
+  UOCR_REQUIRE(ldq >= hd && ldk >= hd && ldv >= hd && ldo >= hd && sq >= 0 && sk >= 0 && sv >= 0 && so >= 0, what,
+               "row strides must be >= hd and slice strides >= 0");
+  UOCR_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && ldq % 4 == 0 && ldk % 4 == 0 &&
+                   ldv % 4 == 0 && ldo % 4 == 0 && sq % 4 == 0 && sk % 4 == 0 && sv % 4 == 0 && so % 4 == 0,
+               what, "operands must be 16-byte aligned with strides of whole 16-byte chunks");
+  return UOCR_ROCM_OK;
+}
+
+}  // namespace
+}  // namespace uocr_rocm
+
+using namespace uocr_rocm;
+
+extern "C" {
+
+int uocr_rocm_attention(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
+                        int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo, int64_t so,
+                        int64_t slices, int64_t rows, int64_t keys, int64_t hd, float scale, const float* mask,
+                        int64_t mask_ld) {
+  constexpr const char* kWhat = "uocr_rocm_attention";
+  if (const int st = check_common(kWhat, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, rows, keys, hd)) {
+    return st;
+  }
+  UOCR_REQUIRE(mask == nullptr || mask_ld >= keys, kWhat, "mask rows must hold every key");
+  AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
+             scale, mask, mask_ld, nullptr, nullptr, 0, 0};
+  return mask != nullptr ? launch<Bias::kMask>(kWhat, stream, hd, slices, a)
+                         : launch<Bias::kNone>(kWhat, stream, hd, slices, a);
+}
+
+int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
+                                int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo,
+                                int64_t so, int64_t slices, int64_t h, int64_t w, int64_t hd, float scale,
+                                const float* rh, const float* rw) {
+  constexpr const char* kWhat = "uocr_rocm_attention_rel_pos";
+  UOCR_REQUIRE(h >= 1 && w >= 1 && h + w <= kMaxRelSpan, kWhat, "need h, w >= 1 and h + w <= 256");
+  const int64_t n = h * w;
+  if (const int st = check_common(kWhat, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, n, n, hd)) {
+    return st;
+  }
+  UOCR_REQUIRE(rh != nullptr && rw != nullptr, kWhat, "null relative-position table");
+  AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(n), static_cast<int>(n),
+             scale, nullptr, 0, rh, rw, static_cast<int>(h), static_cast<int>(w)};
+  return launch<Bias::kRelPos>(kWhat, stream, hd, slices, a);
+}
+
+}  // extern "C"

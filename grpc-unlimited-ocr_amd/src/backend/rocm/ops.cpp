@@ -199,6 +199,20 @@ void rel_pos_softmax_rows(const Context& ctx, float* scores, std::int64_t window
   check(uocr_rocm_rel_pos_softmax_rows(ctx.stream(), scores, windows, q, ldq, h, w, d, rh, rw));
 }
 
+void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
+               std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
+               const float* mask, std::int64_t mask_ld) {
+  check(uocr_rocm_attention(ctx.stream(), q.p, q.ld, q.slice, k.p, k.ld, k.slice, v.p, v.ld, v.slice, out, ldo, so,
+                            slices, rows, keys, hd, scale, mask, mask_ld));
+}
+
+void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
+                       std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
+                       float scale, const float* rh, const float* rw) {
+  check(uocr_rocm_attention_rel_pos(ctx.stream(), q.p, q.ld, q.slice, k.p, k.ld, k.slice, v.p, v.ld, v.slice, out,
+                                    ldo, so, slices, h, w, hd, scale, rh, rw));
+}
+
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
             std::int64_t n, const float* bias, float* y) {
   check(uocr_rocm_linear(ctx.stream(), x, m, k, w_bf16, n, bias, y));

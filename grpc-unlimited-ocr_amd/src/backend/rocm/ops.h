@@ -149,6 +149,20 @@ void rel_pos_bias(const Context& ctx, const float* q, std::int64_t ldq, std::int
                   const float* rh, const float* rw, float* bias);
 void rel_pos_softmax_rows(const Context& ctx, float* scores, std::int64_t windows, const float* q, std::int64_t ldq,
                           std::int64_t h, std::int64_t w, std::int64_t d, const float* rh, const float* rw);
+// New: attention in one pass on the matrix cores, fp32: out[s, t] =
+// softmax(scale q[s, t] . k[s, :] + mask[t, :]) v[s, :] over `slices` slices
+// (row t of slice s at base + s * s_stride + t * ld); mask may be null; and
+// the same with SAM's relative-position bias over h x w windows.
+struct AttnOperand {
+  const float* p;
+  std::int64_t ld, slice;
+};
+void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
+               std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
+               const float* mask, std::int64_t mask_ld);
+void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
+                       std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
+                       float scale, const float* rh, const float* rw);
 // y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]) on the matrix cores, fp32
 // accumulation (m == 1: the GEMV); the reference's linear.
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,

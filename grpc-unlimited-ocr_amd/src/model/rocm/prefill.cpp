@@ -79,7 +79,8 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
   Array x = f32(rows * H);
   x.upload(x_host.data(), rows * H);
   Array h = f32(rows * H), delta = f32(rows * H), q = f32(rows * W), rq = f32(rows * D), z = f32(rows * nblk);
-  Array mask = f32(rows * keys), scores = f32(d.heads * rows * keys), merged = f32(rows * W);
+  const bool one_pass = hd == 64 || hd == 128;
+  Array mask = f32(rows * keys), scores = f32(one_pass ? 1 : d.heads * rows * keys), merged = f32(rows * W);
   const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(D));
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
   for (std::size_t li = 0; li < layers_.size(); ++li) {
@@ -123,12 +124,19 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
     gemm_nt(ctx_, rows, nblk, D, inv_sqrt_d, rq.f32(), D, 0, summaries_[li].f32(), D, 0, z.f32(), nblk, 0, 1);
     route_blocks(ctx_, z.f32(), rows, nblk, first, keys, block_min, block_max, prompt_blocks_, qp_d.i64(), -1,
                  d.router, mask.f32());
-    gemm_nt(ctx_, rows, keys, hd, scale, q.f32(), W, hd, k_cache_[li].f32(), W, hd, scores.f32(), keys, rows * keys,
-            d.heads);
-    scale_add_mask(ctx_, scores.f32(), 1.0f, mask.f32(), d.heads, rows, keys);
-    softmax_rows(ctx_, scores.f32(), d.heads * rows, keys);
-    gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_cache_[li].f32(), W, hd, merged.f32(), W, hd,
-            d.heads);
+    if (one_pass) {
+      // scores, mask, softmax and values in one pass on the matrix cores,
+      // each head's columns read in place
+      attention(ctx_, {q.f32(), W, hd}, {k_cache_[li].f32(), W, hd}, {v_cache_[li].f32(), W, hd}, merged.f32(), W,
+                hd, d.heads, rows, keys, hd, scale, mask.f32(), keys);
+    } else {
+      gemm_nt(ctx_, rows, keys, hd, scale, q.f32(), W, hd, k_cache_[li].f32(), W, hd, scores.f32(), keys,
+              rows * keys, d.heads);
+      scale_add_mask(ctx_, scores.f32(), 1.0f, mask.f32(), d.heads, rows, keys);
+      softmax_rows(ctx_, scores.f32(), d.heads * rows, keys);
+      gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_cache_[li].f32(), W, hd, merged.f32(), W, hd,
+              d.heads);
+    }
     {
       const Array mb = rounded(ctx_, merged.f32(), rows * W);
       linear_bf16x(ctx_, mb.bf16(), rows, W, l.o, H, nullptr, delta.f32());

@@ -240,12 +240,12 @@ const VisionEncoder::Windows& VisionEncoder::windows(std::int64_t g) const {
 
 // Attention of one block over `windows` windows of h x w tokens, rows
 // window-major in x [windows * h * w, width] (cuda_vision.cpp:151-172).
-// With the head dim a multiple of 4 the operands go head-major
-// ([3, heads, rows, hd]) and every (head, window) pair is one slice of one
-// batched product: the scores, the relative-position bias + softmax and
-// the values' product are three launches for the whole layer, whose grids
-// cover the GPU even for one 64 x 64 global window. Otherwise head by head
-// over all windows, as the reference does.
+// The operands go head-major ([3, heads, rows, hd]) so that every (head,
+// window) pair is one slice: with a head dim of 64 or 128 (the model's 64)
+// one launch forms scores, bias, softmax and values on the matrix cores;
+// with another multiple of 4, three batched launches (scores, the
+// relative-position bias + softmax, values); otherwise head by head over all
+// windows, as the reference does.
 void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_t windows, std::int64_t h,
                                   std::int64_t w, float* out) const {
   const auto& b = w_.sam_blocks[index];
@@ -256,7 +256,17 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_
   const Array& rw = rel_table(index, false, w);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
   Array merged = f32(ctx_, rows * c);
-  if (hd % 4 == 0) {
+  if ((hd == 64 || hd == 128) && h + w <= 256) {
+    // one pass on the matrix cores: scores, bias, softmax and values per
+    // (head, window) slice without the scores reaching memory
+    const std::int64_t slices = heads * windows, part = heads * rows * hd;
+    Array split = f32(ctx_, 3 * part), o = f32(ctx_, part);
+    split_heads(ctx_, qkv.f32(), rows, 3, heads, hd, split.f32());
+    const float* q = split.f32();
+    attention_rel_pos(ctx_, {q, hd, n * hd}, {q + part, hd, n * hd}, {q + 2 * part, hd, n * hd}, o.f32(), hd, n * hd,
+                      slices, h, w, hd, scale, rh.f32(), rw.f32());
+    merge_heads(ctx_, o.f32(), heads, rows, hd, merged.f32());
+  } else if (hd % 4 == 0) {
     const std::int64_t slices = heads * windows, part = heads * rows * hd;
     Array split = f32(ctx_, 3 * part), o = f32(ctx_, part), scores = f32(ctx_, slices * n * n);
     split_heads(ctx_, qkv.f32(), rows, 3, heads, hd, split.f32());
@@ -354,15 +364,21 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
   add_inplace(ctx_, x.f32(), clip_positions(g).f32(), n * c);
   layer_norm(ctx_, x.f32(), w_.pre_ln_w, w_.pre_ln_b, n, c, kClipEps);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
-  const bool split = hd % 4 == 0;  // head-major operands, as in sam_attention
-  Array normed = f32(ctx_, n * c), qkv = f32(ctx_, n * 3 * c), scores = f32(ctx_, heads * n * n);
+  const bool one_pass = hd == 64 || hd == 128;  // attention on the matrix cores
+  const bool split = !one_pass && hd % 4 == 0;   // head-major operands, as in sam_attention
+  Array normed = f32(ctx_, n * c), qkv = f32(ctx_, n * 3 * c), scores = f32(ctx_, one_pass ? 1 : heads * n * n);
   Array merged = f32(ctx_, n * c), proj = f32(ctx_, n * c), wide = f32(ctx_, n * cd.mlp);
   Array hm = f32(ctx_, split ? 3 * n * c : 1), o = f32(ctx_, split ? n * c : 1);
   for (const auto& l : w_.clip_layers) {
     copy(ctx_, normed.f32(), x.f32(), n * c);
     layer_norm(ctx_, normed.f32(), l.ln1_w, l.ln1_b, n, c, kClipEps);
     linear(ctx_, normed.f32(), n, c, l.qkv, 3 * c, l.qkv_b, qkv.f32());
-    if (split) {
+    if (one_pass) {
+      // straight from the projection's rows into the heads' columns
+      const float* q = qkv.f32();
+      attention(ctx_, {q, 3 * c, hd}, {q + c, 3 * c, hd}, {q + 2 * c, 3 * c, hd}, merged.f32(), c, hd, heads, n, n, hd,
+                scale, nullptr, 0);
+    } else if (split) {
       split_heads(ctx_, qkv.f32(), n, 3, heads, hd, hm.f32());
       const float* q = hm.f32();
       gemm_nt(ctx_, n, n, hd, scale, q, hd, n * hd, q + n * c, hd, n * hd, scores.f32(), n, n * n, heads);

@@ -394,6 +394,34 @@ UOCR_ROCM_API int uocr_rocm_rel_pos_softmax_rows(void* stream, float* scores, in
                                                  int64_t ldq, int64_t h, int64_t w, int64_t d, const float* rh,
                                                  const float* rw);
 
+/* ---- attention in one pass ------------------------------------------------------- */
+
+/* New: out[s, t] = softmax over keys of (scale * q[s, t] . k[s, key] +
+ * mask[t, key]) times v[s, key], for slices s (heads, or heads of windows)
+ * and query rows t, fp32 on the matrix cores; the scores never reach memory.
+ * Row t of slice s of q sits at q + s * sq + t * ldq (k, v, out alike, in
+ * elements); hd is 64 or 128; operands 16-byte aligned with strides of
+ * whole 16-byte chunks. mask [rows, mask_ld] (shared by the slices, -inf
+ * for a key not attended) or null. A row with no finite score gives zeros.
+ * Replaces the reference's gemm_nt + scale_add_mask (or bias add) +
+ * softmax_rows + gemm_nn sequence (src/model/cuda/cuda_decoder.cpp:88-105,
+ * src/model/cuda/cuda_vision.cpp:251-254). */
+UOCR_ROCM_API int uocr_rocm_attention(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                                      int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out,
+                                      int64_t ldo, int64_t so, int64_t slices, int64_t rows, int64_t keys, int64_t hd,
+                                      float scale, const float* mask, int64_t mask_ld);
+
+/* New: the same over SAM's windows of h x w tokens (rows = keys = h w per
+ * slice) with the decomposed relative-position bias of
+ * uocr_rocm_rel_pos_bias (rh [h, h, hd], rw [w, w, hd], formed from each
+ * slice's own query rows) in place of the mask; h + w <= 256. Replaces the
+ * reference's per-head gemm_nt + rel_pos_bias + add_inplace + softmax_rows
+ * + gemm_nn (src/model/cuda/cuda_vision.cpp:159-170). */
+UOCR_ROCM_API int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                                              int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv,
+                                              float* out, int64_t ldo, int64_t so, int64_t slices, int64_t h,
+                                              int64_t w, int64_t hd, float scale, const float* rh, const float* rw);
+
 /* ---- decode-step neighbours ---------------------------------------------------- */
 
 /* y[n] = bf16(x) . w[n, :] (+ bias[n]): x fp32 [k] rounded to bf16 (nearest

@@ -884,7 +884,7 @@ struct OracleDecoder {
   }
 };
 
-void prefill_then_decode(const ro::Context& ctx) {
+void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
   // A prompt of 48 rows (8 text rows, then two image pages of 20 rows) run
   // through DecodeStep::prefill, then 40 decode steps on the caches it
   // wrote, the logits of each against the oracle's decoder on the same
@@ -893,12 +893,14 @@ void prefill_then_decode(const ro::Context& ctx) {
   // step to 1e-3 and the median step to 1e-5: the device and the oracle make
   // the same routing choices, so only fp32 summation order separates them).
   // Router as the reference test sets it: block 4, one local block,
-  // idx_scale 4.
+  // idx_scale 4. Head dim 16 takes the prefill's three-launch attention
+  // (products, mask + softmax, products), 64 the one-pass attention.
+  std::printf("prefill then decode, head dim %lld\n", static_cast<long long>(head_dim));
   ro::DecoderDims d;
   d.hidden = 64;
   d.heads = 2;
-  d.head_dim = 16;
-  d.index_dim = 16;
+  d.head_dim = head_dim;
+  d.index_dim = head_dim;
   d.vocab = 300;
   d.capacity = 128;
   d.router.block_size = 4;
@@ -1108,7 +1110,8 @@ int main() {
     fused_decode_layer(ctx);
     decode_step(ctx, true);
     decode_step(ctx, false);
-    prefill_then_decode(ctx);
+    prefill_then_decode(ctx, 16);
+    prefill_then_decode(ctx, 64);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());

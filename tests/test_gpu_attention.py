@@ -1,0 +1,112 @@
+"""GPU parity for the one-pass attention (csrc/attention.hip) through the C
+ABI, against the oracle's attention_head (the reference's
+src/backend/reference/ops.cpp:219-251: dot(q, k) * scale + bias, softmax
+with an fp64 total, probabilities times v) slice by slice:
+
+  * no bias, hd 64 and 128, rows and keys not multiples of the 32-key tile
+    or the 128-row workgroup, several slices, head-major operands;
+  * a mask shared by the slices with -inf entries, a causal pattern and a
+    row with every key masked (zeros out), rows != keys;
+  * strided operands as the decoder's prefill holds them (q, k, v columns of
+    [rows, heads * hd] rows, the output into the heads' columns);
+  * SAM's relative-position bias over 14 x 14 windows and a 64 x 64 global
+    window, against the oracle's rel_pos_bias + attention_head;
+Tolerance: 1e-5 of the largest |out| (fp32 sums in another order, the
+running-max rescale).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from parity import assert_f32_close, dev_f32, host_f32, normal
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device(backend):
+    if not torch.cuda.is_available() or backend.device_count() == 0:
+        pytest.skip("no HIP device")
+    torch.cuda.set_device(0)
+    yield
+    torch.cuda.synchronize()
+
+
+def reference(q, k, v, scale, bias=None):
+    return np.stack([oracle.attention_head(q[s], k[s], v[s], bias, scale) for s in range(q.shape[0])])
+
+
+@pytest.mark.parametrize("slices,rows,keys,hd", [(1, 1, 1, 64), (3, 31, 33, 64), (2, 257, 257, 64),
+                                                 (2, 130, 1000, 128), (1, 1024, 1024, 64), (16, 65, 65, 64)])
+def test_attention_against_the_oracle(backend, slices, rows, keys, hd):
+    q, k, v = normal(700 + rows, (slices, rows, hd)), normal(701 + keys, (slices, keys, hd)), normal(702, (slices, keys, hd))
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    want = reference(q, k, v, scale)
+    out = torch.full((slices, rows, hd), float("nan"), device="cuda")
+    backend.attention(dev_f32(q), dev_f32(k), dev_f32(v), out, slices, rows, keys, hd, scale)
+    assert_f32_close(host_f32(out), want, 1e-5, f"attention {slices}x{rows}x{keys} hd {hd}")
+
+
+def test_attention_with_a_mask(backend):
+    slices, rows, keys, hd = 3, 100, 300, 128
+    q, k, v = normal(710, (slices, rows, hd)), normal(711, (slices, keys, hd)), normal(712, (slices, keys, hd))
+    g = np.random.default_rng(713)
+    mask = np.where(g.random((rows, keys)) < 0.3, -np.inf, 0.1 * g.standard_normal((rows, keys))).astype(np.float32)
+    for t in range(rows):  # causal beyond key 200 + t
+        mask[t, 200 + t:] = -np.inf
+    mask[7, :] = -np.inf  # every key masked: zeros
+    mask[8, :] = -np.inf
+    mask[8, 299] = 0.0  # a single live key at the end of the last tile
+    scale = 0.088
+    want = reference(q, k, v, scale, mask)
+    out = torch.full((slices, rows, hd), float("nan"), device="cuda")
+    backend.attention(dev_f32(q), dev_f32(k), dev_f32(v), out, slices, rows, keys, hd, scale, mask=dev_f32(mask))
+    got = host_f32(out)
+    assert np.array_equal(got[:, 7], np.zeros((slices, hd), np.float32))
+    assert_f32_close(got, want, 1e-5, "masked attention")
+
+
+def test_attention_strided_decoder_layout(backend):
+    """q, k, v as the decoder's prefill holds them: head h at columns h * hd
+    of [rows, heads * hd] rows (q inside a wider projection row), the output
+    written into the heads' columns of [rows, heads * hd]."""
+    heads, hd, rows = 4, 128, 77
+    width = heads * hd
+    proj = normal(720, (rows, 5 * width))  # q | ... wider row
+    kc, vc = normal(721, (rows, width)), normal(722, (rows, width))
+    q = proj[:, :width].reshape(rows, heads, hd).transpose(1, 0, 2)
+    k, v = kc.reshape(rows, heads, hd).transpose(1, 0, 2), vc.reshape(rows, heads, hd).transpose(1, 0, 2)
+    mask = np.triu(np.full((rows, rows), -np.inf, np.float32), 1)
+    want = reference(q, k, v, 0.1, mask).transpose(1, 0, 2).reshape(rows, width)
+    out = torch.full((rows, width), float("nan"), device="cuda")
+    backend.attention(dev_f32(proj), dev_f32(kc), dev_f32(vc), out, heads, rows, rows, hd, 0.1, mask=dev_f32(mask),
+                      strides={"q": (0, 5 * width, hd), "k": (0, width, hd), "v": (0, width, hd),
+                               "out": (0, width, hd)})
+    assert_f32_close(host_f32(out), want, 1e-5, "strided attention")
+
+
+@pytest.mark.parametrize("windows,heads,h,w", [(4, 3, 14, 14), (1, 2, 64, 64), (2, 1, 5, 7)])
+def test_attention_rel_pos_against_the_oracle(backend, windows, heads, h, w):
+    hd, n = 64, h * w
+    slices = heads * windows
+    q, k, v = normal(730 + n, (slices, n, hd)), normal(731 + n, (slices, n, hd)), normal(732, (slices, n, hd))
+    rh, rw = normal(733, (h, h, hd)) * 0.3, normal(734, (w, w, hd)) * 0.3
+    scale = 0.125
+    want = np.stack([oracle.attention_head(q[s], k[s], v[s], oracle.rel_pos_bias(q[s], h, w, rh, rw), scale)
+                     for s in range(slices)])
+    out = torch.full((slices, n, hd), float("nan"), device="cuda")
+    backend.attention_rel_pos(dev_f32(q), dev_f32(k), dev_f32(v), out, slices, h, w, hd, scale, dev_f32(rh),
+                              dev_f32(rw))
+    assert_f32_close(host_f32(out), want, 1e-5, f"rel-pos attention {windows}x{heads} {h}x{w}")
+
+
+def test_attention_rejects_bad_shapes(backend):
+    x = torch.zeros(2, 8, 96, device="cuda")
+    with pytest.raises(ValueError):
+        backend.attention(x, x, x, x, 2, 8, 8, 96, 1.0)  # head dim 96
+    y = torch.zeros(1, 8, 64, device="cuda")
+    with pytest.raises(ValueError):
+        backend.attention_rel_pos(y, y, y, y, 1, 200, 100, 64, 1.0, y, y)  # h + w above 256
