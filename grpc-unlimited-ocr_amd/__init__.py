@@ -140,6 +140,9 @@ _SIGNATURES = {
     "uocr_rocm_linear": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_linear_bf16x": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_round_bf16": ([_vp, _vp, _i64, _vp], _int),
+    "uocr_rocm_linear_workspace_floats": ([_i64, _i64, _i64], _i64),
+    "uocr_rocm_linear_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_linear_bf16x_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_gemm_nt": ([_vp, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64],
                           _int),
     "uocr_rocm_gemm_nn": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64], _int),
@@ -482,6 +485,20 @@ def gemv_bf16(x, w, y, bias=None, stream=None):
     if x.numel() != k or y.numel() != n or (bias is not None and bias.numel() != n):
         raise ValueError("gemv_bf16 shapes: x [k], w [n, k], y [n], bias [n]")
     _op("uocr_rocm_gemv_bf16", stream, _ptr(x), k, _ptr(w), n, _f32_param(bias), _ptr(y))
+
+
+def linear_workspace_floats(m, k, n):
+    """Workspace floats linear_ws would split k over (0: no split taken)."""
+    return int(lib().uocr_rocm_linear_workspace_floats(m, k, n))
+
+
+def linear_ws(x, w, y, workspace, bias=None, stream=None):
+    """linear with a workspace for splitting k (new)."""
+    torch = _torch()
+    n, k = w.shape
+    m = x.numel() // k
+    name = "uocr_rocm_linear_bf16x_ws" if x.dtype == torch.bfloat16 else "uocr_rocm_linear_ws"
+    _op(name, stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y), _ptr(workspace), workspace.numel())
 
 
 def linear(x, w, y, bias=None, stream=None):

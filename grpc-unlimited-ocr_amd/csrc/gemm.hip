@@ -22,7 +22,10 @@
 // contiguous run of tiles, ordered in groups of 8 tile-rows sweeping the
 // columns, so the tiles resident on one XCD share x rows and w rows in its
 // L2. The bias is added to each finished sum (one fp32 rounding, as the
-// reference's separate bias pass).
+// reference's separate bias pass). A product with too few tiles to cover
+// the GPU (the vision encoder's CLIP projections: 257 rows) may split k
+// over a caller's workspace: each split writes its partial products and one
+// more launch sums them in split order, then adds the bias.
 
 #include "common.hpp"
 
@@ -66,7 +69,28 @@ struct LinearArgs {
   int64_t m, n;
   int k;
   int tiles_m, tiles_n;
+  // Split k: workgroup b takes tile b % tiles of split b / tiles, columns
+  // [split * k_len, min(k, (split + 1) * k_len)) of the sums, into part +
+  // split * m * n (no bias); part null: one split, into y with the bias.
+  int k_len;
+  float* part;
 };
+
+// The tile, split and k range of this workgroup.
+struct Work {
+  int64_t m0, n0;
+  int split, k_begin, k_end;
+};
+
+__device__ __forceinline__ Work work_of(const LinearArgs& a) {
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int split = static_cast<int>(blockIdx.x) / tiles;
+  int tm, tn;
+  tile_of(static_cast<int>(blockIdx.x) - split * tiles, a.tiles_m, a.tiles_n, tm, tn);
+  const int kb = split * a.k_len;
+  return {static_cast<int64_t>(tm) * kTileM, static_cast<int64_t>(tn) * kTileN, split, kb,
+          a.k - kb < a.k_len ? a.k : kb + a.k_len};
+}
 
 // The registers one k step stages: per thread kChunksPerThread chunks of the
 // x tile (8 elements each: fp32, rounded on the way to LDS, or bf16) and of
@@ -78,13 +102,14 @@ struct Staged {
 };
 
 template <bool kF32X>
-__device__ __forceinline__ void load_step(const LinearArgs& a, int64_t m0, int64_t n0, int k0, Staged<kF32X>& s) {
+__device__ __forceinline__ void load_step(const LinearArgs& a, int64_t m0, int64_t n0, int k0, int k_end,
+                                          Staged<kF32X>& s) {
 #pragma unroll
   for (int i = 0; i < kChunksPerThread; ++i) {
     const int id = static_cast<int>(threadIdx.x) + kGemmThreads * i;
     const int row = id / kRowChunks, c = id % kRowChunks;
     const int kc = k0 + 8 * c;
-    const bool kin = kc < a.k;
+    const bool kin = kc < k_end;
     const int64_t xr = m0 + row, wr = n0 + row;
 #pragma unroll
     for (int h = 0; h < (kF32X ? 2 : 1); ++h) s.xa[i][h] = u32x4{0u, 0u, 0u, 0u};
@@ -105,7 +130,7 @@ __device__ __forceinline__ void load_step(const LinearArgs& a, int64_t m0, int64
 // A k that is not a multiple of 8 (rows not 16-byte aligned): each chunk's
 // 8 elements are loaded one by one, those at or past k read as zero.
 template <bool kF32X>
-__device__ __forceinline__ void load_step_ragged(const LinearArgs& a, int64_t m0, int64_t n0, int k0,
+__device__ __forceinline__ void load_step_ragged(const LinearArgs& a, int64_t m0, int64_t n0, int k0, int k_end,
                                                  Staged<kF32X>& s) {
 #pragma unroll
   for (int i = 0; i < kChunksPerThread; ++i) {
@@ -116,7 +141,7 @@ __device__ __forceinline__ void load_step_ragged(const LinearArgs& a, int64_t m0
     uint32_t xv[8], wv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const bool in = kc + e < a.k;
+      const bool in = kc + e < k_end;
       xv[e] = 0u;
       wv[e] = 0u;
       if (in && xr < a.m) {
@@ -188,21 +213,36 @@ __device__ __forceinline__ void mfma_step(const u32x4* xs, const u32x4* ws, int 
 
 // acc[i][j][r] is y row 8 (r / 4) + 4 half + r % 4 of the 32 x 32 tile,
 // column r32.
-__device__ __forceinline__ void store_tile(const LinearArgs& a, int64_t m0, int64_t n0, int wm, int wn, int half,
-                                           int r32, const f32x16 (&acc)[2][2]) {
+__device__ __forceinline__ void store_tile(const LinearArgs& a, const Work& wk, int wm, int wn, int half, int r32,
+                                           const f32x16 (&acc)[2][2]) {
+  const bool split = a.part != nullptr;
+  float* out = split ? a.part + static_cast<int64_t>(wk.split) * a.m * a.n : a.y;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t col = n0 + 64 * wn + 32 * j + r32;
+    const int64_t col = wk.n0 + 64 * wn + 32 * j + r32;
     if (col >= a.n) continue;
-    const float bv = a.bias != nullptr ? a.bias[col] : 0.0f;
+    const bool add = !split && a.bias != nullptr;
+    const float bv = add ? a.bias[col] : 0.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
-        if (row < a.m) a.y[row * a.n + col] = a.bias != nullptr ? acc[i][j][r] + bv : acc[i][j][r];
+        const int64_t row = wk.m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
+        if (row < a.m) out[row * a.n + col] = add ? acc[i][j][r] + bv : acc[i][j][r];
       }
     }
+  }
+}
+
+// y = the sum of the splits' partial products in split order (+ bias).
+__global__ __launch_bounds__(kBlock) void split_sum_k(const float* __restrict__ part, int splits, int64_t m, int64_t n,
+                                                       const float* __restrict__ bias, float* __restrict__ y) {
+  const int64_t total = m * n;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kBlock) {
+    float v = part[i];
+    for (int sp = 1; sp < splits; ++sp) v += part[sp * total + i];
+    y[i] = bias != nullptr ? v + bias[i % n] : v;
   }
 }
 
@@ -223,35 +263,33 @@ template <bool kF32X, bool kRagged>
 __global__ __launch_bounds__(kGemmThreads) void linear_staged_k(const LinearArgs a) {
   __shared__ u32x4 xs[2][kTileChunks];
   __shared__ u32x4 ws[2][kTileChunks];
-  int tm, tn;
-  tile_of(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * kTileM, n0 = static_cast<int64_t>(tn) * kTileN;
+  const Work wk = work_of(a);
   const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
   const int wm = wave >> 1, wn = wave & 1;
   const int half = lane >> 5, r32 = lane & 31;
   f32x16 acc[2][2];
   zero(acc);
-  const int steps = (a.k + kTileK - 1) / kTileK;
+  const int steps = (wk.k_end - wk.k_begin + kTileK - 1) / kTileK;
   Staged<kF32X> s;
   auto load = [&](int k0) {
     if constexpr (kRagged) {
-      load_step_ragged(a, m0, n0, k0, s);
+      load_step_ragged(a, wk.m0, wk.n0, k0, wk.k_end, s);
     } else {
-      load_step(a, m0, n0, k0, s);
+      load_step(a, wk.m0, wk.n0, k0, wk.k_end, s);
     }
   };
-  load(0);
+  load(wk.k_begin);
   store_step(s, xs[0], ws[0]);
   lds_barrier();
   for (int t = 0; t < steps; ++t) {
     const int buf = t & 1;
     const bool more = t + 1 < steps;
-    if (more) load((t + 1) * kTileK);
+    if (more) load(wk.k_begin + (t + 1) * kTileK);
     mfma_step(xs[buf], ws[buf], wm, wn, half, r32, acc);
     if (more) store_step(s, xs[buf ^ 1], ws[buf ^ 1]);
     lds_barrier();
   }
-  store_tile(a, m0, n0, wm, wn, half, r32, acc);
+  store_tile(a, wk, wm, wn, half, r32, acc);
 }
 
 // bf16 x and k a multiple of 64: tiles go straight from memory into LDS.
@@ -286,23 +324,21 @@ __device__ __forceinline__ void wait_loads_and_barrier() {
 __global__ __launch_bounds__(kGemmThreads) void linear_dma_k(const LinearArgs a) {
   __shared__ u32x4 xs[2][kTileChunks];
   __shared__ u32x4 ws[2][kTileChunks];
-  int tm, tn;
-  tile_of(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * kTileM, n0 = static_cast<int64_t>(tn) * kTileN;
+  const Work wk = work_of(a);
   const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
   const int wm = wave >> 1, wn = wave & 1;
   const int half = lane >> 5, r32 = lane & 31;
   f32x16 acc[2][2];
   zero(acc);
-  const int steps = a.k / kTileK;
-  dma_step(a, m0, n0, 0, xs[0], ws[0], wave, lane);
+  const int steps = (wk.k_end - wk.k_begin) / kTileK;
+  dma_step(a, wk.m0, wk.n0, wk.k_begin, xs[0], ws[0], wave, lane);
   for (int t = 0; t < steps; ++t) {
     const int buf = t & 1;
     wait_loads_and_barrier<0>();  // this step's tiles are in LDS; every wave is done with the other buffer
-    if (t + 1 < steps) dma_step(a, m0, n0, (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
+    if (t + 1 < steps) dma_step(a, wk.m0, wk.n0, wk.k_begin + (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
     mfma_step(xs[buf], ws[buf], wm, wn, half, r32, acc);
   }
-  store_tile(a, m0, n0, wm, wn, half, r32, acc);
+  store_tile(a, wk, wm, wn, half, r32, acc);
 }
 
 __global__ __launch_bounds__(kBlock) void round_bf16_k(const float* __restrict__ src, int64_t n,
@@ -321,8 +357,19 @@ __global__ __launch_bounds__(kBlock) void round_bf16_k(const float* __restrict__
 
 }  // namespace
 
+// The splits of k worth taking for an m x n x k product: enough
+// workgroups to cover the 256 CUs twice where the tiles alone do not, each
+// split at least 4 steps of 64 columns; 1 when the tiles suffice.
+int64_t splits_for(int64_t m, int64_t k, int64_t n) {
+  const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
+  if (tiles >= 512 || k < 8 * kTileK) return 1;
+  int64_t s = (512 + tiles - 1) / tiles;
+  s = s < k / (4 * kTileK) ? s : k / (4 * kTileK);
+  return s < 32 ? s : 32;
+}
+
 int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64_t m, int64_t k, const uint16_t* w,
-                 int64_t n, const float* bias, float* y) {
+                 int64_t n, const float* bias, float* y, float* workspace = nullptr, int64_t workspace_floats = 0) {
   UOCR_REQUIRE(m >= 0 && n >= 0 && k >= 0, what, "m, n and k must be >= 0");
   if (m == 0 || n == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(k >= 1 && k < (int64_t{1} << 30), what, "k must be in [1, 2^30)");
@@ -330,8 +377,24 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
   const bool ragged = k % 8 != 0 || !aligned16(x) || !aligned16(w);
   const int64_t tiles_m = (m + kTileM - 1) / kTileM, tiles_n = (n + kTileN - 1) / kTileN;
   UOCR_REQUIRE(tiles_m * tiles_n < (int64_t{1} << 31), what, "too many tiles");
-  LinearArgs a{x, w, bias, y, m, n, static_cast<int>(k), static_cast<int>(tiles_m), static_cast<int>(tiles_n)};
-  const unsigned grid = static_cast<unsigned>(tiles_m * tiles_n);
+  // split k into the workspace when it holds the partial products
+  int64_t splits = workspace != nullptr ? splits_for(m, k, n) : 1;
+  if (splits > 1 && workspace_floats < splits * m * n) splits = 1;
+  const int64_t k_len = splits > 1 ? (k / splits + kTileK - 1) / kTileK * kTileK : k;
+  splits = (k + k_len - 1) / k_len;
+  UOCR_REQUIRE(tiles_m * tiles_n * splits < (int64_t{1} << 31), what, "too many tiles");
+  LinearArgs a{x,
+               w,
+               bias,
+               y,
+               m,
+               n,
+               static_cast<int>(k),
+               static_cast<int>(tiles_m),
+               static_cast<int>(tiles_n),
+               static_cast<int>(k_len),
+               splits > 1 ? workspace : nullptr};
+  const unsigned grid = static_cast<unsigned>(tiles_m * tiles_n * splits);
   clear_launch_error();
   const hipStream_t st = as_stream(stream);
   if (ragged) {
@@ -346,6 +409,11 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
     linear_dma_k<<<grid, kGemmThreads, 0, st>>>(a);
   } else {
     linear_staged_k<false, false><<<grid, kGemmThreads, 0, st>>>(a);
+  }
+  if (splits > 1) {
+    const int64_t blocks = (m * n + kBlock - 1) / kBlock;
+    split_sum_k<<<static_cast<unsigned>(blocks < 65536 ? blocks : 65536), kBlock, 0, st>>>(
+        workspace, static_cast<int>(splits), m, n, bias, y);
   }
   return check_launch(what);
 }
@@ -369,6 +437,26 @@ int uocr_rocm_linear(void* stream, const float* x, int64_t m, int64_t k, const u
 int uocr_rocm_linear_bf16x(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
                            const float* bias, float* y) {
   return linear_entry("uocr_rocm_linear_bf16x", stream, x, false, m, k, w, n, bias, y);
+}
+
+int64_t uocr_rocm_linear_workspace_floats(int64_t m, int64_t k, int64_t n) {
+  if (m <= 1 || n <= 0 || k <= 0) return 0;
+  const int64_t s = splits_for(m, k, n);
+  return s > 1 ? s * m * n : 0;
+}
+
+int uocr_rocm_linear_ws(void* stream, const float* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
+                        const float* bias, float* y, float* workspace, int64_t workspace_floats) {
+  if (m == 1 && k % 8 == 0 && k <= 12288 && aligned16(x) && aligned16(w)) {
+    return uocr_rocm_gemv_bf16(stream, x, k, w, n, bias, y);
+  }
+  return linear_entry("uocr_rocm_linear_ws", stream, x, true, m, k, w, n, bias, y, workspace, workspace_floats);
+}
+
+int uocr_rocm_linear_bf16x_ws(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
+                              const float* bias, float* y, float* workspace, int64_t workspace_floats) {
+  return linear_entry("uocr_rocm_linear_bf16x_ws", stream, x, false, m, k, w, n, bias, y, workspace,
+                      workspace_floats);
 }
 
 int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst) {

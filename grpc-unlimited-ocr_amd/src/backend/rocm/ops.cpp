@@ -218,6 +218,15 @@ void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, 
   check(uocr_rocm_linear(ctx.stream(), x, m, k, w_bf16, n, bias, y));
 }
 
+std::int64_t linear_workspace_floats(std::int64_t m, std::int64_t k, std::int64_t n) {
+  return uocr_rocm_linear_workspace_floats(m, k, n);
+}
+
+void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
+            std::int64_t n, const float* bias, float* y, float* workspace, std::int64_t workspace_floats) {
+  check(uocr_rocm_linear_ws(ctx.stream(), x, m, k, w_bf16, n, bias, y, workspace, workspace_floats));
+}
+
 void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
                   std::int64_t n, const float* bias, float* y) {
   check(uocr_rocm_linear_bf16x(ctx.stream(), x, m, k, w_bf16, n, bias, y));

@@ -171,6 +171,12 @@ void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, 
 void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
                   std::int64_t n, const float* bias, float* y);
 void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint16_t* dst);
+// New: linear with a workspace for splitting k where the product has too
+// few tiles to cover the GPU (linear_workspace_floats(m, k, n) floats; 0:
+// no split is taken).
+std::int64_t linear_workspace_floats(std::int64_t m, std::int64_t k, std::int64_t n);
+void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
+            std::int64_t n, const float* bias, float* y, float* workspace, std::int64_t workspace_floats);
 
 // Fused decode projections (new): add + RMSNorm as the GEMV's prologue,
 // optionally a gate/up pair with a SwiGLU epilogue. delta, x_out, w_norm

@@ -238,6 +238,17 @@ const VisionEncoder::Windows& VisionEncoder::windows(std::int64_t g) const {
   return windows_.emplace(g, std::move(w)).first->second;
 }
 
+void VisionEncoder::project(const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w, std::int64_t n,
+                            const float* bias, float* y) const {
+  const std::int64_t floats = linear_workspace_floats(m, k, n);
+  if (floats == 0) {
+    linear(ctx_, x, m, k, w, n, bias, y);
+    return;
+  }
+  Array ws = f32(ctx_, floats);
+  linear(ctx_, x, m, k, w, n, bias, y, ws.f32(), floats);
+}
+
 // Attention of one block over `windows` windows of h x w tokens, rows
 // window-major in x [windows * h * w, width] (cuda_vision.cpp:151-172).
 // The operands go head-major ([3, heads, rows, hd]) so that every (head,
@@ -251,7 +262,7 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_
   const auto& b = w_.sam_blocks[index];
   const std::int64_t c = dims_.sam.width, heads = dims_.sam.heads, hd = c / heads, n = h * w, rows = windows * n;
   Array qkv = f32(ctx_, rows * 3 * c);
-  linear(ctx_, x, rows, c, b.qkv, 3 * c, b.qkv_b, qkv.f32());
+  project(x, rows, c, b.qkv, 3 * c, b.qkv_b, qkv.f32());
   const Array& rh = rel_table(index, true, h);
   const Array& rw = rel_table(index, false, w);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
@@ -285,7 +296,7 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_
               n * c, windows);
     }
   }
-  linear(ctx_, merged.f32(), rows, c, b.proj, c, b.proj_b, out);
+  project(merged.f32(), rows, c, b.proj, c, b.proj_b, out);
 }
 
 // One SAM block over x [g * g, width] (cuda_vision.cpp:174-202).
@@ -313,9 +324,9 @@ void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const
   Array hidden = f32(ctx_, cells * c), wide = f32(ctx_, cells * dims_.sam.mlp);
   copy(ctx_, hidden.f32(), x.f32(), cells * c);
   layer_norm(ctx_, hidden.f32(), b.norm2_w, b.norm2_b, cells, c, kSamEps);
-  linear(ctx_, hidden.f32(), cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
+  project(hidden.f32(), cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
   gelu_erf(ctx_, wide.f32(), cells * dims_.sam.mlp);
-  linear(ctx_, wide.f32(), cells, dims_.sam.mlp, b.lin2, c, b.lin2_b, hidden.f32());
+  project(wide.f32(), cells, dims_.sam.mlp, b.lin2, c, b.lin2_b, hidden.f32());
   add_inplace(ctx_, x.f32(), hidden.f32(), cells * c);
 }
 
@@ -329,7 +340,7 @@ void VisionEncoder::conv3(const float* hwc, std::int64_t side, std::int64_t in_c
   Array patches = f32(ctx_, out_side * out_side * in_c * 9);
   im2col(ctx_, chw.f32(), in_c, side, side, 3, 3, stride, 1, patches.f32());
   out = f32(ctx_, out_side * out_side * out_c);
-  linear(ctx_, patches.f32(), out_side * out_side, in_c * 9, w, out_c, nullptr, out.f32());
+  project(patches.f32(), out_side * out_side, in_c * 9, w, out_c, nullptr, out.f32());
 }
 
 // SAM over one image into cells [g4 * g4, net3] (cuda_vision.cpp:204-237).
@@ -339,12 +350,12 @@ void VisionEncoder::sam_forward(const float* image, std::int64_t size, Array& ce
   Array cols = f32(ctx_, g * g * 3 * p * p);
   im2col(ctx_, image, 3, size, size, p, p, static_cast<int>(p), 0, cols.f32());
   Array x = f32(ctx_, g * g * c);
-  linear(ctx_, cols.f32(), g * g, 3 * p * p, w_.patch, c, w_.patch_b, x.f32());
+  project(cols.f32(), g * g, 3 * p * p, w_.patch, c, w_.patch_b, x.f32());
   add_inplace(ctx_, x.f32(), sam_positions(g).f32(), g * g * c);
   for (std::size_t i = 0; i < w_.sam_blocks.size(); ++i) sam_block(i, x, g);
 
   Array y = f32(ctx_, g * g * s.neck);
-  linear(ctx_, x.f32(), g * g, c, w_.neck0, s.neck, nullptr, y.f32());
+  project(x.f32(), g * g, c, w_.neck0, s.neck, nullptr, y.f32());
   layer_norm(ctx_, y.f32(), w_.neck1_w, w_.neck1_b, g * g, s.neck, kSamEps);
   Array z, n2;
   std::int64_t s1 = 0, s2 = 0, s3 = 0;
@@ -372,7 +383,7 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
   for (const auto& l : w_.clip_layers) {
     copy(ctx_, normed.f32(), x.f32(), n * c);
     layer_norm(ctx_, normed.f32(), l.ln1_w, l.ln1_b, n, c, kClipEps);
-    linear(ctx_, normed.f32(), n, c, l.qkv, 3 * c, l.qkv_b, qkv.f32());
+    project(normed.f32(), n, c, l.qkv, 3 * c, l.qkv_b, qkv.f32());
     if (one_pass) {
       // straight from the projection's rows into the heads' columns
       const float* q = qkv.f32();
@@ -390,13 +401,13 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
       softmax_rows(ctx_, scores.f32(), heads * n, n);
       gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, qkv.f32() + 2 * c, 3 * c, hd, merged.f32(), c, hd, heads);
     }
-    linear(ctx_, merged.f32(), n, c, l.out, c, l.out_b, proj.f32());
+    project(merged.f32(), n, c, l.out, c, l.out_b, proj.f32());
     add_inplace(ctx_, x.f32(), proj.f32(), n * c);
     copy(ctx_, normed.f32(), x.f32(), n * c);
     layer_norm(ctx_, normed.f32(), l.ln2_w, l.ln2_b, n, c, kClipEps);
-    linear(ctx_, normed.f32(), n, c, l.fc1, cd.mlp, l.fc1_b, wide.f32());
+    project(normed.f32(), n, c, l.fc1, cd.mlp, l.fc1_b, wide.f32());
     quick_gelu(ctx_, wide.f32(), n * cd.mlp);
-    linear(ctx_, wide.f32(), n, cd.mlp, l.fc2, c, l.fc2_b, proj.f32());
+    project(wide.f32(), n, cd.mlp, l.fc2, c, l.fc2_b, proj.f32());
     add_inplace(ctx_, x.f32(), proj.f32(), n * c);
   }
 }
@@ -410,7 +421,7 @@ void VisionEncoder::encode_view(const float* image_device, std::int64_t size, fl
   clip_forward(cells.f32(), g, clip);
   Array joined = f32(ctx_, n * (cw + sw));
   concat_cols(ctx_, clip.f32() + cw, cw, cells.f32(), sw, n, joined.f32());  // the class row dropped
-  linear(ctx_, joined.f32(), n, cw + sw, w_.projector, dims_.hidden, w_.projector_b, out);
+  project(joined.f32(), n, cw + sw, w_.projector, dims_.hidden, w_.projector_b, out);
 }
 
 std::vector<float> VisionEncoder::encode_view(const View& image) const {

@@ -16,10 +16,12 @@
 //   out = [c[1:] | y] Wproj + b                    [g4 * g4, hidden]
 // Activations are kept as rows [positions, channels]; a 3 x 3 convolution
 // turns its input to [channels, h, w] once for the patch gather. Every
-// matrix product of the projections and convolutions runs on the matrix
-// cores (x rounded to bf16, fp32 sums: the reference's linear); attention is
-// fp32 (gemm_nt, the rel-pos bias + softmax in one pass, gemm_nn) head by
-// head over all windows at once. The learned position grids and the
+// matrix product of the projections and convolutions runs on the bf16
+// matrix cores (x rounded to bf16, fp32 sums: the reference's linear), k
+// split over a workspace where a product has too few tiles (CLIP's 257
+// rows); attention is fp32 on the fp32 matrix cores, one launch per layer
+// for every head and window (scores, bias, softmax and values without the
+// scores reaching memory). The learned position grids and the
 // relative-position tables are resized on the host once per grid size, as
 // the reference does, and kept on the device.
 
@@ -152,6 +154,10 @@ class VisionEncoder {
                                         std::int64_t tiles_high, bool tiled);
 
  private:
+  // y = bf16(x) w^T (+ bias) on the matrix cores, k split over a pool
+  // workspace where the product has too few tiles to cover the GPU.
+  void project(const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w, std::int64_t n,
+               const float* bias, float* y) const;
   void sam_forward(const float* image, std::int64_t size, Array& cells) const;
   void sam_block(std::size_t index, Array& x, std::int64_t g) const;
   void sam_attention(std::size_t index, const float* x, std::int64_t windows, std::int64_t h, std::int64_t w,

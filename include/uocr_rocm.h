@@ -322,6 +322,20 @@ UOCR_ROCM_API int uocr_rocm_linear(void* stream, const float* x, int64_t m, int6
  * into LDS. */
 UOCR_ROCM_API int uocr_rocm_linear_bf16x(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w,
                                          int64_t n, const float* bias, float* y);
+/* New: uocr_rocm_linear and uocr_rocm_linear_bf16x with a workspace of
+ * workspace_floats fp32 values: where the m x n tiles are too few to cover
+ * the GPU, k is split over the workspace (each split's partial products,
+ * then their sum in split order and the bias in one more launch); with a
+ * workspace smaller than uocr_rocm_linear_workspace_floats(m, k, n) (0 when
+ * no split is taken) the product runs unsplit. Allocates nothing. */
+UOCR_ROCM_API int64_t uocr_rocm_linear_workspace_floats(int64_t m, int64_t k, int64_t n);
+UOCR_ROCM_API int uocr_rocm_linear_ws(void* stream, const float* x, int64_t m, int64_t k, const uint16_t* w,
+                                      int64_t n, const float* bias, float* y, float* workspace,
+                                      int64_t workspace_floats);
+UOCR_ROCM_API int uocr_rocm_linear_bf16x_ws(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w,
+                                            int64_t n, const float* bias, float* y, float* workspace,
+                                            int64_t workspace_floats);
+
 /* New: dst[i] = bf16(src[i]), nearest even; both 16-byte aligned. */
 UOCR_ROCM_API int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst);
 

@@ -119,3 +119,34 @@ def test_linear_rejects_bad_shapes(backend):
     w = torch.zeros(3, 16, dtype=torch.bfloat16, device="cuda")
     backend.linear(x, w, y)  # contiguous copies are aligned
     assert torch.count_nonzero(y) == 0
+
+
+@pytest.mark.parametrize("m,k,n,fp32_x", [(257, 1024, 1024, True), (257, 4096, 1024, True), (257, 1024, 3072, False),
+                                          (300, 1280, 520, True), (4096, 3072, 768, True), (5, 2048, 40, False)])
+def test_linear_split_k_against_the_oracle(backend, m, k, n, fp32_x):
+    """Products with too few tiles split k over a workspace (CLIP's 257 rows):
+    the same sums in another order, against the oracle and against the
+    unsplit product."""
+    x = normal(440 + m, (m, k))
+    wb = bf16(0.03 * normal(441 + n, (n, k)))
+    bias = normal(442, n)
+    floats = backend.linear_workspace_floats(m, k, n)
+    ws = torch.full((max(floats, 1),), float("nan"), device="cuda")
+    xd = dev_f32(x)
+    if not fp32_x:
+        xd = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
+        backend.round_bf16(dev_f32(x), xd)
+    y = torch.full((m, n), float("nan"), device="cuda")
+    backend.linear_ws(xd, dev_bf16(wb), y, ws, dev_f32(bias))
+    rows = np.unique(np.array([0, 1, m // 2, m - 1]))
+    want = oracle.linear(oracle.bf16_round(x[rows]), oracle.bf16_to_f32(wb), bias)
+    assert_f32_close(host_f32(y)[rows], want, 1e-5, f"split linear m={m} k={k} n={n} ({floats} floats)")
+    y1 = torch.empty(m, n, device="cuda")
+    backend.linear(xd, dev_bf16(wb), y1, dev_f32(bias))
+    assert_f32_close(host_f32(y), host_f32(y1), 1e-5, "split and unsplit agree")
+    if m >= 257:
+        assert floats > 0, "a 257-row product splits k"
+    small = torch.zeros(1, device="cuda")  # a workspace too small: the product runs unsplit
+    y2 = torch.empty(m, n, device="cuda")
+    backend.linear_ws(xd, dev_bf16(wb), y2, small, dev_f32(bias))
+    assert np.array_equal(host_f32(y2), host_f32(y1))
