@@ -24,6 +24,11 @@
 // register i holds, so P needs no movement; each 32 columns of the head are
 // 16 products into 16 accumulators.
 //
+// With a mask, a wave reads its 32 x 32 block of the mask before a tile's
+// products and skips the tile where every entry is -inf: a causal mask's
+// upper tiles, and all but the selected blocks (32 keys each) of the
+// decoder's routed mask, cost only their share of the K/V staging.
+//
 // Arithmetic: fp32 products and sums on the matrix cores; the scores are
 // scaled, then the bias added (the reference's order); e = exp(s - running
 // max) with the running sum and the output rescaled when the max grows;
@@ -176,71 +181,95 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     const bool more = t + 1 < tiles;
     if (more) load_tile<HD, kThreads>(a, kb, vb, key0 + kKeyTile, kr, vr);
 
-    // S^T = K Q^T: 32 keys x 32 queries
-    f32x16 s;
+    // With a mask, this wave's 32 x 32 block of it first: where every entry
+    // is -inf (a causal or routed mask's dead tiles) the wave skips the
+    // tile's products and softmax; the tile's K and V still reach LDS for
+    // the other waves.
+    float mk[kBias == Bias::kMask ? 16 : 1];
+    bool live = true;
+    if constexpr (kBias == Bias::kMask) {
+      bool any = false;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-    const float* krow = ks + c * T::kKStride + hl * kHalf;
-#pragma unroll
-    for (int i = 0; i < kHalf; i += 4) {
-      const float4 kk = *reinterpret_cast<const float4*>(krow + i);
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.x, qv[i], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.y, qv[i + 1], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.z, qv[i + 2], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.w, qv[i + 3], s, 0, 0, 0);
-    }
-
-    // scale, bias, running max
-    float tmax = -INFINITY;
-    int ky0 = 0, kx0 = 0;
-    if constexpr (kBias == Bias::kRelPos) {
-      ky0 = key0 / a.w;  // once per tile; the lane's keys step from here
-      kx0 = key0 - ky0 * a.w;
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int off = 8 * (r / 4) + 4 * hl + (r % 4), key = key0 + off;
-      float x = s[r] * a.scale;
-      if constexpr (kBias == Bias::kMask) {
-        if (key < a.keys && qin) x = x + a.mask[qrow * a.mask_ld + key];
-      } else if constexpr (kBias == Bias::kRelPos) {
-        int ky = ky0, kx = kx0 + off;
-        while (kx >= a.w) {
-          kx -= a.w;
-          ++ky;
-        }
-        if (key < a.keys) x = x + (my_dots[ky] + my_dots[a.h + kx]);
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + 8 * (r / 4) + 4 * hl + (r % 4);
+        mk[r] = key < a.keys && qin ? a.mask[qrow * a.mask_ld + key] : -INFINITY;
+        any = any || mk[r] != -INFINITY;
       }
-      x = key < a.keys ? x : -INFINITY;
-      s[r] = x;
-      tmax = fmaxf(tmax, x);
+      live = __ballot(any) != 0;
     }
-    tmax = fmaxf(tmax, partner(tmax));
-    const float m_new = fmaxf(m, tmax);
-    const bool dead = m_new == -INFINITY;  // nothing finite yet
-    const float corr = dead ? 1.0f : __builtin_amdgcn_exp2f((m - m_new) * kLog2e);
-    float psum = 0.0f;
+    if (live) {
+      // S^T = K Q^T: 32 keys x 32 queries
+      f32x16 s;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = dead ? 0.0f : __builtin_amdgcn_exp2f((s[r] - m_new) * kLog2e);
-      psum += s[r];
-    }
-    psum += partner(psum);
-    l = l * corr + psum;
-    m = m_new;
+      for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+      const float* krow = ks + c * T::kKStride + hl * kHalf;
 #pragma unroll
-    for (int b = 0; b < kDBlocks; ++b) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[b][r] *= corr;
-    }
+      for (int i = 0; i < kHalf; i += 4) {
+        const float4 kk = *reinterpret_cast<const float4*>(krow + i);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.x, qv[i], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.y, qv[i + 1], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.z, qv[i + 2], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.w, qv[i + 3], s, 0, 0, 0);
+      }
 
-    // O^T += V^T P^T: product i sums keys 8 (i / 4) + i % 4 + 4 h, held in s[i]
+      // scale, bias, running max
+      float tmax = -INFINITY;
+      int ky0 = 0, kx0 = 0;
+      if constexpr (kBias == Bias::kRelPos) {
+        ky0 = key0 / a.w;  // once per tile; the lane's keys step from here
+        kx0 = key0 - ky0 * a.w;
+      }
 #pragma unroll
-    for (int b = 0; b < kDBlocks; ++b) {
+      for (int r = 0; r < 16; ++r) {
+        const int off = 8 * (r / 4) + 4 * hl + (r % 4), key = key0 + off;
+        float x = s[r] * a.scale;
+        if constexpr (kBias == Bias::kMask) {
+          x = x + mk[r];
+        } else if constexpr (kBias == Bias::kRelPos) {
+          int ky = ky0, kx = kx0 + off;
+          while (kx >= a.w) {
+            kx -= a.w;
+            ++ky;
+          }
+          if (key < a.keys) x = x + (my_dots[ky] + my_dots[a.h + kx]);
+        }
+        x = key < a.keys ? x : -INFINITY;
+        s[r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+      tmax = fmaxf(tmax, partner(tmax));
+      const float m_new = fmaxf(m, tmax);
+      const bool dead = m_new == -INFINITY;  // nothing finite yet
+      const float corr = dead ? 1.0f : __builtin_amdgcn_exp2f((m - m_new) * kLog2e);
+      float psum = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = 8 * (i / 4) + 4 * hl + (i % 4);
-        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * HD + 32 * b + c], s[i], o[b], 0, 0, 0);
+      for (int r = 0; r < 16; ++r) {
+        s[r] = dead ? 0.0f : __builtin_amdgcn_exp2f((s[r] - m_new) * kLog2e);
+        psum += s[r];
+      }
+      psum += partner(psum);
+      l = l * corr + psum;
+      m = m_new;
+      // the accumulators are rescaled only when some row's max moved (a
+      // factor of exactly 1 elsewhere): most tiles skip the 16 hd / 32
+      // multiplies and the moves of the accumulators out of and back into
+      // the matrix registers
+      if (__ballot(corr != 1.0f) != 0) {
+#pragma unroll
+        for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[b][r] *= corr;
+        }
+      }
+
+      // O^T += V^T P^T: product i sums keys 8 (i / 4) + i % 4 + 4 h, held in s[i]
+#pragma unroll
+      for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = 8 * (i / 4) + 4 * hl + (i % 4);
+          o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * HD + 32 * b + c], s[i], o[b], 0, 0, 0);
+        }
       }
     }
 
