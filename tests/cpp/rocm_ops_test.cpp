@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <map>
 #include <random>
 #include <stdexcept>
 #include <string>
@@ -25,6 +26,7 @@
 #include "backend/rocm/dtype.h"
 #include "backend/rocm/ops.h"
 #include "model/rocm/decode_step.h"
+#include "model/rocm/model.h"
 #include "../../oracle/uocr_oracle.h"
 
 namespace ro = uocr::rocm;
@@ -884,28 +886,9 @@ struct OracleDecoder {
   }
 };
 
-void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
-  // A prompt of 48 rows (8 text rows, then two image pages of 20 rows) run
-  // through DecodeStep::prefill, then 40 decode steps on the caches it
-  // wrote, the logits of each against the oracle's decoder on the same
-  // weights (the shape of the reference's tests/cuda_decoder_test.cpp:
-  // 99-137, which holds both to 2e-2; here the prefill is held to 1e-4, each
-  // step to 1e-3 and the median step to 1e-5: the device and the oracle make
-  // the same routing choices, so only fp32 summation order separates them).
-  // Router as the reference test sets it: block 4, one local block,
-  // idx_scale 4. Head dim 16 takes the prefill's three-launch attention
-  // (products, mask + softmax, products), 64 the one-pass attention.
-  std::printf("prefill then decode, head dim %lld\n", static_cast<long long>(head_dim));
-  ro::DecoderDims d;
-  d.hidden = 64;
-  d.heads = 2;
-  d.head_dim = head_dim;
-  d.index_dim = head_dim;
-  d.vocab = 300;
-  d.capacity = 128;
-  d.router.block_size = 4;
-  d.router.local_blocks = 1;
-  d.router.idx_scale = 4.0f;
+// The prefill test's decoder weights (2 layers: dense, then mixture of
+// experts) on the oracle's side; embed [vocab, hidden] beside them.
+OracleDecoder make_oracle_decoder(const ro::DecoderDims& d, std::vector<float>& embed) {
   const std::int64_t H = d.hidden, W = d.heads * d.head_dim, D = d.index_dim, V = d.vocab, P = 3 * W + 2 * D;
   OracleDecoder od;
   od.d = d;
@@ -920,7 +903,7 @@ void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
     return w;
   };
   auto bw = [&](std::int64_t n, float sc) { return bf16_rounded(random(static_cast<std::size_t>(n), sc)); };
-  const auto embed = bw(V * H, 0.5f);
+  embed = bw(V * H, 0.5f);
   od.lm = bw(V * H, 0.1f);
   od.final_norm = norm_w(H);
   od.layers.resize(2);
@@ -948,6 +931,34 @@ void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
       l.sd = bw(H * od.shared_ffn, 0.15f);
     }
   }
+  return od;
+}
+
+void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
+  // A prompt of 48 rows (8 text rows, then two image pages of 20 rows) run
+  // through DecodeStep::prefill, then 40 decode steps on the caches it
+  // wrote, the logits of each against the oracle's decoder on the same
+  // weights (the shape of the reference's tests/cuda_decoder_test.cpp:
+  // 99-137, which holds both to 2e-2; here the prefill is held to 1e-4, each
+  // step to 1e-3 and the median step to 1e-5: the device and the oracle make
+  // the same routing choices, so only fp32 summation order separates them).
+  // Router as the reference test sets it: block 4, one local block,
+  // idx_scale 4. Head dim 16 takes the prefill's three-launch attention
+  // (products, mask + softmax, products), 64 the one-pass attention.
+  std::printf("prefill then decode, head dim %lld\n", static_cast<long long>(head_dim));
+  ro::DecoderDims d;
+  d.hidden = 64;
+  d.heads = 2;
+  d.head_dim = head_dim;
+  d.index_dim = head_dim;
+  d.vocab = 300;
+  d.capacity = 128;
+  d.router.block_size = 4;
+  d.router.local_blocks = 1;
+  d.router.idx_scale = 4.0f;
+  const std::int64_t H = d.hidden, W = d.heads * d.head_dim, D = d.index_dim, V = d.vocab;
+  std::vector<float> embed;
+  OracleDecoder od = make_oracle_decoder(d, embed);
   std::vector<ro::Array> keep;
   auto dev = [&](const std::vector<float>& v, ro::DType t) {
     keep.push_back(up(ctx, v, t));
@@ -1022,6 +1033,275 @@ void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
     ro::DecodeStep s2(ctx, bd, b16(embed), lw, f32(od.final_norm), b16(od.lm));
     require_throws_invalid([&] { s2.prefill(x, coords, qp); }, "prefill over a bf16 cache");
   }
+}
+
+// A TensorSource over named host tensors, as a checkpoint would serve them.
+class MapSource final : public ro::TensorSource {
+ public:
+  ro::HostTensor get(const std::string& name) const override {
+    const auto it = t.find(name);
+    if (it == t.end()) throw std::out_of_range("MapSource: no tensor " + name);
+    return it->second;
+  }
+  void put(const std::string& name, std::vector<std::int64_t> shape, std::vector<float> v) {
+    t[name] = ro::HostTensor{std::move(shape), std::move(v)};
+  }
+  const float* at(const std::string& name) const { return t.at(name).data.data(); }
+  std::map<std::string, ro::HostTensor> t;
+};
+
+// The whole model loaded by the reference's checkpoint names
+// (src/weights/architecture.cpp:38-139) through ro::Model: the decoder of
+// prefill_then_decode split back into its named projections and experts,
+// beside the reference's tiny vision model; the decoder's logits against
+// the oracle's decoder on the same weights, the embeddings exactly, the
+// page features against the oracle's encoder, and a missing or misshaped
+// tensor refused.
+void model_by_names(const ro::Context& ctx) {
+  ro::DecoderDims d;
+  d.hidden = 64;
+  d.heads = 2;
+  d.head_dim = 16;
+  d.index_dim = 16;
+  d.vocab = 300;
+  d.capacity = 128;
+  d.router.block_size = 4;
+  d.router.local_blocks = 1;
+  d.router.idx_scale = 4.0f;
+  const std::int64_t H = d.hidden, W = d.heads * d.head_dim, D = d.index_dim, V = d.vocab;
+  std::vector<float> embed;
+  OracleDecoder od = make_oracle_decoder(d, embed);
+  const std::int64_t E = od.experts, F = od.expert_ffn, SF = od.shared_ffn;
+  MapSource src;
+  auto part = [](const std::vector<float>& v, std::int64_t from, std::int64_t n) {
+    return std::vector<float>(v.begin() + from, v.begin() + from + n);
+  };
+  src.put("model.embed_tokens.weight", {V, H}, embed);
+  for (std::int64_t li = 0; li < 2; ++li) {
+    const auto& l = od.layers[static_cast<std::size_t>(li)];
+    const std::string p = "model.layers." + std::to_string(li) + ".", r = p + "self_attn.dash_router.";
+    src.put(p + "input_layernorm.weight", {H}, l.in);
+    src.put(p + "post_attention_layernorm.weight", {H}, l.post);
+    src.put(p + "self_attn.q_proj.weight", {W, H}, part(l.proj, 0, W * H));
+    src.put(p + "self_attn.k_proj.weight", {W, H}, part(l.proj, W * H, W * H));
+    src.put(p + "self_attn.v_proj.weight", {W, H}, part(l.proj, 2 * W * H, W * H));
+    src.put(r + "q_proj.weight", {D, H}, part(l.proj, 3 * W * H, D * H));
+    src.put(r + "k_proj.weight", {D, H}, part(l.proj, 3 * W * H + D * H, D * H));
+    src.put(r + "q_norm.weight", {D}, l.rqn);
+    src.put(r + "k_norm.weight", {D}, l.rkn);
+    src.put(r + "head_cls", {D}, l.cls);
+    src.put(p + "self_attn.o_proj.weight", {H, W}, l.o);
+    if (!l.moe) {
+      src.put(p + "mlp.gate_proj.weight", {od.ffn, H}, l.gate);
+      src.put(p + "mlp.up_proj.weight", {od.ffn, H}, l.up);
+      src.put(p + "mlp.down_proj.weight", {H, od.ffn}, l.down);
+    } else {
+      src.put(p + "mlp.gate.weight", {E, H}, l.router);
+      for (std::int64_t e = 0; e < E; ++e) {
+        const std::string x = p + "mlp.experts." + std::to_string(e) + ".";
+        src.put(x + "gate_proj.weight", {F, H}, part(l.gstack, e * F * H, F * H));
+        src.put(x + "up_proj.weight", {F, H}, part(l.ustack, e * F * H, F * H));
+        src.put(x + "down_proj.weight", {H, F}, part(l.dstack, e * H * F, H * F));
+      }
+      src.put(p + "mlp.shared_experts.gate_proj.weight", {SF, H}, l.sg);
+      src.put(p + "mlp.shared_experts.up_proj.weight", {SF, H}, l.su);
+      src.put(p + "mlp.shared_experts.down_proj.weight", {H, SF}, l.sd);
+    }
+  }
+  src.put("model.norm.weight", {H}, od.final_norm);
+  src.put("lm_head.weight", {V, H}, od.lm);
+
+  // the reference's tiny vision model (tests/vision_test.cpp:17-33) with
+  // the decoder's hidden width
+  ro::VisionDims vd;
+  vd.sam.width = 24;
+  vd.sam.layers = 2;
+  vd.sam.heads = 2;
+  vd.sam.mlp = 48;
+  vd.sam.global_layers = {1};
+  vd.sam.neck = 8;
+  vd.sam.net2 = 12;
+  vd.sam.net3 = 16;
+  vd.clip.width = 16;
+  vd.clip.layers = 2;
+  vd.clip.heads = 2;
+  vd.clip.mlp = 32;
+  const ro::SamDims& sd = vd.sam;
+  const ro::ClipDims& cd = vd.clip;
+  const std::int64_t pg = sd.image / sd.patch, shd = sd.width / sd.heads;
+  auto rnd = [&](std::vector<std::int64_t> shape, bool one = false) {
+    std::int64_t n = 1;
+    for (auto x : shape) n *= x;
+    auto v = bf16_rounded(random(static_cast<std::size_t>(n), 0.05f));
+    if (one) {
+      for (float& x : v) x = ro::bf16_to_f32(ro::f32_to_bf16(x + 1.0f));
+    }
+    return v;
+  };
+  auto vput = [&](const std::string& name, std::vector<std::int64_t> shape, bool one = false) {
+    src.put(name, shape, rnd(shape, one));
+  };
+  const std::string sam = "model.sam_model.";
+  vput(sam + "patch_embed.proj.weight", {sd.width, 3, sd.patch, sd.patch});
+  vput(sam + "patch_embed.proj.bias", {sd.width});
+  vput(sam + "pos_embed", {1, pg, pg, sd.width});
+  for (std::int64_t i = 0; i < sd.layers; ++i) {
+    const std::string p = sam + "blocks." + std::to_string(i) + ".";
+    const std::int64_t span = i == 1 ? pg : sd.window;
+    vput(p + "norm1.weight", {sd.width}, true);
+    vput(p + "norm1.bias", {sd.width});
+    vput(p + "attn.qkv.weight", {3 * sd.width, sd.width});
+    vput(p + "attn.qkv.bias", {3 * sd.width});
+    vput(p + "attn.proj.weight", {sd.width, sd.width});
+    vput(p + "attn.proj.bias", {sd.width});
+    vput(p + "attn.rel_pos_h", {2 * span - 1, shd});
+    vput(p + "attn.rel_pos_w", {2 * span - 1, shd});
+    vput(p + "norm2.weight", {sd.width}, true);
+    vput(p + "norm2.bias", {sd.width});
+    vput(p + "mlp.lin1.weight", {sd.mlp, sd.width});
+    vput(p + "mlp.lin1.bias", {sd.mlp});
+    vput(p + "mlp.lin2.weight", {sd.width, sd.mlp});
+    vput(p + "mlp.lin2.bias", {sd.width});
+  }
+  vput(sam + "neck.0.weight", {sd.neck, sd.width, 1, 1});
+  vput(sam + "neck.1.weight", {sd.neck}, true);
+  vput(sam + "neck.1.bias", {sd.neck});
+  vput(sam + "neck.2.weight", {sd.neck, sd.neck, 3, 3});
+  vput(sam + "neck.3.weight", {sd.neck}, true);
+  vput(sam + "neck.3.bias", {sd.neck});
+  vput(sam + "net_2.weight", {sd.net2, sd.neck, 3, 3});
+  vput(sam + "net_3.weight", {sd.net3, sd.net2, 3, 3});
+  const std::string clip = "model.vision_model.";
+  vput(clip + "embeddings.class_embedding", {cd.width});
+  vput(clip + "embeddings.position_embedding.weight", {cd.positions, cd.width});
+  vput(clip + "pre_layrnorm.weight", {cd.width}, true);
+  vput(clip + "pre_layrnorm.bias", {cd.width});
+  for (std::int64_t i = 0; i < cd.layers; ++i) {
+    const std::string p = clip + "transformer.layers." + std::to_string(i) + ".";
+    vput(p + "layer_norm1.weight", {cd.width}, true);
+    vput(p + "layer_norm1.bias", {cd.width});
+    vput(p + "self_attn.qkv_proj.weight", {3 * cd.width, cd.width});
+    vput(p + "self_attn.qkv_proj.bias", {3 * cd.width});
+    vput(p + "self_attn.out_proj.weight", {cd.width, cd.width});
+    vput(p + "self_attn.out_proj.bias", {cd.width});
+    vput(p + "layer_norm2.weight", {cd.width}, true);
+    vput(p + "layer_norm2.bias", {cd.width});
+    vput(p + "mlp.fc1.weight", {cd.mlp, cd.width});
+    vput(p + "mlp.fc1.bias", {cd.mlp});
+    vput(p + "mlp.fc2.weight", {cd.width, cd.mlp});
+    vput(p + "mlp.fc2.bias", {cd.width});
+  }
+  vput("model.projector.layers.weight", {H, cd.width + sd.net3});
+  vput("model.projector.layers.bias", {H});
+  vput("model.image_newline", {H});
+  vput("model.view_seperator", {H});
+
+  ro::ModelDims md;
+  md.decoder = d;
+  md.layers = 2;
+  md.dense_ffn = od.ffn;
+  md.first_moe_layer = 1;
+  md.routed_experts = E;
+  md.experts_per_token = od.top_k;
+  md.shared_experts = SF / F;
+  md.expert_ffn = F;
+  md.vision = vd;
+  ro::Model model(ctx, src, md);
+
+  // embeddings: the table's rows exactly
+  const std::vector<std::int64_t> ids = {0, 17, 299, 17};
+  const auto emb = model.embed(ids);
+  for (std::size_t i = 0; i < ids.size(); ++i) {
+    require(std::memcmp(emb.data() + i * H, embed.data() + ids[i] * H, static_cast<std::size_t>(H) * 4) == 0,
+            "Model::embed row " + std::to_string(ids[i]));
+  }
+
+  // the decoder: a prompt of 28 rows (8 text, one image page of 20), then 5 steps
+  const std::int64_t rows = 28;
+  std::vector<ro::RopeCoord> coords(rows);
+  std::vector<std::int64_t> qp(rows);
+  for (std::int64_t r = 0; r < rows; ++r) {
+    const bool image = r >= 8;
+    coords[r] = image ? ro::RopeCoord{8 + (r - 8) % 20, 0} : ro::RopeCoord{r, 0};
+    qp[r] = image ? 0 : -1;
+  }
+  od.min_page.assign(7, -1);
+  for (std::int64_t b = 2; b < 7; ++b) od.min_page[b] = 0;
+  od.max_page = od.min_page;
+  model.decoder().set_prompt_blocks(od.min_page, od.max_page);
+  od.inv_tok = rope_inv(d.head_dim / 2 - d.page_pairs, d.rope_theta);
+  od.inv_page = rope_inv(d.page_pairs, d.page_theta);
+  od.kc.assign(2, std::vector<float>(d.capacity * W, 0.0f));
+  od.vc = od.kc;
+  od.rkc.assign(2, std::vector<float>(d.capacity * D, 0.0f));
+  const auto x = random(rows * H, 0.5f);
+  expect("model by names: prefill logits", max_rel(model.decoder().prefill(x, coords, qp), od.forward(x, coords, qp, false)),
+         1e-4);
+  for (std::int64_t t = 0; t < 5; ++t) {
+    const std::int64_t token = 1 + 37 * t;
+    const ro::RopeCoord c{28 + t, 1};
+    const auto g = model.decoder().step(token, c, 0);
+    const std::vector<float> row(embed.begin() + token * H, embed.begin() + (token + 1) * H);
+    expect(("model by names: decode step " + std::to_string(t)).c_str(), max_rel(g, od.forward(row, {c}, {0}, true)),
+           1e-3);
+  }
+
+  // the vision encoder: a base page of a 128-pixel view against the oracle's
+  std::vector<orc_sam_block> blocks(static_cast<std::size_t>(sd.layers));
+  for (std::int64_t i = 0; i < sd.layers; ++i) {
+    const std::string p = sam + "blocks." + std::to_string(i) + ".";
+    orc_sam_block& b = blocks[static_cast<std::size_t>(i)];
+    b = {src.at(p + "norm1.weight"), src.at(p + "norm1.bias"), src.at(p + "attn.qkv.weight"), src.at(p + "attn.qkv.bias"),
+         src.at(p + "attn.proj.weight"), src.at(p + "attn.proj.bias"), src.at(p + "attn.rel_pos_h"),
+         src.at(p + "attn.rel_pos_w"), src.t.at(p + "attn.rel_pos_h").shape[0], src.at(p + "norm2.weight"),
+         src.at(p + "norm2.bias"), src.at(p + "mlp.lin1.weight"), src.at(p + "mlp.lin1.bias"),
+         src.at(p + "mlp.lin2.weight"), src.at(p + "mlp.lin2.bias"), i == 1 ? 1 : 0};
+  }
+  std::vector<orc_clip_layer> clayers(static_cast<std::size_t>(cd.layers));
+  for (std::int64_t i = 0; i < cd.layers; ++i) {
+    const std::string p = clip + "transformer.layers." + std::to_string(i) + ".";
+    clayers[static_cast<std::size_t>(i)] = {
+        src.at(p + "layer_norm1.weight"), src.at(p + "layer_norm1.bias"), src.at(p + "self_attn.qkv_proj.weight"),
+        src.at(p + "self_attn.qkv_proj.bias"), src.at(p + "self_attn.out_proj.weight"),
+        src.at(p + "self_attn.out_proj.bias"), src.at(p + "layer_norm2.weight"), src.at(p + "layer_norm2.bias"),
+        src.at(p + "mlp.fc1.weight"), src.at(p + "mlp.fc1.bias"), src.at(p + "mlp.fc2.weight"),
+        src.at(p + "mlp.fc2.bias")};
+  }
+  orc_vision_weights ow{};
+  ow.sam_dims = {sd.image, sd.patch, sd.width, sd.layers, sd.heads, sd.mlp, sd.window, sd.neck, sd.net2, sd.net3};
+  ow.sam = {src.at(sam + "patch_embed.proj.weight"), src.at(sam + "patch_embed.proj.bias"), src.at(sam + "pos_embed"),
+            blocks.data(), src.at(sam + "neck.0.weight"), src.at(sam + "neck.1.weight"), src.at(sam + "neck.1.bias"),
+            src.at(sam + "neck.2.weight"), src.at(sam + "neck.3.weight"), src.at(sam + "neck.3.bias"),
+            src.at(sam + "net_2.weight"), src.at(sam + "net_3.weight")};
+  ow.clip_dims = {cd.width, cd.layers, cd.heads, cd.mlp, cd.positions};
+  ow.clip = {src.at(clip + "embeddings.class_embedding"), src.at(clip + "embeddings.position_embedding.weight"),
+             src.at(clip + "pre_layrnorm.weight"), src.at(clip + "pre_layrnorm.bias"), clayers.data()};
+  ow.projector_w = src.at("model.projector.layers.weight");
+  ow.projector_b = src.at("model.projector.layers.bias");
+  ow.newline = src.at("model.image_newline");
+  ow.separator = src.at("model.view_seperator");
+  ow.hidden = H;
+  auto img = random(3 * 128 * 128, 0.5f);
+  const auto got = model.encode_page(ro::View{img, 128});
+  std::vector<float> want(got.size());
+  require(orc_encode_page(&ow, img.data(), 128, nullptr, 0, 0, 1, 1, want.data(), 1) ==
+              static_cast<std::int64_t>(got.size()) / H,
+          "model by names: page token count");
+  expect("model by names: page features", max_rel(got, want), 1e-2);
+
+  // a missing tensor and a misshaped one are refused
+  MapSource broken = src;
+  broken.t.erase("model.layers.1.mlp.experts.3.up_proj.weight");
+  bool missing = false;
+  try {
+    ro::Model bad(ctx, broken, md);
+  } catch (const std::out_of_range&) {
+    missing = true;
+  }
+  require(missing, "a missing tensor is refused");
+  MapSource odd = src;
+  odd.put("model.layers.0.self_attn.o_proj.weight", {W, H}, std::vector<float>(static_cast<std::size_t>(W * H + 1)));
+  require_throws_invalid([&] { ro::Model bad(ctx, odd, md); }, "a misshaped tensor is refused");
 }
 
 void step_ops(const ro::Context& ctx) {
@@ -1112,6 +1392,7 @@ int main() {
     decode_step(ctx, false);
     prefill_then_decode(ctx, 16);
     prefill_then_decode(ctx, 64);
+    model_by_names(ctx);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());
