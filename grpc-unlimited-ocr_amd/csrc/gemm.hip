@@ -194,10 +194,16 @@ __device__ __forceinline__ void store_step(const Staged<kF32X>& s, u32x4* xs, u3
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // The 16 matrix products of one 64-wide k step of a wave's 64 x 64 quarter
-// from the tiles in LDS, the operand reads of each 16-wide slice issued
-// before the previous slice's products.
+// from the tiles in LDS. The operand reads of slice kk + 1 go out one
+// between each two products of slice kk, and `issue` (the next step's
+// memory-to-LDS loads, kIssued instructions, or nothing) among the first
+// slice's products: a wave never waits on LDS with products it could have
+// issued (the group barriers pin that order; left to itself the scheduler
+// bunches the reads and waits for them before the products).
+template <int kIssued, class Issue>
 __device__ __forceinline__ void mfma_step(const u32x4* xs, const u32x4* ws, int wm, int wn, int half, int r32,
-                                          f32x16 (&acc)[2][2]) {
+                                          f32x16 (&acc)[2][2], Issue issue) {
+  constexpr int kMfma = 0x008, kDsRead = 0x100, kVmemRead = 0x020;
   bf16x8 fa[2][2], fb[2][2];
   auto read = [&](int kk, int b) {
     const int c = 2 * kk + half;
@@ -207,9 +213,11 @@ __device__ __forceinline__ void mfma_step(const u32x4* xs, const u32x4* ws, int 
     for (int j = 0; j < 2; ++j) fb[b][j] = as_bf16x8(ws[slot(64 * wn + 32 * j + r32, c)]);
   };
   read(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int kk = 0; kk < kTileK / 16; ++kk) {
     if (kk + 1 < kTileK / 16) read(kk + 1, (kk + 1) & 1);
+    if (kk == 0) issue();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -217,6 +225,15 @@ __device__ __forceinline__ void mfma_step(const u32x4* xs, const u32x4* ws, int 
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
       }
     }
+    if (kk + 1 < kTileK / 16) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+        if (kk == 0 && kIssued > 0) __builtin_amdgcn_sched_group_barrier(kVmemRead, (kIssued + 3) / 4, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -294,7 +311,7 @@ __global__ __launch_bounds__(kGemmThreads) void linear_staged_k(const LinearArgs
     const int buf = t & 1;
     const bool more = t + 1 < steps;
     if (more) load(wk.k_begin + (t + 1) * kTileK);
-    mfma_step(xs[buf], ws[buf], wm, wn, half, r32, acc);
+    mfma_step<0>(xs[buf], ws[buf], wm, wn, half, r32, acc, [] {});
     if (more) store_step(s, xs[buf ^ 1], ws[buf ^ 1]);
     lds_barrier();
   }
@@ -344,8 +361,10 @@ __global__ __launch_bounds__(kGemmThreads) void linear_dma_k(const LinearArgs a)
   for (int t = 0; t < steps; ++t) {
     const int buf = t & 1;
     wait_loads_and_barrier<0>();  // this step's tiles are in LDS; every wave is done with the other buffer
-    if (t + 1 < steps) dma_step(a, wk.m0, wk.n0, wk.k_begin + (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
-    mfma_step(xs[buf], ws[buf], wm, wn, half, r32, acc);
+    const bool more = t + 1 < steps;
+    mfma_step<2 * kTileChunks / kGemmThreads>(xs[buf], ws[buf], wm, wn, half, r32, acc, [&] {
+      if (more) dma_step(a, wk.m0, wk.n0, wk.k_begin + (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
+    });
   }
   store_tile(a, wk, wm, wn, half, r32, acc);
 }

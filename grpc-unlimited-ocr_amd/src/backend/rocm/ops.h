@@ -177,6 +177,10 @@ void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint1
 std::int64_t linear_workspace_floats(std::int64_t m, std::int64_t k, std::int64_t n);
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
             std::int64_t n, const float* bias, float* y, float* workspace, std::int64_t workspace_floats);
+// New: the same with x already rounded to bf16.
+void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
+                  const std::uint16_t* w_bf16, std::int64_t n, const float* bias, float* y, float* workspace,
+                  std::int64_t workspace_floats);
 
 // Fused decode projections (new): add + RMSNorm as the GEMV's prologue,
 // optionally a gate/up pair with a SwiGLU epilogue. delta, x_out, w_norm

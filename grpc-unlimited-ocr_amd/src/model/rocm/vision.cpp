@@ -240,13 +240,24 @@ const VisionEncoder::Windows& VisionEncoder::windows(std::int64_t g) const {
 
 void VisionEncoder::project(const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w, std::int64_t n,
                             const float* bias, float* y) const {
+  // Scratch kept across calls (every call is ordered on the one stream):
+  // the split-k workspace, and x rounded to bf16.
+  auto grown = [&](Array& a, DType type, std::int64_t count) -> Array& {
+    if (a.count() < count) a = Array(ctx_, type, count);
+    return a;
+  };
   const std::int64_t floats = linear_workspace_floats(m, k, n);
-  if (floats == 0) {
-    linear(ctx_, x, m, k, w, n, bias, y);
+  float* ws = floats > 0 ? grown(split_ws_, DType::kF32, floats).f32() : nullptr;
+  if (m > 1 && k % 64 == 0 && n >= k) {
+    // x rounded once (the rounding the product applies anyway, bit for bit),
+    // then tiles straight from memory into LDS. The pass costs 6 bytes per
+    // element of x, so it pays where the product is at least as wide as x.
+    Array& xb = grown(x_bf16_, DType::kBF16, m * k);
+    round_bf16(ctx_, x, m * k, xb.bf16());
+    linear_bf16x(ctx_, xb.bf16(), m, k, w, n, bias, y, ws, floats);
     return;
   }
-  Array ws = f32(ctx_, floats);
-  linear(ctx_, x, m, k, w, n, bias, y, ws.f32(), floats);
+  linear(ctx_, x, m, k, w, n, bias, y, ws, floats);
 }
 
 // Attention of one block over `windows` windows of h x w tokens, rows

@@ -181,6 +181,7 @@ class VisionEncoder {
   mutable std::map<std::int64_t, Array> sam_pos_, clip_pos_;
   mutable std::map<std::tuple<std::size_t, bool, std::int64_t>, Array> rel_tables_;
   mutable std::map<std::int64_t, Windows> windows_;
+  mutable Array split_ws_, x_bf16_;  // project()'s scratch, grown on demand
 };
 
 // Host table resizes of the encoder (src/backend/reference/ops.cpp:42-86,
