@@ -22,9 +22,9 @@
 // contiguous run of tiles, ordered in groups of 8 tile-rows sweeping the
 // columns, so the tiles resident on one XCD share x rows and w rows in its
 // L2. The bias is added to each finished sum (one fp32 rounding, as the
-// reference's separate bias pass). A product with too few tiles to cover
-// the GPU (the vision encoder's CLIP projections: 257 rows) may split k
-// over a caller's workspace: each split writes its partial products and one
+// reference's separate bias pass). A product with few tiles and a long k
+// (the vision encoder's convolutions, CLIP's 257-row projections) may split
+// k over a caller's workspace: each split writes its partial products and one
 // more launch sums them in split order, then adds the bias.
 
 #include "common.hpp"
@@ -385,12 +385,15 @@ __global__ __launch_bounds__(kBlock) void round_bf16_k(const float* __restrict__
 
 }  // namespace
 
-// The splits of k worth taking for an m x n x k product: enough
-// workgroups to cover the 256 CUs twice where the tiles alone do not, each
-// split at least 4 steps of 64 columns; 1 when the tiles suffice.
+// The splits of k worth taking for an m x n x k product: a product of
+// fewer than 64 tiles with k >= 1024 gets enough workgroups to cover the 256
+// CUs twice, each split at least 4 steps of 64 columns; any other runs
+// unsplit. (Measured at the vision encoder's shapes: 16-24 tiles with k of
+// 2304-4608 run 1.3-1.9x faster split; 72-234 tiles, or k of 768-1024,
+// lose 5-100% to the partial sums' traffic and the extra launch.)
 int64_t splits_for(int64_t m, int64_t k, int64_t n) {
   const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
-  if (tiles >= 512 || k < 8 * kTileK) return 1;
+  if (tiles >= 64 || k < 16 * kTileK) return 1;
   int64_t s = (512 + tiles - 1) / tiles;
   s = s < k / (4 * kTileK) ? s : k / (4 * kTileK);
   return s < 32 ? s : 32;

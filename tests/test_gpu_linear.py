@@ -124,9 +124,9 @@ def test_linear_rejects_bad_shapes(backend):
 @pytest.mark.parametrize("m,k,n,fp32_x", [(257, 1024, 1024, True), (257, 4096, 1024, True), (257, 1024, 3072, False),
                                           (300, 1280, 520, True), (4096, 3072, 768, True), (5, 2048, 40, False)])
 def test_linear_split_k_against_the_oracle(backend, m, k, n, fp32_x):
-    """Products with too few tiles split k over a workspace (CLIP's 257 rows):
-    the same sums in another order, against the oracle and against the
-    unsplit product."""
+    """Products of few tiles and a long k split k over a workspace (CLIP's 257
+    rows): the same sums in another order, against the oracle and against the
+    unsplit product; wider products or shorter k run unsplit."""
     x = normal(440 + m, (m, k))
     wb = bf16(0.03 * normal(441 + n, (n, k)))
     bias = normal(442, n)
@@ -144,8 +144,11 @@ def test_linear_split_k_against_the_oracle(backend, m, k, n, fp32_x):
     y1 = torch.empty(m, n, device="cuda")
     backend.linear(xd, dev_bf16(wb), y1, dev_f32(bias))
     assert_f32_close(host_f32(y), host_f32(y1), 1e-5, "split and unsplit agree")
-    if m >= 257:
-        assert floats > 0, "a 257-row product splits k"
+    tiles = ((m + 127) // 128) * ((n + 127) // 128)
+    if tiles < 64 and k >= 1024:
+        assert floats > 0, "a product of few tiles and a long k splits"
+    else:
+        assert floats == 0, "a wide product or a short k runs unsplit"
     small = torch.zeros(1, device="cuda")  # a workspace too small: the product runs unsplit
     y2 = torch.empty(m, n, device="cuda")
     backend.linear_ws(xd, dev_bf16(wb), y2, small, dev_f32(bias))
