@@ -45,7 +45,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-enum class Bias { kNone, kMask, kRelPos };
+// kRelPosRows: the relative-position bias where the grid's width is a
+// multiple of the 32-key tile, so a tile's keys are 32 consecutive columns
+// of one grid row: one height term per tile and the width terms as 4-wide
+// vector reads, where kRelPos looks both up per key.
+enum class Bias { kNone, kMask, kRelPos, kRelPosRows };
+template <Bias kBias>
+constexpr bool rel_pos() {
+  return kBias == Bias::kRelPos || kBias == Bias::kRelPosRows;
+}
 constexpr int kQueriesPerWave = 32;
 constexpr int kKeyTile = 32;
 // Waves per workgroup: 4 (128 query rows share each key/value tile), or 2
@@ -53,7 +61,7 @@ constexpr int kKeyTile = 32;
 // (2 waves keep three workgroups on a CU instead of one).
 template <Bias kBias>
 constexpr int waves_of() {
-  return kBias == Bias::kRelPos ? 2 : 4;
+  return rel_pos<kBias>() ? 2 : 4;
 }
 constexpr int kMaxRelSpan = 256;  // h + w of the relative-position bias
 
@@ -67,9 +75,11 @@ struct AttnArgs {
   float scale;
   const float* mask;  // [rows, mask_ld] (kMask)
   int64_t mask_ld;
-  const float* rh;  // [h, h, hd] (kRelPos)
+  const float* rh;  // [h, h, hd] (kRelPos, kRelPosRows)
   const float* rw;  // [w, w, hd]
   int h, w;
+  int dots_ld;  // floats between two query rows' dot products in LDS
+  int dw_off;   // where a row's width terms start (its height terms at 0)
 };
 
 template <int HD, int kThreads>
@@ -120,9 +130,12 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   constexpr int kDBlocks = HD / 32;
   __shared__ __attribute__((aligned(16))) float ks[kKeyTile * T::kKStride];
   __shared__ __attribute__((aligned(16))) float vs[kKeyTile * HD];
-  // kRelPos: per query row its h + w dot products, rows h + w + 1 apart so
-  // that the 32 queries of a wave read 32 different banks
-  extern __shared__ float dots[];
+  // The relative-position bias: per query row its h height terms at 0 and
+  // w width terms at dw_off, rows dots_ld apart: h + w + 1 (odd) for
+  // kRelPos, so that the 32 queries of a wave read 32 different banks; for
+  // kRelPosRows 4 times an odd number with dw_off a multiple of 4, so that
+  // 16 queries' 16-byte reads at one offset cover 16 bank groups.
+  extern __shared__ __attribute__((aligned(16))) float dots[];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hl = lane >> 5, c = lane & 31;
@@ -150,8 +163,8 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     qv[i + 3] = t.w;
   }
 
-  float* my_dots = dots + (wave * kQueriesPerWave + c) * (a.h + a.w + 1);
-  if constexpr (kBias == Bias::kRelPos) {
+  float* my_dots = dots + (wave * kQueriesPerWave + c) * a.dots_ld;
+  if constexpr (rel_pos<kBias>()) {
     // dh[ky] = q . rh[qy, ky] (lane half 0) and dw[kx] = q . rw[qx, kx]
     // (half 1), fp32 in column order, over the whole query row
     const int qy = qin ? qrow / a.w : 0, qx = qin ? qrow - qy * a.w : 0;
@@ -161,7 +174,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     for (int j = 0; j < n_dots; ++j) {
       float s = 0.0f;
       for (int e = 0; e < HD; ++e) s += qr[e] * tab[j * HD + e];
-      my_dots[(hl == 0 ? 0 : a.h) + j] = s;
+      my_dots[(hl == 0 ? 0 : a.dw_off) + j] = s;
     }
   }
 
@@ -215,9 +228,23 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
       // scale, bias, running max
       float tmax = -INFINITY;
       int ky0 = 0, kx0 = 0;
-      if constexpr (kBias == Bias::kRelPos) {
+      if constexpr (rel_pos<kBias>()) {
         ky0 = key0 / a.w;  // once per tile; the lane's keys step from here
         kx0 = key0 - ky0 * a.w;
+      }
+      // kRelPosRows: the tile's height term, and the width terms of this
+      // lane's keys kx0 + 8 g + 4 h + (0..3)
+      float dh = 0.0f, dwv[kBias == Bias::kRelPosRows ? 16 : 1];
+      if constexpr (kBias == Bias::kRelPosRows) {
+        dh = my_dots[ky0];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 t = *reinterpret_cast<const float4*>(my_dots + a.dw_off + kx0 + 8 * g + 4 * hl);
+          dwv[4 * g] = t.x;
+          dwv[4 * g + 1] = t.y;
+          dwv[4 * g + 2] = t.z;
+          dwv[4 * g + 3] = t.w;
+        }
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -231,7 +258,9 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
             kx -= a.w;
             ++ky;
           }
-          if (key < a.keys) x = x + (my_dots[ky] + my_dots[a.h + kx]);
+          if (key < a.keys) x = x + (my_dots[ky] + my_dots[a.dw_off + kx]);
+        } else if constexpr (kBias == Bias::kRelPosRows) {
+          x = x + (dh + dwv[r]);
         }
         x = key < a.keys ? x : -INFINITY;
         s[r] = x;
@@ -299,8 +328,7 @@ int launch(const char* what, void* stream, int64_t hd, int64_t slices, const Att
   constexpr int kThreads = 64 * waves_of<kBias>(), kQueriesPerBlock = waves_of<kBias>() * kQueriesPerWave;
   const dim3 grid(static_cast<unsigned>((a.rows + kQueriesPerBlock - 1) / kQueriesPerBlock),
                   static_cast<unsigned>(slices));
-  const size_t dyn =
-      kBias == Bias::kRelPos ? sizeof(float) * kQueriesPerBlock * static_cast<size_t>(a.h + a.w + 1) : 0;
+  const size_t dyn = rel_pos<kBias>() ? sizeof(float) * kQueriesPerBlock * static_cast<size_t>(a.dots_ld) : 0;
   clear_launch_error();
   if (hd == 64) {
     attention_k<64, kBias><<<grid, kThreads, dyn, as_stream(stream)>>>(a);
@@ -343,7 +371,7 @@ int uocr_rocm_attention(void* stream, const float* q, int64_t ldq, int64_t sq, c
   }
   UOCR_REQUIRE(mask == nullptr || mask_ld >= keys, kWhat, "mask rows must hold every key");
   AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
-             scale, mask, mask_ld, nullptr, nullptr, 0, 0};
+             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0};
   return mask != nullptr ? launch<Bias::kMask>(kWhat, stream, hd, slices, a)
                          : launch<Bias::kNone>(kWhat, stream, hd, slices, a);
 }
@@ -359,9 +387,18 @@ int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64
     return st;
   }
   UOCR_REQUIRE(rh != nullptr && rw != nullptr, kWhat, "null relative-position table");
+  // A grid width of whole tiles takes the per-tile bias terms, the width
+  // terms 16-byte aligned.
+  const bool rows = w % kKeyTile == 0;
+  const int64_t dw_off = rows ? (h + 3) / 4 * 4 : h;
+  int64_t quads = (dw_off + w) / 4;
+  quads += quads % 2 == 0 ? 1 : 0;
+  const int64_t dots_ld = rows ? 4 * quads : h + w + 1;
   AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(n), static_cast<int>(n),
-             scale, nullptr, 0, rh, rw, static_cast<int>(h), static_cast<int>(w)};
-  return launch<Bias::kRelPos>(kWhat, stream, hd, slices, a);
+             scale, nullptr, 0, rh, rw, static_cast<int>(h), static_cast<int>(w), static_cast<int>(dots_ld),
+             static_cast<int>(dw_off)};
+  return rows ? launch<Bias::kRelPosRows>(kWhat, stream, hd, slices, a)
+              : launch<Bias::kRelPos>(kWhat, stream, hd, slices, a);
 }
 
 }  // extern "C"

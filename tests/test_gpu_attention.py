@@ -10,7 +10,8 @@ with an fp64 total, probabilities times v) slice by slice:
   * strided operands as the decoder's prefill holds them (q, k, v columns of
     [rows, heads * hd] rows, the output into the heads' columns);
   * SAM's relative-position bias over 14 x 14 windows and a 64 x 64 global
-    window, against the oracle's rel_pos_bias + attention_head;
+    window (and grids whose width is or is not a multiple of 32), against the
+    oracle's rel_pos_bias + attention_head;
 Tolerance: 1e-5 of the largest |out| (fp32 sums in another order, the
 running-max rescale).
 """
@@ -88,9 +89,13 @@ def test_attention_strided_decoder_layout(backend):
     assert_f32_close(host_f32(out), want, 1e-5, "strided attention")
 
 
-@pytest.mark.parametrize("windows,heads,h,w", [(4, 3, 14, 14), (1, 2, 64, 64), (2, 1, 5, 7)])
-def test_attention_rel_pos_against_the_oracle(backend, windows, heads, h, w):
-    hd, n = 64, h * w
+@pytest.mark.parametrize("windows,heads,h,w,hd", [(4, 3, 14, 14, 64), (1, 2, 64, 64, 64), (2, 1, 5, 7, 64),
+                                                   (2, 1, 5, 32, 64), (1, 2, 3, 64, 64), (1, 1, 6, 32, 128)])
+def test_attention_rel_pos_against_the_oracle(backend, windows, heads, h, w, hd):
+    """Grid widths of whole 32-key tiles (32, 64) take the per-tile bias
+    terms, with h not a multiple of 4 among them; 14 and 7 the per-key
+    lookups."""
+    n = h * w
     slices = heads * windows
     q, k, v = normal(730 + n, (slices, n, hd)), normal(731 + n, (slices, n, hd)), normal(732, (slices, n, hd))
     rh, rw = normal(733, (h, h, hd)) * 0.3, normal(734, (w, w, hd)) * 0.3
