@@ -140,6 +140,8 @@ _SIGNATURES = {
     "uocr_rocm_linear": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_linear_bf16x": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_round_bf16": ([_vp, _vp, _i64, _vp], _int),
+    "uocr_rocm_gelu_erf_to_bf16": ([_vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_quick_gelu_to_bf16": ([_vp, _vp, _vp, _i64], _int),
     "uocr_rocm_linear_workspace_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_linear_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_linear_bf16x_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
@@ -523,6 +525,16 @@ def round_bf16(src, dst, stream=None):
     if src.numel() != dst.numel():
         raise ValueError("round_bf16: src and dst sizes differ")
     _op("uocr_rocm_round_bf16", stream, _ptr(src), src.numel(), _ptr(dst))
+
+
+def act_to_bf16(x, y, quick=False, stream=None):
+    """y = bf16(gelu_erf(x)) (quick: bf16(quick_gelu(x))), x float32 and y
+    bfloat16 of the same size (new: an MLP's activation with the rounding its
+    second projection applies)."""
+    if x.numel() != y.numel():
+        raise ValueError("act_to_bf16: x and y sizes differ")
+    name = "uocr_rocm_quick_gelu_to_bf16" if quick else "uocr_rocm_gelu_erf_to_bf16"
+    _op(name, stream, _ptr(x), _ptr(y), x.numel())
 
 
 def gemm_nt(m, n, k, alpha, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch=1, stream=None):

@@ -214,6 +214,50 @@ int launch_flat(const char* what, void* stream, T* x, const T* y, int64_t n) {
   return check_launch(what);
 }
 
+// ---- activation into bf16 ----------------------------------------------------------
+
+// y = bf16(act(x)): fp32 x in, the activation in fp32 (the same function as
+// the in-place fp32 op), rounded to nearest even on the way out. The MLPs'
+// second projection rounds its input to bf16 anyway, so this is the
+// activation and that rounding in one pass (half the output bytes, and the
+// projection takes its memory-to-LDS path). 8 elements per thread; the last
+// n % 8 (or every element where a pointer is not 16-byte aligned) one per
+// thread.
+template <Flat kOp>
+__global__ __launch_bounds__(kBlock) void act_to_bf16_k(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                                          int64_t n, bool vec) {
+  auto act = [](float v) {
+    if constexpr (kOp == Flat::kGelu) return gelu_of<float>(v);
+    return quick_gelu_f(v);
+  };
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (vec && 8 * t + 8 <= n) {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(x + 8 * t), hi = *reinterpret_cast<const u32x4*>(x + 8 * t + 4);
+    *reinterpret_cast<u32x4*>(y + 8 * t) =
+        u32x4{pack_bf16(act(__uint_as_float(lo.x)), act(__uint_as_float(lo.y))),
+              pack_bf16(act(__uint_as_float(lo.z)), act(__uint_as_float(lo.w))),
+              pack_bf16(act(__uint_as_float(hi.x)), act(__uint_as_float(hi.y))),
+              pack_bf16(act(__uint_as_float(hi.z)), act(__uint_as_float(hi.w)))};
+    return;
+  }
+  for (int64_t i = vec ? 8 * t : t; i < n && (vec ? i < 8 * t + 8 : i == t); ++i) y[i] = f32_to_bf16(act(x[i]));
+}
+
+template <Flat kOp>
+int launch_act_to_bf16(const char* what, void* stream, const float* x, uint16_t* y, int64_t n) {
+  UOCR_REQUIRE(n >= 0, what, "n must be >= 0");
+  if (n == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(x != nullptr && y != nullptr, what, "null pointer");
+  UOCR_REQUIRE(n < kMaxElems, what, "n too large");
+  const bool vec = aligned16(x) && aligned16(y);
+  const int64_t threads = vec ? (n + 7) / 8 : n;
+  const int64_t blocks = (threads + kBlock - 1) / kBlock;
+  UOCR_REQUIRE(blocks < (int64_t{1} << 31), what, "n too large");
+  clear_launch_error();
+  act_to_bf16_k<kOp><<<static_cast<unsigned>(blocks), kBlock, 0, as_stream(stream)>>>(x, y, n, vec);
+  return check_launch(what);
+}
+
 // ---- copy -----------------------------------------------------------------------
 
 // dst = src over n elements, VW per chunk, UNROLL chunks per thread (chunk
@@ -383,6 +427,14 @@ int uocr_rocm_gelu_erf(void* stream, float* x, int64_t n) {
 
 int uocr_rocm_gelu_erf_bf16(void* stream, uint16_t* x, int64_t n) {
   return launch_flat<Flat::kGelu, uint16_t>("uocr_rocm_gelu_erf_bf16", stream, x, nullptr, n);
+}
+
+int uocr_rocm_gelu_erf_to_bf16(void* stream, const float* x, uint16_t* y, int64_t n) {
+  return launch_act_to_bf16<Flat::kGelu>("uocr_rocm_gelu_erf_to_bf16", stream, x, y, n);
+}
+
+int uocr_rocm_quick_gelu_to_bf16(void* stream, const float* x, uint16_t* y, int64_t n) {
+  return launch_act_to_bf16<Flat::kQuickGelu>("uocr_rocm_quick_gelu_to_bf16", stream, x, y, n);
 }
 
 int uocr_rocm_quick_gelu(void* stream, float* x, int64_t n) {

@@ -242,6 +242,14 @@ void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint1
   check(uocr_rocm_round_bf16(ctx.stream(), src, n, dst));
 }
 
+void gelu_erf_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n) {
+  check(uocr_rocm_gelu_erf_to_bf16(ctx.stream(), x, y, n));
+}
+
+void quick_gelu_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n) {
+  check(uocr_rocm_quick_gelu_to_bf16(ctx.stream(), x, y, n));
+}
+
 void add_rms_norm_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out, const float* w_norm,
                             float eps, float* h_out, std::int64_t k, const std::uint16_t* w, std::int64_t n,
                             const float* bias, float* y) {

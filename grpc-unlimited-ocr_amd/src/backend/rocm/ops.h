@@ -171,6 +171,9 @@ void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, 
 void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
                   std::int64_t n, const float* bias, float* y);
 void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint16_t* dst);
+// New: y = bf16(gelu_erf(x)) / bf16(quick_gelu(x)), x fp32 and y bf16.
+void gelu_erf_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n);
+void quick_gelu_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n);
 // New: linear with a workspace for splitting k where the product has too
 // few tiles to cover the GPU (linear_workspace_floats(m, k, n) floats; 0:
 // no split is taken).

@@ -260,6 +260,25 @@ void VisionEncoder::project(const float* x, std::int64_t m, std::int64_t k, cons
   linear(ctx_, x, m, k, w, n, bias, y, ws, floats);
 }
 
+void VisionEncoder::project_bf16(const std::uint16_t* xb, std::int64_t m, std::int64_t k, const std::uint16_t* w,
+                                 std::int64_t n, const float* bias, float* y) const {
+  const std::int64_t floats = linear_workspace_floats(m, k, n);
+  if (floats > 0 && split_ws_.count() < floats) split_ws_ = Array(ctx_, DType::kF32, floats);
+  linear_bf16x(ctx_, xb, m, k, w, n, bias, y, floats > 0 ? split_ws_.f32() : nullptr, floats);
+}
+
+// An MLP's activation straight into bf16 (the rounding its second
+// projection applies), in project()'s scratch.
+const std::uint16_t* VisionEncoder::activated_bf16(const float* x, std::int64_t n, bool quick) const {
+  if (x_bf16_.count() < n) x_bf16_ = Array(ctx_, DType::kBF16, n);
+  if (quick) {
+    quick_gelu_to_bf16(ctx_, x, x_bf16_.bf16(), n);
+  } else {
+    gelu_erf_to_bf16(ctx_, x, x_bf16_.bf16(), n);
+  }
+  return x_bf16_.bf16();
+}
+
 // Attention of one block over `windows` windows of h x w tokens, rows
 // window-major in x [windows * h * w, width] (cuda_vision.cpp:151-172).
 // The operands go head-major ([3, heads, rows, hd]) so that every (head,
@@ -336,8 +355,8 @@ void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const
   copy(ctx_, hidden.f32(), x.f32(), cells * c);
   layer_norm(ctx_, hidden.f32(), b.norm2_w, b.norm2_b, cells, c, kSamEps);
   project(hidden.f32(), cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
-  gelu_erf(ctx_, wide.f32(), cells * dims_.sam.mlp);
-  project(wide.f32(), cells, dims_.sam.mlp, b.lin2, c, b.lin2_b, hidden.f32());
+  project_bf16(activated_bf16(wide.f32(), cells * dims_.sam.mlp, false), cells, dims_.sam.mlp, b.lin2, c, b.lin2_b,
+               hidden.f32());
   add_inplace(ctx_, x.f32(), hidden.f32(), cells * c);
 }
 
@@ -417,8 +436,7 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
     copy(ctx_, normed.f32(), x.f32(), n * c);
     layer_norm(ctx_, normed.f32(), l.ln2_w, l.ln2_b, n, c, kClipEps);
     project(normed.f32(), n, c, l.fc1, cd.mlp, l.fc1_b, wide.f32());
-    quick_gelu(ctx_, wide.f32(), n * cd.mlp);
-    project(wide.f32(), n, cd.mlp, l.fc2, c, l.fc2_b, proj.f32());
+    project_bf16(activated_bf16(wide.f32(), n * cd.mlp, true), n, cd.mlp, l.fc2, c, l.fc2_b, proj.f32());
     add_inplace(ctx_, x.f32(), proj.f32(), n * c);
   }
 }

@@ -158,6 +158,11 @@ class VisionEncoder {
   // workspace where the product has too few tiles to cover the GPU.
   void project(const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w, std::int64_t n,
                const float* bias, float* y) const;
+  // The same with x already bf16.
+  void project_bf16(const std::uint16_t* xb, std::int64_t m, std::int64_t k, const std::uint16_t* w, std::int64_t n,
+                    const float* bias, float* y) const;
+  // bf16(gelu_erf(x)) (quick: bf16(quick_gelu(x))) in project()'s scratch.
+  const std::uint16_t* activated_bf16(const float* x, std::int64_t n, bool quick) const;
   void sam_forward(const float* image, std::int64_t size, Array& cells) const;
   void sam_block(std::size_t index, Array& x, std::int64_t g) const;
   void sam_attention(std::size_t index, const float* x, std::int64_t windows, std::int64_t h, std::int64_t w,

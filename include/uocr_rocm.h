@@ -338,6 +338,13 @@ UOCR_ROCM_API int uocr_rocm_linear_bf16x_ws(void* stream, const uint16_t* x, int
 
 /* New: dst[i] = bf16(src[i]), nearest even; both 16-byte aligned. */
 UOCR_ROCM_API int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst);
+/* New: y[i] = bf16(gelu_erf(x[i])) and y[i] = bf16(quick_gelu(x[i])), x
+ * fp32 [n] and y bf16 [n] (nearest even): an MLP's activation together with
+ * the rounding its second projection applies to its input (the reference's
+ * gelu_erf / quick_gelu then linear, ops.h:14-17,37-38), bitwise the fp32
+ * op followed by uocr_rocm_round_bf16. */
+UOCR_ROCM_API int uocr_rocm_gelu_erf_to_bf16(void* stream, const float* x, uint16_t* y, int64_t n);
+UOCR_ROCM_API int uocr_rocm_quick_gelu_to_bf16(void* stream, const float* x, uint16_t* y, int64_t n);
 
 /* c[s] = alpha a[s] . b[s]^T (gemm_nt: a [m, k], b [n, k]) or c[s] = a[s] . b[s]
  * (gemm_nn: a [m, k], b [k, n]), fp32, row-major with leading dimensions

@@ -149,3 +149,27 @@ def test_split_and_merge_heads_are_exact(backend, rows, parts, heads, hd):
     back = torch.full((rows, heads * hd), float("nan"), device="cuda")
     backend.merge_heads(y[parts - 1].contiguous(), back)
     assert np.array_equal(host_f32(back), x.reshape(rows, parts, heads * hd)[:, parts - 1])
+
+
+@pytest.mark.parametrize("n,offset", [(4096 * 3072, 0), (257 * 4096, 0), (1000003, 0), (77, 1), (8, 0)])
+def test_activation_into_bf16_is_the_fp32_op_then_the_rounding(backend, n, offset):
+    """gelu_erf_to_bf16 / quick_gelu_to_bf16 (the MLPs' activation with the
+    rounding of their second projection) against the fp32 op in place then
+    round_bf16, bit for bit; a ragged n and an unaligned x take the
+    element-by-element path. Values span the activations' regimes (x up to
+    +-12: the erf tail, sigmoid saturation, zeros)."""
+    g = np.random.default_rng(900 + n)
+    x = (g.standard_normal(n + offset) * 4).astype(np.float32)
+    x[offset:offset + min(n, 4)] = [0.0, -12.0, 12.0, -0.0][:min(n, 4)]
+    xd = dev_f32(x)[offset:]
+    for quick in (False, True):
+        want32 = xd.clone()
+        if quick:
+            backend.quick_gelu(want32)
+        else:
+            backend.gelu_erf(want32)
+        want = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+        backend.round_bf16(want32.contiguous(), want)
+        got = torch.full((n,), float("nan"), dtype=torch.bfloat16, device="cuda")
+        backend.act_to_bf16(xd, got, quick=quick)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"quick={quick} n={n} offset={offset}"
