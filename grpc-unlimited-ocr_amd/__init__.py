@@ -141,6 +141,7 @@ _SIGNATURES = {
     "uocr_rocm_linear_bf16x": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_round_bf16": ([_vp, _vp, _i64, _vp], _int),
     "uocr_rocm_gelu_erf_to_bf16": ([_vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_layer_norm_to_bf16": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32], _int),
     "uocr_rocm_quick_gelu_to_bf16": ([_vp, _vp, _vp, _i64], _int),
     "uocr_rocm_linear_workspace_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_linear_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
@@ -525,6 +526,17 @@ def round_bf16(src, dst, stream=None):
     if src.numel() != dst.numel():
         raise ValueError("round_bf16: src and dst sizes differ")
     _op("uocr_rocm_round_bf16", stream, _ptr(src), src.numel(), _ptr(dst))
+
+
+def layer_norm_to_bf16(x, w, b, y, eps, stream=None):
+    """y = bf16(layer_norm(x)) out of place: x float32 [rows, cols] untouched,
+    y bfloat16 of the same shape (new: a LayerNorm read only by a
+    projection, with the projection's rounding)."""
+    cols = w.numel()
+    if x.numel() != y.numel() or b.numel() != cols or (cols and x.numel() % cols):
+        raise ValueError("layer_norm_to_bf16: x and y [rows, cols], w and b [cols]")
+    rows = x.numel() // cols if cols else 0
+    _op("uocr_rocm_layer_norm_to_bf16", stream, _ptr(x), _ptr(w), _ptr(b), _ptr(y), rows, cols, float(eps))
 
 
 def act_to_bf16(x, y, quick=False, stream=None):

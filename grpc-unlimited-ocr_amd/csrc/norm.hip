@@ -37,7 +37,10 @@ namespace {
 
 // kRouter: the router's RMSNorm (non-finite inputs count as 0, output
 // clamp(clamp(x inv, +-1e4) (1 + w), +-1e4); src/model/decoder.cpp:20-34).
-enum class Norm { kRms, kAddRms, kLayer, kRouter, kEmbedRms };
+// kLayerToBf16: layer_norm out of place, x read only and y = bf16 of the
+// normed row (nearest even) into h: the arithmetic of kLayer with the
+// rounding a following projection applies to its input.
+enum class Norm { kRms, kAddRms, kLayer, kRouter, kEmbedRms, kLayerToBf16 };
 
 // kEmbedRms's row source: the bf16 table row of state->token (a zero row for
 // a token outside [0, table_rows) when table_rows >= 0).
@@ -67,6 +70,7 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
                                                 EmbedSrc src) {
   constexpr bool kEmbed = kMode == Norm::kEmbedRms;
   constexpr bool kTwoOut = kMode == Norm::kAddRms || kEmbed;  // writes x' and h
+  constexpr bool kLn = kMode == Norm::kLayer || kMode == Norm::kLayerToBf16;
   constexpr int kRowsPerBlock = TB / kWave / WPR;
   __shared__ float red[kRowsPerBlock][kMaxGroups];
   // One-wave rows in multi-wave workgroups share the norm weights through
@@ -76,7 +80,7 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
   constexpr int kWavesPerGroup = TB / kWave;
   constexpr bool kStage = WPR == 1 && kWavesPerGroup > 1 && VPL <= 8;
   constexpr int kStageSlices = kStage ? (VPL + kWavesPerGroup - 1) / kWavesPerGroup : 1;
-  constexpr bool kStageB = kStage && kMode == Norm::kLayer;
+  constexpr bool kStageB = kStage && kLn;
   __shared__ __attribute__((aligned(16))) float wst[kStage ? VPL * kWave * VW : 1];
   __shared__ __attribute__((aligned(16))) float bst[kStageB ? VPL * kWave * VW : 1];
   const int wave = wave_in_block();
@@ -167,7 +171,7 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
     }
     part[k] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < VW; ++e) part[k] += kMode == Norm::kLayer ? s[k][e] : s[k][e] * s[k][e];
+    for (int e = 0; e < VW; ++e) part[k] += kLn ? s[k][e] : s[k][e] * s[k][e];
     part[k] = live[k] ? part[k] : 0.0f;  // a dropped chunk adds nothing
     // x' = x + delta does not depend on the reduction: it leaves as soon as
     // its chunk is formed, so half of the kernel's writes overlap the row
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
   // rows fold in a few DPP steps and request them after: early weights were
   // 4-8% slower there, every wave asking for the same lines at once.
   constexpr bool kEarlyW = WPR > 1;
-  float wv_e[kEarlyW ? VPL : 1][VW], bv_e[kEarlyW && kMode == Norm::kLayer ? VPL : 1][VW];
+  float wv_e[kEarlyW ? VPL : 1][VW], bv_e[kEarlyW && kLn ? VPL : 1][VW];
   if constexpr (kEarlyW) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -195,12 +199,12 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
       const int v = (wr + WPR * k) * kWave + lane;
       const int vc = v < nvec ? v : nvec - 1;
       load_f32<VW>(w + vc * VW, wv_e[k]);
-      if constexpr (kMode == Norm::kLayer) load_f32<VW>(b + vc * VW, bv_e[k]);
+      if constexpr (kLn) load_f32<VW>(b + vc * VW, bv_e[k]);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
   float inv;
-  if constexpr (kMode == Norm::kLayer) {
+  if constexpr (kLn) {
     const float mean = fold_groups<WPR, VPL>(part, wr, groups, red[rloc]) / static_cast<float>(cols);
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
@@ -248,20 +252,20 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
           wv[e] = wv_e[k][e];
-          if constexpr (kMode == Norm::kLayer) bv[e] = bv_e[k][e];
+          if constexpr (kLn) bv[e] = bv_e[k][e];
         }
       } else if constexpr (kStage) {
         load_f32<VW>(wst + v * VW, wv);
-        if constexpr (kMode == Norm::kLayer) load_f32<VW>(bst + v * VW, bv);
+        if constexpr (kLn) load_f32<VW>(bst + v * VW, bv);
       } else {
         load_f32<VW>(w + v * VW, wv);
-        if constexpr (kMode == Norm::kLayer) load_f32<VW>(b + v * VW, bv);
+        if constexpr (kLn) load_f32<VW>(b + v * VW, bv);
       }
       {
 #pragma clang fp contract(off)
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
-          if constexpr (kMode == Norm::kLayer) {
+          if constexpr (kLn) {
             y[e] = (s[k][e] * inv) * wv[e] + bv[e];
           } else if constexpr (kMode == Norm::kRouter) {
             y[e] = clamp_act(clamp_act(s[k][e] * inv) * (1.0f + wv[e]));
@@ -270,9 +274,15 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
           }
         }
       }
-      Chunk<T, VW> o;
-      o.narrow(y);
-      o.store(orow + at);
+      if constexpr (kMode == Norm::kLayerToBf16) {
+        Chunk<uint16_t, VW> o;  // h is the bf16 output
+        o.narrow(y);
+        o.store(reinterpret_cast<uint16_t*>(h) + off + at);
+      } else {
+        Chunk<T, VW> o;
+        o.narrow(y);
+        o.store(orow + at);
+      }
     }
   }
 }
@@ -404,19 +414,25 @@ int launch_norm(const char* what, void* stream, T* x, const T* delta, const floa
                  "x, delta and h must be distinct buffers");
     UOCR_REQUIRE((cols + kVec<T> - 1) / kVec<T> <= kWave * kMaxGroups, what, "cols too large for one row kernel");
   }
-  if constexpr (kMode == Norm::kLayer) UOCR_REQUIRE(b != nullptr, what, "null b");
+  if constexpr (kMode == Norm::kLayer || kMode == Norm::kLayerToBf16) UOCR_REQUIRE(b != nullptr, what, "null b");
+  if constexpr (kMode == Norm::kLayerToBf16) {
+    UOCR_REQUIRE(h != nullptr, what, "null y");
+    UOCR_REQUIRE((cols + kVec<T> - 1) / kVec<T> <= kWave * kMaxGroups, what, "cols too large for one row kernel");
+  }
   if constexpr (kMode == Norm::kAddRms) {
     UOCR_REQUIRE(delta != nullptr && h != nullptr, what, "null delta or h");
     UOCR_REQUIRE(h != x && delta != x && h != delta, what, "x, delta and h must be distinct buffers");
   }
   constexpr int kV = kVec<T>;
-  const bool vec = cols % kV == 0 && aligned16(x) && aligned16(w) && (kMode != Norm::kLayer || aligned16(b)) &&
+  const bool vec = cols % kV == 0 && aligned16(x) && aligned16(w) &&
+                   ((kMode != Norm::kLayer && kMode != Norm::kLayerToBf16) || aligned16(b)) &&
+                   (kMode != Norm::kLayerToBf16 || aligned16(h)) &&
                    (kMode != Norm::kAddRms || (aligned16(delta) && aligned16(h))) &&
                    (kMode != Norm::kEmbedRms || (aligned16(e.table) && aligned16(h) && (delta == nullptr ||
                                                                                        aligned16(delta))));
   const int64_t nvec = vec ? cols / kV : cols;
   const int64_t groups = (nvec + kWave - 1) / kWave;
-  if constexpr (kMode == Norm::kEmbedRms) {
+  if constexpr (kMode == Norm::kEmbedRms || kMode == Norm::kLayerToBf16) {
     UOCR_REQUIRE(groups <= kMaxGroups, what, "cols too large for one row kernel");
   }
   const hipStream_t s = as_stream(stream);
@@ -428,11 +444,13 @@ int launch_norm(const char* what, void* stream, T* x, const T* delta, const floa
     const int64_t o = r0 * cols;
     T* xp = x + o;
     const T* dp = delta != nullptr ? delta + o : nullptr;
-    T* hp = h != nullptr ? h + o : nullptr;
+    T* hp = h == nullptr ? nullptr
+            : kMode == Norm::kLayerToBf16 ? reinterpret_cast<T*>(reinterpret_cast<uint16_t*>(h) + o)  // bf16 rows
+                                          : h + o;
     if (groups > kMaxGroups) {
       if constexpr (kMode == Norm::kLayer) {
         ln_rows_wide<T><<<static_cast<unsigned>(rn), kBlock, 0, s>>>(xp, w, b, cols, eps);
-      } else if constexpr (kMode != Norm::kEmbedRms) {
+      } else if constexpr (kMode != Norm::kEmbedRms && kMode != Norm::kLayerToBf16) {
         rms_rows_wide<T, kMode == Norm::kAddRms, kMode == Norm::kRouter>
             <<<static_cast<unsigned>(rn), kBlock, 0, s>>>(xp, dp, w, hp, cols, eps);
       }
@@ -483,6 +501,13 @@ int uocr_rocm_add_rms_norm_bf16(void* stream, uint16_t* x, const uint16_t* delta
 int uocr_rocm_layer_norm(void* stream, float* x, const float* w, const float* b, int64_t rows, int64_t cols,
                          float eps) {
   return launch_norm<float, Norm::kLayer>("uocr_rocm_layer_norm", stream, x, nullptr, w, b, nullptr, rows, cols, eps);
+}
+
+int uocr_rocm_layer_norm_to_bf16(void* stream, const float* x, const float* w, const float* b, uint16_t* y,
+                                 int64_t rows, int64_t cols, float eps) {
+  // x is only read in this mode; y travels in the kernel's h slot
+  return launch_norm<float, Norm::kLayerToBf16>("uocr_rocm_layer_norm_to_bf16", stream, const_cast<float*>(x), nullptr,
+                                                w, b, reinterpret_cast<float*>(y), rows, cols, eps);
 }
 
 int uocr_rocm_layer_norm_bf16(void* stream, uint16_t* x, const float* w, const float* b, int64_t rows, int64_t cols,

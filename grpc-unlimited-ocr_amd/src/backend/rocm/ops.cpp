@@ -242,6 +242,11 @@ void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint1
   check(uocr_rocm_round_bf16(ctx.stream(), src, n, dst));
 }
 
+void layer_norm_to_bf16(const Context& ctx, const float* x, const float* w, const float* b, std::uint16_t* y,
+                        std::int64_t rows, std::int64_t cols, float eps) {
+  check(uocr_rocm_layer_norm_to_bf16(ctx.stream(), x, w, b, y, rows, cols, eps));
+}
+
 void gelu_erf_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n) {
   check(uocr_rocm_gelu_erf_to_bf16(ctx.stream(), x, y, n));
 }

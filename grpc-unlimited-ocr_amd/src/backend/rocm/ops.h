@@ -172,6 +172,9 @@ void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, st
                   std::int64_t n, const float* bias, float* y);
 void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint16_t* dst);
 // New: y = bf16(gelu_erf(x)) / bf16(quick_gelu(x)), x fp32 and y bf16.
+// New: y = bf16(layer_norm(x)) out of place (x fp32 untouched, y bf16).
+void layer_norm_to_bf16(const Context& ctx, const float* x, const float* w, const float* b, std::uint16_t* y,
+                        std::int64_t rows, std::int64_t cols, float eps);
 void gelu_erf_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n);
 void quick_gelu_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n);
 // New: linear with a workspace for splitting k where the product has too

@@ -267,8 +267,33 @@ void VisionEncoder::project_bf16(const std::uint16_t* xb, std::int64_t m, std::i
   linear_bf16x(ctx_, xb, m, k, w, n, bias, y, floats > 0 ? split_ws_.f32() : nullptr, floats);
 }
 
+// A LayerNorm whose only reader is a projection, straight into bf16 (the
+// rounding the projection applies), in project()'s scratch; x untouched.
+// Null for rows wider than the one-row kernel's 16384 columns.
+const std::uint16_t* VisionEncoder::normed_bf16(const float* x, std::int64_t rows, std::int64_t c, const float* w,
+                                                const float* b, float eps) const {
+  if (c > 16384) return nullptr;
+  if (x_bf16_.count() < rows * c) x_bf16_ = Array(ctx_, DType::kBF16, rows * c);
+  layer_norm_to_bf16(ctx_, x, w, b, x_bf16_.bf16(), rows, c, eps);
+  return x_bf16_.bf16();
+}
+
 // An MLP's activation straight into bf16 (the rounding its second
 // projection applies), in project()'s scratch.
+// y = LN(x) w^T + bias, x untouched: through bf16 where the one-row kernel
+// takes the width, else LN into `normed` (fp32) and project().
+void VisionEncoder::norm_project(const float* x, std::int64_t rows, std::int64_t c, const float* ln_w,
+                                 const float* ln_b, float eps, Array& normed, const std::uint16_t* w, std::int64_t n,
+                                 const float* bias, float* y) const {
+  if (const std::uint16_t* xb = normed_bf16(x, rows, c, ln_w, ln_b, eps)) {
+    project_bf16(xb, rows, c, w, n, bias, y);
+    return;
+  }
+  copy(ctx_, normed.f32(), x, rows * c);
+  layer_norm(ctx_, normed.f32(), ln_w, ln_b, rows, c, eps);
+  project(normed.f32(), rows, c, w, n, bias, y);
+}
+
 const std::uint16_t* VisionEncoder::activated_bf16(const float* x, std::int64_t n, bool quick) const {
   if (x_bf16_.count() < n) x_bf16_ = Array(ctx_, DType::kBF16, n);
   if (quick) {
@@ -287,12 +312,16 @@ const std::uint16_t* VisionEncoder::activated_bf16(const float* x, std::int64_t 
 // with another multiple of 4, three batched launches (scores, the
 // relative-position bias + softmax, values); otherwise head by head over all
 // windows, as the reference does.
-void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_t windows, std::int64_t h,
-                                  std::int64_t w, float* out) const {
+void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::uint16_t* xb, std::int64_t windows,
+                                  std::int64_t h, std::int64_t w, float* out) const {
   const auto& b = w_.sam_blocks[index];
   const std::int64_t c = dims_.sam.width, heads = dims_.sam.heads, hd = c / heads, n = h * w, rows = windows * n;
   Array qkv = f32(ctx_, rows * 3 * c);
-  project(x, rows, c, b.qkv, 3 * c, b.qkv_b, qkv.f32());
+  if (xb != nullptr) {
+    project_bf16(xb, rows, c, b.qkv, 3 * c, b.qkv_b, qkv.f32());
+  } else {
+    project(x, rows, c, b.qkv, 3 * c, b.qkv_b, qkv.f32());
+  }
   const Array& rh = rel_table(index, true, h);
   const Array& rw = rel_table(index, false, w);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
@@ -333,28 +362,39 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, std::int64_
 void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const {
   const auto& b = w_.sam_blocks[index];
   const std::int64_t c = dims_.sam.width, cells = g * g;
-  Array normed = f32(ctx_, (cells + 1) * c);  // the extra zero row fills the windows' padding
-  normed.zero();
-  copy(ctx_, normed.f32(), x.f32(), cells * c);
-  layer_norm(ctx_, normed.f32(), b.norm1_w, b.norm1_b, cells, c, kSamEps);
   Array attended = f32(ctx_, cells * c);
-  if (global_[index]) {
-    sam_attention(index, normed.f32(), 1, g, g, attended.f32());
+  const std::uint16_t* normed_b = global_[index] ? normed_bf16(x.f32(), cells, c, b.norm1_w, b.norm1_b, kSamEps)
+                                                 : nullptr;
+  if (normed_b != nullptr) {
+    // a global block: the norm's only reader is the qkv projection
+    sam_attention(index, nullptr, normed_b, 1, g, g, attended.f32());
   } else {
-    const std::int64_t win = dims_.sam.window;
-    const Windows& wi = windows(g);
-    const std::int64_t rows = wi.count * win * win;
-    Array slots = f32(ctx_, rows * c), out = f32(ctx_, rows * c);
-    gather_rows(ctx_, normed.f32(), wi.gather.i64(), rows, c, slots.f32());
-    sam_attention(index, slots.f32(), wi.count, win, win, out.f32());
-    gather_rows(ctx_, out.f32(), wi.scatter.i64(), cells, c, attended.f32());
+    Array normed = f32(ctx_, (cells + 1) * c);  // the extra zero row fills the windows' padding
+    normed.zero();
+    copy(ctx_, normed.f32(), x.f32(), cells * c);
+    layer_norm(ctx_, normed.f32(), b.norm1_w, b.norm1_b, cells, c, kSamEps);
+    if (global_[index]) {
+      sam_attention(index, normed.f32(), nullptr, 1, g, g, attended.f32());
+    } else {
+      const std::int64_t win = dims_.sam.window;
+      const Windows& wi = windows(g);
+      const std::int64_t rows = wi.count * win * win;
+      Array slots = f32(ctx_, rows * c), out = f32(ctx_, rows * c);
+      gather_rows(ctx_, normed.f32(), wi.gather.i64(), rows, c, slots.f32());
+      sam_attention(index, slots.f32(), nullptr, wi.count, win, win, out.f32());
+      gather_rows(ctx_, out.f32(), wi.scatter.i64(), cells, c, attended.f32());
+    }
   }
   add_inplace(ctx_, x.f32(), attended.f32(), cells * c);
 
   Array hidden = f32(ctx_, cells * c), wide = f32(ctx_, cells * dims_.sam.mlp);
-  copy(ctx_, hidden.f32(), x.f32(), cells * c);
-  layer_norm(ctx_, hidden.f32(), b.norm2_w, b.norm2_b, cells, c, kSamEps);
-  project(hidden.f32(), cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
+  if (const std::uint16_t* h2 = normed_bf16(x.f32(), cells, c, b.norm2_w, b.norm2_b, kSamEps)) {
+    project_bf16(h2, cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
+  } else {
+    copy(ctx_, hidden.f32(), x.f32(), cells * c);
+    layer_norm(ctx_, hidden.f32(), b.norm2_w, b.norm2_b, cells, c, kSamEps);
+    project(hidden.f32(), cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
+  }
   project_bf16(activated_bf16(wide.f32(), cells * dims_.sam.mlp, false), cells, dims_.sam.mlp, b.lin2, c, b.lin2_b,
                hidden.f32());
   add_inplace(ctx_, x.f32(), hidden.f32(), cells * c);
@@ -411,9 +451,7 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
   Array merged = f32(ctx_, n * c), proj = f32(ctx_, n * c), wide = f32(ctx_, n * cd.mlp);
   Array hm = f32(ctx_, split ? 3 * n * c : 1), o = f32(ctx_, split ? n * c : 1);
   for (const auto& l : w_.clip_layers) {
-    copy(ctx_, normed.f32(), x.f32(), n * c);
-    layer_norm(ctx_, normed.f32(), l.ln1_w, l.ln1_b, n, c, kClipEps);
-    project(normed.f32(), n, c, l.qkv, 3 * c, l.qkv_b, qkv.f32());
+    norm_project(x.f32(), n, c, l.ln1_w, l.ln1_b, kClipEps, normed, l.qkv, 3 * c, l.qkv_b, qkv.f32());
     if (one_pass) {
       // straight from the projection's rows into the heads' columns
       const float* q = qkv.f32();
@@ -433,9 +471,7 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
     }
     project(merged.f32(), n, c, l.out, c, l.out_b, proj.f32());
     add_inplace(ctx_, x.f32(), proj.f32(), n * c);
-    copy(ctx_, normed.f32(), x.f32(), n * c);
-    layer_norm(ctx_, normed.f32(), l.ln2_w, l.ln2_b, n, c, kClipEps);
-    project(normed.f32(), n, c, l.fc1, cd.mlp, l.fc1_b, wide.f32());
+    norm_project(x.f32(), n, c, l.ln2_w, l.ln2_b, kClipEps, normed, l.fc1, cd.mlp, l.fc1_b, wide.f32());
     project_bf16(activated_bf16(wide.f32(), n * cd.mlp, true), n, cd.mlp, l.fc2, c, l.fc2_b, proj.f32());
     add_inplace(ctx_, x.f32(), proj.f32(), n * c);
   }

@@ -163,10 +163,17 @@ class VisionEncoder {
                     const float* bias, float* y) const;
   // bf16(gelu_erf(x)) (quick: bf16(quick_gelu(x))) in project()'s scratch.
   const std::uint16_t* activated_bf16(const float* x, std::int64_t n, bool quick) const;
+  // bf16(LN(x)) in project()'s scratch, x untouched (null: c above 16384).
+  const std::uint16_t* normed_bf16(const float* x, std::int64_t rows, std::int64_t c, const float* w, const float* b,
+                                   float eps) const;
+  // y = LN(x) w^T + bias, x untouched (`normed`: fp32 room for the wide case).
+  void norm_project(const float* x, std::int64_t rows, std::int64_t c, const float* ln_w, const float* ln_b, float eps,
+                    Array& normed, const std::uint16_t* w, std::int64_t n, const float* bias, float* y) const;
   void sam_forward(const float* image, std::int64_t size, Array& cells) const;
   void sam_block(std::size_t index, Array& x, std::int64_t g) const;
-  void sam_attention(std::size_t index, const float* x, std::int64_t windows, std::int64_t h, std::int64_t w,
-                     float* out) const;
+  // x fp32, or xb (non-null) the same rows already in bf16
+  void sam_attention(std::size_t index, const float* x, const std::uint16_t* xb, std::int64_t windows, std::int64_t h,
+                     std::int64_t w, float* out) const;
   void conv3(const float* hwc, std::int64_t side, std::int64_t in_c, const std::uint16_t* w, std::int64_t out_c,
              int stride, Array& out, std::int64_t& out_side) const;
   void clip_forward(const float* cells, std::int64_t g, Array& x) const;

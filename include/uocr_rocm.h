@@ -249,6 +249,14 @@ UOCR_ROCM_API int uocr_rocm_add_rms_norm_bf16(void* stream, uint16_t* x, const u
                                               uint16_t* h, int64_t rows, int64_t cols, float eps);
 UOCR_ROCM_API int uocr_rocm_layer_norm_bf16(void* stream, uint16_t* x, const float* w, const float* b, int64_t rows,
                                             int64_t cols, float eps);
+/* New: y = bf16(layer_norm(x)) out of place, x fp32 [rows, cols] read only and
+ * y bf16 [rows, cols] (nearest even), cols up to 16384: a LayerNorm whose
+ * only reader is a projection, with the rounding the projection applies to
+ * its input (the reference's layer_norm then linear, ops.h:14-17,32-33);
+ * bitwise uocr_rocm_layer_norm on a copy of x followed by
+ * uocr_rocm_round_bf16. */
+UOCR_ROCM_API int uocr_rocm_layer_norm_to_bf16(void* stream, const float* x, const float* w, const float* b,
+                                               uint16_t* y, int64_t rows, int64_t cols, float eps);
 UOCR_ROCM_API int uocr_rocm_gelu_erf_bf16(void* stream, uint16_t* x, int64_t n);
 UOCR_ROCM_API int uocr_rocm_swiglu_bf16(void* stream, const uint16_t* in, uint16_t* out, int64_t rows, int64_t ffn);
 UOCR_ROCM_API int uocr_rocm_rope_bf16(void* stream, uint16_t* x, int64_t rows, int64_t heads, int64_t dim,

@@ -173,3 +173,34 @@ def test_activation_into_bf16_is_the_fp32_op_then_the_rounding(backend, n, offse
         got = torch.full((n,), float("nan"), dtype=torch.bfloat16, device="cuda")
         backend.act_to_bf16(xd, got, quick=quick)
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"quick={quick} n={n} offset={offset}"
+
+
+@pytest.mark.parametrize("rows,cols,offset", [(4096, 768, 0), (257, 1024, 0), (8200, 768, 0), (33, 100, 0), (5, 768, 1),
+                                              (3, 16384, 0)])
+def test_layer_norm_into_bf16_is_the_norm_then_the_rounding(backend, rows, cols, offset):
+    """layer_norm_to_bf16 against layer_norm in place on a copy then
+    round_bf16, bit for bit, x left as it was: one-wave rows, 4-wave groups
+    past 8192 rows, columns not a multiple of 4 and an unaligned x (element
+    by element), rows of 16384 columns spread over 4 waves."""
+    g = np.random.default_rng(910 + rows + cols)
+    x = (g.standard_normal(rows * cols + offset) * 3 + 0.5).astype(np.float32)
+    w = (1 + 0.1 * g.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * g.standard_normal(cols)).astype(np.float32)
+    xd = dev_f32(x)[offset:].view(rows, cols)
+    before = xd.clone()
+    ref = xd.clone()
+    backend.layer_norm(ref, dev_f32(w), dev_f32(b), 1e-6)
+    want = torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(ref, want)
+    got = torch.full((rows, cols), float("nan"), dtype=torch.bfloat16, device="cuda")
+    backend.layer_norm_to_bf16(xd, dev_f32(w), dev_f32(b), got, 1e-6)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"{rows}x{cols} offset {offset}"
+    assert torch.equal(xd, before), "x is read only"
+
+
+def test_layer_norm_into_bf16_rejects_rows_too_wide(backend):
+    x = torch.zeros(1, 16385, device="cuda")
+    w = torch.ones(16385, device="cuda")
+    y = torch.empty(1, 16385, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        backend.layer_norm_to_bf16(x, w, w, y, 1e-6)
