@@ -165,16 +165,31 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
 
   float* my_dots = dots + (wave * kQueriesPerWave + c) * a.dots_ld;
   if constexpr (rel_pos<kBias>()) {
-    // dh[ky] = q . rh[qy, ky] (lane half 0) and dw[kx] = q . rw[qx, kx]
-    // (half 1), fp32 in column order, over the whole query row
+    // dh[ky] = q . rh[qy, ky] and dw[kx] = q . rw[qx, kx]: each lane forms
+    // the partial dot over the half of the columns it holds in qv (fp32 in
+    // column order, the table rows as 16-byte loads), and the two halves'
+    // partials are added, half 0's first, so that both lanes of a query
+    // hold the same sum; half 0 stores the height terms, half 1 the width
+    // terms.
     const int qy = qin ? qrow / a.w : 0, qx = qin ? qrow - qy * a.w : 0;
-    const float* qr = qb + (qin ? qrow : 0) * a.ldq;
-    const int n_dots = hl == 0 ? a.h : a.w;
-    const float* tab = hl == 0 ? a.rh + static_cast<int64_t>(qy) * a.h * HD : a.rw + static_cast<int64_t>(qx) * a.w * HD;
+    const float* th = a.rh + static_cast<int64_t>(qy) * a.h * HD + hl * kHalf;
+    const float* tw = a.rw + static_cast<int64_t>(qx) * a.w * HD + hl * kHalf;
+    const int n_dots = a.h + a.w;
+#pragma unroll 2
     for (int j = 0; j < n_dots; ++j) {
-      float s = 0.0f;
-      for (int e = 0; e < HD; ++e) s += qr[e] * tab[j * HD + e];
-      my_dots[(hl == 0 ? 0 : a.dw_off) + j] = s;
+      const float* row = j < a.h ? th + j * HD : tw + (j - a.h) * HD;
+      float p = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kHalf; i += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(row + i);
+        p = fmaf(qv[i], t.x, p);
+        p = fmaf(qv[i + 1], t.y, p);
+        p = fmaf(qv[i + 2], t.z, p);
+        p = fmaf(qv[i + 3], t.w, p);
+      }
+      const float other = partner(p);
+      const float dot = hl == 0 ? p + other : other + p;
+      if ((j < a.h) == (hl == 0)) my_dots[j < a.h ? j : a.dw_off + (j - a.h)] = dot;
     }
   }
 
@@ -387,6 +402,7 @@ int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64
     return st;
   }
   UOCR_REQUIRE(rh != nullptr && rw != nullptr, kWhat, "null relative-position table");
+  UOCR_REQUIRE(aligned16(rh) && aligned16(rw), kWhat, "relative-position tables must be 16-byte aligned");
   // A grid width of whole tiles takes the per-tile bias terms, the width
   // terms 16-byte aligned.
   const bool rows = w % kKeyTile == 0;

@@ -443,7 +443,8 @@ UOCR_ROCM_API int uocr_rocm_attention(void* stream, const float* q, int64_t ldq,
 /* New: the same over SAM's windows of h x w tokens (rows = keys = h w per
  * slice) with the decomposed relative-position bias of
  * uocr_rocm_rel_pos_bias (rh [h, h, hd], rw [w, w, hd], formed from each
- * slice's own query rows) in place of the mask; h + w <= 256. Replaces the
+ * slice's own query rows; both 16-byte aligned) in place of the mask;
+ * h + w <= 256. Replaces the
  * reference's per-head gemm_nt + rel_pos_bias + add_inplace + softmax_rows
  * + gemm_nn (src/model/cuda/cuda_vision.cpp:159-170). */
 UOCR_ROCM_API int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
