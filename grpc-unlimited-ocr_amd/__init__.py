@@ -146,6 +146,7 @@ _SIGNATURES = {
     "uocr_rocm_linear_workspace_floats": ([_i64, _i64, _i64], _i64),
     "uocr_rocm_linear_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_linear_bf16x_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_linear_bf16x_add_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_gemm_nt": ([_vp, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64],
                           _int),
     "uocr_rocm_gemm_nn": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64], _int),
@@ -502,6 +503,15 @@ def linear_ws(x, w, y, workspace, bias=None, stream=None):
     m = x.numel() // k
     name = "uocr_rocm_linear_bf16x_ws" if x.dtype == torch.bfloat16 else "uocr_rocm_linear_ws"
     _op(name, stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y), _ptr(workspace), workspace.numel())
+
+
+def linear_add(x, w, y, workspace, bias=None, stream=None):
+    """y += bf16 x [m, k] . w[n, k]^T (+ bias) (new: a residual stream's
+    projection, bitwise linear into a temporary then add_inplace)."""
+    n, k = w.shape
+    m = x.numel() // k
+    _op("uocr_rocm_linear_bf16x_add_ws", stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y),
+        _ptr(workspace), workspace.numel())
 
 
 def linear(x, w, y, bias=None, stream=None):

@@ -83,6 +83,9 @@ struct LinearArgs {
   // split * m * n (no bias); part null: one split, into y with the bias.
   int k_len;
   float* part;
+  // y += the product (+ bias): each element y + (sum + bias), as the
+  // product followed by an in-place add
+  bool accumulate;
 };
 
 // The tile, split and k range of this workgroup.
@@ -254,21 +257,27 @@ __device__ __forceinline__ void store_tile(const LinearArgs& a, const Work& wk, 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = wk.m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
-        if (row < a.m) out[row * a.n + col] = add ? acc[i][j][r] + bv : acc[i][j][r];
+        if (row < a.m) {
+          const float v = add ? acc[i][j][r] + bv : acc[i][j][r];
+          out[row * a.n + col] = !split && a.accumulate ? out[row * a.n + col] + v : v;
+        }
       }
     }
   }
 }
 
-// y = the sum of the splits' partial products in split order (+ bias).
+// y = the sum of the splits' partial products in split order (+ bias);
+// accumulate: y += that.
 __global__ __launch_bounds__(kBlock) void split_sum_k(const float* __restrict__ part, int splits, int64_t m, int64_t n,
-                                                       const float* __restrict__ bias, float* __restrict__ y) {
+                                                       const float* __restrict__ bias, float* __restrict__ y,
+                                                       bool accumulate) {
   const int64_t total = m * n;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * kBlock) {
     float v = part[i];
     for (int sp = 1; sp < splits; ++sp) v += part[sp * total + i];
-    y[i] = bias != nullptr ? v + bias[i % n] : v;
+    v = bias != nullptr ? v + bias[i % n] : v;
+    y[i] = accumulate ? y[i] + v : v;
   }
 }
 
@@ -400,7 +409,8 @@ int64_t splits_for(int64_t m, int64_t k, int64_t n) {
 }
 
 int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64_t m, int64_t k, const uint16_t* w,
-                 int64_t n, const float* bias, float* y, float* workspace = nullptr, int64_t workspace_floats = 0) {
+                 int64_t n, const float* bias, float* y, float* workspace = nullptr, int64_t workspace_floats = 0,
+                 bool accumulate = false) {
   UOCR_REQUIRE(m >= 0 && n >= 0 && k >= 0, what, "m, n and k must be >= 0");
   if (m == 0 || n == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(k >= 1 && k < (int64_t{1} << 30), what, "k must be in [1, 2^30)");
@@ -424,7 +434,8 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
                static_cast<int>(tiles_m),
                static_cast<int>(tiles_n),
                static_cast<int>(k_len),
-               splits > 1 ? workspace : nullptr};
+               splits > 1 ? workspace : nullptr,
+               accumulate};
   const unsigned grid = static_cast<unsigned>(tiles_m * tiles_n * splits);
   clear_launch_error();
   const hipStream_t st = as_stream(stream);
@@ -444,7 +455,7 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
   if (splits > 1) {
     const int64_t blocks = (m * n + kBlock - 1) / kBlock;
     split_sum_k<<<static_cast<unsigned>(blocks < 65536 ? blocks : 65536), kBlock, 0, st>>>(
-        workspace, static_cast<int>(splits), m, n, bias, y);
+        workspace, static_cast<int>(splits), m, n, bias, y, accumulate);
   }
   return check_launch(what);
 }
@@ -488,6 +499,12 @@ int uocr_rocm_linear_bf16x_ws(void* stream, const uint16_t* x, int64_t m, int64_
                               const float* bias, float* y, float* workspace, int64_t workspace_floats) {
   return linear_entry("uocr_rocm_linear_bf16x_ws", stream, x, false, m, k, w, n, bias, y, workspace,
                       workspace_floats);
+}
+
+int uocr_rocm_linear_bf16x_add_ws(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
+                                  const float* bias, float* y, float* workspace, int64_t workspace_floats) {
+  return linear_entry("uocr_rocm_linear_bf16x_add_ws", stream, x, false, m, k, w, n, bias, y, workspace,
+                      workspace_floats, true);
 }
 
 int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst) {

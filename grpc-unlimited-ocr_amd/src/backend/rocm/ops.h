@@ -187,6 +187,10 @@ void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, 
 void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
                   const std::uint16_t* w_bf16, std::int64_t n, const float* bias, float* y, float* workspace,
                   std::int64_t workspace_floats);
+// New: y += bf16(x) w^T (+ bias), as linear_bf16x then add_inplace.
+void linear_bf16x_add(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
+                      const std::uint16_t* w_bf16, std::int64_t n, const float* bias, float* y, float* workspace,
+                      std::int64_t workspace_floats);
 
 // Fused decode projections (new): add + RMSNorm as the GEMV's prologue,
 // optionally a gate/up pair with a SwiGLU epilogue. delta, x_out, w_norm

@@ -239,7 +239,7 @@ const VisionEncoder::Windows& VisionEncoder::windows(std::int64_t g) const {
 }
 
 void VisionEncoder::project(const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w, std::int64_t n,
-                            const float* bias, float* y) const {
+                            const float* bias, float* y, bool accumulate) const {
   // Scratch kept across calls (every call is ordered on the one stream):
   // the split-k workspace, and x rounded to bf16.
   auto grown = [&](Array& a, DType type, std::int64_t count) -> Array& {
@@ -248,23 +248,35 @@ void VisionEncoder::project(const float* x, std::int64_t m, std::int64_t k, cons
   };
   const std::int64_t floats = linear_workspace_floats(m, k, n);
   float* ws = floats > 0 ? grown(split_ws_, DType::kF32, floats).f32() : nullptr;
-  if (m > 1 && k % 64 == 0 && n >= k) {
+  if (m > 1 && k % 64 == 0 && (n >= k || accumulate)) {
     // x rounded once (the rounding the product applies anyway, bit for bit),
     // then tiles straight from memory into LDS. The pass costs 6 bytes per
-    // element of x, so it pays where the product is at least as wide as x.
+    // element of x, so it pays where the product is at least as wide as x,
+    // or where it saves the residual add's pass.
     Array& xb = grown(x_bf16_, DType::kBF16, m * k);
     round_bf16(ctx_, x, m * k, xb.bf16());
-    linear_bf16x(ctx_, xb.bf16(), m, k, w, n, bias, y, ws, floats);
+    project_bf16(xb.bf16(), m, k, w, n, bias, y, accumulate);
+    return;
+  }
+  if (accumulate) {
+    Array t = f32(ctx_, m * n);
+    linear(ctx_, x, m, k, w, n, bias, t.f32(), ws, floats);
+    add_inplace(ctx_, y, t.f32(), m * n);
     return;
   }
   linear(ctx_, x, m, k, w, n, bias, y, ws, floats);
 }
 
 void VisionEncoder::project_bf16(const std::uint16_t* xb, std::int64_t m, std::int64_t k, const std::uint16_t* w,
-                                 std::int64_t n, const float* bias, float* y) const {
+                                 std::int64_t n, const float* bias, float* y, bool accumulate) const {
   const std::int64_t floats = linear_workspace_floats(m, k, n);
   if (floats > 0 && split_ws_.count() < floats) split_ws_ = Array(ctx_, DType::kF32, floats);
-  linear_bf16x(ctx_, xb, m, k, w, n, bias, y, floats > 0 ? split_ws_.f32() : nullptr, floats);
+  float* ws = floats > 0 ? split_ws_.f32() : nullptr;
+  if (accumulate) {
+    linear_bf16x_add(ctx_, xb, m, k, w, n, bias, y, ws, floats);
+  } else {
+    linear_bf16x(ctx_, xb, m, k, w, n, bias, y, ws, floats);
+  }
 }
 
 // A LayerNorm whose only reader is a projection, straight into bf16 (the
@@ -313,7 +325,7 @@ const std::uint16_t* VisionEncoder::activated_bf16(const float* x, std::int64_t 
 // relative-position bias + softmax, values); otherwise head by head over all
 // windows, as the reference does.
 void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::uint16_t* xb, std::int64_t windows,
-                                  std::int64_t h, std::int64_t w, float* out) const {
+                                  std::int64_t h, std::int64_t w, float* out, bool accumulate) const {
   const auto& b = w_.sam_blocks[index];
   const std::int64_t c = dims_.sam.width, heads = dims_.sam.heads, hd = c / heads, n = h * w, rows = windows * n;
   Array qkv = f32(ctx_, rows * 3 * c);
@@ -355,49 +367,50 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::
               n * c, windows);
     }
   }
-  project(merged.f32(), rows, c, b.proj, c, b.proj_b, out);
+  project(merged.f32(), rows, c, b.proj, c, b.proj_b, out, accumulate);
 }
 
 // One SAM block over x [g * g, width] (cuda_vision.cpp:174-202).
 void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const {
   const auto& b = w_.sam_blocks[index];
   const std::int64_t c = dims_.sam.width, cells = g * g;
-  Array attended = f32(ctx_, cells * c);
   const std::uint16_t* normed_b = global_[index] ? normed_bf16(x.f32(), cells, c, b.norm1_w, b.norm1_b, kSamEps)
                                                  : nullptr;
   if (normed_b != nullptr) {
-    // a global block: the norm's only reader is the qkv projection
-    sam_attention(index, nullptr, normed_b, 1, g, g, attended.f32());
+    // a global block: the norm's only reader is the qkv projection, and the
+    // output projection adds straight into the residual stream
+    sam_attention(index, nullptr, normed_b, 1, g, g, x.f32(), true);
   } else {
+    Array attended = f32(ctx_, cells * c);
     Array normed = f32(ctx_, (cells + 1) * c);  // the extra zero row fills the windows' padding
     normed.zero();
     copy(ctx_, normed.f32(), x.f32(), cells * c);
     layer_norm(ctx_, normed.f32(), b.norm1_w, b.norm1_b, cells, c, kSamEps);
     if (global_[index]) {
-      sam_attention(index, normed.f32(), nullptr, 1, g, g, attended.f32());
+      sam_attention(index, normed.f32(), nullptr, 1, g, g, attended.f32(), false);
     } else {
       const std::int64_t win = dims_.sam.window;
       const Windows& wi = windows(g);
       const std::int64_t rows = wi.count * win * win;
       Array slots = f32(ctx_, rows * c), out = f32(ctx_, rows * c);
       gather_rows(ctx_, normed.f32(), wi.gather.i64(), rows, c, slots.f32());
-      sam_attention(index, slots.f32(), nullptr, wi.count, win, win, out.f32());
+      sam_attention(index, slots.f32(), nullptr, wi.count, win, win, out.f32(), false);
       gather_rows(ctx_, out.f32(), wi.scatter.i64(), cells, c, attended.f32());
     }
+    add_inplace(ctx_, x.f32(), attended.f32(), cells * c);
   }
-  add_inplace(ctx_, x.f32(), attended.f32(), cells * c);
 
-  Array hidden = f32(ctx_, cells * c), wide = f32(ctx_, cells * dims_.sam.mlp);
+  Array wide = f32(ctx_, cells * dims_.sam.mlp);
   if (const std::uint16_t* h2 = normed_bf16(x.f32(), cells, c, b.norm2_w, b.norm2_b, kSamEps)) {
     project_bf16(h2, cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
   } else {
+    Array hidden = f32(ctx_, cells * c);
     copy(ctx_, hidden.f32(), x.f32(), cells * c);
     layer_norm(ctx_, hidden.f32(), b.norm2_w, b.norm2_b, cells, c, kSamEps);
     project(hidden.f32(), cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
   }
   project_bf16(activated_bf16(wide.f32(), cells * dims_.sam.mlp, false), cells, dims_.sam.mlp, b.lin2, c, b.lin2_b,
-               hidden.f32());
-  add_inplace(ctx_, x.f32(), hidden.f32(), cells * c);
+               x.f32(), true);
 }
 
 // A 3 x 3 convolution (padding 1) of rows hwc [side * side, in_c] into rows
@@ -448,7 +461,7 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
   const bool one_pass = hd == 64 || hd == 128;  // attention on the matrix cores
   const bool split = !one_pass && hd % 4 == 0;   // head-major operands, as in sam_attention
   Array normed = f32(ctx_, n * c), qkv = f32(ctx_, n * 3 * c), scores = f32(ctx_, one_pass ? 1 : heads * n * n);
-  Array merged = f32(ctx_, n * c), proj = f32(ctx_, n * c), wide = f32(ctx_, n * cd.mlp);
+  Array merged = f32(ctx_, n * c), wide = f32(ctx_, n * cd.mlp);
   Array hm = f32(ctx_, split ? 3 * n * c : 1), o = f32(ctx_, split ? n * c : 1);
   for (const auto& l : w_.clip_layers) {
     norm_project(x.f32(), n, c, l.ln1_w, l.ln1_b, kClipEps, normed, l.qkv, 3 * c, l.qkv_b, qkv.f32());
@@ -469,11 +482,9 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
       softmax_rows(ctx_, scores.f32(), heads * n, n);
       gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, qkv.f32() + 2 * c, 3 * c, hd, merged.f32(), c, hd, heads);
     }
-    project(merged.f32(), n, c, l.out, c, l.out_b, proj.f32());
-    add_inplace(ctx_, x.f32(), proj.f32(), n * c);
+    project(merged.f32(), n, c, l.out, c, l.out_b, x.f32(), true);
     norm_project(x.f32(), n, c, l.ln2_w, l.ln2_b, kClipEps, normed, l.fc1, cd.mlp, l.fc1_b, wide.f32());
-    project_bf16(activated_bf16(wide.f32(), n * cd.mlp, true), n, cd.mlp, l.fc2, c, l.fc2_b, proj.f32());
-    add_inplace(ctx_, x.f32(), proj.f32(), n * c);
+    project_bf16(activated_bf16(wide.f32(), n * cd.mlp, true), n, cd.mlp, l.fc2, c, l.fc2_b, x.f32(), true);
   }
 }
 

@@ -156,11 +156,12 @@ class VisionEncoder {
  private:
   // y = bf16(x) w^T (+ bias) on the matrix cores, k split over a pool
   // workspace where the product has too few tiles to cover the GPU.
+  // (accumulate: y += the product, as the product then an in-place add.)
   void project(const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w, std::int64_t n,
-               const float* bias, float* y) const;
+               const float* bias, float* y, bool accumulate = false) const;
   // The same with x already bf16.
   void project_bf16(const std::uint16_t* xb, std::int64_t m, std::int64_t k, const std::uint16_t* w, std::int64_t n,
-                    const float* bias, float* y) const;
+                    const float* bias, float* y, bool accumulate = false) const;
   // bf16(gelu_erf(x)) (quick: bf16(quick_gelu(x))) in project()'s scratch.
   const std::uint16_t* activated_bf16(const float* x, std::int64_t n, bool quick) const;
   // bf16(LN(x)) in project()'s scratch, x untouched (null: c above 16384).
@@ -172,8 +173,9 @@ class VisionEncoder {
   void sam_forward(const float* image, std::int64_t size, Array& cells) const;
   void sam_block(std::size_t index, Array& x, std::int64_t g) const;
   // x fp32, or xb (non-null) the same rows already in bf16
+  // (accumulate: out += the output projection.)
   void sam_attention(std::size_t index, const float* x, const std::uint16_t* xb, std::int64_t windows, std::int64_t h,
-                     std::int64_t w, float* out) const;
+                     std::int64_t w, float* out, bool accumulate) const;
   void conv3(const float* hwc, std::int64_t side, std::int64_t in_c, const std::uint16_t* w, std::int64_t out_c,
              int stride, Array& out, std::int64_t& out_side) const;
   void clip_forward(const float* cells, std::int64_t g, Array& x) const;

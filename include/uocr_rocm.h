@@ -343,6 +343,13 @@ UOCR_ROCM_API int uocr_rocm_linear_ws(void* stream, const float* x, int64_t m, i
 UOCR_ROCM_API int uocr_rocm_linear_bf16x_ws(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w,
                                             int64_t n, const float* bias, float* y, float* workspace,
                                             int64_t workspace_floats);
+/* New: y += bf16(x) . w^T (+ bias), y fp32 [m, n] read and written: each
+ * element becomes y + (sum + bias), bitwise uocr_rocm_linear_bf16x_ws into
+ * a temporary followed by uocr_rocm_add_inplace (the reference's linear then
+ * add_inplace on a residual stream, ops.h:14-17). Same workspace rule. */
+UOCR_ROCM_API int uocr_rocm_linear_bf16x_add_ws(void* stream, const uint16_t* x, int64_t m, int64_t k,
+                                                const uint16_t* w, int64_t n, const float* bias, float* y,
+                                                float* workspace, int64_t workspace_floats);
 
 /* New: dst[i] = bf16(src[i]), nearest even; both 16-byte aligned. */
 UOCR_ROCM_API int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst);

@@ -153,3 +153,26 @@ def test_linear_split_k_against_the_oracle(backend, m, k, n, fp32_x):
     y2 = torch.empty(m, n, device="cuda")
     backend.linear_ws(xd, dev_bf16(wb), y2, small, dev_f32(bias))
     assert np.array_equal(host_f32(y2), host_f32(y1))
+
+
+@pytest.mark.parametrize("m,k,n,with_bias", [(4096, 768, 768, True), (4096, 3072, 768, True), (257, 4096, 1024, True),
+                                             (257, 1024, 1024, False), (33, 100, 70, True), (1, 64, 8, True)])
+def test_linear_add_is_the_product_then_the_add(backend, m, k, n, with_bias):
+    """y += bf16 x . w^T + bias (a residual stream's projection) against the
+    product into a temporary then add_inplace, bit for bit, split over k (257
+    rows, k >= 1024) or not, ragged k, one row."""
+    x = normal(460 + m, (m, k))
+    wb = bf16(0.03 * normal(461 + n, (n, k)))
+    bias = dev_f32(normal(462, n)) if with_bias else None
+    xb = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(dev_f32(x), xb)
+    floats = backend.linear_workspace_floats(m, k, n)
+    ws = torch.full((max(floats, 1),), float("nan"), device="cuda")
+    resid = dev_f32(normal(463, (m, n)))
+    t = torch.empty(m, n, device="cuda")
+    backend.linear_ws(xb, dev_bf16(wb), t, ws, bias)
+    want = resid.clone()
+    backend.add_inplace(want, t)
+    got = resid.clone()
+    backend.linear_add(xb, dev_bf16(wb), got, ws, bias)
+    assert torch.equal(got, want), f"m={m} k={k} n={n} ({floats} workspace floats)"
