@@ -246,20 +246,29 @@ __device__ __forceinline__ void store_tile(const LinearArgs& a, const Work& wk, 
                                            const f32x16 (&acc)[2][2]) {
   const bool split = a.part != nullptr;
   float* out = split ? a.part + static_cast<int64_t>(wk.split) * a.m * a.n : a.y;
+  const bool add = !split && a.bias != nullptr;
+  const bool accumulate = !split && a.accumulate;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int64_t col = wk.n0 + 64 * wn + 32 * j + r32;
     if (col >= a.n) continue;
-    const bool add = !split && a.bias != nullptr;
     const float bv = add ? a.bias[col] : 0.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
+      const int64_t row0 = wk.m0 + 64 * wm + 32 * i + 4 * half;
+      float* const o = out + row0 * a.n + col;  // element r: row row0 + 8 (r / 4) + r % 4
+      auto live = [&](int r) { return row0 + 8 * (r / 4) + (r % 4) < a.m; };
+      auto off = [&](int r) { return static_cast<int64_t>(8 * (r / 4) + (r % 4)) * a.n; };
+      // accumulate: the 16 y values are requested before the first store (a
+      // load issued after a store could alias it and would wait for it)
+      float base[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) base[r] = accumulate && live(r) ? o[off(r)] : 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = wk.m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
-        if (row < a.m) {
+        if (live(r)) {
           const float v = add ? acc[i][j][r] + bv : acc[i][j][r];
-          out[row * a.n + col] = !split && a.accumulate ? out[row * a.n + col] + v : v;
+          o[off(r)] = accumulate ? base[r] + v : v;
         }
       }
     }
