@@ -160,6 +160,9 @@ _SIGNATURES = {
                              _i64, _i64, _f32, _vp, _i64], _int),
     "uocr_rocm_attention_rel_pos": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                      _i64, _i64, _i64, _f32, _vp, _vp], _int),
+    "uocr_rocm_attention_rel_pos_workspace_floats": ([_i64, _i64, _i64], _i64),
+    "uocr_rocm_attention_rel_pos_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                                        _i64, _i64, _i64, _f32, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_split_heads": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_merge_heads": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_rel_pos_bias": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp], _int),
@@ -628,15 +631,26 @@ def attention(q, k, v, out, slices, rows, keys, hd, scale, mask=None, strides=No
         0 if mask is None else mask.shape[-1])
 
 
-def attention_rel_pos(q, k, v, out, slices, h, w, hd, scale, rh, rw, strides=None, stream=None):
-    """attention over h x w windows with SAM's relative-position bias (new)."""
+def attention_rel_pos(q, k, v, out, slices, h, w, hd, scale, rh, rw, strides=None, workspace=None, stream=None):
+    """attention over h x w windows with SAM's relative-position bias (new);
+    with a workspace (attention_rel_pos_workspace_floats) the bias's dot
+    products are formed by a launch of their own first."""
     n = h * w
     st = strides or {}
     qo = _operand(q, *st.get("q", (0, hd, n * hd)))
     ko = _operand(k, *st.get("k", (0, hd, n * hd)))
     vo = _operand(v, *st.get("v", (0, hd, n * hd)))
     oo = _operand(out, *st.get("out", (0, hd, n * hd)))
-    _op("uocr_rocm_attention_rel_pos", stream, *qo, *ko, *vo, *oo, slices, h, w, hd, scale, _ptr(rh), _ptr(rw))
+    if workspace is None:
+        _op("uocr_rocm_attention_rel_pos", stream, *qo, *ko, *vo, *oo, slices, h, w, hd, scale, _ptr(rh), _ptr(rw))
+    else:
+        _op("uocr_rocm_attention_rel_pos_ws", stream, *qo, *ko, *vo, *oo, slices, h, w, hd, scale, _ptr(rh),
+            _ptr(rw), _ptr(workspace), workspace.numel())
+
+
+def attention_rel_pos_workspace_floats(slices, h, w):
+    """Floats of the workspace attention_rel_pos forms the bias's dots in."""
+    return int(lib().uocr_rocm_attention_rel_pos_workspace_floats(slices, h, w))
 
 
 def split_heads(x, parts, heads, hd, y, stream=None):

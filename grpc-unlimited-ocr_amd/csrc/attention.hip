@@ -9,10 +9,12 @@
 // values product (src/model/cuda/cuda_vision.cpp:159-170,251-254,
 // src/model/cuda/cuda_decoder.cpp:88-105): the scores never reach memory.
 //
-// A workgroup of 4 waves (2 with the relative-position bias) takes 128 (64)
-// query rows of one slice; each wave owns 32 of them and walks the keys 32
-// at a time, the key and value tiles staged in LDS for the workgroup (the
-// next tile's loads in flight in registers while the current one is used). Per tile a wave forms S^T = K Q^T (32 keys x 32
+// A workgroup of 4 waves (2 with the relative-position bias over a grid of
+// whole tiles) takes 128 (64) query rows of one slice; each wave owns 32 of
+// them and walks the keys 32 at a time, the key and value tiles staged in
+// LDS for the workgroup (the next tile's loads in flight in registers while
+// the current one is used); a wave past the last row only helps stage the
+// tiles. Per tile a wave forms S^T = K Q^T (32 keys x 32
 // queries, hd / 2 products, each summing 2 of the head's columns: lane half
 // h supplies column h * hd / 2 + i to product i, so a lane keeps its query's
 // half row in registers and reads its key's half row from LDS), which leaves
@@ -57,11 +59,12 @@ constexpr bool rel_pos() {
 constexpr int kQueriesPerWave = 32;
 constexpr int kKeyTile = 32;
 // Waves per workgroup: 4 (128 query rows share each key/value tile), or 2
-// with the relative-position bias, whose per-query dot products take LDS
-// (2 waves keep three workgroups on a CU instead of one).
+// with the relative-position bias over a grid of whole tiles (SAM's global
+// layer: the per-query dot products, h + w of them, take LDS, and 2 waves
+// keep three workgroups on a CU instead of one).
 template <Bias kBias>
 constexpr int waves_of() {
-  return rel_pos<kBias>() ? 2 : 4;
+  return kBias == Bias::kRelPosRows ? 2 : 4;
 }
 constexpr int kMaxRelSpan = 256;  // h + w of the relative-position bias
 
@@ -80,6 +83,11 @@ struct AttnArgs {
   int h, w;
   int dots_ld;  // floats between two query rows' dot products in LDS
   int dw_off;   // where a row's width terms start (its height terms at 0)
+  // The dot products of every (slice, query row) formed beforehand by
+  // rel_dots_k, [slices][rows][dots_ld] in the LDS layout; null: each
+  // workgroup forms its own.
+  const float* table;
+  float* table_out;  // rel_dots_k's output (the same table)
 };
 
 template <int HD, int kThreads>
@@ -165,6 +173,24 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
 
   float* my_dots = dots + (wave * kQueriesPerWave + c) * a.dots_ld;
   if constexpr (rel_pos<kBias>()) {
+    if (a.table != nullptr) {
+      // the workgroup's rows of the table lie contiguous in memory with the
+      // LDS row stride: one coalesced copy by every thread
+      const int first = blockIdx.x * kQueriesPerBlock;
+      const int here = a.rows - first < kQueriesPerBlock ? a.rows - first : kQueriesPerBlock;
+      const float* src = a.table + (slice * a.rows + first) * static_cast<int64_t>(a.dots_ld);
+      const int count = here * a.dots_ld;
+      if constexpr (kBias == Bias::kRelPosRows) {  // dots_ld a multiple of 4
+        for (int i = 4 * static_cast<int>(threadIdx.x); i < count; i += 4 * kThreads) {
+          *reinterpret_cast<float4*>(dots + i) = *reinterpret_cast<const float4*>(src + i);
+        }
+      } else {
+        for (int i = static_cast<int>(threadIdx.x); i < count; i += kThreads) dots[i] = src[i];
+      }
+    }
+  }
+  if constexpr (rel_pos<kBias>()) {
+    if (a.table == nullptr) {
     // dh[ky] = q . rh[qy, ky] and dw[kx] = q . rw[qx, kx]: each lane forms
     // the partial dot over the half of the columns it holds in qv (fp32 in
     // column order, the table rows as 16-byte loads), and the two halves'
@@ -191,6 +217,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
       const float dot = hl == 0 ? p + other : other + p;
       if ((j < a.h) == (hl == 0)) my_dots[j < a.h ? j : a.dw_off + (j - a.h)] = dot;
     }
+    }
   }
 
   store_tile<HD, kThreads>(ks, vs, kr, vr);
@@ -214,7 +241,9 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     // tile's products and softmax; the tile's K and V still reach LDS for
     // the other waves.
     float mk[kBias == Bias::kMask ? 16 : 1];
-    bool live = true;
+    // A wave whose rows all lie past the last query row (the tail workgroup
+    // of a slice) only helps stage the tiles.
+    bool live = q0 < a.rows;
     if constexpr (kBias == Bias::kMask) {
       bool any = false;
 #pragma unroll
@@ -223,7 +252,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
         mk[r] = key < a.keys && qin ? a.mask[qrow * a.mask_ld + key] : -INFINITY;
         any = any || mk[r] != -INFINITY;
       }
-      live = __ballot(any) != 0;
+      live = live && __ballot(any) != 0;
     }
     if (live) {
       // S^T = K Q^T: 32 keys x 32 queries
@@ -338,6 +367,57 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   }
 }
 
+// The relative-position dot products of every (slice, query row) into
+// table [slices][rows][dots_ld] (height terms at 0, width terms at dw_off):
+// block (j, s) takes table slice j of slice s (rh[qy = j] for j < h, else
+// rw[qx = j - h]) and the h or w query rows that use it, stages both in LDS
+// (rows padded to HD + 1 floats: the threads of a pass read different
+// banks), and forms every (query, table row) dot, fp32 in column order.
+// Each table slice is read once per slice here, where a workgroup of the
+// attention forming its own dots reads a width slice per query.
+template <int HD>
+__global__ __launch_bounds__(kBlock) void rel_dots_k(const AttnArgs a) {
+  extern __shared__ float rel_lds[];
+  const int j = static_cast<int>(blockIdx.x);
+  const int64_t slice = blockIdx.y;
+  const bool height = j < a.h;
+  const int nq = height ? a.w : a.h;  // the query rows that use this table slice
+  const int nr = height ? a.h : a.w;  // its rows: dots per query
+  const float* tab = height ? a.rh + static_cast<int64_t>(j) * a.h * HD : a.rw + static_cast<int64_t>(j - a.h) * a.w * HD;
+  auto query = [&](int i) { return height ? j * a.w + i : i * a.w + (j - a.h); };
+  float* qs = rel_lds;
+  float* ts = rel_lds + nq * (HD + 1);
+  const float* qb = a.q + slice * a.sq;
+  for (int e = static_cast<int>(threadIdx.x); e < nq * HD; e += kBlock) {
+    const int i = e / HD, d = e - i * HD;
+    qs[i * (HD + 1) + d] = qb[static_cast<int64_t>(query(i)) * a.ldq + d];
+  }
+  for (int e = static_cast<int>(threadIdx.x); e < nr * HD; e += kBlock) {
+    const int r = e / HD, d = e - r * HD;
+    ts[r * (HD + 1) + d] = tab[e];
+  }
+  __syncthreads();
+  float* out = a.table_out + slice * a.rows * static_cast<int64_t>(a.dots_ld);
+  for (int p = static_cast<int>(threadIdx.x); p < nq * nr; p += kBlock) {
+    const int i = p / nr, r = p - i * nr;
+    const float* qrow = qs + i * (HD + 1);
+    const float* trow = ts + r * (HD + 1);
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int d = 0; d < HD; ++d) acc += qrow[d] * trow[d];
+    out[static_cast<int64_t>(query(i)) * a.dots_ld + (height ? r : a.dw_off + r)] = acc;
+  }
+}
+
+// Dynamic LDS above 64 KB has to be allowed per kernel first.
+template <class Kernel>
+void allow_lds(Kernel kernel, size_t bytes) {
+  if (bytes > 65536) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(bytes));
+  }
+}
+
 template <Bias kBias>
 int launch(const char* what, void* stream, int64_t hd, int64_t slices, const AttnArgs& a) {
   constexpr int kThreads = 64 * waves_of<kBias>(), kQueriesPerBlock = waves_of<kBias>() * kQueriesPerWave;
@@ -346,8 +426,10 @@ int launch(const char* what, void* stream, int64_t hd, int64_t slices, const Att
   const size_t dyn = rel_pos<kBias>() ? sizeof(float) * kQueriesPerBlock * static_cast<size_t>(a.dots_ld) : 0;
   clear_launch_error();
   if (hd == 64) {
+    allow_lds(attention_k<64, kBias>, dyn);
     attention_k<64, kBias><<<grid, kThreads, dyn, as_stream(stream)>>>(a);
   } else {
+    allow_lds(attention_k<128, kBias>, dyn);
     attention_k<128, kBias><<<grid, kThreads, dyn, as_stream(stream)>>>(a);
   }
   return check_launch(what);
@@ -369,6 +451,57 @@ int check_common(const char* what, const float* q, int64_t ldq, int64_t sq, cons
   return UOCR_ROCM_OK;
 }
 
+// The LDS layout of the per-query dot products: a grid width of whole
+// tiles takes the per-tile bias terms with the width terms 16-byte aligned
+// and rows 4 times an odd number of floats apart; otherwise rows h + w + 1
+// apart.
+struct DotsLayout {
+  bool tile_rows;
+  int64_t ld, dw_off;
+};
+
+DotsLayout dots_layout(int64_t h, int64_t w) {
+  const bool tile_rows = w % kKeyTile == 0;
+  const int64_t dw_off = tile_rows ? (h + 3) / 4 * 4 : h;
+  int64_t quads = (dw_off + w) / 4;
+  quads += quads % 2 == 0 ? 1 : 0;
+  return {tile_rows, tile_rows ? 4 * quads : h + w + 1, dw_off};
+}
+
+int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
+                  int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo, int64_t so,
+                  int64_t slices, int64_t h, int64_t w, int64_t hd, float scale, const float* rh, const float* rw,
+                  float* workspace, int64_t workspace_floats) {
+  UOCR_REQUIRE(h >= 1 && w >= 1 && h + w <= kMaxRelSpan, what, "need h, w >= 1 and h + w <= 256");
+  const int64_t n = h * w;
+  if (const int st = check_common(what, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, n, n, hd)) {
+    return st;
+  }
+  UOCR_REQUIRE(rh != nullptr && rw != nullptr, what, "null relative-position table");
+  UOCR_REQUIRE(aligned16(rh) && aligned16(rw), what, "relative-position tables must be 16-byte aligned");
+  const DotsLayout lay = dots_layout(h, w);
+  // the dot table goes to the workspace when it holds it (16-byte aligned)
+  const bool table = workspace != nullptr && aligned16(workspace) && workspace_floats >= slices * n * lay.ld;
+  AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(n), static_cast<int>(n),
+             scale, nullptr, 0, rh, rw, static_cast<int>(h), static_cast<int>(w), static_cast<int>(lay.ld),
+             static_cast<int>(lay.dw_off), table ? workspace : nullptr, table ? workspace : nullptr};
+  if (table) {
+    const size_t lds = sizeof(float) * static_cast<size_t>((h + w) * (hd + 1));
+    const dim3 grid(static_cast<unsigned>(h + w), static_cast<unsigned>(slices));
+    clear_launch_error();
+    if (hd == 64) {
+      allow_lds(rel_dots_k<64>, lds);
+      rel_dots_k<64><<<grid, kBlock, lds, as_stream(stream)>>>(a);
+    } else {
+      allow_lds(rel_dots_k<128>, lds);
+      rel_dots_k<128><<<grid, kBlock, lds, as_stream(stream)>>>(a);
+    }
+    if (const int st = check_launch(what)) return st;
+  }
+  return lay.tile_rows ? launch<Bias::kRelPosRows>(what, stream, hd, slices, a)
+                       : launch<Bias::kRelPos>(what, stream, hd, slices, a);
+}
+
 }  // namespace
 }  // namespace uocr_rocm
 
@@ -386,7 +519,7 @@ int uocr_rocm_attention(void* stream, const float* q, int64_t ldq, int64_t sq, c
   }
   UOCR_REQUIRE(mask == nullptr || mask_ld >= keys, kWhat, "mask rows must hold every key");
   AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
-             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0};
+             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr};
   return mask != nullptr ? launch<Bias::kMask>(kWhat, stream, hd, slices, a)
                          : launch<Bias::kNone>(kWhat, stream, hd, slices, a);
 }
@@ -395,26 +528,22 @@ int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64
                                 int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo,
                                 int64_t so, int64_t slices, int64_t h, int64_t w, int64_t hd, float scale,
                                 const float* rh, const float* rw) {
-  constexpr const char* kWhat = "uocr_rocm_attention_rel_pos";
-  UOCR_REQUIRE(h >= 1 && w >= 1 && h + w <= kMaxRelSpan, kWhat, "need h, w >= 1 and h + w <= 256");
-  const int64_t n = h * w;
-  if (const int st = check_common(kWhat, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, n, n, hd)) {
-    return st;
-  }
-  UOCR_REQUIRE(rh != nullptr && rw != nullptr, kWhat, "null relative-position table");
-  UOCR_REQUIRE(aligned16(rh) && aligned16(rw), kWhat, "relative-position tables must be 16-byte aligned");
-  // A grid width of whole tiles takes the per-tile bias terms, the width
-  // terms 16-byte aligned.
-  const bool rows = w % kKeyTile == 0;
-  const int64_t dw_off = rows ? (h + 3) / 4 * 4 : h;
-  int64_t quads = (dw_off + w) / 4;
-  quads += quads % 2 == 0 ? 1 : 0;
-  const int64_t dots_ld = rows ? 4 * quads : h + w + 1;
-  AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(n), static_cast<int>(n),
-             scale, nullptr, 0, rh, rw, static_cast<int>(h), static_cast<int>(w), static_cast<int>(dots_ld),
-             static_cast<int>(dw_off)};
-  return rows ? launch<Bias::kRelPosRows>(kWhat, stream, hd, slices, a)
-              : launch<Bias::kRelPos>(kWhat, stream, hd, slices, a);
+  return rel_pos_entry("uocr_rocm_attention_rel_pos", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, h, w, hd, scale, rh,
+                       rw, nullptr, 0);
+}
+
+int64_t uocr_rocm_attention_rel_pos_workspace_floats(int64_t slices, int64_t h, int64_t w) {
+  if (slices < 1 || h < 1 || w < 1 || h + w > kMaxRelSpan) return 0;
+  return slices * h * w * dots_layout(h, w).ld;
+}
+
+int uocr_rocm_attention_rel_pos_ws(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                                   int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out,
+                                   int64_t ldo, int64_t so, int64_t slices, int64_t h, int64_t w, int64_t hd,
+                                   float scale, const float* rh, const float* rw, float* workspace,
+                                   int64_t workspace_floats) {
+  return rel_pos_entry("uocr_rocm_attention_rel_pos_ws", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so,
+                       slices, h, w, hd, scale, rh, rw, workspace, workspace_floats);
 }
 
 }  // extern "C"

@@ -213,6 +213,17 @@ void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOpe
                                     ldo, so, slices, h, w, hd, scale, rh, rw));
 }
 
+std::int64_t attention_rel_pos_workspace_floats(std::int64_t slices, std::int64_t h, std::int64_t w) {
+  return uocr_rocm_attention_rel_pos_workspace_floats(slices, h, w);
+}
+
+void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
+                       std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
+                       float scale, const float* rh, const float* rw, float* workspace, std::int64_t workspace_floats) {
+  check(uocr_rocm_attention_rel_pos_ws(ctx.stream(), q.p, q.ld, q.slice, k.p, k.ld, k.slice, v.p, v.ld, v.slice, out,
+                                       ldo, so, slices, h, w, hd, scale, rh, rw, workspace, workspace_floats));
+}
+
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
             std::int64_t n, const float* bias, float* y) {
   check(uocr_rocm_linear(ctx.stream(), x, m, k, w_bf16, n, bias, y));

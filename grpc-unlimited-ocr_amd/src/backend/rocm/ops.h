@@ -163,6 +163,12 @@ void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, 
 void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
                        std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
                        float scale, const float* rh, const float* rw);
+// New: the same with the bias's dot products formed beforehand into a
+// workspace of attention_rel_pos_workspace_floats(slices, h, w) floats.
+std::int64_t attention_rel_pos_workspace_floats(std::int64_t slices, std::int64_t h, std::int64_t w);
+void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
+                       std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
+                       float scale, const float* rh, const float* rw, float* workspace, std::int64_t workspace_floats);
 // y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]) on the matrix cores, fp32
 // accumulation (m == 1: the GEMV); the reference's linear.
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,

@@ -345,8 +345,10 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::
     Array split = f32(ctx_, 3 * part), o = f32(ctx_, part);
     split_heads(ctx_, qkv.f32(), rows, 3, heads, hd, split.f32());
     const float* q = split.f32();
+    const std::int64_t dots = attention_rel_pos_workspace_floats(slices, h, w);
+    Array table = f32(ctx_, dots);  // the bias's dot products, formed once per slice
     attention_rel_pos(ctx_, {q, hd, n * hd}, {q + part, hd, n * hd}, {q + 2 * part, hd, n * hd}, o.f32(), hd, n * hd,
-                      slices, h, w, hd, scale, rh.f32(), rw.f32());
+                      slices, h, w, hd, scale, rh.f32(), rw.f32(), table.f32(), dots);
     merge_heads(ctx_, o.f32(), heads, rows, hd, merged.f32());
   } else if (hd % 4 == 0) {
     const std::int64_t slices = heads * windows, part = heads * rows * hd;

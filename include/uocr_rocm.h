@@ -458,6 +458,18 @@ UOCR_ROCM_API int uocr_rocm_attention_rel_pos(void* stream, const float* q, int6
                                               int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv,
                                               float* out, int64_t ldo, int64_t so, int64_t slices, int64_t h,
                                               int64_t w, int64_t hd, float scale, const float* rh, const float* rw);
+/* New: the same with a workspace for the bias's per-query dot products
+ * (q . rh[qy, ky] and q . rw[qx, kx] of every slice and query row), formed
+ * by one launch that reads each table slice once per slice before the
+ * attention, in place of every workgroup forming its own; the workspace
+ * holds uocr_rocm_attention_rel_pos_workspace_floats(slices, h, w) floats,
+ * 16-byte aligned (a smaller one: the attention forms its own). */
+UOCR_ROCM_API int64_t uocr_rocm_attention_rel_pos_workspace_floats(int64_t slices, int64_t h, int64_t w);
+UOCR_ROCM_API int uocr_rocm_attention_rel_pos_ws(void* stream, const float* q, int64_t ldq, int64_t sq,
+                                                 const float* k, int64_t ldk, int64_t sk, const float* v, int64_t ldv,
+                                                 int64_t sv, float* out, int64_t ldo, int64_t so, int64_t slices,
+                                                 int64_t h, int64_t w, int64_t hd, float scale, const float* rh,
+                                                 const float* rw, float* workspace, int64_t workspace_floats);
 
 /* ---- decode-step neighbours ---------------------------------------------------- */
 

@@ -106,6 +106,19 @@ def test_attention_rel_pos_against_the_oracle(backend, windows, heads, h, w, hd)
     backend.attention_rel_pos(dev_f32(q), dev_f32(k), dev_f32(v), out, slices, h, w, hd, scale, dev_f32(rh),
                               dev_f32(rw))
     assert_f32_close(host_f32(out), want, 1e-5, f"rel-pos attention {windows}x{heads} {h}x{w}")
+    # the dots formed beforehand into a workspace (NaN-filled: every entry read is written)
+    floats = backend.attention_rel_pos_workspace_floats(slices, h, w)
+    assert floats >= slices * n * (h + w)
+    ws = torch.full((floats,), float("nan"), device="cuda")
+    out2 = torch.full((slices, n, hd), float("nan"), device="cuda")
+    backend.attention_rel_pos(dev_f32(q), dev_f32(k), dev_f32(v), out2, slices, h, w, hd, scale, dev_f32(rh),
+                              dev_f32(rw), workspace=ws)
+    assert_f32_close(host_f32(out2), want, 1e-5, f"rel-pos attention with a dot table {windows}x{heads} {h}x{w}")
+    small = torch.zeros(1, device="cuda")  # a workspace too small: the workgroups form their own dots
+    out3 = torch.full((slices, n, hd), float("nan"), device="cuda")
+    backend.attention_rel_pos(dev_f32(q), dev_f32(k), dev_f32(v), out3, slices, h, w, hd, scale, dev_f32(rh),
+                              dev_f32(rw), workspace=small)
+    assert torch.equal(out3, out)
 
 
 def test_attention_rejects_bad_shapes(backend):
