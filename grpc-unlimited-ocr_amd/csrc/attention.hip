@@ -372,7 +372,8 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
 // block (j, s) takes table slice j of slice s (rh[qy = j] for j < h, else
 // rw[qx = j - h]) and the h or w query rows that use it, stages both in LDS
 // (rows padded to HD + 1 floats: the threads of a pass read different
-// banks), and forms every (query, table row) dot, fp32 in column order.
+// banks), and forms every (query, table row) dot, fp32 in column order, 4 x
+// 4 of them per thread (one per thread where there are few).
 // Each table slice is read once per slice here, where a workgroup of the
 // attention forming its own dots reads a width slice per query.
 template <int HD>
@@ -398,14 +399,54 @@ __global__ __launch_bounds__(kBlock) void rel_dots_k(const AttnArgs a) {
   }
   __syncthreads();
   float* out = a.table_out + slice * a.rows * static_cast<int64_t>(a.dots_ld);
-  for (int p = static_cast<int>(threadIdx.x); p < nq * nr; p += kBlock) {
-    const int i = p / nr, r = p - i * nr;
-    const float* qrow = qs + i * (HD + 1);
-    const float* trow = ts + r * (HD + 1);
-    float acc = 0.0f;
+  if (nq * nr < 4 * kBlock) {
+    // few pairs (a small window): one per thread
+    for (int p = static_cast<int>(threadIdx.x); p < nq * nr; p += kBlock) {
+      const int i = p / nr, r = p - i * nr;
+      const float* qrow = qs + i * (HD + 1);
+      const float* trow = ts + r * (HD + 1);
+      float acc = 0.0f;
 #pragma unroll 16
-    for (int d = 0; d < HD; ++d) acc += qrow[d] * trow[d];
-    out[static_cast<int64_t>(query(i)) * a.dots_ld + (height ? r : a.dw_off + r)] = acc;
+      for (int d = 0; d < HD; ++d) acc += qrow[d] * trow[d];
+      out[static_cast<int64_t>(query(i)) * a.dots_ld + (height ? r : a.dw_off + r)] = acc;
+    }
+    return;
+  }
+  // 4 x 4 (query, table row) blocks per thread: 8 LDS reads feed 16 FMAs
+  const int nqb = (nq + 3) / 4, nrb = (nr + 3) / 4;
+  for (int blk = static_cast<int>(threadIdx.x); blk < nqb * nrb; blk += kBlock) {
+    const int i0 = 4 * (blk / nrb), r0 = 4 * (blk - (blk / nrb) * nrb);
+    const float* qrow[4];
+    const float* trow[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      qrow[u] = qs + (i0 + u < nq ? i0 + u : nq - 1) * (HD + 1);
+      trow[u] = ts + (r0 + u < nr ? r0 + u : nr - 1) * (HD + 1);
+    }
+    float acc[4][4] = {};
+#pragma unroll 8
+    for (int d = 0; d < HD; ++d) {
+      float qv[4], tv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        qv[u] = qrow[u][d];
+        tv[u] = trow[u][d];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[u][v] += qv[u] * tv[v];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (i0 + u >= nq) continue;
+      float* orow = out + static_cast<int64_t>(query(i0 + u)) * a.dots_ld + (height ? 0 : a.dw_off);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (r0 + v < nr) orow[r0 + v] = acc[u][v];
+      }
+    }
   }
 }
 
