@@ -94,13 +94,14 @@ struct Work {
   int split, k_begin, k_end;
 };
 
+template <int kTileRows = kTileM>
 __device__ __forceinline__ Work work_of(const LinearArgs& a) {
   const int tiles = a.tiles_m * a.tiles_n;
   const int split = static_cast<int>(blockIdx.x) / tiles;
   int tm, tn;
   tile_of(static_cast<int>(blockIdx.x) - split * tiles, a.tiles_m, a.tiles_n, tm, tn);
   const int kb = split * a.k_len;
-  return {static_cast<int64_t>(tm) * kTileM, static_cast<int64_t>(tn) * kTileN, split, kb,
+  return {static_cast<int64_t>(tm) * kTileRows, static_cast<int64_t>(tn) * kTileN, split, kb,
           a.k - kb < a.k_len ? a.k : kb + a.k_len};
 }
 
@@ -387,6 +388,84 @@ __global__ __launch_bounds__(kGemmThreads) void linear_dma_k(const LinearArgs a)
   store_tile(a, wk, wm, wn, half, r32, acc);
 }
 
+// Products of few rows (CLIP's 257, a short prompt): 32 x 128 tiles, so that
+// a 257-row product has 9 row tiles instead of 3 (the last of them holding
+// one row) and three times the workgroups. Wave w of 4 owns columns
+// 32 w .. 32 w + 31 of the tile, one v_mfma_f32_32x32x16_bf16 tile, its
+// operands read from the same swizzled LDS layout as the 128 x 128 tiles;
+// bf16 x and k a multiple of 64, tiles straight from memory into LDS.
+constexpr int kNarrowM = 32;
+constexpr int kNarrowChunks = kNarrowM * kRowChunks;  // one x chunk per thread
+static_assert(kNarrowChunks == kGemmThreads, "one x tile load per wave");
+
+__device__ __forceinline__ void dma_step_narrow(const LinearArgs& a, int64_t m0, int64_t n0, int k0, u32x4* xs,
+                                                u32x4* ws, int wave, int lane) {
+  const uint16_t* x = static_cast<const uint16_t*>(a.x);
+  {
+    const int s0 = wave * kWave;
+    const int sl = s0 + lane, row = sl / kRowChunks, c = (sl % kRowChunks) ^ swz(row);
+    const int64_t xr = m0 + row < a.m ? m0 + row : a.m - 1;
+    __builtin_amdgcn_global_load_lds(x + xr * a.k + k0 + 8 * c, xs + s0, 16, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < kTileChunks / kGemmThreads; ++i) {
+    const int s0 = (wave * (kTileChunks / kGemmThreads) + i) * kWave;
+    const int sl = s0 + lane, row = sl / kRowChunks, c = (sl % kRowChunks) ^ swz(row);
+    const int64_t wr = n0 + row < a.n ? n0 + row : a.n - 1;
+    __builtin_amdgcn_global_load_lds(a.w + wr * a.k + k0 + 8 * c, ws + s0, 16, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(kGemmThreads) void linear_narrow_k(const LinearArgs a) {
+  __shared__ u32x4 xs[2][kNarrowChunks];
+  __shared__ u32x4 ws[2][kTileChunks];
+  const Work wk = work_of<kNarrowM>(a);
+  const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
+  const int half = lane >> 5, r32 = lane & 31;
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  const int steps = (wk.k_end - wk.k_begin) / kTileK;
+  dma_step_narrow(a, wk.m0, wk.n0, wk.k_begin, xs[0], ws[0], wave, lane);
+  for (int t = 0; t < steps; ++t) {
+    const int buf = t & 1;
+    wait_loads_and_barrier<0>();  // this step's tiles are in LDS; every wave is done with the other buffer
+    if (t + 1 < steps) {
+      dma_step_narrow(a, wk.m0, wk.n0, wk.k_begin + (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
+    }
+    bf16x8 fa[4], fb[4];
+#pragma unroll
+    for (int kk = 0; kk < kTileK / 16; ++kk) {
+      fa[kk] = as_bf16x8(xs[buf][slot(r32, 2 * kk + half)]);
+      fb[kk] = as_bf16x8(ws[buf][slot(32 * wave + r32, 2 * kk + half)]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kTileK / 16; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk], fb[kk], acc, 0, 0, 0);
+  }
+  // acc[r]: row 8 (r / 4) + 4 half + r % 4 of the tile, column 32 wave + r32
+  const bool split = a.part != nullptr;
+  float* out = split ? a.part + static_cast<int64_t>(wk.split) * a.m * a.n : a.y;
+  const int64_t col = wk.n0 + 32 * wave + r32;
+  if (col >= a.n) return;
+  const bool add = !split && a.bias != nullptr;
+  const bool accumulate = !split && a.accumulate;
+  const float bv = add ? a.bias[col] : 0.0f;
+  const int64_t row0 = wk.m0 + 4 * half;
+  float* const o = out + row0 * a.n + col;
+  auto live = [&](int r) { return row0 + 8 * (r / 4) + (r % 4) < a.m; };
+  auto off = [&](int r) { return static_cast<int64_t>(8 * (r / 4) + (r % 4)) * a.n; };
+  float base[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) base[r] = accumulate && live(r) ? o[off(r)] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    if (live(r)) {
+      const float v = add ? acc[r] + bv : acc[r];
+      o[off(r)] = accumulate ? base[r] + v : v;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kBlock) void round_bf16_k(const float* __restrict__ src, int64_t n,
                                                         uint16_t* __restrict__ dst) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8;
@@ -401,17 +480,26 @@ __global__ __launch_bounds__(kBlock) void round_bf16_k(const float* __restrict__
   }
 }
 
+// Products of at most this many rows take the 32-row tiles (bf16 x, k a
+// multiple of 64), splitting k below this many of those tiles when k is at
+// least 2048 (measured at 257 rows: k 4096 runs 2.5x faster split 16 ways,
+// k 1024 loses 20-30% split 3-4 ways).
+constexpr int64_t kNarrowRows = 512;
+constexpr int64_t kNarrowSplitBelow = 256;
+
 }  // namespace
 
 // The splits of k worth taking for an m x n x k product: a product of
-// fewer than 64 tiles with k >= 1024 gets enough workgroups to cover the 256
-// CUs twice, each split at least 4 steps of 64 columns; any other runs
-// unsplit. (Measured at the vision encoder's shapes: 16-24 tiles with k of
-// 2304-4608 run 1.3-1.9x faster split; 72-234 tiles, or k of 768-1024,
-// lose 5-100% to the partial sums' traffic and the extra launch.)
-int64_t splits_for(int64_t m, int64_t k, int64_t n) {
-  const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
-  if (tiles >= 64 || k < 16 * kTileK) return 1;
+// fewer than 64 tiles with k >= 1024 (of 32-row tiles: fewer than 256 with
+// k >= 2048) gets enough workgroups to cover the 256 CUs twice, each split
+// at least 4 steps of 64 columns; any other runs unsplit. (Measured at the
+// vision encoder's shapes: 16-24 tiles with k of 2304-4608 run 1.3-1.9x
+// faster split; 72-234 tiles, or k of 768-1024, lose 5-100% to the partial
+// sums' traffic and the extra launch.)
+int64_t splits_for(int64_t m, int64_t k, int64_t n, bool narrow = false) {
+  const int64_t tile_rows = narrow ? kNarrowM : kTileM;
+  const int64_t tiles = ((m + tile_rows - 1) / tile_rows) * ((n + kTileN - 1) / kTileN);
+  if (tiles >= (narrow ? kNarrowSplitBelow : 64) || k < (narrow ? 32 : 16) * kTileK) return 1;
   int64_t s = (512 + tiles - 1) / tiles;
   s = s < k / (4 * kTileK) ? s : k / (4 * kTileK);
   return s < 32 ? s : 32;
@@ -425,10 +513,12 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
   UOCR_REQUIRE(k >= 1 && k < (int64_t{1} << 30), what, "k must be in [1, 2^30)");
   UOCR_REQUIRE(x != nullptr && w != nullptr && y != nullptr, what, "null x, w or y");
   const bool ragged = k % 8 != 0 || !aligned16(x) || !aligned16(w);
-  const int64_t tiles_m = (m + kTileM - 1) / kTileM, tiles_n = (n + kTileN - 1) / kTileN;
+  const bool narrow = !ragged && !f32x && k % kTileK == 0 && m <= kNarrowRows;
+  const int64_t tile_rows = narrow ? kNarrowM : kTileM;
+  const int64_t tiles_m = (m + tile_rows - 1) / tile_rows, tiles_n = (n + kTileN - 1) / kTileN;
   UOCR_REQUIRE(tiles_m * tiles_n < (int64_t{1} << 31), what, "too many tiles");
   // split k into the workspace when it holds the partial products
-  int64_t splits = workspace != nullptr ? splits_for(m, k, n) : 1;
+  int64_t splits = workspace != nullptr ? splits_for(m, k, n, narrow) : 1;
   if (splits > 1 && workspace_floats < splits * m * n) splits = 1;
   const int64_t k_len = splits > 1 ? (k / splits + kTileK - 1) / kTileK * kTileK : k;
   splits = (k + k_len - 1) / k_len;
@@ -456,6 +546,8 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
     }
   } else if (f32x) {
     linear_staged_k<true, false><<<grid, kGemmThreads, 0, st>>>(a);
+  } else if (narrow) {
+    linear_narrow_k<<<grid, kGemmThreads, 0, st>>>(a);
   } else if (k % kTileK == 0) {
     linear_dma_k<<<grid, kGemmThreads, 0, st>>>(a);
   } else {
@@ -492,7 +584,12 @@ int uocr_rocm_linear_bf16x(void* stream, const uint16_t* x, int64_t m, int64_t k
 
 int64_t uocr_rocm_linear_workspace_floats(int64_t m, int64_t k, int64_t n) {
   if (m <= 1 || n <= 0 || k <= 0) return 0;
-  const int64_t s = splits_for(m, k, n);
+  // enough for either tiling a product of few rows may take
+  int64_t s = splits_for(m, k, n);
+  if (m <= kNarrowRows) {
+    const int64_t sn = splits_for(m, k, n, true);
+    s = sn > s ? sn : s;
+  }
   return s > 1 ? s * m * n : 0;
 }
 
