@@ -388,21 +388,24 @@ __global__ __launch_bounds__(kGemmThreads) void linear_dma_k(const LinearArgs a)
   store_tile(a, wk, wm, wn, half, r32, acc);
 }
 
-// Products of few rows (CLIP's 257, a short prompt): 32 x 128 tiles, so that
-// a 257-row product has 9 row tiles instead of 3 (the last of them holding
-// one row) and three times the workgroups. Wave w of 4 owns columns
-// 32 w .. 32 w + 31 of the tile, one v_mfma_f32_32x32x16_bf16 tile, its
-// operands read from the same swizzled LDS layout as the 128 x 128 tiles;
-// bf16 x and k a multiple of 64, tiles straight from memory into LDS.
+// Products of few rows (CLIP's 257, a short prompt), or of too few 128-row
+// tiles to give every CU one: TM x 128 tiles with TM 32 or 64, so that a
+// 257-row product has 9 row tiles instead of 3 (the last of them holding
+// one row), and a [4096, 768] output 384 tiles instead of 192. Wave w of 4
+// owns columns 32 w .. 32 w + 31 of the tile, TM / 32
+// v_mfma_f32_32x32x16_bf16 tiles, its operands read from the same swizzled
+// LDS layout as the 128 x 128 tiles; bf16 x and k a multiple of 64, tiles
+// straight from memory into LDS.
 constexpr int kNarrowM = 32;
-constexpr int kNarrowChunks = kNarrowM * kRowChunks;  // one x chunk per thread
-static_assert(kNarrowChunks == kGemmThreads, "one x tile load per wave");
 
+template <int TM>
 __device__ __forceinline__ void dma_step_narrow(const LinearArgs& a, int64_t m0, int64_t n0, int k0, u32x4* xs,
                                                 u32x4* ws, int wave, int lane) {
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
-  {
-    const int s0 = wave * kWave;
+  constexpr int kXPerWave = TM * kRowChunks / kGemmThreads;  // x tile loads per wave: 1 or 2
+#pragma unroll
+  for (int i = 0; i < kXPerWave; ++i) {
+    const int s0 = (wave * kXPerWave + i) * kWave;
     const int sl = s0 + lane, row = sl / kRowChunks, c = (sl % kRowChunks) ^ swz(row);
     const int64_t xr = m0 + row < a.m ? m0 + row : a.m - 1;
     __builtin_amdgcn_global_load_lds(x + xr * a.k + k0 + 8 * c, xs + s0, 16, 0, 0);
@@ -416,33 +419,43 @@ __device__ __forceinline__ void dma_step_narrow(const LinearArgs& a, int64_t m0,
   }
 }
 
+template <int TM>
 __global__ __launch_bounds__(kGemmThreads) void linear_narrow_k(const LinearArgs a) {
-  __shared__ u32x4 xs[2][kNarrowChunks];
+  constexpr int FI = TM / 32;
+  __shared__ u32x4 xs[2][TM * kRowChunks];
   __shared__ u32x4 ws[2][kTileChunks];
-  const Work wk = work_of<kNarrowM>(a);
+  const Work wk = work_of<TM>(a);
   const int lane = threadIdx.x & (kWave - 1), wave = wave_in_block();
   const int half = lane >> 5, r32 = lane & 31;
-  f32x16 acc;
+  f32x16 acc[FI];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  for (int i = 0; i < FI; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+  }
   const int steps = (wk.k_end - wk.k_begin) / kTileK;
-  dma_step_narrow(a, wk.m0, wk.n0, wk.k_begin, xs[0], ws[0], wave, lane);
+  dma_step_narrow<TM>(a, wk.m0, wk.n0, wk.k_begin, xs[0], ws[0], wave, lane);
   for (int t = 0; t < steps; ++t) {
     const int buf = t & 1;
     wait_loads_and_barrier<0>();  // this step's tiles are in LDS; every wave is done with the other buffer
     if (t + 1 < steps) {
-      dma_step_narrow(a, wk.m0, wk.n0, wk.k_begin + (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
+      dma_step_narrow<TM>(a, wk.m0, wk.n0, wk.k_begin + (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
     }
-    bf16x8 fa[4], fb[4];
+    bf16x8 fa[4][FI], fb[4];
 #pragma unroll
     for (int kk = 0; kk < kTileK / 16; ++kk) {
-      fa[kk] = as_bf16x8(xs[buf][slot(r32, 2 * kk + half)]);
+#pragma unroll
+      for (int i = 0; i < FI; ++i) fa[kk][i] = as_bf16x8(xs[buf][slot(32 * i + r32, 2 * kk + half)]);
       fb[kk] = as_bf16x8(ws[buf][slot(32 * wave + r32, 2 * kk + half)]);
     }
 #pragma unroll
-    for (int kk = 0; kk < kTileK / 16; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk], fb[kk], acc, 0, 0, 0);
+    for (int kk = 0; kk < kTileK / 16; ++kk) {
+#pragma unroll
+      for (int i = 0; i < FI; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk][i], fb[kk], acc[i], 0, 0, 0);
+    }
   }
-  // acc[r]: row 8 (r / 4) + 4 half + r % 4 of the tile, column 32 wave + r32
+  // acc[i][r]: row 32 i + 8 (r / 4) + 4 half + r % 4 of the tile, column
+  // 32 wave + r32
   const bool split = a.part != nullptr;
   float* out = split ? a.part + static_cast<int64_t>(wk.split) * a.m * a.n : a.y;
   const int64_t col = wk.n0 + 32 * wave + r32;
@@ -450,18 +463,21 @@ __global__ __launch_bounds__(kGemmThreads) void linear_narrow_k(const LinearArgs
   const bool add = !split && a.bias != nullptr;
   const bool accumulate = !split && a.accumulate;
   const float bv = add ? a.bias[col] : 0.0f;
-  const int64_t row0 = wk.m0 + 4 * half;
-  float* const o = out + row0 * a.n + col;
-  auto live = [&](int r) { return row0 + 8 * (r / 4) + (r % 4) < a.m; };
-  auto off = [&](int r) { return static_cast<int64_t>(8 * (r / 4) + (r % 4)) * a.n; };
-  float base[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) base[r] = accumulate && live(r) ? o[off(r)] : 0.0f;
+  for (int i = 0; i < FI; ++i) {
+    const int64_t row0 = wk.m0 + 32 * i + 4 * half;
+    float* const o = out + row0 * a.n + col;
+    auto live = [&](int r) { return row0 + 8 * (r / 4) + (r % 4) < a.m; };
+    auto off = [&](int r) { return static_cast<int64_t>(8 * (r / 4) + (r % 4)) * a.n; };
+    float base[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    if (live(r)) {
-      const float v = add ? acc[r] + bv : acc[r];
-      o[off(r)] = accumulate ? base[r] + v : v;
+    for (int r = 0; r < 16; ++r) base[r] = accumulate && live(r) ? o[off(r)] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (live(r)) {
+        const float v = add ? acc[i][r] + bv : acc[i][r];
+        o[off(r)] = accumulate ? base[r] + v : v;
+      }
     }
   }
 }
@@ -486,6 +502,9 @@ __global__ __launch_bounds__(kBlock) void round_bf16_k(const float* __restrict__
 // k 1024 loses 20-30% split 3-4 ways).
 constexpr int64_t kNarrowRows = 512;
 constexpr int64_t kNarrowSplitBelow = 256;
+// Products of more rows whose 128 x 128 tiles are fewer than this, and that
+// would not split k, take 64 x 128 tiles (twice the workgroups).
+constexpr int64_t kMediumTilesBelow = 256;
 
 }  // namespace
 
@@ -513,12 +532,17 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
   UOCR_REQUIRE(k >= 1 && k < (int64_t{1} << 30), what, "k must be in [1, 2^30)");
   UOCR_REQUIRE(x != nullptr && w != nullptr && y != nullptr, what, "null x, w or y");
   const bool ragged = k % 8 != 0 || !aligned16(x) || !aligned16(w);
-  const bool narrow = !ragged && !f32x && k % kTileK == 0 && m <= kNarrowRows;
-  const int64_t tile_rows = narrow ? kNarrowM : kTileM;
+  const bool dma = !ragged && !f32x && k % kTileK == 0;
+  const int64_t tiles128 = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
+  const bool narrow = dma && m <= kNarrowRows;
+  // 64-row tiles where the 128-row ones are too few and would not be split
+  const bool medium = dma && !narrow && tiles128 < kMediumTilesBelow &&
+                      (workspace == nullptr || splits_for(m, k, n) == 1);
+  const int64_t tile_rows = narrow ? kNarrowM : medium ? 2 * kNarrowM : kTileM;
   const int64_t tiles_m = (m + tile_rows - 1) / tile_rows, tiles_n = (n + kTileN - 1) / kTileN;
   UOCR_REQUIRE(tiles_m * tiles_n < (int64_t{1} << 31), what, "too many tiles");
   // split k into the workspace when it holds the partial products
-  int64_t splits = workspace != nullptr ? splits_for(m, k, n, narrow) : 1;
+  int64_t splits = workspace != nullptr && !medium ? splits_for(m, k, n, narrow) : 1;
   if (splits > 1 && workspace_floats < splits * m * n) splits = 1;
   const int64_t k_len = splits > 1 ? (k / splits + kTileK - 1) / kTileK * kTileK : k;
   splits = (k + k_len - 1) / k_len;
@@ -547,7 +571,9 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
   } else if (f32x) {
     linear_staged_k<true, false><<<grid, kGemmThreads, 0, st>>>(a);
   } else if (narrow) {
-    linear_narrow_k<<<grid, kGemmThreads, 0, st>>>(a);
+    linear_narrow_k<kNarrowM><<<grid, kGemmThreads, 0, st>>>(a);
+  } else if (medium) {
+    linear_narrow_k<2 * kNarrowM><<<grid, kGemmThreads, 0, st>>>(a);
   } else if (k % kTileK == 0) {
     linear_dma_k<<<grid, kGemmThreads, 0, st>>>(a);
   } else {

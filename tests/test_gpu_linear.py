@@ -75,7 +75,7 @@ def test_linear_model_shapes(backend, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(37, 200, 70), (300, 1280, 520), (129, 64, 257), (1, 128, 33), (64, 6848, 96),
-                                   (40, 108, 16)])
+                                   (40, 108, 16), (1000, 640, 384), (2048, 768, 384), (513, 128, 4096)])
 def test_linear_bf16_x_is_linear_on_the_rounded_rows(backend, m, k, n):
     """x already bf16 (k a multiple of 64: tiles loaded straight into LDS;
     otherwise staged): the same sums as linear on the fp32 rows."""
