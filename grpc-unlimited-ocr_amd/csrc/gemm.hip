@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kGemmThreads) void linear_dma_k(const LinearArgs a)
 }
 
 // Products of few rows (CLIP's 257, a short prompt), or of too few 128-row
-// tiles to give every CU one: TM x 128 tiles with TM 32 or 64, so that a
+// tiles to give every CU two: TM x 128 tiles with TM 32 or 64, so that a
 // 257-row product has 9 row tiles instead of 3 (the last of them holding
 // one row), and a [4096, 768] output 384 tiles instead of 192. Wave w of 4
 // owns columns 32 w .. 32 w + 31 of the tile, TM / 32
@@ -502,9 +502,11 @@ __global__ __launch_bounds__(kBlock) void round_bf16_k(const float* __restrict__
 // k 1024 loses 20-30% split 3-4 ways).
 constexpr int64_t kNarrowRows = 512;
 constexpr int64_t kNarrowSplitBelow = 256;
-// Products of more rows whose 128 x 128 tiles are fewer than this, and that
-// would not split k, take 64 x 128 tiles (twice the workgroups).
-constexpr int64_t kMediumTilesBelow = 256;
+// Products of more rows whose 128 x 128 tiles are fewer than this (two
+// workgroups per CU), and that would not split k, take 64 x 128 tiles:
+// twice the workgroups, a shorter tail (the decoder's [4096 <- 1280] -> 1280,
+// 320 tiles: 35.7 -> 32.2 us).
+constexpr int64_t kMediumTilesBelow = 512;
 
 }  // namespace
 
