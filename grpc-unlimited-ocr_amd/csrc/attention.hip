@@ -367,6 +367,179 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   }
 }
 
+// ---- few query rows: the keys split over the waves ---------------------------
+//
+// With few query rows (CLIP: 16 heads x 257 rows are 48 workgroups of 128
+// rows for 256 CUs) one wave's walk over every key tile is the whole call's
+// critical path. Here the 4 waves of a workgroup take the same 32 query rows
+// and every fourth key tile each: its own K and V tiles, straight from
+// memory into its own LDS region (two stages; K rows' 16-byte chunks
+// swizzled by the row so that the S^T reads of 16 rows cover 16 bank
+// groups), the same products and online softmax as attention_k, and at the
+// end the four (max, total, values) records of each row are combined
+// through LDS in wave order. No bias; head dim 64.
+constexpr int kSplitWaves = 4;
+constexpr int kSplitHd = 64;
+constexpr int kSplitTileFloats = kKeyTile * kSplitHd;                     // one operand tile, unpadded
+constexpr size_t kSplitLds = sizeof(float) * kSplitWaves * 2 * 2 * kSplitTileFloats;  // 128 KB
+
+__global__ __launch_bounds__(64 * kSplitWaves) void attention_keysplit_k(const AttnArgs a) {
+  constexpr int HD = kSplitHd, kHalf = HD / 2, kDBlocks = HD / 32;
+  constexpr int kRowChunks = HD / 4;                                  // 16-byte chunks per K or V row
+  constexpr int kLoads = kSplitTileFloats / 4 / kWave;                // memory-to-LDS loads per operand tile
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, c = lane & 31;
+  const int64_t slice = blockIdx.y;
+  const int qrow = blockIdx.x * kQueriesPerWave + c;
+  const bool qin = qrow < a.rows;
+  const float* qb = a.q + slice * a.sq;
+  const float* kb = a.k + slice * a.sk;
+  const float* vb = a.v + slice * a.sv;
+  float* const mine = lds + wave * 2 * 2 * kSplitTileFloats;  // [stage][K | V]
+  const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
+
+  // tile t into stage st: lane l of load i writes LDS chunk i * 64 + l
+  auto stage_tile = [&](int t, int st) {
+    float* ks = mine + st * 2 * kSplitTileFloats;
+    float* vs = ks + kSplitTileFloats;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int sl = i * kWave + lane, row = sl / kRowChunks, cj = sl % kRowChunks;
+      const int key = t * kKeyTile + row < a.keys ? t * kKeyTile + row : a.keys - 1;  // past the end: a valid row
+      __builtin_amdgcn_global_load_lds(kb + static_cast<int64_t>(key) * a.ldk + 4 * (cj ^ (row & 15)),
+                                       ks + i * kWave * 4, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vb + static_cast<int64_t>(key) * a.ldv + 4 * cj, vs + i * kWave * 4, 16, 0,
+                                       0);
+    }
+  };
+
+  float qv[kHalf];
+#pragma unroll
+  for (int i = 0; i < kHalf; i += 4) {
+    float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (qin) t = *reinterpret_cast<const float4*>(qb + qrow * a.ldq + hl * kHalf + i);
+    qv[i] = t.x;
+    qv[i + 1] = t.y;
+    qv[i + 2] = t.z;
+    qv[i + 3] = t.w;
+  }
+  f32x16 o[kDBlocks];
+#pragma unroll
+  for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] = 0.0f;
+  }
+  float m = -INFINITY, l = 0.0f;
+  if (wave < tiles) stage_tile(wave, 0);
+  for (int t = wave, n = 0; t < tiles; t += kSplitWaves, ++n) {
+    const int st = n & 1;
+    const bool more = t + kSplitWaves < tiles;
+    if (more) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the other stage are done
+      stage_tile(t + kSplitWaves, st ^ 1);
+      __builtin_amdgcn_s_waitcnt(((2 * kLoads) & 0xF) | ((((2 * kLoads) >> 4) & 3) << 14) | (7 << 4) | (0xF << 8));
+    } else {
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (0xF << 8));  // vmcnt(0)
+    }
+    const float* ks = mine + st * 2 * kSplitTileFloats;
+    const float* vs = ks + kSplitTileFloats;
+    const int key0 = t * kKeyTile;
+    f32x16 sacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kHalf; i += 4) {
+      const float4 kk = *reinterpret_cast<const float4*>(ks + c * HD + 4 * ((hl * (kHalf / 4) + i / 4) ^ (c & 15)));
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.x, qv[i], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.y, qv[i + 1], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.z, qv[i + 2], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.w, qv[i + 3], sacc, 0, 0, 0);
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = key0 + 8 * (r / 4) + 4 * hl + (r % 4);
+      const float x = key < a.keys ? sacc[r] * a.scale : -INFINITY;
+      sacc[r] = x;
+      tmax = fmaxf(tmax, x);
+    }
+    tmax = fmaxf(tmax, partner(tmax));
+    const float m_new = fmaxf(m, tmax);
+    const bool dead = m_new == -INFINITY;
+    const float corr = dead ? 1.0f : __builtin_amdgcn_exp2f((m - m_new) * kLog2e);
+    float psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = dead ? 0.0f : __builtin_amdgcn_exp2f((sacc[r] - m_new) * kLog2e);
+      psum += sacc[r];
+    }
+    psum += partner(psum);
+    l = l * corr + psum;
+    m = m_new;
+    if (__ballot(corr != 1.0f) != 0) {
+#pragma unroll
+      for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[b][r] *= corr;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = 8 * (i / 4) + 4 * hl + (i % 4);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * HD + 32 * b + c], sacc[i], o[b], 0, 0, 0);
+      }
+    }
+  }
+
+  // the four records of each row through LDS: values [wave][row][HD], then
+  // max and total [wave][row]
+  __syncthreads();
+  float* vals = lds;
+  float* mx = lds + kSplitWaves * kQueriesPerWave * HD;
+  float* tot = mx + kSplitWaves * kQueriesPerWave;
+#pragma unroll
+  for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      vals[(wave * kQueriesPerWave + c) * HD + 32 * b + 8 * (r / 4) + 4 * hl + (r % 4)] = o[b][r];
+    }
+  }
+  if (hl == 0) {
+    mx[wave * kQueriesPerWave + c] = m;
+    tot[wave * kQueriesPerWave + c] = l;
+  }
+  __syncthreads();
+  // thread: row threadIdx.x / 8, columns 8 (threadIdx.x % 8) .. + 7
+  const int row = static_cast<int>(threadIdx.x) / 8, d0 = 8 * (static_cast<int>(threadIdx.x) % 8);
+  const int orow = blockIdx.x * kQueriesPerWave + row;
+  if (orow >= a.rows) return;
+  float big = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kSplitWaves; ++w) big = fmaxf(big, mx[w * kQueriesPerWave + row]);
+  float e[kSplitWaves], total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kSplitWaves; ++w) {
+    const float mw = mx[w * kQueriesPerWave + row];
+    e[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((mw - big) * kLog2e);
+    total += e[w] * tot[w * kQueriesPerWave + row];
+  }
+  const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kSplitWaves; ++w) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += e[w] * vals[(w * kQueriesPerWave + row) * HD + d0 + j];
+  }
+  float* op = a.out + slice * a.so + static_cast<int64_t>(orow) * a.ldo + d0;
+  *reinterpret_cast<float4*>(op) = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<float4*>(op + 4) = make_float4(acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv);
+}
+
 // The relative-position dot products of every (slice, query row) into
 // table [slices][rows][dots_ld] (height terms at 0, width terms at dw_off):
 // block (j, s) takes table slice j of slice s (rh[qy = j] for j < h, else
@@ -561,6 +734,15 @@ int uocr_rocm_attention(void* stream, const float* q, int64_t ldq, int64_t sq, c
   UOCR_REQUIRE(mask == nullptr || mask_ld >= keys, kWhat, "mask rows must hold every key");
   AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
              scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr};
+  if (mask == nullptr && hd == kSplitHd && slices * ((rows + 127) / 128) < 256) {
+    // few query rows: the keys split over a workgroup's waves
+    const dim3 grid(static_cast<unsigned>((rows + kQueriesPerWave - 1) / kQueriesPerWave),
+                    static_cast<unsigned>(slices));
+    clear_launch_error();
+    allow_lds(attention_keysplit_k, kSplitLds);
+    attention_keysplit_k<<<grid, 64 * kSplitWaves, kSplitLds, as_stream(stream)>>>(a);
+    return check_launch(kWhat);
+  }
   return mask != nullptr ? launch<Bias::kMask>(kWhat, stream, hd, slices, a)
                          : launch<Bias::kNone>(kWhat, stream, hd, slices, a);
 }

@@ -4,7 +4,8 @@ src/backend/reference/ops.cpp:219-251: dot(q, k) * scale + bias, softmax
 with an fp64 total, probabilities times v) slice by slice:
 
   * no bias, hd 64 and 128, rows and keys not multiples of the 32-key tile
-    or the 128-row workgroup, several slices, head-major operands;
+    or the 128-row workgroup, several slices, head-major operands (few rows:
+    the keys split over a workgroup's waves);
   * a mask shared by the slices with -inf entries, a causal pattern and a
     row with every key masked (zeros out), rows != keys;
   * strided operands as the decoder's prefill holds them (q, k, v columns of
@@ -41,8 +42,13 @@ def reference(q, k, v, scale, bias=None):
 
 
 @pytest.mark.parametrize("slices,rows,keys,hd", [(1, 1, 1, 64), (3, 31, 33, 64), (2, 257, 257, 64),
-                                                 (2, 130, 1000, 128), (1, 1024, 1024, 64), (16, 65, 65, 64)])
+                                                 (2, 130, 1000, 128), (1, 1024, 1024, 64), (16, 65, 65, 64),
+                                                 (16, 257, 257, 64), (1, 40, 100, 64), (260, 70, 90, 64)])
 def test_attention_against_the_oracle(backend, slices, rows, keys, hd):
+    """Head dim 64 without a mask and fewer than 256 workgroups of 128 rows
+    split the keys over a workgroup's waves (CLIP's 16 x 257; fewer key
+    tiles than waves: 40 x 100); 260 slices take the one-wave-per-32-rows
+    kernel."""
     q, k, v = normal(700 + rows, (slices, rows, hd)), normal(701 + keys, (slices, keys, hd)), normal(702, (slices, keys, hd))
     scale = float(np.float32(1 / np.sqrt(hd)))
     want = reference(q, k, v, scale)
