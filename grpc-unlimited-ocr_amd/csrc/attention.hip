@@ -276,6 +276,22 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
         ky0 = key0 / a.w;  // once per tile; the lane's keys step from here
         kx0 = key0 - ky0 * a.w;
       }
+      // kRelPos: the grid position of the first key of each of this lane's
+      // four groups of 4 consecutive keys (8 g + 4 h), each key then at most
+      // one row further once the grid is at least 4 wide
+      int gky[kBias == Bias::kRelPos ? 4 : 1], gkx[kBias == Bias::kRelPos ? 4 : 1];
+      if constexpr (kBias == Bias::kRelPos) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          int ky = ky0, kx = kx0 + 8 * g + 4 * hl;
+          while (kx >= a.w) {
+            kx -= a.w;
+            ++ky;
+          }
+          gky[g] = ky;
+          gkx[g] = kx;
+        }
+      }
       // kRelPosRows: the tile's height term, and the width terms of this
       // lane's keys kx0 + 8 g + 4 h + (0..3)
       float dh = 0.0f, dwv[kBias == Bias::kRelPosRows ? 16 : 1];
@@ -297,8 +313,8 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
         if constexpr (kBias == Bias::kMask) {
           x = x + mk[r];
         } else if constexpr (kBias == Bias::kRelPos) {
-          int ky = ky0, kx = kx0 + off;
-          while (kx >= a.w) {
+          int ky = gky[r / 4], kx = gkx[r / 4] + r % 4;
+          while (kx >= a.w) {  // at most once for a grid 4 or more wide
             kx -= a.w;
             ++ky;
           }
