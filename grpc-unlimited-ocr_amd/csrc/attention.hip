@@ -767,8 +767,8 @@ int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64
                                 int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo,
                                 int64_t so, int64_t slices, int64_t h, int64_t w, int64_t hd, float scale,
                                 const float* rh, const float* rw) {
-  return rel_pos_entry("uocr_rocm_attention_rel_pos", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, h, w, hd, scale, rh,
-                       rw, nullptr, 0);
+  return rel_pos_entry("uocr_rocm_attention_rel_pos", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices,
+                       h, w, hd, scale, rh, rw, nullptr, 0);
 }
 
 int64_t uocr_rocm_attention_rel_pos_workspace_floats(int64_t slices, int64_t h, int64_t w) {
