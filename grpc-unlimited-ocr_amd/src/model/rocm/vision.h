@@ -126,6 +126,9 @@ struct View {
   std::int64_t size = 0;
 };
 
+// Calls are ordered on the context's stream and share the encoder's caches
+// and scratch: one thread at a time per encoder (an encoder per stream for
+// concurrent views).
 class VisionEncoder {
  public:
   // Shapes are checked here (std::invalid_argument); every device pointer

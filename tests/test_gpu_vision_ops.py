@@ -204,3 +204,19 @@ def test_layer_norm_into_bf16_rejects_rows_too_wide(backend):
     y = torch.empty(1, 16385, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError):
         backend.layer_norm_to_bf16(x, w, w, y, 1e-6)
+
+
+def test_fused_producers_take_empty_inputs_and_refuse_bad_ones(backend):
+    """n = 0 / rows = 0 are no-ops; null pointers are refused before any
+    launch."""
+    x = torch.zeros(0, device="cuda")
+    y = torch.zeros(0, dtype=torch.bfloat16, device="cuda")
+    backend.act_to_bf16(x, y)
+    backend.act_to_bf16(x, y, quick=True)
+    w = torch.ones(8, device="cuda")
+    backend.layer_norm_to_bf16(torch.zeros(0, 8, device="cuda"), w, w, torch.zeros(0, 8, dtype=torch.bfloat16,
+                                                                                    device="cuda"), 1e-6)
+    lib = backend.lib()
+    assert lib.uocr_rocm_gelu_erf_to_bf16(None, None, None, 4) != 0
+    assert lib.uocr_rocm_layer_norm_to_bf16(None, None, None, None, None, 2, 8, 1e-6) != 0
+    assert lib.uocr_rocm_linear_bf16x_add_ws(None, None, 2, 8, None, 4, None, None, None, 0) != 0
