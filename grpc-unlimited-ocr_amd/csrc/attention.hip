@@ -51,9 +51,17 @@ constexpr float kLog2e = 1.4426950408889634f;
 // multiple of the 32-key tile, so a tile's keys are 32 consecutive columns
 // of one grid row: one height term per tile and the width terms as 4-wide
 // vector reads, where kRelPos looks both up per key.
-enum class Bias { kNone, kMask, kRelPos, kRelPosRows };
+// kRelPosTable: kRelPosRows with the per-query dot products read from the
+// table rel_dots_k formed in memory rather than copied into LDS (4 waves a
+// workgroup: no LDS for them).
+enum class Bias { kNone, kMask, kRelPos, kRelPosRows, kRelPosTable };
 template <Bias kBias>
 constexpr bool rel_pos() {
+  return kBias == Bias::kRelPos || kBias == Bias::kRelPosRows || kBias == Bias::kRelPosTable;
+}
+// the per-query dot products held in LDS
+template <Bias kBias>
+constexpr bool dots_in_lds() {
   return kBias == Bias::kRelPos || kBias == Bias::kRelPosRows;
 }
 constexpr int kQueriesPerWave = 32;
@@ -172,7 +180,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   }
 
   float* my_dots = dots + (wave * kQueriesPerWave + c) * a.dots_ld;
-  if constexpr (rel_pos<kBias>()) {
+  if constexpr (dots_in_lds<kBias>()) {
     if (a.table != nullptr) {
       // the workgroup's rows of the table lie contiguous in memory with the
       // LDS row stride: one coalesced copy by every thread
@@ -189,7 +197,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
       }
     }
   }
-  if constexpr (rel_pos<kBias>()) {
+  if constexpr (dots_in_lds<kBias>()) {
     if (a.table == nullptr) {
     // dh[ky] = q . rh[qy, ky] and dw[kx] = q . rw[qx, kx]: each lane forms
     // the partial dot over the half of the columns it holds in qv (fp32 in
@@ -294,12 +302,17 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
       }
       // kRelPosRows: the tile's height term, and the width terms of this
       // lane's keys kx0 + 8 g + 4 h + (0..3)
-      float dh = 0.0f, dwv[kBias == Bias::kRelPosRows ? 16 : 1];
-      if constexpr (kBias == Bias::kRelPosRows) {
-        dh = my_dots[ky0];
+      constexpr bool kRowTerms = kBias == Bias::kRelPosRows || kBias == Bias::kRelPosTable;
+      float dh = 0.0f, dwv[kRowTerms ? 16 : 1];
+      if constexpr (kRowTerms) {
+        // kRelPosTable: the query's row of the table in memory
+        const float* trow = kBias == Bias::kRelPosTable
+                                ? a.table + (slice * a.rows + (qin ? qrow : 0)) * static_cast<int64_t>(a.dots_ld)
+                                : my_dots;
+        dh = trow[ky0];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const float4 t = *reinterpret_cast<const float4*>(my_dots + a.dw_off + kx0 + 8 * g + 4 * hl);
+          const float4 t = *reinterpret_cast<const float4*>(trow + a.dw_off + kx0 + 8 * g + 4 * hl);
           dwv[4 * g] = t.x;
           dwv[4 * g + 1] = t.y;
           dwv[4 * g + 2] = t.z;
@@ -319,7 +332,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
             ++ky;
           }
           if (key < a.keys) x = x + (my_dots[ky] + my_dots[a.dw_off + kx]);
-        } else if constexpr (kBias == Bias::kRelPosRows) {
+        } else if constexpr (kRowTerms) {
           x = x + (dh + dwv[r]);
         }
         x = key < a.keys ? x : -INFINITY;
@@ -653,7 +666,7 @@ int launch(const char* what, void* stream, int64_t hd, int64_t slices, const Att
   constexpr int kThreads = 64 * waves_of<kBias>(), kQueriesPerBlock = waves_of<kBias>() * kQueriesPerWave;
   const dim3 grid(static_cast<unsigned>((a.rows + kQueriesPerBlock - 1) / kQueriesPerBlock),
                   static_cast<unsigned>(slices));
-  const size_t dyn = rel_pos<kBias>() ? sizeof(float) * kQueriesPerBlock * static_cast<size_t>(a.dots_ld) : 0;
+  const size_t dyn = dots_in_lds<kBias>() ? sizeof(float) * kQueriesPerBlock * static_cast<size_t>(a.dots_ld) : 0;
   clear_launch_error();
   if (hd == 64) {
     allow_lds(attention_k<64, kBias>, dyn);
@@ -728,6 +741,7 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
     }
     if (const int st = check_launch(what)) return st;
   }
+  if (lay.tile_rows && table) return launch<Bias::kRelPosTable>(what, stream, hd, slices, a);
   return lay.tile_rows ? launch<Bias::kRelPosRows>(what, stream, hd, slices, a)
                        : launch<Bias::kRelPos>(what, stream, hd, slices, a);
 }
