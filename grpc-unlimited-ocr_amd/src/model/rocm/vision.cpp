@@ -342,14 +342,23 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::
     // one pass on the matrix cores: scores, bias, softmax and values per
     // (head, window) slice without the scores reaching memory
     const std::int64_t slices = heads * windows, part = heads * rows * hd;
-    Array split = f32(ctx_, 3 * part), o = f32(ctx_, part);
-    split_heads(ctx_, qkv.f32(), rows, 3, heads, hd, split.f32());
-    const float* q = split.f32();
     const std::int64_t dots = attention_rel_pos_workspace_floats(slices, h, w);
     Array table = f32(ctx_, dots);  // the bias's dot products, formed once per slice
-    attention_rel_pos(ctx_, {q, hd, n * hd}, {q + part, hd, n * hd}, {q + 2 * part, hd, n * hd}, o.f32(), hd, n * hd,
-                      slices, h, w, hd, scale, rh.f32(), rw.f32(), table.f32(), dots);
-    merge_heads(ctx_, o.f32(), heads, rows, hd, merged.f32());
+    if (windows == 1) {
+      // one window (a global block): the heads straight from the projection's
+      // rows into their columns of the output
+      const float* q = qkv.f32();
+      attention_rel_pos(ctx_, {q, 3 * c, hd}, {q + c, 3 * c, hd}, {q + 2 * c, 3 * c, hd}, merged.f32(), c, hd, slices,
+                        h, w, hd, scale, rh.f32(), rw.f32(), table.f32(), dots);
+    } else {
+      // windows: head-major copies, so that every (head, window) is one slice
+      Array split = f32(ctx_, 3 * part), o = f32(ctx_, part);
+      split_heads(ctx_, qkv.f32(), rows, 3, heads, hd, split.f32());
+      const float* q = split.f32();
+      attention_rel_pos(ctx_, {q, hd, n * hd}, {q + part, hd, n * hd}, {q + 2 * part, hd, n * hd}, o.f32(), hd,
+                        n * hd, slices, h, w, hd, scale, rh.f32(), rw.f32(), table.f32(), dots);
+      merge_heads(ctx_, o.f32(), heads, rows, hd, merged.f32());
+    }
   } else if (hd % 4 == 0) {
     const std::int64_t slices = heads * windows, part = heads * rows * hd;
     Array split = f32(ctx_, 3 * part), o = f32(ctx_, part), scores = f32(ctx_, slices * n * n);
