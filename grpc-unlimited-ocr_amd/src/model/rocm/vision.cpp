@@ -391,6 +391,27 @@ void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const
     // a global block: the norm's only reader is the qkv projection, and the
     // output projection adds straight into the residual stream
     sam_attention(index, nullptr, normed_b, 1, g, g, x.f32(), true);
+  } else if (!global_[index] && c % 2 == 0 && c <= 16384) {
+    // windows: the norm straight into bf16 rows (the rounding the qkv
+    // projection applies), gathered into the windows as pairs of bf16; the
+    // buffer's row past the grid is zero once and for all (the padding)
+    const std::int64_t win = dims_.sam.window;
+    const Windows& wi = windows(g);
+    const std::int64_t rows = wi.count * win * win;
+    auto it = win_normed_.find(g);
+    if (it == win_normed_.end()) {
+      it = win_normed_.emplace(g, Array(ctx_, DType::kBF16, (cells + 1) * c)).first;
+      it->second.zero();
+    }
+    const Array& nb = it->second;
+    layer_norm_to_bf16(ctx_, x.f32(), b.norm1_w, b.norm1_b, nb.bf16(), cells, c, kSamEps);
+    Array slots(ctx_, DType::kBF16, rows * c);
+    Array out = f32(ctx_, rows * c), attended = f32(ctx_, cells * c);
+    gather_rows(ctx_, reinterpret_cast<const float*>(nb.bf16()), wi.gather.i64(), rows, c / 2,
+                reinterpret_cast<float*>(slots.bf16()));
+    sam_attention(index, nullptr, slots.bf16(), wi.count, win, win, out.f32(), false);
+    gather_rows(ctx_, out.f32(), wi.scatter.i64(), cells, c, attended.f32());
+    add_inplace(ctx_, x.f32(), attended.f32(), cells * c);
   } else {
     Array attended = f32(ctx_, cells * c);
     Array normed = f32(ctx_, (cells + 1) * c);  // the extra zero row fills the windows' padding

@@ -199,6 +199,7 @@ class VisionEncoder {
   mutable std::map<std::tuple<std::size_t, bool, std::int64_t>, Array> rel_tables_;
   mutable std::map<std::int64_t, Windows> windows_;
   mutable Array split_ws_, x_bf16_;  // project()'s scratch, grown on demand
+  mutable std::map<std::int64_t, Array> win_normed_;  // per grid: bf16 norm rows + a zero row
 };
 
 // Host table resizes of the encoder (src/backend/reference/ops.cpp:42-86,
