@@ -161,6 +161,9 @@ _SIGNATURES = {
     "uocr_rocm_attention_rel_pos": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                      _i64, _i64, _i64, _f32, _vp, _vp], _int),
     "uocr_rocm_attention_rel_pos_workspace_floats": ([_i64, _i64, _i64], _i64),
+    "uocr_rocm_attention_rel_pos_windows_ws": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
+                                                _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
+                                                _vp, _vp, _i64], _int),
     "uocr_rocm_attention_rel_pos_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                         _i64, _i64, _i64, _f32, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_split_heads": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
@@ -646,6 +649,17 @@ def attention_rel_pos(q, k, v, out, slices, h, w, hd, scale, rh, rw, strides=Non
     else:
         _op("uocr_rocm_attention_rel_pos_ws", stream, *qo, *ko, *vo, *oo, slices, h, w, hd, scale, _ptr(rh),
             _ptr(rw), _ptr(workspace), workspace.numel())
+
+
+def attention_rel_pos_windows(qkv, out, heads, windows, h, w, hd, scale, rh, rw, workspace, stream=None):
+    """attention_rel_pos over heads x windows straight from a window-major
+    qkv projection [windows * h * w, 3 * heads * hd] into the merged rows out
+    [windows * h * w, heads * hd] (new)."""
+    width, n = heads * hd, h * w
+    base = _ptr(qkv)
+    _op("uocr_rocm_attention_rel_pos_windows_ws", stream, base, 3 * width, hd, n * 3 * width, base + 4 * width,
+        3 * width, hd, n * 3 * width, base + 8 * width, 3 * width, hd, n * 3 * width, _ptr(out), width, hd, n * width,
+        heads, windows, h, w, hd, scale, _ptr(rh), _ptr(rw), _ptr(workspace), workspace.numel())
 
 
 def attention_rel_pos_workspace_floats(slices, h, w):

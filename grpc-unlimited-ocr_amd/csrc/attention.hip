@@ -96,6 +96,10 @@ struct AttnArgs {
   // workgroup forms its own.
   const float* table;
   float* table_out;  // rel_dots_k's output (the same table)
+  // Slices in two levels: slice s is (s / inner, s % inner), its operands at
+  // (s / inner) * s_ + (s % inner) * i_ (inner 1: the single level)
+  int inner;
+  int64_t iq, ik, iv, io;
 };
 
 template <int HD, int kThreads>
@@ -137,6 +141,11 @@ __device__ __forceinline__ void store_tile(float* ks, float* vs, const float4 (&
 
 __device__ __forceinline__ float partner(float v) { return __shfl_xor(v, 32); }
 
+// The offset of slice s of an operand with outer stride so and inner stride si.
+__device__ __forceinline__ int64_t slice_at(const AttnArgs& a, int64_t s, int64_t so, int64_t si) {
+  return a.inner == 1 ? s * so : (s / a.inner) * so + (s % a.inner) * si;
+}
+
 template <int HD, Bias kBias>
 __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const AttnArgs a) {
   constexpr int kThreads = 64 * waves_of<kBias>();
@@ -159,9 +168,9 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   const int q0 = blockIdx.x * kQueriesPerBlock + wave * kQueriesPerWave;
   const int qrow = q0 + c;
   const bool qin = qrow < a.rows;
-  const float* qb = a.q + slice * a.sq;
-  const float* kb = a.k + slice * a.sk;
-  const float* vb = a.v + slice * a.sv;
+  const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
+  const float* kb = a.k + slice_at(a, slice, a.sk, a.ik);
+  const float* vb = a.v + slice_at(a, slice, a.sv, a.iv);
 
   // the first tile's loads go out first
   float4 kr[T::kPerThread], vr[T::kPerThread];
@@ -384,7 +393,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
 
   if (!qin) return;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  float* orow = a.out + slice * a.so + qrow * a.ldo;
+  float* orow = a.out + slice_at(a, slice, a.so, a.io) + qrow * a.ldo;
 #pragma unroll
   for (int b = 0; b < kDBlocks; ++b) {
 #pragma unroll
@@ -422,9 +431,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void attention_keysplit_k(const A
   const int64_t slice = blockIdx.y;
   const int qrow = blockIdx.x * kQueriesPerWave + c;
   const bool qin = qrow < a.rows;
-  const float* qb = a.q + slice * a.sq;
-  const float* kb = a.k + slice * a.sk;
-  const float* vb = a.v + slice * a.sv;
+  const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
+  const float* kb = a.k + slice_at(a, slice, a.sk, a.ik);
+  const float* vb = a.v + slice_at(a, slice, a.sv, a.iv);
   float* const mine = lds + wave * 2 * 2 * kSplitTileFloats;  // [stage][K | V]
   const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
 
@@ -564,7 +573,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void attention_keysplit_k(const A
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] += e[w] * vals[(w * kQueriesPerWave + row) * HD + d0 + j];
   }
-  float* op = a.out + slice * a.so + static_cast<int64_t>(orow) * a.ldo + d0;
+  float* op = a.out + slice_at(a, slice, a.so, a.io) + static_cast<int64_t>(orow) * a.ldo + d0;
   *reinterpret_cast<float4*>(op) = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
   *reinterpret_cast<float4*>(op + 4) = make_float4(acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv);
 }
@@ -590,7 +599,7 @@ __global__ __launch_bounds__(kBlock) void rel_dots_k(const AttnArgs a) {
   auto query = [&](int i) { return height ? j * a.w + i : i * a.w + (j - a.h); };
   float* qs = rel_lds;
   float* ts = rel_lds + nq * (HD + 1);
-  const float* qb = a.q + slice * a.sq;
+  const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
   for (int e = static_cast<int>(threadIdx.x); e < nq * HD; e += kBlock) {
     const int i = e / HD, d = e - i * HD;
     qs[i * (HD + 1) + d] = qb[static_cast<int64_t>(query(i)) * a.ldq + d];
@@ -711,10 +720,12 @@ DotsLayout dots_layout(int64_t h, int64_t w) {
   return {tile_rows, tile_rows ? 4 * quads : h + w + 1, dw_off};
 }
 
+// inner > 1: slice s = (s / inner, s % inner) with inner strides iq .. io.
 int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
                   int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo, int64_t so,
                   int64_t slices, int64_t h, int64_t w, int64_t hd, float scale, const float* rh, const float* rw,
-                  float* workspace, int64_t workspace_floats) {
+                  float* workspace, int64_t workspace_floats, int64_t inner = 1, int64_t iq = 0, int64_t ik = 0,
+                  int64_t iv = 0, int64_t io = 0) {
   UOCR_REQUIRE(h >= 1 && w >= 1 && h + w <= kMaxRelSpan, what, "need h, w >= 1 and h + w <= 256");
   const int64_t n = h * w;
   if (const int st = check_common(what, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, n, n, hd)) {
@@ -725,9 +736,13 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
   const DotsLayout lay = dots_layout(h, w);
   // the dot table goes to the workspace when it holds it (16-byte aligned)
   const bool table = workspace != nullptr && aligned16(workspace) && workspace_floats >= slices * n * lay.ld;
+  UOCR_REQUIRE(inner >= 1 && slices % inner == 0 && iq >= 0 && ik >= 0 && iv >= 0 && io >= 0 && iq % 4 == 0 &&
+                   ik % 4 == 0 && iv % 4 == 0 && io % 4 == 0,
+               what, "windows must divide the slices, window strides >= 0 in whole 16-byte chunks");
   AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(n), static_cast<int>(n),
              scale, nullptr, 0, rh, rw, static_cast<int>(h), static_cast<int>(w), static_cast<int>(lay.ld),
-             static_cast<int>(lay.dw_off), table ? workspace : nullptr, table ? workspace : nullptr};
+             static_cast<int>(lay.dw_off), table ? workspace : nullptr, table ? workspace : nullptr,
+             static_cast<int>(inner), iq, ik, iv, io};
   if (table) {
     const size_t lds = sizeof(float) * static_cast<size_t>((h + w) * (hd + 1));
     const dim3 grid(static_cast<unsigned>(h + w), static_cast<unsigned>(slices));
@@ -763,7 +778,7 @@ int uocr_rocm_attention(void* stream, const float* q, int64_t ldq, int64_t sq, c
   }
   UOCR_REQUIRE(mask == nullptr || mask_ld >= keys, kWhat, "mask rows must hold every key");
   AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
-             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr};
+             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 1, 0, 0, 0, 0};
   if (mask == nullptr && hd == kSplitHd && slices * ((rows + 127) / 128) < 256) {
     // few query rows: the keys split over a workgroup's waves
     const dim3 grid(static_cast<unsigned>((rows + kQueriesPerWave - 1) / kQueriesPerWave),
@@ -797,6 +812,18 @@ int uocr_rocm_attention_rel_pos_ws(void* stream, const float* q, int64_t ldq, in
                                    int64_t workspace_floats) {
   return rel_pos_entry("uocr_rocm_attention_rel_pos_ws", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so,
                        slices, h, w, hd, scale, rh, rw, workspace, workspace_floats);
+}
+
+int uocr_rocm_attention_rel_pos_windows_ws(void* stream, const float* q, int64_t ldq, int64_t sq, int64_t wq,
+                                           const float* k, int64_t ldk, int64_t sk, int64_t wk, const float* v,
+                                           int64_t ldv, int64_t sv, int64_t wv, float* out, int64_t ldo, int64_t so,
+                                           int64_t wo, int64_t heads, int64_t windows, int64_t h, int64_t w,
+                                           int64_t hd, float scale, const float* rh, const float* rw, float* workspace,
+                                           int64_t workspace_floats) {
+  constexpr const char* kWhat = "uocr_rocm_attention_rel_pos_windows_ws";
+  UOCR_REQUIRE(heads >= 1 && windows >= 1 && heads * windows < 65536, kWhat, "need heads, windows >= 1");
+  return rel_pos_entry(kWhat, stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, heads * windows, h, w, hd,
+                       scale, rh, rw, workspace, workspace_floats, windows, wq, wk, wv, wo);
 }
 
 }  // extern "C"

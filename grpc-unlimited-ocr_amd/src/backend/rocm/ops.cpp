@@ -217,6 +217,16 @@ std::int64_t attention_rel_pos_workspace_floats(std::int64_t slices, std::int64_
   return uocr_rocm_attention_rel_pos_workspace_floats(slices, h, w);
 }
 
+void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t wq, AttnOperand k, std::int64_t wk,
+                               AttnOperand v, std::int64_t wv, float* out, std::int64_t ldo, std::int64_t so,
+                               std::int64_t wo, std::int64_t heads, std::int64_t windows, std::int64_t h,
+                               std::int64_t w, std::int64_t hd, float scale, const float* rh, const float* rw,
+                               float* workspace, std::int64_t workspace_floats) {
+  check(uocr_rocm_attention_rel_pos_windows_ws(ctx.stream(), q.p, q.ld, q.slice, wq, k.p, k.ld, k.slice, wk, v.p, v.ld,
+                                               v.slice, wv, out, ldo, so, wo, heads, windows, h, w, hd, scale, rh, rw,
+                                               workspace, workspace_floats));
+}
+
 void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
                        std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
                        float scale, const float* rh, const float* rw, float* workspace, std::int64_t workspace_floats) {

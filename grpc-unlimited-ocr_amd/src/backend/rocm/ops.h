@@ -166,6 +166,13 @@ void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOpe
 // New: the same with the bias's dot products formed beforehand into a
 // workspace of attention_rel_pos_workspace_floats(slices, h, w) floats.
 std::int64_t attention_rel_pos_workspace_floats(std::int64_t slices, std::int64_t h, std::int64_t w);
+// New: over heads x windows slices, operand slice (head, window) at
+// p + head * slice + window * window_stride.
+void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t wq, AttnOperand k, std::int64_t wk,
+                               AttnOperand v, std::int64_t wv, float* out, std::int64_t ldo, std::int64_t so,
+                               std::int64_t wo, std::int64_t heads, std::int64_t windows, std::int64_t h,
+                               std::int64_t w, std::int64_t hd, float scale, const float* rh, const float* rw,
+                               float* workspace, std::int64_t workspace_floats);
 void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
                        std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
                        float scale, const float* rh, const float* rw, float* workspace, std::int64_t workspace_floats);

@@ -341,7 +341,7 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::
   if ((hd == 64 || hd == 128) && h + w <= 256) {
     // one pass on the matrix cores: scores, bias, softmax and values per
     // (head, window) slice without the scores reaching memory
-    const std::int64_t slices = heads * windows, part = heads * rows * hd;
+    const std::int64_t slices = heads * windows;
     const std::int64_t dots = attention_rel_pos_workspace_floats(slices, h, w);
     Array table = f32(ctx_, dots);  // the bias's dot products, formed once per slice
     if (windows == 1) {
@@ -351,13 +351,12 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::
       attention_rel_pos(ctx_, {q, 3 * c, hd}, {q + c, 3 * c, hd}, {q + 2 * c, 3 * c, hd}, merged.f32(), c, hd, slices,
                         h, w, hd, scale, rh.f32(), rw.f32(), table.f32(), dots);
     } else {
-      // windows: head-major copies, so that every (head, window) is one slice
-      Array split = f32(ctx_, 3 * part), o = f32(ctx_, part);
-      split_heads(ctx_, qkv.f32(), rows, 3, heads, hd, split.f32());
-      const float* q = split.f32();
-      attention_rel_pos(ctx_, {q, hd, n * hd}, {q + part, hd, n * hd}, {q + 2 * part, hd, n * hd}, o.f32(), hd,
-                        n * hd, slices, h, w, hd, scale, rh.f32(), rw.f32(), table.f32(), dots);
-      merge_heads(ctx_, o.f32(), heads, rows, hd, merged.f32());
+      // windows: slice (head, window) straight from the window-major qkv
+      // rows, into its rows and columns of the merged output
+      const float* q = qkv.f32();
+      attention_rel_pos_windows(ctx_, {q, 3 * c, hd}, n * 3 * c, {q + c, 3 * c, hd}, n * 3 * c, {q + 2 * c, 3 * c, hd},
+                                n * 3 * c, merged.f32(), c, hd, n * c, heads, windows, h, w, hd, scale, rh.f32(),
+                                rw.f32(), table.f32(), dots);
     }
   } else if (hd % 4 == 0) {
     const std::int64_t slices = heads * windows, part = heads * rows * hd;

@@ -465,6 +465,19 @@ UOCR_ROCM_API int uocr_rocm_attention_rel_pos(void* stream, const float* q, int6
  * holds uocr_rocm_attention_rel_pos_workspace_floats(slices, h, w) floats,
  * 16-byte aligned (a smaller one: the attention forms its own). */
 UOCR_ROCM_API int64_t uocr_rocm_attention_rel_pos_workspace_floats(int64_t slices, int64_t h, int64_t w);
+/* New: the same over heads x windows slices, slice (head, window) of each
+ * operand at base + head * s_ + window * w_ (row stride ld_): the heads
+ * and windows straight from a window-major qkv projection's rows [windows *
+ * h * w, 3 * width], the output into the merged rows, with no head-major
+ * copies. Window strides are multiples of 4 floats; the workspace as for
+ * uocr_rocm_attention_rel_pos_ws with slices = heads * windows. */
+UOCR_ROCM_API int uocr_rocm_attention_rel_pos_windows_ws(void* stream, const float* q, int64_t ldq, int64_t sq,
+                                                         int64_t wq, const float* k, int64_t ldk, int64_t sk,
+                                                         int64_t wk, const float* v, int64_t ldv, int64_t sv,
+                                                         int64_t wv, float* out, int64_t ldo, int64_t so, int64_t wo,
+                                                         int64_t heads, int64_t windows, int64_t h, int64_t w,
+                                                         int64_t hd, float scale, const float* rh, const float* rw,
+                                                         float* workspace, int64_t workspace_floats);
 UOCR_ROCM_API int uocr_rocm_attention_rel_pos_ws(void* stream, const float* q, int64_t ldq, int64_t sq,
                                                  const float* k, int64_t ldk, int64_t sk, const float* v, int64_t ldv,
                                                  int64_t sv, float* out, int64_t ldo, int64_t so, int64_t slices,

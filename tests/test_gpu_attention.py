@@ -134,3 +134,28 @@ def test_attention_rejects_bad_shapes(backend):
     y = torch.zeros(1, 8, 64, device="cuda")
     with pytest.raises(ValueError):
         backend.attention_rel_pos(y, y, y, y, 1, 200, 100, 64, 1.0, y, y)  # h + w above 256
+
+
+@pytest.mark.parametrize("windows,heads,h,w", [(3, 2, 14, 14), (2, 3, 5, 32)])
+def test_attention_rel_pos_windows_straight_from_the_rows(backend, windows, heads, h, w):
+    """Slice (head, window) read straight from a window-major qkv projection's
+    rows and written into the merged rows: against the oracle per (head,
+    window) at 1e-5."""
+    hd, n = 64, h * w
+    width = heads * hd
+    qkv = normal(740 + n, (windows * n, 3 * width))
+    rh, rw = normal(741, (h, h, hd)) * 0.3, normal(742, (w, w, hd)) * 0.3
+    scale = 0.125
+    want = np.zeros((windows * n, width), np.float32)
+    for win in range(windows):
+        rows = qkv[win * n:(win + 1) * n]
+        for head in range(heads):
+            q = rows[:, head * hd:(head + 1) * hd]
+            k = rows[:, width + head * hd:width + (head + 1) * hd]
+            v = rows[:, 2 * width + head * hd:2 * width + (head + 1) * hd]
+            want[win * n:(win + 1) * n, head * hd:(head + 1) * hd] = oracle.attention_head(
+                q, k, v, oracle.rel_pos_bias(q, h, w, rh, rw), scale)
+    out = torch.full((windows * n, width), float("nan"), device="cuda")
+    ws = torch.full((backend.attention_rel_pos_workspace_floats(heads * windows, h, w),), float("nan"), device="cuda")
+    backend.attention_rel_pos_windows(dev_f32(qkv), out, heads, windows, h, w, hd, scale, dev_f32(rh), dev_f32(rw), ws)
+    assert_f32_close(host_f32(out), want, 1e-5, f"rel-pos attention over {windows} windows x {heads} heads")
