@@ -147,6 +147,7 @@ _SIGNATURES = {
     "uocr_rocm_linear_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_linear_bf16x_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_linear_bf16x_add_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_linear_bf16x_add_rows": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_gemm_nt": ([_vp, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64],
                           _int),
     "uocr_rocm_gemm_nn": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64], _int),
@@ -518,6 +519,15 @@ def linear_add(x, w, y, workspace, bias=None, stream=None):
     m = x.numel() // k
     _op("uocr_rocm_linear_bf16x_add_ws", stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y),
         _ptr(workspace), workspace.numel())
+
+
+def linear_add_rows(x, w, y, y_row, bias=None, stream=None):
+    """y[y_row[r]] += (bf16 x . w^T + bias)[r], rows mapping to y.shape[0] or
+    more dropped (new: window slots added back into their grid rows)."""
+    n, k = w.shape
+    m = x.numel() // k
+    _op("uocr_rocm_linear_bf16x_add_rows", stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y), _ptr(y_row),
+        y.shape[0])
 
 
 def linear(x, w, y, bias=None, stream=None):

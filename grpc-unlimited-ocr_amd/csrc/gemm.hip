@@ -86,7 +86,35 @@ struct LinearArgs {
   // y += the product (+ bias): each element y + (sum + bias), as the
   // product followed by an in-place add
   bool accumulate;
+  // Non-null: product row r goes to y row row_map[r], dropped when that is
+  // y_rows or more (a scatter of window slots back into a grid); the
+  // TM x 128 kernels only, no split.
+  const int64_t* row_map;
+  int64_t y_rows;
 };
+
+// 16 elements of one output column, product rows row0 + 8 (r / 4) + r % 4
+// (r < 16), into y through the row map.
+__device__ __forceinline__ void store_mapped(const LinearArgs& a, int64_t row0, int64_t col, float bv, bool add,
+                                             const float (&val)[16]) {
+  int64_t at[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t row = row0 + 8 * (r / 4) + (r % 4);
+    const int64_t to = row < a.m ? a.row_map[row] : a.y_rows;
+    at[r] = to < a.y_rows ? to * a.n + col : -1;
+  }
+  float base[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) base[r] = a.accumulate && at[r] >= 0 ? a.y[at[r]] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    if (at[r] >= 0) {
+      const float v = add ? val[r] + bv : val[r];
+      a.y[at[r]] = a.accumulate ? base[r] + v : v;
+    }
+  }
+}
 
 // The tile, split and k range of this workgroup.
 struct Work {
@@ -466,6 +494,13 @@ __global__ __launch_bounds__(kGemmThreads) void linear_narrow_k(const LinearArgs
 #pragma unroll
   for (int i = 0; i < FI; ++i) {
     const int64_t row0 = wk.m0 + 32 * i + 4 * half;
+    if (a.row_map != nullptr) {
+      float val[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) val[r] = acc[i][r];
+      store_mapped(a, row0, col, bv, add, val);
+      continue;
+    }
     float* const o = out + row0 * a.n + col;
     auto live = [&](int r) { return row0 + 8 * (r / 4) + (r % 4) < a.m; };
     auto off = [&](int r) { return static_cast<int64_t>(8 * (r / 4) + (r % 4)) * a.n; };
@@ -528,7 +563,7 @@ int64_t splits_for(int64_t m, int64_t k, int64_t n, bool narrow = false) {
 
 int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64_t m, int64_t k, const uint16_t* w,
                  int64_t n, const float* bias, float* y, float* workspace = nullptr, int64_t workspace_floats = 0,
-                 bool accumulate = false) {
+                 bool accumulate = false, const int64_t* row_map = nullptr, int64_t y_rows = 0) {
   UOCR_REQUIRE(m >= 0 && n >= 0 && k >= 0, what, "m, n and k must be >= 0");
   if (m == 0 || n == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(k >= 1 && k < (int64_t{1} << 30), what, "k must be in [1, 2^30)");
@@ -538,13 +573,15 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
   const int64_t tiles128 = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
   const bool narrow = dma && m <= kNarrowRows;
   // 64-row tiles where the 128-row ones are too few and would not be split
-  const bool medium = dma && !narrow && tiles128 < kMediumTilesBelow &&
-                      (workspace == nullptr || splits_for(m, k, n) == 1);
+  // (and always with a row map)
+  const bool medium = dma && !narrow &&
+                      (row_map != nullptr ||
+                       (tiles128 < kMediumTilesBelow && (workspace == nullptr || splits_for(m, k, n) == 1)));
   const int64_t tile_rows = narrow ? kNarrowM : medium ? 2 * kNarrowM : kTileM;
   const int64_t tiles_m = (m + tile_rows - 1) / tile_rows, tiles_n = (n + kTileN - 1) / kTileN;
   UOCR_REQUIRE(tiles_m * tiles_n < (int64_t{1} << 31), what, "too many tiles");
   // split k into the workspace when it holds the partial products
-  int64_t splits = workspace != nullptr && !medium ? splits_for(m, k, n, narrow) : 1;
+  int64_t splits = workspace != nullptr && !medium && row_map == nullptr ? splits_for(m, k, n, narrow) : 1;
   if (splits > 1 && workspace_floats < splits * m * n) splits = 1;
   const int64_t k_len = splits > 1 ? (k / splits + kTileK - 1) / kTileK * kTileK : k;
   splits = (k + k_len - 1) / k_len;
@@ -560,7 +597,9 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
                static_cast<int>(tiles_n),
                static_cast<int>(k_len),
                splits > 1 ? workspace : nullptr,
-               accumulate};
+               accumulate,
+               row_map,
+               y_rows};
   const unsigned grid = static_cast<unsigned>(tiles_m * tiles_n * splits);
   clear_launch_error();
   const hipStream_t st = as_stream(stream);
@@ -639,6 +678,16 @@ int uocr_rocm_linear_bf16x_add_ws(void* stream, const uint16_t* x, int64_t m, in
                                   const float* bias, float* y, float* workspace, int64_t workspace_floats) {
   return linear_entry("uocr_rocm_linear_bf16x_add_ws", stream, x, false, m, k, w, n, bias, y, workspace,
                       workspace_floats, true);
+}
+
+int uocr_rocm_linear_bf16x_add_rows(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w,
+                                    int64_t n, const float* bias, float* y, const int64_t* y_row, int64_t y_rows) {
+  constexpr const char* kWhat = "uocr_rocm_linear_bf16x_add_rows";
+  UOCR_REQUIRE(y_row != nullptr || m == 0, kWhat, "null row map");
+  UOCR_REQUIRE(y_rows >= 0, kWhat, "y_rows must be >= 0");
+  UOCR_REQUIRE(k % kTileK == 0 && aligned16(x) && aligned16(w), kWhat,
+               "k must be a multiple of 64 and x, w 16-byte aligned");
+  return linear_entry(kWhat, stream, x, false, m, k, w, n, bias, y, nullptr, 0, true, y_row, y_rows);
 }
 
 int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst) {

@@ -265,6 +265,12 @@ void linear_bf16x_add(const Context& ctx, const std::uint16_t* x, std::int64_t m
   check(uocr_rocm_linear_bf16x_add_ws(ctx.stream(), x, m, k, w_bf16, n, bias, y, workspace, workspace_floats));
 }
 
+void linear_bf16x_add_rows(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
+                           const std::uint16_t* w_bf16, std::int64_t n, const float* bias, float* y,
+                           const std::int64_t* y_row, std::int64_t y_rows) {
+  check(uocr_rocm_linear_bf16x_add_rows(ctx.stream(), x, m, k, w_bf16, n, bias, y, y_row, y_rows));
+}
+
 void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint16_t* dst) {
   check(uocr_rocm_round_bf16(ctx.stream(), src, n, dst));
 }

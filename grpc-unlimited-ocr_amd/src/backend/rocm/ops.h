@@ -200,6 +200,10 @@ void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, 
 void linear_bf16x(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
                   const std::uint16_t* w_bf16, std::int64_t n, const float* bias, float* y, float* workspace,
                   std::int64_t workspace_floats);
+// New: y[y_row[r]] += (bf16(x) w^T + bias)[r] for y_row[r] < y_rows.
+void linear_bf16x_add_rows(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
+                           const std::uint16_t* w_bf16, std::int64_t n, const float* bias, float* y,
+                           const std::int64_t* y_row, std::int64_t y_rows);
 // New: y += bf16(x) w^T (+ bias), as linear_bf16x then add_inplace.
 void linear_bf16x_add(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
                       const std::uint16_t* w_bf16, std::int64_t n, const float* bias, float* y, float* workspace,

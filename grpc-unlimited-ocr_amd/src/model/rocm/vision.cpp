@@ -325,7 +325,8 @@ const std::uint16_t* VisionEncoder::activated_bf16(const float* x, std::int64_t 
 // relative-position bias + softmax, values); otherwise head by head over all
 // windows, as the reference does.
 void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::uint16_t* xb, std::int64_t windows,
-                                  std::int64_t h, std::int64_t w, float* out, bool accumulate) const {
+                                  std::int64_t h, std::int64_t w, float* out, bool accumulate,
+                                  const std::int64_t* out_rows, std::int64_t out_count) const {
   const auto& b = w_.sam_blocks[index];
   const std::int64_t c = dims_.sam.width, heads = dims_.sam.heads, hd = c / heads, n = h * w, rows = windows * n;
   Array qkv = f32(ctx_, rows * 3 * c);
@@ -377,6 +378,13 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::
               n * c, windows);
     }
   }
+  if (out_rows != nullptr) {
+    // window slots added straight back into their grid rows (padding dropped)
+    if (x_bf16_.count() < rows * c) x_bf16_ = Array(ctx_, DType::kBF16, rows * c);
+    round_bf16(ctx_, merged.f32(), rows * c, x_bf16_.bf16());
+    linear_bf16x_add_rows(ctx_, x_bf16_.bf16(), rows, c, b.proj, c, b.proj_b, out, out_rows, out_count);
+    return;
+  }
   project(merged.f32(), rows, c, b.proj, c, b.proj_b, out, accumulate);
 }
 
@@ -389,11 +397,12 @@ void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const
   if (normed_b != nullptr) {
     // a global block: the norm's only reader is the qkv projection, and the
     // output projection adds straight into the residual stream
-    sam_attention(index, nullptr, normed_b, 1, g, g, x.f32(), true);
-  } else if (!global_[index] && c % 2 == 0 && c <= 16384) {
-    // windows: the norm straight into bf16 rows (the rounding the qkv
-    // projection applies), gathered into the windows as pairs of bf16; the
-    // buffer's row past the grid is zero once and for all (the padding)
+    sam_attention(index, nullptr, normed_b, 1, g, g, x.f32(), true, nullptr, 0);
+  } else if (!global_[index] && c % 64 == 0 && c <= 16384) {
+    // windows (a width of whole 64-column steps): the norm straight into
+    // bf16 rows (the rounding the qkv projection applies), gathered into the
+    // windows as pairs of bf16; the buffer's row past the grid is zero once
+    // and for all (the padding)
     const std::int64_t win = dims_.sam.window;
     const Windows& wi = windows(g);
     const std::int64_t rows = wi.count * win * win;
@@ -405,12 +414,10 @@ void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const
     const Array& nb = it->second;
     layer_norm_to_bf16(ctx_, x.f32(), b.norm1_w, b.norm1_b, nb.bf16(), cells, c, kSamEps);
     Array slots(ctx_, DType::kBF16, rows * c);
-    Array out = f32(ctx_, rows * c), attended = f32(ctx_, cells * c);
     gather_rows(ctx_, reinterpret_cast<const float*>(nb.bf16()), wi.gather.i64(), rows, c / 2,
                 reinterpret_cast<float*>(slots.bf16()));
-    sam_attention(index, nullptr, slots.bf16(), wi.count, win, win, out.f32(), false);
-    gather_rows(ctx_, out.f32(), wi.scatter.i64(), cells, c, attended.f32());
-    add_inplace(ctx_, x.f32(), attended.f32(), cells * c);
+    // the output projection adds each slot back into its grid row of x
+    sam_attention(index, nullptr, slots.bf16(), wi.count, win, win, x.f32(), true, wi.gather.i64(), cells);
   } else {
     Array attended = f32(ctx_, cells * c);
     Array normed = f32(ctx_, (cells + 1) * c);  // the extra zero row fills the windows' padding
@@ -418,14 +425,14 @@ void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const
     copy(ctx_, normed.f32(), x.f32(), cells * c);
     layer_norm(ctx_, normed.f32(), b.norm1_w, b.norm1_b, cells, c, kSamEps);
     if (global_[index]) {
-      sam_attention(index, normed.f32(), nullptr, 1, g, g, attended.f32(), false);
+      sam_attention(index, normed.f32(), nullptr, 1, g, g, attended.f32(), false, nullptr, 0);
     } else {
       const std::int64_t win = dims_.sam.window;
       const Windows& wi = windows(g);
       const std::int64_t rows = wi.count * win * win;
       Array slots = f32(ctx_, rows * c), out = f32(ctx_, rows * c);
       gather_rows(ctx_, normed.f32(), wi.gather.i64(), rows, c, slots.f32());
-      sam_attention(index, slots.f32(), nullptr, wi.count, win, win, out.f32(), false);
+      sam_attention(index, slots.f32(), nullptr, wi.count, win, win, out.f32(), false, nullptr, 0);
       gather_rows(ctx_, out.f32(), wi.scatter.i64(), cells, c, attended.f32());
     }
     add_inplace(ctx_, x.f32(), attended.f32(), cells * c);

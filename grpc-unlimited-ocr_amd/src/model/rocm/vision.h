@@ -176,9 +176,11 @@ class VisionEncoder {
   void sam_forward(const float* image, std::int64_t size, Array& cells) const;
   void sam_block(std::size_t index, Array& x, std::int64_t g) const;
   // x fp32, or xb (non-null) the same rows already in bf16
-  // (accumulate: out += the output projection.)
+  // (accumulate: out += the output projection; out_rows non-null: row r of
+  // the projection added into out row out_rows[r], dropped at out_count.)
   void sam_attention(std::size_t index, const float* x, const std::uint16_t* xb, std::int64_t windows, std::int64_t h,
-                     std::int64_t w, float* out, bool accumulate) const;
+                     std::int64_t w, float* out, bool accumulate, const std::int64_t* out_rows,
+                     std::int64_t out_count) const;
   void conv3(const float* hwc, std::int64_t side, std::int64_t in_c, const std::uint16_t* w, std::int64_t out_c,
              int stride, Array& out, std::int64_t& out_side) const;
   void clip_forward(const float* cells, std::int64_t g, Array& x) const;

@@ -350,6 +350,15 @@ UOCR_ROCM_API int uocr_rocm_linear_bf16x_ws(void* stream, const uint16_t* x, int
 UOCR_ROCM_API int uocr_rocm_linear_bf16x_add_ws(void* stream, const uint16_t* x, int64_t m, int64_t k,
                                                 const uint16_t* w, int64_t n, const float* bias, float* y,
                                                 float* workspace, int64_t workspace_floats);
+/* New: the same with the product's rows scattered: row r is added into y row
+ * y_row[r] (device int64 [m]; a value of y_rows or more drops the row), y
+ * [y_rows, n]: window slots added back into their grid rows, bitwise the
+ * product, the gather of the kept rows and uocr_rocm_add_inplace. Rows
+ * mapping to one y row must not repeat (each is written once); k is a
+ * multiple of 64 and x, w are 16-byte aligned. */
+UOCR_ROCM_API int uocr_rocm_linear_bf16x_add_rows(void* stream, const uint16_t* x, int64_t m, int64_t k,
+                                                  const uint16_t* w, int64_t n, const float* bias, float* y,
+                                                  const int64_t* y_row, int64_t y_rows);
 
 /* New: dst[i] = bf16(src[i]), nearest even; both 16-byte aligned. */
 UOCR_ROCM_API int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst);

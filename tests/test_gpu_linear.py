@@ -178,3 +178,31 @@ def test_linear_add_is_the_product_then_the_add(backend, m, k, n, with_bias):
     got = resid.clone()
     backend.linear_add(xb, dev_bf16(wb), got, ws, bias)
     assert torch.equal(got, want), f"m={m} k={k} n={n} ({floats} workspace floats)"
+
+
+@pytest.mark.parametrize("m,k,n,y_rows", [(4900, 768, 768, 4096), (300, 128, 96, 257), (5, 64, 40, 3),
+                                          (2048, 256, 4096, 1500)])
+def test_linear_add_rows_scatters_the_kept_rows(backend, m, k, n, y_rows):
+    """y[y_row[r]] += product row r for y_row[r] < y_rows (window slots back
+    into their grid rows, padding slots dropped): bitwise the product, the
+    kept rows gathered, then add_inplace."""
+    g = np.random.default_rng(470 + m)
+    x = normal(471 + m, (m, k))
+    wb = bf16(0.03 * normal(472 + n, (n, k)))
+    bias = dev_f32(normal(473, n))
+    xb = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(dev_f32(x), xb)
+    # a permutation of the y rows onto the first y_rows products, the rest padding
+    y_row = np.full(m, y_rows, np.int64)
+    y_row[g.permutation(m)[:y_rows]] = np.arange(y_rows)
+    resid = dev_f32(normal(474, (y_rows, n)))
+    t = torch.empty(m, n, device="cuda")
+    backend.linear(xb, dev_bf16(wb), t, bias)
+    kept = y_row < y_rows
+    src = np.empty(y_rows, np.int64)
+    src[y_row[kept]] = np.nonzero(kept)[0]
+    want = resid.clone()
+    backend.add_inplace(want, t[torch.from_numpy(src).cuda()].contiguous())
+    got = resid.clone()
+    backend.linear_add_rows(xb, dev_bf16(wb), got, torch.from_numpy(y_row).cuda(), bias)
+    assert torch.equal(got, want), f"m={m} k={k} n={n} y_rows={y_rows}"
