@@ -148,6 +148,8 @@ _SIGNATURES = {
     "uocr_rocm_linear_bf16x_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_linear_bf16x_add_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_linear_bf16x_add_rows": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64], _int),
+    "uocr_rocm_linear_bf16x_gelu_erf_bf16": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
+    "uocr_rocm_linear_bf16x_quick_gelu_bf16": ([_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp], _int),
     "uocr_rocm_gemm_nt": ([_vp, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64],
                           _int),
     "uocr_rocm_gemm_nn": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64], _int),
@@ -528,6 +530,19 @@ def linear_add_rows(x, w, y, y_row, bias=None, stream=None):
     m = x.numel() // k
     _op("uocr_rocm_linear_bf16x_add_rows", stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y), _ptr(y_row),
         y.shape[0])
+
+
+def linear_act(x, w, y, bias=None, quick=False, stream=None):
+    """y = bf16(gelu_erf(bf16 x [m, k] . w[n, k]^T + bias)) (quick:
+    quick_gelu), y bfloat16 [m, n] (new: an MLP's first projection with its
+    activation and the rounding its second projection applies, bitwise
+    linear then act_to_bf16)."""
+    n, k = w.shape
+    m = x.numel() // k
+    if y.numel() != m * n:
+        raise ValueError("linear_act: y [m, n]")
+    name = "uocr_rocm_linear_bf16x_quick_gelu_bf16" if quick else "uocr_rocm_linear_bf16x_gelu_erf_bf16"
+    _op(name, stream, _ptr(x), m, k, _ptr(w), n, _f32_param(bias), _ptr(y))
 
 
 def linear(x, w, y, bias=None, stream=None):

@@ -27,6 +27,7 @@
 // k over a caller's workspace: each split writes its partial products and one
 // more launch sums them in split order, then adds the bias.
 
+#include "act_math.hpp"
 #include "common.hpp"
 
 namespace uocr_rocm {
@@ -91,7 +92,21 @@ struct LinearArgs {
   // TM x 128 kernels only, no split.
   const int64_t* row_map;
   int64_t y_rows;
+  // the activation epilogues' output: y16 = bf16(act(sum + bias)), no split,
+  // no accumulate
+  uint16_t* y16;
 };
+
+// What the epilogue writes: the fp32 sums, or an MLP's activation of them
+// rounded to bf16, bitwise the fp32 product followed by the elementwise
+// activation into bf16 (the same arithmetic, from act_math.hpp).
+enum class Epi { kPlain, kGeluBf16, kQuickGeluBf16 };
+
+template <Epi kEpi>
+__device__ __forceinline__ void store_act(const LinearArgs& a, int64_t row, int64_t col, float v) {
+  v = kEpi == Epi::kGeluBf16 ? gelu_f<10>(v) : quick_gelu_f(v);
+  a.y16[row * a.n + col] = f32_to_bf16(v);
+}
 
 // 16 elements of one output column, product rows row0 + 8 (r / 4) + r % 4
 // (r < 16), into y through the row map.
@@ -271,6 +286,7 @@ __device__ __forceinline__ void mfma_step(const u32x4* xs, const u32x4* ws, int 
 
 // acc[i][j][r] is y row 8 (r / 4) + 4 half + r % 4 of the 32 x 32 tile,
 // column r32.
+template <Epi kEpi = Epi::kPlain>
 __device__ __forceinline__ void store_tile(const LinearArgs& a, const Work& wk, int wm, int wn, int half, int r32,
                                            const f32x16 (&acc)[2][2]) {
   const bool split = a.part != nullptr;
@@ -285,6 +301,14 @@ __device__ __forceinline__ void store_tile(const LinearArgs& a, const Work& wk, 
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int64_t row0 = wk.m0 + 64 * wm + 32 * i + 4 * half;
+      if constexpr (kEpi != Epi::kPlain) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = row0 + 8 * (r / 4) + (r % 4);
+          if (row < a.m) store_act<kEpi>(a, row, col, add ? acc[i][j][r] + bv : acc[i][j][r]);
+        }
+        continue;
+      }
       float* const o = out + row0 * a.n + col;  // element r: row row0 + 8 (r / 4) + r % 4
       auto live = [&](int r) { return row0 + 8 * (r / 4) + (r % 4) < a.m; };
       auto off = [&](int r) { return static_cast<int64_t>(8 * (r / 4) + (r % 4)) * a.n; };
@@ -394,6 +418,7 @@ __device__ __forceinline__ void wait_loads_and_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+template <Epi kEpi>
 __global__ __launch_bounds__(kGemmThreads) void linear_dma_k(const LinearArgs a) {
   __shared__ u32x4 xs[2][kTileChunks];
   __shared__ u32x4 ws[2][kTileChunks];
@@ -413,7 +438,7 @@ __global__ __launch_bounds__(kGemmThreads) void linear_dma_k(const LinearArgs a)
       if (more) dma_step(a, wk.m0, wk.n0, wk.k_begin + (t + 1) * kTileK, xs[buf ^ 1], ws[buf ^ 1], wave, lane);
     });
   }
-  store_tile(a, wk, wm, wn, half, r32, acc);
+  store_tile<kEpi>(a, wk, wm, wn, half, r32, acc);
 }
 
 // Products of few rows (CLIP's 257, a short prompt), or of too few 128-row
@@ -447,7 +472,7 @@ __device__ __forceinline__ void dma_step_narrow(const LinearArgs& a, int64_t m0,
   }
 }
 
-template <int TM>
+template <int TM, Epi kEpi>
 __global__ __launch_bounds__(kGemmThreads) void linear_narrow_k(const LinearArgs a) {
   constexpr int FI = TM / 32;
   __shared__ u32x4 xs[2][TM * kRowChunks];
@@ -494,6 +519,14 @@ __global__ __launch_bounds__(kGemmThreads) void linear_narrow_k(const LinearArgs
 #pragma unroll
   for (int i = 0; i < FI; ++i) {
     const int64_t row0 = wk.m0 + 32 * i + 4 * half;
+    if constexpr (kEpi != Epi::kPlain) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + 8 * (r / 4) + (r % 4);
+        if (row < a.m) store_act<kEpi>(a, row, col, add ? acc[i][r] + bv : acc[i][r]);
+      }
+      continue;
+    }
     if (a.row_map != nullptr) {
       float val[16];
 #pragma unroll
@@ -561,13 +594,28 @@ int64_t splits_for(int64_t m, int64_t k, int64_t n, bool narrow = false) {
   return s < 32 ? s : 32;
 }
 
+// The bf16-x kernels that read their tiles straight into LDS (k a multiple
+// of 64, x and w 16-byte aligned).
+template <Epi kEpi>
+void launch_tiles(const LinearArgs& a, unsigned grid, hipStream_t st, bool narrow, bool medium) {
+  if (narrow) {
+    linear_narrow_k<kNarrowM, kEpi><<<grid, kGemmThreads, 0, st>>>(a);
+  } else if (medium) {
+    linear_narrow_k<2 * kNarrowM, kEpi><<<grid, kGemmThreads, 0, st>>>(a);
+  } else {
+    linear_dma_k<kEpi><<<grid, kGemmThreads, 0, st>>>(a);
+  }
+}
+
 int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64_t m, int64_t k, const uint16_t* w,
                  int64_t n, const float* bias, float* y, float* workspace = nullptr, int64_t workspace_floats = 0,
-                 bool accumulate = false, const int64_t* row_map = nullptr, int64_t y_rows = 0) {
+                 bool accumulate = false, const int64_t* row_map = nullptr, int64_t y_rows = 0,
+                 Epi epi = Epi::kPlain, uint16_t* y16 = nullptr) {
   UOCR_REQUIRE(m >= 0 && n >= 0 && k >= 0, what, "m, n and k must be >= 0");
   if (m == 0 || n == 0) return UOCR_ROCM_OK;
   UOCR_REQUIRE(k >= 1 && k < (int64_t{1} << 30), what, "k must be in [1, 2^30)");
-  UOCR_REQUIRE(x != nullptr && w != nullptr && y != nullptr, what, "null x, w or y");
+  UOCR_REQUIRE(x != nullptr && w != nullptr && (epi == Epi::kPlain ? y != nullptr : y16 != nullptr), what,
+               "null x, w or y");
   const bool ragged = k % 8 != 0 || !aligned16(x) || !aligned16(w);
   const bool dma = !ragged && !f32x && k % kTileK == 0;
   const int64_t tiles128 = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
@@ -581,7 +629,8 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
   const int64_t tiles_m = (m + tile_rows - 1) / tile_rows, tiles_n = (n + kTileN - 1) / kTileN;
   UOCR_REQUIRE(tiles_m * tiles_n < (int64_t{1} << 31), what, "too many tiles");
   // split k into the workspace when it holds the partial products
-  int64_t splits = workspace != nullptr && !medium && row_map == nullptr ? splits_for(m, k, n, narrow) : 1;
+  int64_t splits =
+      workspace != nullptr && !medium && row_map == nullptr && epi == Epi::kPlain ? splits_for(m, k, n, narrow) : 1;
   if (splits > 1 && workspace_floats < splits * m * n) splits = 1;
   const int64_t k_len = splits > 1 ? (k / splits + kTileK - 1) / kTileK * kTileK : k;
   splits = (k + k_len - 1) / k_len;
@@ -599,7 +648,8 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
                splits > 1 ? workspace : nullptr,
                accumulate,
                row_map,
-               y_rows};
+               y_rows,
+               y16};
   const unsigned grid = static_cast<unsigned>(tiles_m * tiles_n * splits);
   clear_launch_error();
   const hipStream_t st = as_stream(stream);
@@ -611,12 +661,12 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
     }
   } else if (f32x) {
     linear_staged_k<true, false><<<grid, kGemmThreads, 0, st>>>(a);
-  } else if (narrow) {
-    linear_narrow_k<kNarrowM><<<grid, kGemmThreads, 0, st>>>(a);
-  } else if (medium) {
-    linear_narrow_k<2 * kNarrowM><<<grid, kGemmThreads, 0, st>>>(a);
+  } else if (epi == Epi::kGeluBf16) {
+    launch_tiles<Epi::kGeluBf16>(a, grid, st, narrow, medium);
+  } else if (epi == Epi::kQuickGeluBf16) {
+    launch_tiles<Epi::kQuickGeluBf16>(a, grid, st, narrow, medium);
   } else if (k % kTileK == 0) {
-    linear_dma_k<<<grid, kGemmThreads, 0, st>>>(a);
+    launch_tiles<Epi::kPlain>(a, grid, st, narrow, medium);
   } else {
     linear_staged_k<false, false><<<grid, kGemmThreads, 0, st>>>(a);
   }
@@ -688,6 +738,24 @@ int uocr_rocm_linear_bf16x_add_rows(void* stream, const uint16_t* x, int64_t m, 
   UOCR_REQUIRE(k % kTileK == 0 && aligned16(x) && aligned16(w), kWhat,
                "k must be a multiple of 64 and x, w 16-byte aligned");
   return linear_entry(kWhat, stream, x, false, m, k, w, n, bias, y, nullptr, 0, true, y_row, y_rows);
+}
+
+int uocr_rocm_linear_bf16x_gelu_erf_bf16(void* stream, const uint16_t* x, int64_t m, int64_t k, const uint16_t* w,
+                                         int64_t n, const float* bias, uint16_t* y) {
+  constexpr const char* kWhat = "uocr_rocm_linear_bf16x_gelu_erf_bf16";
+  UOCR_REQUIRE(k % kTileK == 0 && aligned16(x) && aligned16(w), kWhat,
+               "k must be a multiple of 64 and x, w 16-byte aligned");
+  return linear_entry(kWhat, stream, x, false, m, k, w, n, bias, nullptr, nullptr, 0, false, nullptr, 0,
+                      Epi::kGeluBf16, y);
+}
+
+int uocr_rocm_linear_bf16x_quick_gelu_bf16(void* stream, const uint16_t* x, int64_t m, int64_t k,
+                                           const uint16_t* w, int64_t n, const float* bias, uint16_t* y) {
+  constexpr const char* kWhat = "uocr_rocm_linear_bf16x_quick_gelu_bf16";
+  UOCR_REQUIRE(k % kTileK == 0 && aligned16(x) && aligned16(w), kWhat,
+               "k must be a multiple of 64 and x, w 16-byte aligned");
+  return linear_entry(kWhat, stream, x, false, m, k, w, n, bias, nullptr, nullptr, 0, false, nullptr, 0,
+                      Epi::kQuickGeluBf16, y);
 }
 
 int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n, uint16_t* dst) {

@@ -271,6 +271,13 @@ void linear_bf16x_add_rows(const Context& ctx, const std::uint16_t* x, std::int6
   check(uocr_rocm_linear_bf16x_add_rows(ctx.stream(), x, m, k, w_bf16, n, bias, y, y_row, y_rows));
 }
 
+void linear_bf16x_act_bf16(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
+                           const std::uint16_t* w_bf16, std::int64_t n, const float* bias, std::uint16_t* y,
+                           bool quick) {
+  check(quick ? uocr_rocm_linear_bf16x_quick_gelu_bf16(ctx.stream(), x, m, k, w_bf16, n, bias, y)
+              : uocr_rocm_linear_bf16x_gelu_erf_bf16(ctx.stream(), x, m, k, w_bf16, n, bias, y));
+}
+
 void round_bf16(const Context& ctx, const float* src, std::int64_t n, std::uint16_t* dst) {
   check(uocr_rocm_round_bf16(ctx.stream(), src, n, dst));
 }

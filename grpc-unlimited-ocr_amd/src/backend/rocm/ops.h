@@ -190,6 +190,12 @@ void layer_norm_to_bf16(const Context& ctx, const float* x, const float* w, cons
                         std::int64_t rows, std::int64_t cols, float eps);
 void gelu_erf_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n);
 void quick_gelu_to_bf16(const Context& ctx, const float* x, std::uint16_t* y, std::int64_t n);
+// New: y = bf16(act(bf16(x) w^T + bias)), an MLP's first projection with its
+// activation (quick: quick_gelu, else gelu_erf) in the epilogue, bitwise
+// linear_bf16x then gelu_erf_to_bf16 / quick_gelu_to_bf16; k % 64 == 0.
+void linear_bf16x_act_bf16(const Context& ctx, const std::uint16_t* x, std::int64_t m, std::int64_t k,
+                           const std::uint16_t* w_bf16, std::int64_t n, const float* bias, std::uint16_t* y,
+                           bool quick);
 // New: linear with a workspace for splitting k where the product has too
 // few tiles to cover the GPU (linear_workspace_floats(m, k, n) floats; 0:
 // no split is taken).

@@ -306,6 +306,18 @@ void VisionEncoder::norm_project(const float* x, std::int64_t rows, std::int64_t
   project(normed.f32(), rows, c, w, n, bias, y);
 }
 
+bool VisionEncoder::mlp_bf16(float* x, std::int64_t rows, std::int64_t c, const float* ln_w, const float* ln_b,
+                             float eps, const std::uint16_t* w1, std::int64_t hidden, const float* b1,
+                             const std::uint16_t* w2, const float* b2, bool quick) const {
+  if (c % 64 != 0) return false;
+  const std::uint16_t* h = normed_bf16(x, rows, c, ln_w, ln_b, eps);
+  if (h == nullptr) return false;
+  if (act_bf16_.count() < rows * hidden) act_bf16_ = Array(ctx_, DType::kBF16, rows * hidden);
+  linear_bf16x_act_bf16(ctx_, h, rows, c, w1, hidden, b1, act_bf16_.bf16(), quick);
+  project_bf16(act_bf16_.bf16(), rows, hidden, w2, c, b2, x, true);
+  return true;
+}
+
 const std::uint16_t* VisionEncoder::activated_bf16(const float* x, std::int64_t n, bool quick) const {
   if (x_bf16_.count() < n) x_bf16_ = Array(ctx_, DType::kBF16, n);
   if (quick) {
@@ -438,6 +450,10 @@ void VisionEncoder::sam_block(std::size_t index, Array& x, std::int64_t g) const
     add_inplace(ctx_, x.f32(), attended.f32(), cells * c);
   }
 
+  if (mlp_bf16(x.f32(), cells, c, b.norm2_w, b.norm2_b, kSamEps, b.lin1, dims_.sam.mlp, b.lin1_b, b.lin2, b.lin2_b,
+               false)) {
+    return;
+  }
   Array wide = f32(ctx_, cells * dims_.sam.mlp);
   if (const std::uint16_t* h2 = normed_bf16(x.f32(), cells, c, b.norm2_w, b.norm2_b, kSamEps)) {
     project_bf16(h2, cells, c, b.lin1, dims_.sam.mlp, b.lin1_b, wide.f32());
@@ -521,8 +537,10 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
       gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, qkv.f32() + 2 * c, 3 * c, hd, merged.f32(), c, hd, heads);
     }
     project(merged.f32(), n, c, l.out, c, l.out_b, x.f32(), true);
-    norm_project(x.f32(), n, c, l.ln2_w, l.ln2_b, kClipEps, normed, l.fc1, cd.mlp, l.fc1_b, wide.f32());
-    project_bf16(activated_bf16(wide.f32(), n * cd.mlp, true), n, cd.mlp, l.fc2, c, l.fc2_b, x.f32(), true);
+    if (!mlp_bf16(x.f32(), n, c, l.ln2_w, l.ln2_b, kClipEps, l.fc1, cd.mlp, l.fc1_b, l.fc2, l.fc2_b, true)) {
+      norm_project(x.f32(), n, c, l.ln2_w, l.ln2_b, kClipEps, normed, l.fc1, cd.mlp, l.fc1_b, wide.f32());
+      project_bf16(activated_bf16(wide.f32(), n * cd.mlp, true), n, cd.mlp, l.fc2, c, l.fc2_b, x.f32(), true);
+    }
   }
 }
 

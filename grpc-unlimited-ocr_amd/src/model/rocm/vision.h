@@ -170,6 +170,12 @@ class VisionEncoder {
   // bf16(LN(x)) in project()'s scratch, x untouched (null: c above 16384).
   const std::uint16_t* normed_bf16(const float* x, std::int64_t rows, std::int64_t c, const float* w, const float* b,
                                    float eps) const;
+  // x += act(LN(x) w1^T + b1) w2^T + b2 (act quick_gelu or gelu_erf), both
+  // products' inputs in bf16 and the activation in the first one's epilogue;
+  // false, nothing done, where c is above 16384 or not a multiple of 64.
+  bool mlp_bf16(float* x, std::int64_t rows, std::int64_t c, const float* ln_w, const float* ln_b, float eps,
+                const std::uint16_t* w1, std::int64_t hidden, const float* b1, const std::uint16_t* w2,
+                const float* b2, bool quick) const;
   // y = LN(x) w^T + bias, x untouched (`normed`: fp32 room for the wide case).
   void norm_project(const float* x, std::int64_t rows, std::int64_t c, const float* ln_w, const float* ln_b, float eps,
                     Array& normed, const std::uint16_t* w, std::int64_t n, const float* bias, float* y) const;
@@ -201,6 +207,7 @@ class VisionEncoder {
   mutable std::map<std::tuple<std::size_t, bool, std::int64_t>, Array> rel_tables_;
   mutable std::map<std::int64_t, Windows> windows_;
   mutable Array split_ws_, x_bf16_;  // project()'s scratch, grown on demand
+  mutable Array act_bf16_;           // mlp_bf16()'s activations, grown on demand
   mutable std::map<std::int64_t, Array> win_normed_;  // per grid: bf16 norm rows + a zero row
 };
 

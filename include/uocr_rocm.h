@@ -369,6 +369,19 @@ UOCR_ROCM_API int uocr_rocm_round_bf16(void* stream, const float* src, int64_t n
  * op followed by uocr_rocm_round_bf16. */
 UOCR_ROCM_API int uocr_rocm_gelu_erf_to_bf16(void* stream, const float* x, uint16_t* y, int64_t n);
 UOCR_ROCM_API int uocr_rocm_quick_gelu_to_bf16(void* stream, const float* x, uint16_t* y, int64_t n);
+/* New: an MLP's first projection with its activation in the epilogue,
+ * y = bf16(act(x . w^T + bias)), y bf16 [m, n] (nearest even): the
+ * reference's linear then gelu_erf / quick_gelu (ops.h:14-17,37-38) with
+ * the rounding the second projection applies to its input, bitwise
+ * uocr_rocm_linear_bf16x followed by uocr_rocm_gelu_erf_to_bf16 /
+ * uocr_rocm_quick_gelu_to_bf16 without the fp32 [m, n] between them. k is a
+ * multiple of 64 and x, w are 16-byte aligned. */
+UOCR_ROCM_API int uocr_rocm_linear_bf16x_gelu_erf_bf16(void* stream, const uint16_t* x, int64_t m, int64_t k,
+                                                       const uint16_t* w, int64_t n, const float* bias,
+                                                       uint16_t* y);
+UOCR_ROCM_API int uocr_rocm_linear_bf16x_quick_gelu_bf16(void* stream, const uint16_t* x, int64_t m, int64_t k,
+                                                         const uint16_t* w, int64_t n, const float* bias,
+                                                         uint16_t* y);
 
 /* c[s] = alpha a[s] . b[s]^T (gemm_nt: a [m, k], b [n, k]) or c[s] = a[s] . b[s]
  * (gemm_nn: a [m, k], b [k, n]), fp32, row-major with leading dimensions

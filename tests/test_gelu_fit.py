@@ -1,6 +1,6 @@
 """The GELU kernel's tail polynomials against their derivation
 (grpc-unlimited-ocr_amd/csrc/fit_normal_tail.py), on the CPU: the float32
-coefficients written in act.hip are the ones the fit produces, for both
+coefficients written in act_math.hpp are the ones the fit produces, for both
 degrees, and the errors the kernel's comments state hold for the kernel's
 fp32 arithmetic."""
 
@@ -23,8 +23,8 @@ def _fit():
 
 
 def _kernel_coefficients():
-    """{degree: float32 coefficients in ascending powers} from gelu_f in act.hip."""
-    src = open(os.path.join(CSRC, "act.hip")).read()
+    """{degree: float32 coefficients in ascending powers} from gelu_f in act_math.hpp."""
+    src = open(os.path.join(CSRC, "act_math.hpp")).read()
     body = src[src.index("float gelu_f(float x)"):src.index("float gelu_of(float x)")]
     top = body[body.index("if constexpr (kDegree == 10) {"):]
     rest = top[top.index("} else {") + len("} else {"):]

@@ -180,6 +180,39 @@ def test_linear_add_is_the_product_then_the_add(backend, m, k, n, with_bias):
     assert torch.equal(got, want), f"m={m} k={k} n={n} ({floats} workspace floats)"
 
 
+@pytest.mark.parametrize("m,k,n", [(257, 1024, 4096), (4096, 768, 3072), (1000, 128, 200), (5, 64, 40),
+                                   (600, 256, 4096)])
+@pytest.mark.parametrize("quick", [False, True])
+def test_linear_act_is_the_product_then_the_activation(backend, m, k, n, quick):
+    """y = bf16(act(bf16 x . w^T + bias)), an MLP's first projection with
+    its activation in the epilogue (CLIP's fc1 [257 x 1024 -> 4096] and
+    quick_gelu, SAM's lin1 [4096 x 768 -> 3072] and gelu_erf, few-row,
+    64-row and 128-row tiles, ragged m and n): bitwise the product into fp32
+    then act_to_bf16. Also the rows where act_to_bf16 itself is pinned to
+    the oracle (test_gpu_vision_ops)."""
+    x = normal(480 + m, (m, k))
+    wb = bf16(0.05 * normal(481 + n, (n, k)))
+    bias = dev_f32(normal(482, n))
+    xb = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(dev_f32(x), xb)
+    t = torch.empty(m, n, device="cuda")
+    backend.linear(xb, dev_bf16(wb), t, bias)
+    want = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    backend.act_to_bf16(t, want, quick=quick)
+    got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    backend.linear_act(xb, dev_bf16(wb), got, bias, quick=quick)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"m={m} k={k} n={n} quick={quick}"
+
+
+def test_linear_act_refuses_k_off_the_tile(backend):
+    xb = torch.zeros(4, 72, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(8, 72, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(4, 8, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="multiple of 64"):
+        backend.linear_act(xb, w, y)
+
+
 @pytest.mark.parametrize("m,k,n,y_rows", [(4900, 768, 768, 4096), (300, 128, 96, 257), (5, 64, 40, 3),
                                           (2048, 256, 4096, 1500)])
 def test_linear_add_rows_scatters_the_kept_rows(backend, m, k, n, y_rows):
