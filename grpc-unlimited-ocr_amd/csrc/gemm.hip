@@ -59,11 +59,14 @@ __device__ __forceinline__ int slot(int row, int chunk) { return row * kRowChunk
 constexpr int kXcds = 8;
 constexpr int kGroupRows = 8;
 
-// The tile (tm, tn) of workgroup bid: a contiguous run of tiles per XCD,
-// groups of kGroupRows tile-rows sweeping the columns inside a run.
+// The tile (tm, tn) of workgroup bid: a contiguous run of tiles per XCD
+// (workgroups go to the XCDs in turn, bid mod 8; XCD x holds total / 8
+// tiles, one more for the first total mod 8), groups of kGroupRows
+// tile-rows sweeping the columns inside a run.
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
-  const int t = total % kXcds == 0 ? (bid % kXcds) * (total / kXcds) + bid / kXcds : bid;
+  const int per_xcd = total / kXcds, extra = total % kXcds, xcd = bid % kXcds;
+  const int t = xcd * per_xcd + (xcd < extra ? xcd : extra) + bid / kXcds;
   const int per = kGroupRows * tiles_n, group = t / per, first = group * kGroupRows;
   const int rows = tiles_m - first < kGroupRows ? tiles_m - first : kGroupRows;
   const int in = t - group * per;
