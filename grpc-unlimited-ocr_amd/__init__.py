@@ -167,6 +167,11 @@ _SIGNATURES = {
     "uocr_rocm_attention_rel_pos_windows_ws": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                                                 _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
                                                 _vp, _vp, _i64], _int),
+    "uocr_rocm_attention_bf16": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                                  _i64, _i64, _i64, _f32, _vp, _i64], _int),
+    "uocr_rocm_attention_rel_pos_windows_bf16_ws": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64,
+                                                     _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                                     _f32, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_attention_rel_pos_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                         _i64, _i64, _i64, _f32, _vp, _vp, _vp, _i64], _int),
     "uocr_rocm_split_heads": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
@@ -643,7 +648,7 @@ def concat_cols(a, b, out, stream=None):
 
 
 def _operand(t, offset, ld, slice_stride):
-    return (_ptr(t) + 4 * offset, ld, slice_stride)
+    return (_ptr(t) + t.element_size() * offset, ld, slice_stride)
 
 
 def attention(q, k, v, out, slices, rows, keys, hd, scale, mask=None, strides=None, stream=None):
@@ -655,7 +660,9 @@ def attention(q, k, v, out, slices, rows, keys, hd, scale, mask=None, strides=No
     ko = _operand(k, *st.get("k", (0, hd, keys * hd)))
     vo = _operand(v, *st.get("v", (0, hd, keys * hd)))
     oo = _operand(out, *st.get("out", (0, hd, rows * hd)))
-    _op("uocr_rocm_attention", stream, *qo, *ko, *vo, *oo, slices, rows, keys, hd, scale, _f32_param(mask),
+    # a bfloat16 out: the output rounded to bf16 in the epilogue (new)
+    name = "uocr_rocm_attention_bf16" if out.dtype == _torch().bfloat16 else "uocr_rocm_attention"
+    _op(name, stream, *qo, *ko, *vo, *oo, slices, rows, keys, hd, scale, _f32_param(mask),
         0 if mask is None else mask.shape[-1])
 
 
@@ -679,10 +686,13 @@ def attention_rel_pos(q, k, v, out, slices, h, w, hd, scale, rh, rw, strides=Non
 def attention_rel_pos_windows(qkv, out, heads, windows, h, w, hd, scale, rh, rw, workspace, stream=None):
     """attention_rel_pos over heads x windows straight from a window-major
     qkv projection [windows * h * w, 3 * heads * hd] into the merged rows out
-    [windows * h * w, heads * hd] (new)."""
+    [windows * h * w, heads * hd] (new; a bfloat16 out: the output rounded to
+    bf16 in the epilogue)."""
     width, n = heads * hd, h * w
     base = _ptr(qkv)
-    _op("uocr_rocm_attention_rel_pos_windows_ws", stream, base, 3 * width, hd, n * 3 * width, base + 4 * width,
+    bf16 = out.dtype == _torch().bfloat16
+    name = "uocr_rocm_attention_rel_pos_windows_bf16_ws" if bf16 else "uocr_rocm_attention_rel_pos_windows_ws"
+    _op(name, stream, base, 3 * width, hd, n * 3 * width, base + 4 * width,
         3 * width, hd, n * 3 * width, base + 8 * width, 3 * width, hd, n * 3 * width, _ptr(out), width, hd, n * width,
         heads, windows, h, w, hd, scale, _ptr(rh), _ptr(rw), _ptr(workspace), workspace.numel())
 

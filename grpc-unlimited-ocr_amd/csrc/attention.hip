@@ -100,7 +100,19 @@ struct AttnArgs {
   // (s / inner) * s_ + (s % inner) * i_ (inner 1: the single level)
   int inner;
   int64_t iq, ik, iv, io;
+  // non-null: the output in bf16 (nearest even, the rounding a projection
+  // reading it applies) at the same element offsets; out unused
+  uint16_t* out16;
 };
+
+// Four output values at element offset off: fp32, or bf16 into out16.
+__device__ __forceinline__ void store4(const AttnArgs& a, int64_t off, float v0, float v1, float v2, float v3) {
+  if (a.out16 != nullptr) {
+    *reinterpret_cast<u32x2*>(a.out16 + off) = u32x2{pack_bf16(v0, v1), pack_bf16(v2, v3)};
+  } else {
+    *reinterpret_cast<float4*>(a.out + off) = make_float4(v0, v1, v2, v3);
+  }
+}
 
 template <int HD, int kThreads>
 struct Tile {
@@ -393,14 +405,13 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
 
   if (!qin) return;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  float* orow = a.out + slice_at(a, slice, a.so, a.io) + qrow * a.ldo;
+  const int64_t orow = slice_at(a, slice, a.so, a.io) + qrow * a.ldo;
 #pragma unroll
   for (int b = 0; b < kDBlocks; ++b) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d = 32 * b + 8 * g + 4 * hl;
-      *reinterpret_cast<float4*>(orow + d) =
-          make_float4(o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv);
+      store4(a, orow + d, o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv);
     }
   }
 }
@@ -573,9 +584,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void attention_keysplit_k(const A
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] += e[w] * vals[(w * kQueriesPerWave + row) * HD + d0 + j];
   }
-  float* op = a.out + slice_at(a, slice, a.so, a.io) + static_cast<int64_t>(orow) * a.ldo + d0;
-  *reinterpret_cast<float4*>(op) = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
-  *reinterpret_cast<float4*>(op + 4) = make_float4(acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv);
+  const int64_t op = slice_at(a, slice, a.so, a.io) + static_cast<int64_t>(orow) * a.ldo + d0;
+  store4(a, op, acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+  store4(a, op + 4, acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv);
 }
 
 // The relative-position dot products of every (slice, query row) into
@@ -725,7 +736,7 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
                   int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo, int64_t so,
                   int64_t slices, int64_t h, int64_t w, int64_t hd, float scale, const float* rh, const float* rw,
                   float* workspace, int64_t workspace_floats, int64_t inner = 1, int64_t iq = 0, int64_t ik = 0,
-                  int64_t iv = 0, int64_t io = 0) {
+                  int64_t iv = 0, int64_t io = 0, uint16_t* out16 = nullptr) {
   UOCR_REQUIRE(h >= 1 && w >= 1 && h + w <= kMaxRelSpan, what, "need h, w >= 1 and h + w <= 256");
   const int64_t n = h * w;
   if (const int st = check_common(what, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, n, n, hd)) {
@@ -742,7 +753,8 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
   AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(n), static_cast<int>(n),
              scale, nullptr, 0, rh, rw, static_cast<int>(h), static_cast<int>(w), static_cast<int>(lay.ld),
              static_cast<int>(lay.dw_off), table ? workspace : nullptr, table ? workspace : nullptr,
-             static_cast<int>(inner), iq, ik, iv, io};
+             static_cast<int>(inner), iq, ik, iv, io, out16};
+  if (out16 != nullptr) a.out = nullptr;
   if (table) {
     const size_t lds = sizeof(float) * static_cast<size_t>((h + w) * (hd + 1));
     const dim3 grid(static_cast<unsigned>(h + w), static_cast<unsigned>(slices));
@@ -761,6 +773,32 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
                        : launch<Bias::kRelPos>(what, stream, hd, slices, a);
 }
 
+// out: the fp32 output, or out16 reinterpreted (for the pointer checks) when
+// out16 is non-null.
+int attention_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                    int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo,
+                    int64_t so, int64_t slices, int64_t rows, int64_t keys, int64_t hd, float scale,
+                    const float* mask, int64_t mask_ld, uint16_t* out16) {
+  if (const int st = check_common(what, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, rows, keys, hd)) {
+    return st;
+  }
+  UOCR_REQUIRE(mask == nullptr || mask_ld >= keys, what, "mask rows must hold every key");
+  AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
+             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 1, 0, 0, 0, 0, out16};
+  if (out16 != nullptr) a.out = nullptr;
+  if (mask == nullptr && hd == kSplitHd && slices * ((rows + 127) / 128) < 256) {
+    // few query rows: the keys split over a workgroup's waves
+    const dim3 grid(static_cast<unsigned>((rows + kQueriesPerWave - 1) / kQueriesPerWave),
+                    static_cast<unsigned>(slices));
+    clear_launch_error();
+    allow_lds(attention_keysplit_k, kSplitLds);
+    attention_keysplit_k<<<grid, 64 * kSplitWaves, kSplitLds, as_stream(stream)>>>(a);
+    return check_launch(what);
+  }
+  return mask != nullptr ? launch<Bias::kMask>(what, stream, hd, slices, a)
+                         : launch<Bias::kNone>(what, stream, hd, slices, a);
+}
+
 }  // namespace
 }  // namespace uocr_rocm
 
@@ -772,24 +810,16 @@ int uocr_rocm_attention(void* stream, const float* q, int64_t ldq, int64_t sq, c
                         int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo, int64_t so,
                         int64_t slices, int64_t rows, int64_t keys, int64_t hd, float scale, const float* mask,
                         int64_t mask_ld) {
-  constexpr const char* kWhat = "uocr_rocm_attention";
-  if (const int st = check_common(kWhat, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, rows, keys, hd)) {
-    return st;
-  }
-  UOCR_REQUIRE(mask == nullptr || mask_ld >= keys, kWhat, "mask rows must hold every key");
-  AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
-             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 1, 0, 0, 0, 0};
-  if (mask == nullptr && hd == kSplitHd && slices * ((rows + 127) / 128) < 256) {
-    // few query rows: the keys split over a workgroup's waves
-    const dim3 grid(static_cast<unsigned>((rows + kQueriesPerWave - 1) / kQueriesPerWave),
-                    static_cast<unsigned>(slices));
-    clear_launch_error();
-    allow_lds(attention_keysplit_k, kSplitLds);
-    attention_keysplit_k<<<grid, 64 * kSplitWaves, kSplitLds, as_stream(stream)>>>(a);
-    return check_launch(kWhat);
-  }
-  return mask != nullptr ? launch<Bias::kMask>(kWhat, stream, hd, slices, a)
-                         : launch<Bias::kNone>(kWhat, stream, hd, slices, a);
+  return attention_entry("uocr_rocm_attention", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices,
+                         rows, keys, hd, scale, mask, mask_ld, nullptr);
+}
+
+int uocr_rocm_attention_bf16(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
+                             int64_t sk, const float* v, int64_t ldv, int64_t sv, uint16_t* out, int64_t ldo,
+                             int64_t so, int64_t slices, int64_t rows, int64_t keys, int64_t hd, float scale,
+                             const float* mask, int64_t mask_ld) {
+  return attention_entry("uocr_rocm_attention_bf16", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv,
+                         reinterpret_cast<float*>(out), ldo, so, slices, rows, keys, hd, scale, mask, mask_ld, out);
 }
 
 int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
@@ -824,6 +854,19 @@ int uocr_rocm_attention_rel_pos_windows_ws(void* stream, const float* q, int64_t
   UOCR_REQUIRE(heads >= 1 && windows >= 1 && heads * windows < 65536, kWhat, "need heads, windows >= 1");
   return rel_pos_entry(kWhat, stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, heads * windows, h, w, hd,
                        scale, rh, rw, workspace, workspace_floats, windows, wq, wk, wv, wo);
+}
+
+int uocr_rocm_attention_rel_pos_windows_bf16_ws(void* stream, const float* q, int64_t ldq, int64_t sq, int64_t wq,
+                                                const float* k, int64_t ldk, int64_t sk, int64_t wk, const float* v,
+                                                int64_t ldv, int64_t sv, int64_t wv, uint16_t* out, int64_t ldo,
+                                                int64_t so, int64_t wo, int64_t heads, int64_t windows, int64_t h,
+                                                int64_t w, int64_t hd, float scale, const float* rh, const float* rw,
+                                                float* workspace, int64_t workspace_floats) {
+  constexpr const char* kWhat = "uocr_rocm_attention_rel_pos_windows_bf16_ws";
+  UOCR_REQUIRE(heads >= 1 && windows >= 1 && heads * windows < 65536, kWhat, "need heads, windows >= 1");
+  return rel_pos_entry(kWhat, stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, reinterpret_cast<float*>(out), ldo, so,
+                       heads * windows, h, w, hd, scale, rh, rw, workspace, workspace_floats, windows, wq, wk, wv, wo,
+                       out);
 }
 
 }  // extern "C"

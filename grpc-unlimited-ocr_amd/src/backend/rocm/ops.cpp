@@ -213,6 +213,23 @@ void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOpe
                                     ldo, so, slices, h, w, hd, scale, rh, rw));
 }
 
+void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, std::uint16_t* out, std::int64_t ldo,
+               std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
+               const float* mask, std::int64_t mask_ld) {
+  check(uocr_rocm_attention_bf16(ctx.stream(), q.p, q.ld, q.slice, k.p, k.ld, k.slice, v.p, v.ld, v.slice, out, ldo,
+                                 so, slices, rows, keys, hd, scale, mask, mask_ld));
+}
+
+void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t wq, AttnOperand k, std::int64_t wk,
+                               AttnOperand v, std::int64_t wv, std::uint16_t* out, std::int64_t ldo, std::int64_t so,
+                               std::int64_t wo, std::int64_t heads, std::int64_t windows, std::int64_t h,
+                               std::int64_t w, std::int64_t hd, float scale, const float* rh, const float* rw,
+                               float* workspace, std::int64_t workspace_floats) {
+  check(uocr_rocm_attention_rel_pos_windows_bf16_ws(ctx.stream(), q.p, q.ld, q.slice, wq, k.p, k.ld, k.slice, wk, v.p,
+                                                    v.ld, v.slice, wv, out, ldo, so, wo, heads, windows, h, w, hd,
+                                                    scale, rh, rw, workspace, workspace_floats));
+}
+
 std::int64_t attention_rel_pos_workspace_floats(std::int64_t slices, std::int64_t h, std::int64_t w) {
   return uocr_rocm_attention_rel_pos_workspace_floats(slices, h, w);
 }

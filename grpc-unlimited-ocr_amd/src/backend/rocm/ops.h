@@ -176,6 +176,17 @@ void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t w
 void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
                        std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
                        float scale, const float* rh, const float* rw, float* workspace, std::int64_t workspace_floats);
+// New: attention and attention_rel_pos_windows with the output in bf16 (the
+// rounding the output projection applies), bitwise the fp32 op then
+// round_bf16.
+void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, std::uint16_t* out, std::int64_t ldo,
+               std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
+               const float* mask, std::int64_t mask_ld);
+void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t wq, AttnOperand k, std::int64_t wk,
+                               AttnOperand v, std::int64_t wv, std::uint16_t* out, std::int64_t ldo, std::int64_t so,
+                               std::int64_t wo, std::int64_t heads, std::int64_t windows, std::int64_t h,
+                               std::int64_t w, std::int64_t hd, float scale, const float* rh, const float* rw,
+                               float* workspace, std::int64_t workspace_floats);
 // y[m, n] = bf16(x)[m, k] . w[n, k]^T (+ bias[n]) on the matrix cores, fp32
 // accumulation (m == 1: the GEMV); the reference's linear.
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,

@@ -350,28 +350,32 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::
   const Array& rh = rel_table(index, true, h);
   const Array& rw = rel_table(index, false, w);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
-  Array merged = f32(ctx_, rows * c);
   if ((hd == 64 || hd == 128) && h + w <= 256) {
     // one pass on the matrix cores: scores, bias, softmax and values per
-    // (head, window) slice without the scores reaching memory
+    // (head, window) slice without the scores reaching memory; slice (head,
+    // window) straight from the window-major qkv rows (one window: a global
+    // block), into its rows and columns of the merged output, written in
+    // bf16 (the rounding the output projection applies) in project()'s
+    // scratch, which the qkv projection above has finished reading
     const std::int64_t slices = heads * windows;
     const std::int64_t dots = attention_rel_pos_workspace_floats(slices, h, w);
     Array table = f32(ctx_, dots);  // the bias's dot products, formed once per slice
-    if (windows == 1) {
-      // one window (a global block): the heads straight from the projection's
-      // rows into their columns of the output
-      const float* q = qkv.f32();
-      attention_rel_pos(ctx_, {q, 3 * c, hd}, {q + c, 3 * c, hd}, {q + 2 * c, 3 * c, hd}, merged.f32(), c, hd, slices,
-                        h, w, hd, scale, rh.f32(), rw.f32(), table.f32(), dots);
+    if (x_bf16_.count() < rows * c) x_bf16_ = Array(ctx_, DType::kBF16, rows * c);
+    std::uint16_t* merged = x_bf16_.bf16();
+    const float* q = qkv.f32();
+    attention_rel_pos_windows(ctx_, {q, 3 * c, hd}, n * 3 * c, {q + c, 3 * c, hd}, n * 3 * c, {q + 2 * c, 3 * c, hd},
+                              n * 3 * c, merged, c, hd, n * c, heads, windows, h, w, hd, scale, rh.f32(), rw.f32(),
+                              table.f32(), dots);
+    if (out_rows != nullptr) {
+      // window slots added straight back into their grid rows (padding dropped)
+      linear_bf16x_add_rows(ctx_, merged, rows, c, b.proj, c, b.proj_b, out, out_rows, out_count);
     } else {
-      // windows: slice (head, window) straight from the window-major qkv
-      // rows, into its rows and columns of the merged output
-      const float* q = qkv.f32();
-      attention_rel_pos_windows(ctx_, {q, 3 * c, hd}, n * 3 * c, {q + c, 3 * c, hd}, n * 3 * c, {q + 2 * c, 3 * c, hd},
-                                n * 3 * c, merged.f32(), c, hd, n * c, heads, windows, h, w, hd, scale, rh.f32(),
-                                rw.f32(), table.f32(), dots);
+      project_bf16(merged, rows, c, b.proj, c, b.proj_b, out, accumulate);
     }
-  } else if (hd % 4 == 0) {
+    return;
+  }
+  Array merged = f32(ctx_, rows * c);
+  if (hd % 4 == 0) {
     const std::int64_t slices = heads * windows, part = heads * rows * hd;
     Array split = f32(ctx_, 3 * part), o = f32(ctx_, part), scores = f32(ctx_, slices * n * n);
     split_heads(ctx_, qkv.f32(), rows, 3, heads, hd, split.f32());
@@ -391,7 +395,6 @@ void VisionEncoder::sam_attention(std::size_t index, const float* x, const std::
     }
   }
   if (out_rows != nullptr) {
-    // window slots added straight back into their grid rows (padding dropped)
     if (x_bf16_.count() < rows * c) x_bf16_ = Array(ctx_, DType::kBF16, rows * c);
     round_bf16(ctx_, merged.f32(), rows * c, x_bf16_.bf16());
     linear_bf16x_add_rows(ctx_, x_bf16_.bf16(), rows, c, b.proj, c, b.proj_b, out, out_rows, out_count);
@@ -515,15 +518,18 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
   const bool one_pass = hd == 64 || hd == 128;  // attention on the matrix cores
   const bool split = !one_pass && hd % 4 == 0;   // head-major operands, as in sam_attention
   Array normed = f32(ctx_, n * c), qkv = f32(ctx_, n * 3 * c), scores = f32(ctx_, one_pass ? 1 : heads * n * n);
-  Array merged = f32(ctx_, n * c), wide = f32(ctx_, n * cd.mlp);
+  Array merged = f32(ctx_, one_pass ? 1 : n * c), wide = f32(ctx_, n * cd.mlp);
+  Array merged16(ctx_, DType::kBF16, one_pass ? n * c : 1);
   Array hm = f32(ctx_, split ? 3 * n * c : 1), o = f32(ctx_, split ? n * c : 1);
   for (const auto& l : w_.clip_layers) {
     norm_project(x.f32(), n, c, l.ln1_w, l.ln1_b, kClipEps, normed, l.qkv, 3 * c, l.qkv_b, qkv.f32());
     if (one_pass) {
-      // straight from the projection's rows into the heads' columns
+      // straight from the projection's rows into the heads' columns, in
+      // bf16 (the rounding the output projection applies)
       const float* q = qkv.f32();
-      attention(ctx_, {q, 3 * c, hd}, {q + c, 3 * c, hd}, {q + 2 * c, 3 * c, hd}, merged.f32(), c, hd, heads, n, n, hd,
-                scale, nullptr, 0);
+      attention(ctx_, {q, 3 * c, hd}, {q + c, 3 * c, hd}, {q + 2 * c, 3 * c, hd}, merged16.bf16(), c, hd, heads, n, n,
+                hd, scale, nullptr, 0);
+      project_bf16(merged16.bf16(), n, c, l.out, c, l.out_b, x.f32(), true);
     } else if (split) {
       split_heads(ctx_, qkv.f32(), n, 3, heads, hd, hm.f32());
       const float* q = hm.f32();
@@ -531,12 +537,13 @@ void VisionEncoder::clip_forward(const float* cells, std::int64_t g, Array& x) c
       softmax_rows(ctx_, scores.f32(), heads * n, n);
       gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, q + 2 * n * c, hd, n * hd, o.f32(), hd, n * hd, heads);
       merge_heads(ctx_, o.f32(), heads, n, hd, merged.f32());
+      project(merged.f32(), n, c, l.out, c, l.out_b, x.f32(), true);
     } else {
       gemm_nt(ctx_, n, n, hd, scale, qkv.f32(), 3 * c, hd, qkv.f32() + c, 3 * c, hd, scores.f32(), n, n * n, heads);
       softmax_rows(ctx_, scores.f32(), heads * n, n);
       gemm_nn(ctx_, n, hd, n, scores.f32(), n, n * n, qkv.f32() + 2 * c, 3 * c, hd, merged.f32(), c, hd, heads);
+      project(merged.f32(), n, c, l.out, c, l.out_b, x.f32(), true);
     }
-    project(merged.f32(), n, c, l.out, c, l.out_b, x.f32(), true);
     if (!mlp_bf16(x.f32(), n, c, l.ln2_w, l.ln2_b, kClipEps, l.fc1, cd.mlp, l.fc1_b, l.fc2, l.fc2_b, true)) {
       norm_project(x.f32(), n, c, l.ln2_w, l.ln2_b, kClipEps, normed, l.fc1, cd.mlp, l.fc1_b, wide.f32());
       project_bf16(activated_bf16(wide.f32(), n * cd.mlp, true), n, cd.mlp, l.fc2, c, l.fc2_b, x.f32(), true);

@@ -500,6 +500,22 @@ UOCR_ROCM_API int uocr_rocm_attention_rel_pos_windows_ws(void* stream, const flo
                                                          int64_t heads, int64_t windows, int64_t h, int64_t w,
                                                          int64_t hd, float scale, const float* rh, const float* rw,
                                                          float* workspace, int64_t workspace_floats);
+/* New: uocr_rocm_attention and uocr_rocm_attention_rel_pos_windows_ws with
+ * the output in bf16 (nearest even) at the same element offsets (out
+ * 16-byte aligned): attention whose only reader is the output projection,
+ * with the rounding that projection applies to its input, bitwise the fp32
+ * entry followed by uocr_rocm_round_bf16 (the reference's attention then
+ * linear, cuda_vision.cpp:151-172, 253-256). */
+UOCR_ROCM_API int uocr_rocm_attention_bf16(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                                           int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv,
+                                           uint16_t* out, int64_t ldo, int64_t so, int64_t slices, int64_t rows,
+                                           int64_t keys, int64_t hd, float scale, const float* mask,
+                                           int64_t mask_ld);
+UOCR_ROCM_API int uocr_rocm_attention_rel_pos_windows_bf16_ws(
+    void* stream, const float* q, int64_t ldq, int64_t sq, int64_t wq, const float* k, int64_t ldk, int64_t sk,
+    int64_t wk, const float* v, int64_t ldv, int64_t sv, int64_t wv, uint16_t* out, int64_t ldo, int64_t so,
+    int64_t wo, int64_t heads, int64_t windows, int64_t h, int64_t w, int64_t hd, float scale, const float* rh,
+    const float* rw, float* workspace, int64_t workspace_floats);
 UOCR_ROCM_API int uocr_rocm_attention_rel_pos_ws(void* stream, const float* q, int64_t ldq, int64_t sq,
                                                  const float* k, int64_t ldk, int64_t sk, const float* v, int64_t ldv,
                                                  int64_t sv, float* out, int64_t ldo, int64_t so, int64_t slices,

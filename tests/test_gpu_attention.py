@@ -159,3 +159,43 @@ def test_attention_rel_pos_windows_straight_from_the_rows(backend, windows, head
     ws = torch.full((backend.attention_rel_pos_workspace_floats(heads * windows, h, w),), float("nan"), device="cuda")
     backend.attention_rel_pos_windows(dev_f32(qkv), out, heads, windows, h, w, hd, scale, dev_f32(rh), dev_f32(rw), ws)
     assert_f32_close(host_f32(out), want, 1e-5, f"rel-pos attention over {windows} windows x {heads} heads")
+
+
+@pytest.mark.parametrize("windows,heads,h,w", [(25, 12, 14, 14), (1, 12, 64, 64), (3, 2, 7, 9)])
+def test_attention_rel_pos_windows_into_bf16_is_the_rounded_output(backend, windows, heads, h, w):
+    """The windows' attention written in bf16 (the rounding the output
+    projection applies): bitwise the fp32 output then round_bf16, SAM's
+    windowed and global (one 64 x 64 window) layers."""
+    hd, n = 64, h * w
+    width = heads * hd
+    qkv = dev_f32(normal(750 + n, (windows * n, 3 * width)))
+    rh, rw = dev_f32(normal(751, (h, h, hd)) * 0.3), dev_f32(normal(752, (w, w, hd)) * 0.3)
+    ws = torch.empty(backend.attention_rel_pos_workspace_floats(heads * windows, h, w), device="cuda")
+    out = torch.empty(windows * n, width, device="cuda")
+    backend.attention_rel_pos_windows(qkv, out, heads, windows, h, w, hd, 0.125, rh, rw, ws)
+    want = torch.empty(windows * n, width, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(out, want)
+    got = torch.full((windows * n, width), float("nan"), dtype=torch.bfloat16, device="cuda")
+    backend.attention_rel_pos_windows(qkv, got, heads, windows, h, w, hd, 0.125, rh, rw, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("slices,rows,keys,hd,masked", [(16, 257, 257, 64, False), (4, 300, 300, 64, False),
+                                                        (3, 100, 130, 128, True)])
+def test_attention_into_bf16_is_the_rounded_output(backend, slices, rows, keys, hd, masked):
+    """The one-pass attention written in bf16 (CLIP's heads with the keys
+    split over the waves, the 128-row tiles, a mask, head dim 128): bitwise
+    the fp32 output then round_bf16."""
+    q = dev_f32(normal(760 + rows, (slices, rows, hd)))
+    k = dev_f32(normal(761 + keys, (slices, keys, hd)))
+    v = dev_f32(normal(762, (slices, keys, hd)))
+    mask = dev_f32(np.where(normal(763, (rows, keys)) > 1.0, -np.inf, 0.0).astype(np.float32)) if masked else None
+    out = torch.empty(slices, rows, hd, device="cuda")
+    backend.attention(q, k, v, out, slices, rows, keys, hd, 0.125, mask)
+    want = torch.empty(slices, rows, hd, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(out, want)
+    got = torch.full((slices, rows, hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+    backend.attention(q, k, v, got, slices, rows, keys, hd, 0.125, mask)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
