@@ -156,6 +156,7 @@ _SIGNATURES = {
     "uocr_rocm_gather_rows": ([_vp, _vp, _vp, _i64, _i64, _vp], _int),
     "uocr_rocm_scatter_add_rows": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64], _int),
     "uocr_rocm_im2col": ([_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _int),
+    "uocr_rocm_im2col_bf16": ([_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_chw_to_hwc": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_hwc_to_chw": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "uocr_rocm_concat_cols": ([_vp, _vp, _i64, _vp, _i64, _i64, _vp], _int),
@@ -627,7 +628,9 @@ def im2col(x, kh, kw, stride, pad, cols, stream=None):
     """cols [oh * ow, c * kh * kw] = the patches of x [c, h, w] in weight
     order. Reference: im2col, ops.h:54-56."""
     c, h, w = x.shape
-    _op("uocr_rocm_im2col", stream, _ptr(x), c, h, w, kh, kw, stride, pad, _ptr(cols))
+    # a bfloat16 cols: the patches rounded to bf16 (new)
+    name = "uocr_rocm_im2col_bf16" if cols.dtype == _torch().bfloat16 else "uocr_rocm_im2col"
+    _op(name, stream, _ptr(x), c, h, w, kh, kw, stride, pad, _ptr(cols))
 
 
 def chw_to_hwc(x, y, stream=None):

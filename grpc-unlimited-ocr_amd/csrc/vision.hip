@@ -46,18 +46,25 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxRelDots = 2048;  // h + w
 constexpr int kMaxRelDim = 256;    // head dim
 
+// T float, or uint16_t: the patches rounded to bf16 (nearest even), the
+// rounding the convolution's product applies to them.
+template <class T>
 __global__ __launch_bounds__(kBlock) void im2col_k(const float* __restrict__ x, int c, int h, int w, int kh, int kw,
-                                                    int stride, int pad, int ow, int64_t rows,
-                                                    float* __restrict__ cols) {
+                                                    int stride, int pad, int ow, int64_t rows, T* __restrict__ cols) {
   const int patch = c * kh * kw, khw = kh * kw;
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     const int oy = static_cast<int>(r / ow), ox = static_cast<int>(r - static_cast<int64_t>(oy) * ow);
     const int y0 = oy * stride - pad, x0 = ox * stride - pad;
-    float* out = cols + r * patch;
+    T* out = cols + r * patch;
     for (int e = threadIdx.x; e < patch; e += kBlock) {
       const int ci = e / khw, rem = e - ci * khw, ky = rem / kw, kx = rem - ky * kw;
       const int iy = y0 + ky, ix = x0 + kx;
-      out[e] = (iy >= 0 && iy < h && ix >= 0 && ix < w) ? x[(static_cast<int64_t>(ci) * h + iy) * w + ix] : 0.0f;
+      const float v = (iy >= 0 && iy < h && ix >= 0 && ix < w) ? x[(static_cast<int64_t>(ci) * h + iy) * w + ix] : 0.0f;
+      if constexpr (sizeof(T) == 2) {
+        out[e] = f32_to_bf16(v);
+      } else {
+        out[e] = v;
+      }
     }
   }
 }
@@ -260,13 +267,12 @@ int rel_shape_ok(int64_t ldq, int64_t h, int64_t w, int64_t d) {
 }  // namespace
 }  // namespace uocr_rocm
 
-using namespace uocr_rocm;
+namespace uocr_rocm {
+namespace {
 
-extern "C" {
-
-int uocr_rocm_im2col(void* stream, const float* x, int64_t c, int64_t h, int64_t w, int64_t kh, int64_t kw,
-                     int64_t stride, int64_t pad, float* cols) {
-  constexpr const char* kWhat = "uocr_rocm_im2col";
+template <class T>
+int im2col_entry(const char* kWhat, void* stream, const float* x, int64_t c, int64_t h, int64_t w, int64_t kh,
+                 int64_t kw, int64_t stride, int64_t pad, T* cols) {
   UOCR_REQUIRE(c >= 1 && h >= 1 && w >= 1 && kh >= 1 && kw >= 1 && stride >= 1 && pad >= 0, kWhat,
                "c, h, w, kh, kw and stride must be >= 1 and pad >= 0");
   UOCR_REQUIRE(h < (1 << 24) && w < (1 << 24) && c * kh * kw < (int64_t{1} << 30) && pad < (1 << 20) &&
@@ -280,6 +286,24 @@ int uocr_rocm_im2col(void* stream, const float* x, int64_t c, int64_t h, int64_t
       x, static_cast<int>(c), static_cast<int>(h), static_cast<int>(w), static_cast<int>(kh), static_cast<int>(kw),
       static_cast<int>(stride), static_cast<int>(pad), static_cast<int>(ow), oh * ow, cols);
   return check_launch(kWhat);
+}
+
+}  // namespace
+}  // namespace uocr_rocm
+
+using namespace uocr_rocm;
+
+extern "C" {
+
+
+int uocr_rocm_im2col(void* stream, const float* x, int64_t c, int64_t h, int64_t w, int64_t kh, int64_t kw,
+                     int64_t stride, int64_t pad, float* cols) {
+  return im2col_entry("uocr_rocm_im2col", stream, x, c, h, w, kh, kw, stride, pad, cols);
+}
+
+int uocr_rocm_im2col_bf16(void* stream, const float* x, int64_t c, int64_t h, int64_t w, int64_t kh, int64_t kw,
+                          int64_t stride, int64_t pad, uint16_t* cols) {
+  return im2col_entry("uocr_rocm_im2col_bf16", stream, x, c, h, w, kh, kw, stride, pad, cols);
 }
 
 int uocr_rocm_chw_to_hwc(void* stream, const float* x, int64_t c, int64_t h, int64_t w, float* y) {

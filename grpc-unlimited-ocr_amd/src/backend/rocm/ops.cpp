@@ -167,6 +167,11 @@ void im2col(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, 
   check(uocr_rocm_im2col(ctx.stream(), x, c, h, w, kh, kw, stride, pad, cols));
 }
 
+void im2col(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, std::int64_t kh,
+            std::int64_t kw, int stride, int pad, std::uint16_t* cols) {
+  check(uocr_rocm_im2col_bf16(ctx.stream(), x, c, h, w, kh, kw, stride, pad, cols));
+}
+
 void chw_to_hwc(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, float* y) {
   check(uocr_rocm_chw_to_hwc(ctx.stream(), x, c, h, w, y));
 }

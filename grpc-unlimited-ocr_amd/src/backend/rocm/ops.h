@@ -131,6 +131,10 @@ void scatter_add_rows(const Context& ctx, float* dst, const std::int64_t* index,
 // The vision encoder's layout ops: [c, h, w] patches in weight order
 // (oh = (h + 2 pad - kh) / stride + 1), the two layout transposes, and rows
 // joined side by side.
+// New: im2col into bf16 patches (the rounding the convolution's product
+// applies), bitwise im2col then round_bf16.
+void im2col(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, std::int64_t kh,
+            std::int64_t kw, int stride, int pad, std::uint16_t* cols);
 void im2col(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, std::int64_t kh,
             std::int64_t kw, int stride, int pad, float* cols);
 void chw_to_hwc(const Context& ctx, const float* x, std::int64_t c, std::int64_t h, std::int64_t w, float* y);

@@ -477,9 +477,17 @@ void VisionEncoder::conv3(const float* hwc, std::int64_t side, std::int64_t in_c
   Array chw = f32(ctx_, side * side * in_c);
   hwc_to_chw(ctx_, hwc, side, side, in_c, chw.f32());
   out_side = (side + 2 - 3) / stride + 1;
+  out = f32(ctx_, out_side * out_side * out_c);
+  if ((in_c * 9) % 64 == 0) {
+    // the patches straight into bf16 (the rounding the product applies), its
+    // tiles straight from memory into LDS
+    Array patches(ctx_, DType::kBF16, out_side * out_side * in_c * 9);
+    im2col(ctx_, chw.f32(), in_c, side, side, 3, 3, stride, 1, patches.bf16());
+    project_bf16(patches.bf16(), out_side * out_side, in_c * 9, w, out_c, nullptr, out.f32());
+    return;
+  }
   Array patches = f32(ctx_, out_side * out_side * in_c * 9);
   im2col(ctx_, chw.f32(), in_c, side, side, 3, 3, stride, 1, patches.f32());
-  out = f32(ctx_, out_side * out_side * out_c);
   project(patches.f32(), out_side * out_side, in_c * 9, w, out_c, nullptr, out.f32());
 }
 
@@ -487,10 +495,17 @@ void VisionEncoder::conv3(const float* hwc, std::int64_t side, std::int64_t in_c
 void VisionEncoder::sam_forward(const float* image, std::int64_t size, Array& cells) const {
   const SamDims& s = dims_.sam;
   const std::int64_t p = s.patch, g = size / p, c = s.width;
-  Array cols = f32(ctx_, g * g * 3 * p * p);
-  im2col(ctx_, image, 3, size, size, p, p, static_cast<int>(p), 0, cols.f32());
   Array x = f32(ctx_, g * g * c);
-  project(cols.f32(), g * g, 3 * p * p, w_.patch, c, w_.patch_b, x.f32());
+  if ((3 * p * p) % 64 == 0) {
+    // the patches straight into bf16, as in conv3
+    Array cols(ctx_, DType::kBF16, g * g * 3 * p * p);
+    im2col(ctx_, image, 3, size, size, p, p, static_cast<int>(p), 0, cols.bf16());
+    project_bf16(cols.bf16(), g * g, 3 * p * p, w_.patch, c, w_.patch_b, x.f32());
+  } else {
+    Array cols = f32(ctx_, g * g * 3 * p * p);
+    im2col(ctx_, image, 3, size, size, p, p, static_cast<int>(p), 0, cols.f32());
+    project(cols.f32(), g * g, 3 * p * p, w_.patch, c, w_.patch_b, x.f32());
+  }
   add_inplace(ctx_, x.f32(), sam_positions(g).f32(), g * g * c);
   for (std::size_t i = 0; i < w_.sam_blocks.size(); ++i) sam_block(i, x, g);
 

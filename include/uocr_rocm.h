@@ -411,6 +411,12 @@ UOCR_ROCM_API int uocr_rocm_scatter_add_rows(void* stream, float* dst, const int
  * stride + 1 (ow alike). Replaces im2col (src/backend/cuda/ops.h:54-56). */
 UOCR_ROCM_API int uocr_rocm_im2col(void* stream, const float* x, int64_t c, int64_t h, int64_t w, int64_t kh,
                                    int64_t kw, int64_t stride, int64_t pad, float* cols);
+/* New: the same with cols bf16 (nearest even): the patches with the
+ * rounding the convolution's linear applies to them, bitwise im2col then
+ * uocr_rocm_round_bf16 (the reference's im2col then linear,
+ * cuda_vision.cpp:204-237). */
+UOCR_ROCM_API int uocr_rocm_im2col_bf16(void* stream, const float* x, int64_t c, int64_t h, int64_t w, int64_t kh,
+                                        int64_t kw, int64_t stride, int64_t pad, uint16_t* cols);
 
 /* y [h, w, c] = x [c, h, w] and y [c, h, w] = x [h, w, c] (out of place).
  * Replace chw_to_hwc and hwc_to_chw (src/backend/cuda/ops.h:57-58). */

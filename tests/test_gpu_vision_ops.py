@@ -48,6 +48,11 @@ def test_im2col_is_exact(backend, c, h, w, k, stride, pad):
     cols = torch.full(want.shape, float("nan"), device="cuda")
     backend.im2col(dev_f32(x), k, k, stride, pad, cols)
     assert np.array_equal(host_f32(cols).view(np.uint32), want.view(np.uint32))
+    # into bf16 (the patches with the convolution's rounding): the oracle's
+    # patches rounded to bf16, bit for bit
+    cols16 = torch.full(want.shape, float("nan"), dtype=torch.bfloat16, device="cuda")
+    backend.im2col(dev_f32(x), k, k, stride, pad, cols16)
+    assert np.array_equal(cols16.view(torch.int16).cpu().numpy().view(np.uint16), oracle.f32_to_bf16(want))
 
 
 @pytest.mark.parametrize("c,h,w", [(768, 64, 64), (3, 5, 7), (1024, 16, 16), (65, 3, 67)])
