@@ -1080,6 +1080,32 @@ def main():
                 configs[c]["cpu"] = {**fig, "threads": threads, "kind": "port"}
     line["configs"] = configs
     print(json.dumps(line), flush=True)
+    reap_children()
+
+
+def reap_children():
+    """Ends the bench with no process of its own left behind: any child
+    still alive (none is expected: workload 9's encoder runs under
+    subprocess.run, which waits for it) is named on stderr, asked to end,
+    then killed."""
+    try:
+        import psutil
+    except ImportError:
+        return
+    kids = psutil.Process().children(recursive=True)
+    for p in kids:
+        try:
+            print(f"[bench] child still running at exit: pid {p.pid} {' '.join(p.cmdline())}", file=sys.stderr,
+                  flush=True)
+            p.terminate()
+        except psutil.Error:
+            pass
+    _, alive = psutil.wait_procs(kids, timeout=5)
+    for p in alive:
+        try:
+            p.kill()
+        except psutil.Error:
+            pass
 
 
 if __name__ == "__main__":

@@ -162,6 +162,36 @@ struct Chunk<uint16_t, 1> {
   __device__ __forceinline__ void clear() { raw = 0; }
 };
 
+// ---- row stores without a branch ---------------------------------------------
+// A store through a buffer resource at an offset at or past the resource's
+// size is dropped by the hardware. A row kernel therefore stores every chunk
+// it holds unconditionally: kDropOffset for a chunk past the row's end, and a
+// zero-size resource for a wave past the last row. A store inside a branch
+// would make the compiler wait for every earlier store and load (vmcnt(0))
+// before the next use of a loaded chunk, since it cannot tell whether the
+// store was issued; unconditional stores keep those waits exact. Nontemporal
+// policy, as Chunk::store.
+constexpr uint32_t kDropOffset = 0x80000000u;
+
+__device__ __forceinline__ void buffer_store_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kPolicyNt);
+}
+__device__ __forceinline__ void buffer_store_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kPolicyNt);
+}
+__device__ __forceinline__ void buffer_store_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kPolicyNt);
+}
+__device__ __forceinline__ void buffer_store_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kPolicyNt);
+}
+
+// Chunk c at byte offset `off` of the resource (kDropOffset: nothing stored).
+template <class T, int VW>
+__device__ __forceinline__ void store_chunk(__amdgpu_buffer_rsrc_t r, uint32_t off, const Chunk<T, VW>& c) {
+  buffer_store_nt(r, off, c.raw);
+}
+
 // VW fp32 values (norm weights, cos/sin tables) in 128-bit pieces when VW is
 // a multiple of 4; `p` must then be 16-byte aligned.
 template <int VW>

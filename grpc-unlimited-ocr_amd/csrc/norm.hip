@@ -27,8 +27,13 @@
 //                with clamp to [-1e4, 1e4] (src/model/decoder.cpp:20-34).
 // The output expressions are evaluated without FMA contraction so that each
 // product and sum is rounded where the reference rounds it. Norm weights are
-// shared by every row (cache resident): one-wave rows read them after the
-// reduction, rows spread over several waves just before it.
+// shared by every row (cache resident): they are requested in batches between
+// the reductions (kWeightEarlyQ, kWeightMidQ), or staged once per workgroup
+// through LDS for calls of kOneRowGroupsBelow rows or more. Loads and stores
+// are issued without branches (clamped chunks, dropped stores) so that the
+// compiler's waits on the row loads stay exact.
+
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -62,8 +67,27 @@ __device__ __forceinline__ float clamp_act(float v) { return fminf(fmaxf(v, -kAc
 // and 4.76 us); at 8192 rows the 4-wave groups with shared weights are
 // faster (add+RMSNorm [8192, 2048] 1.5%).
 constexpr int64_t kOneRowGroupsBelow = 8192;
+// Workgroup size for one-wave rows below kOneRowGroupsBelow rows (no weight
+// sharing), and the row count below which a row of 4 or more 64-chunk groups
+// is spread over 4 waves (fp32 RMSNorm [1024, 2048]: one-wave rows and
+// spread rows ran alike; at 512 rows spreading is faster).
+constexpr int kSmallRowsBlock = kWave;
+constexpr int64_t kSpreadRowsBelow = 1024;
+// When a wave that does not share its weights through LDS requests them, in
+// quarters of its chunks: kWeightEarlyQ right after its row loads,
+// kWeightMidQ after the first fold, the rest after the last fold. The
+// weights are 4 (RMSNorm) or 8 (LayerNorm) bytes per element against the
+// row's 2 (bf16) or 4, and they pass through the same per-CU load path as
+// the row: requested with the row they delay the row loads of the waves
+// dispatched next (LayerNorm [4096, 1024] bf16 5.4 us against 4.5 us), and
+// requested one chunk at a time just before its store they wait a round trip
+// each. Swept over 19 norm shapes against the earlier per-chunk loads:
+// 0 / 1 was the best or within 2% on 16 of them (LayerNorm [4096, 1024]
+// bf16 4.70 -> 4.53 us, add+RMSNorm [2048, 2048] bf16 7.47 -> 6.34 us).
+constexpr int kWeightEarlyQ = 0;
+constexpr int kWeightMidQ = 1;
 
-template <class T, int VW, int WPR, int VPL, Norm kMode, int TB>
+template <class T, int VW, int WPR, int VPL, Norm kMode, int TB, bool kShareW>
 __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __restrict__ delta,
                                                 const float* __restrict__ w, const float* __restrict__ b,
                                                 T* __restrict__ h, int64_t rows, int cols, float eps,
@@ -71,6 +95,8 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
   constexpr bool kEmbed = kMode == Norm::kEmbedRms;
   constexpr bool kTwoOut = kMode == Norm::kAddRms || kEmbed;  // writes x' and h
   constexpr bool kLn = kMode == Norm::kLayer || kMode == Norm::kLayerToBf16;
+  constexpr bool kToBf16 = kMode == Norm::kLayerToBf16;  // h holds the bf16 output rows
+  using OutT = typename std::conditional<kToBf16, uint16_t, T>::type;
   constexpr int kRowsPerBlock = TB / kWave / WPR;
   __shared__ float red[kRowsPerBlock][kMaxGroups];
   // One-wave rows in multi-wave workgroups share the norm weights through
@@ -78,16 +104,22 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
   // their row loads, write it to LDS after the fold, and every row reads its
   // weights back from LDS. One request per block instead of one per row.
   constexpr int kWavesPerGroup = TB / kWave;
-  constexpr bool kStage = WPR == 1 && kWavesPerGroup > 1 && VPL <= 8;
+  constexpr bool kStage = kShareW && WPR == 1 && kWavesPerGroup > 1 && VPL <= 8;
   constexpr int kStageSlices = kStage ? (VPL + kWavesPerGroup - 1) / kWavesPerGroup : 1;
   constexpr bool kStageB = kStage && kLn;
+  // Without staging, every wave requests its own weights in three batches
+  // of chunks: kE right after its row loads, kM after the first fold and the
+  // rest after the last fold (kWeightEarlyQ / kWeightMidQ quarters of VPL).
+  constexpr int kE = kStage ? 0 : (VPL * kWeightEarlyQ + 3) / 4;
+  constexpr int kM = kStage ? 0 : ((VPL * kWeightMidQ + 3) / 4 < VPL - kE ? (VPL * kWeightMidQ + 3) / 4 : VPL - kE);
   __shared__ __attribute__((aligned(16))) float wst[kStage ? VPL * kWave * VW : 1];
   __shared__ __attribute__((aligned(16))) float bst[kStageB ? VPL * kWave * VW : 1];
   const int wave = wave_in_block();
   const int lane = threadIdx.x & (kWave - 1);
   const int rloc = wave / WPR, wr = wave % WPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rloc;
-  // Waves past the last row still take part in the block's barriers.
+  // Waves past the last row still take part in the block's barriers; their
+  // stores go to a zero-size resource and are dropped.
   const bool active = row < rows;
   const int nvec = cols / VW;
   const int groups = (nvec + kWave - 1) / kWave;
@@ -127,20 +159,44 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
     }
   }
 
+  // The weights, requested behind the row (clamped chunks, no branch): they
+  // arrive while the row is reduced.
   float wsl[kStageSlices][VW], bsl[kStageB ? kStageSlices : 1][VW];
+  float wv[kStage ? 1 : VPL][VW], bv[!kStage && kLn ? VPL : 1][VW];
+  // Chunks [k0, k1)'s weights; the scheduling barriers keep each batch where
+  // it is written.
+  auto load_weights = [&](auto k0, auto k1) {
+    if constexpr (!kStage && decltype(k0)::value < decltype(k1)::value) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = decltype(k0)::value; k < decltype(k1)::value; ++k) {
+        const int v = (wr + WPR * k) * kWave + lane;
+        const int vc = v < nvec ? v : nvec - 1;
+        load_f32<VW>(w + vc * VW, wv[k]);
+        if constexpr (kLn) load_f32<VW>(b + vc * VW, bv[k]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using C0 = std::integral_constant<int, 0>;
+  using CE = std::integral_constant<int, kE>;
+  using CM = std::integral_constant<int, kE + kM>;
+  using CV = std::integral_constant<int, VPL>;
   if constexpr (kStage) {
 #pragma unroll
     for (int j = 0; j < kStageSlices; ++j) {
       const int g = wave + kWavesPerGroup * j;
-      const int v = g * kWave + lane;
+      const int v = (g < groups ? g : groups - 1) * kWave + lane;
       const int vc = v < nvec ? v : nvec - 1;
-      if (g < groups) {
-        load_f32<VW>(w + vc * VW, wsl[j]);
-        if constexpr (kStageB) load_f32<VW>(b + vc * VW, bsl[j]);
-      }
+      load_f32<VW>(w + vc * VW, wsl[j]);
+      if constexpr (kStageB) load_f32<VW>(b + vc * VW, bsl[j]);
     }
+  } else {
+    load_weights(C0{}, CE{});
   }
 
+  // x' leaves through a resource over this row (nothing for an idle wave).
+  const __amdgpu_buffer_rsrc_t xres = buffer_rsrc(xrow, active ? static_cast<uint32_t>(cols) * sizeof(T) : 0u);
   float s[VPL][VW];
   float part[VPL];
 #pragma unroll
@@ -177,35 +233,16 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
     // its chunk is formed, so half of the kernel's writes overlap the row
     // loads still in flight.
     if constexpr (kTwoOut) {
-      if (live[k]) {
-        Chunk<T, VW> xs;
-        xs.narrow(s[k]);
-        xs.store(xrow + static_cast<uint32_t>(v) * VW);
-      }
+      Chunk<T, VW> xs;
+      xs.narrow(s[k]);
+      store_chunk(xres, v < nvec ? static_cast<uint32_t>(v) * VW * sizeof(T) : kDropOffset, xs);
     }
   }
 
-  // Rows spread over several waves (WPR > 1) fold through LDS and a barrier:
-  // their norm weights are requested before the fold, whose latency then
-  // covers the weights' (fp32 [1024, 2048] RMSNorm 4.47 -> 4.37 us). One-wave
-  // rows fold in a few DPP steps and request them after: early weights were
-  // 4-8% slower there, every wave asking for the same lines at once.
-  constexpr bool kEarlyW = WPR > 1;
-  float wv_e[kEarlyW ? VPL : 1][VW], bv_e[kEarlyW && kLn ? VPL : 1][VW];
-  if constexpr (kEarlyW) {
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int v = (wr + WPR * k) * kWave + lane;
-      const int vc = v < nvec ? v : nvec - 1;
-      load_f32<VW>(w + vc * VW, wv_e[k]);
-      if constexpr (kLn) load_f32<VW>(b + vc * VW, bv_e[k]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
   float inv;
   if constexpr (kLn) {
     const float mean = fold_groups<WPR, VPL>(part, wr, groups, red[rloc]) / static_cast<float>(cols);
+    load_weights(CE{}, CM{});
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
       const int v = (wr + WPR * k) * kWave + lane;
@@ -222,6 +259,7 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
     inv = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + static_cast<double>(eps)));
   } else {
     const float ss = fold_groups<WPR, VPL>(part, wr, groups, red[rloc]);
+    load_weights(CE{}, CM{});
     inv = static_cast<float>(1.0 / sqrt(static_cast<double>(ss) / static_cast<double>(cols) +
                                         static_cast<double>(eps)));
   }
@@ -237,53 +275,45 @@ __global__ __launch_bounds__(TB) void norm_rows(T* __restrict__ x, const T* __re
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
+  } else {
+    load_weights(CM{}, CV{});
   }
-  if (!active) return;
 
-  T* const orow = (kTwoOut ? h : x) + off;
+  OutT* const orow = kToBf16 ? reinterpret_cast<OutT*>(reinterpret_cast<uint16_t*>(h) + off)
+                             : reinterpret_cast<OutT*>((kTwoOut ? h : x) + off);
+  const __amdgpu_buffer_rsrc_t ores = buffer_rsrc(orow, active ? static_cast<uint32_t>(cols) * sizeof(OutT) : 0u);
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = (wr + WPR * k) * kWave + lane;
-    if (v < nvec) {
-      const uint32_t at = static_cast<uint32_t>(v) * VW;
-      float wv[VW], bv[VW], y[VW];
-      if constexpr (kEarlyW) {
+    float wk[VW], bk[VW], y[VW];
+    if constexpr (kStage) {
+      const int vc = v < nvec ? v : nvec - 1;
+      load_f32<VW>(wst + vc * VW, wk);
+      if constexpr (kLn) load_f32<VW>(bst + vc * VW, bk);
+    } else {
 #pragma unroll
-        for (int e = 0; e < VW; ++e) {
-          wv[e] = wv_e[k][e];
-          if constexpr (kLn) bv[e] = bv_e[k][e];
-        }
-      } else if constexpr (kStage) {
-        load_f32<VW>(wst + v * VW, wv);
-        if constexpr (kLn) load_f32<VW>(bst + v * VW, bv);
-      } else {
-        load_f32<VW>(w + v * VW, wv);
-        if constexpr (kLn) load_f32<VW>(b + v * VW, bv);
-      }
-      {
-#pragma clang fp contract(off)
-#pragma unroll
-        for (int e = 0; e < VW; ++e) {
-          if constexpr (kLn) {
-            y[e] = (s[k][e] * inv) * wv[e] + bv[e];
-          } else if constexpr (kMode == Norm::kRouter) {
-            y[e] = clamp_act(clamp_act(s[k][e] * inv) * (1.0f + wv[e]));
-          } else {
-            y[e] = wv[e] * (s[k][e] * inv);
-          }
-        }
-      }
-      if constexpr (kMode == Norm::kLayerToBf16) {
-        Chunk<uint16_t, VW> o;  // h is the bf16 output
-        o.narrow(y);
-        o.store(reinterpret_cast<uint16_t*>(h) + off + at);
-      } else {
-        Chunk<T, VW> o;
-        o.narrow(y);
-        o.store(orow + at);
+      for (int e = 0; e < VW; ++e) {
+        wk[e] = wv[k][e];
+        if constexpr (kLn) bk[e] = bv[k][e];
       }
     }
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        if constexpr (kLn) {
+          y[e] = (s[k][e] * inv) * wk[e] + bk[e];
+        } else if constexpr (kMode == Norm::kRouter) {
+          y[e] = clamp_act(clamp_act(s[k][e] * inv) * (1.0f + wk[e]));
+        } else {
+          y[e] = wk[e] * (s[k][e] * inv);
+        }
+      }
+    }
+    Chunk<OutT, VW> o;
+    o.narrow(y);
+    store_chunk(ores, v < nvec ? static_cast<uint32_t>(v) * VW * sizeof(OutT) : kDropOffset, o);
   }
 }
 
@@ -374,20 +404,44 @@ int check_rows(const char* what, int64_t rows, int64_t cols) {
   return UOCR_ROCM_OK;
 }
 
-template <class T, int VW, int WPR, Norm kMode, int TB>
-void launch_norm_tb(int vpl, hipStream_t s, T* x, const T* delta, const float* w, const float* b, T* h,
-                    int64_t rows, int cols, float eps, const EmbedSrc& e) {
+template <class T, int VW, int WPR, Norm kMode, int TB, bool kShareW, int VPL>
+void launch_vpl(hipStream_t s, T* x, const T* delta, const float* w, const float* b, T* h, int64_t rows, int cols,
+                float eps, const EmbedSrc& e) {
   constexpr int kRowsPerBlock = TB / kWave / WPR;
   const unsigned blocks = static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
-  switch (vpl) {
-    case 1: norm_rows<T, VW, WPR, 1, kMode, TB><<<blocks, TB, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e); break;
-    case 2: norm_rows<T, VW, WPR, 2, kMode, TB><<<blocks, TB, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e); break;
-    case 4: norm_rows<T, VW, WPR, 4, kMode, TB><<<blocks, TB, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e); break;
-    case 8: norm_rows<T, VW, WPR, 8, kMode, TB><<<blocks, TB, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e); break;
-    default:
-      norm_rows<T, VW, WPR, 16, kMode, TB><<<blocks, TB, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e);
-      break;
+  norm_rows<T, VW, WPR, VPL, kMode, TB, kShareW><<<blocks, TB, 0, s>>>(x, delta, w, b, h, rows, cols, eps, e);
+}
+
+// vpl: chunks per lane. One-wave rows (WPR 1) take exactly their group count
+// up to 8, so no chunk of a row is past its end for every lane (such a chunk
+// would still be requested, and its weights and its dropped store with it);
+// rows spread over waves take the next of 1, 2, 4, 8, 16.
+template <class T, int VW, int WPR, Norm kMode, int TB, bool kShareW>
+void launch_norm_tb(int vpl, hipStream_t s, T* x, const T* delta, const float* w, const float* b, T* h,
+                    int64_t rows, int cols, float eps, const EmbedSrc& e) {
+#define UOCR_NORM_VPL(n) launch_vpl<T, VW, WPR, kMode, TB, kShareW, n>(s, x, delta, w, b, h, rows, cols, eps, e)
+  if constexpr (WPR == 1) {
+    switch (vpl) {
+      case 1: UOCR_NORM_VPL(1); return;
+      case 2: UOCR_NORM_VPL(2); return;
+      case 3: UOCR_NORM_VPL(3); return;
+      case 4: UOCR_NORM_VPL(4); return;
+      case 5: UOCR_NORM_VPL(5); return;
+      case 6: UOCR_NORM_VPL(6); return;
+      case 7: UOCR_NORM_VPL(7); return;
+      case 8: UOCR_NORM_VPL(8); return;
+      default: UOCR_NORM_VPL(16); return;
+    }
+  } else {
+    switch (vpl_bucket(vpl)) {
+      case 1: UOCR_NORM_VPL(1); return;
+      case 2: UOCR_NORM_VPL(2); return;
+      case 4: UOCR_NORM_VPL(4); return;
+      case 8: UOCR_NORM_VPL(8); return;
+      default: UOCR_NORM_VPL(16); return;
+    }
   }
+#undef UOCR_NORM_VPL
 }
 
 template <class T, int VW, int WPR, Norm kMode>
@@ -395,11 +449,13 @@ void launch_norm_rows(int vpl, hipStream_t s, T* x, const T* delta, const float*
                       int64_t rows, int cols, float eps, const EmbedSrc& e) {
   if constexpr (WPR == 1) {
     if (rows < kOneRowGroupsBelow) {
-      launch_norm_tb<T, VW, WPR, kMode, kWave>(vpl, s, x, delta, w, b, h, rows, cols, eps, e);
+      launch_norm_tb<T, VW, WPR, kMode, kSmallRowsBlock, false>(vpl, s, x, delta, w, b, h, rows, cols, eps, e);
       return;
     }
+    launch_norm_tb<T, VW, WPR, kMode, kBlock, true>(vpl, s, x, delta, w, b, h, rows, cols, eps, e);
+    return;
   }
-  launch_norm_tb<T, VW, WPR, kMode, kBlock>(vpl, s, x, delta, w, b, h, rows, cols, eps, e);
+  launch_norm_tb<T, VW, WPR, kMode, kBlock, false>(vpl, s, x, delta, w, b, h, rows, cols, eps, e);
 }
 
 template <class T, Norm kMode>
@@ -456,8 +512,8 @@ int launch_norm(const char* what, void* stream, T* x, const T* delta, const floa
       }
       return;
     }
-    const bool spread = groups > 16 || (rn < kFewRows && groups >= 4);
-    const int vpl = vpl_bucket(spread ? (groups + 3) / 4 : groups);
+    const bool spread = groups > 16 || (rn < kSpreadRowsBelow && groups >= 4);
+    const int vpl = static_cast<int>(spread ? (groups + 3) / 4 : groups);
     if (vec) {
       if (spread) launch_norm_rows<T, kV, 4, kMode>(vpl, s, xp, dp, w, b, hp, rn, c32, eps, e);
       else launch_norm_rows<T, kV, 1, kMode>(vpl, s, xp, dp, w, b, hp, rn, c32, eps, e);
