@@ -78,6 +78,11 @@ void copy_to_host(const Context& ctx, PinnedBuffer& dst, const void* device_src,
   check(uocr_rocm_memcpy(dst.data(), device_src, bytes, UOCR_ROCM_D2H, ctx.stream()));
 }
 
+void copy_on_device(const Context& ctx, void* device_dst, const void* device_src, std::size_t bytes) {
+  if (bytes == 0) return;
+  check(uocr_rocm_memcpy(device_dst, device_src, bytes, UOCR_ROCM_D2D, ctx.stream()));
+}
+
 Array::Array(const Context& ctx, DType type, std::int64_t count)
     : ctx_(&ctx), block_(nullptr, StreamRelease{ctx.stream()}), count_(count), type_(type) {
   if (count < 0) throw std::invalid_argument("Array: the element count must not be negative");

@@ -95,6 +95,8 @@ class PinnedBuffer {
 // stream's earlier work and return without waiting for it.
 void copy_to_device(const Context& ctx, void* device_dst, const PinnedBuffer& src, std::size_t bytes);
 void copy_to_host(const Context& ctx, PinnedBuffer& dst, const void* device_src, std::size_t bytes);
+// Queue a copy of `bytes` from one device block to another (non-overlapping).
+void copy_on_device(const Context& ctx, void* device_dst, const void* device_src, std::size_t bytes);
 
 enum class DType : std::uint8_t { kF32, kBF16, kI64, kI8 };
 

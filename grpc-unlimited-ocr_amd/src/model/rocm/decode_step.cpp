@@ -206,6 +206,42 @@ void DecodeStep::reset() {
   last_pos_ = -1;
 }
 
+void DecodeStep::reserve(std::int64_t keys) {
+  if (keys <= dims_.capacity) return;
+  auto& d = dims_;
+  const std::int64_t bs = d.router.block_size;
+  const std::int64_t capacity = std::max<std::int64_t>(keys, d.capacity * 2 + 1024);
+  const std::int64_t blocks = (capacity + bs - 1) / bs;
+  need(blocks <= kMaxRouteBlocks, "the cache cannot grow past 4096 router blocks");
+  const std::int64_t width = d.heads * d.head_dim, used_blocks = (length_ + bs - 1) / bs;
+  // A zeroed array of `count` elements with the first `keep` of `a`'s.
+  auto grow = [&](Array& a, DType type, std::int64_t count, std::int64_t keep, std::size_t elem_bytes) {
+    Array bigger(ctx_, type, count);
+    bigger.zero();
+    copy_on_device(ctx_, bigger.data(), a.data(), static_cast<std::size_t>(keep) * elem_bytes);
+    a = std::move(bigger);
+  };
+  const DType cache_type = d.bf16_cache ? DType::kBF16 : DType::kF32;
+  const std::size_t cache_bytes = d.bf16_cache ? 2 : 4;
+  for (std::size_t i = 0; i < layers_.size(); ++i) {
+    grow(k_cache_[i], cache_type, capacity * width, length_ * width, cache_bytes);
+    grow(v_cache_[i], cache_type, capacity * width, length_ * width, cache_bytes);
+    grow(router_keys_[i], DType::kF32, capacity * d.index_dim, length_ * d.index_dim, 4);
+    grow(summaries_[i], DType::kF32, blocks * d.index_dim, used_blocks * d.index_dim, 4);
+    if (d.trace) {
+      trace_z_[i] = Array(ctx_, DType::kF32, blocks);
+      trace_mask_[i] = Array(ctx_, DType::kF32, capacity);
+    }
+  }
+  grow(block_min_, DType::kI64, blocks, prompt_blocks_, 8);
+  grow(block_max_, DType::kI64, blocks, prompt_blocks_, 8);
+  mask_ = Array(ctx_, DType::kF32, capacity);
+  scratch_ = Array(ctx_, DType::kF32, attend_scratch_floats(d.heads, d.head_dim, capacity));
+  d.capacity = capacity;
+  capacity_blocks_ = blocks;
+  record();  // the buffers moved: the captured step is recorded again
+}
+
 void DecodeStep::set_prompt_blocks(const std::vector<std::int64_t>& min_page,
                                    const std::vector<std::int64_t>& max_page) {
   const auto n = static_cast<std::int64_t>(min_page.size());
@@ -308,6 +344,11 @@ std::vector<float> DecodeStep::step(std::int64_t token, RopeCoord coord, std::in
   ++length_;
   const auto* l = static_cast<const float*>(logits_host_->data());
   return {l, l + dims_.vocab};
+}
+
+const std::vector<std::vector<float>>& DecodeStep::prefill_trace() const {
+  if (!dims_.trace) throw std::logic_error("DecodeStep::prefill_trace: built without DecoderDims::trace");
+  return prefill_masks_;
 }
 
 std::vector<LayerTrace> DecodeStep::trace() const {

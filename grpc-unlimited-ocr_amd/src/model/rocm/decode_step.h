@@ -141,9 +141,30 @@ class DecodeStep {
   // dense or mixture-of-experts MLP (the experts' rows gathered by the
   // device's top-k, their outputs scattered back in expert order). coords
   // holds one rotary coordinate per row; query_pages one page per row, or
-  // is empty (every row unconfined). Needs the fp32 cache.
+  // is empty (every row unconfined). Over a bf16 cache the new keys and
+  // values are rounded to bf16 as they are cached, and the prompt's
+  // attention reads them back from the cache, as the decode steps do. The
+  // rows must fit the cache (reserve).
   std::vector<float> prefill(const std::vector<float>& x, const std::vector<RopeCoord>& coords,
                              const std::vector<std::int64_t>& query_pages = {});
+
+  // Grows every layer's caches to hold at least `keys` positions, as
+  // CudaDecoder::reserve does (src/model/cuda/cuda_decoder.cpp:94-117): the
+  // capacity becomes max(keys, 2 capacity + 1024), the length() rows written
+  // so far (and their blocks' summaries and the prompt blocks' pages) are
+  // copied over, the position-sized buffers are grown, and the step is
+  // recorded again. No-op when keys <= capacity(); std::invalid_argument
+  // past 4096 router blocks.
+  void reserve(std::int64_t keys);
+  std::int64_t capacity() const { return dims_.capacity; }
+  std::int64_t block_size() const { return dims_.router.block_size; }
+  // A new sequence from position 0 over the same caches (what
+  // CudaDecoder::prefill does with its length); nothing is cleared, since
+  // no position at or past length() is read.
+  void rewind() {
+    length_ = 0;
+    last_pos_ = -1;
+  }
 
   // Feeds `token` at the next position (length() before the call), rotated
   // at `coord`, its attention routed within query_page's blocks (-1: any
@@ -164,6 +185,10 @@ class DecodeStep {
   // The last step's per-layer values; throws std::logic_error unless
   // DecoderDims::trace was set.
   std::vector<LayerTrace> trace() const;
+  // The last prefill's key masks, per layer [rows, keys] (keys = the
+  // positions after the prompt); throws std::logic_error unless
+  // DecoderDims::trace was set.
+  const std::vector<std::vector<float>>& prefill_trace() const;
 
  private:
   void validate() const;
@@ -182,6 +207,7 @@ class DecodeStep {
   Array router_logits_, expert_ids_, expert_weights_, expert_scratch_;
   std::vector<Array> k_cache_, v_cache_, router_keys_, summaries_;
   std::vector<Array> trace_x_in_, trace_rqk_, trace_z_, trace_mask_, trace_x_mid_;
+  std::vector<std::vector<float>> prefill_masks_;
   std::unique_ptr<PinnedBuffer> state_host_, logits_host_;
   std::unique_ptr<Graph> graph_;
 };

@@ -194,6 +194,7 @@ Model::Model(const Context& ctx, const TensorSource& weights, const ModelDims& d
   const float* final_norm = vector("model.norm.weight", H);
   const std::uint16_t* lm_head = matrix("lm_head.weight", d.vocab, H);
   decoder_ = std::make_unique<DecodeStep>(ctx, d, embed_, std::move(layers), final_norm, lm_head);
+  session_ = std::make_unique<Decoder>(ctx, *decoder_, embed_, d.vocab, H);
 }
 
 Model::~Model() = default;
@@ -203,14 +204,6 @@ std::vector<float> Model::encode_page(const View& global, const std::vector<View
   return vision_->encode_page(global, tiles, tiles_wide, tiles_high);
 }
 
-std::vector<float> Model::embed(const std::vector<std::int64_t>& ids) const {
-  const auto n = static_cast<std::int64_t>(ids.size());
-  const std::int64_t H = dims_.decoder.hidden;
-  if (n == 0) return {};
-  Array idx(ctx_, DType::kI64, n), out(ctx_, DType::kF32, n * H);
-  idx.upload(ids.data(), n);
-  gather_rows_bf16(ctx_, embed_, dims_.decoder.vocab, idx.i64(), n, H, out.f32());
-  return out.download();
-}
+std::vector<float> Model::embed(const std::vector<std::int64_t>& ids) const { return session_->embed(ids); }
 
 }  // namespace uocr::rocm

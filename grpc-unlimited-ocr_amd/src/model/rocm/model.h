@@ -20,6 +20,7 @@
 
 #include "backend/rocm/context.h"
 #include "model/rocm/decode_step.h"
+#include "model/rocm/decoder.h"
 #include "model/rocm/vision.h"
 
 namespace uocr::rocm {
@@ -69,6 +70,8 @@ class Model {
 
   VisionEncoder& vision() { return *vision_; }
   DecodeStep& decoder() { return *decoder_; }
+  // The decoder as DecoderModel sees it: embed, prefill per document, step.
+  Decoder& decoder_model() { return *session_; }
 
  private:
   const std::uint16_t* matrix(const std::string& name, std::int64_t rows, std::int64_t cols);
@@ -84,6 +87,7 @@ class Model {
   const std::uint16_t* embed_ = nullptr;
   std::unique_ptr<VisionEncoder> vision_;
   std::unique_ptr<DecodeStep> decoder_;
+  std::unique_ptr<Decoder> session_;
 };
 
 }  // namespace uocr::rocm

@@ -50,7 +50,6 @@ void mlp(const Context& ctx, const std::uint16_t* xb, std::int64_t rows, std::in
 std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const std::vector<RopeCoord>& coords,
                                        const std::vector<std::int64_t>& query_pages) {
   const auto& d = dims_;
-  need(!d.bf16_cache, "the prefill attention reads the fp32 cache");
   const auto rows = static_cast<std::int64_t>(coords.size());
   const std::int64_t H = d.hidden, W = d.heads * d.head_dim, hd = d.head_dim, D = d.index_dim;
   need(rows >= 1, "no rows");
@@ -58,7 +57,7 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
   need(query_pages.empty() || static_cast<std::int64_t>(query_pages.size()) == rows,
        "one query page per row, or none");
   const std::int64_t first = length_, keys = first + rows;
-  need(keys <= d.capacity, "the prompt runs past the cache");
+  need(keys <= d.capacity, "the prompt runs past the cache (reserve)");
   const std::int64_t bs = d.router.block_size, nblk = (keys + bs - 1) / bs;
   const std::int64_t n_tok = hd / 2 - d.page_pairs;
   const float eps = d.eps;
@@ -81,8 +80,21 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
   Array h = f32(rows * H), delta = f32(rows * H), q = f32(rows * W), rq = f32(rows * D), z = f32(rows * nblk);
   const bool one_pass = hd == 64 || hd == 128;
   Array mask = f32(rows * keys), scores = f32(one_pass ? 1 : d.heads * rows * keys), merged = f32(rows * W);
+  // Over a bf16 cache: the new keys and values in fp32 before they are
+  // rounded into the cache, and every key and value the prompt attends to
+  // widened back from the cache (positions 0 .. keys - 1 gathered in order).
+  const bool bf16 = d.bf16_cache;
+  Array k_new = f32(bf16 ? rows * W : 1), v_new = f32(bf16 ? rows * W : 1);
+  Array k_read = f32(bf16 ? keys * W : 1), v_read = f32(bf16 ? keys * W : 1);
+  Array positions;
+  if (bf16) {
+    std::vector<std::int64_t> all(static_cast<std::size_t>(keys));
+    for (std::int64_t i = 0; i < keys; ++i) all[static_cast<std::size_t>(i)] = i;
+    positions = ids_on_device(ctx_, all);
+  }
   const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(D));
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  prefill_masks_.clear();
   for (std::size_t li = 0; li < layers_.size(); ++li) {
     const LayerWeights& l = layers_[li];
     // input norm (the previous MLP's output added first)
@@ -93,9 +105,10 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
       add_rms_norm(ctx_, x.f32(), delta.f32(), l.input_norm, h.f32(), rows, H, eps);
     }
     // attention (cuda_decoder.cpp:188-245): the projections, k, v and the
-    // router keys straight into the caches at rows first..
-    float* kc = k_cache_[li].f32() + first * W;
-    float* vc = v_cache_[li].f32() + first * W;
+    // router keys straight into the caches at rows first.. (k and v through
+    // fp32 rows over a bf16 cache)
+    float* kc = bf16 ? k_new.f32() : k_cache_[li].f32() + first * W;
+    float* vc = bf16 ? v_new.f32() : v_cache_[li].f32() + first * W;
     float* rkc = router_keys_[li].f32() + first * D;
     const std::uint16_t* wq = l.qkv;
     const std::uint16_t* wk = wq + W * H;
@@ -120,22 +133,32 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
       rope(ctx_, t, rows, 1, D, tok_d.i64(), page_d.i64(), inv_tok_.f32(), n_tok, inv_page, d.page_pairs,
            d.page_mod);
     }
+    const float* k_all = bf16 ? k_read.f32() : k_cache_[li].f32();
+    const float* v_all = bf16 ? v_read.f32() : v_cache_[li].f32();
+    if (bf16) {
+      round_bf16(ctx_, kc, rows * W, k_cache_[li].bf16() + first * W);
+      round_bf16(ctx_, vc, rows * W, v_cache_[li].bf16() + first * W);
+      gather_rows_bf16(ctx_, k_cache_[li].bf16(), positions.i64(), keys, W, k_read.f32());
+      gather_rows_bf16(ctx_, v_cache_[li].bf16(), positions.i64(), keys, W, v_read.f32());
+    }
     block_summaries(ctx_, router_keys_[li].f32(), keys, D, l.head_cls, bs, summaries_[li].f32());
     gemm_nt(ctx_, rows, nblk, D, inv_sqrt_d, rq.f32(), D, 0, summaries_[li].f32(), D, 0, z.f32(), nblk, 0, 1);
     route_blocks(ctx_, z.f32(), rows, nblk, first, keys, block_min, block_max, prompt_blocks_, qp_d.i64(), -1,
                  d.router, mask.f32());
+    if (d.trace) {
+      prefill_masks_.push_back(mask.download());
+      prefill_masks_.back().resize(static_cast<std::size_t>(rows * keys));
+    }
     if (one_pass) {
       // scores, mask, softmax and values in one pass on the matrix cores,
       // each head's columns read in place
-      attention(ctx_, {q.f32(), W, hd}, {k_cache_[li].f32(), W, hd}, {v_cache_[li].f32(), W, hd}, merged.f32(), W,
-                hd, d.heads, rows, keys, hd, scale, mask.f32(), keys);
+      attention(ctx_, {q.f32(), W, hd}, {k_all, W, hd}, {v_all, W, hd}, merged.f32(), W, hd, d.heads, rows, keys, hd,
+                scale, mask.f32(), keys);
     } else {
-      gemm_nt(ctx_, rows, keys, hd, scale, q.f32(), W, hd, k_cache_[li].f32(), W, hd, scores.f32(), keys,
-              rows * keys, d.heads);
+      gemm_nt(ctx_, rows, keys, hd, scale, q.f32(), W, hd, k_all, W, hd, scores.f32(), keys, rows * keys, d.heads);
       scale_add_mask(ctx_, scores.f32(), 1.0f, mask.f32(), d.heads, rows, keys);
       softmax_rows(ctx_, scores.f32(), d.heads * rows, keys);
-      gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_cache_[li].f32(), W, hd, merged.f32(), W, hd,
-              d.heads);
+      gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_all, W, hd, merged.f32(), W, hd, d.heads);
     }
     {
       const Array mb = rounded(ctx_, merged.f32(), rows * W);

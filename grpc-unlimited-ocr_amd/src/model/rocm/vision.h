@@ -151,6 +151,11 @@ class VisionEncoder {
   // The feature grid of a size x size view: size / 16 through two stride-2
   // 3 x 3 convolutions.
   std::int64_t grid(std::int64_t size) const;
+  // The embeddings encode_page places after each grid row and after the page
+  // (host [hidden] each).
+  const std::vector<float>& newline() const { return w_.newline; }
+  const std::vector<float>& separator() const { return w_.separator; }
+  std::int64_t hidden() const { return dims_.hidden; }
   // g (g + 1) + 1 tokens for the global grid, plus (tile_grid * wide + 1)
   // (tile_grid * high) with tiles (vision_encoder.cpp:70-77).
   static std::int64_t page_image_tokens(std::int64_t global_grid, std::int64_t tile_grid, std::int64_t tiles_wide,

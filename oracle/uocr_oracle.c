@@ -32,6 +32,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "uocr_oracle.h"
+
 #define ORC_API __attribute__((visibility("default")))
 
 /* ---- bf16 (src/tensor/dtype.h:32-46) ----------------------------------- */
@@ -76,7 +78,7 @@ static int g_threads = 1;
 ORC_API void orc_set_threads(int t) { g_threads = t < 1 ? 1 : t; }
 ORC_API int orc_threads(void) { return g_threads; }
 
-typedef void (*row_fn)(void* ctx, int64_t row);
+typedef orc_row_fn row_fn;
 typedef struct {
   row_fn fn;
   void* ctx;
@@ -89,7 +91,7 @@ static void* strip_main(void* arg) {
   return NULL;
 }
 
-static void parallel_for(int64_t count, row_fn fn, void* ctx) {
+void orc_parallel_rows(int64_t count, orc_row_fn fn, void* ctx) {
   int64_t threads = g_threads < count ? g_threads : count;
   if (threads <= 1) {
     for (int64_t i = 0; i < count; ++i) fn(ctx, i);
@@ -109,6 +111,8 @@ static void parallel_for(int64_t count, row_fn fn, void* ctx) {
   free(jobs);
   free(tid);
 }
+
+static void parallel_for(int64_t count, row_fn fn, void* ctx) { orc_parallel_rows(count, fn, ctx); }
 
 /* ---- norms --------------------------------------------------------------- */
 
@@ -329,13 +333,26 @@ ORC_API void orc_router_norm(float* x, const float* w, int64_t rows, int64_t col
 /* linear (ops.cpp:91-109): y[m, n] = dot(x[m], w[n]) (+ bias[n]). The
  * reference's bf16 device paths are compared against this on bf16-rounded
  * x and w (tests/cuda_ops_test.cpp:73-80). */
-ORC_API void orc_linear(const float* x, int64_t m, int64_t k, const float* w, int64_t n, const float* bias, float* y) {
-  for (int64_t r = 0; r < m; ++r) {
-    for (int64_t c = 0; c < n; ++c) {
-      const float sum = ref_dot(x + r * k, w + c * k, k);
-      y[r * n + c] = bias != NULL ? sum + bias[c] : sum;
-    }
+typedef struct {
+  const float* x;
+  const float* w;
+  const float* bias;
+  float* y;
+  int64_t k, n;
+} linear_ctx;
+
+static void linear_row(void* p, int64_t r) {
+  const linear_ctx* c = (const linear_ctx*)p;
+  for (int64_t j = 0; j < c->n; ++j) {
+    const float sum = ref_dot(c->x + r * c->k, c->w + j * c->k, c->k);
+    c->y[r * c->n + j] = c->bias != NULL ? sum + c->bias[j] : sum;
   }
+}
+
+/* Rows over orc_threads() threads, as the reference's parallel_for over m. */
+ORC_API void orc_linear(const float* x, int64_t m, int64_t k, const float* w, int64_t n, const float* bias, float* y) {
+  linear_ctx c = {x, w, bias, y, k, n};
+  parallel_for(m, linear_row, &c);
 }
 
 /* softmax_rows (ops.cpp:169-187): fp32 max, v = exp(v - peak) in fp32,

@@ -18,6 +18,11 @@ void orc_f32_to_bf16_array(const float* src, uint16_t* dst, int64_t n);
 void orc_bf16_to_f32_array(const uint16_t* src, float* dst, int64_t n);
 void orc_set_threads(int t);
 int orc_threads(void);
+/* fn(ctx, r) for every r in [0, count) over orc_threads() threads, thread t
+ * taking rows t, t + T, ... (the reference's parallel_for); a row's result
+ * never depends on T. */
+typedef void (*orc_row_fn)(void* ctx, int64_t row);
+void orc_parallel_rows(int64_t count, orc_row_fn fn, void* ctx);
 void orc_rms_norm(float* x, const float* w, int64_t rows, int64_t cols, float eps);
 void orc_layer_norm(float* x, const float* w, const float* b, int64_t rows, int64_t cols, float eps);
 void orc_gelu_erf(float* x, int64_t n);

@@ -155,20 +155,27 @@ ORC_API void orc_layer_norm_channels(float* x, const float* w, const float* b, i
  * s_j = dot(q_i, k_j) * scale (+ bias[i][j]); peak; e_j = exp(s_j - peak)
  * in fp32 with the total in fp64; inv = float(1 / total); out_i += (e_j *
  * inv) v_j in key order. A row whose every score is -inf stays zero. */
-ORC_API void orc_attention_head(const float* q, const float* k, const float* v, int64_t lq, int64_t lk, int64_t d,
-                                int64_t dv, const float* bias, float scale, float* out) {
+typedef struct {
+  const float *q, *k, *v, *bias;
+  float* out;
+  int64_t lk, d, dv;
+  float scale;
+} attn_ctx;
+
+static void attention_row(void* p, int64_t i) {
+  const attn_ctx* c = (const attn_ctx*)p;
+  const int64_t lk = c->lk, d = c->d, dv = c->dv;
+  float* o = c->out + i * dv;
+  for (int64_t e = 0; e < dv; ++e) o[e] = 0.0f;
   float* s = FLOATS(lk);
-  for (int64_t i = 0; i < lq; ++i) {
-    float* o = out + i * dv;
-    for (int64_t e = 0; e < dv; ++e) o[e] = 0.0f;
-    float peak = -INFINITY;
-    for (int64_t j = 0; j < lk; ++j) {
-      float sj = vdot(q + i * d, k + j * d, d) * scale;
-      if (bias != NULL) sj += bias[i * lk + j];
-      s[j] = sj;
-      peak = sj > peak ? sj : peak;
-    }
-    if (peak == -INFINITY) continue;
+  float peak = -INFINITY;
+  for (int64_t j = 0; j < lk; ++j) {
+    float sj = vdot(c->q + i * d, c->k + j * d, d) * c->scale;
+    if (c->bias != NULL) sj += c->bias[i * lk + j];
+    s[j] = sj;
+    peak = sj > peak ? sj : peak;
+  }
+  if (peak != -INFINITY) {
     double total = 0.0;
     for (int64_t j = 0; j < lk; ++j) {
       s[j] = expf(s[j] - peak);
@@ -176,11 +183,19 @@ ORC_API void orc_attention_head(const float* q, const float* k, const float* v, 
     }
     const float inv = (float)(1.0 / total);
     for (int64_t j = 0; j < lk; ++j) {
-      const float p = s[j] * inv;
-      for (int64_t e = 0; e < dv; ++e) o[e] += p * v[j * dv + e];
+      const float pj = s[j] * inv;
+      for (int64_t e = 0; e < dv; ++e) o[e] += pj * c->v[j * dv + e];
     }
   }
   free(s);
+}
+
+/* Query rows over orc_threads() threads, as the reference's parallel_for
+ * over lq (ops.cpp:225). */
+ORC_API void orc_attention_head(const float* q, const float* k, const float* v, int64_t lq, int64_t lk, int64_t d,
+                                int64_t dv, const float* bias, float scale, float* out) {
+  attn_ctx c = {q, k, v, bias, out, lk, d, dv, scale};
+  orc_parallel_rows(lq, attention_row, &c);
 }
 
 /* ---- resizes (ops.cpp:42-86, 253-296) ------------------------------------- */

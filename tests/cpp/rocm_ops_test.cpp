@@ -26,6 +26,7 @@
 #include "backend/rocm/dtype.h"
 #include "backend/rocm/ops.h"
 #include "model/rocm/decode_step.h"
+#include "model/rocm/decoder.h"
 #include "model/rocm/model.h"
 #include "../../oracle/uocr_oracle.h"
 
@@ -765,6 +766,16 @@ struct OracleDecoder {
   std::vector<std::vector<float>> kc, vc, rkc;
   std::vector<std::int64_t> min_page, max_page;
   std::int64_t length = 0;
+  bool bf16_cache = false;  // keys and values cached rounded to bf16
+  // When set: per layer, the device's key masks [rows, keys] of the call
+  // being checked. Each row's own mask must select the same keys (the same
+  // blocks and window; route_mismatch counts rows that do not), and the
+  // attention then runs on the device's mask, so a block bias that fp32
+  // noise moves (log p of a block at the 1.5-entmax support edge) does not
+  // separate the two decoders' later values.
+  const std::vector<std::vector<float>>* device_masks = nullptr;
+  std::int64_t route_mismatch = 0;
+  double max_bias_diff = 0.0;
 
   static std::vector<float> linear(const std::vector<float>& x, std::int64_t rows, const std::vector<float>& w,
                                    const float* w_at, std::int64_t n, bool round = true) {
@@ -824,6 +835,10 @@ struct OracleDecoder {
                      d.page_pairs, d.page_mod, 0, 0);
       orc_rope_apply(rk.data(), rows, 1, D, tok.data(), page.data(), inv_tok.data(), n_tok, inv_page.data(),
                      d.page_pairs, d.page_mod, 0, 0);
+      if (bf16_cache) {
+        k = bf16_rounded(k);
+        v = bf16_rounded(v);
+      }
       std::copy(k.begin(), k.end(), kc[li].begin() + first * W);
       std::copy(v.begin(), v.end(), vc[li].begin() + first * W);
       std::copy(rk.begin(), rk.end(), rkc[li].begin() + first * D);
@@ -843,6 +858,18 @@ struct OracleDecoder {
                                                      rp.top_m, rp.top_k, rp.idx_scale, rp.floor, rp.sigma, blk.data(),
                                                      bias.data(), valid.data());
         orc_key_mask(blk.data(), bias.data(), valid.data(), width, 1, pos[r], keys, bs, rp.local_blocks, mask.data());
+        if (device_masks != nullptr) {
+          const float* dm = (*device_masks)[li].data() + r * keys;
+          bool same = true;
+          for (std::int64_t j = 0; j < keys; ++j) {
+            same = same && std::isinf(dm[j]) == std::isinf(mask[j]) && (dm[j] == 0.0f) == (mask[j] == 0.0f);
+            if (std::isfinite(dm[j]) && std::isfinite(mask[j])) {
+              max_bias_diff = std::max(max_bias_diff, static_cast<double>(std::fabs(dm[j] - mask[j])));
+            }
+          }
+          route_mismatch += same ? 0 : 1;
+          std::copy(dm, dm + keys, mask.begin());
+        }
         orc_attention_one(q.data() + r * W, kc[li].data(), vc[li].data(), keys, W, d.heads, hd, mask.data(), scale,
                           attn.data() + r * W);
       }
@@ -1027,12 +1054,170 @@ void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
   std::sort(errs.begin(), errs.end());
   expect("decode after prefill worst", errs.back(), 1e-3);
   expect("decode after prefill median", errs[errs.size() / 2], 1e-5);
-  {  // the bf16 cache has no prefill
-    auto bd = d;
-    bd.bf16_cache = true;
-    ro::DecodeStep s2(ctx, bd, b16(embed), lw, f32(od.final_norm), b16(od.lm));
-    require_throws_invalid([&] { s2.prefill(x, coords, qp); }, "prefill over a bf16 cache");
+  require_throws_invalid([&] { step.prefill(std::vector<float>(100 * H, 0.0f), std::vector<ro::RopeCoord>(100)); },
+                         "prefill past the cache");
+}
+
+// The decoder as the reference's DecoderModel sees it (ro::Decoder, the
+// class behind RocmDecoder): token embeddings, prefill(embeds, layout) that
+// starts a document and takes the prompt blocks' pages from the layout's
+// image pages, then step() per token, with the caches growing as
+// CudaDecoder::reserve grows them (src/model/cuda/cuda_decoder.cpp:94-117).
+// The step starts with room for 64 positions: a 48-row prompt and 40 steps
+// cross it at the 17th step (the caches become 64 * 2 + 1024 positions, the
+// 64 rows written so far copied over), each step's logits against the
+// oracle's decoder on the same weights; then a second document of 30 rows
+// and 10 steps over the same caches, and a third of 1220 rows that grows
+// them again. The oracle routes every prompt row and step itself and must
+// select the same keys as the device; it then attends under the device's
+// masks (their block biases differ only by fp32 noise, which the log of an
+// entmax weight at the edge of its support can turn into 1e-3 in the
+// logits; routing given the scores is checked exactly by decode_step and
+// tests/test_gpu_route.py). Over the bf16 cache the oracle rounds its own
+// keys and values: a rounding can land on the other side of a tie from the
+// device's, and the rounded element stays in the cache for every later
+// step, so the bars there are the bf16 tolerance, 1e-2 worst and 2e-3 for
+// the median of a document's steps (documents of 10 steps or more).
+void decoder_model(const ro::Context& ctx, bool bf16_cache) {
+  std::printf("decoder model, %s cache\n", bf16_cache ? "bf16" : "fp32");
+  {  // block_image_pages (src/model/page_layout.cpp:55-69): known answers
+    const auto bp = ro::block_image_pages({-1, -1, 0, 0, 0, 1, 1, -1}, 3);
+    require(bp.min_page == std::vector<std::int64_t>{0, 0, 1} && bp.max_page == std::vector<std::int64_t>{0, 1, 1},
+            "block_image_pages: blocks across a page boundary");
+    const auto none = ro::block_image_pages({-1, -1, -1, -1, -1}, 2);
+    require(none.min_page == std::vector<std::int64_t>(3, -1) && none.max_page == none.min_page,
+            "block_image_pages: blocks without image tokens");
+    require(ro::block_image_pages({}, 4).min_page.empty(), "block_image_pages: empty layout");
   }
+  ro::DecoderDims d;
+  d.hidden = 64;
+  d.heads = 2;
+  d.head_dim = 64;
+  d.index_dim = 64;
+  d.vocab = 300;
+  d.capacity = 64;
+  d.bf16_cache = bf16_cache;
+  d.trace = true;  // the device's key masks, for the oracle
+  d.router.block_size = 4;
+  d.router.local_blocks = 1;
+  d.router.idx_scale = 4.0f;
+  const std::int64_t H = d.hidden, W = d.heads * d.head_dim, D = d.index_dim, V = d.vocab;
+  std::vector<float> embed;
+  OracleDecoder od = make_oracle_decoder(d, embed);
+  od.bf16_cache = bf16_cache;
+  od.inv_tok = rope_inv(d.head_dim / 2 - d.page_pairs, d.rope_theta);
+  od.inv_page = rope_inv(d.page_pairs, d.page_theta);
+  od.kc.assign(2, std::vector<float>(2048 * W, 0.0f));
+  od.vc = od.kc;
+  od.rkc.assign(2, std::vector<float>(2048 * D, 0.0f));
+  std::vector<ro::Array> keep;
+  auto dev = [&](const std::vector<float>& v, ro::DType t) {
+    keep.push_back(up(ctx, v, t));
+    return keep.back().data();
+  };
+  auto b16 = [&](const std::vector<float>& v) { return static_cast<const std::uint16_t*>(dev(v, ro::DType::kBF16)); };
+  auto f32 = [&](const std::vector<float>& v) { return static_cast<const float*>(dev(v, ro::DType::kF32)); };
+  ro::MoeWeights moe;
+  std::vector<ro::LayerWeights> lw(2);
+  for (int li = 0; li < 2; ++li) {
+    const auto& l = od.layers[li];
+    lw[li].input_norm = f32(l.in);
+    lw[li].qkv = b16(l.proj);
+    lw[li].router_q_norm = f32(l.rqn);
+    lw[li].router_k_norm = f32(l.rkn);
+    lw[li].head_cls = f32(l.cls);
+    lw[li].o = b16(l.o);
+    lw[li].post_norm = f32(l.post);
+    if (!l.moe) {
+      lw[li].gate = b16(l.gate);
+      lw[li].up = b16(l.up);
+      lw[li].down = b16(l.down);
+      lw[li].ffn = od.ffn;
+    } else {
+      moe = ro::MoeWeights{f32(l.router), b16(l.ustack), b16(l.gstack), b16(l.dstack), od.experts, od.top_k,
+                           od.expert_ffn, b16(l.sg), b16(l.su), b16(l.sd), od.shared_ffn};
+      lw[li].moe = &moe;
+    }
+  }
+  const std::uint16_t* embed_dev = b16(embed);
+  ro::DecodeStep step(ctx, d, embed_dev, lw, f32(od.final_norm), b16(od.lm));
+  ro::Decoder dec(ctx, step, embed_dev, V, H);
+  require(dec.block_size() == 4 && dec.hidden() == H, "decoder model: block size and width");
+  const double bar_prefill = bf16_cache ? 1e-2 : 1e-4, bar_step = bf16_cache ? 1e-2 : 1e-3,
+               bar_median = bf16_cache ? 2e-3 : 1e-5;
+  const std::string tag = bf16_cache ? " (bf16 cache)" : " (fp32 cache)";
+  // A document: `text` text rows, then `pages` image pages of `per_page`
+  // rows each (the layout layout_prompt gives such a prompt: coordinates per
+  // page bucket, image rows confined to their page).
+  auto document = [&](std::int64_t text, std::int64_t pages, std::int64_t per_page, std::int64_t steps,
+                      const char* name) {
+    const std::int64_t rows = text + pages * per_page;
+    ro::PromptPlan plan;
+    std::vector<std::int64_t> ids(static_cast<std::size_t>(rows));
+    for (std::int64_t r = 0; r < rows; ++r) {
+      const bool image = r >= text;
+      const std::int64_t pg = image ? (r - text) / per_page : -1;
+      plan.coords.push_back(image ? ro::RopeCoord{text + (r - text) % per_page, pg + 1} : ro::RopeCoord{r, 0});
+      plan.image_page.push_back(pg);
+      plan.query_page.push_back(pg);
+      ids[static_cast<std::size_t>(r)] = static_cast<std::int64_t>(rng() % static_cast<unsigned>(V));
+    }
+    const auto embeds = dec.embed(ids);
+    std::vector<float> want_embeds;
+    for (const std::int64_t id : ids) want_embeds.insert(want_embeds.end(), embed.begin() + id * H,
+                                                         embed.begin() + (id + 1) * H);
+    require(same_bits(embeds, want_embeds), std::string(name) + ": embeddings" + tag);
+    const auto blocks = ro::block_image_pages(plan.image_page, d.router.block_size);
+    od.min_page = blocks.min_page;
+    od.max_page = blocks.max_page;
+    od.length = 0;
+    const auto got = dec.prefill(embeds, plan);
+    od.device_masks = &step.prefill_trace();
+    const auto want = od.forward(embeds, plan.coords, plan.query_page, false);
+    expect((std::string(name) + ": prefill logits" + tag).c_str(), max_rel(got, want), bar_prefill);
+    require(dec.length() == rows, std::string(name) + ": length after prefill");
+    std::vector<double> errs;
+    for (std::int64_t t = 0; t < steps; ++t) {
+      const std::int64_t token = static_cast<std::int64_t>(rng() % static_cast<unsigned>(V));
+      const ro::RopeCoord c{per_page + text + t, pages + 1};
+      const std::int64_t page = t % pages;
+      const auto g = dec.step(token, c, page, blocks);
+      const std::vector<float> row(embed.begin() + token * H, embed.begin() + (token + 1) * H);
+      std::vector<std::vector<float>> masks;
+      for (const auto& layer : step.trace()) masks.push_back(layer.mask);
+      od.device_masks = &masks;
+      errs.push_back(max_rel(g, od.forward(row, {c}, {page}, true)));
+      if (errs.back() > bar_step) {
+        expect((std::string(name) + ": step " + std::to_string(t) + tag).c_str(), errs.back(), bar_step);
+      }
+    }
+    od.device_masks = nullptr;
+    std::sort(errs.begin(), errs.end());
+    expect((std::string(name) + ": steps worst" + tag).c_str(), errs.back(), bar_step);
+    if (steps >= 10) expect((std::string(name) + ": steps median" + tag).c_str(), errs[errs.size() / 2], bar_median);
+    require(dec.length() == rows + steps, std::string(name) + ": length after the steps");
+    std::printf("  routes: %lld rows with other keys, block biases within %.2g\n",
+                static_cast<long long>(od.route_mismatch), od.max_bias_diff);
+    // fp32: every row routes to the same keys; over the bf16 cache a rounding
+    // upstream may move a near-tied block choice, in at most 1% of the rows
+    const std::int64_t allowed = bf16_cache ? (rows + steps) / 100 : 0;
+    require(od.route_mismatch <= allowed, std::string(name) + ": the same keys routed as the oracle's" + tag);
+    od.route_mismatch = 0;
+  };
+  document(8, 2, 20, 40, "document 1 (48 rows, 40 steps across the initial 64 positions)");
+  require(step.capacity() == 64 * 2 + 1024, "decoder model: the caches grew as CudaDecoder::reserve grows them");
+  document(6, 1, 24, 10, "document 2 (30 rows over the grown caches)");
+  require(step.capacity() == 64 * 2 + 1024, "decoder model: no growth for a shorter document");
+  // a prompt longer than the grown caches grows them again
+  document(20, 3, 400, 2, "document 3 (1220 rows)");
+  require(step.capacity() == (64 * 2 + 1024) * 2 + 1024, "decoder model: a long prompt grows the caches");
+  ro::PromptPlan two;
+  two.coords.resize(2);
+  two.image_page = {-1, -1};
+  two.query_page = {-1, -1};
+  require_throws_invalid([&] { dec.prefill(std::vector<float>(3 * H, 0.0f), two); },
+                         "decoder model: layout and embeddings disagree");
+  require_throws_invalid([&] { dec.prefill({}, ro::PromptPlan{}); }, "decoder model: an empty prompt");
 }
 
 // A TensorSource over named host tensors, as a checkpoint would serve them.
@@ -1392,6 +1577,8 @@ int main() {
     decode_step(ctx, false);
     prefill_then_decode(ctx, 16);
     prefill_then_decode(ctx, 64);
+    decoder_model(ctx, false);
+    decoder_model(ctx, true);
     model_by_names(ctx);
     errors(ctx);
   } catch (const std::exception& e) {

@@ -32,6 +32,7 @@
 #include <random>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "backend/rocm/context.h"
@@ -60,7 +61,8 @@ double max_rel(const std::vector<float>& got, const std::vector<float>& want) {
 // oracle) and their device copies (bf16 matrices, fp32 vectors).
 class Model {
  public:
-  Model(const ro::Context& ctx, const ro::VisionDims& dims, unsigned seed, bool fast_random)
+  // ctx null: the host values only (the oracle's weights, nothing uploaded).
+  Model(const ro::Context* ctx, const ro::VisionDims& dims, unsigned seed, bool fast_random)
       : ctx_(ctx), dims_(dims), rng_(seed), fast_(fast_random) {
     const ro::SamDims& s = dims.sam;
     const ro::ClipDims& c = dims.clip;
@@ -175,7 +177,8 @@ class Model {
   const float* vec(std::int64_t n, float scale, bool one, const float** host) {
     const std::vector<float> v = values(n, scale, one);
     *host = keep(v);
-    arrays_.emplace_back(ctx_, ro::DType::kF32, n);
+    if (ctx_ == nullptr) return nullptr;
+    arrays_.emplace_back(*ctx_, ro::DType::kF32, n);
     arrays_.back().upload(v.data(), n);
     return arrays_.back().f32();
   }
@@ -183,12 +186,13 @@ class Model {
     const float scale = std::min(0.05f, 1.0f / std::sqrt(static_cast<float>(cols)));
     const std::vector<float> v = values(rows * cols, scale, false);
     *host = keep(v);
-    arrays_.emplace_back(ctx_, ro::DType::kBF16, rows * cols);
+    if (ctx_ == nullptr) return nullptr;
+    arrays_.emplace_back(*ctx_, ro::DType::kBF16, rows * cols);
     arrays_.back().upload(v.data(), rows * cols);
     return arrays_.back().bf16();
   }
 
-  const ro::Context& ctx_;
+  const ro::Context* ctx_;
   ro::VisionDims dims_;
   std::mt19937 rng_;
   std::normal_distribution<float> normal_{0.0f, 1.0f};
@@ -308,7 +312,7 @@ int parity() {
   const ro::Context ctx(0);
   {
     const ro::VisionDims dims = tiny_dims();
-    Model m(ctx, dims, 7, false);
+    Model m(&ctx, dims, 7, false);
     const ro::VisionEncoder enc(ctx, dims, m.device());
     check_page(enc, m, "tiny model, base page (128)", 128, {}, 1, 1);
     check_page(enc, m, "tiny model, tiled page (128 + 2 x 1 tiles of 128)", 128, {128, 128}, 2, 1);
@@ -323,7 +327,7 @@ int parity() {
   }
   {
     const ro::VisionDims dims = mid_dims();
-    Model m(ctx, dims, 11, false);
+    Model m(&ctx, dims, 11, false);
     const ro::VisionEncoder enc(ctx, dims, m.device());
     check_page(enc, m, "real widths, 2 + 2 layers, base page (512: 9 windows, a 32 x 32 global layer)", 512, {}, 1, 1);
   }
@@ -358,7 +362,7 @@ double view_flops(const ro::VisionDims& d, std::int64_t size) {
 int timing(std::int64_t size, int reps) {
   const ro::Context ctx(0);
   const ro::VisionDims dims;  // the model's dims: SAM ViT-B (12 layers) + CLIP-L (24 layers)
-  Model m(ctx, dims, 3, true);
+  Model m(&ctx, dims, 3, true);
   const ro::VisionEncoder enc(ctx, dims, m.device());
   const std::int64_t g = enc.grid(size);
   ro::Array image(ctx, ro::DType::kF32, 3 * size * size), out(ctx, ro::DType::kF32, g * g * dims.hidden);
@@ -383,14 +387,86 @@ int timing(std::int64_t size, int reps) {
   return finite ? 0 : 1;
 }
 
+// The timed configuration (timing(): the model's dims, the xorshift weights
+// of seed 3, the 1024-pixel image of seed 3) through the oracle's encoder on
+// the host: the features [256, 1280] with the device's bf16 input rounding,
+// then without it (the reference's CPU arithmetic), as raw fp32 into `path`.
+// No device is needed; tests/golden/make_vision_view_golden.sh runs it.
+constexpr std::int64_t kGoldenSize = 1024;
+// The median element of the full model's features against the rounded
+// oracle, relative to the largest |feature|.
+constexpr double kGoldenMedianBar = 1e-3;
+
+int golden_write(const char* path) {
+  const ro::VisionDims dims;
+  Model m(nullptr, dims, 3, true);
+  const std::vector<float> pixels = m.image(kGoldenSize);
+  orc_set_threads(static_cast<int>(std::max(1u, std::thread::hardware_concurrency())));
+  const std::int64_t g = kGoldenSize / 64, n = g * g * dims.hidden;
+  std::vector<float> feats(static_cast<std::size_t>(2 * n));
+  for (int round_x = 1; round_x >= 0; --round_x) {
+    const auto t0 = std::chrono::steady_clock::now();
+    float* out = feats.data() + (1 - round_x) * n;
+    if (orc_encode_view(&m.oracle(), pixels.data(), kGoldenSize, out, round_x) != g) {
+      throw std::runtime_error("golden: the oracle refused the view");
+    }
+    std::fprintf(stderr, "oracle encode_view (round_x %d): %.1f s on %d threads\n", round_x,
+                 std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(), orc_threads());
+  }
+  FILE* f = std::fopen(path, "wb");
+  require(f != nullptr, std::string("golden: cannot write ") + path);
+  const std::size_t wrote = std::fwrite(feats.data(), sizeof(float), feats.size(), f);
+  std::fclose(f);
+  require(wrote == feats.size(), "golden: short write");
+  std::printf("wrote %s: 2 x [%lld, %lld] fp32\n", path, static_cast<long long>(g * g),
+              static_cast<long long>(dims.hidden));
+  return 0;
+}
+
+// The device encoder on the timed configuration against golden_write's
+// features, at the encoder's bars (compare(): 1e-2 of the rounded oracle's
+// largest |feature|, 2e-2 of the CPU arithmetic's), plus the median
+// element's distance from the rounded oracle.
+int golden_check(const char* path) {
+  const ro::Context ctx(0);
+  const ro::VisionDims dims;
+  Model m(&ctx, dims, 3, true);
+  const ro::VisionEncoder enc(ctx, dims, m.device());
+  const std::vector<float> pixels = m.image(kGoldenSize);
+  const std::int64_t g = enc.grid(kGoldenSize), n = g * g * dims.hidden;
+  std::vector<float> want(static_cast<std::size_t>(2 * n));
+  FILE* f = std::fopen(path, "rb");
+  require(f != nullptr, std::string("golden: cannot read ") + path);
+  const std::size_t got_n = std::fread(want.data(), sizeof(float), want.size(), f);
+  std::fclose(f);
+  require(got_n == want.size(), "golden: the file holds 2 x [256, 1280] floats");
+  const std::vector<float> got = enc.encode_view(ro::View{pixels, kGoldenSize});
+  const std::vector<float> rounded(want.begin(), want.begin() + n), cpu(want.begin() + n, want.end());
+  std::printf("full model (12 SAM + 24 CLIP layers), 1024-pixel view: median rel %.2e\n", median_rel(got, rounded));
+  compare("full model, 1024-pixel view (the timed configuration)", got, rounded, cpu);
+  require(median_rel(got, rounded) <= kGoldenMedianBar, "full model: median element against the rounded oracle");
+  return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
+  try {
+    if (argc >= 3 && std::strcmp(argv[1], "--golden-write") == 0) return golden_write(argv[2]);
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "%s\n", e.what());
+    return 1;
+  }
   if (ro::device_count() == 0) {
     std::fprintf(stderr, "SKIP: no HIP device\n");
     return 77;
   }
   try {
+    if (argc >= 3 && std::strcmp(argv[1], "--golden-check") == 0) {
+      golden_check(argv[2]);
+      std::printf("ok\n");
+      return 0;
+    }
     if (argc >= 2 && std::strcmp(argv[1], "--time") == 0) {
       const std::int64_t size = argc >= 3 ? std::atoll(argv[2]) : 1024;
       const int reps = argc >= 4 ? std::atoi(argv[3]) : 5;

@@ -162,6 +162,26 @@ def test_norms_independent_of_thread_count(orc):
     assert np.array_equal(l1.view(np.uint32), l7.view(np.uint32))
 
 
+def test_linear_and_attention_independent_of_thread_count(orc):
+    # the reference runs linear and attention_head over rows with
+    # parallel_for too (ops.cpp:100,225): a row's values never depend on T
+    g = rng(4)
+    x = g.standard_normal((37, 96), dtype=np.float32)
+    w = g.standard_normal((45, 96), dtype=np.float32)
+    b = g.standard_normal(45, dtype=np.float32)
+    q = g.standard_normal((29, 16), dtype=np.float32)
+    k = g.standard_normal((41, 16), dtype=np.float32)
+    v = g.standard_normal((41, 24), dtype=np.float32)
+    bias = g.standard_normal((29, 41), dtype=np.float32)
+    orc.set_threads(1)
+    y1, a1 = orc.linear(x, w, b), orc.attention_head(q, k, v, bias, 0.25)
+    orc.set_threads(6)
+    y6, a6 = orc.linear(x, w, b), orc.attention_head(q, k, v, bias, 0.25)
+    orc.set_threads(1)
+    assert np.array_equal(y1.view(np.uint32), y6.view(np.uint32))
+    assert np.array_equal(a1.view(np.uint32), a6.view(np.uint32))
+
+
 # ---- activations -------------------------------------------------------------------------
 
 
