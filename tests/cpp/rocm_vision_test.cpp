@@ -258,8 +258,14 @@ double median_rel(const std::vector<float>& got, const std::vector<float>& want)
 // relative-position bias dropped, a layer skipped) moves the features by
 // 1e-1 and more (tests/test_oracle_vision.py). The ops themselves are held to
 // 1e-5 one by one (tests/test_gpu_vision_ops.py, test_gpu_linear.py).
+// median_bar: the median element's distance from the rounded oracle. On the
+// tiny model almost every element is exact (median 0: no linear input has
+// crossed a rounding boundary yet); at the real widths the median sits at
+// the rounding-noise floor (6e-4 measured), so a slip that shifts most
+// features (a misplaced window slot, a dropped bias term) lifts it well
+// above 2e-3 while leaving the maximum near its own floor.
 void compare(const char* what, const std::vector<float>& got, const std::vector<float>& rounded,
-             const std::vector<float>& cpu) {
+             const std::vector<float>& cpu, double median_bar) {
   require(got.size() == rounded.size() && got.size() == cpu.size(), std::string(what) + ": same token layout");
   for (float v : got) require(std::isfinite(v), std::string(what) + ": finite features");
   const double e_dev = max_rel(got, rounded), e_med = median_rel(got, rounded), e_cpu = max_rel(got, cpu);
@@ -268,10 +274,11 @@ void compare(const char* what, const std::vector<float>& got, const std::vector<
       what, got.size(), e_dev, e_med, e_cpu);
   require(e_dev < 1e-2, std::string(what) + ": within 1e-2 of the oracle with the device's bf16 rounding");
   require(e_cpu < 2e-2, std::string(what) + ": within the reference's bf16 bar of the CPU encoder");
+  require(e_med <= median_bar, std::string(what) + ": the median element against the rounded oracle");
 }
 
 void check_page(const ro::VisionEncoder& enc, Model& m, const char* what, std::int64_t size,
-                const std::vector<std::int64_t>& tile_sizes, std::int64_t wide, std::int64_t high) {
+                const std::vector<std::int64_t>& tile_sizes, std::int64_t wide, std::int64_t high, double median_bar) {
   ro::View global{m.image(size), size};
   std::vector<ro::View> tiles;
   std::vector<float> tile_pixels;
@@ -293,7 +300,7 @@ void check_page(const ro::VisionEncoder& enc, Model& m, const char* what, std::i
   const std::int64_t n0 = orc_encode_page(&m.oracle(), global.pixels.data(), size, tile_pixels.data(),
                                           static_cast<std::int64_t>(tiles.size()), ts, wide, high, cpu.data(), 0);
   require(n1 == rows && n0 == rows, std::string(what) + ": the oracle's token count");
-  compare(what, got, rounded, cpu);
+  compare(what, got, rounded, cpu, median_bar);
   // the separator closes the page; a newline closes every grid row
   const float* sep = m.oracle().separator;
   const float* nl = m.oracle().newline;
@@ -314,9 +321,9 @@ int parity() {
     const ro::VisionDims dims = tiny_dims();
     Model m(&ctx, dims, 7, false);
     const ro::VisionEncoder enc(ctx, dims, m.device());
-    check_page(enc, m, "tiny model, base page (128)", 128, {}, 1, 1);
-    check_page(enc, m, "tiny model, tiled page (128 + 2 x 1 tiles of 128)", 128, {128, 128}, 2, 1);
-    check_page(enc, m, "tiny model, base page (256: 4 padded windows)", 256, {}, 1, 1);
+    check_page(enc, m, "tiny model, base page (128)", 128, {}, 1, 1, 1e-6);
+    check_page(enc, m, "tiny model, tiled page (128 + 2 x 1 tiles of 128)", 128, {128, 128}, 2, 1, 1e-6);
+    check_page(enc, m, "tiny model, base page (256: 4 padded windows)", 256, {}, 1, 1, 1e-6);
     bool threw = false;
     try {
       (void)enc.encode_view(ro::View{std::vector<float>(3 * 100 * 100), 100});
@@ -329,7 +336,8 @@ int parity() {
     const ro::VisionDims dims = mid_dims();
     Model m(&ctx, dims, 11, false);
     const ro::VisionEncoder enc(ctx, dims, m.device());
-    check_page(enc, m, "real widths, 2 + 2 layers, base page (512: 9 windows, a 32 x 32 global layer)", 512, {}, 1, 1);
+    check_page(enc, m, "real widths, 2 + 2 layers, base page (512: 9 windows, a 32 x 32 global layer)", 512, {}, 1, 1,
+               2e-3);
   }
   return 0;
 }
@@ -394,8 +402,8 @@ int timing(std::int64_t size, int reps) {
 // No device is needed; tests/golden/make_vision_view_golden.sh runs it.
 constexpr std::int64_t kGoldenSize = 1024;
 // The median element of the full model's features against the rounded
-// oracle, relative to the largest |feature|.
-constexpr double kGoldenMedianBar = 1e-3;
+// oracle, relative to the largest |feature| (compare()).
+constexpr double kGoldenMedianBar = 2e-3;
 
 int golden_write(const char* path) {
   const ro::VisionDims dims;
@@ -443,8 +451,7 @@ int golden_check(const char* path) {
   const std::vector<float> got = enc.encode_view(ro::View{pixels, kGoldenSize});
   const std::vector<float> rounded(want.begin(), want.begin() + n), cpu(want.begin() + n, want.end());
   std::printf("full model (12 SAM + 24 CLIP layers), 1024-pixel view: median rel %.2e\n", median_rel(got, rounded));
-  compare("full model, 1024-pixel view (the timed configuration)", got, rounded, cpu);
-  require(median_rel(got, rounded) <= kGoldenMedianBar, "full model: median element against the rounded oracle");
+  compare("full model, 1024-pixel view (the timed configuration)", got, rounded, cpu, kGoldenMedianBar);
   return 0;
 }
 

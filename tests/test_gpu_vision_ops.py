@@ -144,6 +144,22 @@ def test_cpp_rocm_vision_test(backend):
     assert r.returncode == 0, r.stdout + r.stderr
 
 
+def test_full_model_view_against_golden(backend):
+    """The timed vision configuration itself (the model's dims: 12 SAM and
+    24 CLIP layers, the seeded weights of the bench's timing run, one
+    1024-pixel view) against the oracle's features of the same model,
+    written on the host by tests/golden/make_vision_view_golden.sh: within
+    1e-2 of the oracle with the device's bf16 input rounding and 2e-2 of the
+    reference's CPU arithmetic (the reference's bar,
+    tests/cuda_vision_test.cpp:121-122), and the median element within 1e-3
+    of the rounded oracle."""
+    binary = os.path.join(os.path.dirname(backend.LIB_PATH), "rocm_vision_test")
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "vision_view1024.f32")
+    r = subprocess.run([binary, "--golden-check", golden], capture_output=True, text=True, timeout=110)
+    sys.stdout.write(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 @pytest.mark.parametrize("rows,parts,heads,hd", [(4900, 3, 12, 64), (65, 3, 16, 64), (7, 1, 2, 12), (3, 2, 5, 4)])
 def test_split_and_merge_heads_are_exact(backend, rows, parts, heads, hd):
     x = normal(660 + rows, (rows, parts * heads * hd))
