@@ -654,9 +654,10 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
     attention routed by the block router (the q, k, v and router q/k
     projections in one GEMV, router norms, PageRope at (tok, page), the
     router key's append, the block summary, the scores of the 252 remote
-    blocks, top-16 1.5-entmax and the key mask in one launch; rope of q and k,
-    both appends and the masked attention over 8192 positions), the final
-    norm fused into the LM-head GEMV. The prompt's first 4096 positions are
+    blocks, top-16 1.5-entmax, the key mask and the list of its live keys in
+    one launch; rope of q and k, both appends and the attention over the live
+    keys alone of 8192 positions), the final norm fused into the LM-head
+    GEMV. The prompt's first 4096 positions are
     128 blocks of 16 pages and the query is confined to one page. Timed over
     the reference's fp32 key/value cache and over a bf16 one. The weights
     (5.8 GB) exceed the Infinity Cache many times over."""
@@ -702,12 +703,16 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
     ids, wts = torch.empty(1, top_k, dtype=torch.int64, device="cuda"), torch.empty(1, top_k, device="cuda")
     rlogits = torch.empty(experts, device="cuda")
     escratch = torch.empty(be.expert_scratch_floats(top_k, expert_ffn), device="cuda")
+    segs = torch.empty(be.KEY_SEGMENT_WORDS, dtype=torch.int32, device="cuda")
+    max_live = (max(params.top_k, 1) + params.local_blocks) * params.block_size
+    seg_splits = be.attend_segments_scratch_floats(heads, hd, max_live) // (heads * (hd + 2))
+    seg_scratch = torch.empty(be.attend_segments_scratch_floats(heads, hd, max_live), device="cuda")
     q, k, v = proj[:width], proj[width:2 * width], proj[2 * width:3 * width]
     rq, rk = proj[3 * width:3 * width + d], proj[3 * width + d:]
 
     def route(L):
         be.route_decode_step(rq, rk, L["rqn"], L["rkn"], 1e-6, inv_tok, inv_page, page_mod, L["cls"], L["rkeys"],
-                             L["summ"], block_min, block_max, state, params, mask)
+                             L["summ"], block_min, block_max, state, params, mask, segments=segs)
 
     def step():
         cur = 0
@@ -719,8 +724,8 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
             if pending is not None:
                 cur = 1 - cur
             route(L)
-            be.attend_rope_kv_step(q, k, v, L["kc"], L["vc"], heads, hd, mask, scale, state, inv_tok, inv_page,
-                                   page_mod, scratch, attn)
+            be.attend_rope_kv_step_segments(q, k, v, L["kc"], L["vc"], heads, hd, segs, max_live, scale, state,
+                                            inv_tok, inv_page, page_mod, seg_scratch, attn)
             be.gemv_bf16(attn, L["o"], o)
             a = act[:L["ffn"]]
             if L["moe"]:  # the shared experts' pair GEMV and the router in one launch
@@ -738,16 +743,18 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
             pending = delta
         be.add_rms_norm_gemv_bf16(xs[cur], lm, logits, delta=pending, w_norm=final_norm)
 
-    route_bytes = bytes_route_decode(pos, d, bs, local, prompt_blocks)
+    route_bytes = bytes_route_decode(pos, d, bs, local, prompt_blocks) + 4 * be.KEY_SEGMENT_WORDS
     # The attention reads the K and V rows of the keys the mask keeps (the
-    # local window and the selected blocks), the mask, q, and writes its out
-    # and split records; `live` is counted from the route of layer 0.
+    # local window and the selected blocks, listed as segments), the
+    # segments, q, and writes its out and split records; `live` is counted
+    # from the route of layer 0.
     route(Ls[0])
     live = int(torch.isfinite(mask).sum().item())
-    fixed_attend = b["attend"] - 2 * cap * width * 4        # q, out and the split records
+    assert live == int(segs[1].item()), "the segments' live count is the mask's"
+    fixed_attend = bytes_attend(0, heads, hd, seg_splits)    # q, out and the split records
 
     def kv_bytes(elem):
-        return 2 * live * width * elem + fixed_attend + 2 * width * elem + cap * 4
+        return 2 * live * width * elem + fixed_attend + 2 * width * elem + 4 * be.KEY_SEGMENT_WORDS
     proj_bytes = bytes_gemv(3 * width + 2 * d, hidden)
     attn_fixed = b["add_rms_norm"] + b["rope"] + route_bytes + proj_bytes + bytes_gemv(hidden, width)
     dense_bytes = 3 * dense_ffn * hidden * 2

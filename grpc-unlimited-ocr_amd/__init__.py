@@ -195,6 +195,9 @@ _SIGNATURES = {
     "uocr_rocm_route_step": ([_vp, _vp, _i64, _vp, _vp, _i64, _vp, ctypes.POINTER(RouteParams), _vp], _int),
     "uocr_rocm_route_decode_step": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64,
                                      _vp, _vp, _i64, _vp, ctypes.POINTER(RouteParams), _i64, _vp, _vp, _vp], _int),
+    "uocr_rocm_route_decode_step_segments": ([_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
+                                              _i64, _vp, _vp, _i64, _vp, ctypes.POINTER(RouteParams), _i64, _vp, _vp,
+                                              _vp, _vp], _int),
     "uocr_rocm_scale_mask_softmax_rows": ([_vp, _vp, _f32, _vp, _i64, _i64, _i64], _int),
     "uocr_rocm_embed_add_rms_norm_step": ([_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _f32], _int),
     "uocr_rocm_embed_add_rms_norm_step_bf16": ([_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _f32], _int),
@@ -205,6 +208,11 @@ _SIGNATURES = {
                                                         _vp, _i64, _vp], _int),
     "uocr_rocm_attend_rope_kv_step": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp,
                                        _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_attend_segments_scratch_floats": ([_i64, _i64, _i64], _i64),
+    "uocr_rocm_attend_rope_kv_step_segments": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _f32, _vp, _vp,
+                                                _i64, _vp, _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_attend_rope_kv_step_segments_bf16": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _f32, _vp,
+                                                     _vp, _i64, _vp, _i64, _vp, _i64, _vp], _int),
     "uocr_rocm_expert_topk": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp], _int),
     "uocr_rocm_expert_scratch_floats": ([_i64, _i64], _i64),
     "uocr_rocm_expert_ffn_one": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp], _int),
@@ -825,21 +833,30 @@ def route_step(z, block_min, block_max, state, params, mask, stream=None):
         _ptr(state), ctypes.byref(params), _ptr(mask))
 
 
+MAX_KEY_SEGMENTS = 33  # UOCR_ROCM_MAX_KEY_SEGMENTS
+KEY_SEGMENT_WORDS = 4 * (1 + MAX_KEY_SEGMENTS)
+
+
 def route_decode_step(rq, rk, q_norm, k_norm, eps, inv_tok, inv_page, page_mod, head_cls, router_keys, summaries,
-                      block_min, block_max, state, params, mask, z_out=None, rqk_out=None, stream=None):
+                      block_min, block_max, state, params, mask, z_out=None, rqk_out=None, segments=None,
+                      stream=None):
     """The router half of a decode step in one launch: router norms, rope,
     the router key's append, the block summary, the scores and the route into
-    mask [capacity] (keys 0..pos). router_keys [capacity, d]."""
+    mask [capacity] (keys 0..pos). router_keys [capacity, d]. segments (int32
+    [KEY_SEGMENT_WORDS] or None) receives the keys the mask keeps: the count,
+    the live keys, then {first key, keys, bias bits, 0} per segment."""
     d = rq.numel()
     capacity = router_keys.numel() // d
     n_tok = 0 if inv_tok is None else inv_tok.numel()
     pb = 0 if block_min is None else block_min.numel()
     if mask.numel() < capacity:
         raise ValueError("route_decode_step: mask [capacity]")
-    _op("uocr_rocm_route_decode_step", stream, _f32_param(rq), _f32_param(rk), _f32_param(q_norm), _f32_param(k_norm),
-        eps, _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod, _f32_param(head_cls), _ptr(router_keys),
-        _ptr(summaries), d, _i64_param(block_min), _i64_param(block_max), pb, _ptr(state), ctypes.byref(params),
-        capacity, _ptr(mask), _ptr(z_out), _ptr(rqk_out))
+    if segments is not None and (segments.dtype != _torch().int32 or segments.numel() < KEY_SEGMENT_WORDS):
+        raise ValueError("route_decode_step: segments int32 [KEY_SEGMENT_WORDS]")
+    _op("uocr_rocm_route_decode_step_segments", stream, _f32_param(rq), _f32_param(rk), _f32_param(q_norm),
+        _f32_param(k_norm), eps, _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod, _f32_param(head_cls),
+        _ptr(router_keys), _ptr(summaries), d, _i64_param(block_min), _i64_param(block_max), pb, _ptr(state),
+        ctypes.byref(params), capacity, _ptr(mask), _ptr(z_out), _ptr(rqk_out), _ptr(segments))
 
 
 # ---- fused decode-step ops -------------------------------------------------------------------
@@ -908,6 +925,31 @@ def attend_rope_kv_step(q, k_row, v_row, k_cache, v_cache, heads, hd, mask, scal
     _op(name, stream, _ptr(q), _ptr(k_row), _ptr(v_row), _ptr(k_cache), _ptr(v_cache),
         heads, hd, _f32_param(mask), scale, _ptr(state), _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod,
         _ptr(scratch), capacity, _ptr(out))
+
+
+def attend_segments_scratch_floats(heads, hd, max_live):
+    """Scratch floats of attend_rope_kv_step_segments."""
+    return int(lib().uocr_rocm_attend_segments_scratch_floats(heads, hd, max_live))
+
+
+def attend_rope_kv_step_segments(q, k_row, v_row, k_cache, v_cache, heads, hd, segments, max_live, scale, state,
+                                 inv_tok, inv_page, page_mod, scratch, out, stream=None):
+    """attend_rope_kv_step over the live keys that route_decode_step listed in
+    segments (int32) instead of a mask; max_live bounds their count and fixes
+    the split count."""
+    capacity = k_cache.numel() // (heads * hd) if heads * hd else 0
+    if segments.dtype != _torch().int32 or segments.numel() < KEY_SEGMENT_WORDS:
+        raise ValueError("segments must be int32 [KEY_SEGMENT_WORDS]")
+    if scratch.numel() < attend_segments_scratch_floats(heads, hd, max_live):
+        raise ValueError("scratch is smaller than attend_segments_scratch_floats(heads, hd, max_live)")
+    n_tok = 0 if inv_tok is None else inv_tok.numel()
+    bf = _is_bf16(k_cache)
+    if _is_bf16(v_cache) != bf:
+        raise ValueError("k_cache and v_cache must share a dtype")
+    name = "uocr_rocm_attend_rope_kv_step_segments_bf16" if bf else "uocr_rocm_attend_rope_kv_step_segments"
+    _op(name, stream, _ptr(q), _ptr(k_row), _ptr(v_row), _ptr(k_cache), _ptr(v_cache), heads, hd, _ptr(segments),
+        max_live, scale, _ptr(state), _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod, _ptr(scratch),
+        capacity, _ptr(out))
 
 
 # ---- mixture of experts at decode -------------------------------------------------------------

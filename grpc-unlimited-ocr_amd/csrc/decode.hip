@@ -34,6 +34,13 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int64_t kMaxHeadDim = 256;
 constexpr int kMaxSplits = 128;
 constexpr int kMaskTile = 2048;
+// The live-key segments a routed step attends to (the key segments of
+// uocr_rocm.h):
+// a header of 4 words and up to kMaxKeySegments segments of 4 words.
+constexpr int kMaxKeySegments = UOCR_ROCM_MAX_KEY_SEGMENTS;
+constexpr int kSegWords = 4 * (1 + kMaxKeySegments);
+// Live keys per split when the attention walks the live segments.
+constexpr int kLiveKeysPerSplit = 32;
 
 // ---- append ---------------------------------------------------------------------
 
@@ -96,6 +103,8 @@ struct AttendArgs {
   const float* inv_page;
   int64_t page_mod;
   int n_tok;
+  // With segments (kSegs): the live keys as segments, in place of the mask.
+  const int* segs;
 };
 
 __device__ __forceinline__ float exp_shift(float s, float m) { return __builtin_amdgcn_exp2f((s - m) * kLog2e); }
@@ -120,9 +129,14 @@ struct Running {
 
 __device__ __forceinline__ float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
-template <class TC, int VW, int G, int VPL, int U, bool kRope, bool kEarly>
+// kSegs: the split owns a run of the live keys (the segments' keys in
+// order) instead of a run of positions; each tile stages its keys' positions
+// and biases in LDS, and split 0 appends the step's key and value (a
+// workgroup that meets key pos takes it from its own rotated copy).
+template <class TC, int VW, int G, int VPL, int U, bool kRope, bool kEarly, bool kSegs = false>
 __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   static_assert(kRope || !kEarly, "the early first batch is the rope kernel's (and only without a mask)");
+  static_assert(!(kSegs && kEarly), "the early first batch needs no mask and no segments");
   constexpr bool kBf16 = sizeof(TC) == 2;
   const TC* kc = static_cast<const TC*>(a.k);
   const TC* vc = static_cast<const TC*>(a.v);
@@ -135,6 +149,8 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   constexpr int64_t kStride = static_cast<int64_t>(kSlots) * U;  // keys per lane-group batch
   static_assert(kMaskTile % kStride == 0, "mask tiles hold whole batches");
   __shared__ float s_mask[kMaskTile];
+  __shared__ int s_key[kSegs ? kMaskTile : 1];
+  __shared__ int s_seg[kSegs ? kSegWords : 1];
   __shared__ float s_m[kSlots];
   __shared__ float s_l[kSlots];
   __shared__ float s_acc[kSlots * G * kPerLane];
@@ -150,6 +166,12 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   const int64_t pos = a.state->pos;
   int64_t keys = pos + 1;
   keys = keys < 0 ? 0 : (keys > a.capacity ? a.capacity : keys);
+  if constexpr (kSegs) {
+    for (int t = static_cast<int>(threadIdx.x); t < kSegWords; t += kBlock) s_seg[t] = a.segs[t];
+    __syncthreads();
+    const int64_t live = s_seg[1];
+    keys = pos < 0 || pos >= a.capacity || live < 0 ? 0 : live;
+  }
   const int64_t chunk = (keys + a.splits - 1) / a.splits;
   const int64_t first = split * chunk;
   const int64_t last = first + chunk < keys ? first + chunk : keys;
@@ -173,26 +195,31 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   // replaced by 0), so the loop has no branch around a load and the next
   // batch's loads stay in flight while the current batch is scored.
   auto issue = [&](KeyBatch<TC, VW, VPL, U>& b, int64_t jb, int64_t t0, int64_t t1) {
+    int64_t kp[U];  // the keys' positions
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
       const bool in = j < t1;
-      b.mk[u] = in ? (a.mask != nullptr ? s_mask[j - t0] : 0.0f) : -INFINITY;
-      b.is_new[u] = kRope && in && j == pos;
+      if constexpr (kSegs) {
+        kp[u] = in ? s_key[j - t0] : 0;
+        b.mk[u] = in ? s_mask[j - t0] : -INFINITY;
+      } else {
+        kp[u] = j;
+        b.mk[u] = in ? (a.mask != nullptr ? s_mask[j - t0] : 0.0f) : -INFINITY;
+      }
+      b.is_new[u] = kRope && in && kp[u] == pos;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
       const bool live = b.mk[u] != -INFINITY && !b.is_new[u];
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) b.k[u][i].load(live ? kc + j * a.width + col[i] : dead + col[i]);
+      for (int i = 0; i < VPL; ++i) b.k[u][i].load(live ? kc + kp[u] * a.width + col[i] : dead + col[i]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = jb + static_cast<int64_t>(kSlots) * u;
       const bool live = b.mk[u] != -INFINITY && !b.is_new[u];
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) b.v[u][i].load(live ? vc + j * a.width + col[i] : dead + col[i]);
+      for (int i = 0; i < VPL; ++i) b.v[u][i].load(live ? vc + kp[u] * a.width + col[i] : dead + col[i]);
     }
   };
 
@@ -237,8 +264,10 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
     }
     if (p < a.hd) s_new[2][p] = kBf16 ? round_bf16(vr) : vr;
     __syncthreads();
-    // The split that holds key pos appends the head's rotated k and its v.
-    if (pos >= first && pos < last) {
+    // The split that holds key pos appends the head's rotated k and its v
+    // (with segments: split 0, whether or not key pos is live).
+    const bool appends = kSegs ? split == 0 && pos >= 0 && pos < a.capacity : pos >= first && pos < last;
+    if (appends) {
       for (int t = threadIdx.x; t < a.hd; t += kBlock) {
         Chunk<TC, 1> kk, vv;
         kk.narrow({s_new[1][t]});
@@ -329,10 +358,31 @@ __global__ __launch_bounds__(kBlock) void attend_partial(const AttendArgs a) {
   // Key tiles: the mask of a tile is staged in LDS by the whole workgroup
   // (one coalesced load per thread per 256 keys); without a mask the split
   // is one tile.
-  const int64_t tile = a.mask != nullptr ? kMaskTile : (last > first ? last - first : 1);
+  const int64_t tile = kSegs || a.mask != nullptr ? kMaskTile : (last > first ? last - first : 1);
   for (int64_t t0 = first; t0 < last; t0 += tile) {
     const int64_t t1 = t0 + tile < last ? t0 + tile : last;
-    if (a.mask != nullptr) {
+    if constexpr (kSegs) {
+      // live key j of this tile: the segment holding it (segments in key
+      // order), its position (at most pos) and its bias
+      __syncthreads();  // the previous tile's readers are done
+      const int nseg = s_seg[0] < kMaxKeySegments ? s_seg[0] : kMaxKeySegments;
+      for (int64_t j = t0 + threadIdx.x; j < t1; j += kBlock) {
+        int64_t cum = 0, key = 0;
+        float bias = -INFINITY;
+        for (int g = 0; g < nseg; ++g) {
+          const int64_t len = s_seg[4 * (1 + g) + 1];
+          if (j < cum + len) {
+            key = s_seg[4 * (1 + g)] + (j - cum);
+            bias = __int_as_float(s_seg[4 * (1 + g) + 2]);
+            break;
+          }
+          cum += len;
+        }
+        s_key[j - t0] = static_cast<int>(key < 0 ? 0 : (key > pos ? pos : key));
+        s_mask[j - t0] = bias;
+      }
+      __syncthreads();
+    } else if (a.mask != nullptr) {
       constexpr int kPer = kMaskTile / kBlock;
       float mv[kPer];
 #pragma unroll
@@ -483,9 +533,22 @@ int attend_splits(int64_t heads, int64_t hd, int64_t capacity, int64_t elem_byte
   return static_cast<int>(s < 1 ? 1 : s);
 }
 
+// Splits over a routed step's live keys: kLiveKeysPerSplit each for the
+// most live keys a call can have, at most 64 (one merge wave).
+int segment_splits(int64_t max_live) {
+  const int64_t s = (max_live + kLiveKeysPerSplit - 1) / kLiveKeysPerSplit;
+  return static_cast<int>(s < 1 ? 1 : (s > kWave ? kWave : s));
+}
+
 template <class TC, int VW, int G, int VPL, int U, bool kRope>
 void launch_partial(hipStream_t s, const AttendArgs& a, int64_t heads) {
   const unsigned blocks = static_cast<unsigned>(heads * a.splits);
+  if constexpr (kRope) {
+    if (a.segs != nullptr) {
+      attend_partial<TC, VW, G, VPL, U, true, false, true><<<blocks, kBlock, 0, s>>>(a);
+      return;
+    }
+  }
   if (kRope && a.mask == nullptr) {
     attend_partial<TC, VW, G, VPL, U, kRope, kRope><<<blocks, kBlock, 0, s>>>(a);
   } else {
@@ -647,6 +710,47 @@ int attend_rope(const char* what, void* stream, const float* q, const float* k_r
   return attend_entry<TC, true>(what, stream, a, heads, out);
 }
 
+template <class TC>
+int attend_rope_segments(const char* what, void* stream, const float* q, const float* k_row, const float* v_row,
+                         TC* k_cache, TC* v_cache, int64_t heads, int64_t hd, const int32_t* segments,
+                         int64_t max_live, float scale, const uocr_rocm_step_state* state, const float* inv_tok,
+                         int64_t n_tok, const float* inv_page, int64_t page_mod, float* scratch, int64_t capacity,
+                         float* out) {
+  UOCR_REQUIRE(heads >= 0 && hd >= 0, what, "heads and hd must be >= 0");
+  if (heads == 0 || hd == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(hd % 2 == 0, what, "head dim must be even and at most 256");
+  if (const int st = check_attend(what, heads, hd, capacity)) return st;
+  UOCR_REQUIRE(max_live >= 1 && max_live <= capacity, what, "max_live must be in [1, capacity]");
+  UOCR_REQUIRE(n_tok >= 0 && n_tok <= hd / 2, what, "n_tok must be in [0, hd / 2]");
+  UOCR_REQUIRE(n_tok == 0 || inv_tok != nullptr, what, "null inv_tok");
+  UOCR_REQUIRE(n_tok == hd / 2 || inv_page != nullptr, what, "null inv_page");
+  UOCR_REQUIRE(q != nullptr && k_row != nullptr && v_row != nullptr && k_cache != nullptr && v_cache != nullptr &&
+                   segments != nullptr && state != nullptr && scratch != nullptr && out != nullptr,
+               what, "null pointer");
+  AttendArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.mask = nullptr;
+  a.segs = segments;
+  a.part = scratch;
+  a.state = state;
+  a.width = heads * hd;
+  a.capacity = capacity;
+  a.scale = scale;
+  a.hd = static_cast<int>(hd);
+  a.splits = segment_splits(max_live);
+  a.k_row = k_row;
+  a.v_row = v_row;
+  a.k_out = k_cache;
+  a.v_out = v_cache;
+  a.inv_tok = inv_tok;
+  a.inv_page = inv_page;
+  a.page_mod = page_mod;
+  a.n_tok = static_cast<int>(n_tok);
+  return attend_entry<TC, true>(what, stream, a, heads, out);
+}
+
 }  // namespace
 
 // uocr_rocm_attend_step's body under a caller-chosen name (the entry point
@@ -698,6 +802,33 @@ int uocr_rocm_attend_rope_kv_step(void* stream, const float* q, const float* k_r
                                   float* out) {
   return attend_rope("uocr_rocm_attend_rope_kv_step", stream, q, k_row, v_row, k_cache, v_cache, heads, hd, mask,
                      scale, state, inv_tok, n_tok, inv_page, page_mod, scratch, capacity, out);
+}
+
+int64_t uocr_rocm_attend_segments_scratch_floats(int64_t heads, int64_t hd, int64_t max_live) {
+  if (heads <= 0 || hd <= 0 || max_live <= 0) return 0;
+  return heads * segment_splits(max_live) * (hd + 2);
+}
+
+int uocr_rocm_attend_rope_kv_step_segments(void* stream, const float* q, const float* k_row, const float* v_row,
+                                           float* k_cache, float* v_cache, int64_t heads, int64_t hd,
+                                           const int32_t* segments, int64_t max_live, float scale,
+                                           const uocr_rocm_step_state* state, const float* inv_tok, int64_t n_tok,
+                                           const float* inv_page, int64_t page_mod, float* scratch, int64_t capacity,
+                                           float* out) {
+  return attend_rope_segments("uocr_rocm_attend_rope_kv_step_segments", stream, q, k_row, v_row, k_cache, v_cache,
+                              heads, hd, segments, max_live, scale, state, inv_tok, n_tok, inv_page, page_mod, scratch,
+                              capacity, out);
+}
+
+int uocr_rocm_attend_rope_kv_step_segments_bf16(void* stream, const float* q, const float* k_row, const float* v_row,
+                                                uint16_t* k_cache, uint16_t* v_cache, int64_t heads, int64_t hd,
+                                                const int32_t* segments, int64_t max_live, float scale,
+                                                const uocr_rocm_step_state* state, const float* inv_tok,
+                                                int64_t n_tok, const float* inv_page, int64_t page_mod,
+                                                float* scratch, int64_t capacity, float* out) {
+  return attend_rope_segments("uocr_rocm_attend_rope_kv_step_segments_bf16", stream, q, k_row, v_row, k_cache,
+                              v_cache, heads, hd, segments, max_live, scale, state, inv_tok, n_tok, inv_page, page_mod,
+                              scratch, capacity, out);
 }
 
 int uocr_rocm_attend_rope_kv_step_bf16(void* stream, const float* q, const float* k_row, const float* v_row,

@@ -381,8 +381,13 @@ __device__ __forceinline__ void route_candidates(const PageRanges& r, int nblk, 
 // the bias on the keys of a valid selected block, -inf elsewhere and past
 // pos (attention_plan.cpp:34-56). Every thread of a kRouteBlock block must
 // call it.
+// segs (decode only; null: none) receives the keys the mask keeps as
+// segments in ascending key order (the key segments of uocr_rocm.h):
+// words 0 and 1 the segment count and the live key count, then per segment
+// {first key, keys, bias bits, 0}: the valid selections by block, each
+// clipped at the local window and at pos, then the window itself.
 __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys, const RouteArgs p, RouteLds sh,
-                             float* __restrict__ mask) {
+                             float* __restrict__ mask, int* __restrict__ segs = nullptr) {
 #pragma clang fp contract(off)
 #pragma unroll
   for (int i = 0; i < kBlocksPerThread; ++i) {
@@ -449,9 +454,47 @@ __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys
     const bool valid = lane < k && sh.cand[blk] != 0;
     const float logp = logf(fmaxf(prob, p.floor));
     const float logp_sum = readlane_f32(prefix_in_order<kMaxTop - 1>(valid ? logp : 0.0f), k - 1);
-    const int count = __popcll(__ballot(valid));
+    const uint64_t vmask = __ballot(valid);
+    const int count = __popcll(vmask);
     const float mu = logp_sum / static_cast<float>(count > 1 ? count : 1);
-    if (valid) sh.block_bias[blk] = (logp - mu) / p.sigma;
+    const float bias = (logp - mu) / p.sigma;
+    if (valid) sh.block_bias[blk] = bias;
+    if (segs != nullptr) {
+      const int64_t wkeys = static_cast<int64_t>(p.local_blocks) * p.block_size;
+      const int64_t wfirst = pos - wkeys + 1 > 0 ? pos - wkeys + 1 : 0;  // first key of the window
+      const int64_t wlen = wkeys > 0 ? pos - wfirst + 1 : 0;
+      // this lane's rank among the valid selections, by block
+      int rank = 0;
+#pragma unroll
+      for (int j = 0; j < kMaxTop; ++j) {
+        const int bj = __builtin_amdgcn_readlane(blk, j);
+        rank += ((vmask >> j) & 1) != 0 && bj < blk ? 1 : 0;
+      }
+      const int64_t first = static_cast<int64_t>(blk) * p.block_size;
+      int64_t end = first + p.block_size;
+      const int64_t stop = wkeys > 0 ? wfirst : pos + 1;  // remote keys end at the window (or at pos)
+      end = end < stop ? end : stop;
+      const int len = valid && end > first ? static_cast<int>(end - first) : 0;
+      const int live = static_cast<int>(wave_sum(static_cast<float>(len))) + static_cast<int>(wlen);
+      if (valid) {
+        int* sg = segs + 4 * (1 + rank);
+        sg[0] = static_cast<int>(first);
+        sg[1] = len;
+        sg[2] = __float_as_int(bias);
+        sg[3] = 0;
+      }
+      if (lane == 0) {
+        if (wlen > 0) {
+          int* sg = segs + 4 * (1 + count);
+          sg[0] = static_cast<int>(wfirst);
+          sg[1] = static_cast<int>(wlen);
+          sg[2] = __float_as_int(0.0f);
+          sg[3] = 0;
+        }
+        segs[0] = count + (wlen > 0 ? 1 : 0);
+        segs[1] = live;
+      }
+    }
   }
   lds_barrier();
 
@@ -640,6 +683,7 @@ struct DecodeRouteArgs {
   float* mask;           // [capacity]; keys 0..pos written
   float* z_out;          // null, or [capacity blocks]: the scores the route read
   float* rqk_out;        // null, or [2 d]: rq and rk after norm and rope
+  int* segs;             // null, or the live keys as segments (route_select)
 };
 
 // The router's RMSNorm of one row of d floats held four per lane (lanes with
@@ -776,7 +820,8 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
 
   // 5. the selection and the key mask over keys 0..pos
   route_select(zs, nblk, pos, pos + 1, a.p,
-               RouteLds{zs, cand, keys, reinterpret_cast<uint64_t*>(keys + kMaxRouteBlocks), any_slots}, a.mask);
+               RouteLds{zs, cand, keys, reinterpret_cast<uint64_t*>(keys + kMaxRouteBlocks), any_slots}, a.mask,
+               a.segs);
 }
 
 // ---- host side -----------------------------------------------------------------------------
@@ -901,6 +946,19 @@ int uocr_rocm_route_decode_step(void* stream, const float* rq, const float* rk, 
                                 int64_t prompt_blocks, const uocr_rocm_step_state* state,
                                 const uocr_rocm_route_params* params, int64_t capacity, float* mask, float* z_out,
                                 float* rqk_out) {
+  return uocr_rocm_route_decode_step_segments(stream, rq, rk, q_norm, k_norm, eps, inv_tok, n_tok, inv_page, page_mod,
+                                              head_cls, router_keys, summaries, d, block_min, block_max,
+                                              prompt_blocks, state, params, capacity, mask, z_out, rqk_out, nullptr);
+}
+
+int uocr_rocm_route_decode_step_segments(void* stream, const float* rq, const float* rk, const float* q_norm,
+                                         const float* k_norm, float eps, const float* inv_tok, int64_t n_tok,
+                                         const float* inv_page, int64_t page_mod, const float* head_cls,
+                                         float* router_keys, float* summaries, int64_t d, const int64_t* block_min,
+                                         const int64_t* block_max, int64_t prompt_blocks,
+                                         const uocr_rocm_step_state* state, const uocr_rocm_route_params* params,
+                                         int64_t capacity, float* mask, float* z_out, float* rqk_out,
+                                         int32_t* segments) {
   constexpr const char* kWhat = "uocr_rocm_route_decode_step";
   RouteArgs p;
   if (const int st = check_params(kWhat, params, &p)) return st;
@@ -919,7 +977,7 @@ int uocr_rocm_route_decode_step(void* stream, const float* rq, const float* rk, 
                "router_keys and summaries must be 16-byte aligned");
   DecodeRouteArgs a{rq, rk, q_norm, k_norm, eps, inv_tok, static_cast<int>(n_tok), inv_page, page_mod, head_cls,
                     router_keys, summaries, static_cast<int>(d), inv_sqrt(d), block_min, block_max, prompt_blocks,
-                    state, capacity, p, mask, z_out, rqk_out};
+                    state, capacity, p, mask, z_out, rqk_out, segments};
   clear_launch_error();
   route_decode_k<<<1, kRouteBlock, 0, as_stream(stream)>>>(a);
   return check_launch(kWhat);

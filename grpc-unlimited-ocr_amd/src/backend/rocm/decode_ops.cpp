@@ -150,11 +150,40 @@ void route_decode_step(const Context& ctx, const float* rq, const float* rk, con
                        std::int64_t page_mod, const float* head_cls, float* router_keys, float* summaries,
                        std::int64_t d, const std::int64_t* block_min, const std::int64_t* block_max,
                        std::int64_t prompt_blocks, const StepState* state, const RouteParams& params,
-                       std::int64_t capacity, float* mask, float* z_out, float* rqk_out) {
+                       std::int64_t capacity, float* mask, float* z_out, float* rqk_out, std::int32_t* segments) {
   const auto p = abi(params);
-  check(uocr_rocm_route_decode_step(ctx.stream(), rq, rk, q_norm, k_norm, eps, inv_tok, n_tok, inv_page, page_mod,
-                                    head_cls, router_keys, summaries, d, block_min, block_max, prompt_blocks,
-                                    abi(state), &p, capacity, mask, z_out, rqk_out));
+  check(uocr_rocm_route_decode_step_segments(ctx.stream(), rq, rk, q_norm, k_norm, eps, inv_tok, n_tok, inv_page,
+                                             page_mod, head_cls, router_keys, summaries, d, block_min, block_max,
+                                             prompt_blocks, abi(state), &p, capacity, mask, z_out, rqk_out,
+                                             segments));
+}
+
+static_assert(kMaxKeySegments == UOCR_ROCM_MAX_KEY_SEGMENTS, "the segment layout of include/uocr_rocm.h");
+
+std::int64_t attend_segments_scratch_floats(std::int64_t heads, std::int64_t hd, std::int64_t max_live) {
+  return uocr_rocm_attend_segments_scratch_floats(heads, hd, max_live);
+}
+
+void attend_rope_kv_step_segments(const Context& ctx, const float* q, const float* k_row, const float* v_row,
+                                  float* k_cache, float* v_cache, std::int64_t heads, std::int64_t hd,
+                                  const std::int32_t* segments, std::int64_t max_live, float scale,
+                                  const StepState* state, const float* inv_tok, std::int64_t n_tok,
+                                  const float* inv_page, std::int64_t page_mod, float* scratch,
+                                  std::int64_t capacity, float* out) {
+  check(uocr_rocm_attend_rope_kv_step_segments(ctx.stream(), q, k_row, v_row, k_cache, v_cache, heads, hd, segments,
+                                               max_live, scale, abi(state), inv_tok, n_tok, inv_page, page_mod,
+                                               scratch, capacity, out));
+}
+
+void attend_rope_kv_step_segments_bf16(const Context& ctx, const float* q, const float* k_row, const float* v_row,
+                                       std::uint16_t* k_cache, std::uint16_t* v_cache, std::int64_t heads,
+                                       std::int64_t hd, const std::int32_t* segments, std::int64_t max_live,
+                                       float scale, const StepState* state, const float* inv_tok,
+                                       std::int64_t n_tok, const float* inv_page, std::int64_t page_mod,
+                                       float* scratch, std::int64_t capacity, float* out) {
+  check(uocr_rocm_attend_rope_kv_step_segments_bf16(ctx.stream(), q, k_row, v_row, k_cache, v_cache, heads, hd,
+                                                    segments, max_live, scale, abi(state), inv_tok, n_tok, inv_page,
+                                                    page_mod, scratch, capacity, out));
 }
 
 }  // namespace uocr::rocm

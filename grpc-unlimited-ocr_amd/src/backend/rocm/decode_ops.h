@@ -102,6 +102,37 @@ void route_decode_step(const Context& ctx, const float* rq, const float* rk, con
                        std::int64_t page_mod, const float* head_cls, float* router_keys, float* summaries,
                        std::int64_t d, const std::int64_t* block_min, const std::int64_t* block_max,
                        std::int64_t prompt_blocks, const StepState* state, const RouteParams& params,
-                       std::int64_t capacity, float* mask, float* z_out = nullptr, float* rqk_out = nullptr);
+                       std::int64_t capacity, float* mask, float* z_out = nullptr, float* rqk_out = nullptr,
+                       std::int32_t* segments = nullptr);
+
+// New: the keys a routed step reads as segments (segments != null above):
+// kKeySegmentWords int32, {segment count, live keys, 0, 0} and then per
+// segment {first key, keys, bias bits, 0} in key order (the selected blocks,
+// clipped at the local window, then the window).
+constexpr std::int64_t kMaxKeySegments = 33;
+constexpr std::int64_t kKeySegmentWords = 4 * (1 + kMaxKeySegments);
+// The most keys the block router lets one step read: the local window and
+// top_k (at least one) whole blocks.
+inline std::int64_t max_live_keys(const RouteParams& p) {
+  return ((p.top_k > 1 ? p.top_k : 1) + p.local_blocks) * p.block_size;
+}
+
+// New: attend_rope_kv_step over those segments' keys alone instead of a mask
+// (each split walks a run of the live keys); max_live bounds the live keys
+// of every call and fixes the split count. Scratch:
+// attend_segments_scratch_floats(heads, hd, max_live) floats.
+std::int64_t attend_segments_scratch_floats(std::int64_t heads, std::int64_t hd, std::int64_t max_live);
+void attend_rope_kv_step_segments(const Context& ctx, const float* q, const float* k_row, const float* v_row,
+                                  float* k_cache, float* v_cache, std::int64_t heads, std::int64_t hd,
+                                  const std::int32_t* segments, std::int64_t max_live, float scale,
+                                  const StepState* state, const float* inv_tok, std::int64_t n_tok,
+                                  const float* inv_page, std::int64_t page_mod, float* scratch,
+                                  std::int64_t capacity, float* out);
+void attend_rope_kv_step_segments_bf16(const Context& ctx, const float* q, const float* k_row, const float* v_row,
+                                       std::uint16_t* k_cache, std::uint16_t* v_cache, std::int64_t heads,
+                                       std::int64_t hd, const std::int32_t* segments, std::int64_t max_live,
+                                       float scale, const StepState* state, const float* inv_tok,
+                                       std::int64_t n_tok, const float* inv_page, std::int64_t page_mod,
+                                       float* scratch, std::int64_t capacity, float* out);
 
 }  // namespace uocr::rocm

@@ -36,6 +36,9 @@
 // router's logits are formed in the shared experts' gate/up launch, the top
 // k inside the routed experts' gate/up launch, and the shared experts' down
 // product and the routed experts' sum in the routed experts' down launch.
+// The router also lists the keys its mask keeps (at most the local window
+// and top_k blocks), and the attention's splits walk that list rather than
+// every mask entry.
 
 #include <cstdint>
 #include <memory>
@@ -203,6 +206,8 @@ class DecodeStep {
   const std::uint16_t* lm_head_;
   std::int64_t length_ = 0, last_pos_ = -1, capacity_blocks_ = 0, prompt_blocks_ = 0;
   Array inv_tok_, inv_page_, state_, x_[2], h_, delta_, proj_, attn_, o_, act_, mask_, logits_, scratch_;
+  Array segments_;  // the router's live keys of the current layer (kKeySegmentWords int32)
+  std::int64_t max_live_ = 1;
   Array block_min_, block_max_;
   Array router_logits_, expert_ids_, expert_weights_, expert_scratch_;
   std::vector<Array> k_cache_, v_cache_, router_keys_, summaries_;

@@ -660,6 +660,24 @@ UOCR_ROCM_API int uocr_rocm_route_decode_step(void* stream, const float* rq, con
                                               const uocr_rocm_route_params* params, int64_t capacity, float* mask,
                                               float* z_out, float* rqk_out);
 
+/* The keys a routed decode query reads, so that its attention visits them
+ * alone (the key segments): int32 [4 (1 + UOCR_ROCM_MAX_KEY_SEGMENTS)],
+ * word 0 the segment count, word 1 the live key count, then per segment
+ * {first key, key count, bias (fp32 bits), 0} in ascending key order: the
+ * valid selected blocks, each clipped at the local window (and at pos), then
+ * the window itself, every key with the value the mask gives it. */
+#define UOCR_ROCM_MAX_KEY_SEGMENTS 33
+/* uocr_rocm_route_decode_step that also writes the mask's live keys as
+ * segments (new; the reference has no counterpart: its attend_step walks the
+ * whole mask, src/backend/cuda/decode_ops.cu:112-195). The mask is written as
+ * before. */
+UOCR_ROCM_API int uocr_rocm_route_decode_step_segments(
+    void* stream, const float* rq, const float* rk, const float* q_norm, const float* k_norm, float eps,
+    const float* inv_tok, int64_t n_tok, const float* inv_page, int64_t page_mod, const float* head_cls,
+    float* router_keys, float* summaries, int64_t d, const int64_t* block_min, const int64_t* block_max,
+    int64_t prompt_blocks, const uocr_rocm_step_state* state, const uocr_rocm_route_params* params, int64_t capacity,
+    float* mask, float* z_out, float* rqk_out, int32_t* segments);
+
 /* ---- fused decode-step ops (new) ---------------------------------------------
  * One launch where the reference's decode step makes several; each gives
  * bitwise the result of the unfused entry points it replaces. */
@@ -743,6 +761,33 @@ UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step_bf16(void* stream, const float* 
                                                      const uocr_rocm_step_state* state, const float* inv_tok,
                                                      int64_t n_tok, const float* inv_page, int64_t page_mod,
                                                      float* scratch, int64_t capacity, float* out);
+
+/* uocr_rocm_attend_rope_kv_step over the live keys of a routed step
+ * (segments from uocr_rocm_route_decode_step_segments) instead of a mask: the
+ * same rope, appends and attention, each split walking a run of the live keys
+ * (new; the mask-walking attend_step of the reference,
+ * src/backend/cuda/decode_ops.cu:112-195, reads every mask entry). max_live:
+ * the most live keys any call of this launch shape has ((max(top_k, 1) +
+ * local_blocks) * block_size for the block router); it fixes the split count,
+ * so a captured step keeps its launch shape. scratch holds
+ * uocr_rocm_attend_segments_scratch_floats(heads, hd, max_live) floats. */
+UOCR_ROCM_API int64_t uocr_rocm_attend_segments_scratch_floats(int64_t heads, int64_t hd, int64_t max_live);
+UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step_segments(void* stream, const float* q, const float* k_row,
+                                                         const float* v_row, float* k_cache, float* v_cache,
+                                                         int64_t heads, int64_t hd, const int32_t* segments,
+                                                         int64_t max_live, float scale,
+                                                         const uocr_rocm_step_state* state, const float* inv_tok,
+                                                         int64_t n_tok, const float* inv_page, int64_t page_mod,
+                                                         float* scratch, int64_t capacity, float* out);
+/* The same over a bf16 cache (as uocr_rocm_attend_rope_kv_step_bf16). */
+UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step_segments_bf16(void* stream, const float* q, const float* k_row,
+                                                              const float* v_row, uint16_t* k_cache,
+                                                              uint16_t* v_cache, int64_t heads, int64_t hd,
+                                                              const int32_t* segments, int64_t max_live, float scale,
+                                                              const uocr_rocm_step_state* state,
+                                                              const float* inv_tok, int64_t n_tok,
+                                                              const float* inv_page, int64_t page_mod, float* scratch,
+                                                              int64_t capacity, float* out);
 
 /* ---- mixture of experts at decode ------------------------------------------ */
 

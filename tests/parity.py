@@ -93,3 +93,55 @@ def host_f32(t) -> np.ndarray:
 def normal(seed, shape, scale=1.0, loc=0.0) -> np.ndarray:
     g = np.random.default_rng(seed)
     return (loc + scale * g.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+
+
+# ---- key segments of a routed decode step ----------------------------------------------------
+
+MAX_KEY_SEGMENTS = 33
+KEY_SEGMENT_WORDS = 4 * (1 + MAX_KEY_SEGMENTS)
+
+
+def key_segments(pos, block_size, local_blocks, blocks, biases) -> np.ndarray:
+    """The segments layout (int32 [KEY_SEGMENT_WORDS]) for a decode query at
+    pos that keeps the given remote blocks (ascending) with their biases and
+    the local window: each block clipped at the window's first key (or at
+    pos), then the window with bias 0."""
+    segs = np.zeros(KEY_SEGMENT_WORDS, np.int32)
+    wkeys = local_blocks * block_size
+    wfirst = max(pos - wkeys + 1, 0)
+    wlen = pos - wfirst + 1 if wkeys > 0 else 0
+    stop = wfirst if wkeys > 0 else pos + 1
+    live, n = 0, 0
+    for b, bias in zip(blocks, biases):
+        first = b * block_size
+        ln = max(0, min(first + block_size, stop) - first)
+        segs[4 * (1 + n):4 * (2 + n)] = [first, ln, np.float32(bias).view(np.int32), 0]
+        live += ln
+        n += 1
+    if wlen > 0:
+        segs[4 * (1 + n):4 * (2 + n)] = [wfirst, wlen, 0, 0]
+        n += 1
+    segs[0], segs[1] = n, live + wlen
+    return segs
+
+
+def mask_from_segments(segs, pos) -> np.ndarray:
+    """The key mask [pos + 1] that segments describe (-inf off them), after
+    checking the layout: segments in ascending key order, none past pos, the
+    live count their sum."""
+    segs = np.asarray(segs, np.int32)
+    n, live = int(segs[0]), int(segs[1])
+    assert 0 <= n <= MAX_KEY_SEGMENTS, f"segment count {n}"
+    mask = np.full(pos + 1, -np.inf, np.float32)
+    total, end = 0, 0
+    for g in range(n):
+        first, ln = int(segs[4 * (1 + g)]), int(segs[4 * (1 + g) + 1])
+        assert ln >= 0, f"segment {g} length {ln}"
+        if ln == 0:
+            continue
+        assert first >= end and first + ln <= pos + 1, f"segment {g} [{first}, {first + ln}) after {end}, pos {pos}"
+        mask[first:first + ln] = segs[4 * (1 + g) + 2:4 * (1 + g) + 3].view(np.float32)[0]
+        total += ln
+        end = first + ln
+    assert total == live, f"live {live} against {total} keys in the segments"
+    return mask

@@ -7,6 +7,10 @@ and is checked against the oracle directly as well:
   add_rms_norm_gemv_bf16         == add_rms_norm (or rms_norm) -> gemv_bf16
   add_rms_norm_swiglu_gemv_bf16  == add_rms_norm -> gemv gate, gemv up -> silu_mul
   attend_rope_kv_step            == rope_qk_step -> append_step x2 -> attend_step
+  attend_rope_kv_step_segments   == attend_rope_kv_step under the mask the
+                                    segments describe (the same caches
+                                    bitwise, the output within 1e-5: its
+                                    splits sum in another order)
 
 and a whole decode layer built from them replays in a graph bitwise like the
 layer built from the unfused ops (the reference's decode_body order,
@@ -16,7 +20,8 @@ import numpy as np
 import pytest
 
 import oracle
-from parity import assert_bf16_close, assert_f32_close, dev_bf16, dev_f32, dev_i64, host_f32, normal
+from parity import (assert_bf16_close, assert_f32_close, dev_bf16, dev_f32, dev_i64, host_f32, key_segments,
+                    mask_from_segments, normal)
 
 pytestmark = pytest.mark.gpu
 
@@ -331,3 +336,83 @@ def test_attend_rope_kv_bf16_cache_matches_unfused(backend, heads, hd, cap, pos,
     rq = oracle.rope(host_f32(q), heads, hd, inv_tok=host_f32(inv), one_tok=pos)
     want = oracle.attention_one(rq, kf, vf, heads, hd, None if mask is None else host_f32(mask)[:keys], scale)
     assert_f32_close(host_f32(out2), want, 1e-5, "attend_rope_kv bf16 cache")
+
+
+@pytest.mark.parametrize("heads,hd,cap,pos,bs,local,nsel,max_live,dtype", [
+    (10, 128, 8192, 5000, 32, 4, 8, 384, "f32"),    # the decoder's router: 8 blocks and the window
+    (10, 128, 8192, 5000, 32, 4, 8, 384, "bf16"),
+    (10, 128, 4096, 4095, 64, 1, 32, 2112, "f32"),  # 33 segments, the step at the cache's end
+    (10, 128, 2048, 1500, 32, 0, 8, 256, "bf16"),   # no window: key pos off the segments
+    (10, 128, 2048, 1500, 32, 0, 0, 32, "f32"),     # nothing live
+    (10, 128, 2048, 100, 32, 4, 0, 384, "f32"),     # the window alone
+    (10, 128, 2048, 1500, 32, 4, 8, 1, "f32"),      # max_live below the live keys: one split
+    (2, 66, 600, 500, 16, 2, 5, 112, "f32"),        # a head that is not whole 16-byte chunks
+    (4, 256, 10000, 9999, 64, 2, 12, 896, "bf16"),  # 256-wide heads past 8192 positions
+    (3, 128, 512, 0, 32, 4, 0, 160, "f32")])        # the first step
+def test_attend_rope_kv_segments_matches_mask(backend, heads, hd, cap, pos, bs, local, nsel, max_live, dtype):
+    width = heads * hd
+    g = np.random.default_rng(390 + pos)
+    q, k_row, v_row = dev_f32(normal(391, width)), dev_f32(normal(392, width)), dev_f32(normal(393, width))
+    inv = dev_f32(oracle.rope_inv(hd // 2, 1e4))
+    remote = max(0, (pos - local * bs + 1) // bs) if local else pos // bs + 1
+    blocks = np.sort(g.choice(remote, size=min(nsel, remote), replace=False)) if remote else np.zeros(0, np.int64)
+    biases = (g.standard_normal(blocks.size) * 0.7).astype(np.float32)
+    segs_host = key_segments(pos, bs, local, blocks, biases)
+    mask_host = np.full(cap, -np.inf, np.float32)
+    mask_host[:pos + 1] = mask_from_segments(segs_host, pos)
+    segs = torch.from_numpy(segs_host).cuda()
+    state = state_of(pos, tok=pos, page=pos // 7)
+    scale = float(1 / np.sqrt(hd))
+    if dtype == "bf16":
+        kc0, vc0 = oracle.f32_to_bf16(normal(394, (cap, width))), oracle.f32_to_bf16(normal(395, (cap, width)))
+        mk = dev_bf16
+    else:
+        kc0, vc0 = normal(394, (cap, width)), normal(395, (cap, width))
+        mk = dev_f32
+    scratch1 = torch.empty(backend.attend_scratch_floats(heads, hd, cap), device="cuda")
+    kc1, vc1 = mk(kc0), mk(vc0)
+    out1 = torch.empty(width, device="cuda")
+    backend.attend_rope_kv_step(q, k_row, v_row, kc1, vc1, heads, hd, dev_f32(mask_host), scale, state, inv, None, 0,
+                                scratch1, out1)
+    scratch2 = torch.full((backend.attend_segments_scratch_floats(heads, hd, max_live),), float("nan"), device="cuda")
+    kc2, vc2 = mk(kc0), mk(vc0)
+    out2 = torch.full((width,), float("nan"), device="cuda")
+    backend.attend_rope_kv_step_segments(q, k_row, v_row, kc2, vc2, heads, hd, segs, max_live, scale, state, inv,
+                                         None, 0, scratch2, out2)
+    if dtype == "bf16":
+        assert torch.equal(kc2.view(torch.int16), kc1.view(torch.int16))
+        assert torch.equal(vc2.view(torch.int16), vc1.view(torch.int16))
+        kf = oracle.bf16_to_f32(kc2.view(torch.int16).cpu().numpy().view(np.uint16))[:pos + 1]
+        vf = oracle.bf16_to_f32(vc2.view(torch.int16).cpu().numpy().view(np.uint16))[:pos + 1]
+    else:
+        assert np.array_equal(bits(kc2), bits(kc1)) and np.array_equal(bits(vc2), bits(vc1))
+        kf, vf = host_f32(kc2)[:pos + 1], host_f32(vc2)[:pos + 1]
+    got = host_f32(out2)
+    if int(segs_host[1]) == 0:
+        assert np.array_equal(got, np.zeros(width, np.float32))  # no live key: zeros, as under an all -inf mask
+        assert np.array_equal(host_f32(out1), got)
+        return
+    assert_f32_close(got, host_f32(out1), 1e-5, "segments against the mask")
+    rq = oracle.rope(host_f32(q), heads, hd, inv_tok=host_f32(inv), one_tok=pos)
+    want = oracle.attention_one(rq, kf, vf, heads, hd, mask_host[:pos + 1], scale)
+    assert_f32_close(got, want, 1e-5, "segments against the oracle")
+
+
+def test_attend_segments_rejects_bad_arguments(backend):
+    heads, hd, cap = 2, 64, 128
+    q = torch.zeros(heads * hd, device="cuda")
+    kc, vc = torch.zeros(cap, heads * hd, device="cuda"), torch.zeros(cap, heads * hd, device="cuda")
+    segs = torch.zeros(4 * 34, dtype=torch.int32, device="cuda")
+    scratch = torch.empty(backend.attend_segments_scratch_floats(heads, hd, 64 * 32), device="cuda")  # 64 splits
+    out = torch.empty(heads * hd, device="cuda")
+    st = state_of(3)
+    inv = dev_f32(oracle.rope_inv(hd // 2, 1e4))
+    with pytest.raises(ValueError, match="max_live"):  # past the capacity
+        backend.attend_rope_kv_step_segments(q, q, q, kc, vc, heads, hd, segs, cap + 1, 1.0, st, inv, None, 0,
+                                             scratch, out)
+    with pytest.raises(ValueError, match="max_live"):
+        backend.attend_rope_kv_step_segments(q, q, q, kc, vc, heads, hd, segs, 0, 1.0, st, inv, None, 0, scratch,
+                                             out)
+    with pytest.raises(ValueError, match="int32"):  # float32 segments
+        backend.attend_rope_kv_step_segments(q, q, q, kc, vc, heads, hd, torch.zeros(4 * 34, device="cuda"), 32, 1.0,
+                                             st, inv, None, 0, scratch, out)

@@ -12,7 +12,9 @@ tests/test_oracle.py pins bit for bit to the reference's own code):
     each bias is within 1e-6 (the device's logf against the host's);
   * the one-launch router half of a decode step equals the separate steps
     bitwise on the same rotated router rows, and a sequence of decode steps
-    keeps the router-key cache and summaries the oracle keeps.
+    keeps the router-key cache and summaries the oracle keeps;
+  * the live-key segments it lists describe exactly its key mask (bitwise,
+    biases included) under several router settings.
 
 Edge cases follow the reference's rules: no block before the window (only
 the window is attended), exact score ties (the lower block first), page
@@ -23,7 +25,7 @@ import numpy as np
 import pytest
 
 import oracle
-from parity import assert_f32_close, dev_f32, dev_i64, host_f32, normal
+from parity import KEY_SEGMENT_WORDS, assert_f32_close, dev_f32, dev_i64, host_f32, mask_from_segments, normal
 
 pytestmark = pytest.mark.gpu
 
@@ -194,9 +196,10 @@ def test_route_decode_step_is_the_separate_steps(backend):
     rkc, sm = dev_f32(cache), dev_f32(summ_full)
     mask = torch.full((cap,), float("nan"), device="cuda")
     z_out, rqk = torch.empty(cap // BS, device="cuda"), torch.empty(2 * D, device="cuda")
+    segs = torch.full((KEY_SEGMENT_WORDS,), -7, dtype=torch.int32, device="cuda")
     backend.route_decode_step(dev_f32(rq), dev_f32(rk), dev_f32(qn), dev_f32(kn), 1e-6, dev_f32(inv_tok),
                               dev_f32(inv_page), 2, dev_f32(cls), rkc, sm, dev_i64(lo), dev_i64(hi), st, p, mask,
-                              z_out=z_out, rqk_out=rqk)
+                              z_out=z_out, rqk_out=rqk, segments=segs)
     rot = host_f32(rqk)
     # the rotated rows against the oracle: router norm (fp64 sum) then the page rope
     tok, page = np.array([pos], np.int64), np.array([5], np.int64)
@@ -223,6 +226,7 @@ def test_route_decode_step_is_the_separate_steps(backend):
     m1, m2 = host_f32(mask), host_f32(mask2)
     assert np.array_equal(m1[:pos + 1].view(np.uint32), m2[:pos + 1].view(np.uint32))
     assert np.all(np.isnan(m1[pos + 1:]))  # only keys 0..pos are written
+    assert np.array_equal(mask_from_segments(segs.cpu().numpy(), pos).view(np.uint32), m1[:pos + 1].view(np.uint32))
     # and the mask is the oracle's selection on these scores
     assert_same_route(m1[:pos + 1], oracle_mask(host_f32(z_out), pos, oracle.RouterParams(), lo, hi, 1), "fused")
 
@@ -239,6 +243,7 @@ def test_route_decode_steps_in_sequence(backend):
     sm = torch.zeros(cap // BS, D, device="cuda")
     mask = torch.empty(cap, device="cuda")
     z_out, rqk = torch.empty(cap // BS, device="cuda"), torch.empty(2 * D, device="cuda")
+    segs = torch.empty(KEY_SEGMENT_WORDS, dtype=torch.int32, device="cuda")
     dqn, dkn, dcls, dt, dp = dev_f32(qn), dev_f32(kn), dev_f32(cls), dev_f32(inv_tok), dev_f32(inv_page)
     host_rk = np.zeros((cap, D), np.float32)
     g = np.random.default_rng(373)
@@ -247,7 +252,10 @@ def test_route_decode_steps_in_sequence(backend):
         rq, rk = (g.standard_normal(D) * 3).astype(np.float32), (g.standard_normal(D) * 3).astype(np.float32)
         st = state_of(pos, tok=pos, page=pos // 300)
         backend.route_decode_step(dev_f32(rq), dev_f32(rk), dqn, dkn, 1e-6, dt, dp, 2, dcls, rkc, sm, None, None, st,
-                                  p, mask, z_out=z_out, rqk_out=rqk)
+                                  p, mask, z_out=z_out, rqk_out=rqk, segments=segs)
+        got_mask = host_f32(mask)[:pos + 1]
+        assert np.array_equal(mask_from_segments(segs.cpu().numpy(), pos).view(np.uint32), got_mask.view(np.uint32)), \
+            f"segments at step {pos}"
         rot = host_f32(rqk)
         host_rk[pos] = rot[D:]
         if pos % 37 == 0 or pos == steps - 1:
@@ -263,6 +271,44 @@ def test_route_decode_steps_in_sequence(backend):
             checked += 1
     assert np.array_equal(host_f32(rkc)[:steps], host_rk[:steps])
     assert checked >= 19
+
+
+@pytest.mark.parametrize("block_size,local_blocks,top_m,top_k,floor", [
+    (32, 0, 16, 8, 1e-6), (32, 4, 16, 1, 1e-6), (64, 1, 32, 32, 1e-6), (16, 2, 8, 8, 0.0), (32, 2, 1, 1, 1e-6)])
+def test_route_segments_describe_the_mask(backend, block_size, local_blocks, top_m, top_k, floor):
+    """The live-key segments of decode steps 0..N under other router settings
+    (no local window: key pos itself live only when selected; one selection;
+    32 selections of 64-key blocks, 33 segments; a zero floor, whose unsupported
+    selections carry a -inf bias), each step against the step's own mask
+    bitwise and its live count within the most a step can keep."""
+    cap, steps = 4096, 600 if block_size != 64 else 2400
+    p = backend.RouteParams()
+    p.block_size, p.local_blocks, p.top_m, p.top_k, p.floor = block_size, local_blocks, top_m, top_k, floor
+    inv_tok, inv_page = rope_tables()
+    qn, kn, cls = normal(380, D, 0.05), normal(381, D, 0.05), normal(382, D)
+    rkc = torch.zeros(cap, D, device="cuda")
+    sm = torch.zeros(cap // block_size, D, device="cuda")
+    mask = torch.empty(cap, device="cuda")
+    segs = torch.empty(KEY_SEGMENT_WORDS, dtype=torch.int32, device="cuda")
+    dqn, dkn, dcls, dt, dp = dev_f32(qn), dev_f32(kn), dev_f32(cls), dev_f32(inv_tok), dev_f32(inv_page)
+    g = np.random.default_rng(383)
+    rows = (g.standard_normal((steps, 2, D)) * 3).astype(np.float32)
+    most = (max(top_k, 1) + local_blocks) * block_size
+    biggest = 0
+    for pos in range(steps):
+        st = state_of(pos, tok=pos, page=pos // 300)
+        backend.route_decode_step(dev_f32(rows[pos, 0]), dev_f32(rows[pos, 1]), dqn, dkn, 1e-6, dt, dp, 2, dcls, rkc,
+                                  sm, None, None, st, p, mask, segments=segs)
+        if pos % 7 and pos < steps - 40:
+            continue
+        hs = segs.cpu().numpy()
+        got_mask = host_f32(mask)[:pos + 1]
+        assert np.array_equal(mask_from_segments(hs, pos).view(np.uint32), got_mask.view(np.uint32)), \
+            f"segments at step {pos}"
+        assert int(hs[1]) <= most
+        biggest = max(biggest, int(hs[0]))
+    if block_size == 64:
+        assert biggest == top_k + local_blocks  # every selection and the window listed
 
 
 def test_route_rejects_bad_shapes(backend):
