@@ -634,15 +634,17 @@ def expert_ffn(be, torch, timer, hidden, ffn, experts, k):
     return report("expert_ffn_one", nbytes, ms)
 
 
-def bytes_route_decode(pos, d, block_size, local_blocks, prompt_blocks):
+def bytes_route_decode(pos, d, block_size, local_blocks, prompt_blocks, mask=True, segment_words=0):
     """The router half of a decode step (route_decode_step) at pos: R rq, rk,
     both norms and head_cls; R the block's earlier router keys, W the new
     one; W the block's summary, R the remote blocks' summaries; R the prompt
-    blocks' page ranges; W the key mask over keys 0..pos."""
+    blocks' page ranges; W the key mask over keys 0..pos (when asked for) and
+    the live-key segments."""
     blk = pos // block_size
     n = pos - blk * block_size + 1
     nrem = max(blk - local_blocks + 1, 0)
-    return 4 * (5 * d + (n - 1) * d + d + d + nrem * d + pos + 1) + 16 * prompt_blocks
+    return (4 * (5 * d + (n - 1) * d + d + d + nrem * d + (pos + 1 if mask else 0) + segment_words)
+            + 16 * prompt_blocks)
 
 
 def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vocab, layers=12):
@@ -710,9 +712,11 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
     q, k, v = proj[:width], proj[width:2 * width], proj[2 * width:3 * width]
     rq, rk = proj[3 * width:3 * width + d], proj[3 * width + d:]
 
-    def route(L):
+    def route(L, with_mask=False):
+        # the step lists the live keys alone (the key mask is for checking)
         be.route_decode_step(rq, rk, L["rqn"], L["rkn"], 1e-6, inv_tok, inv_page, page_mod, L["cls"], L["rkeys"],
-                             L["summ"], block_min, block_max, state, params, mask, segments=segs)
+                             L["summ"], block_min, block_max, state, params, mask if with_mask else None,
+                             segments=segs)
 
     def step():
         cur = 0
@@ -743,12 +747,13 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
             pending = delta
         be.add_rms_norm_gemv_bf16(xs[cur], lm, logits, delta=pending, w_norm=final_norm)
 
-    route_bytes = bytes_route_decode(pos, d, bs, local, prompt_blocks) + 4 * be.KEY_SEGMENT_WORDS
+    route_bytes = bytes_route_decode(pos, d, bs, local, prompt_blocks, mask=False, segment_words=be.KEY_SEGMENT_WORDS)
     # The attention reads the K and V rows of the keys the mask keeps (the
     # local window and the selected blocks, listed as segments), the
     # segments, q, and writes its out and split records; `live` is counted
     # from the route of layer 0.
-    route(Ls[0])
+    mask.fill_(float("-inf"))
+    route(Ls[0], with_mask=True)
     live = int(torch.isfinite(mask).sum().item())
     assert live == int(segs[1].item()), "the segments' live count is the mask's"
     fixed_attend = bytes_attend(0, heads, hd, seg_splits)    # q, out and the split records

@@ -844,13 +844,14 @@ def route_decode_step(rq, rk, q_norm, k_norm, eps, inv_tok, inv_page, page_mod, 
     the router key's append, the block summary, the scores and the route into
     mask [capacity] (keys 0..pos). router_keys [capacity, d]. segments (int32
     [KEY_SEGMENT_WORDS] or None) receives the keys the mask keeps: the count,
-    the live keys, then {first key, keys, bias bits, 0} per segment."""
+    the live keys, then {first key, keys, bias bits, 0} per segment; with
+    segments, mask may be None (not written)."""
     d = rq.numel()
     capacity = router_keys.numel() // d
     n_tok = 0 if inv_tok is None else inv_tok.numel()
     pb = 0 if block_min is None else block_min.numel()
-    if mask.numel() < capacity:
-        raise ValueError("route_decode_step: mask [capacity]")
+    if (mask is None and segments is None) or (mask is not None and mask.numel() < capacity):
+        raise ValueError("route_decode_step: mask [capacity] (or None with segments)")
     if segments is not None and (segments.dtype != _torch().int32 or segments.numel() < KEY_SEGMENT_WORDS):
         raise ValueError("route_decode_step: segments int32 [KEY_SEGMENT_WORDS]")
     _op("uocr_rocm_route_decode_step_segments", stream, _f32_param(rq), _f32_param(rk), _f32_param(q_norm),

@@ -110,8 +110,8 @@ __device__ void summarize(const float* keys, int n, int d, const float (&cls)[4]
     const float a = lane < n ? p[lane] : -3.402823466e+38f;
     const float peak = wave_max(a);
     const float w = lane < n ? expf(a - peak) : 0.0f;
-    // the sum over t in order; lanes past n add +0, which changes nothing
-    float total = readlane_f32(prefix_in_order<kWave - 1>(w), kWave - 1);
+    // the sum over t in order (lanes past n hold +0, which adds nothing)
+    float total = n <= 32 ? readlane_f32(prefix_in_order<31>(w), 31) : readlane_f32(prefix_in_order<kWave - 1>(w), kWave - 1);
     total = fmaxf(total, 1e-6f);
     if (lane < n) p[lane] = w / total;
   }
@@ -249,26 +249,33 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
   return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-// The wave's largest key, in every lane: a DPP butterfly inside each 16-lane
-// row, then the four row maxima. Every lane of the wave must be active.
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
-  uint64_t o = dpp_u64<0xB1>(v);
-  v = o > v ? o : v;
-  o = dpp_u64<0x4E>(v);
-  v = o > v ? o : v;
-  o = dpp_u64<0x141>(v);
-  v = o > v ? o : v;
-  o = dpp_u64<0x140>(v);
-  v = o > v ? o : v;
-  const uint64_t r0 = readlane_u64(v, 0), r1 = readlane_u64(v, 16), r2 = readlane_u64(v, 32),
-                 r3 = readlane_u64(v, 48);
-  const uint64_t a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
-  return a > b ? a : b;
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+
+// The wave's largest of v (unsigned), in every lane: a DPP butterfly inside
+// each 16-lane row, then the four row maxima. Every lane must be active.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  v = umax(v, dpp_u32<0xB1>(v));   // lane ^ 1
+  v = umax(v, dpp_u32<0x4E>(v));   // lane ^ 2
+  v = umax(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = umax(v, dpp_u32<0x140>(v));  // row_mirror
+  const uint32_t r0 = __builtin_amdgcn_readlane(static_cast<int>(v), 0);
+  const uint32_t r1 = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(static_cast<int>(v), 32);
+  const uint32_t r3 = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
+  return umax(umax(r0, r1), umax(r2, r3));
 }
 
 // The m largest of the wave's keys (S per lane, m <= 64): lane j returns the
 // j-th largest (0 past the wave's keys). Each lane sorts its S keys, then m
-// rounds take the largest head and the winning lane drops it.
+// rounds take the largest head and the winning lane drops it. A round finds
+// the largest high word (the score); the low word (the block) decides only
+// between lanes whose heads share it, the common single holder taking a
+// readlane instead. Keys are distinct apart from empty slots (0), so the
+// winner is the lane holding the wave's largest key.
 template <int S>
 __device__ __forceinline__ uint64_t wave_top(uint64_t (&key)[S], int m, int lane) {
 #pragma unroll
@@ -280,15 +287,34 @@ __device__ __forceinline__ uint64_t wave_top(uint64_t (&key)[S], int m, int lane
       key[j + 1] = a > b ? b : a;
     }
   }
-  uint64_t mine = 0;
-#pragma unroll 4
-  for (int j = 0; j < m; ++j) {
-    const uint64_t win = wave_max_key(key[0]);
-    if (lane == j) mine = win;
-    if (key[0] == win) {
+  uint32_t hi[S], lo[S];
 #pragma unroll
-      for (int i = 0; i + 1 < S; ++i) key[i] = key[i + 1];
-      key[S - 1] = 0;
+  for (int i = 0; i < S; ++i) {
+    hi[i] = static_cast<uint32_t>(key[i] >> 32);
+    lo[i] = static_cast<uint32_t>(key[i]);
+  }
+  uint64_t mine = 0;
+  for (int j = 0; j < m; ++j) {
+    const uint32_t top = wave_max_u32(hi[0]);
+    const uint64_t tied = __ballot(hi[0] == top);
+    uint32_t top_lo;
+    int winner;
+    if ((tied & (tied - 1)) == 0) {
+      winner = __builtin_ctzll(tied);
+      top_lo = __builtin_amdgcn_readlane(static_cast<int>(lo[0]), winner);
+    } else {
+      top_lo = wave_max_u32(hi[0] == top ? lo[0] : 0u);
+      winner = __builtin_ctzll(__ballot(hi[0] == top && lo[0] == top_lo));
+    }
+    if (lane == j) mine = (static_cast<uint64_t>(top) << 32) | top_lo;
+    if (lane == winner) {
+#pragma unroll
+      for (int i = 0; i + 1 < S; ++i) {
+        hi[i] = hi[i + 1];
+        lo[i] = lo[i + 1];
+      }
+      hi[S - 1] = 0;
+      lo[S - 1] = 0;
     }
   }
   return mine;
@@ -382,7 +408,8 @@ __device__ __forceinline__ void route_candidates(const PageRanges& r, int nblk, 
 // pos (attention_plan.cpp:34-56). Every thread of a kRouteBlock block must
 // call it.
 // segs (decode only; null: none) receives the keys the mask keeps as
-// segments in ascending key order (the key segments of uocr_rocm.h):
+// segments in ascending key order (the key segments of uocr_rocm.h); with
+// segs, mask may be null (not written).
 // words 0 and 1 the segment count and the live key count, then per segment
 // {first key, keys, bias bits, 0}: the valid selections by block, each
 // clipped at the local window and at pos, then the window itself.
@@ -406,15 +433,40 @@ __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys
   constexpr int kSlice = 4 * kWave;  // blocks per wave
   uint64_t mine = 0;
   if (nblk <= kSlice) {
-    if (wave == 0) {
-      uint64_t key[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int b = lane + kWave * i;
-        key[i] = b < nblk ? order_key(sh.x[b], b) : 0;
-      }
-      mine = wave_top<4>(key, m, lane);
+    // By rank: the keys are distinct, so a block's place in the order is
+    // the count of keys above it. Thread (q, b) counts the keys of quarter q
+    // above block b's; the quarters' counts add in LDS, and each block with
+    // a rank below m puts its key at that rank.
+    static_assert(kRouteBlock == 4 * kSlice, "four quarters of the blocks");
+    uint64_t* key_of = sh.list;                                // [kSlice]
+    int* rank = reinterpret_cast<int*>(sh.list + kSlice);      // [kSlice]
+    uint64_t* top = sh.list + kSlice + kSlice / 2;             // [kMaxTop]
+    const int t = static_cast<int>(threadIdx.x);
+    if (t < kSlice) {
+      key_of[t] = t < nblk ? order_key(sh.x[t], t) : 0;
+      rank[t] = 0;
+      if (t < kMaxTop) top[t] = 0;
     }
+    lds_barrier();
+    // the slots past nblk hold 0, below every key, so every thread counts
+    // its quarter's 64 slots with the same unrolled loop (LDS broadcasts)
+    const int b = t & (kSlice - 1);
+    const int q = __builtin_amdgcn_readfirstlane(t / kSlice);
+    const uint64_t own = key_of[b];
+    const uint64_t* quarter = key_of + q * (kSlice / 4);
+    int above = 0;
+#pragma unroll
+    for (int j = 0; j < kSlice / 4; j += 2) {
+      const u32x4 two = *reinterpret_cast<const u32x4*>(quarter + j);
+      const uint64_t k0 = (static_cast<uint64_t>(two.y) << 32) | two.x;
+      const uint64_t k1 = (static_cast<uint64_t>(two.w) << 32) | two.z;
+      above += (k0 > own ? 1 : 0) + (k1 > own ? 1 : 0);
+    }
+    if (b < nblk) atomicAdd(&rank[b], above);
+    lds_barrier();
+    if (t < nblk && rank[t] < m) top[rank[t]] = key_of[t];
+    lds_barrier();
+    if (wave == 0 && lane < m) mine = top[lane];
   } else {
     // each wave's top m of its slice, then wave 0 takes the top m of those
     uint64_t key[4];
@@ -441,7 +493,10 @@ __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys
     const float val = have ? key_value(mine) : 0.0f;
     const float peak = readlane_f32(val, 0);
     const float v = have ? (val - peak) / 2.0f : 0.0f;
-    const float sum = prefix_in_order<kMaxTop - 1>(v), sum_sq = prefix_in_order<kMaxTop - 1>(v * v);
+    // running sums in lane order over the first m lanes (the later lanes'
+    // sums are never read)
+    auto prefix = [m](float x) { return m <= 16 ? prefix_in_order<15>(x) : prefix_in_order<kMaxTop - 1>(x); };
+    const float sum = prefix(v), sum_sq = prefix(v * v);
     const float rho = static_cast<float>(lane + 1);
     const float mean = sum / rho, mean_sq = sum_sq / rho;
     const float ss = rho * (mean_sq - mean * mean);
@@ -453,7 +508,7 @@ __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys
     const float prob = t * t;
     const bool valid = lane < k && sh.cand[blk] != 0;
     const float logp = logf(fmaxf(prob, p.floor));
-    const float logp_sum = readlane_f32(prefix_in_order<kMaxTop - 1>(valid ? logp : 0.0f), k - 1);
+    const float logp_sum = readlane_f32(prefix(valid ? logp : 0.0f), k - 1);
     const uint64_t vmask = __ballot(valid);
     const int count = __popcll(vmask);
     const float mu = logp_sum / static_cast<float>(count > 1 ? count : 1);
@@ -465,8 +520,7 @@ __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys
       const int64_t wlen = wkeys > 0 ? pos - wfirst + 1 : 0;
       // this lane's rank among the valid selections, by block
       int rank = 0;
-#pragma unroll
-      for (int j = 0; j < kMaxTop; ++j) {
+      for (int j = 0; j < k; ++j) {  // the valid lanes are among the first k
         const int bj = __builtin_amdgcn_readlane(blk, j);
         rank += ((vmask >> j) & 1) != 0 && bj < blk ? 1 : 0;
       }
@@ -497,6 +551,7 @@ __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys
     }
   }
   lds_barrier();
+  if (mask == nullptr) return;  // the segments alone (uniform)
 
   const int64_t window = static_cast<int64_t>(p.local_blocks) * p.block_size;
   const uint32_t bs = static_cast<uint32_t>(p.block_size);
@@ -726,10 +781,8 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
 
   // 1. every load that does not wait for another: first those that need no
   // position (the router rows and their weights, head_cls, the rope
-  // frequency of this thread's pair), then the step state, then the block's
-  // earlier keys, the prompt blocks' page ranges and (the remote blocks being
-  // whole, none of them the block summarized here) the first pass of
-  // summaries
+  // frequency of this thread's pair, the page ranges, the first pass of
+  // summaries), then the step state, then the block's earlier keys
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (wave < 2 && 4 * lane < d) {
     const float* src = wave == 0 ? a.rq : a.rk;
@@ -746,6 +799,17 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   float freq = 0.0f;
   if (pr < half) freq = pr < a.n_tok ? a.inv_tok[pr] : a.inv_page[pr - a.n_tok];
 
+  // the prompt blocks' page ranges (route_candidates checks the query's
+  // page and the block count) and, with a local window (the remote blocks
+  // then being whole, none of them the block summarized here), the first
+  // pass of summaries: rows past the remote blocks are read but not used
+  PageRanges ranges;
+  load_pages(a.block_min, a.block_max, a.prompt_blocks, kMaxRouteBlocks, 0, ranges);
+  const bool early = a.p.local_blocks > 0;
+  const int cap_blocks = static_cast<int>((a.capacity + a.p.block_size - 1) / a.p.block_size);
+  ScoreRows rows;
+  if (early) score_load(a.summaries, d, cap_blocks, 0, rows);
+
   const int64_t pos64 = a.state->pos;
   if (pos64 < 0 || pos64 >= a.capacity) return;  // uniform over the block
   // capacity / block_size <= 4096 blocks of at most 64 keys: 32-bit from here
@@ -758,11 +822,6 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   const int64_t query_page = a.state->query_page;
   StagedKeys staged;
   load_keys(a.router_keys, first, n - 1, d, staged);
-  PageRanges ranges;
-  load_pages(a.block_min, a.block_max, a.prompt_blocks, nblk, query_page, ranges);
-  const bool early = a.p.local_blocks > 0;
-  ScoreRows rows;
-  if (early) score_load(a.summaries, d, nrem, 0, rows);
 
   // 2. router norm of rq (wave 0) and rk (wave 1), then rope at (tok, page)
   if (wave < 2) {
@@ -971,7 +1030,8 @@ int uocr_rocm_route_decode_step_segments(void* stream, const float* rq, const fl
   UOCR_REQUIRE(prompt_blocks >= 0 && (prompt_blocks == 0 || (block_min != nullptr && block_max != nullptr)),
                kWhat, "prompt blocks without their pages");
   UOCR_REQUIRE(rq != nullptr && rk != nullptr && q_norm != nullptr && k_norm != nullptr && head_cls != nullptr &&
-                   router_keys != nullptr && summaries != nullptr && state != nullptr && mask != nullptr,
+                   router_keys != nullptr && summaries != nullptr && state != nullptr &&
+                   (mask != nullptr || segments != nullptr),
                kWhat, "null pointer");
   UOCR_REQUIRE(aligned16(router_keys) && aligned16(summaries), kWhat,
                "router_keys and summaries must be 16-byte aligned");

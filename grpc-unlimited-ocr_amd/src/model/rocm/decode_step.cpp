@@ -109,15 +109,13 @@ DecodeStep::DecodeStep(const Context& ctx, const DecoderDims& dims, const std::u
   attn_ = f32(width);
   o_ = f32(d.hidden);
   act_ = f32(max_ffn);
-  mask_ = f32(d.capacity);
   router_logits_ = f32(max_experts);
   expert_ids_ = Array(ctx_, DType::kI64, max_k);
   expert_weights_ = f32(max_k);
   expert_scratch_ = f32(std::max<std::int64_t>(1, expert_scratch_floats(max_k, max_expert_ffn)));
   logits_ = f32(d.vocab);
   max_live_ = std::max<std::int64_t>(1, std::min(max_live_keys(d.router), d.capacity));
-  scratch_ = f32(std::max(attend_scratch_floats(d.heads, d.head_dim, d.capacity),
-                          attend_segments_scratch_floats(d.heads, d.head_dim, max_live_)));
+  scratch_ = f32(attend_segments_scratch_floats(d.heads, d.head_dim, max_live_));
   segments_ = f32(kKeySegmentWords);  // int32 words
   block_min_ = Array(ctx_, DType::kI64, capacity_blocks_);
   block_max_ = Array(ctx_, DType::kI64, capacity_blocks_);
@@ -238,11 +236,8 @@ void DecodeStep::reserve(std::int64_t keys) {
   }
   grow(block_min_, DType::kI64, blocks, prompt_blocks_, 8);
   grow(block_max_, DType::kI64, blocks, prompt_blocks_, 8);
-  mask_ = Array(ctx_, DType::kF32, capacity);
   max_live_ = std::max<std::int64_t>(1, std::min(max_live_keys(d.router), capacity));
-  scratch_ = Array(ctx_, DType::kF32,
-                   std::max(attend_scratch_floats(d.heads, d.head_dim, capacity),
-                            attend_segments_scratch_floats(d.heads, d.head_dim, max_live_)));
+  scratch_ = Array(ctx_, DType::kF32, attend_segments_scratch_floats(d.heads, d.head_dim, max_live_));
   d.capacity = capacity;
   capacity_blocks_ = blocks;
   record();  // the buffers moved: the captured step is recorded again
@@ -292,9 +287,9 @@ void DecodeStep::body() {
     // key's append, the block's summary, the scores and the key mask.
     route_decode_step(ctx_, rq, rk, l.router_q_norm, l.router_k_norm, d.eps, inv_tok_.f32(), n_tok, inv_page,
                       d.page_mod, l.head_cls, router_keys_[li].f32(), summaries_[li].f32(), d.index_dim, block_min,
-                      block_max, prompt_blocks_, st, d.router, d.capacity, mask_.f32(),
-                      d.trace ? trace_z_[li].f32() : nullptr, d.trace ? trace_rqk_[li].f32() : nullptr, segs);
-    if (d.trace) copy(ctx_, trace_mask_[li].f32(), mask_.f32(), d.capacity);
+                      block_max, prompt_blocks_, st, d.router, d.capacity,
+                      d.trace ? trace_mask_[li].f32() : nullptr, d.trace ? trace_z_[li].f32() : nullptr,
+                      d.trace ? trace_rqk_[li].f32() : nullptr, segs);
     if (d.bf16_cache) {
       attend_rope_kv_step_segments_bf16(ctx_, q, k, v, k_cache_[li].bf16(), v_cache_[li].bf16(), d.heads, d.head_dim,
                                         segs, max_live_, scale, st, inv_tok_.f32(), n_tok, inv_page, d.page_mod,

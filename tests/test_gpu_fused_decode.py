@@ -379,6 +379,12 @@ def test_attend_rope_kv_segments_matches_mask(backend, heads, hd, cap, pos, bs, 
     out2 = torch.full((width,), float("nan"), device="cuda")
     backend.attend_rope_kv_step_segments(q, k_row, v_row, kc2, vc2, heads, hd, segs, max_live, scale, state, inv,
                                          None, 0, scratch2, out2)
+    # a second call on the same scratch (the step's key appended again: the
+    # same caches) gives the same output
+    out3 = torch.full((width,), float("nan"), device="cuda")
+    backend.attend_rope_kv_step_segments(q, k_row, v_row, kc2, vc2, heads, hd, segs, max_live, scale, state, inv,
+                                         None, 0, scratch2, out3)
+    assert np.array_equal(bits(out3), bits(out2))
     if dtype == "bf16":
         assert torch.equal(kc2.view(torch.int16), kc1.view(torch.int16))
         assert torch.equal(vc2.view(torch.int16), vc1.view(torch.int16))
