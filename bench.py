@@ -728,9 +728,10 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
             if pending is not None:
                 cur = 1 - cur
             route(L)
+            # the splits' records stay in seg_scratch; the o projection merges them
             be.attend_rope_kv_step_segments(q, k, v, L["kc"], L["vc"], heads, hd, segs, max_live, scale, state,
-                                            inv_tok, inv_page, page_mod, seg_scratch, attn)
-            be.gemv_bf16(attn, L["o"], o)
+                                            inv_tok, inv_page, page_mod, seg_scratch, None)
+            be.attend_merge_gemv_bf16(seg_scratch, heads, hd, max_live, L["o"], o)
             a = act[:L["ffn"]]
             if L["moe"]:  # the shared experts' pair GEMV and the router in one launch
                 be.add_rms_norm_swiglu_router_gemv_bf16(xs[cur], L["gate"], L["up"], a, L["router"], rlogits,
@@ -765,7 +766,7 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
     dense_bytes = 3 * dense_ffn * hidden * 2
     moe_bytes = 3 * shared_ffn * hidden * 2 + experts * hidden * 4 + 3 * top_k * expert_ffn * hidden * 2
     rest = bytes_gather(1, hidden, 4) + dense_bytes + (layers - 1) * moe_bytes + bytes_gemv(vocab, hidden)
-    launches = 2 + 7 + 8 * (layers - 1)
+    launches = 2 + 6 + 7 * (layers - 1)
     ms_route = timer.graph([lambda L=L: route(L) for L in Ls])[0]
     out = {"workload": f"the model's decode step: embedding, layer 0 dense (FFN {dense_ffn}), layers 1-{layers - 1} "
                        f"mixture of experts ({top_k} of {experts} experts of FFN {expert_ffn}, shared FFN "

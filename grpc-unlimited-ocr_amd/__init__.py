@@ -213,6 +213,7 @@ _SIGNATURES = {
                                                 _i64, _vp, _i64, _vp, _i64, _vp], _int),
     "uocr_rocm_attend_rope_kv_step_segments_bf16": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _f32, _vp,
                                                      _vp, _i64, _vp, _i64, _vp, _i64, _vp], _int),
+    "uocr_rocm_attend_merge_gemv_bf16": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp], _int),
     "uocr_rocm_expert_topk": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp], _int),
     "uocr_rocm_expert_scratch_floats": ([_i64, _i64], _i64),
     "uocr_rocm_expert_ffn_one": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp], _int),
@@ -937,7 +938,8 @@ def attend_rope_kv_step_segments(q, k_row, v_row, k_cache, v_cache, heads, hd, s
                                  inv_tok, inv_page, page_mod, scratch, out, stream=None):
     """attend_rope_kv_step over the live keys that route_decode_step listed in
     segments (int32) instead of a mask; max_live bounds their count and fixes
-    the split count."""
+    the split count. out None: the split records stay in scratch for
+    attend_merge_gemv_bf16."""
     capacity = k_cache.numel() // (heads * hd) if heads * hd else 0
     if segments.dtype != _torch().int32 or segments.numel() < KEY_SEGMENT_WORDS:
         raise ValueError("segments must be int32 [KEY_SEGMENT_WORDS]")
@@ -951,6 +953,19 @@ def attend_rope_kv_step_segments(q, k_row, v_row, k_cache, v_cache, heads, hd, s
     _op(name, stream, _ptr(q), _ptr(k_row), _ptr(v_row), _ptr(k_cache), _ptr(v_cache), heads, hd, _ptr(segments),
         max_live, scale, _ptr(state), _f32_param(inv_tok), n_tok, _f32_param(inv_page), page_mod, _ptr(scratch),
         capacity, _ptr(out))
+
+
+def attend_merge_gemv_bf16(scratch, heads, hd, max_live, w, y, bias=None, x_out=None, stream=None):
+    """y = bf16(merge) . w^T (+ bias) where merge is the attention row that
+    attend_rope_kv_step_segments (out=None, the same heads, hd, max_live) left
+    as split records in scratch; x_out receives the merged row."""
+    n, k = w.shape
+    if k != heads * hd or y.numel() != n or (x_out is not None and x_out.numel() != k):
+        raise ValueError("w [n, heads * hd], y [n], x_out [heads * hd]")
+    if scratch.numel() < attend_segments_scratch_floats(heads, hd, max_live):
+        raise ValueError("scratch is smaller than attend_segments_scratch_floats(heads, hd, max_live)")
+    _op("uocr_rocm_attend_merge_gemv_bf16", stream, _ptr(scratch), heads, hd, max_live, _ptr(w), n,
+        _f32_param(bias), _ptr(y), _ptr(x_out))
 
 
 # ---- mixture of experts at decode -------------------------------------------------------------

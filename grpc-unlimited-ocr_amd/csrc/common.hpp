@@ -401,6 +401,24 @@ inline unsigned blocks_for_rows(int64_t rows) {
 constexpr int64_t kPieceRows = int64_t{1} << 20;
 constexpr int64_t kPieceChunks = int64_t{1} << 28;
 
+// ---- split-K decode attention records (decode.hip writes, decode.hip and
+// gemv.hip merge) -----------------------------------------------------------------
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// exp(s - m) through the hardware's base-2 exponential.
+__device__ __forceinline__ float exp_shift(float s, float m) { return __builtin_amdgcn_exp2f((s - m) * kLog2e); }
+
+// Live keys per split when the attention walks a routed step's live-key
+// segments, and the split count for at most max_live live keys: 32 keys
+// each, at most 64 splits (one merge wave).
+constexpr int kLiveKeysPerSplit = 32;
+
+inline int segment_splits(int64_t max_live) {
+  const int64_t s = (max_live + kLiveKeysPerSplit - 1) / kLiveKeysPerSplit;
+  return static_cast<int>(s < 1 ? 1 : (s > kWave ? kWave : s));
+}
+
 template <class Fn>
 void for_each_piece(int64_t total, int64_t piece, Fn&& fn) {
   int64_t first = 0;

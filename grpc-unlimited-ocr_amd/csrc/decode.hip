@@ -30,7 +30,6 @@
 namespace uocr_rocm {
 namespace {
 
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr int64_t kMaxHeadDim = 256;
 constexpr int kMaxSplits = 128;
 constexpr int kMaskTile = 2048;
@@ -39,8 +38,6 @@ constexpr int kMaskTile = 2048;
 // a header of 4 words and up to kMaxKeySegments segments of 4 words.
 constexpr int kMaxKeySegments = UOCR_ROCM_MAX_KEY_SEGMENTS;
 constexpr int kSegWords = 4 * (1 + kMaxKeySegments);
-// Live keys per split when the attention walks the live segments.
-constexpr int kLiveKeysPerSplit = 32;
 
 // ---- append ---------------------------------------------------------------------
 
@@ -107,7 +104,6 @@ struct AttendArgs {
   const int* segs;
 };
 
-__device__ __forceinline__ float exp_shift(float s, float m) { return __builtin_amdgcn_exp2f((s - m) * kLog2e); }
 
 // The K and V chunks of U keys of one lane group, with each key's mask value
 // (-inf for a key that is masked or past the end: such a key is not read).
@@ -504,7 +500,7 @@ __global__ __launch_bounds__(kBlock) void attend_merge(const float* __restrict__
 #pragma unroll
   for (int r = 0; r < kPerWave; ++r) {
     const int sp = wave + kWavesPerBlock * r;
-    acc = fmaf(sp < splits ? s_w[sp] : 0.0f, vals[r], acc);
+    if (sp < splits) acc = fmaf(s_w[sp], vals[r], acc);
   }
   s_red[wave][lane] = acc;
   __syncthreads();
@@ -533,12 +529,6 @@ int attend_splits(int64_t heads, int64_t hd, int64_t capacity, int64_t elem_byte
   return static_cast<int>(s < 1 ? 1 : s);
 }
 
-// Splits over a routed step's live keys: kLiveKeysPerSplit each for the
-// most live keys a call can have, at most 64 (one merge wave).
-int segment_splits(int64_t max_live) {
-  const int64_t s = (max_live + kLiveKeysPerSplit - 1) / kLiveKeysPerSplit;
-  return static_cast<int>(s < 1 ? 1 : (s > kWave ? kWave : s));
-}
 
 template <class TC, int VW, int G, int VPL, int U, bool kRope>
 void launch_partial(hipStream_t s, const AttendArgs& a, int64_t heads) {
@@ -643,6 +633,7 @@ int attend_entry(const char* what, void* stream, AttendArgs a, int64_t heads, fl
     launch_attend_any<TC, kRope>(s, a, heads);
   }
   if (const int st = check_launch(what); st != UOCR_ROCM_OK) return st;
+  if (out == nullptr) return UOCR_ROCM_OK;  // the records stay for a merging consumer
   launch_merge(s, a, heads, out);
   return check_launch(what);
 }
@@ -725,7 +716,7 @@ int attend_rope_segments(const char* what, void* stream, const float* q, const f
   UOCR_REQUIRE(n_tok == 0 || inv_tok != nullptr, what, "null inv_tok");
   UOCR_REQUIRE(n_tok == hd / 2 || inv_page != nullptr, what, "null inv_page");
   UOCR_REQUIRE(q != nullptr && k_row != nullptr && v_row != nullptr && k_cache != nullptr && v_cache != nullptr &&
-                   segments != nullptr && state != nullptr && scratch != nullptr && out != nullptr,
+                   segments != nullptr && state != nullptr && scratch != nullptr,
                what, "null pointer");
   AttendArgs a{};
   a.q = q;

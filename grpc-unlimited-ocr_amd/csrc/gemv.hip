@@ -84,11 +84,80 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int nchunks
   __syncthreads();
 }
 
-// x in registers: CPL chunks per lane; RPW rows per wave per pass.
-template <int CPL, int RPW>
+// The input of the attention's output projection as the split records of
+// its split-K attention (decode.hip's attend_partial): per head, `splits`
+// records of hd + 2 floats (the running max m, the exp-sum l, the weighted
+// value sums). x_out (optional) receives the merged row in fp32.
+struct MergedX {
+  const float* part;
+  int heads, hd, splits;
+  float* x_out;
+};
+
+// bf16(merge(records)) into xs[0 .. heads hd), one wave per (head, 64-element
+// slice), with attend_merge's arithmetic for splits <= 64: the weights
+// w_s = exp(m_s - max m) (0 for an empty split), the total as the wave sum
+// of w_s l_s over the splits in lanes, the value sum as four partials over
+// the splits s = p, p + 4, ... (fma in split order) added as (p0 + p1) +
+// (p2 + p3), and the row as sum / total (0 without a total). Each lane's
+// first 16 value loads go out before the weights are formed. Every thread of
+// the workgroup calls it.
+__device__ __forceinline__ void stage_merged_x(const MergedX& mx, float* xs) {
+  __shared__ float sw[kGemvWaves][kWave];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int slices = (mx.hd + kWave - 1) / kWave;
+  const int64_t rec_len = mx.hd + 2;
+  constexpr int kBatch = 16;
+  for (int u = wave; u < mx.heads * slices; u += kGemvWaves) {
+    const int h = u / slices;
+    const int e = (u - h * slices) * kWave + lane;
+    const int ec = e < mx.hd ? e : mx.hd - 1;
+    const float* recs = mx.part + static_cast<int64_t>(h) * mx.splits * rec_len;
+    const int sc = lane < mx.splits ? lane : mx.splits - 1;
+    float m = recs[sc * rec_len];
+    const float l = recs[sc * rec_len + 1];
+    float val[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) val[j] = recs[(j < mx.splits ? j : mx.splits - 1) * rec_len + 2 + ec];
+    m = lane < mx.splits ? m : -INFINITY;
+    const float big = wave_max(m);
+    const float wgt = (m == -INFINITY || big == -INFINITY) ? 0.0f : exp_shift(m, big);
+    const float total = wave_sum(wgt * l);
+    sw[wave][lane] = wgt;
+    __builtin_amdgcn_wave_barrier();
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < mx.splits; s0 += kBatch) {
+      if (s0 > 0) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int sp = s0 + j;
+          val[j] = recs[(sp < mx.splits ? sp : mx.splits - 1) * rec_len + 2 + ec];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int sp = s0 + j;
+        if (sp < mx.splits) acc[j & 3] = fmaf(sw[wave][sp], val[j], acc[j & 3]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    const float out = total > 0.0f ? sum / total : 0.0f;
+    if (e < mx.hd) {
+      xs[h * mx.hd + e] = round_bf16(out);
+      if (mx.x_out != nullptr && blockIdx.x == 0) mx.x_out[h * mx.hd + e] = out;
+    }
+  }
+  __syncthreads();
+}
+
+// x in registers: CPL chunks per lane; RPW rows per wave per pass. kMerged:
+// x is the merge of split attention records (mx), formed in the prologue.
+template <int CPL, int RPW, bool kMerged = false>
 __global__ __launch_bounds__(kGemvBlock) void gemv_reg(const float* __restrict__ x, int nchunks,
                                                        const uint16_t* __restrict__ w, int64_t n,
-                                                       const float* __restrict__ bias, float* __restrict__ y) {
+                                                       const float* __restrict__ bias, float* __restrict__ y,
+                                                       const MergedX mx = {}) {
   __shared__ __align__(16) float xs[kWave * kGemvRegChunks * 8];
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t k = static_cast<int64_t>(nchunks) * 8;
@@ -117,11 +186,16 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_reg(const float* __restrict__
   // 129280 x 1280 LM head, 100 launches back to back; the same order was 2%
   // slower on the decode projections).
   constexpr bool kManyRows = RPW > 1;
+  static_assert(!(kMerged && kManyRows), "the merged input serves the few-rows kernel");
   if constexpr (kManyRows) {
     stage_x(x, nchunks, xs);
   } else {
     if (g0 < groups) load_w(g0);
-    stage_x(x, nchunks, xs);
+    if constexpr (kMerged) {
+      stage_merged_x(mx, xs);
+    } else {
+      stage_x(x, nchunks, xs);
+    }
   }
   float xv[CPL][8];
 #pragma unroll
@@ -891,6 +965,35 @@ int uocr_rocm_gemv_bf16(void* stream, const float* x, int64_t k, const uint16_t*
     case kGemvRegChunks: launch_reg<kGemvRegChunks>(s, x, nchunks, w, n, bias, y); break;
     default:
       gemv_lds<<<gemv_blocks(n), kBlock, static_cast<size_t>(k) * sizeof(float), s>>>(x, nchunks, w, n, bias, y);
+      break;
+  }
+  return check_launch(what);
+}
+
+int uocr_rocm_attend_merge_gemv_bf16(void* stream, const float* scratch, int64_t heads, int64_t hd,
+                                     int64_t max_live, const uint16_t* w, int64_t n, const float* bias, float* y,
+                                     float* x_out) {
+  const char* what = "uocr_rocm_attend_merge_gemv_bf16";
+  UOCR_REQUIRE(heads >= 1 && hd >= 1 && n >= 0, what, "heads and hd must be >= 1, n >= 0");
+  const int64_t k = heads * hd;
+  UOCR_REQUIRE(k % 8 == 0 && k <= int64_t{kWave} * kGemvRegChunks * 8, what,
+               "heads * hd must be a multiple of 8 and at most 2048");
+  UOCR_REQUIRE(max_live >= 1, what, "max_live must be >= 1");
+  if (n == 0) return UOCR_ROCM_OK;
+  UOCR_REQUIRE(scratch != nullptr && w != nullptr && y != nullptr, what, "null pointer");
+  UOCR_REQUIRE(aligned16(w), what, "w must be 16-byte aligned");
+  UOCR_REQUIRE(n < (int64_t{1} << 40), what, "n too large");
+  const MergedX mx{scratch, static_cast<int>(heads), static_cast<int>(hd), segment_splits(max_live), x_out};
+  const int nchunks = static_cast<int>(k / 8);
+  const hipStream_t s = as_stream(stream);
+  clear_launch_error();
+  const unsigned blocks = gemv_reg_blocks(n);
+  switch ((nchunks + kWave - 1) / kWave) {
+    case 1: gemv_reg<1, 1, true><<<blocks, kGemvBlock, 0, s>>>(nullptr, nchunks, w, n, bias, y, mx); break;
+    case 2: gemv_reg<2, 1, true><<<blocks, kGemvBlock, 0, s>>>(nullptr, nchunks, w, n, bias, y, mx); break;
+    case 3: gemv_reg<3, 1, true><<<blocks, kGemvBlock, 0, s>>>(nullptr, nchunks, w, n, bias, y, mx); break;
+    default:
+      gemv_reg<kGemvRegChunks, 1, true><<<blocks, kGemvBlock, 0, s>>>(nullptr, nchunks, w, n, bias, y, mx);
       break;
   }
   return check_launch(what);

@@ -186,4 +186,10 @@ void attend_rope_kv_step_segments_bf16(const Context& ctx, const float* q, const
                                                     page_mod, scratch, capacity, out));
 }
 
+void attend_merge_gemv_bf16(const Context& ctx, const float* scratch, std::int64_t heads, std::int64_t hd,
+                            std::int64_t max_live, const std::uint16_t* w, std::int64_t n, const float* bias, float* y,
+                            float* x_out) {
+  check(uocr_rocm_attend_merge_gemv_bf16(ctx.stream(), scratch, heads, hd, max_live, w, n, bias, y, x_out));
+}
+
 }  // namespace uocr::rocm

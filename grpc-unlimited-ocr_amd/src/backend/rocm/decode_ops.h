@@ -120,7 +120,8 @@ inline std::int64_t max_live_keys(const RouteParams& p) {
 // New: attend_rope_kv_step over those segments' keys alone instead of a mask
 // (each split walks a run of the live keys); max_live bounds the live keys
 // of every call and fixes the split count. Scratch:
-// attend_segments_scratch_floats(heads, hd, max_live) floats.
+// attend_segments_scratch_floats(heads, hd, max_live) floats. With out null
+// the splits' records stay in scratch for attend_merge_gemv_bf16.
 std::int64_t attend_segments_scratch_floats(std::int64_t heads, std::int64_t hd, std::int64_t max_live);
 void attend_rope_kv_step_segments(const Context& ctx, const float* q, const float* k_row, const float* v_row,
                                   float* k_cache, float* v_cache, std::int64_t heads, std::int64_t hd,
@@ -134,5 +135,11 @@ void attend_rope_kv_step_segments_bf16(const Context& ctx, const float* q, const
                                        float scale, const StepState* state, const float* inv_tok,
                                        std::int64_t n_tok, const float* inv_page, std::int64_t page_mod,
                                        float* scratch, std::int64_t capacity, float* out);
+// New: y = bf16(the merge of those records) . w^T (+ bias) in one launch,
+// bitwise the attention's own merge then gemv_bf16 (the o projection,
+// cuda_decode_step.cpp:42-44); x_out (optional) receives the merged row.
+void attend_merge_gemv_bf16(const Context& ctx, const float* scratch, std::int64_t heads, std::int64_t hd,
+                            std::int64_t max_live, const std::uint16_t* w, std::int64_t n, const float* bias, float* y,
+                            float* x_out = nullptr);
 
 }  // namespace uocr::rocm

@@ -106,7 +106,6 @@ DecodeStep::DecodeStep(const Context& ctx, const DecoderDims& dims, const std::u
   h_ = f32(d.hidden);
   delta_ = f32(d.hidden);
   proj_ = f32(3 * width + 2 * d.index_dim);
-  attn_ = f32(width);
   o_ = f32(d.hidden);
   act_ = f32(max_ffn);
   router_logits_ = f32(max_experts);
@@ -290,16 +289,18 @@ void DecodeStep::body() {
                       block_max, prompt_blocks_, st, d.router, d.capacity,
                       d.trace ? trace_mask_[li].f32() : nullptr, d.trace ? trace_z_[li].f32() : nullptr,
                       d.trace ? trace_rqk_[li].f32() : nullptr, segs);
+    // The attention's splits leave their records in scratch_; the o
+    // projection merges them in its prologue (no merge launch).
     if (d.bf16_cache) {
       attend_rope_kv_step_segments_bf16(ctx_, q, k, v, k_cache_[li].bf16(), v_cache_[li].bf16(), d.heads, d.head_dim,
                                         segs, max_live_, scale, st, inv_tok_.f32(), n_tok, inv_page, d.page_mod,
-                                        scratch_.f32(), d.capacity, attn_.f32());
+                                        scratch_.f32(), d.capacity, nullptr);
     } else {
       attend_rope_kv_step_segments(ctx_, q, k, v, k_cache_[li].f32(), v_cache_[li].f32(), d.heads, d.head_dim, segs,
                                    max_live_, scale, st, inv_tok_.f32(), n_tok, inv_page, d.page_mod, scratch_.f32(),
-                                   d.capacity, attn_.f32());
+                                   d.capacity, nullptr);
     }
-    gemv_bf16(ctx_, attn_.f32(), width, l.o, d.hidden, nullptr, o_.f32());
+    attend_merge_gemv_bf16(ctx_, scratch_.f32(), d.heads, d.head_dim, max_live_, l.o, d.hidden, nullptr, o_.f32());
     if (l.moe == nullptr) {
       add_rms_norm_swiglu_gemv_bf16(ctx_, x_[cur].f32(), o_.f32(), x_[1 - cur].f32(), l.post_norm, d.eps, nullptr,
                                     d.hidden, l.gate, l.up, l.ffn, act_.f32());

@@ -205,7 +205,7 @@ class DecodeStep {
   const float* final_norm_;
   const std::uint16_t* lm_head_;
   std::int64_t length_ = 0, last_pos_ = -1, capacity_blocks_ = 0, prompt_blocks_ = 0;
-  Array inv_tok_, inv_page_, state_, x_[2], h_, delta_, proj_, attn_, o_, act_, logits_, scratch_;
+  Array inv_tok_, inv_page_, state_, x_[2], h_, delta_, proj_, o_, act_, logits_, scratch_;
   Array segments_;  // the router's live keys of the current layer (kKeySegmentWords int32)
   std::int64_t max_live_ = 1;
   Array block_min_, block_max_;

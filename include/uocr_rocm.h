@@ -770,7 +770,9 @@ UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step_bf16(void* stream, const float* 
  * the most live keys any call of this launch shape has ((max(top_k, 1) +
  * local_blocks) * block_size for the block router); it fixes the split count,
  * so a captured step keeps its launch shape. scratch holds
- * uocr_rocm_attend_segments_scratch_floats(heads, hd, max_live) floats. */
+ * uocr_rocm_attend_segments_scratch_floats(heads, hd, max_live) floats. With
+ * out null the splits' records stay in scratch, unmerged, for
+ * uocr_rocm_attend_merge_gemv_bf16. */
 UOCR_ROCM_API int64_t uocr_rocm_attend_segments_scratch_floats(int64_t heads, int64_t hd, int64_t max_live);
 UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step_segments(void* stream, const float* q, const float* k_row,
                                                          const float* v_row, float* k_cache, float* v_cache,
@@ -788,6 +790,17 @@ UOCR_ROCM_API int uocr_rocm_attend_rope_kv_step_segments_bf16(void* stream, cons
                                                               const float* inv_tok, int64_t n_tok,
                                                               const float* inv_page, int64_t page_mod, float* scratch,
                                                               int64_t capacity, float* out);
+/* y = bf16(merge) . w^T (+ bias), w bf16 [n, heads * hd], where merge is
+ * the attention row that uocr_rocm_attend_rope_kv_step_segments (called with
+ * out null and the same heads, hd and max_live) left as split records in
+ * scratch: bitwise its own merge followed by uocr_rocm_gemv_bf16, in one
+ * launch (new; the reference's decode step runs attend_step, whose last
+ * kernel merges the splits, then the o projection's gemv_bf16,
+ * src/model/cuda/cuda_decode_step.cpp:42-44). heads * hd a multiple of 8, at
+ * most 2048. x_out (optional, [heads * hd]) receives the merged row. */
+UOCR_ROCM_API int uocr_rocm_attend_merge_gemv_bf16(void* stream, const float* scratch, int64_t heads, int64_t hd,
+                                                   int64_t max_live, const uint16_t* w, int64_t n, const float* bias,
+                                                   float* y, float* x_out);
 
 /* ---- mixture of experts at decode ------------------------------------------ */
 

@@ -11,6 +11,7 @@ and is checked against the oracle directly as well:
                                     segments describe (the same caches
                                     bitwise, the output within 1e-5: its
                                     splits sum in another order)
+  attend_merge_gemv_bf16         == attend_rope_kv_step_segments' merge -> gemv_bf16
 
 and a whole decode layer built from them replays in a graph bitwise like the
 layer built from the unfused ops (the reference's decode_body order,
@@ -422,3 +423,47 @@ def test_attend_segments_rejects_bad_arguments(backend):
     with pytest.raises(ValueError, match="int32"):  # float32 segments
         backend.attend_rope_kv_step_segments(q, q, q, kc, vc, heads, hd, torch.zeros(4 * 34, device="cuda"), 32, 1.0,
                                              st, inv, None, 0, scratch, out)
+
+
+@pytest.mark.parametrize("heads,hd,n,nsel,max_live,with_bias", [
+    (10, 128, 1280, 8, 384, False),   # the decoder's o projection, 12 splits
+    (10, 128, 1280, 0, 384, True),    # the window alone: splits without keys
+    (16, 128, 2048, 32, 2112, False),  # 64 splits (k 2048, four chunks per lane)
+    (2, 64, 300, 3, 1, True),         # one split
+    (4, 64, 77, 20, 1344, False)])    # 42 splits, three value batches
+def test_attend_merge_gemv_matches_unfused(backend, heads, hd, n, nsel, max_live, with_bias):
+    """The o projection that merges the attention's split records in its
+    prologue: bitwise the attention's own merge launch followed by gemv_bf16,
+    its merged row bitwise the attention's output."""
+    width = heads * hd
+    cap, bs, local = 4096, 64 if max_live > 1024 else 32, 1 if max_live > 1024 else 4
+    pos = cap - 1
+    g = np.random.default_rng(400 + n)
+    remote = (pos - local * bs + 1) // bs
+    blocks = np.sort(g.choice(remote, size=min(nsel, remote), replace=False))
+    segs = torch.from_numpy(key_segments(pos, bs, local, blocks, (g.standard_normal(blocks.size) * 0.5)
+                                         .astype(np.float32))).cuda()
+    q, k_row, v_row = dev_f32(normal(401, width)), dev_f32(normal(402, width)), dev_f32(normal(403, width))
+    kc, vc = dev_f32(normal(404, (cap, width))), dev_f32(normal(405, (cap, width)))
+    inv = dev_f32(oracle.rope_inv(hd // 2, 1e4))
+    state = state_of(pos, tok=pos)
+    scale = float(1 / np.sqrt(hd))
+    scratch = torch.empty(backend.attend_segments_scratch_floats(heads, hd, max_live), device="cuda")
+    w = weights_bf16(406, (n, width))
+    bias = dev_f32(normal(407, n)) if with_bias else None
+    # unfused: the attention's merge into attn, then the GEMV
+    attn = torch.empty(width, device="cuda")
+    backend.attend_rope_kv_step_segments(q, k_row, v_row, kc, vc, heads, hd, segs, max_live, scale, state, inv, None,
+                                         0, scratch, attn)
+    y1 = torch.empty(n, device="cuda")
+    backend.gemv_bf16(attn, w, y1, bias=bias)
+    # fused: records only, then the merging GEMV
+    backend.attend_rope_kv_step_segments(q, k_row, v_row, kc, vc, heads, hd, segs, max_live, scale, state, inv, None,
+                                         0, scratch, None)
+    y2 = torch.full((n,), float("nan"), device="cuda")
+    merged = torch.full((width,), float("nan"), device="cuda")
+    backend.attend_merge_gemv_bf16(scratch, heads, hd, max_live, w, y2, bias=bias, x_out=merged)
+    assert np.array_equal(bits(merged), bits(attn))
+    assert np.array_equal(bits(y2), bits(y1))
+    with pytest.raises(ValueError):
+        backend.attend_merge_gemv_bf16(scratch, heads, hd, max_live, w[:, :width - 8].contiguous(), y2)
