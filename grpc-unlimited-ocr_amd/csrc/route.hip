@@ -124,84 +124,70 @@ __device__ void summarize(const float* keys, int n, int d, const float (&cls)[4]
   }
 }
 
-// Block scores. A summary row's d / 4 16-byte chunks go to L lanes (d / 4
-// rounded up to 16, 32 or 64), so a wave reads 64 / L rows per load; a pass
-// holds kScoreSteps such loads per lane in registers, all in flight
-// together, then reduces each row over its lanes (DPP inside 16-lane rows,
-// then readlane).
-constexpr int kScoreSteps = 8;
+// Block scores. Each lane takes eight 16-byte chunks of a summary row (32
+// features, past d zero), so a row spans L = d / 32 lanes (rounded up to 1,
+// 2, 4 or 8) and a wave reads 64 / L rows per pass. Lane c of a row takes
+// chunks c, c + L, c + 2 L, ..., so each load instruction reads L adjacent
+// chunks of every row; the lane sums its products in that order and the
+// row's L lanes add by DPP butterfly. All of a pass's loads are in flight
+// together. (Four features per lane over 32 lanes spent most of the time in
+// per-row butterflies and readlanes.)
+constexpr int kScoreChunks = 8;  // 16-byte chunks per lane
 
 struct ScoreRows {
-  u32x4 row[kScoreSteps];
+  u32x4 row[kScoreChunks];
 };
 
-__device__ __forceinline__ int score_lanes(int d) { return d <= 64 ? 16 : (d <= 128 ? 32 : 64); }
+__device__ __forceinline__ int score_lanes(int d) { return d <= 32 ? 1 : (d <= 64 ? 2 : (d <= 128 ? 4 : 8)); }
 
-// Rows per pass: waves * (64 / L) * kScoreSteps.
+// Rows per pass: waves * (64 / L).
 __device__ __forceinline__ int score_pass_rows(int d) {
-  return static_cast<int>(blockDim.x) / kWave * (kWave / score_lanes(d)) * kScoreSteps;
+  return static_cast<int>(blockDim.x) / kWave * (kWave / score_lanes(d));
 }
 
 // Issues the loads of the pass starting at row `base` (rows < n).
 __device__ __forceinline__ void score_load(const float* __restrict__ summaries, int d, int n, int base,
                                            ScoreRows& s) {
   const int wave = wave_in_block(), lane = threadIdx.x & (kWave - 1);
-  const int waves = static_cast<int>(blockDim.x) / kWave;
   const int L = score_lanes(d), R = kWave / L, sub = lane / L, c = lane & (L - 1);
-  const bool on = 4 * c < d;
+  const int b = base + wave * R + sub;
+  const float* row = summaries + static_cast<int64_t>(b) * d;
 #pragma unroll
-  for (int i = 0; i < kScoreSteps; ++i) {
-    const int b = base + (i * waves + wave) * R + sub;
+  for (int i = 0; i < kScoreChunks; ++i) {
+    const int f = 4 * (c + L * i);  // the chunk's first feature
     s.row[i] = u32x4{0u, 0u, 0u, 0u};
-    if (on && b < n) s.row[i] = *reinterpret_cast<const u32x4*>(summaries + static_cast<int64_t>(b) * d + 4 * c);
+    if (b < n && f < d) s.row[i] = *reinterpret_cast<const u32x4*>(row + f);
   }
 }
 
 // z[b] = (rq . summaries[b]) / sqrt d for the pass's rows b < n (unclamped),
-// rq [d] in LDS. Each dot is summed as four products per lane, then over
-// the lanes in a fixed order, the same for every entry point.
+// rq [d] in LDS. Each dot is summed as a lane's products in its chunks'
+// order, then over the row's lanes in a fixed order, the same for every
+// entry point.
 __device__ __forceinline__ void score_reduce(const float* rq, int d, int n, int base, float inv_sqrt_d,
                                              const ScoreRows& s, float* z) {
 #pragma clang fp contract(off)
   const int wave = wave_in_block(), lane = threadIdx.x & (kWave - 1);
-  const int waves = static_cast<int>(blockDim.x) / kWave;
-  const int L = score_lanes(d), R = kWave / L, c = lane & (L - 1);
-  const bool on = 4 * c < d;
-  float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (on) {
+  const int L = score_lanes(d), R = kWave / L, sub = lane / L, c = lane & (L - 1);
+  const int b0 = base + wave * R;  // wave-uniform
+  if (b0 >= n) return;
+  float part = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) q[i] = rq[4 * c + i];
-  }
-#pragma unroll
-  for (int i = 0; i < kScoreSteps; ++i) {
-    const int b0 = base + (i * waves + wave) * R;  // wave-uniform
-    if (b0 < n) {
-      float part = 0.0f;
+  for (int i = 0; i < kScoreChunks; ++i) {
+    const int f = 4 * (c + L * i);
+    if (f < d) {
+      const float* q = rq + f;
       part += q[0] * __uint_as_float(s.row[i].x);
       part += q[1] * __uint_as_float(s.row[i].y);
       part += q[2] * __uint_as_float(s.row[i].z);
       part += q[3] * __uint_as_float(s.row[i].w);
-      part += dpp_f32<0xB1>(part);   // lane ^ 1
-      part += dpp_f32<0x4E>(part);   // lane ^ 2
-      part += dpp_f32<0x141>(part);  // the two quads of each 8 lanes
-      part += dpp_f32<0x140>(part);  // the two halves of each 16-lane row
-      const float r0 = readlane_f32(part, 0), r1 = readlane_f32(part, 16);
-      const float r2 = readlane_f32(part, 32), r3 = readlane_f32(part, 48);
-      if (lane == 0) {
-        if (L == 64) {
-          z[b0] = ((r0 + r1) + (r2 + r3)) * inv_sqrt_d;
-        } else if (L == 32) {
-          z[b0] = (r0 + r1) * inv_sqrt_d;
-          if (b0 + 1 < n) z[b0 + 1] = (r2 + r3) * inv_sqrt_d;
-        } else {
-          z[b0] = r0 * inv_sqrt_d;
-          if (b0 + 1 < n) z[b0 + 1] = r1 * inv_sqrt_d;
-          if (b0 + 2 < n) z[b0 + 2] = r2 * inv_sqrt_d;
-          if (b0 + 3 < n) z[b0 + 3] = r3 * inv_sqrt_d;
-        }
-      }
     }
   }
+  if (L >= 2) part += dpp_f32<0xB1>(part);   // lane ^ 1
+  if (L >= 4) part += dpp_f32<0x4E>(part);   // lane ^ 2
+  if (L >= 8) part += dpp_f32<0x141>(part);  // the two quads of each 8 lanes
+  const int b = b0 + sub;
+  if (c == 0 && b < n) z[b] = part * inv_sqrt_d;
 }
 
 // z[b] for b < n, pass by pass. Every thread of the block must call it.
@@ -781,8 +767,8 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
 
   // 1. every load that does not wait for another: first those that need no
   // position (the router rows and their weights, head_cls, the rope
-  // frequency of this thread's pair, the page ranges, the first pass of
-  // summaries), then the step state, then the block's earlier keys
+  // frequency of this thread's pair, the page ranges), then the step state,
+  // then the block's earlier keys and the first pass of summaries
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (wave < 2 && 4 * lane < d) {
     const float* src = wave == 0 ? a.rq : a.rk;
@@ -800,15 +786,9 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   if (pr < half) freq = pr < a.n_tok ? a.inv_tok[pr] : a.inv_page[pr - a.n_tok];
 
   // the prompt blocks' page ranges (route_candidates checks the query's
-  // page and the block count) and, with a local window (the remote blocks
-  // then being whole, none of them the block summarized here), the first
-  // pass of summaries: rows past the remote blocks are read but not used
+  // page and the block count)
   PageRanges ranges;
   load_pages(a.block_min, a.block_max, a.prompt_blocks, kMaxRouteBlocks, 0, ranges);
-  const bool early = a.p.local_blocks > 0;
-  const int cap_blocks = static_cast<int>((a.capacity + a.p.block_size - 1) / a.p.block_size);
-  ScoreRows rows;
-  if (early) score_load(a.summaries, d, cap_blocks, 0, rows);
 
   const int64_t pos64 = a.state->pos;
   if (pos64 < 0 || pos64 >= a.capacity) return;  // uniform over the block
@@ -822,6 +802,12 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   const int64_t query_page = a.state->query_page;
   StagedKeys staged;
   load_keys(a.router_keys, first, n - 1, d, staged);
+  // with a local window the remote blocks are whole, none of them the
+  // block summarized here: the first pass of their summaries goes out now
+  // (issued after the keys, which are waited for first)
+  const bool early = a.p.local_blocks > 0;
+  ScoreRows rows;
+  if (early) score_load(a.summaries, d, nrem, 0, rows);
 
   // 2. router norm of rq (wave 0) and rk (wave 1), then rope at (tok, page)
   if (wave < 2) {
