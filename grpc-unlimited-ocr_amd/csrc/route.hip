@@ -343,25 +343,15 @@ __device__ __forceinline__ void load_pages(const int64_t* __restrict__ block_min
   }
 }
 
-// Whether v holds in any thread of the block, through one LDS slot per wave
-// (`slots`, kRouteBlock / 64 ints, written once per launch); a
-// kRouteBlock block.
-__device__ __forceinline__ bool block_any(bool v, int* slots) {
-  const uint64_t lanes = __ballot(v);
-  if ((threadIdx.x & (kWave - 1)) == 0) slots[wave_in_block()] = lanes != 0;
-  lds_barrier();
-  int any = 0;
-#pragma unroll
-  for (int w = 0; w < kRouteBlock / kWave; ++w) any |= slots[w];
-  return any != 0;
-}
-
 // cand[b], b < nblk: remote (b <= last_remote) and, for a query on a page,
 // one of the page's prompt blocks; a query whose page has no remote block
-// routes over every remote block (decoder.cpp:42-56). Every thread of a
-// kRouteBlock block must call it.
-__device__ __forceinline__ void route_candidates(const PageRanges& r, int nblk, int64_t last_remote, int64_t page,
-                                                 unsigned char* cand, int* any_slots) {
+// routes over every remote block (decoder.cpp:42-56). In two halves around
+// a workgroup LDS barrier the caller places: the first writes the flags of
+// this thread's blocks and its wave's vote into slots (kRouteBlock / 64
+// ints); the second reads the votes and, with none, applies the fallback to
+// this thread's blocks. Every thread of a kRouteBlock block must call both.
+__device__ __forceinline__ void route_candidates_begin(const PageRanges& r, int nblk, int64_t last_remote,
+                                                       int64_t page, unsigned char* cand, int* slots) {
   int any_local = 0;
 #pragma unroll
   for (int i = 0; i < kBlocksPerThread; ++i) {
@@ -373,13 +363,29 @@ __device__ __forceinline__ void route_candidates(const PageRanges& r, int nblk, 
       any_local |= remote && allowed;
     }
   }
-  if (!block_any(any_local != 0, any_slots)) {
+  const uint64_t lanes = __ballot(any_local != 0);
+  if ((threadIdx.x & (kWave - 1)) == 0) slots[wave_in_block()] = lanes != 0;
+}
+
+__device__ __forceinline__ void route_candidates_end(int nblk, int64_t last_remote, unsigned char* cand,
+                                                     const int* slots) {
+  int any = 0;
+#pragma unroll
+  for (int w = 0; w < kRouteBlock / kWave; ++w) any |= slots[w];
+  if (any == 0) {
 #pragma unroll
     for (int i = 0; i < kBlocksPerThread; ++i) {
       const int b = static_cast<int>(threadIdx.x) + kRouteBlock * i;
       if (b < nblk) cand[b] = b <= last_remote;
     }
   }
+}
+
+__device__ __forceinline__ void route_candidates(const PageRanges& r, int nblk, int64_t last_remote, int64_t page,
+                                                 unsigned char* cand, int* slots) {
+  route_candidates_begin(r, nblk, last_remote, page, cand, slots);
+  lds_barrier();
+  route_candidates_end(nblk, last_remote, cand, slots);
 }
 
 // The selection and the key mask of one query at position pos over nblk
@@ -402,38 +408,40 @@ __device__ __forceinline__ void route_candidates(const PageRanges& r, int nblk, 
 __device__ void route_select(const float* z, int nblk, int64_t pos, int64_t keys, const RouteArgs p, RouteLds sh,
                              float* __restrict__ mask, int* __restrict__ segs = nullptr) {
 #pragma clang fp contract(off)
+  constexpr int kSlice = 4 * kWave;  // blocks per wave
+  // With nblk <= kSlice the top m goes by rank (below), whose keys, counts
+  // and result slots are set here, before the same barrier.
+  static_assert(kRouteBlock == 4 * kSlice, "four quarters of the blocks");
+  uint64_t* key_of = sh.list;                            // [kSlice]
+  int* rank = reinterpret_cast<int*>(sh.list + kSlice);  // [kSlice]
+  uint64_t* top = sh.list + kSlice + kSlice / 2;         // [kMaxTop]
+  const int t = static_cast<int>(threadIdx.x);
 #pragma unroll
   for (int i = 0; i < kBlocksPerThread; ++i) {
-    const int b = static_cast<int>(threadIdx.x) + kRouteBlock * i;
+    const int b = t + kRouteBlock * i;
     if (b < nblk) {
       const float xb = sh.cand[b] ? clamp_act(z[b]) * p.idx_scale : kEntmaxMasked;
       sh.x[b] = xb;
       sh.block_bias[b] = -INFINITY;
+      if (i == 0 && nblk <= kSlice) key_of[b] = order_key(xb, b);
     }
+  }
+  if (nblk <= kSlice && t < kSlice) {
+    if (t >= nblk) key_of[t] = 0;
+    rank[t] = 0;
+    if (t < kMaxTop) top[t] = 0;
   }
   lds_barrier();
 
   const int m = p.top_m < nblk ? (p.top_m > 1 ? p.top_m : 1) : (nblk > 1 ? nblk : 1);
   const int k = p.top_k < m ? (p.top_k > 1 ? p.top_k : 1) : m;
   const int wave = wave_in_block(), lane = threadIdx.x & (kWave - 1);
-  constexpr int kSlice = 4 * kWave;  // blocks per wave
   uint64_t mine = 0;
   if (nblk <= kSlice) {
     // By rank: the keys are distinct, so a block's place in the order is
     // the count of keys above it. Thread (q, b) counts the keys of quarter q
     // above block b's; the quarters' counts add in LDS, and each block with
     // a rank below m puts its key at that rank.
-    static_assert(kRouteBlock == 4 * kSlice, "four quarters of the blocks");
-    uint64_t* key_of = sh.list;                                // [kSlice]
-    int* rank = reinterpret_cast<int*>(sh.list + kSlice);      // [kSlice]
-    uint64_t* top = sh.list + kSlice + kSlice / 2;             // [kMaxTop]
-    const int t = static_cast<int>(threadIdx.x);
-    if (t < kSlice) {
-      key_of[t] = t < nblk ? order_key(sh.x[t], t) : 0;
-      rank[t] = 0;
-      if (t < kMaxTop) top[t] = 0;
-    }
-    lds_barrier();
     // the slots past nblk hold 0, below every key, so every thread counts
     // its quarter's 64 slots with the same unrolled loop (LDS broadcasts)
     const int b = t & (kSlice - 1);
@@ -756,6 +764,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   // scores, then (in place) the entmax inputs.
   __shared__ __attribute__((aligned(16))) float keys[kStageFloats];
   __shared__ float rqk[2][kMaxIndexDim];  // normed, then rotated rq and rk
+  __shared__ float rope_sc[2][kMaxIndexDim / 2];  // the rope's sines and cosines
   __shared__ float zs[kMaxRouteBlocks];
   __shared__ unsigned char cand[kMaxRouteBlocks];
   __shared__ float p_lds[kMaxBlockKeys];
@@ -782,8 +791,9 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   float cls[4];
   load_cls(a.cls, d, cls);
   const int pr = threadIdx.x;
+  const int sc = pr - 2 * kWave;  // waves 2 and 3 form the rope's sines and cosines, pair sc
   float freq = 0.0f;
-  if (pr < half) freq = pr < a.n_tok ? a.inv_tok[pr] : a.inv_page[pr - a.n_tok];
+  if (sc >= 0 && sc < half) freq = sc < a.n_tok ? a.inv_tok[sc] : a.inv_page[sc - a.n_tok];
 
   // the prompt blocks' page ranges (route_candidates checks the query's
   // page and the block count)
@@ -809,7 +819,9 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   ScoreRows rows;
   if (early) score_load(a.summaries, d, nrem, 0, rows);
 
-  // 2. router norm of rq (wave 0) and rk (wave 1), then rope at (tok, page)
+  // 2. router norm of rq (wave 0) and rk (wave 1) while waves 2-3 form the
+  // sines and cosines of (tok, page) and every thread its blocks' candidate
+  // flags; then the rope
   if (wave < 2) {
     router_norm_lane(v, w, d, a.eps, lane);
     if (4 * lane < d) {
@@ -817,14 +829,18 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
       for (int i = 0; i < 4; ++i) rqk[wave][4 * lane + i] = v[i];
     }
   }
-  store_keys(staged, n - 1, d, keys);
-  lds_barrier();
-  if (pr < half) {
+  if (sc >= 0 && sc < half) {
     int64_t pg = a.state->page;
     if (a.page_mod > 0) pg = ((pg % a.page_mod) + a.page_mod) % a.page_mod;
-    const float angle = (pr < a.n_tok ? static_cast<float>(a.state->tok) : static_cast<float>(pg)) * freq;
-    float sn, cs;
-    sincosf(angle, &sn, &cs);
+    const float angle = (sc < a.n_tok ? static_cast<float>(a.state->tok) : static_cast<float>(pg)) * freq;
+    sincosf(angle, &rope_sc[0][sc], &rope_sc[1][sc]);
+  }
+  store_keys(staged, n - 1, d, keys);
+  route_candidates_begin(ranges, nblk, last_remote, query_page, cand, any_slots);
+  lds_barrier();
+  route_candidates_end(nblk, last_remote, cand, any_slots);
+  if (pr < half) {
+    const float sn = rope_sc[0][pr], cs = rope_sc[1][pr];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const float x0 = rqk[r][pr], x1 = rqk[r][pr + half];
@@ -846,8 +862,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_decode_k(DecodeRouteArgs a)
   lds_barrier();
   summarize(keys, n, d, cls, a.inv_sqrt_d, p_lds, a.summaries + blk * d);
 
-  // 4. the candidates, and the scores of the blocks before the window
-  route_candidates(ranges, nblk, last_remote, query_page, cand, any_slots);
+  // 4. the scores of the blocks before the window
   if (!early) {
     __syncthreads();  // the summary just written is one of the rows scored
     score_load(a.summaries, d, nrem, 0, rows);
