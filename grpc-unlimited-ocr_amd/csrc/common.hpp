@@ -383,6 +383,13 @@ inline void clear_launch_error() { (void)hipGetLastError(); }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The plain bf16 product through the BLAS library (gemm_library.hip):
+// UOCR_ROCM_OK, kLibraryDeclined when the product is not one it takes (the
+// caller runs the tile kernels), or an error status.
+constexpr int kLibraryDeclined = -1;
+int library_linear_bf16(const char* what, hipStream_t s, const uint16_t* x, int64_t m, int64_t k,
+                        const uint16_t* w, int64_t n, const float* bias, float* y);
+
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 inline unsigned blocks_for_rows(int64_t rows) {

@@ -259,8 +259,11 @@ double median_rel(const std::vector<float>& got, const std::vector<float>& want)
 // 1e-1 and more (tests/test_oracle_vision.py). The ops themselves are held to
 // 1e-5 one by one (tests/test_gpu_vision_ops.py, test_gpu_linear.py).
 // median_bar: the median element's distance from the rounded oracle. On the
-// tiny model almost every element is exact (median 0: no linear input has
-// crossed a rounding boundary yet); at the real widths the median sits at
+// tiny model's 128-pixel pages almost every element is exact (median 0: no
+// linear input has crossed a rounding boundary yet); its 256-pixel page
+// runs products of 128 rows and more through the BLAS library, whose fp32
+// sums are ordered otherwise than the oracle's (median 1.2e-5 measured, bar
+// 1e-4); at the real widths the median sits at
 // the rounding-noise floor (6e-4 measured), so a slip that shifts most
 // features (a misplaced window slot, a dropped bias term) lifts it well
 // above 2e-3 while leaving the maximum near its own floor.
@@ -323,7 +326,7 @@ int parity() {
     const ro::VisionEncoder enc(ctx, dims, m.device());
     check_page(enc, m, "tiny model, base page (128)", 128, {}, 1, 1, 1e-6);
     check_page(enc, m, "tiny model, tiled page (128 + 2 x 1 tiles of 128)", 128, {128, 128}, 2, 1, 1e-6);
-    check_page(enc, m, "tiny model, base page (256: 4 padded windows)", 256, {}, 1, 1, 1e-6);
+    check_page(enc, m, "tiny model, base page (256: 4 padded windows)", 256, {}, 1, 1, 1e-4);
     bool threw = false;
     try {
       (void)enc.encode_view(ro::View{std::vector<float>(3 * 100 * 100), 100});

@@ -12,9 +12,15 @@ to bf16, fp32 accumulation, bias added to the finished sum).
     the same bf16-rounded operands;
   * k not a multiple of 8 (the vision encoder's convolutions over 12
     channels: 108 columns) loads element by element, against the oracle;
-  * m == 1 goes through the GEMV, bias or none, and bad shapes are refused.
+  * m == 1 goes through the GEMV, bias or none, and bad shapes are refused;
+  * plain products of at least 128 bf16 rows run through hipBLASLt
+    (csrc/gemm_library.hip): against the oracle as above, against the tile
+    kernels (UOCR_ROCM_GEMM=tiles) on the same operands, and bitwise equal
+    from call to call.
 
 Tolerance: 1e-5 of the largest |y| (fp32 accumulation in another order)."""
+
+import os
 
 import numpy as np
 import pytest
@@ -94,8 +100,10 @@ def test_linear_bf16_x_is_linear_on_the_rounded_rows(backend, m, k, n):
     assert_f32_close(host_f32(y), want, 1e-5, f"linear bf16 x m={m} k={k} n={n}")
     y2 = torch.empty(m, n, device="cuda")
     if m > 1:
+        # the same tiles on fp32 rows, within 1e-6; from 128 rows the bf16
+        # rows go to the library, another summation order
         backend.linear(dev_f32(x), dev_bf16(wb), y2, dev_f32(bias))
-        assert_f32_close(host_f32(y2), host_f32(y), 1e-6, "fp32 x and bf16 x agree")
+        assert_f32_close(host_f32(y2), host_f32(y), 1e-6 if m < 128 else 1e-5, "fp32 x and bf16 x agree")
 
 
 def test_linear_one_row_is_the_gemv(backend):
@@ -159,10 +167,11 @@ def test_linear_split_k_against_the_oracle(backend, m, k, n, fp32_x):
 
 @pytest.mark.parametrize("m,k,n,with_bias", [(4096, 768, 768, True), (4096, 3072, 768, True), (257, 4096, 1024, True),
                                              (257, 1024, 1024, False), (33, 100, 70, True), (1, 64, 8, True)])
-def test_linear_add_is_the_product_then_the_add(backend, m, k, n, with_bias):
+def test_linear_add_is_the_product_then_the_add(backend, tiles_only, m, k, n, with_bias):
     """y += bf16 x . w^T + bias (a residual stream's projection) against the
     product into a temporary then add_inplace, bit for bit, split over k (257
-    rows, k >= 1024) or not, ragged k, one row."""
+    rows, k >= 1024) or not, ragged k, one row (every product on the tile
+    kernels, whose sums the fused epilogue shares)."""
     x = normal(460 + m, (m, k))
     wb = bf16(0.03 * normal(461 + n, (n, k)))
     bias = dev_f32(normal(462, n)) if with_bias else None
@@ -183,7 +192,7 @@ def test_linear_add_is_the_product_then_the_add(backend, m, k, n, with_bias):
 @pytest.mark.parametrize("m,k,n", [(257, 1024, 4096), (4096, 768, 3072), (1000, 128, 200), (5, 64, 40),
                                    (600, 256, 4096)])
 @pytest.mark.parametrize("quick", [False, True])
-def test_linear_act_is_the_product_then_the_activation(backend, m, k, n, quick):
+def test_linear_act_is_the_product_then_the_activation(backend, tiles_only, m, k, n, quick):
     """y = bf16(act(bf16 x . w^T + bias)), an MLP's first projection with
     its activation in the epilogue (CLIP's fc1 [257 x 1024 -> 4096] and
     quick_gelu, SAM's lin1 [4096 x 768 -> 3072] and gelu_erf, few-row,
@@ -215,7 +224,7 @@ def test_linear_act_refuses_k_off_the_tile(backend):
 
 @pytest.mark.parametrize("m,k,n,y_rows", [(4900, 768, 768, 4096), (300, 128, 96, 257), (5, 64, 40, 3),
                                           (2048, 256, 4096, 1500)])
-def test_linear_add_rows_scatters_the_kept_rows(backend, m, k, n, y_rows):
+def test_linear_add_rows_scatters_the_kept_rows(backend, tiles_only, m, k, n, y_rows):
     """y[y_row[r]] += product row r for y_row[r] < y_rows (window slots back
     into their grid rows, padding slots dropped): bitwise the product, the
     kept rows gathered, then add_inplace."""
@@ -239,3 +248,45 @@ def test_linear_add_rows_scatters_the_kept_rows(backend, m, k, n, y_rows):
     got = resid.clone()
     backend.linear_add_rows(xb, dev_bf16(wb), got, torch.from_numpy(y_row).cuda(), bias)
     assert torch.equal(got, want), f"m={m} k={k} n={n} y_rows={y_rows}"
+
+
+@pytest.fixture
+def tiles_only():
+    """UOCR_ROCM_GEMM=tiles for the test's duration: every product on the
+    hand-written tile kernels."""
+    old = os.environ.get("UOCR_ROCM_GEMM")
+    os.environ["UOCR_ROCM_GEMM"] = "tiles"
+    yield
+    if old is None:
+        del os.environ["UOCR_ROCM_GEMM"]
+    else:
+        os.environ["UOCR_ROCM_GEMM"] = old
+
+
+@pytest.mark.parametrize("m,k,n,with_bias", [(4096, 1280, 4096, True), (4096, 1280, 6848, False),
+                                             (4096, 6848, 1280, True), (257, 1024, 3072, True), (128, 64, 8, False),
+                                             (300, 1288, 520, True), (1000, 200, 72, True)])
+def test_library_linear_against_the_tiles(backend, m, k, n, with_bias, request):
+    """The decoder's prefill projections, CLIP's 257-row ones and small or
+    ragged shapes through hipBLASLt: against the oracle on sampled rows,
+    against the tile kernels on every element, and bitwise from call to
+    call."""
+    x = normal(450 + m, (m, k))
+    wb = bf16(0.03 * normal(451 + n, (n, k)))
+    bias = normal(452, n) if with_bias else None
+    xb = torch.empty(m, k, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(dev_f32(x), xb)
+    wd = dev_bf16(wb)
+    bd = None if bias is None else dev_f32(bias)
+    y = torch.full((m, n), float("nan"), device="cuda")
+    backend.linear(xb, wd, y, bd)
+    rows = np.unique(np.array([0, 1, m // 3, m // 2, m - 1]))
+    want = oracle.linear(oracle.bf16_round(x[rows]), oracle.bf16_to_f32(wb), bias)
+    assert_f32_close(host_f32(y)[rows], want, 1e-5, f"library linear m={m} k={k} n={n}")
+    y_again = torch.full((m, n), float("nan"), device="cuda")
+    backend.linear(xb, wd, y_again, bd)
+    assert np.array_equal(host_f32(y_again).view(np.uint32), host_f32(y).view(np.uint32))
+    request.getfixturevalue("tiles_only")
+    y_tiles = torch.full((m, n), float("nan"), device="cuda")
+    backend.linear(xb, wd, y_tiles, bd)
+    assert_f32_close(host_f32(y_tiles), host_f32(y), 1e-5, "tiles and library agree")
