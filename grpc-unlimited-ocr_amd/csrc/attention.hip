@@ -416,6 +416,230 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   }
 }
 
+// ---- split-bf16 products for a bf16 output ----------------------------------
+//
+// With the output rounded to bf16 (2^-9 relative) the fp32 products carry
+// more precision than survives. attention_x3_k forms them on the bf16
+// matrix cores (v_mfma_f32_32x32x16_bf16, 8 times the fp32 rate per
+// instruction) with each fp32 operand split into bf16 parts, x = hi + lo
+// (hi = bf16(x), lo = bf16(x - hi)), and a . b = lo_a hi_b + hi_a lo_b +
+// hi_a hi_b accumulated in fp32: about 2^-16 of each product is dropped,
+// three orders below the output's rounding. Head dim 64, the
+// relative-position bias from the dot table (a grid of whole 32-key tiles:
+// SAM's global layers), 4 waves of 32 query rows. The key and value tiles
+// are split once per workgroup as they reach LDS: K rows as hi and lo bf16
+// rows, V transposed (a dimension's 32 keys contiguous, so one 16-byte read
+// gives a lane its 8 keys) and its key order permuted so that the
+// probabilities' registers feed the values' product without movement: the
+// scores' register r of lane half h holds key 8 (r / 4) + 4 h + r % 4, and
+// the product's k index 16 j + 8 h + t reads register 8 j + t, key
+// 16 j + 8 (t / 4) + 4 h + t % 4 (bits 2 and 3 of the key swapped). The
+// scale, bias, online softmax and output are attention_k's.
+constexpr int kX3KStride = 64 + 8;        // K rows in bf16: 144 bytes, 16 lanes' reads on 16 bank groups
+constexpr int kX3VStride = kKeyTile + 8;  // V^T rows: 80 bytes, likewise
+
+__device__ __forceinline__ int x3_key_slot(int key) {  // bits 2 and 3 swapped (an involution)
+  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
+// The hi and lo bf16 parts of two floats, each pair packed (x0 low).
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t* hi, uint32_t* lo) {
+  *hi = pack_bf16(x0, x1);
+  *lo = pack_bf16(x0 - bf16_lo(*hi), x1 - bf16_hi(*hi));
+}
+
+// Eight floats' parts as 8 bf16 each (a matrix-core operand).
+__device__ __forceinline__ void split8(const float (&x)[8], u32x4& hi, u32x4& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) split2(x[2 * i], x[2 * i + 1], &h[i], &l[i]);
+  hi = u32x4{h[0], h[1], h[2], h[3]};
+  lo = u32x4{l[0], l[1], l[2], l[3]};
+}
+
+__device__ __forceinline__ void store_tile_x3(uint16_t* khi, uint16_t* klo, uint16_t* vhi, uint16_t* vlo,
+                                              const float4 (&kr)[Tile<64, 256>::kPerThread],
+                                              const float4 (&vr)[Tile<64, 256>::kPerThread]) {
+#pragma unroll
+  for (int j = 0; j < Tile<64, 256>::kPerThread; ++j) {
+    const int idx = static_cast<int>(threadIdx.x) + 256 * j;
+    const int row = idx / 16, c4 = idx % 16;
+    uint32_t h[2], l[2];
+    split2(kr[j].x, kr[j].y, &h[0], &l[0]);
+    split2(kr[j].z, kr[j].w, &h[1], &l[1]);
+    *reinterpret_cast<u32x2*>(khi + row * kX3KStride + 4 * c4) = u32x2{h[0], h[1]};
+    *reinterpret_cast<u32x2*>(klo + row * kX3KStride + 4 * c4) = u32x2{l[0], l[1]};
+    split2(vr[j].x, vr[j].y, &h[0], &l[0]);
+    split2(vr[j].z, vr[j].w, &h[1], &l[1]);
+    const int slot = x3_key_slot(row);
+    const uint16_t hv[4] = {static_cast<uint16_t>(h[0]), static_cast<uint16_t>(h[0] >> 16),
+                            static_cast<uint16_t>(h[1]), static_cast<uint16_t>(h[1] >> 16)};
+    const uint16_t lv[4] = {static_cast<uint16_t>(l[0]), static_cast<uint16_t>(l[0] >> 16),
+                            static_cast<uint16_t>(l[1]), static_cast<uint16_t>(l[1] >> 16)};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vhi[(4 * c4 + e) * kX3VStride + slot] = hv[e];
+      vlo[(4 * c4 + e) * kX3VStride + slot] = lv[e];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
+  constexpr int HD = 64, kThreads = 256, kQueriesPerBlock = 4 * kQueriesPerWave;
+  using T = Tile<HD, kThreads>;
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  __shared__ __attribute__((aligned(16))) uint16_t khi[kKeyTile * kX3KStride];
+  __shared__ __attribute__((aligned(16))) uint16_t klo[kKeyTile * kX3KStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vhi[HD * kX3VStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vlo[HD * kX3VStride];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, c = lane & 31;
+  const int64_t slice = blockIdx.y;
+  const int q0 = blockIdx.x * kQueriesPerBlock + wave * kQueriesPerWave;
+  const int qrow = q0 + c;
+  const bool qin = qrow < a.rows;
+  const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
+  const float* kb = a.k + slice_at(a, slice, a.sk, a.ik);
+  const float* vb = a.v + slice_at(a, slice, a.sv, a.iv);
+  auto mfma = [](u32x4 x, u32x4 y, f32x16 acc) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x), __builtin_bit_cast(bf16x8, y),
+                                                   acc, 0, 0, 0);
+  };
+
+  float4 kr[T::kPerThread], vr[T::kPerThread];
+  load_tile<HD, kThreads>(a, kb, vb, 0, kr, vr);
+
+  // this lane's query columns 16 b + 8 h + (0..7), b < 4, split
+  u32x4 qh[4], ql[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    float4 t0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), t1 = t0;
+    if (qin) {
+      const float* qr = qb + qrow * a.ldq + 16 * b + 8 * hl;
+      t0 = *reinterpret_cast<const float4*>(qr);
+      t1 = *reinterpret_cast<const float4*>(qr + 4);
+    }
+    const float x[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+    split8(x, qh[b], ql[b]);
+  }
+
+  store_tile_x3(khi, klo, vhi, vlo, kr, vr);
+  __syncthreads();
+
+  f32x16 o[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] = 0.0f;
+  }
+  float m = -INFINITY, l = 0.0f;
+  const bool live = q0 < a.rows;
+  const float* trow = a.table + (slice * a.rows + (qin ? qrow : 0)) * static_cast<int64_t>(a.dots_ld);
+  const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
+  for (int t = 0; t < tiles; ++t) {
+    const int key0 = t * kKeyTile;
+    const bool more = t + 1 < tiles;
+    if (more) load_tile<HD, kThreads>(a, kb, vb, key0 + kKeyTile, kr, vr);
+    if (live) {
+      // S^T = K Q^T: 32 keys x 32 queries, the small products first
+      f32x16 s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int at = c * kX3KStride + 16 * b + 8 * hl;
+        const u32x4 kh = *reinterpret_cast<const u32x4*>(khi + at);
+        const u32x4 kl = *reinterpret_cast<const u32x4*>(klo + at);
+        s = mfma(kl, qh[b], s);
+        s = mfma(kh, ql[b], s);
+        s = mfma(kh, qh[b], s);
+      }
+      // scale, the tile's bias terms (one height term, the lane's 16 width
+      // terms), running max
+      const int ky0 = key0 / a.w, kx0 = key0 - ky0 * a.w;
+      const float dh = trow[ky0];
+      float dwv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 tw = *reinterpret_cast<const float4*>(trow + a.dw_off + kx0 + 8 * g + 4 * hl);
+        dwv[4 * g] = tw.x;
+        dwv[4 * g + 1] = tw.y;
+        dwv[4 * g + 2] = tw.z;
+        dwv[4 * g + 3] = tw.w;
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + 8 * (r / 4) + 4 * hl + (r % 4);
+        float x = s[r] * a.scale;
+        x = x + (dh + dwv[r]);
+        x = key < a.keys ? x : -INFINITY;
+        s[r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+      tmax = fmaxf(tmax, partner(tmax));
+      const float m_new = fmaxf(m, tmax);
+      const bool dead = m_new == -INFINITY;
+      const float corr = dead ? 1.0f : __builtin_amdgcn_exp2f((m - m_new) * kLog2e);
+      float psum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = dead ? 0.0f : __builtin_amdgcn_exp2f((s[r] - m_new) * kLog2e);
+        psum += s[r];
+      }
+      psum += partner(psum);
+      l = l * corr + psum;
+      m = m_new;
+      if (__ballot(corr != 1.0f) != 0) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[b][r] *= corr;
+        }
+      }
+      // P split: product j takes registers 8 j .. 8 j + 7
+      u32x4 ph[2], pl[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float x[8] = {s[8 * j],     s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
+                            s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]};
+        split8(x, ph[j], pl[j]);
+      }
+      // O^T += V^T P^T over the permuted key slots
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int at = (32 * b + c) * kX3VStride + 16 * j + 8 * hl;
+          const u32x4 vh = *reinterpret_cast<const u32x4*>(vhi + at);
+          const u32x4 vl = *reinterpret_cast<const u32x4*>(vlo + at);
+          o[b] = mfma(vl, ph[j], o[b]);
+          o[b] = mfma(vh, pl[j], o[b]);
+          o[b] = mfma(vh, ph[j], o[b]);
+        }
+      }
+    }
+    __syncthreads();  // every wave is done with this tile
+    if (more) {
+      store_tile_x3(khi, klo, vhi, vlo, kr, vr);
+      __syncthreads();
+    }
+  }
+
+  if (!qin) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const int64_t orow = slice_at(a, slice, a.so, a.io) + qrow * a.ldo;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * b + 8 * g + 4 * hl;
+      store4(a, orow + d, o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv);
+    }
+  }
+}
+
 // ---- few query rows: the keys split over the waves ---------------------------
 //
 // With few query rows (CLIP: 16 heads x 257 rows are 48 workgroups of 128
@@ -767,6 +991,14 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
       rel_dots_k<128><<<grid, kBlock, lds, as_stream(stream)>>>(a);
     }
     if (const int st = check_launch(what)) return st;
+  }
+  if (lay.tile_rows && table && out16 != nullptr && hd == 64) {
+    // a bf16 output: the products on the bf16 matrix cores, operands split
+    const dim3 grid(static_cast<unsigned>((n + 4 * kQueriesPerWave - 1) / (4 * kQueriesPerWave)),
+                    static_cast<unsigned>(slices));
+    clear_launch_error();
+    attention_x3_k<<<grid, 256, 0, as_stream(stream)>>>(a);
+    return check_launch(what);
   }
   if (lay.tile_rows && table) return launch<Bias::kRelPosTable>(what, stream, hd, slices, a);
   return lay.tile_rows ? launch<Bias::kRelPosRows>(what, stream, hd, slices, a)
