@@ -507,8 +507,22 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
                                                    acc, 0, 0, 0);
   };
 
+  // Tile loads with every address in range (rows past the keys read the
+  // last key's row; their scores are -inf, their probabilities 0) and no
+  // branch, so that a tile's use waits only for its own loads, not for the
+  // next tile's in flight.
   float4 kr[T::kPerThread], vr[T::kPerThread];
-  load_tile<HD, kThreads>(a, kb, vb, 0, kr, vr);
+  auto load_kv = [&](int key0) {
+#pragma unroll
+    for (int j = 0; j < T::kPerThread; ++j) {
+      const int idx = static_cast<int>(threadIdx.x) + kThreads * j;
+      const int row = idx / (HD / 4), c4 = idx % (HD / 4);
+      const int key = key0 + row < a.keys ? key0 + row : a.keys - 1;
+      kr[j] = *reinterpret_cast<const float4*>(kb + key * a.ldk + 4 * c4);
+      vr[j] = *reinterpret_cast<const float4*>(vb + key * a.ldv + 4 * c4);
+    }
+  };
+  load_kv(0);
 
   // this lane's query columns 16 b + 8 h + (0..7), b < 4, split
   u32x4 qh[4], ql[4];
@@ -537,10 +551,35 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
   const bool live = q0 < a.rows;
   const float* trow = a.table + (slice * a.rows + (qin ? qrow : 0)) * static_cast<int64_t>(a.dots_ld);
   const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
+  // a tile's bias terms: its height term and the lane's 16 width terms
+  // (keys kx0 + 8 g + 4 h + (0..3)), requested a tile ahead like K and V
+  auto load_bias = [&](int key0, float& dh, float (&dwv)[16]) {
+    const int ky0 = key0 / a.w, kx0 = key0 - ky0 * a.w;
+    dh = trow[ky0];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 tw = *reinterpret_cast<const float4*>(trow + a.dw_off + kx0 + 8 * g + 4 * hl);
+      dwv[4 * g] = tw.x;
+      dwv[4 * g + 1] = tw.y;
+      dwv[4 * g + 2] = tw.z;
+      dwv[4 * g + 3] = tw.w;
+    }
+  };
+  float dh = 0.0f, dwv[16], dh_next = 0.0f, dwv_next[16];
+  load_bias(0, dh_next, dwv_next);
   for (int t = 0; t < tiles; ++t) {
     const int key0 = t * kKeyTile;
     const bool more = t + 1 < tiles;
-    if (more) load_tile<HD, kThreads>(a, kb, vb, key0 + kKeyTile, kr, vr);
+    // this tile's bias terms, requested an iteration ago, taken before the
+    // next tile's requests go out (so that the copy waits for nothing
+    // newer); then the next tile's operands (the last tile's again after
+    // the last)
+    dh = dh_next;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dwv[r] = dwv_next[r];
+    const int next0 = more ? key0 + kKeyTile : key0;
+    load_kv(next0);
+    load_bias(next0, dh_next, dwv_next);
     if (live) {
       // S^T = K Q^T: 32 keys x 32 queries, the small products first
       f32x16 s;
@@ -555,19 +594,7 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
         s = mfma(kh, ql[b], s);
         s = mfma(kh, qh[b], s);
       }
-      // scale, the tile's bias terms (one height term, the lane's 16 width
-      // terms), running max
-      const int ky0 = key0 / a.w, kx0 = key0 - ky0 * a.w;
-      const float dh = trow[ky0];
-      float dwv[16];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 tw = *reinterpret_cast<const float4*>(trow + a.dw_off + kx0 + 8 * g + 4 * hl);
-        dwv[4 * g] = tw.x;
-        dwv[4 * g + 1] = tw.y;
-        dwv[4 * g + 2] = tw.z;
-        dwv[4 * g + 3] = tw.w;
-      }
+      // scale, the tile's bias terms, running max
       float tmax = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {

@@ -388,7 +388,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // caller runs the tile kernels), or an error status.
 constexpr int kLibraryDeclined = -1;
 int library_linear_bf16(const char* what, hipStream_t s, const uint16_t* x, int64_t m, int64_t k,
-                        const uint16_t* w, int64_t n, const float* bias, float* y);
+                        const uint16_t* w, int64_t n, const float* bias, float* y, bool accumulate);
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 

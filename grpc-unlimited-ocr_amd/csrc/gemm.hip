@@ -25,9 +25,10 @@
 // reference's separate bias pass). A product with few tiles and a long k
 // (the vision encoder's convolutions, CLIP's 257-row projections) may split
 // k over a caller's workspace: each split writes its partial products and one
-// more launch sums them in split order, then adds the bias. Plain products of
-// bf16 rows (no epilogue beyond the bias), at least 128 of them, go to
-// hipBLASLt instead (gemm_library.hip); the tiles take everything else.
+// more launch sums them in split order, then adds the bias. Products of bf16
+// rows with no epilogue beyond the bias and the add into y, at least 128
+// rows, go to hipBLASLt instead (gemm_library.hip); the tiles take the
+// activation epilogues, the row scatter, fp32 rows and few rows.
 
 #include "act_math.hpp"
 #include "common.hpp"
@@ -621,9 +622,11 @@ int linear_entry(const char* what, void* stream, const void* x, bool f32x, int64
   UOCR_REQUIRE(k >= 1 && k < (int64_t{1} << 30), what, "k must be in [1, 2^30)");
   UOCR_REQUIRE(x != nullptr && w != nullptr && (epi == Epi::kPlain ? y != nullptr : y16 != nullptr), what,
                "null x, w or y");
-  // plain products of bf16 rows go to the BLAS library when it takes them
-  if (!f32x && epi == Epi::kPlain && !accumulate && row_map == nullptr) {
-    const int st = library_linear_bf16(what, as_stream(stream), static_cast<const uint16_t*>(x), m, k, w, n, bias, y);
+  // products of bf16 rows with no epilogue beyond the bias (and the add
+  // into y) go to the BLAS library when it takes them
+  if (!f32x && epi == Epi::kPlain && row_map == nullptr) {
+    const int st =
+        library_linear_bf16(what, as_stream(stream), static_cast<const uint16_t*>(x), m, k, w, n, bias, y, accumulate);
     if (st != kLibraryDeclined) return st;
   }
   const bool ragged = k % 8 != 0 || !aligned16(x) || !aligned16(w);

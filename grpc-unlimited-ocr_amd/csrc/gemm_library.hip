@@ -2,12 +2,12 @@
 // (+ bias[n]) with x and w bf16 and y fp32 through hipBLASLt, the ROCm
 // counterpart of the cuBLAS call inside the reference's cuda::linear
 // (src/backend/cuda/ops.cu:268-287: a bf16 GEMM with fp32 compute, then the
-// bias). The hand-written tile kernels (gemm.hip) keep every product with a
-// fused epilogue (activation into bf16, residual add, row scatter), split k
-// over a caller's workspace, fp32 x, or few rows; this path takes the plain
-// products of at least kLibraryMinRows rows, where the library's tiles run
-// about 1.7x the hand-written ones (963 against 537 TFLOP/s over a dense
-// decoder layer's four projections at 4096 rows, random bf16 operands).
+// bias). The hand-written tile kernels (gemm.hip) keep the products with an
+// activation epilogue into bf16 or a row scatter, fp32 x, and few rows; this
+// path takes the plain products (bias, and an add into y, allowed) of at
+// least kLibraryMinRows rows, where the library's tiles run about 1.6x the
+// hand-written ones (865 against 537 TFLOP/s over a dense decoder layer's
+// four projections at 4096 rows, random bf16 operands).
 //
 // In hipBLASLt's column-major terms y^T [n, m] = w [k, n]^T . x^T [k, m]:
 // A = w transposed (lda k), B = x (ldb k), D = y (ldd n), and the bias
@@ -16,12 +16,16 @@
 // workspace, so no algorithm splits k over one (every candidate this path
 // takes is GSU0); the results are deterministic from call to call.
 //
+// With accumulate the product is added to y (beta 1, C = D = y):
+// y + (sum + bias) up to the order of the two additions.
+//
 // Plans are kept per (device, m, n, k, bias). A new shape's first call,
-// when its stream is not capturing a graph, times up to kCandidates of the
-// library's heuristic candidates on that stream (one warm-up and two timed
-// runs each, so the call waits for the stream) and keeps the fastest; under
-// capture it takes the heuristic's first. UOCR_ROCM_GEMM=tiles in the
-// environment sends every product to the hand-written kernels.
+// when its stream is not capturing a graph and the call does not accumulate
+// (the timing runs overwrite y), times up to kCandidates of the library's
+// heuristic candidates on that stream (one warm-up and two timed runs each,
+// so the call waits for the stream) and keeps the fastest; otherwise it
+// takes the heuristic's first. UOCR_ROCM_GEMM=tiles in the environment
+// sends every product to the hand-written kernels.
 
 #include <hipblaslt/hipblaslt.h>
 
@@ -102,8 +106,8 @@ bool make_plan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool bias, 
 }
 
 hipblasStatus_t run(hipblasLtHandle_t h, const Plan& p, const hipblasLtMatmulAlgo_t& algo, const uint16_t* x,
-                    const uint16_t* w, float* y, hipStream_t s) {
-  const float alpha = 1.0f, beta = 0.0f;
+                    const uint16_t* w, float* y, hipStream_t s, bool accumulate = false) {
+  const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
   return hipblasLtMatmul(h, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.d, y, p.d, &algo, nullptr, 0, s);
 }
 
@@ -113,7 +117,7 @@ hipblasStatus_t run(hipblasLtHandle_t h, const Plan& p, const hipblasLtMatmulAlg
 // is not one it takes (the caller runs the tiles); an error status when a
 // call into the runtime or the library failed.
 int library_linear_bf16(const char* what, hipStream_t s, const uint16_t* x, int64_t m, int64_t k,
-                        const uint16_t* w, int64_t n, const float* bias, float* y) {
+                        const uint16_t* w, int64_t n, const float* bias, float* y, bool accumulate) {
   if (m < kLibraryMinRows || k % 8 != 0 || !aligned16(x) || !aligned16(w) || !aligned16(y) || tiles_forced()) {
     return kLibraryDeclined;
   }
@@ -135,7 +139,8 @@ int library_linear_bf16(const char* what, hipStream_t s, const uint16_t* x, int6
     if (!make_plan(h, m, n, k, bias != nullptr, p, found, count)) return kLibraryDeclined;
     p.algo = found[0].algo;
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    if (count > 1 && hipStreamIsCapturing(s, &capture) == hipSuccess && capture == hipStreamCaptureStatusNone) {
+    if (count > 1 && !accumulate && hipStreamIsCapturing(s, &capture) == hipSuccess &&
+        capture == hipStreamCaptureStatusNone) {
       if (bias != nullptr) {
         hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
       }
@@ -165,7 +170,7 @@ int library_linear_bf16(const char* what, hipStream_t s, const uint16_t* x, int6
   if (bias != nullptr) {
     hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
   }
-  if (run(h, p, p.algo, x, w, y, s) != HIPBLAS_STATUS_SUCCESS) {
+  if (run(h, p, p.algo, x, w, y, s, accumulate) != HIPBLAS_STATUS_SUCCESS) {
     return fail(UOCR_ROCM_RUNTIME_ERROR, what, "hipblasLtMatmul failed");
   }
   return UOCR_ROCM_OK;
