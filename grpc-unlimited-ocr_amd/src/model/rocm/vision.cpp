@@ -313,7 +313,21 @@ bool VisionEncoder::mlp_bf16(float* x, std::int64_t rows, std::int64_t c, const 
   const std::uint16_t* h = normed_bf16(x, rows, c, ln_w, ln_b, eps);
   if (h == nullptr) return false;
   if (act_bf16_.count() < rows * hidden) act_bf16_ = Array(ctx_, DType::kBF16, rows * hidden);
-  linear_bf16x_act_bf16(ctx_, h, rows, c, w1, hidden, b1, act_bf16_.bf16(), quick);
+  if (rows >= kWideMlpRows) {
+    // many rows: the first product in fp32 through the library's tiles, then
+    // the activation into bf16 as its own pass (the same values as the
+    // fused epilogue on the same sums; a 1024-pixel view's 12 SAM and 24
+    // CLIP MLPs this way took the view from 6.49 to 6.16 ms)
+    if (mlp_wide_.count() < rows * hidden) mlp_wide_ = Array(ctx_, DType::kF32, rows * hidden);
+    project_bf16(h, rows, c, w1, hidden, b1, mlp_wide_.f32());
+    if (quick) {
+      quick_gelu_to_bf16(ctx_, mlp_wide_.f32(), act_bf16_.bf16(), rows * hidden);
+    } else {
+      gelu_erf_to_bf16(ctx_, mlp_wide_.f32(), act_bf16_.bf16(), rows * hidden);
+    }
+  } else {
+    linear_bf16x_act_bf16(ctx_, h, rows, c, w1, hidden, b1, act_bf16_.bf16(), quick);
+  }
   project_bf16(act_bf16_.bf16(), rows, hidden, w2, c, b2, x, true);
   return true;
 }

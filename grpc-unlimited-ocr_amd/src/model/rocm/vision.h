@@ -213,6 +213,11 @@ class VisionEncoder {
   mutable std::map<std::int64_t, Windows> windows_;
   mutable Array split_ws_, x_bf16_;  // project()'s scratch, grown on demand
   mutable Array act_bf16_;           // mlp_bf16()'s activations, grown on demand
+  mutable Array mlp_wide_;           // mlp_bf16()'s fp32 first product (many rows), grown on demand
+  // From this many rows on, an MLP's first product runs unfused (the
+  // library's product, then the activation pass) instead of through the
+  // tile kernel's activation epilogue.
+  static constexpr std::int64_t kWideMlpRows = 128;
   mutable std::map<std::int64_t, Array> win_normed_;  // per grid: bf16 norm rows + a zero row
 };
 
