@@ -55,6 +55,43 @@ def test_expert_topk_ties_and_masked_rows(backend):
     assert_f32_close(w, want_w, 1e-6, "expert scores")
 
 
+def test_expert_topk_near_ties_against_the_host_rule(backend):
+    """The prefill's experts are picked on the device with expert_topk's
+    arithmetic, where the reference's prefill (rows > 1,
+    cuda_decoder.cpp:158-172) picks them on the host after its CPU softmax.
+    Both rank by score with the lower index on a tie, and both scores are
+    monotone in the logits, so the two choices can differ only where two
+    logits one or two ulp apart round to one score on one side and not on
+    the other. Planted at the k-th place: exact ties agree; a pair one ulp
+    apart agrees or swaps exactly that pair."""
+    rows, experts, k = 256, 64, 6
+    g = np.random.default_rng(920)
+    logits = (g.standard_normal((rows, experts)) * 2.0).astype(np.float32)
+    pairs = []
+    for r in range(rows):
+        order = np.argsort(-logits[r], kind="stable")
+        a, b = int(order[k - 1]), int(order[k])  # the k-th and the (k+1)-th
+        lo, hi = min(a, b), max(a, b)
+        base = np.float32(logits[r, order[k - 1]])
+        if r % 2 == 0:  # an exact tie: the lower index must win on both sides
+            logits[r, lo] = logits[r, hi] = base
+        else:  # one ulp apart, the higher index above
+            logits[r, lo] = base
+            logits[r, hi] = np.nextafter(base, np.float32(np.inf), dtype=np.float32)
+        pairs.append((lo, hi))
+    ids, _ = topk(backend, logits, k)
+    want_ids, _ = oracle.expert_topk(logits, k)
+    swaps = 0
+    for r in range(rows):
+        got, want = set(ids[r].tolist()), set(want_ids[r].tolist())
+        if r % 2 == 0:
+            assert got == want, f"row {r}: an exact tie chose differently"
+        elif got != want:
+            assert got ^ want == set(pairs[r]), f"row {r}: {sorted(got ^ want)} against the planted {pairs[r]}"
+            swaps += 1
+    assert swaps < rows // 2  # most one-ulp pairs still resolve alike
+
+
 def expert_stacks(seed, experts, hidden, ffn):
     g = oracle.f32_to_bf16(normal(seed, (experts, ffn, hidden), 0.04))
     u = oracle.f32_to_bf16(normal(seed + 1, (experts, ffn, hidden), 0.04))
