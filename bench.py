@@ -928,6 +928,10 @@ def _kernel_label(name):
     import re
 
     name = re.sub(r"uocr_rocm::\(anonymous namespace\)::", "", name).replace("void ", "").strip()
+    if name.startswith("Cijk_"):  # hipBLASLt's generated kernels: keep the macro tile and the k split
+        tile = re.search(r"_MT(\d+x\d+x\d+)_", name)
+        gsu = re.search(r"_(GSU\d+)_", name)
+        return "hipBLASLt " + " ".join(m.group(1) for m in (tile, gsu) if m)
     if name.endswith(")"):  # drop the trailing "(params)", keeping "(Norm)1"-style template arguments
         depth = 0
         for i in range(len(name) - 1, -1, -1):
