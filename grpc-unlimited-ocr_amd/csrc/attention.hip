@@ -103,6 +103,8 @@ struct AttnArgs {
   // non-null: the output in bf16 (nearest even, the rounding a projection
   // reading it applies) at the same element offsets; out unused
   uint16_t* out16;
+  // rel_dots_k's products are stored times this (1: the dots themselves)
+  float table_mul = 1.0f;
 };
 
 // Four output values at element offset off: fp32, or bf16 into out16.
@@ -434,9 +436,26 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
 // scores' register r of lane half h holds key 8 (r / 4) + 4 h + r % 4, and
 // the product's k index 16 j + 8 h + t reads register 8 j + t, key
 // 16 j + 8 (t / 4) + 4 h + t % 4 (bits 2 and 3 of the key swapped). The
-// scale, bias, online softmax and output are attention_k's.
+// scores are kept in log2 units (the queries times scale log2(e) before the
+// split, the dot table formed times log2(e)), and the online softmax moves
+// a row's reference point only when a tile passes it by more than
+// kX3Slack, so that most tiles rescale nothing.
 constexpr int kX3KStride = 64 + 8;        // K rows in bf16: 144 bytes, 16 lanes' reads on 16 bank groups
 constexpr int kX3VStride = kKeyTile + 8;  // V^T rows: 80 bytes, likewise
+
+constexpr float kX3Slack = 8.0f;           // log2 of the largest probability before a rescale
+
+// The maximum and the sum of lane l's and lane l ^ 32's values, in both
+// lanes (v_permlane32_swap: r[0] holds the low half's values in both halves,
+// r[1] the high half's).
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ int x3_key_slot(int key) {  // bits 2 and 3 swapped (an involution)
   return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
@@ -488,10 +507,12 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
   constexpr int HD = 64, kThreads = 256, kQueriesPerBlock = 4 * kQueriesPerWave;
   using T = Tile<HD, kThreads>;
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-  __shared__ __attribute__((aligned(16))) uint16_t khi[kKeyTile * kX3KStride];
-  __shared__ __attribute__((aligned(16))) uint16_t klo[kKeyTile * kX3KStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vhi[HD * kX3VStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vlo[HD * kX3VStride];
+  // two stages: tile t + 1 is split into one while tile t is read from the other
+  constexpr int kKElems = kKeyTile * kX3KStride, kVElems = HD * kX3VStride;
+  __shared__ __attribute__((aligned(16))) uint16_t khi_s[2 * kKElems];
+  __shared__ __attribute__((aligned(16))) uint16_t klo_s[2 * kKElems];
+  __shared__ __attribute__((aligned(16))) uint16_t vhi_s[2 * kVElems];
+  __shared__ __attribute__((aligned(16))) uint16_t vlo_s[2 * kVElems];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hl = lane >> 5, c = lane & 31;
@@ -507,24 +528,33 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
                                                    acc, 0, 0, 0);
   };
 
-  // Tile loads with every address in range (rows past the keys read the
-  // last key's row; their scores are -inf, their probabilities 0) and no
-  // branch, so that a tile's use waits only for its own loads, not for the
-  // next tile's in flight.
+  // Tile loads: the keys are whole tiles (the grid's width is a multiple of
+  // the tile), so every row is in range; this thread's row offsets are
+  // formed once, a tile's offset added per load. No branch, so that a
+  // tile's use waits only for its own loads, not for the next tile's.
   float4 kr[T::kPerThread], vr[T::kPerThread];
+  const float* kp[T::kPerThread];
+  const float* vp[T::kPerThread];
+#pragma unroll
+  for (int j = 0; j < T::kPerThread; ++j) {
+    const int idx = static_cast<int>(threadIdx.x) + kThreads * j;
+    const int row = idx / (HD / 4), c4 = idx % (HD / 4);
+    kp[j] = kb + row * a.ldk + 4 * c4;
+    vp[j] = vb + row * a.ldv + 4 * c4;
+  }
   auto load_kv = [&](int key0) {
+    const int64_t ko = key0 * a.ldk, vo = key0 * a.ldv;
 #pragma unroll
     for (int j = 0; j < T::kPerThread; ++j) {
-      const int idx = static_cast<int>(threadIdx.x) + kThreads * j;
-      const int row = idx / (HD / 4), c4 = idx % (HD / 4);
-      const int key = key0 + row < a.keys ? key0 + row : a.keys - 1;
-      kr[j] = *reinterpret_cast<const float4*>(kb + key * a.ldk + 4 * c4);
-      vr[j] = *reinterpret_cast<const float4*>(vb + key * a.ldv + 4 * c4);
+      kr[j] = *reinterpret_cast<const float4*>(kp[j] + ko);
+      vr[j] = *reinterpret_cast<const float4*>(vp[j] + vo);
     }
   };
   load_kv(0);
 
-  // this lane's query columns 16 b + 8 h + (0..7), b < 4, split
+  // this lane's query columns 16 b + 8 h + (0..7), b < 4, times the scale
+  // and log2(e) (the scores in log2 units, for exp2), split
+  const float qmul = a.scale * kLog2e;
   u32x4 qh[4], ql[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
@@ -534,11 +564,14 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
       t0 = *reinterpret_cast<const float4*>(qr);
       t1 = *reinterpret_cast<const float4*>(qr + 4);
     }
-    const float x[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+    const float x[8] = {t0.x * qmul, t0.y * qmul, t0.z * qmul, t0.w * qmul,
+                        t1.x * qmul, t1.y * qmul, t1.z * qmul, t1.w * qmul};
     split8(x, qh[b], ql[b]);
   }
 
-  store_tile_x3(khi, klo, vhi, vlo, kr, vr);
+  store_tile_x3(khi_s, klo_s, vhi_s, vlo_s, kr, vr);
+  const int tiles = a.keys / kKeyTile;  // whole tiles: the grid's width is a multiple of the tile
+  load_kv(tiles > 1 ? kKeyTile : 0);    // tile 1 (tile 0 again when there is no tile 1)
   __syncthreads();
 
   f32x16 o[2];
@@ -547,12 +580,18 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[b][r] = 0.0f;
   }
-  float m = -INFINITY, l = 0.0f;
+  // m: the row's reference point in log2 units, the running maximum or at
+  // most kX3Slack below it, so that a probability is at most 2^kX3Slack
+  // (exact enough in fp32 and in its bf16 parts; the output divides by a
+  // total over the same reference). It moves, and the sums are rescaled,
+  // only when a tile's maximum passes it by more than that. lh: the total
+  // of this lane half's probabilities (the halves added at the end).
+  float m = -INFINITY, lh = 0.0f;
   const bool live = q0 < a.rows;
   const float* trow = a.table + (slice * a.rows + (qin ? qrow : 0)) * static_cast<int64_t>(a.dots_ld);
-  const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
-  // a tile's bias terms: its height term and the lane's 16 width terms
-  // (keys kx0 + 8 g + 4 h + (0..3)), requested a tile ahead like K and V
+  // a tile's bias terms (in log2 units: the table was formed times log2(e)):
+  // its height term and the lane's 16 width terms (keys kx0 + 8 g + 4 h +
+  // (0..3)), requested a tile ahead like K and V
   auto load_bias = [&](int key0, float& dh, float (&dwv)[16]) {
     const int ky0 = key0 / a.w, kx0 = key0 - ky0 * a.w;
     dh = trow[ky0];
@@ -565,65 +604,80 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
       dwv[4 * g + 3] = tw.w;
     }
   };
-  float dh = 0.0f, dwv[16], dh_next = 0.0f, dwv_next[16];
-  load_bias(0, dh_next, dwv_next);
-  for (int t = 0; t < tiles; ++t) {
+  // One key tile, read from LDS stage `stage`, its bias terms in (dh, dwv).
+  // First tile t + 1 (in kr, vr since tile t - 1) is split into the other
+  // stage and tile t + 2 requested; the next tile's bias terms are requested
+  // into (dh_next, dwv_next) (two register sets used in turn: no copies).
+  // One barrier per tile: after it, stage t + 1 is whole and no wave still
+  // reads stage t, which tile t + 1 then refills with tile t + 2.
+  auto tile = [&](int t, int stage, const float dh, const float (&dwv)[16], float& dh_next,
+                  float (&dwv_next)[16]) {
     const int key0 = t * kKeyTile;
     const bool more = t + 1 < tiles;
-    // this tile's bias terms, requested an iteration ago, taken before the
-    // next tile's requests go out (so that the copy waits for nothing
-    // newer); then the next tile's operands (the last tile's again after
-    // the last)
-    dh = dh_next;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) dwv[r] = dwv_next[r];
-    const int next0 = more ? key0 + kKeyTile : key0;
-    load_kv(next0);
-    load_bias(next0, dh_next, dwv_next);
+    if (more) {
+      store_tile_x3(khi_s + (1 - stage) * kKElems, klo_s + (1 - stage) * kKElems, vhi_s + (1 - stage) * kVElems,
+                    vlo_s + (1 - stage) * kVElems, kr, vr);
+    }
+    load_kv(t + 2 < tiles ? key0 + 2 * kKeyTile : key0);  // the current tile again past the end
+    load_bias(more ? key0 + kKeyTile : key0, dh_next, dwv_next);
+    const uint16_t* khi = khi_s + stage * kKElems;
+    const uint16_t* klo = klo_s + stage * kKElems;
+    const uint16_t* vhi = vhi_s + stage * kVElems;
+    const uint16_t* vlo = vlo_s + stage * kVElems;
     if (live) {
+      // every K operand of the tile read from LDS before the first product,
+      // then the V operands before the softmax (their latency behind it)
+      u32x4 kh[4], kl[4], vh[2][2], vl[2][2];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int at = c * kX3KStride + 16 * b + 8 * hl;
+        kh[b] = *reinterpret_cast<const u32x4*>(khi + at);
+        kl[b] = *reinterpret_cast<const u32x4*>(klo + at);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the products
       // S^T = K Q^T: 32 keys x 32 queries, the small products first
       f32x16 s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.0f;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int at = c * kX3KStride + 16 * b + 8 * hl;
-        const u32x4 kh = *reinterpret_cast<const u32x4*>(khi + at);
-        const u32x4 kl = *reinterpret_cast<const u32x4*>(klo + at);
-        s = mfma(kl, qh[b], s);
-        s = mfma(kh, ql[b], s);
-        s = mfma(kh, qh[b], s);
+        s = mfma(kl[b], qh[b], s);
+        s = mfma(kh[b], ql[b], s);
+        s = mfma(kh[b], qh[b], s);
       }
-      // scale, the tile's bias terms, running max
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int at = (32 * b + c) * kX3VStride + 16 * j + 8 * hl;
+          vh[b][j] = *reinterpret_cast<const u32x4*>(vhi + at);
+          vl[b][j] = *reinterpret_cast<const u32x4*>(vlo + at);
+        }
+      }
+      // the bias terms, the tile's row maximum
       float tmax = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = key0 + 8 * (r / 4) + 4 * hl + (r % 4);
-        float x = s[r] * a.scale;
-        x = x + (dh + dwv[r]);
-        x = key < a.keys ? x : -INFINITY;
-        s[r] = x;
-        tmax = fmaxf(tmax, x);
+        s[r] = s[r] + (dh + dwv[r]);
+        tmax = fmaxf(tmax, s[r]);
       }
-      tmax = fmaxf(tmax, partner(tmax));
-      const float m_new = fmaxf(m, tmax);
-      const bool dead = m_new == -INFINITY;
-      const float corr = dead ? 1.0f : __builtin_amdgcn_exp2f((m - m_new) * kLog2e);
-      float psum = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = dead ? 0.0f : __builtin_amdgcn_exp2f((s[r] - m_new) * kLog2e);
-        psum += s[r];
-      }
-      psum += partner(psum);
-      l = l * corr + psum;
-      m = m_new;
-      if (__ballot(corr != 1.0f) != 0) {
+      tmax = max_halves(tmax);
+      const bool grow = tmax > m + kX3Slack;
+      if (__ballot(grow) != 0) {
+        const float m_new = grow ? tmax : m;
+        const float corr = grow ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+        lh *= corr;
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[b][r] *= corr;
         }
+        m = m_new;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = __builtin_amdgcn_exp2f(s[r] - m);
+        lh += s[r];
       }
       // P split: product j takes registers 8 j .. 8 j + 7
       u32x4 ph[2], pl[2];
@@ -638,22 +692,22 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
       for (int b = 0; b < 2; ++b) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const int at = (32 * b + c) * kX3VStride + 16 * j + 8 * hl;
-          const u32x4 vh = *reinterpret_cast<const u32x4*>(vhi + at);
-          const u32x4 vl = *reinterpret_cast<const u32x4*>(vlo + at);
-          o[b] = mfma(vl, ph[j], o[b]);
-          o[b] = mfma(vh, pl[j], o[b]);
-          o[b] = mfma(vh, ph[j], o[b]);
+          o[b] = mfma(vl[b][j], ph[j], o[b]);
+          o[b] = mfma(vh[b][j], pl[j], o[b]);
+          o[b] = mfma(vh[b][j], ph[j], o[b]);
         }
       }
     }
-    __syncthreads();  // every wave is done with this tile
-    if (more) {
-      store_tile_x3(khi, klo, vhi, vlo, kr, vr);
-      __syncthreads();
-    }
+    __syncthreads();
+  };
+  float dh_a = 0.0f, dwv_a[16], dh_b = 0.0f, dwv_b[16];
+  load_bias(0, dh_a, dwv_a);
+  for (int t = 0; t < tiles; t += 2) {
+    tile(t, 0, dh_a, dwv_a, dh_b, dwv_b);
+    if (t + 1 < tiles) tile(t + 1, 1, dh_b, dwv_b, dh_a, dwv_a);
   }
 
+  const float l = sum_halves(lh);
   if (!qin) return;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   const int64_t orow = slice_at(a, slice, a.so, a.io) + qrow * a.ldo;
@@ -881,7 +935,7 @@ __global__ __launch_bounds__(kBlock) void rel_dots_k(const AttnArgs a) {
       float acc = 0.0f;
 #pragma unroll 16
       for (int d = 0; d < HD; ++d) acc += qrow[d] * trow[d];
-      out[static_cast<int64_t>(query(i)) * a.dots_ld + (height ? r : a.dw_off + r)] = acc;
+      out[static_cast<int64_t>(query(i)) * a.dots_ld + (height ? r : a.dw_off + r)] = acc * a.table_mul;
     }
     return;
   }
@@ -917,7 +971,7 @@ __global__ __launch_bounds__(kBlock) void rel_dots_k(const AttnArgs a) {
       float* orow = out + static_cast<int64_t>(query(i0 + u)) * a.dots_ld + (height ? 0 : a.dw_off);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        if (r0 + v < nr) orow[r0 + v] = acc[u][v];
+        if (r0 + v < nr) orow[r0 + v] = acc[u][v] * a.table_mul;
       }
     }
   }
@@ -1006,6 +1060,9 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
              static_cast<int>(lay.dw_off), table ? workspace : nullptr, table ? workspace : nullptr,
              static_cast<int>(inner), iq, ik, iv, io, out16};
   if (out16 != nullptr) a.out = nullptr;
+  // the split-operand kernel takes the bias in log2 units
+  const bool x3 = lay.tile_rows && table && out16 != nullptr && hd == 64;
+  if (x3) a.table_mul = kLog2e;
   if (table) {
     const size_t lds = sizeof(float) * static_cast<size_t>((h + w) * (hd + 1));
     const dim3 grid(static_cast<unsigned>(h + w), static_cast<unsigned>(slices));
@@ -1019,7 +1076,7 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
     }
     if (const int st = check_launch(what)) return st;
   }
-  if (lay.tile_rows && table && out16 != nullptr && hd == 64) {
+  if (x3) {
     // a bf16 output: the products on the bf16 matrix cores, operands split
     const dim3 grid(static_cast<unsigned>((n + 4 * kQueriesPerWave - 1) / (4 * kQueriesPerWave)),
                     static_cast<unsigned>(slices));
