@@ -503,8 +503,19 @@ __device__ __forceinline__ void store_tile_x3(uint16_t* khi, uint16_t* klo, uint
   }
 }
 
+// kRows 0: a grid of whole tiles, each key tile 32 keys of one grid row
+// (the global layers); kRows 1, 2 or 4: each key tile kRows grid rows of at
+// most 32 / kRows keys (the windows: 14 x 14 takes 2 rows of 14 per tile),
+// a row's keys in the 32 / kRows slots from slot row * 32 / kRows, the
+// slots past the row's width dead. Register r of lane half h holds slot
+// 8 (r / 4) + 4 h + r % 4, which lies in row (r / 4) kRows / 4 of the tile
+// whatever h: the height term is a register chosen at compile time, the
+// width terms (dead slots -inf) the same in every tile.
+template <int kRows>
 __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
   constexpr int HD = 64, kThreads = 256, kQueriesPerBlock = 4 * kQueriesPerWave;
+  constexpr int kSlotsPerRow = kRows == 0 ? kKeyTile : kKeyTile / kRows;
+  constexpr int kDh = kRows == 0 ? 1 : kRows;  // height terms per tile
   using T = Tile<HD, kThreads>;
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
   // two stages: tile t + 1 is split into one while tile t is read from the other
@@ -527,27 +538,43 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x), __builtin_bit_cast(bf16x8, y),
                                                    acc, 0, 0, 0);
   };
+  const int tiles = kRows == 0 ? a.keys / kKeyTile : (a.h + kRows - 1) / kRows;
 
-  // Tile loads: the keys are whole tiles (the grid's width is a multiple of
-  // the tile), so every row is in range; this thread's row offsets are
-  // formed once, a tile's offset added per load. No branch, so that a
-  // tile's use waits only for its own loads, not for the next tile's.
+  // Tile loads, every address in range and no branch, so that a tile's use
+  // waits only for its own loads, not for the next tile's. kRows 0: the
+  // keys are whole tiles, this thread's row offsets formed once and a
+  // tile's offset added per load. Otherwise a slot's key is its tile row's
+  // grid row (the last grid row past the last) and its column (the last
+  // column for a dead slot; its score is -inf, its probability 0).
   float4 kr[T::kPerThread], vr[T::kPerThread];
   const float* kp[T::kPerThread];
   const float* vp[T::kPerThread];
+  int srow[T::kPerThread], scol[T::kPerThread], sc4[T::kPerThread];
 #pragma unroll
   for (int j = 0; j < T::kPerThread; ++j) {
     const int idx = static_cast<int>(threadIdx.x) + kThreads * j;
-    const int row = idx / (HD / 4), c4 = idx % (HD / 4);
-    kp[j] = kb + row * a.ldk + 4 * c4;
-    vp[j] = vb + row * a.ldv + 4 * c4;
+    const int slot = idx / (HD / 4), c4 = idx % (HD / 4);
+    kp[j] = kb + slot * a.ldk + 4 * c4;
+    vp[j] = vb + slot * a.ldv + 4 * c4;
+    srow[j] = slot / kSlotsPerRow;
+    scol[j] = min(slot % kSlotsPerRow, a.w - 1);
+    sc4[j] = 4 * c4;
   }
-  auto load_kv = [&](int key0) {
-    const int64_t ko = key0 * a.ldk, vo = key0 * a.ldv;
+  auto load_kv = [&](int t) {
+    if constexpr (kRows == 0) {
+      const int64_t ko = static_cast<int64_t>(t) * kKeyTile * a.ldk, vo = static_cast<int64_t>(t) * kKeyTile * a.ldv;
 #pragma unroll
-    for (int j = 0; j < T::kPerThread; ++j) {
-      kr[j] = *reinterpret_cast<const float4*>(kp[j] + ko);
-      vr[j] = *reinterpret_cast<const float4*>(vp[j] + vo);
+      for (int j = 0; j < T::kPerThread; ++j) {
+        kr[j] = *reinterpret_cast<const float4*>(kp[j] + ko);
+        vr[j] = *reinterpret_cast<const float4*>(vp[j] + vo);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < T::kPerThread; ++j) {
+        const int key = min(t * kRows + srow[j], a.h - 1) * a.w + scol[j];
+        kr[j] = *reinterpret_cast<const float4*>(kb + key * a.ldk + sc4[j]);
+        vr[j] = *reinterpret_cast<const float4*>(vb + key * a.ldv + sc4[j]);
+      }
     }
   };
   load_kv(0);
@@ -570,8 +597,7 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
   }
 
   store_tile_x3(khi_s, klo_s, vhi_s, vlo_s, kr, vr);
-  const int tiles = a.keys / kKeyTile;  // whole tiles: the grid's width is a multiple of the tile
-  load_kv(tiles > 1 ? kKeyTile : 0);    // tile 1 (tile 0 again when there is no tile 1)
+  load_kv(tiles > 1 ? 1 : 0);  // tile 1 (tile 0 again when there is no tile 1)
   __syncthreads();
 
   f32x16 o[2];
@@ -589,37 +615,58 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
   float m = -INFINITY, lh = 0.0f;
   const bool live = q0 < a.rows;
   const float* trow = a.table + (slice * a.rows + (qin ? qrow : 0)) * static_cast<int64_t>(a.dots_ld);
-  // a tile's bias terms (in log2 units: the table was formed times log2(e)):
-  // its height term and the lane's 16 width terms (keys kx0 + 8 g + 4 h +
-  // (0..3)), requested a tile ahead like K and V
-  auto load_bias = [&](int key0, float& dh, float (&dwv)[16]) {
-    const int ky0 = key0 / a.w, kx0 = key0 - ky0 * a.w;
-    dh = trow[ky0];
+  // The bias terms, in log2 units (the table was formed times log2(e)).
+  // kRows 0: a tile's height term and the lane's 16 width terms (keys
+  // kx0 + 8 g + 4 h + (0..3)). Otherwise the width terms of the lane's
+  // slots, once, and a tile's kRows height terms (-inf past the grid).
+  float dwc[16];
+  if constexpr (kRows != 0) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float4 tw = *reinterpret_cast<const float4*>(trow + a.dw_off + kx0 + 8 * g + 4 * hl);
-      dwv[4 * g] = tw.x;
-      dwv[4 * g + 1] = tw.y;
-      dwv[4 * g + 2] = tw.z;
-      dwv[4 * g + 3] = tw.w;
+    for (int r = 0; r < 16; ++r) {
+      const int col = (8 * (r / 4) + 4 * hl + r % 4) % kSlotsPerRow;
+      const float t = trow[a.dw_off + min(col, a.w - 1)];
+      dwc[r] = col < a.w ? t : -INFINITY;
+    }
+  }
+  struct Bias {
+    float dh[kDh];
+    float dw[kRows == 0 ? 16 : 1];
+  };
+  auto load_bias = [&](int t, Bias& bias) {
+    if constexpr (kRows == 0) {
+      const int key0 = t * kKeyTile, ky0 = key0 / a.w, kx0 = key0 - ky0 * a.w;
+      bias.dh[0] = trow[ky0];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 tw = *reinterpret_cast<const float4*>(trow + a.dw_off + kx0 + 8 * g + 4 * hl);
+        bias.dw[4 * g] = tw.x;
+        bias.dw[4 * g + 1] = tw.y;
+        bias.dw[4 * g + 2] = tw.z;
+        bias.dw[4 * g + 3] = tw.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) {
+        const int row = t * kRows + i;
+        const float d = trow[min(row, a.h - 1)];
+        bias.dh[i] = row < a.h ? d : -INFINITY;
+      }
     }
   };
-  // One key tile, read from LDS stage `stage`, its bias terms in (dh, dwv).
+  // One key tile, read from LDS stage `stage`, its bias terms in `bias`.
   // First tile t + 1 (in kr, vr since tile t - 1) is split into the other
   // stage and tile t + 2 requested; the next tile's bias terms are requested
-  // into (dh_next, dwv_next) (two register sets used in turn: no copies).
-  // One barrier per tile: after it, stage t + 1 is whole and no wave still
-  // reads stage t, which tile t + 1 then refills with tile t + 2.
-  auto tile = [&](int t, int stage, const float dh, const float (&dwv)[16], float& dh_next,
-                  float (&dwv_next)[16]) {
-    const int key0 = t * kKeyTile;
+  // into `next` (two register sets used in turn: no copies). One barrier
+  // per tile: after it, stage t + 1 is whole and no wave still reads stage
+  // t, which tile t + 1 then refills with tile t + 2.
+  auto tile = [&](int t, int stage, const Bias& bias, Bias& next) {
     const bool more = t + 1 < tiles;
     if (more) {
       store_tile_x3(khi_s + (1 - stage) * kKElems, klo_s + (1 - stage) * kKElems, vhi_s + (1 - stage) * kVElems,
                     vlo_s + (1 - stage) * kVElems, kr, vr);
     }
-    load_kv(t + 2 < tiles ? key0 + 2 * kKeyTile : key0);  // the current tile again past the end
-    load_bias(more ? key0 + kKeyTile : key0, dh_next, dwv_next);
+    load_kv(t + 2 < tiles ? t + 2 : t);  // the current tile again past the end
+    load_bias(more ? t + 1 : t, next);
     const uint16_t* khi = khi_s + stage * kKElems;
     const uint16_t* klo = klo_s + stage * kKElems;
     const uint16_t* vhi = vhi_s + stage * kVElems;
@@ -658,7 +705,11 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
       float tmax = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[r] = s[r] + (dh + dwv[r]);
+        if constexpr (kRows == 0) {
+          s[r] = s[r] + (bias.dh[0] + bias.dw[r]);
+        } else {
+          s[r] = s[r] + (bias.dh[(r / 4) * kRows / 4] + dwc[r]);
+        }
         tmax = fmaxf(tmax, s[r]);
       }
       tmax = max_halves(tmax);
@@ -700,11 +751,11 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
     }
     __syncthreads();
   };
-  float dh_a = 0.0f, dwv_a[16], dh_b = 0.0f, dwv_b[16];
-  load_bias(0, dh_a, dwv_a);
+  Bias bias_a, bias_b;
+  load_bias(0, bias_a);
   for (int t = 0; t < tiles; t += 2) {
-    tile(t, 0, dh_a, dwv_a, dh_b, dwv_b);
-    if (t + 1 < tiles) tile(t + 1, 1, dh_b, dwv_b, dh_a, dwv_a);
+    tile(t, 0, bias_a, bias_b);
+    if (t + 1 < tiles) tile(t + 1, 1, bias_b, bias_a);
   }
 
   const float l = sum_halves(lh);
@@ -1060,8 +1111,17 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
              static_cast<int>(lay.dw_off), table ? workspace : nullptr, table ? workspace : nullptr,
              static_cast<int>(inner), iq, ik, iv, io, out16};
   if (out16 != nullptr) a.out = nullptr;
-  // the split-operand kernel takes the bias in log2 units
-  const bool x3 = lay.tile_rows && table && out16 != nullptr && hd == 64;
+  // a bf16 output from the dot table with head dim 64: the split-operand
+  // kernel, whose tiles are 32 keys of one grid row (whole tiles) or 4, 2
+  // or 1 grid rows of at most 8, 16 or 31 keys; it takes the bias in log2
+  // units
+  const int x3_rows = !(table && out16 != nullptr && hd == 64) ? -1
+                      : lay.tile_rows                          ? 0
+                      : w <= 8                                 ? 4
+                      : w <= 16                                ? 2
+                      : w < kKeyTile                           ? 1
+                                                               : -1;
+  const bool x3 = x3_rows >= 0;
   if (x3) a.table_mul = kLog2e;
   if (table) {
     const size_t lds = sizeof(float) * static_cast<size_t>((h + w) * (hd + 1));
@@ -1081,7 +1141,12 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
     const dim3 grid(static_cast<unsigned>((n + 4 * kQueriesPerWave - 1) / (4 * kQueriesPerWave)),
                     static_cast<unsigned>(slices));
     clear_launch_error();
-    attention_x3_k<<<grid, 256, 0, as_stream(stream)>>>(a);
+    switch (x3_rows) {
+      case 0: attention_x3_k<0><<<grid, 256, 0, as_stream(stream)>>>(a); break;
+      case 1: attention_x3_k<1><<<grid, 256, 0, as_stream(stream)>>>(a); break;
+      case 2: attention_x3_k<2><<<grid, 256, 0, as_stream(stream)>>>(a); break;
+      default: attention_x3_k<4><<<grid, 256, 0, as_stream(stream)>>>(a); break;
+    }
     return check_launch(what);
   }
   if (lay.tile_rows && table) return launch<Bias::kRelPosTable>(what, stream, hd, slices, a);

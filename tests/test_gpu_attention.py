@@ -163,20 +163,22 @@ def test_attention_rel_pos_windows_straight_from_the_rows(backend, windows, head
 
 @pytest.mark.parametrize("windows,heads,h,w,amp", [(25, 12, 14, 14, 1.0), (1, 12, 64, 64, 1.0), (3, 2, 7, 9, 1.0),
                                                    (2, 3, 5, 32, 1.0), (3, 2, 1, 32, 1.0), (1, 2, 2, 32, 1.0),
-                                                   (1, 2, 8, 32, 6.0)])
+                                                   (1, 2, 8, 32, 6.0), (2, 2, 5, 6, 1.0), (1, 2, 3, 20, 1.0),
+                                                   (2, 2, 14, 14, 6.0), (1, 2, 2, 40, 1.0)])
 def test_attention_rel_pos_windows_into_bf16_is_the_rounded_output(backend, windows, heads, h, w, amp):
     """The windows' attention written in bf16 (the rounding the output
     projection applies): the fp32 output then round_bf16, SAM's windowed and
-    global (one 64 x 64 window) layers. Bitwise where the products stay fp32
-    (windows narrower than a 32-key tile row); a grid of whole tiles takes
-    the products on the bf16 matrix cores with split operands, which moves
-    some outputs across a bf16 rounding boundary: there every element is
-    within one bf16 step of the fp32 output, most equal to its rounding, and
-    the result within 2^-8 of the oracle (a bf16 step: the output's own
-    rounding and a moved boundary). One tile, two tiles, an odd count; amp
-    6 spreads the scores (standard deviation about 36) so that later tiles
-    pass a row's reference point by more than the kernel's slack and the
-    sums are rescaled mid-row."""
+    global (one 64 x 64 window) layers. Grids of whole 32-key tile rows, and
+    grids under 32 wide (4, 2 or 1 grid rows per key tile: widths 6, 9 and
+    14, 20), take the products on the bf16 matrix cores with split operands,
+    which moves some outputs across a bf16 rounding boundary: there every
+    element is within one bf16 step of the fp32 output, most equal to its
+    rounding, and the result within 2^-8 of the oracle (a bf16 step: the
+    output's own rounding and a moved boundary). Other widths (40) keep the
+    fp32 products: bitwise. One tile, two tiles, an odd count, a last tile
+    with grid rows past the grid; amp 6 spreads the scores (standard
+    deviation about 36) so that later tiles pass a row's reference point by
+    more than the kernel's slack and the sums are rescaled mid-row."""
     hd, n = 64, h * w
     width = heads * hd
     qkv = dev_f32(normal(750 + n, (windows * n, 3 * width)) * np.float32(amp))
@@ -189,7 +191,7 @@ def test_attention_rel_pos_windows_into_bf16_is_the_rounded_output(backend, wind
     got = torch.full((windows * n, width), float("nan"), dtype=torch.bfloat16, device="cuda")
     backend.attention_rel_pos_windows(qkv, got, heads, windows, h, w, hd, 0.125, rh, rw, ws)
     torch.cuda.synchronize()
-    if w % 32 != 0:
+    if w % 32 != 0 and w > 32:
         assert torch.equal(got.view(torch.int16), want.view(torch.int16))
         return
     got_f = oracle.bf16_to_f32(got.view(torch.int16).cpu().numpy().view(np.uint16))
