@@ -946,17 +946,18 @@ __global__ __launch_bounds__(64 * kSplitWaves) void attention_keysplit_k(const A
 }
 
 // The relative-position dot products of every (slice, query row) into
-// table [slices][rows][dots_ld] (height terms at 0, width terms at dw_off):
-// block (j, s) takes table slice j of slice s (rh[qy = j] for j < h, else
-// rw[qx = j - h]) and the h or w query rows that use it, stages both in LDS
-// (rows padded to HD + 1 floats: the threads of a pass read different
-// banks), and forms every (query, table row) dot, fp32 in column order, 4 x
-// 4 of them per thread (one per thread where there are few).
+// table [slices][rows][dots_ld] (height terms at 0, width terms at dw_off),
+// on the fp32 matrix cores: block (j, s) takes table slice j of slice s
+// (rh[qy = j] for j < h, else rw[qx = j - h]) and the h or w query rows that
+// use it, a product Q_j [queries, hd] . T_j^T [hd, table rows] in 32 x 32
+// tiles, one tile per wave at a time. Lane l of a tile holds query row
+// l % 32 and table row l % 32 (past the last: the last), columns
+// 32 (l / 32) + (0..31) of each 64-column chunk straight from memory; step
+// i of the chunk's 32 v_mfma_f32_32x32x2f32 takes columns i and 32 + i.
 // Each table slice is read once per slice here, where a workgroup of the
 // attention forming its own dots reads a width slice per query.
 template <int HD>
-__global__ __launch_bounds__(kBlock) void rel_dots_k(const AttnArgs a) {
-  extern __shared__ float rel_lds[];
+__global__ __launch_bounds__(256) void rel_dots_k(const AttnArgs a) {
   const int j = static_cast<int>(blockIdx.x);
   const int64_t slice = blockIdx.y;
   const bool height = j < a.h;
@@ -964,65 +965,47 @@ __global__ __launch_bounds__(kBlock) void rel_dots_k(const AttnArgs a) {
   const int nr = height ? a.h : a.w;  // its rows: dots per query
   const float* tab = height ? a.rh + static_cast<int64_t>(j) * a.h * HD : a.rw + static_cast<int64_t>(j - a.h) * a.w * HD;
   auto query = [&](int i) { return height ? j * a.w + i : i * a.w + (j - a.h); };
-  float* qs = rel_lds;
-  float* ts = rel_lds + nq * (HD + 1);
   const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
-  for (int e = static_cast<int>(threadIdx.x); e < nq * HD; e += kBlock) {
-    const int i = e / HD, d = e - i * HD;
-    qs[i * (HD + 1) + d] = qb[static_cast<int64_t>(query(i)) * a.ldq + d];
-  }
-  for (int e = static_cast<int>(threadIdx.x); e < nr * HD; e += kBlock) {
-    const int r = e / HD, d = e - r * HD;
-    ts[r * (HD + 1) + d] = tab[e];
-  }
-  __syncthreads();
   float* out = a.table_out + slice * a.rows * static_cast<int64_t>(a.dots_ld);
-  if (nq * nr < 4 * kBlock) {
-    // few pairs (a small window): one per thread
-    for (int p = static_cast<int>(threadIdx.x); p < nq * nr; p += kBlock) {
-      const int i = p / nr, r = p - i * nr;
-      const float* qrow = qs + i * (HD + 1);
-      const float* trow = ts + r * (HD + 1);
-      float acc = 0.0f;
-#pragma unroll 16
-      for (int d = 0; d < HD; ++d) acc += qrow[d] * trow[d];
-      out[static_cast<int64_t>(query(i)) * a.dots_ld + (height ? r : a.dw_off + r)] = acc * a.table_mul;
-    }
-    return;
-  }
-  // 4 x 4 (query, table row) blocks per thread: 8 LDS reads feed 16 FMAs
-  const int nqb = (nq + 3) / 4, nrb = (nr + 3) / 4;
-  for (int blk = static_cast<int>(threadIdx.x); blk < nqb * nrb; blk += kBlock) {
-    const int i0 = 4 * (blk / nrb), r0 = 4 * (blk - (blk / nrb) * nrb);
-    const float* qrow[4];
-    const float* trow[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int tq = (nq + 31) / 32, tr = (nr + 31) / 32;
+  const int waves = static_cast<int>(blockDim.x) / 64;
+  for (int tile = wave; tile < tq * tr; tile += waves) {
+    const int iq = tile / tr, ir = tile - iq * tr;
+    const int qi = min(iq * 32 + l32, nq - 1), ti = min(ir * 32 + l32, nr - 1);
+    const float* qrow = qb + static_cast<int64_t>(query(qi)) * a.ldq + 32 * hh;
+    const float* trow = tab + static_cast<int64_t>(ti) * HD + 32 * hh;
+    f32x16 acc;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      qrow[u] = qs + (i0 + u < nq ? i0 + u : nq - 1) * (HD + 1);
-      trow[u] = ts + (r0 + u < nr ? r0 + u : nr - 1) * (HD + 1);
-    }
-    float acc[4][4] = {};
-#pragma unroll 8
-    for (int d = 0; d < HD; ++d) {
-      float qv[4], tv[4];
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        qv[u] = qrow[u][d];
-        tv[u] = trow[u][d];
+    for (int k0 = 0; k0 < HD; k0 += 64) {
+      float qv[32], tv[32];
+#pragma unroll
+      for (int i = 0; i < 32; i += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(qrow + k0 + i);
+        const float4 y = *reinterpret_cast<const float4*>(trow + k0 + i);
+        qv[i] = x.x;
+        qv[i + 1] = x.y;
+        qv[i + 2] = x.z;
+        qv[i + 3] = x.w;
+        tv[i] = y.x;
+        tv[i + 1] = y.y;
+        tv[i + 2] = y.z;
+        tv[i + 3] = y.w;
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[u][v] += qv[u] * tv[v];
-      }
+      for (int i = 0; i < 32; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(qv[i], tv[i], acc, 0, 0, 0);
     }
+    // D[query][table row]: register r of lane l holds query 8 (r / 4) +
+    // 4 (l / 32) + r % 4 of the tile, table row l % 32
+    const int t = ir * 32 + l32;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (i0 + u >= nq) continue;
-      float* orow = out + static_cast<int64_t>(query(i0 + u)) * a.dots_ld + (height ? 0 : a.dw_off);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        if (r0 + v < nr) orow[r0 + v] = acc[u][v] * a.table_mul;
+    for (int r = 0; r < 16; ++r) {
+      const int q = iq * 32 + 8 * (r / 4) + 4 * hh + r % 4;
+      if (q < nq && t < nr) {
+        out[static_cast<int64_t>(query(q)) * a.dots_ld + (height ? t : a.dw_off + t)] = acc[r] * a.table_mul;
       }
     }
   }
@@ -1124,15 +1107,15 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
   const bool x3 = x3_rows >= 0;
   if (x3) a.table_mul = kLog2e;
   if (table) {
-    const size_t lds = sizeof(float) * static_cast<size_t>((h + w) * (hd + 1));
+    // one wave per 32 x 32 tile of a block's product, up to 4 waves
+    const int64_t tiles = ((h + 31) / 32) * ((w + 31) / 32);
+    const unsigned threads = static_cast<unsigned>(64 * (tiles < 4 ? tiles : 4));
     const dim3 grid(static_cast<unsigned>(h + w), static_cast<unsigned>(slices));
     clear_launch_error();
     if (hd == 64) {
-      allow_lds(rel_dots_k<64>, lds);
-      rel_dots_k<64><<<grid, kBlock, lds, as_stream(stream)>>>(a);
+      rel_dots_k<64><<<grid, threads, 0, as_stream(stream)>>>(a);
     } else {
-      allow_lds(rel_dots_k<128>, lds);
-      rel_dots_k<128><<<grid, kBlock, lds, as_stream(stream)>>>(a);
+      rel_dots_k<128><<<grid, threads, 0, as_stream(stream)>>>(a);
     }
     if (const int st = check_launch(what)) return st;
   }
