@@ -1011,6 +1011,59 @@ __global__ __launch_bounds__(256) void rel_dots_k(const AttnArgs a) {
   }
 }
 
+// rel_dots_k for grids at most 16 by 16 (SAM's 14 x 14 windows): a table
+// slice's product is one 16 x 16 tile of v_mfma_f32_16x16x4f32, a wave per
+// table slice, four table slices per workgroup. Lane l holds query row and
+// table row l % 16 (past the last: the last), columns 16 (l / 16) + (0..15)
+// of each 64-column chunk; step i of the chunk takes columns i, 16 + i,
+// 32 + i and 48 + i. Register r of lane l then holds query 4 (l / 16) + r,
+// table row l % 16.
+template <int HD>
+__global__ __launch_bounds__(256) void rel_dots16_k(const AttnArgs a) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = static_cast<int>(blockIdx.x) * 4 + wave;
+  if (j >= a.h + a.w) return;  // the whole wave (no barrier follows)
+  const int64_t slice = blockIdx.y;
+  const bool height = j < a.h;
+  const int nq = height ? a.w : a.h;
+  const int nr = height ? a.h : a.w;
+  const float* tab = height ? a.rh + static_cast<int64_t>(j) * a.h * HD : a.rw + static_cast<int64_t>(j - a.h) * a.w * HD;
+  auto query = [&](int i) { return height ? j * a.w + i : i * a.w + (j - a.h); };
+  const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
+  float* out = a.table_out + slice * a.rows * static_cast<int64_t>(a.dots_ld);
+  const int g = lane >> 4, l16 = lane & 15;
+  const float* qrow = qb + static_cast<int64_t>(query(min(l16, nq - 1))) * a.ldq + 16 * g;
+  const float* trow = tab + static_cast<int64_t>(min(l16, nr - 1)) * HD + 16 * g;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int k0 = 0; k0 < HD; k0 += 64) {
+    float qv[16], tv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(qrow + k0 + i);
+      const float4 y = *reinterpret_cast<const float4*>(trow + k0 + i);
+      qv[i] = x.x;
+      qv[i + 1] = x.y;
+      qv[i + 2] = x.z;
+      qv[i + 3] = x.w;
+      tv[i] = y.x;
+      tv[i + 1] = y.y;
+      tv[i + 2] = y.z;
+      tv[i + 3] = y.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i], tv[i], acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int q = 4 * g + r;
+    if (q < nq && l16 < nr) {
+      out[static_cast<int64_t>(query(q)) * a.dots_ld + (height ? l16 : a.dw_off + l16)] = acc[r] * a.table_mul;
+    }
+  }
+}
+
 // Dynamic LDS above 64 KB has to be allowed per kernel first.
 template <class Kernel>
 void allow_lds(Kernel kernel, size_t bytes) {
@@ -1107,15 +1160,25 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
   const bool x3 = x3_rows >= 0;
   if (x3) a.table_mul = kLog2e;
   if (table) {
-    // one wave per 32 x 32 tile of a block's product, up to 4 waves
-    const int64_t tiles = ((h + 31) / 32) * ((w + 31) / 32);
-    const unsigned threads = static_cast<unsigned>(64 * (tiles < 4 ? tiles : 4));
-    const dim3 grid(static_cast<unsigned>(h + w), static_cast<unsigned>(slices));
     clear_launch_error();
-    if (hd == 64) {
-      rel_dots_k<64><<<grid, threads, 0, as_stream(stream)>>>(a);
+    if (h <= 16 && w <= 16) {
+      // a 16 x 16 tile per table slice, four slices per workgroup
+      const dim3 grid(static_cast<unsigned>((h + w + 3) / 4), static_cast<unsigned>(slices));
+      if (hd == 64) {
+        rel_dots16_k<64><<<grid, 256, 0, as_stream(stream)>>>(a);
+      } else {
+        rel_dots16_k<128><<<grid, 256, 0, as_stream(stream)>>>(a);
+      }
     } else {
-      rel_dots_k<128><<<grid, threads, 0, as_stream(stream)>>>(a);
+      // one wave per 32 x 32 tile of a block's product, up to 4 waves
+      const int64_t tiles = ((h + 31) / 32) * ((w + 31) / 32);
+      const unsigned threads = static_cast<unsigned>(64 * (tiles < 4 ? tiles : 4));
+      const dim3 grid(static_cast<unsigned>(h + w), static_cast<unsigned>(slices));
+      if (hd == 64) {
+        rel_dots_k<64><<<grid, threads, 0, as_stream(stream)>>>(a);
+      } else {
+        rel_dots_k<128><<<grid, threads, 0, as_stream(stream)>>>(a);
+      }
     }
     if (const int st = check_launch(what)) return st;
   }
