@@ -105,6 +105,10 @@ struct AttnArgs {
   uint16_t* out16;
   // rel_dots_k's products are stored times this (1: the dots themselves)
   float table_mul = 1.0f;
+  // non-null: the split-operand kernel's key and value tiles, formed by the
+  // dot-table launch (kv_tiles_of), for key tiles of x3_rows grid rows
+  uint16_t* kvx = nullptr;
+  int x3_rows = -1;
 };
 
 // Four output values at element offset off: fp32, or bf16 into out16.
@@ -427,11 +431,11 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
 // (hi = bf16(x), lo = bf16(x - hi)), and a . b = lo_a hi_b + hi_a lo_b +
 // hi_a hi_b accumulated in fp32: about 2^-16 of each product is dropped,
 // three orders below the output's rounding. Head dim 64, the
-// relative-position bias from the dot table (a grid of whole 32-key tiles:
-// SAM's global layers), 4 waves of 32 query rows. The key and value tiles
-// are split once per workgroup as they reach LDS: K rows as hi and lo bf16
-// rows, V transposed (a dimension's 32 keys contiguous, so one 16-byte read
-// gives a lane its 8 keys) and its key order permuted so that the
+// relative-position bias from the dot table, 4 waves of 32 query rows. The
+// key and value tiles come split from the dot-table launch (x3_split_tiles):
+// K rows as hi and lo bf16 rows, V transposed (a dimension's 32 keys
+// contiguous, so one 16-byte read gives a lane its 8 keys) and its key
+// order permuted so that the
 // probabilities' registers feed the values' product without movement: the
 // scores' register r of lane half h holds key 8 (r / 4) + 4 h + r % 4, and
 // the product's k index 16 j + 8 h + t reads register 8 j + t, key
@@ -476,6 +480,9 @@ __device__ __forceinline__ void split8(const float (&x)[8], u32x4& hi, u32x4& lo
   lo = u32x4{l[0], l[1], l[2], l[3]};
 }
 
+// A tile's fp32 K and V rows (32 slots, 16-byte chunks spread over 256
+// threads) split into LDS: K rows as hi and lo bf16 rows, V^T rows in the
+// permuted slot order.
 __device__ __forceinline__ void store_tile_x3(uint16_t* khi, uint16_t* klo, uint16_t* vhi, uint16_t* vlo,
                                               const float4 (&kr)[Tile<64, 256>::kPerThread],
                                               const float4 (&vr)[Tile<64, 256>::kPerThread]) {
@@ -503,6 +510,65 @@ __device__ __forceinline__ void store_tile_x3(uint16_t* khi, uint16_t* klo, uint
   }
 }
 
+// ---- key and value tiles in bf16 parts, formed once per slice ---------------
+//
+// On a grid of whole tiles (SAM's global layers) the split-operand kernel
+// reads each key tile once per workgroup of query rows (32 of them per head
+// at 4096 rows); splitting its fp32 K and V rows there cost every workgroup
+// the same VALU work. The dot-table launch forms them once instead, per
+// tile 4 parts of 2048 bf16 (16 KB, the fp32 rows' size): K hi and lo
+// [32 slots][64], V^T hi and lo [64 dims][32 slots] in the permuted slot
+// order (x3_key_slot), unpadded; the attention copies them into its padded
+// LDS rows with 16-byte writes (measured: 333 to 290 us for 12 heads of
+// 4096 rows, table launch included). A window's tile is read by two or
+// three workgroups, where the extra pass cost more than it saved (51 to 58
+// us over 25 windows of 196): windows split their tiles in the attention.
+constexpr int kX3PartElems = kKeyTile * 64;       // one part of one tile
+constexpr int kX3TileFloats = 4 * kX3PartElems / 2;  // a tile's four parts, in floats
+
+// Key tiles of a slice, and the key of a tile's slot (a dead slot: the
+// nearest key, whose score the attention sets to -inf).
+__device__ __forceinline__ int x3_tiles(const AttnArgs& a) {
+  return a.x3_rows == 0 ? a.keys / kKeyTile : (a.h + a.x3_rows - 1) / a.x3_rows;
+}
+__device__ __forceinline__ int x3_key(const AttnArgs& a, int t, int slot) {
+  if (a.x3_rows == 0) return t * kKeyTile + slot;
+  const int per_row = kKeyTile / a.x3_rows;
+  return min(t * a.x3_rows + slot / per_row, a.h - 1) * a.w + min(slot % per_row, a.w - 1);
+}
+
+// Tiles first, first + stride, ... of `slice` into a.kvx; 16-byte chunks
+// spread over the block's threads.
+__device__ void x3_split_tiles(const AttnArgs& a, int64_t slice, int first, int stride) {
+  const float* kb = a.k + slice_at(a, slice, a.sk, a.ik);
+  const float* vb = a.v + slice_at(a, slice, a.sv, a.iv);
+  const int tiles = x3_tiles(a);
+  for (int t = first; t < tiles; t += stride) {
+    uint16_t* base = a.kvx + (slice * tiles + t) * static_cast<int64_t>(4 * kX3PartElems);
+    for (int c = static_cast<int>(threadIdx.x); c < kX3PartElems / 8; c += static_cast<int>(blockDim.x)) {
+      // K: slot c / 8, dims 8 (c % 8) .. + 7
+      const int slot = c / 8, d0 = 8 * (c % 8);
+      const float* kr = kb + static_cast<int64_t>(x3_key(a, t, slot)) * a.ldk + d0;
+      const float4 k0 = *reinterpret_cast<const float4*>(kr), k1 = *reinterpret_cast<const float4*>(kr + 4);
+      const float kx[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+      u32x4 hi, lo;
+      split8(kx, hi, lo);
+      *reinterpret_cast<u32x4*>(base + slot * 64 + d0) = hi;
+      *reinterpret_cast<u32x4*>(base + kX3PartElems + slot * 64 + d0) = lo;
+      // V^T: dim c / 4, slot positions 8 (c % 4) .. + 7
+      const int dim = c / 4, p0 = 8 * (c % 4);
+      float vx[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vx[e] = vb[static_cast<int64_t>(x3_key(a, t, x3_key_slot(p0 + e))) * a.ldv + dim];
+      }
+      split8(vx, hi, lo);
+      *reinterpret_cast<u32x4*>(base + 2 * kX3PartElems + dim * kKeyTile + p0) = hi;
+      *reinterpret_cast<u32x4*>(base + 3 * kX3PartElems + dim * kKeyTile + p0) = lo;
+    }
+  }
+}
+
 // kRows 0: a grid of whole tiles, each key tile 32 keys of one grid row
 // (the global layers); kRows 1, 2 or 4: each key tile kRows grid rows of at
 // most 32 / kRows keys (the windows: 14 x 14 takes 2 rows of 14 per tile),
@@ -513,12 +579,11 @@ __device__ __forceinline__ void store_tile_x3(uint16_t* khi, uint16_t* klo, uint
 // width terms (dead slots -inf) the same in every tile.
 template <int kRows>
 __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
-  constexpr int HD = 64, kThreads = 256, kQueriesPerBlock = 4 * kQueriesPerWave;
-  constexpr int kSlotsPerRow = kRows == 0 ? kKeyTile : kKeyTile / kRows;
+  constexpr int HD = 64, kQueriesPerBlock = 4 * kQueriesPerWave;
+  constexpr int kSlotsPerRow = kKeyTile / (kRows == 0 ? 1 : kRows);
   constexpr int kDh = kRows == 0 ? 1 : kRows;  // height terms per tile
-  using T = Tile<HD, kThreads>;
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-  // two stages: tile t + 1 is split into one while tile t is read from the other
+  // two stages: tile t + 1 is written into one while tile t is read from the other
   constexpr int kKElems = kKeyTile * kX3KStride, kVElems = HD * kX3VStride;
   __shared__ __attribute__((aligned(16))) uint16_t khi_s[2 * kKElems];
   __shared__ __attribute__((aligned(16))) uint16_t klo_s[2 * kKElems];
@@ -532,49 +597,65 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
   const int qrow = q0 + c;
   const bool qin = qrow < a.rows;
   const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
-  const float* kb = a.k + slice_at(a, slice, a.sk, a.ik);
-  const float* vb = a.v + slice_at(a, slice, a.sv, a.iv);
   auto mfma = [](u32x4 x, u32x4 y, f32x16 acc) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x), __builtin_bit_cast(bf16x8, y),
                                                    acc, 0, 0, 0);
   };
-  const int tiles = kRows == 0 ? a.keys / kKeyTile : (a.h + kRows - 1) / kRows;
+  const int tiles = x3_tiles(a);
 
-  // Tile loads, every address in range and no branch, so that a tile's use
-  // waits only for its own loads, not for the next tile's. kRows 0: the
-  // keys are whole tiles, this thread's row offsets formed once and a
-  // tile's offset added per load. Otherwise a slot's key is its tile row's
-  // grid row (the last grid row past the last) and its column (the last
-  // column for a dead slot; its score is -inf, its probability 0).
-  float4 kr[T::kPerThread], vr[T::kPerThread];
-  const float* kp[T::kPerThread];
-  const float* vp[T::kPerThread];
-  int srow[T::kPerThread], scol[T::kPerThread], sc4[T::kPerThread];
+  // kRows 0: this thread's 16-byte chunk of each of a tile's four parts
+  // (formed by the dot-table launch): K slot tid / 8, dims 8 (tid % 8) ..
+  // + 7; V^T dim tid / 4, slot positions 8 (tid % 4) .. + 7. Otherwise its
+  // two 16-byte chunks of the fp32 K and V rows, split as they reach LDS: a
+  // slot's key is its tile row's grid row (the last grid row past the last)
+  // and its column (the last column for a dead slot; its score is -inf, its
+  // probability 0). Every address in range and no branch, so that a tile's
+  // use waits only for its own loads.
+  const int tid = static_cast<int>(threadIdx.x);
+  const int kslot = tid / 8, kd0 = 8 * (tid % 8), vdim = tid / 4, vp0 = 8 * (tid % 4);
+  const uint16_t* kvs = a.kvx + slice * tiles * static_cast<int64_t>(4 * kX3PartElems);
+  const float* kb = a.k + slice_at(a, slice, a.sk, a.ik);
+  const float* vb = a.v + slice_at(a, slice, a.sv, a.iv);
+  u32x4 kv[4];
+  float4 kr[2], vr[2];
+  int srow[2], scol[2], sc4[2];
 #pragma unroll
-  for (int j = 0; j < T::kPerThread; ++j) {
-    const int idx = static_cast<int>(threadIdx.x) + kThreads * j;
+  for (int j = 0; j < 2; ++j) {
+    const int idx = tid + 256 * j;
     const int slot = idx / (HD / 4), c4 = idx % (HD / 4);
-    kp[j] = kb + slot * a.ldk + 4 * c4;
-    vp[j] = vb + slot * a.ldv + 4 * c4;
     srow[j] = slot / kSlotsPerRow;
     scol[j] = min(slot % kSlotsPerRow, a.w - 1);
     sc4[j] = 4 * c4;
   }
   auto load_kv = [&](int t) {
     if constexpr (kRows == 0) {
-      const int64_t ko = static_cast<int64_t>(t) * kKeyTile * a.ldk, vo = static_cast<int64_t>(t) * kKeyTile * a.ldv;
-#pragma unroll
-      for (int j = 0; j < T::kPerThread; ++j) {
-        kr[j] = *reinterpret_cast<const float4*>(kp[j] + ko);
-        vr[j] = *reinterpret_cast<const float4*>(vp[j] + vo);
-      }
+      const uint16_t* base = kvs + static_cast<int64_t>(t) * (4 * kX3PartElems);
+      kv[0] = *reinterpret_cast<const u32x4*>(base + kslot * 64 + kd0);
+      kv[1] = *reinterpret_cast<const u32x4*>(base + kX3PartElems + kslot * 64 + kd0);
+      kv[2] = *reinterpret_cast<const u32x4*>(base + 2 * kX3PartElems + vdim * kKeyTile + vp0);
+      kv[3] = *reinterpret_cast<const u32x4*>(base + 3 * kX3PartElems + vdim * kKeyTile + vp0);
     } else {
 #pragma unroll
-      for (int j = 0; j < T::kPerThread; ++j) {
+      for (int j = 0; j < 2; ++j) {
         const int key = min(t * kRows + srow[j], a.h - 1) * a.w + scol[j];
         kr[j] = *reinterpret_cast<const float4*>(kb + key * a.ldk + sc4[j]);
         vr[j] = *reinterpret_cast<const float4*>(vb + key * a.ldv + sc4[j]);
       }
+    }
+  };
+  // the tile into LDS stage `stage`, K rows and V^T rows padded
+  auto store_kv = [&](int stage) {
+    uint16_t* khi = khi_s + stage * kKElems;
+    uint16_t* klo = klo_s + stage * kKElems;
+    uint16_t* vhi = vhi_s + stage * kVElems;
+    uint16_t* vlo = vlo_s + stage * kVElems;
+    if constexpr (kRows == 0) {
+      *reinterpret_cast<u32x4*>(khi + kslot * kX3KStride + kd0) = kv[0];
+      *reinterpret_cast<u32x4*>(klo + kslot * kX3KStride + kd0) = kv[1];
+      *reinterpret_cast<u32x4*>(vhi + vdim * kX3VStride + vp0) = kv[2];
+      *reinterpret_cast<u32x4*>(vlo + vdim * kX3VStride + vp0) = kv[3];
+    } else {
+      store_tile_x3(khi, klo, vhi, vlo, kr, vr);
     }
   };
   load_kv(0);
@@ -596,7 +677,7 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
     split8(x, qh[b], ql[b]);
   }
 
-  store_tile_x3(khi_s, klo_s, vhi_s, vlo_s, kr, vr);
+  store_kv(0);
   load_kv(tiles > 1 ? 1 : 0);  // tile 1 (tile 0 again when there is no tile 1)
   __syncthreads();
 
@@ -654,17 +735,14 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
     }
   };
   // One key tile, read from LDS stage `stage`, its bias terms in `bias`.
-  // First tile t + 1 (in kr, vr since tile t - 1) is split into the other
+  // First tile t + 1 (in kv since tile t - 1) is written into the other
   // stage and tile t + 2 requested; the next tile's bias terms are requested
   // into `next` (two register sets used in turn: no copies). One barrier
   // per tile: after it, stage t + 1 is whole and no wave still reads stage
   // t, which tile t + 1 then refills with tile t + 2.
   auto tile = [&](int t, int stage, const Bias& bias, Bias& next) {
     const bool more = t + 1 < tiles;
-    if (more) {
-      store_tile_x3(khi_s + (1 - stage) * kKElems, klo_s + (1 - stage) * kKElems, vhi_s + (1 - stage) * kVElems,
-                    vlo_s + (1 - stage) * kVElems, kr, vr);
-    }
+    if (more) store_kv(1 - stage);
     load_kv(t + 2 < tiles ? t + 2 : t);  // the current tile again past the end
     load_bias(more ? t + 1 : t, next);
     const uint16_t* khi = khi_s + stage * kKElems;
@@ -960,6 +1038,7 @@ template <int HD>
 __global__ __launch_bounds__(256) void rel_dots_k(const AttnArgs a) {
   const int j = static_cast<int>(blockIdx.x);
   const int64_t slice = blockIdx.y;
+  if (HD == 64 && a.kvx != nullptr) x3_split_tiles(a, slice, j, static_cast<int>(gridDim.x));
   const bool height = j < a.h;
   const int nq = height ? a.w : a.h;  // the query rows that use this table slice
   const int nr = height ? a.h : a.w;  // its rows: dots per query
@@ -1022,9 +1101,9 @@ template <int HD>
 __global__ __launch_bounds__(256) void rel_dots16_k(const AttnArgs a) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t slice = blockIdx.y;
   const int j = static_cast<int>(blockIdx.x) * 4 + wave;
   if (j >= a.h + a.w) return;  // the whole wave (no barrier follows)
-  const int64_t slice = blockIdx.y;
   const bool height = j < a.h;
   const int nq = height ? a.w : a.h;
   const int nr = height ? a.h : a.w;
@@ -1123,6 +1202,23 @@ DotsLayout dots_layout(int64_t h, int64_t w) {
   return {tile_rows, tile_rows ? 4 * quads : h + w + 1, dw_off};
 }
 
+// Grid rows per key tile of the split-operand kernel: 0 for a grid of
+// whole 32-key tiles, 4, 2 or 1 for grids at most 8, 16 or 31 wide, -1
+// otherwise.
+int x3_rows_for(int64_t h, int64_t w) {
+  if (w % kKeyTile == 0) return 0;
+  return w <= 8 ? 4 : w <= 16 ? 2 : w < kKeyTile ? 1 : -1;
+}
+
+// Where the split key and value tiles start in the workspace (after the dot
+// table, at a 256-byte boundary), and their floats (grids of whole tiles).
+int64_t x3_tiles_offset(int64_t slices, int64_t h, int64_t w) {
+  return (slices * h * w * dots_layout(h, w).ld + 63) / 64 * 64;
+}
+int64_t x3_tiles_floats(int64_t slices, int64_t h, int64_t w, int rows) {
+  return rows == 0 ? slices * (h * w / kKeyTile) * kX3TileFloats : 0;  // grids of whole tiles only
+}
+
 // inner > 1: slice s = (s / inner, s % inner) with inner strides iq .. io.
 int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
                   int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo, int64_t so,
@@ -1139,6 +1235,14 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
   const DotsLayout lay = dots_layout(h, w);
   // the dot table goes to the workspace when it holds it (16-byte aligned)
   const bool table = workspace != nullptr && aligned16(workspace) && workspace_floats >= slices * n * lay.ld;
+  // a bf16 output from the dot table with head dim 64: the split-operand
+  // kernel, whose tiles are 32 keys of one grid row (whole tiles) or 4, 2
+  // or 1 grid rows of at most 8, 16 or 31 keys, when the workspace also
+  // holds the split key and value tiles
+  int x3_rows = table && out16 != nullptr && hd == 64 ? x3_rows_for(h, w) : -1;
+  if (x3_rows == 0 && workspace_floats < x3_tiles_offset(slices, h, w) + x3_tiles_floats(slices, h, w, 0)) {
+    x3_rows = -1;  // no room for the split tiles of a whole-tile grid: the fp32 products
+  }
   UOCR_REQUIRE(inner >= 1 && slices % inner == 0 && iq >= 0 && ik >= 0 && iv >= 0 && io >= 0 && iq % 4 == 0 &&
                    ik % 4 == 0 && iv % 4 == 0 && io % 4 == 0,
                what, "windows must divide the slices, window strides >= 0 in whole 16-byte chunks");
@@ -1147,18 +1251,12 @@ int rel_pos_entry(const char* what, void* stream, const float* q, int64_t ldq, i
              static_cast<int>(lay.dw_off), table ? workspace : nullptr, table ? workspace : nullptr,
              static_cast<int>(inner), iq, ik, iv, io, out16};
   if (out16 != nullptr) a.out = nullptr;
-  // a bf16 output from the dot table with head dim 64: the split-operand
-  // kernel, whose tiles are 32 keys of one grid row (whole tiles) or 4, 2
-  // or 1 grid rows of at most 8, 16 or 31 keys; it takes the bias in log2
-  // units
-  const int x3_rows = !(table && out16 != nullptr && hd == 64) ? -1
-                      : lay.tile_rows                          ? 0
-                      : w <= 8                                 ? 4
-                      : w <= 16                                ? 2
-                      : w < kKeyTile                           ? 1
-                                                               : -1;
   const bool x3 = x3_rows >= 0;
-  if (x3) a.table_mul = kLog2e;
+  if (x3) {
+    a.table_mul = kLog2e;  // the split-operand kernel takes the bias in log2 units
+    if (x3_rows == 0) a.kvx = reinterpret_cast<uint16_t*>(workspace + x3_tiles_offset(slices, h, w));
+    a.x3_rows = x3_rows;
+  }
   if (table) {
     clear_launch_error();
     if (h <= 16 && w <= 16) {
@@ -1259,7 +1357,9 @@ int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64
 
 int64_t uocr_rocm_attention_rel_pos_workspace_floats(int64_t slices, int64_t h, int64_t w) {
   if (slices < 1 || h < 1 || w < 1 || h + w > kMaxRelSpan) return 0;
-  return slices * h * w * dots_layout(h, w).ld;
+  const int rows = x3_rows_for(h, w);
+  if (rows != 0) return slices * h * w * dots_layout(h, w).ld;
+  return x3_tiles_offset(slices, h, w) + x3_tiles_floats(slices, h, w, 0);
 }
 
 int uocr_rocm_attention_rel_pos_ws(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
