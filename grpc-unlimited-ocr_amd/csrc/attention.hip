@@ -381,8 +381,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
       m = m_new;
       // the accumulators are rescaled only when some row's max moved (a
       // factor of exactly 1 elsewhere): most tiles skip the 16 hd / 32
-      // multiplies and the moves of the accumulators out of and back into
-      // the matrix registers
+      // multiplies
       if (__ballot(corr != 1.0f) != 0) {
 #pragma unroll
         for (int b = 0; b < kDBlocks; ++b) {
