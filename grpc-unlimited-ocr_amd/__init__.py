@@ -170,6 +170,9 @@ _SIGNATURES = {
                                                 _vp, _vp, _i64], _int),
     "uocr_rocm_attention_bf16": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                   _i64, _i64, _i64, _f32, _vp, _i64], _int),
+    "uocr_rocm_attention_masked_workspace_floats": ([_i64, _i64, _i64, _i64], _i64),
+    "uocr_rocm_attention_masked_bf16_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
+                                            _i64, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_attention_rel_pos_windows_bf16_ws": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64,
                                                      _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                                      _f32, _vp, _vp, _vp, _i64], _int),
@@ -676,6 +679,28 @@ def attention(q, k, v, out, slices, rows, keys, hd, scale, mask=None, strides=No
     name = "uocr_rocm_attention_bf16" if out.dtype == _torch().bfloat16 else "uocr_rocm_attention"
     _op(name, stream, *qo, *ko, *vo, *oo, slices, rows, keys, hd, scale, _f32_param(mask),
         0 if mask is None else mask.shape[-1])
+
+
+def attention_masked(q, k, v, out, slices, rows, keys, hd, scale, mask, workspace, strides=None, stream=None):
+    """attention with a mask into a bfloat16 out on the bf16 matrix cores,
+    each fp32 operand split into bf16 hi + lo parts (new); workspace holds
+    attention_masked_workspace_floats(slices, rows, keys, hd) floats (the
+    mask's live tiles and the split key and value tiles). Strides as for
+    attention."""
+    if out.dtype != _torch().bfloat16:
+        raise ValueError("attention_masked writes a bfloat16 out")
+    st = strides or {}
+    qo = _operand(q, *st.get("q", (0, hd, rows * hd)))
+    ko = _operand(k, *st.get("k", (0, hd, keys * hd)))
+    vo = _operand(v, *st.get("v", (0, hd, keys * hd)))
+    oo = _operand(out, *st.get("out", (0, hd, rows * hd)))
+    _op("uocr_rocm_attention_masked_bf16_ws", stream, *qo, *ko, *vo, *oo, slices, rows, keys, hd, scale, _ptr(mask),
+        mask.shape[-1], _ptr(workspace), workspace.numel())
+
+
+def attention_masked_workspace_floats(slices, rows, keys, hd):
+    """Floats of attention_masked's workspace."""
+    return int(lib().uocr_rocm_attention_masked_workspace_floats(slices, rows, keys, hd))
 
 
 def attention_rel_pos(q, k, v, out, slices, h, w, hd, scale, rh, rw, strides=None, workspace=None, stream=None):

@@ -849,6 +849,349 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
   }
 }
 
+// ---- a mask on split operands --------------------------------------------------
+//
+// The decoder prefill's attention (a mask [rows, keys] shared by the heads,
+// -inf where a key is not attended: past the query's position, and off the
+// router's selected blocks and window) into bf16 on the bf16 matrix cores
+// with split operands, as attention_x3_k does for SAM, for head dim 64 or
+// 128. A first launch (mask_tiles_k) sets a bit per (128 query rows, 32-key
+// tile) where some entry of that mask block is finite; a workgroup then walks
+// only its live tiles, staging each (the fp32 K and V rows split into hi and
+// lo parts as they reach LDS, V transposed and permuted as in
+// attention_x3_k) and reading its rows' 32 x 32 mask block one tile ahead;
+// a wave whose block is all -inf skips the tile's products. Workgroups go
+// out last row block first (under a causal mask the longest walks first).
+constexpr int kMaskRowBlock = 4 * kQueriesPerWave;  // query rows per workgroup
+constexpr int kMaskMapKeys = 32 * kKeyTile;         // keys per map word (a bit per tile)
+
+// Four mask entries from key4 (a multiple of 4) of a row: one 16-byte read
+// where rows are whole 16-byte chunks apart (mask_ld % 4 == 0 and the mask
+// 16-byte aligned; mask_ld >= keys, so a read that starts below keys stays
+// in its row), else element by element; -inf from key `keys` on.
+__device__ __forceinline__ float4 mask4(const float* row, int key4, int keys, bool vec) {
+  float4 m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  if (vec) {
+    m = *reinterpret_cast<const float4*>(row + key4);
+  } else {
+    m.x = row[key4];
+    if (key4 + 1 < keys) m.y = row[key4 + 1];
+    if (key4 + 2 < keys) m.z = row[key4 + 2];
+    if (key4 + 3 < keys) m.w = row[key4 + 3];
+  }
+  if (key4 + 1 >= keys) m.y = -INFINITY;
+  if (key4 + 2 >= keys) m.z = -INFINITY;
+  if (key4 + 3 >= keys) m.w = -INFINITY;
+  return m;
+}
+
+__device__ __forceinline__ bool mask_vec(const float* mask, int64_t mask_ld) {
+  return (mask_ld & 3) == 0 && (reinterpret_cast<uintptr_t>(mask) & 15) == 0;
+}
+
+// Map word (row block blockIdx.y, word blockIdx.x): bit j set where some
+// entry of rows [128 rb, 128 rb + 128) x keys of tile 32 wd + j is not -inf
+// (NaN counts as live). Thread: keys 4 tid .. 4 tid + 3 of the word's 1024,
+// over every row of the block.
+__global__ __launch_bounds__(256) void mask_tiles_k(const float* __restrict__ mask, int64_t mask_ld, int rows,
+                                                    int keys, uint32_t* __restrict__ map, int words) {
+  __shared__ uint32_t part[4];
+  const int rb = blockIdx.y, wd = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int key4 = kMaskMapKeys * wd + 4 * static_cast<int>(threadIdx.x);
+  const bool vec = mask_vec(mask, mask_ld);
+  bool any = false;
+  if (key4 < keys) {
+    const int r0 = rb * kMaskRowBlock, r1 = min(r0 + kMaskRowBlock, rows);
+#pragma unroll 8
+    for (int r = r0; r < r1; ++r) {
+      const float4 m = mask4(mask + r * mask_ld, key4, keys, vec);
+      any = any || m.x != -INFINITY || m.y != -INFINITY || m.z != -INFINITY || m.w != -INFINITY;
+    }
+  }
+  // lanes 8 j .. 8 j + 7 of wave w: tile 8 w + j of the word
+  const uint64_t b = __ballot(any);
+  uint32_t bits = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) bits |= ((b >> (8 * j)) & 0xffu) != 0 ? (1u << j) : 0u;
+  if (lane == 0) part[wave] = bits << (8 * wave);
+  __syncthreads();
+  if (threadIdx.x == 0) map[static_cast<int64_t>(rb) * words + wd] = part[0] | part[1] | part[2] | part[3];
+}
+
+// Key tile t of slice s (blockIdx (t, s)) split once for every workgroup
+// that reads it, 4 parts of 32 x HD bf16 (8 HD bytes per key): K hi and lo
+// [32 slots][HD], V^T hi and lo [HD][32 slots] in the permuted slot order
+// (x3_key_slot); a slot past the last key holds the last key (its mask
+// entry is -inf). 16-byte chunks spread over the block's threads.
+template <int HD>
+__global__ __launch_bounds__(256) void x3m_split_k(const AttnArgs a, int tiles) {
+  constexpr int kPart = kKeyTile * HD;
+  const int t = blockIdx.x;
+  const int64_t slice = blockIdx.y;
+  const float* kb = a.k + slice_at(a, slice, a.sk, a.ik);
+  const float* vb = a.v + slice_at(a, slice, a.sv, a.iv);
+  uint16_t* base = a.kvx + (slice * tiles + t) * static_cast<int64_t>(4 * kPart);
+  for (int c = static_cast<int>(threadIdx.x); c < kPart / 8; c += 256) {
+    // K: slot c / (HD / 8), dims 8 (c % (HD / 8)) .. + 7
+    const int slot = c / (HD / 8), d0 = 8 * (c % (HD / 8));
+    const float* kr = kb + static_cast<int64_t>(min(t * kKeyTile + slot, a.keys - 1)) * a.ldk + d0;
+    const float4 k0 = *reinterpret_cast<const float4*>(kr), k1 = *reinterpret_cast<const float4*>(kr + 4);
+    const float kx[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    u32x4 hi, lo;
+    split8(kx, hi, lo);
+    *reinterpret_cast<u32x4*>(base + slot * HD + d0) = hi;
+    *reinterpret_cast<u32x4*>(base + kPart + slot * HD + d0) = lo;
+    // V^T: dim c / 4, slot positions 8 (c % 4) .. + 7
+    const int dim = c / 4, p0 = 8 * (c % 4);
+    float vx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = min(t * kKeyTile + x3_key_slot(p0 + e), a.keys - 1);
+      vx[e] = vb[static_cast<int64_t>(key) * a.ldv + dim];
+    }
+    split8(vx, hi, lo);
+    *reinterpret_cast<u32x4*>(base + 2 * kPart + dim * kKeyTile + p0) = hi;
+    *reinterpret_cast<u32x4*>(base + 3 * kPart + dim * kKeyTile + p0) = lo;
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const uint32_t* __restrict__ map, int words,
+                                                       int row_blocks, int slices) {
+  constexpr int kNB = HD / 16;           // 16-column blocks of a query or key row
+  constexpr int kDB = HD / 32;           // 32-dimension blocks of the output
+  constexpr int kKS = HD + 8;            // K rows in bf16: an odd number of 16-byte groups apart
+  constexpr int kVS = kX3VStride;        // V^T rows
+  constexpr int kKElems = kKeyTile * kKS, kVElems = HD * kVS;
+  constexpr int kPer = kKeyTile * HD / 8 / 256;  // 16-byte chunks of one split part per thread: 1 or 2
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  __shared__ __attribute__((aligned(16))) uint16_t khi_s[2 * kKElems];
+  __shared__ __attribute__((aligned(16))) uint16_t klo_s[2 * kKElems];
+  __shared__ __attribute__((aligned(16))) uint16_t vhi_s[2 * kVElems];
+  __shared__ __attribute__((aligned(16))) uint16_t vlo_s[2 * kVElems];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, c = lane & 31;
+  const int tid = static_cast<int>(threadIdx.x);
+  // workgroup: every slice's last row block first, then the one before
+  const int rb = row_blocks - 1 - static_cast<int>(blockIdx.x) / slices;
+  const int64_t slice = static_cast<int>(blockIdx.x) % slices;
+  const int q0 = rb * kMaskRowBlock + wave * kQueriesPerWave;
+  const int qrow = q0 + c;
+  const bool qin = qrow < a.rows;
+  const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
+  const int64_t orow = slice_at(a, slice, a.so, a.io) + static_cast<int64_t>(qrow) * a.ldo;
+  auto mfma = [](u32x4 x, u32x4 y, f32x16 acc) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x), __builtin_bit_cast(bf16x8, y),
+                                                   acc, 0, 0, 0);
+  };
+
+  // the live tiles of this row block, in order (uniform: scalar reads)
+  const uint32_t* tmap = map + static_cast<int64_t>(rb) * words;
+  const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
+  auto next_live = [&](int t) {  // the first live tile after t, or tiles
+    int u = t + 1;
+    while (u < tiles) {
+      const uint32_t w = tmap[u >> 5] >> (u & 31);
+      if (w != 0) return u + __builtin_ctz(w);
+      u = (u | 31) + 1;
+    }
+    return tiles;
+  };
+  int t = next_live(-1);
+  if (t >= tiles) {  // no key attended by any row of the block: zeros
+    if (qin) {
+#pragma unroll
+      for (int d = 4 * hl; d < HD; d += 8) store4(a, orow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    return;
+  }
+
+  // this thread's 16-byte chunks of each of a tile's four split parts
+  // (formed by x3m_split_k), copied into the padded LDS rows
+  constexpr int kPart = kKeyTile * HD;
+  const uint16_t* kvs = a.kvx + slice * tiles * static_cast<int64_t>(4 * kPart);
+  u32x4 kv[4][kPer];
+  auto load_kv = [&](int tt) {
+    const uint16_t* base = kvs + static_cast<int64_t>(tt) * (4 * kPart);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int c = tid + 256 * j;
+#pragma unroll
+      for (int part = 0; part < 4; ++part) {
+        kv[part][j] = *reinterpret_cast<const u32x4*>(base + part * kPart + 8 * c);
+      }
+    }
+  };
+  // into LDS stage `stage`: K rows [32][HD] and V^T rows [HD][32], padded
+  auto store_kv = [&](int stage) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int c = tid + 256 * j;
+      const int slot = c / (HD / 8), d0 = 8 * (c % (HD / 8)), dim = c / 4, p0 = 8 * (c % 4);
+      *reinterpret_cast<u32x4*>(khi_s + stage * kKElems + slot * kKS + d0) = kv[0][j];
+      *reinterpret_cast<u32x4*>(klo_s + stage * kKElems + slot * kKS + d0) = kv[1][j];
+      *reinterpret_cast<u32x4*>(vhi_s + stage * kVElems + dim * kVS + p0) = kv[2][j];
+      *reinterpret_cast<u32x4*>(vlo_s + stage * kVElems + dim * kVS + p0) = kv[3][j];
+    }
+  };
+  // this lane's 16 mask entries of a tile (register r: key 8 (r / 4) + 4 h +
+  // r % 4 of the tile), -inf past the keys or the rows
+  struct Block {
+    float m[16];
+  };
+  const bool vec = mask_vec(a.mask, a.mask_ld);
+  const float* mrow = a.mask + static_cast<int64_t>(qin ? qrow : 0) * a.mask_ld;
+  auto load_mask = [&](int tt, Block& blk) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int key4 = tt * kKeyTile + 8 * g + 4 * hl;
+      float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      if (qin && key4 < a.keys) v = mask4(mrow, key4, a.keys, vec);
+      blk.m[4 * g] = v.x;
+      blk.m[4 * g + 1] = v.y;
+      blk.m[4 * g + 2] = v.z;
+      blk.m[4 * g + 3] = v.w;
+    }
+  };
+
+  load_kv(t);
+  // the lane's query columns 16 b + 8 h + (0..7) times scale log2(e), split
+  const float qmul = a.scale * kLog2e;
+  u32x4 qh[kNB], ql[kNB];
+#pragma unroll
+  for (int b = 0; b < kNB; ++b) {
+    float4 t0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), t1 = t0;
+    if (qin) {
+      const float* qr = qb + static_cast<int64_t>(qrow) * a.ldq + 16 * b + 8 * hl;
+      t0 = *reinterpret_cast<const float4*>(qr);
+      t1 = *reinterpret_cast<const float4*>(qr + 4);
+    }
+    const float x[8] = {t0.x * qmul, t0.y * qmul, t0.z * qmul, t0.w * qmul,
+                        t1.x * qmul, t1.y * qmul, t1.z * qmul, t1.w * qmul};
+    split8(x, qh[b], ql[b]);
+  }
+  Block blk_a, blk_b;
+  load_mask(t, blk_a);
+  store_kv(0);
+  int n1 = next_live(t);
+  load_kv(n1 < tiles ? n1 : t);
+  __syncthreads();
+
+  f32x16 o[kDB];
+#pragma unroll
+  for (int b = 0; b < kDB; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] = 0.0f;
+  }
+  // m: the row's reference point in log2 units, as in attention_x3_k (-inf
+  // until a finite score is seen); lh: this lane half's total
+  float m = -INFINITY, lh = 0.0f;
+  const bool rows_live = q0 < a.rows;
+  // Live tile t from LDS stage `stage`, its mask block in `cur`; the next
+  // live tile n1 (in kr, vr) goes to the other stage, the one after (n2) is
+  // requested, and n1's mask block into `next`. One barrier per tile.
+  auto tile = [&](int tt, int nx1, int nx2, int stage, const Block& cur, Block& next) {
+    if (nx1 < tiles) store_kv(1 - stage);
+    load_kv(nx2 < tiles ? nx2 : tt);  // in range; not stored past the last tile
+    load_mask(nx1 < tiles ? nx1 : tt, next);
+    bool any = false;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) any = any || cur.m[r] != -INFINITY;
+    if (rows_live && __ballot(any) != 0) {
+      const uint16_t* khi = khi_s + stage * kKElems;
+      const uint16_t* klo = klo_s + stage * kKElems;
+      const uint16_t* vhi = vhi_s + stage * kVElems;
+      const uint16_t* vlo = vlo_s + stage * kVElems;
+      // S^T = K Q^T + the mask in log2 units (32 keys x 32 queries): the
+      // products accumulate onto the mask block, the small ones first
+      f32x16 s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = cur.m[r] * kLog2e;
+#pragma unroll
+      for (int b = 0; b < kNB; ++b) {
+        const int at = c * kKS + 16 * b + 8 * hl;
+        const u32x4 kh = *reinterpret_cast<const u32x4*>(khi + at);
+        const u32x4 kl = *reinterpret_cast<const u32x4*>(klo + at);
+        s = mfma(kl, qh[b], s);
+        s = mfma(kh, ql[b], s);
+        s = mfma(kh, qh[b], s);
+      }
+      // the tile's row maximum
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
+      tmax = max_halves(tmax);
+      const bool grow = tmax > m + kX3Slack;
+      if (__ballot(grow) != 0) {
+        const float m_new = grow ? tmax : m;
+        const float corr = grow ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+        lh *= corr;
+#pragma unroll
+        for (int b = 0; b < kDB; ++b) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[b][r] *= corr;
+        }
+        m = m_new;
+      }
+      // a row with no finite score yet: its probabilities are 0
+      const float ref = m == -INFINITY ? INFINITY : m;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = __builtin_amdgcn_exp2f(s[r] - ref);
+        lh += s[r];
+      }
+      u32x4 ph[2], pl[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float x[8] = {s[8 * j],     s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
+                            s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]};
+        split8(x, ph[j], pl[j]);
+      }
+      // O^T += V^T P^T over the permuted key slots
+#pragma unroll
+      for (int b = 0; b < kDB; ++b) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int at = (32 * b + c) * kVS + 16 * j + 8 * hl;
+          const u32x4 vh = *reinterpret_cast<const u32x4*>(vhi + at);
+          const u32x4 vl = *reinterpret_cast<const u32x4*>(vlo + at);
+          o[b] = mfma(vl, ph[j], o[b]);
+          o[b] = mfma(vh, pl[j], o[b]);
+          o[b] = mfma(vh, ph[j], o[b]);
+        }
+      }
+    }
+    __syncthreads();
+  };
+  // two mask blocks used in turn (no copies): tiles alternate stages 0, 1
+  while (true) {
+    int n2 = n1 < tiles ? next_live(n1) : tiles;
+    tile(t, n1, n2, 0, blk_a, blk_b);
+    t = n1;
+    if (t >= tiles) break;
+    n1 = n2;
+    n2 = n1 < tiles ? next_live(n1) : tiles;
+    tile(t, n1, n2, 1, blk_b, blk_a);
+    t = n1;
+    if (t >= tiles) break;
+    n1 = n2;
+  }
+
+  const float l = sum_halves(lh);
+  if (!qin) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+  for (int b = 0; b < kDB; ++b) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * b + 8 * g + 4 * hl;
+      store4(a, orow + d, o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv);
+    }
+  }
+}
+
 // ---- few query rows: the keys split over the waves ---------------------------
 //
 // With few query rows (CLIP: 16 heads x 257 rows are 48 workgroups of 128
@@ -1323,6 +1666,62 @@ int attention_entry(const char* what, void* stream, const float* q, int64_t ldq,
                          : launch<Bias::kNone>(what, stream, hd, slices, a);
 }
 
+// The masked split-operand attention's workspace: the mask's tile map
+// (words per row block), then at a 256-byte boundary the split key and
+// value tiles (64 hd floats per tile of 32 keys).
+int64_t mask_map_words(int64_t keys) { return (keys + kMaskMapKeys - 1) / kMaskMapKeys; }
+int64_t mask_map_floats(int64_t rows, int64_t keys) {
+  return (rows + kMaskRowBlock - 1) / kMaskRowBlock * mask_map_words(keys);
+}
+int64_t masked_tiles_offset(int64_t rows, int64_t keys) { return (mask_map_floats(rows, keys) + 63) / 64 * 64; }
+int64_t masked_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
+  return masked_tiles_offset(rows, keys) + slices * ((keys + kKeyTile - 1) / kKeyTile) * 64 * hd;
+}
+
+int masked_split_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                       int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv, uint16_t* out, int64_t ldo,
+                       int64_t so, int64_t slices, int64_t rows, int64_t keys, int64_t hd, float scale,
+                       const float* mask, int64_t mask_ld, float* workspace, int64_t workspace_floats) {
+  if (const int st = check_common(what, q, ldq, sq, k, ldk, sk, v, ldv, sv, reinterpret_cast<const float*>(out), ldo,
+                                  so, slices, rows, keys, hd)) {
+    return st;
+  }
+  UOCR_REQUIRE(mask != nullptr && mask_ld >= keys, what, "mask [rows, mask_ld] with mask_ld >= keys");
+  const int64_t row_blocks = (rows + kMaskRowBlock - 1) / kMaskRowBlock, words = mask_map_words(keys);
+  UOCR_REQUIRE(row_blocks < 65536 && row_blocks * slices < (int64_t{1} << 31), what,
+               "need rows < 2^23 and row blocks x slices < 2^31");
+  UOCR_REQUIRE(workspace != nullptr && aligned16(workspace) &&
+                   workspace_floats >= masked_workspace_floats(slices, rows, keys, hd),
+               what, "workspace: 16-byte aligned, uocr_rocm_attention_masked_workspace_floats floats");
+  AttnArgs a{q, k, v, nullptr, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
+             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 1, 0, 0, 0, 0, out};
+  a.kvx = reinterpret_cast<uint16_t*>(workspace + masked_tiles_offset(rows, keys));
+  uint32_t* map = reinterpret_cast<uint32_t*>(workspace);
+  const int64_t tiles = (keys + kKeyTile - 1) / kKeyTile;
+  clear_launch_error();
+  mask_tiles_k<<<dim3(static_cast<unsigned>(words), static_cast<unsigned>(row_blocks)), 256, 0, as_stream(stream)>>>(
+      mask, mask_ld, static_cast<int>(rows), static_cast<int>(keys), map, static_cast<int>(words));
+  if (const int st = check_launch(what)) return st;
+  const dim3 split_grid(static_cast<unsigned>(tiles), static_cast<unsigned>(slices));
+  clear_launch_error();
+  if (hd == 64) {
+    x3m_split_k<64><<<split_grid, 256, 0, as_stream(stream)>>>(a, static_cast<int>(tiles));
+  } else {
+    x3m_split_k<128><<<split_grid, 256, 0, as_stream(stream)>>>(a, static_cast<int>(tiles));
+  }
+  if (const int st = check_launch(what)) return st;
+  const unsigned grid = static_cast<unsigned>(row_blocks * slices);
+  clear_launch_error();
+  if (hd == 64) {
+    attention_x3m_k<64><<<grid, 256, 0, as_stream(stream)>>>(a, map, static_cast<int>(words),
+                                                             static_cast<int>(row_blocks), static_cast<int>(slices));
+  } else {
+    attention_x3m_k<128><<<grid, 256, 0, as_stream(stream)>>>(a, map, static_cast<int>(words),
+                                                              static_cast<int>(row_blocks), static_cast<int>(slices));
+  }
+  return check_launch(what);
+}
+
 }  // namespace
 }  // namespace uocr_rocm
 
@@ -1344,6 +1743,20 @@ int uocr_rocm_attention_bf16(void* stream, const float* q, int64_t ldq, int64_t 
                              const float* mask, int64_t mask_ld) {
   return attention_entry("uocr_rocm_attention_bf16", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv,
                          reinterpret_cast<float*>(out), ldo, so, slices, rows, keys, hd, scale, mask, mask_ld, out);
+}
+
+int64_t uocr_rocm_attention_masked_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
+  if (slices < 1 || rows < 1 || keys < 1 || (hd != 64 && hd != 128)) return 0;
+  return masked_workspace_floats(slices, rows, keys, hd);
+}
+
+int uocr_rocm_attention_masked_bf16_ws(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                                       int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv,
+                                       uint16_t* out, int64_t ldo, int64_t so, int64_t slices, int64_t rows,
+                                       int64_t keys, int64_t hd, float scale, const float* mask, int64_t mask_ld,
+                                       float* workspace, int64_t workspace_floats) {
+  return masked_split_entry("uocr_rocm_attention_masked_bf16_ws", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo,
+                            so, slices, rows, keys, hd, scale, mask, mask_ld, workspace, workspace_floats);
 }
 
 int uocr_rocm_attention_rel_pos(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,

@@ -186,6 +186,15 @@ void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOpe
 void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, std::uint16_t* out, std::int64_t ldo,
                std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
                const float* mask, std::int64_t mask_ld);
+// New: attention with a mask into bf16 on the bf16 matrix cores with split
+// operands, walking only the key tiles the mask leaves live; the workspace
+// holds attention_masked_workspace_floats(slices, rows, keys, hd) floats.
+std::int64_t attention_masked_workspace_floats(std::int64_t slices, std::int64_t rows, std::int64_t keys,
+                                               std::int64_t hd);
+void attention_masked(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, std::uint16_t* out,
+                      std::int64_t ldo, std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys,
+                      std::int64_t hd, float scale, const float* mask, std::int64_t mask_ld, float* workspace,
+                      std::int64_t workspace_floats);
 void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t wq, AttnOperand k, std::int64_t wk,
                                AttnOperand v, std::int64_t wv, std::uint16_t* out, std::int64_t ldo, std::int64_t so,
                                std::int64_t wo, std::int64_t heads, std::int64_t windows, std::int64_t h,

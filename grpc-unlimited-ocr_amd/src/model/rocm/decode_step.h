@@ -70,6 +70,11 @@ struct DecoderDims {
   std::int64_t page_mod = 2;    // page coordinate taken mod this (0: as given)
   RouteParams router;           // block size, local window, top m / top k, entmax scale and prior
   bool bf16_cache = false;      // key/value cache in bf16 (half the bytes) instead of the reference's fp32
+  // The prompt's attention on the bf16 matrix cores with each fp32 operand
+  // split into bf16 hi + lo parts (attention_masked: 4-5x faster over long
+  // prompts, each attention output within one bf16 step of the fp32
+  // products' rounding) instead of the fp32 products the reference keeps.
+  bool split_attention = false;
   bool trace = false;           // keep each layer's intermediate values of the last step (for checking)
 };
 

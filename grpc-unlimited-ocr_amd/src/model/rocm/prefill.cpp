@@ -79,7 +79,13 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
   x.upload(x_host.data(), rows * H);
   Array h = f32(rows * H), delta = f32(rows * H), q = f32(rows * W), rq = f32(rows * D), z = f32(rows * nblk);
   const bool one_pass = hd == 64 || hd == 128;
-  Array mask = f32(rows * keys), scores = f32(one_pass ? 1 : d.heads * rows * keys), merged = f32(rows * W);
+  const bool split = one_pass && d.split_attention;
+  Array mask = f32(rows * keys), scores = f32(one_pass ? 1 : d.heads * rows * keys);
+  Array merged = f32(split ? 1 : rows * W);
+  // the split-operand attention's bf16 output rows (the o projection's input) and workspace
+  Array attn_b(ctx_, DType::kBF16, split ? rows * W : 1);
+  const std::int64_t attn_ws_floats = split ? attention_masked_workspace_floats(d.heads, rows, keys, hd) : 1;
+  Array attn_ws = f32(attn_ws_floats);
   // Over a bf16 cache: the new keys and values in fp32 before they are
   // rounded into the cache, and every key and value the prompt attends to
   // widened back from the cache (positions 0 .. keys - 1 gathered in order).
@@ -149,18 +155,25 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
       prefill_masks_.push_back(mask.download());
       prefill_masks_.back().resize(static_cast<std::size_t>(rows * keys));
     }
-    if (one_pass) {
-      // scores, mask, softmax and values in one pass on the matrix cores,
-      // each head's columns read in place
-      attention(ctx_, {q.f32(), W, hd}, {k_all, W, hd}, {v_all, W, hd}, merged.f32(), W, hd, d.heads, rows, keys, hd,
-                scale, mask.f32(), keys);
+    if (split) {
+      // scores, mask, softmax and values in one pass on the bf16 matrix
+      // cores with split operands, each head's columns read in place, the
+      // output in bf16 (the rounding the o projection applies to its input)
+      attention_masked(ctx_, {q.f32(), W, hd}, {k_all, W, hd}, {v_all, W, hd}, attn_b.bf16(), W, hd, d.heads, rows,
+                       keys, hd, scale, mask.f32(), keys, attn_ws.f32(), attn_ws_floats);
+      linear_bf16x(ctx_, attn_b.bf16(), rows, W, l.o, H, nullptr, delta.f32());
     } else {
-      gemm_nt(ctx_, rows, keys, hd, scale, q.f32(), W, hd, k_all, W, hd, scores.f32(), keys, rows * keys, d.heads);
-      scale_add_mask(ctx_, scores.f32(), 1.0f, mask.f32(), d.heads, rows, keys);
-      softmax_rows(ctx_, scores.f32(), d.heads * rows, keys);
-      gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_all, W, hd, merged.f32(), W, hd, d.heads);
-    }
-    {
+      if (one_pass) {
+        // scores, mask, softmax and values in one pass on the fp32 matrix
+        // cores, each head's columns read in place
+        attention(ctx_, {q.f32(), W, hd}, {k_all, W, hd}, {v_all, W, hd}, merged.f32(), W, hd, d.heads, rows, keys,
+                  hd, scale, mask.f32(), keys);
+      } else {
+        gemm_nt(ctx_, rows, keys, hd, scale, q.f32(), W, hd, k_all, W, hd, scores.f32(), keys, rows * keys, d.heads);
+        scale_add_mask(ctx_, scores.f32(), 1.0f, mask.f32(), d.heads, rows, keys);
+        softmax_rows(ctx_, scores.f32(), d.heads * rows, keys);
+        gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_all, W, hd, merged.f32(), W, hd, d.heads);
+      }
       const Array mb = rounded(ctx_, merged.f32(), rows * W);
       linear_bf16x(ctx_, mb.bf16(), rows, W, l.o, H, nullptr, delta.f32());
     }

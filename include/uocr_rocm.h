@@ -517,6 +517,26 @@ UOCR_ROCM_API int uocr_rocm_attention_bf16(void* stream, const float* q, int64_t
                                            uint16_t* out, int64_t ldo, int64_t so, int64_t slices, int64_t rows,
                                            int64_t keys, int64_t hd, float scale, const float* mask,
                                            int64_t mask_ld);
+/* New: uocr_rocm_attention_bf16 with a mask, on the bf16 matrix cores with
+ * each fp32 operand split into bf16 hi + lo parts (a . b = lo_a hi_b +
+ * hi_a lo_b + hi_a hi_b in fp32: about 2^-16 of each product dropped, far
+ * below the output's bf16 rounding, so not bitwise the fp32 entry's
+ * rounding). Two launches first fill the workspace
+ * (uocr_rocm_attention_masked_workspace_floats(slices, rows, keys, hd)
+ * floats, 16-byte aligned): a bit per (128 query rows, 32-key tile) where
+ * some mask entry is finite, and every key tile split once; the attention
+ * stages and multiplies only the live tiles. mask non-null, mask_ld >=
+ * keys. The decoder prefill's
+ * attention of CudaDecoder::attention (src/model/cuda/cuda_decoder.cpp:
+ * 88-105) followed by the bf16 rounding its output projection applies. */
+UOCR_ROCM_API int64_t uocr_rocm_attention_masked_workspace_floats(int64_t slices, int64_t rows, int64_t keys,
+                                                                 int64_t hd);
+UOCR_ROCM_API int uocr_rocm_attention_masked_bf16_ws(void* stream, const float* q, int64_t ldq, int64_t sq,
+                                                     const float* k, int64_t ldk, int64_t sk, const float* v,
+                                                     int64_t ldv, int64_t sv, uint16_t* out, int64_t ldo, int64_t so,
+                                                     int64_t slices, int64_t rows, int64_t keys, int64_t hd,
+                                                     float scale, const float* mask, int64_t mask_ld,
+                                                     float* workspace, int64_t workspace_floats);
 UOCR_ROCM_API int uocr_rocm_attention_rel_pos_windows_bf16_ws(
     void* stream, const float* q, int64_t ldq, int64_t sq, int64_t wq, const float* k, int64_t ldk, int64_t sk,
     int64_t wk, const float* v, int64_t ldv, int64_t sv, int64_t wv, uint16_t* out, int64_t ldo, int64_t so,

@@ -961,7 +961,7 @@ OracleDecoder make_oracle_decoder(const ro::DecoderDims& d, std::vector<float>& 
   return od;
 }
 
-void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
+void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim, bool split = false) {
   // A prompt of 48 rows (8 text rows, then two image pages of 20 rows) run
   // through DecodeStep::prefill, then 40 decode steps on the caches it
   // wrote, the logits of each against the oracle's decoder on the same
@@ -971,9 +971,15 @@ void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
   // the same routing choices, so only fp32 summation order separates them).
   // Router as the reference test sets it: block 4, one local block,
   // idx_scale 4. Head dim 16 takes the prefill's three-launch attention
-  // (products, mask + softmax, products), 64 the one-pass attention.
-  std::printf("prefill then decode, head dim %lld\n", static_cast<long long>(head_dim));
+  // (products, mask + softmax, products), 64 the one-pass attention. With
+  // split, the prompt's attention takes the split-operand products (each
+  // attention output within one bf16 step of the fp32 products' rounding):
+  // a moved rounding can move a routing choice, so the logits are held to
+  // the reference test's own 2e-2.
+  std::printf("prefill then decode, head dim %lld%s\n", static_cast<long long>(head_dim),
+              split ? ", split-operand attention" : "");
   ro::DecoderDims d;
+  d.split_attention = split;
   d.hidden = 64;
   d.heads = 2;
   d.head_dim = head_dim;
@@ -1038,7 +1044,8 @@ void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
   const auto x = random(rows * H, 0.5f);
   const auto got = step.prefill(x, coords, qp);
   const auto want = od.forward(x, coords, qp, false);
-  expect("prefill logits (48 rows)", max_rel(got, want), 1e-4);
+  const double bar_prefill = split ? 2e-2 : 1e-4, bar_step = split ? 2e-2 : 1e-3, bar_median = split ? 2e-2 : 1e-5;
+  expect("prefill logits (48 rows)", max_rel(got, want), bar_prefill);
   require(step.length() == rows, "prefill length");
   std::vector<double> errs;
   for (std::int64_t t = 0; t < 40; ++t) {
@@ -1049,11 +1056,13 @@ void prefill_then_decode(const ro::Context& ctx, std::int64_t head_dim) {
     const std::vector<float> row(embed.begin() + token * H, embed.begin() + (token + 1) * H);
     const auto w = od.forward(row, {c}, {page}, true);
     errs.push_back(max_rel(g, w));
-    if (errs.back() > 1e-3) expect(("decode after prefill, step " + std::to_string(t)).c_str(), errs.back(), 1e-3);
+    if (errs.back() > bar_step) {
+      expect(("decode after prefill, step " + std::to_string(t)).c_str(), errs.back(), bar_step);
+    }
   }
   std::sort(errs.begin(), errs.end());
-  expect("decode after prefill worst", errs.back(), 1e-3);
-  expect("decode after prefill median", errs[errs.size() / 2], 1e-5);
+  expect("decode after prefill worst", errs.back(), bar_step);
+  expect("decode after prefill median", errs[errs.size() / 2], bar_median);
   require_throws_invalid([&] { step.prefill(std::vector<float>(100 * H, 0.0f), std::vector<ro::RopeCoord>(100)); },
                          "prefill past the cache");
 }
@@ -1580,6 +1589,11 @@ int main() {
     decoder_model(ctx, false);
     decoder_model(ctx, true);
     model_by_names(ctx);
+    // last, so that the checks above draw the same random inputs whatever
+    // is added here (their tight bars assume the device and the oracle route
+    // alike, which a near-tie in other inputs can break)
+    prefill_then_decode(ctx, 64, true);
+    prefill_then_decode(ctx, 128, true);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());

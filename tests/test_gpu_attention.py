@@ -243,3 +243,96 @@ def test_attention_into_bf16_is_the_rounded_output(backend, slices, rows, keys, 
     backend.attention(q, k, v, got, slices, rows, keys, hd, 0.125, mask)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def _routed_mask(rows, keys, seed):
+    """A prefill's routed mask: query t at position keys - rows + t attends
+    its window (the keys of the last 4 32-key blocks up to its position,
+    bias 0) and up to 3 earlier blocks with a bias each; -inf elsewhere and
+    past its position."""
+    g = np.random.default_rng(seed)
+    mask = np.full((rows, keys), -np.inf, np.float32)
+    for t in range(rows):
+        pos = keys - rows + t
+        mask[t, max(0, (pos // 32 - 3) * 32):pos + 1] = 0.0
+        earlier = pos // 32 - 3
+        if earlier > 0:
+            for b in g.choice(earlier, size=min(3, earlier), replace=False):
+                mask[t, 32 * b:32 * b + 32] = np.float32(0.5 * g.standard_normal())
+    return mask
+
+
+@pytest.mark.parametrize("slices,rows,keys,hd,kind,amp", [(3, 100, 300, 128, "random", 1.0),
+                                                          (2, 257, 257, 64, "causal", 1.0),
+                                                          (4, 300, 1100, 128, "routed", 1.0),
+                                                          (1, 1, 33, 128, "random", 1.0),
+                                                          (2, 130, 40, 64, "causal", 1.0),
+                                                          (2, 200, 2100, 128, "routed", 4.0),
+                                                          (1, 200, 64, 128, "dead", 1.0)])
+def test_attention_masked_split_operands(backend, slices, rows, keys, hd, kind, amp):
+    """uocr_rocm_attention_masked_bf16_ws: the masked attention into bf16 on
+    the bf16 matrix cores with split operands, the workgroups walking only
+    the 32-key tiles their 128 rows attend. Masks: random -inf entries with
+    a causal edge, a row with no live key and a row whose one live key ends
+    the last tile; causal; a prefill's routed mask (window plus selected
+    blocks, past the position -inf); a first row block with no live key at
+    all (zeros). As for SAM's split products: every element within one bf16
+    step of the fp32 kernel's output (floor 2^-14 of the largest), most
+    equal to its rounding, within 2^-8 of the oracle; amp 4 spreads the
+    scores so that rows rescale mid-walk, and there the bar is the
+    oracle's alone at 2^-6."""
+    q = normal(770 + rows, (slices, rows, hd)) * np.float32(amp)
+    k, v = normal(771 + keys, (slices, keys, hd)), normal(772, (slices, keys, hd))
+    g = np.random.default_rng(773)
+    if kind == "random" or kind == "dead":
+        mask = np.where(g.random((rows, keys)) < 0.3, -np.inf, 0.1 * g.standard_normal((rows, keys)))
+        mask = mask.astype(np.float32)
+        if kind == "dead":
+            mask[:128] = -np.inf
+        else:
+            for t in range(rows):
+                mask[t, max(1, keys - rows - 50 + t):] = -np.inf
+            mask[0, :] = -np.inf
+            if rows > 8:
+                mask[8, :] = -np.inf
+                mask[8, keys - 1] = 0.0
+    elif kind == "causal":
+        mask = np.triu(np.full((rows, keys), -np.inf, np.float32), 1 + keys - rows)
+    else:
+        mask = _routed_mask(rows, keys, 774)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    qd, kd, vd, md = dev_f32(q), dev_f32(k), dev_f32(v), dev_f32(mask)
+    out = torch.empty(slices, rows, hd, device="cuda")
+    backend.attention(qd, kd, vd, out, slices, rows, keys, hd, scale, md)
+    want = torch.empty(slices, rows, hd, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(out, want)
+    ws = torch.empty(backend.attention_masked_workspace_floats(slices, rows, keys, hd), device="cuda")
+    got = torch.full((slices, rows, hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+    backend.attention_masked(qd, kd, vd, got, slices, rows, keys, hd, scale, md, ws)
+    torch.cuda.synchronize()
+    got_f = oracle.bf16_to_f32(got.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(slices, rows, hd)
+    out_f = host_f32(out)
+    dead = ~np.isfinite(mask).any(axis=1)
+    assert np.array_equal(got_f[:, dead], np.zeros_like(got_f[:, dead]))
+    if amp == 1.0:
+        tol = 2.0**-8 * np.abs(out_f) + 2.0**-14 * np.abs(out_f).max()
+        assert np.all(np.abs(got_f - out_f) <= tol), float(np.max(np.abs(got_f - out_f) - tol))
+        assert np.mean(got.view(torch.int16).cpu().numpy() == want.view(torch.int16).cpu().numpy()) > 0.9
+    bar = 2.0**-8 if amp == 1.0 else 2.0**-6
+    for s in sorted({0, slices - 1}):
+        want_o = oracle.attention_head(q[s], k[s], v[s], mask, scale)
+        assert_f32_close(got_f[s], want_o, bar, f"masked split-bf16 attention, {kind} mask, slice {s}")
+
+
+def test_attention_masked_refuses_what_it_cannot_take(backend):
+    q = torch.zeros(1, 64, 128, device="cuda")
+    out = torch.empty(1, 64, 128, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(backend.attention_masked_workspace_floats(1, 64, 64, 128), device="cuda")
+    mask = torch.zeros(64, 64, device="cuda")
+    with pytest.raises(ValueError):  # a workspace one float short
+        backend.attention_masked(q, q, q, out, 1, 64, 64, 128, 0.1, mask, ws[:-1])
+    with pytest.raises(ValueError):  # mask rows shorter than the keys
+        m2 = torch.zeros(64, 60, device="cuda")
+        backend.attention_masked(q, q, q, out, 1, 64, 64, 128, 0.1, m2, ws)
+    with pytest.raises(ValueError):  # an fp32 out
+        backend.attention_masked(q, q, q, q, 1, 64, 64, 128, 0.1, mask, ws)
