@@ -956,9 +956,27 @@ __global__ __launch_bounds__(256) void x3m_split_k(const AttnArgs a, int tiles) 
   }
 }
 
+// Where a row block's live tiles are many, workgroup (row block, j) walks
+// the j-th run of `chunk` of them and leaves per row the partial record
+// (m, l, unnormalised O: X3Partials) that x3m_merge_k combines; a row block
+// with one run writes its output itself.
+struct X3Partials {
+  int chunk;     // live tiles per workgroup
+  int chunks;    // runs per row block (workgroups per row block and slice)
+  float* o;      // [slices][row blocks][chunks][128 rows][hd]
+  float* ml;     // [slices][row blocks][chunks][128 rows][2]: m, l
+};
+
+// The live tiles of a row block (the bits of its map words).
+__device__ __forceinline__ int live_tiles(const uint32_t* tmap, int words) {
+  int n = 0;
+  for (int w = 0; w < words; ++w) n += __builtin_popcount(tmap[w]);
+  return n;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const uint32_t* __restrict__ map, int words,
-                                                       int row_blocks, int slices) {
+                                                       int row_blocks, int slices, X3Partials part) {
   constexpr int kNB = HD / 16;           // 16-column blocks of a query or key row
   constexpr int kDB = HD / 32;           // 32-dimension blocks of the output
   constexpr int kKS = HD + 8;            // K rows in bf16: an odd number of 16-byte groups apart
@@ -974,8 +992,9 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hl = lane >> 5, c = lane & 31;
   const int tid = static_cast<int>(threadIdx.x);
-  // workgroup: every slice's last row block first, then the one before
-  const int rb = row_blocks - 1 - static_cast<int>(blockIdx.x) / slices;
+  // workgroup: (row block, run, slice), every slice's last row block first
+  const int run = static_cast<int>(blockIdx.x) / slices % part.chunks;
+  const int rb = row_blocks - 1 - static_cast<int>(blockIdx.x) / slices / part.chunks;
   const int64_t slice = static_cast<int>(blockIdx.x) % slices;
   const int q0 = rb * kMaskRowBlock + wave * kQueriesPerWave;
   const int qrow = q0 + c;
@@ -999,14 +1018,21 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
     }
     return tiles;
   };
-  int t = next_live(-1);
-  if (t >= tiles) {  // no key attended by any row of the block: zeros
-    if (qin) {
+  const int live = live_tiles(tmap, words);
+  const int runs = (live + part.chunk - 1) / part.chunk;
+  if (live == 0) {  // no key attended by any row of the block: zeros
+    if (run == 0 && qin) {
 #pragma unroll
       for (int d = 4 * hl; d < HD; d += 8) store4(a, orow + d, 0.0f, 0.0f, 0.0f, 0.0f);
     }
     return;
   }
+  if (run >= runs) return;  // uniform over the workgroup, before any barrier
+  // the first live tile of this run: skip run * chunk of them
+  int t = -1;
+  for (int skip = run * part.chunk; skip >= 0; --skip) t = next_live(t);
+  // the run's live tiles i = 0 .. chunk - 1 (past the run: tiles)
+  auto after = [&](int tt, int i) { return i + 1 < part.chunk && tt < tiles ? next_live(tt) : tiles; };
 
   // this thread's 16-byte chunks of each of a tile's four split parts
   // (formed by x3m_split_k), copied into the padded LDS rows
@@ -1044,11 +1070,16 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
   const bool vec = mask_vec(a.mask, a.mask_ld);
   const float* mrow = a.mask + static_cast<int64_t>(qin ? qrow : 0) * a.mask_ld;
   auto load_mask = [&](int tt, Block& blk) {
+    const bool whole = vec && (tt + 1) * kKeyTile <= a.keys;  // uniform: every key of the tile exists
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int key4 = tt * kKeyTile + 8 * g + 4 * hl;
       float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-      if (qin && key4 < a.keys) v = mask4(mrow, key4, a.keys, vec);
+      if (whole) {
+        if (qin) v = *reinterpret_cast<const float4*>(mrow + key4);
+      } else if (qin && key4 < a.keys) {
+        v = mask4(mrow, key4, a.keys, vec);
+      }
       blk.m[4 * g] = v.x;
       blk.m[4 * g + 1] = v.y;
       blk.m[4 * g + 2] = v.z;
@@ -1075,7 +1106,8 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
   Block blk_a, blk_b;
   load_mask(t, blk_a);
   store_kv(0);
-  int n1 = next_live(t);
+  int i = 0;  // t's place in the run
+  int n1 = after(t, i);
   load_kv(n1 < tiles ? n1 : t);
   __syncthreads();
 
@@ -1167,20 +1199,37 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
   };
   // two mask blocks used in turn (no copies): tiles alternate stages 0, 1
   while (true) {
-    int n2 = n1 < tiles ? next_live(n1) : tiles;
+    int n2 = after(n1, i + 1);
     tile(t, n1, n2, 0, blk_a, blk_b);
     t = n1;
+    ++i;
     if (t >= tiles) break;
     n1 = n2;
-    n2 = n1 < tiles ? next_live(n1) : tiles;
+    n2 = after(n1, i + 1);
     tile(t, n1, n2, 1, blk_b, blk_a);
     t = n1;
+    ++i;
     if (t >= tiles) break;
     n1 = n2;
   }
 
   const float l = sum_halves(lh);
   if (!qin) return;
+  if (runs > 1) {
+    // the partial record: m and l (lane half 0), O unnormalised
+    const int64_t rec = ((slice * row_blocks + rb) * part.chunks + run) * kMaskRowBlock + (qrow - rb * kMaskRowBlock);
+    if (hl == 0) *reinterpret_cast<float2*>(part.ml + 2 * rec) = make_float2(m, l);
+#pragma unroll
+    for (int b = 0; b < kDB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * b + 8 * g + 4 * hl;
+        *reinterpret_cast<float4*>(part.o + rec * HD + d) =
+            make_float4(o[b][4 * g], o[b][4 * g + 1], o[b][4 * g + 2], o[b][4 * g + 3]);
+      }
+    }
+    return;
+  }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
   for (int b = 0; b < kDB; ++b) {
@@ -1190,6 +1239,52 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
       store4(a, orow + d, o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv);
     }
   }
+}
+
+// The rows of row blocks walked in several runs: out = sum_j 2^(m_j - M) O_j
+// / sum_j 2^(m_j - M) l_j with M the largest m_j (a run where the row saw
+// no finite score holds m = -inf, l = 0, O = 0 and weighs 0; no finite
+// score at all: zeros), into bf16. Workgroup (row block, slice); thread:
+// row tid / 2, dimensions (tid % 2) hd / 2 .. + hd / 2 - 1.
+template <int HD>
+__global__ __launch_bounds__(256) void x3m_merge_k(const AttnArgs a, const uint32_t* __restrict__ map, int words,
+                                                   int row_blocks, X3Partials part) {
+  constexpr int kHalf = HD / 2;
+  const int rb = blockIdx.x;
+  const int64_t slice = blockIdx.y;
+  const int live = live_tiles(map + static_cast<int64_t>(rb) * words, words);
+  const int runs = (live + part.chunk - 1) / part.chunk;
+  if (runs <= 1) return;
+  const int r = static_cast<int>(threadIdx.x) / 2, d0 = kHalf * (static_cast<int>(threadIdx.x) % 2);
+  const int qrow = rb * kMaskRowBlock + r;
+  if (qrow >= a.rows) return;
+  const int64_t rec0 = (slice * row_blocks + rb) * part.chunks * kMaskRowBlock + r;
+  float big = -INFINITY;
+  for (int j = 0; j < runs; ++j) big = fmaxf(big, part.ml[2 * (rec0 + j * kMaskRowBlock)]);
+  const float ref = big == -INFINITY ? 0.0f : big;
+  float acc[kHalf];
+#pragma unroll
+  for (int e = 0; e < kHalf; ++e) acc[e] = 0.0f;
+  float total = 0.0f;
+  for (int j = 0; j < runs; ++j) {
+    const int64_t rec = rec0 + j * kMaskRowBlock;
+    const float2 ml = *reinterpret_cast<const float2*>(part.ml + 2 * rec);
+    const float wgt = __builtin_amdgcn_exp2f(ml.x - ref);  // 0 for m = -inf
+    total += wgt * ml.y;
+    const float* src = part.o + rec * HD + d0;
+#pragma unroll
+    for (int e = 0; e < kHalf; e += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(src + e);
+      acc[e] += wgt * v.x;
+      acc[e + 1] += wgt * v.y;
+      acc[e + 2] += wgt * v.z;
+      acc[e + 3] += wgt * v.w;
+    }
+  }
+  const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+  const int64_t orow = slice_at(a, slice, a.so, a.io) + static_cast<int64_t>(qrow) * a.ldo + d0;
+#pragma unroll
+  for (int e = 0; e < kHalf; e += 4) store4(a, orow + e, acc[e] * inv, acc[e + 1] * inv, acc[e + 2] * inv, acc[e + 3] * inv);
 }
 
 // ---- few query rows: the keys split over the waves ---------------------------
@@ -1674,8 +1769,34 @@ int64_t mask_map_floats(int64_t rows, int64_t keys) {
   return (rows + kMaskRowBlock - 1) / kMaskRowBlock * mask_map_words(keys);
 }
 int64_t masked_tiles_offset(int64_t rows, int64_t keys) { return (mask_map_floats(rows, keys) + 63) / 64 * 64; }
-int64_t masked_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
+// Live tiles per workgroup: every live tile of a row block, unless the row
+// blocks of all slices fill fewer than the slots of two workgroups per CU
+// (256 CUs); then a row block's walk is cut into runs of at most the tiles
+// one slot would get if every tile were live (at least 32), so that the
+// longest walks of a causal mask no longer set the time. Then the runs per
+// row block, and the partial records (O, then m and l) after the split tiles.
+constexpr int64_t kSlots = 2 * 256;
+constexpr int64_t kMinRunTiles = 32;
+int64_t masked_run_tiles(int64_t slices, int64_t rows, int64_t keys) {
+  const int64_t tiles = (keys + kKeyTile - 1) / kKeyTile;
+  const int64_t blocks = slices * ((rows + kMaskRowBlock - 1) / kMaskRowBlock);
+  if (blocks >= kSlots) return tiles;
+  const int64_t share = (tiles * blocks + kSlots - 1) / kSlots;
+  return share > kMinRunTiles ? share : kMinRunTiles;
+}
+int64_t masked_runs(int64_t slices, int64_t rows, int64_t keys) {
+  const int64_t per = masked_run_tiles(slices, rows, keys);
+  return ((keys + kKeyTile - 1) / kKeyTile + per - 1) / per;
+}
+int64_t masked_partials_offset(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
   return masked_tiles_offset(rows, keys) + slices * ((keys + kKeyTile - 1) / kKeyTile) * 64 * hd;
+}
+int64_t masked_partial_rows(int64_t slices, int64_t rows, int64_t keys) {
+  const int64_t runs = masked_runs(slices, rows, keys);
+  return runs > 1 ? slices * ((rows + kMaskRowBlock - 1) / kMaskRowBlock) * runs * kMaskRowBlock : 0;
+}
+int64_t masked_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
+  return masked_partials_offset(slices, rows, keys, hd) + masked_partial_rows(slices, rows, keys) * (hd + 2);
 }
 
 int masked_split_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
@@ -1710,14 +1831,27 @@ int masked_split_entry(const char* what, void* stream, const float* q, int64_t l
     x3m_split_k<128><<<split_grid, 256, 0, as_stream(stream)>>>(a, static_cast<int>(tiles));
   }
   if (const int st = check_launch(what)) return st;
-  const unsigned grid = static_cast<unsigned>(row_blocks * slices);
+  const int64_t runs = masked_runs(slices, rows, keys);
+  float* po = workspace + masked_partials_offset(slices, rows, keys, hd);
+  X3Partials part{static_cast<int>(masked_run_tiles(slices, rows, keys)), static_cast<int>(runs), runs > 1 ? po : nullptr,
+                  runs > 1 ? po + masked_partial_rows(slices, rows, keys) * hd : nullptr};
+  UOCR_REQUIRE(row_blocks * runs * slices < (int64_t{1} << 31), what, "too many workgroups");
+  const unsigned grid = static_cast<unsigned>(row_blocks * runs * slices);
+  const int w = static_cast<int>(words), rbs = static_cast<int>(row_blocks), sl = static_cast<int>(slices);
   clear_launch_error();
   if (hd == 64) {
-    attention_x3m_k<64><<<grid, 256, 0, as_stream(stream)>>>(a, map, static_cast<int>(words),
-                                                             static_cast<int>(row_blocks), static_cast<int>(slices));
+    attention_x3m_k<64><<<grid, 256, 0, as_stream(stream)>>>(a, map, w, rbs, sl, part);
   } else {
-    attention_x3m_k<128><<<grid, 256, 0, as_stream(stream)>>>(a, map, static_cast<int>(words),
-                                                              static_cast<int>(row_blocks), static_cast<int>(slices));
+    attention_x3m_k<128><<<grid, 256, 0, as_stream(stream)>>>(a, map, w, rbs, sl, part);
+  }
+  if (runs == 1) return check_launch(what);
+  if (const int st = check_launch(what)) return st;
+  const dim3 merge_grid(static_cast<unsigned>(row_blocks), static_cast<unsigned>(slices));
+  clear_launch_error();
+  if (hd == 64) {
+    x3m_merge_k<64><<<merge_grid, 256, 0, as_stream(stream)>>>(a, map, w, rbs, part);
+  } else {
+    x3m_merge_k<128><<<merge_grid, 256, 0, as_stream(stream)>>>(a, map, w, rbs, part);
   }
   return check_launch(what);
 }

@@ -268,7 +268,8 @@ def _routed_mask(rows, keys, seed):
                                                           (1, 1, 33, 128, "random", 1.0),
                                                           (2, 130, 40, 64, "causal", 1.0),
                                                           (2, 200, 2100, 128, "routed", 4.0),
-                                                          (1, 200, 64, 128, "dead", 1.0)])
+                                                          (1, 200, 64, 128, "dead", 1.0),
+                                                          (2, 150, 3000, 64, "random", 1.0)])
 def test_attention_masked_split_operands(backend, slices, rows, keys, hd, kind, amp):
     """uocr_rocm_attention_masked_bf16_ws: the masked attention into bf16 on
     the bf16 matrix cores with split operands, the workgroups walking only
@@ -276,11 +277,13 @@ def test_attention_masked_split_operands(backend, slices, rows, keys, hd, kind, 
     a causal edge, a row with no live key and a row whose one live key ends
     the last tile; causal; a prefill's routed mask (window plus selected
     blocks, past the position -inf); a first row block with no live key at
-    all (zeros). As for SAM's split products: every element within one bf16
-    step of the fp32 kernel's output (floor 2^-14 of the largest), most
-    equal to its rounding, within 2^-8 of the oracle; amp 4 spreads the
-    scores so that rows rescale mid-walk, and there the bar is the
-    oracle's alone at 2^-6."""
+    all (zeros). Few row blocks over many keys (1100, 2100, 3000) cut a
+    block's walk into runs of at least 32 live tiles whose partial records
+    a merge launch combines. As for SAM's split products: every element
+    within one bf16 step of the fp32 kernel's output (floor 2^-14 of the
+    largest), most equal to its rounding, within 2^-8 of the oracle; amp 4
+    spreads the scores so that rows rescale mid-walk, and there the bar is
+    the oracle's alone at 2^-6."""
     q = normal(770 + rows, (slices, rows, hd)) * np.float32(amp)
     k, v = normal(771 + keys, (slices, keys, hd)), normal(772, (slices, keys, hd))
     g = np.random.default_rng(773)
