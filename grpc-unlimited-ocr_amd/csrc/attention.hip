@@ -164,6 +164,30 @@ __device__ __forceinline__ int64_t slice_at(const AttnArgs& a, int64_t s, int64_
   return a.inner == 1 ? s * so : (s / a.inner) * so + (s % a.inner) * si;
 }
 
+// Four mask entries from key4 (a multiple of 4) of a row: one 16-byte read
+// where rows are whole 16-byte chunks apart (mask_ld % 4 == 0 and the mask
+// 16-byte aligned; mask_ld >= keys, so a read that starts below keys stays
+// in its row), else element by element; -inf from key `keys` on.
+__device__ __forceinline__ float4 mask4(const float* row, int key4, int keys, bool vec) {
+  float4 m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  if (vec) {
+    m = *reinterpret_cast<const float4*>(row + key4);
+  } else {
+    m.x = row[key4];
+    if (key4 + 1 < keys) m.y = row[key4 + 1];
+    if (key4 + 2 < keys) m.z = row[key4 + 2];
+    if (key4 + 3 < keys) m.w = row[key4 + 3];
+  }
+  if (key4 + 1 >= keys) m.y = -INFINITY;
+  if (key4 + 2 >= keys) m.z = -INFINITY;
+  if (key4 + 3 >= keys) m.w = -INFINITY;
+  return m;
+}
+
+__device__ __forceinline__ bool mask_vec(const float* mask, int64_t mask_ld) {
+  return (mask_ld & 3) == 0 && (reinterpret_cast<uintptr_t>(mask) & 15) == 0;
+}
+
 template <int HD, Bias kBias>
 __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const AttnArgs a) {
   constexpr int kThreads = 64 * waves_of<kBias>();
@@ -183,7 +207,9 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hl = lane >> 5, c = lane & 31;
   const int64_t slice = blockIdx.y;
-  const int q0 = blockIdx.x * kQueriesPerBlock + wave * kQueriesPerWave;
+  // with a mask, the last row blocks first (under a causal mask the longest walks)
+  const int rblk = kBias == Bias::kMask ? static_cast<int>(gridDim.x - 1 - blockIdx.x) : static_cast<int>(blockIdx.x);
+  const int q0 = rblk * kQueriesPerBlock + wave * kQueriesPerWave;
   const int qrow = q0 + c;
   const bool qin = qrow < a.rows;
   const float* qb = a.q + slice_at(a, slice, a.sq, a.iq);
@@ -211,7 +237,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     if (a.table != nullptr) {
       // the workgroup's rows of the table lie contiguous in memory with the
       // LDS row stride: one coalesced copy by every thread
-      const int first = blockIdx.x * kQueriesPerBlock;
+      const int first = rblk * kQueriesPerBlock;
       const int here = a.rows - first < kQueriesPerBlock ? a.rows - first : kQueriesPerBlock;
       const float* src = a.table + (slice * a.rows + first) * static_cast<int64_t>(a.dots_ld);
       const int count = here * a.dots_ld;
@@ -266,27 +292,48 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   }
   float m = -INFINITY, l = 0.0f;
   const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
+  // With a mask, this wave's 32 x 32 block of it (register r: key 8 (r / 4)
+  // + 4 h + r % 4 of the tile; -inf past the keys or the rows), read a tile
+  // ahead: where every entry is -inf (a causal or routed mask's dead tiles)
+  // the wave skips the tile's products and softmax; the tile's K and V
+  // still reach LDS for the other waves.
+  constexpr int kMk = kBias == Bias::kMask ? 16 : 1;
+  float mk[kMk], mn[kMk];
+  const bool vec = kBias == Bias::kMask && mask_vec(a.mask, a.mask_ld);
+  const float* mrow = a.mask + static_cast<int64_t>(qin ? qrow : 0) * a.mask_ld;
+  auto load_mask = [&](int tt, float (&dst)[kMk]) {
+    if constexpr (kBias == Bias::kMask) {
+      const bool whole = vec && (tt + 1) * kKeyTile <= a.keys;  // uniform
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int key4 = tt * kKeyTile + 8 * g + 4 * hl;
+        float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (whole) {
+          if (qin) v = *reinterpret_cast<const float4*>(mrow + key4);
+        } else if (qin && key4 < a.keys) {
+          v = mask4(mrow, key4, a.keys, vec);
+        }
+        dst[4 * g] = v.x;
+        dst[4 * g + 1] = v.y;
+        dst[4 * g + 2] = v.z;
+        dst[4 * g + 3] = v.w;
+      }
+    }
+  };
+  load_mask(0, mk);
   for (int t = 0; t < tiles; ++t) {
     const int key0 = t * kKeyTile;
     const bool more = t + 1 < tiles;
     if (more) load_tile<HD, kThreads>(a, kb, vb, key0 + kKeyTile, kr, vr);
+    load_mask(more ? t + 1 : t, mn);
 
-    // With a mask, this wave's 32 x 32 block of it first: where every entry
-    // is -inf (a causal or routed mask's dead tiles) the wave skips the
-    // tile's products and softmax; the tile's K and V still reach LDS for
-    // the other waves.
-    float mk[kBias == Bias::kMask ? 16 : 1];
     // A wave whose rows all lie past the last query row (the tail workgroup
     // of a slice) only helps stage the tiles.
     bool live = q0 < a.rows;
     if constexpr (kBias == Bias::kMask) {
       bool any = false;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = key0 + 8 * (r / 4) + 4 * hl + (r % 4);
-        mk[r] = key < a.keys && qin ? a.mask[qrow * a.mask_ld + key] : -INFINITY;
-        any = any || mk[r] != -INFINITY;
-      }
+      for (int r = 0; r < 16; ++r) any = any || mk[r] != -INFINITY;
       live = live && __ballot(any) != 0;
     }
     if (live) {
@@ -405,6 +452,10 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     if (more) {
       store_tile<HD, kThreads>(ks, vs, kr, vr);
       __syncthreads();
+    }
+    if constexpr (kBias == Bias::kMask) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mk[r] = mn[r];
     }
   }
 
@@ -864,30 +915,6 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
 // out last row block first (under a causal mask the longest walks first).
 constexpr int kMaskRowBlock = 4 * kQueriesPerWave;  // query rows per workgroup
 constexpr int kMaskMapKeys = 32 * kKeyTile;         // keys per map word (a bit per tile)
-
-// Four mask entries from key4 (a multiple of 4) of a row: one 16-byte read
-// where rows are whole 16-byte chunks apart (mask_ld % 4 == 0 and the mask
-// 16-byte aligned; mask_ld >= keys, so a read that starts below keys stays
-// in its row), else element by element; -inf from key `keys` on.
-__device__ __forceinline__ float4 mask4(const float* row, int key4, int keys, bool vec) {
-  float4 m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-  if (vec) {
-    m = *reinterpret_cast<const float4*>(row + key4);
-  } else {
-    m.x = row[key4];
-    if (key4 + 1 < keys) m.y = row[key4 + 1];
-    if (key4 + 2 < keys) m.z = row[key4 + 2];
-    if (key4 + 3 < keys) m.w = row[key4 + 3];
-  }
-  if (key4 + 1 >= keys) m.y = -INFINITY;
-  if (key4 + 2 >= keys) m.z = -INFINITY;
-  if (key4 + 3 >= keys) m.w = -INFINITY;
-  return m;
-}
-
-__device__ __forceinline__ bool mask_vec(const float* mask, int64_t mask_ld) {
-  return (mask_ld & 3) == 0 && (reinterpret_cast<uintptr_t>(mask) & 15) == 0;
-}
 
 // Map word (row block blockIdx.y, word blockIdx.x): bit j set where some
 // entry of rows [128 rb, 128 rb + 128) x keys of tile 32 wd + j is not -inf
