@@ -19,9 +19,11 @@
 // matrix product of the projections and convolutions runs on the bf16
 // matrix cores (x rounded to bf16, fp32 sums: the reference's linear), k
 // split over a workspace where a product has too few tiles (CLIP's 257
-// rows); attention is fp32 on the fp32 matrix cores, one launch per layer
-// for every head and window (scores, bias, softmax and values without the
-// scores reaching memory). The learned position grids and the
+// rows); attention is one launch per layer for every head and window
+// (scores, bias, softmax and values without the scores reaching memory),
+// its output rounded to bf16 for the output projection: SAM's on the bf16
+// matrix cores with each fp32 operand split into bf16 hi + lo parts,
+// CLIP's on the fp32 matrix cores. The learned position grids and the
 // relative-position tables are resized on the host once per grid size, as
 // the reference does, and kept on the device.
 
