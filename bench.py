@@ -439,15 +439,19 @@ def config6(be, torch, timer):
     b_qg = bytes_gelu(qg_rows * qg_cols, 2)
     ms_qg = time_kernel(timer, lambda: bf16_randn(torch, (qg_rows, qg_cols)), lambda x: be.quick_gelu(x))
     # the decoder prefill's whole attention over the same causal mask, head
-    # dim 128, in one pass: fp32 products, and split-operand bf16 products
-    # into bf16 (tile map and split tiles included)
+    # dim 128, in one pass: fp32 products (without and with the workspace:
+    # the mask's live tiles, runs merged), and split-operand bf16 products
+    # into bf16 (tile map, split tiles and merge included)
     hd = 128
     out32 = torch.empty(heads, rows, hd, device="cuda")
     out16 = torch.empty(heads, rows, hd, dtype=torch.bfloat16, device="cuda")
     ws = torch.empty(be.attention_masked_workspace_floats(heads, rows, keys, hd), device="cuda")
     qkv = lambda: tuple(torch.randn(heads, rows, hd, device="cuda") for _ in range(3))  # noqa: E731
+    ws32 = torch.empty(be.attention_workspace_floats(heads, rows, keys, hd), device="cuda")
     ms_a32 = time_kernel(timer, qkv, lambda s: be.attention(s[0], s[1], s[2], out32, heads, rows, keys, hd, 0.088,
                                                             mask))
+    ms_a32w = time_kernel(timer, qkv, lambda s: be.attention(s[0], s[1], s[2], out32, heads, rows, keys, hd, 0.088,
+                                                             mask, workspace=ws32))
     ms_a16 = time_kernel(timer, qkv, lambda s: be.attention_masked(s[0], s[1], s[2], out16, heads, rows, keys, hd,
                                                                    0.088, mask, ws))
     flop = 4.0 * heads * hd * rows * (rows + 1) / 2  # the causal mask's live (query, key) pairs
@@ -456,7 +460,8 @@ def config6(be, torch, timer):
                         "pass; quick GELU [4096, 4096] bf16",
             "step": report("scale_mask_softmax", b_mask, ms_fused),
             "pair_scale_add_mask_then_softmax": report("pair", b_sm + b_mask, ms_pair),
-            "attention_10x4096x128_causal": {"one_pass_fp32": attn(ms_a32), "split_bf16": attn(ms_a16),
+            "attention_10x4096x128_causal": {"one_pass_fp32": attn(ms_a32), "one_pass_fp32_ws": attn(ms_a32w),
+                                             "split_bf16": attn(ms_a16),
                                              "live_flop": flop},
             "kernels": {"scale_mask_softmax_rows_f32": report("scale_mask_softmax", b_mask, ms_fused),
                         "scale_add_mask_f32": report("scale_add_mask", b_mask, ms_mask),

@@ -170,6 +170,11 @@ _SIGNATURES = {
                                                 _vp, _vp, _i64], _int),
     "uocr_rocm_attention_bf16": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                   _i64, _i64, _i64, _f32, _vp, _i64], _int),
+    "uocr_rocm_attention_workspace_floats": ([_i64, _i64, _i64, _i64], _i64),
+    "uocr_rocm_attention_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
+                                _i64, _i64, _f32, _vp, _i64, _vp, _i64], _int),
+    "uocr_rocm_attention_bf16_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                                     _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64], _int),
     "uocr_rocm_attention_masked_workspace_floats": ([_i64, _i64, _i64, _i64], _i64),
     "uocr_rocm_attention_masked_bf16_ws": ([_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                                             _i64, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64], _int),
@@ -666,10 +671,12 @@ def _operand(t, offset, ld, slice_stride):
     return (_ptr(t) + t.element_size() * offset, ld, slice_stride)
 
 
-def attention(q, k, v, out, slices, rows, keys, hd, scale, mask=None, strides=None, stream=None):
+def attention(q, k, v, out, slices, rows, keys, hd, scale, mask=None, strides=None, workspace=None, stream=None):
     """out[s, t] = softmax(scale q[s, t] . k[s, :] + mask[t, :]) v[s, :] in one
     pass (new). strides: {name: (offset, ld, slice_stride)} for q, k, v, out
-    (elements); default head-major [slices, rows or keys, hd]."""
+    (elements); default head-major [slices, rows or keys, hd]. workspace
+    (attention_workspace_floats floats): a mask's live tiles walked alone,
+    long walks cut into runs merged by a last launch."""
     st = strides or {}
     qo = _operand(q, *st.get("q", (0, hd, rows * hd)))
     ko = _operand(k, *st.get("k", (0, hd, keys * hd)))
@@ -677,8 +684,16 @@ def attention(q, k, v, out, slices, rows, keys, hd, scale, mask=None, strides=No
     oo = _operand(out, *st.get("out", (0, hd, rows * hd)))
     # a bfloat16 out: the output rounded to bf16 in the epilogue (new)
     name = "uocr_rocm_attention_bf16" if out.dtype == _torch().bfloat16 else "uocr_rocm_attention"
-    _op(name, stream, *qo, *ko, *vo, *oo, slices, rows, keys, hd, scale, _f32_param(mask),
-        0 if mask is None else mask.shape[-1])
+    args = (*qo, *ko, *vo, *oo, slices, rows, keys, hd, scale, _f32_param(mask), 0 if mask is None else mask.shape[-1])
+    if workspace is None:
+        _op(name, stream, *args)
+    else:
+        _op(name + "_ws", stream, *args, _ptr(workspace), workspace.numel())
+
+
+def attention_workspace_floats(slices, rows, keys, hd):
+    """Floats of attention's workspace for a mask."""
+    return int(lib().uocr_rocm_attention_workspace_floats(slices, rows, keys, hd))
 
 
 def attention_masked(q, k, v, out, slices, rows, keys, hd, scale, mask, workspace, strides=None, stream=None):

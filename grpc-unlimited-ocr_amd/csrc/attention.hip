@@ -109,6 +109,16 @@ struct AttnArgs {
   // dot-table launch (kv_tiles_of), for key tiles of x3_rows grid rows
   uint16_t* kvx = nullptr;
   int x3_rows = -1;
+  // non-null (attention_k with a mask): the mask's live-tile map (a bit per
+  // 128 query rows and 32-key tile, map_words words per row block); a row
+  // block's walk is cut into `runs` runs of run_tiles live tiles, and where
+  // a block takes more than one, each run leaves per row (m, l) in part_ml
+  // and its unnormalised output in part_o ([slices][row blocks][runs][128
+  // rows]) for the merge launch
+  const uint32_t* map = nullptr;
+  int map_words = 0, run_tiles = 0, runs = 1;
+  float* part_o = nullptr;
+  float* part_ml = nullptr;
 };
 
 // Four output values at element offset off: fp32, or bf16 into out16.
@@ -188,6 +198,24 @@ __device__ __forceinline__ bool mask_vec(const float* mask, int64_t mask_ld) {
   return (mask_ld & 3) == 0 && (reinterpret_cast<uintptr_t>(mask) & 15) == 0;
 }
 
+// The live tiles of a row block (the bits of its map words).
+__device__ __forceinline__ int live_tiles(const uint32_t* tmap, int words) {
+  int n = 0;
+  for (int w = 0; w < words; ++w) n += __builtin_popcount(tmap[w]);
+  return n;
+}
+
+// The first live tile after t of a row block's map (tiles: none).
+__device__ __forceinline__ int next_live_tile(const uint32_t* tmap, int tiles, int t) {
+  int u = t + 1;
+  while (u < tiles) {
+    const uint32_t w = tmap[u >> 5] >> (u & 31);
+    if (w != 0) return u + __builtin_ctz(w);
+    u = (u | 31) + 1;
+  }
+  return tiles;
+}
+
 template <int HD, Bias kBias>
 __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const AttnArgs a) {
   constexpr int kThreads = 64 * waves_of<kBias>();
@@ -207,8 +235,11 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hl = lane >> 5, c = lane & 31;
   const int64_t slice = blockIdx.y;
-  // with a mask, the last row blocks first (under a causal mask the longest walks)
-  const int rblk = kBias == Bias::kMask ? static_cast<int>(gridDim.x - 1 - blockIdx.x) : static_cast<int>(blockIdx.x);
+  // with a mask, the last row blocks first (under a causal mask the longest
+  // walks); with a map, workgroup x is (row block, run)
+  const int run = kBias == Bias::kMask ? static_cast<int>(blockIdx.x) % a.runs : 0;
+  const int rblk = kBias == Bias::kMask ? static_cast<int>(gridDim.x / a.runs - 1 - blockIdx.x / a.runs)
+                                        : static_cast<int>(blockIdx.x);
   const int q0 = rblk * kQueriesPerBlock + wave * kQueriesPerWave;
   const int qrow = q0 + c;
   const bool qin = qrow < a.rows;
@@ -216,9 +247,35 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   const float* kb = a.k + slice_at(a, slice, a.sk, a.ik);
   const float* vb = a.v + slice_at(a, slice, a.sv, a.iv);
 
+  // the tiles this workgroup walks: every one, or with a map the live tiles
+  // of its run (uniform: scalar reads)
+  const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
+  const bool mapped = kBias == Bias::kMask && a.map != nullptr;
+  const uint32_t* tmap = mapped ? a.map + static_cast<int64_t>(rblk) * a.map_words : nullptr;
+  const int64_t orow = slice_at(a, slice, a.so, a.io) + static_cast<int64_t>(qrow) * a.ldo;
+  int first = 0, block_runs = 1;
+  if (mapped) {
+    const int live = live_tiles(tmap, a.map_words);
+    block_runs = (live + a.run_tiles - 1) / a.run_tiles;
+    if (live == 0) {  // no key attended by any row of the block: zeros
+      if (run == 0 && qin) {
+#pragma unroll
+        for (int d = 4 * hl; d < HD; d += 8) store4(a, orow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+      }
+      return;
+    }
+    if (run >= block_runs) return;  // uniform, before any barrier
+    first = -1;
+    for (int skip = run * a.run_tiles; skip >= 0; --skip) first = next_live_tile(tmap, tiles, first);
+  }
+  // the tile after t (i: t's place in the run), or tiles
+  auto after = [&](int t, int i) {
+    return mapped ? (i + 1 < a.run_tiles ? next_live_tile(tmap, tiles, t) : tiles) : t + 1;
+  };
+
   // the first tile's loads go out first
   float4 kr[T::kPerThread], vr[T::kPerThread];
-  load_tile<HD, kThreads>(a, kb, vb, 0, kr, vr);
+  load_tile<HD, kThreads>(a, kb, vb, first * kKeyTile, kr, vr);
 
   // this lane's half of its query row
   float qv[kHalf];
@@ -291,7 +348,6 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     for (int r = 0; r < 16; ++r) o[b][r] = 0.0f;
   }
   float m = -INFINITY, l = 0.0f;
-  const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
   // With a mask, this wave's 32 x 32 block of it (register r: key 8 (r / 4)
   // + 4 h + r % 4 of the tile; -inf past the keys or the rows), read a tile
   // ahead: where every entry is -inf (a causal or routed mask's dead tiles)
@@ -320,12 +376,13 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
       }
     }
   };
-  load_mask(0, mk);
-  for (int t = 0; t < tiles; ++t) {
+  load_mask(first, mk);
+  for (int t = first, i = 0; t < tiles; ++i) {
     const int key0 = t * kKeyTile;
-    const bool more = t + 1 < tiles;
-    if (more) load_tile<HD, kThreads>(a, kb, vb, key0 + kKeyTile, kr, vr);
-    load_mask(more ? t + 1 : t, mn);
+    const int nxt = after(t, i);
+    const bool more = nxt < tiles;
+    if (more) load_tile<HD, kThreads>(a, kb, vb, nxt * kKeyTile, kr, vr);
+    load_mask(more ? nxt : t, mn);
 
     // A wave whose rows all lie past the last query row (the tail workgroup
     // of a slice) only helps stage the tiles.
@@ -457,11 +514,27 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
 #pragma unroll
       for (int r = 0; r < 16; ++r) mk[r] = mn[r];
     }
+    t = nxt;
   }
 
   if (!qin) return;
+  if (mapped && block_runs > 1) {
+    // the run's partial record: (m, l) (lane half 0) and O unnormalised
+    const int row_blocks = static_cast<int>(gridDim.x) / a.runs;
+    const int64_t rec = ((slice * row_blocks + rblk) * a.runs + run) * kQueriesPerBlock + (qrow - rblk * kQueriesPerBlock);
+    if (hl == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * rec) = make_float2(m, l);
+#pragma unroll
+    for (int b = 0; b < kDBlocks; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * b + 8 * g + 4 * hl;
+        *reinterpret_cast<float4*>(a.part_o + rec * HD + d) =
+            make_float4(o[b][4 * g], o[b][4 * g + 1], o[b][4 * g + 2], o[b][4 * g + 3]);
+      }
+    }
+    return;
+  }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  const int64_t orow = slice_at(a, slice, a.so, a.io) + qrow * a.ldo;
 #pragma unroll
   for (int b = 0; b < kDBlocks; ++b) {
 #pragma unroll
@@ -994,13 +1067,6 @@ struct X3Partials {
   float* ml;     // [slices][row blocks][chunks][128 rows][2]: m, l
 };
 
-// The live tiles of a row block (the bits of its map words).
-__device__ __forceinline__ int live_tiles(const uint32_t* tmap, int words) {
-  int n = 0;
-  for (int w = 0; w < words; ++w) n += __builtin_popcount(tmap[w]);
-  return n;
-}
-
 template <int HD>
 __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const uint32_t* __restrict__ map, int words,
                                                        int row_blocks, int slices, X3Partials part) {
@@ -1268,14 +1334,15 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
   }
 }
 
-// The rows of row blocks walked in several runs: out = sum_j 2^(m_j - M) O_j
-// / sum_j 2^(m_j - M) l_j with M the largest m_j (a run where the row saw
+// The rows of row blocks walked in several runs: out = sum_j 2^(u (m_j - M))
+// O_j / sum_j 2^(u (m_j - M)) l_j with M the largest m_j and u the records'
+// unit (1: m in log2 units; log2(e): natural units) (a run where the row saw
 // no finite score holds m = -inf, l = 0, O = 0 and weighs 0; no finite
 // score at all: zeros), into bf16. Workgroup (row block, slice); thread:
 // row tid / 2, dimensions (tid % 2) hd / 2 .. + hd / 2 - 1.
 template <int HD>
 __global__ __launch_bounds__(256) void x3m_merge_k(const AttnArgs a, const uint32_t* __restrict__ map, int words,
-                                                   int row_blocks, X3Partials part) {
+                                                   int row_blocks, X3Partials part, float unit) {
   constexpr int kHalf = HD / 2;
   const int rb = blockIdx.x;
   const int64_t slice = blockIdx.y;
@@ -1296,7 +1363,7 @@ __global__ __launch_bounds__(256) void x3m_merge_k(const AttnArgs a, const uint3
   for (int j = 0; j < runs; ++j) {
     const int64_t rec = rec0 + j * kMaskRowBlock;
     const float2 ml = *reinterpret_cast<const float2*>(part.ml + 2 * rec);
-    const float wgt = __builtin_amdgcn_exp2f(ml.x - ref);  // 0 for m = -inf
+    const float wgt = __builtin_amdgcn_exp2f((ml.x - ref) * unit);  // 0 for m = -inf
     total += wgt * ml.y;
     const float* src = part.o + rec * HD + d0;
 #pragma unroll
@@ -1796,19 +1863,18 @@ int64_t mask_map_floats(int64_t rows, int64_t keys) {
   return (rows + kMaskRowBlock - 1) / kMaskRowBlock * mask_map_words(keys);
 }
 int64_t masked_tiles_offset(int64_t rows, int64_t keys) { return (mask_map_floats(rows, keys) + 63) / 64 * 64; }
-// Live tiles per workgroup: every live tile of a row block, unless the row
-// blocks of all slices fill fewer than the slots of two workgroups per CU
-// (256 CUs); then a row block's walk is cut into runs of at most the tiles
-// one slot would get if every tile were live (at least 32), so that the
-// longest walks of a causal mask no longer set the time. Then the runs per
+// Live tiles per workgroup: at most the tiles one of 512 slots (two
+// workgroups on each of 256 CUs) would get if every tile of every row block
+// were live, and at least 32; a row block with more live tiles has its walk
+// cut into runs, so that the longest walks of a causal mask no longer set
+// the time (row blocks enough to fill the slots: no cut). Then the runs per
 // row block, and the partial records (O, then m and l) after the split tiles.
 constexpr int64_t kSlots = 2 * 256;
 constexpr int64_t kMinRunTiles = 32;
 int64_t masked_run_tiles(int64_t slices, int64_t rows, int64_t keys) {
   const int64_t tiles = (keys + kKeyTile - 1) / kKeyTile;
   const int64_t blocks = slices * ((rows + kMaskRowBlock - 1) / kMaskRowBlock);
-  if (blocks >= kSlots) return tiles;
-  const int64_t share = (tiles * blocks + kSlots - 1) / kSlots;
+  const int64_t share = (tiles * blocks + kSlots - 1) / kSlots;  // >= tiles: no run is cut
   return share > kMinRunTiles ? share : kMinRunTiles;
 }
 int64_t masked_runs(int64_t slices, int64_t rows, int64_t keys) {
@@ -1824,6 +1890,73 @@ int64_t masked_partial_rows(int64_t slices, int64_t rows, int64_t keys) {
 }
 int64_t masked_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
   return masked_partials_offset(slices, rows, keys, hd) + masked_partial_rows(slices, rows, keys) * (hd + 2);
+}
+
+// The fp32 masked attention with a workspace: the tile map, then the runs'
+// partial records (runs sized as for the split-operand kernel).
+int64_t fp32_partial_rows(int64_t slices, int64_t rows, int64_t keys) {
+  const int64_t runs = masked_runs(slices, rows, keys);
+  return runs > 1 ? slices * ((rows + kMaskRowBlock - 1) / kMaskRowBlock) * runs * kMaskRowBlock : 0;
+}
+int64_t fp32_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
+  return masked_tiles_offset(rows, keys) + fp32_partial_rows(slices, rows, keys) * (hd + 2);
+}
+
+int masked_fp32_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                      int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo,
+                      int64_t so, int64_t slices, int64_t rows, int64_t keys, int64_t hd, float scale,
+                      const float* mask, int64_t mask_ld, float* workspace, int64_t workspace_floats,
+                      uint16_t* out16) {
+  if (mask == nullptr) {
+    return attention_entry(what, stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, rows, keys, hd,
+                           scale, mask, mask_ld, out16);
+  }
+  if (const int st = check_common(what, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices, rows, keys, hd)) {
+    return st;
+  }
+  UOCR_REQUIRE(mask_ld >= keys, what, "mask rows must hold every key");
+  const int64_t row_blocks = (rows + kMaskRowBlock - 1) / kMaskRowBlock, words = mask_map_words(keys);
+  UOCR_REQUIRE(row_blocks < 65536 && slices < 65536, what, "need rows < 2^23");
+  UOCR_REQUIRE(workspace != nullptr && aligned16(workspace) &&
+                   workspace_floats >= fp32_workspace_floats(slices, rows, keys, hd),
+               what, "workspace: 16-byte aligned, uocr_rocm_attention_workspace_floats floats");
+  AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
+             scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 1, 0, 0, 0, 0, out16};
+  if (out16 != nullptr) a.out = nullptr;
+  const int64_t runs = masked_runs(slices, rows, keys);
+  uint32_t* map = reinterpret_cast<uint32_t*>(workspace);
+  a.map = map;
+  a.map_words = static_cast<int>(words);
+  a.run_tiles = static_cast<int>(masked_run_tiles(slices, rows, keys));
+  a.runs = static_cast<int>(runs);
+  float* po = workspace + masked_tiles_offset(rows, keys);
+  a.part_o = runs > 1 ? po : nullptr;
+  a.part_ml = runs > 1 ? po + fp32_partial_rows(slices, rows, keys) * hd : nullptr;
+  UOCR_REQUIRE(row_blocks * runs < (int64_t{1} << 31), what, "too many workgroups");
+  clear_launch_error();
+  mask_tiles_k<<<dim3(static_cast<unsigned>(words), static_cast<unsigned>(row_blocks)), 256, 0, as_stream(stream)>>>(
+      mask, mask_ld, static_cast<int>(rows), static_cast<int>(keys), map, static_cast<int>(words));
+  if (const int st = check_launch(what)) return st;
+  const dim3 grid(static_cast<unsigned>(row_blocks * runs), static_cast<unsigned>(slices));
+  clear_launch_error();
+  if (hd == 64) {
+    attention_k<64, Bias::kMask><<<grid, 256, 0, as_stream(stream)>>>(a);
+  } else {
+    attention_k<128, Bias::kMask><<<grid, 256, 0, as_stream(stream)>>>(a);
+  }
+  if (runs == 1) return check_launch(what);
+  if (const int st = check_launch(what)) return st;
+  X3Partials part{a.run_tiles, a.runs, a.part_o, a.part_ml};
+  const dim3 merge_grid(static_cast<unsigned>(row_blocks), static_cast<unsigned>(slices));
+  clear_launch_error();
+  if (hd == 64) {
+    x3m_merge_k<64><<<merge_grid, 256, 0, as_stream(stream)>>>(a, map, static_cast<int>(words),
+                                                               static_cast<int>(row_blocks), part, kLog2e);
+  } else {
+    x3m_merge_k<128><<<merge_grid, 256, 0, as_stream(stream)>>>(a, map, static_cast<int>(words),
+                                                                static_cast<int>(row_blocks), part, kLog2e);
+  }
+  return check_launch(what);
 }
 
 int masked_split_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
@@ -1876,9 +2009,9 @@ int masked_split_entry(const char* what, void* stream, const float* q, int64_t l
   const dim3 merge_grid(static_cast<unsigned>(row_blocks), static_cast<unsigned>(slices));
   clear_launch_error();
   if (hd == 64) {
-    x3m_merge_k<64><<<merge_grid, 256, 0, as_stream(stream)>>>(a, map, w, rbs, part);
+    x3m_merge_k<64><<<merge_grid, 256, 0, as_stream(stream)>>>(a, map, w, rbs, part, 1.0f);
   } else {
-    x3m_merge_k<128><<<merge_grid, 256, 0, as_stream(stream)>>>(a, map, w, rbs, part);
+    x3m_merge_k<128><<<merge_grid, 256, 0, as_stream(stream)>>>(a, map, w, rbs, part, 1.0f);
   }
   return check_launch(what);
 }
@@ -1904,6 +2037,28 @@ int uocr_rocm_attention_bf16(void* stream, const float* q, int64_t ldq, int64_t 
                              const float* mask, int64_t mask_ld) {
   return attention_entry("uocr_rocm_attention_bf16", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv,
                          reinterpret_cast<float*>(out), ldo, so, slices, rows, keys, hd, scale, mask, mask_ld, out);
+}
+
+int64_t uocr_rocm_attention_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
+  if (slices < 1 || rows < 1 || keys < 1 || (hd != 64 && hd != 128)) return 0;
+  return fp32_workspace_floats(slices, rows, keys, hd);
+}
+
+int uocr_rocm_attention_ws(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
+                           int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out, int64_t ldo, int64_t so,
+                           int64_t slices, int64_t rows, int64_t keys, int64_t hd, float scale, const float* mask,
+                           int64_t mask_ld, float* workspace, int64_t workspace_floats) {
+  return masked_fp32_entry("uocr_rocm_attention_ws", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv, out, ldo, so, slices,
+                           rows, keys, hd, scale, mask, mask_ld, workspace, workspace_floats, nullptr);
+}
+
+int uocr_rocm_attention_bf16_ws(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k, int64_t ldk,
+                                int64_t sk, const float* v, int64_t ldv, int64_t sv, uint16_t* out, int64_t ldo,
+                                int64_t so, int64_t slices, int64_t rows, int64_t keys, int64_t hd, float scale,
+                                const float* mask, int64_t mask_ld, float* workspace, int64_t workspace_floats) {
+  return masked_fp32_entry("uocr_rocm_attention_bf16_ws", stream, q, ldq, sq, k, ldk, sk, v, ldv, sv,
+                           reinterpret_cast<float*>(out), ldo, so, slices, rows, keys, hd, scale, mask, mask_ld,
+                           workspace, workspace_floats, out);
 }
 
 int64_t uocr_rocm_attention_masked_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {

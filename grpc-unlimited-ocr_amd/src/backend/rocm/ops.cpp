@@ -235,6 +235,17 @@ void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t w
                                                     scale, rh, rw, workspace, workspace_floats));
 }
 
+std::int64_t attention_workspace_floats(std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd) {
+  return uocr_rocm_attention_workspace_floats(slices, rows, keys, hd);
+}
+
+void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, std::uint16_t* out, std::int64_t ldo,
+               std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
+               const float* mask, std::int64_t mask_ld, float* workspace, std::int64_t workspace_floats) {
+  check(uocr_rocm_attention_bf16_ws(ctx.stream(), q.p, q.ld, q.slice, k.p, k.ld, k.slice, v.p, v.ld, v.slice, out, ldo,
+                                    so, slices, rows, keys, hd, scale, mask, mask_ld, workspace, workspace_floats));
+}
+
 std::int64_t attention_masked_workspace_floats(std::int64_t slices, std::int64_t rows, std::int64_t keys,
                                                std::int64_t hd) {
   return uocr_rocm_attention_masked_workspace_floats(slices, rows, keys, hd);

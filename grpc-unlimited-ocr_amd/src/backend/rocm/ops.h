@@ -186,6 +186,14 @@ void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOpe
 void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, std::uint16_t* out, std::int64_t ldo,
                std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
                const float* mask, std::int64_t mask_ld);
+// New: attention with a mask and a workspace of
+// attention_workspace_floats(slices, rows, keys, hd) floats: the mask's live
+// tiles walked alone, long walks cut into runs merged by a last launch;
+// fp32 products, the bf16 output bitwise the fp32 one rounded.
+std::int64_t attention_workspace_floats(std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd);
+void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, std::uint16_t* out, std::int64_t ldo,
+               std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
+               const float* mask, std::int64_t mask_ld, float* workspace, std::int64_t workspace_floats);
 // New: attention with a mask into bf16 on the bf16 matrix cores with split
 // operands, walking only the key tiles the mask leaves live; the workspace
 // holds attention_masked_workspace_floats(slices, rows, keys, hd) floats.

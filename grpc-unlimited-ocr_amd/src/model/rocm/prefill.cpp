@@ -81,10 +81,12 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
   const bool one_pass = hd == 64 || hd == 128;
   const bool split = one_pass && d.split_attention;
   Array mask = f32(rows * keys), scores = f32(one_pass ? 1 : d.heads * rows * keys);
-  Array merged = f32(split ? 1 : rows * W);
-  // the split-operand attention's bf16 output rows (the o projection's input) and workspace
-  Array attn_b(ctx_, DType::kBF16, split ? rows * W : 1);
-  const std::int64_t attn_ws_floats = split ? attention_masked_workspace_floats(d.heads, rows, keys, hd) : 1;
+  Array merged = f32(one_pass ? 1 : rows * W);
+  // the one-pass attention's bf16 output rows (the o projection's input) and workspace
+  Array attn_b(ctx_, DType::kBF16, one_pass ? rows * W : 1);
+  const std::int64_t attn_ws_floats = !one_pass ? 1
+                                      : split   ? attention_masked_workspace_floats(d.heads, rows, keys, hd)
+                                                : attention_workspace_floats(d.heads, rows, keys, hd);
   Array attn_ws = f32(attn_ws_floats);
   // Over a bf16 cache: the new keys and values in fp32 before they are
   // rounded into the cache, and every key and value the prompt attends to
@@ -162,18 +164,19 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
       attention_masked(ctx_, {q.f32(), W, hd}, {k_all, W, hd}, {v_all, W, hd}, attn_b.bf16(), W, hd, d.heads, rows,
                        keys, hd, scale, mask.f32(), keys, attn_ws.f32(), attn_ws_floats);
       linear_bf16x(ctx_, attn_b.bf16(), rows, W, l.o, H, nullptr, delta.f32());
+    } else if (one_pass) {
+      // scores, mask, softmax and values in one pass on the fp32 matrix
+      // cores, each head's columns read in place, only the key tiles the
+      // mask leaves live, the output rounded to bf16 as the o projection
+      // takes it
+      attention(ctx_, {q.f32(), W, hd}, {k_all, W, hd}, {v_all, W, hd}, attn_b.bf16(), W, hd, d.heads, rows, keys, hd,
+                scale, mask.f32(), keys, attn_ws.f32(), attn_ws_floats);
+      linear_bf16x(ctx_, attn_b.bf16(), rows, W, l.o, H, nullptr, delta.f32());
     } else {
-      if (one_pass) {
-        // scores, mask, softmax and values in one pass on the fp32 matrix
-        // cores, each head's columns read in place
-        attention(ctx_, {q.f32(), W, hd}, {k_all, W, hd}, {v_all, W, hd}, merged.f32(), W, hd, d.heads, rows, keys,
-                  hd, scale, mask.f32(), keys);
-      } else {
-        gemm_nt(ctx_, rows, keys, hd, scale, q.f32(), W, hd, k_all, W, hd, scores.f32(), keys, rows * keys, d.heads);
-        scale_add_mask(ctx_, scores.f32(), 1.0f, mask.f32(), d.heads, rows, keys);
-        softmax_rows(ctx_, scores.f32(), d.heads * rows, keys);
-        gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_all, W, hd, merged.f32(), W, hd, d.heads);
-      }
+      gemm_nt(ctx_, rows, keys, hd, scale, q.f32(), W, hd, k_all, W, hd, scores.f32(), keys, rows * keys, d.heads);
+      scale_add_mask(ctx_, scores.f32(), 1.0f, mask.f32(), d.heads, rows, keys);
+      softmax_rows(ctx_, scores.f32(), d.heads * rows, keys);
+      gemm_nn(ctx_, rows, hd, keys, scores.f32(), keys, rows * keys, v_all, W, hd, merged.f32(), W, hd, d.heads);
       const Array mb = rounded(ctx_, merged.f32(), rows * W);
       linear_bf16x(ctx_, mb.bf16(), rows, W, l.o, H, nullptr, delta.f32());
     }

@@ -517,6 +517,27 @@ UOCR_ROCM_API int uocr_rocm_attention_bf16(void* stream, const float* q, int64_t
                                            uint16_t* out, int64_t ldo, int64_t so, int64_t slices, int64_t rows,
                                            int64_t keys, int64_t hd, float scale, const float* mask,
                                            int64_t mask_ld);
+/* New: uocr_rocm_attention and uocr_rocm_attention_bf16 with a workspace
+ * (uocr_rocm_attention_workspace_floats(slices, rows, keys, hd) floats,
+ * 16-byte aligned) for a mask: a first launch marks, per 128 query rows,
+ * the 32-key tiles where some mask entry is finite, and the fp32 products
+ * walk only those; where the row blocks of all slices leave CUs idle, a
+ * block's walk is cut into runs whose (max, total, values) records a last
+ * launch combines, so a causal mask's longest walks no longer set the time.
+ * fp32 arithmetic throughout (the sums of a cut row in another order); the
+ * bf16 entry is bitwise the fp32 one then uocr_rocm_round_bf16. A null mask
+ * takes the entries above (the workspace unused). */
+UOCR_ROCM_API int64_t uocr_rocm_attention_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd);
+UOCR_ROCM_API int uocr_rocm_attention_ws(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                                         int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv, float* out,
+                                         int64_t ldo, int64_t so, int64_t slices, int64_t rows, int64_t keys,
+                                         int64_t hd, float scale, const float* mask, int64_t mask_ld,
+                                         float* workspace, int64_t workspace_floats);
+UOCR_ROCM_API int uocr_rocm_attention_bf16_ws(void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
+                                              int64_t ldk, int64_t sk, const float* v, int64_t ldv, int64_t sv,
+                                              uint16_t* out, int64_t ldo, int64_t so, int64_t slices, int64_t rows,
+                                              int64_t keys, int64_t hd, float scale, const float* mask,
+                                              int64_t mask_ld, float* workspace, int64_t workspace_floats);
 /* New: uocr_rocm_attention_bf16 with a mask, on the bf16 matrix cores with
  * each fp32 operand split into bf16 hi + lo parts (a . b = lo_a hi_b +
  * hi_a lo_b + hi_a hi_b in fp32: about 2^-16 of each product dropped, far

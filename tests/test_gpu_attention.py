@@ -262,6 +262,59 @@ def _routed_mask(rows, keys, seed):
     return mask
 
 
+def _test_mask(kind, rows, keys):
+    """random: 30% -inf entries, a causal edge, a row with no live key and a
+    row whose one live key ends the last tile; dead: the first 128 rows with
+    no live key; causal; routed (_routed_mask)."""
+    g = np.random.default_rng(773)
+    if kind == "random" or kind == "dead":
+        mask = np.where(g.random((rows, keys)) < 0.3, -np.inf, 0.1 * g.standard_normal((rows, keys)))
+        mask = mask.astype(np.float32)
+        if kind == "dead":
+            mask[:128] = -np.inf
+        else:
+            for t in range(rows):
+                mask[t, max(1, keys - rows - 50 + t):] = -np.inf
+            mask[0, :] = -np.inf
+            if rows > 8:
+                mask[8, :] = -np.inf
+                mask[8, keys - 1] = 0.0
+        return mask
+    if kind == "causal":
+        return np.triu(np.full((rows, keys), -np.inf, np.float32), 1 + keys - rows)
+    return _routed_mask(rows, keys, 774)
+
+
+@pytest.mark.parametrize("slices,rows,keys,hd,kind", [(3, 100, 300, 128, "random"), (2, 150, 3000, 64, "random"),
+                                                      (4, 300, 1100, 128, "routed"), (1, 200, 64, 128, "dead"),
+                                                      (2, 257, 257, 64, "causal"), (2, 130, 2500, 128, "causal")])
+def test_attention_with_a_workspace(backend, slices, rows, keys, hd, kind):
+    """uocr_rocm_attention_ws / _bf16_ws: the fp32 one-pass attention over a
+    mask walking only the tiles its row blocks attend (a first row block
+    with no live key: zeros), few row blocks over many keys (1100, 2500,
+    3000) cut into runs whose records a merge launch combines: the oracle at
+    the fp32 bar, and the bf16 entry bitwise the fp32 one rounded."""
+    q, k, v = normal(780 + rows, (slices, rows, hd)), normal(781 + keys, (slices, keys, hd)), normal(782, (slices, keys, hd))
+    mask = _test_mask(kind, rows, keys)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    qd, kd, vd, md = dev_f32(q), dev_f32(k), dev_f32(v), dev_f32(mask)
+    ws = torch.empty(backend.attention_workspace_floats(slices, rows, keys, hd), device="cuda")
+    out = torch.full((slices, rows, hd), float("nan"), device="cuda")
+    backend.attention(qd, kd, vd, out, slices, rows, keys, hd, scale, md, workspace=ws)
+    want16 = torch.empty(slices, rows, hd, dtype=torch.bfloat16, device="cuda")
+    backend.round_bf16(out, want16)
+    got16 = torch.full((slices, rows, hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+    backend.attention(qd, kd, vd, got16, slices, rows, keys, hd, scale, md, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(got16.view(torch.int16), want16.view(torch.int16))
+    got = host_f32(out)
+    dead = ~np.isfinite(mask).any(axis=1)
+    assert np.array_equal(got[:, dead], np.zeros_like(got[:, dead]))
+    assert_f32_close(got, reference(q, k, v, scale, mask), 1e-5, f"attention with a workspace, {kind} mask")
+    with pytest.raises(ValueError):  # a workspace one float short
+        backend.attention(qd, kd, vd, out, slices, rows, keys, hd, scale, md, workspace=ws[:-1])
+
+
 @pytest.mark.parametrize("slices,rows,keys,hd,kind,amp", [(3, 100, 300, 128, "random", 1.0),
                                                           (2, 257, 257, 64, "causal", 1.0),
                                                           (4, 300, 1100, 128, "routed", 1.0),
@@ -286,23 +339,7 @@ def test_attention_masked_split_operands(backend, slices, rows, keys, hd, kind, 
     the oracle's alone at 2^-6."""
     q = normal(770 + rows, (slices, rows, hd)) * np.float32(amp)
     k, v = normal(771 + keys, (slices, keys, hd)), normal(772, (slices, keys, hd))
-    g = np.random.default_rng(773)
-    if kind == "random" or kind == "dead":
-        mask = np.where(g.random((rows, keys)) < 0.3, -np.inf, 0.1 * g.standard_normal((rows, keys)))
-        mask = mask.astype(np.float32)
-        if kind == "dead":
-            mask[:128] = -np.inf
-        else:
-            for t in range(rows):
-                mask[t, max(1, keys - rows - 50 + t):] = -np.inf
-            mask[0, :] = -np.inf
-            if rows > 8:
-                mask[8, :] = -np.inf
-                mask[8, keys - 1] = 0.0
-    elif kind == "causal":
-        mask = np.triu(np.full((rows, keys), -np.inf, np.float32), 1 + keys - rows)
-    else:
-        mask = _routed_mask(rows, keys, 774)
+    mask = _test_mask(kind, rows, keys)
     scale = float(np.float32(1 / np.sqrt(hd)))
     qd, kd, vd, md = dev_f32(q), dev_f32(k), dev_f32(v), dev_f32(mask)
     out = torch.empty(slices, rows, hd, device="cuda")
