@@ -149,10 +149,10 @@ int library_linear_bf16(const char* what, hipStream_t s, const uint16_t* x, int6
         float best = 0.0f;
         for (int i = 0; i < count; ++i) {
           if (run(h, p, found[i].algo, x, w, y, s) != HIPBLAS_STATUS_SUCCESS) continue;
-          hipEventRecord(e0, s);
+          if (hipEventRecord(e0, s) != hipSuccess) continue;
           run(h, p, found[i].algo, x, w, y, s);
           run(h, p, found[i].algo, x, w, y, s);
-          hipEventRecord(e1, s);
+          if (hipEventRecord(e1, s) != hipSuccess) continue;
           float ms = 0.0f;
           if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
           if (best == 0.0f || ms < best) {
@@ -161,8 +161,8 @@ int library_linear_bf16(const char* what, hipStream_t s, const uint16_t* x, int6
           }
         }
       }
-      if (e0 != nullptr) hipEventDestroy(e0);
-      if (e1 != nullptr) hipEventDestroy(e1);
+      if (e0 != nullptr) (void)hipEventDestroy(e0);
+      if (e1 != nullptr) (void)hipEventDestroy(e1);
     }
     it = lib.plans.emplace(key, p).first;
   }
