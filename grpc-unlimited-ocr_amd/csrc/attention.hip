@@ -260,7 +260,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     if (live == 0) {  // no key attended by any row of the block: zeros
       if (run == 0 && qin) {
 #pragma unroll
-        for (int d = 4 * hl; d < HD; d += 8) store4(a, orow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+        for (int e = 0; e < HD / 8; ++e) store4(a, orow + 8 * e + 4 * hl, 0.0f, 0.0f, 0.0f, 0.0f);
       }
       return;
     }
@@ -1116,7 +1116,7 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
   if (live == 0) {  // no key attended by any row of the block: zeros
     if (run == 0 && qin) {
 #pragma unroll
-      for (int d = 4 * hl; d < HD; d += 8) store4(a, orow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+      for (int e = 0; e < HD / 8; ++e) store4(a, orow + 8 * e + 4 * hl, 0.0f, 0.0f, 0.0f, 0.0f);
     }
     return;
   }
