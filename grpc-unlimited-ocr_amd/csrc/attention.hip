@@ -135,6 +135,7 @@ struct Tile {
   static constexpr int kChunks = kKeyTile * HD / 4;           // float4 chunks of one operand tile
   static constexpr int kPerThread = kChunks / kThreads;       // 2 to 8
   static constexpr int kKStride = HD + 4;                     // padded K rows: 16-lane reads conflict-free
+  static constexpr int kVTStride = kKeyTile + 4;              // V^T rows (a dimension's 32 keys): 9 16-byte groups
 };
 
 template <int HD, int kThreads>
@@ -163,7 +164,12 @@ __device__ __forceinline__ void store_tile(float* ks, float* vs, const float4 (&
     const int idx = static_cast<int>(threadIdx.x) + kThreads * j;
     const int row = idx / (HD / 4), c4 = idx % (HD / 4);
     *reinterpret_cast<float4*>(ks + row * Tile<HD, kThreads>::kKStride + 4 * c4) = kr[j];
-    *reinterpret_cast<float4*>(vs + row * HD + 4 * c4) = vr[j];
+    // V transposed: the values' product reads 4 keys of a dimension at once
+    float* vt = vs + 4 * c4 * Tile<HD, kThreads>::kVTStride + row;
+    vt[0] = vr[j].x;
+    vt[Tile<HD, kThreads>::kVTStride] = vr[j].y;
+    vt[2 * Tile<HD, kThreads>::kVTStride] = vr[j].z;
+    vt[3 * Tile<HD, kThreads>::kVTStride] = vr[j].w;
   }
 }
 
@@ -205,11 +211,23 @@ __device__ __forceinline__ int live_tiles(const uint32_t* tmap, int words) {
   return n;
 }
 
-// The first live tile after t of a row block's map (tiles: none).
-__device__ __forceinline__ int next_live_tile(const uint32_t* tmap, int tiles, int t) {
+// A walk over a row block's map: the word last read is kept, so a walk
+// reads each word once (a scalar load per 32 tiles, not per tile).
+struct MapCursor {
+  const uint32_t* words;
+  int idx;
+  uint32_t w;
+};
+
+// The first live tile after t (tiles: none).
+__device__ __forceinline__ int next_live_tile(MapCursor& m, int tiles, int t) {
   int u = t + 1;
   while (u < tiles) {
-    const uint32_t w = tmap[u >> 5] >> (u & 31);
+    if ((u >> 5) != m.idx) {
+      m.idx = u >> 5;
+      m.w = m.words[m.idx];
+    }
+    const uint32_t w = m.w >> (u & 31);
     if (w != 0) return u + __builtin_ctz(w);
     u = (u | 31) + 1;
   }
@@ -224,7 +242,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   constexpr int kHalf = HD / 2;  // columns per lane half in the scores' products
   constexpr int kDBlocks = HD / 32;
   __shared__ __attribute__((aligned(16))) float ks[kKeyTile * T::kKStride];
-  __shared__ __attribute__((aligned(16))) float vs[kKeyTile * HD];
+  __shared__ __attribute__((aligned(16))) float vs[HD * T::kVTStride];  // V^T
   // The relative-position bias: per query row its h height terms at 0 and
   // w width terms at dw_off, rows dots_ld apart: h + w + 1 (odd) for
   // kRelPos, so that the 32 queries of a wave read 32 different banks; for
@@ -252,6 +270,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
   const bool mapped = kBias == Bias::kMask && a.map != nullptr;
   const uint32_t* tmap = mapped ? a.map + static_cast<int64_t>(rblk) * a.map_words : nullptr;
+  MapCursor cursor{tmap, -1, 0u};
   const int64_t orow = slice_at(a, slice, a.so, a.io) + static_cast<int64_t>(qrow) * a.ldo;
   int first = 0, block_runs = 1;
   if (mapped) {
@@ -266,11 +285,11 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     }
     if (run >= block_runs) return;  // uniform, before any barrier
     first = -1;
-    for (int skip = run * a.run_tiles; skip >= 0; --skip) first = next_live_tile(tmap, tiles, first);
+    for (int skip = run * a.run_tiles; skip >= 0; --skip) first = next_live_tile(cursor, tiles, first);
   }
   // the tile after t (i: t's place in the run), or tiles
   auto after = [&](int t, int i) {
-    return mapped ? (i + 1 < a.run_tiles ? next_live_tile(tmap, tiles, t) : tiles) : t + 1;
+    return mapped ? (i + 1 < a.run_tiles ? next_live_tile(cursor, tiles, t) : tiles) : t + 1;
   };
 
   // the first tile's loads go out first
@@ -494,13 +513,18 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
         }
       }
 
-      // O^T += V^T P^T: product i sums keys 8 (i / 4) + i % 4 + 4 h, held in s[i]
+      // O^T += V^T P^T: product i = 4 g + e sums keys 8 g + 4 h + e, held
+      // in s[i]; the lane's four values of dimension 32 b + c for keys 8 g
+      // + 4 h .. + 3 are one 16-byte read of its V^T row
 #pragma unroll
       for (int b = 0; b < kDBlocks; ++b) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = 8 * (i / 4) + 4 * hl + (i % 4);
-          o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * HD + 32 * b + c], s[i], o[b], 0, 0, 0);
+        for (int g = 0; g < 4; ++g) {
+          const float4 vt = *reinterpret_cast<const float4*>(vs + (32 * b + c) * T::kVTStride + 8 * g + 4 * hl);
+          o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt.x, s[4 * g], o[b], 0, 0, 0);
+          o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt.y, s[4 * g + 1], o[b], 0, 0, 0);
+          o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt.z, s[4 * g + 2], o[b], 0, 0, 0);
+          o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt.w, s[4 * g + 3], o[b], 0, 0, 0);
         }
       }
     }
@@ -1102,15 +1126,8 @@ __global__ __launch_bounds__(256) void attention_x3m_k(const AttnArgs a, const u
   // the live tiles of this row block, in order (uniform: scalar reads)
   const uint32_t* tmap = map + static_cast<int64_t>(rb) * words;
   const int tiles = (a.keys + kKeyTile - 1) / kKeyTile;
-  auto next_live = [&](int t) {  // the first live tile after t, or tiles
-    int u = t + 1;
-    while (u < tiles) {
-      const uint32_t w = tmap[u >> 5] >> (u & 31);
-      if (w != 0) return u + __builtin_ctz(w);
-      u = (u | 31) + 1;
-    }
-    return tiles;
-  };
+  MapCursor cursor{tmap, -1, 0u};
+  auto next_live = [&](int t) { return next_live_tile(cursor, tiles, t); };  // the first live tile after t, or tiles
   const int live = live_tiles(tmap, words);
   const int runs = (live + part.chunk - 1) / part.chunk;
   if (live == 0) {  // no key attended by any row of the block: zeros
@@ -1863,7 +1880,7 @@ int64_t mask_map_floats(int64_t rows, int64_t keys) {
   return (rows + kMaskRowBlock - 1) / kMaskRowBlock * mask_map_words(keys);
 }
 int64_t masked_tiles_offset(int64_t rows, int64_t keys) { return (mask_map_floats(rows, keys) + 63) / 64 * 64; }
-// Live tiles per workgroup: at most the tiles one of 512 slots (two
+// Live tiles per workgroup: at most the tiles one of the slots (512: two
 // workgroups on each of 256 CUs) would get if every tile of every row block
 // were live, and at least 32; a row block with more live tiles has its walk
 // cut into runs, so that the longest walks of a causal mask no longer set
@@ -1871,14 +1888,14 @@ int64_t masked_tiles_offset(int64_t rows, int64_t keys) { return (mask_map_float
 // row block, and the partial records (O, then m and l) after the split tiles.
 constexpr int64_t kSlots = 2 * 256;
 constexpr int64_t kMinRunTiles = 32;
-int64_t masked_run_tiles(int64_t slices, int64_t rows, int64_t keys) {
+int64_t masked_run_tiles(int64_t slices, int64_t rows, int64_t keys, int64_t slots = kSlots) {
   const int64_t tiles = (keys + kKeyTile - 1) / kKeyTile;
   const int64_t blocks = slices * ((rows + kMaskRowBlock - 1) / kMaskRowBlock);
-  const int64_t share = (tiles * blocks + kSlots - 1) / kSlots;  // >= tiles: no run is cut
+  const int64_t share = (tiles * blocks + slots - 1) / slots;  // >= tiles: no run is cut
   return share > kMinRunTiles ? share : kMinRunTiles;
 }
-int64_t masked_runs(int64_t slices, int64_t rows, int64_t keys) {
-  const int64_t per = masked_run_tiles(slices, rows, keys);
+int64_t masked_runs(int64_t slices, int64_t rows, int64_t keys, int64_t slots = kSlots) {
+  const int64_t per = masked_run_tiles(slices, rows, keys, slots);
   return ((keys + kKeyTile - 1) / kKeyTile + per - 1) / per;
 }
 int64_t masked_partials_offset(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
@@ -1893,13 +1910,15 @@ int64_t masked_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int6
 }
 
 // The fp32 masked attention with a workspace: the tile map, then the runs'
-// partial records (runs sized as for the split-operand kernel).
-int64_t fp32_partial_rows(int64_t slices, int64_t rows, int64_t keys) {
-  const int64_t runs = masked_runs(slices, rows, keys);
+// partial records. Its head dim 128 holds one 4-wave workgroup per CU (the
+// registers), so 256 slots there; 64 holds two.
+int64_t fp32_slots(int64_t hd) { return hd == 128 ? kSlots / 2 : kSlots; }
+int64_t fp32_partial_rows(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
+  const int64_t runs = masked_runs(slices, rows, keys, fp32_slots(hd));
   return runs > 1 ? slices * ((rows + kMaskRowBlock - 1) / kMaskRowBlock) * runs * kMaskRowBlock : 0;
 }
 int64_t fp32_workspace_floats(int64_t slices, int64_t rows, int64_t keys, int64_t hd) {
-  return masked_tiles_offset(rows, keys) + fp32_partial_rows(slices, rows, keys) * (hd + 2);
+  return masked_tiles_offset(rows, keys) + fp32_partial_rows(slices, rows, keys, hd) * (hd + 2);
 }
 
 int masked_fp32_entry(const char* what, void* stream, const float* q, int64_t ldq, int64_t sq, const float* k,
@@ -1923,15 +1942,15 @@ int masked_fp32_entry(const char* what, void* stream, const float* q, int64_t ld
   AttnArgs a{q, k, v, out, ldq, sq, ldk, sk, ldv, sv, ldo, so, static_cast<int>(rows), static_cast<int>(keys),
              scale, mask, mask_ld, nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 1, 0, 0, 0, 0, out16};
   if (out16 != nullptr) a.out = nullptr;
-  const int64_t runs = masked_runs(slices, rows, keys);
+  const int64_t runs = masked_runs(slices, rows, keys, fp32_slots(hd));
   uint32_t* map = reinterpret_cast<uint32_t*>(workspace);
   a.map = map;
   a.map_words = static_cast<int>(words);
-  a.run_tiles = static_cast<int>(masked_run_tiles(slices, rows, keys));
+  a.run_tiles = static_cast<int>(masked_run_tiles(slices, rows, keys, fp32_slots(hd)));
   a.runs = static_cast<int>(runs);
   float* po = workspace + masked_tiles_offset(rows, keys);
   a.part_o = runs > 1 ? po : nullptr;
-  a.part_ml = runs > 1 ? po + fp32_partial_rows(slices, rows, keys) * hd : nullptr;
+  a.part_ml = runs > 1 ? po + fp32_partial_rows(slices, rows, keys, hd) * hd : nullptr;
   UOCR_REQUIRE(row_blocks * runs < (int64_t{1} << 31), what, "too many workgroups");
   clear_launch_error();
   mask_tiles_k<<<dim3(static_cast<unsigned>(words), static_cast<unsigned>(row_blocks)), 256, 0, as_stream(stream)>>>(
