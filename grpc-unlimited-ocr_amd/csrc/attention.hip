@@ -1013,34 +1013,39 @@ __global__ __launch_bounds__(256) void attention_x3_k(const AttnArgs a) {
 constexpr int kMaskRowBlock = 4 * kQueriesPerWave;  // query rows per workgroup
 constexpr int kMaskMapKeys = 32 * kKeyTile;         // keys per map word (a bit per tile)
 
-// Map word (row block blockIdx.y, word blockIdx.x): bit j set where some
-// entry of rows [128 rb, 128 rb + 128) x keys of tile 32 wd + j is not -inf
-// (NaN counts as live). Thread: keys 4 tid .. 4 tid + 3 of the word's 1024,
-// over every row of the block.
+// Map byte (row block blockIdx.y, byte blockIdx.x of the row block's words):
+// bit j set where some entry of rows [128 rb, 128 rb + 128) x keys of tile
+// 8 blockIdx.x + j is not -inf (NaN counts as live; tiles past the keys
+// clear). Wave w: rows 32 w .. 32 w + 31 of the block; lane: keys 4 lane ..
+// 4 lane + 3 of the byte's 256; the four waves' votes OR'ed in LDS.
 __global__ __launch_bounds__(256) void mask_tiles_k(const float* __restrict__ mask, int64_t mask_ld, int rows,
                                                     int keys, uint32_t* __restrict__ map, int words) {
   __shared__ uint32_t part[4];
-  const int rb = blockIdx.y, wd = blockIdx.x;
+  const int rb = blockIdx.y, byte = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int key4 = kMaskMapKeys * wd + 4 * static_cast<int>(threadIdx.x);
+  const int key4 = 8 * kKeyTile * byte + 4 * lane;
   const bool vec = mask_vec(mask, mask_ld);
   bool any = false;
   if (key4 < keys) {
-    const int r0 = rb * kMaskRowBlock, r1 = min(r0 + kMaskRowBlock, rows);
+    const int r0 = rb * kMaskRowBlock + wave * kQueriesPerWave;
+    const int r1 = min(r0 + kQueriesPerWave, rows);
 #pragma unroll 8
     for (int r = r0; r < r1; ++r) {
       const float4 m = mask4(mask + r * mask_ld, key4, keys, vec);
       any = any || m.x != -INFINITY || m.y != -INFINITY || m.z != -INFINITY || m.w != -INFINITY;
     }
   }
-  // lanes 8 j .. 8 j + 7 of wave w: tile 8 w + j of the word
+  // lanes 8 j .. 8 j + 7: tile j of the byte
   const uint64_t b = __ballot(any);
   uint32_t bits = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) bits |= ((b >> (8 * j)) & 0xffu) != 0 ? (1u << j) : 0u;
-  if (lane == 0) part[wave] = bits << (8 * wave);
+  if (lane == 0) part[wave] = bits;
   __syncthreads();
-  if (threadIdx.x == 0) map[static_cast<int64_t>(rb) * words + wd] = part[0] | part[1] | part[2] | part[3];
+  if (threadIdx.x == 0) {
+    reinterpret_cast<uint8_t*>(map + static_cast<int64_t>(rb) * words)[byte] =
+        static_cast<uint8_t>(part[0] | part[1] | part[2] | part[3]);
+  }
 }
 
 // Key tile t of slice s (blockIdx (t, s)) split once for every workgroup
@@ -1953,7 +1958,8 @@ int masked_fp32_entry(const char* what, void* stream, const float* q, int64_t ld
   a.part_ml = runs > 1 ? po + fp32_partial_rows(slices, rows, keys, hd) * hd : nullptr;
   UOCR_REQUIRE(row_blocks * runs < (int64_t{1} << 31), what, "too many workgroups");
   clear_launch_error();
-  mask_tiles_k<<<dim3(static_cast<unsigned>(words), static_cast<unsigned>(row_blocks)), 256, 0, as_stream(stream)>>>(
+  mask_tiles_k<<<dim3(static_cast<unsigned>(4 * words), static_cast<unsigned>(row_blocks)), 256, 0,
+                 as_stream(stream)>>>(
       mask, mask_ld, static_cast<int>(rows), static_cast<int>(keys), map, static_cast<int>(words));
   if (const int st = check_launch(what)) return st;
   const dim3 grid(static_cast<unsigned>(row_blocks * runs), static_cast<unsigned>(slices));
@@ -1999,7 +2005,8 @@ int masked_split_entry(const char* what, void* stream, const float* q, int64_t l
   uint32_t* map = reinterpret_cast<uint32_t*>(workspace);
   const int64_t tiles = (keys + kKeyTile - 1) / kKeyTile;
   clear_launch_error();
-  mask_tiles_k<<<dim3(static_cast<unsigned>(words), static_cast<unsigned>(row_blocks)), 256, 0, as_stream(stream)>>>(
+  mask_tiles_k<<<dim3(static_cast<unsigned>(4 * words), static_cast<unsigned>(row_blocks)), 256, 0,
+                 as_stream(stream)>>>(
       mask, mask_ld, static_cast<int>(rows), static_cast<int>(keys), map, static_cast<int>(words));
   if (const int st = check_launch(what)) return st;
   const dim3 split_grid(static_cast<unsigned>(tiles), static_cast<unsigned>(slices));
