@@ -590,15 +590,18 @@ def config8(be, torch, timer):
     """The prefill pass's projections on the matrix cores (`linear` over bf16
     activations, fp32 sums and output) at Unlimited-OCR-2's decoder shapes for
     a 4096-token prompt: q/k/v + router q/k [4096 <- 1280], o [1280 <- 1280],
-    the dense FFN's gate and up [6848 <- 1280] and down [1280 <- 6848], the
-    shared experts' gate/up [1792 <- 1280] and down [1280 <- 1792]. Each
-    GEMM is timed on its own over fresh weight sets; the step is one dense
-    layer's six projections plus the o projection in sequence."""
+    the dense FFN's gate and up stacked [2 x 6848 <- 1280] (one product, as
+    the prompt pass forms them) and down [1280 <- 6848], the shared experts'
+    gate/up [2 x 1792 <- 1280] and down [1280 <- 1792]; gate and up apart
+    [6848 <- 1280] are timed beside them. Each GEMM is timed on its own over
+    fresh weight sets; the step is one dense layer's projections in
+    sequence: qkv+router, o, gate+up, down."""
     rows, hidden = 4096, 1280
-    shapes = {"qkv_router": (4096, 1280), "o": (1280, 1280), "gate": (6848, 1280), "up": (6848, 1280),
-              "down": (1280, 6848), "shared_gate_up": (2 * 1792, 1280), "shared_down": (1280, 1792)}
+    shapes = {"qkv_router": (4096, 1280), "o": (1280, 1280), "gate_up": (2 * 6848, 1280), "down": (1280, 6848),
+              "gate": (6848, 1280), "up": (6848, 1280), "shared_gate_up": (2 * 1792, 1280),
+              "shared_down": (1280, 1792)}
     xs = {k: bf16_randn(torch, (rows, k)) for k in {1280, 6848, 1792}}
-    ys = {n: torch.empty(rows, n, device="cuda") for n in {4096, 1280, 6848, 2 * 1792}}
+    ys = {n: torch.empty(rows, n, device="cuda") for n in {4096, 1280, 6848, 2 * 6848, 2 * 1792}}
     kern = {}
     total_flop, total_us = 0.0, 0.0
     for name, (n, k) in shapes.items():
@@ -608,12 +611,12 @@ def config8(be, torch, timer):
         tf = flop / (ms * 1e-3) / 1e12
         kern[name] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
                       "m": rows, "n": n, "k": k}
-        if name in ("qkv_router", "o", "gate", "up", "down"):
+        if name in ("qkv_router", "o", "gate_up", "down"):
             total_flop += flop
             total_us += ms * 1e3
     tf = total_flop / (total_us * 1e-6) / 1e12
     return {"workload": "prefill projections of a dense decoder layer for a 4096-token prompt (bf16 activations, "
-                        "bf16 weights, fp32 sums): qkv+router, o, gate, up, down",
+                        "bf16 weights, fp32 sums): qkv+router, o, gate+up stacked, down",
             "step": {"us": round(total_us, 2), "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
                      "bound": "mfma"},
             "kernels": kern}

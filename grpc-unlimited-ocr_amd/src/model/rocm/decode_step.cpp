@@ -79,6 +79,15 @@ DecodeStep::DecodeStep(const Context& ctx, const DecoderDims& dims, const std::u
   validate();
   const auto& d = dims_;
   capacity_blocks_ = (d.capacity + d.router.block_size - 1) / d.router.block_size;
+  for (const auto& l : layers_) {
+    const bool moe = l.moe != nullptr;
+    const std::int64_t f = moe ? l.moe->shared_ffn : l.ffn, part = f * d.hidden;
+    Array gu(ctx_, DType::kBF16, 2 * part);
+    const auto bytes = static_cast<std::size_t>(part) * sizeof(std::uint16_t);
+    copy_on_device(ctx_, gu.bf16(), moe ? l.moe->shared_gate : l.gate, bytes);
+    copy_on_device(ctx_, gu.bf16() + part, moe ? l.moe->shared_up : l.up, bytes);
+    gate_up_.push_back(std::move(gu));
+  }
   std::int64_t max_ffn = 1, max_experts = 1, max_k = 1, max_expert_ffn = 1;
   for (const auto& l : layers_) {
     if (l.moe == nullptr) {

@@ -217,6 +217,9 @@ class DecodeStep {
   Array router_logits_, expert_ids_, expert_weights_, expert_scratch_;
   std::vector<Array> k_cache_, v_cache_, router_keys_, summaries_;
   std::vector<Array> trace_x_in_, trace_rqk_, trace_z_, trace_mask_, trace_x_mid_;
+  // per layer, the dense MLP's (or the shared experts') gate and up rows
+  // stacked [2 ffn, hidden]: the prompt pass forms both in one product
+  std::vector<Array> gate_up_;
   std::vector<std::vector<float>> prefill_masks_;
   std::unique_ptr<PinnedBuffer> state_host_, logits_host_;
   std::unique_ptr<Graph> graph_;

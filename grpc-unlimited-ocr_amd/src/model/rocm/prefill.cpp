@@ -35,6 +35,17 @@ Array rounded(const Context& ctx, const float* x, std::int64_t n) {
 // y [rows, hidden] = silu(x Wg) * (x Wu) Wd over bf16 weights: gate and up
 // [ffn, hidden], down [hidden, ffn] (the reference's mlp,
 // cuda_decoder.cpp:117-135); xb is x rounded to bf16.
+// The same with gate and up stacked [2 ffn, hidden]: one product gives
+// [gate | up] per row, then the SwiGLU over the concatenated rows.
+void mlp_stacked(const Context& ctx, const std::uint16_t* xb, std::int64_t rows, std::int64_t hidden,
+                 const std::uint16_t* gate_up, const std::uint16_t* down, std::int64_t ffn, float* y) {
+  Array gu(ctx, DType::kF32, rows * 2 * ffn), act(ctx, DType::kF32, rows * ffn);
+  linear_bf16x(ctx, xb, rows, hidden, gate_up, 2 * ffn, nullptr, gu.f32());
+  swiglu(ctx, gu.f32(), act.f32(), rows, ffn);
+  const Array ab = rounded(ctx, act.f32(), rows * ffn);
+  linear_bf16x(ctx, ab.bf16(), rows, ffn, down, hidden, nullptr, y);
+}
+
 void mlp(const Context& ctx, const std::uint16_t* xb, std::int64_t rows, std::int64_t hidden, const std::uint16_t* gate,
          const std::uint16_t* up, const std::uint16_t* down, std::int64_t ffn, float* y) {
   Array g(ctx, DType::kF32, rows * ffn), u(ctx, DType::kF32, rows * ffn);
@@ -183,7 +194,7 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
     add_rms_norm(ctx_, x.f32(), delta.f32(), l.post_norm, h.f32(), rows, H, eps);
     const Array hb = rounded(ctx_, h.f32(), rows * H);
     if (l.moe == nullptr) {
-      mlp(ctx_, hb.bf16(), rows, H, l.gate, l.up, l.down, l.ffn, delta.f32());
+      mlp_stacked(ctx_, hb.bf16(), rows, H, gate_up_[li].bf16(), l.down, l.ffn, delta.f32());
       continue;
     }
     // mixture of experts (cuda_decoder.cpp:137-186): the device's softmax
@@ -212,7 +223,7 @@ std::vector<float> DecodeStep::prefill(const std::vector<float>& x_host, const s
         weight_of[static_cast<std::size_t>(e)].push_back(wts_h[at]);
       }
     }
-    mlp(ctx_, hb.bf16(), rows, H, m.shared_gate, m.shared_up, m.shared_down, m.shared_ffn, delta.f32());
+    mlp_stacked(ctx_, hb.bf16(), rows, H, gate_up_[li].bf16(), m.shared_down, m.shared_ffn, delta.f32());
     Array routed = f32(rows * H);
     routed.zero();
     for (std::int64_t e = 0; e < m.experts; ++e) {
