@@ -287,7 +287,8 @@ def _test_mask(kind, rows, keys):
 
 @pytest.mark.parametrize("slices,rows,keys,hd,kind", [(3, 100, 300, 128, "random"), (2, 150, 3000, 64, "random"),
                                                       (4, 300, 1100, 128, "routed"), (1, 200, 64, 128, "dead"),
-                                                      (2, 257, 257, 64, "causal"), (2, 130, 2500, 128, "causal")])
+                                                      (2, 257, 257, 64, "causal"), (2, 130, 2500, 128, "causal"),
+                                                      (1, 1, 1, 64, "causal")])
 def test_attention_with_a_workspace(backend, slices, rows, keys, hd, kind):
     """uocr_rocm_attention_ws / _bf16_ws: the fp32 one-pass attention over a
     mask walking only the tiles its row blocks attend (a first row block
@@ -322,7 +323,8 @@ def test_attention_with_a_workspace(backend, slices, rows, keys, hd, kind):
                                                           (2, 130, 40, 64, "causal", 1.0),
                                                           (2, 200, 2100, 128, "routed", 4.0),
                                                           (1, 200, 64, 128, "dead", 1.0),
-                                                          (2, 150, 3000, 64, "random", 1.0)])
+                                                          (2, 150, 3000, 64, "random", 1.0),
+                                                          (1, 1, 1, 128, "causal", 1.0)])
 def test_attention_masked_split_operands(backend, slices, rows, keys, hd, kind, amp):
     """uocr_rocm_attention_masked_bf16_ws: the masked attention into bf16 on
     the bf16 matrix cores with split operands, the workgroups walking only
