@@ -206,3 +206,27 @@ def test_step_op_empty_shapes_and_scratch_size(backend):
     assert lib.uocr_rocm_attend_scratch_floats(10, 128, 2048) == 10 * 32 * 130
     assert lib.uocr_rocm_attend_scratch_floats(32, 64, 1 << 20) == 32 * 64 * 66
     assert lib.uocr_rocm_attend_scratch_floats(1, 64, 7) == 1 * 1 * 66
+
+
+def test_masked_attention_workspace_sizes(backend):
+    """The masked attention paths' workspaces: the tile map (a word per 1024
+    keys per 128 query rows, rounded up to 64 floats), then for the split
+    path the split key and value tiles (64 hd floats per 32-key tile and
+    slice), and the runs' records (hd + 2 floats per row and run) where the
+    row blocks leave slots idle. Invalid shapes give 0."""
+    fp32 = backend.attention_workspace_floats
+    split = backend.attention_masked_workspace_floats
+    for f in (fp32, split):
+        assert f(0, 64, 64, 128) == 0 and f(1, 0, 64, 128) == 0 and f(1, 64, 0, 128) == 0
+        assert f(1, 64, 64, 96) == 0
+    # 48 rows over 48 keys: one map word, no runs
+    assert fp32(2, 48, 48, 64) == 64
+    assert split(2, 48, 48, 64) == 64 + 2 * 2 * 64 * 64
+    # 10 heads x 4096 rows and keys at hd 128: 32 row blocks x 4 words of map;
+    # the split path cuts a walk into runs of 80 tiles (2 per block), the fp32
+    # path (one workgroup per CU) keeps whole walks
+    tiles, blocks = 128, 32
+    assert fp32(10, 4096, 4096, 128) == blocks * 4 * 1
+    assert split(10, 4096, 4096, 128) == blocks * 4 + 10 * tiles * 64 * 128 + 10 * blocks * 2 * 128 * 130
+    # few row blocks over many keys: both cut walks into runs
+    assert fp32(1, 128, 8192, 64) > 64
