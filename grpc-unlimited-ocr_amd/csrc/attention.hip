@@ -241,8 +241,13 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   using T = Tile<HD, kThreads>;
   constexpr int kHalf = HD / 2;  // columns per lane half in the scores' products
   constexpr int kDBlocks = HD / 32;
-  __shared__ __attribute__((aligned(16))) float ks[kKeyTile * T::kKStride];
-  __shared__ __attribute__((aligned(16))) float vs[HD * T::kVTStride];  // V^T
+  // Two LDS stages of K and V^T without the relative-position bias (tile t
+  // + 1 is written into one while tile t is read from the other: one barrier
+  // a tile); one with it, whose per-query dot products take the LDS.
+  constexpr int kStages = rel_pos<kBias>() ? 1 : 2;
+  constexpr int kKElems = kKeyTile * T::kKStride, kVElems = HD * T::kVTStride;
+  __shared__ __attribute__((aligned(16))) float ks[kStages * kKElems];
+  __shared__ __attribute__((aligned(16))) float vs[kStages * kVElems];  // V^T
   // The relative-position bias: per query row its h height terms at 0 and
   // w width terms at dw_off, rows dots_ld apart: h + w + 1 (odd) for
   // kRelPos, so that the 32 queries of a wave read 32 different banks; for
@@ -358,6 +363,10 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
   }
 
   store_tile<HD, kThreads>(ks, vs, kr, vr);
+  int nxt = after(first, 0);  // the tile after the current one
+  if constexpr (kStages == 2) {
+    if (nxt < tiles) load_tile<HD, kThreads>(a, kb, vb, nxt * kKeyTile, kr, vr);
+  }
   __syncthreads();
 
   f32x16 o[kDBlocks];
@@ -396,12 +405,21 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     }
   };
   load_mask(first, mk);
+  int st = 0;  // the LDS stage holding the current tile
   for (int t = first, i = 0; t < tiles; ++i) {
     const int key0 = t * kKeyTile;
-    const int nxt = after(t, i);
     const bool more = nxt < tiles;
-    if (more) load_tile<HD, kThreads>(a, kb, vb, nxt * kKeyTile, kr, vr);
+    int nxt2 = tiles;  // (two stages) the tile after nxt, requested now
+    if constexpr (kStages == 2) {
+      if (more) store_tile<HD, kThreads>(ks + (st ^ 1) * kKElems, vs + (st ^ 1) * kVElems, kr, vr);
+      nxt2 = more ? after(nxt, i + 1) : tiles;
+      if (nxt2 < tiles) load_tile<HD, kThreads>(a, kb, vb, nxt2 * kKeyTile, kr, vr);
+    } else {
+      if (more) load_tile<HD, kThreads>(a, kb, vb, nxt * kKeyTile, kr, vr);
+    }
     load_mask(more ? nxt : t, mn);
+    const float* kcur = ks + st * kKElems;
+    const float* vcur = vs + st * kVElems;
 
     // A wave whose rows all lie past the last query row (the tail workgroup
     // of a slice) only helps stage the tiles.
@@ -417,7 +435,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
       f32x16 s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-      const float* krow = ks + c * T::kKStride + hl * kHalf;
+      const float* krow = kcur + c * T::kKStride + hl * kHalf;
 #pragma unroll
       for (int i = 0; i < kHalf; i += 4) {
         const float4 kk = *reinterpret_cast<const float4*>(krow + i);
@@ -520,7 +538,7 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
       for (int b = 0; b < kDBlocks; ++b) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const float4 vt = *reinterpret_cast<const float4*>(vs + (32 * b + c) * T::kVTStride + 8 * g + 4 * hl);
+          const float4 vt = *reinterpret_cast<const float4*>(vcur + (32 * b + c) * T::kVTStride + 8 * g + 4 * hl);
           o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt.x, s[4 * g], o[b], 0, 0, 0);
           o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt.y, s[4 * g + 1], o[b], 0, 0, 0);
           o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt.z, s[4 * g + 2], o[b], 0, 0, 0);
@@ -530,15 +548,23 @@ __global__ __launch_bounds__(64 * waves_of<kBias>()) void attention_k(const Attn
     }
 
     __syncthreads();  // every wave is done with this tile
-    if (more) {
-      store_tile<HD, kThreads>(ks, vs, kr, vr);
-      __syncthreads();
+    if constexpr (kStages == 1) {
+      if (more) {
+        store_tile<HD, kThreads>(ks, vs, kr, vr);
+        __syncthreads();
+      }
     }
     if constexpr (kBias == Bias::kMask) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mk[r] = mn[r];
     }
     t = nxt;
+    if constexpr (kStages == 2) {
+      nxt = nxt2;
+      st ^= 1;
+    } else {
+      nxt = more ? after(t, i + 1) : tiles;
+    }
   }
 
   if (!qin) return;
