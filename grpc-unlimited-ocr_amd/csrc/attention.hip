@@ -11,10 +11,12 @@
 //
 // A workgroup of 4 waves (2 with the relative-position bias over a grid of
 // whole tiles) takes 128 (64) query rows of one slice; each wave owns 32 of
-// them and walks the keys 32 at a time, the key and value tiles staged in
-// LDS for the workgroup (the next tile's loads in flight in registers while
-// the current one is used); a wave past the last row only helps stage the
-// tiles. Per tile a wave forms S^T = K Q^T (32 keys x 32
+// them and walks the keys 32 at a time, the key tiles and transposed value
+// tiles staged in LDS for the workgroup (the next tile's loads in flight in
+// registers while the current one is used; without the relative-position
+// bias two LDS stages, the next tile written while the current one is
+// read); a wave past the last row only helps stage the tiles. Per tile a
+// wave forms S^T = K Q^T (32 keys x 32
 // queries, hd / 2 products, each summing 2 of the head's columns: lane half
 // h supplies column h * hd / 2 + i to product i, so a lane keeps its query's
 // half row in registers and reads its key's half row from LDS), which leaves
@@ -23,7 +25,8 @@
 // rescale and sum are per lane plus one exchange with the partner lane. The
 // values' product O^T += V^T P^T takes the probabilities straight from those
 // registers: product i sums keys 8 (i / 4) + r % 4 + 4 h, exactly the keys
-// register i holds, so P needs no movement; each 32 columns of the head are
+// register i holds, so P needs no movement, and a lane's V^T values for four
+// consecutive products are one 16-byte read; each 32 columns of the head are
 // 16 products into 16 accumulators.
 //
 // With a mask, a wave reads its 32 x 32 block of the mask before a tile's
