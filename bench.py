@@ -807,6 +807,10 @@ def decode_step_12(be, torch, timer, hidden, heads, hd, ffn, cap, scratch, b, vo
         total = rest + layers * (attn_fixed + kv_bytes(4 if dtype == torch.float32 else 2))
         ms = timer.graph([step])[0]
         out[name] = {"step": report(f"decode step, {name}", total, ms), "us_per_token": round(ms * 1e3, 2)}
+        if name == "fp32_cache":
+            # one step per replay, as DecodeStep::step replays its graph once
+            # per token: the replay's own start and end no longer shared
+            out[name]["us_per_token_one_replay"] = round(timer.graph([step], steps=1)[0] * 1e3, 2)
         for L in Ls:
             del L["kc"], L["vc"]
     out["step"] = out["fp32_cache"]["step"]
