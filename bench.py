@@ -47,6 +47,12 @@ the GPU clocks up), the K timed steps are captured once into a HIP graph and
 replayed; HIP events on the replay stream bracket each replay, with a device
 synchronisation on both sides, and the median of 5 replays is reported (each
 replay's time includes its one graph launch and the replay's fixed cost).
+Each timed replay follows an untimed replay of the same graph on the same
+stream with no host synchronisation between them, so that timing starts
+with the GPU's memory system already at work: after the idle gap of a host
+synchronisation, the first microseconds of a memory-bound chain run slower
+(measured on workload 5 at 20 steps: 51.0 us per step timed from idle, 50.0
+us behind a 256 MiB copy; 49.0-49.4 us either way at 100 steps).
 Per-kernel and per-workload figures come from the same procedure with
 max(K, 100) launches per replay, so the replay's fixed cost of about 10 us
 is spread over at least 100 launches; the headline times exactly K steps.
@@ -174,6 +180,10 @@ class Timer:
         for _ in range(self.replays):
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
+            # an untimed replay right before the timed one, with no host
+            # synchronisation between them: timing starts with the memory
+            # system at work, not waking from the idle gap of the sync
+            g.replay()
             start.record()
             g.replay()
             end.record()
