@@ -77,25 +77,6 @@ void embed_add_rms_norm_step(const Context& ctx, const std::uint16_t* table, std
   check(uocr_rocm_embed_add_rms_norm_step(ctx.stream(), table, table_rows, abi(state), delta, w, x, h, cols, eps));
 }
 
-void embed_add_rms_norm_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
-                                  const StepState* state, const std::uint16_t* delta, const float* w,
-                                  std::uint16_t* x, std::uint16_t* h, std::int64_t cols, float eps) {
-  check(uocr_rocm_embed_add_rms_norm_step_bf16(ctx.stream(), table, table_rows, abi(state), delta, w, x, h, cols,
-                                               eps));
-}
-
-void append_step_bf16(const Context& ctx, std::uint16_t* cache, const float* row, std::int64_t width,
-                      const StepState* state, std::int64_t capacity) {
-  check(uocr_rocm_append_step_bf16(ctx.stream(), cache, row, width, abi(state), capacity));
-}
-
-void attend_step_bf16(const Context& ctx, const float* q, const std::uint16_t* k_cache, const std::uint16_t* v_cache,
-                      std::int64_t heads, std::int64_t hd, const float* mask, float scale, const StepState* state,
-                      float* scratch, std::int64_t capacity, float* out) {
-  check(uocr_rocm_attend_step_bf16(ctx.stream(), q, k_cache, v_cache, heads, hd, mask, scale, abi(state), scratch,
-                                   capacity, out));
-}
-
 void attend_rope_kv_step_bf16(const Context& ctx, const float* q, const float* k_row, const float* v_row,
                               std::uint16_t* k_cache, std::uint16_t* v_cache, std::int64_t heads, std::int64_t hd,
                               const float* mask, float scale, const StepState* state, const float* inv_tok,

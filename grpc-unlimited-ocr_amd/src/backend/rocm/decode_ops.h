@@ -52,12 +52,8 @@ void attend_step(const Context& ctx, const float* q, const float* k_cache, const
                  std::int64_t capacity, float* out);
 
 // New: a bf16 key/value cache (rows rounded to bf16 on append, widened to
-// fp32 in the attention); half the cache bytes.
-void append_step_bf16(const Context& ctx, std::uint16_t* cache, const float* row, std::int64_t width,
-                      const StepState* state, std::int64_t capacity = -1);
-void attend_step_bf16(const Context& ctx, const float* q, const std::uint16_t* k_cache, const std::uint16_t* v_cache,
-                      std::int64_t heads, std::int64_t hd, const float* mask, float scale, const StepState* state,
-                      float* scratch, std::int64_t capacity, float* out);
+// fp32 in the attention); half the cache bytes. The fused step of
+// attend_rope_kv_step below over such a cache.
 void attend_rope_kv_step_bf16(const Context& ctx, const float* q, const float* k_row, const float* v_row,
                               std::uint16_t* k_cache, std::uint16_t* v_cache, std::int64_t heads, std::int64_t hd,
                               const float* mask, float scale, const StepState* state, const float* inv_tok,
@@ -69,9 +65,6 @@ void attend_rope_kv_step_bf16(const Context& ctx, const float* q, const float* k
 void embed_add_rms_norm_step(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
                              const StepState* state, const float* delta, const float* w, float* x, float* h,
                              std::int64_t cols, float eps);
-void embed_add_rms_norm_step_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
-                                  const StepState* state, const std::uint16_t* delta, const float* w,
-                                  std::uint16_t* x, std::uint16_t* h, std::int64_t cols, float eps);
 
 // New: rope_qk_step on (q, k_row), the appends of the rotated key and of
 // v_row at pos, and attend_step, in attend_step's two launches; q, k_row and
@@ -129,6 +122,8 @@ void attend_rope_kv_step_segments(const Context& ctx, const float* q, const floa
                                   const StepState* state, const float* inv_tok, std::int64_t n_tok,
                                   const float* inv_page, std::int64_t page_mod, float* scratch,
                                   std::int64_t capacity, float* out);
+// The same over a bf16 key/value cache (the rotated key and v_row rounded
+// to bf16 on append, cache rows widened to fp32 in the attention).
 void attend_rope_kv_step_segments_bf16(const Context& ctx, const float* q, const float* k_row, const float* v_row,
                                        std::uint16_t* k_cache, std::uint16_t* v_cache, std::int64_t heads,
                                        std::int64_t hd, const std::int32_t* segments, std::int64_t max_live,

@@ -66,11 +66,6 @@ void rope_qk(const Context& ctx, float* q, std::int64_t q_heads, float* k, std::
                           page_mod, one_tok, one_page));
 }
 
-void rms_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std::int64_t rows, std::int64_t cols,
-                   float eps) {
-  check(uocr_rocm_rms_norm_bf16(ctx.stream(), x, w, rows, cols, eps));
-}
-
 void add_rms_norm_bf16(const Context& ctx, std::uint16_t* x, const std::uint16_t* delta, const float* w,
                        std::uint16_t* h, std::int64_t rows, std::int64_t cols, float eps) {
   check(uocr_rocm_add_rms_norm_bf16(ctx.stream(), x, delta, w, h, rows, cols, eps));
@@ -90,14 +85,6 @@ void swiglu_bf16(const Context& ctx, const std::uint16_t* in, std::uint16_t* out
   check(uocr_rocm_swiglu_bf16(ctx.stream(), in, out, rows, ffn));
 }
 
-void rope_bf16(const Context& ctx, std::uint16_t* x, std::int64_t rows, std::int64_t heads, std::int64_t dim,
-               const std::int64_t* tok, const std::int64_t* page, const float* inv_tok, std::int64_t n_tok,
-               const float* inv_page, std::int64_t n_page, std::int64_t page_mod, std::int64_t one_tok,
-               std::int64_t one_page) {
-  check(uocr_rocm_rope_bf16(ctx.stream(), x, rows, heads, dim, tok, page, inv_tok, n_tok, inv_page, n_page, page_mod,
-                            one_tok, one_page));
-}
-
 void rope_qk_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_heads, std::uint16_t* k, std::int64_t k_heads,
                   std::int64_t rows, std::int64_t dim, const std::int64_t* tok, const std::int64_t* page,
                   const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t n_page,
@@ -106,25 +93,11 @@ void rope_qk_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_heads, st
                                n_page, page_mod, one_tok, one_page));
 }
 
-void gather_rows_bf16_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
-                           const std::int64_t* index, std::int64_t rows, std::int64_t cols, std::uint16_t* dst) {
-  check(uocr_rocm_gather_rows_bf16_bf16(ctx.stream(), table, table_rows, index, rows, cols, dst));
-}
-
 void router_norm(const Context& ctx, float* x, const float* w, std::int64_t rows, std::int64_t cols, float eps) {
   check(uocr_rocm_router_norm(ctx.stream(), x, w, rows, cols, eps));
 }
 
-void router_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std::int64_t rows, std::int64_t cols,
-                      float eps) {
-  check(uocr_rocm_router_norm_bf16(ctx.stream(), x, w, rows, cols, eps));
-}
-
 void quick_gelu(const Context& ctx, float* x, std::int64_t n) { check(uocr_rocm_quick_gelu(ctx.stream(), x, n)); }
-
-void quick_gelu_bf16(const Context& ctx, std::uint16_t* x, std::int64_t n) {
-  check(uocr_rocm_quick_gelu_bf16(ctx.stream(), x, n));
-}
 
 void softmax_rows(const Context& ctx, float* x, std::int64_t rows, std::int64_t cols) {
   check(uocr_rocm_softmax_rows(ctx.stream(), x, rows, cols));
@@ -211,13 +184,6 @@ void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, 
                             slices, rows, keys, hd, scale, mask, mask_ld));
 }
 
-void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
-                       std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
-                       float scale, const float* rh, const float* rw) {
-  check(uocr_rocm_attention_rel_pos(ctx.stream(), q.p, q.ld, q.slice, k.p, k.ld, k.slice, v.p, v.ld, v.slice, out,
-                                    ldo, so, slices, h, w, hd, scale, rh, rw));
-}
-
 void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, std::uint16_t* out, std::int64_t ldo,
                std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
                const float* mask, std::int64_t mask_ld) {
@@ -272,13 +238,6 @@ void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t w
   check(uocr_rocm_attention_rel_pos_windows_ws(ctx.stream(), q.p, q.ld, q.slice, wq, k.p, k.ld, k.slice, wk, v.p, v.ld,
                                                v.slice, wv, out, ldo, so, wo, heads, windows, h, w, hd, scale, rh, rw,
                                                workspace, workspace_floats));
-}
-
-void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
-                       std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
-                       float scale, const float* rh, const float* rw, float* workspace, std::int64_t workspace_floats) {
-  check(uocr_rocm_attention_rel_pos_ws(ctx.stream(), q.p, q.ld, q.slice, k.p, k.ld, k.slice, v.p, v.ld, v.slice, out,
-                                       ldo, so, slices, h, w, hd, scale, rh, rw, workspace, workspace_floats));
 }
 
 void linear(const Context& ctx, const float* x, std::int64_t m, std::int64_t k, const std::uint16_t* w_bf16,
@@ -390,11 +349,6 @@ void moe_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::i
                  const std::uint16_t* shared_down, std::int64_t shared_ffn, float* scratch, float* out) {
   check(uocr_rocm_moe_ffn_one(ctx.stream(), x, hidden, ffn, gate, up, down, experts, logits, k, ids, weights,
                               shared_act, shared_down, shared_ffn, scratch, out));
-}
-
-void gemv_f32(const Context& ctx, const float* x, std::int64_t k, const float* w, std::int64_t n, const float* bias,
-              float* y) {
-  check(uocr_rocm_gemv_f32(ctx.stream(), x, k, w, n, bias, y));
 }
 
 }  // namespace uocr::rocm

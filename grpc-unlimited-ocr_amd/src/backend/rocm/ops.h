@@ -69,8 +69,6 @@ void rope_qk(const Context& ctx, float* q, std::int64_t q_heads, float* k, std::
 
 // ---- bf16 activations ------------------------------------------------------------
 
-void rms_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std::int64_t rows, std::int64_t cols,
-                   float eps);
 void add_rms_norm_bf16(const Context& ctx, std::uint16_t* x, const std::uint16_t* delta, const float* w,
                        std::uint16_t* h, std::int64_t rows, std::int64_t cols, float eps);
 void layer_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, const float* b, std::int64_t rows,
@@ -78,26 +76,16 @@ void layer_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, const
 void gelu_erf_bf16(const Context& ctx, std::uint16_t* x, std::int64_t n);
 void swiglu_bf16(const Context& ctx, const std::uint16_t* in, std::uint16_t* out, std::int64_t rows,
                  std::int64_t ffn);
-void rope_bf16(const Context& ctx, std::uint16_t* x, std::int64_t rows, std::int64_t heads, std::int64_t dim,
-               const std::int64_t* tok, const std::int64_t* page, const float* inv_tok, std::int64_t n_tok,
-               const float* inv_page, std::int64_t n_page, std::int64_t page_mod, std::int64_t one_tok = 0,
-               std::int64_t one_page = 0);
 void rope_qk_bf16(const Context& ctx, std::uint16_t* q, std::int64_t q_heads, std::uint16_t* k, std::int64_t k_heads,
                   std::int64_t rows, std::int64_t dim, const std::int64_t* tok, const std::int64_t* page,
                   const float* inv_tok, std::int64_t n_tok, const float* inv_page, std::int64_t n_page,
                   std::int64_t page_mod, std::int64_t one_tok = 0, std::int64_t one_page = 0);
-// Embedding rows kept in bf16 (a bit copy).
-void gather_rows_bf16_bf16(const Context& ctx, const std::uint16_t* table, std::int64_t table_rows,
-                           const std::int64_t* index, std::int64_t rows, std::int64_t cols, std::uint16_t* dst);
 
 // ---- row ops beside the path (reference signatures, src/backend/cuda/ops.h:35-46) -------
 
 // The router's norm: non-finite inputs zeroed, scaled by (1 + w), clamped to +-1e4.
 void router_norm(const Context& ctx, float* x, const float* w, std::int64_t rows, std::int64_t cols, float eps);
-void router_norm_bf16(const Context& ctx, std::uint16_t* x, const float* w, std::int64_t rows, std::int64_t cols,
-                      float eps);
 void quick_gelu(const Context& ctx, float* x, std::int64_t n);
-void quick_gelu_bf16(const Context& ctx, std::uint16_t* x, std::int64_t n);
 // Each row of x [rows, cols] becomes its softmax, in place. A row whose
 // entries are all -inf becomes all zeros.
 void softmax_rows(const Context& ctx, float* x, std::int64_t rows, std::int64_t cols);
@@ -164,9 +152,6 @@ struct AttnOperand {
 void attention(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
                std::int64_t so, std::int64_t slices, std::int64_t rows, std::int64_t keys, std::int64_t hd, float scale,
                const float* mask, std::int64_t mask_ld);
-void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
-                       std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
-                       float scale, const float* rh, const float* rw);
 // New: the same with the bias's dot products formed beforehand into a
 // workspace of attention_rel_pos_workspace_floats(slices, h, w) floats.
 std::int64_t attention_rel_pos_workspace_floats(std::int64_t slices, std::int64_t h, std::int64_t w);
@@ -177,9 +162,6 @@ void attention_rel_pos_windows(const Context& ctx, AttnOperand q, std::int64_t w
                                std::int64_t wo, std::int64_t heads, std::int64_t windows, std::int64_t h,
                                std::int64_t w, std::int64_t hd, float scale, const float* rh, const float* rw,
                                float* workspace, std::int64_t workspace_floats);
-void attention_rel_pos(const Context& ctx, AttnOperand q, AttnOperand k, AttnOperand v, float* out, std::int64_t ldo,
-                       std::int64_t so, std::int64_t slices, std::int64_t h, std::int64_t w, std::int64_t hd,
-                       float scale, const float* rh, const float* rw, float* workspace, std::int64_t workspace_floats);
 // New: attention and attention_rel_pos_windows with the output in bf16 (the
 // rounding the output projection applies), bitwise the fp32 op then
 // round_bf16.
@@ -258,7 +240,7 @@ void add_rms_norm_swiglu_gemv_bf16(const Context& ctx, const float* x, const flo
                                    const std::uint16_t* w_gate, const std::uint16_t* w_up, std::int64_t ffn,
                                    float* act);
 // New: the SwiGLU pair above and the fp32 router logits [experts] on the
-// unrounded h in one launch, bitwise it followed by gemv_f32(h, router).
+// unrounded h in one launch, bitwise it followed by uocr_rocm_gemv_f32(h, router).
 void add_rms_norm_swiglu_router_gemv_bf16(const Context& ctx, const float* x, const float* delta, float* x_out,
                                           const float* w_norm, float eps, float* h_out, std::int64_t k,
                                           const std::uint16_t* w_gate, const std::uint16_t* w_up, std::int64_t ffn,
@@ -292,9 +274,6 @@ void moe_ffn_one(const Context& ctx, const float* x, std::int64_t hidden, std::i
                  const std::uint16_t* gate, const std::uint16_t* up, const std::uint16_t* down, std::int64_t experts,
                  const float* logits, std::int64_t k, std::int64_t* ids, float* weights, const float* shared_act,
                  const std::uint16_t* shared_down, std::int64_t shared_ffn, float* scratch, float* out);
-// y[n] = x . w[n, :] (+ bias) with fp32 weights: the gate logits.
-void gemv_f32(const Context& ctx, const float* x, std::int64_t k, const float* w, std::int64_t n, const float* bias,
-              float* y);
 
 // ---- the block router (src/backend/cuda/ops.h:97-124) -----------------------------------
 

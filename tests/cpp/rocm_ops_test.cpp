@@ -28,6 +28,7 @@
 #include "model/rocm/decode_step.h"
 #include "model/rocm/decoder.h"
 #include "model/rocm/model.h"
+#include "uocr_rocm.h"
 #include "../../oracle/uocr_oracle.h"
 
 namespace ro = uocr::rocm;
@@ -1545,6 +1546,90 @@ void step_ops(const ro::Context& ctx) {
   }
 }
 
+// The fused wrappers a CudaDecoder-style caller is shown in the integration
+// notes, each against the unfused calls it replaces, bit for bit.
+void fused_wrappers(const ro::Context& ctx) {
+  {  // rope_qk: rope on q, then rope on k
+    const std::int64_t rows = 5, qh = 4, kh = 2, dim = 16;
+    const auto q = random(rows * qh * dim), k = random(rows * kh * dim);
+    const std::vector<std::int64_t> tok{0, 5, 300, 7, 2}, page{0, 1, 2, 3, 9};
+    const auto inv_tok = rope_inv(7, 1e4);
+    const std::vector<float> inv_page{1.0f};
+    auto dt = up_ids(ctx, tok), dp = up_ids(ctx, page), dit = up(ctx, inv_tok), dip = up(ctx, inv_page);
+    auto q1 = up(ctx, q), k1 = up(ctx, k), q2 = up(ctx, q), k2 = up(ctx, k);
+    ro::rope_qk(ctx, q1.f32(), qh, k1.f32(), kh, rows, dim, dt.i64(), dp.i64(), dit.f32(), 7, dip.f32(), 1, 2);
+    ro::rope(ctx, q2.f32(), rows, qh, dim, dt.i64(), dp.i64(), dit.f32(), 7, dip.f32(), 1, 2);
+    ro::rope(ctx, k2.f32(), rows, kh, dim, dt.i64(), dp.i64(), dit.f32(), 7, dip.f32(), 1, 2);
+    require(same_bits(q1.download(), q2.download()) && same_bits(k1.download(), k2.download()),
+            "rope_qk is rope on q and rope on k");
+  }
+  {  // scale_mask_softmax_rows: scale_add_mask, then softmax_rows
+    const std::int64_t batch = 3, rows = 5, cols = 300;
+    const auto x = random(batch * rows * cols, 3.0f);
+    auto mask = random(rows * cols);
+    for (std::int64_t c = 0; c < cols; c += 7) mask[static_cast<std::size_t>(c)] = -INFINITY;
+    for (std::int64_t c = 0; c < cols; ++c) mask[static_cast<std::size_t>(3 * cols + c)] = -INFINITY;
+    auto dm = up(ctx, mask), a = up(ctx, x), b = up(ctx, x);
+    ro::scale_mask_softmax_rows(ctx, a.f32(), 0.125f, dm.f32(), batch, rows, cols);
+    ro::scale_add_mask(ctx, b.f32(), 0.125f, dm.f32(), batch, rows, cols);
+    ro::softmax_rows(ctx, b.f32(), batch * rows, cols);
+    require(same_bits(a.download(), b.download()), "scale_mask_softmax_rows is scale_add_mask then softmax_rows");
+  }
+  {  // embed_add_rms_norm_step: embed_step (+ add_inplace), copy, rms_norm
+    const std::int64_t vocab = 6, cols = 1280;
+    const float eps = 1e-6f;
+    const auto table = random(vocab * cols), w = random(cols), delta = random(cols);
+    auto dt = up(ctx, table, ro::DType::kBF16), dw = up(ctx, w), dd = up(ctx, delta);
+    ro::Array state(ctx, ro::DType::kI64, 5);
+    const std::int64_t s[5] = {4, 0, 0, 0, -1};
+    state.upload(s, 5);
+    const auto* st = reinterpret_cast<const ro::StepState*>(state.data());
+    for (const bool with_delta : {false, true}) {
+      ro::Array x1(ctx, ro::DType::kF32, cols), h1(ctx, ro::DType::kF32, cols), x2(ctx, ro::DType::kF32, cols),
+          h2(ctx, ro::DType::kF32, cols);
+      ro::embed_add_rms_norm_step(ctx, dt.bf16(), vocab, st, with_delta ? dd.f32() : nullptr, dw.f32(), x1.f32(),
+                                  h1.f32(), cols, eps);
+      ro::embed_step(ctx, dt.bf16(), st, cols, x2.f32());
+      if (with_delta) ro::add_inplace(ctx, x2.f32(), dd.f32(), cols);
+      ro::copy(ctx, h2.f32(), x2.f32(), cols);
+      ro::rms_norm(ctx, h2.f32(), dw.f32(), 1, cols, eps);
+      require(same_bits(x1.download(), x2.download()) && same_bits(h1.download(), h2.download()),
+              std::string("embed_add_rms_norm_step is embed_step, ") + (with_delta ? "add_inplace, " : "") +
+                  "copy and rms_norm");
+    }
+  }
+  {  // attend_rope_kv_step_bf16: rope_qk_step, two bf16 appends, attend_step_bf16
+    const std::int64_t heads = 4, hd = 64, cap = 64, width = heads * hd, pos = 40;
+    const float scale = 0.125f;
+    const auto kc = random(cap * width), vc = random(cap * width), q = random(width), kr = random(width),
+               vr = random(width);
+    const auto inv = rope_inv(hd / 2, 1e4);
+    auto dinv = up(ctx, inv), dq = up(ctx, q), dkr = up(ctx, kr), dvr = up(ctx, vr);
+    auto ka = up(ctx, kc, ro::DType::kBF16), va = up(ctx, vc, ro::DType::kBF16), kb = up(ctx, kc, ro::DType::kBF16),
+         vb = up(ctx, vc, ro::DType::kBF16), q2 = up(ctx, q), k2 = up(ctx, kr);
+    const std::int64_t floats = ro::attend_scratch_floats(heads, hd, cap);
+    ro::Array state(ctx, ro::DType::kI64, 5), sa(ctx, ro::DType::kF32, floats), sb(ctx, ro::DType::kF32, floats),
+        oa(ctx, ro::DType::kF32, width), ob(ctx, ro::DType::kF32, width);
+    const std::int64_t s[5] = {0, pos, pos, 0, -1};
+    state.upload(s, 5);
+    const auto* st = reinterpret_cast<const ro::StepState*>(state.data());
+    const auto* abi = reinterpret_cast<const uocr_rocm_step_state*>(state.data());
+    ro::attend_rope_kv_step_bf16(ctx, dq.f32(), dkr.f32(), dvr.f32(), ka.bf16(), va.bf16(), heads, hd, nullptr, scale,
+                                 st, dinv.f32(), hd / 2, nullptr, 0, sa.f32(), cap, oa.f32());
+    ro::rope_qk_step(ctx, q2.f32(), heads, k2.f32(), heads, hd, st, dinv.f32(), hd / 2, nullptr, 0);
+    require(uocr_rocm_append_step_bf16(ctx.stream(), kb.bf16(), k2.f32(), width, abi, cap) == UOCR_ROCM_OK &&
+                uocr_rocm_append_step_bf16(ctx.stream(), vb.bf16(), dvr.f32(), width, abi, cap) == UOCR_ROCM_OK &&
+                uocr_rocm_attend_step_bf16(ctx.stream(), q2.f32(), kb.bf16(), vb.bf16(), heads, hd, nullptr, scale,
+                                           abi, sb.f32(), cap, ob.f32()) == UOCR_ROCM_OK,
+            "the unfused bf16-cache step");
+    require(same_bits(oa.download(), ob.download()) && ka.download_bf16() == kb.download_bf16() &&
+                va.download_bf16() == vb.download_bf16(),
+            "attend_rope_kv_step_bf16 is rope_qk_step, two bf16 appends and attend_step_bf16");
+    require(same_bits(dq.download(), q) && same_bits(dkr.download(), kr), "q and k_row are left unrotated");
+  }
+  std::printf("%-26s bitwise\n", "fused wrappers");
+}
+
 void errors(const ro::Context& ctx) {
   ro::Array x(ctx, ro::DType::kF32, 64), w(ctx, ro::DType::kF32, 64);
   require_throws_invalid([&] { ro::rms_norm(ctx, x.f32(), w.f32(), -1, 64, 1e-6f); }, "negative rows");
@@ -1594,6 +1679,7 @@ int main() {
     // alike, which a near-tie in other inputs can break)
     prefill_then_decode(ctx, 64, true);
     prefill_then_decode(ctx, 128, true);
+    fused_wrappers(ctx);
     errors(ctx);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "%s\n", e.what());
