@@ -1547,7 +1547,8 @@ void step_ops(const ro::Context& ctx) {
 }
 
 // The fused wrappers a CudaDecoder-style caller is shown in the integration
-// notes, each against the unfused calls it replaces, bit for bit.
+// notes, each against the unfused calls it replaces, bit for bit; and the
+// reference-named wrappers that no model path here calls.
 void fused_wrappers(const ro::Context& ctx) {
   {  // rope_qk: rope on q, then rope on k
     const std::int64_t rows = 5, qh = 4, kh = 2, dim = 16;
@@ -1626,6 +1627,36 @@ void fused_wrappers(const ro::Context& ctx) {
                 va.download_bf16() == vb.download_bf16(),
             "attend_rope_kv_step_bf16 is rope_qk_step, two bf16 appends and attend_step_bf16");
     require(same_bits(dq.download(), q) && same_bits(dkr.download(), kr), "q and k_row are left unrotated");
+  }
+  {  // the reference-named wrappers no model path calls: rope_step, chw_to_hwc, rel_pos_bias
+    const std::int64_t heads = 3, dim = 16;
+    const auto x = random(heads * dim), inv_tok = rope_inv(7, 1e4);
+    const std::vector<float> inv_page{1.0f};
+    auto dit = up(ctx, inv_tok), dip = up(ctx, inv_page), a = up(ctx, x), b = up(ctx, x);
+    ro::Array state(ctx, ro::DType::kI64, 5);
+    const std::int64_t s[5] = {0, 12, 300, 3, -1};
+    state.upload(s, 5);
+    ro::rope_step(ctx, a.f32(), heads, dim, reinterpret_cast<const ro::StepState*>(state.data()), dit.f32(), 7,
+                  dip.f32(), 2);
+    ro::rope(ctx, b.f32(), 1, heads, dim, nullptr, nullptr, dit.f32(), 7, dip.f32(), 1, 2, 300, 3);
+    require(same_bits(a.download(), b.download()), "rope_step is rope at the state's coordinates");
+
+    const std::int64_t c = 5, h = 7, w = 9, d = 24, ldq = 32;
+    const auto img = random(c * h * w);
+    std::vector<float> want(img.size());
+    orc_chw_to_hwc(img.data(), c, h, w, want.data());
+    auto di = up(ctx, img);
+    ro::Array dy(ctx, ro::DType::kF32, c * h * w);
+    ro::chw_to_hwc(ctx, di.f32(), c, h, w, dy.f32());
+    require(same_bits(dy.download(), want), "chw_to_hwc is the oracle's transpose");
+
+    const auto q = random(h * w * ldq), rh = random(h * h * d), rw = random(w * w * d);
+    std::vector<float> bias(h * w * h * w);
+    orc_rel_pos_bias(q.data(), ldq, h, w, d, rh.data(), rw.data(), bias.data());
+    auto dq = up(ctx, q), drh = up(ctx, rh), drw = up(ctx, rw);
+    ro::Array db(ctx, ro::DType::kF32, h * w * h * w);
+    ro::rel_pos_bias(ctx, dq.f32(), ldq, h, w, d, drh.f32(), drw.f32(), db.f32());
+    expect("rel_pos_bias", max_rel(db.download(), bias), 1e-5);
   }
   std::printf("%-26s bitwise\n", "fused wrappers");
 }
