@@ -1546,8 +1546,8 @@ void step_ops(const ro::Context& ctx) {
   }
 }
 
-// The fused wrappers a CudaDecoder-style caller is shown in the integration
-// notes, each against the unfused calls it replaces, bit for bit; and the
+// The fused wrappers that a CudaDecoder-style caller would take in place of
+// its unfused calls, each against those calls, bit for bit; and the
 // reference-named wrappers that no model path here calls.
 void fused_wrappers(const ro::Context& ctx) {
   {  // rope_qk: rope on q, then rope on k
